@@ -1,0 +1,81 @@
+/* tlgemm.h -- C ABI of libtlgemm.so, the MI355X (gfx950) implementation of
+ * tinylm.c's three fp32 matmul primitives.
+ *
+ * Plain C: pointers, ints and sizes only.  HIP streams are passed as `void *`
+ * (a hipStream_t; NULL = the null stream).
+ *
+ * Layout contract (identical to the reference): dense row-major fp32, leading
+ * dimension = row width, any M, K, N >= 0, buffers never alias (the reference
+ * marks every pointer `restrict`).  `mm` overwrites its output (beta = 0);
+ * `mm_bt` and `mm_atb` add into theirs (beta = 1), exactly once per call.
+ */
+#ifndef TLGEMM_H
+#define TLGEMM_H
+#include <stddef.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes of the int-returning entry points. */
+#define TLG_OK       0
+#define TLG_EINVAL  -1   /* bad argument (negative dimension, NULL pointer)  */
+#define TLG_EHIP    -2   /* HIP runtime error; tlg_last_error() has the text */
+#define TLG_ENOMEM  -3   /* device allocation failed                         */
+#define TLG_ESTATE  -4   /* library not initialised / registry conflict      */
+
+/* ---- lifetime ---------------------------------------------------------- */
+/* Select `device`, create the library's default stream and workspace.  Safe
+ * to call more than once.  No reference counterpart: tinylm.c needs no set-up
+ * for its CPU kernels; the -DUSE_HIP seam calls this lazily. */
+int  tlg_init(int device);
+/* Free the workspace, every registered mirror and the default stream. */
+void tlg_shutdown(void);
+/* Text of the most recent error on this thread ("" if none). */
+const char *tlg_last_error(void);
+
+/* ---- drop-in, host pointers, synchronous ------------------------------- */
+/* These keep the reference's signatures and its error behaviour (no status:
+ * a failure prints the HIP error with file:line and aborts, where tinylm.c
+ * exits on fatal errors, tinylm.c:137).  Operands that lie inside a range
+ * given to tlg_register() are used in place on the device; all others are
+ * copied in (and the output copied back) within the call.  The call returns
+ * once the result is in host memory (or in the registered mirror). */
+
+/* Y[M*N] = X[M*K] @ W[K*N]  (set).  Replaces mm(), tinylm.c:438-449. */
+void tlg_sgemm_nn(float *Y, const float *X, const float *W, int M, int K, int N);
+/* dX[M*K] += dY[M*N] @ W[K*N]^T  (accumulate).  Replaces mm_bt(), tinylm.c:480-489. */
+void tlg_sgemm_nt_acc(float *dX, const float *dY, const float *W, int M, int K, int N);
+/* dW[K*N] += X[M*K]^T @ dY[M*N]  (accumulate).  Replaces mm_atb(), tinylm.c:510-537. */
+void tlg_sgemm_tn_acc(float *dW, const float *X, const float *dY, int M, int K, int N);
+
+/* ---- host-buffer mirrors (device residency for long-lived buffers) ------ */
+/* Give [host, host+bytes) a device mirror, initialised from host memory.
+ * Intended for the flat parameter and gradient buffers (tinylm.c:2739-2740)
+ * and any activation the caller keeps on the device.  Ranges must not
+ * overlap.  No reference counterpart (the reference is host-only). */
+int tlg_register(void *host, size_t bytes);
+int tlg_unregister(void *host);
+/* Copy host -> mirror (e.g. after the optimizer step) / mirror -> host (e.g.
+ * gradients before the grad-norm).  `host` is the registered base pointer. */
+int tlg_push(void *host);
+int tlg_pull(void *host);
+/* Device address that mirrors `host` (which may point inside a range), or
+ * NULL if it is not registered. */
+void *tlg_mirror(const void *host);
+
+/* ---- device pointers, asynchronous on `stream` -------------------------- */
+/* Same arithmetic as the drop-in entries on device-resident buffers; returns
+ * TLG_OK once the kernels are enqueued.  These are what a device-resident
+ * caller (the step drivers in tinylm-c_amd/host) uses. */
+int tlg_dev_sgemm_nn(float *Y, const float *X, const float *W, int M, int K, int N, void *stream);
+int tlg_dev_sgemm_nt_acc(float *dX, const float *dY, const float *W, int M, int K, int N, void *stream);
+int tlg_dev_sgemm_tn_acc(float *dW, const float *X, const float *dY, int M, int K, int N, void *stream);
+/* dst[0..n) = 0 on `stream`, by a fill kernel (never a memset node, so a
+ * captured graph replays it correctly).  The reference's memset() before an
+ * accumulating GEMM, e.g. tinylm.c:1015, :1104, :1113, :1123, :1134. */
+int tlg_dev_zero(float *dst, size_t n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

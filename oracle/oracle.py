@@ -1,0 +1,208 @@
+"""numpy front end of the CPU oracle (liboracle.so) and of the compiled
+reference (_ref/libtlref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, always as the checker or the CPU baseline,
+never as a product path.
+"""
+import ctypes
+import os
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libtlref.so")
+
+_fp = ctypes.POINTER(ctypes.c_float)
+_ip = ctypes.POINTER(ctypes.c_int)
+_i = ctypes.c_int
+
+
+def _f(a):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_fp)
+
+
+def _n(a):
+    assert a.dtype == np.int32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_ip)
+
+
+class _Prims:
+    """mm / mm_bt / mm_atb on numpy arrays with the reference's semantics."""
+
+    prefix = ""
+
+    def mm(self, X, W, Y=None):
+        M, K = X.shape
+        N = W.shape[1]
+        if Y is None:
+            Y = np.empty((M, N), np.float32)
+        getattr(self.dll, self.prefix + "mm")(_f(Y), _f(X), _f(W), M, K, N)
+        return Y
+
+    def mm_bt(self, dX, dY, W):
+        """dX += dY @ W.T in place (W is [K][N])."""
+        M, N = dY.shape
+        K = W.shape[0]
+        getattr(self.dll, self.prefix + "mm_bt")(_f(dX), _f(dY), _f(W), M, K, N)
+        return dX
+
+    def mm_atb(self, dW, X, dY):
+        """dW += X.T @ dY in place."""
+        M, K = X.shape
+        N = dY.shape[1]
+        getattr(self.dll, self.prefix + "mm_atb")(_f(dW), _f(X), _f(dY), M, K, N)
+        return dW
+
+
+class Oracle(_Prims):
+    prefix = "orc_"
+
+    def __init__(self, path=LIB):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run make -C oracle")
+        d = ctypes.CDLL(path)
+        for n in ("orc_mm", "orc_mm_bt", "orc_mm_atb", "orc_mm_f64", "orc_mm_bt_f64", "orc_mm_atb_f64"):
+            getattr(d, n).argtypes = [_fp, _fp, _fp, _i, _i, _i]
+            getattr(d, n).restype = None
+        d.orc_rnd_normal.restype = ctypes.c_float
+        d.orc_xorshift.restype = ctypes.c_uint64
+        d.orc_rng_seed.argtypes = [ctypes.c_uint64]
+        d.orc_rng_state.restype = ctypes.c_uint64
+        d.orc_fill_normal.argtypes = [_fp, ctypes.c_size_t, ctypes.c_float]
+        d.orc_set_pool.argtypes = [_i]
+        d.orc_set_threads.argtypes = [_i]
+        d.orc_threads.restype = _i
+        d.orc_moe_forward.argtypes = [_i, _i, _i, _i, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _ip, _fp, _fp]
+        d.orc_moe_backward.argtypes = [_i, _i, _i, _i, _fp, _fp, _fp, _fp, _fp, _fp, _fp,
+                                       _fp, _fp, _fp, _fp, _ip, _fp, _fp]
+        self.dll = d
+
+    # fp64 textbook references (accumulating forms add into the prefill)
+    def mm_f64(self, X, W):
+        M, K = X.shape
+        N = W.shape[1]
+        Y = np.empty((M, N), np.float32)
+        self.dll.orc_mm_f64(_f(Y), _f(X), _f(W), M, K, N)
+        return Y
+
+    def mm_bt_f64(self, dX, dY, W):
+        M, N = dY.shape
+        self.dll.orc_mm_bt_f64(_f(dX), _f(dY), _f(W), M, W.shape[0], N)
+        return dX
+
+    def mm_atb_f64(self, dW, X, dY):
+        M, K = X.shape
+        self.dll.orc_mm_atb_f64(_f(dW), _f(X), _f(dY), M, K, dY.shape[1])
+        return dW
+
+    def seed(self, s):
+        self.dll.orc_rng_seed(s)
+
+    def normal(self, shape, scale=1.0):
+        a = np.empty(shape, np.float32)
+        self.dll.orc_fill_normal(_f(a), a.size, scale)
+        return a
+
+    def set_threads(self, n):
+        self.dll.orc_set_threads(n)
+
+    def threads(self):
+        return self.dll.orc_threads()
+
+    def set_pool(self, n):
+        self.dll.orc_set_pool(n)
+
+    def moe_forward(self, fnorm, fin, wr, w1, w3, w2):
+        N, D = fnorm.shape
+        E = wr.shape[1]
+        F = w1.shape[2]
+        out = np.empty((N, D), np.float32)
+        assign = np.empty(N, np.int32)
+        gate = np.empty(N, np.float32)
+        rprobs = np.empty((N, E), np.float32)
+        self.dll.orc_moe_forward(N, D, F, E, _f(fnorm), _f(fin), _f(out), _f(wr), _f(w1), _f(w3),
+                                 _f(w2), _n(assign), _f(gate), _f(rprobs))
+        return out, assign, gate, rprobs
+
+    def moe_backward(self, fnorm, dout, wr, w1, w3, w2, gwr, gw1, gw3, gw2, assign, gate, rprobs):
+        N, D = fnorm.shape
+        E = wr.shape[1]
+        F = w1.shape[2]
+        dfn = np.empty((N, D), np.float32)
+        self.dll.orc_moe_backward(N, D, F, E, _f(fnorm), _f(dout), _f(dfn), _f(wr), _f(w1), _f(w3),
+                                  _f(w2), _f(gwr), _f(gw1), _f(gw3), _f(gw2), _n(assign), _f(gate),
+                                  _f(rprobs))
+        return dfn
+
+
+class Reference(_Prims):
+    """The reference's own kernels (built by `make -C oracle ref` from
+    /root/reference/tinylm.c; present only where that tree was)."""
+
+    prefix = "tlref_"
+
+    def __init__(self, path=REF_LIB):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        d = ctypes.CDLL(path)
+        for n in ("tlref_mm", "tlref_mm_bt", "tlref_mm_atb"):
+            getattr(d, n).argtypes = [_fp, _fp, _fp, _i, _i, _i]
+            getattr(d, n).restype = None
+        d.tlref_seed.argtypes = [ctypes.c_uint64]
+        d.tlref_normal.restype = ctypes.c_float
+        d.tlref_threads.argtypes = [_i]
+        d.tlref_moe_forward.argtypes = [_i, _i, _i, _i, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _ip, _fp, _fp]
+        d.tlref_moe_backward.argtypes = [_i, _i, _i, _i, _fp, _fp, _fp, _fp, _fp, _fp, _fp,
+                                         _fp, _fp, _fp, _fp, _ip, _fp, _fp]
+        self.dll = d
+
+    def seed(self, s):
+        self.dll.tlref_seed(s)
+
+    def normal(self, shape, scale=1.0):
+        a = np.empty(shape, np.float32)
+        flat = a.reshape(-1)
+        for i in range(flat.size):
+            flat[i] = scale * self.dll.tlref_normal()
+        return a
+
+    def set_threads(self, n):
+        self.dll.tlref_threads(n)
+
+    def moe_forward(self, fnorm, fin, wr, w1, w3, w2):
+        N, D = fnorm.shape
+        E = wr.shape[1]
+        F = w1.shape[2]
+        out = np.empty((N, D), np.float32)
+        assign = np.empty(N, np.int32)
+        gate = np.empty(N, np.float32)
+        rprobs = np.empty((N, E), np.float32)
+        self.dll.tlref_moe_forward(N, D, F, E, _f(fnorm), _f(fin), _f(out), _f(wr), _f(w1), _f(w3),
+                                   _f(w2), _n(assign), _f(gate), _f(rprobs))
+        return out, assign, gate, rprobs
+
+    def moe_backward(self, fnorm, dout, wr, w1, w3, w2, gwr, gw1, gw3, gw2, assign, gate, rprobs):
+        N, D = fnorm.shape
+        E = wr.shape[1]
+        F = w1.shape[2]
+        dfn = np.empty((N, D), np.float32)
+        self.dll.tlref_moe_backward(N, D, F, E, _f(fnorm), _f(dout), _f(dfn), _f(wr), _f(w1),
+                                    _f(w3), _f(w2), _f(gwr), _f(gw1), _f(gw3), _f(gw2), _n(assign),
+                                    _f(gate), _f(rprobs))
+        return dfn
+
+
+def normwise_rel(got, ref):
+    """max|got - ref| / mean|ref|: the reference selftest's metric
+    (tinylm.c:4782-4784)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    if ref.size == 0:
+        return 0.0
+    den = np.abs(ref).mean()
+    num = np.abs(got - ref).max()
+    if den == 0.0:
+        return float(num)
+    return float(num / den)

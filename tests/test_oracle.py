@@ -1,0 +1,199 @@
+"""CPU tests that pin the oracle (oracle/tl_oracle.c) before anything is
+checked against it.
+
+* every golden fixture written by the reference's own compiled kernels must be
+  reproduced bit for bit (same blocking, same FMA chains, same flags);
+* the fp64 oracles must agree exactly with integer matmuls done by numpy,
+  including the transposes and the accumulator prefill;
+* set vs accumulate semantics, identity and linearity invariants;
+* the MoE restatement against the reference fixtures and against an fp64
+  autograd brute force (torch on the CPU) of the same loss.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import golden, load_npz
+from oracle import normwise_rel
+
+PRIMS = golden("prim_*.npz")
+
+
+def test_fixture_set_present():
+    assert len(PRIMS) >= 10
+    assert golden("moe_*.npz") and golden("chain_dnorm.npz") and golden("rng_normal.npz")
+
+
+@pytest.mark.parametrize("path", PRIMS, ids=[os.path.basename(p)[5:-4] for p in PRIMS])
+def test_oracle_matches_reference_bit_exact(orc, path):
+    d = load_npz(path)
+    Y = np.full_like(d["Y"], -777.0)
+    orc.mm(d["X"], d["W"], Y)
+    assert np.array_equal(Y, d["Y"]), "mm differs from tinylm.c mm"
+    dX = d["dX0"].copy()
+    orc.mm_bt(dX, d["dY"], d["W"])
+    assert np.array_equal(dX, d["dX"]), "mm_bt differs from tinylm.c mm_bt"
+    dW = d["dW0"].copy()
+    orc.mm_atb(dW, d["X"], d["dY"])
+    assert np.array_equal(dW, d["dW"]), "mm_atb differs from tinylm.c mm_atb"
+
+
+@pytest.mark.parametrize("path", PRIMS, ids=[os.path.basename(p)[5:-4] for p in PRIMS])
+def test_fixtures_against_fp64(orc, path):
+    """The reference outputs sit within the selftest's metric of fp64."""
+    d = load_npz(path)
+    assert normwise_rel(d["Y"], orc.mm_f64(d["X"], d["W"])) < 1e-5
+    assert normwise_rel(d["dX"], orc.mm_bt_f64(d["dX0"].copy(), d["dY"], d["W"])) < 1e-5
+    assert normwise_rel(d["dW"], orc.mm_atb_f64(d["dW0"].copy(), d["X"], d["dY"])) < 1e-5
+
+
+def test_pool_dispatch_keeps_results(orc):
+    """The emulated decode pool only changes which thread runs a row."""
+    d = load_npz(golden("prim_selftest_*.npz")[0])
+    for nt in (1, 3, 7):
+        orc.set_pool(nt)
+        try:
+            assert np.array_equal(orc.mm(d["X"], d["W"]), d["Y"])
+            dX = d["dX0"].copy()
+            assert np.array_equal(orc.mm_bt(dX, d["dY"], d["W"]), d["dX"])
+        finally:
+            orc.set_pool(1)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1, 1), (5, 7, 3), (13, 17, 19), (64, 9, 33)])
+def test_fp64_oracle_exact_on_integers(orc, M, K, N):
+    """Small integers make every product and sum exact in float64, so the fp64
+    oracles must equal numpy's int64 matmul exactly -- this pins operand order,
+    transposes and the prefill of the accumulating forms."""
+    r = np.random.default_rng(M * 1000 + K * 10 + N)
+    X = r.integers(-8, 9, (M, K))
+    W = r.integers(-8, 9, (K, N))
+    dY = r.integers(-8, 9, (M, N))
+    P1 = r.integers(-50, 51, (M, K))
+    P2 = r.integers(-50, 51, (K, N))
+    f = lambda a: np.ascontiguousarray(a, dtype=np.float32)  # noqa: E731
+    assert np.array_equal(orc.mm_f64(f(X), f(W)), f(X @ W))
+    assert np.array_equal(orc.mm_bt_f64(f(P1), f(dY), f(W)), f(P1 + dY @ W.T))
+    assert np.array_equal(orc.mm_atb_f64(f(P2), f(X), f(dY)), f(P2 + X.T @ dY))
+    # the restated fp32 kernels are exact here too
+    assert np.array_equal(orc.mm(f(X), f(W)), f(X @ W))
+    assert np.array_equal(orc.mm_bt(f(P1), f(dY), f(W)), f(P1 + dY @ W.T))
+    assert np.array_equal(orc.mm_atb(f(P2), f(X), f(dY)), f(P2 + X.T @ dY))
+
+
+def test_set_and_accumulate_semantics(orc):
+    r = np.random.default_rng(7)
+    X = r.standard_normal((9, 6), dtype=np.float32)
+    W = r.standard_normal((6, 11), dtype=np.float32)
+    dY = r.standard_normal((9, 11), dtype=np.float32)
+    Y = np.full((9, 11), np.nan, np.float32)
+    orc.mm(X, W, Y)
+    assert np.isfinite(Y).all()                      # mm overwrites (tinylm.c:461)
+    z = orc.mm_bt(np.zeros((9, 6), np.float32), dY, W)
+    p = np.full((9, 6), 3.0, np.float32)
+    orc.mm_bt(p, dY, W)
+    np.testing.assert_allclose(p, z + 3.0, rtol=0, atol=1e-5)
+    z = orc.mm_atb(np.zeros((6, 11), np.float32), X, dY)
+    p = np.full((6, 11), -2.0, np.float32)
+    orc.mm_atb(p, X, dY)
+    np.testing.assert_allclose(p, z - 2.0, rtol=0, atol=1e-5)
+
+
+def test_identity_and_linearity(orc):
+    r = np.random.default_rng(11)
+    X = r.standard_normal((10, 8), dtype=np.float32)
+    assert np.array_equal(orc.mm(X, np.eye(8, dtype=np.float32)), X)
+    W = r.standard_normal((8, 5), dtype=np.float32)
+    X2 = r.standard_normal((10, 8), dtype=np.float32)
+    lhs = orc.mm(X + 2 * X2, W)
+    rhs = orc.mm(X, W) + 2 * orc.mm(X2, W)
+    assert normwise_rel(lhs, rhs) < 1e-6
+
+
+def test_chain_fixture(orc):
+    d = load_npz(golden("chain_dnorm.npz")[0])
+    out = np.zeros_like(d["out"])
+    orc.mm_bt(out, d["dq"], d["Wq"])
+    orc.mm_bt(out, d["dk"], d["Wk"])
+    orc.mm_bt(out, d["dv"], d["Wv"])
+    assert np.array_equal(out, d["out"])
+
+
+def test_rng_matches_reference(orc):
+    d = load_npz(golden("rng_normal.npz")[0])
+    orc.seed(int(d["seed"]))
+    assert np.array_equal(orc.normal(d["z"].shape), d["z"])
+
+
+def test_xorshift_closed_form(orc):
+    """xorshift64(13,7,17) from state 1: first output is a known constant."""
+    orc.seed(1)
+    x = 1
+    for _ in range(5):
+        x ^= (x << 13) & 0xFFFFFFFFFFFFFFFF
+        x ^= x >> 7
+        x ^= (x << 17) & 0xFFFFFFFFFFFFFFFF
+        assert orc.dll.orc_xorshift() == x
+    assert x != 1
+
+
+MOES = golden("moe_*.npz")
+
+
+@pytest.mark.parametrize("path", MOES, ids=[os.path.basename(p)[4:-4] for p in MOES])
+def test_moe_oracle_matches_reference(orc, path):
+    d = load_npz(path)
+    out, assign, gate, rprobs = orc.moe_forward(d["fnorm"], d["fin"], d["wr"], d["w1"], d["w3"], d["w2"])
+    assert np.array_equal(assign, d["assign"])
+    assert normwise_rel(out, d["out"]) < 1e-6
+    assert normwise_rel(gate, d["gate"]) < 1e-6
+    assert normwise_rel(rprobs, d["rprobs"]) < 1e-6
+    g = [d[k].copy() for k in ("gwr0", "gw10", "gw30", "gw20")]
+    dfn = orc.moe_backward(d["fnorm"], d["dout"], d["wr"], d["w1"], d["w3"], d["w2"], *g,
+                           assign, gate, rprobs)
+    assert normwise_rel(dfn, d["dfn"]) < 1e-5
+    for got, key in zip(g, ("gwr", "gw1", "gw3", "gw2")):
+        assert normwise_rel(got, d[key]) < 1e-5, key
+
+
+def test_moe_tie_rule():
+    d = load_npz(golden("moe_tie_*.npz")[0])
+    # experts 1 and 2 have identical router columns; the lower index must win
+    assert (d["assign"] != 2).all() and (d["assign"] == 1).any()
+
+
+def test_moe_oracle_against_fp64_autograd(orc):
+    """Brute force in float64: out = fin + p[a(n)] * SwiGLU_a(n)(x_n) and the
+    loss L = <out, dout> + 0.01*E*sum_e (cnt_e/N) * mean_n p[n,e] (the
+    load-balance term whose gradient tinylm.c:937 adds) differentiated by
+    torch autograd; routing a(n) is the argmax, held fixed."""
+    torch = pytest.importorskip("torch")
+    d = load_npz(golden("moe_n96_*.npz")[0])
+    N, D, E = d["fnorm"].shape[0], d["fnorm"].shape[1], d["wr"].shape[1]
+    t = lambda a: torch.tensor(a, dtype=torch.float64, requires_grad=True)  # noqa: E731
+    x, wr, w1, w3, w2 = t(d["fnorm"]), t(d["wr"]), t(d["w1"]), t(d["w3"]), t(d["w2"])
+    fin = torch.tensor(d["fin"], dtype=torch.float64)
+    dout = torch.tensor(d["dout"], dtype=torch.float64)
+    p = torch.softmax(x @ wr, dim=1)
+    a = torch.argmax(p, dim=1)
+    out = fin.clone()
+    for e in range(E):
+        rows = (a == e).nonzero().flatten()
+        if len(rows) == 0:
+            continue
+        xe = x[rows]
+        h = torch.nn.functional.silu(xe @ w1[e]) * (xe @ w3[e])
+        out = out.index_add(0, rows, p[rows, e:e + 1] * (h @ w2[e]))
+    cnt = torch.bincount(a, minlength=E).to(torch.float64)
+    loss = (out * dout).sum() + 0.01 * E * ((cnt / N) * p.mean(dim=0)).sum()
+    loss.backward()
+    o_out, o_assign, gate, rprobs = orc.moe_forward(d["fnorm"], d["fin"], d["wr"], d["w1"], d["w3"], d["w2"])
+    assert np.array_equal(o_assign, a.numpy().astype(np.int32))
+    assert normwise_rel(o_out, out.detach().numpy()) < 1e-5
+    z = [np.zeros_like(d[k]) for k in ("gwr0", "gw10", "gw30", "gw20")]
+    dfn = orc.moe_backward(d["fnorm"], d["dout"], d["wr"], d["w1"], d["w3"], d["w2"], *z,
+                           o_assign, gate, rprobs)
+    assert normwise_rel(dfn, x.grad.numpy()) < 1e-4
+    for got, ref in zip(z, (wr.grad, w1.grad, w3.grad, w2.grad)):
+        assert normwise_rel(got, ref.numpy()) < 1e-4

@@ -1,0 +1,274 @@
+// tlg_api.hip -- the C ABI of libtlgemm.so (declared in include/tlgemm.h):
+// lifetime, error text, host-buffer mirrors, the synchronous host-pointer
+// drop-ins for mm / mm_bt / mm_atb and their asynchronous device twins.
+#include "tlg_internal.h"
+#include <mutex>
+#include <vector>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+TlgState g_tlg = {0, 0, nullptr, nullptr, 0, nullptr, 0};
+
+static thread_local char t_err[512];
+static std::recursive_mutex g_mu;
+
+// Workspace for split reductions: partial tiles (64 MiB) and one arrival
+// counter per output tile.  Sized for the largest split plan the launcher
+// makes on the BASELINE shapes; a bigger plan falls back to splits = 1.
+static const size_t kWsFloats = (size_t)16 << 20;
+static const size_t kCounters = 1 << 16;
+
+int tlg_fail(int code, const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_err, sizeof t_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int tlg_fail_hip(hipError_t e, const char *what, const char *file, int line)
+{
+    return tlg_fail(TLG_EHIP, "%s:%d: %s failed: %s", file, line, what, hipGetErrorString(e));
+}
+
+extern "C" const char *tlg_last_error(void) { return t_err; }
+
+static int init_locked(int device)
+{
+    if (g_tlg.initialised) return TLG_OK;
+    int n = 0;
+    TLG_HIP(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return tlg_fail(TLG_EINVAL, "tlg_init: device %d of %d", device, n);
+    TLG_HIP(hipSetDevice(device));
+    TLG_HIP(hipStreamCreateWithFlags(&g_tlg.stream, hipStreamNonBlocking));
+    void *p = nullptr;
+    if (hipMalloc(&p, kWsFloats * sizeof(float)) != hipSuccess)
+        return tlg_fail(TLG_ENOMEM, "tlg_init: workspace of %zu bytes", kWsFloats * sizeof(float));
+    g_tlg.ws = (float *)p;
+    g_tlg.ws_floats = kWsFloats;
+    if (hipMalloc(&p, kCounters * sizeof(unsigned int)) != hipSuccess)
+        return tlg_fail(TLG_ENOMEM, "tlg_init: tile counters");
+    g_tlg.cnt = (unsigned int *)p;
+    g_tlg.cnt_n = kCounters;
+    TLG_HIP(hipMemset(g_tlg.cnt, 0, kCounters * sizeof(unsigned int)));
+    TLG_HIP(hipDeviceSynchronize());
+    g_tlg.device = device;
+    g_tlg.initialised = 1;
+    return TLG_OK;
+}
+
+extern "C" int tlg_init(int device)
+{
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    return init_locked(device);
+}
+
+int tlg_ensure_init(void)
+{
+    if (g_tlg.initialised) return TLG_OK;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    return init_locked(0);
+}
+
+// ------------------------------------------------------------- mirrors --
+struct Mirror { char *host; size_t bytes; char *dev; };
+static std::vector<Mirror> g_mirrors;
+
+static Mirror *find_mirror(const void *p, size_t need)
+{
+    const char *c = (const char *)p;
+    for (auto &m : g_mirrors)
+        if (c >= m.host && c < m.host + m.bytes) {
+            if (c + need > m.host + m.bytes) return nullptr;
+            return &m;
+        }
+    return nullptr;
+}
+
+extern "C" int tlg_register(void *host, size_t bytes)
+{
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = init_locked(g_tlg.initialised ? g_tlg.device : 0);
+    if (rc) return rc;
+    if (!host || bytes == 0) return tlg_fail(TLG_EINVAL, "tlg_register: empty range");
+    const char *h = (const char *)host;
+    for (auto &m : g_mirrors)
+        if (h < m.host + m.bytes && m.host < h + bytes)
+            return tlg_fail(TLG_ESTATE, "tlg_register: range overlaps a registered range");
+    void *d = nullptr;
+    if (hipMalloc(&d, bytes) != hipSuccess) return tlg_fail(TLG_ENOMEM, "tlg_register: %zu bytes", bytes);
+    hipError_t e = hipMemcpy(d, host, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) { (void)hipFree(d); return tlg_fail_hip(e, "hipMemcpy", __FILE__, __LINE__); }
+    g_mirrors.push_back({(char *)host, bytes, (char *)d});
+    return TLG_OK;
+}
+
+extern "C" int tlg_unregister(void *host)
+{
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    for (size_t i = 0; i < g_mirrors.size(); i++)
+        if (g_mirrors[i].host == (char *)host) {
+            TLG_HIP(hipDeviceSynchronize());
+            TLG_HIP(hipFree(g_mirrors[i].dev));
+            g_mirrors.erase(g_mirrors.begin() + i);
+            return TLG_OK;
+        }
+    return tlg_fail(TLG_ESTATE, "tlg_unregister: %p is not a registered base", host);
+}
+
+static int copy_mirror(void *host, bool to_dev)
+{
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    for (auto &m : g_mirrors)
+        if (m.host == (char *)host) {
+            TLG_HIP(hipStreamSynchronize(g_tlg.stream));
+            if (to_dev) TLG_HIP(hipMemcpy(m.dev, m.host, m.bytes, hipMemcpyHostToDevice));
+            else        TLG_HIP(hipMemcpy(m.host, m.dev, m.bytes, hipMemcpyDeviceToHost));
+            return TLG_OK;
+        }
+    return tlg_fail(TLG_ESTATE, "%p is not a registered base", host);
+}
+
+extern "C" int tlg_push(void *host) { return copy_mirror(host, true); }
+extern "C" int tlg_pull(void *host) { return copy_mirror(host, false); }
+
+extern "C" void *tlg_mirror(const void *host)
+{
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    Mirror *m = find_mirror(host, 1);
+    return m ? m->dev + ((const char *)host - m->host) : nullptr;
+}
+
+void tlg_shutdown_impl(void);
+extern "C" void tlg_shutdown(void)
+{
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g_tlg.initialised) return;
+    (void)hipDeviceSynchronize();
+    for (auto &m : g_mirrors) (void)hipFree(m.dev);
+    g_mirrors.clear();
+    tlg_shutdown_impl();
+    (void)hipFree(g_tlg.ws);
+    (void)hipFree(g_tlg.cnt);
+    (void)hipStreamDestroy(g_tlg.stream);
+    g_tlg = TlgState{0, 0, nullptr, nullptr, 0, nullptr, 0};
+}
+
+// ------------------------------------------------ host-pointer drop-ins --
+// Staging buffers for operands that are not registered: grown on demand,
+// kept for the life of the library.
+struct Stage { void *p = nullptr; size_t bytes = 0; };
+static Stage g_stage[3];
+
+void tlg_shutdown_impl(void)
+{
+    for (auto &s : g_stage) { (void)hipFree(s.p); s = Stage(); }
+}
+
+static int stage_ptr(int slot, size_t bytes, void **out)
+{
+    Stage &s = g_stage[slot];
+    if (s.bytes < bytes) {
+        if (s.p) TLG_HIP(hipFree(s.p));
+        s.p = nullptr; s.bytes = 0;
+        if (hipMalloc(&s.p, bytes) != hipSuccess) return tlg_fail(TLG_ENOMEM, "staging %zu bytes", bytes);
+        s.bytes = bytes;
+    }
+    *out = s.p;
+    return TLG_OK;
+}
+
+// Device address for a host operand of `bytes`: the mirror when registered,
+// else a staging slot (filled from the host when `upload`).
+static int resolve(int slot, const void *host, size_t bytes, bool upload, void **dev, bool *mirrored)
+{
+    Mirror *m = find_mirror(host, bytes);
+    if (m) { *dev = m->dev + ((const char *)host - m->host); *mirrored = true; return TLG_OK; }
+    for (auto &mm : g_mirrors) {
+        const char *c = (const char *)host;
+        if (c >= mm.host && c < mm.host + mm.bytes)
+            return tlg_fail(TLG_ESTATE, "operand runs past the end of its registered range");
+    }
+    *mirrored = false;
+    int rc = stage_ptr(slot, bytes, dev);
+    if (rc) return rc;
+    if (upload) TLG_HIP(hipMemcpyAsync(*dev, host, bytes, hipMemcpyHostToDevice, g_tlg.stream));
+    return TLG_OK;
+}
+
+// out[o_rows x o_cols] (beta) <- kind(A, B); A is a_elems floats, B b_elems.
+static int host_gemm(TlgKind kind, float *out, const float *A, const float *B,
+                     int M, int K, int N)
+{
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = init_locked(g_tlg.initialised ? g_tlg.device : 0);
+    if (rc) return rc;
+    if (M < 0 || K < 0 || N < 0) return tlg_fail(TLG_EINVAL, "negative dimension");
+    size_t nA, nB, nC;
+    int Mo, No, R, lda, ldb, beta;
+    switch (kind) {
+    case TLG_NN: nA = (size_t)M * K; nB = (size_t)K * N; nC = (size_t)M * N;
+                 Mo = M; No = N; R = K; lda = K; ldb = N; beta = 0; break;
+    case TLG_NT: nA = (size_t)M * N; nB = (size_t)K * N; nC = (size_t)M * K;
+                 Mo = M; No = K; R = N; lda = N; ldb = N; beta = 1; break;
+    default:     nA = (size_t)M * K; nB = (size_t)M * N; nC = (size_t)K * N;
+                 Mo = K; No = N; R = M; lda = K; ldb = N; beta = 1; break;
+    }
+    if (nC == 0) return TLG_OK;
+    void *dA = nullptr, *dB = nullptr, *dC = nullptr;
+    bool mA = false, mB = false, mC = false;
+    if (nA) { rc = resolve(0, A, nA * 4, true, &dA, &mA); if (rc) return rc; }
+    if (nB) { rc = resolve(1, B, nB * 4, true, &dB, &mB); if (rc) return rc; }
+    rc = resolve(2, out, nC * 4, beta != 0, &dC, &mC);
+    if (rc) return rc;
+    rc = tlg_gemm_launch(kind, (const float *)dA, (const float *)dB, (float *)dC,
+                         Mo, No, R, lda, ldb, No, beta, g_tlg.stream);
+    if (rc) return rc;
+    if (!mC) TLG_HIP(hipMemcpyAsync(out, dC, nC * 4, hipMemcpyDeviceToHost, g_tlg.stream));
+    TLG_HIP(hipStreamSynchronize(g_tlg.stream));
+    return TLG_OK;
+}
+
+// The reference's primitives return nothing and exit on fatal errors
+// (tinylm.c:137); the drop-ins abort with the error text instead of
+// returning wrong data.
+static void die_on(int rc, const char *who)
+{
+    if (rc == TLG_OK) return;
+    fprintf(stderr, "[tlgemm] %s: %s\n", who, t_err);
+    fflush(stderr);
+    abort();
+}
+
+extern "C" void tlg_sgemm_nn(float *Y, const float *X, const float *W, int M, int K, int N)
+{ die_on(host_gemm(TLG_NN, Y, X, W, M, K, N), "tlg_sgemm_nn"); }
+extern "C" void tlg_sgemm_nt_acc(float *dX, const float *dY, const float *W, int M, int K, int N)
+{ die_on(host_gemm(TLG_NT, dX, dY, W, M, K, N), "tlg_sgemm_nt_acc"); }
+extern "C" void tlg_sgemm_tn_acc(float *dW, const float *X, const float *dY, int M, int K, int N)
+{ die_on(host_gemm(TLG_TN, dW, X, dY, M, K, N), "tlg_sgemm_tn_acc"); }
+
+// ----------------------------------------------------- device twins --
+extern "C" int tlg_dev_sgemm_nn(float *Y, const float *X, const float *W, int M, int K, int N, void *stream)
+{
+    if (M < 0 || K < 0 || N < 0) return tlg_fail(TLG_EINVAL, "negative dimension");
+    return tlg_gemm_launch(TLG_NN, X, W, Y, M, N, K, K, N, N, 0, (hipStream_t)stream);
+}
+extern "C" int tlg_dev_sgemm_nt_acc(float *dX, const float *dY, const float *W, int M, int K, int N, void *stream)
+{
+    if (M < 0 || K < 0 || N < 0) return tlg_fail(TLG_EINVAL, "negative dimension");
+    return tlg_gemm_launch(TLG_NT, dY, W, dX, M, K, N, N, N, K, 1, (hipStream_t)stream);
+}
+extern "C" int tlg_dev_sgemm_tn_acc(float *dW, const float *X, const float *dY, int M, int K, int N, void *stream)
+{
+    if (M < 0 || K < 0 || N < 0) return tlg_fail(TLG_EINVAL, "negative dimension");
+    return tlg_gemm_launch(TLG_TN, X, dY, dW, K, N, M, K, N, N, 1, (hipStream_t)stream);
+}
+extern "C" int tlg_dev_zero(float *dst, size_t n, void *stream)
+{
+    int rc = tlg_ensure_init();
+    if (rc) return rc;
+    return tlg_zero_launch(dst, n, (hipStream_t)stream);
+}

@@ -1,0 +1,42 @@
+// tlg_internal.h -- shared declarations of libtlgemm.so's translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+#include "../../include/tlgemm.h"
+
+// Record a HIP failure as the thread's last error and return TLG_EHIP.
+int tlg_fail_hip(hipError_t e, const char *what, const char *file, int line);
+int tlg_fail(int code, const char *fmt, ...);
+
+#define TLG_HIP(call)                                                        \
+    do {                                                                     \
+        hipError_t e_ = (call);                                              \
+        if (e_ != hipSuccess) return tlg_fail_hip(e_, #call, __FILE__, __LINE__); \
+    } while (0)
+
+// Library state shared by the kernels' launchers (tlg_api.hip owns it).
+struct TlgState {
+    int initialised;
+    int device;
+    hipStream_t stream;        // default stream for the host-pointer entries
+    float *ws;                 // split-reduction partials
+    size_t ws_floats;
+    unsigned int *cnt;         // per-tile arrival counters (kept at zero between launches)
+    size_t cnt_n;
+};
+extern TlgState g_tlg;
+int tlg_ensure_init(void);
+
+// Which operand layout a GEMM launch sees (see tlg_gemm.hip).
+enum TlgKind { TLG_NN = 0, TLG_NT = 1, TLG_TN = 2 };
+
+// C[Mo x No] (beta ? += : =) sum_r A(i,r) B(r,j) on `st`, with the operand
+// layouts of `kind`:
+//   NN: A(i,r) = A[i*lda + r], B(r,j) = B[r*ldb + j]    (mm)
+//   NT: A(i,r) = A[i*lda + r], B(r,j) = B[j*ldb + r]    (mm_bt)
+//   TN: A(i,r) = A[r*lda + i], B(r,j) = B[r*ldb + j]    (mm_atb)
+int tlg_gemm_launch(TlgKind kind, const float *A, const float *B, float *C,
+                    int Mo, int No, int R, int lda, int ldb, int ldc, int beta,
+                    hipStream_t st);
+int tlg_zero_launch(float *dst, size_t n, hipStream_t st);
