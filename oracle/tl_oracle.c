@@ -7,7 +7,7 @@
  * Why the loop nests mirror the reference's blocking: mm and mm_atb compute
  * every output element as ONE sequential multiply-add chain (over k for mm,
  * over m for mm_atb).  Keeping the same chain order -- and compiling with the
- * reference's flags (-O3 -march=native -ffast-math -funroll-loops -fopenmp) so
+ * reference's flags (-O3 -ffast-math -funroll-loops -fopenmp, an FMA ISA) so
  * the multiply-adds contract to FMA the same way -- makes the restatement
  * bit-identical to tinylm.c for those two.  mm_bt is a dot product that
  * -ffast-math vectorises with reassociation; the 4-row blocking is kept so
@@ -183,15 +183,27 @@ void orc_mm_atb(float *dW, const float *X, const float *dY, int M, int K, int N)
 }
 
 /* ------------------------------------------------------- fp64 oracles --- */
+/* Textbook sums in double.  Loop orders stream rows (a double accumulator row
+ * per output row) so the large configurations finish in seconds; every
+ * product and partial sum is in double, so the order does not matter at the
+ * fp32 precision the results are stored in. */
 void orc_mm_f64(float *Y, const float *X, const float *W, int M, int K, int N)
 {
-    #pragma omp parallel for schedule(static)
-    for (int m = 0; m < M; m++)
-        for (int n = 0; n < N; n++) {
-            double s = 0.0;
-            for (int k = 0; k < K; k++) s += (double)X[(size_t)m * K + k] * (double)W[(size_t)k * N + n];
-            Y[(size_t)m * N + n] = (float)s;
+    #pragma omp parallel
+    {
+        double *acc = malloc(sizeof(double) * (size_t)(N > 0 ? N : 1));
+        #pragma omp for schedule(static)
+        for (int m = 0; m < M; m++) {
+            for (int n = 0; n < N; n++) acc[n] = 0.0;
+            for (int k = 0; k < K; k++) {
+                const double x = (double)X[(size_t)m * K + k];
+                const float *w = W + (size_t)k * N;
+                for (int n = 0; n < N; n++) acc[n] += x * (double)w[n];
+            }
+            for (int n = 0; n < N; n++) Y[(size_t)m * N + n] = (float)acc[n];
         }
+        free(acc);
+    }
 }
 void orc_mm_bt_f64(float *dX, const float *dY, const float *W, int M, int K, int N)
 {
@@ -205,13 +217,21 @@ void orc_mm_bt_f64(float *dX, const float *dY, const float *W, int M, int K, int
 }
 void orc_mm_atb_f64(float *dW, const float *X, const float *dY, int M, int K, int N)
 {
-    #pragma omp parallel for schedule(static)
-    for (int k = 0; k < K; k++)
-        for (int n = 0; n < N; n++) {
-            double s = (double)dW[(size_t)k * N + n];
-            for (int m = 0; m < M; m++) s += (double)X[(size_t)m * K + k] * (double)dY[(size_t)m * N + n];
-            dW[(size_t)k * N + n] = (float)s;
+    #pragma omp parallel
+    {
+        double *acc = malloc(sizeof(double) * (size_t)(N > 0 ? N : 1));
+        #pragma omp for schedule(static)
+        for (int k = 0; k < K; k++) {
+            for (int n = 0; n < N; n++) acc[n] = (double)dW[(size_t)k * N + n];
+            for (int m = 0; m < M; m++) {
+                const double x = (double)X[(size_t)m * K + k];
+                const float *g = dY + (size_t)m * N;
+                for (int n = 0; n < N; n++) acc[n] += x * (double)g[n];
+            }
+            for (int n = 0; n < N; n++) dW[(size_t)k * N + n] = (float)acc[n];
         }
+        free(acc);
+    }
 }
 
 /* ----------------------------------------------------------------- RNG --- */
