@@ -1,0 +1,318 @@
+#!/usr/bin/env python3
+"""Benchmark of the fp32 GEMM hot path (tinylm.c's mm / mm_bt / mm_atb) on MI355X.
+
+A "step" is one pass of the reference's GEMM call sequence over one batch:
+for the default workload ("m3"), every forward and
+backward projection GEMM of a 6-layer training step on 4096 rows plus the
+tied-unembedding head (129 GEMMs, 124.0 GFLOP), in the order and with the
+operands tinylm.c's forward/backward use (tinylm-c_amd/host/tl_plan.c),
+issued through libtlgemm's C ABI on device-resident buffers (replayed as one
+HIP graph).  Inputs are synthetic seeded Gaussians (X ~ N(0,1),
+W ~ N(0,0.02^2), dY ~ N(0,0.01^2)) already in HBM when timing starts.
+
+Prints one JSON line: train tokens/s (value), the dominant kernel's roofline,
+an M=1 decode GEMV figure and the CPU baseline -- the
+reference's own kernels (oracle/_ref) timed on this host on a bounded sample.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(REPO, "tinylm-c_amd"), os.path.join(REPO, "oracle")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_FP32_MFMA_TFLOPS = 157.3      # MI355X dense fp32 matrix peak
+PEAK_HBM_GBS = 8000.0              # MI355X HBM3E
+RIDGE = PEAK_FP32_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)   # flop per byte
+
+# BASELINE.json configs (reference argument labels, tinylm.c:361-393 layout)
+TRAIN = {
+    "nano": dict(R=2048, D=128, KD=32, F=384, V=2048, L=1, n_mtp=0),
+    "m3": dict(R=4096, D=256, KD=64, F=768, V=2048, L=6, n_mtp=0),
+    "m8": dict(R=8192, D=384, KD=96, F=1024, V=2048, L=8, n_mtp=2),
+}
+DECODE = dict(D=384, KD=96, F=1024, V=2048, L=8)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def check(rc, what):
+    if rc != 0:
+        import tlgemm
+        raise RuntimeError(f"{what} failed ({rc}): {tlgemm.load().tlg_last_error().decode()}")
+
+
+def roofline_class(flops, nbytes):
+    return "mfma" if flops / max(nbytes, 1.0) >= RIDGE else "hbm"
+
+
+def time_steps(lib, fn, stream, n):
+    e0, e1 = lib.tlg_event_create(), lib.tlg_event_create()
+    check(lib.tlg_stream_sync(stream), "sync")
+    t0 = time.perf_counter()
+    check(lib.tlg_event_record(e0, stream), "event")
+    for _ in range(n):
+        check(fn(), "step")
+    check(lib.tlg_event_record(e1, stream), "event")
+    check(lib.tlg_stream_sync(stream), "sync")
+    wall = time.perf_counter() - t0
+    ms = lib.tlg_event_elapsed_ms(e0, e1)
+    lib.tlg_event_destroy(e0)
+    lib.tlg_event_destroy(e1)
+    return ms, wall
+
+
+def kernel_census(lib, host, plan, run, stream, reps):
+    """Average launch duration per kernel instance, from HIP events on the
+    stream the kernels run on: each GEMM call of the step is launched `reps`
+    times back to back between two events."""
+    import tlgemm  # noqa: F401
+    ev = [lib.tlg_event_create() for _ in range(2 * len(plan.calls))]
+    for i, c in enumerate(plan.calls):
+        if c["op"] == "zero":
+            continue
+        check(lib.tlg_event_record(ev[2 * i], stream), "event")
+        for _ in range(reps):
+            check(host.dll.tl_run_call(run, i, stream), "call")
+        check(lib.tlg_event_record(ev[2 * i + 1], stream), "event")
+    check(lib.tlg_stream_sync(stream), "sync")
+    groups = {}
+    for i, c in enumerate(plan.calls):
+        if c["op"] == "zero":
+            continue
+        ms = lib.tlg_event_elapsed_ms(ev[2 * i], ev[2 * i + 1]) / reps
+        name, splits = lib.kernel_name(c["op"], c["M"], c["K"], c["N"])
+        g = groups.setdefault(name, dict(launches=0, ms=0.0, flops=0.0, bytes=0.0, shapes=set()))
+        M, K, N = c["M"], c["K"], c["N"]
+        g["launches"] += 1
+        g["ms"] += ms
+        g["flops"] += 2.0 * M * K * N
+        acc = c["op"] != "mm"
+        out = M * N if c["op"] == "mm" else (M * K if c["op"] == "mm_bt" else K * N)
+        ins = {"mm": M * K + K * N, "mm_bt": M * N + K * N, "mm_atb": M * K + M * N}[c["op"]]
+        g["bytes"] += 4.0 * (ins + out * (2 if acc else 1))
+        g["shapes"].add(f"{c['op']}({M},{K},{N})x{splits}")
+    for e in ev:
+        lib.tlg_event_destroy(e)
+    return groups
+
+
+def read_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed PMC summary
+    (profiles/traffic_m3.txt: FETCH_SIZE + WRITE_SIZE per dispatch, scaled by
+    the copy-kernel calibration), or None if not measured."""
+    path = os.path.join(REPO, "profiles", "traffic_m3.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = line.strip().split("\t")
+        if len(parts) >= 2 and parts[0] == kernel:
+            try:
+                return float(parts[1])
+            except ValueError:
+                return None
+    return None
+
+
+def bench_decode(lib, host, stream, steps, M=1, pool=6):
+    """cfg3: per token 8 layers x 7 GEMVs + unembed at M rows; the weights
+    (52.7 MB) rotate through `pool` copies (> 256 MB Infinity Cache)."""
+    plan = host.plan_decode(M, **DECODE)
+    run = host.dll.tl_run_new(ctypes.byref(plan.raw), pool)
+    if not run:
+        raise RuntimeError("tl_run_new(decode) failed")
+    check(host.dll.tl_run_fill(run, 7, stream), "fill")
+    check(host.dll.tl_run_graph_build(run, stream), "graph")
+    step = lambda: host.dll.tl_run_graph_step(run, stream)  # noqa: E731
+    for _ in range(2 * pool):
+        check(step(), "decode warmup")
+    ms, _ = time_steps(lib, step, stream, steps)
+    wbytes = sum(4.0 * c["K"] * c["N"] for c in plan.calls if c["op"] != "zero")
+    allbytes = sum(4.0 * (c["M"] * c["K"] + c["K"] * c["N"] + c["M"] * c["N"] * (2 if c["op"] != "mm" else 1))
+                   for c in plan.calls if c["op"] != "zero")
+    per_tok_ms = ms / steps
+    host.dll.tl_run_free(run)
+    return {
+        "rows": M, "steps": steps, "us_per_token": round(per_tok_ms * 1e3, 3),
+        "tok_s": round(M * 1e3 / per_tok_ms, 1),
+        "weight_bytes_per_token": int(wbytes),
+        "hbm_gbs": round(allbytes / (per_tok_ms * 1e-3) / 1e9, 1),
+        "hbm_frac": round(allbytes / (per_tok_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "gemv_launches_per_token": sum(1 for c in plan.calls if c["op"] != "zero"),
+        "weight_pool_copies": pool,
+    }
+
+
+def cpu_baseline(host, cfgname, steps, threads):
+    """The reference's own mm / mm_bt / mm_atb (oracle/_ref, compiled from
+    tinylm.c) running the same plan on host cores; falls back to the
+    fixture-pinned restatement (kind "port") when _ref is absent."""
+    import numpy as np
+    import oracle
+    try:
+        prims, kind = oracle.Reference(), "reference"
+    except FileNotFoundError:
+        prims, kind = oracle.Oracle(), "port"
+    prims.set_threads(threads)
+    cfg = TRAIN[cfgname]
+    plan = host.plan_train(**cfg)
+    rng = np.random.default_rng(5)
+    scale = {0: 1.0, 1: 0.02, 2: 0.01, 3: 0.0}
+    arrays = {}
+    for name, n, init in plan.bufs:
+        a = rng.standard_normal(n, dtype=np.float32) if init != 3 else np.zeros(n, np.float32)
+        if init != 3:
+            a *= np.float32(scale[init])
+        arrays[name] = a
+    oracle.run_plan_cpu(plan, arrays, prims)           # warmup
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        oracle.run_plan_cpu(plan, arrays, prims)
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(cfg["R"] * steps / dt, 1), "unit": "train tokens/s (GEMM set only)",
+        "cores": threads, "kind": kind,
+        "sample": f"{steps} full {cfgname} GEMM-set steps ({sum(1 for c in plan.calls if c['op'] != 'zero')} "
+                  f"calls each) after 1 warmup, OpenMP static, {threads} threads, gcc -O3 -ffast-math "
+                  f"-funroll-loops -march=x86-64-v3; {dt:.1f} s timed",
+        "s_per_step": round(dt / steps, 4),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="m3", choices=sorted(TRAIN))
+    ap.add_argument("--eager", action="store_true", help="launch calls one by one instead of a HIP graph")
+    ap.add_argument("--census-reps", type=int, default=5)
+    ap.add_argument("--decode-steps", type=int, default=512)
+    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
+              "(the path would shard M across GPUs with one all-reduce of dW; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import tlgemm
+    lib = tlgemm.load()
+    check(lib.tlg_init(0), "tlg_init")
+    host = tlgemm.host()
+    cfg = TRAIN[args.config]
+    plan = host.plan_train(**cfg)
+    run = host.dll.tl_run_new(ctypes.byref(plan.raw), 1)
+    if not run:
+        raise RuntimeError("tl_run_new failed: " + lib.tlg_last_error().decode())
+    stream = lib.tlg_stream_create()
+    check(host.dll.tl_run_fill(run, 1234567891011, stream), "fill")
+    if args.eager:
+        step = lambda: host.dll.tl_run_step(run, stream)  # noqa: E731
+    else:
+        check(host.dll.tl_run_graph_build(run, stream), "graph build")
+        step = lambda: host.dll.tl_run_graph_step(run, stream)  # noqa: E731
+    log(f"[bench] {args.config}: {len(plan.calls)} calls/step, {plan.flops() / 1e9:.2f} GFLOP/step; "
+        f"warmup {args.warmup}")
+    for _ in range(args.warmup):
+        check(step(), "warmup")
+    check(lib.tlg_stream_sync(stream), "sync")
+    ms, wall = time_steps(lib, step, stream, args.steps)
+    ms_step = ms / args.steps
+    tok_s = cfg["R"] * args.steps / (ms / 1e3)
+    tflops = plan.flops() / (ms_step / 1e3) / 1e12
+    log(f"[bench] timed {args.steps} steps: {ms_step:.4f} ms/step (wall {wall / args.steps * 1e3:.4f}), "
+        f"{tok_s:,.0f} tok/s, {tflops:.1f} TFLOP/s")
+
+    # summed per-GEMM roofline time of the step: max(flops/peak, bytes/HBM)
+    roof_ms = 0.0
+    for c in plan.calls:
+        if c["op"] == "zero":
+            roof_ms += 4.0 * c["n"] / (PEAK_HBM_GBS * 1e9) * 1e3
+            continue
+        M, K, N = c["M"], c["K"], c["N"]
+        fl = 2.0 * M * K * N
+        out = M * N if c["op"] == "mm" else (M * K if c["op"] == "mm_bt" else K * N)
+        ins = {"mm": M * K + K * N, "mm_bt": M * N + K * N, "mm_atb": M * K + M * N}[c["op"]]
+        by = 4.0 * (ins + out * (1 if c["op"] == "mm" else 2))
+        roof_ms += max(fl / (PEAK_FP32_MFMA_TFLOPS * 1e12), by / (PEAK_HBM_GBS * 1e9)) * 1e3
+
+    groups = kernel_census(lib, host, plan, run, stream, args.census_reps)
+    dom_name, dom = max(groups.items(), key=lambda kv: kv[1]["ms"])
+    bound = roofline_class(dom["flops"], dom["bytes"])
+    avg_ms = dom["ms"] / dom["launches"]
+    if bound == "mfma":
+        achieved = dom["flops"] / dom["launches"] / (avg_ms / 1e3) / 1e12
+        peak, unit = PEAK_FP32_MFMA_TFLOPS, "TFLOP/s"
+    else:
+        achieved = dom["bytes"] / dom["launches"] / (avg_ms / 1e3) / 1e9
+        peak, unit = PEAK_HBM_GBS, "GB/s"
+    census = {k: {"launches": v["launches"], "avg_us": round(v["ms"] / v["launches"] * 1e3, 3),
+                  "share": round(v["ms"] / sum(g["ms"] for g in groups.values()), 4),
+                  "tflops": round(v["flops"] / (v["ms"] / 1e3) / 1e12, 2),
+                  "shapes": sorted(v["shapes"])} for k, v in groups.items()}
+    for k, v in sorted(census.items(), key=lambda kv: -kv[1]["share"]):
+        log(f"[census] {k}: {v['launches']} launches avg {v['avg_us']} us, share {v['share']}, "
+            f"{v['tflops']} TFLOP/s")
+
+    decode = None
+    if args.decode_steps > 0:
+        decode = bench_decode(lib, host, stream, args.decode_steps)
+        log(f"[decode] M=1: {decode}")
+
+    cpu = None
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        log(f"[cpu] timing the reference kernels on {threads} threads ...")
+        cpu = cpu_baseline(host, args.config, args.cpu_steps, threads)
+        log(f"[cpu] {cpu}")
+
+    host.dll.tl_run_free(run)
+    result = {
+        "metric": "train tokens/s (m3-scale); GEMM TFLOP/s & % roofline; M=1 decode tok/s",
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: seeded Gaussian activations/weights/gradients resident in HBM",
+        "config": {
+            "workload": f"BASELINE {args.config} training-step GEMM set: {len(plan.calls)} calls "
+                        f"(tinylm.c forward/backward order), {plan.flops() / 1e9:.2f} GFLOP/step, "
+                        f"{'eager launches' if args.eager else 'one HIP graph per step'}",
+            "rows": cfg["R"], "d_model": cfg["D"], "kv_dim": cfg["KD"], "ffn": cfg["F"],
+            "vocab": cfg["V"], "layers": cfg["L"], "mtp_heads": cfg["n_mtp"],
+            "global_batch": cfg["R"] // 256, "seq_len": 256, "parallelism": "single GPU",
+        },
+        "tflops": round(tflops, 2),
+        "step_roofline": {"sum_of_gemm_roof_ms": round(roof_ms, 4),
+                          "frac": round(roof_ms / ms_step, 4)},
+        "roofline": {
+            "kernel": dom_name, "bound": bound, "achieved": round(achieved, 2), "peak": peak,
+            "unit": unit, "frac": round(achieved / peak, 4),
+            "traffic": read_traffic(dom_name),
+            "launches_per_step": dom["launches"], "avg_launch_us": round(avg_ms * 1e3, 3),
+        },
+        "kernels": census,
+        "decode_m1": decode,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

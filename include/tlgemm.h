@@ -75,6 +75,48 @@ int tlg_dev_sgemm_tn_acc(float *dW, const float *X, const float *dY, int M, int 
  * accumulating GEMM, e.g. tinylm.c:1015, :1104, :1113, :1123, :1134. */
 int tlg_dev_zero(float *dst, size_t n, void *stream);
 
+/* ---- runtime wrappers for C host code ---------------------------------- */
+/* So the C step drivers (tinylm-c_amd/host) keep buffers and timing on the
+ * device without including HIP headers.  No reference counterpart. */
+void *tlg_dev_malloc(size_t bytes);                       /* NULL on failure */
+int   tlg_dev_free(void *p);
+int   tlg_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
+int   tlg_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream);
+int   tlg_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream);
+void *tlg_stream_create(void);                            /* default priority */
+int   tlg_stream_destroy(void *stream);
+int   tlg_stream_sync(void *stream);
+void *tlg_event_create(void);
+int   tlg_event_destroy(void *ev);
+int   tlg_event_record(void *ev, void *stream);
+float tlg_event_elapsed_ms(void *start, void *stop);      /* < 0 on error */
+/* dst[i] = scale * z_i, z_i ~ N(0,1) from a counter-based generator keyed by
+ * (seed, i): splitmix64 -> two uniforms -> Box-Muller.  Deterministic for a
+ * given (seed, n), independent of launch shape. */
+int   tlg_dev_fill_normal(float *dst, size_t n, unsigned long long seed, float scale, void *stream);
+/* Which kernel instance a device call of the primitive `op` (0 mm, 1 mm_bt,
+ * 2 mm_atb) with reference arguments (M, K, N) and aligned operands launches,
+ * written to buf as rocprofv3 names it (e.g. "k_gemm<64, 64, 32, 2, 1, true>"),
+ * and how many workgroups share each output tile's reduction (*splits). */
+int   tlg_kernel_name(int op, int M, int K, int N, char *buf, int len, int *splits);
+/* Tuning hook: force tile configuration `cfg` (index into the kernel's tile
+ * table, -1 = automatic choice) and `splits` reduction splits for every
+ * following GEMM launch.  For sweeps only; results stay exact either way. */
+int   tlg_tune_force(int cfg, int splits);
+/* Measurement probes (no reference counterpart).  tlg_dev_copy: dst = src,
+ * n floats (n % 4 == 0, 16-byte aligned) -- achievable HBM bandwidth and the
+ * calibration kernel for HBM byte counters.  tlg_dev_mfma_peak: `blocks`
+ * workgroups of 4 waves each issue 4*iters register-only fp32 MFMAs
+ * (32x32x2, 4096 flop each) and write blocks*256 floats to out. */
+int   tlg_dev_copy(float *dst, const float *src, size_t n, void *stream);
+int   tlg_dev_mfma_peak(float *out, int blocks, int iters, void *stream);
+/* Stream capture into a HIP graph: begin, enqueue work, end -> executable
+ * graph handle; replay with tlg_graph_launch. */
+int   tlg_graph_begin(void *stream);
+void *tlg_graph_end(void *stream);
+int   tlg_graph_launch(void *graph, void *stream);
+int   tlg_graph_destroy(void *graph);
+
 #ifdef __cplusplus
 }
 #endif

@@ -206,3 +206,70 @@ def normwise_rel(got, ref):
     if den == 0.0:
         return float(num)
     return float(num / den)
+
+
+def reference_train_log(B, T, D, H, KV, F, V, L, n_mtp, path=os.path.join(HERE, "_ref", "libtlref_seq.so")):
+    """GEMM call list of the reference's own forward + backward (tinylm.c:968-1154),
+    from _ref/libtlref_seq.so: list of (op, (out, off), (a, off), (b, off), M, K, N)
+    with buffers named after tinylm.c's P / G / Acts fields."""
+    d = ctypes.CDLL(path)
+    d.tlref_train_log.argtypes = [_i] * 9 + [ctypes.POINTER(ctypes.c_longlong), _i]
+    d.tlref_train_log.restype = _i
+    d.tlref_seq_name.argtypes = [_i]
+    d.tlref_seq_name.restype = ctypes.c_char_p
+    cap = 4096
+    buf = (ctypes.c_longlong * (10 * cap))()
+    n = d.tlref_train_log(B, T, D, H, KV, F, V, L, n_mtp, buf, cap)
+    ops = {0: "mm", 1: "mm_bt", 2: "mm_atb"}
+    name = lambda i: d.tlref_seq_name(int(i)).decode()  # noqa: E731
+    out = []
+    for i in range(n):
+        o = buf[10 * i:10 * i + 10]
+        out.append((ops[o[0]], (name(o[1]), o[2]), (name(o[3]), o[4]), (name(o[5]), o[6]), o[7], o[8], o[9]))
+    return out
+
+
+def run_plan_cpu(plan, arrays, prims):
+    """Execute a plan's calls (tlgemm.Plan.calls) on the CPU.
+
+    `arrays` maps buffer name -> flat float32 numpy array; `prims` is an
+    Oracle (the restatement) or a Reference (the reference's own kernels).
+    Each call gets row-major views at the plan's offsets, exactly the
+    operands the device executor hands the HIP kernels."""
+    names = [b[0] for b in plan.bufs]
+
+    def view(name, off, rows, cols):
+        return arrays[name][off:off + rows * cols].reshape(rows, cols)
+
+    for c in plan.calls:
+        out = names[c["out"]]
+        if c["op"] == "zero":
+            arrays[out][c["out_off"]:c["out_off"] + c["n"]] = 0.0
+            continue
+        M, K, N = c["M"], c["K"], c["N"]
+        a, b = names[c["a"]], names[c["b"]]
+        if c["op"] == "mm":
+            prims.mm(view(a, c["a_off"], M, K), view(b, c["b_off"], K, N), view(out, c["out_off"], M, N))
+        elif c["op"] == "mm_bt":
+            prims.mm_bt(view(out, c["out_off"], M, K), view(a, c["a_off"], M, N), view(b, c["b_off"], K, N))
+        else:
+            prims.mm_atb(view(out, c["out_off"], K, N), view(a, c["a_off"], M, K), view(b, c["b_off"], M, N))
+
+
+class F64Prims:
+    """mm / mm_bt / mm_atb with the fp64 textbook sums (orc_*_f64), usable by
+    run_plan_cpu to execute a whole plan in double precision."""
+
+    def __init__(self, orc):
+        self.o = orc
+
+    def mm(self, X, W, Y):
+        M, K = X.shape
+        self.o.dll.orc_mm_f64(_f(Y), _f(X), _f(W), M, K, W.shape[1])
+        return Y
+
+    def mm_bt(self, dX, dY, W):
+        return self.o.mm_bt_f64(dX, dY, W)
+
+    def mm_atb(self, dW, X, dY):
+        return self.o.mm_atb_f64(dW, X, dY)

@@ -110,6 +110,17 @@ def rng_case(ref, seed):
     np.savez(os.path.join(HERE, "rng_normal.npz"), seed=seed, z=z)
 
 
+def seq_case(name, B, T, D, H, KV, F, V, L, n_mtp):
+    """GEMM call list of the reference's own forward + backward (compiled from
+    tinylm.c:539-1154 with logged call sites, oracle/Makefile)."""
+    import json
+    from oracle import reference_train_log
+    log = reference_train_log(B, T, D, H, KV, F, V, L, n_mtp)
+    json.dump({"B": B, "T": T, "D": D, "H": H, "KV": KV, "F": F, "V": V, "L": L, "n_mtp": n_mtp,
+               "calls": [[op, list(o), list(a), list(b), M, K, N] for op, o, a, b, M, K, N in log]},
+              open(os.path.join(HERE, f"seq_{name}.json"), "w"))
+
+
 def main():
     if not os.path.isdir("/root/reference"):
         sys.exit("make_golden.py needs /root/reference (build container only)")
@@ -121,6 +132,8 @@ def main():
     moe_case(ref, "n96_d32_f48_e4", 96, 32, 48, 4, 31337)
     moe_case(ref, "tie_n64_d16_f24_e4", 64, 16, 24, 4, 4242, tie=True)
     rng_case(ref, 1234567891011)
+    seq_case("train_l2_mtp2", 2, 16, 32, 4, 1, 48, 64, 2, 2)
+    seq_case("train_l3", 1, 24, 48, 6, 2, 40, 96, 3, 0)
     print("fixtures written to", HERE)
 
 

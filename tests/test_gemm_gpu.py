@@ -220,3 +220,23 @@ def test_host_registry_device_residency(lib, orc):
     finally:
         lib.check(lib.tlg_unregister(buf.ctypes.data), "unregister")
     assert lib.tlg_mirror(buf.ctypes.data) is None
+
+
+@pytest.mark.parametrize("cfg", range(6))
+def test_every_tile_config(lib, orc, cfg):
+    """Each instantiated tile shape, with and without a split reduction, on a
+    ragged shape (scalar staging) and an aligned one (float4 staging)."""
+    try:
+        for splits in (1, 3):
+            lib.check(lib.tlg_tune_force(cfg, splits), "force")
+            for M, K, N in ((201, 131, 259), (256, 160, 192)):
+                X = seeded((M, K), 1.0, "X")
+                W = seeded((K, N), 0.02, "W")
+                dY = seeded((M, N), 0.01, "dY")
+                P1 = seeded((M, K), 1.0, "P1")
+                P2 = seeded((K, N), 0.02, "P2")
+                assert normwise_rel(run_mm(lib, X, W), orc.mm_f64(X, W)) <= TOL
+                assert normwise_rel(run_mm_bt(lib, P1, dY, W), orc.mm_bt_f64(P1.copy(), dY, W)) <= TOL
+                assert normwise_rel(run_mm_atb(lib, P2, X, dY), orc.mm_atb_f64(P2.copy(), X, dY)) <= TOL
+    finally:
+        lib.check(lib.tlg_tune_force(-1, 0), "auto")

@@ -1,0 +1,130 @@
+"""GPU parity of whole GEMM steps: the plan executor (C, libtlhost.so) runs a
+step's calls on device-resident buffers through libtlgemm; the CPU oracle runs
+the same calls on copies of the same initial buffers; every buffer must agree
+to the north_star bar (max|err| / mean|ref| <= 1e-4).  Also: HIP-graph replays
+equal eager launches bit for bit, replay after replay."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import bench
+import tlgemm
+from oracle import F64Prims, normwise_rel, run_plan_cpu
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def snapshot(lib, host, plan, run, stream):
+    out = {}
+    for i, (name, n, _) in enumerate(plan.bufs):
+        a = np.empty(n, np.float32)
+        ptr = host.dll.tl_run_buf(run, i)
+        lib.check(lib.tlg_memcpy_d2h(a.ctypes.data, ptr, a.nbytes, stream), "d2h")
+        out[name] = a
+    lib.check(lib.tlg_stream_sync(stream), "sync")
+    return out
+
+
+def new_run(lib, host, plan, pool=1, seed=99):
+    stream = lib.tlg_stream_create()
+    run = host.dll.tl_run_new(ctypes.byref(plan.raw), pool)
+    assert run, lib.tlg_last_error()
+    lib.check(host.dll.tl_run_fill(run, seed, stream), "fill")
+    return run, stream
+
+
+@pytest.mark.parametrize("name", ["nano", "m3", "m8"])
+def test_train_step_matches_oracle(lib, orc, name):
+    host = tlgemm.host()
+    plan = host.plan_train(**bench.TRAIN[name])
+    print("train step", name, len(plan.calls), "calls", flush=True)
+    run, stream = new_run(lib, host, plan)
+    try:
+        init = snapshot(lib, host, plan, run, stream)
+        lib.check(host.dll.tl_run_step(run, stream), "step")
+        got = snapshot(lib, host, plan, run, stream)
+    finally:
+        host.dll.tl_run_free(run)
+    f64 = {k: v.copy() for k, v in init.items()}
+    orc.set_threads(16)
+    run_plan_cpu(plan, init, orc)            # the reference arithmetic
+    run_plan_cpu(plan, f64, F64Prims(orc))   # textbook sums in double
+    worst = []
+    for bname, _, _ in plan.bufs:
+        for label, a, b in plan.regions(bname):
+            e_ref = normwise_rel(got[bname][a:b], init[bname][a:b])
+            e_64 = normwise_rel(got[bname][a:b], f64[bname][a:b])
+            ref_64 = normwise_rel(init[bname][a:b], f64[bname][a:b])
+            worst.append((e_ref, e_64, ref_64, label))
+    worst.sort(reverse=True)
+    print("worst regions (gpu-vs-ref, gpu-vs-fp64, ref-vs-fp64):",
+          [(f"{a:.2e}", f"{b:.2e}", f"{c:.2e}", lab) for a, b, c, lab in worst[:4]], flush=True)
+    for e_ref, e_64, _, label in worst:
+        assert e_ref <= TOL, f"{name}: {label} vs reference arithmetic {e_ref:.3e}"
+        assert e_64 <= TOL, f"{name}: {label} vs fp64 {e_64:.3e}"
+
+
+def test_graph_replays_match_eager(lib):
+    """Replay a captured step several times with eager work (re-fills) in
+    between; each replay must equal the eager step bit for bit."""
+    host = tlgemm.host()
+    plan = host.plan_train(**bench.TRAIN["nano"])
+    run, stream = new_run(lib, host, plan, seed=5)
+    try:
+        lib.check(host.dll.tl_run_step(run, stream), "eager")
+        eager = snapshot(lib, host, plan, run, stream)
+        lib.check(host.dll.tl_run_graph_build(run, stream), "graph")
+        for rep in range(3):
+            lib.check(host.dll.tl_run_fill(run, 5, stream), "refill")
+            lib.check(host.dll.tl_run_graph_step(run, stream), "replay")
+            got = snapshot(lib, host, plan, run, stream)
+            for bname, _, _ in plan.bufs:
+                assert np.array_equal(got[bname], eager[bname]), f"replay {rep}: {bname}"
+    finally:
+        host.dll.tl_run_free(run)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+def test_decode_step_matches_oracle(lib, orc, M):
+    host = tlgemm.host()
+    plan = host.plan_decode(M, **bench.DECODE)
+    run, stream = new_run(lib, host, plan, pool=2, seed=3)
+    try:
+        init = snapshot(lib, host, plan, run, stream)
+        lib.check(host.dll.tl_run_graph_build(run, stream), "graph")
+        for _ in range(2):                                # both pool copies
+            lib.check(host.dll.tl_run_graph_step(run, stream), "step")
+        got = snapshot(lib, host, plan, run, stream)
+    finally:
+        host.dll.tl_run_free(run)
+    orc.set_pool(7)                                       # decode dispatch rule
+    try:
+        run_plan_cpu(plan, init, orc)
+    finally:
+        orc.set_pool(1)
+    for bname, _, _ in plan.bufs:
+        assert normwise_rel(got[bname], init[bname]) <= TOL, bname
+
+
+def test_use_hip_seam(lib, orc):
+    """mm / mm_bt / mm_atb with tinylm.c's exact signatures (libtlhost.so,
+    built -DUSE_HIP) on host buffers."""
+    host = tlgemm.host()
+    r = np.random.default_rng(8)
+    M, K, N = 257, 96, 130
+    X = r.standard_normal((M, K), dtype=np.float32)
+    W = (0.02 * r.standard_normal((K, N))).astype(np.float32)
+    dY = (0.01 * r.standard_normal((M, N))).astype(np.float32)
+    Y = np.full((M, N), np.nan, np.float32)
+    host.dll.mm(Y.ctypes.data, X.ctypes.data, W.ctypes.data, M, K, N)
+    assert normwise_rel(Y, orc.mm(X, W)) <= TOL
+    dX = r.standard_normal((M, K), dtype=np.float32)
+    ref = orc.mm_bt(dX.copy(), dY, W)
+    host.dll.mm_bt(dX.ctypes.data, dY.ctypes.data, W.ctypes.data, M, K, N)
+    assert normwise_rel(dX, ref) <= TOL
+    dW = r.standard_normal((K, N), dtype=np.float32)
+    ref = orc.mm_atb(dW.copy(), X, dY)
+    host.dll.mm_atb(dW.ctypes.data, X.ctypes.data, dY.ctypes.data, M, K, N)
+    assert normwise_rel(dW, ref) <= TOL

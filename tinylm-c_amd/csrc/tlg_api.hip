@@ -9,16 +9,15 @@
 #include <stdlib.h>
 #include <string.h>
 
-TlgState g_tlg = {0, 0, nullptr, nullptr, 0, nullptr, 0};
+TlgState g_tlg = {0, 0, nullptr, nullptr, 0};
 
 static thread_local char t_err[512];
 static std::recursive_mutex g_mu;
 
-// Workspace for split reductions: partial tiles (64 MiB) and one arrival
-// counter per output tile.  Sized for the largest split plan the launcher
-// makes on the BASELINE shapes; a bigger plan falls back to splits = 1.
+// Workspace for split reductions (64 MiB of partial sums): sized for the
+// largest split plan the launcher makes on the BASELINE shapes; a bigger plan
+// falls back to splits = 1.
 static const size_t kWsFloats = (size_t)16 << 20;
-static const size_t kCounters = 1 << 16;
 
 int tlg_fail(int code, const char *fmt, ...)
 {
@@ -49,11 +48,6 @@ static int init_locked(int device)
         return tlg_fail(TLG_ENOMEM, "tlg_init: workspace of %zu bytes", kWsFloats * sizeof(float));
     g_tlg.ws = (float *)p;
     g_tlg.ws_floats = kWsFloats;
-    if (hipMalloc(&p, kCounters * sizeof(unsigned int)) != hipSuccess)
-        return tlg_fail(TLG_ENOMEM, "tlg_init: tile counters");
-    g_tlg.cnt = (unsigned int *)p;
-    g_tlg.cnt_n = kCounters;
-    TLG_HIP(hipMemset(g_tlg.cnt, 0, kCounters * sizeof(unsigned int)));
     TLG_HIP(hipDeviceSynchronize());
     g_tlg.device = device;
     g_tlg.initialised = 1;
@@ -152,9 +146,8 @@ extern "C" void tlg_shutdown(void)
     g_mirrors.clear();
     tlg_shutdown_impl();
     (void)hipFree(g_tlg.ws);
-    (void)hipFree(g_tlg.cnt);
     (void)hipStreamDestroy(g_tlg.stream);
-    g_tlg = TlgState{0, 0, nullptr, nullptr, 0, nullptr, 0};
+    g_tlg = TlgState{0, 0, nullptr, nullptr, 0};
 }
 
 // ------------------------------------------------ host-pointer drop-ins --
@@ -271,4 +264,95 @@ extern "C" int tlg_dev_zero(float *dst, size_t n, void *stream)
     int rc = tlg_ensure_init();
     if (rc) return rc;
     return tlg_zero_launch(dst, n, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------- runtime wrappers --
+extern "C" void *tlg_dev_malloc(size_t bytes)
+{
+    if (tlg_ensure_init()) return nullptr;
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) {
+        tlg_fail(TLG_ENOMEM, "tlg_dev_malloc: %zu bytes", bytes);
+        return nullptr;
+    }
+    return p;
+}
+extern "C" int tlg_dev_free(void *p) { TLG_HIP(hipFree(p)); return TLG_OK; }
+extern "C" int tlg_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream)
+{ TLG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream)); return TLG_OK; }
+extern "C" int tlg_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream)
+{ TLG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream)); return TLG_OK; }
+extern "C" int tlg_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream)
+{ TLG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream)); return TLG_OK; }
+extern "C" void *tlg_stream_create(void)
+{
+    if (tlg_ensure_init()) return nullptr;
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    return s;
+}
+extern "C" int tlg_stream_destroy(void *s) { TLG_HIP(hipStreamDestroy((hipStream_t)s)); return TLG_OK; }
+extern "C" int tlg_stream_sync(void *s) { TLG_HIP(hipStreamSynchronize((hipStream_t)s)); return TLG_OK; }
+extern "C" void *tlg_event_create(void)
+{
+    if (tlg_ensure_init()) return nullptr;
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+extern "C" int tlg_event_destroy(void *e) { TLG_HIP(hipEventDestroy((hipEvent_t)e)); return TLG_OK; }
+extern "C" int tlg_event_record(void *e, void *s) { TLG_HIP(hipEventRecord((hipEvent_t)e, (hipStream_t)s)); return TLG_OK; }
+extern "C" float tlg_event_elapsed_ms(void *a, void *b)
+{
+    float ms = -1.f;
+    hipError_t e = hipEventElapsedTime(&ms, (hipEvent_t)a, (hipEvent_t)b);
+    if (e != hipSuccess) { tlg_fail_hip(e, "hipEventElapsedTime", __FILE__, __LINE__); return -1.f; }
+    return ms;
+}
+extern "C" int tlg_graph_begin(void *s)
+{ TLG_HIP(hipStreamBeginCapture((hipStream_t)s, hipStreamCaptureModeThreadLocal)); return TLG_OK; }
+extern "C" void *tlg_graph_end(void *s)
+{
+    hipGraph_t g = nullptr;
+    hipGraphExec_t x = nullptr;
+    hipError_t e = hipStreamEndCapture((hipStream_t)s, &g);
+    if (e != hipSuccess) { tlg_fail_hip(e, "hipStreamEndCapture", __FILE__, __LINE__); return nullptr; }
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) { tlg_fail_hip(e, "hipGraphInstantiate", __FILE__, __LINE__); return nullptr; }
+    return x;
+}
+extern "C" int tlg_graph_launch(void *g, void *s) { TLG_HIP(hipGraphLaunch((hipGraphExec_t)g, (hipStream_t)s)); return TLG_OK; }
+extern "C" int tlg_graph_destroy(void *g) { TLG_HIP(hipGraphExecDestroy((hipGraphExec_t)g)); return TLG_OK; }
+
+int tlg_fill_normal_launch(float *dst, size_t n, unsigned long long seed, float scale, hipStream_t st);
+extern "C" int tlg_dev_fill_normal(float *dst, size_t n, unsigned long long seed, float scale, void *stream)
+{
+    int rc = tlg_ensure_init();
+    if (rc) return rc;
+    return tlg_fill_normal_launch(dst, n, seed, scale, (hipStream_t)stream);
+}
+
+extern "C" int tlg_kernel_name(int op, int M, int K, int N, char *buf, int len, int *splits)
+{
+    if (!buf || len <= 0) return tlg_fail(TLG_EINVAL, "tlg_kernel_name: no buffer");
+    switch (op) {
+    case 0: return tlg_describe(TLG_NN, M, N, K, buf, len, splits);
+    case 1: return tlg_describe(TLG_NT, M, K, N, buf, len, splits);
+    case 2: return tlg_describe(TLG_TN, K, N, M, buf, len, splits);
+    default: return tlg_fail(TLG_EINVAL, "tlg_kernel_name: op %d", op);
+    }
+}
+
+int tlg_copy_launch(float *dst, const float *src, size_t n, hipStream_t st);
+int tlg_mfma_peak_launch(float *out, int blocks, int iters, hipStream_t st);
+extern "C" int tlg_dev_copy(float *dst, const float *src, size_t n, void *stream)
+{
+    int rc = tlg_ensure_init();
+    return rc ? rc : tlg_copy_launch(dst, src, n, (hipStream_t)stream);
+}
+extern "C" int tlg_dev_mfma_peak(float *out, int blocks, int iters, void *stream)
+{
+    int rc = tlg_ensure_init();
+    return rc ? rc : tlg_mfma_peak_launch(out, blocks, iters, (hipStream_t)stream);
 }

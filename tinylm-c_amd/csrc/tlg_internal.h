@@ -22,8 +22,6 @@ struct TlgState {
     hipStream_t stream;        // default stream for the host-pointer entries
     float *ws;                 // split-reduction partials
     size_t ws_floats;
-    unsigned int *cnt;         // per-tile arrival counters (kept at zero between launches)
-    size_t cnt_n;
 };
 extern TlgState g_tlg;
 int tlg_ensure_init(void);
@@ -40,3 +38,4 @@ int tlg_gemm_launch(TlgKind kind, const float *A, const float *B, float *C,
                     int Mo, int No, int R, int lda, int ldb, int ldc, int beta,
                     hipStream_t st);
 int tlg_zero_launch(float *dst, size_t n, hipStream_t st);
+int tlg_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len, int *splits);

@@ -37,6 +37,27 @@ SIGNATURES = {
     "tlg_dev_sgemm_nt_acc": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "tlg_dev_sgemm_tn_acc": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "tlg_dev_zero": (_i, [_vp, _sz, _vp]),
+    "tlg_dev_malloc": (_vp, [_sz]),
+    "tlg_dev_free": (_i, [_vp]),
+    "tlg_memcpy_h2d": (_i, [_vp, _vp, _sz, _vp]),
+    "tlg_memcpy_d2h": (_i, [_vp, _vp, _sz, _vp]),
+    "tlg_memcpy_d2d": (_i, [_vp, _vp, _sz, _vp]),
+    "tlg_stream_create": (_vp, []),
+    "tlg_stream_destroy": (_i, [_vp]),
+    "tlg_stream_sync": (_i, [_vp]),
+    "tlg_event_create": (_vp, []),
+    "tlg_event_destroy": (_i, [_vp]),
+    "tlg_event_record": (_i, [_vp, _vp]),
+    "tlg_event_elapsed_ms": (ctypes.c_float, [_vp, _vp]),
+    "tlg_dev_fill_normal": (_i, [_vp, _sz, ctypes.c_ulonglong, ctypes.c_float, _vp]),
+    "tlg_kernel_name": (_i, [_i, _i, _i, _i, ctypes.c_char_p, _i, _ip]),
+    "tlg_tune_force": (_i, [_i, _i]),
+    "tlg_dev_copy": (_i, [_vp, _vp, _sz, _vp]),
+    "tlg_dev_mfma_peak": (_i, [_vp, _i, _i, _vp]),
+    "tlg_graph_begin": (_i, [_vp]),
+    "tlg_graph_end": (_vp, [_vp]),
+    "tlg_graph_launch": (_i, [_vp, _vp]),
+    "tlg_graph_destroy": (_i, [_vp]),
 }
 
 
@@ -87,6 +108,14 @@ class Lib:
     def zero(self, p, n, stream=0):
         return self.check(self.dll.tlg_dev_zero(p, n, stream), "tlg_dev_zero")
 
+    def kernel_name(self, op, M, K, N):
+        """(rocprof kernel name, splits) a device call of op 'mm'/'mm_bt'/'mm_atb' uses."""
+        buf = ctypes.create_string_buffer(128)
+        sp = ctypes.c_int(0)
+        code = {"mm": 0, "mm_bt": 1, "mm_atb": 2}[op]
+        self.check(self.dll.tlg_kernel_name(code, M, K, N, buf, 128, ctypes.byref(sp)), "tlg_kernel_name")
+        return buf.value.decode(), sp.value
+
 
 _LIB = None
 
@@ -96,3 +125,142 @@ def load():
     if _LIB is None:
         _LIB = Lib()
     return _LIB
+
+
+# ----------------------------------------------------------- host library --
+HOST_PATH = os.path.join(HERE, "libtlhost.so")
+HOST_HEADER = os.path.join(HERE, "host", "tl_plan.h")
+OPS = {0: "mm", 1: "mm_bt", 2: "mm_atb", 3: "zero"}
+
+
+class TlBuf(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 16), ("floats", ctypes.c_size_t), ("init", ctypes.c_int)]
+
+
+class TlCall(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_int), ("out", ctypes.c_int), ("a", ctypes.c_int), ("b", ctypes.c_int),
+                ("out_off", ctypes.c_size_t), ("a_off", ctypes.c_size_t), ("b_off", ctypes.c_size_t),
+                ("M", ctypes.c_int), ("K", ctypes.c_int), ("N", ctypes.c_int),
+                ("n", ctypes.c_size_t), ("line", ctypes.c_int), ("what", ctypes.c_char * 16)]
+
+
+class TlPlan(ctypes.Structure):
+    _fields_ = [("nbuf", ctypes.c_int), ("ncall", ctypes.c_int), ("cap", ctypes.c_int),
+                ("buf", TlBuf * 48), ("call", ctypes.POINTER(TlCall)),
+                ("R", ctypes.c_int), ("D", ctypes.c_int), ("KD", ctypes.c_int), ("F", ctypes.c_int),
+                ("V", ctypes.c_int), ("L", ctypes.c_int), ("n_mtp", ctypes.c_int)]
+
+
+class TlWeightMap(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_size_t) for n in
+                ("emb", "an1", "wq", "wk", "wv", "wo", "an2", "w1", "w3", "w2", "nf", "mtp0", "total")]
+
+
+class Plan:
+    """A built TlPlan: buffers (name, floats, init) and calls as dicts."""
+
+    def __init__(self, host, raw):
+        self.host = host
+        self.raw = raw
+        self.bufs = [(b.name.decode(), b.floats, b.init) for b in raw.buf[:raw.nbuf]]
+        self.calls = []
+        for i in range(raw.ncall):
+            c = raw.call[i]
+            self.calls.append(dict(op=OPS[c.op], out=c.out, a=c.a, b=c.b, out_off=c.out_off,
+                                   a_off=c.a_off, b_off=c.b_off, M=c.M, K=c.K, N=c.N, n=c.n,
+                                   line=c.line, what=c.what.decode()))
+
+    def buf_id(self, name):
+        return [b[0] for b in self.bufs].index(name)
+
+    def flops(self):
+        return sum(2.0 * c["M"] * c["K"] * c["N"] for c in self.calls if c["op"] != "zero")
+
+    def regions(self, name):
+        """(label, start, end) float ranges of buffer `name` that separate GEMM
+        outputs: one per weight matrix for P/G (map_weights layout), one per
+        layer slice for the per-layer activation buffers, else the whole."""
+        r = self.raw
+        n = self.bufs[self.buf_id(name)][1]
+        if name in ("P", "G"):
+            out = []
+            for l in range(r.L):
+                m = TlWeightMap()
+                self.host.dll.tl_weight_map(r.V, r.D, r.KD, r.F, r.L, r.n_mtp, l, ctypes.byref(m))
+                if l == 0:
+                    out.append(("emb", m.emb, m.emb + r.V * r.D))
+                for w, sz in (("wq", r.D * r.D), ("wk", r.D * r.KD), ("wv", r.D * r.KD),
+                              ("wo", r.D * r.D), ("w1", r.D * r.F), ("w3", r.D * r.F), ("w2", r.F * r.D)):
+                    off = getattr(m, w)
+                    out.append((f"{w}[{l}]", off, off + sz))
+            for k in range(r.n_mtp):
+                off = m.mtp0 + k * r.D * r.D
+                out.append((f"mtp[{k}]", off, off + r.D * r.D))
+            return out
+        if self.raw.L > 1 and n % self.raw.L == 0 and name in (
+                "a_in", "a_norm", "q", "k", "v", "att_ctx", "f_in", "f_norm", "g", "u"):
+            s = n // self.raw.L
+            return [(f"{name}[{l}]", l * s, (l + 1) * s) for l in range(self.raw.L)]
+        return [(name, 0, n)]
+
+    def __del__(self):
+        try:
+            self.host.dll.tl_plan_free(ctypes.byref(self.raw))
+        except Exception:
+            pass
+
+
+class Host:
+    """libtlhost.so: the -DUSE_HIP seam (mm/mm_bt/mm_atb) and the plan executor."""
+
+    def __init__(self, path=HOST_PATH):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built; run __graft_entry__.build()")
+        d = ctypes.CDLL(path)
+        P = ctypes.POINTER(TlPlan)
+        d.tl_plan_train.argtypes = [P] + [_i] * 7
+        d.tl_plan_train.restype = _i
+        d.tl_plan_decode.argtypes = [P] + [_i] * 6
+        d.tl_plan_decode.restype = _i
+        d.tl_weight_map.argtypes = [_i] * 7 + [ctypes.POINTER(TlWeightMap)]
+        d.tl_weight_map.restype = None
+        d.tl_plan_free.argtypes = [P]
+        d.tl_plan_free.restype = None
+        d.tl_run_new.argtypes = [P, _i]
+        d.tl_run_new.restype = _vp
+        d.tl_run_free.argtypes = [_vp]
+        d.tl_run_free.restype = None
+        d.tl_run_fill.argtypes = [_vp, ctypes.c_ulonglong, _vp]
+        d.tl_run_buf.argtypes = [_vp, _i]
+        d.tl_run_buf.restype = _vp
+        for n in ("tl_run_step", "tl_run_graph_build", "tl_run_graph_step"):
+            getattr(d, n).argtypes = [_vp, _vp]
+            getattr(d, n).restype = _i
+        d.tl_run_call.argtypes = [_vp, _i, _vp]
+        d.tl_run_call.restype = _i
+        for n in ("mm", "mm_bt", "mm_atb"):
+            getattr(d, n).argtypes = [_vp, _vp, _vp, _i, _i, _i]
+            getattr(d, n).restype = None
+        self.dll = d
+
+    def plan_train(self, R, D, KD, F, V, L, n_mtp=0):
+        raw = TlPlan()
+        if self.dll.tl_plan_train(ctypes.byref(raw), R, D, KD, F, V, L, n_mtp) != 0:
+            raise ValueError("tl_plan_train failed")
+        return Plan(self, raw)
+
+    def plan_decode(self, M, D, KD, F, V, L):
+        raw = TlPlan()
+        if self.dll.tl_plan_decode(ctypes.byref(raw), M, D, KD, F, V, L) != 0:
+            raise ValueError("tl_plan_decode failed")
+        return Plan(self, raw)
+
+
+_HOST = None
+
+
+def host():
+    global _HOST
+    if _HOST is None:
+        _HOST = Host()
+    return _HOST
