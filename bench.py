@@ -104,6 +104,40 @@ def kernel_census(lib, host, plan, run, stream, reps):
     return groups
 
 
+GROUP_KERNEL = "k_group<64, 64, 32, 2>"
+
+
+def launch_census(lib, host, run, stream, reps):
+    """Average duration of each launch of a grouped step, from HIP events the
+    executor records on the kernels' stream before every launch (reps steps),
+    summed per kernel instance."""
+    L = host.dll.tl_run_grouped_launches(run)
+    ev = [lib.tlg_event_create() for _ in range(L + 2)]
+    arr = (ctypes.c_void_p * (L + 2))(*ev)
+    dt = [0.0] * (L + 1)
+    for _ in range(reps):
+        check(host.dll.tl_run_time_launches(run, arr, L + 2, stream), "timed step")
+        check(lib.tlg_stream_sync(stream), "sync")
+        for k in range(L + 1):
+            dt[k] += lib.tlg_event_elapsed_ms(ev[k], ev[k + 1]) / reps
+    groups = {}
+    fl, by = ctypes.c_double(), ctypes.c_double()
+    for k in range(L + 1):
+        kind = host.dll.tl_run_launch_info(run, k, ctypes.byref(fl), ctypes.byref(by))
+        if kind == 2 and dt[k] < 1e-4:
+            continue                      # no split partials left: nothing launched
+        name = "k_zero" if kind == 1 else GROUP_KERNEL
+        g = groups.setdefault(name, dict(launches=0, ms=0.0, flops=0.0, bytes=0.0, shapes=set()))
+        g["launches"] += 1
+        g["ms"] += dt[k]
+        g["flops"] += fl.value
+        g["bytes"] += by.value
+        g["shapes"].add({0: "grouped GEMMs", 1: "clear", 2: "split flush"}[kind])
+    for e in ev:
+        lib.tlg_event_destroy(e)
+    return groups
+
+
 def read_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed PMC summary
     (profiles/traffic_m3.txt: FETCH_SIZE + WRITE_SIZE per dispatch, scaled by
@@ -129,7 +163,7 @@ def bench_decode(lib, host, stream, steps, M=1, pool=6):
     if not run:
         raise RuntimeError("tl_run_new(decode) failed")
     check(host.dll.tl_run_fill(run, 7, stream), "fill")
-    check(host.dll.tl_run_graph_build(run, stream), "graph")
+    check(host.dll.tl_run_graph_build(run, stream, 1), "graph")
     step = lambda: host.dll.tl_run_graph_step(run, stream)  # noqa: E731
     for _ in range(2 * pool):
         check(step(), "decode warmup")
@@ -192,7 +226,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="m3", choices=sorted(TRAIN))
-    ap.add_argument("--eager", action="store_true", help="launch calls one by one instead of a HIP graph")
+    ap.add_argument("--eager", action="store_true", help="enqueue each step directly instead of replaying a HIP graph")
+    ap.add_argument("--calls", action="store_true",
+                    help="one launch per reference call instead of one grouped launch per GEMM run")
     ap.add_argument("--census-reps", type=int, default=5)
     ap.add_argument("--decode-steps", type=int, default=512)
     ap.add_argument("--cpu-steps", type=int, default=3)
@@ -216,13 +252,16 @@ def main():
         raise RuntimeError("tl_run_new failed: " + lib.tlg_last_error().decode())
     stream = lib.tlg_stream_create()
     check(host.dll.tl_run_fill(run, 1234567891011, stream), "fill")
+    grouped = 0 if args.calls else 1
+    launches = host.dll.tl_run_grouped_launches(run) if grouped else None
     if args.eager:
-        step = lambda: host.dll.tl_run_step(run, stream)  # noqa: E731
+        fn = host.dll.tl_run_step_grouped if grouped else host.dll.tl_run_step
+        step = lambda: fn(run, stream)  # noqa: E731
     else:
-        check(host.dll.tl_run_graph_build(run, stream), "graph build")
+        check(host.dll.tl_run_graph_build(run, stream, grouped), "graph build")
         step = lambda: host.dll.tl_run_graph_step(run, stream)  # noqa: E731
-    log(f"[bench] {args.config}: {len(plan.calls)} calls/step, {plan.flops() / 1e9:.2f} GFLOP/step; "
-        f"warmup {args.warmup}")
+    log(f"[bench] {args.config}: {len(plan.calls)} calls/step, {plan.flops() / 1e9:.2f} GFLOP/step, "
+        f"{launches if grouped else 'one launch per call'} grouped launches; warmup {args.warmup}")
     for _ in range(args.warmup):
         check(step(), "warmup")
     check(lib.tlg_stream_sync(stream), "sync")
@@ -246,7 +285,10 @@ def main():
         by = 4.0 * (ins + out * (1 if c["op"] == "mm" else 2))
         roof_ms += max(fl / (PEAK_FP32_MFMA_TFLOPS * 1e12), by / (PEAK_HBM_GBS * 1e9)) * 1e3
 
-    groups = kernel_census(lib, host, plan, run, stream, args.census_reps)
+    if grouped:
+        groups = launch_census(lib, host, run, stream, args.census_reps)
+    else:
+        groups = kernel_census(lib, host, plan, run, stream, args.census_reps)
     dom_name, dom = max(groups.items(), key=lambda kv: kv[1]["ms"])
     bound = roofline_class(dom["flops"], dom["bytes"])
     avg_ms = dom["ms"] / dom["launches"]
@@ -293,7 +335,8 @@ def main():
         "config": {
             "workload": f"BASELINE {args.config} training-step GEMM set: {len(plan.calls)} calls "
                         f"(tinylm.c forward/backward order), {plan.flops() / 1e9:.2f} GFLOP/step, "
-                        f"{'eager launches' if args.eager else 'one HIP graph per step'}",
+                        f"{'grouped: %d launches per step' % launches if grouped else 'one launch per call'}, "
+                        f"{'enqueued directly' if args.eager else 'replayed as one HIP graph'}",
             "rows": cfg["R"], "d_model": cfg["D"], "kv_dim": cfg["KD"], "ffn": cfg["F"],
             "vocab": cfg["V"], "layers": cfg["L"], "mtp_heads": cfg["n_mtp"],
             "global_batch": cfg["R"] // 256, "seq_len": 256, "parallelism": "single GPU",

@@ -75,6 +75,39 @@ int tlg_dev_sgemm_tn_acc(float *dW, const float *X, const float *dY, int M, int 
  * accumulating GEMM, e.g. tinylm.c:1015, :1104, :1113, :1123, :1134. */
 int tlg_dev_zero(float *dst, size_t n, void *stream);
 
+/* ---- grouped launches (device pointers, asynchronous) -------------------
+ * The GEMMs a caller issues back to back with no other work in between --
+ * e.g. the Q, K and V projections of one layer (tinylm.c:981-983), or the
+ * dnorm chain and the Q/K/V weight gradients (tinylm.c:1135-1141) -- run as
+ * one kernel launch.  No reference counterpart: this is what the device step
+ * executor (tinylm-c_amd/host/tl_exec.c) uses to cut per-kernel overhead.
+ *
+ * A call is one primitive with the reference's arguments, or for mm_bt a
+ * chain of up to 3 primitives accumulating into the same dX:
+ *   dX (beta ? += : =) sum_s dY_s[M x N_s] @ W_s[K x N_s]^T
+ * (N_0 = N).  beta = 0 turns "memset(C); mm_bt(C, ...)" into one call.
+ * mm always sets.  The calls of one group must be independent (no call
+ * reads or writes what another writes).  All operands must be 16-byte
+ * aligned with row widths that are multiples of 4.
+ *
+ * mm_atb calls with long reductions split them across workgroups; their
+ * partial sums are added into C by the NEXT grouped launch on the stream
+ * (the kernel boundary makes them visible) or by tlg_dev_gemm_flush, which
+ * must be called before C is read.  Any single-call entry point flushes
+ * first.  One stream at a time may use grouped launches. */
+typedef struct {
+    int op;                  /* 0 mm, 1 mm_bt, 2 mm_atb */
+    int beta;                /* mm_bt / mm_atb: 1 add into C, 0 overwrite C */
+    float *C;                /* Y, dX or dW */
+    int M, K, N;             /* the primitive's arguments (N = N_0) */
+    int nseg;                /* 1, or 2..3 for an mm_bt chain */
+    const float *A[3];       /* X / dY_s / X  (first operand of segment s) */
+    const float *B[3];       /* W / W_s  / dY (second operand of segment s) */
+    int Nseg[3];             /* N_s for s >= 1 (mm_bt chains) */
+} TlgGemmCall;
+int tlg_dev_gemm_group(const TlgGemmCall *calls, int n, void *stream);
+int tlg_dev_gemm_flush(void *stream);
+
 /* ---- runtime wrappers for C host code ---------------------------------- */
 /* So the C step drivers (tinylm-c_amd/host) keep buffers and timing on the
  * device without including HIP headers.  No reference counterpart. */

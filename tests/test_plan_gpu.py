@@ -35,15 +35,17 @@ def new_run(lib, host, plan, pool=1, seed=99):
     return run, stream
 
 
+@pytest.mark.parametrize("grouped", [0, 1], ids=["calls", "grouped"])
 @pytest.mark.parametrize("name", ["nano", "m3", "m8"])
-def test_train_step_matches_oracle(lib, orc, name):
+def test_train_step_matches_oracle(lib, orc, name, grouped):
     host = tlgemm.host()
     plan = host.plan_train(**bench.TRAIN[name])
-    print("train step", name, len(plan.calls), "calls", flush=True)
+    print("train step", name, len(plan.calls), "calls", "grouped" if grouped else "", flush=True)
     run, stream = new_run(lib, host, plan)
     try:
         init = snapshot(lib, host, plan, run, stream)
-        lib.check(host.dll.tl_run_step(run, stream), "step")
+        step = host.dll.tl_run_step_grouped if grouped else host.dll.tl_run_step
+        lib.check(step(run, stream), "step")
         got = snapshot(lib, host, plan, run, stream)
     finally:
         host.dll.tl_run_free(run)
@@ -66,16 +68,18 @@ def test_train_step_matches_oracle(lib, orc, name):
         assert e_64 <= TOL, f"{name}: {label} vs fp64 {e_64:.3e}"
 
 
-def test_graph_replays_match_eager(lib):
+@pytest.mark.parametrize("grouped", [0, 1], ids=["calls", "grouped"])
+def test_graph_replays_match_eager(lib, grouped):
     """Replay a captured step several times with eager work (re-fills) in
     between; each replay must equal the eager step bit for bit."""
     host = tlgemm.host()
-    plan = host.plan_train(**bench.TRAIN["nano"])
+    plan = host.plan_train(**bench.TRAIN["m8"] if grouped else bench.TRAIN["nano"])
     run, stream = new_run(lib, host, plan, seed=5)
     try:
-        lib.check(host.dll.tl_run_step(run, stream), "eager")
+        step = host.dll.tl_run_step_grouped if grouped else host.dll.tl_run_step
+        lib.check(step(run, stream), "eager")
         eager = snapshot(lib, host, plan, run, stream)
-        lib.check(host.dll.tl_run_graph_build(run, stream), "graph")
+        lib.check(host.dll.tl_run_graph_build(run, stream, grouped), "graph")
         for rep in range(3):
             lib.check(host.dll.tl_run_fill(run, 5, stream), "refill")
             lib.check(host.dll.tl_run_graph_step(run, stream), "replay")
@@ -86,14 +90,15 @@ def test_graph_replays_match_eager(lib):
         host.dll.tl_run_free(run)
 
 
+@pytest.mark.parametrize("grouped", [0, 1], ids=["calls", "grouped"])
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
-def test_decode_step_matches_oracle(lib, orc, M):
+def test_decode_step_matches_oracle(lib, orc, M, grouped):
     host = tlgemm.host()
     plan = host.plan_decode(M, **bench.DECODE)
     run, stream = new_run(lib, host, plan, pool=2, seed=3)
     try:
         init = snapshot(lib, host, plan, run, stream)
-        lib.check(host.dll.tl_run_graph_build(run, stream), "graph")
+        lib.check(host.dll.tl_run_graph_build(run, stream, grouped), "graph")
         for _ in range(2):                                # both pool copies
             lib.check(host.dll.tl_run_graph_step(run, stream), "step")
         got = snapshot(lib, host, plan, run, stream)

@@ -356,3 +356,14 @@ extern "C" int tlg_dev_mfma_peak(float *out, int blocks, int iters, void *stream
     int rc = tlg_ensure_init();
     return rc ? rc : tlg_mfma_peak_launch(out, blocks, iters, (hipStream_t)stream);
 }
+
+extern "C" int tlg_dev_gemm_group(const TlgGemmCall *calls, int n, void *stream)
+{
+    if (n < 0 || (n > 0 && !calls)) return tlg_fail(TLG_EINVAL, "tlg_dev_gemm_group: bad call list");
+    return tlg_group_launch(calls, n, (hipStream_t)stream);
+}
+extern "C" int tlg_dev_gemm_flush(void *stream)
+{
+    int rc = tlg_ensure_init();
+    return rc ? rc : tlg_group_flush_launch((hipStream_t)stream);
+}

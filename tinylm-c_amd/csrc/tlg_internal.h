@@ -39,3 +39,5 @@ int tlg_gemm_launch(TlgKind kind, const float *A, const float *B, float *C,
                     hipStream_t st);
 int tlg_zero_launch(float *dst, size_t n, hipStream_t st);
 int tlg_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len, int *splits);
+int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st);
+int tlg_group_flush_launch(hipStream_t st);

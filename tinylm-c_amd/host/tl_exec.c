@@ -12,6 +12,7 @@
 #include <string.h>
 
 #define TL_MAXPOOL 16
+#define TL_MAXLAUNCH 1024
 
 struct TlRun {
     const TlPlan *plan;
@@ -21,6 +22,11 @@ struct TlRun {
     int p_id;                   /* buffer id of P (-1 if none) */
     int pool, cur;
     void *graph[TL_MAXPOOL];
+    /* optional per-launch timing of grouped steps (tl_run_time_launches) */
+    void **ev;
+    int nev;
+    double lflops[TL_MAXLAUNCH], lbytes[TL_MAXLAUNCH];
+    int lkind[TL_MAXLAUNCH];             /* 0 grouped GEMM, 1 clear, 2 flush */
 };
 
 static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -118,14 +124,232 @@ int tl_run_step(TlRun *r, void *stream)
     return 0;
 }
 
-int tl_run_graph_build(TlRun *r, void *stream)
+/* ---- grouped step ------------------------------------------------------- */
+/* Float range [lo, hi) of buffer `id` touched by an operand. */
+typedef struct { int id; size_t lo, hi; } Span;
+
+static int spans_overlap(Span a, Span b) { return a.id == b.id && a.lo < b.hi && b.lo < a.hi; }
+
+/* Output and input ranges of a GEMM call (reference argument meaning). */
+static void call_spans(const TlCall *c, Span *out, Span *a, Span *b)
+{
+    const size_t M = c->M, K = c->K, N = c->N;
+    size_t no, na, nb;
+    switch (c->op) {
+    case TL_MM:    no = M * N; na = M * K; nb = K * N; break;
+    case TL_MM_BT: no = M * K; na = M * N; nb = K * N; break;
+    default:       no = K * N; na = M * K; nb = M * N; break;
+    }
+    if (c->op == TL_ZERO) no = c->n;
+    out->id = c->out; out->lo = c->out_off; out->hi = c->out_off + no;
+    a->id = c->a; a->lo = c->a_off; a->hi = c->a_off + na;
+    b->id = c->b; b->lo = c->b_off; b->hi = c->b_off + nb;
+}
+
+#define TL_GROUP_MAX 8
+
+typedef struct {
+    TlgGemmCall call[TL_GROUP_MAX];
+    Span wr[TL_GROUP_MAX], rd[2 * TL_GROUP_MAX * 3];
+    int n, nrd;
+} Group;
+
+/* Record the event that opens launch k (timing runs only). */
+static int mark(TlRun *r, int k, void *stream)
+{
+    if (!r->ev || k >= r->nev) return 0;
+    return tlg_event_record(r->ev[k], stream);
+}
+
+static void note(TlRun *r, int k, int kind, double flops, double bytes)
+{
+    if (k >= TL_MAXLAUNCH) return;
+    r->lkind[k] = kind;
+    r->lflops[k] = flops;
+    r->lbytes[k] = bytes;
+}
+
+static double gemm_flops(const TlgGemmCall *c)
+{
+    double f = 0.0;
+    for (int s = 0; s < c->nseg; s++)
+        f += 2.0 * c->M * c->K * (double)(s ? c->Nseg[s] : c->N);
+    return f;
+}
+
+static double gemm_bytes(const TlgGemmCall *c)
+{
+    const double M = c->M, K = c->K;
+    double b = 0.0;
+    for (int s = 0; s < c->nseg; s++) {
+        const double N = s ? c->Nseg[s] : c->N;
+        if (c->op == 0) b += M * K + K * N;
+        else if (c->op == 1) b += M * N + K * N;
+        else b += M * K + M * N;
+    }
+    const double out = c->op == 0 ? M * c->N : (c->op == 1 ? M * K : K * c->N);
+    return 4.0 * (b + out * (c->beta ? 2.0 : 1.0));
+}
+
+static int group_launch(TlRun *r, Group *g, void *stream, int dry, int *launches)
+{
+    if (g->n == 0) return 0;
+    double fl = 0.0, by = 0.0;
+    for (int k = 0; k < g->n; k++) { fl += gemm_flops(&g->call[k]); by += gemm_bytes(&g->call[k]); }
+    note(r, *launches, 0, fl, by);
+    int rc = dry ? 0 : mark(r, *launches, stream);
+    if (!rc && !dry) rc = tlg_dev_gemm_group(g->call, g->n, stream);
+    (*launches)++;
+    g->n = g->nrd = 0;
+    return rc;
+}
+
+/* Does call c conflict with what group g already reads or writes? */
+static int group_conflict(const Group *g, const TlCall *c)
+{
+    Span o, a, b;
+    call_spans(c, &o, &a, &b);
+    for (int k = 0; k < g->n; k++)
+        if (spans_overlap(o, g->wr[k]) || spans_overlap(a, g->wr[k]) || spans_overlap(b, g->wr[k]))
+            return 1;
+    for (int k = 0; k < g->nrd; k++)
+        if (spans_overlap(o, g->rd[k])) return 1;
+    return 0;
+}
+
+/* Index of the first GEMM after call z (same run) that writes exactly the
+ * range z clears, accumulating, with nothing in between touching it; -1 if
+ * the clear must stay a clear. */
+static int clear_target(const TlPlan *p, int z, int end)
+{
+    Span zo, za, zb;
+    call_spans(&p->call[z], &zo, &za, &zb);
+    for (int j = z + 1; j < end; j++) {
+        const TlCall *c = &p->call[j];
+        Span o, a, b;
+        call_spans(c, &o, &a, &b);
+        if (c->op == TL_ZERO) { if (spans_overlap(o, zo)) return -1; continue; }
+        if (spans_overlap(a, zo) || spans_overlap(b, zo)) return -1;
+        if (spans_overlap(o, zo))
+            return (c->op != TL_MM && o.lo == zo.lo && o.hi == zo.hi) ? j : -1;
+    }
+    return -1;
+}
+
+static int grouped(TlRun *r, void *stream, int dry)
+{
+    const TlPlan *p = r->plan;
+    int launches = 0, rc = 0;
+    char *set = calloc((size_t)p->ncall, 1);       /* GEMM turned into a setting one */
+    char *gone = calloc((size_t)p->ncall, 1);      /* clear folded into a GEMM */
+    if (!set || !gone) { free(set); free(gone); return TLG_ENOMEM; }
+    Group g;
+    g.n = g.nrd = 0;
+    for (int i = 0; i < p->ncall && rc == 0;) {
+        int end = i;
+        while (end < p->ncall && p->call[end].run == p->call[i].run) end++;
+        for (int z = i; z < end; z++)
+            if (p->call[z].op == TL_ZERO) {
+                const int t = clear_target(p, z, end);
+                if (t >= 0) { set[t] = 1; gone[z] = 1; }
+            }
+        for (int j = i; j < end && rc == 0; j++) {
+            const TlCall *c = &p->call[j];
+            if (gone[j]) continue;
+            if (c->op == TL_ZERO) {
+                rc = group_launch(r, &g, stream, dry, &launches);
+                note(r, launches, 1, 0.0, 4.0 * (double)c->n);
+                if (!rc && !dry) rc = mark(r, launches, stream);
+                if (!rc && !dry) rc = tlg_dev_zero(ptr(r, c->out, c->out_off), c->n, stream);
+                launches++;
+                continue;
+            }
+            Span o, a, b;
+            call_spans(c, &o, &a, &b);
+            /* extend an mm_bt chain into the same dX */
+            if (g.n > 0 && c->op == TL_MM_BT && !set[j]) {
+                TlgGemmCall *last = &g.call[g.n - 1];
+                if (last->op == 1 && last->nseg < 3 && last->C == ptr(r, c->out, c->out_off) &&
+                    last->M == c->M && last->K == c->K) {
+                    int clash = 0;
+                    for (int k = 0; k < g.n; k++)
+                        if (spans_overlap(a, g.wr[k]) || spans_overlap(b, g.wr[k])) clash = 1;
+                    if (!clash) {
+                        last->A[last->nseg] = ptr(r, c->a, c->a_off);
+                        last->B[last->nseg] = ptr(r, c->b, c->b_off);
+                        last->Nseg[last->nseg] = c->N;
+                        last->nseg++;
+                        g.rd[g.nrd++] = a;
+                        g.rd[g.nrd++] = b;
+                        continue;
+                    }
+                }
+            }
+            if (g.n == TL_GROUP_MAX || group_conflict(&g, c)) rc = group_launch(r, &g, stream, dry, &launches);
+            if (rc) break;
+            TlgGemmCall *k = &g.call[g.n];
+            memset(k, 0, sizeof *k);
+            k->op = c->op;
+            k->beta = (c->op == TL_MM || set[j]) ? 0 : 1;
+            k->C = ptr(r, c->out, c->out_off);
+            k->M = c->M; k->K = c->K; k->N = c->N;
+            k->nseg = 1;
+            k->A[0] = ptr(r, c->a, c->a_off);
+            k->B[0] = ptr(r, c->b, c->b_off);
+            g.wr[g.n] = o;
+            g.rd[g.nrd++] = a;
+            g.rd[g.nrd++] = b;
+            g.n++;
+        }
+        if (!rc) rc = group_launch(r, &g, stream, dry, &launches);
+        i = end;
+    }
+    /* the flush reduces the last launch's split partials (if any) */
+    note(r, launches, 2, 0.0, 0.0);
+    if (!rc && !dry) rc = mark(r, launches, stream);
+    if (!rc && !dry) rc = tlg_dev_gemm_flush(stream);
+    if (!rc && !dry) rc = mark(r, launches + 1, stream);
+    free(set);
+    free(gone);
+    if (rc) return rc;
+    if (!dry) r->cur = (r->cur + 1) % r->pool;
+    return dry ? launches : 0;
+}
+
+int tl_run_time_launches(TlRun *r, void **events, int nevents, void *stream)
+{
+    r->ev = events;
+    r->nev = nevents;
+    int rc = grouped(r, stream, 0);
+    r->ev = NULL;
+    r->nev = 0;
+    return rc;
+}
+
+int tl_run_launch_info(TlRun *r, int k, double *flops, double *bytes)
+{
+    if (k < 0 || k >= TL_MAXLAUNCH) return -1;
+    *flops = r->lflops[k];
+    *bytes = r->lbytes[k];
+    return r->lkind[k];
+}
+
+int tl_run_step_grouped(TlRun *r, void *stream) { return grouped(r, stream, 0); }
+int tl_run_grouped_launches(TlRun *r) { return grouped(r, NULL, 1); }
+
+int tl_run_graph_build(TlRun *r, void *stream, int grouped_step)
 {
     for (int c = 0; c < r->pool; c++) {
         if (r->graph[c]) { tlg_graph_destroy(r->graph[c]); r->graph[c] = NULL; }
         r->cur = c;
         int rc = tlg_graph_begin(stream);
         if (rc) return rc;
-        for (int i = 0; i < r->plan->ncall && rc == 0; i++) rc = tl_run_call(r, i, stream);
+        if (grouped_step) {
+            rc = grouped(r, stream, 0);
+            r->cur = c;
+        } else {
+            for (int i = 0; i < r->plan->ncall && rc == 0; i++) rc = tl_run_call(r, i, stream);
+        }
         void *g = tlg_graph_end(stream);
         if (rc) return rc;
         if (!g) return TLG_EHIP;

@@ -66,6 +66,10 @@ static TlCall *push(TlPlan *p)
     return c;
 }
 
+/* The reference runs non-GEMM code here (norms, RoPE, attention, SwiGLU,
+ * softmax, residual adds): the next GEMM starts a new run. */
+static void glue(TlPlan *p) { p->run++; }
+
 static int gemm(TlPlan *p, int op, int line, const char *what,
                 int out, size_t oo, int a, size_t ao, int b, size_t bo, int M, int K, int N)
 {
@@ -77,6 +81,7 @@ static int gemm(TlPlan *p, int op, int line, const char *what,
     c->a = a; c->a_off = ao;
     c->b = b; c->b_off = bo;
     c->M = M; c->K = K; c->N = N;
+    c->run = p->run;
     return 0;
 }
 
@@ -88,6 +93,7 @@ static int zero(TlPlan *p, int line, const char *what, int out, size_t off, size
     strncpy(c->what, what, TL_NAMELEN - 1);
     c->out = out; c->out_off = off; c->n = n;
     c->a = c->b = -1;
+    c->run = p->run;
     return 0;
 }
 
@@ -149,17 +155,23 @@ int tl_plan_train(TlPlan *p, int R, int D, int KD, int F, int V, int L, int n_mt
         CHK(gemm(p, TL_MM, 981, "q", q, ld, a_norm, ld, P, w.wq, R, D, D));
         CHK(gemm(p, TL_MM, 982, "k", k, lk, a_norm, ld, P, w.wk, R, D, KD));
         CHK(gemm(p, TL_MM, 983, "v", v, lk, a_norm, ld, P, w.wv, R, D, KD));
+        glue(p);                                    /* RoPE, attention :984-990 */
         CHK(gemm(p, TL_MM, 993, "o", f_in, ld, att_ctx, ld, P, w.wo, R, D, D));
+        glue(p);                                    /* residual, rmsnorm :994-997 */
         CHK(gemm(p, TL_MM, 1002, "w1", g, lf, f_norm, ld, P, w.w1, R, D, F));
         CHK(gemm(p, TL_MM, 1003, "w3", u, lf, f_norm, ld, P, w.w3, R, D, F));
+        glue(p);                                    /* silu(g)*u :1004-1006 */
         if (l + 1 < L) CHK(gemm(p, TL_MM, 1008, "w2", a_in, ld + RD, dact, 0, P, w.w2, R, F, D));
         else           CHK(gemm(p, TL_MM, 1008, "w2", x_final, 0, dact, 0, P, w.w2, R, F, D));
+        glue(p);                                    /* residual :1009-1010, next rmsnorm */
     }
     CHK(zero(p, 1015, "logits", logits, 0, RV));
     CHK(gemm(p, TL_MM_BT, 1016, "logits", logits, 0, fn_norm, 0, P, m0.emb, R, V, D));
 
+    glue(p);                                        /* softmax + CE :1017-1028 */
     /* ---- memset(G) then backward, tinylm.c:2628, :1072-1154 ---- */
     CHK(zero(p, 2628, "G", G, 0, m0.total));
+    glue(p);                                        /* dlogits :1076-1082 */
     CHK(gemm(p, TL_MM, 1085, "dfn", dfn, 0, dlogits, 0, P, m0.emb, R, V, D));
     CHK(gemm(p, TL_MM_ATB, 1086, "dEmb", G, m0.emb, dlogits, 0, fn_norm, 0, R, V, D));
     /* MTP heads (mtp_grad, :1036-1069): t1=datt hk=dnorm dhk=dq dt1=dain
@@ -167,10 +179,13 @@ int tl_plan_train(TlPlan *p, int R, int D, int KD, int F, int V, int L, int n_mt
     for (int kk = 0; kk < n_mtp; kk++) {
         const size_t wk = m0.mtp0 + (size_t)kk * D * D;
         CHK(gemm(p, TL_MM, 1044, "mtp.t1", datt, 0, fn_norm, 0, P, wk, R, D, D));
+        glue(p);                                    /* hk = fn + silu(t1) :1045-1046 */
         CHK(zero(p, 1047, "mtp.lg", logits, 0, RV));
         CHK(gemm(p, TL_MM_BT, 1048, "mtp.lg", logits, 0, dnorm, 0, P, m0.emb, R, V, D));
+        glue(p);                                    /* softmax -> dl :1049-1057 */
         CHK(gemm(p, TL_MM_ATB, 1058, "mtp.dEmb", G, m0.emb, dlogits, 0, dnorm, 0, R, V, D));
         CHK(gemm(p, TL_MM, 1060, "mtp.dhk", dq, 0, dlogits, 0, P, m0.emb, R, V, D));
+        glue(p);                                    /* dfn += dhk, dt1 :1061-1065 */
         CHK(gemm(p, TL_MM_ATB, 1066, "mtp.dWk", G, wk, fn_norm, 0, dain, 0, R, D, D));
         CHK(gemm(p, TL_MM_BT, 1067, "mtp.dfn", dfn, 0, dain, 0, P, wk, R, D, D));
     }
@@ -178,17 +193,21 @@ int tl_plan_train(TlPlan *p, int R, int D, int KD, int F, int V, int L, int n_mt
         TlWeightMap w;
         tl_weight_map(V, D, KD, F, L, n_mtp, l, &w);
         const size_t ld = (size_t)l * RD;
+        glue(p);                                    /* rmsnorm_bwd / silu recompute :1091-1102 */
         CHK(gemm(p, TL_MM_ATB, 1103, "dW2", G, w.w2, du, 0, dout, 0, R, F, D));
         CHK(zero(p, 1104, "dact", dact, 0, RF));
         CHK(gemm(p, TL_MM_BT, 1105, "dact", dact, 0, dout, 0, P, w.w2, R, F, D));
+        glue(p);                                    /* SwiGLU backward :1106-1112 */
         CHK(zero(p, 1113, "dfnorm", dfnorm, 0, RD));
         CHK(gemm(p, TL_MM_BT, 1114, "dfnorm.w1", dfnorm, 0, dg, 0, P, w.w1, R, D, F));
         CHK(gemm(p, TL_MM_BT, 1115, "dfnorm.w3", dfnorm, 0, du, 0, P, w.w3, R, D, F));
         CHK(gemm(p, TL_MM_ATB, 1116, "dW1", G, w.w1, f_norm, ld, dg, 0, R, D, F));
         CHK(gemm(p, TL_MM_ATB, 1117, "dW3", G, w.w3, f_norm, ld, du, 0, R, D, F));
+        glue(p);                                    /* rmsnorm_bwd :1119-1121 */
         CHK(zero(p, 1123, "datt", datt, 0, RD));
         CHK(gemm(p, TL_MM_BT, 1124, "datt", datt, 0, dfin, 0, P, w.wo, R, D, D));
         CHK(gemm(p, TL_MM_ATB, 1125, "dWo", G, w.wo, att_ctx, ld, dfin, 0, R, D, D));
+        glue(p);                                    /* attention + RoPE backward :1127-1133 */
         CHK(zero(p, 1135, "dnorm", dnorm, 0, RD));
         CHK(gemm(p, TL_MM_BT, 1136, "dnorm.q", dnorm, 0, dq, 0, P, w.wq, R, D, D));
         CHK(gemm(p, TL_MM_BT, 1137, "dnorm.k", dnorm, 0, dk, 0, P, w.wk, R, D, KD));
@@ -226,10 +245,14 @@ int tl_plan_decode(TlPlan *p, int M, int D, int KD, int F, int V, int L)
         CHK(gemm(p, TL_MM, 3748, "q", q, 0, xn, 0, P, w.wq, M, D, D));
         CHK(gemm(p, TL_MM, 3749, "k", k, 0, xn, 0, P, w.wk, M, D, KD));
         CHK(gemm(p, TL_MM, 3750, "v", v, 0, xn, 0, P, w.wv, M, D, KD));
+        glue(p);                                    /* RoPE, KV store, attention :3756-3810 */
         CHK(gemm(p, TL_MM, 3812, "o", tmp, 0, ctx, 0, P, w.wo, M, D, D));
+        glue(p);                                    /* residual, rmsnorm :3813-3815 */
         CHK(gemm(p, TL_MM, 3821, "w1", g, 0, xn, 0, P, w.w1, M, D, F));
         CHK(gemm(p, TL_MM, 3822, "w3", u, 0, xn, 0, P, w.w3, M, D, F));
+        glue(p);                                    /* silu(g)*u :3823 */
         CHK(gemm(p, TL_MM, 3824, "w2", tmp, 0, u, 0, P, w.w2, M, F, D));
+        glue(p);                                    /* residual, next rmsnorm :3825 */
     }
     CHK(zero(p, 3035, "logits", logits, 0, (size_t)M * V));
     CHK(gemm(p, TL_MM_BT, 3035, "head", logits, 0, fn, 0, P, m0.emb, M, V, D));

@@ -42,6 +42,9 @@ typedef struct {
     size_t n;               /* TL_ZERO: floats cleared                      */
     int line;               /* tinylm.c line of the call                    */
     char what[TL_NAMELEN];  /* short label, e.g. "q", "dW2", "logits"       */
+    int run;                /* GEMM run: calls with the same run index are
+                               issued back to back by the reference with no
+                               non-GEMM code between them                   */
 } TlCall;
 
 typedef struct {
@@ -50,6 +53,7 @@ typedef struct {
     TlCall *call;
     /* model shape the plan was built for */
     int R, D, KD, F, V, L, n_mtp;
+    int run;                /* current run index while building */
 } TlPlan;
 
 /* Offsets of one layer's weights inside the flat P/G buffer
@@ -87,10 +91,25 @@ float *tl_run_buf(TlRun *r, int id);
 int    tl_run_step(TlRun *r, void *stream);
 /* Enqueue call i only (for per-call timing). */
 int    tl_run_call(TlRun *r, int i, void *stream);
-/* Capture one step into a HIP graph and replay it.  The graph is bound to
+/* Enqueue one step with each GEMM run as one grouped launch
+ * (tlg_dev_gemm_group): a memset followed by an accumulating GEMM into the
+ * same range becomes a setting GEMM, consecutive mm_bt into one dX become a
+ * chain.  Same results up to fp32 rounding (and the sign of exact zeros). */
+int    tl_run_step_grouped(TlRun *r, void *stream);
+/* Number of kernel launches a grouped step issues (for reports), not
+ * counting the final flush of split partials. */
+int    tl_run_grouped_launches(TlRun *r);
+/* One grouped step with events[k] recorded on `stream` before launch k and
+ * events[L+1] after the flush (L = tl_run_grouped_launches; nevents >= L+2).
+ * tl_run_launch_info then gives launch k's kind (0 grouped GEMMs, 1 clear,
+ * 2 flush) and its algorithmic flops and compulsory bytes. */
+int    tl_run_time_launches(TlRun *r, void **events, int nevents, void *stream);
+int    tl_run_launch_info(TlRun *r, int k, double *flops, double *bytes);
+/* Capture one step into a HIP graph and replay it (grouped != 0: the grouped
+ * step, else call by call).  The graph is bound to
  * the pool copy current at capture; tl_run_graph_step replays the graph for
  * that copy (one graph per pool copy). */
-int    tl_run_graph_build(TlRun *r, void *stream);
+int    tl_run_graph_build(TlRun *r, void *stream, int grouped);
 int    tl_run_graph_step(TlRun *r, void *stream);
 
 #ifdef __cplusplus

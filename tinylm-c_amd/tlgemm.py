@@ -54,6 +54,8 @@ SIGNATURES = {
     "tlg_tune_force": (_i, [_i, _i]),
     "tlg_dev_copy": (_i, [_vp, _vp, _sz, _vp]),
     "tlg_dev_mfma_peak": (_i, [_vp, _i, _i, _vp]),
+    "tlg_dev_gemm_group": (_i, [_vp, _i, _vp]),
+    "tlg_dev_gemm_flush": (_i, [_vp]),
     "tlg_graph_begin": (_i, [_vp]),
     "tlg_graph_end": (_vp, [_vp]),
     "tlg_graph_launch": (_i, [_vp, _vp]),
@@ -141,14 +143,16 @@ class TlCall(ctypes.Structure):
     _fields_ = [("op", ctypes.c_int), ("out", ctypes.c_int), ("a", ctypes.c_int), ("b", ctypes.c_int),
                 ("out_off", ctypes.c_size_t), ("a_off", ctypes.c_size_t), ("b_off", ctypes.c_size_t),
                 ("M", ctypes.c_int), ("K", ctypes.c_int), ("N", ctypes.c_int),
-                ("n", ctypes.c_size_t), ("line", ctypes.c_int), ("what", ctypes.c_char * 16)]
+                ("n", ctypes.c_size_t), ("line", ctypes.c_int), ("what", ctypes.c_char * 16),
+                ("run", ctypes.c_int)]
 
 
 class TlPlan(ctypes.Structure):
     _fields_ = [("nbuf", ctypes.c_int), ("ncall", ctypes.c_int), ("cap", ctypes.c_int),
                 ("buf", TlBuf * 48), ("call", ctypes.POINTER(TlCall)),
                 ("R", ctypes.c_int), ("D", ctypes.c_int), ("KD", ctypes.c_int), ("F", ctypes.c_int),
-                ("V", ctypes.c_int), ("L", ctypes.c_int), ("n_mtp", ctypes.c_int)]
+                ("V", ctypes.c_int), ("L", ctypes.c_int), ("n_mtp", ctypes.c_int),
+                ("run", ctypes.c_int)]
 
 
 class TlWeightMap(ctypes.Structure):
@@ -168,7 +172,7 @@ class Plan:
             c = raw.call[i]
             self.calls.append(dict(op=OPS[c.op], out=c.out, a=c.a, b=c.b, out_off=c.out_off,
                                    a_off=c.a_off, b_off=c.b_off, M=c.M, K=c.K, N=c.N, n=c.n,
-                                   line=c.line, what=c.what.decode()))
+                                   line=c.line, what=c.what.decode(), run=c.run))
 
     def buf_id(self, name):
         return [b[0] for b in self.bufs].index(name)
@@ -233,9 +237,17 @@ class Host:
         d.tl_run_fill.argtypes = [_vp, ctypes.c_ulonglong, _vp]
         d.tl_run_buf.argtypes = [_vp, _i]
         d.tl_run_buf.restype = _vp
-        for n in ("tl_run_step", "tl_run_graph_build", "tl_run_graph_step"):
+        for n in ("tl_run_step", "tl_run_step_grouped", "tl_run_graph_step"):
             getattr(d, n).argtypes = [_vp, _vp]
             getattr(d, n).restype = _i
+        d.tl_run_graph_build.argtypes = [_vp, _vp, _i]
+        d.tl_run_graph_build.restype = _i
+        d.tl_run_grouped_launches.argtypes = [_vp]
+        d.tl_run_grouped_launches.restype = _i
+        d.tl_run_time_launches.argtypes = [_vp, ctypes.POINTER(_vp), _i, _vp]
+        d.tl_run_time_launches.restype = _i
+        d.tl_run_launch_info.argtypes = [_vp, _i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
+        d.tl_run_launch_info.restype = _i
         d.tl_run_call.argtypes = [_vp, _i, _vp]
         d.tl_run_call.restype = _i
         for n in ("mm", "mm_bt", "mm_atb"):
