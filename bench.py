@@ -104,9 +104,6 @@ def kernel_census(lib, host, plan, run, stream, reps):
     return groups
 
 
-GROUP_KERNEL = "k_group<64, 64, 32, 2>"
-
-
 def launch_census(lib, host, run, stream, reps):
     """Average duration of each launch of a grouped step, from HIP events the
     executor records on the kernels' stream before every launch (reps steps),
@@ -122,11 +119,13 @@ def launch_census(lib, host, run, stream, reps):
             dt[k] += lib.tlg_event_elapsed_ms(ev[k], ev[k + 1]) / reps
     groups = {}
     fl, by = ctypes.c_double(), ctypes.c_double()
+    table = []
     for k in range(L + 1):
         kind = host.dll.tl_run_launch_info(run, k, ctypes.byref(fl), ctypes.byref(by))
+        table.append((k, kind, fl.value, by.value, dt[k]))
         if kind == 2 and dt[k] < 1e-4:
             continue                      # no split partials left: nothing launched
-        name = "k_zero" if kind == 1 else GROUP_KERNEL
+        name = "k_zero" if kind == 1 else lib.tlg_group_kernel().decode()
         g = groups.setdefault(name, dict(launches=0, ms=0.0, flops=0.0, bytes=0.0, shapes=set()))
         g["launches"] += 1
         g["ms"] += dt[k]
@@ -135,6 +134,10 @@ def launch_census(lib, host, run, stream, reps):
         g["shapes"].add({0: "grouped GEMMs", 1: "clear", 2: "split flush"}[kind])
     for e in ev:
         lib.tlg_event_destroy(e)
+    if os.environ.get("TLG_BENCH_LAUNCHES"):
+        for k, kind, f, b, ms in table:
+            log(f"[launch {k:3d}] kind {kind} {f / 1e9:7.3f} GF {b / 1e6:8.2f} MB {ms * 1e3:8.2f} us "
+                f"{f / (ms * 1e-3) / 1e12 if ms > 0 else 0:6.1f} TF")
     return groups
 
 
@@ -230,6 +233,7 @@ def main():
     ap.add_argument("--calls", action="store_true",
                     help="one launch per reference call instead of one grouped launch per GEMM run")
     ap.add_argument("--census-reps", type=int, default=5)
+    ap.add_argument("--group-cfg", type=int, default=None, help="tile config of grouped launches (tuning)")
     ap.add_argument("--decode-steps", type=int, default=512)
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--cpu-threads", type=int, default=0)
@@ -245,6 +249,8 @@ def main():
     lib = tlgemm.load()
     check(lib.tlg_init(0), "tlg_init")
     host = tlgemm.host()
+    if args.group_cfg is not None:
+        check(lib.tlg_tune_group(args.group_cfg), "tlg_tune_group")
     cfg = TRAIN[args.config]
     plan = host.plan_train(**cfg)
     run = host.dll.tl_run_new(ctypes.byref(plan.raw), 1)

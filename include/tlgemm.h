@@ -107,6 +107,11 @@ typedef struct {
 } TlgGemmCall;
 int tlg_dev_gemm_group(const TlgGemmCall *calls, int n, void *stream);
 int tlg_dev_gemm_flush(void *stream);
+/* Kernel instance grouped launches use, as rocprofv3 names it. */
+const char *tlg_group_kernel(void);
+/* Tuning hook: tile configuration of grouped launches (3, 4 or 5; the
+ * default 4 is 64x64 tiles with each wave over a quarter of every stage). */
+int tlg_tune_group(int cfg);
 
 /* ---- runtime wrappers for C host code ---------------------------------- */
 /* So the C step drivers (tinylm-c_amd/host) keep buffers and timing on the

@@ -133,3 +133,23 @@ def test_use_hip_seam(lib, orc):
     ref = orc.mm_atb(dW.copy(), X, dY)
     host.dll.mm_atb(dW.ctypes.data, X.ctypes.data, dY.ctypes.data, M, K, N)
     assert normwise_rel(dW, ref) <= TOL
+
+
+@pytest.mark.parametrize("gcfg", [0, 1, 3, 4, 8, 9, 10, 11, 12, 13, 14, 15])
+def test_group_tile_configs(lib, orc, gcfg):
+    """Every tile shape grouped launches can use, on the nano step."""
+    host = tlgemm.host()
+    plan = host.plan_train(**bench.TRAIN["nano"])
+    lib.check(lib.tlg_tune_group(gcfg), "tune")
+    run, stream = new_run(lib, host, plan, seed=gcfg)
+    try:
+        init = snapshot(lib, host, plan, run, stream)
+        lib.check(host.dll.tl_run_step_grouped(run, stream), "step")
+        got = snapshot(lib, host, plan, run, stream)
+    finally:
+        host.dll.tl_run_free(run)
+        lib.check(lib.tlg_tune_group(-1), "tune")
+    run_plan_cpu(plan, init, orc)
+    for bname, _, _ in plan.bufs:
+        for label, a, b in plan.regions(bname):
+            assert normwise_rel(got[bname][a:b], init[bname][a:b]) <= TOL, (gcfg, label)

@@ -367,3 +367,6 @@ extern "C" int tlg_dev_gemm_flush(void *stream)
     int rc = tlg_ensure_init();
     return rc ? rc : tlg_group_flush_launch((hipStream_t)stream);
 }
+
+const char *tlg_group_kernel_name(void);
+extern "C" const char *tlg_group_kernel(void) { return tlg_group_kernel_name(); }

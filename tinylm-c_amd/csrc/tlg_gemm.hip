@@ -127,150 +127,216 @@ struct LdsSize {
     static constexpr int value = (LAY == RC) ? OUTER * (BK + 4) : BK * (OUTER + 4);
 };
 
-// Fragment of one 32-wide MFMA block: the BK/2 r-values lane (o, h) feeds.
-template <int LAY, int OUTER, int BK>
-__device__ __forceinline__ void read_frag(const float *__restrict__ L, int o_base, int lane,
-                                          float (&f)[BK / 2])
+// Fragment of one 32-wide MFMA block: the RW/2 r-values lane (o, h) feeds,
+// from the RW reduction steps [r_base, r_base + RW) of a BK-step stage.
+template <int LAY, int OUTER, int BK, int RW>
+__device__ __forceinline__ void read_frag(const float *__restrict__ L, int o_base, int r_base, int lane,
+                                          float (&f)[RW / 2])
 {
     const int o = o_base + (lane & 31), h = lane >> 5;
     if (LAY == RC) {
-        const float *p = L + o * (BK + 4) + h * (BK / 2);
+        const float *p = L + o * (BK + 4) + r_base + h * (RW / 2);
 #pragma unroll
-        for (int s = 0; s < BK / 2; s += 4) {
+        for (int s = 0; s < RW / 2; s += 4) {
             const f32x4 x = *reinterpret_cast<const f32x4 *>(p + s);
             f[s] = x[0]; f[s + 1] = x[1]; f[s + 2] = x[2]; f[s + 3] = x[3];
         }
     } else {
 #pragma unroll
-        for (int s = 0; s < BK / 2; s++) f[s] = L[(h * (BK / 2) + s) * (OUTER + 4) + o];
+        for (int s = 0; s < RW / 2; s++) f[s] = L[(r_base + h * (RW / 2) + s) * (OUTER + 4) + o];
     }
 }
 
-// Tile geometry shared by the kernels.
-template <int BM, int BN, int BK, int WGM>
+// Tile geometry.  The 4 waves of a workgroup form a WGM x WGN grid over the
+// BM x BN tile and WK groups along the reduction: with WK > 1 every wave
+// computes its (BM/WGM) x (BN/WGN) sub-tile over RW = BK/WK of each stage's
+// reduction steps, and the WK partial sub-tiles are summed through LDS in
+// fixed order at the end.  WK > 1 gives small tiles several independent MFMA
+// accumulator chains per wave instead of one dependent chain.
+template <int BM_, int BN_, int BK_, int WGM_, int WK_, int NR_ = 2, int NCH_ = 0>
 struct Tile {
-    static constexpr int WGN = 4 / WGM;
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WK = WK_, NR = NR_;
+    static constexpr int WGN = 4 / (WGM * WK);
     static constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 32, FN = WN / 32;
-    static_assert(WGM * WGN == 4 && FM >= 1 && FN >= 1, "4 waves, 32x32 blocks");
+    static constexpr int RW = BK / WK;
+    // accumulator chains per 32x32 block (the reduction steps of a block
+    // alternate between its NCH chains, summed in fixed order at the store);
+    // measured on MI355X: one chain is as fast and keeps occupancy higher
+    static constexpr int NCH = NCH_ ? NCH_ : 1;
+    static_assert(WGM * WGN * WK == 4 && FM >= 1 && FN >= 1, "4 waves, 32x32 blocks");
+    static_assert(RW >= 8 && RW % 8 == 0, "a wave takes a multiple of 8 reduction steps per stage");
+    static constexpr int TILE = BM * BN;
     template <int LA, int LB>
-    static constexpr int lds() { return 2 * (LdsSize<LA, BM, BK>::value + LdsSize<LB, BN, BK>::value); }
-    static constexpr int lds_max()
-    {
-        constexpr int a = lds<RC, OC>(), b = lds<RC, RC>(), c = lds<OC, OC>();
-        return a > b ? (a > c ? a : c) : (b > c ? b : c);
-    }
+    static constexpr int stage_lds() { return 2 * (LdsSize<LA, BM, BK>::value + LdsSize<LB, BN, BK>::value); }
+    static constexpr int red_lds() { return WK > 1 ? WK * TILE : 0; }
+    static constexpr int mx(int a, int b) { return a > b ? a : b; }
+    template <int LA, int LB>
+    static constexpr int lds() { return mx(stage_lds<LA, LB>(), red_lds()); }
+    static constexpr int lds_max() { return mx(mx(lds<RC, OC>(), lds<RC, RC>()), lds<OC, OC>()); }
+    __device__ static int wave() { return threadIdx.x >> 6; }
+    __device__ static int wk() { return wave() / (WGM * WGN); }
+    __device__ static int wm() { return (wave() % (WGM * WGN)) / WGN; }
+    __device__ static int wn() { return (wave() % (WGM * WGN)) % WGN; }
 };
 
 // acc += A(i0.., r) B(r, j0..) over r in [rbeg, rend).  A tile's loads run
-// two stages ahead: register set S&1 holds stage S while stage S-2 computes
-// from LDS; LDS buffer S&1 holds stage S from the store after stage S-1.
-template <int BM, int BN, int BK, int WGM, int LA, int LB, bool VEC>
+// NR stages ahead through NR register sets; LDS is double buffered.
+template <class T, int LA, int LB, bool VEC>
 __device__ __forceinline__ void tile_accumulate(float *__restrict__ smem, const float *__restrict__ A,
                                                 const float *__restrict__ B, int lda, int ldb,
                                                 int i0, int j0, int Mo, int No, int rbeg, int rend,
-                                                f32x16 (&acc)[Tile<BM, BN, BK, WGM>::FM][Tile<BM, BN, BK, WGM>::FN])
+                                                f32x16 (&acc)[T::FM][T::FN][T::NCH])
 {
-    using T = Tile<BM, BN, BK, WGM>;
+    constexpr int BM = T::BM, BN = T::BN, BK = T::BK, RW = T::RW;
     constexpr int SA = LdsSize<LA, BM, BK>::value, SB = LdsSize<LB, BN, BK>::value;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / T::WGN, wn = wave % T::WGN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wm = T::wm(), wn = T::wn(), rb = T::wk() * RW;
     const int nsteps = (rend - rbeg + BK - 1) / BK;
     if (nsteps <= 0) return;
 
-    TileLoader<LA, BM, BK, VEC> la0, la1;
-    TileLoader<LB, BN, BK, VEC> lb0, lb1;
+    TileLoader<LA, BM, BK, VEC> la0, la1, la2;
+    TileLoader<LB, BN, BK, VEC> lb0, lb1, lb2;
     la0.load(A, lda, i0, Mo, rbeg, rend, tid);
     lb0.load(B, ldb, j0, No, rbeg, rend, tid);
     if (nsteps > 1) {
         la1.load(A, lda, i0, Mo, rbeg + BK, rend, tid);
         lb1.load(B, ldb, j0, No, rbeg + BK, rend, tid);
     }
+    if (T::NR > 2 && nsteps > 2) {
+        la2.load(A, lda, i0, Mo, rbeg + 2 * BK, rend, tid);
+        lb2.load(B, ldb, j0, No, rbeg + 2 * BK, rend, tid);
+    }
     la0.store(smem, tid);
     lb0.store(smem + SA, tid);
     __syncthreads();
 
     auto compute = [&](const float *As, const float *Bs) {
-        float fa[T::FM][BK / 2], fb[T::FN][BK / 2];
+        float fa[T::FM][RW / 2], fb[T::FN][RW / 2];
 #pragma unroll
-        for (int a = 0; a < T::FM; a++) read_frag<LA, BM, BK>(As, wm * T::WM + a * 32, lane, fa[a]);
+        for (int a = 0; a < T::FM; a++) read_frag<LA, BM, BK, RW>(As, wm * T::WM + a * 32, rb, lane, fa[a]);
 #pragma unroll
-        for (int b = 0; b < T::FN; b++) read_frag<LB, BN, BK>(Bs, wn * T::WN + b * 32, lane, fb[b]);
+        for (int b = 0; b < T::FN; b++) read_frag<LB, BN, BK, RW>(Bs, wn * T::WN + b * 32, rb, lane, fb[b]);
 #pragma unroll
-        for (int s = 0; s < BK / 2; s++)
+        for (int s = 0; s < RW / 2; s++)
 #pragma unroll
             for (int a = 0; a < T::FM; a++)
 #pragma unroll
                 for (int b = 0; b < T::FN; b++)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[a][s], fb[b][s], acc[a][b], 0, 0, 0);
+                    acc[a][b][s % T::NCH] =
+                        __builtin_amdgcn_mfma_f32_32x32x2f32(fa[a][s], fb[b][s], acc[a][b][s % T::NCH], 0, 0, 0);
     };
 
-    // Stage st lives in LDS buffer st&1.  Its half-iteration prefetches stage
-    // st+2 into the register set stage st came from, computes, then moves
-    // stage st+1 from the other register set into the other LDS buffer.
-    int st = 0;
-    for (; st + 1 < nsteps; st += 2) {
-        if (st + 2 < nsteps) {
-            la0.load(A, lda, i0, Mo, rbeg + (st + 2) * BK, rend, tid);
-            lb0.load(B, ldb, j0, No, rbeg + (st + 2) * BK, rend, tid);
+    // Stage st lives in LDS buffer st&1 and, before that, in register set
+    // st % NR.  Step st prefetches stage st+NR into the set stage st came
+    // from, computes stage st, then moves stage st+1 from its register set
+    // into the other LDS buffer.  NR = 3 keeps loads three stages ahead.
+    auto step = [&](int st, auto &lac, auto &lbc, auto &lan, auto &lbn) {
+        if (st + T::NR < nsteps) {
+            lac.load(A, lda, i0, Mo, rbeg + (st + T::NR) * BK, rend, tid);
+            lbc.load(B, ldb, j0, No, rbeg + (st + T::NR) * BK, rend, tid);
         }
-        compute(smem, smem + SA);
-        la1.store(smem + SA + SB, tid);
-        lb1.store(smem + 2 * SA + SB, tid);
-        __syncthreads();
-        if (st + 3 < nsteps) {
-            la1.load(A, lda, i0, Mo, rbeg + (st + 3) * BK, rend, tid);
-            lb1.load(B, ldb, j0, No, rbeg + (st + 3) * BK, rend, tid);
-        }
-        compute(smem + SA + SB, smem + 2 * SA + SB);
-        if (st + 2 < nsteps) {
-            la0.store(smem, tid);
-            lb0.store(smem + SA, tid);
+        float *cur = smem + (st & 1) * (SA + SB);
+        compute(cur, cur + SA);
+        if (st + 1 < nsteps) {
+            float *nxt = smem + ((st + 1) & 1) * (SA + SB);
+            lan.store(nxt, tid);
+            lbn.store(nxt + SA, tid);
         }
         __syncthreads();
-    }
-    if (st < nsteps) {              // odd stage count: the last stage is in buffer 0
-        compute(smem, smem + SA);
-        __syncthreads();
+    };
+    if constexpr (T::NR == 2) {
+        for (int st = 0; st < nsteps; st += 2) {
+            step(st, la0, lb0, la1, lb1);
+            if (st + 1 < nsteps) step(st + 1, la1, lb1, la0, lb0);
+        }
+    } else {
+        for (int st = 0; st < nsteps; st += 3) {
+            step(st, la0, lb0, la1, lb1);
+            if (st + 1 < nsteps) step(st + 1, la1, lb1, la2, lb2);
+            if (st + 2 < nsteps) step(st + 2, la2, lb2, la0, lb0);
+        }
     }
 }
 
 // C (beta ? += : =) acc for the valid part of the tile.  32x32 MFMA result
 // layout: lane l, register v holds row 8*(v/4) + 4*(l/32) + v%4, column l%32.
-template <int BM, int BN, int BK, int WGM>
-__device__ __forceinline__ void tile_store(const f32x16 (&acc)[Tile<BM, BN, BK, WGM>::FM][Tile<BM, BN, BK, WGM>::FN],
-                                           float *__restrict__ C, int ldc, int beta, int Mo, int No,
-                                           int i0, int j0)
+// With WK > 1 the wave groups' partial tiles go through `red` (LDS, WK*BM*BN
+// floats, free once tile_accumulate has returned) and are summed in wave-group
+// order, so the result does not depend on timing.
+template <class T>
+__device__ __forceinline__ void tile_store(const f32x16 (&accs)[T::FM][T::FN][T::NCH], float *__restrict__ C,
+                                           int ldc, int beta, int Mo, int No, int i0, int j0,
+                                           float *__restrict__ red)
 {
-    using T = Tile<BM, BN, BK, WGM>;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave / T::WGN, wn = wave % T::WGN;
-    const int h = lane >> 5, col = lane & 31;
+    const int lane = threadIdx.x & 63;
+    f32x16 acc[T::FM][T::FN];
 #pragma unroll
     for (int a = 0; a < T::FM; a++)
 #pragma unroll
         for (int b = 0; b < T::FN; b++) {
-            const int j = j0 + wn * T::WN + b * 32 + col;
-            if (j >= No) continue;
+            acc[a][b] = accs[a][b][0];
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int i = i0 + wm * T::WM + a * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                if (i < Mo) {
-                    float *p = C + (size_t)i * ldc + j;
-                    *p = beta ? (*p + acc[a][b][v]) : acc[a][b][v];
+            for (int c = 1; c < T::NCH; c++) acc[a][b] += accs[a][b][c];
+        }
+    if constexpr (T::WK == 1) {
+        const int wm = T::wm(), wn = T::wn();
+        const int h = lane >> 5, col = lane & 31;
+#pragma unroll
+        for (int a = 0; a < T::FM; a++)
+#pragma unroll
+            for (int b = 0; b < T::FN; b++) {
+                const int j = j0 + wn * T::WN + b * 32 + col;
+                if (j >= No) continue;
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const int i = i0 + wm * T::WM + a * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                    if (i < Mo) {
+                        float *p = C + (size_t)i * ldc + j;
+                        *p = beta ? (*p + acc[a][b][v]) : acc[a][b][v];
+                    }
                 }
             }
+    } else {
+        // fragment-order index of (wave-in-group g, a, b, v, lane)
+        const int g = T::wave() % (T::WGM * T::WGN);
+        float *mine = red + T::wk() * T::TILE;
+#pragma unroll
+        for (int a = 0; a < T::FM; a++)
+#pragma unroll
+            for (int b = 0; b < T::FN; b++)
+#pragma unroll
+                for (int v = 0; v < 16; v++)
+                    mine[(((g * T::FM + a) * T::FN + b) * 16 + v) * 64 + lane] = acc[a][b][v];
+        __syncthreads();
+#pragma unroll 4
+        for (int f = threadIdx.x; f < T::TILE; f += 256) {
+            float s = red[f];
+#pragma unroll
+            for (int k = 1; k < T::WK; k++) s += red[k * T::TILE + f];
+            const int l = f & 63, v = (f >> 6) & 15, ab = f >> 10;
+            const int b = ab % T::FN, a = (ab / T::FN) % T::FM, gg = ab / (T::FN * T::FM);
+            const int i = i0 + (gg / T::WGN) * T::WM + a * 32 + 8 * (v >> 2) + 4 * (l >> 5) + (v & 3);
+            const int j = j0 + (gg % T::WGN) * T::WN + b * 32 + (l & 31);
+            if (i < Mo && j < No) {
+                float *p = C + (size_t)i * ldc + j;
+                *p = beta ? (*p + s) : s;
+            }
         }
+        __syncthreads();            // `red` aliases the stage buffers of the next tile
+    }
 }
 
-template <int FM, int FN>
-__device__ __forceinline__ void zero_acc(f32x16 (&acc)[FM][FN])
+template <int FM, int FN, int NCH>
+__device__ __forceinline__ void zero_acc(f32x16 (&acc)[FM][FN][NCH])
 {
 #pragma unroll
     for (int a = 0; a < FM; a++)
 #pragma unroll
         for (int b = 0; b < FN; b++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) acc[a][b][v] = 0.f;
+            for (int c = 0; c < NCH; c++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[a][b][c][v] = 0.f;
 }
 
 // ------------------------------------------------------- single problem --
@@ -288,25 +354,23 @@ struct GemmArgs {
     float *ws;       // splits x Mo x No partials (splits > 1)
 };
 
-template <int BM, int BN, int BK, int WGM, int LA, int LB, bool VEC>
+template <class T, int LA, int LB, bool VEC>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g)
 {
-    using T = Tile<BM, BN, BK, WGM>;
     __shared__ __attribute__((aligned(16))) float smem[T::template lds<LA, LB>()];
     const int item = xcd_remap(blockIdx.x, gridDim.x);
     const int z = item / g.tiles, tile = item % g.tiles;
-    const int i0 = (tile / g.tiles_n) * BM, j0 = (tile % g.tiles_n) * BN;
+    const int i0 = (tile / g.tiles_n) * T::BM, j0 = (tile % g.tiles_n) * T::BN;
     const int rbeg = z * g.rps;
     const int rend = min(g.R, rbeg + g.rps);
-    f32x16 acc[T::FM][T::FN];
+    f32x16 acc[T::FM][T::FN][T::NCH];
     zero_acc(acc);
-    tile_accumulate<BM, BN, BK, WGM, LA, LB, VEC>(smem, g.A, g.B, g.lda, g.ldb, i0, j0, g.Mo, g.No,
-                                                  rbeg, rend, acc);
+    tile_accumulate<T, LA, LB, VEC>(smem, g.A, g.B, g.lda, g.ldb, i0, j0, g.Mo, g.No, rbeg, rend, acc);
     // a split writes its partial (beta 0) into workspace slice z
     if (g.splits > 1)
-        tile_store<BM, BN, BK, WGM>(acc, g.ws + (size_t)z * g.Mo * g.No, g.No, 0, g.Mo, g.No, i0, j0);
+        tile_store<T>(acc, g.ws + (size_t)z * g.Mo * g.No, g.No, 0, g.Mo, g.No, i0, j0, smem);
     else
-        tile_store<BM, BN, BK, WGM>(acc, g.C, g.ldc, g.beta, g.Mo, g.No, i0, j0);
+        tile_store<T>(acc, g.C, g.ldc, g.beta, g.Mo, g.No, i0, j0, smem);
 }
 
 // C (beta ? += : =) sum_{z < splits} ws[z], in z order; Mo x No elements.
@@ -336,7 +400,7 @@ __global__ void k_split_reduce(const float *__restrict__ ws, float *__restrict__
 enum { PK_NN = 0, PK_NT = 1, PK_TN = 2, PK_RED = 3 };
 #define TLG_MAXSEG 3
 #define TLG_MAXPROB 16
-#define TLG_RED_CHUNK (256 * 4)
+#define TLG_RED_CHUNK 256
 
 struct Seg { const float *A, *B; int R, lda, ldb; };
 struct Prob {
@@ -345,7 +409,7 @@ struct Prob {
     int Mo, No, ldc, beta;
     int kind, nseg;
     int tiles_n, tiles, splits, rps;
-    int item0;            // first work item of this problem
+    int items;            // work items: tiles * splits, or reduction chunks
     Seg seg[TLG_MAXSEG];
 };
 struct GroupArgs {
@@ -353,45 +417,58 @@ struct GroupArgs {
     Prob p[TLG_MAXPROB];
 };
 
-template <int BM, int BN, int BK, int WGM, int LA, int LB>
+template <class T, int LA, int LB>
 __device__ __forceinline__ void group_tile(float *smem, const Prob &P, int local)
 {
-    using T = Tile<BM, BN, BK, WGM>;
     const int z = local / P.tiles, tile = local % P.tiles;
-    const int i0 = (tile / P.tiles_n) * BM, j0 = (tile % P.tiles_n) * BN;
-    f32x16 acc[T::FM][T::FN];
+    const int i0 = (tile / P.tiles_n) * T::BM, j0 = (tile % P.tiles_n) * T::BN;
+    f32x16 acc[T::FM][T::FN][T::NCH];
     zero_acc(acc);
     if (P.splits > 1) {
         const Seg &s = P.seg[0];
         const int rbeg = z * P.rps, rend = min(s.R, rbeg + P.rps);
-        tile_accumulate<BM, BN, BK, WGM, LA, LB, true>(smem, s.A, s.B, s.lda, s.ldb, i0, j0, P.Mo, P.No,
-                                                       rbeg, rend, acc);
-        tile_store<BM, BN, BK, WGM>(acc, (float *)P.ws + (size_t)z * P.Mo * P.No, P.No, 0, P.Mo, P.No, i0, j0);
+        tile_accumulate<T, LA, LB, true>(smem, s.A, s.B, s.lda, s.ldb, i0, j0, P.Mo, P.No, rbeg, rend, acc);
+        tile_store<T>(acc, (float *)P.ws + (size_t)z * P.Mo * P.No, P.No, 0, P.Mo, P.No, i0, j0, smem);
         return;
     }
     for (int k = 0; k < P.nseg; k++) {
         const Seg &s = P.seg[k];
-        tile_accumulate<BM, BN, BK, WGM, LA, LB, true>(smem, s.A, s.B, s.lda, s.ldb, i0, j0, P.Mo, P.No,
-                                                       0, s.R, acc);
-        if (k + 1 < P.nseg) __syncthreads();      // LDS reuse by the next segment
+        tile_accumulate<T, LA, LB, true>(smem, s.A, s.B, s.lda, s.ldb, i0, j0, P.Mo, P.No, 0, s.R, acc);
     }
-    tile_store<BM, BN, BK, WGM>(acc, P.C, P.ldc, P.beta, P.Mo, P.No, i0, j0);
+    tile_store<T>(acc, P.C, P.ldc, P.beta, P.Mo, P.No, i0, j0, smem);
 }
 
-template <int BM, int BN, int BK, int WGM>
+// Work-item mapping of a grouped launch.  The dispatcher deals workgroup b
+// to XCD b % 8; XCD x takes an equal contiguous slice of EVERY problem's
+// items (so each XCD's L2 sees neighbouring tiles of a problem, and every
+// XCD gets the same mix of long and short items), problem by problem in
+// list order (the host lists problems longest item first).  Workgroups past
+// their XCD's share exit at once.
+__device__ __forceinline__ int group_item(const GroupArgs &g, int b, int *local)
+{
+    const int x = b & 7;
+    int slot = b >> 3;
+    for (int p = 0; p < g.nprob; p++) {
+        const int n = g.p[p].items;
+        const int lo = (x * n) >> 3, hi = ((x + 1) * n) >> 3;
+        if (slot < hi - lo) { *local = lo + slot; return p; }
+        slot -= hi - lo;
+    }
+    return -1;
+}
+
+template <class T>
 __global__ __launch_bounds__(256) void k_group(GroupArgs g)
 {
-    using T = Tile<BM, BN, BK, WGM>;
     __shared__ __attribute__((aligned(16))) float smem[T::lds_max()];
-    const int item = xcd_remap(blockIdx.x, gridDim.x);
-    int p = 0;
-    while (p + 1 < g.nprob && item >= g.p[p + 1].item0) p++;
+    int local = 0;
+    const int p = group_item(g, blockIdx.x, &local);
+    if (p < 0) return;
     const Prob &P = g.p[p];
-    const int local = item - P.item0;
     switch (P.kind) {
-    case PK_NN: group_tile<BM, BN, BK, WGM, RC, OC>(smem, P, local); break;
-    case PK_NT: group_tile<BM, BN, BK, WGM, RC, RC>(smem, P, local); break;
-    case PK_TN: group_tile<BM, BN, BK, WGM, OC, OC>(smem, P, local); break;
+    case PK_NN: group_tile<T, RC, OC>(smem, P, local); break;
+    case PK_NT: group_tile<T, RC, RC>(smem, P, local); break;
+    case PK_TN: group_tile<T, OC, OC>(smem, P, local); break;
     default: {
         const size_t n = (size_t)P.Mo * P.No;
         const size_t e0 = (size_t)local * TLG_RED_CHUNK;
@@ -421,35 +498,68 @@ int tlg_zero_launch(float *dst, size_t n, hipStream_t st)
 
 // ---------------------------------------------------------------- launch --
 // Tile shapes: BM x BN output per workgroup, BK reduction steps per stage,
-// WGM waves along M (4 / WGM along N).
-struct TileCfg { int bm, bn, bk, wgm; };
+// WGM x WGN waves over the tile, WK wave groups along the reduction.
+struct TileCfg { int bm, bn, bk, wgm, wk; };
 static const TileCfg kCfgs[] = {
-    {128, 128, 16, 2},   // 0: wave tile 64x64
-    {128, 64, 32, 2},    // 1: 64x32
-    {64, 128, 32, 2},    // 2: 32x64
-    {64, 64, 32, 2},     // 3: 32x32
-    {32, 128, 32, 1},    // 4: 32x32, waves side by side along N
-    {128, 32, 32, 4},    // 5: 32x32, waves stacked along M
+    {128, 128, 16, 2, 1},   // 0: wave tile 64x64, 4 accumulator chains
+    {128, 64, 32, 2, 1},    // 1: 64x32
+    {64, 128, 32, 2, 1},    // 2: 32x64
+    {64, 64, 32, 2, 1},     // 3: 32x32, one chain per wave
+    {64, 64, 32, 1, 4},     // 4: 64x64 per wave over a quarter of each stage
+    {64, 64, 64, 1, 4},     // 5: same, 64-step stages
+    {64, 128, 32, 1, 2},    // 6: 64x64 per wave, half of each stage
+    {128, 64, 32, 2, 2},    // 7: 64x64 per wave, half of each stage
+    {64, 64, 64, 2, 1},     // 8: 32x32 per wave, 64-step stages
+    {64, 64, 32, 2, 1},     // 9-12: 64x64 tiles (prefetch / chain variants)
+    {64, 64, 32, 2, 1},
+    {64, 64, 32, 2, 1},
+    {64, 64, 32, 2, 1},
+    {32, 64, 32, 1, 2},     // 13: 32x32 per wave, half of each stage
+    {64, 32, 32, 2, 2},     // 14: 32x32 per wave, half of each stage
+    {32, 32, 32, 1, 4},     // 15: 32x32 per wave, a quarter of each stage
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
+using T0 = Tile<128, 128, 16, 2, 1>;
+using T1 = Tile<128, 64, 32, 2, 1>;
+using T2 = Tile<64, 128, 32, 2, 1>;
+using T3 = Tile<64, 64, 32, 2, 1>;
+using T4 = Tile<64, 64, 32, 1, 4>;
+using T5 = Tile<64, 64, 64, 1, 4>;
+using T6 = Tile<64, 128, 32, 1, 2>;
+using T7 = Tile<128, 64, 32, 2, 2>;
+using T8 = Tile<64, 64, 64, 2, 1>;
+// grouped-launch variants for sweeps: prefetch depth NR, chains per block
+using T9 = Tile<64, 64, 32, 2, 1, 2, 2>;
+using T10 = Tile<64, 64, 32, 2, 1, 2, 1>;
+using T11 = Tile<64, 64, 32, 2, 1, 3, 1>;
+using T12 = Tile<64, 64, 32, 2, 1, 3, 4>;
+using T13 = Tile<32, 64, 32, 1, 2>;
+using T14 = Tile<64, 32, 32, 2, 2>;
+using T15 = Tile<32, 32, 32, 1, 4>;
 
-template <int BM, int BN, int BK, int WGM, int LA, int LB>
+template <class T, int LA, int LB>
 static void launch_t(const GemmArgs &a, int grid, bool vec, hipStream_t st)
 {
-    if (vec) hipLaunchKernelGGL((k_gemm<BM, BN, BK, WGM, LA, LB, true>), dim3(grid), dim3(256), 0, st, a);
-    else     hipLaunchKernelGGL((k_gemm<BM, BN, BK, WGM, LA, LB, false>), dim3(grid), dim3(256), 0, st, a);
+    if (vec) hipLaunchKernelGGL((k_gemm<T, LA, LB, true>), dim3(grid), dim3(256), 0, st, a);
+    else     hipLaunchKernelGGL((k_gemm<T, LA, LB, false>), dim3(grid), dim3(256), 0, st, a);
 }
 
 template <int LA, int LB>
 static void launch_kind(int ci, const GemmArgs &a, int grid, bool vec, hipStream_t st)
 {
     switch (ci) {
-    case 0: launch_t<128, 128, 16, 2, LA, LB>(a, grid, vec, st); break;
-    case 1: launch_t<128, 64, 32, 2, LA, LB>(a, grid, vec, st); break;
-    case 2: launch_t<64, 128, 32, 2, LA, LB>(a, grid, vec, st); break;
-    case 3: launch_t<64, 64, 32, 2, LA, LB>(a, grid, vec, st); break;
-    case 4: launch_t<32, 128, 32, 1, LA, LB>(a, grid, vec, st); break;
-    default: launch_t<128, 32, 32, 4, LA, LB>(a, grid, vec, st); break;
+    case 0: launch_t<T0, LA, LB>(a, grid, vec, st); break;
+    case 1: launch_t<T1, LA, LB>(a, grid, vec, st); break;
+    case 2: launch_t<T2, LA, LB>(a, grid, vec, st); break;
+    case 3: launch_t<T3, LA, LB>(a, grid, vec, st); break;
+    case 4: launch_t<T4, LA, LB>(a, grid, vec, st); break;
+    case 5: launch_t<T5, LA, LB>(a, grid, vec, st); break;
+    case 6: launch_t<T6, LA, LB>(a, grid, vec, st); break;
+    case 7: launch_t<T7, LA, LB>(a, grid, vec, st); break;
+    case 13: launch_t<T13, LA, LB>(a, grid, vec, st); break;
+    case 14: launch_t<T14, LA, LB>(a, grid, vec, st); break;
+    case 15: launch_t<T15, LA, LB>(a, grid, vec, st); break;
+    default: launch_t<T8, LA, LB>(a, grid, vec, st); break;
     }
 }
 
@@ -516,8 +626,8 @@ int tlg_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len, int *s
     const int la = (kind == TLG_TN) ? OC : RC;
     const int lb = (kind == TLG_NT) ? RC : OC;
     const bool vec = (la == RC ? (R % 4 == 0) : (Mo % 4 == 0)) && (lb == RC ? (R % 4 == 0) : (No % 4 == 0));
-    snprintf(buf, (size_t)len, "k_gemm<%d, %d, %d, %d, %d, %d, %s>", c.bm, c.bn, c.bk, c.wgm,
-             la, lb, vec ? "true" : "false");
+    snprintf(buf, (size_t)len, "k_gemm<Tile<%d, %d, %d, %d, %d, 2, 0>, %d, %d, %s>", c.bm, c.bn, c.bk, c.wgm,
+             c.wk, la, lb, vec ? "true" : "false");
     if (splits) *splits = p.splits;
     return TLG_OK;
 }
@@ -596,22 +706,109 @@ int tlg_gemm_launch(TlgKind kind, const float *A, const float *B, float *C,
 // the halves alternate so a launch never overwrites partials still pending.
 static Prob g_pending[TLG_MAXPROB];
 static int g_npending = 0;
+#include <stdlib.h>
 static int g_ws_half = 0;
 
-typedef void (*GroupLauncher)(const GroupArgs &, int, hipStream_t);
-template <int BM, int BN, int BK, int WGM>
-static void launch_group_t(const GroupArgs &a, int grid, hipStream_t st)
+// Tile shape of a grouped launch (all problems of a group share it): the
+// largest of 128x128, 128x64 and 64x64 that still gives every CU about
+// `g_min_waves` workgroups, so big groups load fewer bytes per flop and small
+// ones keep the CUs busy.  tlg_tune_group pins one shape for sweeps.
+static int g_group_cfg = -1;
+static double g_min_waves = 2.0;
+static int g_cand[4] = {3, 13, 15, -1};   // 64x64, 32x64, 32x32
+static int g_rtarget = 384;
+static int g_group_last = 3;          // shape of the most recent grouped launch
+
+static void group_env(void)
 {
-    hipLaunchKernelGGL((k_group<BM, BN, BK, WGM>), dim3(grid), dim3(256), 0, st, a);
+    static int done = 0;
+    if (done) return;
+    done = 1;
+    const char *e = getenv("TLG_GROUP_MINWAVES");
+    if (e && atof(e) > 0) g_min_waves = atof(e);
+    e = getenv("TLG_GROUP_CFG");
+    if (e && *e) g_group_cfg = atoi(e);
+    e = getenv("TLG_GROUP_CANDS");            // e.g. "3,13,15"
+    if (e && *e) {
+        int k = 0;
+        for (const char *q = e; *q && k < 3; ) {
+            g_cand[k++] = atoi(q);
+            while (*q && *q != ',') q++;
+            if (*q == ',') q++;
+        }
+        g_cand[k] = -1;
+    }
+    e = getenv("TLG_GROUP_RTARGET");
+    if (e && atoi(e) >= 64) g_rtarget = atoi(e);
 }
 
-static int add_reductions(GroupArgs &a, int &items)
+static void launch_group(int ci, const GroupArgs &a, int grid, hipStream_t st)
+{
+    switch (ci) {
+    case 0: hipLaunchKernelGGL((k_group<T0>), dim3(grid), dim3(256), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((k_group<T1>), dim3(grid), dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((k_group<T4>), dim3(grid), dim3(256), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((k_group<T8>), dim3(grid), dim3(256), 0, st, a); break;
+    case 9: hipLaunchKernelGGL((k_group<T9>), dim3(grid), dim3(256), 0, st, a); break;
+    case 10: hipLaunchKernelGGL((k_group<T10>), dim3(grid), dim3(256), 0, st, a); break;
+    case 11: hipLaunchKernelGGL((k_group<T11>), dim3(grid), dim3(256), 0, st, a); break;
+    case 12: hipLaunchKernelGGL((k_group<T12>), dim3(grid), dim3(256), 0, st, a); break;
+    case 13: hipLaunchKernelGGL((k_group<T13>), dim3(grid), dim3(256), 0, st, a); break;
+    case 14: hipLaunchKernelGGL((k_group<T14>), dim3(grid), dim3(256), 0, st, a); break;
+    case 15: hipLaunchKernelGGL((k_group<T15>), dim3(grid), dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((k_group<T3>), dim3(grid), dim3(256), 0, st, a); break;
+    }
+    g_group_last = ci;
+}
+
+extern "C" int tlg_tune_group(int cfg)
+{
+    if (cfg != -1 && cfg != 0 && cfg != 1 && cfg != 3 && cfg != 4 && (cfg < 8 || cfg > 15))
+        return tlg_fail(TLG_EINVAL, "tlg_tune_group: config %d", cfg);
+    g_group_cfg = cfg;
+    return TLG_OK;
+}
+
+const char *tlg_group_kernel_name(void)
+{
+    switch (g_group_last) {
+    case 0: return "k_group<Tile<128, 128, 16, 2, 1, 2, 0> >";
+    case 1: return "k_group<Tile<128, 64, 32, 2, 1, 2, 0> >";
+    case 4: return "k_group<Tile<64, 64, 32, 1, 4, 2, 0> >";
+    case 8: return "k_group<Tile<64, 64, 64, 2, 1, 2, 0> >";
+    case 9: return "k_group<Tile<64, 64, 32, 2, 1, 2, 2> >";
+    case 10: return "k_group<Tile<64, 64, 32, 2, 1, 2, 1> >";
+    case 11: return "k_group<Tile<64, 64, 32, 2, 1, 3, 1> >";
+    case 12: return "k_group<Tile<64, 64, 32, 2, 1, 3, 4> >";
+    case 13: return "k_group<Tile<32, 64, 32, 1, 2, 2, 0> >";
+    case 14: return "k_group<Tile<64, 32, 32, 2, 2, 2, 0> >";
+    case 15: return "k_group<Tile<32, 32, 32, 1, 4, 2, 0> >";
+    default: return "k_group<Tile<64, 64, 32, 2, 1, 2, 0> >";
+    }
+}
+
+// Grid for the XCD-sliced mapping of group_item: 8 x the largest per-XCD
+// share.
+static int group_grid(const GroupArgs &a)
+{
+    int most = 0;
+    for (int x = 0; x < 8; x++) {
+        int t = 0;
+        for (int p = 0; p < a.nprob; p++) {
+            const int n = a.p[p].items;
+            t += ((x + 1) * n >> 3) - (x * n >> 3);
+        }
+        if (t > most) most = t;
+    }
+    return 8 * most;
+}
+
+static int add_reductions(GroupArgs &a)
 {
     for (int k = 0; k < g_npending; k++) {
         Prob r = g_pending[k];
         r.kind = PK_RED;
-        r.item0 = items;
-        items += (int)(((size_t)r.Mo * r.No + TLG_RED_CHUNK - 1) / TLG_RED_CHUNK);
+        r.items = (int)(((size_t)r.Mo * r.No + TLG_RED_CHUNK - 1) / TLG_RED_CHUNK);
         a.p[a.nprob++] = r;
     }
     g_npending = 0;
@@ -623,9 +820,8 @@ int tlg_group_flush_launch(hipStream_t st)
     if (g_npending == 0) return TLG_OK;
     GroupArgs a;
     a.nprob = 0;
-    int items = 0;
-    add_reductions(a, items);
-    launch_group_t<64, 64, 32, 2>(a, items, st);
+    add_reductions(a);
+    launch_group(3, a, group_grid(a), st);
     TLG_HIP(hipGetLastError());
     return TLG_OK;
 }
@@ -642,11 +838,31 @@ static bool overlap(const char *a0, const char *a1, const char *b0, const char *
     return a0 < b1 && b0 < a1;
 }
 
+// Split problem P's reduction so one item runs about `rtarget` steps; partials
+// go to ws (bounded by ws_cap floats).
+static void plan_split(Prob &P, int R, int rtarget, float *ws, size_t &ws_used, size_t ws_cap)
+{
+    P.splits = 1;
+    P.rps = R;
+    if (P.kind != PK_TN || R <= rtarget + rtarget / 2) return;
+    int sp = cdiv(R, rtarget);
+    if (sp > 32) sp = 32;
+    const int rps = cdiv(cdiv(R, sp), 64) * 64;      // a multiple of every group BK
+    sp = cdiv(R, rps);
+    if (sp > 1 && ws_used + (size_t)sp * P.Mo * P.No <= ws_cap) {
+        P.splits = sp;
+        P.rps = rps;
+        P.ws = ws + ws_used;
+        ws_used += (size_t)sp * P.Mo * P.No;
+    }
+}
+
 int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
 {
     if (n <= 0) return TLG_OK;
     int rc = tlg_ensure_init();
     if (rc) return rc;
+    group_env();
     if (n > TLG_MAXPROB / 2) return tlg_fail(TLG_EINVAL, "tlg_dev_gemm_group: at most %d calls", TLG_MAXPROB / 2);
 
     // Pending reductions write their C; a call that touches such a range must
@@ -674,31 +890,16 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
         }
     }
 
-    GroupArgs a;
-    a.nprob = 0;
-    int items = 0;
-    add_reductions(a, items);
-    float *ws = g_tlg.ws + (size_t)g_ws_half * (g_tlg.ws_floats / 2);
-    size_t ws_used = 0;
-    const size_t ws_cap = g_tlg.ws_floats / 2;
-    // reduction length the non-split problems of this group run per tile:
-    // split problems aim for about the same per-item work
+    // Problems as the kernel sees them (tiles and splits filled in below).
+    Prob probs[TLG_MAXPROB / 2];
+    int Rtot[TLG_MAXPROB / 2];
     int rmax = 0;
-    for (int i = 0; i < n; i++) {
-        const TlgGemmCall &c = calls[i];
-        if (c.op == 2) continue;
-        int r = 0;
-        for (int s = 0; s < c.nseg; s++) r += (c.op == 0) ? c.K : (s ? c.Nseg[s] : c.N);
-        if (r > rmax) rmax = r;
-    }
-    const int rtarget = rmax > 384 ? rmax : 384;
-
     for (int i = 0; i < n; i++) {
         const TlgGemmCall &c = calls[i];
         if (c.op < 0 || c.op > 2 || c.nseg < 1 || c.nseg > TLG_MAXSEG || (c.nseg > 1 && c.op != 1))
             return tlg_fail(TLG_EINVAL, "tlg_dev_gemm_group: call %d: bad op/nseg", i);
         if (c.M < 0 || c.K < 0 || c.N < 0) return tlg_fail(TLG_EINVAL, "negative dimension");
-        Prob P;
+        Prob &P = probs[i];
         memset(&P, 0, sizeof P);
         P.kind = c.op == 0 ? PK_NN : (c.op == 1 ? PK_NT : PK_TN);
         P.C = c.C;
@@ -723,28 +924,68 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
         P.ldc = P.No;
         if (!vec || !c.C || R == 0 || P.Mo == 0 || P.No == 0)
             return tlg_fail(TLG_EINVAL, "tlg_dev_gemm_group: call %d needs aligned, non-empty operands", i);
-        P.tiles_n = cdiv(P.No, 64);
-        P.tiles = cdiv(P.Mo, 64) * P.tiles_n;
-        P.splits = 1;
-        P.rps = R;
-        if (P.kind == PK_TN && R > rtarget + rtarget / 2) {
-            int sp = cdiv(R, rtarget);
-            if (sp > 32) sp = 32;
-            int rps = cdiv(cdiv(R, sp), 32) * 32;
-            sp = cdiv(R, rps);
-            if (sp > 1 && ws_used + (size_t)sp * P.Mo * P.No <= ws_cap) {
-                P.splits = sp;
-                P.rps = rps;
-                P.ws = ws + ws_used;
-                ws_used += (size_t)sp * P.Mo * P.No;
+        Rtot[i] = R;
+        if (c.op != 2 && R > rmax) rmax = R;
+    }
+    // split problems aim for about the per-item work of the unsplit ones
+    const int rtarget = rmax > g_rtarget ? rmax : g_rtarget;
+
+    // tile shape: pinned, or the largest with >= g_min_waves waves of items
+    int ci = g_group_cfg;
+    if (ci < 0) {
+        int last = 3;
+        ci = -1;
+        for (int k = 0; k < 4 && g_cand[k] >= 0 && ci < 0; k++) {
+            last = g_cand[k];
+            const TileCfg &tc = kCfgs[g_cand[k]];
+            double items = 0;
+            for (int i = 0; i < n; i++) {
+                const double tiles = (double)cdiv(probs[i].Mo, tc.bm) * cdiv(probs[i].No, tc.bn);
+                const double sp = (probs[i].kind == PK_TN && Rtot[i] > rtarget + rtarget / 2)
+                                ? (double)cdiv(Rtot[i], rtarget) : 1.0;
+                items += tiles * sp;
             }
+            if (items >= g_min_waves * 256) ci = g_cand[k];
         }
-        P.item0 = items;
-        items += P.tiles * P.splits;
+        if (ci < 0) ci = last;                 // smallest candidate
+    }
+    // geometry of the chosen shape (the sweep variants 9-12 are 64x64 tiles)
+    const TileCfg &tc = kCfgs[(ci >= 0 && ci < kNumCfgs) ? ci : 3];
+
+    GroupArgs a;
+    a.nprob = 0;
+    add_reductions(a);
+    float *ws = g_tlg.ws + (size_t)g_ws_half * (g_tlg.ws_floats / 2);
+    size_t ws_used = 0;
+    const size_t ws_cap = g_tlg.ws_floats / 2;
+    int order[TLG_MAXPROB / 2];
+    double cost[TLG_MAXPROB / 2];
+    for (int i = 0; i < n; i++) {
+        Prob &P = probs[i];
+        P.tiles_n = cdiv(P.No, tc.bn);
+        P.tiles = cdiv(P.Mo, tc.bm) * P.tiles_n;
+        plan_split(P, Rtot[i], rtarget, ws, ws_used, ws_cap);
+        P.items = P.tiles * P.splits;
+        cost[i] = (double)P.rps;              // reduction steps per item
+        order[i] = i;
+    }
+    // longest item first (stable: ties keep call order)
+    for (int i = 1; i < n; i++)
+        for (int j = i; j > 0 && cost[order[j]] > cost[order[j - 1]]; j--) {
+            const int t = order[j]; order[j] = order[j - 1]; order[j - 1] = t;
+        }
+    // the reduction items of the previous launch are short: they go last
+    Prob red[TLG_MAXPROB];
+    const int nred = a.nprob;
+    for (int k = 0; k < nred; k++) red[k] = a.p[k];
+    a.nprob = 0;
+    for (int k = 0; k < n; k++) {
+        const Prob &P = probs[order[k]];
         a.p[a.nprob++] = P;
         if (P.splits > 1) g_pending[g_npending++] = P;
     }
-    launch_group_t<64, 64, 32, 2>(a, items, st);
+    for (int k = 0; k < nred; k++) a.p[a.nprob++] = red[k];
+    launch_group(ci, a, group_grid(a), st);
     TLG_HIP(hipGetLastError());
     if (g_npending) g_ws_half ^= 1;
     return TLG_OK;

@@ -56,6 +56,8 @@ SIGNATURES = {
     "tlg_dev_mfma_peak": (_i, [_vp, _i, _i, _vp]),
     "tlg_dev_gemm_group": (_i, [_vp, _i, _vp]),
     "tlg_dev_gemm_flush": (_i, [_vp]),
+    "tlg_group_kernel": (ctypes.c_char_p, []),
+    "tlg_tune_group": (_i, [_i]),
     "tlg_graph_begin": (_i, [_vp]),
     "tlg_graph_end": (_vp, [_vp]),
     "tlg_graph_launch": (_i, [_vp, _vp]),
