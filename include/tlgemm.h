@@ -109,9 +109,45 @@ int tlg_dev_gemm_group(const TlgGemmCall *calls, int n, void *stream);
 int tlg_dev_gemm_flush(void *stream);
 /* Kernel instance grouped launches use, as rocprofv3 names it. */
 const char *tlg_group_kernel(void);
-/* Tuning hook: tile configuration of grouped launches (3, 4 or 5; the
- * default 4 is 64x64 tiles with each wave over a quarter of every stage). */
+/* Tuning hook: pin the tile configuration of grouped launches (an index of
+ * the kernel's tile table; -1 = automatic: 64x64, 32x64 or 32x32 tiles,
+ * the largest that still gives the CUs about two waves of work items). */
 int tlg_tune_group(int cfg);
+
+/* ---- top-1 mixture-of-experts FFN --------------------------------------- */
+/* The MoE layer of tinylm.c with K = 1 routing and no router bias (the
+ * training default): N tokens of width D, E experts (1..64) of hidden width
+ * F.  Weights as the reference stores them per layer: wr [D*E], w1 and w3
+ * E x [D*F], w2 E x [F*D] (Weights.wr/w1/w3/w2 of one layer).  D and F must
+ * be multiples of 4 and the float operands 16-byte aligned (wr, gwr excepted).
+ *
+ * Forward, replaces moe_forward (tinylm.c:857-891): router logits fnorm.wr,
+ * softmax over all E into rprobs[N*E], top-1 expert assign[N] (strict-greater
+ * argmax, ties to the lowest index, tinylm.c:814-827) with gate[N] =
+ * rprobs[n][assign[n]], and out[n] = fin[n] + gate[n] * W2_e(silu(W1_e x) *
+ * W3_e x) with x = fnorm[n].
+ * Backward, replaces moe_backward (tinylm.c:895-947): from dout[N*D] and the
+ * forward's assign/gate/rprobs, sets d_fnorm[N*D] and adds into gwr, gw1,
+ * gw3, gw2 (expert GEMM grads, the router's softmax backward with the
+ * 0.01 * E * (cnt_e / N) / N load-balance term, dWr).
+ * Device-pointer forms enqueue on `stream` (asynchronous; scratch kept by the
+ * library, grown on demand).  Host-pointer forms are synchronous and abort on
+ * error like the GEMM drop-ins; operands inside a registered range are used
+ * in place. */
+int  tlg_dev_moe_grouped_fwd(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,
+                             const float *wr, const float *w1, const float *w3, const float *w2,
+                             int *assign, float *gate, float *rprobs, void *stream);
+int  tlg_dev_moe_grouped_bwd(const float *fnorm, const float *dout, float *d_fnorm, const int *assign,
+                             const float *gate, const float *rprobs, int N, int D, int F, int E,
+                             const float *wr, const float *w1, const float *w3, const float *w2,
+                             float *gwr, float *gw1, float *gw3, float *gw2, void *stream);
+void tlg_moe_grouped_fwd(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,
+                         const float *wr, const float *w1, const float *w3, const float *w2,
+                         int *assign, float *gate, float *rprobs);
+void tlg_moe_grouped_bwd(const float *fnorm, const float *dout, float *d_fnorm, const int *assign,
+                         const float *gate, const float *rprobs, int N, int D, int F, int E,
+                         const float *wr, const float *w1, const float *w3, const float *w2,
+                         float *gwr, float *gw1, float *gw3, float *gw2);
 
 /* ---- runtime wrappers for C host code ---------------------------------- */
 /* So the C step drivers (tinylm-c_amd/host) keep buffers and timing on the

@@ -154,11 +154,13 @@ extern "C" void tlg_shutdown(void)
 // Staging buffers for operands that are not registered: grown on demand,
 // kept for the life of the library.
 struct Stage { void *p = nullptr; size_t bytes = 0; };
-static Stage g_stage[3];
+static Stage g_stage[16];
 
+void tlg_moe_release(void);
 void tlg_shutdown_impl(void)
 {
     for (auto &s : g_stage) { (void)hipFree(s.p); s = Stage(); }
+    tlg_moe_release();
 }
 
 static int stage_ptr(int slot, size_t bytes, void **out)
@@ -370,3 +372,123 @@ extern "C" int tlg_dev_gemm_flush(void *stream)
 
 const char *tlg_group_kernel_name(void);
 extern "C" const char *tlg_group_kernel(void) { return tlg_group_kernel_name(); }
+
+// ------------------------------------------------------------- top-1 MoE --
+int tlg_moe_fwd_launch(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,
+                       const float *wr, const float *w1, const float *w3, const float *w2, int *assign,
+                       float *gate, float *rprobs, hipStream_t st);
+int tlg_moe_bwd_launch(const float *fnorm, const float *dout, float *d_fnorm, const int *assign,
+                       const float *gate, const float *rprobs, int N, int D, int F, int E, const float *wr,
+                       const float *w1, const float *w3, const float *w2, float *gwr, float *gw1, float *gw3,
+                       float *gw2, hipStream_t st);
+
+extern "C" int tlg_dev_moe_grouped_fwd(const float *fnorm, const float *fin, float *out, int N, int D, int F,
+                                       int E, const float *wr, const float *w1, const float *w3,
+                                       const float *w2, int *assign, float *gate, float *rprobs, void *stream)
+{
+    return tlg_moe_fwd_launch(fnorm, fin, out, N, D, F, E, wr, w1, w3, w2, assign, gate, rprobs,
+                              (hipStream_t)stream);
+}
+
+extern "C" int tlg_dev_moe_grouped_bwd(const float *fnorm, const float *dout, float *d_fnorm,
+                                       const int *assign, const float *gate, const float *rprobs, int N, int D,
+                                       int F, int E, const float *wr, const float *w1, const float *w3,
+                                       const float *w2, float *gwr, float *gw1, float *gw3, float *gw2,
+                                       void *stream)
+{
+    return tlg_moe_bwd_launch(fnorm, dout, d_fnorm, assign, gate, rprobs, N, D, F, E, wr, w1, w3, w2, gwr, gw1,
+                              gw3, gw2, (hipStream_t)stream);
+}
+
+// Host-pointer operands of a MoE call: device addresses (mirror or staging
+// slot) and which results go back to host memory at the end.
+struct HostOps {
+    int next = 0;
+    struct Back { void *host, *dev; size_t bytes; } back[8];
+    int nback = 0;
+    int rc = TLG_OK;
+    template <class P>
+    P *get(P *host, size_t bytes, bool upload, bool download)
+    {
+        if (rc) return nullptr;
+        void *dev = nullptr;
+        bool mirrored = false;
+        rc = resolve(next++, (const void *)host, bytes, upload, &dev, &mirrored);
+        if (rc) return nullptr;
+        if (download && !mirrored) back[nback++] = {(void *)host, dev, bytes};
+        return (P *)dev;
+    }
+    int finish()
+    {
+        for (int k = 0; k < nback && !rc; k++)
+            if (hipMemcpyAsync(back[k].host, back[k].dev, back[k].bytes, hipMemcpyDeviceToHost, g_tlg.stream) !=
+                hipSuccess)
+                rc = tlg_fail(TLG_EHIP, "MoE result copy");
+        if (!rc && hipStreamSynchronize(g_tlg.stream) != hipSuccess) rc = tlg_fail(TLG_EHIP, "MoE stream sync");
+        return rc;
+    }
+};
+
+static int host_moe_fwd(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,
+                        const float *wr, const float *w1, const float *w3, const float *w2, int *assign,
+                        float *gate, float *rprobs)
+{
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = init_locked(g_tlg.initialised ? g_tlg.device : 0);
+    if (rc) return rc;
+    if (N <= 0 || D <= 0 || F <= 0 || E <= 0) return N == 0 ? TLG_OK : tlg_fail(TLG_EINVAL, "MoE: bad shape");
+    const size_t nd = (size_t)N * D * 4, wf = (size_t)E * D * F * 4;
+    HostOps h;
+    const float *dfn = h.get(fnorm, nd, true, false), *dfi = h.get(fin, nd, true, false);
+    float *dout = h.get(out, nd, false, true);
+    const float *dwr = h.get(wr, (size_t)D * E * 4, true, false);
+    const float *d1 = h.get(w1, wf, true, false), *d3 = h.get(w3, wf, true, false), *d2 = h.get(w2, wf, true, false);
+    int *das = h.get(assign, (size_t)N * 4, false, true);
+    float *dg = h.get(gate, (size_t)N * 4, false, true), *dpr = h.get(rprobs, (size_t)N * E * 4, false, true);
+    if (h.rc) return h.rc;
+    rc = tlg_moe_fwd_launch(dfn, dfi, dout, N, D, F, E, dwr, d1, d3, d2, das, dg, dpr, g_tlg.stream);
+    if (rc) return rc;
+    return h.finish();
+}
+
+static int host_moe_bwd(const float *fnorm, const float *dout, float *d_fnorm, const int *assign,
+                        const float *gate, const float *rprobs, int N, int D, int F, int E, const float *wr,
+                        const float *w1, const float *w3, const float *w2, float *gwr, float *gw1, float *gw3,
+                        float *gw2)
+{
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    int rc = init_locked(g_tlg.initialised ? g_tlg.device : 0);
+    if (rc) return rc;
+    if (N <= 0 || D <= 0 || F <= 0 || E <= 0) return N == 0 ? TLG_OK : tlg_fail(TLG_EINVAL, "MoE: bad shape");
+    const size_t nd = (size_t)N * D * 4, wf = (size_t)E * D * F * 4;
+    HostOps h;
+    const float *dfn = h.get(fnorm, nd, true, false), *ddo = h.get(dout, nd, true, false);
+    float *ddf = h.get(d_fnorm, nd, false, true);
+    const int *das = h.get(assign, (size_t)N * 4, true, false);
+    const float *dg = h.get(gate, (size_t)N * 4, true, false), *dpr = h.get(rprobs, (size_t)N * E * 4, true, false);
+    const float *dwr = h.get(wr, (size_t)D * E * 4, true, false);
+    const float *d1 = h.get(w1, wf, true, false), *d3 = h.get(w3, wf, true, false), *d2 = h.get(w2, wf, true, false);
+    float *gr = h.get(gwr, (size_t)D * E * 4, true, true);
+    float *g1 = h.get(gw1, wf, true, true), *g3 = h.get(gw3, wf, true, true), *g2 = h.get(gw2, wf, true, true);
+    if (h.rc) return h.rc;
+    rc = tlg_moe_bwd_launch(dfn, ddo, ddf, das, dg, dpr, N, D, F, E, dwr, d1, d3, d2, gr, g1, g3, g2, g_tlg.stream);
+    if (rc) return rc;
+    return h.finish();
+}
+
+extern "C" void tlg_moe_grouped_fwd(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,
+                                    const float *wr, const float *w1, const float *w3, const float *w2,
+                                    int *assign, float *gate, float *rprobs)
+{
+    die_on(host_moe_fwd(fnorm, fin, out, N, D, F, E, wr, w1, w3, w2, assign, gate, rprobs), "tlg_moe_grouped_fwd");
+}
+
+extern "C" void tlg_moe_grouped_bwd(const float *fnorm, const float *dout, float *d_fnorm, const int *assign,
+                                    const float *gate, const float *rprobs, int N, int D, int F, int E,
+                                    const float *wr, const float *w1, const float *w3, const float *w2,
+                                    float *gwr, float *gw1, float *gw3, float *gw2)
+{
+    die_on(host_moe_bwd(fnorm, dout, d_fnorm, assign, gate, rprobs, N, D, F, E, wr, w1, w3, w2, gwr, gw1, gw3,
+                        gw2),
+           "tlg_moe_grouped_bwd");
+}

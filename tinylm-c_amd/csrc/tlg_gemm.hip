@@ -410,6 +410,15 @@ struct Prob {
     int kind, nseg;
     int tiles_n, tiles, splits, rps;
     int items;            // work items: tiles * splits, or reduction chunks
+    // Expert-batched problem (nexp > 0): the rows of a top-1 MoE layer are
+    // grouped by expert, expert e owning rows [eoff[e], eoff[e+1]) of every
+    // row operand.  NN / NT: the output rows are expert rows and the weight
+    // operand B of expert e is B + e*es.  TN: the reduction runs over expert
+    // rows in slices of rps, and the output of expert e is C + e*es.  `unit`
+    // is the row extent of one item (BM for NN / NT, rps for TN).
+    const int *eoff;
+    long long es;
+    int nexp, unit;
     Seg seg[TLG_MAXSEG];
 };
 struct GroupArgs {
@@ -417,9 +426,92 @@ struct GroupArgs {
     Prob p[TLG_MAXPROB];
 };
 
+// Real work items of an expert-batched problem, from the device-resident
+// row offsets: sum over experts of ceil(rows_e / unit) row units, times the
+// column tiles (NN / NT) or the output tiles (TN).
+__device__ __forceinline__ int expert_items(const Prob &P)
+{
+    int units = 0;
+    for (int e = 0; e < P.nexp; e++) {
+        const int c = P.eoff[e + 1] - P.eoff[e];
+        units += c > 0 ? (c + P.unit - 1) / P.unit : 0;
+    }
+    return units * (P.kind == PK_TN ? P.tiles : P.tiles_n);
+}
+
+// Item -> (expert e, row unit t of that expert, first partial slot of e).
+// Returns false when the item is past the experts' real work.
+__device__ __forceinline__ bool expert_of(const Prob &P, int t, int *e_out, int *t_out, int *base,
+                                          int *rows, int *slot0)
+{
+    int slot = 0;
+    for (int e = 0; e < P.nexp; e++) {
+        const int b = P.eoff[e], c = P.eoff[e + 1] - b;
+        const int n = c > 0 ? (c + P.unit - 1) / P.unit : 0;
+        if (t < n) { *e_out = e; *t_out = t; *base = b; *rows = c; *slot0 = slot; return true; }
+        t -= n;
+        slot += n;
+    }
+    return false;
+}
+
+template <class T, int LA, int LB>
+__device__ __forceinline__ void expert_tile(float *smem, const Prob &P, int local)
+{
+    f32x16 acc[T::FM][T::FN][T::NCH];
+    int e, t, base, rows, slot0;
+    if (P.kind != PK_TN) {
+        if (!expert_of(P, local / P.tiles_n, &e, &t, &base, &rows, &slot0)) return;
+        const int i0 = t * T::BM, j0 = (local % P.tiles_n) * T::BN;
+        zero_acc(acc);
+        for (int k = 0; k < P.nseg; k++) {
+            const Seg &s = P.seg[k];
+            tile_accumulate<T, LA, LB, true>(smem, s.A + (size_t)base * s.lda, s.B + (size_t)e * P.es, s.lda,
+                                             s.ldb, i0, j0, rows, P.No, 0, s.R, acc);
+        }
+        tile_store<T>(acc, P.C + (size_t)base * P.ldc, P.ldc, P.beta, rows, P.No, i0, j0, smem);
+    } else {
+        if (!expert_of(P, local / P.tiles, &e, &t, &base, &rows, &slot0)) return;
+        const int tile = local % P.tiles;
+        const int i0 = (tile / P.tiles_n) * T::BM, j0 = (tile % P.tiles_n) * T::BN;
+        const int rbeg = base + t * P.unit, rend = min(base + rows, rbeg + P.unit);
+        const Seg &s = P.seg[0];
+        zero_acc(acc);
+        tile_accumulate<T, LA, LB, true>(smem, s.A, s.B, s.lda, s.ldb, i0, j0, P.Mo, P.No, rbeg, rend, acc);
+        tile_store<T>(acc, (float *)P.ws + (size_t)(slot0 + t) * P.Mo * P.No, P.No, 0, P.Mo, P.No, i0, j0,
+                      smem);
+    }
+}
+
+// Reduction of an expert TN problem: C_e (beta ? += : =) the sum of expert
+// e's partial slots, in slot order.
+__device__ __forceinline__ void expert_reduce(const Prob &P, int local)
+{
+    const size_t n = (size_t)P.Mo * P.No;
+    const int chunks = (int)((n + TLG_RED_CHUNK - 1) / TLG_RED_CHUNK);
+    const int e = local / chunks;
+    int slot0 = 0;
+    for (int k = 0; k < e; k++) {
+        const int c = P.eoff[k + 1] - P.eoff[k];
+        slot0 += c > 0 ? (c + P.unit - 1) / P.unit : 0;
+    }
+    const int c = P.eoff[e + 1] - P.eoff[e];
+    const int ns = c > 0 ? (c + P.unit - 1) / P.unit : 0;
+    const size_t e0 = (size_t)(local % chunks) * TLG_RED_CHUNK;
+    const size_t e1 = e0 + TLG_RED_CHUNK < n ? e0 + TLG_RED_CHUNK : n;
+    float *C = P.C + (size_t)e * P.es;
+    if (ns == 0) {
+        if (!P.beta)
+            for (size_t i = e0 + threadIdx.x; i < e1; i += blockDim.x) C[i] = 0.f;
+        return;
+    }
+    reduce_range(P.ws + (size_t)slot0 * n, C, P.No, P.No, ns, P.beta, e0, e1, n);
+}
+
 template <class T, int LA, int LB>
 __device__ __forceinline__ void group_tile(float *smem, const Prob &P, int local)
 {
+    if (P.nexp) { expert_tile<T, LA, LB>(smem, P, local); return; }
     const int z = local / P.tiles, tile = local % P.tiles;
     const int i0 = (tile / P.tiles_n) * T::BM, j0 = (tile % P.tiles_n) * T::BN;
     f32x16 acc[T::FM][T::FN][T::NCH];
@@ -449,7 +541,8 @@ __device__ __forceinline__ int group_item(const GroupArgs &g, int b, int *local)
     const int x = b & 7;
     int slot = b >> 3;
     for (int p = 0; p < g.nprob; p++) {
-        const int n = g.p[p].items;
+        // expert-batched GEMMs: the real item count, known only on the device
+        const int n = (g.p[p].nexp && g.p[p].kind != PK_RED) ? expert_items(g.p[p]) : g.p[p].items;
         const int lo = (x * n) >> 3, hi = ((x + 1) * n) >> 3;
         if (slot < hi - lo) { *local = lo + slot; return p; }
         slot -= hi - lo;
@@ -470,6 +563,7 @@ __global__ __launch_bounds__(256) void k_group(GroupArgs g)
     case PK_NT: group_tile<T, RC, RC>(smem, P, local); break;
     case PK_TN: group_tile<T, OC, OC>(smem, P, local); break;
     default: {
+        if (P.nexp) { expert_reduce(P, local); break; }
         const size_t n = (size_t)P.Mo * P.No;
         const size_t e0 = (size_t)local * TLG_RED_CHUNK;
         const size_t e1 = e0 + TLG_RED_CHUNK < n ? e0 + TLG_RED_CHUNK : n;
@@ -988,6 +1082,124 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
     launch_group(ci, a, group_grid(a), st);
     TLG_HIP(hipGetLastError());
     if (g_npending) g_ws_half ^= 1;
+    return TLG_OK;
+}
+
+// ----------------------------------------------- expert-batched launch --
+// One launch runs `n` expert-batched GEMMs (every expert of each), then, if
+// any is a TN problem, one more launch adds their partial slots into the
+// outputs.  Rows per expert live on the device (eoff), so the host sizes the
+// grid for the worst case: ceil(rows_e / u) summed over experts is at most
+// rows / u + E units of u rows.
+int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E, int rows, hipStream_t st)
+{
+    if (n <= 0) return TLG_OK;
+    int rc = tlg_ensure_init();
+    if (rc) return rc;
+    if (n > TLG_MAXPROB / 2) return tlg_fail(TLG_EINVAL, "expert launch: at most %d calls", TLG_MAXPROB / 2);
+    if (!eoff || E < 1 || rows < 0) return tlg_fail(TLG_EINVAL, "expert launch: bad row offsets");
+    if (rows == 0) return TLG_OK;
+    // the partial slots below reuse the whole workspace
+    rc = tlg_group_flush_launch(st);
+    if (rc) return rc;
+
+    const int ci = 3;
+    const TileCfg &tc = kCfgs[ci];
+    Prob probs[TLG_MAXPROB / 2];
+    int rmax = 0;
+    for (int i = 0; i < n; i++) {
+        const TlgExpertCall &c = calls[i];
+        if (c.op < 0 || c.op > 2 || c.nseg < 1 || c.nseg > 2 || (c.nseg > 1 && c.op != 1))
+            return tlg_fail(TLG_EINVAL, "expert launch: call %d: bad op/nseg", i);
+        Prob &P = probs[i];
+        memset(&P, 0, sizeof P);
+        P.kind = c.op == 0 ? PK_NN : (c.op == 1 ? PK_NT : PK_TN);
+        P.C = c.C;
+        P.beta = c.beta ? 1 : 0;
+        P.nseg = c.nseg;
+        P.eoff = eoff;
+        P.nexp = E;
+        P.es = c.es;
+        int R = 0;
+        bool vec = c.C && (c.es % 4 == 0);
+        for (int s = 0; s < c.nseg; s++) {
+            const int Ns = s ? c.Nseg[s] : c.N;
+            Seg &g = P.seg[s];
+            g.A = c.A[s]; g.B = c.B[s];
+            switch (c.op) {
+            case 0: P.No = c.N; g.R = c.K; g.lda = c.K; g.ldb = c.N; break;
+            case 1: P.No = c.K; g.R = Ns; g.lda = Ns; g.ldb = Ns; break;
+            default: P.Mo = c.K; P.No = c.N; g.R = rows; g.lda = c.K; g.ldb = c.N; break;
+            }
+            R += g.R;
+            vec = vec && g.A && g.B && al16(g.A) && al16(g.B) && g.lda % 4 == 0 && g.ldb % 4 == 0 && g.R > 0;
+        }
+        P.ldc = P.No;
+        if (!vec || P.No <= 0 || (c.op == 2 && P.Mo <= 0) || P.No % 4 || P.Mo % 4)
+            return tlg_fail(TLG_EINVAL, "expert launch: call %d needs aligned operands, widths %% 4 == 0", i);
+        if (c.op != 2 && R > rmax) rmax = R;
+    }
+    // reduction slices of the TN problems: about the reduction length of the
+    // row problems of the launch, halved until the partials fit
+    int rps = cdiv(rmax > g_rtarget ? rmax : g_rtarget, 64) * 64;
+    auto need = [&](int u) {
+        size_t t = 0;
+        for (int i = 0; i < n; i++)
+            if (probs[i].kind == PK_TN) t += (size_t)(rows / u + E) * probs[i].Mo * probs[i].No;
+        return t;
+    };
+    while (need(rps) > g_tlg.ws_floats && rps < rows) rps *= 2;
+    if (need(rps) > g_tlg.ws_floats)
+        return tlg_fail(TLG_ENOMEM, "expert launch: %d experts' partials exceed the workspace", E);
+
+    GroupArgs a, red;
+    a.nprob = red.nprob = 0;
+    size_t used = 0;
+    int order[TLG_MAXPROB / 2];
+    for (int i = 0; i < n; i++) {
+        Prob &P = probs[i];
+        P.tiles_n = cdiv(P.No, tc.bn);
+        if (P.kind == PK_TN) {
+            P.tiles = cdiv(P.Mo, tc.bm) * P.tiles_n;
+            P.unit = rps;
+            P.rps = rps;
+            P.items = P.tiles * (rows / rps + E);
+            P.ws = g_tlg.ws + used;
+            used += (size_t)(rows / rps + E) * P.Mo * P.No;
+        } else {
+            P.unit = tc.bm;
+            P.items = (cdiv(rows, tc.bm) + E) * P.tiles_n;
+        }
+        order[i] = i;
+    }
+    // longest item first: TN items run rps rows, the others their full R
+    auto cost = [&](const Prob &P) {
+        int r = 0;
+        for (int s = 0; s < P.nseg; s++) r += P.seg[s].R;
+        return P.kind == PK_TN ? P.unit : r;
+    };
+    for (int i = 1; i < n; i++)
+        for (int j = i; j > 0 && cost(probs[order[j]]) > cost(probs[order[j - 1]]); j--) {
+            const int t = order[j]; order[j] = order[j - 1]; order[j - 1] = t;
+        }
+    for (int k = 0; k < n; k++) {
+        const Prob &P = probs[order[k]];
+        a.p[a.nprob++] = P;
+        if (P.kind == PK_TN) {
+            Prob r = P;
+            r.kind = PK_RED;
+            r.items = E * (int)(((size_t)P.Mo * P.No + TLG_RED_CHUNK - 1) / TLG_RED_CHUNK);
+            red.p[red.nprob++] = r;
+        }
+    }
+    // an XCD's share of the real items can exceed its share of the upper
+    // bound by one per expert problem
+    launch_group(ci, a, group_grid(a) + 8 * n, st);
+    TLG_HIP(hipGetLastError());
+    if (red.nprob) {
+        launch_group(ci, red, group_grid(red), st);
+        TLG_HIP(hipGetLastError());
+    }
     return TLG_OK;
 }
 

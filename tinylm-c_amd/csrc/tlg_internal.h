@@ -41,3 +41,22 @@ int tlg_zero_launch(float *dst, size_t n, hipStream_t st);
 int tlg_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len, int *splits);
 int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st);
 int tlg_group_flush_launch(hipStream_t st);
+
+// One GEMM over every expert of a top-1 MoE layer whose token rows are
+// grouped by expert: expert e owns rows [eoff[e], eoff[e+1]) of each row
+// operand (eoff: E+1 ints in device memory).  Dimensions use the labels of
+// the reference's primitives with M = the expert's row count:
+//   op 0 (mm):     C[rows]  = A[rows] B_e                 B_e = B + e*es
+//   op 1 (mm_bt):  C[rows] (beta)= sum_s A_s[rows] B_{s,e}^T  (nseg <= 2)
+//   op 2 (mm_atb): C_e (beta)= A[rows]^T B[rows]          C_e = C + e*es
+struct TlgExpertCall {
+    int op, beta;
+    float *C;
+    int K, N;
+    int nseg;
+    const float *A[2];
+    const float *B[2];
+    int Nseg[2];
+    long long es;
+};
+int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E, int rows, hipStream_t st);

@@ -62,6 +62,12 @@ SIGNATURES = {
     "tlg_graph_end": (_vp, [_vp]),
     "tlg_graph_launch": (_i, [_vp, _vp]),
     "tlg_graph_destroy": (_i, [_vp]),
+    "tlg_dev_moe_grouped_fwd": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "tlg_dev_moe_grouped_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp,
+                                     _vp, _vp, _vp, _vp, _vp]),
+    "tlg_moe_grouped_fwd": (None, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "tlg_moe_grouped_bwd": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp,
+                                   _vp, _vp, _vp, _vp]),
 }
 
 
@@ -111,6 +117,20 @@ class Lib:
 
     def zero(self, p, n, stream=0):
         return self.check(self.dll.tlg_dev_zero(p, n, stream), "tlg_dev_zero")
+
+    def moe_fwd(self, fnorm, fin, out, N, D, F, E, wr, w1, w3, w2, assign, gate, rprobs, stream=0):
+        """Device-pointer top-1 MoE forward (tinylm.c:857-891)."""
+        return self.check(self.dll.tlg_dev_moe_grouped_fwd(fnorm, fin, out, N, D, F, E, wr, w1, w3, w2,
+                                                           assign, gate, rprobs, stream),
+                          "tlg_dev_moe_grouped_fwd")
+
+    def moe_bwd(self, fnorm, dout, d_fnorm, assign, gate, rprobs, N, D, F, E, wr, w1, w3, w2,
+                gwr, gw1, gw3, gw2, stream=0):
+        """Device-pointer top-1 MoE backward (tinylm.c:895-947)."""
+        return self.check(self.dll.tlg_dev_moe_grouped_bwd(fnorm, dout, d_fnorm, assign, gate, rprobs,
+                                                           N, D, F, E, wr, w1, w3, w2, gwr, gw1, gw3,
+                                                           gw2, stream),
+                          "tlg_dev_moe_grouped_bwd")
 
     def kernel_name(self, op, M, K, N):
         """(rocprof kernel name, splits) a device call of op 'mm'/'mm_bt'/'mm_atb' uses."""
