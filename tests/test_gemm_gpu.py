@@ -148,6 +148,66 @@ def test_decode_rows(lib, orc, M, K, N):
     assert normwise_rel(run_mm_atb(lib, Q, X, dY), orc.mm_atb_f64(Q.copy(), X, dY)) <= TOL
 
 
+GEMV_SHAPES = [(1, 1, 1), (1, 5003, 65), (2, 384, 96), (3, 131, 259), (5, 64, 1), (6, 1024, 384),
+               (7, 9, 700), (8, 2048, 384), (8, 384, 1024)]
+
+
+@pytest.mark.parametrize("M,K,N", GEMV_SHAPES, ids=[f"{m}x{k}x{n}" for m, k, n in GEMV_SHAPES])
+def test_gemv_kernels(lib, M, K, N):
+    """M <= 8 mm / mm_bt take the weight-streaming GEMV kernels; ragged K/N,
+    every row bucket, set semantics on a NaN-filled Y, accumulate onto a
+    prefill, against the fp64 oracle."""
+    from oracle import Oracle
+    orc = Oracle()
+    print("gemv", M, K, N, flush=True)
+    assert lib.kernel_name("mm", M, K, N)[0].startswith("k_gemv")
+    assert lib.kernel_name("mm_bt", M, K, N)[0].startswith("k_gemv")
+    X = seeded((M, K), 1.0, "X")
+    W = seeded((K, N), 0.02, "W")
+    dY = seeded((M, N), 1.0, "dY")
+    P = seeded((M, K), 1.0, "P")
+    assert normwise_rel(run_mm(lib, X, W), orc.mm_f64(X, W)) <= TOL
+    got = run_mm_bt(lib, P, dY, W)
+    ref = orc.mm_bt_f64(P.copy(), dY, W)
+    assert normwise_rel(got, ref) <= TOL
+    assert normwise_rel(got - P, ref - P) <= TOL * 10
+
+
+def test_gemv_group(lib):
+    """A grouped launch of M <= 8 calls (the decode runs: several mm on one
+    input, an mm_bt chain into one output) against fp64; then the same with
+    one call at M > 8, which sends the whole group to the MFMA tiles."""
+    from oracle import Oracle
+    orc = Oracle()
+    t = _torch()
+    for M in (3, 8, 9):
+        X = seeded((M, 384), 1.0, "gX")
+        Ws = [seeded((384, n), 0.02, f"gW{n}") for n in (96, 1024)]
+        dYs = [seeded((M, n), 1.0, f"gdY{n}") for n in (384, 96, 1024)]
+        Wb = [seeded((384, n), 0.02, f"gWb{n}") for n in (384, 96, 1024)]
+        P = seeded((M, 384), 1.0, "gP")
+        keep = [dev(a) for a in [X] + Ws + dYs + Wb]
+        x, w96, w1024, d384, d96, d1024, b384, b96, b1024 = keep
+        y96 = t.full((M, 96), float("nan"), device="cuda")
+        y1024 = t.full((M, 1024), float("nan"), device="cuda")
+        dx = dev(P)
+        lib.group([
+            dict(op="mm", C=y96.data_ptr(), M=M, K=384, N=96, A=[x.data_ptr()], B=[w96.data_ptr()]),
+            dict(op="mm", C=y1024.data_ptr(), M=M, K=384, N=1024, A=[x.data_ptr()], B=[w1024.data_ptr()]),
+            dict(op="mm_bt", beta=1, C=dx.data_ptr(), M=M, K=384, N=384, Nseg=[384, 96, 1024],
+                 A=[d384.data_ptr(), d96.data_ptr(), d1024.data_ptr()],
+                 B=[b384.data_ptr(), b96.data_ptr(), b1024.data_ptr()]),
+        ], stream())
+        assert normwise_rel(y96.cpu().numpy(), orc.mm_f64(X, Ws[0])) <= TOL
+        assert normwise_rel(y1024.cpu().numpy(), orc.mm_f64(X, Ws[1])) <= TOL
+        ref = P.astype(np.float64)
+        for a, b in zip(dYs, Wb):
+            ref = ref + a.astype(np.float64) @ b.astype(np.float64).T
+        assert normwise_rel(dx.cpu().numpy(), ref) <= TOL
+        if M <= 8:
+            assert lib.tlg_group_kernel().decode().startswith("k_gemv")
+
+
 def test_empty_dimensions(lib):
     t = _torch()
     # K = 0: mm clears Y (tinylm.c:461), the accumulating forms leave theirs

@@ -715,6 +715,11 @@ int tlg_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len, int *s
         if (splits) *splits = 0;
         return TLG_OK;
     }
+    if (tlg_gemv_fits(kind, Mo)) {
+        snprintf(buf, (size_t)len, "%s", tlg_gemv_kernel_name(Mo));
+        if (splits) *splits = 1;
+        return TLG_OK;
+    }
     const GemmPlan p = plan_gemm(Mo, No, R);
     const TileCfg &c = kCfgs[p.ci];
     const int la = (kind == TLG_TN) ? OC : RC;
@@ -768,6 +773,8 @@ int tlg_gemm_launch(TlgKind kind, const float *A, const float *B, float *C,
     rc = tlg_group_flush_launch(st);
     if (rc) return rc;
 
+    if (tlg_gemv_fits(kind, Mo)) return tlg_gemv_launch(kind, A, B, C, Mo, No, R, lda, ldb, ldc, beta, st);
+
     const int la = (kind == TLG_TN) ? OC : RC;
     const int lb = (kind == TLG_NT) ? RC : OC;
     // float4 staging needs 16-byte aligned operands whose contiguous extent
@@ -812,6 +819,7 @@ static double g_min_waves = 2.0;
 static int g_cand[4] = {3, 13, 15, -1};   // 64x64, 32x64, 32x32
 static int g_rtarget = 384;
 static int g_group_last = 3;          // shape of the most recent grouped launch
+static const char *g_group_last_name = nullptr;   // set when that launch was a GEMV group
 
 static void group_env(void)
 {
@@ -853,6 +861,7 @@ static void launch_group(int ci, const GroupArgs &a, int grid, hipStream_t st)
     default: hipLaunchKernelGGL((k_group<T3>), dim3(grid), dim3(256), 0, st, a); break;
     }
     g_group_last = ci;
+    g_group_last_name = nullptr;
 }
 
 extern "C" int tlg_tune_group(int cfg)
@@ -865,6 +874,7 @@ extern "C" int tlg_tune_group(int cfg)
 
 const char *tlg_group_kernel_name(void)
 {
+    if (g_group_last_name) return g_group_last_name;
     switch (g_group_last) {
     case 0: return "k_group<Tile<128, 128, 16, 2, 1, 2, 0> >";
     case 1: return "k_group<Tile<128, 64, 32, 2, 1, 2, 0> >";
@@ -958,6 +968,23 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
     if (rc) return rc;
     group_env();
     if (n > TLG_MAXPROB / 2) return tlg_fail(TLG_EINVAL, "tlg_dev_gemm_group: at most %d calls", TLG_MAXPROB / 2);
+
+    // Decode runs (every call mm / mm_bt at M <= 8) go to the GEMV kernels.
+    bool gemv = true;
+    int mmax = 1;
+    for (int i = 0; i < n && gemv; i++) {
+        gemv = (calls[i].op == 0 || calls[i].op == 1) && calls[i].M >= 1 && calls[i].M <= 8 && calls[i].K > 0 &&
+               calls[i].N > 0 && calls[i].nseg >= 1 && calls[i].nseg <= TLG_MAXSEG &&
+               (calls[i].nseg == 1 || calls[i].op == 1);
+        if (calls[i].M > mmax) mmax = calls[i].M;
+    }
+    if (gemv) {
+        rc = tlg_group_flush_launch(st);
+        if (rc) return rc;
+        rc = tlg_gemv_group_launch(calls, n, st);
+        g_group_last_name = tlg_gemv_kernel_name(mmax);
+        return rc;
+    }
 
     // Pending reductions write their C; a call that touches such a range must
     // see them first, so they go in a launch of their own.

@@ -60,3 +60,10 @@ struct TlgExpertCall {
     long long es;
 };
 int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E, int rows, hipStream_t st);
+
+// M <= 8 forms of mm / mm_bt (tlg_gemv.hip): weight-streaming GEMV kernels.
+bool tlg_gemv_fits(TlgKind kind, int Mo);
+int tlg_gemv_launch(TlgKind kind, const float *A, const float *B, float *C, int Mo, int No, int R, int lda,
+                    int ldb, int ldc, int beta, hipStream_t st);
+int tlg_gemv_group_launch(const TlgGemmCall *calls, int n, hipStream_t st);
+const char *tlg_gemv_kernel_name(int M);
