@@ -107,6 +107,8 @@ typedef struct {
 } TlgGemmCall;
 int tlg_dev_gemm_group(const TlgGemmCall *calls, int n, void *stream);
 int tlg_dev_gemm_flush(void *stream);
+/* Number of split reductions still pending (what a flush would launch). */
+int tlg_dev_gemm_pending(void);
 /* Kernel instance grouped launches use, as rocprofv3 names it. */
 const char *tlg_group_kernel(void);
 /* Tuning hook: pin the tile configuration of grouped launches (an index of

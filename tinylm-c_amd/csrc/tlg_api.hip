@@ -370,6 +370,9 @@ extern "C" int tlg_dev_gemm_flush(void *stream)
     return rc ? rc : tlg_group_flush_launch((hipStream_t)stream);
 }
 
+int tlg_group_pending(void);
+extern "C" int tlg_dev_gemm_pending(void) { return tlg_group_pending(); }
+
 const char *tlg_group_kernel_name(void);
 extern "C" const char *tlg_group_kernel(void) { return tlg_group_kernel_name(); }
 

@@ -551,9 +551,8 @@ __device__ __forceinline__ int group_item(const GroupArgs &g, int b, int *local)
 }
 
 template <class T>
-__global__ __launch_bounds__(256) void k_group(GroupArgs g)
+__device__ __forceinline__ void group_body(const GroupArgs &g, float *smem)
 {
-    __shared__ __attribute__((aligned(16))) float smem[T::lds_max()];
     int local = 0;
     const int p = group_item(g, blockIdx.x, &local);
     if (p < 0) return;
@@ -570,6 +569,22 @@ __global__ __launch_bounds__(256) void k_group(GroupArgs g)
         reduce_range(P.ws, P.C, P.No, P.ldc, P.splits, P.beta, e0, e1, n);
     }
     }
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void k_group(GroupArgs g)
+{
+    __shared__ __attribute__((aligned(16))) float smem[T::lds_max()];
+    group_body<T>(g, smem);
+}
+
+// The same code for the expert-batched launches of the MoE layer, under its
+// own name so profiles separate MoE launches from the dense grouped GEMMs.
+template <class T>
+__global__ __launch_bounds__(256) void k_expert_group(GroupArgs g)
+{
+    __shared__ __attribute__((aligned(16))) float smem[T::lds_max()];
+    group_body<T>(g, smem);
 }
 
 __global__ void k_zero(float *__restrict__ p, size_t n)
@@ -811,12 +826,14 @@ static int g_npending = 0;
 static int g_ws_half = 0;
 
 // Tile shape of a grouped launch (all problems of a group share it): the
-// largest of 128x128, 128x64 and 64x64 that still gives every CU about
-// `g_min_waves` workgroups, so big groups load fewer bytes per flop and small
-// ones keep the CUs busy.  tlg_tune_group pins one shape for sweeps.
+// first candidate that still gives every CU about `g_min_waves` workgroups,
+// else the last.  Measured on MI355X over the m3 training step, 64x64 tiles
+// alone are as fast as any mix with 32x64 / 32x32 / 128x128 tiles (within
+// 0.5%), so the default list holds 64x64 only; TLG_GROUP_CANDS overrides it
+// and tlg_tune_group pins one shape for sweeps.
 static int g_group_cfg = -1;
 static double g_min_waves = 2.0;
-static int g_cand[4] = {3, 13, 15, -1};   // 64x64, 32x64, 32x32
+static int g_cand[4] = {3, -1, -1, -1};   // 64x64
 static int g_rtarget = 384;
 static int g_group_last = 3;          // shape of the most recent grouped launch
 static const char *g_group_last_name = nullptr;   // set when that launch was a GEMV group
@@ -918,6 +935,8 @@ static int add_reductions(GroupArgs &a)
     g_npending = 0;
     return TLG_OK;
 }
+
+int tlg_group_pending(void) { return g_npending; }
 
 int tlg_group_flush_launch(hipStream_t st)
 {
@@ -1130,8 +1149,7 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     rc = tlg_group_flush_launch(st);
     if (rc) return rc;
 
-    const int ci = 3;
-    const TileCfg &tc = kCfgs[ci];
+    const TileCfg &tc = kCfgs[3];      // k_expert_group<T3>: 64 x 64 tiles
     Prob probs[TLG_MAXPROB / 2];
     int rmax = 0;
     for (int i = 0; i < n; i++) {
@@ -1221,10 +1239,11 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     }
     // an XCD's share of the real items can exceed its share of the upper
     // bound by one per expert problem
-    launch_group(ci, a, group_grid(a) + 8 * n, st);
+    static_assert(sizeof(GroupArgs) <= 4096, "kernel arguments");
+    hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(a) + 8 * n), dim3(256), 0, st, a);
     TLG_HIP(hipGetLastError());
     if (red.nprob) {
-        launch_group(ci, red, group_grid(red), st);
+        hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(red)), dim3(256), 0, st, red);
         TLG_HIP(hipGetLastError());
     }
     return TLG_OK;

@@ -27,6 +27,7 @@ struct TlRun {
     int nev;
     double lflops[TL_MAXLAUNCH], lbytes[TL_MAXLAUNCH];
     int lkind[TL_MAXLAUNCH];             /* 0 grouped GEMM, 1 clear, 2 flush */
+    const char *lname[TL_MAXLAUNCH];     /* kernel of each launch (NULL: none) */
 };
 
 static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -199,6 +200,7 @@ static int group_launch(TlRun *r, Group *g, void *stream, int dry, int *launches
     note(r, *launches, 0, fl, by);
     int rc = dry ? 0 : mark(r, *launches, stream);
     if (!rc && !dry) rc = tlg_dev_gemm_group(g->call, g->n, stream);
+    if (!rc && !dry && *launches < TL_MAXLAUNCH) r->lname[*launches] = tlg_group_kernel();
     (*launches)++;
     g->n = g->nrd = 0;
     return rc;
@@ -261,6 +263,7 @@ static int grouped(TlRun *r, void *stream, int dry)
                 note(r, launches, 1, 0.0, 4.0 * (double)c->n);
                 if (!rc && !dry) rc = mark(r, launches, stream);
                 if (!rc && !dry) rc = tlg_dev_zero(ptr(r, c->out, c->out_off), c->n, stream);
+                if (!dry && launches < TL_MAXLAUNCH) r->lname[launches] = "k_zero";
                 launches++;
                 continue;
             }
@@ -307,7 +310,10 @@ static int grouped(TlRun *r, void *stream, int dry)
     /* the flush reduces the last launch's split partials (if any) */
     note(r, launches, 2, 0.0, 0.0);
     if (!rc && !dry) rc = mark(r, launches, stream);
+    /* the flush launches a kernel only if split partials are pending */
+    const int pending = dry ? 0 : tlg_dev_gemm_pending();
     if (!rc && !dry) rc = tlg_dev_gemm_flush(stream);
+    if (!rc && !dry && launches < TL_MAXLAUNCH) r->lname[launches] = pending > 0 ? tlg_group_kernel() : NULL;
     if (!rc && !dry) rc = mark(r, launches + 1, stream);
     free(set);
     free(gone);
@@ -324,6 +330,12 @@ int tl_run_time_launches(TlRun *r, void **events, int nevents, void *stream)
     r->ev = NULL;
     r->nev = 0;
     return rc;
+}
+
+const char *tl_run_launch_kernel(TlRun *r, int k)
+{
+    if (k < 0 || k >= TL_MAXLAUNCH) return NULL;
+    return r->lname[k];
 }
 
 int tl_run_launch_info(TlRun *r, int k, double *flops, double *bytes)

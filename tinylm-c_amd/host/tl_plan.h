@@ -105,6 +105,9 @@ int    tl_run_grouped_launches(TlRun *r);
  * 2 flush) and its algorithmic flops and compulsory bytes. */
 int    tl_run_time_launches(TlRun *r, void **events, int nevents, void *stream);
 int    tl_run_launch_info(TlRun *r, int k, double *flops, double *bytes);
+/* Kernel that launch k of the last timed step ran, as rocprofv3 names it
+ * (without "void " and the argument list), or NULL if nothing launched. */
+const char *tl_run_launch_kernel(TlRun *r, int k);
 /* Capture one step into a HIP graph and replay it (grouped != 0: the grouped
  * step, else call by call).  The graph is bound to
  * the pool copy current at capture; tl_run_graph_step replays the graph for

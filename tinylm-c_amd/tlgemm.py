@@ -56,6 +56,7 @@ SIGNATURES = {
     "tlg_dev_mfma_peak": (_i, [_vp, _i, _i, _vp]),
     "tlg_dev_gemm_group": (_i, [_vp, _i, _vp]),
     "tlg_dev_gemm_flush": (_i, [_vp]),
+    "tlg_dev_gemm_pending": (_i, []),
     "tlg_group_kernel": (ctypes.c_char_p, []),
     "tlg_tune_group": (_i, [_i]),
     "tlg_graph_begin": (_i, [_vp]),
@@ -291,6 +292,8 @@ class Host:
         d.tl_run_time_launches.restype = _i
         d.tl_run_launch_info.argtypes = [_vp, _i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
         d.tl_run_launch_info.restype = _i
+        d.tl_run_launch_kernel.argtypes = [_vp, _i]
+        d.tl_run_launch_kernel.restype = ctypes.c_char_p
         d.tl_run_call.argtypes = [_vp, _i, _vp]
         d.tl_run_call.restype = _i
         for n in ("mm", "mm_bt", "mm_atb"):
