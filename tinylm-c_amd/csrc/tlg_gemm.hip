@@ -194,17 +194,21 @@ __device__ __forceinline__ void tile_accumulate(float *__restrict__ smem, const 
     const int nsteps = (rend - rbeg + BK - 1) / BK;
     if (nsteps <= 0) return;
 
+    // Every prefetch is issued unconditionally: a stage past the end re-reads
+    // the last stage's (in-bounds) addresses and is never stored.  Loads under
+    // a branch would leave the compiler unsure how many are outstanding where
+    // the paths meet, and it would then wait for all of them, the prefetch
+    // included, before every LDS store.
+    auto stage_r = [&](int st) { return rbeg + min(st, nsteps - 1) * BK; };
     TileLoader<LA, BM, BK, VEC> la0, la1, la2;
     TileLoader<LB, BN, BK, VEC> lb0, lb1, lb2;
     la0.load(A, lda, i0, Mo, rbeg, rend, tid);
     lb0.load(B, ldb, j0, No, rbeg, rend, tid);
-    if (nsteps > 1) {
-        la1.load(A, lda, i0, Mo, rbeg + BK, rend, tid);
-        lb1.load(B, ldb, j0, No, rbeg + BK, rend, tid);
-    }
-    if (T::NR > 2 && nsteps > 2) {
-        la2.load(A, lda, i0, Mo, rbeg + 2 * BK, rend, tid);
-        lb2.load(B, ldb, j0, No, rbeg + 2 * BK, rend, tid);
+    la1.load(A, lda, i0, Mo, stage_r(1), rend, tid);
+    lb1.load(B, ldb, j0, No, stage_r(1), rend, tid);
+    if constexpr (T::NR > 2) {
+        la2.load(A, lda, i0, Mo, stage_r(2), rend, tid);
+        lb2.load(B, ldb, j0, No, stage_r(2), rend, tid);
     }
     la0.store(smem, tid);
     lb0.store(smem + SA, tid);
@@ -231,10 +235,8 @@ __device__ __forceinline__ void tile_accumulate(float *__restrict__ smem, const 
     // from, computes stage st, then moves stage st+1 from its register set
     // into the other LDS buffer.  NR = 3 keeps loads three stages ahead.
     auto step = [&](int st, auto &lac, auto &lbc, auto &lan, auto &lbn) {
-        if (st + T::NR < nsteps) {
-            lac.load(A, lda, i0, Mo, rbeg + (st + T::NR) * BK, rend, tid);
-            lbc.load(B, ldb, j0, No, rbeg + (st + T::NR) * BK, rend, tid);
-        }
+        lac.load(A, lda, i0, Mo, stage_r(st + T::NR), rend, tid);
+        lbc.load(B, ldb, j0, No, stage_r(st + T::NR), rend, tid);
         float *cur = smem + (st & 1) * (SA + SB);
         compute(cur, cur + SA);
         if (st + 1 < nsteps) {

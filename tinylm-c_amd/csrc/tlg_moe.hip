@@ -62,7 +62,16 @@ __global__ __launch_bounds__(256) void k_moe_route(const float *__restrict__ X, 
         for (int p = tid; p < 64 * E; p += 256) {
             const int t = p / E, e = p % E;
             float l = lg[p];
-            for (int d = 0; d < dn; d++) l = fmaf(xs[t][d], wsm[d * E + e], l);
+            int d = 0;
+            // the chain stays sequential; its LDS operands are fetched 8 ahead
+            for (; d + 8 <= dn; d += 8) {
+                float xv[8], wv[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) { xv[u] = xs[t][d + u]; wv[u] = wsm[(d + u) * E + e]; }
+#pragma unroll
+                for (int u = 0; u < 8; u++) l = fmaf(xv[u], wv[u], l);
+            }
+            for (; d < dn; d++) l = fmaf(xs[t][d], wsm[d * E + e], l);
             lg[p] = l;
         }
     }
