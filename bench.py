@@ -165,6 +165,49 @@ def read_traffic(kernel):
     return None
 
 
+def roof_time_ms(plan):
+    """Summed per-GEMM roofline time of a step: max(flops / MFMA peak,
+    compulsory bytes / HBM peak) per call, clears at HBM speed."""
+    roof_ms = 0.0
+    for c in plan.calls:
+        if c["op"] == "zero":
+            roof_ms += 4.0 * c["n"] / (PEAK_HBM_GBS * 1e9) * 1e3
+            continue
+        M, K, N = c["M"], c["K"], c["N"]
+        fl = 2.0 * M * K * N
+        out = M * N if c["op"] == "mm" else (M * K if c["op"] == "mm_bt" else K * N)
+        ins = {"mm": M * K + K * N, "mm_bt": M * N + K * N, "mm_atb": M * K + M * N}[c["op"]]
+        by = 4.0 * (ins + out * (1 if c["op"] == "mm" else 2))
+        roof_ms += max(fl / (PEAK_FP32_MFMA_TFLOPS * 1e12), by / (PEAK_HBM_GBS * 1e9)) * 1e3
+    return roof_ms
+
+
+def bench_train_config(lib, host, stream, name, steps):
+    """Another BASELINE training config (nano = configs[0], m8 = configs[2]):
+    the same grouped, graph-replayed GEMM step."""
+    cfg = TRAIN[name]
+    plan = host.plan_train(**cfg)
+    run = host.dll.tl_run_new(ctypes.byref(plan.raw), 1)
+    if not run:
+        raise RuntimeError("tl_run_new failed: " + lib.tlg_last_error().decode())
+    check(host.dll.tl_run_fill(run, 1234567891011, stream), "fill")
+    check(host.dll.tl_run_graph_build(run, stream, 1), "graph build")
+    step = lambda: host.dll.tl_run_graph_step(run, stream)  # noqa: E731
+    for _ in range(5):
+        check(step(), "warmup")
+    ms, _ = time_steps(lib, step, stream, steps)
+    per = ms / steps
+    roof = roof_time_ms(plan)
+    launches = host.dll.tl_run_grouped_launches(run)
+    host.dll.tl_run_free(run)
+    return {
+        "calls": len(plan.calls), "grouped_launches": launches, "gflop": round(plan.flops() / 1e9, 2),
+        "steps": steps, "ms_per_step": round(per, 4), "tok_s": round(cfg["R"] / (per * 1e-3), 1),
+        "tflops": round(plan.flops() / (per * 1e-3) / 1e12, 2),
+        "sum_of_gemm_roof_ms": round(roof, 4), "roof_frac": round(roof / per, 4),
+    }
+
+
 def bench_decode(lib, host, stream, steps, M=1, pool=6):
     """cfg3: per token 8 layers x 7 GEMVs + unembed at M rows, one grouped
     launch per GEMV run (q/k/v, o, w1/w3, w2, head: the reference runs glue
@@ -326,6 +369,7 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--moe-steps", type=int, default=20)
+    ap.add_argument("--other-steps", type=int, default=20, help="timed steps of the other training configs")
     ap.add_argument("--no-probes", action="store_true", help="skip the copy / MFMA peak probes")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -367,18 +411,7 @@ def main():
     log(f"[bench] timed {args.steps} steps: {ms_step:.4f} ms/step (wall {wall / args.steps * 1e3:.4f}), "
         f"{tok_s:,.0f} tok/s, {tflops:.1f} TFLOP/s")
 
-    # summed per-GEMM roofline time of the step: max(flops/peak, bytes/HBM)
-    roof_ms = 0.0
-    for c in plan.calls:
-        if c["op"] == "zero":
-            roof_ms += 4.0 * c["n"] / (PEAK_HBM_GBS * 1e9) * 1e3
-            continue
-        M, K, N = c["M"], c["K"], c["N"]
-        fl = 2.0 * M * K * N
-        out = M * N if c["op"] == "mm" else (M * K if c["op"] == "mm_bt" else K * N)
-        ins = {"mm": M * K + K * N, "mm_bt": M * N + K * N, "mm_atb": M * K + M * N}[c["op"]]
-        by = 4.0 * (ins + out * (1 if c["op"] == "mm" else 2))
-        roof_ms += max(fl / (PEAK_FP32_MFMA_TFLOPS * 1e12), by / (PEAK_HBM_GBS * 1e9)) * 1e3
+    roof_ms = roof_time_ms(plan)
 
     if grouped:
         groups = launch_census(lib, host, run, stream, args.census_reps)
@@ -408,6 +441,12 @@ def main():
         log(f"[census] {k}: {v['launches']} launches avg {v['avg_us']} us, share {v['share']}, "
             f"{v['tflops']} TFLOP/s")
 
+    others = {}
+    if args.other_steps > 0:
+        for name in TRAIN:
+            if name != args.config:
+                others[name] = bench_train_config(lib, host, stream, name, args.other_steps)
+                log(f"[train] {name}: {others[name]}")
     decode = {}
     if args.decode_steps > 0:
         for M in (1, 2, 4, 8):
@@ -466,6 +505,7 @@ def main():
             "algorithmic_flops_per_launch": round(dom["flops"] / dom["launches"]),
         },
         "kernels": census,
+        "other_configs": others,
         "decode_m1": decode.get(1),
         "decode": {str(k): v for k, v in decode.items()},
         "moe": moe,
