@@ -115,6 +115,11 @@ const char *tlg_group_kernel(void);
  * the kernel's tile table; -1 = automatic: 64x64, 32x64 or 32x32 tiles,
  * the largest that still gives the CUs about two waves of work items). */
 int tlg_tune_group(int cfg);
+/* Tuning hook: the automatic policy itself -- candidate tile configs (up to
+ * 3, first that yields min_waves x 256 work items wins, else the last; ncands
+ * 0 keeps the list), min_waves (<= 0 keeps it) and the target reduction
+ * steps per split work item (0 keeps it).  Applies to later launches. */
+int tlg_tune_group_policy(const int *cands, int ncands, double min_waves, int rtarget);
 
 /* ---- top-1 mixture-of-experts FFN --------------------------------------- */
 /* The MoE layer of tinylm.c with K = 1 routing and no router bias (the

@@ -62,11 +62,11 @@ __device__ __forceinline__ int xcd_remap(int b, int nb)
 
 // Stage one operand tile into registers.  OUTER = tile extent along the
 // operand's output index, rows/cols beyond `oext` or r beyond `rend` read 0.
-template <int LAY, int OUTER, int BK, bool VEC>
+template <int LAY, int OUTER, int BK, bool VEC, int NT>
 struct TileLoader {
     static constexpr int NCH = OUTER * BK / 4;        // float4 chunks per tile
-    static constexpr int PER = NCH / 256;             // chunks per thread
-    static_assert(NCH % 256 == 0, "tile must split evenly over 256 threads");
+    static constexpr int PER = NCH / NT;              // chunks per thread
+    static_assert(NCH % NT == 0, "tile must split evenly over the workgroup's threads");
     f32x4 v[PER];
     unsigned ok;                                      // bit q: chunk q in range
 
@@ -80,7 +80,7 @@ struct TileLoader {
         ok = 0;
 #pragma unroll
         for (int q = 0; q < PER; q++) {
-            const int e = tid + 256 * q;
+            const int e = tid + NT * q;
             int o, r;
             if (LAY == RC) { o = e / (BK / 4); r = (e % (BK / 4)) * 4; }
             else           { r = e / (OUTER / 4); o = (e % (OUTER / 4)) * 4; }
@@ -111,7 +111,7 @@ struct TileLoader {
     {
 #pragma unroll
         for (int q = 0; q < PER; q++) {
-            const int e = tid + 256 * q;
+            const int e = tid + NT * q;
             int o, r;
             if (LAY == RC) { o = e / (BK / 4); r = (e % (BK / 4)) * 4; }
             else           { r = e / (OUTER / 4); o = (e % (OUTER / 4)) * 4; }
@@ -153,17 +153,18 @@ __device__ __forceinline__ void read_frag(const float *__restrict__ L, int o_bas
 // reduction steps, and the WK partial sub-tiles are summed through LDS in
 // fixed order at the end.  WK > 1 gives small tiles several independent MFMA
 // accumulator chains per wave instead of one dependent chain.
-template <int BM_, int BN_, int BK_, int WGM_, int WK_, int NR_ = 2, int NCH_ = 0>
+template <int BM_, int BN_, int BK_, int WGM_, int WK_, int NR_ = 2, int NCH_ = 0, int NW_ = 4>
 struct Tile {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WK = WK_, NR = NR_;
-    static constexpr int WGN = 4 / (WGM * WK);
+    static constexpr int NW = NW_, THREADS = 64 * NW_;      // waves / threads per workgroup
+    static constexpr int WGN = NW / (WGM * WK);
     static constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 32, FN = WN / 32;
     static constexpr int RW = BK / WK;
     // accumulator chains per 32x32 block (the reduction steps of a block
     // alternate between its NCH chains, summed in fixed order at the store);
     // measured on MI355X: one chain is as fast and keeps occupancy higher
     static constexpr int NCH = NCH_ ? NCH_ : 1;
-    static_assert(WGM * WGN * WK == 4 && FM >= 1 && FN >= 1, "4 waves, 32x32 blocks");
+    static_assert(WGM * WGN * WK == NW && FM >= 1 && FN >= 1, "NW waves, 32x32 blocks");
     static_assert(RW >= 8 && RW % 8 == 0, "a wave takes a multiple of 8 reduction steps per stage");
     static constexpr int TILE = BM * BN;
     template <int LA, int LB>
@@ -200,8 +201,8 @@ __device__ __forceinline__ void tile_accumulate(float *__restrict__ smem, const 
     // the paths meet, and it would then wait for all of them, the prefetch
     // included, before every LDS store.
     auto stage_r = [&](int st) { return rbeg + min(st, nsteps - 1) * BK; };
-    TileLoader<LA, BM, BK, VEC> la0, la1, la2;
-    TileLoader<LB, BN, BK, VEC> lb0, lb1, lb2;
+    TileLoader<LA, BM, BK, VEC, T::THREADS> la0, la1, la2;
+    TileLoader<LB, BN, BK, VEC, T::THREADS> lb0, lb1, lb2;
     la0.load(A, lda, i0, Mo, rbeg, rend, tid);
     lb0.load(B, ldb, j0, No, rbeg, rend, tid);
     la1.load(A, lda, i0, Mo, stage_r(1), rend, tid);
@@ -311,7 +312,7 @@ __device__ __forceinline__ void tile_store(const f32x16 (&accs)[T::FM][T::FN][T:
                     mine[(((g * T::FM + a) * T::FN + b) * 16 + v) * 64 + lane] = acc[a][b][v];
         __syncthreads();
 #pragma unroll 4
-        for (int f = threadIdx.x; f < T::TILE; f += 256) {
+        for (int f = threadIdx.x; f < T::TILE; f += T::THREADS) {
             float s = red[f];
 #pragma unroll
             for (int k = 1; k < T::WK; k++) s += red[k * T::TILE + f];
@@ -357,7 +358,7 @@ struct GemmArgs {
 };
 
 template <class T, int LA, int LB, bool VEC>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs g)
+__global__ __launch_bounds__(T::THREADS) void k_gemm(GemmArgs g)
 {
     __shared__ __attribute__((aligned(16))) float smem[T::template lds<LA, LB>()];
     const int item = xcd_remap(blockIdx.x, gridDim.x);
@@ -574,7 +575,7 @@ __device__ __forceinline__ void group_body(const GroupArgs &g, float *smem)
 }
 
 template <class T>
-__global__ __launch_bounds__(256) void k_group(GroupArgs g)
+__global__ __launch_bounds__(T::THREADS) void k_group(GroupArgs g)
 {
     __shared__ __attribute__((aligned(16))) float smem[T::lds_max()];
     group_body<T>(g, smem);
@@ -583,7 +584,7 @@ __global__ __launch_bounds__(256) void k_group(GroupArgs g)
 // The same code for the expert-batched launches of the MoE layer, under its
 // own name so profiles separate MoE launches from the dense grouped GEMMs.
 template <class T>
-__global__ __launch_bounds__(256) void k_expert_group(GroupArgs g)
+__global__ __launch_bounds__(T::THREADS) void k_expert_group(GroupArgs g)
 {
     __shared__ __attribute__((aligned(16))) float smem[T::lds_max()];
     group_body<T>(g, smem);
@@ -610,7 +611,7 @@ int tlg_zero_launch(float *dst, size_t n, hipStream_t st)
 // ---------------------------------------------------------------- launch --
 // Tile shapes: BM x BN output per workgroup, BK reduction steps per stage,
 // WGM x WGN waves over the tile, WK wave groups along the reduction.
-struct TileCfg { int bm, bn, bk, wgm, wk; };
+struct TileCfg { int bm, bn, bk, wgm, wk, nw; };   // nw 0 = 4 waves
 static const TileCfg kCfgs[] = {
     {128, 128, 16, 2, 1},   // 0: wave tile 64x64, 4 accumulator chains
     {128, 64, 32, 2, 1},    // 1: 64x32
@@ -628,6 +629,10 @@ static const TileCfg kCfgs[] = {
     {32, 64, 32, 1, 2},     // 13: 32x32 per wave, half of each stage
     {64, 32, 32, 2, 2},     // 14: 32x32 per wave, half of each stage
     {32, 32, 32, 1, 4},     // 15: 32x32 per wave, a quarter of each stage
+    {64, 64, 32, 2, 1, 2},  // 16: 2 waves, 32x64 per wave
+    {64, 64, 32, 1, 1, 2},  // 17: 2 waves, 64x32 per wave
+    {64, 64, 16, 2, 1},     // 18: 32x32 per wave, 16-step stages
+    {64, 64, 16, 2, 1},     // 19: same, loads three stages ahead
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
 using T0 = Tile<128, 128, 16, 2, 1>;
@@ -647,6 +652,10 @@ using T12 = Tile<64, 64, 32, 2, 1, 3, 4>;
 using T13 = Tile<32, 64, 32, 1, 2>;
 using T14 = Tile<64, 32, 32, 2, 2>;
 using T15 = Tile<32, 32, 32, 1, 4>;
+using T16 = Tile<64, 64, 32, 2, 1, 2, 0, 2>;
+using T17 = Tile<64, 64, 32, 1, 1, 2, 0, 2>;
+using T18 = Tile<64, 64, 16, 2, 1, 2, 0, 4>;
+using T19 = Tile<64, 64, 16, 2, 1, 3, 0, 4>;
 
 template <class T, int LA, int LB>
 static void launch_t(const GemmArgs &a, int grid, bool vec, hipStream_t st)
@@ -750,7 +759,8 @@ int tlg_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len, int *s
 
 extern "C" int tlg_tune_force(int cfg, int splits)
 {
-    if (cfg >= kNumCfgs) return tlg_fail(TLG_EINVAL, "tlg_tune_force: config %d of %d", cfg, kNumCfgs);
+    // single-call launches instantiate configs 0-15 (16+ are grouped-only shapes)
+    if (cfg >= 16) return tlg_fail(TLG_EINVAL, "tlg_tune_force: config %d of 16", cfg);
     g_force_cfg = cfg;
     g_force_splits = splits;
     return TLG_OK;
@@ -828,15 +838,19 @@ static int g_npending = 0;
 static int g_ws_half = 0;
 
 // Tile shape of a grouped launch (all problems of a group share it): the
-// first candidate that still gives every CU about `g_min_waves` workgroups,
-// else the last.  Measured on MI355X over the m3 training step, 64x64 tiles
-// alone are as fast as any mix with 32x64 / 32x32 / 128x128 tiles (within
-// 0.5%), so the default list holds 64x64 only; TLG_GROUP_CANDS overrides it
-// and tlg_tune_group pins one shape for sweeps.
+// first candidate that still gives every CU `g_min_waves` workgroups, else
+// the last.  Measured on MI355X over the m3 training step (graph replay):
+// 64x64 tiles where a launch has >= 3 x 256 of them, else 64x32 tiles whose
+// two wave pairs split each stage's reduction (more, smaller work items and
+// 5 waves per SIMD instead of 4), with dW splits of about 512 reduction
+// steps: 1.548 ms/step, against 1.637 for 64x64 tiles and 384-step splits
+// (m8: 6.95 against 7.91 ms).  TLG_GROUP_CANDS, TLG_GROUP_MINWAVES and
+// TLG_GROUP_RTARGET (or tlg_tune_group_policy) override the policy,
+// tlg_tune_group pins one shape.
 static int g_group_cfg = -1;
-static double g_min_waves = 2.0;
-static int g_cand[4] = {3, -1, -1, -1};   // 64x64
-static int g_rtarget = 384;
+static double g_min_waves = 3.0;
+static int g_cand[4] = {3, 14, -1, -1};   // 64x64, then 64x32 (2 x 2 waves)
+static int g_rtarget = 512;
 static int g_group_last = 3;          // shape of the most recent grouped launch
 static const char *g_group_last_name = nullptr;   // set when that launch was a GEMV group
 
@@ -863,29 +877,56 @@ static void group_env(void)
     if (e && atoi(e) >= 64) g_rtarget = atoi(e);
 }
 
+template <class T>
+static void lgroup(const GroupArgs &a, int grid, hipStream_t st)
+{
+    hipLaunchKernelGGL((k_group<T>), dim3(grid), dim3(T::THREADS), 0, st, a);
+}
+
 static void launch_group(int ci, const GroupArgs &a, int grid, hipStream_t st)
 {
     switch (ci) {
-    case 0: hipLaunchKernelGGL((k_group<T0>), dim3(grid), dim3(256), 0, st, a); break;
-    case 1: hipLaunchKernelGGL((k_group<T1>), dim3(grid), dim3(256), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((k_group<T4>), dim3(grid), dim3(256), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((k_group<T8>), dim3(grid), dim3(256), 0, st, a); break;
-    case 9: hipLaunchKernelGGL((k_group<T9>), dim3(grid), dim3(256), 0, st, a); break;
-    case 10: hipLaunchKernelGGL((k_group<T10>), dim3(grid), dim3(256), 0, st, a); break;
-    case 11: hipLaunchKernelGGL((k_group<T11>), dim3(grid), dim3(256), 0, st, a); break;
-    case 12: hipLaunchKernelGGL((k_group<T12>), dim3(grid), dim3(256), 0, st, a); break;
-    case 13: hipLaunchKernelGGL((k_group<T13>), dim3(grid), dim3(256), 0, st, a); break;
-    case 14: hipLaunchKernelGGL((k_group<T14>), dim3(grid), dim3(256), 0, st, a); break;
-    case 15: hipLaunchKernelGGL((k_group<T15>), dim3(grid), dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL((k_group<T3>), dim3(grid), dim3(256), 0, st, a); break;
+    case 0: lgroup<T0>(a, grid, st); break;
+    case 1: lgroup<T1>(a, grid, st); break;
+    case 4: lgroup<T4>(a, grid, st); break;
+    case 8: lgroup<T8>(a, grid, st); break;
+    case 9: lgroup<T9>(a, grid, st); break;
+    case 10: lgroup<T10>(a, grid, st); break;
+    case 11: lgroup<T11>(a, grid, st); break;
+    case 12: lgroup<T12>(a, grid, st); break;
+    case 13: lgroup<T13>(a, grid, st); break;
+    case 14: lgroup<T14>(a, grid, st); break;
+    case 15: lgroup<T15>(a, grid, st); break;
+    case 16: lgroup<T16>(a, grid, st); break;
+    case 17: lgroup<T17>(a, grid, st); break;
+    case 18: lgroup<T18>(a, grid, st); break;
+    case 19: lgroup<T19>(a, grid, st); break;
+    default: lgroup<T3>(a, grid, st); break;
     }
     g_group_last = ci;
     g_group_last_name = nullptr;
 }
 
+extern "C" int tlg_tune_group_policy(const int *cands, int ncands, double min_waves, int rtarget)
+{
+    group_env();
+    if (ncands < 0 || ncands > 3 || (ncands > 0 && !cands) || min_waves < 0 || (rtarget && rtarget < 64))
+        return tlg_fail(TLG_EINVAL, "tlg_tune_group_policy: bad arguments");
+    for (int k = 0; k < ncands; k++)
+        if (cands[k] < 0 || cands[k] >= kNumCfgs || cands[k] == 2 || (cands[k] >= 5 && cands[k] <= 7))
+            return tlg_fail(TLG_EINVAL, "tlg_tune_group_policy: config %d", cands[k]);
+    if (ncands > 0) {
+        for (int k = 0; k < ncands; k++) g_cand[k] = cands[k];
+        g_cand[ncands] = -1;
+    }
+    if (min_waves > 0) g_min_waves = min_waves;
+    if (rtarget) g_rtarget = rtarget;
+    return TLG_OK;
+}
+
 extern "C" int tlg_tune_group(int cfg)
 {
-    if (cfg != -1 && cfg != 0 && cfg != 1 && cfg != 3 && cfg != 4 && (cfg < 8 || cfg > 15))
+    if (cfg != -1 && cfg != 0 && cfg != 1 && cfg != 3 && cfg != 4 && (cfg < 8 || cfg > 19))
         return tlg_fail(TLG_EINVAL, "tlg_tune_group: config %d", cfg);
     g_group_cfg = cfg;
     return TLG_OK;
@@ -906,6 +947,10 @@ const char *tlg_group_kernel_name(void)
     case 13: return "k_group<Tile<32, 64, 32, 1, 2, 2, 0> >";
     case 14: return "k_group<Tile<64, 32, 32, 2, 2, 2, 0> >";
     case 15: return "k_group<Tile<32, 32, 32, 1, 4, 2, 0> >";
+    case 16: return "k_group<Tile<64, 64, 32, 2, 1, 2, 0, 2> >";
+    case 17: return "k_group<Tile<64, 64, 32, 1, 1, 2, 0, 2> >";
+    case 18: return "k_group<Tile<64, 64, 16, 2, 1, 2, 0, 4> >";
+    case 19: return "k_group<Tile<64, 64, 16, 2, 1, 3, 0, 4> >";
     default: return "k_group<Tile<64, 64, 32, 2, 1, 2, 0> >";
     }
 }
