@@ -633,6 +633,8 @@ static const TileCfg kCfgs[] = {
     {64, 64, 32, 1, 1, 2},  // 17: 2 waves, 64x32 per wave
     {64, 64, 16, 2, 1},     // 18: 32x32 per wave, 16-step stages
     {64, 64, 16, 2, 1},     // 19: same, loads three stages ahead
+    {64, 64, 32, 2, 2, 8},  // 20: 8 waves, 32x32 per wave, half of each stage
+    {64, 32, 64, 2, 2},     // 21: 32x32 per wave, half of each 64-step stage
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
 using T0 = Tile<128, 128, 16, 2, 1>;
@@ -656,6 +658,8 @@ using T16 = Tile<64, 64, 32, 2, 1, 2, 0, 2>;
 using T17 = Tile<64, 64, 32, 1, 1, 2, 0, 2>;
 using T18 = Tile<64, 64, 16, 2, 1, 2, 0, 4>;
 using T19 = Tile<64, 64, 16, 2, 1, 3, 0, 4>;
+using T20 = Tile<64, 64, 32, 2, 2, 2, 0, 8>;
+using T21 = Tile<64, 32, 64, 2, 2, 2, 0, 4>;
 
 template <class T, int LA, int LB>
 static void launch_t(const GemmArgs &a, int grid, bool vec, hipStream_t st)
@@ -901,6 +905,8 @@ static void launch_group(int ci, const GroupArgs &a, int grid, hipStream_t st)
     case 17: lgroup<T17>(a, grid, st); break;
     case 18: lgroup<T18>(a, grid, st); break;
     case 19: lgroup<T19>(a, grid, st); break;
+    case 20: lgroup<T20>(a, grid, st); break;
+    case 21: lgroup<T21>(a, grid, st); break;
     default: lgroup<T3>(a, grid, st); break;
     }
     g_group_last = ci;
@@ -926,7 +932,7 @@ extern "C" int tlg_tune_group_policy(const int *cands, int ncands, double min_wa
 
 extern "C" int tlg_tune_group(int cfg)
 {
-    if (cfg != -1 && cfg != 0 && cfg != 1 && cfg != 3 && cfg != 4 && (cfg < 8 || cfg > 19))
+    if (cfg != -1 && cfg != 0 && cfg != 1 && cfg != 3 && cfg != 4 && (cfg < 8 || cfg > 21))
         return tlg_fail(TLG_EINVAL, "tlg_tune_group: config %d", cfg);
     g_group_cfg = cfg;
     return TLG_OK;
@@ -951,6 +957,8 @@ const char *tlg_group_kernel_name(void)
     case 17: return "k_group<Tile<64, 64, 32, 1, 1, 2, 0, 2> >";
     case 18: return "k_group<Tile<64, 64, 16, 2, 1, 2, 0, 4> >";
     case 19: return "k_group<Tile<64, 64, 16, 2, 1, 3, 0, 4> >";
+    case 20: return "k_group<Tile<64, 64, 32, 2, 2, 2, 0, 8> >";
+    case 21: return "k_group<Tile<64, 32, 64, 2, 2, 2, 0, 4> >";
     default: return "k_group<Tile<64, 64, 32, 2, 1, 2, 0> >";
     }
 }
