@@ -420,12 +420,13 @@ def main():
     dom_name, dom = max(groups.items(), key=lambda kv: kv[1]["ms"])
     bound = roofline_class(dom["flops"], dom["bytes"])
     # Average launch duration of the dominant kernel over the timed region:
-    # the step time less the other kernels' (event-timed) share, over its
-    # launches per step.  (Events around single launches also count the gap
-    # before each launch; inside the graph replay the launches run back to
-    # back, which is what rocprofv3's kernel trace measures.)
-    other_ms = sum(g["ms"] for k, g in groups.items() if k != dom_name)
-    avg_ms = (ms_step - other_ms) / dom["launches"]
+    # the timed step time apportioned to the kernels by their event-timed
+    # shares, over the kernel's launches per step.  (Events around single
+    # launches also count the gap before each launch; inside the graph replay
+    # the launches run back to back, which is what rocprofv3's kernel trace
+    # measures.)
+    event_total = sum(g["ms"] for g in groups.values())
+    avg_ms = ms_step * (dom["ms"] / event_total) / dom["launches"]
     event_avg_ms = dom["ms"] / dom["launches"]
     if bound == "mfma":
         achieved = dom["flops"] / dom["launches"] / (avg_ms / 1e3) / 1e12
@@ -434,6 +435,7 @@ def main():
         achieved = dom["bytes"] / dom["launches"] / (avg_ms / 1e3) / 1e9
         peak, unit = PEAK_HBM_GBS, "GB/s"
     census = {k: {"launches": v["launches"], "avg_us": round(v["ms"] / v["launches"] * 1e3, 3),
+                  "timed_avg_us": round(ms_step * (v["ms"] / event_total) / v["launches"] * 1e3, 3),
                   "share": round(v["ms"] / sum(g["ms"] for g in groups.values()), 4),
                   "tflops": round(v["flops"] / (v["ms"] / 1e3) / 1e12, 2),
                   "shapes": sorted(v["shapes"])} for k, v in groups.items()}

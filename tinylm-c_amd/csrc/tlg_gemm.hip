@@ -1204,7 +1204,6 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     rc = tlg_group_flush_launch(st);
     if (rc) return rc;
 
-    const TileCfg &tc = kCfgs[3];      // k_expert_group<T3>: 64 x 64 tiles
     Prob probs[TLG_MAXPROB / 2];
     int rmax = 0;
     for (int i = 0; i < n; i++) {
@@ -1252,6 +1251,19 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     if (need(rps) > g_tlg.ws_floats)
         return tlg_fail(TLG_ENOMEM, "expert launch: %d experts' partials exceed the workspace", E);
 
+    // tile shape as for dense grouped launches: 64x64 tiles when the launch
+    // has about g_min_waves x 256 of them, else 64x32 split-stage tiles
+    auto items_for = [&](const TileCfg &c) {
+        double t = 0;
+        for (int i = 0; i < n; i++) {
+            const Prob &P = probs[i];
+            const double tn = cdiv(P.No, c.bn);
+            t += P.kind == PK_TN ? cdiv(P.Mo, c.bm) * tn * (rows / rps + E) : (cdiv(rows, c.bm) + E) * tn;
+        }
+        return t;
+    };
+    const int ci = items_for(kCfgs[3]) >= g_min_waves * 256 ? 3 : 14;
+    const TileCfg &tc = kCfgs[ci];
     GroupArgs a, red;
     a.nprob = red.nprob = 0;
     size_t used = 0;
@@ -1295,10 +1307,13 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     // an XCD's share of the real items can exceed its share of the upper
     // bound by one per expert problem
     static_assert(sizeof(GroupArgs) <= 4096, "kernel arguments");
-    hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(a) + 8 * n), dim3(256), 0, st, a);
+    if (ci == 3)
+        hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(a) + 8 * n), dim3(T3::THREADS), 0, st, a);
+    else
+        hipLaunchKernelGGL((k_expert_group<T14>), dim3(group_grid(a) + 8 * n), dim3(T14::THREADS), 0, st, a);
     TLG_HIP(hipGetLastError());
     if (red.nprob) {
-        hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(red)), dim3(256), 0, st, red);
+        hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(red)), dim3(T3::THREADS), 0, st, red);
         TLG_HIP(hipGetLastError());
     }
     return TLG_OK;

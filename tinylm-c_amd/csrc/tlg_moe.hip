@@ -35,49 +35,55 @@
 #define TLG_MOE_MAXE 64          // the reference's dp[64] (:937)
 
 // ------------------------------------------------------------ routing --
-// 64 tokens per workgroup.  Logit (t, e) is the chain
+// MOE_TOK tokens per workgroup.  Logit (t, e) is the chain
 //   l = 0; for d in 0..D-1: l = fma(x[t][d], wr[d][e], l)
-// which is how the reference's mm evaluates each output (:462-466).
+// which is how the reference's mm evaluates each output (:462-466).  The
+// token rows and router columns are staged in LDS (dynamic: `dch` columns of
+// d at a time, all of D when it fits), so one round of loads serves the
+// whole chain.
+#define MOE_TOK 16
 __global__ __launch_bounds__(256) void k_moe_route(const float *__restrict__ X, const float *__restrict__ Wr,
-                                                   int N, int D, int E, float *__restrict__ rprobs,
+                                                   int N, int D, int E, int dch, float *__restrict__ rprobs,
                                                    int *__restrict__ assign, float *__restrict__ gate)
 {
-    __shared__ float xs[64][65];
-    __shared__ float wsm[64 * TLG_MOE_MAXE];
-    __shared__ float lg[64 * TLG_MOE_MAXE];
-    const int n0 = blockIdx.x * 64, tid = threadIdx.x;
-    for (int p = tid; p < 64 * E; p += 256) lg[p] = 0.f;
-    for (int d0 = 0; d0 < D; d0 += 64) {
-        const int dn = min(64, D - d0);
+    extern __shared__ float lds_route[];
+    float *xs = lds_route;                          // [MOE_TOK][dch + 1]
+    float *wsm = xs + MOE_TOK * (dch + 1);          // [dch][E]
+    float *lg = wsm + dch * E;                      // [MOE_TOK][E]
+    const int n0 = blockIdx.x * MOE_TOK, tid = threadIdx.x;
+    for (int p = tid; p < MOE_TOK * E; p += 256) lg[p] = 0.f;
+    for (int d0 = 0; d0 < D; d0 += dch) {
+        const int dn = min(dch, D - d0);
         __syncthreads();
-        for (int p = tid; p < 64 * 64; p += 256) {
-            const int t = p >> 6, d = p & 63;
-            xs[t][d] = (n0 + t < N && d < dn) ? X[(size_t)(n0 + t) * D + d0 + d] : 0.f;
+        for (int p = tid; p < MOE_TOK * dch; p += 256) {
+            const int t = p / dch, d = p - t * dch;
+            xs[t * (dch + 1) + d] = (n0 + t < N && d < dn) ? X[(size_t)(n0 + t) * D + d0 + d] : 0.f;
         }
-        for (int p = tid; p < 64 * E; p += 256) {
+        for (int p = tid; p < dch * E; p += 256) {
             const int d = p / E;
             wsm[p] = d < dn ? Wr[(size_t)(d0 + d) * E + p % E] : 0.f;
         }
         __syncthreads();
-        for (int p = tid; p < 64 * E; p += 256) {
+        for (int p = tid; p < MOE_TOK * E; p += 256) {
             const int t = p / E, e = p % E;
+            const float *xr = xs + t * (dch + 1);
             float l = lg[p];
             int d = 0;
             // the chain stays sequential; its LDS operands are fetched 8 ahead
             for (; d + 8 <= dn; d += 8) {
                 float xv[8], wv[8];
 #pragma unroll
-                for (int u = 0; u < 8; u++) { xv[u] = xs[t][d + u]; wv[u] = wsm[(d + u) * E + e]; }
+                for (int u = 0; u < 8; u++) { xv[u] = xr[d + u]; wv[u] = wsm[(d + u) * E + e]; }
 #pragma unroll
                 for (int u = 0; u < 8; u++) l = fmaf(xv[u], wv[u], l);
             }
-            for (; d < dn; d++) l = fmaf(xs[t][d], wsm[d * E + e], l);
+            for (; d < dn; d++) l = fmaf(xr[d], wsm[d * E + e], l);
             lg[p] = l;
         }
     }
     __syncthreads();
     const int t = tid, n = n0 + t;
-    if (t >= 64 || n >= N) return;
+    if (t >= MOE_TOK || n >= N) return;
     // softmax over all E (:862-867), then moe_route's slot 0 (:818-825)
     const float *r = lg + t * E;
     float *pr = rprobs + (size_t)n * E;
@@ -96,6 +102,18 @@ __global__ __launch_bounds__(256) void k_moe_route(const float *__restrict__ X, 
     const int sel = best < 0 ? 0 : best;
     assign[n] = sel;
     gate[n] = pr[sel];
+}
+
+// LDS columns per round of k_moe_route: all of D when the staged rows and
+// router columns fit in 48 KB, else 64.
+static int route_dch(int D, int E)
+{
+    const size_t whole = (size_t)MOE_TOK * (D + 1) + (size_t)D * E + (size_t)MOE_TOK * E;
+    return whole * 4 <= 48 * 1024 ? D : 64;
+}
+static size_t route_lds(int dch, int E)
+{
+    return 4 * ((size_t)MOE_TOK * (dch + 1) + (size_t)dch * E + (size_t)MOE_TOK * E);
 }
 
 // ------------------------------------------------------- expert index --
@@ -432,8 +450,9 @@ int tlg_moe_fwd_launch(const float *fnorm, const float *fin, float *out, int N, 
     if ((rc = tlg_group_flush_launch(st))) return rc;
     MoeScratch s;
     if ((rc = moe_scratch(N, D, F, E, &s))) return rc;
-    hipLaunchKernelGGL(k_moe_route, dim3((N + 63) / 64), dim3(256), 0, st, fnorm, wr, N, D, E, rprobs, assign,
-                       gate);
+    const int dch = route_dch(D, E);
+    hipLaunchKernelGGL(k_moe_route, dim3((N + MOE_TOK - 1) / MOE_TOK), dim3(256), route_lds(dch, E), st, fnorm, wr,
+                       N, D, E, dch, rprobs, assign, gate);
     TLG_HIP(hipGetLastError());
     if ((rc = moe_index(assign, N, E, s, st))) return rc;
     if ((rc = moe_experts_fwd(fnorm, N, D, F, E, w1, w3, w2, s, st))) return rc;
