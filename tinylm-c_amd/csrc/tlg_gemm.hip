@@ -755,7 +755,7 @@ int tlg_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len, int *s
     const int la = (kind == TLG_TN) ? OC : RC;
     const int lb = (kind == TLG_NT) ? RC : OC;
     const bool vec = (la == RC ? (R % 4 == 0) : (Mo % 4 == 0)) && (lb == RC ? (R % 4 == 0) : (No % 4 == 0));
-    snprintf(buf, (size_t)len, "k_gemm<Tile<%d, %d, %d, %d, %d, 2, 0>, %d, %d, %s>", c.bm, c.bn, c.bk, c.wgm,
+    snprintf(buf, (size_t)len, "k_gemm<Tile<%d, %d, %d, %d, %d, 2, 0, 4>, %d, %d, %s>", c.bm, c.bn, c.bk, c.wgm,
              c.wk, la, lb, vec ? "true" : "false");
     if (splits) *splits = p.splits;
     return TLG_OK;
@@ -942,24 +942,24 @@ const char *tlg_group_kernel_name(void)
 {
     if (g_group_last_name) return g_group_last_name;
     switch (g_group_last) {
-    case 0: return "k_group<Tile<128, 128, 16, 2, 1, 2, 0> >";
-    case 1: return "k_group<Tile<128, 64, 32, 2, 1, 2, 0> >";
-    case 4: return "k_group<Tile<64, 64, 32, 1, 4, 2, 0> >";
-    case 8: return "k_group<Tile<64, 64, 64, 2, 1, 2, 0> >";
-    case 9: return "k_group<Tile<64, 64, 32, 2, 1, 2, 2> >";
-    case 10: return "k_group<Tile<64, 64, 32, 2, 1, 2, 1> >";
-    case 11: return "k_group<Tile<64, 64, 32, 2, 1, 3, 1> >";
-    case 12: return "k_group<Tile<64, 64, 32, 2, 1, 3, 4> >";
-    case 13: return "k_group<Tile<32, 64, 32, 1, 2, 2, 0> >";
-    case 14: return "k_group<Tile<64, 32, 32, 2, 2, 2, 0> >";
-    case 15: return "k_group<Tile<32, 32, 32, 1, 4, 2, 0> >";
+    case 0: return "k_group<Tile<128, 128, 16, 2, 1, 2, 0, 4> >";
+    case 1: return "k_group<Tile<128, 64, 32, 2, 1, 2, 0, 4> >";
+    case 4: return "k_group<Tile<64, 64, 32, 1, 4, 2, 0, 4> >";
+    case 8: return "k_group<Tile<64, 64, 64, 2, 1, 2, 0, 4> >";
+    case 9: return "k_group<Tile<64, 64, 32, 2, 1, 2, 2, 4> >";
+    case 10: return "k_group<Tile<64, 64, 32, 2, 1, 2, 1, 4> >";
+    case 11: return "k_group<Tile<64, 64, 32, 2, 1, 3, 1, 4> >";
+    case 12: return "k_group<Tile<64, 64, 32, 2, 1, 3, 4, 4> >";
+    case 13: return "k_group<Tile<32, 64, 32, 1, 2, 2, 0, 4> >";
+    case 14: return "k_group<Tile<64, 32, 32, 2, 2, 2, 0, 4> >";
+    case 15: return "k_group<Tile<32, 32, 32, 1, 4, 2, 0, 4> >";
     case 16: return "k_group<Tile<64, 64, 32, 2, 1, 2, 0, 2> >";
     case 17: return "k_group<Tile<64, 64, 32, 1, 1, 2, 0, 2> >";
     case 18: return "k_group<Tile<64, 64, 16, 2, 1, 2, 0, 4> >";
     case 19: return "k_group<Tile<64, 64, 16, 2, 1, 3, 0, 4> >";
     case 20: return "k_group<Tile<64, 64, 32, 2, 2, 2, 0, 8> >";
     case 21: return "k_group<Tile<64, 32, 64, 2, 2, 2, 0, 4> >";
-    default: return "k_group<Tile<64, 64, 32, 2, 1, 2, 0> >";
+    default: return "k_group<Tile<64, 64, 32, 2, 1, 2, 0, 4> >";
     }
 }
 

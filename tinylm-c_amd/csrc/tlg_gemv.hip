@@ -87,7 +87,7 @@ __device__ __forceinline__ void gemv_nn(const GvProb &P, int blk, float *As, flo
         const int kc = GV_ACHUNK / P.M;
         for (int r0 = 0; r0 < g.R; r0 += kc) {
             const int kn = min(kc, g.R - r0);
-            // rows k = q + 32 u of this chunk, in batches of NN_U: every load
+            // rows k = q + SLOTS u of this chunk, in batches of NN_U: every load
             // of a batch is issued before any is used (rows past the chunk
             // read a clamped address and are zeroed), and the next batch is
             // in flight while the current one is consumed
