@@ -138,7 +138,8 @@ int tlg_tune_group_policy(const int *cands, int ncands, double min_waves, int rt
  * gw3, gw2 (expert GEMM grads, the router's softmax backward with the
  * 0.01 * E * (cnt_e / N) / N load-balance term, dWr).
  * Device-pointer forms enqueue on `stream` (asynchronous; scratch kept by the
- * library, grown on demand).  Host-pointer forms are synchronous and abort on
+ * library, grown on demand -- growing synchronizes the device, and calls on
+ * different streams must not overlap).  Host-pointer forms are synchronous and abort on
  * error like the GEMM drop-ins; operands inside a registered range are used
  * in place. */
 int  tlg_dev_moe_grouped_fwd(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,

@@ -329,7 +329,9 @@ __global__ void k_moe_dfnorm(const float *__restrict__ dX, const int *__restrict
 
 // -------------------------------------------------------------- scratch --
 // One arena, grown on demand and kept until tlg_shutdown (like the
-// reference's me_ensure, :840-848).
+// reference's me_ensure, :840-848).  Growing it synchronizes the device, so
+// the first call at a new size cannot be captured into a graph; calls on
+// different streams must not overlap (they share the arena).
 struct MoeScratch {
     int *idx, *pos, *eoff;
     float *dgate, *drt, *Xg, *y, *dy, *g, *u, *a, *da;
@@ -347,9 +349,9 @@ void tlg_moe_release(void)
 static int moe_scratch(int N, int D, int F, int E, MoeScratch *s)
 {
     const size_t n = (size_t)N;
-    size_t sizes[13] = {n * 4, n * 4, (size_t)(TLG_MOE_MAXE + 1) * 4, n * 4, n * E * 4,
-                        n * D * 4, n * D * 4, n * D * 4, n * F * 4, n * F * 4, n * F * 4, n * F * 4, 0};
-    size_t total = 0, offs[13];
+    const size_t sizes[12] = {n * 4, n * 4, (size_t)(TLG_MOE_MAXE + 1) * 4, n * 4, n * E * 4,
+                              n * D * 4, n * D * 4, n * D * 4, n * F * 4, n * F * 4, n * F * 4, n * F * 4};
+    size_t total = 0, offs[12];
     for (int k = 0; k < 12; k++) {
         offs[k] = total;
         total += (sizes[k] + 255) & ~(size_t)255;
@@ -405,7 +407,7 @@ static bool moe_ptrs_ok(std::initializer_list<const void *> ps)
     return true;
 }
 
-// Routing + index (forward), or index only (backward).
+// Per-expert row index of the routed tokens (idx, pos, eoff).
 static int moe_index(const int *assign, int N, int E, const MoeScratch &s, hipStream_t st)
 {
     hipLaunchKernelGGL(k_moe_index, dim3(1), dim3(1024), 0, st, assign, N, E, s.idx, s.pos, s.eoff);
