@@ -353,6 +353,40 @@ def cpu_baseline(host, cfgname, steps, threads):
     }
 
 
+def cpu_decode_baseline(host, M, steps, threads):
+    """configs[3] decode GEMVs on the host with the reference's own kernels,
+    dispatched as tinylm.c dispatches them (mm at M <= 4 and mm_bt at M = 1
+    run serially through tl_for, tinylm.c:446, :486; larger M use OpenMP),
+    one weight copy (cache-resident, as the reference's own decode runs), the
+    call list looped in C."""
+    import numpy as np
+    import oracle
+    try:
+        prims, kind = oracle.Reference(), "reference"
+    except FileNotFoundError:
+        prims, kind = oracle.Oracle(), "port"
+    prims.set_threads(threads)
+    plan = host.plan_decode(M, **DECODE)
+    rng = np.random.default_rng(6)
+    arrays = {}
+    for name, n, init in plan.bufs:
+        a = rng.standard_normal(n, dtype=np.float32) if init != 3 else np.zeros(n, np.float32)
+        if init == 1:
+            a *= np.float32(0.02)
+        arrays[name] = a
+    calls = oracle.plan_calls_native(plan, arrays)
+    prims.run_calls(calls, 3)                           # warmup
+    t0 = time.perf_counter()
+    prims.run_calls(calls, steps)
+    dt = time.perf_counter() - t0
+    return {
+        "rows": M, "us_per_step": round(dt / steps * 1e6, 1), "tok_s": round(M * steps / dt, 1),
+        "cores": threads, "kind": kind,
+        "sample": f"{steps} decode steps ({sum(1 for c in plan.calls if c['op'] != 'zero')} GEMVs each), "
+                  f"{dt:.2f} s",
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -468,6 +502,9 @@ def main():
         log(f"[cpu] timing the reference kernels on {threads} threads ...")
         cpu = cpu_baseline(host, args.config, args.cpu_steps, threads)
         log(f"[cpu] {cpu}")
+        if args.decode_steps > 0:
+            cpu["decode"] = {str(M): cpu_decode_baseline(host, M, 200 if M == 1 else 50, threads) for M in (1, 8)}
+            log(f"[cpu] decode {cpu['decode']}")
 
     host.dll.tl_run_free(run)
     result = {

@@ -77,7 +77,13 @@ class Oracle(_Prims):
         d.orc_moe_forward.argtypes = [_i, _i, _i, _i, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _ip, _fp, _fp]
         d.orc_moe_backward.argtypes = [_i, _i, _i, _i, _fp, _fp, _fp, _fp, _fp, _fp, _fp,
                                        _fp, _fp, _fp, _fp, _ip, _fp, _fp]
+        d.orc_run_calls.argtypes = [ctypes.c_void_p, _i, _i]
+        d.orc_run_calls.restype = None
         self.dll = d
+
+    def run_calls(self, arr, reps=1):
+        """Run plan_calls_native(...) `reps` times in C."""
+        self.dll.orc_run_calls(ctypes.cast(arr, ctypes.c_void_p), len(arr), reps)
 
     # fp64 textbook references (accumulating forms add into the prefill)
     def mm_f64(self, X, W):
@@ -171,6 +177,14 @@ class Reference(_Prims):
     def set_threads(self, n):
         self.dll.tlref_threads(n)
 
+    def run_calls(self, arr, reps=1):
+        """Run plan_calls_native(...) `reps` times in C through the
+        reference's own mm / mm_bt / mm_atb."""
+        f = self.dll.tlref_run_calls
+        f.argtypes = [ctypes.c_void_p, _i, _i]
+        f.restype = None
+        f(ctypes.cast(arr, ctypes.c_void_p), len(arr), reps)
+
     def moe_forward(self, fnorm, fin, wr, w1, w3, w2):
         N, D = fnorm.shape
         E = wr.shape[1]
@@ -254,6 +268,34 @@ def run_plan_cpu(plan, arrays, prims):
             prims.mm_bt(view(out, c["out_off"], M, K), view(a, c["a_off"], M, N), view(b, c["b_off"], K, N))
         else:
             prims.mm_atb(view(out, c["out_off"], K, N), view(a, c["a_off"], M, K), view(b, c["b_off"], M, N))
+
+
+class _Call(ctypes.Structure):
+    """OrcCall / TlrefCall: one call of a plan for the C loop runners."""
+    _fields_ = [("op", ctypes.c_int), ("out", ctypes.c_void_p), ("a", ctypes.c_void_p), ("b", ctypes.c_void_p),
+                ("M", ctypes.c_int), ("K", ctypes.c_int), ("N", ctypes.c_int), ("n", ctypes.c_size_t)]
+
+
+def plan_calls_native(plan, arrays):
+    """The plan's calls as a C array of (op, pointers into `arrays`, dims),
+    for prims.run_calls: the same operands run_plan_cpu passes."""
+    names = [b[0] for b in plan.bufs]
+    ops = {"mm": 0, "mm_bt": 1, "mm_atb": 2, "zero": 3}
+    arr = (_Call * len(plan.calls))()
+
+    def ptr(name, off):
+        a = arrays[name]
+        return a.ctypes.data + 4 * off
+
+    for i, c in enumerate(plan.calls):
+        d = arr[i]
+        d.op = ops[c["op"]]
+        d.out = ptr(names[c["out"]], c["out_off"])
+        if c["op"] != "zero":
+            d.a = ptr(names[c["a"]], c["a_off"])
+            d.b = ptr(names[c["b"]], c["b_off"])
+        d.M, d.K, d.N, d.n = c["M"], c["K"], c["N"], c["n"]
+    return arr
 
 
 class F64Prims:

@@ -42,3 +42,20 @@ void tlref_moe_backward(int N, int D, int F, int E, const float *fnorm, const fl
     tlref_moe_setup(&c, &g, D, F, E, gwr, gw1, gw3, gw2, ga, gb, gc, gd);
     moe_backward(&c, &w, &g, 0, fnorm, dout, d_fnorm, assign, gate, rprobs, N);
 }
+
+/* A plan's call list run in C (no interpreter between the calls), for the
+ * CPU baseline of short calls such as the decode GEMVs: op 0 mm, 1 mm_bt,
+ * 2 mm_atb, 3 memset of n floats; `reps` passes over the list. */
+typedef struct { int op; float *out; const float *a, *b; int M, K, N; size_t n; } TlrefCall;
+void tlref_run_calls(const TlrefCall *c, int n, int reps)
+{
+    for (int r = 0; r < reps; r++)
+        for (int i = 0; i < n; i++) {
+            switch (c[i].op) {
+            case 0: mm(c[i].out, c[i].a, c[i].b, c[i].M, c[i].K, c[i].N); break;
+            case 1: mm_bt(c[i].out, c[i].a, c[i].b, c[i].M, c[i].K, c[i].N); break;
+            case 2: mm_atb(c[i].out, c[i].a, c[i].b, c[i].M, c[i].K, c[i].N); break;
+            default: memset(c[i].out, 0, c[i].n * sizeof(float)); break;
+            }
+        }
+}

@@ -408,3 +408,16 @@ void orc_moe_backward(int N, int D, int F, int E,
     free(xs); free(g); free(u); free(a); free(y); free(dy); free(da); free(dg); free(du);
     free(dx); free(drt); free(dgate); free(idx); free(cnt);
 }
+
+void orc_run_calls(const OrcCall *c, int n, int reps)
+{
+    for (int r = 0; r < reps; r++)
+        for (int i = 0; i < n; i++) {
+            switch (c[i].op) {
+            case 0: orc_mm(c[i].out, c[i].a, c[i].b, c[i].M, c[i].K, c[i].N); break;
+            case 1: orc_mm_bt(c[i].out, c[i].a, c[i].b, c[i].M, c[i].K, c[i].N); break;
+            case 2: orc_mm_atb(c[i].out, c[i].a, c[i].b, c[i].M, c[i].K, c[i].N); break;
+            default: memset(c[i].out, 0, c[i].n * sizeof(float)); break;
+            }
+        }
+}

@@ -71,6 +71,11 @@ void orc_moe_backward(int N, int D, int F, int E,
                       float *gwr, float *gw1, float *gw3, float *gw2,
                       const int *assign, const float *gate, const float *rprobs);
 
+/* A plan's call list run in C (CPU baseline of short calls): op 0 mm,
+ * 1 mm_bt, 2 mm_atb, 3 memset of n floats; `reps` passes over the list. */
+typedef struct { int op; float *out; const float *a, *b; int M, K, N; size_t n; } OrcCall;
+void orc_run_calls(const OrcCall *c, int n, int reps);
+
 #ifdef __cplusplus
 }
 #endif
