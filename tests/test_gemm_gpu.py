@@ -300,3 +300,16 @@ def test_every_tile_config(lib, orc, cfg):
                 assert normwise_rel(run_mm_atb(lib, P2, X, dY), orc.mm_atb_f64(P2.copy(), X, dY)) <= TOL
     finally:
         lib.check(lib.tlg_tune_force(-1, 0), "auto")
+
+
+@pytest.mark.parametrize("args", [[], ["1", "384", "384"], ["8", "2048", "384"], ["512", "256", "768", "7"]],
+                         ids=["selftest", "decode", "unembed", "ffn"])
+def test_c_selftest_through_seam(args):
+    """host/tl_selftest.c: mm / mm_bt / mm_atb called with the reference's
+    signatures (the -DUSE_HIP seam), checked against double precision loops
+    like tinylm.c's own selftest (tinylm.c:4750-4788), at the 1e-4 bar."""
+    import subprocess
+    exe = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "tinylm-c_amd", "tl_selftest")
+    r = subprocess.run([exe] + args, capture_output=True, text=True, timeout=100)
+    print(r.stdout, r.stderr, flush=True)
+    assert r.returncode == 0 and "PASS" in r.stdout
