@@ -96,7 +96,7 @@ int tlg_dev_zero(float *dst, size_t n, void *stream);
  * must be called before C is read.  Any single-call entry point flushes
  * first.  One stream at a time may use grouped launches. */
 typedef struct {
-    int op;                  /* 0 mm, 1 mm_bt, 2 mm_atb */
+    int op;                  /* 0 mm, 1 mm_bt, 2 mm_atb, 3 clear C[0, M*N) */
     int beta;                /* mm_bt / mm_atb: 1 add into C, 0 overwrite C */
     float *C;                /* Y, dX or dW */
     int M, K, N;             /* the primitive's arguments (N = N_0) */

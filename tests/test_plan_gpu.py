@@ -28,11 +28,21 @@ def snapshot(lib, host, plan, run, stream):
 
 
 def new_run(lib, host, plan, pool=1, seed=99):
+    """A device run of `plan` with every buffer seeded; buffers the plan
+    starts from zero (outputs, G) are filled with noise instead, so a clear
+    or a setting GEMM that did not happen cannot pass for one that did."""
     stream = lib.tlg_stream_create()
     run = host.dll.tl_run_new(ctypes.byref(plan.raw), pool)
     assert run, lib.tlg_last_error()
-    lib.check(host.dll.tl_run_fill(run, seed, stream), "fill")
+    fill(lib, host, plan, run, stream, seed)
     return run, stream
+
+
+def fill(lib, host, plan, run, stream, seed):
+    lib.check(host.dll.tl_run_fill(run, seed, stream), "fill")
+    for i, (name, n, init) in enumerate(plan.bufs):
+        if init == 3:
+            lib.check(lib.tlg_dev_fill_normal(host.dll.tl_run_buf(run, i), n, seed * 31 + i, 1.0, stream), name)
 
 
 @pytest.mark.parametrize("grouped", [0, 1], ids=["calls", "grouped"])
@@ -81,7 +91,7 @@ def test_graph_replays_match_eager(lib, grouped):
         eager = snapshot(lib, host, plan, run, stream)
         lib.check(host.dll.tl_run_graph_build(run, stream, grouped), "graph")
         for rep in range(3):
-            lib.check(host.dll.tl_run_fill(run, 5, stream), "refill")
+            fill(lib, host, plan, run, stream, 5)
             lib.check(host.dll.tl_run_graph_step(run, stream), "replay")
             got = snapshot(lib, host, plan, run, stream)
             for bname, _, _ in plan.bufs:

@@ -400,7 +400,8 @@ __global__ void k_split_reduce(const float *__restrict__ ws, float *__restrict__
 }
 
 // ------------------------------------------------------ grouped problems --
-enum { PK_NN = 0, PK_NT = 1, PK_TN = 2, PK_RED = 3 };
+enum { PK_NN = 0, PK_NT = 1, PK_TN = 2, PK_RED = 3, PK_ZERO = 4 };
+#define TLG_ZERO_CHUNK 4096          // floats a clear's work item sets to 0
 #define TLG_MAXSEG 3
 #define TLG_MAXPROB 16
 #define TLG_RED_CHUNK 256
@@ -564,6 +565,12 @@ __device__ __forceinline__ void group_body(const GroupArgs &g, float *smem)
     case PK_NN: group_tile<T, RC, OC>(smem, P, local); break;
     case PK_NT: group_tile<T, RC, RC>(smem, P, local); break;
     case PK_TN: group_tile<T, OC, OC>(smem, P, local); break;
+    case PK_ZERO: {
+        const size_t n = (size_t)P.Mo * P.No, e0 = (size_t)local * TLG_ZERO_CHUNK;
+        const size_t e1 = e0 + TLG_ZERO_CHUNK < n ? e0 + TLG_ZERO_CHUNK : n;
+        for (size_t e = e0 + threadIdx.x; e < e1; e += blockDim.x) P.C[e] = 0.f;
+        break;
+    }
     default: {
         if (P.nexp) { expert_reduce(P, local); break; }
         const size_t n = (size_t)P.Mo * P.No;
@@ -1073,7 +1080,7 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
             const char *o0, *o1;
             span(c.C, Mo, No, No, &o0, &o1);
             bool hit = overlap(c0, c1, o0, o1);
-            for (int s = 0; s < c.nseg && !hit; s++) {
+            for (int s = 0; s < c.nseg && !hit && op != 3; s++) {
                 const int Ns = s ? c.Nseg[s] : c.N;
                 const char *x0, *x1, *y0, *y1;
                 if (op == 0)      { span(c.A[s], c.M, c.K, c.K, &x0, &x1); span(c.B[s], c.K, Ns, Ns, &y0, &y1); }
@@ -1091,6 +1098,21 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
     int rmax = 0;
     for (int i = 0; i < n; i++) {
         const TlgGemmCall &c = calls[i];
+        if (c.op == 3) {
+            // a clear of C[0, M*N) riding along with the GEMMs
+            if (c.M <= 0 || c.N <= 0 || !c.C)
+                return tlg_fail(TLG_EINVAL, "tlg_dev_gemm_group: call %d: empty clear", i);
+            Prob &P = probs[i];
+            memset(&P, 0, sizeof P);
+            P.kind = PK_ZERO;
+            P.C = c.C;
+            P.Mo = c.M;
+            P.No = c.N;
+            P.ldc = c.N;
+            P.items = (int)(((size_t)c.M * c.N + TLG_ZERO_CHUNK - 1) / TLG_ZERO_CHUNK);
+            Rtot[i] = 0;
+            continue;
+        }
         if (c.op < 0 || c.op > 2 || c.nseg < 1 || c.nseg > TLG_MAXSEG || (c.nseg > 1 && c.op != 1))
             return tlg_fail(TLG_EINVAL, "tlg_dev_gemm_group: call %d: bad op/nseg", i);
         if (c.M < 0 || c.K < 0 || c.N < 0) return tlg_fail(TLG_EINVAL, "negative dimension");
@@ -1135,6 +1157,7 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
             const TileCfg &tc = kCfgs[g_cand[k]];
             double items = 0;
             for (int i = 0; i < n; i++) {
+                if (probs[i].kind == PK_ZERO) continue;
                 const double tiles = (double)cdiv(probs[i].Mo, tc.bm) * cdiv(probs[i].No, tc.bn);
                 const double sp = (probs[i].kind == PK_TN && Rtot[i] > rtarget + rtarget / 2)
                                 ? (double)cdiv(Rtot[i], rtarget) : 1.0;
@@ -1157,12 +1180,13 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
     double cost[TLG_MAXPROB / 2];
     for (int i = 0; i < n; i++) {
         Prob &P = probs[i];
+        order[i] = i;
+        if (P.kind == PK_ZERO) { cost[i] = 0.0; continue; }
         P.tiles_n = cdiv(P.No, tc.bn);
         P.tiles = cdiv(P.Mo, tc.bm) * P.tiles_n;
         plan_split(P, Rtot[i], rtarget, ws, ws_used, ws_cap);
         P.items = P.tiles * P.splits;
         cost[i] = (double)P.rps;              // reduction steps per item
-        order[i] = i;
     }
     // longest item first (stable: ties keep call order)
     for (int i = 1; i < n; i++)

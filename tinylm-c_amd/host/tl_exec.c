@@ -8,6 +8,7 @@
  */
 #include "tl_plan.h"
 #include "../../include/tlgemm.h"
+#include <limits.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -172,6 +173,7 @@ static void note(TlRun *r, int k, int kind, double flops, double bytes)
 
 static double gemm_flops(const TlgGemmCall *c)
 {
+    if (c->op == 3) return 0.0;
     double f = 0.0;
     for (int s = 0; s < c->nseg; s++)
         f += 2.0 * c->M * c->K * (double)(s ? c->Nseg[s] : c->N);
@@ -180,6 +182,7 @@ static double gemm_flops(const TlgGemmCall *c)
 
 static double gemm_bytes(const TlgGemmCall *c)
 {
+    if (c->op == 3) return 4.0 * (double)c->M * (double)c->N;
     const double M = c->M, K = c->K;
     double b = 0.0;
     for (int s = 0; s < c->nseg; s++) {
@@ -303,6 +306,28 @@ static int grouped(TlRun *r, void *stream, int dry)
             g.rd[g.nrd++] = a;
             g.rd[g.nrd++] = b;
             g.n++;
+        }
+        /* a clear the plan marks hoistable (nothing between the two runs
+         * touches its range) rides along with this run's launch */
+        if (!rc && g.n > 0 && end < p->ncall) {
+            int e2 = end, all = 1;
+            while (e2 < p->ncall && p->call[e2].run == p->call[end].run) e2++;
+            for (int z = end; z < e2; z++)
+                if (p->call[z].op != TL_ZERO || !p->call[z].hoist || p->call[z].n > (size_t)INT_MAX) all = 0;
+            for (int z = end; all && z < e2 && g.n < TL_GROUP_MAX; z++) {
+                const TlCall *c = &p->call[z];
+                if (group_conflict(&g, c)) continue;
+                Span o, a, b;
+                call_spans(c, &o, &a, &b);
+                TlgGemmCall *k = &g.call[g.n];
+                memset(k, 0, sizeof *k);
+                k->op = 3;
+                k->C = ptr(r, c->out, c->out_off);
+                k->M = (int)c->n;
+                k->N = 1;
+                g.wr[g.n++] = o;
+                gone[z] = 1;
+            }
         }
         if (!rc) rc = group_launch(r, &g, stream, dry, &launches);
         i = end;

@@ -171,6 +171,9 @@ int tl_plan_train(TlPlan *p, int R, int D, int KD, int F, int V, int L, int n_mt
     glue(p);                                        /* softmax + CE :1017-1028 */
     /* ---- memset(G) then backward, tinylm.c:2628, :1072-1154 ---- */
     CHK(zero(p, 2628, "G", G, 0, m0.total));
+    /* softmax / cross-entropy between the head GEMM and this memset touch
+     * logits, dlogits and the loss only: the clear may run with the head */
+    p->call[p->ncall - 1].hoist = 1;
     glue(p);                                        /* dlogits :1076-1082 */
     CHK(gemm(p, TL_MM, 1085, "dfn", dfn, 0, dlogits, 0, P, m0.emb, R, V, D));
     CHK(gemm(p, TL_MM_ATB, 1086, "dEmb", G, m0.emb, dlogits, 0, fn_norm, 0, R, V, D));

@@ -45,6 +45,10 @@ typedef struct {
     int run;                /* GEMM run: calls with the same run index are
                                issued back to back by the reference with no
                                non-GEMM code between them                   */
+    int hoist;              /* TL_ZERO only: nothing the reference runs
+                               between the previous GEMM run and this clear
+                               reads or writes the cleared range, so the
+                               clear may run with that run's launch         */
 } TlCall;
 
 typedef struct {

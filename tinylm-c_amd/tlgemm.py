@@ -189,7 +189,7 @@ class TlCall(ctypes.Structure):
                 ("out_off", ctypes.c_size_t), ("a_off", ctypes.c_size_t), ("b_off", ctypes.c_size_t),
                 ("M", ctypes.c_int), ("K", ctypes.c_int), ("N", ctypes.c_int),
                 ("n", ctypes.c_size_t), ("line", ctypes.c_int), ("what", ctypes.c_char * 16),
-                ("run", ctypes.c_int)]
+                ("run", ctypes.c_int), ("hoist", ctypes.c_int)]
 
 
 class TlPlan(ctypes.Structure):
