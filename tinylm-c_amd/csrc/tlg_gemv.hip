@@ -27,6 +27,7 @@
 // kernel arguments, workgroups dealt to problems in order.
 #include "tlg_internal.h"
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define GV_WAVES 8              // waves per workgroup (512 threads)
@@ -222,16 +223,16 @@ __device__ __forceinline__ void gemv_nt(const GvProb &P, int blk, float *As)
     }
 }
 
-template <int MB>
+template <int MB, int COLS>
 __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv(GvArgs g)
 {
     __shared__ float As[GV_ACHUNK];
-    __shared__ float red[GV_WAVES * MB * nn_cols(MB)];
+    __shared__ float red[GV_WAVES * MB * COLS];
     int b = blockIdx.x, p = 0;
     while (p < g.nprob && b >= g.p[p].blocks) { b -= g.p[p].blocks; p++; }
     if (p >= g.nprob) return;
     const GvProb &P = g.p[p];
-    if (P.kind == TLG_NN) gemv_nn<MB, nn_cols(MB)>(P, b, As, red);
+    if (P.kind == TLG_NN) gemv_nn<MB, COLS>(P, b, As, red);
     else gemv_nt<MB>(P, b, As);
 }
 
@@ -240,22 +241,49 @@ bool tlg_gemv_fits(TlgKind kind, int Mo) { return kind != TLG_TN && Mo >= 1 && M
 
 static int rows_bucket(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
-static void set_blocks(GvProb &P, int mb)
+static void set_blocks(GvProb &P, int cols)
 {
-    const int per = P.kind == TLG_NN ? nn_cols(mb) : GV_WAVES * GV_NT_ROWS;
+    const int per = P.kind == TLG_NN ? cols : GV_WAVES * GV_NT_ROWS;
     P.blocks = (P.No + per - 1) / per;
 }
 
-static int launch(const GvArgs &a, int mb, hipStream_t st)
+// Columns per workgroup of the mm form for a launch: nn_cols(), unless
+// TLG_GEMV_COLS (4, 8 or 16) pins it for sweeps.
+static int launch_cols(int mb)
 {
+    static int forced = -1;
+    if (forced < 0) {
+        const char *e = getenv("TLG_GEMV_COLS");
+        const int v = e ? atoi(e) : 0;
+        forced = (v == 4 || v == 8 || v == 16) ? v : 0;
+    }
+    return forced ? forced : nn_cols(mb);
+}
+
+template <int MB>
+static void launch_mb(const GvArgs &a, int grid, int cols, hipStream_t st)
+{
+    switch (cols) {
+    case 4: hipLaunchKernelGGL((k_gemv<MB, 4>), dim3(grid), dim3(64 * GV_WAVES), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((k_gemv<MB, 8>), dim3(grid), dim3(64 * GV_WAVES), 0, st, a); break;
+    default: hipLaunchKernelGGL((k_gemv<MB, 16>), dim3(grid), dim3(64 * GV_WAVES), 0, st, a); break;
+    }
+}
+
+static int launch(GvArgs &a, int mb, hipStream_t st)
+{
+    const int cols = launch_cols(mb);
     int grid = 0;
-    for (int i = 0; i < a.nprob; i++) grid += a.p[i].blocks;
+    for (int i = 0; i < a.nprob; i++) {
+        set_blocks(a.p[i], cols);
+        grid += a.p[i].blocks;
+    }
     if (grid == 0) return TLG_OK;
     switch (mb) {
-    case 1: hipLaunchKernelGGL(k_gemv<1>, dim3(grid), dim3(64 * GV_WAVES), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(k_gemv<2>, dim3(grid), dim3(64 * GV_WAVES), 0, st, a); break;
-    case 4: hipLaunchKernelGGL(k_gemv<4>, dim3(grid), dim3(64 * GV_WAVES), 0, st, a); break;
-    default: hipLaunchKernelGGL(k_gemv<8>, dim3(grid), dim3(64 * GV_WAVES), 0, st, a); break;
+    case 1: launch_mb<1>(a, grid, cols, st); break;
+    case 2: launch_mb<2>(a, grid, cols, st); break;
+    case 4: launch_mb<4>(a, grid, cols, st); break;
+    default: launch_mb<8>(a, grid, cols, st); break;
     }
     TLG_HIP(hipGetLastError());
     return TLG_OK;
@@ -263,12 +291,13 @@ static int launch(const GvArgs &a, int mb, hipStream_t st)
 
 const char *tlg_gemv_kernel_name(int M)
 {
-    switch (rows_bucket(M)) {
-    case 1: return "k_gemv<1>";
-    case 2: return "k_gemv<2>";
-    case 4: return "k_gemv<4>";
-    default: return "k_gemv<8>";
-    }
+    // as rocprofv3 names the instance the launch uses
+    static char names[4][3][24];
+    const int mb = rows_bucket(M), cols = launch_cols(mb);
+    const int mi = mb == 1 ? 0 : mb == 2 ? 1 : mb == 4 ? 2 : 3, ci = cols == 4 ? 0 : cols == 8 ? 1 : 2;
+    char *n = names[mi][ci];
+    if (!n[0]) snprintf(n, sizeof names[0][0], "k_gemv<%d, %d>", mb, cols);
+    return n;
 }
 
 int tlg_gemv_launch(TlgKind kind, const float *A, const float *B, float *C, int Mo, int No, int R, int lda,
@@ -279,7 +308,6 @@ int tlg_gemv_launch(TlgKind kind, const float *A, const float *B, float *C, int 
     GvProb &P = a.p[0];
     P.C = C; P.kind = kind; P.M = Mo; P.No = No; P.ldc = ldc; P.beta = beta; P.nseg = 1;
     P.seg[0] = GvSeg{A, B, R, lda, ldb};
-    set_blocks(P, rows_bucket(Mo));
     a.nprob = 1;
     return launch(a, rows_bucket(Mo), st);
 }
@@ -314,6 +342,5 @@ int tlg_gemv_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
         if (P.M > mmax) mmax = P.M;
     }
     a.nprob = n;
-    for (int i = 0; i < n; i++) set_blocks(a.p[i], rows_bucket(mmax));
     return launch(a, rows_bucket(mmax), st);
 }
