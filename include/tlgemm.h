@@ -86,9 +86,12 @@ int tlg_dev_zero(float *dst, size_t n, void *stream);
  * chain of up to 3 primitives accumulating into the same dX:
  *   dX (beta ? += : =) sum_s dY_s[M x N_s] @ W_s[K x N_s]^T
  * (N_0 = N).  beta = 0 turns "memset(C); mm_bt(C, ...)" into one call.
- * mm always sets.  The calls of one group must be independent (no call
- * reads or writes what another writes).  All operands must be 16-byte
- * aligned with row widths that are multiples of 4.
+ * mm always sets.  op 3 clears C[0, M*N) (K, nseg and the operands are
+ * ignored), so a memset can ride along with the GEMMs of a launch.  The calls
+ * of one group must be independent (no call reads or writes what another
+ * writes).  All operands must be 16-byte aligned with row widths that are
+ * multiples of 4 (TLG_EINVAL otherwise).  When every call is an mm or mm_bt
+ * with M <= 8 the group runs on the GEMV kernels instead.
  *
  * mm_atb calls with long reductions split them across workgroups; their
  * partial sums are added into C by the NEXT grouped launch on the stream
@@ -112,8 +115,8 @@ int tlg_dev_gemm_pending(void);
 /* Kernel instance grouped launches use, as rocprofv3 names it. */
 const char *tlg_group_kernel(void);
 /* Tuning hook: pin the tile configuration of grouped launches (an index of
- * the kernel's tile table; -1 = automatic: 64x64, 32x64 or 32x32 tiles,
- * the largest that still gives the CUs about two waves of work items). */
+ * the kernel's tile table; -1 = automatic: 64x64 tiles when a launch has at
+ * least 3 x 256 of them, else 64x32 tiles whose wave pairs split each stage). */
 int tlg_tune_group(int cfg);
 /* Tuning hook: the automatic policy itself -- candidate tile configs (up to
  * 3, first that yields min_waves x 256 work items wins, else the last; ncands
