@@ -165,6 +165,21 @@ def read_traffic(kernel):
     return None
 
 
+AUTOTUNE_CANDS = (3, 14, 13, 15, 0, 1, 20)
+
+
+def autotune(lib, host, run, stream, reps=3):
+    """Per-launch tile choice by timing (tl_run_autotune), before any timed
+    or captured step; returns {config: launches}."""
+    arr = (ctypes.c_int * len(AUTOTUNE_CANDS))(*AUTOTUNE_CANDS)
+    check(host.dll.tl_run_autotune(run, arr, len(AUTOTUNE_CANDS), reps, stream), "autotune")
+    picks = {}
+    for k in range(host.dll.tl_run_grouped_launches(run)):
+        c = host.dll.tl_run_launch_config(run, k)
+        picks[c] = picks.get(c, 0) + 1
+    return picks
+
+
 def roof_time_ms(plan):
     """Summed per-GEMM roofline time of a step: max(flops / MFMA peak,
     compulsory bytes / HBM peak) per call, clears at HBM speed."""
@@ -182,7 +197,7 @@ def roof_time_ms(plan):
     return roof_ms
 
 
-def bench_train_config(lib, host, stream, name, steps):
+def bench_train_config(lib, host, stream, name, steps, tune=True):
     """Another BASELINE training config (nano = configs[0], m8 = configs[2]):
     the same grouped, graph-replayed GEMM step."""
     cfg = TRAIN[name]
@@ -191,6 +206,7 @@ def bench_train_config(lib, host, stream, name, steps):
     if not run:
         raise RuntimeError("tl_run_new failed: " + lib.tlg_last_error().decode())
     check(host.dll.tl_run_fill(run, 1234567891011, stream), "fill")
+    tuned = autotune(lib, host, run, stream) if tune else None
     check(host.dll.tl_run_graph_build(run, stream, 1), "graph build")
     step = lambda: host.dll.tl_run_graph_step(run, stream)  # noqa: E731
     for _ in range(5):
@@ -205,6 +221,7 @@ def bench_train_config(lib, host, stream, name, steps):
         "steps": steps, "ms_per_step": round(per, 4), "tok_s": round(cfg["R"] / (per * 1e-3), 1),
         "tflops": round(plan.flops() / (per * 1e-3) / 1e12, 2),
         "sum_of_gemm_roof_ms": round(roof, 4), "roof_frac": round(roof / per, 4),
+        "tile_configs": tuned,
     }
 
 
@@ -405,6 +422,8 @@ def main():
     ap.add_argument("--moe-steps", type=int, default=20)
     ap.add_argument("--other-steps", type=int, default=20, help="timed steps of the other training configs")
     ap.add_argument("--no-probes", action="store_true", help="skip the copy / MFMA peak probes")
+    ap.add_argument("--no-autotune", action="store_true",
+                    help="keep the library's automatic tile policy instead of timing candidates per launch")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
@@ -427,6 +446,7 @@ def main():
     check(host.dll.tl_run_fill(run, 1234567891011, stream), "fill")
     grouped = 0 if args.calls else 1
     launches = host.dll.tl_run_grouped_launches(run) if grouped else None
+    tuned = autotune(lib, host, run, stream) if grouped and args.group_cfg is None and not args.no_autotune else None
     if args.eager:
         fn = host.dll.tl_run_step_grouped if grouped else host.dll.tl_run_step
         step = lambda: fn(run, stream)  # noqa: E731
@@ -481,7 +501,8 @@ def main():
     if args.other_steps > 0:
         for name in TRAIN:
             if name != args.config:
-                others[name] = bench_train_config(lib, host, stream, name, args.other_steps)
+                others[name] = bench_train_config(lib, host, stream, name, args.other_steps,
+                                                  tune=not args.no_autotune)
                 log(f"[train] {name}: {others[name]}")
     decode = {}
     if args.decode_steps > 0:
@@ -530,6 +551,7 @@ def main():
             "global_batch": cfg["R"] // 256, "seq_len": 256, "parallelism": "single GPU",
         },
         "tflops": round(tflops, 2),
+        "tile_configs": tuned,
         "step_roofline": {"sum_of_gemm_roof_ms": round(roof_ms, 4),
                           "frac": round(roof_ms / ms_step, 4)},
         "roofline": {

@@ -163,3 +163,33 @@ def test_group_tile_configs(lib, orc, gcfg):
     for bname, _, _ in plan.bufs:
         for label, a, b in plan.regions(bname):
             assert normwise_rel(got[bname][a:b], init[bname][a:b]) <= TOL, (gcfg, label)
+
+
+def test_autotuned_step_matches_oracle(lib, orc):
+    """tl_run_autotune gives each grouped launch its own tile shape; the
+    mixed step (eager and replayed from a graph) still meets the bar."""
+    host = tlgemm.host()
+    plan = host.plan_train(**bench.TRAIN["nano"])
+    run, stream = new_run(lib, host, plan, seed=11)
+    try:
+        cands = (ctypes.c_int * 4)(3, 14, 15, 0)
+        lib.check(host.dll.tl_run_autotune(run, cands, 4, 2, stream), "autotune")
+        picks = [host.dll.tl_run_launch_config(run, k) for k in range(host.dll.tl_run_grouped_launches(run))]
+        print("per-launch configs", picks, flush=True)
+        assert all(p in (-1, 3, 14, 15, 0) for p in picks)
+        fill(lib, host, plan, run, stream, 11)
+        init = snapshot(lib, host, plan, run, stream)
+        lib.check(host.dll.tl_run_step_grouped(run, stream), "step")
+        got = snapshot(lib, host, plan, run, stream)
+        fill(lib, host, plan, run, stream, 11)
+        lib.check(host.dll.tl_run_graph_build(run, stream, 1), "graph")
+        fill(lib, host, plan, run, stream, 11)
+        lib.check(host.dll.tl_run_graph_step(run, stream), "replay")
+        replay = snapshot(lib, host, plan, run, stream)
+    finally:
+        host.dll.tl_run_free(run)
+    run_plan_cpu(plan, init, orc)
+    for bname, _, _ in plan.bufs:
+        assert np.array_equal(got[bname], replay[bname]), bname
+        for label, a, b in plan.regions(bname):
+            assert normwise_rel(got[bname][a:b], init[bname][a:b]) <= TOL, label

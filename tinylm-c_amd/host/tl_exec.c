@@ -29,6 +29,9 @@ struct TlRun {
     double lflops[TL_MAXLAUNCH], lbytes[TL_MAXLAUNCH];
     int lkind[TL_MAXLAUNCH];             /* 0 grouped GEMM, 1 clear, 2 flush */
     const char *lname[TL_MAXLAUNCH];     /* kernel of each launch (NULL: none) */
+    /* tile configuration of each grouped launch: 0 = the library's automatic
+     * policy, else config + 1 (set by tl_run_autotune) */
+    int lcfg[TL_MAXLAUNCH];
 };
 
 static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -202,7 +205,12 @@ static int group_launch(TlRun *r, Group *g, void *stream, int dry, int *launches
     for (int k = 0; k < g->n; k++) { fl += gemm_flops(&g->call[k]); by += gemm_bytes(&g->call[k]); }
     note(r, *launches, 0, fl, by);
     int rc = dry ? 0 : mark(r, *launches, stream);
-    if (!rc && !dry) rc = tlg_dev_gemm_group(g->call, g->n, stream);
+    if (!rc && !dry) {
+        const int cfg = *launches < TL_MAXLAUNCH ? r->lcfg[*launches] - 1 : -1;
+        if (cfg >= 0) rc = tlg_tune_group(cfg);
+        if (!rc) rc = tlg_dev_gemm_group(g->call, g->n, stream);
+        if (cfg >= 0) { const int rc2 = tlg_tune_group(-1); if (!rc) rc = rc2; }
+    }
     if (!rc && !dry && *launches < TL_MAXLAUNCH) r->lname[*launches] = tlg_group_kernel();
     (*launches)++;
     g->n = g->nrd = 0;
@@ -402,4 +410,47 @@ int tl_run_graph_step(TlRun *r, void *stream)
     int rc = tlg_graph_launch(r->graph[r->cur], stream);
     r->cur = (r->cur + 1) % r->pool;
     return rc;
+}
+
+/* Per-launch tile choice by measurement: run `reps` timed steps with every
+ * candidate configuration applied to all grouped launches, then give each
+ * launch the candidate with the least time.  Numerically every candidate is
+ * a valid schedule of the same sums (the plan tests cover each one). */
+int tl_run_autotune(TlRun *r, const int *cands, int ncands, int reps, void *stream)
+{
+    if (!r || !cands || ncands <= 0 || reps <= 0) return -1;
+    const int L = grouped(r, stream, 1);
+    if (L < 0 || L + 2 > TL_MAXLAUNCH) return -1;
+    double *best = malloc(sizeof(double) * (size_t)L);
+    void **ev = malloc(sizeof(void *) * (size_t)(L + 2));
+    int *pick = malloc(sizeof(int) * (size_t)L);
+    if (!best || !ev || !pick) { free(best); free(ev); free(pick); return TLG_ENOMEM; }
+    int rc = 0, made = 0;
+    for (; made < L + 2; made++)
+        if (!(ev[made] = tlg_event_create())) { rc = -1; break; }
+    for (int k = 0; k < L; k++) { best[k] = 1e30; pick[k] = 0; }
+    for (int c = 0; c < ncands && !rc; c++) {
+        for (int k = 0; k < L; k++) r->lcfg[k] = cands[c] + 1;
+        double *t = calloc((size_t)L, sizeof(double));
+        if (!t) { rc = TLG_ENOMEM; break; }
+        rc = tl_run_step_grouped(r, stream);                /* warm up this shape */
+        for (int rep = 0; rep < reps && !rc; rep++) {
+            rc = tl_run_time_launches(r, ev, L + 2, stream);
+            if (!rc) rc = tlg_stream_sync(stream);
+            for (int k = 0; k < L && !rc; k++) t[k] += tlg_event_elapsed_ms(ev[k], ev[k + 1]);
+        }
+        for (int k = 0; k < L && !rc; k++)
+            if (r->lkind[k] == 0 && t[k] < best[k]) { best[k] = t[k]; pick[k] = cands[c] + 1; }
+        free(t);
+    }
+    for (int k = 0; k < L; k++) r->lcfg[k] = rc ? 0 : pick[k];
+    for (int k = 0; k < made; k++) tlg_event_destroy(ev[k]);
+    free(best); free(ev); free(pick);
+    return rc;
+}
+
+int tl_run_launch_config(TlRun *r, int k)
+{
+    if (!r || k < 0 || k >= TL_MAXLAUNCH) return -1;
+    return r->lcfg[k] - 1;
 }

@@ -112,6 +112,12 @@ int    tl_run_launch_info(TlRun *r, int k, double *flops, double *bytes);
 /* Kernel that launch k of the last timed step ran, as rocprofv3 names it
  * (without "void " and the argument list), or NULL if nothing launched. */
 const char *tl_run_launch_kernel(TlRun *r, int k);
+/* Choose each grouped launch's tile configuration by timing: `reps` steps per
+ * candidate (indices of the library's tile table, see tlg_tune_group), each
+ * launch keeping its fastest.  Later grouped steps and graphs use the choice;
+ * tl_run_launch_config reports it (-1 = the library's automatic policy). */
+int    tl_run_autotune(TlRun *r, const int *cands, int ncands, int reps, void *stream);
+int    tl_run_launch_config(TlRun *r, int k);
 /* Capture one step into a HIP graph and replay it (grouped != 0: the grouped
  * step, else call by call).  The graph is bound to
  * the pool copy current at capture; tl_run_graph_step replays the graph for

@@ -293,6 +293,10 @@ class Host:
         d.tl_run_time_launches.restype = _i
         d.tl_run_launch_info.argtypes = [_vp, _i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
         d.tl_run_launch_info.restype = _i
+        d.tl_run_autotune.argtypes = [_vp, _ip, _i, _i, _vp]
+        d.tl_run_autotune.restype = _i
+        d.tl_run_launch_config.argtypes = [_vp, _i]
+        d.tl_run_launch_config.restype = _i
         d.tl_run_launch_kernel.argtypes = [_vp, _i]
         d.tl_run_launch_kernel.restype = ctypes.c_char_p
         d.tl_run_call.argtypes = [_vp, _i, _vp]
