@@ -433,11 +433,11 @@ struct GroupArgs {
 // Real work items of an expert-batched problem, from the device-resident
 // row offsets: sum over experts of ceil(rows_e / unit) row units, times the
 // column tiles (NN / NT) or the output tiles (TN).
-__device__ __forceinline__ int expert_items(const Prob &P)
+__device__ __forceinline__ int expert_items(const Prob &P, const int *eo)
 {
     int units = 0;
     for (int e = 0; e < P.nexp; e++) {
-        const int c = P.eoff[e + 1] - P.eoff[e];
+        const int c = eo[e + 1] - eo[e];
         units += c > 0 ? (c + P.unit - 1) / P.unit : 0;
     }
     return units * (P.kind == PK_TN ? P.tiles : P.tiles_n);
@@ -445,12 +445,12 @@ __device__ __forceinline__ int expert_items(const Prob &P)
 
 // Item -> (expert e, row unit t of that expert, first partial slot of e).
 // Returns false when the item is past the experts' real work.
-__device__ __forceinline__ bool expert_of(const Prob &P, int t, int *e_out, int *t_out, int *base,
-                                          int *rows, int *slot0)
+__device__ __forceinline__ bool expert_of(const Prob &P, const int *eo, int t, int *e_out, int *t_out,
+                                          int *base, int *rows, int *slot0)
 {
     int slot = 0;
     for (int e = 0; e < P.nexp; e++) {
-        const int b = P.eoff[e], c = P.eoff[e + 1] - b;
+        const int b = eo[e], c = eo[e + 1] - b;
         const int n = c > 0 ? (c + P.unit - 1) / P.unit : 0;
         if (t < n) { *e_out = e; *t_out = t; *base = b; *rows = c; *slot0 = slot; return true; }
         t -= n;
@@ -460,12 +460,12 @@ __device__ __forceinline__ bool expert_of(const Prob &P, int t, int *e_out, int 
 }
 
 template <class T, int LA, int LB>
-__device__ __forceinline__ void expert_tile(float *smem, const Prob &P, int local)
+__device__ __forceinline__ void expert_tile(float *smem, const Prob &P, int local, const int *eo)
 {
     f32x16 acc[T::FM][T::FN][T::NCH];
     int e, t, base, rows, slot0;
     if (P.kind != PK_TN) {
-        if (!expert_of(P, local / P.tiles_n, &e, &t, &base, &rows, &slot0)) return;
+        if (!expert_of(P, eo, local / P.tiles_n, &e, &t, &base, &rows, &slot0)) return;
         const int i0 = t * T::BM, j0 = (local % P.tiles_n) * T::BN;
         zero_acc(acc);
         for (int k = 0; k < P.nseg; k++) {
@@ -475,7 +475,7 @@ __device__ __forceinline__ void expert_tile(float *smem, const Prob &P, int loca
         }
         tile_store<T>(acc, P.C + (size_t)base * P.ldc, P.ldc, P.beta, rows, P.No, i0, j0, smem);
     } else {
-        if (!expert_of(P, local / P.tiles, &e, &t, &base, &rows, &slot0)) return;
+        if (!expert_of(P, eo, local / P.tiles, &e, &t, &base, &rows, &slot0)) return;
         const int tile = local % P.tiles;
         const int i0 = (tile / P.tiles_n) * T::BM, j0 = (tile % P.tiles_n) * T::BN;
         const int rbeg = base + t * P.unit, rend = min(base + rows, rbeg + P.unit);
@@ -489,17 +489,17 @@ __device__ __forceinline__ void expert_tile(float *smem, const Prob &P, int loca
 
 // Reduction of an expert TN problem: C_e (beta ? += : =) the sum of expert
 // e's partial slots, in slot order.
-__device__ __forceinline__ void expert_reduce(const Prob &P, int local)
+__device__ __forceinline__ void expert_reduce(const Prob &P, int local, const int *eo)
 {
     const size_t n = (size_t)P.Mo * P.No;
     const int chunks = (int)((n + TLG_RED_CHUNK - 1) / TLG_RED_CHUNK);
     const int e = local / chunks;
     int slot0 = 0;
     for (int k = 0; k < e; k++) {
-        const int c = P.eoff[k + 1] - P.eoff[k];
+        const int c = eo[k + 1] - eo[k];
         slot0 += c > 0 ? (c + P.unit - 1) / P.unit : 0;
     }
-    const int c = P.eoff[e + 1] - P.eoff[e];
+    const int c = eo[e + 1] - eo[e];
     const int ns = c > 0 ? (c + P.unit - 1) / P.unit : 0;
     const size_t e0 = (size_t)(local % chunks) * TLG_RED_CHUNK;
     const size_t e1 = e0 + TLG_RED_CHUNK < n ? e0 + TLG_RED_CHUNK : n;
@@ -513,9 +513,9 @@ __device__ __forceinline__ void expert_reduce(const Prob &P, int local)
 }
 
 template <class T, int LA, int LB>
-__device__ __forceinline__ void group_tile(float *smem, const Prob &P, int local)
+__device__ __forceinline__ void group_tile(float *smem, const Prob &P, int local, const int *eo)
 {
-    if (P.nexp) { expert_tile<T, LA, LB>(smem, P, local); return; }
+    if (P.nexp) { expert_tile<T, LA, LB>(smem, P, local, eo); return; }
     const int z = local / P.tiles, tile = local % P.tiles;
     const int i0 = (tile / P.tiles_n) * T::BM, j0 = (tile % P.tiles_n) * T::BN;
     f32x16 acc[T::FM][T::FN][T::NCH];
@@ -540,13 +540,13 @@ __device__ __forceinline__ void group_tile(float *smem, const Prob &P, int local
 // XCD gets the same mix of long and short items), problem by problem in
 // list order (the host lists problems longest item first).  Workgroups past
 // their XCD's share exit at once.
-__device__ __forceinline__ int group_item(const GroupArgs &g, int b, int *local)
+__device__ __forceinline__ int group_item(const GroupArgs &g, int b, int *local, const int *eo)
 {
     const int x = b & 7;
     int slot = b >> 3;
     for (int p = 0; p < g.nprob; p++) {
         // expert-batched GEMMs: the real item count, known only on the device
-        const int n = (g.p[p].nexp && g.p[p].kind != PK_RED) ? expert_items(g.p[p]) : g.p[p].items;
+        const int n = (g.p[p].nexp && g.p[p].kind != PK_RED) ? expert_items(g.p[p], eo) : g.p[p].items;
         const int lo = (x * n) >> 3, hi = ((x + 1) * n) >> 3;
         if (slot < hi - lo) { *local = lo + slot; return p; }
         slot -= hi - lo;
@@ -554,17 +554,19 @@ __device__ __forceinline__ int group_item(const GroupArgs &g, int b, int *local)
     return -1;
 }
 
+// `eo`: the expert row offsets of an expert-batched launch, staged in LDS
+// (nullptr for dense launches, which have no expert problems).
 template <class T>
-__device__ __forceinline__ void group_body(const GroupArgs &g, float *smem)
+__device__ __forceinline__ void group_body(const GroupArgs &g, float *smem, const int *eo)
 {
     int local = 0;
-    const int p = group_item(g, blockIdx.x, &local);
+    const int p = group_item(g, blockIdx.x, &local, eo);
     if (p < 0) return;
     const Prob &P = g.p[p];
     switch (P.kind) {
-    case PK_NN: group_tile<T, RC, OC>(smem, P, local); break;
-    case PK_NT: group_tile<T, RC, RC>(smem, P, local); break;
-    case PK_TN: group_tile<T, OC, OC>(smem, P, local); break;
+    case PK_NN: group_tile<T, RC, OC>(smem, P, local, eo); break;
+    case PK_NT: group_tile<T, RC, RC>(smem, P, local, eo); break;
+    case PK_TN: group_tile<T, OC, OC>(smem, P, local, eo); break;
     case PK_ZERO: {
         const size_t n = (size_t)P.Mo * P.No, e0 = (size_t)local * TLG_ZERO_CHUNK;
         const size_t e1 = e0 + TLG_ZERO_CHUNK < n ? e0 + TLG_ZERO_CHUNK : n;
@@ -572,7 +574,7 @@ __device__ __forceinline__ void group_body(const GroupArgs &g, float *smem)
         break;
     }
     default: {
-        if (P.nexp) { expert_reduce(P, local); break; }
+        if (P.nexp) { expert_reduce(P, local, eo); break; }
         const size_t n = (size_t)P.Mo * P.No;
         const size_t e0 = (size_t)local * TLG_RED_CHUNK;
         const size_t e1 = e0 + TLG_RED_CHUNK < n ? e0 + TLG_RED_CHUNK : n;
@@ -585,16 +587,23 @@ template <class T>
 __global__ __launch_bounds__(T::THREADS) void k_group(GroupArgs g)
 {
     __shared__ __attribute__((aligned(16))) float smem[T::lds_max()];
-    group_body<T>(g, smem);
+    group_body<T>(g, smem, nullptr);
 }
 
 // The same code for the expert-batched launches of the MoE layer, under its
 // own name so profiles separate MoE launches from the dense grouped GEMMs.
+// Every problem of such a launch shares one row-offset array; it is staged in
+// LDS once, so finding a work item's expert costs no dependent global loads.
+#define TLG_MAX_EXPERTS 64
 template <class T>
 __global__ __launch_bounds__(T::THREADS) void k_expert_group(GroupArgs g)
 {
     __shared__ __attribute__((aligned(16))) float smem[T::lds_max()];
-    group_body<T>(g, smem);
+    __shared__ int eo[TLG_MAX_EXPERTS + 1];
+    const int E = g.p[0].nexp;
+    for (int i = threadIdx.x; i <= E; i += blockDim.x) eo[i] = g.p[0].eoff[i];
+    __syncthreads();
+    group_body<T>(g, smem, eo);
 }
 
 __global__ void k_zero(float *__restrict__ p, size_t n)
@@ -1222,7 +1231,8 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     int rc = tlg_ensure_init();
     if (rc) return rc;
     if (n > TLG_MAXPROB / 2) return tlg_fail(TLG_EINVAL, "expert launch: at most %d calls", TLG_MAXPROB / 2);
-    if (!eoff || E < 1 || rows < 0) return tlg_fail(TLG_EINVAL, "expert launch: bad row offsets");
+    if (!eoff || E < 1 || E > TLG_MAX_EXPERTS || rows < 0)
+        return tlg_fail(TLG_EINVAL, "expert launch: bad row offsets or %d experts", E);
     if (rows == 0) return TLG_OK;
     // the partial slots below reuse the whole workspace
     rc = tlg_group_flush_launch(st);
