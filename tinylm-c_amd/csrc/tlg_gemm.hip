@@ -405,6 +405,7 @@ enum { PK_NN = 0, PK_NT = 1, PK_TN = 2, PK_RED = 3, PK_ZERO = 4 };
 #define TLG_MAXSEG 3
 #define TLG_MAXPROB 16
 #define TLG_RED_CHUNK 256
+#define TLG_ERED_CHUNK 2048            // elements per work item of an expert reduction
 
 struct Seg { const float *A, *B; int R, lda, ldb; };
 struct Prob {
@@ -492,7 +493,7 @@ __device__ __forceinline__ void expert_tile(float *smem, const Prob &P, int loca
 __device__ __forceinline__ void expert_reduce(const Prob &P, int local, const int *eo)
 {
     const size_t n = (size_t)P.Mo * P.No;
-    const int chunks = (int)((n + TLG_RED_CHUNK - 1) / TLG_RED_CHUNK);
+    const int chunks = (int)((n + TLG_ERED_CHUNK - 1) / TLG_ERED_CHUNK);
     const int e = local / chunks;
     int slot0 = 0;
     for (int k = 0; k < e; k++) {
@@ -501,8 +502,8 @@ __device__ __forceinline__ void expert_reduce(const Prob &P, int local, const in
     }
     const int c = eo[e + 1] - eo[e];
     const int ns = c > 0 ? (c + P.unit - 1) / P.unit : 0;
-    const size_t e0 = (size_t)(local % chunks) * TLG_RED_CHUNK;
-    const size_t e1 = e0 + TLG_RED_CHUNK < n ? e0 + TLG_RED_CHUNK : n;
+    const size_t e0 = (size_t)(local % chunks) * TLG_ERED_CHUNK;
+    const size_t e1 = e0 + TLG_ERED_CHUNK < n ? e0 + TLG_ERED_CHUNK : n;
     float *C = P.C + (size_t)e * P.es;
     if (ns == 0) {
         if (!P.beta)
@@ -871,6 +872,7 @@ static int g_group_cfg = -1;
 static double g_min_waves = 3.0;
 static int g_cand[4] = {3, 14, -1, -1};   // 64x64, then 64x32 (2 x 2 waves)
 static int g_rtarget = 512;
+static int g_erps = 1024;                // expert TN slice (TLG_EXPERT_RPS)
 static int g_group_last = 3;          // shape of the most recent grouped launch
 static const char *g_group_last_name = nullptr;   // set when that launch was a GEMV group
 
@@ -893,6 +895,8 @@ static void group_env(void)
         }
         g_cand[k] = -1;
     }
+    e = getenv("TLG_EXPERT_RPS");
+    if (e && atoi(e) >= 64) g_erps = atoi(e);
     e = getenv("TLG_GROUP_RTARGET");
     if (e && atoi(e) >= 64) g_rtarget = atoi(e);
 }
@@ -1238,8 +1242,8 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     rc = tlg_group_flush_launch(st);
     if (rc) return rc;
 
+    group_env();
     Prob probs[TLG_MAXPROB / 2];
-    int rmax = 0;
     for (int i = 0; i < n; i++) {
         const TlgExpertCall &c = calls[i];
         if (c.op < 0 || c.op > 2 || c.nseg < 1 || c.nseg > 2 || (c.nseg > 1 && c.op != 1))
@@ -1253,7 +1257,6 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
         P.eoff = eoff;
         P.nexp = E;
         P.es = c.es;
-        int R = 0;
         bool vec = c.C && (c.es % 4 == 0);
         for (int s = 0; s < c.nseg; s++) {
             const int Ns = s ? c.Nseg[s] : c.N;
@@ -1264,17 +1267,15 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
             case 1: P.No = c.K; g.R = Ns; g.lda = Ns; g.ldb = Ns; break;
             default: P.Mo = c.K; P.No = c.N; g.R = rows; g.lda = c.K; g.ldb = c.N; break;
             }
-            R += g.R;
             vec = vec && g.A && g.B && al16(g.A) && al16(g.B) && g.lda % 4 == 0 && g.ldb % 4 == 0 && g.R > 0;
         }
         P.ldc = P.No;
         if (!vec || P.No <= 0 || (c.op == 2 && P.Mo <= 0) || P.No % 4 || P.Mo % 4)
             return tlg_fail(TLG_EINVAL, "expert launch: call %d needs aligned operands, widths %% 4 == 0", i);
-        if (c.op != 2 && R > rmax) rmax = R;
     }
-    // reduction slices of the TN problems: about the reduction length of the
-    // row problems of the launch, halved until the partials fit
-    int rps = cdiv(rmax > g_rtarget ? rmax : g_rtarget, 64) * 64;
+    // reduction slices of the TN problems (g_erps rows, doubled until the
+    // partials fit): short slices balance experts of very different sizes
+    int rps = cdiv(g_erps, 64) * 64;
     auto need = [&](int u) {
         size_t t = 0;
         for (int i = 0; i < n; i++)
@@ -1334,7 +1335,7 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
         if (P.kind == PK_TN) {
             Prob r = P;
             r.kind = PK_RED;
-            r.items = E * (int)(((size_t)P.Mo * P.No + TLG_RED_CHUNK - 1) / TLG_RED_CHUNK);
+            r.items = E * (int)(((size_t)P.Mo * P.No + TLG_ERED_CHUNK - 1) / TLG_ERED_CHUNK);
             red.p[red.nprob++] = r;
         }
     }
