@@ -12,9 +12,10 @@ W ~ N(0,0.02^2), dY ~ N(0,0.01^2)) already in HBM when timing starts.
 
 Prints one JSON line: train tokens/s (value), the dominant kernel's roofline,
 the decode GEMV figures at M = 1, 2, 4, 8, the top-1
-MoE layer, the achievable copy / MFMA peaks of this box, and the
-CPU baseline -- the reference's own kernels (oracle/_ref) timed on this host
-on a bounded sample.
+MoE layer, the whole device-resident training step (forward +
+backward + AdamW at the same model shape, "train_step"), the achievable
+copy / MFMA peaks of this box, and the CPU baseline -- the reference's own
+kernels and whole step (oracle/_ref) timed on this host on a bounded sample.
 """
 import argparse
 import ctypes
@@ -404,6 +405,83 @@ def cpu_decode_baseline(host, M, steps, threads):
     }
 
 
+def model_of(name):
+    """The TRAIN config as a whole model (head_dim 32, T = 256)."""
+    cfg = TRAIN[name]
+    return dict(V=cfg["V"], D=cfg["D"], L=cfg["L"], H=cfg["D"] // 32, KV=cfg["KD"] // 32, F=cfg["F"], T=256,
+                n_mtp=cfg["n_mtp"]), cfg["R"] // 256
+
+
+def bench_full_step(lib, host, stream, name, steps, warmup=3):
+    """The whole training step on the device (host/tl_train.h): forward,
+    backward with the MTP heads, gradnorm and AdamW -- tinylm.c's
+    train_loop body (:2627-2633), every activation resident in HBM --
+    replayed as one HIP graph.  Weights ~ N(0, 0.02^2) drawn on the device,
+    random tokens."""
+    import numpy as np
+    kw, B = model_of(name)
+    tr = host.train(kw, B)
+    check(lib.tlg_dev_fill_normal(tr.buf(0), tr.np, 99, 0.02, stream), "fill P")
+    rng = np.random.default_rng(3)
+    N = B * kw["T"]
+    tok, tgt = (rng.integers(0, kw["V"], N).astype(np.int32) for _ in range(2))
+    tm = rng.integers(0, kw["V"], (max(kw["n_mtp"], 1), N)).astype(np.int32) if kw["n_mtp"] else None
+    tr.set_batch(tok, tgt, tm, stream)
+    tr.set_hyper(3e-4, 0.9, 0.95, 0.1, 1, stream)
+    tr.step(stream)                                   # sizes every scratch buffer
+    loss0 = tr.loss(stream)
+    phases = tr.time_phases(stream)
+    tr.graph_build(stream)
+    for _ in range(warmup):
+        tr.graph_step(stream)
+    check(lib.tlg_stream_sync(stream), "sync")
+    ms, _ = time_steps(lib, lambda: tr.graph_step(stream), stream, steps)
+    loss1 = tr.loss(stream)
+    ms_step = ms / steps
+    return {"model": kw, "batch": B, "rows": N, "params": tr.np, "steps": steps,
+            "ms_per_step": round(ms_step, 4), "tok_s": round(N / (ms_step / 1e3), 1),
+            "phases_ms_eager": {"forward": round(phases[0], 4), "backward": round(phases[1], 4),
+                                "gradnorm_adamw": round(phases[2], 4)},
+            "loss_first": round(loss0, 4), "loss_after": round(loss1, 4)}
+
+
+def cpu_full_step(name, threads, steps=2):
+    """The reference's own forward + memset(G) + backward + gradnorm + AdamW
+    (tinylm.c:2627-2633, compiled from its lines into oracle/_ref) on host
+    cores at the same model shape; None when _ref is absent."""
+    import numpy as np
+    import oracle
+    try:
+        st = oracle.StepFns("reference")
+    except FileNotFoundError:
+        return None
+    ref = oracle.Reference()
+    ref.set_threads(threads)
+    kw, B = model_of(name)
+    m = oracle.model(**kw)
+    P = st.init_params(m, 1234567891011)
+    rng = np.random.default_rng(3)
+    N = B * m.T
+    tok, tgt = (rng.integers(0, m.V, N).astype(np.int32) for _ in range(2))
+    tm = rng.integers(0, m.V, (max(m.n_mtp, 1), N)).astype(np.int32)
+    M, V = np.zeros_like(P), np.zeros_like(P)
+
+    def one(t):
+        _, G = st.train_step(m, B, P, tok, tgt, tm)
+        gn = st.gradnorm(G)
+        st.adamw(P, G, M, V, 3e-4, 0.9, 0.95, 0.1, t, 1.0 / gn if gn > 1.0 else 1.0)
+
+    one(1)                                             # warmup (as cmd_bench, :4732)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        one(i + 2)
+    dt = time.perf_counter() - t0
+    return {"value": round(N * steps / dt, 1), "unit": "train tokens/s (whole step)", "cores": threads,
+            "kind": "reference", "s_per_step": round(dt / steps, 4),
+            "sample": f"{steps} whole {name} training steps (forward + backward + gradnorm + AdamW, the "
+                      f"reference's own code) after 1 warmup, {threads} OpenMP threads; {dt:.1f} s timed"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -424,6 +502,8 @@ def main():
     ap.add_argument("--no-probes", action="store_true", help="skip the copy / MFMA peak probes")
     ap.add_argument("--no-autotune", action="store_true",
                     help="keep the library's automatic tile policy instead of timing candidates per launch")
+    ap.add_argument("--full-steps", type=int, default=30,
+                    help="timed whole training steps (forward + backward + AdamW on the device); 0 skips")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
@@ -513,6 +593,11 @@ def main():
     if args.moe_steps > 0:
         moe = bench_moe(lib, stream, args.moe_steps)
         log(f"[moe] {moe}")
+    full = None
+    if args.full_steps > 0:
+        full = bench_full_step(lib, host, stream, args.config, args.full_steps)
+        full["gemm_set_share"] = round(ms_step / full["ms_per_step"], 4)
+        log(f"[full step] {full}")
     peaks = None if args.no_probes else probes(lib, stream)
     if peaks:
         log(f"[probes] {peaks}")
@@ -523,6 +608,9 @@ def main():
         log(f"[cpu] timing the reference kernels on {threads} threads ...")
         cpu = cpu_baseline(host, args.config, args.cpu_steps, threads)
         log(f"[cpu] {cpu}")
+        if args.full_steps > 0:
+            cpu["train_step"] = cpu_full_step(args.config, threads)
+            log(f"[cpu] whole step {cpu['train_step']}")
         if args.decode_steps > 0:
             cpu["decode"] = {str(M): cpu_decode_baseline(host, M, 200 if M == 1 else 50, threads) for M in (1, 8)}
             log(f"[cpu] decode {cpu['decode']}")
@@ -570,6 +658,7 @@ def main():
         "decode_m1": decode.get(1),
         "decode": {str(k): v for k, v in decode.items()},
         "moe": moe,
+        "train_step": full,
         "achievable": peaks,
         "cpu_baseline": cpu,
     }

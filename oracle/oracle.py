@@ -315,3 +315,174 @@ class F64Prims:
 
     def mm_atb(self, dW, X, dY):
         return self.o.mm_atb_f64(dW, X, dY)
+
+
+# ---- training-step glue (tl_oracle_step.c / the reference's own functions) ----
+SEQ_LIB = os.path.join(HERE, "_ref", "libtlref_seq.so")
+_sz = ctypes.c_size_t
+_fl = ctypes.c_float
+
+
+class OrcModel(ctypes.Structure):
+    """tl_oracle.h OrcModel: the model shape (tinylm.c Cfg without QK-norm)."""
+    _fields_ = [(n, ctypes.c_int) for n in ("V", "D", "L", "H", "KV", "F", "T", "n_mtp", "n_exp", "win",
+                                            "full_every")] + [("rope_base", ctypes.c_float)]
+
+
+def model(V, D, L, H, KV, F, T, n_mtp=0, n_exp=0, win=0, full_every=0, rope_base=10000.0):
+    return OrcModel(V, D, L, H, KV, F, T, n_mtp, n_exp, win, full_every, rope_base)
+
+
+class OrcLayerMap(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_size_t) for n in ("emb", "an1", "wq", "wk", "wv", "wo", "an2", "wr", "w1", "w3",
+                                               "w2", "nf", "mtp0", "total")]
+
+
+class StepFns:
+    """The step's non-GEMM functions and a whole forward + backward step,
+    either from the oracle's restatement (which="oracle", liboracle.so) or
+    from the reference's own compiled code (which="reference",
+    _ref/libtlref_seq.so).  Same methods and semantics for both, so a test
+    can hold one against the other."""
+
+    def __init__(self, which="oracle"):
+        self.ref = which == "reference"
+        path = SEQ_LIB if self.ref else LIB
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        d = ctypes.CDLL(path)
+        p = "tlref_" if self.ref else "orc_"
+        self.p, self.dll = p, d
+        sig = {
+            "rmsnorm_fwd": (None, [_fp, _fp, _fp, _fp, _i, _i]),
+            "rmsnorm_bwd": (None, [_fp, _fp, _fp, _fp, _fp, _fp, _i, _i]),
+            "attn_fwd": (None, [_fp, _fp, _fp, _fp, _i, _i, _i, _i, _i, _i]),
+            "attn_bwd": (None, [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _i, _i, _i, _i, _i, _i]),
+            "adamw": (None, [_fp, _fp, _fp, _fp, _sz, _fl, _fl, _fl, _fl, _i, _fl]),
+            "gradnorm": (_fl, [_fp, _sz]),
+        }
+        if self.ref:
+            sig.update({
+                "rope_table": (None, [_fp, _fp, _i, _i]),
+                "rope": (None, [_fp, _ip, _i, _i, _i, _i, _i]),
+                "param_count": (_sz, [_i] * 9),
+                "init_params": (None, [_fp, ctypes.c_ulonglong] + [_i] * 9),
+                "train_step": (_fl, [_fp, _fp, _ip, _ip, _ip] + [_i] * 12),
+            })
+        else:
+            sig.update({
+                "rope_table": (None, [_fp, _fp, _i, _i, _fl]),
+                "rope": (None, [_fp, _ip, _i, _i, _i, _i, _fp, _fp, _i]),
+                "param_map": (None, [ctypes.POINTER(OrcModel), _i, ctypes.POINTER(OrcLayerMap)]),
+                "init_params": (None, [ctypes.POINTER(OrcModel), _fp, ctypes.c_uint64]),
+                "train_step": (_fl, [ctypes.POINTER(OrcModel), _i, _fp, _fp, _ip, _ip, _ip]),
+                "xent": (ctypes.c_double, [_fp, _ip, _fp, _fl, _i, _i]),
+                "embed_fwd": (None, [_fp, _fp, _ip, _i, _i]),
+                "embed_bwd": (None, [_fp, _fp, _ip, _i, _i]),
+            })
+        for name, (res, args) in sig.items():
+            f = getattr(d, p + name)
+            f.restype, f.argtypes = res, args
+
+    def _fn(self, name):
+        return getattr(self.dll, self.p + name)
+
+    def rmsnorm_fwd(self, x, g):
+        rows, D = x.shape
+        out = np.empty_like(x)
+        rinv = np.empty(rows, np.float32)
+        self._fn("rmsnorm_fwd")(_f(x), _f(g), _f(out), _f(rinv), rows, D)
+        return out, rinv
+
+    def rmsnorm_bwd(self, x, g, rinv, dy, dx, dg):
+        """dx += ..., dg += ... in place."""
+        rows, D = x.shape
+        self._fn("rmsnorm_bwd")(_f(x), _f(g), _f(rinv), _f(dy), _f(dx), _f(dg), rows, D)
+
+    def rope_table(self, maxpos, hd):
+        cs = np.empty((maxpos, hd // 2), np.float32)
+        sn = np.empty_like(cs)
+        if self.ref:
+            self._fn("rope_table")(_f(cs), _f(sn), maxpos, hd)
+        else:
+            self._fn("rope_table")(_f(cs), _f(sn), maxpos, hd, 10000.0)
+        return cs, sn
+
+    def rope(self, buf, T, nh, hd, back, pos=None):
+        """In place on buf [rows][nh*hd]; row r at pos[r], else r % T."""
+        rows = buf.shape[0]
+        if pos is None:
+            pos = (np.arange(rows) % T).astype(np.int32)
+        maxpos = int(pos.max()) + 1 if rows else 1
+        if self.ref:
+            self._fn("rope")(_f(buf), _n(pos), rows, nh, hd, maxpos, back)
+        else:
+            cs, sn = self.rope_table(maxpos, hd)
+            self._fn("rope")(_f(buf), _n(pos), T, rows, nh, hd, _f(cs), _f(sn), back)
+
+    def attn_fwd(self, q, k, v, B, T, H, KV, hd, win=0):
+        out = np.zeros_like(q)
+        self._fn("attn_fwd")(_f(q), _f(k), _f(v), _f(out), B, T, H, KV, hd, win)
+        return out
+
+    def attn_bwd(self, q, k, v, datt, B, T, H, KV, hd, win=0):
+        dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+        self._fn("attn_bwd")(_f(q), _f(k), _f(v), _f(datt), _f(dq), _f(dk), _f(dv), B, T, H, KV, hd, win)
+        return dq, dk, dv
+
+    def adamw(self, P, G, M, V, lr, b1, b2, wd, t, gscale):
+        self._fn("adamw")(_f(P), _f(G), _f(M), _f(V), P.size, lr, b1, b2, wd, t, gscale)
+
+    def gradnorm(self, G):
+        return float(self._fn("gradnorm")(_f(G), G.size))
+
+    # whole model
+    def param_count(self, m):
+        if self.ref:
+            return int(self._fn("param_count")(m.V, m.D, m.L, m.H, m.KV, m.F, m.T, m.n_mtp, m.n_exp))
+        mp = OrcLayerMap()
+        self._fn("param_map")(ctypes.byref(m), 0, ctypes.byref(mp))
+        return int(mp.total)
+
+    def layer_map(self, m, l):
+        """map_weights offsets of layer l (oracle side)."""
+        mp = OrcLayerMap()
+        getattr(self.dll, "orc_param_map")(ctypes.byref(m), l, ctypes.byref(mp))
+        return {n: int(getattr(mp, n)) for n, _ in OrcLayerMap._fields_}
+
+    def init_params(self, m, seed):
+        P = np.empty(self.param_count(m), np.float32)
+        if self.ref:
+            self._fn("init_params")(_f(P), seed, m.V, m.D, m.L, m.H, m.KV, m.F, m.T, m.n_mtp, m.n_exp)
+        else:
+            self._fn("init_params")(ctypes.byref(m), _f(P), seed)
+        return P
+
+    def train_step(self, m, B, P, tok, tgt, tgt_mtp=None):
+        """forward + memset(G) + backward; returns (loss, G)."""
+        G = np.zeros_like(P)
+        N = B * m.T
+        tm = tgt_mtp if tgt_mtp is not None and m.n_mtp else np.zeros((max(m.n_mtp, 1), N), np.int32)
+        tm = np.ascontiguousarray(tm, np.int32)
+        if self.ref:
+            loss = self._fn("train_step")(_f(P), _f(G), _n(tok), _n(tgt), _n(tm), B, m.V, m.D, m.L, m.H, m.KV,
+                                          m.F, m.T, m.n_mtp, m.n_exp, m.win, m.full_every)
+        else:
+            loss = self._fn("train_step")(ctypes.byref(m), B, _f(P), _f(G), _n(tok), _n(tgt), _n(tm))
+        return float(loss), G
+
+
+def param_regions(st, m):
+    """(name, start, end) of every parameter tensor of model m in
+    map_weights order (tinylm.c:361-393), from the oracle's layout."""
+    D, KD, F, E = m.D, m.KV * (m.D // m.H), m.F, max(m.n_exp, 1)
+    out = [("emb", 0, m.V * D)]
+    for l in range(m.L):
+        w = st.layer_map(m, l)
+        sizes = dict(an1=D, wq=D * D, wk=D * KD, wv=D * KD, wo=D * D, an2=D, wr=D * m.n_exp, w1=E * D * F,
+                     w3=E * D * F, w2=E * F * D)
+        out += [(f"{k}[{l}]", w[k], w[k] + n) for k, n in sizes.items() if n]
+    w = st.layer_map(m, 0)
+    out.append(("nf", w["nf"], w["nf"] + D))
+    out += [(f"mtp[{k}]", w["mtp0"] + k * D * D, w["mtp0"] + (k + 1) * D * D) for k in range(m.n_mtp)]
+    return out

@@ -20,6 +20,14 @@
  *   orc_moe_*                       brute-force per-token expert evaluation in
  *                                   fp64 (tests/test_oracle.py) and the reference
  *                                   MoE compiled from its own source (fixtures).
+ *   orc_rmsnorm_*, orc_rope*,       (tl_oracle_step.c) fixtures written by the
+ *   orc_attn_*, orc_adamw,          reference's own compiled functions
+ *   orc_gradnorm, orc_train_step    (tests/golden/step_*.npz), fp64 forms and
+ *                                   closed forms (rotation norms, softmax rows
+ *                                   summing to one, finite-difference
+ *                                   gradients) in tests/test_oracle.py.
+ *   orc_xent, orc_embed_*           the whole-step fixtures (loss and the
+ *                                   embedding gradient) and closed forms.
  */
 #ifndef TL_ORACLE_H
 #define TL_ORACLE_H
@@ -70,6 +78,37 @@ void orc_moe_backward(int N, int D, int F, int E,
                       const float *wr, const float *w1, const float *w3, const float *w2,
                       float *gwr, float *gw1, float *gw3, float *gw2,
                       const int *assign, const float *gate, const float *rprobs);
+
+/* ---- training-step glue (tl_oracle_step.c), tinylm.c:539-1176 ---------- */
+void   orc_embed_fwd(float *out, const float *emb, const int *tok, int N, int D);           /* :972-976   */
+void   orc_embed_bwd(float *demb, const float *dout, const int *tok, int N, int D);        /* :1149-1153 */
+void   orc_rmsnorm_fwd(const float *x, const float *g, float *out, float *rinv, int rows, int D); /* :540 */
+void   orc_rmsnorm_bwd(const float *x, const float *g, const float *rinv, const float *dy, float *dx,
+                       float *dg, int rows, int D);                                         /* :565-588 */
+void   orc_rope_table(float *cs, float *sn, int maxpos, int hd, float base);               /* :605-619 */
+void   orc_rope(float *buf, const int *pos, int T, int rows, int nh, int hd, const float *cs,
+                const float *sn, int back);                                                 /* :630-651 */
+void   orc_attn_fwd(const float *q, const float *k, const float *v, float *out, int B, int T, int H,
+                    int KV, int hd, int win);                                               /* :699-732 */
+void   orc_attn_bwd(const float *q, const float *k, const float *v, const float *datt, float *dq,
+                    float *dk, float *dv, int B, int T, int H, int KV, int hd, int win);    /* :734-783 */
+double orc_xent(const float *logits, const int *tgt, float *dl, float scale, int N, int V);
+float  orc_gradnorm(const float *G, size_t n);                                               /* :1171 */
+void   orc_adamw(float *P, const float *G, float *M, float *V, size_t n, float lr, float b1, float b2,
+                 float wd, int t, float gscale);                                             /* :1159 */
+
+/* A model (tinylm.c Cfg :35-59 without QK-norm / shared experts) and its
+ * flat parameter layout (map_weights :361-393; wr and the E expert slots when
+ * n_exp > 0). */
+typedef struct { int V, D, L, H, KV, F, T, n_mtp, n_exp, win, full_every; float rope_base; } OrcModel;
+typedef struct { size_t emb, an1, wq, wk, wv, wo, an2, wr, w1, w3, w2, nf, mtp0, total; } OrcLayerMap;
+void  orc_param_map(const OrcModel *m, int layer, OrcLayerMap *o);
+/* init_params (:395-419) from the reference generator seeded with `seed` */
+void  orc_init_params(const OrcModel *m, float *P, uint64_t seed);
+/* forward + memset(G) + backward of one batch of B sequences; returns the
+ * loss.  tgt_mtp: n_mtp x (B*T) targets of the MTP heads. */
+float orc_train_step(const OrcModel *m, int B, const float *P, float *G, const int *tok, const int *tgt,
+                     const int *tgt_mtp);
 
 /* A plan's call list run in C (CPU baseline of short calls): op 0 mm,
  * 1 mm_bt, 2 mm_atb, 3 memset of n floats; `reps` passes over the list. */

@@ -7,7 +7,8 @@ Run in the build container only (needs /root/reference):
 
 It loads oracle/_ref/libtlref.so -- mm / mm_bt / mm_atb, the RNG and the MoE
 layer of /root/reference/tinylm.c compiled from their own lines by
-oracle/Makefile -- draws every input with the reference's rnd_normal
+oracle/Makefile -- and _ref/libtlref_seq.so (the training step's norms, RoPE,
+attention, AdamW and whole forward + backward passes), draws every input with the reference's rnd_normal
 (tinylm.c:127-134) and records inputs and outputs as .npz files next to this
 script.  The fixtures are data (inputs and expected outputs); no reference
 source is stored.  Tests check both the CPU oracle and the GPU path against
@@ -121,6 +122,69 @@ def seq_case(name, B, T, D, H, KV, F, V, L, n_mtp):
               open(os.path.join(HERE, f"seq_{name}.json"), "w"))
 
 
+def step_cases(ref):
+    """The training step's non-GEMM functions and whole steps, through the
+    reference's own code (oracle/_ref/libtlref_seq.so: tinylm.c:539-1176
+    compiled from its lines): rmsnorm, RoPE, attention, AdamW / gradnorm,
+    and forward + backward of three small models."""
+    from oracle import StepFns, model
+    st = StepFns("reference")
+    rng = np.random.default_rng(77)
+    f32 = lambda *s, sc=1.0: (sc * rng.standard_normal(s)).astype(np.float32)  # noqa: E731
+
+    # rmsnorm forward / backward with non-zero dx and dg prefills
+    x, g = f32(37, 48), (1.0 + f32(48, sc=0.1)).astype(np.float32)
+    out, rinv = st.rmsnorm_fwd(x, g)
+    dy, dx0, dg0 = f32(37, 48, sc=0.01), f32(37, 48, sc=0.01), f32(48, sc=0.01)
+    dx, dg = dx0.copy(), dg0.copy()
+    st.rmsnorm_bwd(x, g, rinv, dy, dx, dg)
+    np.savez(os.path.join(HERE, "step_rmsnorm.npz"), x=x, g=g, out=out, rinv=rinv, dy=dy, dx0=dx0, dx=dx,
+             dg0=dg0, dg=dg)
+
+    # RoPE: rope_init's table and rope_apply both ways at positions r % T
+    cs, sn = st.rope_table(64, 32)
+    buf = f32(40, 3 * 32)
+    fwd, back = buf.copy(), buf.copy()
+    st.rope(fwd, 16, 3, 32, 0)
+    st.rope(back, 16, 3, 32, 1)
+    np.savez(os.path.join(HERE, "step_rope.npz"), T=16, nh=3, hd=32, cs=cs, sn=sn, buf=buf, fwd=fwd, back=back)
+
+    # attention forward / backward (GQA; one ragged sequence with a window)
+    for name, B, T, H, KV, win in (("gqa_b2_t40_h4_kv2", 2, 40, 4, 2, 0), ("win_b1_t70_h2_kv1", 1, 70, 2, 1, 24)):
+        hd = 32
+        q, k, v = f32(B * T, H * hd), f32(B * T, KV * hd), f32(B * T, KV * hd)
+        out = st.attn_fwd(q, k, v, B, T, H, KV, hd, win)
+        datt = f32(B * T, H * hd, sc=0.01)
+        dq, dk, dv = st.attn_bwd(q, k, v, datt, B, T, H, KV, hd, win)
+        np.savez(os.path.join(HERE, f"step_attn_{name}.npz"), B=B, T=T, H=H, KV=KV, hd=hd, win=win, q=q, k=k,
+                 v=v, out=out, datt=datt, dq=dq, dk=dk, dv=dv)
+
+    # AdamW step t = 3 with a clip scale, and the gradient norm
+    n = 1000
+    P, G, M, V = f32(n, sc=0.02), f32(n, sc=0.01), f32(n, sc=0.001), np.abs(f32(n, sc=1e-5))
+    gn = st.gradnorm(G)
+    P1, M1, V1 = P.copy(), M.copy(), V.copy()
+    st.adamw(P1, G, M1, V1, 3e-4, 0.9, 0.95, 0.1, 3, 0.5)
+    np.savez(os.path.join(HERE, "step_adamw.npz"), P=P, G=G, M=M, V=V, gnorm=np.float32(gn), lr=3e-4, b1=0.9,
+             b2=0.95, wd=0.1, t=3, gscale=0.5, P1=P1, M1=M1, V1=V1)
+
+    # whole steps: forward + memset(G) + backward (train_loop, :2627-2629)
+    for name, kw, B, seed in (
+            ("dense_mtp1", dict(V=64, D=64, L=2, H=2, KV=1, F=48, T=32, n_mtp=1), 2, 11),
+            ("window", dict(V=96, D=64, L=2, H=2, KV=2, F=32, T=48, win=20, full_every=2), 1, 12),
+            ("moe_e4", dict(V=64, D=64, L=1, H=2, KV=1, F=48, T=32, n_exp=4), 2, 13)):
+        m = model(**kw)
+        P = st.init_params(m, 1234567891011 + seed)
+        N = B * m.T
+        tok = rng.integers(0, m.V, N).astype(np.int32)
+        tgt = rng.integers(0, m.V, N).astype(np.int32)
+        tm = rng.integers(0, m.V, (max(m.n_mtp, 1), N)).astype(np.int32)
+        loss, G = st.train_step(m, B, P, tok, tgt, tm)
+        np.savez(os.path.join(HERE, f"step_train_{name}.npz"), B=B, model=np.array(
+            [m.V, m.D, m.L, m.H, m.KV, m.F, m.T, m.n_mtp, m.n_exp, m.win, m.full_every], np.int32),
+            P=P, tok=tok, tgt=tgt, tgt_mtp=tm, loss=np.float32(loss), G=G)
+
+
 def main():
     if not os.path.isdir("/root/reference"):
         sys.exit("make_golden.py needs /root/reference (build container only)")
@@ -134,6 +198,7 @@ def main():
     rng_case(ref, 1234567891011)
     seq_case("train_l2_mtp2", 2, 16, 32, 4, 1, 48, 64, 2, 2)
     seq_case("train_l3", 1, 24, 48, 6, 2, 40, 96, 3, 0)
+    step_cases(ref)
     print("fixtures written to", HERE)
 
 

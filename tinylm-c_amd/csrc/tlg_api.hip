@@ -157,10 +157,12 @@ struct Stage { void *p = nullptr; size_t bytes = 0; };
 static Stage g_stage[16];
 
 void tlg_moe_release(void);
+void tlg_train_release(void);
 void tlg_shutdown_impl(void)
 {
     for (auto &s : g_stage) { (void)hipFree(s.p); s = Stage(); }
     tlg_moe_release();
+    tlg_train_release();
 }
 
 static int stage_ptr(int slot, size_t bytes, void **out)

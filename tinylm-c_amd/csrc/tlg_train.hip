@@ -1,0 +1,958 @@
+// tlg_train.hip -- the non-GEMM work of tinylm.c's training step on gfx950,
+// so that a whole forward + backward + AdamW step stays in HBM: embedding
+// gather/scatter, RMSNorm, RoPE, causal GQA attention (MFMA), the residual
+// adds, SwiGLU, softmax cross-entropy, the MTP head's SiLU residual, the
+// global gradient norm and AdamW.
+//
+// Reference (tinylm.c): embedding :972-976 / :1149-1153, rmsnorm_fwd
+// :540-563, rmsnorm_bwd :565-588, rope_init / rope_apply :605-651,
+// attn_fwd :699-732, attn_bwd :734-783, siluf :786, residual adds :994-995
+// :1009-1010, SwiGLU :1005-1006 / :1100-1112, softmax-CE :1019-1028,
+// dlogits :1076-1082, mtp_grad glue :1036-1069, adamw :1159-1170,
+// global_gradnorm :1171-1176.
+//
+// Data layout in HBM: the reference's own (row-major [rows][width] activations,
+// flat P / G with map_weights' offsets).  Attention additionally keeps, per
+// layer, the log-sum-exp of each (row, head) softmax ([rows][H] floats) so
+// the backward pass rebuilds P without a max/sum pass.
+//
+// Attention uses v_mfma_f32_32x32x2_f32 on 32 x 32 tiles with head_dim 32 (the
+// width of every BASELINE model).  A wave owns 32 queries of one head.  The
+// forward computes S^T = K Q^T, so in the MFMA result each lane holds one
+// query (lane % 32) and 16 keys: the softmax max and sum are in-lane plus one
+// exchange with lane ^ 32, and the same registers are the B operand of
+// O^T = V^T P^T with no shuffle.  The backward uses the same trick for dQ
+// (dS^T as the B operand) and the untransposed S for dK / dV (P and dS as the
+// A operand, contracting over queries); dK / dV of the heads sharing a KV head
+// are summed in a fixed order through LDS, so every result is deterministic.
+#include "tlg_internal.h"
+#include "../../include/tltrain.h"
+#include <math.h>
+#include <string.h>
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+static inline unsigned grid_for(size_t work, size_t per_block, unsigned cap)
+{
+    size_t b = (work + per_block - 1) / per_block;
+    if (b < 1) b = 1;
+    return (unsigned)(b > cap ? cap : b);
+}
+static inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// -------------------------------------------------------------- scratch --
+// One arena for the small per-call scratch (norm partials, attention's
+// dO.O rows, loss rows, the embedding index); grown on demand and kept until
+// tlg_shutdown.  Growing it synchronizes the device, so the first call at a
+// new size cannot be captured into a graph; calls on different streams must
+// not overlap.
+static void *g_tr_mem = nullptr;
+static size_t g_tr_bytes = 0;
+
+void tlg_train_release(void)
+{
+    if (g_tr_mem) (void)hipFree(g_tr_mem);
+    g_tr_mem = nullptr;
+    g_tr_bytes = 0;
+}
+
+static int tr_scratch(size_t bytes, void **out)
+{
+    bytes = (bytes + 255) & ~(size_t)255;
+    if (bytes > g_tr_bytes) {
+        TLG_HIP(hipDeviceSynchronize());
+        tlg_train_release();
+        if (hipMalloc(&g_tr_mem, bytes) != hipSuccess) {
+            g_tr_mem = nullptr;
+            return tlg_fail(TLG_ENOMEM, "training scratch of %zu bytes", bytes);
+        }
+        g_tr_bytes = bytes;
+    }
+    *out = g_tr_mem;
+    return TLG_OK;
+}
+
+static int begin(void)
+{
+    return tlg_ensure_init();
+}
+
+// ------------------------------------------------------------ embedding --
+// out[n] = emb[tok[n]]; a row whose token is outside [0, V) becomes NaN.
+__global__ void k_embed_fwd(const float *__restrict__ emb, const int *__restrict__ tok, int N, int D, int V,
+                            float *__restrict__ out)
+{
+    const int d4 = D >> 2;
+    const size_t total = (size_t)N * d4;
+    for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total; q += (size_t)gridDim.x * blockDim.x) {
+        const size_t n = q / d4, c = q % d4;
+        const int t = tok[n];
+        f32x4 v;
+        if (t >= 0 && t < V) v = reinterpret_cast<const f32x4 *>(emb)[(size_t)t * d4 + c];
+        else v = f32x4{NAN, NAN, NAN, NAN};
+        reinterpret_cast<f32x4 *>(out)[q] = v;
+    }
+}
+
+__global__ void k_fill_int(int *__restrict__ p, int n, int v)
+{
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = v;
+}
+
+__global__ void k_tok_count(const int *__restrict__ tok, int N, int V, int *__restrict__ cnt)
+{
+    for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < N; n += gridDim.x * blockDim.x) {
+        const int t = tok[n];
+        if (t >= 0 && t < V) atomicAdd(&cnt[t], 1);
+    }
+}
+
+// Exclusive scan of cnt[V] into off[V+1] by one 1024-thread workgroup, and
+// cur[] = off[] (the placement cursors).
+__global__ __launch_bounds__(1024) void k_tok_scan(const int *__restrict__ cnt, int V, int *__restrict__ off,
+                                                   int *__restrict__ cur)
+{
+    __shared__ int part[1024];
+    const int t = threadIdx.x;
+    const int per = (V + 1023) / 1024;
+    const int lo = t * per, hi = min(V, lo + per);
+    int s = 0;
+    for (int i = lo; i < hi; i++) s += cnt[i];
+    part[t] = s;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+        const int add = t >= o ? part[t - o] : 0;
+        __syncthreads();
+        part[t] += add;
+        __syncthreads();
+    }
+    int run = part[t] - s;
+    for (int i = lo; i < hi; i++) {
+        off[i] = run;
+        cur[i] = run;
+        run += cnt[i];
+    }
+    if (t == 1023) off[V] = part[1023];
+}
+
+__global__ void k_tok_place(const int *__restrict__ tok, int N, int V, int *__restrict__ cur, int *__restrict__ idx)
+{
+    for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < N; n += gridDim.x * blockDim.x) {
+        const int t = tok[n];
+        if (t >= 0 && t < V) idx[atomicAdd(&cur[t], 1)] = n;
+    }
+}
+
+// demb[v] += dout[n] for the rows n with tok[n] == v, in increasing n, as the
+// reference's sequential scatter does (so the sums are bit-identical).  One
+// wave per vocabulary row; the bucket's rows are visited in order by
+// selecting the smallest index above the last one.
+__global__ __launch_bounds__(256) void k_embed_bwd(const float *__restrict__ dout, const int *__restrict__ off,
+                                                   const int *__restrict__ idx, int V, int D,
+                                                   float *__restrict__ demb)
+{
+    const int lane = threadIdx.x & 63;
+    const int v = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (v >= V) return;
+    const int b = off[v], k = off[v + 1] - b;
+    float *de = demb + (size_t)v * D;
+    int last = -1;
+    for (int j = 0; j < k; j++) {
+        int m = 0x7fffffff;
+        for (int e = lane; e < k; e += 64) {
+            const int n = idx[b + e];
+            if (n > last && n < m) m = n;
+        }
+        for (int o = 32; o > 0; o >>= 1) m = min(m, __shfl_xor(m, o));
+        const float *d = dout + (size_t)m * D;
+        for (int i = lane; i < D; i += 64) de[i] += d[i];
+        last = m;
+    }
+}
+
+// -------------------------------------------------------------- rmsnorm --
+// One wave per row: s = 1 / sqrt(sum(x^2) / D + 1e-5), out = x * s * g.
+__global__ __launch_bounds__(256) void k_rms_fwd(const float *__restrict__ x, const float *__restrict__ g,
+                                                 float *__restrict__ out, float *__restrict__ rinv, int rows, int D)
+{
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const int d4 = D >> 2;
+    const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (size_t)r * D);
+    float ms = 0.f;
+    for (int i = lane; i < d4; i += 64) {
+        const f32x4 v = xr[i];
+        ms += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    for (int o = 32; o > 0; o >>= 1) ms += __shfl_xor(ms, o);
+    const float s = 1.0f / sqrtf(ms / (float)D + 1e-5f);
+    if (lane == 0 && rinv) rinv[r] = s;
+    f32x4 *orow = reinterpret_cast<f32x4 *>(out + (size_t)r * D);
+    const f32x4 *g4 = reinterpret_cast<const f32x4 *>(g);
+    for (int i = lane; i < d4; i += 64) {
+        const f32x4 v = xr[i], w = g4[i];
+        orow[i] = f32x4{v.x * s * w.x, v.y * s * w.y, v.z * s * w.z, v.w * s * w.w};
+    }
+}
+
+// dx = base + s g dy - (s^3 / D) (x . g dy) x (base = dx_in, or 0 when
+// dx_in is null; dx_in may be dx itself) for RMS_ROWS rows per
+// workgroup (one wave per row); the workgroup's share of dg = sum_r x s dy
+// goes to part[blockIdx.x][D] (summed in a fixed order by k_rms_dg).
+#define RMS_ROWS 16
+#define RMS_MAXV 8            // float4 columns per lane: D <= 64 * 4 * 8
+__global__ __launch_bounds__(256) void k_rms_bwd(const float *__restrict__ x, const float *__restrict__ g,
+                                                 const float *__restrict__ rinv, const float *__restrict__ dy,
+                                                 const float *dx_in, float *dx, int rows, int D,
+                                                 float *__restrict__ part)
+{
+    __shared__ f32x4 red[3][64 * RMS_MAXV];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d4 = D >> 2;
+    const f32x4 *g4 = reinterpret_cast<const f32x4 *>(g);
+    f32x4 acc[RMS_MAXV];
+#pragma unroll
+    for (int j = 0; j < RMS_MAXV; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int r0 = blockIdx.x * RMS_ROWS;
+    for (int rr = wave; rr < RMS_ROWS; rr += 4) {
+        const int r = r0 + rr;
+        if (r >= rows) break;
+        const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (size_t)r * D);
+        const f32x4 *dr = reinterpret_cast<const f32x4 *>(dy + (size_t)r * D);
+        const float s = rinv[r];
+        float c = 0.f;
+#pragma unroll
+        for (int j = 0; j < RMS_MAXV; j++) {
+            const int i = lane + 64 * j;
+            if (i < d4) {
+                const f32x4 a = xr[i], w = g4[i], d = dr[i];
+                c += a.x * w.x * d.x + a.y * w.y * d.y + a.z * w.z * d.z + a.w * w.w * d.w;
+            }
+        }
+        for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
+        const float coef = s * s * s / (float)D * c;
+        const f32x4 *xin = dx_in ? reinterpret_cast<const f32x4 *>(dx_in + (size_t)r * D) : nullptr;
+        f32x4 *xo = reinterpret_cast<f32x4 *>(dx + (size_t)r * D);
+#pragma unroll
+        for (int j = 0; j < RMS_MAXV; j++) {
+            const int i = lane + 64 * j;
+            if (i < d4) {
+                const f32x4 a = xr[i], w = g4[i], d = dr[i];
+                const f32x4 base = xin ? xin[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+                f32x4 o;
+                o.x = base.x + (s * w.x * d.x - coef * a.x);
+                o.y = base.y + (s * w.y * d.y - coef * a.y);
+                o.z = base.z + (s * w.z * d.z - coef * a.z);
+                o.w = base.w + (s * w.w * d.w - coef * a.w);
+                xo[i] = o;
+                acc[j].x += a.x * s * d.x;
+                acc[j].y += a.y * s * d.y;
+                acc[j].z += a.z * s * d.z;
+                acc[j].w += a.w * s * d.w;
+            }
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int j = 0; j < RMS_MAXV; j++) red[wave - 1][j * 64 + lane] = acc[j];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        f32x4 *pr = reinterpret_cast<f32x4 *>(part + (size_t)blockIdx.x * D);
+#pragma unroll
+        for (int j = 0; j < RMS_MAXV; j++) {
+            const int i = lane + 64 * j;
+            if (i < d4) {
+                f32x4 t = acc[j];
+                for (int w = 0; w < 3; w++) t += red[w][j * 64 + lane];
+                pr[i] = t;
+            }
+        }
+    }
+}
+
+__global__ void k_rms_dg(const float *__restrict__ part, int nblk, int D, float *__restrict__ dg)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= D) return;
+    float s = 0.f;
+    for (int b = 0; b < nblk; b++) s += part[(size_t)b * D + i];
+    dg[i] += s;
+}
+
+// ----------------------------------------------------------------- rope --
+// In place on [rows][nh * hd]: the pair (v[i], v[i + hd/2]) of each head is
+// rotated by the angle of row r's position (pos[r], or r % T when pos is
+// null); back = 1 applies the transpose (the backward pass).  Positions
+// outside the table turn the row into NaN.
+__global__ void k_rope(float *__restrict__ buf, const int *__restrict__ pos, int T, int rows, int nh, int hd,
+                       const float *__restrict__ cs, const float *__restrict__ sn, int maxpos, int back)
+{
+    const int half = hd >> 1;
+    const size_t total = (size_t)rows * nh * half;
+    for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total; q += (size_t)gridDim.x * blockDim.x) {
+        const int i = (int)(q % half);
+        const size_t rh = q / half;
+        const int h = (int)(rh % nh);
+        const size_t r = rh / nh;
+        const int t = pos ? pos[r] : (int)(r % T);
+        float *v = buf + r * nh * hd + (size_t)h * hd;
+        if (t < 0 || t >= maxpos) {
+            v[i] = NAN;
+            v[i + half] = NAN;
+            continue;
+        }
+        const float c = cs[(size_t)t * half + i], s = sn[(size_t)t * half + i];
+        const float a = v[i], b = v[i + half];
+        if (!back) {
+            v[i] = a * c - b * s;
+            v[i + half] = b * c + a * s;
+        } else {
+            v[i] = a * c + b * s;
+            v[i + half] = -a * s + b * c;
+        }
+    }
+}
+
+// ------------------------------------------------------------ attention --
+#define AT_HD 32
+// Row (within a 32 x 32 tile) of register r of lane l in the MFMA result.
+__device__ __forceinline__ int at_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+// 16 contiguous floats from p (16-byte aligned), or zeros.
+__device__ __forceinline__ void ld16(const float *p, bool ok, float (&o)[16])
+{
+    if (ok) {
+        const f32x4 *q = reinterpret_cast<const f32x4 *>(p);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const f32x4 t = q[k];
+            o[4 * k] = t.x;
+            o[4 * k + 1] = t.y;
+            o[4 * k + 2] = t.z;
+            o[4 * k + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; k++) o[k] = 0.f;
+    }
+}
+
+// Key s is visible from query q: causal, inside the sequence, and inside
+// the sliding window when win > 0 (s >= q - win + 1, attn_fwd's lo).
+__device__ __forceinline__ bool at_visible(int s, int q, int T, int win)
+{
+    return s <= q && q < T && (win <= 0 || s > q - win);
+}
+
+// First key block any query of block qb can see.
+__device__ __forceinline__ int at_kb0(int qb, int win)
+{
+    if (win <= 0) return 0;
+    const int lo = qb * 32 - win + 1;
+    return lo > 0 ? lo / 32 : 0;
+}
+
+// One wave per (b, h, 32-query block), four per workgroup, heaviest blocks
+// (latest queries) first.  out = softmax(q k^T * scale) v per head (GQA:
+// head h reads KV head h / (H / KV)); lse = max + log(sum) per (row, head).
+__global__ __launch_bounds__(256) void k_attn_fwd(const float *__restrict__ q, const float *__restrict__ k,
+                                                  const float *__restrict__ v, float *__restrict__ out,
+                                                  float *__restrict__ lse, int B, int T, int H, int KV, int win,
+                                                  float scale)
+{
+    const int lane = threadIdx.x & 63;
+    const int nqb = (T + 31) >> 5;
+    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= B * H * nqb) return;
+    const int qb = nqb - 1 - item / (B * H);
+    const int bh = item % (B * H);
+    const int b = bh / H, h = bh % H, kvh = h / (H / KV);
+    const int D = H * AT_HD, KD = KV * AT_HD;
+    const int lq = lane & 31, hh = lane >> 5;
+    const int qi = qb * 32 + lq;
+    const bool qok = qi < T;
+    float qv[16];
+    ld16(q + (size_t)(b * T + (qok ? qi : 0)) * D + h * AT_HD + 16 * hh, qok, qv);
+    const float *kb_ = k + (size_t)b * T * KD + kvh * AT_HD;
+    const float *vb_ = v + (size_t)b * T * KD + kvh * AT_HD;
+    f32x16 o;
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[r] = 0.f;
+    float m = -INFINITY, l = 0.f;
+    for (int kb = at_kb0(qb, win); kb <= qb; kb++) {
+        const int s0 = kb * 32, sl = s0 + lq;
+        float kv[16];
+        ld16(kb_ + (size_t)(sl < T ? sl : 0) * KD + 16 * hh, sl < T, kv);
+        f32x16 st;
+#pragma unroll
+        for (int r = 0; r < 16; r++) st[r] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[j], qv[j], st, 0, 0, 0);
+        // st[r] = S^T[s0 + at_row(r)][qi]
+        float sc[16], bm = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int s = s0 + at_row(r, lane);
+            sc[r] = (at_visible(s, qi, T, win) && s < T) ? st[r] * scale : -INFINITY;
+            bm = fmaxf(bm, sc[r]);
+        }
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        const float mn = fmaxf(m, bm);
+        const float alpha = mn == -INFINITY ? 1.f : expf(m - mn);
+        float ps = 0.f, p[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            p[r] = sc[r] == -INFINITY ? 0.f : expf(sc[r] - mn);
+            ps += p[r];
+        }
+        l = l * alpha + ps;
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[r] *= alpha;
+        // O^T[d][q] += sum_s V[s][d] P^T[s][q]
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int s = s0 + at_row(r, lane);
+            const float vv = s < T ? vb_[(size_t)s * KD + lq] : 0.f;
+            o = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, p[r], o, 0, 0, 0);
+        }
+        m = mn;
+    }
+    l += __shfl_xor(l, 32);
+    if (!qok) return;
+    const float inv = 1.0f / l;
+    float *orow = out + (size_t)(b * T + qi) * D + h * AT_HD;
+#pragma unroll
+    for (int g4 = 0; g4 < 4; g4++)
+        *reinterpret_cast<f32x4 *>(orow + 8 * g4 + 4 * hh) =
+            f32x4{o[4 * g4] * inv, o[4 * g4 + 1] * inv, o[4 * g4 + 2] * inv, o[4 * g4 + 3] * inv};
+    if (hh == 0) lse[(size_t)(b * T + qi) * H + h] = m + logf(l);
+}
+
+// dQ, one wave per (b, h, 32-query block); also writes Dq = dO . O per
+// (row, head) for k_attn_bwd_dkv.  dS = P (dP - Dq) scale (attn_bwd's
+// dsc), dQ = dS K.
+__global__ __launch_bounds__(256) void k_attn_bwd_dq(const float *__restrict__ q, const float *__restrict__ k,
+                                                     const float *__restrict__ v, const float *__restrict__ o,
+                                                     const float *__restrict__ dout, const float *__restrict__ lse,
+                                                     float *__restrict__ Dq, float *__restrict__ dq, int B, int T,
+                                                     int H, int KV, int win, float scale)
+{
+    const int lane = threadIdx.x & 63;
+    const int nqb = (T + 31) >> 5;
+    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= B * H * nqb) return;
+    const int qb = nqb - 1 - item / (B * H);
+    const int bh = item % (B * H);
+    const int b = bh / H, h = bh % H, kvh = h / (H / KV);
+    const int D = H * AT_HD, KD = KV * AT_HD;
+    const int lq = lane & 31, hh = lane >> 5;
+    const int qi = qb * 32 + lq;
+    const bool qok = qi < T;
+    const size_t qoff = (size_t)(b * T + (qok ? qi : 0)) * D + h * AT_HD + 16 * hh;
+    float qv[16], dov[16], ov[16];
+    ld16(q + qoff, qok, qv);
+    ld16(dout + qoff, qok, dov);
+    ld16(o + qoff, qok, ov);
+    float dd = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) dd += dov[j] * ov[j];
+    dd += __shfl_xor(dd, 32);
+    const size_t rh = (size_t)(b * T + (qok ? qi : 0)) * H + h;
+    if (qok && hh == 0) Dq[rh] = dd;
+    const float ls = qok ? lse[rh] : 0.f;
+    const float *kb_ = k + (size_t)b * T * KD + kvh * AT_HD;
+    const float *vb_ = v + (size_t)b * T * KD + kvh * AT_HD;
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.f;
+    for (int kb = at_kb0(qb, win); kb <= qb; kb++) {
+        const int s0 = kb * 32, sl = s0 + lq;
+        float kv[16], vv[16];
+        ld16(kb_ + (size_t)(sl < T ? sl : 0) * KD + 16 * hh, sl < T, kv);
+        ld16(vb_ + (size_t)(sl < T ? sl : 0) * KD + 16 * hh, sl < T, vv);
+        f32x16 st, dp;
+#pragma unroll
+        for (int r = 0; r < 16; r++) { st[r] = 0.f; dp[r] = 0.f; }
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[j], qv[j], st, 0, 0, 0);
+            dp = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[j], dov[j], dp, 0, 0, 0);
+        }
+        float ds[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int s = s0 + at_row(r, lane);
+            if (at_visible(s, qi, T, win) && s < T) {
+                const float p = expf(st[r] * scale - ls);
+                ds[r] = p * (dp[r] - dd) * scale;
+            } else {
+                ds[r] = 0.f;
+            }
+        }
+        // dQ^T[d][q] += sum_s K[s][d] dS^T[s][q]
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int s = s0 + at_row(r, lane);
+            const float kk = s < T ? kb_[(size_t)s * KD + lq] : 0.f;
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kk, ds[r], acc, 0, 0, 0);
+        }
+    }
+    if (!qok) return;
+    float *orow = dq + (size_t)(b * T + qi) * D + h * AT_HD;
+#pragma unroll
+    for (int g4 = 0; g4 < 4; g4++)
+        *reinterpret_cast<f32x4 *>(orow + 8 * g4 + 4 * hh) =
+            f32x4{acc[4 * g4], acc[4 * g4 + 1], acc[4 * g4 + 2], acc[4 * g4 + 3]};
+}
+
+// dK, dV: one workgroup per (b, kv head, 32-key block), first key blocks
+// (most queries) first.  Its four waves share the (head, query block) pairs
+// that see the block; each accumulates dV = P^T dO and dK = dS^T Q for its
+// pairs, and the four partials are summed in wave order.
+__global__ __launch_bounds__(256) void k_attn_bwd_dkv(const float *__restrict__ q, const float *__restrict__ k,
+                                                      const float *__restrict__ v, const float *__restrict__ dout,
+                                                      const float *__restrict__ lse, const float *__restrict__ Dq,
+                                                      float *__restrict__ dk, float *__restrict__ dv, int B, int T,
+                                                      int H, int KV, int win, float scale)
+{
+    __shared__ float red[3][2][16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nkb = (T + 31) >> 5;
+    const int item = blockIdx.x;
+    const int kb = item / (B * KV);
+    const int bkv = item % (B * KV);
+    const int b = bkv / KV, kvh = bkv % KV, G = H / KV;
+    const int D = H * AT_HD, KD = KV * AT_HD;
+    const int lq = lane & 31, hh = lane >> 5;
+    const int s0 = kb * 32, sl = s0 + lq;
+    const bool sok = sl < T;
+    const size_t koff = (size_t)(b * T + (sok ? sl : 0)) * KD + kvh * AT_HD + 16 * hh;
+    float kv[16], vv[16];
+    ld16(k + koff, sok, kv);
+    ld16(v + koff, sok, vv);
+    int qb_last = nkb - 1;
+    if (win > 0) qb_last = min(qb_last, (s0 + 31 + win - 1) >> 5);
+    const int npairs = G * (qb_last - kb + 1);
+    f32x16 ak, av;
+#pragma unroll
+    for (int r = 0; r < 16; r++) { ak[r] = 0.f; av[r] = 0.f; }
+    for (int pi = wave; pi < npairs; pi += 4) {
+        const int h = kvh * G + pi % G;
+        const int q0 = (kb + pi / G) * 32;
+        const int ql = q0 + lq;
+        const bool qok = ql < T;
+        const size_t qoff = (size_t)(b * T + (qok ? ql : 0)) * D + h * AT_HD + 16 * hh;
+        float qa[16], da[16];
+        ld16(q + qoff, qok, qa);
+        ld16(dout + qoff, qok, da);
+        f32x16 st, dp;
+#pragma unroll
+        for (int r = 0; r < 16; r++) { st[r] = 0.f; dp[r] = 0.f; }
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            st = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[j], kv[j], st, 0, 0, 0);
+            dp = __builtin_amdgcn_mfma_f32_32x32x2f32(da[j], vv[j], dp, 0, 0, 0);
+        }
+        // st[r] = S[q0 + at_row(r)][sl], dp likewise
+        float pp[16], ds[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int qq = q0 + at_row(r, lane);
+            if (at_visible(sl, qq, T, win) && sok) {
+                const size_t rh = (size_t)(b * T + qq) * H + h;
+                pp[r] = expf(st[r] * scale - lse[rh]);
+                ds[r] = pp[r] * (dp[r] - Dq[rh]) * scale;
+            } else {
+                pp[r] = 0.f;
+                ds[r] = 0.f;
+            }
+        }
+        // dV[s][d] += sum_q P[q][s] dO[q][d];  dK[s][d] += sum_q dS[q][s] Q[q][d]
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int qq = q0 + at_row(r, lane);
+            const size_t off = (size_t)(b * T + (qq < T ? qq : 0)) * D + h * AT_HD + lq;
+            const float dob = qq < T ? dout[off] : 0.f;
+            const float qbv = qq < T ? q[off] : 0.f;
+            av = __builtin_amdgcn_mfma_f32_32x32x2f32(pp[r], dob, av, 0, 0, 0);
+            ak = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[r], qbv, ak, 0, 0, 0);
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            red[wave - 1][0][r][lane] = ak[r];
+            red[wave - 1][1][r][lane] = av[r];
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        float a = ak[r], c = av[r];
+        for (int w = 0; w < 3; w++) {
+            a += red[w][0][r][lane];
+            c += red[w][1][r][lane];
+        }
+        const int s = s0 + at_row(r, lane);
+        if (s < T) {
+            const size_t off = (size_t)(b * T + s) * KD + kvh * AT_HD + lq;
+            dk[off] = a;
+            dv[off] = c;
+        }
+    }
+}
+
+// ----------------------------------------------------------- elementwise --
+enum { EW_ADD = 0, EW_SWIGLU = 1, EW_SWIGLU_BWD = 2, EW_SILU_RES = 3, EW_SILU_BWD = 4 };
+
+// ADD:        y += x
+// SWIGLU:     y = silu(a) * b                     silu(z) = z / (1 + e^-z)
+// SWIGLU_BWD: y = dact * b * silu'(a), y2 = dact * silu(a)   (dact = x)
+// SILU_RES:   y = x + silu(a)                     (MTP's hk = fn + silu(t1))
+// SILU_BWD:   y = x * silu'(a)                    (MTP's dt1)
+__global__ void k_ew(int op, size_t n, float *__restrict__ y, float *__restrict__ y2, const float *__restrict__ x,
+                     const float *__restrict__ a, const float *__restrict__ bb)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        switch (op) {
+        case EW_ADD: y[i] += x[i]; break;
+        case EW_SWIGLU: {
+            const float z = a[i];
+            y[i] = z / (1.0f + expf(-z)) * bb[i];
+            break;
+        }
+        case EW_SWIGLU_BWD: {
+            const float z = a[i], d = x[i];
+            const float sg = 1.0f / (1.0f + expf(-z));
+            const float si = z * sg, ds = sg + z * sg * (1.0f - sg);
+            y[i] = d * bb[i] * ds;
+            y2[i] = d * si;
+            break;
+        }
+        case EW_SILU_RES: {
+            const float z = a[i];
+            y[i] = x[i] + z / (1.0f + expf(-z));
+            break;
+        }
+        default: {
+            const float z = a[i];
+            const float sg = 1.0f / (1.0f + expf(-z));
+            y[i] = x[i] * (sg + z * sg * (1.0f - sg));
+            break;
+        }
+        }
+    }
+}
+
+// ---------------------------------------------------- softmax + CE rows --
+// One wave per row of logits[N][V]: p = softmax(row), dl = p * scale with
+// scale subtracted at the target; rowloss[r] = -log(p[target] + 1e-12) in
+// double when rowloss is given.  A target outside [0, V) gives a NaN loss.
+__global__ __launch_bounds__(256) void k_xent(const float *__restrict__ logits, const int *__restrict__ tgt,
+                                              float *__restrict__ dl, double *__restrict__ rowloss, float scale,
+                                              int N, int V)
+{
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= N) return;
+    const float *lg = logits + (size_t)r * V;
+    float mx = -INFINITY;
+    for (int i = lane; i < V; i += 64) mx = fmaxf(mx, lg[i]);
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float sum = 0.f;
+    for (int i = lane; i < V; i += 64) sum += expf(lg[i] - mx);
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    const float inv = 1.0f / sum;
+    const int t = tgt[r];
+    float *d = dl + (size_t)r * V;
+    for (int i = lane; i < V; i += 64) {
+        const float p = expf(lg[i] - mx) * inv;
+        float g = p * scale;
+        if (i == t) {
+            g -= scale;
+            if (rowloss) rowloss[r] = -log((double)p + 1e-12);
+        }
+        d[i] = g;
+    }
+    if (rowloss && lane == 0 && (t < 0 || t >= V)) rowloss[r] = NAN;
+}
+
+// Sum of n doubles by one workgroup in a fixed order; out = (float)(sum / n).
+__global__ __launch_bounds__(1024) void k_sum_loss(const double *__restrict__ rowloss, int n, float *__restrict__ out)
+{
+    __shared__ double s[1024];
+    double a = 0.0;
+    for (int i = threadIdx.x; i < n; i += 1024) a += rowloss[i];
+    s[threadIdx.x] = a;
+    __syncthreads();
+    for (int o = 512; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) s[threadIdx.x] += s[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[0] = (float)(s[0] / n);
+}
+
+// ------------------------------------------------------ gradnorm, AdamW --
+#define GN_BLOCKS 1024
+__global__ __launch_bounds__(256) void k_sumsq(const float *__restrict__ G, size_t n, double *__restrict__ part)
+{
+    __shared__ double s[256];
+    double a = 0.0;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)GN_BLOCKS * 256) {
+        const double g = G[i];
+        a += g * g;
+    }
+    s[threadIdx.x] = a;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) s[threadIdx.x] += s[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part[blockIdx.x] = s[0];
+}
+
+__global__ __launch_bounds__(1024) void k_norm_final(const double *__restrict__ part, float *__restrict__ norm)
+{
+    __shared__ double s[1024];
+    s[threadIdx.x] = part[threadIdx.x];
+    __syncthreads();
+    for (int o = 512; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) s[threadIdx.x] += s[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) norm[0] = (float)sqrt(s[0]);
+}
+
+// hyper = {lr, b1, b2, wd, bc1, bc2}; gscale = 1 / norm when norm > 1.
+__global__ __launch_bounds__(256) void k_adamw(float *__restrict__ P, const float *__restrict__ G,
+                                               float *__restrict__ M, float *__restrict__ Vv, size_t n,
+                                               const float *__restrict__ hyper, const float *__restrict__ norm)
+{
+    const float lr = hyper[0], b1 = hyper[1], b2 = hyper[2], wd = hyper[3], bc1 = hyper[4], bc2 = hyper[5];
+    float gs = 1.0f;
+    if (norm) {
+        const float gn = norm[0];
+        gs = gn > 1.0f ? 1.0f / gn : 1.0f;
+    }
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const float g = G[i] * gs;
+        const float m = b1 * M[i] + (1 - b1) * g;
+        const float vv = b2 * Vv[i] + (1 - b2) * g * g;
+        M[i] = m;
+        Vv[i] = vv;
+        const float mh = m / bc1, vh = vv / bc2;
+        P[i] -= lr * (mh / (sqrtf(vh) + 1e-8f) + wd * P[i]);
+    }
+}
+
+// ============================================================== entries ==
+#define ST(s) ((hipStream_t)(s))
+#define LAUNCH_CHECK() TLG_HIP(hipGetLastError())
+
+extern "C" int tlg_dev_embed_fwd(float *out, const float *emb, const int *tok, int N, int D, int V, void *stream)
+{
+    int rc = begin();
+    if (rc) return rc;
+    if (N < 0 || D <= 0 || V <= 0 || D % 4 || !al16(out) || !al16(emb))
+        return tlg_fail(TLG_EINVAL, "embed_fwd: N=%d D=%d V=%d (D %% 4 == 0, aligned rows)", N, D, V);
+    if (N == 0) return TLG_OK;
+    hipLaunchKernelGGL(k_embed_fwd, dim3(grid_for((size_t)N * D / 4, 256, 8192)), dim3(256), 0, ST(stream), emb,
+                       tok, N, D, V, out);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_embed_bwd(float *demb, const float *dout, const int *tok, int N, int D, int V, void *stream)
+{
+    int rc = begin();
+    if (rc) return rc;
+    if (N < 0 || D <= 0 || V <= 0) return tlg_fail(TLG_EINVAL, "embed_bwd: N=%d D=%d V=%d", N, D, V);
+    if (N == 0) return TLG_OK;
+    void *ws;
+    const size_t vb = ((size_t)(V + 1) * 4 + 255) & ~(size_t)255;
+    if ((rc = tr_scratch(3 * vb + (size_t)N * 4, &ws))) return rc;
+    int *cnt = (int *)ws, *off = (int *)((char *)ws + vb), *cur = (int *)((char *)ws + 2 * vb);
+    int *idx = (int *)((char *)ws + 3 * vb);
+    hipStream_t st = ST(stream);
+    hipLaunchKernelGGL(k_fill_int, dim3(grid_for(V, 256, 1024)), dim3(256), 0, st, cnt, V, 0);
+    hipLaunchKernelGGL(k_tok_count, dim3(grid_for(N, 256, 1024)), dim3(256), 0, st, tok, N, V, cnt);
+    hipLaunchKernelGGL(k_tok_scan, dim3(1), dim3(1024), 0, st, cnt, V, off, cur);
+    hipLaunchKernelGGL(k_tok_place, dim3(grid_for(N, 256, 1024)), dim3(256), 0, st, tok, N, V, cur, idx);
+    hipLaunchKernelGGL(k_embed_bwd, dim3((V + 3) / 4), dim3(256), 0, st, dout, off, idx, V, D, demb);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_rmsnorm_fwd(const float *x, const float *g, float *out, float *rinv, int rows, int D,
+                                   void *stream)
+{
+    int rc = begin();
+    if (rc) return rc;
+    if (rows < 0 || D <= 0 || D % 4 || !al16(x) || !al16(g) || !al16(out))
+        return tlg_fail(TLG_EINVAL, "rmsnorm_fwd: rows=%d D=%d (D %% 4 == 0, aligned rows)", rows, D);
+    if (rows == 0) return TLG_OK;
+    hipLaunchKernelGGL(k_rms_fwd, dim3((rows + 3) / 4), dim3(256), 0, ST(stream), x, g, out, rinv, rows, D);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_rmsnorm_bwd(const float *x, const float *g, const float *rinv, const float *dy,
+                                   const float *dx_in, float *dx, float *dg, int rows, int D, void *stream)
+{
+    int rc = begin();
+    if (rc) return rc;
+    if (rows < 0 || D <= 0 || D % 4 || D > 256 * RMS_MAXV || !al16(x) || !al16(g) || !al16(dy) || !al16(dx) ||
+        (dx_in && !al16(dx_in)))
+        return tlg_fail(TLG_EINVAL, "rmsnorm_bwd: rows=%d D=%d (D %% 4 == 0, D <= %d, aligned rows)", rows, D,
+                        256 * RMS_MAXV);
+    if (rows == 0) return TLG_OK;
+    const int nblk = (rows + RMS_ROWS - 1) / RMS_ROWS;
+    void *ws;
+    if ((rc = tr_scratch((size_t)nblk * D * 4, &ws))) return rc;
+    hipStream_t st = ST(stream);
+    hipLaunchKernelGGL(k_rms_bwd, dim3(nblk), dim3(256), 0, st, x, g, rinv, dy, dx_in, dx, rows, D, (float *)ws);
+    hipLaunchKernelGGL(k_rms_dg, dim3((D + 255) / 256), dim3(256), 0, st, (const float *)ws, nblk, D, dg);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_rope(float *buf, const int *pos, int T, int rows, int nheads, int hd, const float *cos_t,
+                            const float *sin_t, int maxpos, int back, void *stream)
+{
+    int rc = begin();
+    if (rc) return rc;
+    if (rows < 0 || nheads <= 0 || hd <= 0 || hd % 2 || maxpos <= 0 || (!pos && T <= 0))
+        return tlg_fail(TLG_EINVAL, "rope: rows=%d nheads=%d hd=%d T=%d maxpos=%d", rows, nheads, hd, T, maxpos);
+    if (rows == 0) return TLG_OK;
+    const size_t total = (size_t)rows * nheads * (hd / 2);
+    hipLaunchKernelGGL(k_rope, dim3(grid_for(total, 256, 8192)), dim3(256), 0, ST(stream), buf, pos, T, rows, nheads,
+                       hd, cos_t, sin_t, maxpos, back);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+static int attn_check(const char *who, int B, int T, int H, int KV, int hd)
+{
+    if (B < 0 || T < 0 || H <= 0 || KV <= 0 || H % KV || hd != AT_HD)
+        return tlg_fail(TLG_EINVAL, "%s: B=%d T=%d H=%d KV=%d hd=%d (head_dim 32, H %% KV == 0)", who, B, T, H, KV,
+                        hd);
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_attn_fwd(const float *q, const float *k, const float *v, float *out, float *lse, int B, int T,
+                                int H, int KV, int hd, int win, void *stream)
+{
+    int rc = begin();
+    if (rc || (rc = attn_check("attn_fwd", B, T, H, KV, hd))) return rc;
+    if (!al16(q) || !al16(k) || !al16(v) || !al16(out) || !lse)
+        return tlg_fail(TLG_EINVAL, "attn_fwd: unaligned operand or no lse buffer");
+    if (B == 0 || T == 0) return TLG_OK;
+    const int items = B * H * ((T + 31) / 32);
+    hipLaunchKernelGGL(k_attn_fwd, dim3((items + 3) / 4), dim3(256), 0, ST(stream), q, k, v, out, lse, B, T, H, KV,
+                       win, 1.0f / sqrtf((float)hd));
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_attn_bwd(const float *q, const float *k, const float *v, const float *out, const float *lse,
+                                const float *datt, float *dq, float *dk, float *dv, int B, int T, int H, int KV,
+                                int hd, int win, void *stream)
+{
+    int rc = begin();
+    if (rc || (rc = attn_check("attn_bwd", B, T, H, KV, hd))) return rc;
+    if (!al16(q) || !al16(k) || !al16(v) || !al16(out) || !al16(datt) || !al16(dq) || !lse || !dk || !dv)
+        return tlg_fail(TLG_EINVAL, "attn_bwd: unaligned or missing operand");
+    if (B == 0 || T == 0) return TLG_OK;
+    void *ws;
+    if ((rc = tr_scratch((size_t)B * T * H * 4, &ws))) return rc;
+    const float scale = 1.0f / sqrtf((float)hd);
+    const int items = B * H * ((T + 31) / 32);
+    hipStream_t st = ST(stream);
+    hipLaunchKernelGGL(k_attn_bwd_dq, dim3((items + 3) / 4), dim3(256), 0, st, q, k, v, out, datt, lse, (float *)ws,
+                       dq, B, T, H, KV, win, scale);
+    hipLaunchKernelGGL(k_attn_bwd_dkv, dim3(((T + 31) / 32) * B * KV), dim3(256), 0, st, q, k, v, datt, lse,
+                       (const float *)ws, dk, dv, B, T, H, KV, win, scale);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+static int ew(int op, size_t n, float *y, float *y2, const float *x, const float *a, const float *b, void *stream)
+{
+    int rc = begin();
+    if (rc) return rc;
+    if (n == 0) return TLG_OK;
+    hipLaunchKernelGGL(k_ew, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ST(stream), op, n, y, y2, x, a, b);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_add(float *y, const float *x, size_t n, void *stream)
+{
+    return ew(EW_ADD, n, y, nullptr, x, nullptr, nullptr, stream);
+}
+extern "C" int tlg_dev_swiglu_fwd(float *act, const float *g, const float *u, size_t n, void *stream)
+{
+    return ew(EW_SWIGLU, n, act, nullptr, nullptr, g, u, stream);
+}
+extern "C" int tlg_dev_swiglu_bwd(const float *dact, const float *g, const float *u, float *dg, float *du, size_t n,
+                                  void *stream)
+{
+    return ew(EW_SWIGLU_BWD, n, dg, du, dact, g, u, stream);
+}
+extern "C" int tlg_dev_silu_res(float *hk, const float *fn, const float *t1, size_t n, void *stream)
+{
+    return ew(EW_SILU_RES, n, hk, nullptr, fn, t1, nullptr, stream);
+}
+extern "C" int tlg_dev_silu_bwd(float *dt1, const float *dhk, const float *t1, size_t n, void *stream)
+{
+    return ew(EW_SILU_BWD, n, dt1, nullptr, dhk, t1, nullptr, stream);
+}
+
+extern "C" int tlg_dev_xent(const float *logits, const int *tgt, float *dlogits, float *loss, float scale, int N,
+                            int V, void *stream)
+{
+    int rc = begin();
+    if (rc) return rc;
+    if (N < 0 || V <= 0) return tlg_fail(TLG_EINVAL, "xent: N=%d V=%d", N, V);
+    if (N == 0) return TLG_OK;
+    double *rows = nullptr;
+    if (loss) {
+        void *ws;
+        if ((rc = tr_scratch((size_t)N * 8, &ws))) return rc;
+        rows = (double *)ws;
+    }
+    hipStream_t st = ST(stream);
+    hipLaunchKernelGGL(k_xent, dim3((N + 3) / 4), dim3(256), 0, st, logits, tgt, dlogits, rows, scale, N, V);
+    if (loss) hipLaunchKernelGGL(k_sum_loss, dim3(1), dim3(1024), 0, st, (const double *)rows, N, loss);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_gradnorm(const float *G, size_t n, float *norm, void *stream)
+{
+    int rc = begin();
+    if (rc) return rc;
+    void *ws;
+    if ((rc = tr_scratch(GN_BLOCKS * 8, &ws))) return rc;
+    hipStream_t st = ST(stream);
+    hipLaunchKernelGGL(k_sumsq, dim3(GN_BLOCKS), dim3(256), 0, st, G, n, (double *)ws);
+    hipLaunchKernelGGL(k_norm_final, dim3(1), dim3(1024), 0, st, (const double *)ws, norm);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_adamw(float *P, const float *G, float *M, float *V, size_t n, const float *hyper,
+                             const float *norm, void *stream)
+{
+    int rc = begin();
+    if (rc) return rc;
+    if (!hyper) return tlg_fail(TLG_EINVAL, "adamw: hyper is required");
+    if (n == 0) return TLG_OK;
+    hipLaunchKernelGGL(k_adamw, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ST(stream), P, G, M, V, n, hyper, norm);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}

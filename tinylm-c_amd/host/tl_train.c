@@ -1,0 +1,418 @@
+/* tl_train.c -- a device-resident training step of tinylm.c over the
+ * libtlgemm C ABI (see tl_train.h).
+ *
+ * The step issues, on one stream and in the reference's order, the GEMMs of
+ * forward / mtp_grad / backward (tinylm.c:968-1154) as grouped launches (the
+ * calls the reference makes back to back with nothing between them share a
+ * launch, tlg_dev_gemm_group), the non-GEMM work through include/tltrain.h,
+ * then global_gradnorm and AdamW (:2630-2633).  memset + mm_bt pairs become
+ * setting mm_bt calls (beta = 0), and the reference's memcpy(dfin, dout) /
+ * memcpy(dain, dfin) / memcpy(dout, dain) become rmsnorm_bwd bases and a
+ * pointer swap.
+ */
+#include "tl_train.h"
+#include "../../include/tlgemm.h"
+#include "../../include/tltrain.h"
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+typedef struct { size_t emb, an1, wq, wk, wv, wo, an2, wr, w1, w3, w2, nf, mtp0, total; } Map;
+
+struct TlTrain {
+    TlModel m;
+    int B, N, hd, KD, E;
+    size_t np;
+    void *arena;
+    float *P, *G, *Mo, *Vo;
+    int *tok, *tgt, *tgt_mtp, *assign;
+    float *hyper, *loss, *gnorm, *rcos, *rsin;
+    /* per layer, L slices each (the Acts fields the backward pass reads) */
+    float *a_in, *a_norm, *q, *k, *v, *ctx, *f_in, *f_norm, *g, *u, *a_rinv, *f_rinv, *lse, *gate, *rprobs;
+    /* one each */
+    float *x_final, *fn, *fn_rinv, *logits, *dl, *dout, *act, *dg, *du, *dfnorm, *dfin, *datt, *dq, *dk, *dv,
+          *dnorm, *dain, *dfn;
+    float hyper_host[8];
+    void *graph;
+};
+
+/* map_weights (tinylm.c:361-393) without QK-norm: emb | per layer an1 wq wk
+ * wv wo an2 [wr] w1 w3 w2 (E expert slots) | nf | mtp heads. */
+static void wmap(const TlTrain *t, int l, Map *o)
+{
+    const TlModel *m = &t->m;
+    const size_t D = m->D, KD = t->KD, F = m->F, E = t->E > 0 ? t->E : 1, R = t->E > 0 ? D * t->E : 0;
+    const size_t per = D + D * D + 2 * D * KD + D * D + D + R + E * 3 * D * F;
+    o->emb = 0;
+    o->an1 = (size_t)m->V * D + (size_t)l * per;
+    o->wq = o->an1 + D;
+    o->wk = o->wq + D * D;
+    o->wv = o->wk + D * KD;
+    o->wo = o->wv + D * KD;
+    o->an2 = o->wo + D * D;
+    o->wr = o->an2 + D;
+    o->w1 = o->wr + R;
+    o->w3 = o->w1 + E * D * F;
+    o->w2 = o->w3 + E * D * F;
+    o->nf = (size_t)m->V * D + (size_t)m->L * per;
+    o->mtp0 = o->nf + D;
+    o->total = o->mtp0 + (size_t)m->n_mtp * D * D;
+}
+
+static int lwin(const TlModel *m, int l)        /* cfg_lwin, tinylm.c:64-68 */
+{
+    if (m->win <= 0) return 0;
+    if (m->full_every > 0 && ((l + 1) % m->full_every) == 0) return 0;
+    return m->win;
+}
+
+/* ---- allocation ---------------------------------------------------------- */
+typedef struct { void **dst; size_t bytes; } Slot;
+
+TlTrain *tl_train_new(const TlModel *m, int B)
+{
+    if (!m || B <= 0 || m->V <= 0 || m->D <= 0 || m->L <= 0 || m->H <= 0 || m->KV <= 0 || m->F <= 0 ||
+        m->T <= 0 || m->n_mtp < 0 || m->n_exp < 0 || m->n_exp == 1 || m->D % m->H || m->H % m->KV ||
+        m->D / m->H != 32 || m->D % 4 || m->F % 4 || m->V % 4)
+        return NULL;
+    TlTrain *t = calloc(1, sizeof *t);
+    if (!t) return NULL;
+    t->m = *m;
+    t->B = B;
+    t->N = B * m->T;
+    t->hd = m->D / m->H;
+    t->KD = m->KV * t->hd;
+    t->E = m->n_exp;
+    Map mp;
+    wmap(t, 0, &mp);
+    t->np = mp.total;
+    const size_t N = t->N, L = m->L, D = m->D, KD = t->KD, F = m->F, V = m->V, H = m->H, E = t->E;
+    const size_t ND = N * D, NK = N * KD, NF = N * F, half = t->hd / 2;
+    const int dense = E == 0;
+    Slot s[] = {
+        {(void **)&t->P, 4 * t->np}, {(void **)&t->G, 4 * t->np}, {(void **)&t->Mo, 4 * t->np},
+        {(void **)&t->Vo, 4 * t->np}, {(void **)&t->tok, 4 * N}, {(void **)&t->tgt, 4 * N},
+        {(void **)&t->tgt_mtp, 4 * N * (m->n_mtp ? m->n_mtp : 1)}, {(void **)&t->hyper, 32},
+        {(void **)&t->loss, 4}, {(void **)&t->gnorm, 4}, {(void **)&t->rcos, 4 * m->T * half},
+        {(void **)&t->rsin, 4 * m->T * half},
+        {(void **)&t->a_in, 4 * L * ND}, {(void **)&t->a_norm, 4 * L * ND}, {(void **)&t->q, 4 * L * ND},
+        {(void **)&t->k, 4 * L * NK}, {(void **)&t->v, 4 * L * NK}, {(void **)&t->ctx, 4 * L * ND},
+        {(void **)&t->f_in, 4 * L * ND}, {(void **)&t->f_norm, 4 * L * ND},
+        {(void **)&t->g, dense ? 4 * L * NF : 0}, {(void **)&t->u, dense ? 4 * L * NF : 0},
+        {(void **)&t->a_rinv, 4 * L * N}, {(void **)&t->f_rinv, 4 * L * N}, {(void **)&t->lse, 4 * L * N * H},
+        {(void **)&t->assign, 4 * L * N * !dense}, {(void **)&t->gate, 4 * L * N * !dense},
+        {(void **)&t->rprobs, 4 * L * N * E},
+        {(void **)&t->x_final, 4 * ND}, {(void **)&t->fn, 4 * ND}, {(void **)&t->fn_rinv, 4 * N},
+        {(void **)&t->logits, 4 * N * V}, {(void **)&t->dl, 4 * N * V}, {(void **)&t->dout, 4 * ND},
+        {(void **)&t->act, dense ? 4 * NF : 0}, {(void **)&t->dg, dense ? 4 * NF : 0},
+        {(void **)&t->du, dense ? 4 * NF : 0}, {(void **)&t->dfnorm, 4 * ND}, {(void **)&t->dfin, 4 * ND},
+        {(void **)&t->datt, 4 * ND}, {(void **)&t->dq, 4 * ND}, {(void **)&t->dk, 4 * NK},
+        {(void **)&t->dv, 4 * NK}, {(void **)&t->dnorm, 4 * ND}, {(void **)&t->dain, 4 * ND},
+        {(void **)&t->dfn, 4 * ND},
+    };
+    const int ns = (int)(sizeof s / sizeof s[0]);
+    size_t total = 0;
+    for (int i = 0; i < ns; i++) total += (s[i].bytes + 255) & ~(size_t)255;
+    t->arena = tlg_dev_malloc(total);
+    if (!t->arena) { free(t); return NULL; }
+    char *p = t->arena;
+    for (int i = 0; i < ns; i++) {
+        *s[i].dst = s[i].bytes ? p : NULL;
+        p += (s[i].bytes + 255) & ~(size_t)255;
+    }
+    /* rope_init's tables (tinylm.c:611-618) for positions 0..T-1 */
+    float *cs = malloc(4 * m->T * half), *sn = malloc(4 * m->T * half);
+    int rc = !cs || !sn;
+    for (int tt = 0; !rc && tt < m->T; tt++)
+        for (size_t i = 0; i < half; i++) {
+            const float inv = powf(m->rope_base, -(2.0f * i) / t->hd);
+            const float a = tt * inv;
+            cs[tt * half + i] = cosf(a);
+            sn[tt * half + i] = sinf(a);
+        }
+    void *st = tlg_stream_create();
+    if (!rc) rc = tlg_memcpy_h2d(t->rcos, cs, 4 * m->T * half, st) || tlg_memcpy_h2d(t->rsin, sn, 4 * m->T * half, st);
+    for (int i = 0; !rc && i < 4; i++) rc = tlg_dev_zero(tl_train_buf(t, i), t->np, st);
+    if (!rc) rc = tlg_stream_sync(st);
+    if (!rc) rc = tl_train_set_hyper(t, 3e-4f, 0.9f, 0.95f, 0.1f, 1, st);
+    if (st) tlg_stream_destroy(st);
+    free(cs);
+    free(sn);
+    if (rc) { tl_train_free(t); return NULL; }
+    return t;
+}
+
+void tl_train_free(TlTrain *t)
+{
+    if (!t) return;
+    if (t->graph) tlg_graph_destroy(t->graph);
+    if (t->arena) tlg_dev_free(t->arena);
+    free(t);
+}
+
+size_t tl_train_nparams(const TlTrain *t) { return t ? t->np : 0; }
+
+float *tl_train_buf(TlTrain *t, int which)
+{
+    switch (which) {
+    case 0: return t->P;
+    case 1: return t->G;
+    case 2: return t->Mo;
+    case 3: return t->Vo;
+    default: return NULL;
+    }
+}
+
+float *tl_train_act(TlTrain *t, const char *name, int layer)
+{
+    const size_t N = t->N, ND = N * t->m.D, NK = N * t->KD, NF = N * t->m.F;
+    const size_t l = layer < 0 || layer >= t->m.L ? 0 : (size_t)layer;
+    struct { const char *n; float *p; size_t per; } tab[] = {
+        {"a_in", t->a_in, ND}, {"a_norm", t->a_norm, ND}, {"q", t->q, ND}, {"k", t->k, NK}, {"v", t->v, NK},
+        {"att_ctx", t->ctx, ND}, {"f_in", t->f_in, ND}, {"f_norm", t->f_norm, ND}, {"g", t->g, NF},
+        {"u", t->u, NF}, {"a_rinv", t->a_rinv, N}, {"f_rinv", t->f_rinv, N}, {"lse", t->lse, N * t->m.H},
+        {"x_final", t->x_final, 0}, {"fn_norm", t->fn, 0}, {"fn_rinv", t->fn_rinv, 0},
+        {"logits", t->logits, 0}, {"dlogits", t->dl, 0}, {"dfn", t->dfn, 0},
+    };
+    for (size_t i = 0; i < sizeof tab / sizeof tab[0]; i++)
+        if (!strcmp(name, tab[i].n)) return tab[i].p ? tab[i].p + l * tab[i].per : NULL;
+    return NULL;
+}
+
+/* ---- host <-> device at step boundaries ------------------------------------ */
+int tl_train_upload(TlTrain *t, const float *P, void *st)
+{
+    int rc = tlg_memcpy_h2d(t->P, P, 4 * t->np, st);
+    if (!rc) rc = tlg_dev_zero(t->Mo, t->np, st);
+    if (!rc) rc = tlg_dev_zero(t->Vo, t->np, st);
+    if (!rc) rc = tlg_stream_sync(st);
+    return rc;
+}
+
+int tl_train_set_batch(TlTrain *t, const int *tok, const int *tgt, const int *tgt_mtp, void *st)
+{
+    const int N = t->N, V = t->m.V, nm = t->m.n_mtp;
+    for (int i = 0; i < N; i++)
+        if (tok[i] < 0 || tok[i] >= V || tgt[i] < 0 || tgt[i] >= V) return TLG_EINVAL;
+    for (int i = 0; i < N * nm; i++)
+        if (!tgt_mtp || tgt_mtp[i] < 0 || tgt_mtp[i] >= V) return TLG_EINVAL;
+    int rc = tlg_memcpy_h2d(t->tok, tok, 4 * (size_t)N, st);
+    if (!rc) rc = tlg_memcpy_h2d(t->tgt, tgt, 4 * (size_t)N, st);
+    if (!rc && nm) rc = tlg_memcpy_h2d(t->tgt_mtp, tgt_mtp, 4 * (size_t)N * nm, st);
+    if (!rc) rc = tlg_stream_sync(st);
+    return rc;
+}
+
+int tl_train_set_hyper(TlTrain *t, float lr, float b1, float b2, float wd, int step, void *st)
+{
+    float *h = t->hyper_host;
+    h[0] = lr; h[1] = b1; h[2] = b2; h[3] = wd;
+    h[4] = 1.0f - powf(b1, step);                 /* adamw's bc1, bc2 (:1161) */
+    h[5] = 1.0f - powf(b2, step);
+    int rc = tlg_memcpy_h2d(t->hyper, h, 8 * sizeof(float), st);
+    if (!rc) rc = tlg_stream_sync(st);
+    return rc;
+}
+
+static float read1(const float *dev, void *st)
+{
+    float x = NAN;
+    if (tlg_memcpy_d2h(&x, dev, 4, st) || tlg_stream_sync(st)) return NAN;
+    return x;
+}
+float tl_train_loss(TlTrain *t, void *st) { return read1(t->loss, st); }
+float tl_train_gnorm(TlTrain *t, void *st) { return read1(t->gnorm, st); }
+
+/* ---- GEMM calls ------------------------------------------------------------ */
+static TlgGemmCall MM(float *Y, const float *X, const float *W, int M, int K, int N)
+{
+    TlgGemmCall c;
+    memset(&c, 0, sizeof c);
+    c.op = 0; c.C = Y; c.M = M; c.K = K; c.N = N; c.nseg = 1; c.A[0] = X; c.B[0] = W;
+    return c;
+}
+static TlgGemmCall BT(float *dX, int beta, const float *dY, const float *W, int M, int K, int N)
+{
+    TlgGemmCall c = MM(dX, dY, W, M, K, N);
+    c.op = 1; c.beta = beta;
+    return c;
+}
+static TlgGemmCall ATB(float *dW, const float *X, const float *dY, int M, int K, int N)
+{
+    TlgGemmCall c = MM(dW, X, dY, M, K, N);
+    c.op = 2; c.beta = 1;
+    return c;
+}
+/* dX (beta ? += : =) sum_s dY_s W_s^T, s < n (an mm_bt chain into one dX) */
+static TlgGemmCall BTN(float *dX, int beta, int M, int K, int n, const float *const *dY, const float *const *W,
+                       const int *Ns)
+{
+    TlgGemmCall c = BT(dX, beta, dY[0], W[0], M, K, Ns[0]);
+    c.nseg = n;
+    for (int s = 1; s < n; s++) { c.A[s] = dY[s]; c.B[s] = W[s]; c.Nseg[s] = Ns[s]; }
+    return c;
+}
+
+#define CK(x) do { int rc_ = (x); if (rc_) return rc_; } while (0)
+#define GROUP(st, ...) do { TlgGemmCall cs_[] = {__VA_ARGS__}; \
+        CK(tlg_dev_gemm_group(cs_, (int)(sizeof cs_ / sizeof cs_[0]), st)); } while (0)
+
+/* ---- forward, tinylm.c:968-1029 ------------------------------------------- */
+int tl_train_forward(TlTrain *t, void *st)
+{
+    const TlModel *m = &t->m;
+    const int N = t->N, D = m->D, KD = t->KD, F = m->F, V = m->V, H = m->H, KV = m->KV, T = m->T, E = t->E;
+    const size_t ND = (size_t)N * D, NK = (size_t)N * KD, NF = (size_t)N * F;
+    const float *P = t->P;
+    Map w;
+    wmap(t, 0, &w);
+    CK(tlg_dev_embed_fwd(t->a_in, P + w.emb, t->tok, N, D, V, st));
+    for (int l = 0; l < m->L; l++) {
+        wmap(t, l, &w);
+        float *xin = t->a_in + l * ND, *an = t->a_norm + l * ND, *q = t->q + l * ND, *k = t->k + l * NK,
+              *v = t->v + l * NK, *cx = t->ctx + l * ND, *fi = t->f_in + l * ND, *fnl = t->f_norm + l * ND;
+        CK(tlg_dev_rmsnorm_fwd(xin, P + w.an1, an, t->a_rinv + (size_t)l * N, N, D, st));
+        GROUP(st, MM(q, an, P + w.wq, N, D, D), MM(k, an, P + w.wk, N, D, KD), MM(v, an, P + w.wv, N, D, KD));
+        CK(tlg_dev_rope(q, NULL, T, N, H, t->hd, t->rcos, t->rsin, T, 0, st));
+        CK(tlg_dev_rope(k, NULL, T, N, KV, t->hd, t->rcos, t->rsin, T, 0, st));
+        CK(tlg_dev_attn_fwd(q, k, v, cx, t->lse + (size_t)l * N * H, t->B, T, H, KV, t->hd, lwin(m, l), st));
+        GROUP(st, MM(fi, cx, P + w.wo, N, D, D));
+        CK(tlg_dev_add(fi, xin, ND, st));
+        CK(tlg_dev_rmsnorm_fwd(fi, P + w.an2, fnl, t->f_rinv + (size_t)l * N, N, D, st));
+        float *out = l + 1 < m->L ? t->a_in + (l + 1) * ND : t->x_final;
+        if (E > 0) {
+            CK(tlg_dev_moe_grouped_fwd(fnl, fi, out, N, D, F, E, P + w.wr, P + w.w1, P + w.w3, P + w.w2,
+                                       t->assign + (size_t)l * N, t->gate + (size_t)l * N,
+                                       t->rprobs + (size_t)l * N * E, st));
+        } else {
+            float *g = t->g + l * NF, *u = t->u + l * NF;
+            GROUP(st, MM(g, fnl, P + w.w1, N, D, F), MM(u, fnl, P + w.w3, N, D, F));
+            CK(tlg_dev_swiglu_fwd(t->act, g, u, NF, st));
+            GROUP(st, MM(out, t->act, P + w.w2, N, F, D));
+            CK(tlg_dev_add(out, fi, ND, st));
+        }
+    }
+    CK(tlg_dev_rmsnorm_fwd(t->x_final, P + w.nf, t->fn, t->fn_rinv, N, D, st));
+    GROUP(st, BT(t->logits, 0, t->fn, P + w.emb, N, V, D));
+    /* softmax-CE, with backward's dlogits (:1076-1082) from the same pass */
+    CK(tlg_dev_xent(t->logits, t->tgt, t->dl, t->loss, 1.0f / N, N, V, st));
+    return 0;
+}
+
+/* ---- backward, tinylm.c:1072-1154 with mtp_grad :1036-1069 ---------------- */
+int tl_train_backward(TlTrain *t, void *st)
+{
+    const TlModel *m = &t->m;
+    const int N = t->N, D = m->D, KD = t->KD, F = m->F, V = m->V, H = m->H, KV = m->KV, T = m->T, E = t->E;
+    const size_t ND = (size_t)N * D, NK = (size_t)N * KD, NF = (size_t)N * F;
+    const float *P = t->P;
+    float *G = t->G;
+    Map w;
+    wmap(t, 0, &w);
+    CK(tlg_dev_zero(G, t->np, st));                                   /* memset(G), :2628 */
+    GROUP(st, MM(t->dfn, t->dl, P + w.emb, N, V, D), ATB(G + w.emb, t->dl, t->fn, N, V, D));
+    for (int h = 0; h < m->n_mtp; h++) {
+        const float wk = 0.2f * powf(0.8f, (float)h);
+        const float *Wk = P + w.mtp0 + (size_t)h * D * D;
+        float *t1 = t->datt, *hk = t->dnorm, *dhk = t->dq, *dt1 = t->dain;   /* the reference's scratch */
+        GROUP(st, MM(t1, t->fn, Wk, N, D, D));
+        CK(tlg_dev_silu_res(hk, t->fn, t1, ND, st));
+        GROUP(st, BT(t->logits, 0, hk, P + w.emb, N, V, D));
+        CK(tlg_dev_xent(t->logits, t->tgt_mtp + (size_t)h * N, t->dl, NULL, wk / N, N, V, st));
+        GROUP(st, ATB(G + w.emb, t->dl, hk, N, V, D), MM(dhk, t->dl, P + w.emb, N, V, D));
+        CK(tlg_dev_add(t->dfn, dhk, ND, st));
+        CK(tlg_dev_silu_bwd(dt1, dhk, t1, ND, st));
+        GROUP(st, ATB(G + w.mtp0 + (size_t)h * D * D, t->fn, dt1, N, D, D), BT(t->dfn, 1, dt1, Wk, N, D, D));
+    }
+    float *dout = t->dout, *dain = t->dain;
+    CK(tlg_dev_rmsnorm_bwd(t->x_final, P + w.nf, t->fn_rinv, t->dfn, NULL, dout, G + w.nf, N, D, st));
+    for (int l = m->L - 1; l >= 0; l--) {
+        wmap(t, l, &w);
+        float *xin = t->a_in + l * ND, *an = t->a_norm + l * ND, *q = t->q + l * ND, *k = t->k + l * NK,
+              *v = t->v + l * NK, *cx = t->ctx + l * ND, *fi = t->f_in + l * ND, *fnl = t->f_norm + l * ND;
+        if (E > 0) {
+            CK(tlg_dev_moe_grouped_bwd(fnl, dout, t->dfnorm, t->assign + (size_t)l * N, t->gate + (size_t)l * N,
+                                       t->rprobs + (size_t)l * N * E, N, D, F, E, P + w.wr, P + w.w1, P + w.w3,
+                                       P + w.w2, G + w.wr, G + w.w1, G + w.w3, G + w.w2, st));
+        } else {
+            float *g = t->g + l * NF, *u = t->u + l * NF;
+            CK(tlg_dev_swiglu_fwd(t->du, g, u, NF, st));                 /* act recompute, :1097-1098 */
+            GROUP(st, ATB(G + w.w2, t->du, dout, N, F, D), BT(t->act, 0, dout, P + w.w2, N, F, D));
+            CK(tlg_dev_swiglu_bwd(t->act, g, u, t->dg, t->du, NF, st));
+            const float *dy[2] = {t->dg, t->du}, *wt[2] = {P + w.w1, P + w.w3};
+            const int ns[2] = {F, F};
+            GROUP(st, BTN(t->dfnorm, 0, N, D, 2, dy, wt, ns), ATB(G + w.w1, fnl, t->dg, N, D, F),
+                  ATB(G + w.w3, fnl, t->du, N, D, F));
+        }
+        CK(tlg_dev_rmsnorm_bwd(fi, P + w.an2, t->f_rinv + (size_t)l * N, t->dfnorm, dout, t->dfin, G + w.an2, N, D,
+                               st));
+        GROUP(st, BT(t->datt, 0, t->dfin, P + w.wo, N, D, D), ATB(G + w.wo, cx, t->dfin, N, D, D));
+        CK(tlg_dev_attn_bwd(q, k, v, cx, t->lse + (size_t)l * N * H, t->datt, t->dq, t->dk, t->dv, t->B, T, H, KV,
+                            t->hd, lwin(m, l), st));
+        CK(tlg_dev_rope(t->dq, NULL, T, N, H, t->hd, t->rcos, t->rsin, T, 1, st));
+        CK(tlg_dev_rope(t->dk, NULL, T, N, KV, t->hd, t->rcos, t->rsin, T, 1, st));
+        const float *dy[3] = {t->dq, t->dk, t->dv}, *wt[3] = {P + w.wq, P + w.wk, P + w.wv};
+        const int ns[3] = {D, KD, KD};
+        GROUP(st, BTN(t->dnorm, 0, N, D, 3, dy, wt, ns), ATB(G + w.wq, an, t->dq, N, D, D),
+              ATB(G + w.wk, an, t->dk, N, D, KD), ATB(G + w.wv, an, t->dv, N, D, KD));
+        CK(tlg_dev_rmsnorm_bwd(xin, P + w.an1, t->a_rinv + (size_t)l * N, t->dnorm, t->dfin, dain, G + w.an1, N, D,
+                               st));
+        float *tmp = dout; dout = dain; dain = tmp;                    /* memcpy(dout, dain), :1146 */
+    }
+    wmap(t, 0, &w);
+    CK(tlg_dev_embed_bwd(G + w.emb, dout, t->tok, N, D, V, st));
+    CK(tlg_dev_gemm_flush(st));
+    return 0;
+}
+
+/* ---- global_gradnorm + AdamW, tinylm.c:2630-2633 -------------------------- */
+int tl_train_optimize(TlTrain *t, void *st)
+{
+    CK(tlg_dev_gradnorm(t->G, t->np, t->gnorm, st));
+    CK(tlg_dev_adamw(t->P, t->G, t->Mo, t->Vo, t->np, t->hyper, t->gnorm, st));
+    return 0;
+}
+
+int tl_train_step(TlTrain *t, void *st)
+{
+    CK(tl_train_forward(t, st));
+    CK(tl_train_backward(t, st));
+    return tl_train_optimize(t, st);
+}
+
+int tl_train_graph_build(TlTrain *t, void *st)
+{
+    if (t->graph) { tlg_graph_destroy(t->graph); t->graph = NULL; }
+    CK(tlg_graph_begin(st));
+    const int rc = tl_train_step(t, st);
+    void *g = tlg_graph_end(st);
+    if (rc) { if (g) tlg_graph_destroy(g); return rc; }
+    if (!g) return TLG_EHIP;
+    t->graph = g;
+    return 0;
+}
+
+int tl_train_graph_step(TlTrain *t, void *st)
+{
+    if (!t->graph) return TLG_EINVAL;
+    return tlg_graph_launch(t->graph, st);
+}
+
+int tl_train_time_phases(TlTrain *t, float *ms, void *st)
+{
+    void *ev[4];
+    for (int i = 0; i < 4; i++) if (!(ev[i] = tlg_event_create())) return TLG_EHIP;
+    int rc = tlg_event_record(ev[0], st);
+    if (!rc) rc = tl_train_forward(t, st);
+    if (!rc) rc = tlg_event_record(ev[1], st);
+    if (!rc) rc = tl_train_backward(t, st);
+    if (!rc) rc = tlg_event_record(ev[2], st);
+    if (!rc) rc = tl_train_optimize(t, st);
+    if (!rc) rc = tlg_event_record(ev[3], st);
+    if (!rc) rc = tlg_stream_sync(st);
+    for (int i = 0; !rc && i < 3; i++) ms[i] = tlg_event_elapsed_ms(ev[i], ev[i + 1]);
+    for (int i = 0; i < 4; i++) tlg_event_destroy(ev[i]);
+    return rc;
+}

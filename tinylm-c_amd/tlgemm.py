@@ -13,6 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libtlgemm.so")
 HEADER = os.path.join(REPO, "include", "tlgemm.h")
+TRAIN_HEADER = os.path.join(REPO, "include", "tltrain.h")
 
 _fp = ctypes.POINTER(ctypes.c_float)
 _ip = ctypes.POINTER(ctypes.c_int)
@@ -70,14 +71,34 @@ SIGNATURES = {
     "tlg_moe_grouped_fwd": (None, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tlg_moe_grouped_bwd": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp,
                                    _vp, _vp, _vp, _vp]),
+    # include/tltrain.h
+    "tlg_dev_embed_fwd": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "tlg_dev_embed_bwd": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "tlg_dev_rmsnorm_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp]),
+    "tlg_dev_rmsnorm_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp]),
+    "tlg_dev_rope": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp]),
+    "tlg_dev_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "tlg_dev_attn_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "tlg_dev_add": (_i, [_vp, _vp, _sz, _vp]),
+    "tlg_dev_swiglu_fwd": (_i, [_vp, _vp, _vp, _sz, _vp]),
+    "tlg_dev_swiglu_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "tlg_dev_silu_res": (_i, [_vp, _vp, _vp, _sz, _vp]),
+    "tlg_dev_silu_bwd": (_i, [_vp, _vp, _vp, _sz, _vp]),
+    "tlg_dev_xent": (_i, [_vp, _vp, _vp, _vp, ctypes.c_float, _i, _i, _vp]),
+    "tlg_dev_gradnorm": (_i, [_vp, _sz, _vp, _vp]),
+    "tlg_dev_adamw": (_i, [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp]),
 }
 
 
-def header_symbols(path=HEADER):
-    """Function names declared in a C header (tlg_*/tl_* prototypes)."""
-    text = open(path).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(tlg?_[a-z0-9_]+)\s*\(", text)))
+def header_symbols(path=None):
+    """Function names declared in a C header (tlg_*/tl_* prototypes); by
+    default the library's two public headers."""
+    names = set()
+    for p in ([path] if path else [HEADER, TRAIN_HEADER]):
+        text = open(p).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(tlg?_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 class TlgError(RuntimeError):
@@ -205,6 +226,94 @@ class TlWeightMap(ctypes.Structure):
                 ("emb", "an1", "wq", "wk", "wv", "wo", "an2", "w1", "w3", "w2", "nf", "mtp0", "total")]
 
 
+class TlModel(ctypes.Structure):
+    """host/tl_train.h TlModel (tinylm.c Cfg fields of the training step)."""
+    _fields_ = [(n, ctypes.c_int) for n in ("V", "D", "L", "H", "KV", "F", "T", "n_mtp", "n_exp", "win",
+                                            "full_every")] + [("rope_base", ctypes.c_float)]
+
+
+class Train:
+    """One TlTrain: device P / G / AdamW state and activations of a model."""
+
+    def __init__(self, host, model, B):
+        if isinstance(model, dict):
+            model = TlModel(**{"rope_base": 10000.0, **model})
+        self.host, self.model, self.B = host, model, B
+        self.N = B * model.T
+        self.h = host.dll.tl_train_new(ctypes.byref(model), B)
+        if not self.h:
+            raise TlgError("tl_train_new failed: bad model shape or out of device memory")
+        self.np = host.dll.tl_train_nparams(self.h)
+
+    def buf(self, which):
+        """Device address of 0 P, 1 G, 2 M, 3 V."""
+        return self.host.dll.tl_train_buf(self.h, which)
+
+    def act(self, name, layer=0):
+        return self.host.dll.tl_train_act(self.h, name.encode(), layer)
+
+    def _ck(self, rc, what):
+        if rc != 0:
+            lib = load()
+            raise TlgError(f"{what} failed ({rc}): {lib.dll.tlg_last_error().decode(errors='replace')}")
+        return 0
+
+    def upload(self, P, stream):
+        import numpy as np
+        P = np.ascontiguousarray(P, np.float32)
+        assert P.size == self.np
+        return self._ck(self.host.dll.tl_train_upload(self.h, P.ctypes.data, stream), "tl_train_upload")
+
+    def set_batch(self, tok, tgt, tgt_mtp, stream):
+        import numpy as np
+        tok = np.ascontiguousarray(tok, np.int32)
+        tgt = np.ascontiguousarray(tgt, np.int32)
+        tm = None if tgt_mtp is None else np.ascontiguousarray(tgt_mtp, np.int32)
+        return self._ck(self.host.dll.tl_train_set_batch(self.h, tok.ctypes.data, tgt.ctypes.data,
+                                                  None if tm is None else tm.ctypes.data, stream),
+                 "tl_train_set_batch")
+
+    def set_hyper(self, lr, b1, b2, wd, step, stream):
+        return self._ck(self.host.dll.tl_train_set_hyper(self.h, lr, b1, b2, wd, step, stream), "tl_train_set_hyper")
+
+    def forward(self, stream):
+        return self._ck(self.host.dll.tl_train_forward(self.h, stream), "tl_train_forward")
+
+    def backward(self, stream):
+        return self._ck(self.host.dll.tl_train_backward(self.h, stream), "tl_train_backward")
+
+    def optimize(self, stream):
+        return self._ck(self.host.dll.tl_train_optimize(self.h, stream), "tl_train_optimize")
+
+    def step(self, stream):
+        return self._ck(self.host.dll.tl_train_step(self.h, stream), "tl_train_step")
+
+    def graph_build(self, stream):
+        return self._ck(self.host.dll.tl_train_graph_build(self.h, stream), "tl_train_graph_build")
+
+    def graph_step(self, stream):
+        return self._ck(self.host.dll.tl_train_graph_step(self.h, stream), "tl_train_graph_step")
+
+    def loss(self, stream):
+        return float(self.host.dll.tl_train_loss(self.h, stream))
+
+    def gnorm(self, stream):
+        return float(self.host.dll.tl_train_gnorm(self.h, stream))
+
+    def time_phases(self, stream):
+        ms = (ctypes.c_float * 3)()
+        self._ck(self.host.dll.tl_train_time_phases(self.h, ms, stream), "tl_train_time_phases")
+        return list(ms)
+
+    def __del__(self):
+        try:
+            if self.h:
+                self.host.dll.tl_train_free(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
 class Plan:
     """A built TlPlan: buffers (name, floats, init) and calls as dicts."""
 
@@ -304,7 +413,34 @@ class Host:
         for n in ("mm", "mm_bt", "mm_atb"):
             getattr(d, n).argtypes = [_vp, _vp, _vp, _i, _i, _i]
             getattr(d, n).restype = None
+        # host/tl_train.h
+        d.tl_train_new.argtypes = [ctypes.POINTER(TlModel), _i]
+        d.tl_train_new.restype = _vp
+        d.tl_train_free.argtypes = [_vp]
+        d.tl_train_free.restype = None
+        d.tl_train_nparams.argtypes = [_vp]
+        d.tl_train_nparams.restype = _sz
+        d.tl_train_buf.argtypes = [_vp, _i]
+        d.tl_train_buf.restype = _vp
+        d.tl_train_act.argtypes = [_vp, ctypes.c_char_p, _i]
+        d.tl_train_act.restype = _vp
+        d.tl_train_upload.argtypes = [_vp, _vp, _vp]
+        d.tl_train_set_batch.argtypes = [_vp, _vp, _vp, _vp, _vp]
+        d.tl_train_set_hyper.argtypes = [_vp, ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float, _i, _vp]
+        for n in ("tl_train_forward", "tl_train_backward", "tl_train_optimize", "tl_train_step",
+                  "tl_train_graph_build", "tl_train_graph_step"):
+            getattr(d, n).argtypes = [_vp, _vp]
+            getattr(d, n).restype = _i
+        for n in ("tl_train_loss", "tl_train_gnorm"):
+            getattr(d, n).argtypes = [_vp, _vp]
+            getattr(d, n).restype = ctypes.c_float
+        d.tl_train_time_phases.argtypes = [_vp, ctypes.POINTER(ctypes.c_float), _vp]
         self.dll = d
+
+    def train(self, model, B):
+        """A device-resident training step (host/tl_train.h) for `model`
+        (a TlModel or a dict of its fields) and batches of B sequences."""
+        return Train(self, model, B)
 
     def plan_train(self, R, D, KD, F, V, L, n_mtp=0):
         raw = TlPlan()
