@@ -99,9 +99,9 @@ def test_rmsnorm_fixture(lib):
 
 
 # --------------------------------------------------------------------- rope --
-@pytest.mark.parametrize("rows,T,nh", [(4096, 256, 8), (40, 16, 3), (70, 70, 1)])
-def test_rope(lib, st, rows, T, nh):
-    hd = 32
+@pytest.mark.parametrize("rows,T,nh,hd", [(4096, 256, 8, 32), (40, 16, 3, 32), (70, 70, 1, 32), (50, 10, 2, 6)])
+def test_rope(lib, st, rows, T, nh, hd):
+    """hd 32: the float4 kernel; hd 6: the scalar one."""
     r = np.random.default_rng(rows)
     buf = r.standard_normal((rows, nh * hd)).astype(np.float32)
     cs, sn = st.rope_table(T, hd)

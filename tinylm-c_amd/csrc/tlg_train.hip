@@ -17,7 +17,8 @@
 // the backward pass rebuilds P without a max/sum pass.
 //
 // Attention uses v_mfma_f32_32x32x2_f32 on 32 x 32 tiles with head_dim 32 (the
-// width of every BASELINE model).  A wave owns 32 queries of one head.  The
+// width of every BASELINE model).  A wave works on 32 queries of one head
+// (the workgroup's waves split the key blocks and merge in a fixed order).  The
 // forward computes S^T = K Q^T, so in the MFMA result each lane holds one
 // query (lane % 32) and 16 keys: the softmax max and sum are in-lane plus one
 // exchange with lane ^ 32, and the same registers are the B operand of
@@ -273,13 +274,23 @@ __global__ __launch_bounds__(256) void k_rms_bwd(const float *__restrict__ x, co
     }
 }
 
-__global__ void k_rms_dg(const float *__restrict__ part, int nblk, int D, float *__restrict__ dg)
+// dg += sum over the nblk partial rows, one wave per float4 column: lane l
+// adds partials l, l + 64, ... in order, then a fixed butterfly.
+__global__ __launch_bounds__(256) void k_rms_dg(const float *__restrict__ part, int nblk, int D,
+                                                float *__restrict__ dg)
 {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= D) return;
-    float s = 0.f;
-    for (int b = 0; b < nblk; b++) s += part[(size_t)b * D + i];
-    dg[i] += s;
+    const int lane = threadIdx.x & 63;
+    const int c = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (c >= (D >> 2)) return;
+    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int b = lane; b < nblk; b += 64) s += reinterpret_cast<const f32x4 *>(part + (size_t)b * D)[c];
+    for (int o = 32; o > 0; o >>= 1) {
+        s.x += __shfl_xor(s.x, o);
+        s.y += __shfl_xor(s.y, o);
+        s.z += __shfl_xor(s.z, o);
+        s.w += __shfl_xor(s.w, o);
+    }
+    if (lane == 0) reinterpret_cast<f32x4 *>(dg)[c] += s;
 }
 
 // ----------------------------------------------------------------- rope --
@@ -312,6 +323,37 @@ __global__ void k_rope(float *__restrict__ buf, const int *__restrict__ pos, int
         } else {
             v[i] = a * c + b * s;
             v[i + half] = -a * s + b * c;
+        }
+    }
+}
+
+// The same on four consecutive pairs per thread (hd / 2 a multiple of 4,
+// 16-byte aligned rows and tables).
+__global__ void k_rope4(float *__restrict__ buf, const int *__restrict__ pos, int T, int rows, int nh, int hd,
+                        const float *__restrict__ cs, const float *__restrict__ sn, int maxpos, int back)
+{
+    const int half = hd >> 1, h4 = half >> 2, per_row = nh * h4;
+    const int total = rows * per_row;
+    for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < total; q += gridDim.x * blockDim.x) {
+        const int r = q / per_row, rem = q - r * per_row;
+        const int h = rem / h4, i = (rem - h * h4) * 4;
+        const int t = pos ? pos[r] : r % T;
+        f32x4 *va = reinterpret_cast<f32x4 *>(buf + (size_t)r * nh * hd + h * hd + i);
+        f32x4 *vb = reinterpret_cast<f32x4 *>(buf + (size_t)r * nh * hd + h * hd + half + i);
+        if (t < 0 || t >= maxpos) {
+            *va = f32x4{NAN, NAN, NAN, NAN};
+            *vb = f32x4{NAN, NAN, NAN, NAN};
+            continue;
+        }
+        const f32x4 c = *reinterpret_cast<const f32x4 *>(cs + (size_t)t * half + i);
+        const f32x4 sv = *reinterpret_cast<const f32x4 *>(sn + (size_t)t * half + i);
+        const f32x4 a = *va, b = *vb;
+        if (!back) {
+            *va = a * c - b * sv;
+            *vb = b * c + a * sv;
+        } else {
+            *va = a * c + b * sv;
+            *vb = -a * sv + b * c;
         }
     }
 }
@@ -355,18 +397,22 @@ __device__ __forceinline__ int at_kb0(int qb, int win)
     return lo > 0 ? lo / 32 : 0;
 }
 
-// One wave per (b, h, 32-query block), four per workgroup, heaviest blocks
-// (latest queries) first.  out = softmax(q k^T * scale) v per head (GQA:
+// One workgroup per (b, h, 32-query block), heaviest blocks (latest
+// queries) first; its four waves take the visible key blocks in turn
+// (kb = kb0 + wave, + 4, ...) and their partial softmax states are merged
+// in wave order through LDS.  out = softmax(q k^T * scale) v per head (GQA:
 // head h reads KV head h / (H / KV)); lse = max + log(sum) per (row, head).
+#define AT_W 4
 __global__ __launch_bounds__(256) void k_attn_fwd(const float *__restrict__ q, const float *__restrict__ k,
                                                   const float *__restrict__ v, float *__restrict__ out,
                                                   float *__restrict__ lse, int B, int T, int H, int KV, int win,
                                                   float scale)
 {
-    const int lane = threadIdx.x & 63;
+    __shared__ float sm_o[AT_W - 1][16][64];
+    __shared__ float sm_m[AT_W - 1][64], sm_l[AT_W - 1][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nqb = (T + 31) >> 5;
-    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= B * H * nqb) return;
+    const int item = blockIdx.x;
     const int qb = nqb - 1 - item / (B * H);
     const int bh = item % (B * H);
     const int b = bh / H, h = bh % H, kvh = h / (H / KV);
@@ -382,10 +428,16 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const float *__restrict__ q, c
 #pragma unroll
     for (int r = 0; r < 16; r++) o[r] = 0.f;
     float m = -INFINITY, l = 0.f;
-    for (int kb = at_kb0(qb, win); kb <= qb; kb++) {
+    for (int kb = at_kb0(qb, win) + wave; kb <= qb; kb += AT_W) {
         const int s0 = kb * 32, sl = s0 + lq;
         float kv[16];
         ld16(kb_ + (size_t)(sl < T ? sl : 0) * KD + 16 * hh, sl < T, kv);
+        float vv[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int s = s0 + at_row(r, lane);
+            vv[r] = s < T ? vb_[(size_t)s * KD + lq] : 0.f;
+        }
         f32x16 st;
 #pragma unroll
         for (int r = 0; r < 16; r++) st[r] = 0.f;
@@ -396,7 +448,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const float *__restrict__ q, c
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int s = s0 + at_row(r, lane);
-            sc[r] = (at_visible(s, qi, T, win) && s < T) ? st[r] * scale : -INFINITY;
+            sc[r] = at_visible(s, qi, T, win) ? st[r] * scale : -INFINITY;
             bm = fmaxf(bm, sc[r]);
         }
         bm = fmaxf(bm, __shfl_xor(bm, 32));
@@ -413,37 +465,54 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const float *__restrict__ q, c
         for (int r = 0; r < 16; r++) o[r] *= alpha;
         // O^T[d][q] += sum_s V[s][d] P^T[s][q]
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int s = s0 + at_row(r, lane);
-            const float vv = s < T ? vb_[(size_t)s * KD + lq] : 0.f;
-            o = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, p[r], o, 0, 0, 0);
-        }
+        for (int r = 0; r < 16; r++) o = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[r], p[r], o, 0, 0, 0);
         m = mn;
     }
+    if (wave > 0) {
+        sm_m[wave - 1][lane] = m;
+        sm_l[wave - 1][lane] = l;
+#pragma unroll
+        for (int r = 0; r < 16; r++) sm_o[wave - 1][r][lane] = o[r];
+    }
+    __syncthreads();
+    if (wave != 0 || !qok) return;
+    float M = m;
+    for (int w = 0; w < AT_W - 1; w++) M = fmaxf(M, sm_m[w][lane]);
+    const float a0 = m == -INFINITY ? 0.f : expf(m - M);
+    l *= a0;
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[r] *= a0;
+    for (int w = 0; w < AT_W - 1; w++) {
+        const float mw = sm_m[w][lane];
+        const float aw = mw == -INFINITY ? 0.f : expf(mw - M);
+        l += sm_l[w][lane] * aw;
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[r] += sm_o[w][r][lane] * aw;
+    }
     l += __shfl_xor(l, 32);
-    if (!qok) return;
     const float inv = 1.0f / l;
     float *orow = out + (size_t)(b * T + qi) * D + h * AT_HD;
 #pragma unroll
     for (int g4 = 0; g4 < 4; g4++)
         *reinterpret_cast<f32x4 *>(orow + 8 * g4 + 4 * hh) =
             f32x4{o[4 * g4] * inv, o[4 * g4 + 1] * inv, o[4 * g4 + 2] * inv, o[4 * g4 + 3] * inv};
-    if (hh == 0) lse[(size_t)(b * T + qi) * H + h] = m + logf(l);
+    if (hh == 0) lse[(size_t)(b * T + qi) * H + h] = M + logf(l);
 }
 
-// dQ, one wave per (b, h, 32-query block); also writes Dq = dO . O per
-// (row, head) for k_attn_bwd_dkv.  dS = P (dP - Dq) scale (attn_bwd's
-// dsc), dQ = dS K.
+// dQ, one workgroup per (b, h, 32-query block), its waves taking the key
+// blocks in turn and summing their partial dQ in wave order; also writes
+// Dq = dO . O per (row, head) for k_attn_bwd_dkv.  dS = P (dP - Dq) scale
+// (attn_bwd's dsc), dQ = dS K.
 __global__ __launch_bounds__(256) void k_attn_bwd_dq(const float *__restrict__ q, const float *__restrict__ k,
                                                      const float *__restrict__ v, const float *__restrict__ o,
                                                      const float *__restrict__ dout, const float *__restrict__ lse,
                                                      float *__restrict__ Dq, float *__restrict__ dq, int B, int T,
                                                      int H, int KV, int win, float scale)
 {
-    const int lane = threadIdx.x & 63;
+    __shared__ float sm_a[AT_W - 1][16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nqb = (T + 31) >> 5;
-    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= B * H * nqb) return;
+    const int item = blockIdx.x;
     const int qb = nqb - 1 - item / (B * H);
     const int bh = item % (B * H);
     const int b = bh / H, h = bh % H, kvh = h / (H / KV);
@@ -461,18 +530,23 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const float *__restrict__ q
     for (int j = 0; j < 16; j++) dd += dov[j] * ov[j];
     dd += __shfl_xor(dd, 32);
     const size_t rh = (size_t)(b * T + (qok ? qi : 0)) * H + h;
-    if (qok && hh == 0) Dq[rh] = dd;
+    if (qok && hh == 0 && wave == 0) Dq[rh] = dd;
     const float ls = qok ? lse[rh] : 0.f;
     const float *kb_ = k + (size_t)b * T * KD + kvh * AT_HD;
     const float *vb_ = v + (size_t)b * T * KD + kvh * AT_HD;
     f32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0.f;
-    for (int kb = at_kb0(qb, win); kb <= qb; kb++) {
+    for (int kb = at_kb0(qb, win) + wave; kb <= qb; kb += AT_W) {
         const int s0 = kb * 32, sl = s0 + lq;
-        float kv[16], vv[16];
+        float kv[16], vv[16], kk[16];
         ld16(kb_ + (size_t)(sl < T ? sl : 0) * KD + 16 * hh, sl < T, kv);
         ld16(vb_ + (size_t)(sl < T ? sl : 0) * KD + 16 * hh, sl < T, vv);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int s = s0 + at_row(r, lane);
+            kk[r] = s < T ? kb_[(size_t)s * KD + lq] : 0.f;
+        }
         f32x16 st, dp;
 #pragma unroll
         for (int r = 0; r < 16; r++) { st[r] = 0.f; dp[r] = 0.f; }
@@ -485,7 +559,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const float *__restrict__ q
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int s = s0 + at_row(r, lane);
-            if (at_visible(s, qi, T, win) && s < T) {
+            if (at_visible(s, qi, T, win)) {
                 const float p = expf(st[r] * scale - ls);
                 ds[r] = p * (dp[r] - dd) * scale;
             } else {
@@ -494,13 +568,18 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const float *__restrict__ q
         }
         // dQ^T[d][q] += sum_s K[s][d] dS^T[s][q]
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int s = s0 + at_row(r, lane);
-            const float kk = s < T ? kb_[(size_t)s * KD + lq] : 0.f;
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kk, ds[r], acc, 0, 0, 0);
-        }
+        for (int r = 0; r < 16; r++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[r], ds[r], acc, 0, 0, 0);
     }
-    if (!qok) return;
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) sm_a[wave - 1][r][lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave != 0 || !qok) return;
+    for (int w = 0; w < AT_W - 1; w++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[r] += sm_a[w][r][lane];
+    }
     float *orow = dq + (size_t)(b * T + qi) * D + h * AT_HD;
 #pragma unroll
     for (int g4 = 0; g4 < 4; g4++)
@@ -509,16 +588,17 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const float *__restrict__ q
 }
 
 // dK, dV: one workgroup per (b, kv head, 32-key block), first key blocks
-// (most queries) first.  Its four waves share the (head, query block) pairs
+// (most queries) first.  Its eight waves share the (head, query block) pairs
 // that see the block; each accumulates dV = P^T dO and dK = dS^T Q for its
-// pairs, and the four partials are summed in wave order.
-__global__ __launch_bounds__(256) void k_attn_bwd_dkv(const float *__restrict__ q, const float *__restrict__ k,
+// pairs, and the partials are summed in wave order through LDS.
+#define AT_KW 8
+__global__ __launch_bounds__(512) void k_attn_bwd_dkv(const float *__restrict__ q, const float *__restrict__ k,
                                                       const float *__restrict__ v, const float *__restrict__ dout,
                                                       const float *__restrict__ lse, const float *__restrict__ Dq,
                                                       float *__restrict__ dk, float *__restrict__ dv, int B, int T,
                                                       int H, int KV, int win, float scale)
 {
-    __shared__ float red[3][2][16][64];
+    __shared__ float red[AT_KW - 1][2][16][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nkb = (T + 31) >> 5;
     const int item = blockIdx.x;
@@ -539,15 +619,26 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dkv(const float *__restrict__ 
     f32x16 ak, av;
 #pragma unroll
     for (int r = 0; r < 16; r++) { ak[r] = 0.f; av[r] = 0.f; }
-    for (int pi = wave; pi < npairs; pi += 4) {
+    for (int pi = wave; pi < npairs; pi += AT_KW) {
         const int h = kvh * G + pi % G;
         const int q0 = (kb + pi / G) * 32;
         const int ql = q0 + lq;
         const bool qok = ql < T;
         const size_t qoff = (size_t)(b * T + (qok ? ql : 0)) * D + h * AT_HD + 16 * hh;
-        float qa[16], da[16];
+        float qa[16], da[16], dob[16], qbv[16], lr[16], dr[16];
         ld16(q + qoff, qok, qa);
         ld16(dout + qoff, qok, da);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int qq = q0 + at_row(r, lane);
+            const bool ok = qq < T;
+            const size_t off = (size_t)(b * T + (ok ? qq : 0)) * D + h * AT_HD + lq;
+            const size_t rh = (size_t)(b * T + (ok ? qq : 0)) * H + h;
+            dob[r] = ok ? dout[off] : 0.f;
+            qbv[r] = ok ? q[off] : 0.f;
+            lr[r] = ok ? lse[rh] : 0.f;
+            dr[r] = ok ? Dq[rh] : 0.f;
+        }
         f32x16 st, dp;
 #pragma unroll
         for (int r = 0; r < 16; r++) { st[r] = 0.f; dp[r] = 0.f; }
@@ -561,10 +652,9 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dkv(const float *__restrict__ 
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int qq = q0 + at_row(r, lane);
-            if (at_visible(sl, qq, T, win) && sok) {
-                const size_t rh = (size_t)(b * T + qq) * H + h;
-                pp[r] = expf(st[r] * scale - lse[rh]);
-                ds[r] = pp[r] * (dp[r] - Dq[rh]) * scale;
+            if (at_visible(sl, qq, T, win)) {
+                pp[r] = expf(st[r] * scale - lr[r]);
+                ds[r] = pp[r] * (dp[r] - dr[r]) * scale;
             } else {
                 pp[r] = 0.f;
                 ds[r] = 0.f;
@@ -573,12 +663,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dkv(const float *__restrict__ 
         // dV[s][d] += sum_q P[q][s] dO[q][d];  dK[s][d] += sum_q dS[q][s] Q[q][d]
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const int qq = q0 + at_row(r, lane);
-            const size_t off = (size_t)(b * T + (qq < T ? qq : 0)) * D + h * AT_HD + lq;
-            const float dob = qq < T ? dout[off] : 0.f;
-            const float qbv = qq < T ? q[off] : 0.f;
-            av = __builtin_amdgcn_mfma_f32_32x32x2f32(pp[r], dob, av, 0, 0, 0);
-            ak = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[r], qbv, ak, 0, 0, 0);
+            av = __builtin_amdgcn_mfma_f32_32x32x2f32(pp[r], dob[r], av, 0, 0, 0);
+            ak = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[r], qbv[r], ak, 0, 0, 0);
         }
     }
     if (wave > 0) {
@@ -593,7 +679,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dkv(const float *__restrict__ 
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         float a = ak[r], c = av[r];
-        for (int w = 0; w < 3; w++) {
+        for (int w = 0; w < AT_KW - 1; w++) {
             a += red[w][0][r][lane];
             c += red[w][1][r][lane];
         }
@@ -675,6 +761,58 @@ __global__ __launch_bounds__(256) void k_xent(const float *__restrict__ logits, 
         if (i == t) {
             g -= scale;
             if (rowloss) rowloss[r] = -log((double)p + 1e-12);
+        }
+        d[i] = g;
+    }
+    if (rowloss && lane == 0 && (t < 0 || t >= V)) rowloss[r] = NAN;
+}
+
+// The same with the row held in registers (V % 4 == 0, V <= 256 * XV):
+// one read of the logits, and each e^(l - max) evaluated once and used for
+// both the sum and the probability, as the reference's loop does.
+#define XENT_XV 8
+__global__ __launch_bounds__(256) void k_xent_reg(const float *__restrict__ logits, const int *__restrict__ tgt,
+                                                  float *__restrict__ dl, double *__restrict__ rowloss, float scale,
+                                                  int N, int V)
+{
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= N) return;
+    const int v4 = V >> 2;
+    const f32x4 *lg = reinterpret_cast<const f32x4 *>(logits + (size_t)r * V);
+    f32x4 x[XENT_XV];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < XENT_XV; j++) {
+        const int i = lane + 64 * j;
+        x[j] = i < v4 ? lg[i] : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        mx = fmaxf(mx, fmaxf(fmaxf(x[j].x, x[j].y), fmaxf(x[j].z, x[j].w)));
+    }
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < XENT_XV; j++) {
+        x[j] = f32x4{expf(x[j].x - mx), expf(x[j].y - mx), expf(x[j].z - mx), expf(x[j].w - mx)};
+        sum += (x[j].x + x[j].y) + (x[j].z + x[j].w);
+    }
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    const float inv = 1.0f / sum;
+    const int t = tgt[r];
+    f32x4 *d = reinterpret_cast<f32x4 *>(dl + (size_t)r * V);
+#pragma unroll
+    for (int j = 0; j < XENT_XV; j++) {
+        const int i = lane + 64 * j;
+        if (i >= v4) continue;
+        const f32x4 p = x[j] * inv;
+        f32x4 g = p * scale;
+        if ((t >> 2) == i) {
+            const int c = t & 3;
+            const float pt = c == 0 ? p.x : c == 1 ? p.y : c == 2 ? p.z : p.w;
+            if (c == 0) g.x -= scale;
+            else if (c == 1) g.y -= scale;
+            else if (c == 2) g.z -= scale;
+            else g.w -= scale;
+            if (rowloss) rowloss[r] = -log((double)pt + 1e-12);
         }
         d[i] = g;
     }
@@ -806,7 +944,7 @@ extern "C" int tlg_dev_rmsnorm_bwd(const float *x, const float *g, const float *
     int rc = begin();
     if (rc) return rc;
     if (rows < 0 || D <= 0 || D % 4 || D > 256 * RMS_MAXV || !al16(x) || !al16(g) || !al16(dy) || !al16(dx) ||
-        (dx_in && !al16(dx_in)))
+        !al16(dg) || (dx_in && !al16(dx_in)))
         return tlg_fail(TLG_EINVAL, "rmsnorm_bwd: rows=%d D=%d (D %% 4 == 0, D <= %d, aligned rows)", rows, D,
                         256 * RMS_MAXV);
     if (rows == 0) return TLG_OK;
@@ -815,7 +953,7 @@ extern "C" int tlg_dev_rmsnorm_bwd(const float *x, const float *g, const float *
     if ((rc = tr_scratch((size_t)nblk * D * 4, &ws))) return rc;
     hipStream_t st = ST(stream);
     hipLaunchKernelGGL(k_rms_bwd, dim3(nblk), dim3(256), 0, st, x, g, rinv, dy, dx_in, dx, rows, D, (float *)ws);
-    hipLaunchKernelGGL(k_rms_dg, dim3((D + 255) / 256), dim3(256), 0, st, (const float *)ws, nblk, D, dg);
+    hipLaunchKernelGGL(k_rms_dg, dim3((D / 4 + 3) / 4), dim3(256), 0, st, (const float *)ws, nblk, D, dg);
     LAUNCH_CHECK();
     return TLG_OK;
 }
@@ -829,8 +967,12 @@ extern "C" int tlg_dev_rope(float *buf, const int *pos, int T, int rows, int nhe
         return tlg_fail(TLG_EINVAL, "rope: rows=%d nheads=%d hd=%d T=%d maxpos=%d", rows, nheads, hd, T, maxpos);
     if (rows == 0) return TLG_OK;
     const size_t total = (size_t)rows * nheads * (hd / 2);
-    hipLaunchKernelGGL(k_rope, dim3(grid_for(total, 256, 8192)), dim3(256), 0, ST(stream), buf, pos, T, rows, nheads,
-                       hd, cos_t, sin_t, maxpos, back);
+    if ((hd / 2) % 4 == 0 && total / 4 < (1u << 30) && al16(buf) && al16(cos_t) && al16(sin_t))
+        hipLaunchKernelGGL(k_rope4, dim3(grid_for(total / 4, 256, 8192)), dim3(256), 0, ST(stream), buf, pos, T,
+                           rows, nheads, hd, cos_t, sin_t, maxpos, back);
+    else
+        hipLaunchKernelGGL(k_rope, dim3(grid_for(total, 256, 8192)), dim3(256), 0, ST(stream), buf, pos, T, rows,
+                           nheads, hd, cos_t, sin_t, maxpos, back);
     LAUNCH_CHECK();
     return TLG_OK;
 }
@@ -852,7 +994,7 @@ extern "C" int tlg_dev_attn_fwd(const float *q, const float *k, const float *v, 
         return tlg_fail(TLG_EINVAL, "attn_fwd: unaligned operand or no lse buffer");
     if (B == 0 || T == 0) return TLG_OK;
     const int items = B * H * ((T + 31) / 32);
-    hipLaunchKernelGGL(k_attn_fwd, dim3((items + 3) / 4), dim3(256), 0, ST(stream), q, k, v, out, lse, B, T, H, KV,
+    hipLaunchKernelGGL(k_attn_fwd, dim3(items), dim3(64 * AT_W), 0, ST(stream), q, k, v, out, lse, B, T, H, KV,
                        win, 1.0f / sqrtf((float)hd));
     LAUNCH_CHECK();
     return TLG_OK;
@@ -872,9 +1014,9 @@ extern "C" int tlg_dev_attn_bwd(const float *q, const float *k, const float *v, 
     const float scale = 1.0f / sqrtf((float)hd);
     const int items = B * H * ((T + 31) / 32);
     hipStream_t st = ST(stream);
-    hipLaunchKernelGGL(k_attn_bwd_dq, dim3((items + 3) / 4), dim3(256), 0, st, q, k, v, out, datt, lse, (float *)ws,
-                       dq, B, T, H, KV, win, scale);
-    hipLaunchKernelGGL(k_attn_bwd_dkv, dim3(((T + 31) / 32) * B * KV), dim3(256), 0, st, q, k, v, datt, lse,
+    hipLaunchKernelGGL(k_attn_bwd_dq, dim3(items), dim3(64 * AT_W), 0, st, q, k, v, out, datt, lse, (float *)ws, dq,
+                       B, T, H, KV, win, scale);
+    hipLaunchKernelGGL(k_attn_bwd_dkv, dim3(((T + 31) / 32) * B * KV), dim3(64 * AT_KW), 0, st, q, k, v, datt, lse,
                        (const float *)ws, dk, dv, B, T, H, KV, win, scale);
     LAUNCH_CHECK();
     return TLG_OK;
@@ -926,7 +1068,10 @@ extern "C" int tlg_dev_xent(const float *logits, const int *tgt, float *dlogits,
         rows = (double *)ws;
     }
     hipStream_t st = ST(stream);
-    hipLaunchKernelGGL(k_xent, dim3((N + 3) / 4), dim3(256), 0, st, logits, tgt, dlogits, rows, scale, N, V);
+    if (V % 4 == 0 && V <= 256 * XENT_XV && al16(logits) && al16(dlogits))
+        hipLaunchKernelGGL(k_xent_reg, dim3((N + 3) / 4), dim3(256), 0, st, logits, tgt, dlogits, rows, scale, N, V);
+    else
+        hipLaunchKernelGGL(k_xent, dim3((N + 3) / 4), dim3(256), 0, st, logits, tgt, dlogits, rows, scale, N, V);
     if (loss) hipLaunchKernelGGL(k_sum_loss, dim3(1), dim3(1024), 0, st, (const double *)rows, N, loss);
     LAUNCH_CHECK();
     return TLG_OK;
