@@ -51,7 +51,8 @@ int tlg_dev_rope(float *buf, const int *pos, int T, int rows, int nheads, int hd
 /* attn_fwd, tinylm.c:699-732: causal GQA attention of B sequences of T rows,
  * q [B*T][H*hd], k / v [B*T][KV*hd], out [B*T][H*hd]; head h reads KV head
  * h / (H/KV); win > 0 is the sliding window (cfg_lwin, :64-68).  Also writes
- * lse [B*T][H], the log-sum-exp of each softmax, for attn_bwd.  hd must be 32. */
+ * lse [B*T][H], the base-2 log-sum-exp of each row's scaled scores (log2 of
+ * sum_s 2^(q.k_s * scale * log2 e)), for attn_bwd.  hd must be 32. */
 int tlg_dev_attn_fwd(const float *q, const float *k, const float *v, float *out, float *lse, int B, int T, int H,
                      int KV, int hd, int win, void *stream);
 

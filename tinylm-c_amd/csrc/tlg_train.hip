@@ -397,11 +397,28 @@ __device__ __forceinline__ int at_kb0(int qb, int win)
     return lo > 0 ? lo / 32 : 0;
 }
 
+// K of block kb in the MFMA A layout (row s0 + lane % 32, 16 dims from
+// 16 * (lane / 32)) and V in the transposed-B layout (row s0 + at_row(r),
+// dim lane % 32); zeros past T.
+__device__ __forceinline__ void at_load_kv(const float *kb_, const float *vb_, int kb, int T, int KD, int lane,
+                                           float (&kv)[16], float (&vv)[16])
+{
+    const int s0 = kb * 32, sl = s0 + (lane & 31);
+    ld16(kb_ + (size_t)(sl < T ? sl : 0) * KD + 16 * (lane >> 5), sl < T, kv);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int s = s0 + at_row(r, lane);
+        vv[r] = s < T ? vb_[(size_t)s * KD + (lane & 31)] : 0.f;
+    }
+}
+
 // One workgroup per (b, h, 32-query block), heaviest blocks (latest
 // queries) first; its four waves take the visible key blocks in turn
 // (kb = kb0 + wave, + 4, ...) and their partial softmax states are merged
 // in wave order through LDS.  out = softmax(q k^T * scale) v per head (GQA:
-// head h reads KV head h / (H / KV)); lse = max + log(sum) per (row, head).
+// head h reads KV head h / (H / KV)); lse = log2 of the softmax's
+// denominator sum_s 2^(s * scale * log2 e) per (row, head), which the
+// backward kernels turn back into P with one exp2 per score.
 #define AT_W 4
 __global__ __launch_bounds__(256) void k_attn_fwd(const float *__restrict__ q, const float *__restrict__ k,
                                                   const float *__restrict__ v, float *__restrict__ out,
@@ -427,17 +444,18 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const float *__restrict__ q, c
     f32x16 o;
 #pragma unroll
     for (int r = 0; r < 16; r++) o[r] = 0.f;
+    // scores in the base-2 domain: p = 2^(s * scale * log2(e) - m)
+    const float c2 = scale * 1.44269504088896341f;
     float m = -INFINITY, l = 0.f;
-    for (int kb = at_kb0(qb, win) + wave; kb <= qb; kb += AT_W) {
-        const int s0 = kb * 32, sl = s0 + lq;
-        float kv[16];
-        ld16(kb_ + (size_t)(sl < T ? sl : 0) * KD + 16 * hh, sl < T, kv);
-        float vv[16];
+    float kn[16], vn[16];                       // next block's K / V (prefetched)
+    int kb = at_kb0(qb, win) + wave;
+    if (kb <= qb) at_load_kv(kb_, vb_, kb, T, KD, lane, kn, vn);
+    for (; kb <= qb; kb += AT_W) {
+        const int s0 = kb * 32;
+        float kv[16], vv[16];
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int s = s0 + at_row(r, lane);
-            vv[r] = s < T ? vb_[(size_t)s * KD + lq] : 0.f;
-        }
+        for (int j = 0; j < 16; j++) { kv[j] = kn[j]; vv[j] = vn[j]; }
+        if (kb + AT_W <= qb) at_load_kv(kb_, vb_, kb + AT_W, T, KD, lane, kn, vn);
         f32x16 st;
 #pragma unroll
         for (int r = 0; r < 16; r++) st[r] = 0.f;
@@ -448,16 +466,16 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const float *__restrict__ q, c
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int s = s0 + at_row(r, lane);
-            sc[r] = at_visible(s, qi, T, win) ? st[r] * scale : -INFINITY;
+            sc[r] = at_visible(s, qi, T, win) ? st[r] * c2 : -INFINITY;
             bm = fmaxf(bm, sc[r]);
         }
         bm = fmaxf(bm, __shfl_xor(bm, 32));
         const float mn = fmaxf(m, bm);
-        const float alpha = mn == -INFINITY ? 1.f : expf(m - mn);
+        const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
         float ps = 0.f, p[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            p[r] = sc[r] == -INFINITY ? 0.f : expf(sc[r] - mn);
+            p[r] = sc[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc[r] - mn);
             ps += p[r];
         }
         l = l * alpha + ps;
@@ -478,13 +496,13 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const float *__restrict__ q, c
     if (wave != 0 || !qok) return;
     float M = m;
     for (int w = 0; w < AT_W - 1; w++) M = fmaxf(M, sm_m[w][lane]);
-    const float a0 = m == -INFINITY ? 0.f : expf(m - M);
+    const float a0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
     l *= a0;
 #pragma unroll
     for (int r = 0; r < 16; r++) o[r] *= a0;
     for (int w = 0; w < AT_W - 1; w++) {
         const float mw = sm_m[w][lane];
-        const float aw = mw == -INFINITY ? 0.f : expf(mw - M);
+        const float aw = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
         l += sm_l[w][lane] * aw;
 #pragma unroll
         for (int r = 0; r < 16; r++) o[r] += sm_o[w][r][lane] * aw;
@@ -496,7 +514,22 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const float *__restrict__ q, c
     for (int g4 = 0; g4 < 4; g4++)
         *reinterpret_cast<f32x4 *>(orow + 8 * g4 + 4 * hh) =
             f32x4{o[4 * g4] * inv, o[4 * g4 + 1] * inv, o[4 * g4 + 2] * inv, o[4 * g4 + 3] * inv};
-    if (hh == 0) lse[(size_t)(b * T + qi) * H + h] = M + logf(l);
+    if (hh == 0) lse[(size_t)(b * T + qi) * H + h] = M + __builtin_amdgcn_logf(l);
+}
+
+// K and V of block kb in the A layout, and K again in the transposed-B
+// layout (for dQ = dS K); zeros past T.
+__device__ __forceinline__ void at_load_kvk(const float *kb_, const float *vb_, int kb, int T, int KD, int lane,
+                                            float (&kv)[16], float (&vv)[16], float (&kk)[16])
+{
+    const int s0 = kb * 32, sl = s0 + (lane & 31);
+    ld16(kb_ + (size_t)(sl < T ? sl : 0) * KD + 16 * (lane >> 5), sl < T, kv);
+    ld16(vb_ + (size_t)(sl < T ? sl : 0) * KD + 16 * (lane >> 5), sl < T, vv);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int s = s0 + at_row(r, lane);
+        kk[r] = s < T ? kb_[(size_t)s * KD + (lane & 31)] : 0.f;
+    }
 }
 
 // dQ, one workgroup per (b, h, 32-query block), its waves taking the key
@@ -534,19 +567,19 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const float *__restrict__ q
     const float ls = qok ? lse[rh] : 0.f;
     const float *kb_ = k + (size_t)b * T * KD + kvh * AT_HD;
     const float *vb_ = v + (size_t)b * T * KD + kvh * AT_HD;
+    const float c2 = scale * 1.44269504088896341f;
     f32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0.f;
-    for (int kb = at_kb0(qb, win) + wave; kb <= qb; kb += AT_W) {
-        const int s0 = kb * 32, sl = s0 + lq;
+    float kn[16], vn[16], kkn[16];              // next block (prefetched)
+    int kb = at_kb0(qb, win) + wave;
+    if (kb <= qb) at_load_kvk(kb_, vb_, kb, T, KD, lane, kn, vn, kkn);
+    for (; kb <= qb; kb += AT_W) {
+        const int s0 = kb * 32;
         float kv[16], vv[16], kk[16];
-        ld16(kb_ + (size_t)(sl < T ? sl : 0) * KD + 16 * hh, sl < T, kv);
-        ld16(vb_ + (size_t)(sl < T ? sl : 0) * KD + 16 * hh, sl < T, vv);
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int s = s0 + at_row(r, lane);
-            kk[r] = s < T ? kb_[(size_t)s * KD + lq] : 0.f;
-        }
+        for (int j = 0; j < 16; j++) { kv[j] = kn[j]; vv[j] = vn[j]; kk[j] = kkn[j]; }
+        if (kb + AT_W <= qb) at_load_kvk(kb_, vb_, kb + AT_W, T, KD, lane, kn, vn, kkn);
         f32x16 st, dp;
 #pragma unroll
         for (int r = 0; r < 16; r++) { st[r] = 0.f; dp[r] = 0.f; }
@@ -560,7 +593,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const float *__restrict__ q
         for (int r = 0; r < 16; r++) {
             const int s = s0 + at_row(r, lane);
             if (at_visible(s, qi, T, win)) {
-                const float p = expf(st[r] * scale - ls);
+                const float p = __builtin_amdgcn_exp2f(st[r] * c2 - ls);
                 ds[r] = p * (dp[r] - dd) * scale;
             } else {
                 ds[r] = 0.f;
@@ -616,6 +649,7 @@ __global__ __launch_bounds__(512) void k_attn_bwd_dkv(const float *__restrict__ 
     int qb_last = nkb - 1;
     if (win > 0) qb_last = min(qb_last, (s0 + 31 + win - 1) >> 5);
     const int npairs = G * (qb_last - kb + 1);
+    const float c2 = scale * 1.44269504088896341f;
     f32x16 ak, av;
 #pragma unroll
     for (int r = 0; r < 16; r++) { ak[r] = 0.f; av[r] = 0.f; }
@@ -653,7 +687,7 @@ __global__ __launch_bounds__(512) void k_attn_bwd_dkv(const float *__restrict__ 
         for (int r = 0; r < 16; r++) {
             const int qq = q0 + at_row(r, lane);
             if (at_visible(sl, qq, T, win)) {
-                pp[r] = expf(st[r] * scale - lr[r]);
+                pp[r] = __builtin_amdgcn_exp2f(st[r] * c2 - lr[r]);
                 ds[r] = pp[r] * (dp[r] - dr[r]) * scale;
             } else {
                 pp[r] = 0.f;
