@@ -486,3 +486,77 @@ def param_regions(st, m):
     out.append(("nf", w["nf"], w["nf"] + D))
     out += [(f"mtp[{k}]", w["mtp0"] + k * D * D, w["mtp0"] + (k + 1) * D * D) for k in range(m.n_mtp)]
     return out
+
+
+class Decoder:
+    """The oracle's decode restatement (orc_dec_*, forward_chunk of
+    tinylm.c:3721-3830): a ring KV cache of W positions, f32 (kvdt 0) or
+    f16 (kvdt 1) storage, fast_expf (exact 0) or expf (exact 1)."""
+
+    def __init__(self, m, P, W, kvdt=1, exact=0, maxpos=4096, path=LIB):
+        d = ctypes.CDLL(path)
+        d.orc_dec_new.argtypes = [ctypes.POINTER(OrcModel), _i, _i, _i, _i]
+        d.orc_dec_new.restype = ctypes.c_void_p
+        d.orc_dec_free.argtypes = [ctypes.c_void_p]
+        d.orc_dec_chunk.argtypes = [ctypes.c_void_p, _fp, _ip, _i, _i, _fp]
+        self.dll, self.m, self.P = d, m, np.ascontiguousarray(P, np.float32)
+        self.h = d.orc_dec_new(ctypes.byref(m), W, kvdt, exact, maxpos)
+
+    def chunk(self, tok, start):
+        tok = np.ascontiguousarray(tok, np.int32)
+        out = np.empty((tok.size, self.m.V), np.float32)
+        self.dll.orc_dec_chunk(self.h, _f(self.P), _n(tok), tok.size, start, _f(out))
+        return out
+
+    def __del__(self):
+        try:
+            self.dll.orc_dec_free(self.h)
+        except Exception:
+            pass
+
+
+def ref_forward_logits(m, B, P, tok, path=SEQ_LIB):
+    """forward()'s logits [B*T][V] from the reference's own code."""
+    d = ctypes.CDLL(path)
+    d.tlref_forward_logits.argtypes = [_fp, _ip, _fp] + [_i] * 11
+    out = np.empty((B * m.T, m.V), np.float32)
+    d.tlref_forward_logits(_f(np.ascontiguousarray(P, np.float32)), _n(np.ascontiguousarray(tok, np.int32)),
+                           _f(out), B, m.V, m.D, m.L, m.H, m.KV, m.F, m.T, m.n_exp, m.win, m.full_every)
+    return out
+
+
+def half_fns(which="oracle"):
+    """(f2h, h2f, fast_expf) on numpy arrays from the oracle or the reference."""
+    if which == "oracle":
+        d = ctypes.CDLL(LIB)
+        d.orc_f2h.restype, d.orc_f2h.argtypes = ctypes.c_ushort, [ctypes.c_float]
+        d.orc_h2f.restype, d.orc_h2f.argtypes = ctypes.c_float, [ctypes.c_ushort]
+        d.orc_fast_expf.restype, d.orc_fast_expf.argtypes = ctypes.c_float, [ctypes.c_float]
+        f2h = lambda x: np.array([d.orc_f2h(float(v)) for v in x], np.uint16)  # noqa: E731
+        h2f = lambda h: np.array([d.orc_h2f(int(v)) for v in h], np.float32)  # noqa: E731
+        fe = lambda x: np.array([d.orc_fast_expf(float(v)) for v in x], np.float32)  # noqa: E731
+        return f2h, h2f, fe
+    d = ctypes.CDLL(SEQ_LIB)
+    up = ctypes.POINTER(ctypes.c_ushort)
+    d.tlref_f2h.argtypes = [_fp, up, _i]
+    d.tlref_h2f.argtypes = [up, _fp, _i]
+    d.tlref_fast_expf.argtypes = [_fp, _fp, _i]
+
+    def f2h(x):
+        x = np.ascontiguousarray(x, np.float32)
+        h = np.empty(x.size, np.uint16)
+        d.tlref_f2h(_f(x), h.ctypes.data_as(up), x.size)
+        return h
+
+    def h2f(h):
+        h = np.ascontiguousarray(h, np.uint16)
+        x = np.empty(h.size, np.float32)
+        d.tlref_h2f(h.ctypes.data_as(up), _f(x), h.size)
+        return x
+
+    def fe(x):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        d.tlref_fast_expf(_f(x), _f(y), x.size)
+        return y
+    return f2h, h2f, fe

@@ -210,3 +210,22 @@ float tlref_train_step(float *P, float *G, const int *tok, const int *tgt, const
     tlref_acts_free(a, &c);
     return loss;
 }
+
+/* forward()'s logits (tinylm.c:968-1018; no targets) for B sequences. */
+void tlref_forward_logits(const float *P, const int *tok, float *logits, int B, int V, int D, int L, int H, int KV,
+                          int F, int T, int n_exp, int win, int full_every)
+{
+    Cfg c = tlref_mkcfg(V, D, L, H, KV, F, T, 0, n_exp, win, full_every);
+    tlref_rope_reset(&c, c.T);
+    Weights w;
+    map_weights(&c, (float *)P, &w);
+    memset(&w.ng, 0, sizeof w.ng);
+    Acts *a = acts_new(&c, B);
+    forward(&c, &w, a, tok, NULL);
+    memcpy(logits, a->logits, sizeof(float) * (size_t)B * T * V);
+    tlref_acts_free(a, &c);
+}
+/* The decode path's KV-cache conversions and softmax exponential. */
+void tlref_f2h(const float *x, unsigned short *h, int n) { for (int i = 0; i < n; i++) h[i] = f2h(x[i]); }
+void tlref_h2f(const unsigned short *h, float *x, int n) { for (int i = 0; i < n; i++) x[i] = h2f(h[i]); }
+void tlref_fast_expf(const float *x, float *y, int n) { for (int i = 0; i < n; i++) y[i] = fast_expf(x[i]); }

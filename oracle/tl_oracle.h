@@ -110,6 +110,19 @@ void  orc_init_params(const OrcModel *m, float *P, uint64_t seed);
 float orc_train_step(const OrcModel *m, int B, const float *P, float *G, const int *tok, const int *tgt,
                      const int *tgt_mtp);
 
+/* ---- decode: forward_chunk (:3721-3830), fp32 weights, dense FFN ---------
+ * A ring KV cache of W positions per layer stored as f32 (kvdt 0) or f16
+ * (kvdt 1, the reference default), the unsplit attention path, and the
+ * softmax exponential fast_expf (exact_exp 0, the default) or expf.  maxpos
+ * sizes the RoPE table (positions 0..maxpos-1). */
+typedef struct OrcDec OrcDec;
+OrcDec *orc_dec_new(const OrcModel *m, int W, int kvdt, int exact_exp, int maxpos);
+void    orc_dec_free(OrcDec *d);
+void    orc_dec_chunk(OrcDec *d, const float *P, const int *tok, int m, int start_pos, float *logits);
+float          orc_fast_expf(float x);         /* :3181-3191 */
+unsigned short orc_f2h(float f);               /* :3158-3168 (F16C path) */
+float          orc_h2f(unsigned short h);      /* :3147-3157 */
+
 /* A plan's call list run in C (CPU baseline of short calls): op 0 mm,
  * 1 mm_bt, 2 mm_atb, 3 memset of n floats; `reps` passes over the list. */
 typedef struct { int op; float *out; const float *a, *b; int M, K, N; size_t n; } OrcCall;

@@ -439,3 +439,168 @@ void orc_init_params(const OrcModel *m, float *P, uint64_t seed)
     }
     for (size_t i = 0; i < D; i++) P[w.nf + i] = 1.0f;
 }
+
+/* ---- decode: forward_chunk (tinylm.c:3721-3830) with fp32 weights --------
+ * KV ring cache of W positions per layer, stored as f32 or f16 (kv_store
+ * :3236-3250, the f16 default of kv_dtype_env :3138-3146), attention over the
+ * ring window with the unsplit attn_body path (:3639-3715: scores, max,
+ * exp, normalise, then the weighted sum of V), the softmax exponential either
+ * the reference's fast_expf (:3181-3191, its default) or expf. */
+#include <immintrin.h>
+
+/* fast_expf: clamp, x * log2(e) split into integer and fraction, 2^f by the
+ * reference's degree-5 Horner polynomial, 2^k written into the exponent. */
+float orc_fast_expf(float x)
+{
+    x = x < -87.0f ? -87.0f : (x > 88.0f ? 88.0f : x);
+    const float t = x * 1.44269504088896f;
+    const float k = floorf(t), f = t - k;
+    const float p = 1.0f + f * (0.6931471805f + f * (0.2402265069f + f * (0.0555041087f +
+                                                                        f * (0.0096181291f + f * 0.0013333558f))));
+    const unsigned int bits = (unsigned int)(((int)k + 127) << 23);
+    float two_k;
+    memcpy(&two_k, &bits, 4);
+    return p * two_k;
+}
+unsigned short orc_f2h(float f) { return _cvtss_sh(f, 0); }      /* IEEE round to nearest even */
+float orc_h2f(unsigned short h) { return _cvtsh_ss(h); }
+
+struct OrcDec {
+    OrcModel m;
+    int W, kvdt, exact, maxpos;
+    void **K, **V;
+    float *cs, *sn;
+};
+
+OrcDec *orc_dec_new(const OrcModel *m, int W, int kvdt, int exact_exp, int maxpos)
+{
+    OrcDec *d = calloc(1, sizeof *d);
+    const int hd = m->D / m->H, KD = m->KV * hd, esz = kvdt ? 2 : 4;
+    d->m = *m; d->W = W; d->kvdt = kvdt; d->exact = exact_exp; d->maxpos = maxpos;
+    d->K = calloc(m->L, sizeof(void *));
+    d->V = calloc(m->L, sizeof(void *));
+    for (int l = 0; l < m->L; l++) {
+        d->K[l] = calloc((size_t)W * KD, esz);
+        d->V[l] = calloc((size_t)W * KD, esz);
+    }
+    d->cs = zalloc((size_t)maxpos * (hd / 2));
+    d->sn = zalloc((size_t)maxpos * (hd / 2));
+    orc_rope_table(d->cs, d->sn, maxpos, hd, m->rope_base);
+    return d;
+}
+
+void orc_dec_free(OrcDec *d)
+{
+    if (!d) return;
+    for (int l = 0; l < d->m.L; l++) { free(d->K[l]); free(d->V[l]); }
+    free(d->K); free(d->V); free(d->cs); free(d->sn); free(d);
+}
+
+/* q . row with the row stored as f32 (sequential, dot_f :3086-3088) or f16
+ * (eight fma lanes, then (l0..3 + l4..7) and two pairwise adds: kv_dot's F16C
+ * path :3200-3207) */
+static float dec_dot(const float *q, const void *row, int n, int kvdt)
+{
+    if (!kvdt) {
+        const float *r = row;
+        float s = 0.0f;
+        for (int i = 0; i < n; i++) s += q[i] * r[i];
+        return s;
+    }
+    const unsigned short *h = row;
+    float acc[8] = {0};
+    int i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int j = 0; j < 8; j++) acc[j] = fmaf(q[i + j], orc_h2f(h[i + j]), acc[j]);
+    const float l0 = acc[0] + acc[4], l1 = acc[1] + acc[5], l2 = acc[2] + acc[6], l3 = acc[3] + acc[7];
+    float s = (l0 + l1) + (l2 + l3);
+    for (; i < n; i++) s += q[i] * orc_h2f(h[i]);
+    return s;
+}
+static float dec_val(const void *row, int i, int kvdt)
+{
+    return kvdt ? orc_h2f(((const unsigned short *)row)[i]) : ((const float *)row)[i];
+}
+
+/* m tokens at positions start..start+m-1; logits [m][V] (main head). */
+void orc_dec_chunk(OrcDec *d, const float *P, const int *tok, int m, int start, float *logits)
+{
+    const OrcModel *md = &d->m;
+    const int D = md->D, H = md->H, KV = md->KV, hd = D / H, KD = KV * hd, F = md->F, V = md->V, W = d->W,
+              grp = H / KV, esz = d->kvdt ? 2 : 4;
+    const float scale = 1.0f / sqrtf((float)hd);
+    OrcLayerMap w;
+    orc_param_map(md, 0, &w);
+    float *x = zalloc((size_t)m * D), *xn = zalloc((size_t)m * D), *q = zalloc((size_t)m * D),
+          *k = zalloc((size_t)m * KD), *v = zalloc((size_t)m * KD), *ctx = zalloc((size_t)m * D),
+          *tmp = zalloc((size_t)m * D), *g = zalloc((size_t)m * F), *u = zalloc((size_t)m * F),
+          *rinv = zalloc(m), *pr = zalloc(W);
+    int *pos = calloc(m, sizeof(int));
+    for (int j = 0; j < m; j++) {
+        memcpy(x + (size_t)j * D, P + w.emb + (size_t)tok[j] * D, sizeof(float) * D);
+        pos[j] = start + j;
+    }
+    for (int l = 0; l < md->L; l++) {
+        orc_param_map(md, l, &w);
+        orc_rmsnorm_fwd(x, P + w.an1, xn, rinv, m, D);
+        orc_mm(q, xn, P + w.wq, m, D, D);
+        orc_mm(k, xn, P + w.wk, m, D, KD);
+        orc_mm(v, xn, P + w.wv, m, D, KD);
+        orc_rope(q, pos, 1, m, H, hd, d->cs, d->sn, 0);
+        orc_rope(k, pos, 1, m, KV, hd, d->cs, d->sn, 0);
+        int eff = layer_win(md, l), wlim = (eff > 0 && eff < W) ? eff : W;
+        for (int j = 0; j < m; j++) {               /* kv_store into the ring */
+            const int slot = (start + j) % W;
+            for (int i = 0; i < KD; i++) {
+                if (d->kvdt) {
+                    ((unsigned short *)d->K[l])[(size_t)slot * KD + i] = orc_f2h(k[(size_t)j * KD + i]);
+                    ((unsigned short *)d->V[l])[(size_t)slot * KD + i] = orc_f2h(v[(size_t)j * KD + i]);
+                } else {
+                    ((float *)d->K[l])[(size_t)slot * KD + i] = k[(size_t)j * KD + i];
+                    ((float *)d->V[l])[(size_t)slot * KD + i] = v[(size_t)j * KD + i];
+                }
+            }
+        }
+        for (int j = 0; j < m; j++)
+            for (int h = 0; h < H; h++) {
+                const int p = pos[j], lo = p >= wlim ? p - wlim + 1 : 0, cnt = p - lo + 1, kh = h / grp;
+                const float *qh = q + (size_t)j * D + (size_t)h * hd;
+                float mx = -1e30f;
+                for (int t = 0; t < cnt; t++) {
+                    const int slot = (lo + t) % W;
+                    const char *kr = (const char *)d->K[l] + ((size_t)slot * KD + (size_t)kh * hd) * esz;
+                    pr[t] = dec_dot(qh, kr, hd, d->kvdt) * scale;
+                    if (pr[t] > mx) mx = pr[t];
+                }
+                float s = 0.0f;
+                for (int t = 0; t < cnt; t++) {
+                    pr[t] = d->exact ? expf(pr[t] - mx) : orc_fast_expf(pr[t] - mx);
+                    s += pr[t];
+                }
+                const float inv = s > 0 ? 1.0f / s : 0.0f;
+                for (int t = 0; t < cnt; t++) pr[t] *= inv;
+                float *acc = ctx + (size_t)j * D + (size_t)h * hd;
+                for (int i = 0; i < hd; i++) acc[i] = 0.0f;
+                for (int t = 0; t < cnt; t++) {
+                    const int slot = (lo + t) % W;
+                    const char *vr = (const char *)d->V[l] + ((size_t)slot * KD + (size_t)kh * hd) * esz;
+                    for (int i = 0; i < hd; i++) acc[i] = fmaf(pr[t], dec_val(vr, i, d->kvdt), acc[i]);
+                }
+            }
+        orc_mm(tmp, ctx, P + w.wo, m, D, D);
+        for (size_t i = 0; i < (size_t)m * D; i++) x[i] += tmp[i];
+        orc_rmsnorm_fwd(x, P + w.an2, xn, rinv, m, D);
+        orc_mm(g, xn, P + w.w1, m, D, F);
+        orc_mm(u, xn, P + w.w3, m, D, F);
+        for (size_t i = 0; i < (size_t)m * F; i++) u[i] = silu(g[i]) * u[i];
+        orc_mm(tmp, u, P + w.w2, m, F, D);
+        for (size_t i = 0; i < (size_t)m * D; i++) x[i] += tmp[i];
+    }
+    orc_param_map(md, 0, &w);
+    orc_rmsnorm_fwd(x, P + w.nf, xn, rinv, m, D);
+    memset(logits, 0, sizeof(float) * (size_t)m * V);
+    orc_mm_bt(logits, xn, P + w.emb, m, V, D);
+    float *all[] = {x, xn, q, k, v, ctx, tmp, g, u, rinv, pr};
+    for (size_t i = 0; i < sizeof all / sizeof all[0]; i++) free(all[i]);
+    free(pos);
+}

@@ -185,6 +185,29 @@ def step_cases(ref):
             P=P, tok=tok, tgt=tgt, tgt_mtp=tm, loss=np.float32(loss), G=G)
 
 
+def decode_cases():
+    """The decode path's pins: the reference's forward() logits of a small
+    model (a token-by-token decode with an f32 cache and expf must give
+    them), and its f2h / h2f / fast_expf on a spread of inputs."""
+    from oracle import StepFns, half_fns, model, ref_forward_logits
+    st = StepFns("reference")
+    m = model(V=96, D=64, L=2, H=2, KV=1, F=48, T=40)
+    P = st.init_params(m, 5)
+    P[m.V * m.D:] += (0.05 * np.random.default_rng(1).standard_normal(P.size - m.V * m.D)).astype(np.float32)
+    tok = np.random.default_rng(2).integers(0, m.V, m.T).astype(np.int32)
+    logits = ref_forward_logits(m, 1, P, tok)
+    np.savez(os.path.join(HERE, "step_decode_forward.npz"), model=np.array(
+        [m.V, m.D, m.L, m.H, m.KV, m.F, m.T], np.int32), P=P, tok=tok, logits=logits)
+    f2h, h2f, fe = half_fns("reference")
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(3000) * 10, rng.standard_normal(1000) * 1e-5,
+                        [0.0, -0.0, 65504.0, 65520.0, 1e6, -1e6, 6e-8, 3e-8, 2.98e-8]]).astype(np.float32)
+    h = f2h(x)
+    e_in = np.concatenate([-np.abs(rng.standard_normal(3000) * 8), [-100.0, -87.0, 0.0, 1.0, 88.0, 100.0]])
+    e_in = e_in.astype(np.float32)
+    np.savez(os.path.join(HERE, "step_half_exp.npz"), x=x, h=h, hx=h2f(h), e_in=e_in, e_out=fe(e_in))
+
+
 def main():
     if not os.path.isdir("/root/reference"):
         sys.exit("make_golden.py needs /root/reference (build container only)")
@@ -199,6 +222,7 @@ def main():
     seq_case("train_l2_mtp2", 2, 16, 32, 4, 1, 48, 64, 2, 2)
     seq_case("train_l3", 1, 24, 48, 6, 2, 40, 96, 3, 0)
     step_cases(ref)
+    decode_cases()
     print("fixtures written to", HERE)
 
 

@@ -244,3 +244,61 @@ def test_train_step_matches_reference_on_fresh_inputs(st):
     assert abs(l1 - l2) <= 1e-6 * l2
     for name, a, b in param_regions(st, m):
         assert normwise_rel(G1[a:b], G2[a:b]) <= 1e-5, name
+
+
+# ------------------------------------------------------------------ decode --
+def test_half_and_fast_expf_match_reference_fixture():
+    from oracle import half_fns
+    d = load_npz(golden("step_half_exp.npz")[0])
+    f2h, h2f, fe = half_fns("oracle")
+    assert np.array_equal(f2h(d["x"]), d["h"])
+    assert np.array_equal(h2f(d["h"]), d["hx"])
+    assert np.array_equal(fe(d["e_in"]), d["e_out"])
+    # closed forms: f16 keeps 11 significant bits (relative step <= 2^-11
+    # in the normal range); fast_expf is within 1e-4 of exp and exact at 0
+    normal = (np.abs(d["x"]) > 6.2e-5) & (np.abs(d["x"]) < 65504)
+    rel = np.abs(d["hx"][normal].astype(np.float64) - d["x"][normal]) / np.abs(d["x"][normal])
+    assert rel.max() <= 2.0 ** -11
+    ok = (d["e_in"] > -80) & (d["e_in"] <= 88)          # inside the clamp
+    assert np.allclose(d["e_out"][ok], np.exp(d["e_in"][ok].astype(np.float64)), rtol=1e-4, atol=0)
+    assert d["e_out"][d["e_in"] == 0.0][0] == 1.0
+
+
+def test_decode_matches_reference_forward_fixture():
+    """Decoding token by token through the ring cache (f32 cache, expf) gives
+    the reference's own forward() logits; the f16 cache and fast_expf (the
+    reference's decode defaults) move them by their rounding only."""
+    from oracle import Decoder
+    d = load_npz(golden("step_decode_forward.npz")[0])
+    V, D, L, H, KV, F, T = (int(x) for x in d["model"])
+    m = model(V=V, D=D, L=L, H=H, KV=KV, F=F, T=T)
+    for kvdt, exact, bar in ((0, 1, 5e-6), (0, 0, 5e-4), (1, 1, 5e-3), (1, 0, 5e-3)):
+        dec = Decoder(m, d["P"], T, kvdt=kvdt, exact=exact, maxpos=64)
+        lg = np.concatenate([dec.chunk(d["tok"][i:i + 1], i) for i in range(T)])
+        assert normwise_rel(lg, d["logits"]) <= bar, (kvdt, exact)
+        dec2 = Decoder(m, d["P"], T, kvdt=kvdt, exact=exact, maxpos=64)
+        chunks = np.concatenate([dec2.chunk(d["tok"][0:7], 0), dec2.chunk(d["tok"][7:15], 7),
+                                 dec2.chunk(d["tok"][15:], 15)])
+        assert np.array_equal(chunks, lg), "chunked prefill differs from token-by-token decode"
+
+
+def test_decode_ring_closed_forms():
+    """A ring of W slots equals an unbounded cache while positions < W, and
+    with a window of w attends to exactly the last w positions: decoding with
+    win = W' through a ring of W' slots equals a larger ring with win = W'."""
+    from oracle import Decoder
+    kw = dict(V=64, D=64, L=1, H=2, KV=1, F=32, T=16)
+    m = model(**kw)
+    P = StepFns("oracle").init_params(m, 9)
+    tok = np.random.default_rng(1).integers(0, 64, 40).astype(np.int32)
+    big = Decoder(m, P, 64, kvdt=0, exact=1, maxpos=64)
+    ring = Decoder(m, P, 16, kvdt=0, exact=1, maxpos=64)
+    a = np.concatenate([big.chunk(tok[i:i + 1], i) for i in range(16)])
+    b = np.concatenate([ring.chunk(tok[i:i + 1], i) for i in range(16)])
+    assert np.array_equal(a, b)
+    mw = model(**dict(kw, win=16))
+    big_w = Decoder(mw, P, 64, kvdt=0, exact=1, maxpos=64)
+    ring2 = Decoder(m, P, 16, kvdt=0, exact=1, maxpos=64)
+    a = np.concatenate([big_w.chunk(tok[i:i + 1], i) for i in range(40)])
+    b = np.concatenate([ring2.chunk(tok[i:i + 1], i) for i in range(40)])
+    assert np.array_equal(a, b)

@@ -1,0 +1,62 @@
+/* tl_decode.h -- device-resident decoding of tinylm.c (libtlhost.so, plain C
+ * over include/tlgemm.h, tltrain.h and tldecode.h).
+ *
+ * One TlDecode holds a model's fp32 weights (map_weights' layout) and a KV
+ * ring cache of W positions per layer in HBM and runs forward_chunk
+ * (tinylm.c:3721-3830) for chunks of m <= mmax rows: the embedding at the
+ * chunk's positions, per layer RMSNorm -> [Q, K, V] -> RoPE -> ring store ->
+ * attention over the ring window -> [O] + residual -> RMSNorm -> [W1, W3] ->
+ * SwiGLU -> [W2] + residual, the final norm and [logits] (brackets: one
+ * grouped launch, GEMV kernels at m <= 8).  The cache holds f16 (the
+ * reference's default, kv_dtype_env :3138-3146) or f32 elements; the softmax
+ * uses the reference's fast_expf (default) or expf.
+ *
+ * Greedy decoding stays on the device: the argmax of the last logits row
+ * becomes the next step's token and position in a device-side state, so one
+ * captured step per weight copy replays token after token with no host
+ * round trip.  Scope: dense FFN, head_dim 32, no QK-norm, W <= 4096.
+ */
+#ifndef TL_DECODE_H
+#define TL_DECODE_H
+#include <stddef.h>
+#include "tl_train.h"
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct TlDecode TlDecode;
+
+/* W: ring positions (the reference uses the training context T); kv_f16: 1
+ * f16 cache (default), 0 f32; exact_exp: 0 fast_expf (default), 1 expf;
+ * maxpos: RoPE table length (positions 0..maxpos-1); mmax: largest chunk;
+ * pool: copies of the weights, the greedy graph steps rotate through them so
+ * the weights stream from HBM rather than the last-level cache.  NULL on
+ * bad shapes or allocation failure. */
+TlDecode *tl_decode_new(const TlModel *m, int W, int kv_f16, int exact_exp, int maxpos, int mmax, int pool);
+void      tl_decode_free(TlDecode *d);
+size_t    tl_decode_nparams(const TlDecode *d);
+float    *tl_decode_params(TlDecode *d, int copy);      /* device P (copy < pool) */
+float    *tl_decode_logits(TlDecode *d);                /* device [mmax][V]        */
+
+/* Copy host weights into every copy; clear the caches and the state. */
+int tl_decode_upload(TlDecode *d, const float *P, void *stream);
+int tl_decode_reset(TlDecode *d, void *stream);
+/* forward_chunk of m host tokens at positions start..start+m-1 (weights
+ * copy 0); logits -> tl_decode_logits. */
+int tl_decode_chunk(TlDecode *d, const int *tok, int m, int start, void *stream);
+/* Prefill a prompt in chunks of <= mmax (positions 0..n-1), then take the
+ * greedy token: the state now holds position n and that token. */
+int tl_decode_prime(TlDecode *d, const int *prompt, int n, void *stream);
+/* One greedy token step from the device state (weights copy `copy`). */
+int tl_decode_greedy_step(TlDecode *d, int copy, void *stream);
+/* Capture the greedy step once per weight copy; tl_decode_graph_step
+ * replays the next copy's graph. */
+int tl_decode_graph_build(TlDecode *d, void *stream);
+int tl_decode_graph_step(TlDecode *d, void *stream);
+/* Synchronize and read the state: {next position, rows, last token}. */
+int tl_decode_state(TlDecode *d, int *state, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -14,6 +14,7 @@ REPO = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libtlgemm.so")
 HEADER = os.path.join(REPO, "include", "tlgemm.h")
 TRAIN_HEADER = os.path.join(REPO, "include", "tltrain.h")
+DECODE_HEADER = os.path.join(REPO, "include", "tldecode.h")
 
 _fp = ctypes.POINTER(ctypes.c_float)
 _ip = ctypes.POINTER(ctypes.c_int)
@@ -87,6 +88,11 @@ SIGNATURES = {
     "tlg_dev_xent": (_i, [_vp, _vp, _vp, _vp, ctypes.c_float, _i, _i, _vp]),
     "tlg_dev_gradnorm": (_i, [_vp, _sz, _vp, _vp]),
     "tlg_dev_adamw": (_i, [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp]),
+    # include/tldecode.h
+    "tlg_dev_dec_embed": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "tlg_dev_kv_store": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp]),
+    "tlg_dev_dec_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "tlg_dev_dec_argmax": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
 }
 
 
@@ -94,7 +100,7 @@ def header_symbols(path=None):
     """Function names declared in a C header (tlg_*/tl_* prototypes); by
     default the library's two public headers."""
     names = set()
-    for p in ([path] if path else [HEADER, TRAIN_HEADER]):
+    for p in ([path] if path else [HEADER, TRAIN_HEADER, DECODE_HEADER]):
         text = open(p).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names |= set(re.findall(r"\b(tlg?_[a-z0-9_]+)\s*\(", text))
@@ -314,6 +320,75 @@ class Train:
             pass
 
 
+class Decode:
+    """One TlDecode: device weights, KV ring cache and greedy state."""
+
+    def __init__(self, host, model, W, kv_f16, exact_exp, maxpos, mmax, pool):
+        if isinstance(model, dict):
+            model = TlModel(**{"rope_base": 10000.0, **model})
+        self.host, self.model = host, model
+        self.h = host.dll.tl_decode_new(ctypes.byref(model), W, kv_f16, exact_exp, maxpos, mmax, pool)
+        if not self.h:
+            raise TlgError("tl_decode_new failed: bad model shape or out of device memory")
+        self.np = host.dll.tl_decode_nparams(self.h)
+
+    def _ck(self, rc, what):
+        if rc != 0:
+            raise TlgError(f"{what} failed ({rc}): {load().dll.tlg_last_error().decode(errors='replace')}")
+        return 0
+
+    def upload(self, P, stream):
+        import numpy as np
+        P = np.ascontiguousarray(P, np.float32)
+        assert P.size == self.np
+        return self._ck(self.host.dll.tl_decode_upload(self.h, P.ctypes.data, stream), "tl_decode_upload")
+
+    def reset(self, stream):
+        return self._ck(self.host.dll.tl_decode_reset(self.h, stream), "tl_decode_reset")
+
+    def chunk(self, tok, start, stream):
+        """forward_chunk of host tokens; returns the logits [m][V] (host)."""
+        import numpy as np
+        tok = np.ascontiguousarray(tok, np.int32)
+        self._ck(self.host.dll.tl_decode_chunk(self.h, tok.ctypes.data, tok.size, start, stream), "tl_decode_chunk")
+        return self.logits(tok.size, stream)
+
+    def logits(self, m, stream):
+        import numpy as np
+        out = np.empty((m, self.model.V), np.float32)
+        L = load()
+        L.check(L.tlg_memcpy_d2h(out.ctypes.data, self.host.dll.tl_decode_logits(self.h), out.nbytes, stream), "d2h")
+        L.check(L.tlg_stream_sync(stream), "sync")
+        return out
+
+    def prime(self, prompt, stream):
+        import numpy as np
+        p = np.ascontiguousarray(prompt, np.int32)
+        return self._ck(self.host.dll.tl_decode_prime(self.h, p.ctypes.data, p.size, stream), "tl_decode_prime")
+
+    def greedy_step(self, stream, copy=0):
+        return self._ck(self.host.dll.tl_decode_greedy_step(self.h, copy, stream), "tl_decode_greedy_step")
+
+    def graph_build(self, stream):
+        return self._ck(self.host.dll.tl_decode_graph_build(self.h, stream), "tl_decode_graph_build")
+
+    def graph_step(self, stream):
+        return self._ck(self.host.dll.tl_decode_graph_step(self.h, stream), "tl_decode_graph_step")
+
+    def state(self, stream):
+        s = (ctypes.c_int * 3)()
+        self._ck(self.host.dll.tl_decode_state(self.h, s, stream), "tl_decode_state")
+        return list(s)
+
+    def __del__(self):
+        try:
+            if self.h:
+                self.host.dll.tl_decode_free(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
 class Plan:
     """A built TlPlan: buffers (name, floats, init) and calls as dicts."""
 
@@ -435,7 +510,32 @@ class Host:
             getattr(d, n).argtypes = [_vp, _vp]
             getattr(d, n).restype = ctypes.c_float
         d.tl_train_time_phases.argtypes = [_vp, ctypes.POINTER(ctypes.c_float), _vp]
+        # host/tl_decode.h
+        d.tl_decode_new.argtypes = [ctypes.POINTER(TlModel), _i, _i, _i, _i, _i, _i]
+        d.tl_decode_new.restype = _vp
+        d.tl_decode_free.argtypes = [_vp]
+        d.tl_decode_free.restype = None
+        d.tl_decode_nparams.argtypes = [_vp]
+        d.tl_decode_nparams.restype = _sz
+        for n in ("tl_decode_params",):
+            getattr(d, n).argtypes = [_vp, _i]
+            getattr(d, n).restype = _vp
+        d.tl_decode_logits.argtypes = [_vp]
+        d.tl_decode_logits.restype = _vp
+        for n in ("tl_decode_upload", "tl_decode_state"):
+            getattr(d, n).argtypes = [_vp, _vp, _vp]
+            getattr(d, n).restype = _i
+        for n in ("tl_decode_reset", "tl_decode_graph_build", "tl_decode_graph_step"):
+            getattr(d, n).argtypes = [_vp, _vp]
+            getattr(d, n).restype = _i
+        d.tl_decode_chunk.argtypes = [_vp, _vp, _i, _i, _vp]
+        d.tl_decode_prime.argtypes = [_vp, _vp, _i, _vp]
+        d.tl_decode_greedy_step.argtypes = [_vp, _i, _vp]
         self.dll = d
+
+    def decode(self, model, W, kv_f16=1, exact_exp=0, maxpos=4096, mmax=8, pool=1):
+        """Device-resident decoding (host/tl_decode.h)."""
+        return Decode(self, model, W, kv_f16, exact_exp, maxpos, mmax, pool)
 
     def train(self, model, B):
         """A device-resident training step (host/tl_train.h) for `model`
