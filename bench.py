@@ -445,6 +445,63 @@ def bench_full_step(lib, host, stream, name, steps, warmup=3):
             "loss_first": round(loss0, 4), "loss_after": round(loss1, 4)}
 
 
+DECODE_MODEL = dict(V=2048, D=384, L=8, H=12, KV=3, F=1024, T=256)
+
+
+def bench_decode_step(lib, host, stream, steps, pool=6, prompt_len=16, warmup=8):
+    """The whole decode step on the device (host/tl_decode.h): greedy
+    single-token steps of the m8 model through a 256-position f16 KV ring
+    with the reference's fast_expf (its decode defaults), token and position
+    kept in device memory, one captured graph per weight copy; `pool` copies
+    rotate so the 52.7 MB of weights stream from HBM.  Weights ~ N(0, 0.02^2)
+    drawn on the device."""
+    import numpy as np
+    maxpos = prompt_len + warmup + steps + 8
+    dec = host.decode(DECODE_MODEL, 256, kv_f16=1, exact_exp=0, maxpos=maxpos, mmax=8, pool=pool)
+    for c in range(pool):
+        check(lib.tlg_dev_fill_normal(dec.params(c), dec.np, 77, 0.02, stream), "fill P")
+    dec.reset(stream)
+    prompt = np.random.default_rng(5).integers(0, DECODE_MODEL["V"], prompt_len).astype(np.int32)
+    t0 = time.perf_counter()
+    dec.prime(prompt, stream)
+    prefill_ms = (time.perf_counter() - t0) * 1e3
+    dec.graph_build(stream)
+    for _ in range(warmup):
+        dec.graph_step(stream)
+    check(lib.tlg_stream_sync(stream), "sync")
+    ms, _ = time_steps(lib, lambda: dec.graph_step(stream), stream, steps)
+    state = dec.state(stream)
+    per = ms / steps
+    return {"model": DECODE_MODEL, "kv_cache": "f16 ring, 256 positions", "exp": "fast_expf",
+            "weights_pool": pool, "steps": steps, "ms_per_token": round(per, 4),
+            "tok_s": round(1e3 / per, 1), "prefill_ms_host_timed": round(prefill_ms, 3),
+            "final_position": state[0], "launches_per_token": 8 * 13 + 4}
+
+
+def cpu_decode_step(threads, steps=40):
+    """The oracle's forward_chunk restatement (kind "port": the reference's
+    decode state is not compiled from its lines) at M = 1 on host cores."""
+    import numpy as np
+    import oracle
+    st = oracle.StepFns("oracle")
+    st.dll.orc_set_threads(threads)
+    m = oracle.model(**DECODE_MODEL)
+    P = st.init_params(m, 1)
+    dec = oracle.Decoder(m, P, 256, kvdt=1, exact=0, maxpos=steps + 32)
+    prompt = np.random.default_rng(5).integers(0, m.V, 16).astype(np.int32)
+    lg = dec.chunk(prompt, 0)
+    tok, pos = int(np.argmax(lg[-1])), 16
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        lg = dec.chunk(np.array([tok], np.int32), pos)
+        tok, pos = int(np.argmax(lg[-1])), pos + 1
+    dt = time.perf_counter() - t0
+    return {"value": round(steps / dt, 1), "unit": "decode tokens/s (whole step, M = 1)", "cores": threads,
+            "kind": "port", "ms_per_token": round(dt / steps * 1e3, 3),
+            "sample": f"{steps} greedy single-token steps of the m8 decode model after a 16-token prefill, "
+                      f"f16 ring cache, fast_expf; {dt:.2f} s timed"}
+
+
 def cpu_full_step(name, threads, steps=2):
     """The reference's own forward + memset(G) + backward + gradnorm + AdamW
     (tinylm.c:2627-2633, compiled from its lines into oracle/_ref) on host
@@ -502,6 +559,8 @@ def main():
     ap.add_argument("--no-probes", action="store_true", help="skip the copy / MFMA peak probes")
     ap.add_argument("--no-autotune", action="store_true",
                     help="keep the library's automatic tile policy instead of timing candidates per launch")
+    ap.add_argument("--decode-full-steps", type=int, default=512,
+                    help="timed greedy decode steps of the whole device decode step; 0 skips")
     ap.add_argument("--full-steps", type=int, default=30,
                     help="timed whole training steps (forward + backward + AdamW on the device); 0 skips")
     args = ap.parse_args()
@@ -598,6 +657,10 @@ def main():
         full = bench_full_step(lib, host, stream, args.config, args.full_steps)
         full["gemm_set_share"] = round(ms_step / full["ms_per_step"], 4)
         log(f"[full step] {full}")
+    dec_full = None
+    if args.decode_full_steps > 0:
+        dec_full = bench_decode_step(lib, host, stream, args.decode_full_steps)
+        log(f"[decode step] {dec_full}")
     peaks = None if args.no_probes else probes(lib, stream)
     if peaks:
         log(f"[probes] {peaks}")
@@ -611,6 +674,9 @@ def main():
         if args.full_steps > 0:
             cpu["train_step"] = cpu_full_step(args.config, threads)
             log(f"[cpu] whole step {cpu['train_step']}")
+        if args.decode_full_steps > 0:
+            cpu["decode_step"] = cpu_decode_step(threads)
+            log(f"[cpu] decode step {cpu['decode_step']}")
         if args.decode_steps > 0:
             cpu["decode"] = {str(M): cpu_decode_baseline(host, M, 200 if M == 1 else 50, threads) for M in (1, 8)}
             log(f"[cpu] decode {cpu['decode']}")
@@ -659,6 +725,7 @@ def main():
         "decode": {str(k): v for k, v in decode.items()},
         "moe": moe,
         "train_step": full,
+        "decode_step": dec_full,
         "achievable": peaks,
         "cpu_baseline": cpu,
     }

@@ -346,6 +346,10 @@ class Decode:
     def reset(self, stream):
         return self._ck(self.host.dll.tl_decode_reset(self.h, stream), "tl_decode_reset")
 
+    def params(self, copy=0):
+        """Device address of weight copy `copy`."""
+        return self.host.dll.tl_decode_params(self.h, copy)
+
     def chunk(self, tok, start, stream):
         """forward_chunk of host tokens; returns the logits [m][V] (host)."""
         import numpy as np
