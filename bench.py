@@ -448,7 +448,7 @@ def bench_full_step(lib, host, stream, name, steps, warmup=3):
 DECODE_MODEL = dict(V=2048, D=384, L=8, H=12, KV=3, F=1024, T=256)
 
 
-def bench_decode_step(lib, host, stream, steps, pool=6, prompt_len=16, warmup=8):
+def bench_decode_step(lib, host, stream, steps, pool=6, prompt_len=16, warmup=8, fused=1):
     """The whole decode step on the device (host/tl_decode.h): greedy
     single-token steps of the m8 model through a 256-position f16 KV ring
     with the reference's fast_expf (its decode defaults), token and position
@@ -458,6 +458,7 @@ def bench_decode_step(lib, host, stream, steps, pool=6, prompt_len=16, warmup=8)
     import numpy as np
     maxpos = prompt_len + warmup + steps + 8
     dec = host.decode(DECODE_MODEL, 256, kv_f16=1, exact_exp=0, maxpos=maxpos, mmax=8, pool=pool)
+    dec.set_fused(fused)
     for c in range(pool):
         check(lib.tlg_dev_fill_normal(dec.params(c), dec.np, 77, 0.02, stream), "fill P")
     dec.reset(stream)
@@ -475,7 +476,8 @@ def bench_decode_step(lib, host, stream, steps, pool=6, prompt_len=16, warmup=8)
     return {"model": DECODE_MODEL, "kv_cache": "f16 ring, 256 positions", "exp": "fast_expf",
             "weights_pool": pool, "steps": steps, "ms_per_token": round(per, 4),
             "tok_s": round(1e3 / per, 1), "prefill_ms_host_timed": round(prefill_ms, 3),
-            "final_position": state[0], "launches_per_token": 8 * 13 + 4}
+            "final_position": state[0], "fused": bool(fused),
+            "launches_per_token": 1 + 8 * 5 + 2 if fused else 1 + 8 * 13 + 3}
 
 
 def cpu_decode_step(threads, steps=40):
@@ -561,6 +563,8 @@ def main():
                     help="keep the library's automatic tile policy instead of timing candidates per launch")
     ap.add_argument("--decode-full-steps", type=int, default=512,
                     help="timed greedy decode steps of the whole device decode step; 0 skips")
+    ap.add_argument("--decode-mode", default="both", choices=("both", "fused", "unfused"),
+                    help="decode step: fused launches, glue as separate launches, or both (fused first)")
     ap.add_argument("--full-steps", type=int, default=30,
                     help="timed whole training steps (forward + backward + AdamW on the device); 0 skips")
     args = ap.parse_args()
@@ -659,8 +663,14 @@ def main():
         log(f"[full step] {full}")
     dec_full = None
     if args.decode_full_steps > 0:
-        dec_full = bench_decode_step(lib, host, stream, args.decode_full_steps)
+        if args.decode_mode == "unfused":
+            dec_full = bench_decode_step(lib, host, stream, args.decode_full_steps, fused=0)
+        else:
+            dec_full = bench_decode_step(lib, host, stream, args.decode_full_steps)
         log(f"[decode step] {dec_full}")
+        if args.decode_mode == "both":
+            dec_full["unfused"] = bench_decode_step(lib, host, stream, min(args.decode_full_steps, 128), fused=0)
+            log(f"[decode step, unfused] {dec_full['unfused']}")
     peaks = None if args.no_probes else probes(lib, stream)
     if peaks:
         log(f"[probes] {peaks}")

@@ -38,6 +38,47 @@ int tlg_dev_kv_store(const float *k, const float *v, const int *pos, int m, int 
 int tlg_dev_dec_attn(const float *q, const void *Kc, const void *Vc, const int *pos, float *ctx, int m, int H,
                      int KV, int hd, int W, int win, int f16, int exact_exp, void *stream);
 
+/* ---- fused decode launches (no reference counterpart: the reference runs
+ * the glue between its GEMVs as separate loops; these fold it into the
+ * GEMV and attention launches so a token step needs 5 launches per layer).
+ *
+ * One GEMV of a decode run: mm (op 0) or mm_bt (op 1) with the reference's
+ * argument labels (M <= 8), whose activation rows A [M][R] (R = K for mm, N
+ * for mm_bt) pass through a prologue as they are read:
+ *   pro 0  A as it is
+ *   pro 1  rmsnorm_fwd (tinylm.c:540-548): A[m][r] * s_m * gain[r] with
+ *          s_m = 1 / sqrt(sum_r A[m][r]^2 / R + 1e-5)
+ *   pro 2  SwiGLU (:786, :3821-3823): silu(A[m][r]) * A2[m][r], silu(z) =
+ *          z / (1 + e^-z)
+ * and beta = 1 adds the result into C (the residual adds x += tmp of
+ * forward_chunk, :3818, :3824), beta = 0 sets it. */
+typedef struct {
+    int op;                  /* 0 mm, 1 mm_bt */
+    int beta;                /* 1 C += result, 0 C = result */
+    float *C;
+    int M, K, N;
+    const float *A, *B;      /* X and W (mm), dY and W (mm_bt) */
+    int pro;                 /* 0 none, 1 rmsnorm with gain, 2 SwiGLU with A2 */
+    const float *gain;       /* pro 1: [R] */
+    const float *A2;         /* pro 2: [M][R] */
+} TlgDecGemv;
+
+/* Up to 8 independent GEMVs (none reads what another writes) in one launch. */
+int tlg_dev_dec_gemv(const TlgDecGemv *calls, int n, void *stream);
+
+/* RoPE, the ring store and the attention of forward_chunk (:3766-3815) in one
+ * launch, for the m new rows at positions pos[j]: q [m][H*hd] and k [m][KD]
+ * arrive before RoPE (rope_apply :645-651 with the tables cs / sn [maxpos][hd/2]
+ * of rope_init :605-618, a position outside them gives NaN), v [m][KD];
+ * every row's K and V go to slot pos % W (rounded to f16 for an f16 cache),
+ * and row j attends as tlg_dev_dec_attn does, over the ring as the
+ * reference's hoisted stores leave it (a slot written by this chunk holds
+ * the new row).  q, k and v are left as they are.  The m positions must be
+ * consecutive (pos[j] = pos[0] + j), as forward_chunk's are. */
+int tlg_dev_dec_rope_attn(const float *q, const float *k, const float *v, const int *pos, const float *cs,
+                          const float *sn, int maxpos, void *Kc, void *Vc, float *ctx, int m, int H, int KV, int hd,
+                          int W, int win, int f16, int exact_exp, void *stream);
+
 /* Greedy decoding, argmax_v (tinylm.c:3844: the first maximum) of the last
  * of m rows of logits [m][V]; then state[0] += m, state[1] = 1,
  * state[2] = tok[0] = the token, so the next step decodes it. */

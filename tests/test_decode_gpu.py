@@ -47,15 +47,128 @@ def params(kw, seed):
 SMALL = dict(V=128, D=96, L=2, H=3, KV=1, F=64, T=32)
 
 
+def _dev(a):
+    return _t().from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _silu(z):
+    return z / (1.0 + np.exp(-z))
+
+
+def test_dec_gemv_prologues(lib):
+    """tlg_dev_dec_gemv: RMSNorm and SwiGLU prologues, set and residual-add
+    epilogues, mm and mm_bt, several problems per launch -- against the
+    oracle's rmsnorm_fwd + mm / mm_bt and float64."""
+    import tlgemm
+    t = _t()
+    st = StepFns("oracle")
+    r = np.random.default_rng(11)
+    D, F, V = 96, 136, 200
+    for M in (1, 3, 8):
+        x = r.standard_normal((M, D)).astype(np.float32)
+        gain = (1.0 + 0.1 * r.standard_normal(D)).astype(np.float32)
+        wq = (0.02 * r.standard_normal((D, D))).astype(np.float32)
+        wk = (0.02 * r.standard_normal((D, 32))).astype(np.float32)
+        g = r.standard_normal((M, F)).astype(np.float32)
+        u = r.standard_normal((M, F)).astype(np.float32)
+        w2 = (0.02 * r.standard_normal((F, D))).astype(np.float32)
+        emb = (0.02 * r.standard_normal((V, D))).astype(np.float32)
+        res = r.standard_normal((M, D)).astype(np.float32)
+        dx, dgain, dwq, dwk, dgg, du, dw2 = (_dev(a) for a in (x, gain, wq, wk, g, u, w2))
+        demb, dres = _dev(emb), _dev(res)
+        q = t.full((M, D), float("nan"), device="cuda")
+        k = t.full((M, 32), float("nan"), device="cuda")
+        lg = t.full((M, V), float("nan"), device="cuda")
+        C = tlgemm.TlgDecGemv
+        calls = (C * 3)(C(0, 0, q.data_ptr(), M, D, D, dx.data_ptr(), dwq.data_ptr(), 1, dgain.data_ptr(), None),
+                        C(0, 0, k.data_ptr(), M, D, 32, dx.data_ptr(), dwk.data_ptr(), 1, dgain.data_ptr(), None),
+                        C(1, 0, lg.data_ptr(), M, V, D, dx.data_ptr(), demb.data_ptr(), 1, dgain.data_ptr(), None))
+        lib.check(lib.tlg_dev_dec_gemv(calls, 3, stream()), "dec_gemv")
+        # res += (silu(u) * g) @ w2: SwiGLU prologue (A = u, A2 = g), residual add
+        one = (C * 1)(C(0, 1, dres.data_ptr(), M, F, D, du.data_ptr(), dw2.data_ptr(), 2, None, dgg.data_ptr()))
+        lib.check(lib.tlg_dev_dec_gemv(one, 1, stream()), "dec_gemv swiglu")
+        t.cuda.synchronize()
+        xn, _ = st.rmsnorm_fwd(x, gain)
+        orc_q = xn.astype(np.float64) @ wq
+        assert normwise_rel(q.cpu().numpy(), orc_q) <= TOL, M
+        assert normwise_rel(k.cpu().numpy(), xn.astype(np.float64) @ wk) <= TOL, M
+        assert normwise_rel(lg.cpu().numpy(), xn.astype(np.float64) @ emb.T.astype(np.float64)) <= TOL, M
+        act = _silu(u.astype(np.float64)) * g.astype(np.float64)
+        want = res.astype(np.float64) + act @ w2.astype(np.float64)
+        got = dres.cpu().numpy()
+        assert normwise_rel(got - res, want - res) <= TOL, M
+        print("dec_gemv", M, "ok", flush=True)
+
+
+def test_dec_gemv_rejects_bad_calls(lib):
+    import tlgemm
+    C = tlgemm.TlgDecGemv
+    x = _t().zeros(16, device="cuda")
+    bad = [C(0, 0, x.data_ptr(), 9, 4, 4, x.data_ptr(), x.data_ptr(), 0, None, None),     # M > 8
+           C(2, 0, x.data_ptr(), 1, 4, 4, x.data_ptr(), x.data_ptr(), 0, None, None),     # op
+           C(0, 0, x.data_ptr(), 1, 4, 4, x.data_ptr(), x.data_ptr(), 1, None, None),     # RMS without gain
+           C(0, 0, x.data_ptr(), 1, 4, 4, x.data_ptr(), x.data_ptr(), 2, None, None)]     # SwiGLU without A2
+    for c in bad:
+        assert lib.tlg_dev_dec_gemv((C * 1)(c), 1, stream()) != 0
+
+
+@pytest.mark.parametrize("f16,W,p0,m,win", [(1, 32, 5, 1, 0), (0, 32, 29, 8, 0), (1, 32, 70, 8, 0),
+                                             (0, 32, 100, 3, 12), (1, 256, 250, 1, 0), (0, 16, 16, 8, 0)])
+def test_dec_rope_attn_matches_separate_launches(lib, f16, W, p0, m, win):
+    """The fused RoPE + ring store + attention launch equals the separate
+    launches (rope, kv_store of every row, then attention): the same ctx and
+    the same cache, including chunks whose new slots alias window positions
+    of earlier rows (the ring wraps inside the chunk)."""
+    t = _t()
+    r = np.random.default_rng(p0 * 7 + m)
+    H, KV, hd, maxpos = 6, 2, 32, 512
+    D, KD = H * hd, KV * hd
+    st = StepFns("oracle")
+    cs, sn = st.rope_table(maxpos, hd)
+    q = r.standard_normal((m, D)).astype(np.float32)
+    k = r.standard_normal((m, KD)).astype(np.float32)
+    v = r.standard_normal((m, KD)).astype(np.float32)
+    cache_dt = np.float16 if f16 else np.float32
+    K0 = r.standard_normal((W, KD)).astype(cache_dt)
+    V0 = r.standard_normal((W, KD)).astype(cache_dt)
+    pos = _dev(np.arange(p0, p0 + m, dtype=np.int32))
+    dcs, dsn = _dev(cs), _dev(sn)
+    dq, dk, dv = _dev(q), _dev(k), _dev(v)
+    Ka, Va, Kb, Vb = _dev(K0), _dev(V0), _dev(K0), _dev(V0)
+    ca = t.full((m, D), float("nan"), device="cuda")
+    cb = t.full((m, D), float("nan"), device="cuda")
+    lib.check(lib.tlg_dev_dec_rope_attn(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), pos.data_ptr(), dcs.data_ptr(),
+                                        dsn.data_ptr(), maxpos, Ka.data_ptr(), Va.data_ptr(), ca.data_ptr(), m, H, KV,
+                                        hd, W, win, f16, 0, stream()), "rope_attn")
+    q2, k2 = dq.clone(), dk.clone()
+    lib.check(lib.tlg_dev_rope(q2.data_ptr(), pos.data_ptr(), 1, m, H, hd, dcs.data_ptr(), dsn.data_ptr(), maxpos, 0,
+                               stream()), "rope q")
+    lib.check(lib.tlg_dev_rope(k2.data_ptr(), pos.data_ptr(), 1, m, KV, hd, dcs.data_ptr(), dsn.data_ptr(), maxpos, 0,
+                               stream()), "rope k")
+    lib.check(lib.tlg_dev_kv_store(k2.data_ptr(), dv.data_ptr(), pos.data_ptr(), m, KD, W, f16, Kb.data_ptr(),
+                                   Vb.data_ptr(), stream()), "kv_store")
+    lib.check(lib.tlg_dev_dec_attn(q2.data_ptr(), Kb.data_ptr(), Vb.data_ptr(), pos.data_ptr(), cb.data_ptr(), m, H, KV,
+                                   hd, W, win, f16, 0, stream()), "attn")
+    t.cuda.synchronize()
+    assert t.equal(dq, _dev(q)) and t.equal(dk, _dev(k)), "inputs must be left as they are"
+    tolc = 2e-3 if f16 else 1e-6        # one f16 ulp where RoPE's fp32 rounding differs
+    ka, kb = Ka.cpu().numpy().astype(np.float64), Kb.cpu().numpy().astype(np.float64)
+    assert np.abs(ka - kb).max() <= tolc * np.abs(kb).max(), "K cache"
+    assert t.equal(Va, Vb), "V cache"
+    assert normwise_rel(ca.cpu().numpy(), cb.cpu().numpy()) <= (TOL_F16 if f16 else 1e-5)
+
+
+@pytest.mark.parametrize("fused", [1, 0], ids=["fused", "unfused"])
 @pytest.mark.parametrize("kvdt,exact", [(1, 0), (0, 1), (1, 1), (0, 0)], ids=["f16-fast", "f32-exact", "f16-exact",
                                                                           "f32-fast"])
-def test_chunks_match_oracle(lib, kvdt, exact):
+def test_chunks_match_oracle(lib, kvdt, exact, fused):
     """Chunks of 1..8 rows over 90 positions of a 32-slot ring (wraps twice)."""
     import tlgemm
     m, P = params(SMALL, 3)
     W = 32
-    print("decode chunks", kvdt, exact, flush=True)
+    print("decode chunks", kvdt, exact, fused, flush=True)
     dec = tlgemm.host().decode(SMALL, W, kv_f16=kvdt, exact_exp=exact, maxpos=256, mmax=8)
+    dec.set_fused(fused)
     dec.upload(P, stream())
     orc = Decoder(m, P, W, kvdt=kvdt, exact=exact, maxpos=256)
     toks = np.random.default_rng(4).integers(0, m.V, 90).astype(np.int32)
@@ -73,11 +186,13 @@ def test_chunks_match_oracle(lib, kvdt, exact):
     print("worst chunk", f"{worst:.2e}", flush=True)
 
 
-def test_sliding_window_chunks(lib):
+@pytest.mark.parametrize("fused", [1, 0], ids=["fused", "unfused"])
+def test_sliding_window_chunks(lib, fused):
     import tlgemm
     kw = dict(SMALL, win=12, full_every=2)
     m, P = params(kw, 5)
     dec = tlgemm.host().decode(kw, 32, kv_f16=1, exact_exp=0, maxpos=128, mmax=8)
+    dec.set_fused(fused)
     dec.upload(P, stream())
     orc = Decoder(m, P, 32, kvdt=1, exact=0, maxpos=128)
     toks = np.random.default_rng(6).integers(0, m.V, 60).astype(np.int32)
@@ -111,8 +226,9 @@ def same_stream(got, want, rows, rel):
     return len(got)
 
 
-@pytest.mark.parametrize("shape,kvdt", [("small", 0), ("small", 1), ("m8", 1)])
-def test_greedy_tokens_match_oracle(lib, shape, kvdt):
+@pytest.mark.parametrize("shape,kvdt,fused", [("small", 0, 1), ("small", 1, 1), ("m8", 1, 1), ("small", 0, 0),
+                                               ("m8", 1, 0)])
+def test_greedy_tokens_match_oracle(lib, shape, kvdt, fused):
     """Prefill a prompt, then greedy steps on the device only (argmax ->
     next token and position in device memory), eager and replayed from a
     graph per weight copy; the token stream equals the oracle's."""
@@ -128,6 +244,7 @@ def test_greedy_tokens_match_oracle(lib, shape, kvdt):
     s = lib.tlg_stream_create()
     for mode in ("eager", "graph"):
         dec = tlgemm.host().decode(kw, W, kv_f16=kvdt, exact_exp=0, maxpos=512, mmax=8, pool=2)
+        dec.set_fused(fused)
         dec.upload(P, s)
         dec.prime(prompt, s)
         if mode == "graph":

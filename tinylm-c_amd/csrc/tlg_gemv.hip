@@ -26,6 +26,7 @@
 // on the same input; w1, w3) run as one launch: a problem table in the
 // kernel arguments, workgroups dealt to problems in order.
 #include "tlg_internal.h"
+#include "../../include/tldecode.h"
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -44,11 +45,18 @@
 __host__ __device__ constexpr int nn_cols(int mb) { return mb <= 2 ? 8 : 16; }
 
 struct GvSeg { const float *A, *B; int R, lda, ldb; };
+// Activation prologues (decode: the glue before a GEMV, applied while the
+// rows are staged): GV_PRO_RMS stages x * s * gain with s = 1 / sqrt(sum(x^2)
+// / R + 1e-5) of the whole row (rmsnorm_fwd, tinylm.c:540-548); GV_PRO_SWIGLU
+// stages silu(a) * a2 with silu(z) = z / (1 + e^-z) (:786, :1005-1006).
+enum { GV_PRO_NONE = 0, GV_PRO_RMS = 1, GV_PRO_SWIGLU = 2 };
 struct GvProb {
     float *C;
     int kind;                    // TLG_NN or TLG_NT
     int M, No, ldc, beta, nseg;
     int blocks;
+    int pro;                     // GV_PRO_* (single-segment problems only)
+    const float *gain, *A2;      // RMS gain [R]; SwiGLU second operand (layout of A)
     GvSeg seg[GV_MAXSEG];
 };
 struct GvArgs {
@@ -56,12 +64,38 @@ struct GvArgs {
     GvProb p[GV_MAXPROB];
 };
 
-// Stage activation rows A[m][r0 .. r0+kc) (m < M) into LDS as As[m*kc + r-r0].
-__device__ __forceinline__ void stage_rows(float *As, const float *__restrict__ A, int lda, int M, int r0, int kc)
+// Stage activation rows A[m][r0 .. r0+kc) (m < M) into LDS as As[m*kc + r-r0],
+// through the problem's prologue: SwiGLU completes here; RMSNorm stages the
+// raw rows and its gain (Gs) in the same pass -- one global round trip --
+// and rms_finish applies the scales.
+__device__ __forceinline__ void stage_rows(float *As, float *Gs, const GvProb &P, const GvSeg &g, int r0, int kc)
 {
-    for (int e = threadIdx.x; e < M * kc; e += blockDim.x) {
+    for (int e = threadIdx.x; e < P.M * kc; e += blockDim.x) {
         const int m = e / kc, r = e - m * kc;
-        As[e] = A[(size_t)m * lda + r0 + r];
+        const size_t i = (size_t)m * g.lda + r0 + r;
+        float a = g.A[i];
+        if (P.pro == GV_PRO_SWIGLU) a = a / (1.0f + expf(-a)) * P.A2[i];
+        else if (P.pro == GV_PRO_RMS && m == 0) Gs[r] = P.gain[r0 + r];
+        As[e] = a;
+    }
+}
+
+// RMSNorm of the staged rows (the whole row is in LDS: M * R <= GV_ACHUNK):
+// s_m = 1 / sqrt(sum_k x^2 / R + 1e-5), one wave per row (M <= GV_WAVES),
+// then x * s_m * gain in place.
+__device__ __forceinline__ void rms_finish(float *As, const float *Gs, float *rsc, int M, int R)
+{
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (w < M) {
+        float ms = 0.f;
+        for (int k = lane; k < R; k += 64) ms = fmaf(As[w * R + k], As[w * R + k], ms);
+        for (int o = 32; o > 0; o >>= 1) ms += __shfl_xor(ms, o);
+        if (lane == 0) rsc[w] = 1.0f / sqrtf(ms / (float)R + 1e-5f);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < M * R; e += blockDim.x) {
+        const int m = e / R, r = e - m * R;
+        As[e] = As[e] * rsc[m] * Gs[r];
     }
 }
 
@@ -72,7 +106,7 @@ __device__ __forceinline__ void stage_rows(float *As, const float *__restrict__ 
 // slots move through W together.  The partial sums of a column meet in fixed
 // order (shuffles within a wave, then LDS across waves).
 template <int MB, int COLS>
-__device__ __forceinline__ void gemv_nn(const GvProb &P, int blk, float *As, float *red)
+__device__ __forceinline__ void gemv_nn(const GvProb &P, int blk, float *As, float *red, float *rsc, float *Gs)
 {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     constexpr int SUBS = 64 / COLS, SLOTS = GV_WAVES * SUBS;
@@ -103,8 +137,12 @@ __device__ __forceinline__ void gemv_nn(const GvProb &P, int blk, float *As, flo
             };
             load(b, q);
             __syncthreads();                     // previous chunk fully read
-            stage_rows(As, g.A, g.lda, P.M, r0, kn);
+            stage_rows(As, Gs, P, g, r0, kn);
             __syncthreads();
+            if (P.pro == GV_PRO_RMS) {
+                rms_finish(As, Gs, rsc, P.M, kn);
+                __syncthreads();
+            }
             for (int k = q; k < kn; k += SLOTS * NN_U) {
                 if (k + SLOTS * NN_U < kn) load(nb, k + SLOTS * NN_U);
 #pragma unroll
@@ -145,7 +183,7 @@ __device__ __forceinline__ void gemv_nn(const GvProb &P, int blk, float *As, flo
 // stride the reduction index n (coalesced), and each of the 2*M dot
 // products ends in a butterfly reduction over the 64 lanes.
 template <int MB>
-__device__ __forceinline__ void gemv_nt(const GvProb &P, int blk, float *As)
+__device__ __forceinline__ void gemv_nt(const GvProb &P, int blk, float *As, float *rsc, float *Gs)
 {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int k0 = (blk * GV_WAVES + w) * GV_NT_ROWS;
@@ -176,8 +214,12 @@ __device__ __forceinline__ void gemv_nt(const GvProb &P, int blk, float *As)
             };
             load(b, lane);
             __syncthreads();
-            stage_rows(As, g.A, g.lda, P.M, r0, kn);
+            stage_rows(As, Gs, P, g, r0, kn);
             __syncthreads();
+            if (P.pro == GV_PRO_RMS) {
+                rms_finish(As, Gs, rsc, P.M, kn);
+                __syncthreads();
+            }
             for (int n = lane; n < kn; n += 64 * NT_U) {
                 if (n + 64 * NT_U < kn) load(nb, n + 64 * NT_U);
 #pragma unroll
@@ -228,12 +270,14 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv(GvArgs g)
 {
     __shared__ float As[GV_ACHUNK];
     __shared__ float red[GV_WAVES * MB * COLS];
+    __shared__ float rsc[GV_WAVES];
+    __shared__ float Gs[GV_ACHUNK];
     int b = blockIdx.x, p = 0;
     while (p < g.nprob && b >= g.p[p].blocks) { b -= g.p[p].blocks; p++; }
     if (p >= g.nprob) return;
     const GvProb &P = g.p[p];
-    if (P.kind == TLG_NN) gemv_nn<MB, COLS>(P, b, As, red);
-    else gemv_nt<MB>(P, b, As);
+    if (P.kind == TLG_NN) gemv_nn<MB, COLS>(P, b, As, red, rsc, Gs);
+    else gemv_nt<MB>(P, b, As, rsc, Gs);
 }
 
 // ---------------------------------------------------------------- host --
@@ -340,6 +384,48 @@ int tlg_gemv_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
                 return tlg_fail(TLG_EINVAL, "GEMV group: call %d: empty or NULL operand", i);
         if (!P.C || P.No <= 0) return tlg_fail(TLG_EINVAL, "GEMV group: call %d: empty output", i);
         if (P.M > mmax) mmax = P.M;
+    }
+    a.nprob = n;
+    return launch(a, rows_bucket(mmax), st);
+}
+
+// A decode run with the glue folded in (include/tldecode.h): the calls'
+// prologues (RMSNorm, SwiGLU) apply while the activation rows are staged,
+// and beta = 1 adds the result into C (mm's residual add).
+extern "C" int tlg_dev_dec_gemv(const TlgDecGemv *calls, int n, void *stream)
+{
+    int rc = tlg_ensure_init();
+    if (rc) return rc;
+    if (!calls || n <= 0 || n > GV_MAXPROB) return tlg_fail(TLG_EINVAL, "dec_gemv: 1 to %d calls", GV_MAXPROB);
+    hipStream_t st = (hipStream_t)stream;
+    rc = tlg_group_flush_launch(st);             // pending split reductions land first
+    if (rc) return rc;
+    GvArgs a;
+    memset(&a, 0, sizeof a);
+    int mmax = 1;
+    for (int i = 0; i < n; i++) {
+        const TlgDecGemv &c = calls[i];
+        GvProb &P = a.p[i];
+        if ((c.op != 0 && c.op != 1) || c.M < 1 || c.M > 8 || c.K <= 0 || c.N <= 0 || !c.A || !c.B || !c.C ||
+            c.pro < GV_PRO_NONE || c.pro > GV_PRO_SWIGLU || (c.pro == GV_PRO_RMS && !c.gain) ||
+            (c.pro == GV_PRO_SWIGLU && !c.A2) || (c.pro == GV_PRO_RMS && c.M * (c.op == 0 ? c.K : c.N) > GV_ACHUNK))
+            return tlg_fail(TLG_EINVAL, "dec_gemv: call %d: op=%d M=%d K=%d N=%d pro=%d", i, c.op, c.M, c.K, c.N,
+                            c.pro);
+        P.C = c.C;
+        P.M = c.M;
+        P.nseg = 1;
+        P.beta = c.beta ? 1 : 0;
+        P.pro = c.pro;
+        P.gain = c.gain;
+        P.A2 = c.A2;
+        if (c.op == 0) {
+            P.kind = TLG_NN; P.No = c.N; P.ldc = c.N;
+            P.seg[0] = GvSeg{c.A, c.B, c.K, c.K, c.N};
+        } else {
+            P.kind = TLG_NT; P.No = c.K; P.ldc = c.K;
+            P.seg[0] = GvSeg{c.A, c.B, c.N, c.N, c.N};
+        }
+        if (c.M > mmax) mmax = c.M;
     }
     a.nprob = n;
     return launch(a, rows_bucket(mmax), st);

@@ -22,6 +22,7 @@ struct TlDecode {
     int *pos, *tok, *state;
     void *graph[TLD_MAXPOOL];
     int next_graph;
+    int unfused;                 /* 1: the glue as separate launches (tl_decode_set_fused) */
 };
 
 /* map_weights (tinylm.c:361-393), dense FFN, no QK-norm */
@@ -56,7 +57,7 @@ TlDecode *tl_decode_new(const TlModel *m, int W, int kv_f16, int exact_exp, int 
 {
     if (!m || m->n_exp != 0 || m->D <= 0 || m->H <= 0 || m->KV <= 0 || m->D % m->H || m->H % m->KV ||
         m->D / m->H != 32 || m->D % 4 || m->F % 4 || m->V % 4 || m->L <= 0 || W <= 0 || W > 4096 ||
-        maxpos <= 0 || mmax <= 0 || mmax > W || pool <= 0 || pool > TLD_MAXPOOL)
+        maxpos <= 0 || mmax <= 0 || mmax > 8 || mmax > W || pool <= 0 || pool > TLD_MAXPOOL)
         return NULL;
     TlDecode *d = calloc(1, sizeof *d);
     if (!d) return NULL;
@@ -166,9 +167,51 @@ static TlgGemmCall MMc(float *Y, const float *X, const float *Wt, int M, int K, 
 #define GROUP(st, ...) do { TlgGemmCall cs_[] = {__VA_ARGS__}; \
         CK(tlg_dev_gemm_group(cs_, (int)(sizeof cs_ / sizeof cs_[0]), st)); } while (0)
 
+static TlgDecGemv DG(int op, int beta, float *C, int M, int K, int N, const float *A, const float *Bw, int pro,
+                     const float *gain, const float *A2)
+{
+    TlgDecGemv c;
+    c.op = op; c.beta = beta; c.C = C; c.M = M; c.K = K; c.N = N; c.A = A; c.B = Bw;
+    c.pro = pro; c.gain = gain; c.A2 = A2;
+    return c;
+}
+
+#define DGEMV(st, ...) do { TlgDecGemv cs_[] = {__VA_ARGS__}; \
+        CK(tlg_dev_dec_gemv(cs_, (int)(sizeof cs_ / sizeof cs_[0]), st)); } while (0)
+
+/* The fused form: per layer 5 launches --
+ *   [RMSNorm -> Q, K, V]  [RoPE, ring store, attention]  [O, x += ]
+ *   [RMSNorm -> W1, W3]   [SwiGLU -> W2, x += ]
+ * then [final RMSNorm -> logits]. */
+static int run_chunk_fused(TlDecode *d, int m, int use_state, int start, int copy, void *st)
+{
+    const TlModel *md = &d->m;
+    const int D = md->D, H = md->H, KV = md->KV, KD = d->KD, F = md->F, V = md->V, hd = d->hd;
+    const float *P = d->P[copy];
+    DMap w;
+    dmap(d, 0, &w);
+    CK(tlg_dev_dec_embed(d->x, d->pos, P + w.emb, d->tok, use_state ? d->state : NULL, start, m, D, V, st));
+    for (int l = 0; l < md->L; l++) {
+        dmap(d, l, &w);
+        DGEMV(st, DG(0, 0, d->q, m, D, D, d->x, P + w.wq, 1, P + w.an1, NULL),
+              DG(0, 0, d->k, m, D, KD, d->x, P + w.wk, 1, P + w.an1, NULL),
+              DG(0, 0, d->v, m, D, KD, d->x, P + w.wv, 1, P + w.an1, NULL));
+        CK(tlg_dev_dec_rope_attn(d->q, d->k, d->v, d->pos, d->rcos, d->rsin, d->maxpos, d->Kc[l], d->Vc[l], d->ctx, m,
+                                 H, KV, hd, d->W, dwin(md, l), d->f16, d->exact, st));
+        DGEMV(st, DG(0, 1, d->x, m, D, D, d->ctx, P + w.wo, 0, NULL, NULL));
+        DGEMV(st, DG(0, 0, d->g, m, D, F, d->x, P + w.w1, 1, P + w.an2, NULL),
+              DG(0, 0, d->u, m, D, F, d->x, P + w.w3, 1, P + w.an2, NULL));
+        DGEMV(st, DG(0, 1, d->x, m, F, D, d->g, P + w.w2, 2, NULL, d->u));
+    }
+    dmap(d, 0, &w);
+    DGEMV(st, DG(1, 0, d->logits, m, V, D, d->x, P + w.emb, 1, P + w.nf, NULL));   /* memset + mm_bt */
+    return 0;
+}
+
 /* m rows of d->tok at positions state[0] + j (use_state) or start + j */
 static int run_chunk(TlDecode *d, int m, int use_state, int start, int copy, void *st)
 {
+    if (!d->unfused) return run_chunk_fused(d, m, use_state, start, copy, st);
     const TlModel *md = &d->m;
     const int D = md->D, H = md->H, KV = md->KV, KD = d->KD, F = md->F, V = md->V, hd = d->hd;
     const float *P = d->P[copy];
@@ -262,5 +305,14 @@ int tl_decode_state(TlDecode *d, int *state, void *st)
     CK(tlg_memcpy_d2h(s, d->state, sizeof s, st));
     CK(tlg_stream_sync(st));
     memcpy(state, s, 3 * sizeof(int));
+    return 0;
+}
+
+int tl_decode_set_fused(TlDecode *d, int fused)
+{
+    if (!d) return TLG_EINVAL;
+    d->unfused = fused ? 0 : 1;
+    for (int c = 0; c < TLD_MAXPOOL; c++)          /* captured steps are stale */
+        if (d->graph[c]) { tlg_graph_destroy(d->graph[c]); d->graph[c] = NULL; }
     return 0;
 }

@@ -6,8 +6,11 @@
  * (tinylm.c:3721-3830) for chunks of m <= mmax rows: the embedding at the
  * chunk's positions, per layer RMSNorm -> [Q, K, V] -> RoPE -> ring store ->
  * attention over the ring window -> [O] + residual -> RMSNorm -> [W1, W3] ->
- * SwiGLU -> [W2] + residual, the final norm and [logits] (brackets: one
- * grouped launch, GEMV kernels at m <= 8).  The cache holds f16 (the
+ * SwiGLU -> [W2] + residual, the final norm and [logits].  By default the
+ * glue rides in the neighbouring launches (tldecode.h's fused entries: the
+ * norms and SwiGLU as GEMV prologues, the residual adds as GEMV epilogues,
+ * RoPE and the ring store inside the attention launch): 5 launches per layer
+ * plus the embedding, the head and the argmax.  The cache holds f16 (the
  * reference's default, kv_dtype_env :3138-3146) or f32 elements; the softmax
  * uses the reference's fast_expf (default) or expf.
  *
@@ -28,7 +31,8 @@ typedef struct TlDecode TlDecode;
 
 /* W: ring positions (the reference uses the training context T); kv_f16: 1
  * f16 cache (default), 0 f32; exact_exp: 0 fast_expf (default), 1 expf;
- * maxpos: RoPE table length (positions 0..maxpos-1); mmax: largest chunk;
+ * maxpos: RoPE table length (positions 0..maxpos-1); mmax: largest chunk
+ * (1..8, the GEMV kernels' row limit);
  * pool: copies of the weights, the greedy graph steps rotate through them so
  * the weights stream from HBM rather than the last-level cache.  NULL on
  * bad shapes or allocation failure. */
@@ -53,6 +57,9 @@ int tl_decode_greedy_step(TlDecode *d, int copy, void *stream);
  * replays the next copy's graph. */
 int tl_decode_graph_build(TlDecode *d, void *stream);
 int tl_decode_graph_step(TlDecode *d, void *stream);
+/* 1 (default): the fused launches; 0: every glue op as its own launch, as
+ * the reference orders them (for comparison).  Drops captured graphs. */
+int tl_decode_set_fused(TlDecode *d, int fused);
 /* Synchronize and read the state: {next position, rows, last token}. */
 int tl_decode_state(TlDecode *d, int *state, void *stream);
 

@@ -93,6 +93,9 @@ SIGNATURES = {
     "tlg_dev_kv_store": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp]),
     "tlg_dev_dec_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp]),
     "tlg_dev_dec_argmax": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
+    "tlg_dev_dec_gemv": (_i, [_vp, _i, _vp]),
+    "tlg_dev_dec_rope_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i,
+                                   _vp]),
 }
 
 
@@ -116,6 +119,13 @@ class TlgGemmCall(ctypes.Structure):
     _fields_ = [("op", ctypes.c_int), ("beta", ctypes.c_int), ("C", _vp),
                 ("M", ctypes.c_int), ("K", ctypes.c_int), ("N", ctypes.c_int), ("nseg", ctypes.c_int),
                 ("A", _vp * 3), ("B", _vp * 3), ("Nseg", ctypes.c_int * 3)]
+
+
+class TlgDecGemv(ctypes.Structure):
+    """include/tldecode.h TlgDecGemv: one GEMV of a fused decode launch."""
+    _fields_ = [("op", ctypes.c_int), ("beta", ctypes.c_int), ("C", _vp),
+                ("M", ctypes.c_int), ("K", ctypes.c_int), ("N", ctypes.c_int), ("A", _vp), ("B", _vp),
+                ("pro", ctypes.c_int), ("gain", _vp), ("A2", _vp)]
 
 
 class Lib:
@@ -379,6 +389,11 @@ class Decode:
     def graph_step(self, stream):
         return self._ck(self.host.dll.tl_decode_graph_step(self.h, stream), "tl_decode_graph_step")
 
+    def set_fused(self, fused):
+        """1: glue folded into the GEMV / attention launches (default);
+        0: every glue op as its own launch."""
+        return self._ck(self.host.dll.tl_decode_set_fused(self.h, 1 if fused else 0), "tl_decode_set_fused")
+
     def state(self, stream):
         s = (ctypes.c_int * 3)()
         self._ck(self.host.dll.tl_decode_state(self.h, s, stream), "tl_decode_state")
@@ -535,6 +550,8 @@ class Host:
         d.tl_decode_chunk.argtypes = [_vp, _vp, _i, _i, _vp]
         d.tl_decode_prime.argtypes = [_vp, _vp, _i, _vp]
         d.tl_decode_greedy_step.argtypes = [_vp, _i, _vp]
+        d.tl_decode_set_fused.argtypes = [_vp, _i]
+        d.tl_decode_set_fused.restype = _i
         self.dll = d
 
     def decode(self, model, W, kv_f16=1, exact_exp=0, maxpos=4096, mmax=8, pool=1):
