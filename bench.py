@@ -168,14 +168,32 @@ def read_traffic(kernel):
 
 AUTOTUNE_CANDS = (3, 14, 13, 15, 0, 1, 20)
 
+# Tile configuration of every grouped launch of each training step: per launch
+# the choice tl_run_autotune made most often over 7 timing runs (5 timed steps
+# per candidate each) on an MI355X.  A fixed table keeps the step's kernels --
+# and so the roofline kernel and its rocprofv3 profiles -- the same from box
+# to box; --autotune re-times the candidates instead.
+TUNED = {
+    "nano": [15, 15, 14, 15, 3, 15, 15, 15, 15, 15],
+    "m3": [13, 14, 3, 14, 14, 20, 3, 14, 14, 14, 3, 14, 14, 15, 3, 14, 14, 15, 3, 14, 14, 15, 3, 14, 3, 20, 3, 15, 13, 15, 3, 15, 13, 15, 3, 15, 13, 15, 3, 15, 13, 15, 20, 15, 13, 15, 3, 15, 13, 15],
+    "m8": [14, 3, 0, 20, 3, 3, 0, 3, 14, 3, 0, 3, 14, 3, 0, 3, 14, 3, 0, 3, 14, 3, 0, 3, 14, 3, 0, 3, 14, 3, 0, 3, 0, 3, 0, 3, 3, 0, 3, 14, 3, 3, 3, 3, 0, 3, 3, 3, 0, 3, 3, 3, 0, 3, 3, 3, 0, 3, 3, 3, 0, 3, 3, 3, 0, 3, 3, 3, 0, 3, 3, 3],
+}
 
-def autotune(lib, host, run, stream, reps=3):
-    """Per-launch tile choice by timing (tl_run_autotune), before any timed
-    or captured step; returns {config: launches}."""
-    arr = (ctypes.c_int * len(AUTOTUNE_CANDS))(*AUTOTUNE_CANDS)
-    check(host.dll.tl_run_autotune(run, arr, len(AUTOTUNE_CANDS), reps, stream), "autotune")
+
+def apply_tiles(lib, host, run, stream, name, retime=False, reps=3):
+    """Set each grouped launch's tile configuration (the TUNED table, or a
+    fresh timing when retime or the table does not fit); returns {config:
+    launches}."""
+    L = host.dll.tl_run_grouped_launches(run)
+    table = TUNED.get(name)
+    if retime or table is None or len(table) != L:
+        arr = (ctypes.c_int * len(AUTOTUNE_CANDS))(*AUTOTUNE_CANDS)
+        check(host.dll.tl_run_autotune(run, arr, len(AUTOTUNE_CANDS), reps, stream), "autotune")
+    else:
+        for k, c in enumerate(table):
+            check(host.dll.tl_run_set_launch_config(run, k, c), "set tile config")
     picks = {}
-    for k in range(host.dll.tl_run_grouped_launches(run)):
+    for k in range(L):
         c = host.dll.tl_run_launch_config(run, k)
         picks[c] = picks.get(c, 0) + 1
     return picks
@@ -198,7 +216,7 @@ def roof_time_ms(plan):
     return roof_ms
 
 
-def bench_train_config(lib, host, stream, name, steps, tune=True):
+def bench_train_config(lib, host, stream, name, steps, tune=True, retime=False):
     """Another BASELINE training config (nano = configs[0], m8 = configs[2]):
     the same grouped, graph-replayed GEMM step."""
     cfg = TRAIN[name]
@@ -207,7 +225,7 @@ def bench_train_config(lib, host, stream, name, steps, tune=True):
     if not run:
         raise RuntimeError("tl_run_new failed: " + lib.tlg_last_error().decode())
     check(host.dll.tl_run_fill(run, 1234567891011, stream), "fill")
-    tuned = autotune(lib, host, run, stream) if tune else None
+    tuned = apply_tiles(lib, host, run, stream, name, retime) if tune else None
     check(host.dll.tl_run_graph_build(run, stream, 1), "graph build")
     step = lambda: host.dll.tl_run_graph_step(run, stream)  # noqa: E731
     for _ in range(5):
@@ -560,11 +578,13 @@ def main():
     ap.add_argument("--other-steps", type=int, default=20, help="timed steps of the other training configs")
     ap.add_argument("--no-probes", action="store_true", help="skip the copy / MFMA peak probes")
     ap.add_argument("--no-autotune", action="store_true",
-                    help="keep the library's automatic tile policy instead of timing candidates per launch")
+                    help="keep the library's automatic tile policy instead of the tuned per-launch table")
+    ap.add_argument("--autotune", action="store_true",
+                    help="time the tile candidates per launch on this box instead of using the tuned table")
     ap.add_argument("--decode-full-steps", type=int, default=512,
                     help="timed greedy decode steps of the whole device decode step; 0 skips")
-    ap.add_argument("--decode-mode", default="both", choices=("both", "fused", "unfused"),
-                    help="decode step: fused launches, glue as separate launches, or both (fused first)")
+    ap.add_argument("--decode-mode", default="fused", choices=("both", "fused", "unfused"),
+                    help="decode step: fused launches (default), glue as separate launches, or both")
     ap.add_argument("--full-steps", type=int, default=30,
                     help="timed whole training steps (forward + backward + AdamW on the device); 0 skips")
     args = ap.parse_args()
@@ -589,7 +609,8 @@ def main():
     check(host.dll.tl_run_fill(run, 1234567891011, stream), "fill")
     grouped = 0 if args.calls else 1
     launches = host.dll.tl_run_grouped_launches(run) if grouped else None
-    tuned = autotune(lib, host, run, stream) if grouped and args.group_cfg is None and not args.no_autotune else None
+    tuned = (apply_tiles(lib, host, run, stream, args.config, args.autotune)
+             if grouped and args.group_cfg is None and not args.no_autotune else None)
     if args.eager:
         fn = host.dll.tl_run_step_grouped if grouped else host.dll.tl_run_step
         step = lambda: fn(run, stream)  # noqa: E731
@@ -645,7 +666,7 @@ def main():
         for name in TRAIN:
             if name != args.config:
                 others[name] = bench_train_config(lib, host, stream, name, args.other_steps,
-                                                  tune=not args.no_autotune)
+                                                  tune=not args.no_autotune, retime=args.autotune)
                 log(f"[train] {name}: {others[name]}")
     decode = {}
     if args.decode_steps > 0:

@@ -449,6 +449,13 @@ int tl_run_autotune(TlRun *r, const int *cands, int ncands, int reps, void *stre
     return rc;
 }
 
+int tl_run_set_launch_config(TlRun *r, int k, int cfg)
+{
+    if (!r || k < 0 || k >= TL_MAXLAUNCH || cfg < -1) return -1;
+    r->lcfg[k] = cfg + 1;
+    return 0;
+}
+
 int tl_run_launch_config(TlRun *r, int k)
 {
     if (!r || k < 0 || k >= TL_MAXLAUNCH) return -1;

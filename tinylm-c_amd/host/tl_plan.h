@@ -118,6 +118,9 @@ const char *tl_run_launch_kernel(TlRun *r, int k);
  * tl_run_launch_config reports it (-1 = the library's automatic policy). */
 int    tl_run_autotune(TlRun *r, const int *cands, int ncands, int reps, void *stream);
 int    tl_run_launch_config(TlRun *r, int k);
+/* Pin launch k's tile configuration (an index of the library's tile table,
+ * -1 = the automatic policy): a tuned table applied without re-timing. */
+int    tl_run_set_launch_config(TlRun *r, int k, int cfg);
 /* Capture one step into a HIP graph and replay it (grouped != 0: the grouped
  * step, else call by call).  The graph is bound to
  * the pool copy current at capture; tl_run_graph_step replays the graph for

@@ -500,6 +500,8 @@ class Host:
         d.tl_run_autotune.restype = _i
         d.tl_run_launch_config.argtypes = [_vp, _i]
         d.tl_run_launch_config.restype = _i
+        d.tl_run_set_launch_config.argtypes = [_vp, _i, _i]
+        d.tl_run_set_launch_config.restype = _i
         d.tl_run_launch_kernel.argtypes = [_vp, _i]
         d.tl_run_launch_kernel.restype = ctypes.c_char_p
         d.tl_run_call.argtypes = [_vp, _i, _vp]
