@@ -498,6 +498,33 @@ def bench_decode_step(lib, host, stream, steps, pool=6, prompt_len=16, warmup=8,
             "launches_per_token": 1 + 8 * 5 + 2 if fused else 1 + 8 * 13 + 3}
 
 
+def bench_decode_persist(lib, host, stream, steps, pool=6, prompt_len=16, warmup=16):
+    """The same greedy decode as bench_decode_step, run by the persistent
+    kernel (tl_decode_persist: every token of the timed run in ONE cooperative
+    launch, workgroups exchanging each phase's outputs through memory); the
+    weight copies rotate per token, so the weights stream from HBM."""
+    import numpy as np
+    maxpos = prompt_len + warmup + steps + 8
+    dec = host.decode(DECODE_MODEL, 256, kv_f16=1, exact_exp=0, maxpos=maxpos, mmax=8, pool=pool)
+    for c in range(pool):
+        check(lib.tlg_dev_fill_normal(dec.params(c), dec.np, 77, 0.02, stream), "fill P")
+    dec.reset(stream)
+    prompt = np.random.default_rng(5).integers(0, DECODE_MODEL["V"], prompt_len).astype(np.int32)
+    dec.prime(prompt, stream)
+    dec.persist(warmup, stream)
+    dec.persist_status(stream)
+    ms, _ = time_steps(lib, lambda: dec.persist(steps, stream), stream, 1)
+    dec.persist_status(stream)
+    state = dec.state(stream)
+    per = ms / steps
+    wbytes = 4 * (DECODE_MODEL["V"] * 384 + 8 * (384 * 384 * 2 + 2 * 384 * 96 + 3 * 384 * 1024))
+    return {"model": DECODE_MODEL, "kv_cache": "f16 ring, 256 positions", "exp": "fast_expf",
+            "weights_pool": pool, "steps": steps, "launches": 1, "ms_per_token": round(per, 4),
+            "tok_s": round(1e3 / per, 1), "weight_bytes_per_token": wbytes,
+            "weight_gbs": round(wbytes / (per * 1e-3) / 1e9, 1),
+            "hbm_frac": round(wbytes / (per * 1e-3) / 8e12, 4), "final_position": state[0]}
+
+
 def cpu_decode_step(threads, steps=40):
     """The oracle's forward_chunk restatement (kind "port": the reference's
     decode state is not compiled from its lines) at M = 1 on host cores."""
@@ -585,6 +612,8 @@ def main():
                     help="timed greedy decode steps of the whole device decode step; 0 skips")
     ap.add_argument("--decode-mode", default="fused", choices=("both", "fused", "unfused"),
                     help="decode step: fused launches (default), glue as separate launches, or both")
+    ap.add_argument("--decode-persist-steps", type=int, default=512,
+                    help="greedy decode steps in one persistent launch (tl_decode_persist); 0 skips")
     ap.add_argument("--full-steps", type=int, default=30,
                     help="timed whole training steps (forward + backward + AdamW on the device); 0 skips")
     args = ap.parse_args()
@@ -692,6 +721,10 @@ def main():
         if args.decode_mode == "both":
             dec_full["unfused"] = bench_decode_step(lib, host, stream, min(args.decode_full_steps, 128), fused=0)
             log(f"[decode step, unfused] {dec_full['unfused']}")
+    dec_persist = None
+    if args.decode_persist_steps > 0:
+        dec_persist = bench_decode_persist(lib, host, stream, args.decode_persist_steps)
+        log(f"[decode step, persistent] {dec_persist}")
     peaks = None if args.no_probes else probes(lib, stream)
     if peaks:
         log(f"[probes] {peaks}")
@@ -757,6 +790,7 @@ def main():
         "moe": moe,
         "train_step": full,
         "decode_step": dec_full,
+        "decode_step_persistent": dec_persist,
         "achievable": peaks,
         "cpu_baseline": cpu,
     }

@@ -84,6 +84,53 @@ int tlg_dev_dec_rope_attn(const float *q, const float *k, const float *v, const 
  * state[2] = tok[0] = the token, so the next step decodes it. */
 int tlg_dev_dec_argmax(const float *logits, int V, int m, int *state, int *tok, void *stream);
 
+/* ---- persistent greedy decoding (no reference counterpart: the reference
+ * calls forward_chunk once per generated token, :3721-3830 and :3844; this
+ * runs n such single-token steps, each followed by the greedy argmax, in ONE
+ * cooperative launch of one workgroup per CU).
+ *
+ * The step is forward_chunk at m = 1 on a dense model with head_dim 32
+ * (D = 32 H <= 384), F <= 1024 and F % 32 == 0, V % 8 == 0 and V <= 4096,
+ * W <= 256, L <= 32: per layer RMSNorm -> Q, K, V -> RoPE -> ring store ->
+ * attention over the window -> O + residual -> RMSNorm -> W1, W3 -> SwiGLU ->
+ * W2 + residual; the final norm and the tied head; argmax_v (the first
+ * maximum).  Token i of the launch decodes at position state[0] + i with
+ * weights P[(copy0 + i) % pool] (map_weights' layout, every copy equal), the
+ * first token being state[2].  At the end state = {state[0] + n, 1, last
+ * greedy token, exchange sequence}, tok[0] = the last greedy token, logits =
+ * the last step's logits row and toks_out[i] (if not NULL) = the token that
+ * step i chose.  Arithmetic: the reference's formulas (RMSNorm, RoPE,
+ * fast_expf or expf, SwiGLU, f16 or f32 ring elements), with fp32 sums in a
+ * fixed order that differs from the reference's sequential one.
+ *
+ * xbuf is an exchange area of tlg_dec_persist_xbytes() bytes that must be
+ * zero before the first launch and after every reset of state[3] (the
+ * workgroups pass each phase's outputs through it, tagged with a sequence
+ * number kept in state[3]).  Launches on one decoder must not overlap.  A
+ * workgroup that waits 0.5 s for its inputs aborts the launch; then
+ * tlg_dec_persist_status() returns TLG_EHIP and the decoder's state and
+ * cache are undefined until it is reset. */
+#define TLG_PD_MAXL 32
+typedef struct {
+    const float *P[16];      /* weight copies                                */
+    int pool, copy0;
+    int V, D, L, H, KV, F;
+    int win, full_every;     /* sliding window per layer (cfg_lwin :64-68)   */
+    int W, f16, exact, maxpos;
+    const float *cs, *sn;    /* RoPE tables [maxpos][16]                     */
+    void *Kc[TLG_PD_MAXL], *Vc[TLG_PD_MAXL];
+    float *logits;           /* [V]                                          */
+    int *state;              /* 4 ints                                       */
+    int *tok;                /* 1 int                                        */
+    int *toks_out;           /* [n] or NULL                                  */
+    void *xbuf;
+} TlgDecPersist;
+
+size_t tlg_dec_persist_xbytes(int V, int D, int L, int F);
+int tlg_dev_dec_persist(const TlgDecPersist *a, int n, void *stream);
+/* Synchronize `stream`; TLG_OK, or TLG_EHIP if a launch on xbuf aborted. */
+int tlg_dec_persist_status(void *xbuf, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

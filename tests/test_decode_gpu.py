@@ -261,3 +261,128 @@ def test_greedy_tokens_match_oracle(lib, shape, kvdt, fused):
         print(mode, "tokens agree for", agree, "of", steps, flush=True)
         if kvdt == 0:
             assert got == want, (mode, got, want)
+
+
+M8 = dict(V=2048, D=384, L=8, H=12, KV=3, F=1024, T=256)
+
+
+def _persist_run(kw, P, W, kvdt, prompt, splits, exact=0, pool=2):
+    """Prime, then greedy steps in persistent launches of the given sizes;
+    returns (tokens, final logits row, final state)."""
+    import tlgemm
+    t = _t()
+    s = stream()
+    dec = tlgemm.host().decode(kw, W, kv_f16=kvdt, exact_exp=exact, maxpos=512, mmax=8, pool=pool)
+    dec.upload(P, s)
+    dec.prime(prompt, s)
+    first = dec.state(s)[2]
+    toks = []
+    for n in splits:
+        buf = t.full((n,), -1, dtype=t.int32, device="cuda")
+        dec.persist(n, s, buf.data_ptr())
+        dec.persist_status(s)
+        toks += buf.cpu().tolist()
+    row = dec.logits(1, s)[0]
+    return dec, [first] + toks, row, dec.state(s)
+
+
+@pytest.mark.parametrize("shape,kvdt,exact", [("small", 0, 0), ("small", 1, 0), ("small", 0, 1), ("m8", 1, 0),
+                                              ("m8", 0, 0)])
+def test_persist_matches_oracle(lib, shape, kvdt, exact):
+    """Greedy decoding in one persistent launch (tlg_dev_dec_persist): the
+    token stream equals the oracle's (up to a near-tie), the last step's
+    logits match the oracle's on the same tokens, the state advances."""
+    kw = SMALL if shape == "small" else M8
+    W = 32 if shape == "small" else 256
+    steps = 40 if shape == "small" else 24
+    m, P = params(kw, 7)
+    prompt = np.random.default_rng(8).integers(0, m.V, 13).astype(np.int32)
+    StepFns("oracle").dll.orc_set_threads(16)
+    orc = Decoder(m, P, W, kvdt=kvdt, exact=exact, maxpos=512)
+    want, rows = oracle_greedy(orc, prompt, steps)
+    print("persist", shape, kvdt, exact, flush=True)
+    _, got, row, st = _persist_run(kw, P, W, kvdt, prompt, [steps], exact=exact)
+    assert st[0] == len(prompt) + steps and st[1] == 1
+    # got[i] is the token fed to step i (got[0] from the prefill), got[steps] the last choice
+    agree = same_stream(got[:steps], want, rows, 1e-5 if kvdt == 0 else TOL_F16)
+    print("persist tokens agree for", agree, "of", steps, flush=True)
+    if agree == steps:
+        # the last step decoded got[steps - 1] at position len(prompt) + steps - 1
+        lg = orc.chunk(np.array([got[steps - 1]], np.int32), len(prompt) + steps - 1)[-1]
+        e = normwise_rel(row, lg)
+        print("persist last logits", f"{e:.2e}", flush=True)
+        assert e <= (TOL_F16 if kvdt else TOL)
+        assert got[steps] == int(np.argmax(row)) == st[2]
+    if kvdt == 0 and exact == 0:
+        assert agree == steps
+
+
+@pytest.mark.parametrize("shape", ["small", "m8"])
+def test_persist_equals_graph_steps(lib, shape):
+    """The persistent launch and the captured greedy step (fused launches)
+    run the same decode: same tokens and, for an f32 ring, logits within
+    the fp32 bar; launches of 1, 5 and 10 steps equal one of 16."""
+    import tlgemm
+    kw = SMALL if shape == "small" else M8
+    W = 32 if shape == "small" else 256
+    m, P = params(kw, 9)
+    prompt = np.random.default_rng(10).integers(0, m.V, 11).astype(np.int32)
+    s = lib.tlg_stream_create()         # graph capture needs a stream of its own
+    print("persist vs graph", shape, flush=True)
+    ref = tlgemm.host().decode(kw, W, kv_f16=0, exact_exp=0, maxpos=512, mmax=8, pool=2)
+    ref.upload(P, s)
+    ref.prime(prompt, s)
+    ref.graph_build(s)
+    gtoks = [ref.state(s)[2]]
+    for _ in range(16):
+        ref.graph_step(s)
+        gtoks.append(ref.state(s)[2])
+    grow = ref.logits(1, s)[0]
+    _, one, row1, st1 = _persist_run(kw, P, W, 0, prompt, [16])
+    _, many, rowm, stm = _persist_run(kw, P, W, 0, prompt, [1, 5, 10])
+    print("graph", gtoks[:8], "persist", one[:8], flush=True)
+    assert one == many and st1 == stm
+    assert np.array_equal(row1, rowm), "split launches must be bit-identical"
+    assert one == gtoks
+    assert normwise_rel(row1, grow) <= TOL
+
+
+def test_persist_after_reprime(lib):
+    """A second prefill keeps the exchange sequence (state[3]), so a later
+    persistent launch never matches words an earlier one left: decoding the
+    same prompt twice on one decoder gives the same tokens both times.  The
+    model has sliding-window layers; its tokens follow the oracle's."""
+    import tlgemm
+    kw = dict(SMALL, win=12, full_every=2)
+    m, P = params(kw, 5)
+    prompt = np.random.default_rng(6).integers(0, m.V, 9).astype(np.int32)
+    s = stream()
+    t = _t()
+    dec = tlgemm.host().decode(kw, 32, kv_f16=1, exact_exp=0, maxpos=256, mmax=8, pool=3)
+    dec.upload(P, s)
+    runs = []
+    for rep in range(2):
+        print("reprime", rep, flush=True)
+        dec.prime(prompt, s)
+        first = dec.state(s)[2]
+        buf = t.full((30,), -1, dtype=t.int32, device="cuda")
+        dec.persist(30, s, buf.data_ptr())
+        dec.persist_status(s)
+        runs.append([first] + buf.cpu().tolist())
+    assert runs[0] == runs[1]
+    want, rows = oracle_greedy(Decoder(m, P, 32, kvdt=1, exact=0, maxpos=256), prompt, 30)
+    agree = same_stream(runs[0][:30], want, rows, TOL_F16)
+    print("window model tokens agree for", agree, "of 30", flush=True)
+
+
+def test_persist_rejects_bad_shapes(lib):
+    """Shapes outside the persistent kernel's scope fail with an error, no launch."""
+    import tlgemm
+    kw = dict(V=128, D=416, L=1, H=13, KV=1, F=64, T=32)       # D > 384
+    m, P = params(kw, 1)
+    s = stream()
+    dec = tlgemm.host().decode(kw, 32, kv_f16=1, exact_exp=0, maxpos=64, mmax=8, pool=1)
+    dec.upload(P, s)
+    dec.prime(np.array([1, 2, 3], np.int32), s)
+    with pytest.raises(tlgemm.TlgError):
+        dec.persist(4, s)

@@ -20,18 +20,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 static inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-// The reference's fast_expf: clamp, split x log2(e) into integer and
-// fraction, 2^f by its degree-5 Horner polynomial, 2^k into the exponent.
-__device__ __forceinline__ float dec_fast_expf(float x)
-{
-    x = x < -87.0f ? -87.0f : (x > 88.0f ? 88.0f : x);
-    const float t = x * 1.44269504088896f;
-    const float k = floorf(t), f = t - k;
-    const float p = 1.0f + f * (0.6931471805f + f * (0.2402265069f + f * (0.0555041087f +
-                                                                        f * (0.0096181291f + f * 0.0013333558f))));
-    return p * __uint_as_float((unsigned int)(((int)k + 127) << 23));
-}
-
 // state[0] = first position of the next chunk, state[1] = rows of the next
 // chunk, state[2] = last greedy token.
 // x[j] = emb[tok[j]], pos[j] = state[0] + j (or start + j when state is null).
@@ -293,7 +281,7 @@ __device__ __forceinline__ void attn_wg(const float *__restrict__ q, const float
         float sum = 0.f;
         if (live)
             for (int t = tb + lane; t < te; t += 64) {
-                const float ex = exact ? expf(pr[t] - mx) : dec_fast_expf(pr[t] - mx);
+                const float ex = exact ? expf(pr[t] - mx) : tlg_fast_expf(pr[t] - mx);
                 pr[t] = ex;
                 sum += ex;
             }

@@ -67,3 +67,16 @@ int tlg_gemv_launch(TlgKind kind, const float *A, const float *B, float *C, int 
                     int ldb, int ldc, int beta, hipStream_t st);
 int tlg_gemv_group_launch(const TlgGemmCall *calls, int n, hipStream_t st);
 const char *tlg_gemv_kernel_name(int M);
+
+// The reference's fast_expf (tinylm.c:3181-3191): clamp, split x log2(e) into
+// integer and fraction, 2^f by its degree-5 Horner polynomial, 2^k into the
+// exponent.
+__device__ __forceinline__ float tlg_fast_expf(float x)
+{
+    x = x < -87.0f ? -87.0f : (x > 88.0f ? 88.0f : x);
+    const float t = x * 1.44269504088896f;
+    const float k = floorf(t), f = t - k;
+    const float p = 1.0f + f * (0.6931471805f + f * (0.2402265069f + f * (0.0555041087f +
+                                                                        f * (0.0096181291f + f * 0.0013333558f))));
+    return p * __uint_as_float((unsigned int)(((int)k + 127) << 23));
+}

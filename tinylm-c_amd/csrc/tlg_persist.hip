@@ -1,0 +1,785 @@
+// tlg_persist.hip -- n greedy single-token decode steps in ONE launch on gfx950.
+//
+// tinylm.c generates token after token with forward_chunk (:3721-3830) and
+// argmax_v (:3844).  At M = 1 each GEMV moves 0.1-3 MB, which HBM delivers in
+// well under a microsecond, while every dependent kernel launch costs several:
+// a graph of 43 launches per token is bound by the gaps between them.  Here one
+// workgroup per CU stays resident for the whole run (a cooperative launch
+// guarantees they are all resident at once) and the workgroups hand each
+// phase's outputs to each other through memory:
+//
+//   work items of a token, in phase order; item i belongs to workgroup i % NB
+//     layer l:  H attention items   (RMSNorm, the head's Q and its group's K, V
+//                                    columns, RoPE, ring store, attention)
+//               D/32 O items        (32 output columns of ctx . Wo)
+//               F/16 SwiGLU items   (16 columns of RMSNorm(x) . W1 and . W3,
+//                                    then silu(g) * u)
+//               D/32 W2 items       (32 columns of act . W2)
+//     head:     V/8 items           (8 vocabulary rows of fn . emb^T and their
+//                                    first maximum), item j to workgroup j % NB
+//   exchange  every output element is a 64-bit word (value | tag << 32) written
+//             with an agent-scope relaxed atomic store (global_store sc1: it goes
+//             to the device-coherent level, not only the XCD's L2); a consumer
+//             reads the words it needs with agent-scope atomic loads until all of
+//             them carry its phase's tag.  Tags count phases over launches
+//             (state[3]), so a stale word never matches.  Per layer four
+//             exchanges (ctx, O out, act, W2 out), per token one more (argmax
+//             candidates, double-buffered by token parity).
+//   residual  every workgroup keeps x in LDS and adds each O / W2 output row to
+//             it in the same order, so all copies are bit-identical; RMSNorm is
+//             computed where it is needed.
+//   prefetch  nothing an item reads from memory except its inputs waits on the
+//             critical path: after finishing an item a workgroup loads the
+//             weight panel and RMSNorm gain of its next one into registers
+//             (about 256 items later, 2-3 layers ahead); the RoPE factors of
+//             the position come at the token's start; the ring rows of the
+//             keys before the position half a layer before the attention.
+//             Token i reads weight copy (copy0 + i) % pool.
+//   KV ring   ring rows are read with agent-scope atomic loads (another
+//             workgroup, possibly on another XCD, wrote them), 8 (f16) or 16
+//             (f32) threads per row so a load instruction covers whole rows,
+//             and the new row is stored the same way; the writer waits for
+//             those stores to complete before it publishes its ctx, so every
+//             later reader, which depends on that ctx, sees the row.
+//
+// No dependency points forward (an item only waits for earlier phases), so the
+// run always progresses; every wait is bounded (0.5 s of the real-time
+// counter), after which the workgroup raises an abort flag that ends every
+// other wait too, and the kernel returns.
+//
+// Reference arithmetic followed: rmsnorm_fwd :540-548 (1/sqrt(ss/D + 1e-5),
+// x * s * g), rope_apply :645-651 with rope_init's tables, kv_store :3236-3250
+// (f16 round to nearest even or f32), attn_body :3639-3715 (scores q.k hd^-1/2,
+// fast_expf :3181-3191 or expf, normalise then sum p_t v_t), SwiGLU silu(g) * u
+// with silu(z) = z / (1 + e^-z) (:786, :3821-3823), residual adds :3818, :3824,
+// the head mm_bt :3829-3830 and argmax_v :3844.  Sums run in a fixed order of
+// their own (the same in every workgroup and launch), not the reference's.
+#include "tlg_internal.h"
+#include "../../include/tldecode.h"
+#include <math.h>
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned long long u64;
+typedef unsigned int u32;
+
+#define PD_T 512            // threads per workgroup (8 waves, 2 per SIMD)
+#define PD_NW 8
+#define PD_MAXQ 6           // row slices of a K = D panel: D / 64 with D <= 384
+#define PD_MAXFQ 16         // row slices of a K = F panel: F / 64 with F <= 1024
+#define PD_WB 18            // f32x4 per thread of the weight panel: 3 * PD_MAXQ
+#define PD_MAXD 384
+#define PD_MAXF 1024
+#define PD_MAXW 256         // ring positions
+#define PD_MAXHI 512        // head items V / 8
+#define PD_SPIN 50000000ull // 0.5 s of the 100 MHz real-time counter
+
+static_assert(PD_WB >= 3 * PD_MAXQ && PD_WB >= PD_MAXFQ, "weight panel");
+static_assert(PD_MAXD <= PD_T, "one gain element per thread");
+
+// Exchange area (64-bit words): control words, then per layer ctx [D], O out
+// [D], act [F], W2 out [D], then the argmax candidates [2][V/8][2].
+struct PdLayout {
+    size_t ctrl, ctx, yo, act, y2, cand, total;
+};
+__host__ __device__ static inline PdLayout pd_layout(int V, int D, int L, int F)
+{
+    PdLayout o;
+    size_t p = 0;
+    o.ctrl = p;  p += 8;
+    o.ctx = p;   p += (size_t)L * D;
+    o.yo = p;    p += (size_t)L * D;
+    o.act = p;   p += (size_t)L * F;
+    o.y2 = p;    p += (size_t)L * D;
+    o.cand = p;  p += (size_t)2 * (V / 8) * 2;
+    o.total = p;
+    return o;
+}
+
+// Every access of this kernel goes through global-address-space pointers:
+// flat loads would also count against lgkmcnt, so each LDS barrier would wait
+// for the weight prefetches in flight.
+#define GAS __attribute__((address_space(1)))
+template <class T> __device__ __forceinline__ GAS T *gp(T *p) { return (GAS T *)p; }
+
+__device__ __forceinline__ u64 pd_ld(const u64 *p)
+{
+    return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void pd_st(u64 *p, u64 v)
+{
+    __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 pd_word(float v, u32 tag) { return ((u64)tag << 32) | (u64)__float_as_uint(v); }
+
+// A pointer every thread holds the same value of (read from LDS, say), moved
+// to scalar registers so addresses are a scalar base plus a 32-bit offset.
+template <class T> __device__ __forceinline__ T *pd_uni(T *p)
+{
+    const u64 v = (u64)(uintptr_t)p;
+    const u32 lo = __builtin_amdgcn_readfirstlane((u32)v), hi = __builtin_amdgcn_readfirstlane((u32)(v >> 32));
+    return (T *)(uintptr_t)(((u64)hi << 32) | lo);
+}
+template <class T> __device__ __forceinline__ T pd_at(const void *base, u32 byteoff)
+{
+    return *reinterpret_cast<const GAS T *>(reinterpret_cast<const GAS char *>(gp(base)) + byteoff);
+}
+
+// Wait until this wave's stores have completed (vmcnt counts stores on gfx9).
+__device__ __forceinline__ void pd_wait_stores()
+{
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);        // vmcnt(0) expcnt(7) lgkmcnt(15)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Wait until the n words src[0..n) carry `tag`; then dst[e] = (ADD ? dst[e] +
+// : ) their values.  Called by every thread; false after an abort.
+template <int KPL, int ADD>
+__device__ bool pd_fetch(const u64 *src, int n, u32 tag, float *dst, u32 *abortp)
+{
+    const int tid = threadIdx.x;
+    const u64 t0 = wall_clock64();
+    for (;;) {
+        u64 w[KPL];
+#pragma unroll
+        for (int k = 0; k < KPL; k++)
+            w[k] = pd_ld(reinterpret_cast<const u64 *>(reinterpret_cast<const char *>(src) +
+                                                        8u * (u32)min(tid + PD_T * k, n - 1)));
+        int bad = 0;
+#pragma unroll
+        for (int k = 0; k < KPL; k++) bad |= (tid + PD_T * k < n) && (u32)(w[k] >> 32) != tag;
+        if (!__syncthreads_or(bad)) {
+#pragma unroll
+            for (int k = 0; k < KPL; k++) {
+                const int e = tid + PD_T * k;
+                if (e < n) dst[e] = ADD ? dst[e] + __uint_as_float((u32)w[k]) : __uint_as_float((u32)w[k]);
+            }
+            __syncthreads();
+            return true;
+        }
+        int stop = 0;
+        if (tid == 0)
+            stop = __hip_atomic_load(gp(abortp), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u ||
+                   wall_clock64() - t0 > PD_SPIN;
+        if (__syncthreads_or(stop)) {
+            if (tid == 0) __hip_atomic_store(gp(abortp), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return false;
+        }
+    }
+}
+
+// dst[j] = x[j] * s * g[j], s = 1 / sqrt(sum x^2 / D + 1e-5) (rmsnorm_fwd);
+// thread j < D holds its gain element gj.
+__device__ void pd_rmsnorm(const float *x, float gj, float *dst, int D, float *sw)
+{
+    const int tid = threadIdx.x;
+    const float xj = tid < D ? x[tid] : 0.f;
+    float ss = xj * xj;
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((tid & 63) == 0) sw[tid >> 6] = ss;
+    __syncthreads();
+    float tot = sw[0];
+#pragma unroll
+    for (int w = 1; w < PD_NW; w++) tot += sw[w];
+    const float s = 1.0f / sqrtf(tot / (float)D + 1e-5f);
+    if (tid < D) dst[tid] = xj * s * gj;
+    __syncthreads();
+}
+
+// Column-panel GEMV.  Thread (c4 = tid & 7, rg = tid >> 3) holds
+// w[i] = W[(rg + 64 i) * N + col0 + 4 c4 .. + 3] for rows rg + 64 i < K
+// (rows past K load row K - 1, unused: every element is written, so the panel
+// stays in registers).
+template <int MAXI>
+__device__ __forceinline__ void pd_load_cols(f32x4 *w, const float *__restrict__ W, int N, int col0, int K)
+{
+    const int c4 = threadIdx.x & 7, rg = threadIdx.x >> 3;
+#pragma unroll
+    for (int i = 0; i < MAXI; i++)
+        w[i] = pd_at<f32x4>(W, 4u * ((u32)min(rg + 64 * i, K - 1) * (u32)N + (u32)(col0 + 4 * c4)));
+}
+
+template <int MAXI>
+__device__ __forceinline__ f32x4 pd_dot(const float *vin, const f32x4 *w, int K)
+{
+    const int rg = threadIdx.x >> 3;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < MAXI; i++)
+        if (rg + 64 * i < K) {
+            const float xv = vin[rg + 64 * i];
+            acc.x = fmaf(xv, w[i].x, acc.x);
+            acc.y = fmaf(xv, w[i].y, acc.y);
+            acc.z = fmaf(xv, w[i].z, acc.z);
+            acc.w = fmaf(xv, w[i].w, acc.w);
+        }
+    return acc;
+}
+
+// The 64 row groups' partials of one panel: shuffles inside a wave, then
+// (pd_colsum_read) the 8 waves in order through LDS (red: 64 f32x4).
+__device__ __forceinline__ void pd_colsum_put(f32x4 acc, f32x4 *red)
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int o = 8; o < 64; o <<= 1) {
+        acc.x += __shfl_xor(acc.x, o);
+        acc.y += __shfl_xor(acc.y, o);
+        acc.z += __shfl_xor(acc.z, o);
+        acc.w += __shfl_xor(acc.w, o);
+    }
+    if ((tid & 56) == 0) red[(tid >> 6) * 8 + (tid & 7)] = acc;
+}
+__device__ __forceinline__ float pd_colsum_read(const f32x4 *red, int col)
+{
+    const float *rf = reinterpret_cast<const float *>(red);
+    float r = rf[col];
+#pragma unroll
+    for (int w = 1; w < PD_NW; w++) r += rf[32 * w + col];
+    return r;
+}
+// one panel: thread tid < 32 gets column tid
+__device__ __forceinline__ float pd_colsum(f32x4 acc, f32x4 *red)
+{
+    pd_colsum_put(acc, red);
+    __syncthreads();
+    return threadIdx.x < 32 ? pd_colsum_read(red, threadIdx.x) : 0.f;
+}
+
+// The weight panel of layer item g (index within a token) in thread order and
+// the RMSNorm gain element of thread tid (items that normalise x):
+//   attention (k < NA): Wq columns of head k, Wk and Wv columns of its KV head
+//     at panel offsets 0, PD_MAXQ, 2 PD_MAXQ; gain an1
+//   O: Wo columns; SwiGLU: threads c4 < 4 the W1 columns 16 c + 4 c4 .. + 3,
+//     c4 >= 4 the same columns of W3; gain an2; W2: W2 columns (K = F)
+// Every kind writes the whole panel, so it stays in registers.
+__device__ __forceinline__ void pd_load_item(f32x4 (&wb)[PD_WB], float &gn, const float *__restrict__ P, int g,
+                                             int NPL, int NA, int NO, int NS, size_t lay0, size_t per, int D, int KD,
+                                             int F, int grp)
+{
+    const int l = g / NPL, k = g % NPL;
+    const size_t an1 = lay0 + (size_t)l * per, wq = an1 + D, wk = wq + (size_t)D * D, wv = wk + (size_t)D * KD,
+                 wo = wv + (size_t)D * KD, an2 = wo + (size_t)D * D, w1 = an2 + D, w3 = w1 + (size_t)D * F,
+                 w2 = w3 + (size_t)D * F;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    const int tid = threadIdx.x, c4 = tid & 7;
+    const u32 gof = 4u * (u32)min(tid, D - 1);
+    if (k < NA) {
+        const int gq = k / grp;
+        pd_load_cols<PD_MAXQ>(wb, P + wq, D, k * 32, D);
+        pd_load_cols<PD_MAXQ>(wb + PD_MAXQ, P + wk, KD, gq * 32, D);
+        pd_load_cols<PD_MAXQ>(wb + 2 * PD_MAXQ, P + wv, KD, gq * 32, D);
+        gn = pd_at<float>(P + an1, gof);
+    } else if (k < NA + NO) {
+        pd_load_cols<PD_MAXQ>(wb, P + wo, D, (k - NA) * 32, D);
+#pragma unroll
+        for (int i = PD_MAXQ; i < PD_WB; i++) wb[i] = z;
+        gn = 0.f;
+    } else if (k < NA + NO + NS) {
+        // columns 16 c .. 16 c + 15 of W1 (c4 < 4) and of W3 (c4 >= 4): thread
+        // c4 reads the float4 at 16 c + 4 (c4 & 3); pd_load_cols' 4 c4 offset is
+        // taken back by col0
+        const int c = k - NA - NO;
+        const float *W = c4 < 4 ? P + w1 : P + w3;
+        pd_load_cols<PD_MAXQ>(wb, W, F, 16 * c - 4 * (c4 & 4), D);
+#pragma unroll
+        for (int i = PD_MAXQ; i < PD_WB; i++) wb[i] = z;
+        gn = pd_at<float>(P + an2, gof);
+    } else {
+        pd_load_cols<PD_MAXFQ>(wb, P + w2, D, (k - NA - NO - NS) * 32, F);
+#pragma unroll
+        for (int i = PD_MAXFQ; i < PD_WB; i++) wb[i] = z;
+        gn = 0.f;
+    }
+}
+
+// Head item j: wave r holds vocabulary row 8 j + r, thread c = tid & 63 the
+// float4s c and c + 64 of it (those below D / 4).
+__device__ __forceinline__ void pd_load_head(f32x4 (&hb)[2], const float *__restrict__ emb, int j, int D)
+{
+    const int tid = threadIdx.x;
+    const float *rows = emb + (size_t)8 * j * D;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+        hb[i] = pd_at<f32x4>(rows, 4u * ((u32)(tid >> 6) * (u32)D + 4u * (u32)min((tid & 63) + 64 * i, D / 4 - 1)));
+}
+
+// Ring rows of 32 elements as 64-bit words: NW per row (8 f16, 16 f32), EPW
+// elements per word; thread (key slot tid / NW, word tid % NW).
+template <int F16> struct PdRing;
+template <> struct PdRing<1> {
+    typedef _Float16 E;
+    static constexpr int NW = 8, EPW = 4, LOG2NW = 3;
+    __device__ static float get(u64 w, int e)
+    {
+        return (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> (16 * e)));
+    }
+    __device__ static float round(float v) { return (float)(_Float16)v; }
+    __device__ static u64 pack(const float *v)
+    {
+        u64 r = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) r |= (u64)__builtin_bit_cast(unsigned short, (_Float16)v[c]) << (16 * c);
+        return r;
+    }
+};
+template <> struct PdRing<0> {
+    typedef float E;
+    static constexpr int NW = 16, EPW = 2, LOG2NW = 4;
+    __device__ static float get(u64 w, int e) { return __uint_as_float((u32)(w >> (32 * e))); }
+    __device__ static float round(float v) { return v; }
+    __device__ static u64 pack(const float *v)
+    {
+        return (u64)__float_as_uint(v[0]) | ((u64)__float_as_uint(v[1]) << 32);
+    }
+};
+#define PD_MAXR 8           // key rounds: PD_MAXW / (PD_T / NW), 8 for f32 (4 for f16)
+
+// The visible window of `pos` in layer l: positions lo .. pos, cnt of them.
+__device__ __forceinline__ void pd_window(const TlgDecPersist &a, int l, int pos, int *lo, int *cnt)
+{
+    int wl = a.win;
+    if (wl <= 0 || (a.full_every > 0 && ((l + 1) % a.full_every) == 0)) wl = 0;   // cfg_lwin :64-68
+    const int wlim = (wl > 0 && wl < a.W) ? wl : a.W;
+    *lo = pos >= wlim ? pos - wlim + 1 : 0;
+    *cnt = pos - *lo + 1;
+}
+
+// Ring words of the keys before `pos` (the window's first cnt - 1 keys) for
+// KV head kvh of layer l: round r, thread (key slot, word); K words if LK, V
+// words if LV.
+template <int F16, int LK, int LV>
+__device__ __forceinline__ void pd_ring_load(u64 (&kw)[PD_MAXR], u64 (&vw)[PD_MAXR], const void *Kc, const void *Vc,
+                                             int kvh, int KD, int W, int lo, int cnt)
+{
+    typedef PdRing<F16> R;
+    constexpr int KPR = PD_T / R::NW, MAXR = PD_MAXW / KPR;
+    const int tid = threadIdx.x, key0 = tid >> R::LOG2NW, wd = tid & (R::NW - 1);
+    const u32 rowb = (u32)KD * (u32)sizeof(typename R::E);          // bytes per ring row
+    const char *Kb = pd_uni(reinterpret_cast<const char *>(Kc) + (size_t)kvh * 32 * sizeof(typename R::E));
+    const char *Vb = pd_uni(reinterpret_cast<const char *>(Vc) + (size_t)kvh * 32 * sizeof(typename R::E));
+#pragma unroll
+    for (int r = 0; r < MAXR; r++) {
+        const int t = key0 + KPR * r;
+        if (t < cnt - 1) {
+            const u32 off = (u32)((lo + t) % W) * rowb + 8u * (u32)wd;
+            if (LK) kw[r] = pd_ld(reinterpret_cast<const u64 *>(Kb + off));
+            if (LV) vw[r] = pd_ld(reinterpret_cast<const u64 *>(Vb + off));
+        }
+    }
+}
+
+struct PdShared {
+    float x[PD_MAXD], xn[PD_MAXD], in[PD_MAXF];
+    f32x4 red[3][8 * PD_NW];
+    float sw[2 * PD_NW];
+    int swi[PD_NW];
+    float q[32], k[32], v[32], ctxw[PD_NW][32];
+    float lg[8];
+    int tok;
+    const float *P[16];                 // the launch's pointer tables, indexed at run time
+    void *Kc[TLG_PD_MAXL], *Vc[TLG_PD_MAXL];
+};
+
+// The first maximum over the argmax candidates of a token (argmax_v: ties to
+// the lowest index) into sh.tok.  false after an abort.
+__device__ __forceinline__ bool pd_argmax(PdShared &sh, const u64 *cand, int NHI, u32 tag, u32 *abortp)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (!pd_fetch<2, 0>(cand, 2 * NHI, tag, sh.in, abortp)) return false;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    if (tid < NHI) {
+        bv = sh.in[2 * tid];
+        bi = (int)__float_as_uint(sh.in[2 * tid + 1]);
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v = __shfl_xor(bv, o);
+        const int i = __shfl_xor(bi, o);
+        if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+    }
+    if (lane == 0) { sh.sw[wave] = bv; sh.swi[wave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        float v0 = sh.sw[0];
+        int i0 = sh.swi[0];
+        for (int w = 1; w < PD_NW; w++) {
+            const float v = sh.sw[w];
+            const int i = sh.swi[w];
+            if (v > v0 || (v == v0 && i < i0)) { v0 = v; i0 = i; }
+        }
+        sh.tok = i0 == 0x7fffffff ? 0 : i0;
+    }
+    __syncthreads();
+    return true;
+}
+
+// One attention item (layer l, query head h) at position pos: RMSNorm (gain
+// element gn), the head's q and its KV head's k, v from the panel in wb, RoPE
+// (this thread's factors rc, rs for pair tid & 15), the ring store (by the
+// group's first head), softmax attention over the window with the ring words
+// kw / vw already loaded (f32 rings: vw loaded here), then ctx_h published
+// with `tag`.
+template <int F16>
+__device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_WB], float gn, float rc, float rs,
+                                             const u64 (&kw)[PD_MAXR], u64 (&vw)[PD_MAXR], const TlgDecPersist &a,
+                                             int l, int h, int pos, int D, int KD, int grp, u64 *ctxout, u32 tag)
+{
+    typedef PdRing<F16> R;
+    constexpr int NW = R::NW, KPR = PD_T / NW, MAXR = PD_MAXW / KPR;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kvh = h / grp, key0 = tid >> R::LOG2NW, wd = tid & (NW - 1);
+    int lo, cnt;
+    pd_window(a, l, pos, &lo, &cnt);
+    pd_rmsnorm(sh.x, gn, sh.xn, D, sh.sw);
+    pd_colsum_put(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]);
+    pd_colsum_put(pd_dot<PD_MAXQ>(sh.xn, wb + PD_MAXQ, D), sh.red[1]);
+    pd_colsum_put(pd_dot<PD_MAXQ>(sh.xn, wb + 2 * PD_MAXQ, D), sh.red[2]);
+    if (!F16) {                          // f32 rings: V words now, for register room
+        u64 none[PD_MAXR];
+        pd_ring_load<F16, 0, 1>(none, vw, sh.Kc[l], sh.Vc[l], kvh, KD, a.W, lo, cnt);
+    }
+    __syncthreads();
+    // q, k, v columns; RoPE of q and the new k (rope_apply's pairs (i, i + 16));
+    // new k and v in the ring's format
+    if (tid < 96) {
+        const int m = tid >> 5;
+        const float c = pd_colsum_read(sh.red[m], tid & 31);
+        (m == 0 ? sh.q : m == 1 ? sh.k : sh.v)[tid & 31] = c;
+    }
+    __syncthreads();
+    {
+        const bool inpos = pos >= 0 && pos < a.maxpos;
+        const int i = tid & 15;
+        if (tid < 16) {
+            const float x0 = sh.q[i], x1 = sh.q[i + 16];
+            sh.q[i] = inpos ? x0 * rc - x1 * rs : NAN;
+            sh.q[i + 16] = inpos ? x1 * rc + x0 * rs : NAN;
+        } else if (tid < 32) {
+            const float x0 = sh.k[i], x1 = sh.k[i + 16];
+            sh.k[i] = R::round(inpos ? x0 * rc - x1 * rs : NAN);
+            sh.k[i + 16] = R::round(inpos ? x1 * rc + x0 * rs : NAN);
+        } else if (tid < 64) {
+            sh.v[tid - 32] = R::round(sh.v[tid - 32]);
+        }
+    }
+    __syncthreads();
+    const bool writer = (h % grp) == 0;
+    if (writer && tid < 2 * NW) {                              // ring slot pos % W
+        const int w = tid & (NW - 1);
+        char *row = reinterpret_cast<char *>(tid < NW ? sh.Kc[l] : sh.Vc[l]) +
+                    ((size_t)(pos % a.W) * KD + (size_t)kvh * 32) * sizeof(typename R::E);
+        pd_st(reinterpret_cast<u64 *>(row) + w, R::pack((tid < NW ? sh.k : sh.v) + R::EPW * w));
+    }
+    // scores: key t = key0 + KPR r; t < cnt - 1 from the ring, t = cnt - 1 the new
+    // row; the NW threads of a key sum their words' partial dots
+    const float scale = 1.0f / sqrtf(32.0f);
+    float sc[MAXR];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < MAXR; r++) {
+        const int t = key0 + KPR * r;
+        float part = 0.f;
+#pragma unroll
+        for (int e = 0; e < R::EPW; e++) {
+            const int d = R::EPW * wd + e;
+            part = fmaf(sh.q[d], t < cnt - 1 ? R::get(kw[r], e) : sh.k[d], part);
+        }
+#pragma unroll
+        for (int o = 1; o < NW; o <<= 1) part += __shfl_xor(part, o);
+        sc[r] = t < cnt ? part * scale : -INFINITY;
+        mx = fmaxf(mx, sc[r]);
+    }
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) sh.sw[wave] = mx;
+    __syncthreads();
+    mx = sh.sw[0];
+#pragma unroll
+    for (int w = 1; w < PD_NW; w++) mx = fmaxf(mx, sh.sw[w]);
+    float sum = 0.f;
+#pragma unroll
+    for (int r = 0; r < MAXR; r++) {
+        const int t = key0 + KPR * r;
+        sc[r] = t < cnt ? (a.exact ? expf(sc[r] - mx) : tlg_fast_expf(sc[r] - mx)) : 0.f;
+        if (wd == 0) sum += sc[r];                             // once per key
+    }
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    if (lane == 0) sh.sw[PD_NW + wave] = sum;
+    __syncthreads();
+    float tot = sh.sw[PD_NW];
+#pragma unroll
+    for (int w = 1; w < PD_NW; w++) tot += sh.sw[PD_NW + w];
+    const float inv = tot > 0.f ? 1.0f / tot : 0.f;
+    // ctx[d] = sum_t p_t v_t[d]: thread (key slot, word) over its keys, then the
+    // key slots of a word: shuffles in the wave, the 8 waves in order via LDS
+    float acc[R::EPW];
+#pragma unroll
+    for (int e = 0; e < R::EPW; e++) acc[e] = 0.f;
+#pragma unroll
+    for (int r = 0; r < MAXR; r++) {
+        const int t = key0 + KPR * r;
+        const float p = sc[r] * inv;
+#pragma unroll
+        for (int e = 0; e < R::EPW; e++) {
+            const float vv = t < cnt - 1 ? R::get(vw[r], e) : sh.v[R::EPW * wd + e];
+            acc[e] = t < cnt ? fmaf(p, vv, acc[e]) : acc[e];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < R::EPW; e++) {
+        for (int o = NW; o < 64; o <<= 1) acc[e] += __shfl_xor(acc[e], o);
+        if (lane < NW) sh.ctxw[wave][R::EPW * lane + e] = acc[e];
+    }
+    __syncthreads();
+    if (tid < 32) {
+        float cx = sh.ctxw[0][tid];
+#pragma unroll
+        for (int w = 1; w < PD_NW; w++) cx += sh.ctxw[w][tid];
+        if (writer) pd_wait_stores();                          // the ring row first
+        pd_st(ctxout + tid, pd_word(cx, tag));
+    }
+    __syncthreads();
+}
+
+template <int F16>
+__global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
+{
+    __shared__ PdShared sh;
+    const int tid = threadIdx.x;
+    const int NB = gridDim.x, b = blockIdx.x;
+    const int D = a.D, F = a.F, V = a.V, L = a.L, H = a.H, KD = a.KV * 32, grp = a.H / a.KV;
+    const int NA = H, NO = D / 32, NS = F / 16, NPL = NA + NO + NS + D / 32, NLI = L * NPL, NHI = V / 8;
+    const u32 NPH = 4u * (u32)L + 1u;
+    const size_t per = (size_t)D + (size_t)D * D + 2 * (size_t)D * KD + (size_t)D * D + D + 3 * (size_t)D * F;
+    const size_t lay0 = (size_t)V * D;
+    u64 *xb = reinterpret_cast<u64 *>(a.xbuf);
+    const PdLayout lay = pd_layout(V, D, L, F);
+    u32 *abortp = reinterpret_cast<u32 *>(xb + lay.ctrl);
+    const int pos0 = gp(a.state)[0];
+    const u32 base = (u32)gp(a.state)[3];
+    int tok = gp(a.state)[2];
+    if (b >= NLI && b >= NHI) return;
+    if (tid == 0) {                      // constant indices: scalar kernel-argument loads
+#pragma unroll
+        for (int i = 0; i < 16; i++) sh.P[i] = a.P[i];
+#pragma unroll
+        for (int i = 0; i < TLG_PD_MAXL; i++) { sh.Kc[i] = a.Kc[i]; sh.Vc[i] = a.Vc[i]; }
+    }
+    __syncthreads();
+
+    // this workgroup's items: layer items g = b, b + NB, ... < NLI of every
+    // token (panel and gain prefetched one item ahead into wb, gn), head items
+    // j = b, b + NB, ... < NHI (the first prefetched at the token's start)
+    f32x4 wb[PD_WB];
+    float gn = 0.f;
+    f32x4 hb[2];
+    u64 kw[PD_MAXR], vw[PD_MAXR];
+    if (b < NLI)
+        pd_load_item(wb, gn, pd_uni(sh.P[a.copy0 % a.pool]), b, NPL, NA, NO, NS, lay0, per, D, KD, F, grp);
+    // this workgroup's first attention item in layer l (query head), or -1
+    auto attn_head = [&](int l) -> int {
+        const int s = l * NPL, g = s + ((b - s) % NB + NB) % NB;
+        return g < s + NA ? g - s : -1;
+    };
+
+    for (int t = 0; t < n; t++) {
+        const float *P = pd_uni(sh.P[(a.copy0 + t) % a.pool]);
+        const int pos = pos0 + t;
+        const u32 tag0 = base + (u32)t * NPH + 1u;            // tag of phase 0 of this token
+        // ---- token start: the previous step's greedy token, x = emb[tok]
+        if (t > 0) {
+            if (!pd_argmax(sh, xb + lay.cand + (size_t)((t - 1) & 1) * NHI * 2, NHI, tag0 - 1u, abortp)) return;
+            tok = sh.tok;
+            if (b == 0 && tid == 0 && a.toks_out) gp(a.toks_out)[t - 1] = tok;
+        }
+        if (tid < D) sh.x[tid] = (tok >= 0 && tok < V) ? gp(P)[(size_t)tok * D + tid] : NAN;
+        pd_load_head(hb, P, min(b, NHI - 1), D);
+        const float hg = pd_at<float>(P + lay0 + (size_t)L * per, 4u * (u32)min(tid, D - 1));
+        const bool inpos = pos >= 0 && pos < a.maxpos;
+        const float rc = inpos ? gp(a.cs)[(size_t)pos * 16 + (tid & 15)] : 0.f;
+        const float rs = inpos ? gp(a.sn)[(size_t)pos * 16 + (tid & 15)] : 0.f;
+        {   // ring words of layer 0's attention
+            const int h = attn_head(0);
+            int lo, cnt;
+            pd_window(a, 0, pos, &lo, &cnt);
+            if (h >= 0) pd_ring_load<F16, 1, F16>(kw, vw, sh.Kc[0], sh.Vc[0], h / grp, KD, a.W, lo, cnt);
+        }
+        __syncthreads();
+
+        for (int l = 0; l < L; l++) {
+            const int g0 = l * NPL;
+            const u32 tl = tag0 + 4u * (u32)l;                  // ctx, O out, act, W2 out: tl .. tl + 3
+            u64 *ctx = xb + lay.ctx + (size_t)l * D, *yo = xb + lay.yo + (size_t)l * D;
+            u64 *act = xb + lay.act + (size_t)l * F, *y2 = xb + lay.y2 + (size_t)l * D;
+            // first item index >= g0 + k0 that belongs to this workgroup
+#define PD_FIRST(k0) ((g0 + (k0)) + ((b - (g0 + (k0))) % NB + NB) % NB)
+// the next item's panel (past the last token: a harmless reload, so that wb is
+// always overwritten)
+#define PD_NEXT(g)                                                                                           \
+    do {                                                                                                     \
+        const int ng_ = (g) + NB < NLI ? (g) + NB : b, nt_ = min((g) + NB < NLI ? t : t + 1, n - 1);          \
+        pd_load_item(wb, gn, pd_uni(sh.P[(a.copy0 + nt_) % a.pool]), ng_, NPL, NA, NO, NS, lay0, per, D, KD, F, \
+                     grp);                                                                                   \
+    } while (0)
+
+            for (int g = PD_FIRST(0); g < g0 + NA; g += NB) {
+                if (g != PD_FIRST(0)) {      // a second attention item in this layer: its ring words
+                    int lo, cnt;
+                    pd_window(a, l, pos, &lo, &cnt);
+                    pd_ring_load<F16, 1, F16>(kw, vw, sh.Kc[l], sh.Vc[l], (g - g0) / grp, KD, a.W, lo, cnt);
+                }
+                pd_attention<F16>(sh, wb, gn, rc, rs, kw, vw, a, l, g - g0, pos, D, KD, grp,
+                                  ctx + (size_t)(g - g0) * 32, tl);
+                PD_NEXT(g);
+            }
+            for (int g = PD_FIRST(NA); g < g0 + NA + NO; g += NB) {        // O: ctx . Wo
+                if (!pd_fetch<1, 0>(ctx, D, tl, sh.in, abortp)) return;
+                const float r = pd_colsum(pd_dot<PD_MAXQ>(sh.in, wb, D), sh.red[0]);
+                if (tid < 32) pd_st(yo + (size_t)(g - g0 - NA) * 32 + tid, pd_word(r, tl + 1u));
+                __syncthreads();
+                PD_NEXT(g);
+            }
+            if (!pd_fetch<1, 1>(yo, D, tl + 1u, sh.x, abortp)) return;     // x += O out
+            if (l + 1 < L) {                 // ring words of the next layer's attention, early
+                const int h = attn_head(l + 1);
+                int lo, cnt;
+                pd_window(a, l + 1, pos, &lo, &cnt);
+                if (h >= 0)
+                    pd_ring_load<F16, 1, F16>(kw, vw, sh.Kc[l + 1], sh.Vc[l + 1], h / grp, KD, a.W, lo, cnt);
+            }
+            bool normed = false;
+            for (int g = PD_FIRST(NA + NO); g < g0 + NA + NO + NS; g += NB) {    // silu(xn . W1) * (xn . W3)
+                if (!normed) { pd_rmsnorm(sh.x, gn, sh.xn, D, sh.sw); normed = true; }
+                const float r = pd_colsum(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]);
+                const float u = __shfl(r, (tid & 15) + 16);               // W3 column of this W1 column
+                if (tid < 16)
+                    pd_st(act + (size_t)(g - g0 - NA - NO) * 16 + tid, pd_word(r / (1.0f + expf(-r)) * u, tl + 2u));
+                __syncthreads();
+                PD_NEXT(g);
+            }
+            for (int g = PD_FIRST(NA + NO + NS); g < g0 + NPL; g += NB) {       // act . W2
+                if (!pd_fetch<2, 0>(act, F, tl + 2u, sh.in, abortp)) return;
+                const float r = pd_colsum(pd_dot<PD_MAXFQ>(sh.in, wb, F), sh.red[0]);
+                if (tid < 32) pd_st(y2 + (size_t)(g - g0 - NA - NO - NS) * 32 + tid, pd_word(r, tl + 3u));
+                __syncthreads();
+                PD_NEXT(g);
+            }
+            if (!pd_fetch<1, 1>(y2, D, tl + 3u, sh.x, abortp)) return;     // x += W2 out
+#undef PD_FIRST
+#undef PD_NEXT
+        }
+
+        // ---- head: final RMSNorm, 8 vocabulary rows per item, their first maximum
+        if (b < NHI) {
+            const u32 th = tag0 + 4u * (u32)L;
+            u64 *cand = xb + lay.cand + (size_t)(t & 1) * NHI * 2;
+            pd_rmsnorm(sh.x, hg, sh.xn, D, sh.sw);
+            for (int j = b; j < NHI; j += NB) {
+                f32x4 hw[2] = {hb[0], hb[1]};
+                if (j != b) pd_load_head(hw, P, j, D);
+                const int r = tid >> 6, c = tid & 63;
+                float acc = 0.f;
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+                    if (4 * (c + 64 * i) < D) {
+                        const f32x4 f = *reinterpret_cast<const f32x4 *>(sh.xn + 4 * (c + 64 * i));
+                        acc = fmaf(f.x, hw[i].x, acc);
+                        acc = fmaf(f.y, hw[i].y, acc);
+                        acc = fmaf(f.z, hw[i].z, acc);
+                        acc = fmaf(f.w, hw[i].w, acc);
+                    }
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) acc += __shfl_xor(acc, o);
+                if (c == 0) {
+                    sh.lg[r] = acc;
+                    gp(a.logits)[(size_t)8 * j + r] = acc;
+                }
+                __syncthreads();
+                if (tid == 0) {
+                    float bv = -INFINITY;
+                    int bi = 0x7fffffff;
+                    for (int rr = 0; rr < 8; rr++)
+                        if (sh.lg[rr] > bv) { bv = sh.lg[rr]; bi = 8 * j + rr; }
+                    pd_st(cand + (size_t)2 * j, pd_word(bv, th));
+                    pd_st(cand + (size_t)2 * j + 1, ((u64)th << 32) | (u64)(u32)bi);
+                }
+                __syncthreads();
+            }
+        }
+    }
+
+    // ---- the last step's greedy token and the state for the next launch
+    if (b == 0) {
+        const u32 th = base + (u32)n * NPH;                    // head tag of token n - 1
+        if (!pd_argmax(sh, xb + lay.cand + (size_t)((n - 1) & 1) * NHI * 2, NHI, th, abortp)) return;
+        if (tid == 0) {
+            const int tk = sh.tok;
+            if (a.toks_out) gp(a.toks_out)[n - 1] = tk;
+            GAS int *st = gp(a.state);
+            st[0] = pos0 + n;
+            st[1] = 1;
+            st[2] = tk;
+            st[3] = (int)(base + (u32)n * NPH);
+            gp(a.tok)[0] = tk;
+        }
+    }
+}
+
+// ============================================================== entries ==
+extern "C" size_t tlg_dec_persist_xbytes(int V, int D, int L, int F)
+{
+    if (V <= 0 || D <= 0 || L <= 0 || F <= 0) return 0;
+    return pd_layout(V, D, L, F).total * sizeof(u64);
+}
+
+static int g_pd_cus = 0;
+
+extern "C" int tlg_dev_dec_persist(const TlgDecPersist *a, int n, void *stream)
+{
+    int rc = tlg_ensure_init();
+    if (rc) return rc;
+    if (!a || n <= 0 || a->pool <= 0 || a->pool > 16 || a->copy0 < 0 || a->H <= 0 || a->KV <= 0 ||
+        a->H % a->KV || a->D != 32 * a->H || a->D > PD_MAXD || a->F <= 0 || a->F % 32 || a->F > PD_MAXF ||
+        a->V <= 0 || a->V % 8 || a->V / 8 > PD_MAXHI || a->L <= 0 || a->L > TLG_PD_MAXL || a->W <= 0 ||
+        a->W > PD_MAXW || a->maxpos <= 0 || !a->cs || !a->sn || !a->logits || !a->state || !a->tok || !a->xbuf)
+        return tlg_fail(TLG_EINVAL,
+                        "dec_persist: n=%d V=%d D=%d L=%d H=%d KV=%d F=%d W=%d pool=%d (head_dim 32, D <= %d, "
+                        "F %% 32 == 0 and F <= %d, V %% 8 == 0 and V <= %d, W <= %d, L <= %d)",
+                        n, a ? a->V : 0, a ? a->D : 0, a ? a->L : 0, a ? a->H : 0, a ? a->KV : 0, a ? a->F : 0,
+                        a ? a->W : 0, a ? a->pool : 0, PD_MAXD, PD_MAXF, 8 * PD_MAXHI, PD_MAXW, TLG_PD_MAXL);
+    for (int c = 0; c < a->pool; c++)
+        if (!a->P[c] || ((uintptr_t)a->P[c] & 15u)) return tlg_fail(TLG_EINVAL, "dec_persist: weight copy %d", c);
+    for (int l = 0; l < a->L; l++)
+        if (!a->Kc[l] || !a->Vc[l] || ((uintptr_t)a->Kc[l] & 63u) || ((uintptr_t)a->Vc[l] & 63u))
+            return tlg_fail(TLG_EINVAL, "dec_persist: cache of layer %d", l);
+    if ((uintptr_t)a->xbuf & 15u) return tlg_fail(TLG_EINVAL, "dec_persist: xbuf alignment");
+    if (!g_pd_cus) {
+        int cus = 0;
+        TLG_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, g_tlg.device));
+        g_pd_cus = cus;
+    }
+    const int nli = a->L * (a->H + 2 * (a->D / 32) + a->F / 16), nhi = a->V / 8;
+    int nb = nli > nhi ? nli : nhi;
+    if (nb > g_pd_cus) nb = g_pd_cus;
+    const void *fn = a->f16 ? (const void *)k_dec_persist<1> : (const void *)k_dec_persist<0>;
+    int per_cu = 0;
+    TLG_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, PD_T, 0));
+    if (per_cu < 1) return tlg_fail(TLG_EHIP, "dec_persist: the kernel does not fit on a CU");
+    TlgDecPersist args = *a;
+    int nn = n;
+    void *kargs[] = {&args, &nn};
+    TLG_HIP(hipLaunchCooperativeKernel(fn, dim3(nb), dim3(PD_T), kargs, 0, (hipStream_t)stream));
+    return TLG_OK;
+}
+
+extern "C" int tlg_dec_persist_status(void *xbuf, void *stream)
+{
+    int rc = tlg_ensure_init();
+    if (rc) return rc;
+    if (!xbuf) return tlg_fail(TLG_EINVAL, "dec_persist_status: xbuf");
+    u32 flag = 0;
+    TLG_HIP(hipMemcpyAsync(&flag, xbuf, sizeof flag, hipMemcpyDeviceToHost, (hipStream_t)stream));
+    TLG_HIP(hipStreamSynchronize((hipStream_t)stream));
+    if (flag) return tlg_fail(TLG_EHIP, "dec_persist: a workgroup's wait for its inputs expired (launch aborted)");
+    return TLG_OK;
+}

@@ -20,8 +20,11 @@ struct TlDecode {
     void **Kc, **Vc;
     float *rcos, *rsin, *x, *xn, *q, *k, *v, *ctx, *tmp, *g, *u, *act, *fn, *logits;
     int *pos, *tok, *state;
+    void *xbuf;                  /* the persistent decode's exchange area */
+    size_t xbytes;
     void *graph[TLD_MAXPOOL];
     int next_graph;
+    int next_copy;               /* weight copy of the next persistent step */
     int unfused;                 /* 1: the glue as separate launches (tl_decode_set_fused) */
 };
 
@@ -85,12 +88,16 @@ TlDecode *tl_decode_new(const TlModel *m, int W, int kv_f16, int exact_exp, int 
     const int nf = (int)(sizeof fixed / sizeof fixed[0]);
     size_t total = 0;
     for (int i = 0; i < nf; i++) total += (fixed[i].bytes + 255) & ~(size_t)255;
+    d->xbytes = tlg_dec_persist_xbytes(m->V, m->D, m->L, m->F);
+    total += (d->xbytes + 255) & ~(size_t)255;
     total += (size_t)pool * ((4 * d->np + 255) & ~(size_t)255);
     total += (size_t)m->L * 2 * ((kvb + 255) & ~(size_t)255);
     d->arena = tlg_dev_malloc(total);
     if (!d->arena) { tl_decode_free(d); return NULL; }
     char *p = d->arena;
     for (int i = 0; i < nf; i++) { *fixed[i].dst = p; p += (fixed[i].bytes + 255) & ~(size_t)255; }
+    d->xbuf = p;
+    p += (d->xbytes + 255) & ~(size_t)255;
     for (int c = 0; c < pool; c++) { d->P[c] = (float *)p; p += (4 * d->np + 255) & ~(size_t)255; }
     for (int l = 0; l < m->L; l++) {
         d->Kc[l] = p; p += (kvb + 255) & ~(size_t)255;
@@ -139,8 +146,10 @@ int tl_decode_reset(TlDecode *d, void *st)
         if (!rc) rc = tlg_dev_zero((float *)d->Vc[l], kvf, st);
         if (rc) return rc;
     }
+    int rc = tlg_dev_zero((float *)d->xbuf, d->xbytes / 4, st);   /* sequence 0: every tag stale */
+    if (rc) return rc;
     const int zero[4] = {0, 0, 0, 0};
-    int rc = tlg_memcpy_h2d(d->state, zero, sizeof zero, st);
+    rc = tlg_memcpy_h2d(d->state, zero, sizeof zero, st);
     if (!rc) rc = tlg_stream_sync(st);
     return rc;
 }
@@ -263,8 +272,8 @@ int tl_decode_prime(TlDecode *d, const int *prompt, int n, void *st)
         CK(tl_decode_chunk(d, prompt + i, m, i, st));
         i += m;
     }
-    const int s[4] = {n - m, m, 0, 0};                /* the last chunk; argmax advances it */
-    CK(tlg_memcpy_h2d(d->state, s, sizeof s, st));
+    const int s[3] = {n - m, m, 0};                   /* the last chunk; argmax advances it */
+    CK(tlg_memcpy_h2d(d->state, s, sizeof s, st));    /* state[3] (exchange sequence) is kept */
     CK(tlg_dev_dec_argmax(d->logits, d->m.V, m, d->state, d->tok, st));
     return tlg_stream_sync(st);
 }
@@ -315,4 +324,31 @@ int tl_decode_set_fused(TlDecode *d, int fused)
     for (int c = 0; c < TLD_MAXPOOL; c++)          /* captured steps are stale */
         if (d->graph[c]) { tlg_graph_destroy(d->graph[c]); d->graph[c] = NULL; }
     return 0;
+}
+
+/* ---- persistent greedy decoding (tldecode.h tlg_dev_dec_persist) ------------- */
+int tl_decode_persist(TlDecode *d, int n, int *toks_out, void *st)
+{
+    if (!d || n <= 0) return TLG_EINVAL;
+    const TlModel *md = &d->m;
+    TlgDecPersist a;
+    memset(&a, 0, sizeof a);
+    if (md->L > TLG_PD_MAXL) return TLG_EINVAL;
+    for (int c = 0; c < d->pool; c++) a.P[c] = d->P[c];
+    a.pool = d->pool;
+    a.copy0 = d->next_copy;
+    a.V = md->V; a.D = md->D; a.L = md->L; a.H = md->H; a.KV = md->KV; a.F = md->F;
+    a.win = md->win; a.full_every = md->full_every;
+    a.W = d->W; a.f16 = d->f16; a.exact = d->exact; a.maxpos = d->maxpos;
+    a.cs = d->rcos; a.sn = d->rsin;
+    for (int l = 0; l < md->L; l++) { a.Kc[l] = d->Kc[l]; a.Vc[l] = d->Vc[l]; }
+    a.logits = d->logits; a.state = d->state; a.tok = d->tok; a.toks_out = toks_out; a.xbuf = d->xbuf;
+    CK(tlg_dev_dec_persist(&a, n, st));
+    d->next_copy = (d->next_copy + n) % d->pool;
+    return 0;
+}
+
+int tl_decode_persist_status(TlDecode *d, void *st)
+{
+    return d ? tlg_dec_persist_status(d->xbuf, st) : TLG_EINVAL;
 }

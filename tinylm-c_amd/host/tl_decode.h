@@ -60,6 +60,14 @@ int tl_decode_graph_step(TlDecode *d, void *stream);
 /* 1 (default): the fused launches; 0: every glue op as its own launch, as
  * the reference orders them (for comparison).  Drops captured graphs. */
 int tl_decode_set_fused(TlDecode *d, int fused);
+/* n greedy token steps from the device state in ONE persistent launch
+ * (tldecode.h tlg_dev_dec_persist), weight copies rotating per token;
+ * toks_out: device [n] for the chosen tokens, or NULL.  Same state, logits
+ * and cache as n tl_decode_greedy_step calls.  Needs D = 32 H <= 384,
+ * F <= 1024 (F % 32 == 0), V % 8 == 0, W <= 256.  tl_decode_persist_status
+ * synchronizes and reports an aborted launch (TLG_EHIP; then reset). */
+int tl_decode_persist(TlDecode *d, int n, int *toks_out, void *stream);
+int tl_decode_persist_status(TlDecode *d, void *stream);
 /* Synchronize and read the state: {next position, rows, last token}. */
 int tl_decode_state(TlDecode *d, int *state, void *stream);
 

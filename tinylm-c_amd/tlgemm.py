@@ -96,6 +96,9 @@ SIGNATURES = {
     "tlg_dev_dec_gemv": (_i, [_vp, _i, _vp]),
     "tlg_dev_dec_rope_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i,
                                    _vp]),
+    "tlg_dec_persist_xbytes": (_sz, [_i, _i, _i, _i]),
+    "tlg_dev_dec_persist": (_i, [_vp, _i, _vp]),
+    "tlg_dec_persist_status": (_i, [_vp, _vp]),
 }
 
 
@@ -389,6 +392,15 @@ class Decode:
     def graph_step(self, stream):
         return self._ck(self.host.dll.tl_decode_graph_step(self.h, stream), "tl_decode_graph_step")
 
+    def persist(self, n, stream, toks=None):
+        """n greedy steps in one persistent launch (asynchronous); toks: a
+        device int32 buffer of n entries for the chosen tokens, or None."""
+        return self._ck(self.host.dll.tl_decode_persist(self.h, n, toks, stream), "tl_decode_persist")
+
+    def persist_status(self, stream):
+        """Synchronize; raises if a persistent launch aborted."""
+        return self._ck(self.host.dll.tl_decode_persist_status(self.h, stream), "tl_decode_persist_status")
+
     def set_fused(self, fused):
         """1: glue folded into the GEMV / attention launches (default);
         0: every glue op as its own launch."""
@@ -552,6 +564,10 @@ class Host:
         d.tl_decode_chunk.argtypes = [_vp, _vp, _i, _i, _vp]
         d.tl_decode_prime.argtypes = [_vp, _vp, _i, _vp]
         d.tl_decode_greedy_step.argtypes = [_vp, _i, _vp]
+        d.tl_decode_persist.argtypes = [_vp, _i, _vp, _vp]
+        d.tl_decode_persist.restype = _i
+        d.tl_decode_persist_status.argtypes = [_vp, _vp]
+        d.tl_decode_persist_status.restype = _i
         d.tl_decode_set_fused.argtypes = [_vp, _i]
         d.tl_decode_set_fused.restype = _i
         self.dll = d
