@@ -168,14 +168,44 @@ __device__ bool pd_fetch(const u64 *src, int n, u32 tag, float *dst, u32 *abortp
     }
 }
 
+// Cross-lane steps on the VALU (DPP) rather than through LDS permutes, which
+// wait one at a time: row_shr scans within 16-lane rows, then row_bcast:15 /
+// :31 carry the rows upward; lane 63 ends with the total, read back as a
+// scalar.  A fixed order, the same in every wave.
+template <int CTRL, int ROWMASK> __device__ __forceinline__ float pd_dpp(float fill, float x)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(x), CTRL, ROWMASK, 0xf,
+                                                      false));
+}
+__device__ __forceinline__ float pd_wave_sum(float x)
+{
+    x += pd_dpp<0x111, 0xf>(0.f, x);          // row_shr:1
+    x += pd_dpp<0x112, 0xf>(0.f, x);          // row_shr:2
+    x += pd_dpp<0x114, 0xf>(0.f, x);          // row_shr:4
+    x += pd_dpp<0x118, 0xf>(0.f, x);          // row_shr:8
+    x += pd_dpp<0x142, 0xa>(0.f, x);          // row_bcast:15 into rows 1, 3
+    x += pd_dpp<0x143, 0xc>(0.f, x);          // row_bcast:31 into rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+__device__ __forceinline__ float pd_wave_max(float x)
+{
+    x = fmaxf(x, pd_dpp<0x111, 0xf>(-INFINITY, x));
+    x = fmaxf(x, pd_dpp<0x112, 0xf>(-INFINITY, x));
+    x = fmaxf(x, pd_dpp<0x114, 0xf>(-INFINITY, x));
+    x = fmaxf(x, pd_dpp<0x118, 0xf>(-INFINITY, x));
+    x = fmaxf(x, pd_dpp<0x142, 0xa>(-INFINITY, x));
+    x = fmaxf(x, pd_dpp<0x143, 0xc>(-INFINITY, x));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
 // dst[j] = x[j] * s * g[j], s = 1 / sqrt(sum x^2 / D + 1e-5) (rmsnorm_fwd);
 // thread j < D holds its gain element gj.
 __device__ void pd_rmsnorm(const float *x, float gj, float *dst, int D, float *sw)
 {
     const int tid = threadIdx.x;
-    const float xj = tid < D ? x[tid] : 0.f;
-    float ss = xj * xj;
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    const float xr = x[min(tid, D - 1)];
+    const float xj = tid < D ? xr : 0.f;
+    const float ss = pd_wave_sum(xj * xj);
     if ((tid & 63) == 0) sw[tid >> 6] = ss;
     __syncthreads();
     float tot = sw[0];
@@ -202,40 +232,41 @@ __device__ __forceinline__ void pd_load_cols(f32x4 *w, const float *__restrict__
 template <int MAXI>
 __device__ __forceinline__ f32x4 pd_dot(const float *vin, const f32x4 *w, int K)
 {
+    // branch-free: every row's LDS read is issued at once (rows past K read row
+    // K - 1 and are not added)
     const int rg = threadIdx.x >> 3;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < MAXI; i++)
-        if (rg + 64 * i < K) {
-            const float xv = vin[rg + 64 * i];
-            acc.x = fmaf(xv, w[i].x, acc.x);
-            acc.y = fmaf(xv, w[i].y, acc.y);
-            acc.z = fmaf(xv, w[i].z, acc.z);
-            acc.w = fmaf(xv, w[i].w, acc.w);
-        }
+    for (int i = 0; i < MAXI; i++) {
+        const bool in = rg + 64 * i < K;
+        const float xv = vin[min(rg + 64 * i, K - 1)];
+        acc.x = in ? fmaf(xv, w[i].x, acc.x) : acc.x;
+        acc.y = in ? fmaf(xv, w[i].y, acc.y) : acc.y;
+        acc.z = in ? fmaf(xv, w[i].z, acc.z) : acc.z;
+        acc.w = in ? fmaf(xv, w[i].w, acc.w) : acc.w;
+    }
     return acc;
 }
 
-// The 64 row groups' partials of one panel: shuffles inside a wave, then
-// (pd_colsum_read) the 8 waves in order through LDS (red: 64 f32x4).
+// The 64 row groups' partials of one panel: the two row groups of a 16-lane
+// row meet with row_ror:8 (lane ^ 8), then the 32 row pairs go through LDS
+// (red: 32 x 8 f32x4) and pd_colsum_read adds them in order.
+#define PD_RED (PD_T / 16 * 8)
 __device__ __forceinline__ void pd_colsum_put(f32x4 acc, f32x4 *red)
 {
     const int tid = threadIdx.x;
-#pragma unroll
-    for (int o = 8; o < 64; o <<= 1) {
-        acc.x += __shfl_xor(acc.x, o);
-        acc.y += __shfl_xor(acc.y, o);
-        acc.z += __shfl_xor(acc.z, o);
-        acc.w += __shfl_xor(acc.w, o);
-    }
-    if ((tid & 56) == 0) red[(tid >> 6) * 8 + (tid & 7)] = acc;
+    acc.x += pd_dpp<0x128, 0xf>(0.f, acc.x);
+    acc.y += pd_dpp<0x128, 0xf>(0.f, acc.y);
+    acc.z += pd_dpp<0x128, 0xf>(0.f, acc.z);
+    acc.w += pd_dpp<0x128, 0xf>(0.f, acc.w);
+    if ((tid & 8) == 0) red[(tid >> 4) * 8 + (tid & 7)] = acc;
 }
 __device__ __forceinline__ float pd_colsum_read(const f32x4 *red, int col)
 {
     const float *rf = reinterpret_cast<const float *>(red);
     float r = rf[col];
 #pragma unroll
-    for (int w = 1; w < PD_NW; w++) r += rf[32 * w + col];
+    for (int g = 1; g < PD_T / 16; g++) r += rf[32 * g + col];
     return r;
 }
 // one panel: thread tid < 32 gets column tid
@@ -358,58 +389,64 @@ __device__ __forceinline__ void pd_ring_load(u64 (&kw)[PD_MAXR], u64 (&vw)[PD_MA
     const u32 rowb = (u32)KD * (u32)sizeof(typename R::E);          // bytes per ring row
     const char *Kb = pd_uni(reinterpret_cast<const char *>(Kc) + (size_t)kvh * 32 * sizeof(typename R::E));
     const char *Vb = pd_uni(reinterpret_cast<const char *>(Vc) + (size_t)kvh * 32 * sizeof(typename R::E));
+    // every round loads (keys past the window reload an earlier slot, unused):
+    // straight-line loads are issued back to back, with no wait between them
 #pragma unroll
     for (int r = 0; r < MAXR; r++) {
-        const int t = key0 + KPR * r;
-        if (t < cnt - 1) {
-            const u32 off = (u32)((lo + t) % W) * rowb + 8u * (u32)wd;
-            if (LK) kw[r] = pd_ld(reinterpret_cast<const u64 *>(Kb + off));
-            if (LV) vw[r] = pd_ld(reinterpret_cast<const u64 *>(Vb + off));
-        }
+        const int t = min(key0 + KPR * r, max(cnt - 2, 0));
+        const u32 off = (u32)((lo + t) % W) * rowb + 8u * (u32)wd;
+        if (LK) kw[r] = pd_ld(reinterpret_cast<const u64 *>(Kb + off));
+        if (LV) vw[r] = pd_ld(reinterpret_cast<const u64 *>(Vb + off));
     }
 }
 
 struct PdShared {
     float x[PD_MAXD], xn[PD_MAXD], in[PD_MAXF];
-    f32x4 red[3][8 * PD_NW];
+    f32x4 red[3][PD_RED];
     float sw[2 * PD_NW];
-    int swi[PD_NW];
-    float q[32], k[32], v[32], ctxw[PD_NW][32];
+    float q[32], k[32], v[32], ctxw[PD_T / 16][32];
+    u64 key[PD_T];
     float lg[8];
     int tok;
     const float *P[16];                 // the launch's pointer tables, indexed at run time
     void *Kc[TLG_PD_MAXL], *Vc[TLG_PD_MAXL];
 };
 
+// argmax_v order as one unsigned key: larger value first, then the lower index
+__device__ __forceinline__ u64 pd_argkey(float v, u32 i)
+{
+    u32 b = __float_as_uint(v + 0.0f);                          // -0 as +0: equal values tie
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);           // order-preserving map of the float
+    return ((u64)b << 32) | (u64)(~i);
+}
+
 // The first maximum over the argmax candidates of a token (argmax_v: ties to
-// the lowest index) into sh.tok.  false after an abort.
+// the lowest index; no candidate above -inf gives token 0, as the reference's
+// scan does) into sh.tok: the keys' maximum through LDS, 8 at a time.  false
+// after an abort.
 __device__ __forceinline__ bool pd_argmax(PdShared &sh, const u64 *cand, int NHI, u32 tag, u32 *abortp)
 {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x;
     if (!pd_fetch<2, 0>(cand, 2 * NHI, tag, sh.in, abortp)) return false;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    u64 kx = 0;
     if (tid < NHI) {
-        bv = sh.in[2 * tid];
-        bi = (int)__float_as_uint(sh.in[2 * tid + 1]);
+        const u32 i = __float_as_uint(sh.in[2 * tid + 1]);
+        kx = i == 0x7fffffffu ? 0 : pd_argkey(sh.in[2 * tid], i);
     }
-    for (int o = 32; o > 0; o >>= 1) {
-        const float v = __shfl_xor(bv, o);
-        const int i = __shfl_xor(bi, o);
-        if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-    }
-    if (lane == 0) { sh.sw[wave] = bv; sh.swi[wave] = bi; }
+    sh.key[tid] = kx;
     __syncthreads();
-    if (tid == 0) {
-        float v0 = sh.sw[0];
-        int i0 = sh.swi[0];
-        for (int w = 1; w < PD_NW; w++) {
-            const float v = sh.sw[w];
-            const int i = sh.swi[w];
-            if (v > v0 || (v == v0 && i < i0)) { v0 = v; i0 = i; }
+    for (int n = PD_T / 8; n >= 1; n /= 8) {       // 64, then 8, then 1 keys
+        u64 m = 0;
+        if (tid < n) {
+            m = sh.key[8 * tid];
+#pragma unroll
+            for (int j = 1; j < 8; j++) m = max(m, sh.key[8 * tid + j]);
         }
-        sh.tok = i0 == 0x7fffffff ? 0 : i0;
+        __syncthreads();
+        if (tid < n) sh.key[tid] = m;
+        __syncthreads();
     }
+    if (tid == 0) sh.tok = sh.key[0] == 0 ? 0 : (int)(~(u32)sh.key[0]);
     __syncthreads();
     return true;
 }
@@ -440,28 +477,18 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
         pd_ring_load<F16, 0, 1>(none, vw, sh.Kc[l], sh.Vc[l], kvh, KD, a.W, lo, cnt);
     }
     __syncthreads();
-    // q, k, v columns; RoPE of q and the new k (rope_apply's pairs (i, i + 16));
-    // new k and v in the ring's format
+    // q, k, v columns (thread 32 m + i: column i of q, k, v for m = 0, 1, 2);
+    // RoPE of q and the new k (rope_apply's pairs (i, i + 16), the partner
+    // column from the lane i ^ 16); new k and v in the ring's format
     if (tid < 96) {
-        const int m = tid >> 5;
-        const float c = pd_colsum_read(sh.red[m], tid & 31);
-        (m == 0 ? sh.q : m == 1 ? sh.k : sh.v)[tid & 31] = c;
-    }
-    __syncthreads();
-    {
+        const int m = tid >> 5, i = tid & 31;
+        const float c = pd_colsum_read(sh.red[m], i);
+        const float o = __shfl_xor(c, 16);
         const bool inpos = pos >= 0 && pos < a.maxpos;
-        const int i = tid & 15;
-        if (tid < 16) {
-            const float x0 = sh.q[i], x1 = sh.q[i + 16];
-            sh.q[i] = inpos ? x0 * rc - x1 * rs : NAN;
-            sh.q[i + 16] = inpos ? x1 * rc + x0 * rs : NAN;
-        } else if (tid < 32) {
-            const float x0 = sh.k[i], x1 = sh.k[i + 16];
-            sh.k[i] = R::round(inpos ? x0 * rc - x1 * rs : NAN);
-            sh.k[i + 16] = R::round(inpos ? x1 * rc + x0 * rs : NAN);
-        } else if (tid < 64) {
-            sh.v[tid - 32] = R::round(sh.v[tid - 32]);
-        }
+        const float rot = inpos ? (i < 16 ? c * rc - o * rs : c * rc + o * rs) : NAN;
+        if (m == 0) sh.q[i] = rot;
+        else if (m == 1) sh.k[i] = R::round(rot);
+        else sh.v[i] = R::round(c);
     }
     __syncthreads();
     const bool writer = (h % grp) == 0;
@@ -483,14 +510,24 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
 #pragma unroll
         for (int e = 0; e < R::EPW; e++) {
             const int d = R::EPW * wd + e;
-            part = fmaf(sh.q[d], t < cnt - 1 ? R::get(kw[r], e) : sh.k[d], part);
+            const float kn = sh.k[d];
+            part = fmaf(sh.q[d], t < cnt - 1 ? R::get(kw[r], e) : kn, part);
         }
-#pragma unroll
-        for (int o = 1; o < NW; o <<= 1) part += __shfl_xor(part, o);
+        // the NW lanes of the key: butterflies inside quads (quad_perm), then the
+        // two quads of an 8-lane group (row_ror:n reads lane (i - n) mod 16, so
+        // lanes 0-3 of the group take row_ror:12, lanes 4-7 row_ror:4), for f32
+        // the two halves of the 16-lane row (row_ror:8)
+        part += pd_dpp<0xB1, 0xf>(0.f, part);
+        part += pd_dpp<0x4E, 0xf>(0.f, part);
+        {
+            const float r4 = pd_dpp<0x124, 0xf>(0.f, part), r12 = pd_dpp<0x12C, 0xf>(0.f, part);
+            part += (lane & 4) ? r4 : r12;
+        }
+        if (NW == 16) part += pd_dpp<0x128, 0xf>(0.f, part);
         sc[r] = t < cnt ? part * scale : -INFINITY;
         mx = fmaxf(mx, sc[r]);
     }
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    mx = pd_wave_max(mx);
     if (lane == 0) sh.sw[wave] = mx;
     __syncthreads();
     mx = sh.sw[0];
@@ -503,7 +540,7 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
         sc[r] = t < cnt ? (a.exact ? expf(sc[r] - mx) : tlg_fast_expf(sc[r] - mx)) : 0.f;
         if (wd == 0) sum += sc[r];                             // once per key
     }
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    sum = pd_wave_sum(sum);
     if (lane == 0) sh.sw[PD_NW + wave] = sum;
     __syncthreads();
     float tot = sh.sw[PD_NW];
@@ -521,20 +558,24 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
         const float p = sc[r] * inv;
 #pragma unroll
         for (int e = 0; e < R::EPW; e++) {
-            const float vv = t < cnt - 1 ? R::get(vw[r], e) : sh.v[R::EPW * wd + e];
+            const float vn = sh.v[R::EPW * wd + e];
+            const float vv = t < cnt - 1 ? R::get(vw[r], e) : vn;
             acc[e] = t < cnt ? fmaf(p, vv, acc[e]) : acc[e];
         }
     }
+    // the key slots of a word: for f16 the two slots of a 16-lane row meet with
+    // row_ror:8, then each row's partials go through LDS, added in row order
+    const int row = tid >> 4;
 #pragma unroll
     for (int e = 0; e < R::EPW; e++) {
-        for (int o = NW; o < 64; o <<= 1) acc[e] += __shfl_xor(acc[e], o);
-        if (lane < NW) sh.ctxw[wave][R::EPW * lane + e] = acc[e];
+        if (NW == 8) acc[e] += pd_dpp<0x128, 0xf>(0.f, acc[e]);
+        if ((tid & 15) < NW) sh.ctxw[row][R::EPW * wd + e] = acc[e];
     }
     __syncthreads();
     if (tid < 32) {
         float cx = sh.ctxw[0][tid];
 #pragma unroll
-        for (int w = 1; w < PD_NW; w++) cx += sh.ctxw[w][tid];
+        for (int rr = 1; rr < PD_T / 16; rr++) cx += sh.ctxw[rr][tid];
         if (writer) pd_wait_stores();                          // the ring row first
         pd_st(ctxout + tid, pd_word(cx, tag));
     }
@@ -688,8 +729,7 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
                         acc = fmaf(f.z, hw[i].z, acc);
                         acc = fmaf(f.w, hw[i].w, acc);
                     }
-#pragma unroll
-                for (int o = 1; o < 64; o <<= 1) acc += __shfl_xor(acc, o);
+                acc = pd_wave_sum(acc);
                 if (c == 0) {
                     sh.lg[r] = acc;
                     gp(a.logits)[(size_t)8 * j + r] = acc;
