@@ -263,11 +263,19 @@ __device__ __forceinline__ void pd_colsum_put(f32x4 acc, f32x4 *red)
 }
 __device__ __forceinline__ float pd_colsum_read(const f32x4 *red, int col)
 {
+    // all 32 reads issued before the adds (four chains of 8, then their sum)
     const float *rf = reinterpret_cast<const float *>(red);
-    float r = rf[col];
+    float v[PD_T / 16];
 #pragma unroll
-    for (int g = 1; g < PD_T / 16; g++) r += rf[32 * g + col];
-    return r;
+    for (int g = 0; g < PD_T / 16; g++) v[g] = rf[32 * g + col];
+    float r[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        r[c] = v[8 * c];
+#pragma unroll
+        for (int g = 1; g < 8; g++) r[c] += v[8 * c + g];
+    }
+    return (r[0] + r[1]) + (r[2] + r[3]);
 }
 // one panel: thread tid < 32 gets column tid
 __device__ __forceinline__ float pd_colsum(f32x4 acc, f32x4 *red)
