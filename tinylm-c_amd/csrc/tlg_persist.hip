@@ -216,6 +216,29 @@ __device__ void pd_rmsnorm(const float *x, float gj, float *dst, int D, float *s
     __syncthreads();
 }
 
+// RMSNorm folded into the GEMV that follows it: xg[j] = x[j] g[j] (thread j
+// holds g[j]) and the waves' sums of x^2, then one barrier; the caller scales
+// the GEMV's column sums by s = pd_norm_scale(sw, D).  (The reference
+// normalises first, x * s * g, then multiplies; the two differ only in fp32
+// rounding.)
+__device__ __forceinline__ void pd_norm_prep(const float *x, float gj, float *xg, int D, float *sw)
+{
+    const int tid = threadIdx.x;
+    const float xr = x[min(tid, D - 1)];
+    const float xj = tid < D ? xr : 0.f;
+    if (tid < D) xg[tid] = xj * gj;
+    const float ss = pd_wave_sum(xj * xj);
+    if ((tid & 63) == 0) sw[tid >> 6] = ss;
+    __syncthreads();
+}
+__device__ __forceinline__ float pd_norm_scale(const float *sw, int D)
+{
+    float tot = sw[0];
+#pragma unroll
+    for (int w = 1; w < PD_NW; w++) tot += sw[w];
+    return 1.0f / sqrtf(tot / (float)D + 1e-5f);
+}
+
 // Column-panel GEMV.  Thread (c4 = tid & 7, rg = tid >> 3) holds
 // w[i] = W[(rg + 64 i) * N + col0 + 4 c4 .. + 3] for rows rg + 64 i < K
 // (rows past K load row K - 1, unused: every element is written, so the panel
@@ -232,10 +255,22 @@ __device__ __forceinline__ void pd_load_cols(f32x4 *w, const float *__restrict__
 template <int MAXI>
 __device__ __forceinline__ f32x4 pd_dot(const float *vin, const f32x4 *w, int K)
 {
-    // branch-free: every row's LDS read is issued at once (rows past K read row
-    // K - 1 and are not added)
+    // branch-free: every row's LDS read is issued at once.  K = 64 MAXI (every
+    // BASELINE shape) needs no guard; otherwise rows past K read row K - 1 and
+    // are not added.
     const int rg = threadIdx.x >> 3;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (K == 64 * MAXI) {
+#pragma unroll
+        for (int i = 0; i < MAXI; i++) {
+            const float xv = vin[rg + 64 * i];
+            acc.x = fmaf(xv, w[i].x, acc.x);
+            acc.y = fmaf(xv, w[i].y, acc.y);
+            acc.z = fmaf(xv, w[i].z, acc.z);
+            acc.w = fmaf(xv, w[i].w, acc.w);
+        }
+        return acc;
+    }
 #pragma unroll
     for (int i = 0; i < MAXI; i++) {
         const bool in = rg + 64 * i < K;
@@ -476,7 +511,7 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
     const int kvh = h / grp, key0 = tid >> R::LOG2NW, wd = tid & (NW - 1);
     int lo, cnt;
     pd_window(a, l, pos, &lo, &cnt);
-    pd_rmsnorm(sh.x, gn, sh.xn, D, sh.sw);
+    pd_norm_prep(sh.x, gn, sh.xn, D, sh.sw);
     pd_colsum_put(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]);
     pd_colsum_put(pd_dot<PD_MAXQ>(sh.xn, wb + PD_MAXQ, D), sh.red[1]);
     pd_colsum_put(pd_dot<PD_MAXQ>(sh.xn, wb + 2 * PD_MAXQ, D), sh.red[2]);
@@ -488,9 +523,10 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
     // q, k, v columns (thread 32 m + i: column i of q, k, v for m = 0, 1, 2);
     // RoPE of q and the new k (rope_apply's pairs (i, i + 16), the partner
     // column from the lane i ^ 16); new k and v in the ring's format
+    const float sn = pd_norm_scale(sh.sw, D);
     if (tid < 96) {
         const int m = tid >> 5, i = tid & 31;
-        const float c = pd_colsum_read(sh.red[m], i);
+        const float c = pd_colsum_read(sh.red[m], i) * sn;
         const float o = __shfl_xor(c, 16);
         const bool inpos = pos >= 0 && pos < a.maxpos;
         const float rot = inpos ? (i < 16 ? c * rc - o * rs : c * rc + o * rs) : NAN;
@@ -698,8 +734,8 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
             }
             bool normed = false;
             for (int g = PD_FIRST(NA + NO); g < g0 + NA + NO + NS; g += NB) {    // silu(xn . W1) * (xn . W3)
-                if (!normed) { pd_rmsnorm(sh.x, gn, sh.xn, D, sh.sw); normed = true; }
-                const float r = pd_colsum(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]);
+                if (!normed) { pd_norm_prep(sh.x, gn, sh.xn, D, sh.sw); normed = true; }
+                const float r = pd_colsum(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]) * pd_norm_scale(sh.sw, D);
                 const float u = __shfl(r, (tid & 15) + 16);               // W3 column of this W1 column
                 if (tid < 16)
                     pd_st(act + (size_t)(g - g0 - NA - NO) * 16 + tid, pd_word(r / (1.0f + expf(-r)) * u, tl + 2u));
