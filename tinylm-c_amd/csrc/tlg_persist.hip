@@ -133,14 +133,19 @@ __device__ __forceinline__ void pd_wait_stores()
 }
 
 // Wait until the n words src[0..n) carry `tag`; then dst[e] = (ADD ? dst[e] +
-// : ) their values.  Called by every thread; false after an abort.
+// : ) their values.  Called by every thread; false after an abort.  Each wave
+// polls its own words (thread tid: words tid + PD_T k) until they all carry
+// the tag, deciding with a wave vote, so the poll loop has no barrier; lane 0
+// checks the abort flag and the time limit every 8th round; one barrier at the
+// end joins the waves.
 template <int KPL, int ADD>
 __device__ bool pd_fetch(const u64 *src, int n, u32 tag, float *dst, u32 *abortp)
 {
     const int tid = threadIdx.x;
     const u64 t0 = wall_clock64();
-    for (;;) {
-        u64 w[KPL];
+    u64 w[KPL];
+    int stop = 0;
+    for (int it = 0;; it++) {
 #pragma unroll
         for (int k = 0; k < KPL; k++)
             w[k] = pd_ld(reinterpret_cast<const u64 *>(reinterpret_cast<const char *>(src) +
@@ -148,24 +153,27 @@ __device__ bool pd_fetch(const u64 *src, int n, u32 tag, float *dst, u32 *abortp
         int bad = 0;
 #pragma unroll
         for (int k = 0; k < KPL; k++) bad |= (tid + PD_T * k < n) && (u32)(w[k] >> 32) != tag;
-        if (!__syncthreads_or(bad)) {
-#pragma unroll
-            for (int k = 0; k < KPL; k++) {
-                const int e = tid + PD_T * k;
-                if (e < n) dst[e] = ADD ? dst[e] + __uint_as_float((u32)w[k]) : __uint_as_float((u32)w[k]);
-            }
-            __syncthreads();
-            return true;
-        }
-        int stop = 0;
-        if (tid == 0)
-            stop = __hip_atomic_load(gp(abortp), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u ||
-                   wall_clock64() - t0 > PD_SPIN;
-        if (__syncthreads_or(stop)) {
-            if (tid == 0) __hip_atomic_store(gp(abortp), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return false;
+        if (__ballot(bad) == 0ull) break;
+        if ((it & 7) == 7) {
+            int s = 0;
+            if ((tid & 63) == 0)
+                s = __hip_atomic_load(gp(abortp), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u ||
+                    wall_clock64() - t0 > PD_SPIN;
+            if (__ballot(s) != 0ull) { stop = 1; break; }
         }
     }
+    if (!stop) {
+#pragma unroll
+        for (int k = 0; k < KPL; k++) {
+            const int e = tid + PD_T * k;
+            if (e < n) dst[e] = ADD ? dst[e] + __uint_as_float((u32)w[k]) : __uint_as_float((u32)w[k]);
+        }
+    }
+    if (__syncthreads_or(stop)) {
+        if (tid == 0) __hip_atomic_store(gp(abortp), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+    }
+    return true;
 }
 
 // Cross-lane steps on the VALU (DPP) rather than through LDS permutes, which
