@@ -510,7 +510,7 @@ __device__ __forceinline__ bool pd_argmax(PdShared &sh, const u64 *cand, int NHI
 // with `tag`.
 template <int F16>
 __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_WB], float gn, float rc, float rs,
-                                             const u64 (&kw)[PD_MAXR], u64 (&vw)[PD_MAXR], const TlgDecPersist &a,
+                                             u64 (&kw)[PD_MAXR], u64 (&vw)[PD_MAXR], const TlgDecPersist &a,
                                              int l, int h, int pos, int D, int KD, int grp, u64 *ctxout, u32 tag)
 {
     typedef PdRing<F16> R;
@@ -550,9 +550,18 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
                     ((size_t)(pos % a.W) * KD + (size_t)kvh * 32) * sizeof(typename R::E);
         pd_st(reinterpret_cast<u64 *>(row) + w, R::pack((tid < NW ? sh.k : sh.v) + R::EPW * w));
     }
-    // scores: key t = key0 + KPR r; t < cnt - 1 from the ring, t = cnt - 1 the new
-    // row; the NW threads of a key sum their words' partial dots
+    // key t = key0 + KPR r; t < cnt - 1 come from the ring words loaded, the new
+    // row t = cnt - 1 (round nr, key slot ns) is spliced into its threads' words
+    const int nr = (cnt - 1) / KPR, ns = (cnt - 1) % KPR;
+    const bool newslot = key0 == ns;
+    const u64 knew = R::pack(sh.k + R::EPW * wd);
+#pragma unroll
+    for (int r = 0; r < MAXR; r++) kw[r] = (newslot && r == nr) ? knew : kw[r];
+    // scores: the NW threads of a key sum their words' partial dots
     const float scale = 1.0f / sqrtf(32.0f);
+    float qv[R::EPW];
+#pragma unroll
+    for (int e = 0; e < R::EPW; e++) qv[e] = sh.q[R::EPW * wd + e];
     float sc[MAXR];
     float mx = -INFINITY;
 #pragma unroll
@@ -560,11 +569,7 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
         const int t = key0 + KPR * r;
         float part = 0.f;
 #pragma unroll
-        for (int e = 0; e < R::EPW; e++) {
-            const int d = R::EPW * wd + e;
-            const float kn = sh.k[d];
-            part = fmaf(sh.q[d], t < cnt - 1 ? R::get(kw[r], e) : kn, part);
-        }
+        for (int e = 0; e < R::EPW; e++) part = fmaf(qv[e], R::get(kw[r], e), part);
         // the NW lanes of the key: butterflies inside quads (quad_perm), then the
         // two quads of an 8-lane group (row_ror:n reads lane (i - n) mod 16, so
         // lanes 0-3 of the group take row_ror:12, lanes 4-7 row_ror:4), for f32
@@ -601,6 +606,10 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
     const float inv = tot > 0.f ? 1.0f / tot : 0.f;
     // ctx[d] = sum_t p_t v_t[d]: thread (key slot, word) over its keys, then the
     // key slots of a word: shuffles in the wave, the 8 waves in order via LDS
+    // (keys t >= cnt hold clamped ring words, masked off)
+    const u64 vnew = R::pack(sh.v + R::EPW * wd);
+#pragma unroll
+    for (int r = 0; r < MAXR; r++) vw[r] = (newslot && r == nr) ? vnew : vw[r];
     float acc[R::EPW];
 #pragma unroll
     for (int e = 0; e < R::EPW; e++) acc[e] = 0.f;
@@ -609,11 +618,7 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
         const int t = key0 + KPR * r;
         const float p = sc[r] * inv;
 #pragma unroll
-        for (int e = 0; e < R::EPW; e++) {
-            const float vn = sh.v[R::EPW * wd + e];
-            const float vv = t < cnt - 1 ? R::get(vw[r], e) : vn;
-            acc[e] = t < cnt ? fmaf(p, vv, acc[e]) : acc[e];
-        }
+        for (int e = 0; e < R::EPW; e++) acc[e] = t < cnt ? fmaf(p, R::get(vw[r], e), acc[e]) : acc[e];
     }
     // the key slots of a word: for f16 the two slots of a 16-lane row meet with
     // row_ror:8, then each row's partials go through LDS, added in row order
