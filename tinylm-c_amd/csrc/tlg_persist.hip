@@ -133,14 +133,19 @@ __device__ __forceinline__ void pd_wait_stores()
 }
 
 // Wait until the n words src[0..n) carry `tag`; then dst[e] = (ADD ? dst[e] +
-// : ) their values.  Called by every thread; false after an abort.  Each wave
+// : ) their values, and with NORM (x += delta, n <= PD_T) the norm parts of the
+// new x for gain element gn (pd_norm_parts into xn, sw) before the closing
+// barrier.  Called by every thread; false after an abort.  Each wave
 // polls its own words (thread tid: words tid + PD_T k) until they all carry
 // the tag, deciding with a wave vote, so the poll loop has no barrier; lane 0
 // checks the abort flag and the time limit every 8th round; one barrier at the
 // end joins the waves.
-template <int KPL, int ADD>
-__device__ bool pd_fetch(const u64 *src, int n, u32 tag, float *dst, u32 *abortp)
+__device__ __forceinline__ void pd_norm_parts(float xv, float gj, float *xg, int D, float *sw);
+template <int KPL, int ADD, int NORM = 0>
+__device__ bool pd_fetch(const u64 *src, int n, u32 tag, float *dst, u32 *abortp, float gn = 0.f,
+                         float *xn = nullptr, float *sw = nullptr)
 {
+    static_assert(!NORM || (KPL == 1 && ADD), "the norm parts follow x += delta");
     const int tid = threadIdx.x;
     const u64 t0 = wall_clock64();
     u64 w[KPL];
@@ -163,11 +168,16 @@ __device__ bool pd_fetch(const u64 *src, int n, u32 tag, float *dst, u32 *abortp
         }
     }
     if (!stop) {
+        float nv = 0.f;
 #pragma unroll
         for (int k = 0; k < KPL; k++) {
             const int e = tid + PD_T * k;
-            if (e < n) dst[e] = ADD ? dst[e] + __uint_as_float((u32)w[k]) : __uint_as_float((u32)w[k]);
+            if (e < n) {
+                nv = ADD ? dst[e] + __uint_as_float((u32)w[k]) : __uint_as_float((u32)w[k]);
+                dst[e] = nv;
+            }
         }
+        if (NORM) pd_norm_parts(nv, gn, xn, n, sw);
     }
     if (__syncthreads_or(stop)) {
         if (tid == 0) __hip_atomic_store(gp(abortp), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -225,19 +235,17 @@ __device__ void pd_rmsnorm(const float *x, float gj, float *dst, int D, float *s
 }
 
 // RMSNorm folded into the GEMV that follows it: xg[j] = x[j] g[j] (thread j
-// holds g[j]) and the waves' sums of x^2, then one barrier; the caller scales
-// the GEMV's column sums by s = pd_norm_scale(sw, D).  (The reference
-// normalises first, x * s * g, then multiplies; the two differ only in fp32
-// rounding.)
-__device__ __forceinline__ void pd_norm_prep(const float *x, float gj, float *xg, int D, float *sw)
+// holds x[j] in xv and g[j] in gj) and the waves' sums of x^2, made visible by
+// the caller's next barrier; the GEMV's column sums are then scaled by s =
+// pd_norm_scale(sw, D).  (The reference normalises first, x * s * g, then
+// multiplies; the two differ only in fp32 rounding.)  Called by whole waves.
+__device__ __forceinline__ void pd_norm_parts(float xv, float gj, float *xg, int D, float *sw)
 {
     const int tid = threadIdx.x;
-    const float xr = x[min(tid, D - 1)];
-    const float xj = tid < D ? xr : 0.f;
+    const float xj = tid < D ? xv : 0.f;
     if (tid < D) xg[tid] = xj * gj;
     const float ss = pd_wave_sum(xj * xj);
     if ((tid & 63) == 0) sw[tid >> 6] = ss;
-    __syncthreads();
 }
 __device__ __forceinline__ float pd_norm_scale(const float *sw, int D)
 {
@@ -502,14 +510,15 @@ __device__ __forceinline__ bool pd_argmax(PdShared &sh, const u64 *cand, int NHI
     return true;
 }
 
-// One attention item (layer l, query head h) at position pos: RMSNorm (gain
-// element gn), the head's q and its KV head's k, v from the panel in wb, RoPE
+// One attention item (layer l, query head h) at position pos, after the norm
+// parts of x (sh.xn, sh.sw; gain an1): the head's q and its KV head's k, v
+// from the panel in wb scaled by the norm's s, RoPE
 // (this thread's factors rc, rs for pair tid & 15), the ring store (by the
 // group's first head), softmax attention over the window with the ring words
 // kw / vw already loaded (f32 rings: vw loaded here), then ctx_h published
 // with `tag`.
 template <int F16>
-__device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_WB], float gn, float rc, float rs,
+__device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_WB], float rc, float rs,
                                              u64 (&kw)[PD_MAXR], u64 (&vw)[PD_MAXR], const TlgDecPersist &a,
                                              int l, int h, int pos, int D, int KD, int grp, u64 *ctxout, u32 tag)
 {
@@ -519,7 +528,6 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
     const int kvh = h / grp, key0 = tid >> R::LOG2NW, wd = tid & (NW - 1);
     int lo, cnt;
     pd_window(a, l, pos, &lo, &cnt);
-    pd_norm_prep(sh.x, gn, sh.xn, D, sh.sw);
     pd_colsum_put(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]);
     pd_colsum_put(pd_dot<PD_MAXQ>(sh.xn, wb + PD_MAXQ, D), sh.red[1]);
     pd_colsum_put(pd_dot<PD_MAXQ>(sh.xn, wb + 2 * PD_MAXQ, D), sh.red[2]);
@@ -584,6 +592,10 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
         sc[r] = t < cnt ? part * scale : -INFINITY;
         mx = fmaxf(mx, sc[r]);
     }
+    // softmax: the maximum M over the waves first (fast_expf's error depends on
+    // its argument, so every p_t is exp(s_t - M) as the reference forms it);
+    // the sum and the unnormalised context then meet at one barrier, and the
+    // context is divided by the sum at the end
     mx = pd_wave_max(mx);
     if (lane == 0) sh.sw[wave] = mx;
     __syncthreads();
@@ -594,18 +606,14 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
 #pragma unroll
     for (int r = 0; r < MAXR; r++) {
         const int t = key0 + KPR * r;
-        sc[r] = t < cnt ? (a.exact ? expf(sc[r] - mx) : tlg_fast_expf(sc[r] - mx)) : 0.f;
+        const float e = a.exact ? expf(sc[r] - mx) : tlg_fast_expf(sc[r] - mx);
+        sc[r] = t < cnt ? e : 0.f;
         if (wd == 0) sum += sc[r];                             // once per key
     }
     sum = pd_wave_sum(sum);
     if (lane == 0) sh.sw[PD_NW + wave] = sum;
-    __syncthreads();
-    float tot = sh.sw[PD_NW];
-#pragma unroll
-    for (int w = 1; w < PD_NW; w++) tot += sh.sw[PD_NW + w];
-    const float inv = tot > 0.f ? 1.0f / tot : 0.f;
     // ctx[d] = sum_t p_t v_t[d]: thread (key slot, word) over its keys, then the
-    // key slots of a word: shuffles in the wave, the 8 waves in order via LDS
+    // key slots of a word: shuffles in the wave, the rows through LDS
     // (keys t >= cnt hold clamped ring words, masked off)
     const u64 vnew = R::pack(sh.v + R::EPW * wd);
 #pragma unroll
@@ -616,9 +624,8 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
 #pragma unroll
     for (int r = 0; r < MAXR; r++) {
         const int t = key0 + KPR * r;
-        const float p = sc[r] * inv;
 #pragma unroll
-        for (int e = 0; e < R::EPW; e++) acc[e] = t < cnt ? fmaf(p, R::get(vw[r], e), acc[e]) : acc[e];
+        for (int e = 0; e < R::EPW; e++) acc[e] = t < cnt ? fmaf(sc[r], R::get(vw[r], e), acc[e]) : acc[e];
     }
     // the key slots of a word: for f16 the two slots of a 16-lane row meet with
     // row_ror:8, then each row's partials go through LDS, added in row order
@@ -630,12 +637,39 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
     }
     __syncthreads();
     if (tid < 32) {
+        float tot = sh.sw[PD_NW];
+#pragma unroll
+        for (int w = 1; w < PD_NW; w++) tot += sh.sw[PD_NW + w];
         float cx = sh.ctxw[0][tid];
 #pragma unroll
         for (int rr = 1; rr < PD_T / 16; rr++) cx += sh.ctxw[rr][tid];
+        cx *= tot > 0.f ? 1.0f / tot : 0.f;
         if (writer) pd_wait_stores();                          // the ring row first
         pd_st(ctxout + tid, pd_word(cx, tag));
     }
+    __syncthreads();
+}
+
+// An O or W2 item: the 32 columns of the panel in wb against in[0..K), out[c]
+// = their sums, published with `tag`.
+template <int MAXI>
+__device__ __forceinline__ void pd_gemv_item(PdShared &sh, const float *in, const f32x4 (&wb)[PD_WB], int K, u64 *out,
+                                             u32 tag)
+{
+    const float r = pd_colsum(pd_dot<MAXI>(in, wb, K), sh.red[0]);
+    if (threadIdx.x < 32) pd_st(out + threadIdx.x, pd_word(r, tag));
+    __syncthreads();
+}
+
+// A SwiGLU item (after the norm parts of the layer's second norm): the 16 W1 and
+// the 16 W3 columns of the panel against xn, scaled by the norm's s, then
+// out[c] = silu(W1 col) * (W3 col) (:786, :3821-3823), published with `tag`.
+__device__ __forceinline__ void pd_swiglu_item(PdShared &sh, const f32x4 (&wb)[PD_WB], int D, u64 *out, u32 tag)
+{
+    const int tid = threadIdx.x;
+    const float r = pd_colsum(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]) * pd_norm_scale(sh.sw, D);
+    const float u = __shfl(r, (tid & 15) + 16);                   // W3 column of this W1 column
+    if (tid < 16) pd_st(out + tid, pd_word(r / (1.0f + expf(-r)) * u, tag));
     __syncthreads();
 }
 
@@ -690,7 +724,11 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
             tok = sh.tok;
             if (b == 0 && tid == 0 && a.toks_out) gp(a.toks_out)[t - 1] = tok;
         }
-        if (tid < D) sh.x[tid] = (tok >= 0 && tok < V) ? gp(P)[(size_t)tok * D + tid] : NAN;
+        {   // x = emb[tok], with the norm parts for the first item's gain (attention: an1)
+            const float xv = (tok >= 0 && tok < V) ? gp(P)[(size_t)min(tid, D - 1) + (size_t)tok * D] : NAN;
+            if (tid < D) sh.x[tid] = xv;
+            pd_norm_parts(xv, gn, sh.xn, D, sh.sw);
+        }
         pd_load_head(hb, P, min(b, NHI - 1), D);
         const float hg = pd_at<float>(P + lay0 + (size_t)L * per, 4u * (u32)min(tid, D - 1));
         const bool inpos = pos >= 0 && pos < a.maxpos;
@@ -721,23 +759,24 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
     } while (0)
 
             for (int g = PD_FIRST(0); g < g0 + NA; g += NB) {
-                if (g != PD_FIRST(0)) {      // a second attention item in this layer: its ring words
-                    int lo, cnt;
+                if (g != PD_FIRST(0)) {      // a second attention item in this layer: its ring words,
+                    int lo, cnt;             // and the norm parts again (the first one's softmax used sw)
                     pd_window(a, l, pos, &lo, &cnt);
                     pd_ring_load<F16, 1, F16>(kw, vw, sh.Kc[l], sh.Vc[l], (g - g0) / grp, KD, a.W, lo, cnt);
+                    pd_norm_parts(sh.x[min(tid, D - 1)], gn, sh.xn, D, sh.sw);
+                    __syncthreads();
                 }
-                pd_attention<F16>(sh, wb, gn, rc, rs, kw, vw, a, l, g - g0, pos, D, KD, grp,
+                pd_attention<F16>(sh, wb, rc, rs, kw, vw, a, l, g - g0, pos, D, KD, grp,
                                   ctx + (size_t)(g - g0) * 32, tl);
                 PD_NEXT(g);
             }
             for (int g = PD_FIRST(NA); g < g0 + NA + NO; g += NB) {        // O: ctx . Wo
                 if (!pd_fetch<1, 0>(ctx, D, tl, sh.in, abortp)) return;
-                const float r = pd_colsum(pd_dot<PD_MAXQ>(sh.in, wb, D), sh.red[0]);
-                if (tid < 32) pd_st(yo + (size_t)(g - g0 - NA) * 32 + tid, pd_word(r, tl + 1u));
-                __syncthreads();
+                pd_gemv_item<PD_MAXQ>(sh, sh.in, wb, D, yo + (size_t)(g - g0 - NA) * 32, tl + 1u);
                 PD_NEXT(g);
             }
-            if (!pd_fetch<1, 1>(yo, D, tl + 1u, sh.x, abortp)) return;     // x += O out
+            // x += O out, with the norm parts for the next item's gain (SwiGLU: an2)
+            if (!pd_fetch<1, 1, 1>(yo, D, tl + 1u, sh.x, abortp, gn, sh.xn, sh.sw)) return;
             if (l + 1 < L) {                 // ring words of the next layer's attention, early
                 const int h = attn_head(l + 1);
                 int lo, cnt;
@@ -745,24 +784,17 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
                 if (h >= 0)
                     pd_ring_load<F16, 1, F16>(kw, vw, sh.Kc[l + 1], sh.Vc[l + 1], h / grp, KD, a.W, lo, cnt);
             }
-            bool normed = false;
             for (int g = PD_FIRST(NA + NO); g < g0 + NA + NO + NS; g += NB) {    // silu(xn . W1) * (xn . W3)
-                if (!normed) { pd_norm_prep(sh.x, gn, sh.xn, D, sh.sw); normed = true; }
-                const float r = pd_colsum(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]) * pd_norm_scale(sh.sw, D);
-                const float u = __shfl(r, (tid & 15) + 16);               // W3 column of this W1 column
-                if (tid < 16)
-                    pd_st(act + (size_t)(g - g0 - NA - NO) * 16 + tid, pd_word(r / (1.0f + expf(-r)) * u, tl + 2u));
-                __syncthreads();
+                pd_swiglu_item(sh, wb, D, act + (size_t)(g - g0 - NA - NO) * 16, tl + 2u);
                 PD_NEXT(g);
             }
             for (int g = PD_FIRST(NA + NO + NS); g < g0 + NPL; g += NB) {       // act . W2
                 if (!pd_fetch<2, 0>(act, F, tl + 2u, sh.in, abortp)) return;
-                const float r = pd_colsum(pd_dot<PD_MAXFQ>(sh.in, wb, F), sh.red[0]);
-                if (tid < 32) pd_st(y2 + (size_t)(g - g0 - NA - NO - NS) * 32 + tid, pd_word(r, tl + 3u));
-                __syncthreads();
+                pd_gemv_item<PD_MAXFQ>(sh, sh.in, wb, F, y2 + (size_t)(g - g0 - NA - NO - NS) * 32, tl + 3u);
                 PD_NEXT(g);
             }
-            if (!pd_fetch<1, 1>(y2, D, tl + 3u, sh.x, abortp)) return;     // x += W2 out
+            // x += W2 out, with the norm parts for the next item's gain (attention: an1)
+            if (!pd_fetch<1, 1, 1>(y2, D, tl + 3u, sh.x, abortp, gn, sh.xn, sh.sw)) return;
 #undef PD_FIRST
 #undef PD_NEXT
         }
