@@ -205,19 +205,27 @@ __device__ __forceinline__ float pd_wave_sum(float x)
     x += pd_dpp<0x143, 0xc>(0.f, x);          // row_bcast:31 into rows 2, 3
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
 }
-__device__ __forceinline__ float pd_wave_max(float x)
+// The maximum (sum) over a wave's key groups when the NW lanes of a key hold
+// the same value: the two keys of a 16-lane row (NW = 8) meet by row_ror:8,
+// then the four rows by lane reads.
+__device__ __forceinline__ float pd_lane(float v, int l)
 {
-    x = fmaxf(x, pd_dpp<0x111, 0xf>(-INFINITY, x));
-    x = fmaxf(x, pd_dpp<0x112, 0xf>(-INFINITY, x));
-    x = fmaxf(x, pd_dpp<0x114, 0xf>(-INFINITY, x));
-    x = fmaxf(x, pd_dpp<0x118, 0xf>(-INFINITY, x));
-    x = fmaxf(x, pd_dpp<0x142, 0xa>(-INFINITY, x));
-    x = fmaxf(x, pd_dpp<0x143, 0xc>(-INFINITY, x));
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+template <int NW> __device__ __forceinline__ float pd_keys_max(float v)
+{
+    if (NW == 8) v = fmaxf(v, pd_dpp<0x128, 0xf>(-INFINITY, v));
+    return fmaxf(fmaxf(pd_lane(v, 0), pd_lane(v, 16)), fmaxf(pd_lane(v, 32), pd_lane(v, 48)));
+}
+template <int NW> __device__ __forceinline__ float pd_keys_sum(float v)
+{
+    if (NW == 8) v += pd_dpp<0x128, 0xf>(0.f, v);
+    return (pd_lane(v, 0) + pd_lane(v, 16)) + (pd_lane(v, 32) + pd_lane(v, 48));
 }
 
-// dst[j] = x[j] * s * g[j], s = 1 / sqrt(sum x^2 / D + 1e-5) (rmsnorm_fwd);
-// thread j < D holds its gain element gj.
+// dst[j] = x[j] * s * g[j], s = 1 / sqrt(sum x^2 / D + 1e-5) (rmsnorm_fwd,
+// tinylm.c:546; here the hardware reciprocal square root, within 2 ulp of the
+// reference's square root then divide); thread j < D holds its gain element gj.
 __device__ void pd_rmsnorm(const float *x, float gj, float *dst, int D, float *sw)
 {
     const int tid = threadIdx.x;
@@ -229,7 +237,7 @@ __device__ void pd_rmsnorm(const float *x, float gj, float *dst, int D, float *s
     float tot = sw[0];
 #pragma unroll
     for (int w = 1; w < PD_NW; w++) tot += sw[w];
-    const float s = 1.0f / sqrtf(tot / (float)D + 1e-5f);
+    const float s = rsqrtf(tot / (float)D + 1e-5f);
     if (tid < D) dst[tid] = xj * s * gj;
     __syncthreads();
 }
@@ -252,7 +260,7 @@ __device__ __forceinline__ float pd_norm_scale(const float *sw, int D)
     float tot = sw[0];
 #pragma unroll
     for (int w = 1; w < PD_NW; w++) tot += sw[w];
-    return 1.0f / sqrtf(tot / (float)D + 1e-5f);
+    return rsqrtf(tot / (float)D + 1e-5f);
 }
 
 // Column-panel GEMV.  Thread (c4 = tid & 7, rg = tid >> 3) holds
@@ -266,6 +274,29 @@ __device__ __forceinline__ void pd_load_cols(f32x4 *w, const float *__restrict__
 #pragma unroll
     for (int i = 0; i < MAXI; i++)
         w[i] = pd_at<f32x4>(W, 4u * ((u32)min(rg + 64 * i, K - 1) * (u32)N + (u32)(col0 + 4 * c4)));
+}
+
+// The rows of vin that thread tid's panel entries meet (rg + 64 i, clamped), read
+// once for several panels; pd_dot_r is pd_dot on them.
+template <int MAXI> __device__ __forceinline__ void pd_rows(const float *vin, int K, float (&xv)[MAXI])
+{
+    const int rg = threadIdx.x >> 3;
+#pragma unroll
+    for (int i = 0; i < MAXI; i++) xv[i] = vin[min(rg + 64 * i, K - 1)];
+}
+template <int MAXI> __device__ __forceinline__ f32x4 pd_dot_r(const float (&xv)[MAXI], const f32x4 *w, int K)
+{
+    const int rg = threadIdx.x >> 3;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < MAXI; i++) {
+        const bool in = K == 64 * MAXI || rg + 64 * i < K;
+        acc.x = in ? fmaf(xv[i], w[i].x, acc.x) : acc.x;
+        acc.y = in ? fmaf(xv[i], w[i].y, acc.y) : acc.y;
+        acc.z = in ? fmaf(xv[i], w[i].z, acc.z) : acc.z;
+        acc.w = in ? fmaf(xv[i], w[i].w, acc.w) : acc.w;
+    }
+    return acc;
 }
 
 template <int MAXI>
@@ -528,9 +559,13 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
     const int kvh = h / grp, key0 = tid >> R::LOG2NW, wd = tid & (NW - 1);
     int lo, cnt;
     pd_window(a, l, pos, &lo, &cnt);
-    pd_colsum_put(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]);
-    pd_colsum_put(pd_dot<PD_MAXQ>(sh.xn, wb + PD_MAXQ, D), sh.red[1]);
-    pd_colsum_put(pd_dot<PD_MAXQ>(sh.xn, wb + 2 * PD_MAXQ, D), sh.red[2]);
+    {
+        float xv[PD_MAXQ];
+        pd_rows<PD_MAXQ>(sh.xn, D, xv);
+        pd_colsum_put(pd_dot_r<PD_MAXQ>(xv, wb, D), sh.red[0]);
+        pd_colsum_put(pd_dot_r<PD_MAXQ>(xv, wb + PD_MAXQ, D), sh.red[1]);
+        pd_colsum_put(pd_dot_r<PD_MAXQ>(xv, wb + 2 * PD_MAXQ, D), sh.red[2]);
+    }
     if (!F16) {                          // f32 rings: V words now, for register room
         u64 none[PD_MAXR];
         pd_ring_load<F16, 0, 1>(none, vw, sh.Kc[l], sh.Vc[l], kvh, KD, a.W, lo, cnt);
@@ -596,7 +631,7 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
     // its argument, so every p_t is exp(s_t - M) as the reference forms it);
     // the sum and the unnormalised context then meet at one barrier, and the
     // context is divided by the sum at the end
-    mx = pd_wave_max(mx);
+    mx = pd_keys_max<NW>(mx);
     if (lane == 0) sh.sw[wave] = mx;
     __syncthreads();
     mx = sh.sw[0];
@@ -608,9 +643,9 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
         const int t = key0 + KPR * r;
         const float e = a.exact ? expf(sc[r] - mx) : tlg_fast_expf(sc[r] - mx);
         sc[r] = t < cnt ? e : 0.f;
-        if (wd == 0) sum += sc[r];                             // once per key
+        sum += sc[r];
     }
-    sum = pd_wave_sum(sum);
+    sum = pd_keys_sum<NW>(sum);
     if (lane == 0) sh.sw[PD_NW + wave] = sum;
     // ctx[d] = sum_t p_t v_t[d]: thread (key slot, word) over its keys, then the
     // key slots of a word: shuffles in the wave, the rows through LDS
