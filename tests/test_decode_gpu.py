@@ -347,6 +347,32 @@ def test_persist_equals_graph_steps(lib, shape):
     assert normwise_rel(row1, grow) <= TOL
 
 
+def test_persist_from_model_file(lib, tmp_path):
+    """A model file in the reference's format (magic, header, fp32 body,
+    tokenizer blob: model_save_bundle, tinylm.c:1895-1913) read by
+    host/tl_ckpt.h drives the decoder: its header gives the model and its
+    body the weights, and greedy decoding gives the tokens and logits of the
+    same weights passed in directly."""
+    import struct
+
+    import tlgemm
+    kw = dict(SMALL, win=12, full_every=2)
+    m, P = params(kw, 21)
+    path = tmp_path / "small.tlm"
+    with open(path, "wb") as f:                   # TLM5: the window fields are recorded
+        f.write(b"TLM5" + struct.pack("<13i", m.V, m.D, m.L, m.H, m.KV, m.F, m.T, 0, 0, 0, 0, 12, 2))
+        f.write(P.tobytes())
+        f.write(struct.pack("<i", 3) + b"tok")
+    info, Pf = tlgemm.host().load_checkpoint(path)
+    kf = {k: info[k] for k in ("V", "D", "L", "H", "KV", "F", "T", "n_mtp", "n_exp", "win", "full_every")}
+    assert kf == dict(kw, n_mtp=0, n_exp=0) and np.array_equal(Pf, P)
+    prompt = np.random.default_rng(22).integers(0, m.V, 9).astype(np.int32)
+    print("model file decode", flush=True)
+    _, want, wrow, _ = _persist_run(kw, P, 32, 1, prompt, [12])
+    _, got, grow, _ = _persist_run(kf, Pf, 32, 1, prompt, [12])
+    assert got == want and np.array_equal(grow, wrow)
+
+
 def test_persist_after_reprime(lib):
     """A second prefill keeps the exchange sequence (state[3]), so a later
     persistent launch never matches words an earlier one left: decoding the

@@ -240,6 +240,22 @@ class TlPlan(ctypes.Structure):
                 ("run", ctypes.c_int)]
 
 
+class TlCkpt(ctypes.Structure):
+    """host/tl_ckpt.h: the header of a tinylm.c model file."""
+    _fields_ = [(n, _i) for n in ("version", "V", "D", "L", "H", "KV", "F", "T", "eot", "tmpl", "n_mtp",
+                                  "n_exp", "win", "full_every", "n_shared", "qknorm", "topk")] + [
+        ("n_params", _sz), ("params_offset", _sz), ("tok_len", ctypes.c_longlong)]
+
+
+class CheckpointError(ValueError):
+    """A model file tl_ckpt_open / tl_ckpt_read refused; `code` is the
+    TL_CKPT_E* value."""
+
+    def __init__(self, code, text, path):
+        super().__init__(f"{path}: {text} (code {code})")
+        self.code = code
+
+
 class TlWeightMap(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in
                 ("emb", "an1", "wq", "wk", "wv", "wo", "an2", "w1", "w3", "w2", "nf", "mtp0", "total")]
@@ -490,6 +506,17 @@ class Host:
         d.tl_weight_map.restype = None
         d.tl_plan_free.argtypes = [P]
         d.tl_plan_free.restype = None
+        C = ctypes.POINTER(TlCkpt)
+        d.tl_ckpt_open.argtypes = [ctypes.c_char_p, C]
+        d.tl_ckpt_open.restype = _i
+        d.tl_ckpt_read.argtypes = [ctypes.c_char_p, C, _vp, _sz]
+        d.tl_ckpt_read.restype = _i
+        d.tl_ckpt_param_count.argtypes = [C]
+        d.tl_ckpt_param_count.restype = _sz
+        d.tl_ckpt_error.argtypes = [_i]
+        d.tl_ckpt_error.restype = ctypes.c_char_p
+        d.tl_ckpt_model.argtypes = [C, ctypes.POINTER(TlModel)]
+        d.tl_ckpt_model.restype = None
         d.tl_run_new.argtypes = [P, _i]
         d.tl_run_new.restype = _vp
         d.tl_run_free.argtypes = [_vp]
@@ -571,6 +598,23 @@ class Host:
         d.tl_decode_set_fused.argtypes = [_vp, _i]
         d.tl_decode_set_fused.restype = _i
         self.dll = d
+
+    def load_checkpoint(self, path):
+        """A tinylm.c model file (host/tl_ckpt.h): (header fields as a dict,
+        the fp32 parameters in map_weights' order as a numpy array).  Raises
+        CheckpointError for files the reader refuses (quantized TLQ files,
+        a bad magic, a truncated body)."""
+        import numpy as np
+        info = TlCkpt()
+        bpath = os.fsencode(path)
+        rc = self.dll.tl_ckpt_open(bpath, ctypes.byref(info))
+        if rc != 0:
+            raise CheckpointError(rc, self.dll.tl_ckpt_error(rc).decode(), path)
+        P = np.empty(info.n_params, np.float32)
+        rc = self.dll.tl_ckpt_read(bpath, ctypes.byref(info), P.ctypes.data, P.size)
+        if rc != 0:
+            raise CheckpointError(rc, self.dll.tl_ckpt_error(rc).decode(), path)
+        return {n: getattr(info, n) for n, _ in TlCkpt._fields_}, P
 
     def decode(self, model, W, kv_f16=1, exact_exp=0, maxpos=4096, mmax=8, pool=1):
         """Device-resident decoding (host/tl_decode.h)."""
