@@ -223,25 +223,6 @@ template <int NW> __device__ __forceinline__ float pd_keys_sum(float v)
     return (pd_lane(v, 0) + pd_lane(v, 16)) + (pd_lane(v, 32) + pd_lane(v, 48));
 }
 
-// dst[j] = x[j] * s * g[j], s = 1 / sqrt(sum x^2 / D + 1e-5) (rmsnorm_fwd,
-// tinylm.c:546; here the hardware reciprocal square root, within 2 ulp of the
-// reference's square root then divide); thread j < D holds its gain element gj.
-__device__ void pd_rmsnorm(const float *x, float gj, float *dst, int D, float *sw)
-{
-    const int tid = threadIdx.x;
-    const float xr = x[min(tid, D - 1)];
-    const float xj = tid < D ? xr : 0.f;
-    const float ss = pd_wave_sum(xj * xj);
-    if ((tid & 63) == 0) sw[tid >> 6] = ss;
-    __syncthreads();
-    float tot = sw[0];
-#pragma unroll
-    for (int w = 1; w < PD_NW; w++) tot += sw[w];
-    const float s = rsqrtf(tot / (float)D + 1e-5f);
-    if (tid < D) dst[tid] = xj * s * gj;
-    __syncthreads();
-}
-
 // RMSNorm folded into the GEMV that follows it: xg[j] = x[j] g[j] (thread j
 // holds x[j] in xv and g[j] in gj) and the waves' sums of x^2, made visible by
 // the caller's next barrier; the GEMV's column sums are then scaled by s =
@@ -255,6 +236,9 @@ __device__ __forceinline__ void pd_norm_parts(float xv, float gj, float *xg, int
     const float ss = pd_wave_sum(xj * xj);
     if ((tid & 63) == 0) sw[tid >> 6] = ss;
 }
+// s = 1 / sqrt(sum x^2 / D + 1e-5) (rmsnorm_fwd, tinylm.c:546) from the waves'
+// sums; the hardware reciprocal square root, within 2 ulp of the reference's
+// square root then divide.
 __device__ __forceinline__ float pd_norm_scale(const float *sw, int D)
 {
     float tot = sw[0];
@@ -828,17 +812,19 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
                 pd_gemv_item<PD_MAXFQ>(sh, sh.in, wb, F, y2 + (size_t)(g - g0 - NA - NO - NS) * 32, tl + 3u);
                 PD_NEXT(g);
             }
-            // x += W2 out, with the norm parts for the next item's gain (attention: an1)
-            if (!pd_fetch<1, 1, 1>(y2, D, tl + 3u, sh.x, abortp, gn, sh.xn, sh.sw)) return;
+            // x += W2 out, with the norm parts for the next item's gain (attention: an1;
+            // after the last layer the head's final-norm gain)
+            if (!pd_fetch<1, 1, 1>(y2, D, tl + 3u, sh.x, abortp, l + 1 < L ? gn : hg, sh.xn, sh.sw)) return;
 #undef PD_FIRST
 #undef PD_NEXT
         }
 
-        // ---- head: final RMSNorm, 8 vocabulary rows per item, their first maximum
+        // ---- head: 8 vocabulary rows per item against x g (final-norm gain), scaled
+        // by the norm's s, and their first maximum
         if (b < NHI) {
             const u32 th = tag0 + 4u * (u32)L;
             u64 *cand = xb + lay.cand + (size_t)(t & 1) * NHI * 2;
-            pd_rmsnorm(sh.x, hg, sh.xn, D, sh.sw);
+            const float s = pd_norm_scale(sh.sw, D);        // norm parts from the last x fetch
             for (int j = b; j < NHI; j += NB) {
                 f32x4 hw[2] = {hb[0], hb[1]};
                 if (j != b) pd_load_head(hw, P, j, D);
@@ -853,7 +839,7 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
                         acc = fmaf(f.z, hw[i].z, acc);
                         acc = fmaf(f.w, hw[i].w, acc);
                     }
-                acc = pd_wave_sum(acc);
+                acc = pd_wave_sum(acc) * s;
                 if (c == 0) {
                     sh.lg[r] = acc;
                     gp(a.logits)[(size_t)8 * j + r] = acc;
