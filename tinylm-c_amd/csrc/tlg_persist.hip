@@ -496,8 +496,20 @@ __device__ __forceinline__ u64 pd_argkey(float v, u32 i)
 
 // The first maximum over the argmax candidates of a token (argmax_v: ties to
 // the lowest index; no candidate above -inf gives token 0, as the reference's
-// scan does) into sh.tok: the keys' maximum through LDS, 8 at a time.  false
-// after an abort.
+// scan does) into sh.tok: each wave's largest key by DPP, then the 8 waves'
+// through LDS.  false after an abort.
+// The maximum of the lanes' unsigned words (row_shr scan, then row_bcast),
+// every lane gets it; 0 is the identity.
+__device__ __forceinline__ u32 pd_wave_umax(u32 x)
+{
+    x = max(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false));
+    x = max(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false));
+    x = max(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false));
+    x = max(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false));
+    x = max(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false));
+    x = max(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));
+    return (u32)__builtin_amdgcn_readlane((int)x, 63);
+}
 __device__ __forceinline__ bool pd_argmax(PdShared &sh, const u64 *cand, int NHI, u32 tag, u32 *abortp)
 {
     const int tid = threadIdx.x;
@@ -507,20 +519,18 @@ __device__ __forceinline__ bool pd_argmax(PdShared &sh, const u64 *cand, int NHI
         const u32 i = __float_as_uint(sh.in[2 * tid + 1]);
         kx = i == 0x7fffffffu ? 0 : pd_argkey(sh.in[2 * tid], i);
     }
-    sh.key[tid] = kx;
+    // a wave's largest key: its largest high word, then the largest low word
+    // among the lanes holding that high word; then the 8 waves' keys via LDS
+    const u32 hm = pd_wave_umax((u32)(kx >> 32));
+    const u32 lm = pd_wave_umax((u32)(kx >> 32) == hm ? (u32)kx : 0u);
+    if ((tid & 63) == 0) sh.key[tid >> 6] = ((u64)hm << 32) | lm;
     __syncthreads();
-    for (int n = PD_T / 8; n >= 1; n /= 8) {       // 64, then 8, then 1 keys
-        u64 m = 0;
-        if (tid < n) {
-            m = sh.key[8 * tid];
+    if (tid == 0) {
+        u64 m = sh.key[0];
 #pragma unroll
-            for (int j = 1; j < 8; j++) m = max(m, sh.key[8 * tid + j]);
-        }
-        __syncthreads();
-        if (tid < n) sh.key[tid] = m;
-        __syncthreads();
+        for (int w = 1; w < PD_NW; w++) m = max(m, sh.key[w]);
+        sh.tok = m == 0 ? 0 : (int)(~(u32)m);
     }
-    if (tid == 0) sh.tok = sh.key[0] == 0 ? 0 : (int)(~(u32)sh.key[0]);
     __syncthreads();
     return true;
 }
