@@ -707,7 +707,12 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
 {
     __shared__ PdShared sh;
     const int tid = threadIdx.x;
-    const int NB = gridDim.x, b = blockIdx.x;
+    // workgroup b runs on XCD b % 8 (round-robin dispatch); items are owned by the
+    // virtual index b' = (b % 8) NB / 8 + b / 8, so consecutive items (a layer's
+    // attention and O items, its W2 items) share an XCD, whose exchanges are
+    // shorter than across XCDs
+    const int NB = gridDim.x,
+              b = (NB % 8) ? (int)blockIdx.x : (int)(blockIdx.x % 8u) * (NB / 8) + (int)(blockIdx.x / 8u);
     const int D = a.D, F = a.F, V = a.V, L = a.L, H = a.H, KD = a.KV * 32, grp = a.H / a.KV;
     const int NA = H, NO = D / 32, NS = F / 16, NPL = NA + NO + NS + D / 32, NLI = L * NPL, NHI = V / 8;
     const u32 NPH = 4u * (u32)L + 1u;
