@@ -316,7 +316,7 @@ __device__ __forceinline__ f32x4 pd_dot(const float *vin, const f32x4 *w, int K)
 
 // The 64 row groups' partials of one panel: the two row groups of a 16-lane
 // row meet with row_ror:8 (lane ^ 8), then the 32 row pairs go through LDS
-// (red: 32 x 8 f32x4) and pd_colsum_read adds them in order.
+// (red: 32 x 8 f32x4) and pd_colsum_half adds them.
 #define PD_RED (PD_T / 16 * 8)
 __device__ __forceinline__ void pd_colsum_put(f32x4 acc, f32x4 *red)
 {
@@ -327,28 +327,42 @@ __device__ __forceinline__ void pd_colsum_put(f32x4 acc, f32x4 *red)
     acc.w += pd_dpp<0x128, 0xf>(0.f, acc.w);
     if ((tid & 8) == 0) red[(tid >> 4) * 8 + (tid & 7)] = acc;
 }
-__device__ __forceinline__ float pd_colsum_read(const f32x4 *red, int col)
+// Column col's sum read by two lanes (2 k, 2 k + 1): lane h adds row pairs
+// 16 h .. 16 h + 15 as two in-order chains of 8, (r0 + r1) or (r2 + r3), and
+// one quad_perm exchange forms (r0 + r1) + (r2 + r3) in both lanes.
+__device__ __forceinline__ float pd_colsum_half(const f32x4 *red, int col)
 {
-    // all 32 reads issued before the adds (four chains of 8, then their sum)
+    const int h = threadIdx.x & 1;
     const float *rf = reinterpret_cast<const float *>(red);
-    float v[PD_T / 16];
+    float v[16];
 #pragma unroll
-    for (int g = 0; g < PD_T / 16; g++) v[g] = rf[32 * g + col];
-    float r[4];
+    for (int g = 0; g < 16; g++) v[g] = rf[32 * (16 * h + g) + col];
+    float r0 = v[0], r1 = v[8];
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        r[c] = v[8 * c];
-#pragma unroll
-        for (int g = 1; g < 8; g++) r[c] += v[8 * c + g];
+    for (int g = 1; g < 8; g++) {
+        r0 += v[g];
+        r1 += v[8 + g];
     }
-    return (r[0] + r[1]) + (r[2] + r[3]);
+    const float r = r0 + r1;
+    return r + pd_dpp<0xB1, 0xf>(0.f, r);         // quad_perm [1, 0, 3, 2]: the other half
 }
-// one panel: thread tid < 32 gets column tid
-__device__ __forceinline__ float pd_colsum(f32x4 acc, f32x4 *red)
+// Which column lane t of a 64-lane group reads: column t / 2 (PAIRS 0), or for
+// t = 4 p + 2 m + h column p + 16 m (PAIRS 1: the columns i, i + 16 of a RoPE
+// pair or of a SwiGLU W1 / W3 pair sit in one quad, the partner at lane ^ 2).
+template <int PAIRS> __device__ __forceinline__ int pd_half_col(int t)
+{
+    return PAIRS ? ((t >> 2) & 15) + 16 * ((t >> 1) & 1) : (t >> 1) & 31;
+}
+__device__ __forceinline__ float pd_pair_other(float v)
+{
+    return pd_dpp<0x4E, 0xf>(0.f, v);             // quad_perm [2, 3, 0, 1]: lane ^ 2
+}
+// one panel: the lanes of wave 0 get the sum of column pd_half_col<PAIRS>(tid)
+template <int PAIRS> __device__ __forceinline__ float pd_colsum(f32x4 acc, f32x4 *red)
 {
     pd_colsum_put(acc, red);
     __syncthreads();
-    return threadIdx.x < 32 ? pd_colsum_read(red, threadIdx.x) : 0.f;
+    return threadIdx.x < 64 ? pd_colsum_half(red, pd_half_col<PAIRS>(threadIdx.x)) : 0.f;
 }
 
 // The weight panel of layer item g (index within a token) in thread order and
@@ -538,7 +552,7 @@ __device__ __forceinline__ bool pd_argmax(PdShared &sh, const u64 *cand, int NHI
 // One attention item (layer l, query head h) at position pos, after the norm
 // parts of x (sh.xn, sh.sw; gain an1): the head's q and its KV head's k, v
 // from the panel in wb scaled by the norm's s, RoPE
-// (this thread's factors rc, rs for pair tid & 15), the ring store (by the
+// (this thread's factors rc, rs for pair (tid >> 2) & 15), the ring store (by the
 // group's first head), softmax attention over the window with the ring words
 // kw / vw already loaded (f32 rings: vw loaded here), then ctx_h published
 // with `tag`.
@@ -569,15 +583,17 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
     // RoPE of q and the new k (rope_apply's pairs (i, i + 16), the partner
     // column from the lane i ^ 16); new k and v in the ring's format
     const float sn = pd_norm_scale(sh.sw, D);
-    if (tid < 96) {
-        const int m = tid >> 5, i = tid & 31;
-        const float c = pd_colsum_read(sh.red[m], i) * sn;
-        const float o = __shfl_xor(c, 16);
+    if (tid < 192) {                     // wave m reads panel m, pairs (i, i + 16) in quads
+        const int m = tid >> 6, i = pd_half_col<1>(tid);
+        const float c = pd_colsum_half(sh.red[m], i) * sn;
+        const float o = pd_pair_other(c);
         const bool inpos = pos >= 0 && pos < a.maxpos;
         const float rot = inpos ? (i < 16 ? c * rc - o * rs : c * rc + o * rs) : NAN;
-        if (m == 0) sh.q[i] = rot;
-        else if (m == 1) sh.k[i] = R::round(rot);
-        else sh.v[i] = R::round(c);
+        if ((tid & 1) == 0) {
+            if (m == 0) sh.q[i] = rot;
+            else if (m == 1) sh.k[i] = R::round(rot);
+            else sh.v[i] = R::round(c);
+        }
     }
     __syncthreads();
     const bool writer = (h % grp) == 0;
@@ -685,8 +701,9 @@ template <int MAXI>
 __device__ __forceinline__ void pd_gemv_item(PdShared &sh, const float *in, const f32x4 (&wb)[PD_WB], int K, u64 *out,
                                              u32 tag)
 {
-    const float r = pd_colsum(pd_dot<MAXI>(in, wb, K), sh.red[0]);
-    if (threadIdx.x < 32) pd_st(out + threadIdx.x, pd_word(r, tag));
+    const int tid = threadIdx.x;
+    const float r = pd_colsum<0>(pd_dot<MAXI>(in, wb, K), sh.red[0]);
+    if (tid < 64 && (tid & 1) == 0) pd_st(out + (tid >> 1), pd_word(r, tag));
     __syncthreads();
 }
 
@@ -696,9 +713,10 @@ __device__ __forceinline__ void pd_gemv_item(PdShared &sh, const float *in, cons
 __device__ __forceinline__ void pd_swiglu_item(PdShared &sh, const f32x4 (&wb)[PD_WB], int D, u64 *out, u32 tag)
 {
     const int tid = threadIdx.x;
-    const float r = pd_colsum(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]) * pd_norm_scale(sh.sw, D);
-    const float u = __shfl(r, (tid & 15) + 16);                   // W3 column of this W1 column
-    if (tid < 16) pd_st(out + tid, pd_word(r / (1.0f + expf(-r)) * u, tag));
+    // lanes 4 p, 4 p + 1 of wave 0 hold W1 column p, lanes 4 p + 2, 4 p + 3 its W3 column
+    const float r = pd_colsum<1>(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]) * pd_norm_scale(sh.sw, D);
+    const float u = pd_pair_other(r);
+    if (tid < 64 && (tid & 3) == 0) pd_st(out + (tid >> 2), pd_word(r / (1.0f + expf(-r)) * u, tag));
     __syncthreads();
 }
 
@@ -766,8 +784,9 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
         pd_load_head(hb, P, min(b, NHI - 1), D);
         const float hg = pd_at<float>(P + lay0 + (size_t)L * per, 4u * (u32)min(tid, D - 1));
         const bool inpos = pos >= 0 && pos < a.maxpos;
-        const float rc = inpos ? gp(a.cs)[(size_t)pos * 16 + (tid & 15)] : 0.f;
-        const float rs = inpos ? gp(a.sn)[(size_t)pos * 16 + (tid & 15)] : 0.f;
+        // RoPE factors of pair (tid >> 2) & 15, the pair this thread's quad reads
+        const float rc = inpos ? gp(a.cs)[(size_t)pos * 16 + ((tid >> 2) & 15)] : 0.f;
+        const float rs = inpos ? gp(a.sn)[(size_t)pos * 16 + ((tid >> 2) & 15)] : 0.f;
         {   // ring words of layer 0's attention
             const int h = attn_head(0);
             int lo, cnt;
