@@ -716,7 +716,10 @@ __device__ __forceinline__ void pd_swiglu_item(PdShared &sh, const f32x4 (&wb)[P
     // lanes 4 p, 4 p + 1 of wave 0 hold W1 column p, lanes 4 p + 2, 4 p + 3 its W3 column
     const float r = pd_colsum<1>(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]) * pd_norm_scale(sh.sw, D);
     const float u = pd_pair_other(r);
-    if (tid < 64 && (tid & 3) == 0) pd_st(out + (tid >> 2), pd_word(r / (1.0f + expf(-r)) * u, tag));
+    // silu(r) = r / (1 + e^-r) with the hardware exp2 and reciprocal (a few ulp
+    // from the reference's expf and divide)
+    const float e = __builtin_amdgcn_exp2f(-r * 1.44269504088896f);
+    if (tid < 64 && (tid & 3) == 0) pd_st(out + (tid >> 2), pd_word(r * __builtin_amdgcn_rcpf(1.0f + e) * u, tag));
     __syncthreads();
 }
 
