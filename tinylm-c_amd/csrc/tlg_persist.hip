@@ -567,6 +567,7 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
     const int kvh = h / grp, key0 = tid >> R::LOG2NW, wd = tid & (NW - 1);
     int lo, cnt;
     pd_window(a, l, pos, &lo, &cnt);
+    const float sn = pd_norm_scale(sh.sw, D);        // read before the softmax reuses sw
     {
         float xv[PD_MAXQ];
         pd_rows<PD_MAXQ>(sh.xn, D, xv);
@@ -582,7 +583,6 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
     // q, k, v columns (thread 32 m + i: column i of q, k, v for m = 0, 1, 2);
     // RoPE of q and the new k (rope_apply's pairs (i, i + 16), the partner
     // column from the lane i ^ 16); new k and v in the ring's format
-    const float sn = pd_norm_scale(sh.sw, D);
     if (tid < 192) {                     // wave m reads panel m, pairs (i, i + 16) in quads
         const int m = tid >> 6, i = pd_half_col<1>(tid);
         const float c = pd_colsum_half(sh.red[m], i) * sn;
@@ -714,7 +714,8 @@ __device__ __forceinline__ void pd_swiglu_item(PdShared &sh, const f32x4 (&wb)[P
 {
     const int tid = threadIdx.x;
     // lanes 4 p, 4 p + 1 of wave 0 hold W1 column p, lanes 4 p + 2, 4 p + 3 its W3 column
-    const float r = pd_colsum<1>(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]) * pd_norm_scale(sh.sw, D);
+    const float sn = pd_norm_scale(sh.sw, D);
+    const float r = pd_colsum<1>(pd_dot<PD_MAXQ>(sh.xn, wb, D), sh.red[0]) * sn;
     const float u = pd_pair_other(r);
     // silu(r) = r / (1 + e^-r) with the hardware exp2 and reciprocal (a few ulp
     // from the reference's expf and divide)
