@@ -681,16 +681,22 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
         if ((tid & 15) < NW) sh.ctxw[row][R::EPW * wd + e] = acc[e];
     }
     __syncthreads();
-    if (tid < 32) {
+    if (tid < 64) {                      // lanes 2 d, 2 d + 1: rows 0-15 and 16-31 of ctx[d]
         float tot = sh.sw[PD_NW];
 #pragma unroll
         for (int w = 1; w < PD_NW; w++) tot += sh.sw[PD_NW + w];
-        float cx = sh.ctxw[0][tid];
+        const int d = tid >> 1, r0 = 16 * (tid & 1);
+        float c0 = sh.ctxw[r0][d], c1 = sh.ctxw[r0 + 8][d];
 #pragma unroll
-        for (int rr = 1; rr < PD_T / 16; rr++) cx += sh.ctxw[rr][tid];
-        cx *= tot > 0.f ? 1.0f / tot : 0.f;
+        for (int rr = 1; rr < 8; rr++) {
+            c0 += sh.ctxw[r0 + rr][d];
+            c1 += sh.ctxw[r0 + 8 + rr][d];
+        }
+        float cx = c0 + c1;
+        cx += pd_dpp<0xB1, 0xf>(0.f, cx);             // quad_perm [1, 0, 3, 2]: the other half
+        cx *= tot > 0.f ? __builtin_amdgcn_rcpf(tot) : 0.f;
         if (writer) pd_wait_stores();                          // the ring row first
-        pd_st(ctxout + tid, pd_word(cx, tag));
+        if ((tid & 1) == 0) pd_st(ctxout + d, pd_word(cx, tag));
     }
     __syncthreads();
 }
