@@ -70,6 +70,17 @@ void *tlg_mirror(const void *host);
 int tlg_dev_sgemm_nn(float *Y, const float *X, const float *W, int M, int K, int N, void *stream);
 int tlg_dev_sgemm_nt_acc(float *dX, const float *dY, const float *W, int M, int K, int N, void *stream);
 int tlg_dev_sgemm_tn_acc(float *dW, const float *X, const float *dY, int M, int K, int N, void *stream);
+/* tlg_dev_sgemm_tn_acc without any device allocation.  No counterpart in the
+ * reference: this is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arithmetic and kernels; the split-reduction partials go
+ * to a fixed 16 MiB device array of the library (one per GPU, held until the
+ * process ends) instead of the workspace tlg_init allocates, and the call
+ * does not initialise the library.  Limit: K * N <= 2^21 floats (an 8 MiB
+ * dW), else TLG_EINVAL; the split count is capped to what the array holds.
+ * Calls that overlap on one GPU (two streams, two threads) share that array
+ * and race; serialise them. */
+int tlg_dev_sgemm_tn_acc_noalloc(float *dW, const float *X, const float *dY, int M, int K, int N, void *stream);
 /* dst[0..n) = 0 on `stream`, by a fill kernel (never a memset node, so a
  * captured graph replays it correctly).  The reference's memset() before an
  * accumulating GEMM, e.g. tinylm.c:1015, :1104, :1113, :1123, :1134. */

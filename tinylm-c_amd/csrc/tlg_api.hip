@@ -14,10 +14,6 @@ TlgState g_tlg = {0, 0, nullptr, nullptr, 0};
 static thread_local char t_err[512];
 static std::recursive_mutex g_mu;
 
-// Workspace for split reductions (64 MiB of partial sums): sized for the
-// largest split plan the launcher makes on the BASELINE shapes; a bigger plan
-// falls back to splits = 1.
-static const size_t kWsFloats = (size_t)16 << 20;
 
 int tlg_fail(int code, const char *fmt, ...)
 {
@@ -44,10 +40,10 @@ static int init_locked(int device)
     TLG_HIP(hipSetDevice(device));
     TLG_HIP(hipStreamCreateWithFlags(&g_tlg.stream, hipStreamNonBlocking));
     void *p = nullptr;
-    if (hipMalloc(&p, kWsFloats * sizeof(float)) != hipSuccess)
-        return tlg_fail(TLG_ENOMEM, "tlg_init: workspace of %zu bytes", kWsFloats * sizeof(float));
+    if (hipMalloc(&p, TLG_WS_FLOATS * sizeof(float)) != hipSuccess)
+        return tlg_fail(TLG_ENOMEM, "tlg_init: workspace of %zu bytes", TLG_WS_FLOATS * sizeof(float));
     g_tlg.ws = (float *)p;
-    g_tlg.ws_floats = kWsFloats;
+    g_tlg.ws_floats = TLG_WS_FLOATS;
     TLG_HIP(hipDeviceSynchronize());
     g_tlg.device = device;
     g_tlg.initialised = 1;

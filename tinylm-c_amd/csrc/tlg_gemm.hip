@@ -41,6 +41,7 @@
 // previous grouped launch.  The kernel boundary between the two launches is
 // what makes the partials visible, so a split costs no extra launch.
 #include "tlg_internal.h"
+#include <mutex>
 #include <stdio.h>
 #include <string.h>
 
@@ -735,21 +736,21 @@ static GemmPlan make_plan(int ci, int Mo, int No, int R, int splits, size_t ws_f
 // workgroups over the 256 CUs; when even 64x64 tiles are too few (small
 // outputs with long reductions, i.e. mm_atb's dW), split the reduction so
 // every split keeps >= 256 reduction steps.
-static GemmPlan plan_gemm(int Mo, int No, int R)
+static GemmPlan plan_gemm(int Mo, int No, int R, size_t ws_floats)
 {
     if (g_force_cfg >= 0 && g_force_cfg < kNumCfgs)
-        return make_plan(g_force_cfg, Mo, No, R, g_force_splits, g_tlg.ws_floats);
+        return make_plan(g_force_cfg, Mo, No, R, g_force_splits, ws_floats);
     static const int order[] = {0, 1, 2, 3};
     for (int k = 0; k < 4; k++) {
         const TileCfg &c = kCfgs[order[k]];
         const int tiles = cdiv(Mo, c.bm) * cdiv(No, c.bn);
-        if (tiles >= 240) return make_plan(order[k], Mo, No, R, 1, g_tlg.ws_floats);
+        if (tiles >= 240) return make_plan(order[k], Mo, No, R, 1, ws_floats);
     }
     const int tiles = cdiv(Mo, 64) * cdiv(No, 64);
     int splits = cdiv(256, tiles);
     const int maxs = R / 256 > 1 ? R / 256 : 1;
     if (splits > maxs) splits = maxs;
-    return make_plan(3, Mo, No, R, splits, g_tlg.ws_floats);
+    return make_plan(3, Mo, No, R, splits, ws_floats);
 }
 
 // Name of the kernel instance a device-pointer call with aligned operands
@@ -767,7 +768,7 @@ int tlg_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len, int *s
         if (splits) *splits = 1;
         return TLG_OK;
     }
-    const GemmPlan p = plan_gemm(Mo, No, R);
+    const GemmPlan p = plan_gemm(Mo, No, R, g_tlg.ws_floats);
     const TileCfg &c = kCfgs[p.ci];
     const int la = (kind == TLG_TN) ? OC : RC;
     const int lb = (kind == TLG_NT) ? RC : OC;
@@ -799,6 +800,43 @@ static int launch_reduce(const float *ws, float *C, int Mo, int No, int ldc, int
     return TLG_OK;
 }
 
+// One GEMM on `st` whose split partials (if any) go to ws[0, ws_floats).
+// Allocates nothing: the caller owns ws (the library's workspace, or the
+// no-allocation scratch below).  max_splits caps the reduction split.
+static int gemm_launch_ws(TlgKind kind, const float *A, const float *B, float *C, int Mo, int No, int R,
+                          int lda, int ldb, int ldc, int beta, float *ws, size_t ws_floats, hipStream_t st)
+{
+    if (tlg_gemv_fits(kind, Mo)) return tlg_gemv_launch(kind, A, B, C, Mo, No, R, lda, ldb, ldc, beta, st);
+
+    const int la = (kind == TLG_TN) ? OC : RC;
+    const int lb = (kind == TLG_NT) ? RC : OC;
+    // float4 staging needs 16-byte aligned operands whose contiguous extent
+    // and leading dimension are multiples of 4.
+    const bool vec = al16(A) && al16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
+                     (la == RC ? (R % 4 == 0) : (Mo % 4 == 0)) &&
+                     (lb == RC ? (R % 4 == 0) : (No % 4 == 0));
+    // the split count the library workspace would give, reduced to what ws holds
+    GemmPlan pl = plan_gemm(Mo, No, R, TLG_WS_FLOATS);
+    if (pl.splits > 1 && (size_t)pl.splits * Mo * No > ws_floats)
+        pl = make_plan(pl.ci, Mo, No, R, (int)(ws_floats / ((size_t)Mo * No)), ws_floats);
+
+    GemmArgs a;
+    a.A = A; a.B = B; a.C = C;
+    a.Mo = Mo; a.No = No; a.R = R;
+    a.lda = lda; a.ldb = ldb; a.ldc = ldc;
+    a.beta = beta;
+    a.tiles_n = pl.tiles_n; a.tiles = pl.tiles;
+    a.splits = pl.splits; a.rps = pl.rps;
+    a.ws = ws;
+    const int grid = pl.tiles * pl.splits;
+    if (la == RC && lb == OC)      launch_kind<RC, OC>(pl.ci, a, grid, vec, st);
+    else if (la == RC && lb == RC) launch_kind<RC, RC>(pl.ci, a, grid, vec, st);
+    else                           launch_kind<OC, OC>(pl.ci, a, grid, vec, st);
+    TLG_HIP(hipGetLastError());
+    if (pl.splits > 1) return launch_reduce(ws, C, Mo, No, ldc, pl.splits, beta, st);
+    return TLG_OK;
+}
+
 int tlg_gemm_launch(TlgKind kind, const float *A, const float *B, float *C,
                     int Mo, int No, int R, int lda, int ldb, int ldc, int beta,
                     hipStream_t st)
@@ -820,33 +858,61 @@ int tlg_gemm_launch(TlgKind kind, const float *A, const float *B, float *C,
     // left for its successor
     rc = tlg_group_flush_launch(st);
     if (rc) return rc;
+    return gemm_launch_ws(kind, A, B, C, Mo, No, R, lda, ldb, ldc, beta, g_tlg.ws, g_tlg.ws_floats, st);
+}
 
-    if (tlg_gemv_fits(kind, Mo)) return tlg_gemv_launch(kind, A, B, C, Mo, No, R, lda, ldb, ldc, beta, st);
+// --------------------------------------------- mm_atb without allocation --
+// Callers that must not allocate device memory (code under HIP graph
+// capture, serving loops, harnesses that forbid hipMalloc) get mm_atb with
+// its split partials in this fixed array instead of the library workspace.
+// Each GPU the library runs on holds its own copy until the process ends.
+// Host code never passes `scratch` itself to a kernel (on the host the name
+// is only a stand-in); it uses the device address hipGetSymbolAddress gives
+// for the current device, looked up once per device.
+#define TLG_SCRATCH_FLOATS ((size_t)4 << 20)          // 16 MiB
+static __device__ __align__(256) float scratch[TLG_SCRATCH_FLOATS];
 
-    const int la = (kind == TLG_TN) ? OC : RC;
-    const int lb = (kind == TLG_NT) ? RC : OC;
-    // float4 staging needs 16-byte aligned operands whose contiguous extent
-    // and leading dimension are multiples of 4.
-    const bool vec = al16(A) && al16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
-                     (la == RC ? (R % 4 == 0) : (Mo % 4 == 0)) &&
-                     (lb == RC ? (R % 4 == 0) : (No % 4 == 0));
-    const GemmPlan pl = plan_gemm(Mo, No, R);
+#define TLG_MAX_DEVICES 64
+static float *g_scratch_dev[TLG_MAX_DEVICES];
+static std::mutex g_scratch_mu;
 
-    GemmArgs a;
-    a.A = A; a.B = B; a.C = C;
-    a.Mo = Mo; a.No = No; a.R = R;
-    a.lda = lda; a.ldb = ldb; a.ldc = ldc;
-    a.beta = beta;
-    a.tiles_n = pl.tiles_n; a.tiles = pl.tiles;
-    a.splits = pl.splits; a.rps = pl.rps;
-    a.ws = g_tlg.ws;
-    const int grid = pl.tiles * pl.splits;
-    if (la == RC && lb == OC)      launch_kind<RC, OC>(pl.ci, a, grid, vec, st);
-    else if (la == RC && lb == RC) launch_kind<RC, RC>(pl.ci, a, grid, vec, st);
-    else                           launch_kind<OC, OC>(pl.ci, a, grid, vec, st);
-    TLG_HIP(hipGetLastError());
-    if (pl.splits > 1) return launch_reduce(g_tlg.ws, C, Mo, No, ldc, pl.splits, beta, st);
+static int scratch_for_current_device(float **out)
+{
+    int dev = -1;
+    TLG_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= TLG_MAX_DEVICES) return tlg_fail(TLG_EINVAL, "no-alloc scratch: device %d", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void *p = nullptr;
+        TLG_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return tlg_fail(TLG_EHIP, "no-alloc scratch: no device address on device %d", dev);
+        g_scratch_dev[dev] = (float *)p;
+    }
+    *out = g_scratch_dev[dev];
     return TLG_OK;
+}
+
+extern "C" int tlg_dev_sgemm_tn_acc_noalloc(float *dW, const float *X, const float *dY, int M, int K, int N,
+                                            void *stream)
+{
+    if (M < 0 || K < 0 || N < 0) return tlg_fail(TLG_EINVAL, "negative dimension");
+    if ((size_t)K * N > TLG_SCRATCH_FLOATS / 2)
+        return tlg_fail(TLG_EINVAL,
+                        "tlg_dev_sgemm_tn_acc_noalloc: dW of %d x %d floats exceeds the no-allocation limit of "
+                        "%zu floats (half the %zu-float scratch)",
+                        K, N, TLG_SCRATCH_FLOATS / 2, TLG_SCRATCH_FLOATS);
+    if (K == 0 || N == 0 || M == 0) return TLG_OK;         // mm_atb adds nothing
+    if (!dW || !X || !dY) return tlg_fail(TLG_EINVAL, "NULL pointer");
+    hipStream_t st = (hipStream_t)stream;
+    float *ws = nullptr;
+    int rc = scratch_for_current_device(&ws);
+    if (rc) return rc;
+    // partials a grouped launch left for its successor must land first
+    if (g_tlg.initialised) {
+        rc = tlg_group_flush_launch(st);
+        if (rc) return rc;
+    }
+    return gemm_launch_ws(TLG_TN, X, dY, dW, K, N, M, K, N, N, 1, ws, TLG_SCRATCH_FLOATS, st);
 }
 
 // ------------------------------------------------------- grouped launch --

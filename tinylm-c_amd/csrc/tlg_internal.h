@@ -15,6 +15,11 @@ int tlg_fail(int code, const char *fmt, ...);
         if (e_ != hipSuccess) return tlg_fail_hip(e_, #call, __FILE__, __LINE__); \
     } while (0)
 
+// Workspace for split reductions (64 MiB of partial sums), allocated by
+// tlg_init: sized for the largest split plan the launchers make on the
+// BASELINE shapes; a bigger plan falls back to fewer splits.
+#define TLG_WS_FLOATS ((size_t)16 << 20)
+
 // Library state shared by the kernels' launchers (tlg_api.hip owns it).
 struct TlgState {
     int initialised;

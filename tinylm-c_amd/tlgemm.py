@@ -38,6 +38,7 @@ SIGNATURES = {
     "tlg_dev_sgemm_nn": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "tlg_dev_sgemm_nt_acc": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "tlg_dev_sgemm_tn_acc": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "tlg_dev_sgemm_tn_acc_noalloc": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "tlg_dev_zero": (_i, [_vp, _sz, _vp]),
     "tlg_dev_malloc": (_vp, [_sz]),
     "tlg_dev_free": (_i, [_vp]),
