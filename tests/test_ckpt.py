@@ -158,3 +158,43 @@ def test_refused_files(host, tmp_path):
     # a TLM1 file (no tokenizer field) of exactly header + body is whole
     write_model(tmp_path / "v1.bin", 1, BASE, P)
     assert host.load_checkpoint(tmp_path / "v1.bin")[0]["tok_len"] == -1
+
+
+E_UNSUP = -6
+
+
+def test_models_the_step_cannot_run_are_refused(host, tmp_path):
+    """QK-norm gains shift every later weight (map_weights, tinylm.c:377-381),
+    shared experts are refused by the reference itself (check_supported,
+    :1946-1953) and top-k > 1 routing is not the top-1 layer built here: the
+    header reads, but tl_ckpt_model refuses to describe such a model."""
+    def model_rc(version, cfg):
+        info = tlgemm.TlCkpt(version=version, **{k: int(cfg.get(k, 0)) for k in FIELDS[:HDR_INTS[version]]})
+        m = tlgemm.TlModel()
+        return host.dll.tl_ckpt_model(ctypes.byref(info), ctypes.byref(m)), m
+
+    rc, m = model_rc(6, dict(BASE, qknorm=1))
+    assert rc == E_UNSUP and m.V == 0
+    assert model_rc(6, dict(BASE, n_exp=4, n_shared=1))[0] == E_UNSUP
+    assert model_rc(7, dict(BASE, n_exp=4, topk=2))[0] == E_UNSUP
+    assert model_rc(7, dict(BASE, n_exp=4, topk=1))[0] == 0
+    assert model_rc(7, dict(BASE, topk=2))[0] == 0                # dense: topk unused
+    assert host.dll.tl_ckpt_error(E_UNSUP).decode().startswith("model uses QK-norm")
+
+
+def test_header_whose_count_overflows_is_refused(host, tmp_path):
+    """A crafted header whose parameter count does not fit in 64-bit byte
+    offsets is refused as describing no model (not wrapped to a small count
+    that would pass the length check)."""
+    cfg = dict(BASE, D=1 << 24, F=1 << 24, H=1 << 19, KV=1, n_exp=65536, n_shared=65536, L=65536)
+    write_model(tmp_path / "big.bin", 6, cfg, np.zeros(4, np.float32))
+    with pytest.raises(tlgemm.CheckpointError) as e:
+        host.load_checkpoint(tmp_path / "big.bin")
+    assert e.value.code == E_SHAPE
+    # the largest fields a header can hold, still refused without wrapping
+    cfg = dict(BASE, V=2**31 - 1, D=2**31 - 1, F=2**31 - 1, H=1, KV=1, L=2**31 - 1, n_exp=2**31 - 1,
+               n_shared=2**31 - 1, n_mtp=2**31 - 1)
+    write_model(tmp_path / "max.bin", 6, cfg, np.zeros(4, np.float32))
+    with pytest.raises(tlgemm.CheckpointError) as e:
+        host.load_checkpoint(tmp_path / "max.bin")
+    assert e.value.code == E_SHAPE

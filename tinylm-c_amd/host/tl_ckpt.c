@@ -11,30 +11,37 @@
 /* header ints by version (hdr_ints, tinylm.c:1692-1700) */
 static const int k_hdr_ints[8] = {0, 8, 9, 10, 11, 13, 15, 16};
 
+/* param_count's terms in unsigned 128-bit arithmetic: every field is below
+ * 2^31, so the largest term, L * (n_exp + n_shared) * 3 * D * F, stays below
+ * 2^127 and nothing wraps here; callers refuse a total that does not fit in
+ * a size_t of bytes. */
+typedef unsigned __int128 u128;
+static u128 param_count_wide(const TlCkpt *c)
+{
+    const u128 D = (u128)c->D, F = (u128)c->F, hd = (u128)(c->D / c->H);
+    const u128 KD = (u128)c->KV * hd;
+    const u128 slots = c->n_exp > 0 ? (u128)c->n_exp + (u128)c->n_shared : 1;
+    const u128 per = D + D * D + 2 * D * KD + D * D + (c->qknorm ? 2 * hd : 0) + D +
+                     (c->n_exp > 0 ? D * (u128)c->n_exp : 0) + slots * 3 * D * F;
+    return (u128)c->V * D + (u128)c->L * per + D + (u128)c->n_mtp * D * D;
+}
+
 size_t tl_ckpt_param_count(const TlCkpt *c)
 {
-    const size_t D = (size_t)c->D, F = (size_t)c->F, hd = (size_t)(c->D / c->H);
-    const size_t KD = (size_t)c->KV * hd;
-    const size_t slots = c->n_exp > 0 ? (size_t)c->n_exp + (size_t)c->n_shared : 1;
-    const size_t per = D + D * D + 2 * D * KD + D * D + (c->qknorm ? 2 * hd : 0) + D +
-                       (c->n_exp > 0 ? D * (size_t)c->n_exp : 0) + slots * 3 * D * F;
-    return (size_t)c->V * D + (size_t)c->L * per + D + (size_t)c->n_mtp * D * D;
+    const u128 n = param_count_wide(c);
+    return n > (u128)(SIZE_MAX / 4) ? 0 : (size_t)n;
 }
 
 /* The reference derives sizes from any header (cfg_from_hdr, cfg_derive); only
- * headers whose sizes mean nothing (non-positive dimensions, negative counts,
- * sizes that would overflow) are refused here. */
+ * headers whose sizes mean nothing (non-positive dimensions, negative counts)
+ * or whose parameter count does not fit in memory addresses are refused. */
 static int shape_ok(const TlCkpt *c)
 {
     if (c->V <= 0 || c->D <= 0 || c->L <= 0 || c->H <= 0 || c->KV <= 0 || c->F <= 0 || c->T <= 0) return 0;
     if (c->n_mtp < 0 || c->n_exp < 0 || c->n_shared < 0 || c->win < 0 || c->full_every < 0 || c->topk < 0)
         return 0;
-    /* keep every product in param_count far from size_t overflow */
-    const int64_t big = (int64_t)1 << 24;
-    if (c->V > big || c->D > big || c->F > big || c->L > 65536 || c->n_exp > 65536 || c->n_shared > 65536 ||
-        c->n_mtp > 65536)
-        return 0;
-    return 1;
+    const u128 n = param_count_wide(c);
+    return n >= 1 && n <= (u128)(SIZE_MAX / 4);
 }
 
 static void fill_fields(TlCkpt *c, const int32_t *h)
@@ -71,8 +78,11 @@ int tl_ckpt_open(const char *path, TlCkpt *c)
     if (!shape_ok(c)) { rc = TL_CKPT_ESHAPE; goto out; }
     c->n_params = tl_ckpt_param_count(c);
     c->params_offset = 4 + 4 * (size_t)nh;
+    /* the body must fit in what follows the header (compared without
+     * forming 4 * n_params, which a crafted header could make wrap) */
+    if ((uint64_t)size < (uint64_t)c->params_offset ||
+        ((uint64_t)size - c->params_offset) / 4 < (uint64_t)c->n_params) { rc = TL_CKPT_ETRUNC; goto out; }
     const uint64_t end_params = (uint64_t)c->params_offset + 4 * (uint64_t)c->n_params;
-    if ((uint64_t)size < end_params) { rc = TL_CKPT_ETRUNC; goto out; }
     /* model_load_full reads the tokenizer length after the parameters from
      * TLM2 on, when the file still holds 4 bytes; a blob it announces must fit */
     if (c->version >= 2 && (uint64_t)size >= end_params + 4) {
@@ -98,14 +108,21 @@ int tl_ckpt_read(const char *path, const TlCkpt *c, float *P, size_t n)
     return rc;
 }
 
-void tl_ckpt_model(const TlCkpt *c, TlModel *m)
+int tl_ckpt_model(const TlCkpt *c, TlModel *m)
 {
     memset(m, 0, sizeof *m);
+    /* Layouts the training step and the decoder would misread: QK-norm gains
+     * sit between Wo and an2 (map_weights, tinylm.c:377-381) and shift every
+     * later weight; shared experts are refused by the reference itself
+     * (check_supported, :1946-1953); routing to more than one expert is not
+     * the top-1 layer built here (moe_route, :814-827). */
+    if (c->qknorm != 0 || c->n_shared > 0 || (c->n_exp > 0 && c->topk > 1)) return TL_CKPT_EUNSUP;
     m->V = c->V; m->D = c->D; m->L = c->L; m->H = c->H;
     m->KV = c->KV; m->F = c->F; m->T = c->T;
     m->n_mtp = c->n_mtp; m->n_exp = c->n_exp;
     m->win = c->win; m->full_every = c->full_every;
     m->rope_base = 10000.0f;
+    return TL_CKPT_OK;
 }
 
 const char *tl_ckpt_error(int code)
@@ -117,6 +134,7 @@ const char *tl_ckpt_error(int code)
     case TL_CKPT_EQUANT: return "quantized model file (TLQ1-TLQ4): not read by the fp32 path";
     case TL_CKPT_ESHAPE: return "header fields describe no model";
     case TL_CKPT_ETRUNC: return "file shorter than its header announces";
+    case TL_CKPT_EUNSUP: return "model uses QK-norm, shared experts or top-k > 1 routing, which this build does not run";
     default: return "unknown error";
     }
 }

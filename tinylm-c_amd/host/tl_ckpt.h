@@ -40,6 +40,7 @@ typedef struct {
 #define TL_CKPT_EQUANT -3             /* a quantized TLQ1-TLQ4 file */
 #define TL_CKPT_ESHAPE -4             /* header fields that describe no model */
 #define TL_CKPT_ETRUNC -5             /* the file ends before what its header announces */
+#define TL_CKPT_EUNSUP -6             /* a model the step / decoder here cannot run */
 
 /* Parse the header of `path` into *c and check that the file holds the
  * parameters (and the tokenizer blob it announces).  TL_CKPT_OK or an error
@@ -49,7 +50,8 @@ int tl_ckpt_open(const char *path, TlCkpt *c);
 /* param_count (tinylm.c:345-358) of the model c describes: embedding, per
  * layer an1, Wq, Wk, Wv, Wo, the QK-norm gains when qknorm, an2, the router
  * when n_exp > 0, the FFN of every expert slot (n_exp + n_shared routed and
- * shared experts, or 1 dense FFN), then the final norm and the n_mtp heads. */
+ * shared experts, or 1 dense FFN), then the final norm and the n_mtp heads.
+ * 0 when the count times 4 bytes does not fit in a size_t. */
 size_t tl_ckpt_param_count(const TlCkpt *c);
 
 /* Read the c->n_params parameters of `path` (opened by tl_ckpt_open) into P,
@@ -57,8 +59,11 @@ size_t tl_ckpt_param_count(const TlCkpt *c);
 int tl_ckpt_read(const char *path, const TlCkpt *c, float *P, size_t n);
 
 /* The model fields the training step and the decoder take (rope_base 10000,
- * as cfg_from_hdr sets it). */
-void tl_ckpt_model(const TlCkpt *c, TlModel *m);
+ * as cfg_from_hdr sets it).  TL_CKPT_OK, or TL_CKPT_EUNSUP (and *m zeroed)
+ * for a model they would misread: QK-norm gains (qknorm != 0), shared
+ * experts (n_shared > 0, which the reference refuses too) or MoE routing to
+ * topk > 1 experts. */
+int tl_ckpt_model(const TlCkpt *c, TlModel *m);
 
 /* A short text for an error code. */
 const char *tl_ckpt_error(int code);

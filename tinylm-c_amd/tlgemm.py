@@ -517,7 +517,7 @@ class Host:
         d.tl_ckpt_error.argtypes = [_i]
         d.tl_ckpt_error.restype = ctypes.c_char_p
         d.tl_ckpt_model.argtypes = [C, ctypes.POINTER(TlModel)]
-        d.tl_ckpt_model.restype = None
+        d.tl_ckpt_model.restype = _i
         d.tl_run_new.argtypes = [P, _i]
         d.tl_run_new.restype = _vp
         d.tl_run_free.argtypes = [_vp]
