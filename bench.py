@@ -353,16 +353,58 @@ def probes(lib, stream):
     return {"hbm_copy_gbs": round(hbm, 1), "copy_bytes_each_way": 4 * n, "mfma_fp32_tflops": round(mfma, 1)}
 
 
-def cpu_baseline(host, cfgname, steps, threads):
-    """The reference's own mm / mm_bt / mm_atb (oracle/_ref, compiled from
-    tinylm.c) running the same plan on host cores; falls back to the
-    fixture-pinned restatement (kind "port") when _ref is absent."""
+def host_cpu_share():
+    """Threads for the CPU baseline: the physical cores this process may run
+    on (distinct (package, core) pairs of its affinity set, so no two threads
+    share a core's SMT siblings), capped by the box's CPU share for one GPU
+    when OMP_NUM_THREADS states it (16 on the GPU boxes).  Returns (threads,
+    facts about the host) -- read at run time, printed in the report."""
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            with open(base + "physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(base + "core_id") as f:
+                core = f.read().strip()
+            cores.add((pkg, core))
+        except OSError:
+            cores.add(("?", str(c)))
+    phys = len(cores)
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(phys, share) if share > 0 else phys
+    return max(threads, 1), {"affinity_cpus": len(cpus), "physical_cores": phys,
+                             "omp_num_threads_env": share or None}
+
+
+CPU_FLAGS = ("gcc -O3 -march=x86-64-v3 -ffast-math -funroll-loops -fopenmp -flto (the reference's portable "
+             "flags; x86-64-v3: 256-bit AVX2 vectors, as -mprefer-vector-width=256)")
+
+
+def median_time(fn, reps, warmup=2):
+    """2 untimed warmups (as cmd_bench, tinylm.c:4732), then the median of
+    `reps` timed runs, in seconds."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2], ts
+
+
+def cpu_baseline(host, cfgname, reps, threads, facts):
+    """The build's CPU restatement of mm / mm_bt / mm_atb (oracle/liboracle:
+    the reference's blocking and FMA chains, bit-identical to tinylm.c's own
+    kernels on the committed fixtures) running the whole plan on host cores,
+    OpenMP static over the reference's 4-row blocks (tinylm.c:447-448, :515)."""
     import numpy as np
     import oracle
-    try:
-        prims, kind = oracle.Reference(), "reference"
-    except FileNotFoundError:
-        prims, kind = oracle.Oracle(), "port"
+    prims = oracle.Oracle()
+    prims.set_pool(1)
     prims.set_threads(threads)
     cfg = TRAIN[cfgname]
     plan = host.plan_train(**cfg)
@@ -374,33 +416,31 @@ def cpu_baseline(host, cfgname, steps, threads):
         if init != 3:
             a *= np.float32(scale[init])
         arrays[name] = a
-    oracle.run_plan_cpu(plan, arrays, prims)           # warmup
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        oracle.run_plan_cpu(plan, arrays, prims)
-    dt = time.perf_counter() - t0
+    calls = oracle.plan_calls_native(plan, arrays)
+    dt, ts = median_time(lambda: prims.run_calls(calls, 1), reps)
     return {
-        "value": round(cfg["R"] * steps / dt, 1), "unit": "train tokens/s (GEMM set only)",
-        "cores": threads, "kind": kind,
-        "sample": f"{steps} full {cfgname} GEMM-set steps ({sum(1 for c in plan.calls if c['op'] != 'zero')} "
-                  f"calls each) after 1 warmup, OpenMP static, {threads} threads, gcc -O3 -ffast-math "
-                  f"-funroll-loops -march=x86-64-v3; {dt:.1f} s timed",
-        "s_per_step": round(dt / steps, 4),
+        "value": round(cfg["R"] / dt, 1), "unit": "train tokens/s (GEMM set only)",
+        "cores": threads, "kind": "port", "host": facts,
+        "sample": f"median of {reps} full {cfgname} GEMM-set steps "
+                  f"({sum(1 for c in plan.calls if c['op'] != 'zero')} calls each, the plan looped in C) after 2 "
+                  f"warmups, OpenMP static on {threads} threads pinned one per physical core; {CPU_FLAGS}; "
+                  f"{sum(ts):.1f} s timed",
+        "s_per_step": round(dt, 4),
     }
 
 
 def cpu_decode_baseline(host, M, steps, threads):
-    """configs[3] decode GEMVs on the host with the reference's own kernels,
-    dispatched as tinylm.c dispatches them (mm at M <= 4 and mm_bt at M = 1
-    run serially through tl_for, tinylm.c:446, :486; larger M use OpenMP),
-    one weight copy (cache-resident, as the reference's own decode runs), the
-    call list looped in C."""
+    """configs[3] decode GEMVs on the host with the restatement, one weight
+    copy (cache-resident, as the reference's own decode runs), the call list
+    looped in C, two dispatches: "as_dispatched" is the reference's decode
+    rule with its worker pool live (tl_for runs a range of fewer items than
+    workers on the caller, tinylm.c:237-239, so mm at M <= 8 (:444-446) and
+    mm_bt at M = 1 (:486) run serially); "threaded" splits each GEMV's
+    outputs over the OpenMP threads (not what the reference does; the same
+    per-element chains)."""
     import numpy as np
     import oracle
-    try:
-        prims, kind = oracle.Reference(), "reference"
-    except FileNotFoundError:
-        prims, kind = oracle.Oracle(), "port"
+    prims = oracle.Oracle()
     prims.set_threads(threads)
     plan = host.plan_decode(M, **DECODE)
     rng = np.random.default_rng(6)
@@ -411,16 +451,19 @@ def cpu_decode_baseline(host, M, steps, threads):
             a *= np.float32(0.02)
         arrays[name] = a
     calls = oracle.plan_calls_native(plan, arrays)
-    prims.run_calls(calls, 3)                           # warmup
-    t0 = time.perf_counter()
-    prims.run_calls(calls, steps)
-    dt = time.perf_counter() - t0
-    return {
-        "rows": M, "us_per_step": round(dt / steps * 1e6, 1), "tok_s": round(M * steps / dt, 1),
-        "cores": threads, "kind": kind,
-        "sample": f"{steps} decode steps ({sum(1 for c in plan.calls if c['op'] != 'zero')} GEMVs each), "
-                  f"{dt:.2f} s",
-    }
+    out = {"rows": M, "kind": "port", "gemvs_per_step": sum(1 for c in plan.calls if c["op"] != "zero")}
+    for label, pool, split, nthr in (("as_dispatched", threads, 0, threads), ("threaded", 1, 1, threads)):
+        prims.set_pool(pool)
+        prims.dll.orc_set_gemv_split(split)
+        try:
+            dt, ts = median_time(lambda: prims.run_calls(calls, steps), 5)
+        finally:
+            prims.set_pool(1)
+            prims.dll.orc_set_gemv_split(0)
+        out[label] = {"us_per_step": round(dt / steps * 1e6, 1), "tok_s": round(M * steps / dt, 1),
+                      "cores": 1 if label == "as_dispatched" else nthr,
+                      "sample": f"median of 5 runs of {steps} decode steps after 2 warmups ({sum(ts):.2f} s)"}
+    return out
 
 
 def model_of(name):
@@ -534,33 +577,32 @@ def cpu_decode_step(threads, steps=40):
     st.dll.orc_set_threads(threads)
     m = oracle.model(**DECODE_MODEL)
     P = st.init_params(m, 1)
-    dec = oracle.Decoder(m, P, 256, kvdt=1, exact=0, maxpos=steps + 32)
+    dec = oracle.Decoder(m, P, 256, kvdt=1, exact=0, maxpos=8 * steps + 32)
     prompt = np.random.default_rng(5).integers(0, m.V, 16).astype(np.int32)
     lg = dec.chunk(prompt, 0)
-    tok, pos = int(np.argmax(lg[-1])), 16
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        lg = dec.chunk(np.array([tok], np.int32), pos)
-        tok, pos = int(np.argmax(lg[-1])), pos + 1
-    dt = time.perf_counter() - t0
+    state = [int(np.argmax(lg[-1])), 16]
+
+    def run():
+        for _ in range(steps):
+            lg = dec.chunk(np.array([state[0]], np.int32), state[1])
+            state[0], state[1] = int(np.argmax(lg[-1])), state[1] + 1
+
+    dt, ts = median_time(run, 5)
     return {"value": round(steps / dt, 1), "unit": "decode tokens/s (whole step, M = 1)", "cores": threads,
             "kind": "port", "ms_per_token": round(dt / steps * 1e3, 3),
-            "sample": f"{steps} greedy single-token steps of the m8 decode model after a 16-token prefill, "
-                      f"f16 ring cache, fast_expf; {dt:.2f} s timed"}
+            "sample": f"median of 5 runs of {steps} greedy single-token steps of the m8 decode model (after a "
+                      f"16-token prefill and 2 warmup runs), f16 ring cache, fast_expf; {sum(ts):.2f} s timed"}
 
 
-def cpu_full_step(name, threads, steps=2):
-    """The reference's own forward + memset(G) + backward + gradnorm + AdamW
-    (tinylm.c:2627-2633, compiled from its lines into oracle/_ref) on host
-    cores at the same model shape; None when _ref is absent."""
+def cpu_full_step(name, threads, reps=5):
+    """The restatement's whole training step (oracle/tl_oracle_step.c:
+    forward + memset(G) + backward + gradnorm + AdamW, tinylm.c:2627-2633,
+    pinned to the reference's own code by the step fixtures) on host cores
+    at the same model shape."""
     import numpy as np
     import oracle
-    try:
-        st = oracle.StepFns("reference")
-    except FileNotFoundError:
-        return None
-    ref = oracle.Reference()
-    ref.set_threads(threads)
+    st = oracle.StepFns("oracle")
+    st.dll.orc_set_threads(threads)
     kw, B = model_of(name)
     m = oracle.model(**kw)
     P = st.init_params(m, 1234567891011)
@@ -569,21 +611,19 @@ def cpu_full_step(name, threads, steps=2):
     tok, tgt = (rng.integers(0, m.V, N).astype(np.int32) for _ in range(2))
     tm = rng.integers(0, m.V, (max(m.n_mtp, 1), N)).astype(np.int32)
     M, V = np.zeros_like(P), np.zeros_like(P)
+    t = [0]
 
-    def one(t):
+    def one():
+        t[0] += 1
         _, G = st.train_step(m, B, P, tok, tgt, tm)
         gn = st.gradnorm(G)
-        st.adamw(P, G, M, V, 3e-4, 0.9, 0.95, 0.1, t, 1.0 / gn if gn > 1.0 else 1.0)
+        st.adamw(P, G, M, V, 3e-4, 0.9, 0.95, 0.1, t[0], 1.0 / gn if gn > 1.0 else 1.0)
 
-    one(1)                                             # warmup (as cmd_bench, :4732)
-    t0 = time.perf_counter()
-    for i in range(steps):
-        one(i + 2)
-    dt = time.perf_counter() - t0
-    return {"value": round(N * steps / dt, 1), "unit": "train tokens/s (whole step)", "cores": threads,
-            "kind": "reference", "s_per_step": round(dt / steps, 4),
-            "sample": f"{steps} whole {name} training steps (forward + backward + gradnorm + AdamW, the "
-                      f"reference's own code) after 1 warmup, {threads} OpenMP threads; {dt:.1f} s timed"}
+    dt, ts = median_time(one, reps)
+    return {"value": round(N / dt, 1), "unit": "train tokens/s (whole step)", "cores": threads,
+            "kind": "port", "s_per_step": round(dt, 4),
+            "sample": f"median of {reps} whole {name} training steps (forward + backward + gradnorm + AdamW) "
+                      f"after 2 warmups, {threads} OpenMP threads; {sum(ts):.1f} s timed"}
 
 
 def main():
@@ -598,7 +638,7 @@ def main():
     ap.add_argument("--census-reps", type=int, default=5)
     ap.add_argument("--group-cfg", type=int, default=None, help="tile config of grouped launches (tuning)")
     ap.add_argument("--decode-steps", type=int, default=512)
-    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-steps", type=int, default=5, help="timed CPU-baseline steps (median of them)")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--moe-steps", type=int, default=20)
@@ -623,6 +663,10 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    # one OpenMP thread per physical core for the CPU baseline (read by
+    # libgomp when the oracle library first loads, after this point)
+    os.environ.setdefault("OMP_PLACES", "cores")
+    os.environ.setdefault("OMP_PROC_BIND", "close")
     import tlgemm
     lib = tlgemm.load()
     check(lib.tlg_init(0), "tlg_init")
@@ -731,9 +775,11 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        log(f"[cpu] timing the reference kernels on {threads} threads ...")
-        cpu = cpu_baseline(host, args.config, args.cpu_steps, threads)
+        threads, facts = host_cpu_share()
+        if args.cpu_threads:
+            threads = args.cpu_threads
+        log(f"[cpu] host {facts}: timing the CPU restatement on {threads} threads ...")
+        cpu = cpu_baseline(host, args.config, args.cpu_steps, threads, facts)
         log(f"[cpu] {cpu}")
         if args.full_steps > 0:
             cpu["train_step"] = cpu_full_step(args.config, threads)
@@ -742,7 +788,7 @@ def main():
             cpu["decode_step"] = cpu_decode_step(threads)
             log(f"[cpu] decode step {cpu['decode_step']}")
         if args.decode_steps > 0:
-            cpu["decode"] = {str(M): cpu_decode_baseline(host, M, 200 if M == 1 else 50, threads) for M in (1, 8)}
+            cpu["decode"] = {str(M): cpu_decode_baseline(host, M, 100 if M == 1 else 30, threads) for M in (1, 8)}
             log(f"[cpu] decode {cpu['decode']}")
 
     host.dll.tl_run_free(run)

@@ -72,6 +72,7 @@ class Oracle(_Prims):
         d.orc_rng_state.restype = ctypes.c_uint64
         d.orc_fill_normal.argtypes = [_fp, ctypes.c_size_t, ctypes.c_float]
         d.orc_set_pool.argtypes = [_i]
+        d.orc_set_gemv_split.argtypes = [_i]
         d.orc_set_threads.argtypes = [_i]
         d.orc_threads.restype = _i
         d.orc_moe_forward.argtypes = [_i, _i, _i, _i, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _ip, _fp, _fp]

@@ -45,8 +45,8 @@ void orc_set_threads(int nt) {
  * x[row][k] * W[k][:] into the row: per element, y = fma(x_k, w_k, y) for
  * k = 0..K-1 in order (tinylm.c:456-467).  A short final block runs the same
  * chain one row at a time (tinylm.c:468-476). */
-static void mm_block(float *restrict Y, const float *restrict X, const float *restrict W,
-                     int M, int K, int N, int b)
+static void mm_block_cols(float *restrict Y, const float *restrict X, const float *restrict W,
+                          int M, int K, int N, int b, int n0, int n1)
 {
     const int r0 = b * 4;
     const int nr = (M - r0 < 4) ? (M - r0) : 4;
@@ -59,11 +59,11 @@ static void mm_block(float *restrict Y, const float *restrict X, const float *re
         const float *restrict xb = xa + K;
         const float *restrict xc = xb + K;
         const float *restrict xd = xc + K;
-        for (int n = 0; n < N; n++) { ya[n] = 0.0f; yb[n] = 0.0f; yc[n] = 0.0f; yd[n] = 0.0f; }
+        for (int n = n0; n < n1; n++) { ya[n] = 0.0f; yb[n] = 0.0f; yc[n] = 0.0f; yd[n] = 0.0f; }
         for (int k = 0; k < K; k++) {
             const float ca = xa[k], cb = xb[k], cc = xc[k], cd = xd[k];
             const float *restrict wk = W + (size_t)k * N;
-            for (int n = 0; n < N; n++) {
+            for (int n = n0; n < n1; n++) {
                 const float w = wk[n];
                 ya[n] += ca * w; yb[n] += cb * w; yc[n] += cc * w; yd[n] += cd * w;
             }
@@ -73,14 +73,28 @@ static void mm_block(float *restrict Y, const float *restrict X, const float *re
     for (int i = 0; i < nr; i++) {
         float *restrict y = Y + (size_t)(r0 + i) * N;
         const float *restrict x = X + (size_t)(r0 + i) * K;
-        for (int n = 0; n < N; n++) y[n] = 0.0f;
+        for (int n = n0; n < n1; n++) y[n] = 0.0f;
         for (int k = 0; k < K; k++) {
             const float c = x[k];
             const float *restrict wk = W + (size_t)k * N;
-            for (int n = 0; n < N; n++) y[n] += c * wk[n];
+            for (int n = n0; n < n1; n++) y[n] += c * wk[n];
         }
     }
 }
+static void mm_block(float *restrict Y, const float *restrict X, const float *restrict W,
+                     int M, int K, int N, int b)
+{
+    mm_block_cols(Y, X, W, M, K, N, b, 0, N);
+}
+
+/* The threaded GEMV variant of the CPU decode baseline (not the reference's
+ * dispatch, which runs M <= 8 serially): M <= 8 calls split their outputs
+ * over the OpenMP threads -- mm by column ranges, mm_bt by ranges of W rows
+ * that start at multiples of 4 -- and every element keeps the reference's
+ * own chain, so the results equal the serial ones. */
+static int g_gemv_split = 0;
+void orc_set_gemv_split(int on) { g_gemv_split = on != 0; }
+#define ORC_SPLIT_COLS 64
 
 /* Dispatch rule of tinylm.c:444-448: a single block, or a live decode pool,
  * goes through tl_for (serial when the block count is below the worker count,
@@ -88,6 +102,15 @@ static void mm_block(float *restrict Y, const float *restrict X, const float *re
 void orc_mm(float *Y, const float *X, const float *W, int M, int K, int N)
 {
     const int nblk = (M + 3) / 4;
+    if (g_gemv_split && M <= 8) {
+        const int nc = (N + ORC_SPLIT_COLS - 1) / ORC_SPLIT_COLS;
+        #pragma omp parallel for schedule(static)
+        for (int c = 0; c < nc; c++) {
+            const int n1 = (c + 1) * ORC_SPLIT_COLS < N ? (c + 1) * ORC_SPLIT_COLS : N;
+            for (int b = 0; b < nblk; b++) mm_block_cols(Y, X, W, M, K, N, b, c * ORC_SPLIT_COLS, n1);
+        }
+        return;
+    }
     if (nblk == 1 || g_pool > 1) {
         if (g_pool <= 1 || nblk < g_pool) {
             for (int b = 0; b < nblk; b++) mm_block(Y, X, W, M, K, N, b);
@@ -104,13 +127,13 @@ void orc_mm(float *Y, const float *X, const float *W, int M, int K, int N)
 /* --------------------------------------------------------------- mm_bt --- */
 /* Row m of dX += dY W^T: four W rows at a time, each a dot product over n with
  * its own accumulator, added into dx once (tinylm.c:494-506). */
-static void mmbt_row(float *restrict dX, const float *restrict dY, const float *restrict W,
-                     int K, int N, int m)
+static void mmbt_rows(float *restrict dX, const float *restrict dY, const float *restrict W,
+                      int K, int N, int m, int k0, int k1)
 {
     const float *restrict g = dY + (size_t)m * N;
     float *restrict o = dX + (size_t)m * K;
-    int k = 0;
-    for (; k + 4 <= K; k += 4) {
+    int k = k0;
+    for (; k + 4 <= k1; k += 4) {
         const float *restrict wa = W + (size_t)k * N;
         const float *restrict wb = wa + N;
         const float *restrict wc = wb + N;
@@ -122,7 +145,7 @@ static void mmbt_row(float *restrict dX, const float *restrict dY, const float *
         }
         o[k] += sa; o[k + 1] += sb; o[k + 2] += sc; o[k + 3] += sd;
     }
-    for (; k < K; k++) {
+    for (; k < k1; k++) {
         const float *restrict w = W + (size_t)k * N;
         float s = 0.0f;
         for (int n = 0; n < N; n++) s += g[n] * w[n];
@@ -130,9 +153,24 @@ static void mmbt_row(float *restrict dX, const float *restrict dY, const float *
     }
 }
 
+static void mmbt_row(float *restrict dX, const float *restrict dY, const float *restrict W,
+                     int K, int N, int m)
+{
+    mmbt_rows(dX, dY, W, K, N, m, 0, K);
+}
+
 /* tinylm.c:486-488: M==1 or a live pool -> tl_for over rows, else OpenMP. */
 void orc_mm_bt(float *dX, const float *dY, const float *W, int M, int K, int N)
 {
+    if (g_gemv_split && M <= 8) {
+        const int nc = (K + ORC_SPLIT_COLS - 1) / ORC_SPLIT_COLS;
+        #pragma omp parallel for schedule(static)
+        for (int c = 0; c < nc; c++) {
+            const int k1 = (c + 1) * ORC_SPLIT_COLS < K ? (c + 1) * ORC_SPLIT_COLS : K;
+            for (int m = 0; m < M; m++) mmbt_rows(dX, dY, W, K, N, m, c * ORC_SPLIT_COLS, k1);
+        }
+        return;
+    }
     if (M == 1 || g_pool > 1) {
         if (g_pool <= 1 || M < g_pool) {
             for (int m = 0; m < M; m++) mmbt_row(dX, dY, W, K, N, m);

@@ -50,6 +50,11 @@ void orc_mm_atb(float *dW, const float *X, const float *dY, int M, int K, int N)
  * workers: ranges of fewer than nt items run serially on the caller. */
 void orc_set_pool(int nt);
 int  orc_threads(void);            /* OpenMP threads the oracle will use */
+/* on != 0: M <= 8 mm / mm_bt calls split their outputs over the OpenMP
+ * threads (column / W-row ranges, each element's chain unchanged): the
+ * threaded variant of the CPU decode baseline.  0 (default): the
+ * reference's dispatch. */
+void orc_set_gemv_split(int on);
 void orc_set_threads(int nt);      /* omp_set_num_threads */
 
 /* ---- fp64 textbook references (the selftest pattern, tinylm.c:4764-4766),

@@ -412,3 +412,51 @@ def test_persist_rejects_bad_shapes(lib):
     dec.prime(np.array([1, 2, 3], np.int32), s)
     with pytest.raises(tlgemm.TlgError):
         dec.persist(4, s)
+
+
+@pytest.mark.parametrize("kvdt,win", [(0, 0), (1, 0), (0, 96)], ids=["f32", "f16", "f32-win96"])
+def test_persist_ring_wraps_m8(lib, kvdt, win):
+    """configs[3]'s decode model with its 256-slot ring filled and wrapped:
+    a 250-token prompt, then 48 greedy steps in one persistent launch, so
+    positions 250..297 overwrite ring slots 0..41 (every key round of the f16
+    ring and every round of the f32 ring holds live keys, the new key lands
+    in round 0 again).  The f32 ring's tokens equal the oracle's throughout;
+    the f16 ring's may part only at a near-tie, and must agree for at least
+    the first 8 steps.  The logits row of the last step both sides decoded
+    from the same tokens -- the final step, or the step where the streams
+    part -- matches the oracle's.  The window case (96 keys in alternate
+    layers) checks windows wider than one key round."""
+    kw = dict(M8, win=win, full_every=2) if win else M8
+    W, steps, plen = 256, 48, 250
+    m, P = params(kw, 31)
+    prompt = np.random.default_rng(32).integers(0, m.V, plen).astype(np.int32)
+    StepFns("oracle").dll.orc_set_threads(16)
+    orc = Decoder(m, P, W, kvdt=kvdt, exact=0, maxpos=512)
+    want, rows = oracle_greedy(orc, prompt, steps)
+    print("ring wrap", kvdt, win, flush=True)
+    _, got, row, st = _persist_run(kw, P, W, kvdt, prompt, [steps])
+    assert st[0] == plen + steps
+    agree = same_stream(got[:steps], want, rows, 1e-5 if kvdt == 0 else TOL_F16)
+    print("ring wrap tokens agree for", agree, "of", steps, flush=True)
+    bar = TOL_F16 if kvdt else TOL
+    if agree == steps:
+        lg = Decoder(m, P, W, kvdt=kvdt, exact=0, maxpos=512)
+        lg.chunk(prompt, 0)
+        for i in range(steps - 1):
+            lg.chunk(np.array([got[i]], np.int32), plen + i)
+        want_row = lg.chunk(np.array([got[steps - 1]], np.int32), plen + steps - 1)[-1]
+        e = normwise_rel(row, want_row)
+        assert got[steps] == int(np.argmax(row)) == st[2]
+    else:
+        # the streams part at token `agree`, chosen from the logits of step
+        # agree - 1: decode exactly that far and compare that row
+        assert agree >= 1, "the prefill's own token differs"
+        _, got2, row2, _ = _persist_run(kw, P, W, kvdt, prompt, [agree])
+        assert got2 == got[:agree + 1]
+        e = normwise_rel(row2, rows[agree])
+    print("ring wrap logits", f"{e:.2e}", flush=True)
+    assert e <= bar
+    if kvdt == 0:
+        assert agree == steps
+    else:
+        assert agree >= 8

@@ -61,6 +61,28 @@ def test_pool_dispatch_keeps_results(orc):
             orc.set_pool(1)
 
 
+def test_split_gemv_keeps_results(orc):
+    """The threaded GEMV variant of the CPU decode baseline (outputs split
+    over threads) leaves every element's chain alone: bit-identical to the
+    reference-dispatched results, on the decode fixtures (M = 1..8, ragged)."""
+    orc.set_threads(4)
+    try:
+        for path in golden("prim_decode_*.npz") + golden("prim_tiny_*.npz"):
+            d = load_npz(path)
+            if d["X"].shape[0] > 8:
+                continue
+            orc.dll.orc_set_gemv_split(1)
+            try:
+                Y = orc.mm(d["X"], d["W"])
+                dX = orc.mm_bt(d["dX0"].copy(), d["dY"], d["W"])
+            finally:
+                orc.dll.orc_set_gemv_split(0)
+            assert np.array_equal(Y, d["Y"]), path
+            assert np.array_equal(dX, d["dX"]), path
+    finally:
+        orc.set_threads(os.cpu_count() or 1)
+
+
 @pytest.mark.parametrize("M,K,N", [(1, 1, 1), (5, 7, 3), (13, 17, 19), (64, 9, 33)])
 def test_fp64_oracle_exact_on_integers(orc, M, K, N):
     """Small integers make every product and sum exact in float64, so the fp64

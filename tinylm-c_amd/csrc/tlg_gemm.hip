@@ -50,17 +50,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 enum { RC = 0, OC = 1 };
 
-// Workgroup id -> logical work item, so that consecutive logical items land
-// on the same XCD (the dispatcher deals workgroups round-robin over the 8
-// XCDs and each XCD has its own L2).  A bijection on [0, nb).
-__device__ __forceinline__ int xcd_remap(int b, int nb)
-{
-    const int per = nb >> 3, rem = nb & 7;
-    const int x = b & 7, slot = b >> 3;
-    const int base = (x < rem) ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
-    return base + slot;
-}
-
 // Stage one operand tile into registers.  OUTER = tile extent along the
 // operand's output index, rows/cols beyond `oext` or r beyond `rend` read 0.
 template <int LAY, int OUTER, int BK, bool VEC, int NT>

@@ -272,7 +272,10 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv(GvArgs g)
     __shared__ float red[GV_WAVES * MB * COLS];
     __shared__ float rsc[GV_WAVES];
     __shared__ float Gs[GV_ACHUNK];
-    int b = blockIdx.x, p = 0;
+    // consecutive column blocks share cache lines (a block reads COLS floats
+    // of each row, a line holds 32): dealt to one XCD they meet in its L2
+    // instead of being fetched from HBM once per XCD
+    int b = xcd_remap(blockIdx.x, gridDim.x), p = 0;
     while (p < g.nprob && b >= g.p[p].blocks) { b -= g.p[p].blocks; p++; }
     if (p >= g.nprob) return;
     const GvProb &P = g.p[p];

@@ -73,6 +73,17 @@ int tlg_gemv_launch(TlgKind kind, const float *A, const float *B, float *C, int 
 int tlg_gemv_group_launch(const TlgGemmCall *calls, int n, hipStream_t st);
 const char *tlg_gemv_kernel_name(int M);
 
+// Workgroup id -> logical work item, so that consecutive logical items land
+// on the same XCD (the dispatcher deals workgroups round-robin over the 8
+// XCDs and each XCD has its own L2).  A bijection on [0, nb).
+__device__ __forceinline__ int xcd_remap(int b, int nb)
+{
+    const int per = nb >> 3, rem = nb & 7;
+    const int x = b & 7, slot = b >> 3;
+    const int base = (x < rem) ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
+    return base + slot;
+}
+
 // The reference's fast_expf (tinylm.c:3181-3191): clamp, split x log2(e) into
 // integer and fraction, 2^f by its degree-5 Horner polynomial, 2^k into the
 // exponent.
