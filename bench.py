@@ -336,7 +336,8 @@ def bench_moe(lib, stream, steps):
 
 def probes(lib, stream):
     """Achievable peaks on this box: a streaming copy (k_copy, 1 GiB each
-    way) and register-only fp32 MFMA (k_mfma_peak)."""
+    way), a streaming read (k_read, 1 GiB) and register-only fp32 MFMA
+    (k_mfma_peak)."""
     n = 1 << 28
     src, dst = lib.tlg_dev_malloc(4 * n), lib.tlg_dev_malloc(4 * n)
     check(lib.tlg_dev_fill_normal(src, n, 3, 1.0, stream), "fill")
@@ -344,13 +345,18 @@ def probes(lib, stream):
         check(lib.tlg_dev_copy(dst, src, n, stream), "copy")
     ms, _ = time_steps(lib, lambda: lib.tlg_dev_copy(dst, src, n, stream), stream, 5)
     hbm = 2 * 4.0 * n / (ms / 5 * 1e-3) / 1e9
+    for _ in range(2):
+        check(lib.tlg_dev_read(src, n, dst, stream), "read")
+    ms_r, _ = time_steps(lib, lambda: lib.tlg_dev_read(src, n, dst, stream), stream, 5)
+    hbm_read = 4.0 * n / (ms_r / 5 * 1e-3) / 1e9
     blocks, iters = 2048, 2000
     check(lib.tlg_dev_mfma_peak(dst, blocks, iters, stream), "mfma")
     ms2, _ = time_steps(lib, lambda: lib.tlg_dev_mfma_peak(dst, blocks, iters, stream), stream, 5)
     mfma = blocks * 4 * 4 * iters * 4096.0 / (ms2 / 5 * 1e-3) / 1e12
     lib.tlg_dev_free(src)
     lib.tlg_dev_free(dst)
-    return {"hbm_copy_gbs": round(hbm, 1), "copy_bytes_each_way": 4 * n, "mfma_fp32_tflops": round(mfma, 1)}
+    return {"hbm_copy_gbs": round(hbm, 1), "hbm_read_gbs": round(hbm_read, 1), "copy_bytes_each_way": 4 * n,
+            "mfma_fp32_tflops": round(mfma, 1)}
 
 
 def host_cpu_share():

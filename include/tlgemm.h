@@ -205,6 +205,10 @@ int   tlg_tune_force(int cfg, int splits);
  * workgroups of 4 waves each issue 4*iters register-only fp32 MFMAs
  * (32x32x2, 4096 flop each) and write blocks*256 floats to out. */
 int   tlg_dev_copy(float *dst, const float *src, size_t n, void *stream);
+/* Achievable HBM read bandwidth: streams n floats of src (n % 4 == 0,
+ * 16-byte aligned) and writes nothing but, in a case no finite input
+ * reaches, sink[0]. */
+int   tlg_dev_read(const float *src, size_t n, float *sink, void *stream);
 int   tlg_dev_mfma_peak(float *out, int blocks, int iters, void *stream);
 /* Stream capture into a HIP graph: begin, enqueue work, end -> executable
  * graph handle; replay with tlg_graph_launch. */

@@ -414,26 +414,29 @@ def test_persist_rejects_bad_shapes(lib):
         dec.persist(4, s)
 
 
-@pytest.mark.parametrize("kvdt,win", [(0, 0), (1, 0), (0, 96)], ids=["f32", "f16", "f32-win96"])
-def test_persist_ring_wraps_m8(lib, kvdt, win):
+@pytest.mark.parametrize("kvdt,win,plen,steps", [(0, 0, 250, 48), (1, 0, 250, 48), (0, 96, 250, 48),
+                                                  (0, 0, 13, 300), (1, 0, 13, 300)],
+                         ids=["f32", "f16", "f32-win96", "f32-300", "f16-300"])
+def test_persist_ring_wraps_m8(lib, kvdt, win, plen, steps):
     """configs[3]'s decode model with its 256-slot ring filled and wrapped:
     a 250-token prompt, then 48 greedy steps in one persistent launch, so
     positions 250..297 overwrite ring slots 0..41 (every key round of the f16
     ring and every round of the f32 ring holds live keys, the new key lands
-    in round 0 again).  The f32 ring's tokens equal the oracle's throughout;
+    in round 0 again); and 300 greedy steps after a 13-token prompt, which
+    fill the ring from the persistent launch itself and wrap it.  The f32 ring's tokens equal the oracle's throughout;
     the f16 ring's may part only at a near-tie, and must agree for at least
     the first 8 steps.  The logits row of the last step both sides decoded
     from the same tokens -- the final step, or the step where the streams
     part -- matches the oracle's.  The window case (96 keys in alternate
     layers) checks windows wider than one key round."""
     kw = dict(M8, win=win, full_every=2) if win else M8
-    W, steps, plen = 256, 48, 250
+    W = 256
     m, P = params(kw, 31)
     prompt = np.random.default_rng(32).integers(0, m.V, plen).astype(np.int32)
     StepFns("oracle").dll.orc_set_threads(16)
     orc = Decoder(m, P, W, kvdt=kvdt, exact=0, maxpos=512)
     want, rows = oracle_greedy(orc, prompt, steps)
-    print("ring wrap", kvdt, win, flush=True)
+    print("ring wrap", kvdt, win, plen, steps, flush=True)
     _, got, row, st = _persist_run(kw, P, W, kvdt, prompt, [steps])
     assert st[0] == plen + steps
     agree = same_stream(got[:steps], want, rows, 1e-5 if kvdt == 0 else TOL_F16)

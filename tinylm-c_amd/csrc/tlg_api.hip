@@ -345,11 +345,17 @@ extern "C" int tlg_kernel_name(int op, int M, int K, int N, char *buf, int len, 
 }
 
 int tlg_copy_launch(float *dst, const float *src, size_t n, hipStream_t st);
+int tlg_read_launch(const float *src, size_t n, float *sink, hipStream_t st);
 int tlg_mfma_peak_launch(float *out, int blocks, int iters, hipStream_t st);
 extern "C" int tlg_dev_copy(float *dst, const float *src, size_t n, void *stream)
 {
     int rc = tlg_ensure_init();
     return rc ? rc : tlg_copy_launch(dst, src, n, (hipStream_t)stream);
+}
+extern "C" int tlg_dev_read(const float *src, size_t n, float *sink, void *stream)
+{
+    int rc = tlg_ensure_init();
+    return rc ? rc : tlg_read_launch(src, n, sink, (hipStream_t)stream);
 }
 extern "C" int tlg_dev_mfma_peak(float *out, int blocks, int iters, void *stream)
 {

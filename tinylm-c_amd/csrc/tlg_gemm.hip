@@ -1450,23 +1450,72 @@ int tlg_fill_normal_launch(float *dst, size_t n, unsigned long long seed, float 
 // ------------------------------------------------------ measurement probes --
 // Plain streaming copy (the calibration kernel for HBM byte counters and the
 // achievable-bandwidth probe): dst[i] = src[i], float4 per thread.
-__global__ void k_copy(const f32x4 *__restrict__ src, f32x4 *__restrict__ dst, size_t n4)
+// Streaming probes: each thread moves 8 float4 per round (all 8 loads in
+// flight before any is used), rounds stride over the grid's chunks of 8 x 256
+// float4; loads and stores are nontemporal (the data is not reused).
+#define TLG_CP_U 8
+__global__ __launch_bounds__(256) void k_copy(const f32x4 *__restrict__ src, f32x4 *__restrict__ dst, size_t n4)
 {
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
-        dst[i] = __builtin_nontemporal_load(src + i);
+    const size_t chunk = (size_t)TLG_CP_U * 256;
+    for (size_t c = (size_t)blockIdx.x * chunk; c < n4; c += (size_t)gridDim.x * chunk) {
+        f32x4 v[TLG_CP_U];
+#pragma unroll
+        for (int k = 0; k < TLG_CP_U; k++) {
+            const size_t i = c + threadIdx.x + (size_t)k * 256;
+            v[k] = __builtin_nontemporal_load(src + (i < n4 ? i : n4 - 1));
+        }
+#pragma unroll
+        for (int k = 0; k < TLG_CP_U; k++) {
+            const size_t i = c + threadIdx.x + (size_t)k * 256;
+            if (i < n4) __builtin_nontemporal_store(v[k], dst + i);
+        }
+    }
+}
+
+// Read-only stream: the sum of src (kept so the loads are not removed) goes
+// to sink[0] only if it equals a value no probe input produces.
+__global__ __launch_bounds__(256) void k_read(const f32x4 *__restrict__ src, size_t n4, float *__restrict__ sink)
+{
+    const size_t chunk = (size_t)TLG_CP_U * 256;
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    for (size_t c = (size_t)blockIdx.x * chunk; c < n4; c += (size_t)gridDim.x * chunk) {
+        f32x4 v[TLG_CP_U];
+#pragma unroll
+        for (int k = 0; k < TLG_CP_U; k++) {
+            const size_t i = c + threadIdx.x + (size_t)k * 256;
+            v[k] = __builtin_nontemporal_load(src + (i < n4 ? i : n4 - 1));
+        }
+#pragma unroll
+        for (int k = 0; k < TLG_CP_U; k++) a += v[k];
+    }
+    if (a.x + a.y + a.z + a.w == -1.2345e30f) sink[0] = 1.f;
+}
+
+static size_t stream_blocks(size_t n4)
+{
+    size_t blocks = (n4 + TLG_CP_U * 256 - 1) / (TLG_CP_U * 256);
+    return blocks > 256 * 8 ? 256 * 8 : blocks;
 }
 
 int tlg_copy_launch(float *dst, const float *src, size_t n, hipStream_t st)
 {
     if (n % 4 || ((uintptr_t)dst & 15) || ((uintptr_t)src & 15))
         return tlg_fail(TLG_EINVAL, "tlg_dev_copy: needs 16-byte aligned buffers and n %% 4 == 0");
-    const size_t n4 = n / 4;
-    size_t blocks = (n4 + 255) / 256;
-    if (blocks > 256 * 16) blocks = 256 * 16;
+    const size_t n4 = n / 4, blocks = stream_blocks(n4);
     if (blocks == 0) return TLG_OK;
     hipLaunchKernelGGL(k_copy, dim3((unsigned)blocks), dim3(256), 0, st,
                        (const f32x4 *)src, (f32x4 *)dst, n4);
+    TLG_HIP(hipGetLastError());
+    return TLG_OK;
+}
+
+int tlg_read_launch(const float *src, size_t n, float *sink, hipStream_t st)
+{
+    if (n % 4 || ((uintptr_t)src & 15) || !sink)
+        return tlg_fail(TLG_EINVAL, "tlg_dev_read: needs a 16-byte aligned buffer, n %% 4 == 0 and a sink");
+    const size_t n4 = n / 4, blocks = stream_blocks(n4);
+    if (blocks == 0) return TLG_OK;
+    hipLaunchKernelGGL(k_read, dim3((unsigned)blocks), dim3(256), 0, st, (const f32x4 *)src, n4, sink);
     TLG_HIP(hipGetLastError());
     return TLG_OK;
 }

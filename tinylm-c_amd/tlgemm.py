@@ -56,6 +56,7 @@ SIGNATURES = {
     "tlg_kernel_name": (_i, [_i, _i, _i, _i, ctypes.c_char_p, _i, _ip]),
     "tlg_tune_force": (_i, [_i, _i]),
     "tlg_dev_copy": (_i, [_vp, _vp, _sz, _vp]),
+    "tlg_dev_read": (_i, [_vp, _sz, _vp, _vp]),
     "tlg_dev_mfma_peak": (_i, [_vp, _i, _i, _vp]),
     "tlg_dev_gemm_group": (_i, [_vp, _i, _vp]),
     "tlg_dev_gemm_flush": (_i, [_vp]),
