@@ -574,6 +574,40 @@ def bench_decode_persist(lib, host, stream, steps, pool=6, prompt_len=16, warmup
             "hbm_frac": round(wbytes / (per * 1e-3) / 8e12, 4), "final_position": state[0]}
 
 
+def bench_decode_chunks(lib, host, stream, M, positions=512, pool=6, prompt_len=16):
+    """configs[3] at M rows: forward_chunk over `positions` given tokens in
+    chunks of M rows (prefill / speculative verification), every chunk of the
+    timed run in ONE persistent launch (tl_decode_chunks); the weight copies
+    rotate per chunk, so each chunk streams the 52.7 MB of weights from HBM
+    once for its M tokens."""
+    import numpy as np
+    n = positions // M
+    warm = max(1, 64 // M)
+    maxpos = prompt_len + (warm + n) * M + 8
+    dec = host.decode(DECODE_MODEL, 256, kv_f16=1, exact_exp=0, maxpos=maxpos, mmax=8, pool=pool)
+    for c in range(pool):
+        check(lib.tlg_dev_fill_normal(dec.params(c), dec.np, 77, 0.02, stream), "fill P")
+    dec.reset(stream)
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, DECODE_MODEL["V"], prompt_len).astype(np.int32)
+    toks = rng.integers(0, DECODE_MODEL["V"], (warm + n) * M).astype(np.int32)
+    dtoks = lib.tlg_dev_malloc(toks.nbytes)
+    check(lib.tlg_memcpy_h2d(dtoks, toks.ctypes.data, toks.nbytes, stream), "tokens")
+    dec.prime(prompt, stream)
+    dec.persist_chunks(M, dtoks, warm, stream)
+    dec.persist_status(stream)
+    ms, _ = time_steps(lib, lambda: dec.persist_chunks(M, dtoks + 4 * warm * M, n, stream), stream, 1)
+    dec.persist_status(stream)
+    state = dec.state(stream)
+    lib.tlg_dev_free(dtoks)
+    per = ms / n
+    wbytes = 4 * (DECODE_MODEL["V"] * 384 + 8 * (384 * 384 * 2 + 2 * 384 * 96 + 3 * 384 * 1024))
+    return {"rows": M, "chunks": n, "launches": 1, "kv_cache": "f16 ring, 256 positions", "exp": "fast_expf",
+            "weights_pool": pool, "us_per_chunk": round(per * 1e3, 3), "tok_s": round(M * 1e3 / per, 1),
+            "weight_bytes_per_chunk": wbytes, "weight_gbs": round(wbytes / (per * 1e-3) / 1e9, 1),
+            "hbm_frac": round(wbytes / (per * 1e-3) / 8e12, 4), "final_position": state[0]}
+
+
 def cpu_decode_step(threads, steps=40):
     """The oracle's forward_chunk restatement (kind "port": the reference's
     decode state is not compiled from its lines) at M = 1 on host cores."""
@@ -775,6 +809,10 @@ def main():
     if args.decode_persist_steps > 0:
         dec_persist = bench_decode_persist(lib, host, stream, args.decode_persist_steps)
         log(f"[decode step, persistent] {dec_persist}")
+        dec_persist["chunks"] = {}
+        for M in (1, 2, 4, 8):
+            dec_persist["chunks"][str(M)] = bench_decode_chunks(lib, host, stream, M)
+            log(f"[decode chunks, persistent] M={M}: {dec_persist['chunks'][str(M)]}")
     peaks = None if args.no_probes else probes(lib, stream)
     if peaks:
         log(f"[probes] {peaks}")

@@ -128,6 +128,19 @@ typedef struct {
 
 size_t tlg_dec_persist_xbytes(int V, int D, int L, int F);
 int tlg_dev_dec_persist(const TlgDecPersist *a, int n, void *stream);
+/* forward_chunk (tinylm.c:3721-3830) at m rows (m = 1, 2, 4 or 8; m <= W)
+ * for n chunks of given tokens, in ONE cooperative launch of one workgroup
+ * per CU -- the prefill loop (:3977) and speculative decoding's verification
+ * chunk (:3989) at the decoder's shapes (those of tlg_dev_dec_persist).
+ * Chunk i feeds toks[i m .. i m + m) (device memory) at positions state[0] +
+ * i m .. + m - 1 with weights P[(copy0 + i) % pool].  At the end state =
+ * {state[0] + n m, 1, argmax of the last row, exchange sequence}, tok[0] =
+ * that argmax, logits[m][V] = the last chunk's rows and toks_out[i m + j]
+ * (if not NULL) = argmax_v of chunk i's row j.  Ring rows are stored as the
+ * reference's hoisted kv_store leaves them (:3775-3780): a window key whose
+ * slot a later row of the chunk overwrote reads that row's key.  xbuf, the
+ * state and the abort behaviour are shared with tlg_dev_dec_persist. */
+int tlg_dev_dec_chunks(const TlgDecPersist *a, int m, const int *toks, int n, void *stream);
 /* Synchronize `stream`; TLG_OK, or TLG_EHIP if a launch on xbuf aborted. */
 int tlg_dec_persist_status(void *xbuf, void *stream);
 

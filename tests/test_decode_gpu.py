@@ -463,3 +463,104 @@ def test_persist_ring_wraps_m8(lib, kvdt, win, plen, steps):
         assert agree == steps
     else:
         assert agree >= 8
+
+
+def _rows_agree(got, rows, rel):
+    """Per-row argmax tokens equal the oracle's, or differ only at a near-tie
+    of the oracle's row (the device's token within rel * max|logit| of the
+    best); returns the number of exact matches."""
+    same = 0
+    for g, row in zip(got, rows):
+        w = int(np.argmax(row))
+        if g == w:
+            same += 1
+        else:
+            assert row[w] - row[g] <= rel * np.abs(row).max(), (g, w)
+    return same
+
+
+@pytest.mark.parametrize("shape,kvdt,m", [("small", 0, 1), ("small", 0, 2), ("small", 1, 4), ("small", 0, 8),
+                                          ("m8", 0, 2), ("m8", 0, 4), ("m8", 1, 8), ("m8", 0, 8),
+                                          ("m8win", 0, 8)])
+def test_persist_chunks_match_oracle(lib, shape, kvdt, m):
+    """forward_chunk at m rows in one persistent launch (tlg_dev_dec_chunks):
+    chunks of given tokens that run past the ring's end (so rows of a chunk
+    overwrite slots inside their own windows, as the reference's hoisted
+    kv_store does), against the oracle run on the same tokens and chunking:
+    every row's argmax (up to near-ties), the last chunk's logits within the
+    bar, the state advanced by n * m."""
+    t = _t()
+    kw = SMALL if shape == "small" else (dict(M8, win=96, full_every=2) if shape == "m8win" else M8)
+    W = 32 if shape == "small" else 256
+    plen, total = (5, 48) if shape == "small" else (200, 96)
+    n = total // m
+    mdl, P = params(kw, 41)
+    r = np.random.default_rng(42)
+    prompt = r.integers(0, mdl.V, plen).astype(np.int32)
+    toks = r.integers(0, mdl.V, n * m).astype(np.int32)
+    StepFns("oracle").dll.orc_set_threads(16)
+    orc = Decoder(mdl, P, W, kvdt=kvdt, exact=0, maxpos=512)
+    orc.chunk(prompt, 0)
+    rows = []
+    for i in range(n):
+        rows.append(orc.chunk(toks[i * m:(i + 1) * m], plen + i * m))
+    print("chunks", shape, kvdt, m, n, flush=True)
+    import tlgemm
+    s = stream()
+    dec = tlgemm.host().decode(kw, W, kv_f16=kvdt, exact_exp=0, maxpos=512, mmax=8, pool=2)
+    dec.upload(P, s)
+    dec.prime(prompt, s)
+    dt = _dev(toks)
+    out = t.full((n * m,), -1, dtype=t.int32, device="cuda")
+    dec.persist_chunks(m, dt.data_ptr(), n, s, out.data_ptr())
+    dec.persist_status(s)
+    st = dec.state(s)
+    assert st[0] == plen + n * m
+    got = out.cpu().numpy()
+    bar = TOL_F16 if kvdt else TOL
+    same = _rows_agree(got, np.concatenate(rows), 1e-5 if kvdt == 0 else TOL_F16)
+    print("chunk rows agree for", same, "of", n * m, flush=True)
+    last = dec.logits(m, s)
+    e = normwise_rel(last, rows[-1])
+    print("last chunk logits", f"{e:.2e}", flush=True)
+    assert e <= bar
+    assert st[2] == got[-1]
+    assert same >= (n * m if kvdt == 0 else n * m // 2)
+
+
+def test_persist_chunks_equal_graph_chunks(lib):
+    """The persistent chunks and the graph path's chunks (tl_decode_chunk)
+    run the same forward_chunk: equal argmax rows and, on an f32 ring, the
+    last chunk's logits within the fp32 bar; one launch of 6 chunks equals
+    launches of 1, 2 and 3 chunks bit for bit."""
+    t = _t()
+    import tlgemm
+    kw, W, m = M8, 256, 4
+    mdl, P = params(kw, 43)
+    r = np.random.default_rng(44)
+    prompt = r.integers(0, mdl.V, 30).astype(np.int32)
+    toks = r.integers(0, mdl.V, 24).astype(np.int32)
+    s = stream()
+    ref = tlgemm.host().decode(kw, W, kv_f16=0, exact_exp=0, maxpos=512, mmax=8, pool=1)
+    ref.upload(P, s)
+    ref.prime(prompt, s)
+    grows = [ref.chunk(toks[i * m:(i + 1) * m], 30 + i * m, s) for i in range(6)]
+
+    def run(splits):
+        dec = tlgemm.host().decode(kw, W, kv_f16=0, exact_exp=0, maxpos=512, mmax=8, pool=2)
+        dec.upload(P, s)
+        dec.prime(prompt, s)
+        dt = _dev(toks)
+        out = t.full((24,), -1, dtype=t.int32, device="cuda")
+        c0 = 0
+        for k in splits:
+            dec.persist_chunks(m, dt.data_ptr() + 4 * c0 * m, k, s, out.data_ptr() + 4 * c0 * m)
+            dec.persist_status(s)
+            c0 += k
+        return out.cpu().numpy(), dec.logits(m, s)
+
+    one, lg1 = run([6])
+    many, lgm = run([1, 2, 3])
+    assert np.array_equal(one, many) and np.array_equal(lg1, lgm), "split launches must be bit-identical"
+    assert list(one) == [int(np.argmax(row)) for g in grows for row in g]
+    assert normwise_rel(lg1, grows[-1]) <= TOL

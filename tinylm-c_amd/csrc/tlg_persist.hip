@@ -919,11 +919,617 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
     }
 }
 
+// ================================================================ chunks ==
+// forward_chunk at m = MR rows (tinylm.c:3721-3830) for n chunks of MR
+// consecutive positions whose tokens are given (prefill; the verification
+// chunk of speculative decoding, :3989), in ONE cooperative launch.  The M
+// rows share every weight load, so a step streams the same 52.7 MB (the
+// configs[3] model) for MR tokens.
+//
+// Phases of a layer (item i of a chunk to workgroup i % NB, as above):
+//   QKV  (D + 2 KD) / 32 items  32 columns of [Wq | Wk | Wv] (one head) for
+//                                the MR rows of RMSNorm(x); RoPE on q and k;
+//                                the k and v items store the MR new ring rows
+//                                of their KV head (kv_store, :3775-3780) and
+//                                publish them in the ring's precision
+//   ATT  H * MR items            head h, row j: softmax attention of q_j over
+//                                the window of position pos + j (attn_body,
+//                                :3639-3715): ring keys before pos, the
+//                                chunk's new keys pos .. pos + j, and -- as the
+//                                reference's hoisted stores leave the ring --
+//                                a window key whose slot a later row of the
+//                                chunk wrote reads that row's key
+//   O    D / 32                  32 columns of ctx . Wo, every row
+//   SW   F / 16                  RMSNorm(x) . W1 and . W3, 16 columns each,
+//                                silu(g) * u
+//   W2   D / 32                  32 columns of act . W2
+//   head V / 8 items per chunk   8 vocabulary rows against the final-normed
+//                                rows, their first maximum per row
+// Every workgroup adds the O and W2 outputs of every layer into its own copy
+// of the MR residual rows (same order everywhere, bit-identical copies).  A
+// chunk starts once the previous chunk's argmax candidates are all there, so
+// chunk t + 1 reads ring rows chunk t completed, and no exchange word is
+// rewritten while a workgroup of the previous chunk may still read it.
+#define PC_MAXMR 8
+#define PC_MAXQKV (3 * PD_MAXD)     // D + 2 KD with KD <= D
+
+struct PcLayout {
+    size_t ctrl, qkv, ctx, yo, act, y2, cand, total;
+};
+__host__ __device__ static inline PcLayout pc_layout(int V, int D, int KD, int L, int F, int MR)
+{
+    PcLayout o;
+    size_t p = 0;
+    o.ctrl = p; p += 8;
+    o.qkv = p;  p += (size_t)L * MR * (D + 2 * KD);
+    o.ctx = p;  p += (size_t)L * MR * D;
+    o.yo = p;   p += (size_t)L * MR * D;
+    o.act = p;  p += (size_t)L * MR * F;
+    o.y2 = p;   p += (size_t)L * MR * D;
+    o.cand = p; p += (size_t)2 * MR * (V / 8) * 2;
+    o.total = p;
+    return o;
+}
+
+template <int MR> struct PcShared {
+    float x[MR][PD_MAXD], xn[MR][PD_MAXD];
+    float in[MR * PD_MAXF];
+    f32x4 red[MR][PD_RED];
+    float sw[MR][PD_NW];
+    float col[MR][64];                  // an item's column results (q / k / v, SwiGLU g and u)
+    float q[32], kn[MR][32], vn[MR][32];
+    float ctxw[PD_T / 16][32];
+    float sm[2 * PD_NW];
+    u64 key[PD_NW];
+    float lg[MR][8];
+    int tok[MR];
+    const float *P[16];
+    void *Kc[TLG_PD_MAXL], *Vc[TLG_PD_MAXL];
+};
+
+// The norm parts of the MR rows of x (tid < D holds element tid of every row)
+// for gain element gj: xg[j][tid] = x[j][tid] g and the waves' sums of x^2
+// (sw[j][wave]); made visible by the caller's next barrier.
+template <int MR>
+__device__ __forceinline__ void pc_norm_parts(const float (&x)[MR][PD_MAXD], float gj, float (&xg)[MR][PD_MAXD],
+                                              int D, float (&sw)[MR][PD_NW])
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < MR; j++) {
+        const float xv = tid < D ? x[j][tid] : 0.f;
+        if (tid < D) xg[j][tid] = xv * gj;
+        const float ss = pd_wave_sum(xv * xv);
+        if ((tid & 63) == 0) sw[j][tid >> 6] = ss;
+    }
+}
+
+// Column panel against the MR rows of vin (row stride PD_MAXD, or F for the
+// W2 input): thread (c4, rg) sums rows rg + 64 i of its 4 columns for every
+// row, then pd_colsum_put per row.  After the caller's barrier, red[j] holds
+// row j's partials.
+template <int MAXI, int MR>
+__device__ __forceinline__ void pc_panel(const float *vin, int ldv, const f32x4 *w, int K, f32x4 (*red)[PD_RED])
+{
+    const int rg = threadIdx.x >> 3;
+    // two rows at a time: all the rows' activations at once would need MR x
+    // MAXI registers next to the panel's
+#pragma unroll 2
+    for (int j = 0; j < MR; j++) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < MAXI; i++) {
+            const bool in = K == 64 * MAXI || rg + 64 * i < K;
+            const float xv = vin[j * ldv + min(rg + 64 * i, K - 1)];
+            acc.x = in ? fmaf(xv, w[i].x, acc.x) : acc.x;
+            acc.y = in ? fmaf(xv, w[i].y, acc.y) : acc.y;
+            acc.z = in ? fmaf(xv, w[i].z, acc.z) : acc.z;
+            acc.w = in ? fmaf(xv, w[i].w, acc.w) : acc.w;
+        }
+        pd_colsum_put(acc, red[j]);
+    }
+}
+
+// Wait until the n words at src + idx(e), e < n, carry `tag`, then dst[e] =
+// their values (KPL words per thread).  Like pd_fetch, for gathered words.
+template <int KPL, class IDX>
+__device__ bool pc_gather(const u64 *src, int n, IDX idx, u32 tag, float *dst, u32 *abortp)
+{
+    const int tid = threadIdx.x;
+    const u64 t0 = wall_clock64();
+    u64 w[KPL];
+    int stop = 0;
+    for (int it = 0;; it++) {
+#pragma unroll
+        for (int k = 0; k < KPL; k++) w[k] = pd_ld(src + idx(min(tid + PD_T * k, n - 1)));
+        int bad = 0;
+#pragma unroll
+        for (int k = 0; k < KPL; k++) bad |= (tid + PD_T * k < n) && (u32)(w[k] >> 32) != tag;
+        if (__ballot(bad) == 0ull) break;
+        if ((it & 7) == 7) {
+            int s = 0;
+            if ((tid & 63) == 0)
+                s = __hip_atomic_load(gp(abortp), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u ||
+                    wall_clock64() - t0 > PD_SPIN;
+            if (__ballot(s) != 0ull) { stop = 1; break; }
+        }
+    }
+    if (!stop) {
+#pragma unroll
+        for (int k = 0; k < KPL; k++)
+            if (tid + PD_T * k < n) dst[tid + PD_T * k] = __uint_as_float((u32)w[k]);
+    }
+    if (__syncthreads_or(stop)) {
+        if (tid == 0) __hip_atomic_store(gp(abortp), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+    }
+    return true;
+}
+
+// x[j] += the MR x D words of src (row-major), the norm parts for gain gj
+// after; false after an abort.
+template <int MR>
+__device__ bool pc_add_rows(PcShared<MR> &sh, const u64 *src, int D, u32 tag, float gj, u32 *abortp)
+{
+    constexpr int KPL = (MR * PD_MAXD + PD_T - 1) / PD_T;
+    if (!pd_fetch<KPL, 0>(src, MR * D, tag, sh.in, abortp)) return false;
+    const int tid = threadIdx.x;
+    if (tid < D)
+#pragma unroll
+        for (int j = 0; j < MR; j++) sh.x[j][tid] += sh.in[j * D + tid];
+    pc_norm_parts<MR>(sh.x, gj, sh.xn, D, sh.sw);
+    __syncthreads();
+    return true;
+}
+
+// The first maximum of each row's argmax candidates (2 words per head item:
+// value, index) into sh.tok[j]; false after an abort.
+template <int MR>
+__device__ bool pc_argmax(PcShared<MR> &sh, const u64 *cand, int NHI, u32 tag, u32 *abortp)
+{
+    const int tid = threadIdx.x;
+    if (!pd_fetch<(2 * MR * PD_MAXHI + PD_T - 1) / PD_T, 0>(cand, 2 * MR * NHI, tag, sh.in, abortp))
+        return false;
+#pragma unroll 1
+    for (int j = 0; j < MR; j++) {
+        u64 kx = 0;
+        if (tid < NHI) {
+            const u32 i = __float_as_uint(sh.in[(j * NHI + tid) * 2 + 1]);
+            kx = i == 0x7fffffffu ? 0 : pd_argkey(sh.in[(j * NHI + tid) * 2], i);
+        }
+        const u32 hm = pd_wave_umax((u32)(kx >> 32));
+        const u32 lm = pd_wave_umax((u32)(kx >> 32) == hm ? (u32)kx : 0u);
+        if ((tid & 63) == 0) sh.key[tid >> 6] = ((u64)hm << 32) | lm;
+        __syncthreads();
+        if (tid == 0) {
+            u64 m = sh.key[0];
+#pragma unroll
+            for (int w = 1; w < PD_NW; w++) m = max(m, sh.key[w]);
+            sh.tok[j] = m == 0 ? 0 : (int)(~(u32)m);
+        }
+        __syncthreads();
+    }
+    return true;
+}
+
+// Attention of row j (position p = pos + j) of query head h, layer l: the
+// ring words kw / vw of the window's keys before pos are loaded (pd_ring_load
+// with key count cnt - j ... see the caller); sh.q holds q_j, sh.kn / sh.vn the
+// chunk's new rows of the head's KV head.  ctx_j of the head is published.
+template <int F16, int MR>
+__device__ __forceinline__ void pc_attention(PcShared<MR> &sh, u64 (&kw)[PD_MAXR], u64 (&vw)[PD_MAXR],
+                                             const TlgDecPersist &a, int pos, int j, int lo, int cnt, u64 *ctxout,
+                                             u32 tag)
+{
+    typedef PdRing<F16> R;
+    constexpr int NW = R::NW, KPR = PD_T / NW, MAXR = PD_MAXW / KPR;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int key0 = tid >> R::LOG2NW, wd = tid & (NW - 1);
+    // key t = lo + key0 + KPR r (window order).  Position tp = lo + t: a new
+    // row (tp >= pos) or a slot a later row of the chunk overwrote (tp <
+    // pos - W + MR) reads that row of the chunk; every other key its ring word
+    float qv[R::EPW];
+#pragma unroll
+    for (int e = 0; e < R::EPW; e++) qv[e] = sh.q[R::EPW * wd + e];
+    const float scale = 1.0f / sqrtf(32.0f);
+    float sc[MAXR];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < MAXR; r++) {
+        const int t = key0 + KPR * r, tp = lo + t;
+        const int nr = tp >= pos ? tp - pos : tp - pos + a.W;      // chunk row of the key, if any
+        if (t < cnt && nr >= 0 && nr < MR) {
+            kw[r] = R::pack(&sh.kn[nr][R::EPW * wd]);
+            vw[r] = R::pack(&sh.vn[nr][R::EPW * wd]);
+        }
+        float part = 0.f;
+#pragma unroll
+        for (int e = 0; e < R::EPW; e++) part = fmaf(qv[e], R::get(kw[r], e), part);
+        part += pd_dpp<0xB1, 0xf>(0.f, part);
+        part += pd_dpp<0x4E, 0xf>(0.f, part);
+        {
+            const float r4 = pd_dpp<0x124, 0xf>(0.f, part), r12 = pd_dpp<0x12C, 0xf>(0.f, part);
+            part += (lane & 4) ? r4 : r12;
+        }
+        if (NW == 16) part += pd_dpp<0x128, 0xf>(0.f, part);
+        sc[r] = t < cnt ? part * scale : -INFINITY;
+        mx = fmaxf(mx, sc[r]);
+    }
+    mx = pd_keys_max<NW>(mx);
+    if (lane == 0) sh.sm[wave] = mx;
+    __syncthreads();
+    mx = sh.sm[0];
+#pragma unroll
+    for (int w = 1; w < PD_NW; w++) mx = fmaxf(mx, sh.sm[w]);
+    float sum = 0.f;
+#pragma unroll
+    for (int r = 0; r < MAXR; r++) {
+        const int t = key0 + KPR * r;
+        const float e = a.exact ? expf(sc[r] - mx) : tlg_fast_expf(sc[r] - mx);
+        sc[r] = t < cnt ? e : 0.f;
+        sum += sc[r];
+    }
+    sum = pd_keys_sum<NW>(sum);
+    if (lane == 0) sh.sm[PD_NW + wave] = sum;
+    float acc[R::EPW];
+#pragma unroll
+    for (int e = 0; e < R::EPW; e++) acc[e] = 0.f;
+#pragma unroll
+    for (int r = 0; r < MAXR; r++) {
+        const int t = key0 + KPR * r;
+#pragma unroll
+        for (int e = 0; e < R::EPW; e++) acc[e] = t < cnt ? fmaf(sc[r], R::get(vw[r], e), acc[e]) : acc[e];
+    }
+    const int row = tid >> 4;
+#pragma unroll
+    for (int e = 0; e < R::EPW; e++) {
+        if (NW == 8) acc[e] += pd_dpp<0x128, 0xf>(0.f, acc[e]);
+        if ((tid & 15) < NW) sh.ctxw[row][R::EPW * wd + e] = acc[e];
+    }
+    __syncthreads();
+    if (tid < 64) {
+        float tot = sh.sm[PD_NW];
+#pragma unroll
+        for (int w = 1; w < PD_NW; w++) tot += sh.sm[PD_NW + w];
+        const int d = tid >> 1, r0 = 16 * (tid & 1);
+        float c0 = sh.ctxw[r0][d], c1 = sh.ctxw[r0 + 8][d];
+#pragma unroll
+        for (int rr = 1; rr < 8; rr++) {
+            c0 += sh.ctxw[r0 + rr][d];
+            c1 += sh.ctxw[r0 + 8 + rr][d];
+        }
+        float cx = c0 + c1;
+        cx += pd_dpp<0xB1, 0xf>(0.f, cx);
+        cx = tot > 0.f ? (a.exact ? cx / tot : cx * __builtin_amdgcn_rcpf(tot)) : 0.f;
+        if ((tid & 1) == 0) pd_st(ctxout + d, pd_word(cx, tag));
+    }
+    __syncthreads();
+}
+
+// Item counts of a chunk layer at MR rows.  Every GEMV phase has one item per
+// (column block, row) -- SW items take RS rows -- so the VALU work of an item
+// stays that of a single row and the MR rows spread over MR times as many
+// workgroups; the items of one column block are consecutive (one XCD), so
+// the panel they all read comes from that XCD's L2 after the first.
+struct PcItems {
+    int NQ, NQI, NA, NOI, RS, NSI, NWI, NPL;
+    __device__ PcItems(int MR, int D, int KD, int H, int F)
+    {
+        NQ = (D + 2 * KD) / 32;
+        NQI = NQ * MR;
+        NA = H * MR;
+        NOI = (D / 32) * MR;
+        RS = MR >= 4 ? MR / 4 : 1;
+        NSI = (F / 16) * (MR / RS);
+        NWI = (D / 32) * MR;
+        NPL = NQI + NA + NOI + NSI + NWI;
+    }
+};
+
+// The weight panel of chunk item g (index within a chunk's layer items):
+// QKV: 32 columns of Wq (q heads), Wk or Wv (KV heads); O: Wo; SW: W1 | W3
+// (threads c4 < 4 / >= 4); W2 (K = F); ATT items load no panel.  The RMSNorm
+// gain element of thread tid for items that normalise x.
+__device__ __forceinline__ void pc_load_item(f32x4 (&wb)[PD_MAXFQ], float &gn, const float *__restrict__ P, int g,
+                                             const PcItems &it, int MR, int H, int KV, size_t lay0, size_t per,
+                                             int D, int KD, int F)
+{
+    const int l = g / it.NPL, k = g % it.NPL;
+    const size_t an1 = lay0 + (size_t)l * per, wq = an1 + D, wk = wq + (size_t)D * D, wv = wk + (size_t)D * KD,
+                 wo = wv + (size_t)D * KD, an2 = wo + (size_t)D * D, w1 = an2 + D, w3 = w1 + (size_t)D * F,
+                 w2 = w3 + (size_t)D * F;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    const int tid = threadIdx.x, c4 = tid & 7;
+    const u32 gof = 4u * (u32)min(tid, D - 1);
+    gn = 0.f;
+    if (k < it.NQI) {
+        const int c = k / MR;
+        if (c < H) pd_load_cols<PD_MAXQ>(wb, P + wq, D, c * 32, D);
+        else if (c < H + KV) pd_load_cols<PD_MAXQ>(wb, P + wk, KD, (c - H) * 32, D);
+        else pd_load_cols<PD_MAXQ>(wb, P + wv, KD, (c - H - KV) * 32, D);
+        gn = pd_at<float>(P + an1, gof);
+    } else if (k < it.NQI + it.NA) {
+#pragma unroll
+        for (int i = 0; i < PD_MAXQ; i++) wb[i] = z;
+    } else if (k < it.NQI + it.NA + it.NOI) {
+        pd_load_cols<PD_MAXQ>(wb, P + wo, D, ((k - it.NQI - it.NA) / MR) * 32, D);
+    } else if (k < it.NQI + it.NA + it.NOI + it.NSI) {
+        const int c = (k - it.NQI - it.NA - it.NOI) / (MR / it.RS);
+        const float *W = c4 < 4 ? P + w1 : P + w3;
+        pd_load_cols<PD_MAXQ>(wb, W, F, 16 * c - 4 * (c4 & 4), D);
+        gn = pd_at<float>(P + an2, gof);
+    } else {
+        pd_load_cols<PD_MAXFQ>(wb, P + w2, D, ((k - it.NQI - it.NA - it.NOI - it.NSI) / MR) * 32, F);
+        return;
+    }
+#pragma unroll
+    for (int i = PD_MAXQ; i < PD_MAXFQ; i++) wb[i] = z;
+}
+
+// The 32 column sums of panel row j after pc_panel<..., 1> into red[0]:
+// wave 0's lanes 2 i, 2 i + 1 get column i (PAIRS 0), or the SwiGLU pairing
+// (PAIRS 1); the caller's barrier precedes.
+template <int PAIRS> __device__ __forceinline__ float pc_cols(const f32x4 *red)
+{
+    return threadIdx.x < 64 ? pd_colsum_half(red, pd_half_col<PAIRS>(threadIdx.x)) : 0.f;
+}
+
+template <int F16, int MR>
+__global__ __launch_bounds__(PD_T, 1) void k_dec_chunk(TlgDecPersist a, const int *toks_in, int n)
+{
+    typedef PdRing<F16> R;
+    __shared__ PcShared<MR> sh;
+    const int tid = threadIdx.x;
+    const int NB = gridDim.x,
+              b = (NB % 8) ? (int)blockIdx.x : (int)(blockIdx.x % 8u) * (NB / 8) + (int)(blockIdx.x / 8u);
+    const int D = a.D, F = a.F, V = a.V, L = a.L, H = a.H, KV = a.KV, KD = a.KV * 32, grp = a.H / a.KV;
+    const int QN = D + 2 * KD;
+    const PcItems it(MR, D, KD, H, F);
+    const int NPL = it.NPL, NLI = L * NPL, NHI = V / 8;
+    const u32 NPH = 5u * (u32)L + 1u;
+    const size_t per = (size_t)D + (size_t)D * D + 2 * (size_t)D * KD + (size_t)D * D + D + 3 * (size_t)D * F;
+    const size_t lay0 = (size_t)V * D;
+    u64 *xb = reinterpret_cast<u64 *>(a.xbuf);
+    const PcLayout lay = pc_layout(V, D, KD, L, F, MR);
+    u32 *abortp = reinterpret_cast<u32 *>(xb + lay.ctrl);
+    const int pos0 = gp(a.state)[0];
+    const u32 base = (u32)gp(a.state)[3];
+    if (b >= NLI && b >= NHI) return;
+    if (tid == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) sh.P[i] = a.P[i];
+#pragma unroll
+        for (int i = 0; i < TLG_PD_MAXL; i++) { sh.Kc[i] = a.Kc[i]; sh.Vc[i] = a.Vc[i]; }
+    }
+    __syncthreads();
+
+    f32x4 wb[PD_MAXFQ];
+    float gn = 0.f;
+    u64 kw[PD_MAXR], vw[PD_MAXR];
+    if (b < NLI) pc_load_item(wb, gn, pd_uni(sh.P[a.copy0 % a.pool]), b, it, MR, H, KV, lay0, per, D, KD, F);
+
+    for (int t = 0; t < n; t++) {
+        const float *P = pd_uni(sh.P[(a.copy0 + t) % a.pool]);
+        const int pos = pos0 + t * MR;
+        const u32 tag0 = base + (u32)t * NPH + 1u;
+        if (t > 0) {            // the previous chunk's head is complete: its greedy tokens
+            if (!pc_argmax<MR>(sh, xb + lay.cand + (size_t)((t - 1) & 1) * MR * NHI * 2, NHI, tag0 - 1u, abortp))
+                return;
+            if (b == 0 && tid < MR && a.toks_out) gp(a.toks_out)[(size_t)(t - 1) * MR + tid] = sh.tok[tid];
+        }
+        // x = emb[token] for the MR rows, norm parts for the first item's gain
+        if (tid < D)
+#pragma unroll
+            for (int j = 0; j < MR; j++) {
+                const int tk = gp(toks_in)[(size_t)t * MR + j];
+                sh.x[j][tid] = (tk >= 0 && tk < V) ? gp(P)[(size_t)tk * D + tid] : NAN;
+            }
+        __syncthreads();
+        pc_norm_parts<MR>(sh.x, gn, sh.xn, D, sh.sw);
+        __syncthreads();
+        const float hg = pd_at<float>(P + lay0 + (size_t)L * per, 4u * (u32)min(tid, D - 1));
+
+        for (int l = 0; l < L; l++) {
+            const int g0 = l * NPL;
+            const u32 tl = tag0 + 5u * (u32)l;              // qkv, ctx, yo, act, y2: tl .. tl + 4
+            u64 *qkv = xb + lay.qkv + (size_t)l * MR * QN, *ctx = xb + lay.ctx + (size_t)l * MR * D;
+            u64 *yo = xb + lay.yo + (size_t)l * MR * D, *act = xb + lay.act + (size_t)l * MR * F;
+            u64 *y2 = xb + lay.y2 + (size_t)l * MR * D;
+            const int kA = it.NQI, kO = kA + it.NA, kS = kO + it.NOI, kW = kS + it.NSI;
+#define PC_FIRST(k0) ((g0 + (k0)) + ((b - (g0 + (k0))) % NB + NB) % NB)
+#define PC_NEXT(g)                                                                                            \
+    do {                                                                                                      \
+        const int ng_ = (g) + NB < NLI ? (g) + NB : b, nt_ = min((g) + NB < NLI ? t : t + 1, n - 1);           \
+        pc_load_item(wb, gn, pd_uni(sh.P[(a.copy0 + nt_) % a.pool]), ng_, it, MR, H, KV, lay0, per, D, KD, F); \
+    } while (0)
+            // ---- QKV: 32 columns of one head, one row
+            for (int g = PC_FIRST(0); g < g0 + kA; g += NB) {
+                const int c = (g - g0) / MR, j = (g - g0) % MR, p = pos + j;  // c < H: q; < H + KV: k; else v
+                pc_panel<PD_MAXQ, 1>(&sh.xn[j][0], PD_MAXD, wb, D, sh.red);
+                __syncthreads();
+                if (tid < 64) {
+                    float s = 0.f;
+#pragma unroll
+                    for (int w = 0; w < PD_NW; w++) s += sh.sw[j][w];
+                    const float v = pc_cols<0>(sh.red[0]) * rsqrtf(s / (float)D + 1e-5f);
+                    if ((tid & 1) == 0) sh.col[0][tid >> 1] = v;
+                }
+                __syncthreads();
+                if (tid < 32) {                              // RoPE (q, k), ring precision (k, v)
+                    const int i = tid;
+                    const float cv = sh.col[0][i], o = sh.col[0][i ^ 16];
+                    float r = cv;
+                    if (c < H + KV) {
+                        const bool inpos = p >= 0 && p < a.maxpos;
+                        const float rc = inpos ? gp(a.cs)[(size_t)p * 16 + (i & 15)] : 0.f;
+                        const float rs = inpos ? gp(a.sn)[(size_t)p * 16 + (i & 15)] : 0.f;
+                        r = inpos ? (i < 16 ? cv * rc - o * rs : cv * rc + o * rs) : NAN;
+                    }
+                    if (c >= H) r = R::round(r);
+                    sh.col[0][32 + i] = r;
+                }
+                __syncthreads();
+                if (c >= H && tid < R::NW) {                 // the ring row of position p (kv_store)
+                    const int kvh = c < H + KV ? c - H : c - H - KV;
+                    char *row = reinterpret_cast<char *>(c < H + KV ? sh.Kc[l] : sh.Vc[l]) +
+                                ((size_t)(p % a.W) * KD + (size_t)kvh * 32) * sizeof(typename R::E);
+                    pd_st(reinterpret_cast<u64 *>(row) + tid, R::pack(&sh.col[0][32 + R::EPW * tid]));
+                    pd_wait_stores();
+                }
+                __syncthreads();
+                if (tid < 32) {
+                    const int off = c < H ? c * 32 : c < H + KV ? D + (c - H) * 32 : D + KD + (c - H - KV) * 32;
+                    pd_st(qkv + (size_t)j * QN + off + tid, pd_word(sh.col[0][32 + tid], tl));
+                }
+                PC_NEXT(g);
+            }
+            // ---- ATT: head h, row j
+            for (int g = PC_FIRST(kA); g < g0 + kO; g += NB) {
+                const int h = (g - g0 - kA) % H, j = (g - g0 - kA) / H, kvh = h / grp, p = pos + j;
+                int lo, cnt;
+                pd_window(a, l, p, &lo, &cnt);
+                // ring words of the window's keys (those of the chunk's rows are
+                // replaced in pc_attention); issued before the wait for this chunk's rows
+                pd_ring_load<F16, 1, 1>(kw, vw, sh.Kc[l], sh.Vc[l], kvh, KD, a.W, lo, cnt + 1);
+                // q_j of head h, then the chunk's k and v rows of KV head kvh
+                auto qi = [&](int e) -> size_t {
+                    if (e < 32) return (size_t)j * QN + h * 32 + e;
+                    e -= 32;
+                    const int r = e / 64, w = e % 64;
+                    return (size_t)r * QN + D + (w < 32 ? 0 : KD) + kvh * 32 + (w & 31);
+                };
+                if (!pc_gather<(32 + MR * 64 + PD_T - 1) / PD_T>(qkv, 32 + MR * 64, qi, tl, sh.in, abortp)) return;
+                if (tid < 32) sh.q[tid] = sh.in[tid];
+                if (tid < MR * 64) {
+                    const int r = tid / 64, w = tid % 64;
+                    if (w < 32) sh.kn[r][w] = sh.in[32 + tid];
+                    else sh.vn[r][w - 32] = sh.in[32 + tid];
+                }
+                __syncthreads();
+                pc_attention<F16, MR>(sh, kw, vw, a, pos, j, lo, cnt, ctx + (size_t)j * D + h * 32, tl + 1u);
+                PC_NEXT(g);
+            }
+            // ---- O: 32 columns of ctx_j . Wo
+            for (int g = PC_FIRST(kO); g < g0 + kS; g += NB) {
+                const int c = (g - g0 - kO) / MR, j = (g - g0 - kO) % MR;
+                if (!pd_fetch<(PD_MAXD + PD_T - 1) / PD_T, 0>(ctx + (size_t)j * D, D, tl + 1u, sh.in, abortp)) return;
+                pc_panel<PD_MAXQ, 1>(sh.in, D, wb, D, sh.red);
+                __syncthreads();
+                const float v = pc_cols<0>(sh.red[0]);
+                if (tid < 64 && (tid & 1) == 0) pd_st(yo + (size_t)j * D + c * 32 + (tid >> 1), pd_word(v, tl + 2u));
+                __syncthreads();
+                PC_NEXT(g);
+            }
+            // every workgroup: x += O out, norm parts for the SwiGLU gain (an2)
+            if (!pc_add_rows<MR>(sh, yo, D, tl + 2u, gn, abortp)) return;
+            // ---- SW: silu(xn . W1) * (xn . W3), 16 columns, RS rows
+            for (int g = PC_FIRST(kS); g < g0 + kW; g += NB) {
+                const int c = (g - g0 - kS) / (MR / it.RS), j0 = ((g - g0 - kS) % (MR / it.RS)) * it.RS;
+                pc_panel<PD_MAXQ, (MR >= 4 ? MR / 4 : 1)>(&sh.xn[j0][0], PD_MAXD, wb, D, sh.red);
+                __syncthreads();
+                for (int jj = tid >> 6; jj < it.RS; jj += PD_NW) {
+                    const int j = j0 + jj;
+                    float s = 0.f;
+#pragma unroll
+                    for (int w = 0; w < PD_NW; w++) s += sh.sw[j][w];
+                    const float sn = rsqrtf(s / (float)D + 1e-5f);
+                    const float r = pd_colsum_half(sh.red[jj], pd_half_col<1>(tid & 63)) * sn;
+                    const float u = pd_pair_other(r);
+                    float sg;
+                    if (a.exact) sg = r / (1.0f + expf(-r));
+                    else sg = r * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-r * 1.44269504088896f));
+                    if (((tid & 63) & 3) == 0)
+                        pd_st(act + (size_t)j * F + c * 16 + ((tid & 63) >> 2), pd_word(sg * u, tl + 3u));
+                }
+                __syncthreads();
+                PC_NEXT(g);
+            }
+            // ---- W2: 32 columns of act_j . W2 (K = F)
+            for (int g = PC_FIRST(kW); g < g0 + NPL; g += NB) {
+                const int c = (g - g0 - kW) / MR, j = (g - g0 - kW) % MR;
+                if (!pd_fetch<(PD_MAXF + PD_T - 1) / PD_T, 0>(act + (size_t)j * F, F, tl + 3u, sh.in, abortp)) return;
+                pc_panel<PD_MAXFQ, 1>(sh.in, F, wb, F, sh.red);
+                __syncthreads();
+                const float v = pc_cols<0>(sh.red[0]);
+                if (tid < 64 && (tid & 1) == 0) pd_st(y2 + (size_t)j * D + c * 32 + (tid >> 1), pd_word(v, tl + 4u));
+                __syncthreads();
+                PC_NEXT(g);
+            }
+            // every workgroup: x += W2 out, norm parts for the next gain (an1, or
+            // the final norm's after the last layer)
+            if (!pc_add_rows<MR>(sh, y2, D, tl + 4u, l + 1 < L ? gn : hg, abortp)) return;
+#undef PC_FIRST
+#undef PC_NEXT
+        }
+
+        // ---- head: 8 vocabulary rows per item against the MR final-normed rows
+        if (b < NHI) {
+            const u32 th = tag0 + 5u * (u32)L;
+            u64 *cand = xb + lay.cand + (size_t)(t & 1) * MR * NHI * 2;
+            for (int hj = b; hj < NHI; hj += NB) {
+                f32x4 hw[2];
+                pd_load_head(hw, P, hj, D);
+                const int r = tid >> 6, c = tid & 63;
+#pragma unroll 2
+                for (int j = 0; j < MR; j++) {
+                    float s = 0.f;
+#pragma unroll
+                    for (int w = 0; w < PD_NW; w++) s += sh.sw[j][w];
+                    const float sn = rsqrtf(s / (float)D + 1e-5f);
+                    float acc = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 2; i++)
+                        if (4 * (c + 64 * i) < D) {
+                            const f32x4 f = *reinterpret_cast<const f32x4 *>(&sh.xn[j][4 * (c + 64 * i)]);
+                            acc = fmaf(f.x, hw[i].x, acc);
+                            acc = fmaf(f.y, hw[i].y, acc);
+                            acc = fmaf(f.z, hw[i].z, acc);
+                            acc = fmaf(f.w, hw[i].w, acc);
+                        }
+                    acc = pd_wave_sum(acc) * sn;
+                    if (c == 0) {
+                        sh.lg[j][r] = acc;
+                        if (t == n - 1) gp(a.logits)[(size_t)j * V + 8 * hj + r] = acc;
+                    }
+                }
+                __syncthreads();
+                if (tid < MR) {
+                    float bv = -INFINITY;
+                    int bi = 0x7fffffff;
+                    for (int rr = 0; rr < 8; rr++)
+                        if (sh.lg[tid][rr] > bv) { bv = sh.lg[tid][rr]; bi = 8 * hj + rr; }
+                    pd_st(cand + ((size_t)tid * NHI + hj) * 2, pd_word(bv, th));
+                    pd_st(cand + ((size_t)tid * NHI + hj) * 2 + 1, ((u64)th << 32) | (u64)(u32)bi);
+                }
+                __syncthreads();
+            }
+        }
+    }
+
+    // ---- the last chunk's greedy tokens and the state for the next launch
+    if (b == 0) {
+        const u32 th = base + (u32)n * NPH;
+        if (!pc_argmax<MR>(sh, xb + lay.cand + (size_t)((n - 1) & 1) * MR * NHI * 2, NHI, th, abortp)) return;
+        if (tid < MR && a.toks_out) gp(a.toks_out)[(size_t)(n - 1) * MR + tid] = sh.tok[tid];
+        if (tid == 0) {
+            const int tk = sh.tok[MR - 1];
+            GAS int *st = gp(a.state);
+            st[0] = pos0 + n * MR;
+            st[1] = 1;
+            st[2] = tk;
+            st[3] = (int)(base + (u32)n * NPH);
+            gp(a.tok)[0] = tk;
+        }
+    }
+}
+
 // ============================================================== entries ==
 extern "C" size_t tlg_dec_persist_xbytes(int V, int D, int L, int F)
 {
     if (V <= 0 || D <= 0 || L <= 0 || F <= 0) return 0;
-    return pd_layout(V, D, L, F).total * sizeof(u64);
+    // the single-token layout or the chunk layout at 8 rows (KD <= D), whichever is larger
+    const size_t a = pd_layout(V, D, L, F).total, c = pc_layout(V, D, D, L, F, PC_MAXMR).total;
+    return (a > c ? a : c) * sizeof(u64);
 }
 
 static int g_pd_cus = 0;
@@ -962,6 +1568,54 @@ extern "C" int tlg_dev_dec_persist(const TlgDecPersist *a, int n, void *stream)
     TlgDecPersist args = *a;
     int nn = n;
     void *kargs[] = {&args, &nn};
+    TLG_HIP(hipLaunchCooperativeKernel(fn, dim3(nb), dim3(PD_T), kargs, 0, (hipStream_t)stream));
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_dec_chunks(const TlgDecPersist *a, int m, const int *toks, int n, void *stream)
+{
+    int rc = tlg_ensure_init();
+    if (rc) return rc;
+    if (!a || n <= 0 || !toks || !(m == 1 || m == 2 || m == 4 || m == 8) || a->pool <= 0 || a->pool > 16 ||
+        a->copy0 < 0 || a->H <= 0 || a->KV <= 0 || a->H % a->KV || a->D != 32 * a->H || a->D > PD_MAXD ||
+        a->F <= 0 || a->F % 32 || a->F > PD_MAXF || a->V <= 0 || a->V % 8 || a->V / 8 > PD_MAXHI || a->L <= 0 ||
+        a->L > TLG_PD_MAXL || a->W < m || a->W > PD_MAXW || a->maxpos <= 0 || !a->cs || !a->sn || !a->logits ||
+        !a->state || !a->tok || !a->xbuf)
+        return tlg_fail(TLG_EINVAL,
+                        "dec_chunks: m=%d n=%d V=%d D=%d L=%d H=%d KV=%d F=%d W=%d (m in 1, 2, 4, 8; head_dim 32, "
+                        "D <= %d, F %% 32 == 0 and F <= %d, V %% 8 == 0 and V <= %d, m <= W <= %d, L <= %d)",
+                        m, n, a ? a->V : 0, a ? a->D : 0, a ? a->L : 0, a ? a->H : 0, a ? a->KV : 0, a ? a->F : 0,
+                        a ? a->W : 0, PD_MAXD, PD_MAXF, 8 * PD_MAXHI, PD_MAXW, TLG_PD_MAXL);
+    for (int c = 0; c < a->pool; c++)
+        if (!a->P[c] || ((uintptr_t)a->P[c] & 15u)) return tlg_fail(TLG_EINVAL, "dec_chunks: weight copy %d", c);
+    for (int l = 0; l < a->L; l++)
+        if (!a->Kc[l] || !a->Vc[l] || ((uintptr_t)a->Kc[l] & 63u) || ((uintptr_t)a->Vc[l] & 63u))
+            return tlg_fail(TLG_EINVAL, "dec_chunks: cache of layer %d", l);
+    if ((uintptr_t)a->xbuf & 15u) return tlg_fail(TLG_EINVAL, "dec_chunks: xbuf alignment");
+    if (!g_pd_cus) {
+        int cus = 0;
+        TLG_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, g_tlg.device));
+        g_pd_cus = cus;
+    }
+    const int rs = m >= 4 ? m / 4 : 1;
+    const int npl = (a->H + (a->D + 2 * a->KV * 32) / 32 + 2 * (a->D / 32)) * m + (a->F / 16) * (m / rs);
+    const int nli = a->L * npl, nhi = a->V / 8;
+    int nb = nli > nhi ? nli : nhi;
+    if (nb > g_pd_cus) nb = g_pd_cus;
+    const void *fn = nullptr;
+    switch (m) {
+    case 1: fn = a->f16 ? (const void *)k_dec_chunk<1, 1> : (const void *)k_dec_chunk<0, 1>; break;
+    case 2: fn = a->f16 ? (const void *)k_dec_chunk<1, 2> : (const void *)k_dec_chunk<0, 2>; break;
+    case 4: fn = a->f16 ? (const void *)k_dec_chunk<1, 4> : (const void *)k_dec_chunk<0, 4>; break;
+    default: fn = a->f16 ? (const void *)k_dec_chunk<1, 8> : (const void *)k_dec_chunk<0, 8>; break;
+    }
+    int per_cu = 0;
+    TLG_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, PD_T, 0));
+    if (per_cu < 1) return tlg_fail(TLG_EHIP, "dec_chunks: the kernel does not fit on a CU");
+    TlgDecPersist args = *a;
+    const int *tk = toks;
+    int nn = n;
+    void *kargs[] = {&args, &tk, &nn};
     TLG_HIP(hipLaunchCooperativeKernel(fn, dim3(nb), dim3(PD_T), kargs, 0, (hipStream_t)stream));
     return TLG_OK;
 }

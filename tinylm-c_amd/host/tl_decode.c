@@ -327,9 +327,30 @@ int tl_decode_set_fused(TlDecode *d, int fused)
 }
 
 /* ---- persistent greedy decoding (tldecode.h tlg_dev_dec_persist) ------------- */
+static int persist_args(TlDecode *d, TlgDecPersist *pa, int *toks_out);
+
 int tl_decode_persist(TlDecode *d, int n, int *toks_out, void *st)
 {
     if (!d || n <= 0) return TLG_EINVAL;
+    TlgDecPersist a;
+    CK(persist_args(d, &a, toks_out));
+    CK(tlg_dev_dec_persist(&a, n, st));
+    d->next_copy = (d->next_copy + n) % d->pool;
+    return 0;
+}
+
+int tl_decode_chunks(TlDecode *d, int m, const int *dtoks, int n, int *toks_out, void *st)
+{
+    if (!d || n <= 0 || m <= 0 || m > d->mmax || !dtoks) return TLG_EINVAL;
+    TlgDecPersist a;
+    CK(persist_args(d, &a, toks_out));
+    CK(tlg_dev_dec_chunks(&a, m, dtoks, n, st));
+    d->next_copy = (d->next_copy + n) % d->pool;
+    return 0;
+}
+
+static int persist_args(TlDecode *d, TlgDecPersist *pa, int *toks_out)
+{
     const TlModel *md = &d->m;
     TlgDecPersist a;
     memset(&a, 0, sizeof a);
@@ -343,8 +364,7 @@ int tl_decode_persist(TlDecode *d, int n, int *toks_out, void *st)
     a.cs = d->rcos; a.sn = d->rsin;
     for (int l = 0; l < md->L; l++) { a.Kc[l] = d->Kc[l]; a.Vc[l] = d->Vc[l]; }
     a.logits = d->logits; a.state = d->state; a.tok = d->tok; a.toks_out = toks_out; a.xbuf = d->xbuf;
-    CK(tlg_dev_dec_persist(&a, n, st));
-    d->next_copy = (d->next_copy + n) % d->pool;
+    *pa = a;
     return 0;
 }
 

@@ -67,6 +67,12 @@ int tl_decode_set_fused(TlDecode *d, int fused);
  * F <= 1024 (F % 32 == 0), V % 8 == 0, W <= 256.  tl_decode_persist_status
  * synchronizes and reports an aborted launch (TLG_EHIP; then reset). */
 int tl_decode_persist(TlDecode *d, int n, int *toks_out, void *stream);
+/* n chunks of m rows (m = 1, 2, 4, 8; m <= mmax) of the device tokens dtoks[n
+ * m] in ONE persistent launch (tldecode.h tlg_dev_dec_chunks): forward_chunk
+ * over given tokens (prefill, speculative verification); toks_out[n m] (device,
+ * or NULL) gets every row's argmax, logits the last chunk's m rows.  Same
+ * shape limits as tl_decode_persist. */
+int tl_decode_chunks(TlDecode *d, int m, const int *dtoks, int n, int *toks_out, void *stream);
 int tl_decode_persist_status(TlDecode *d, void *stream);
 /* Synchronize and read the state: {next position, rows, last token}. */
 int tl_decode_state(TlDecode *d, int *state, void *stream);

@@ -100,6 +100,7 @@ SIGNATURES = {
                                    _vp]),
     "tlg_dec_persist_xbytes": (_sz, [_i, _i, _i, _i]),
     "tlg_dev_dec_persist": (_i, [_vp, _i, _vp]),
+    "tlg_dev_dec_chunks": (_i, [_vp, _i, _vp, _i, _vp]),
     "tlg_dec_persist_status": (_i, [_vp, _vp]),
 }
 
@@ -415,6 +416,12 @@ class Decode:
         device int32 buffer of n entries for the chosen tokens, or None."""
         return self._ck(self.host.dll.tl_decode_persist(self.h, n, toks, stream), "tl_decode_persist")
 
+    def persist_chunks(self, m, toks, n, stream, out=None):
+        """n chunks of m rows of the device int32 tokens `toks` (n * m of
+        them) in one persistent launch (asynchronous); out: a device int32
+        buffer of n * m entries for every row's argmax, or None."""
+        return self._ck(self.host.dll.tl_decode_chunks(self.h, m, toks, n, out, stream), "tl_decode_chunks")
+
     def persist_status(self, stream):
         """Synchronize; raises if a persistent launch aborted."""
         return self._ck(self.host.dll.tl_decode_persist_status(self.h, stream), "tl_decode_persist_status")
@@ -595,6 +602,8 @@ class Host:
         d.tl_decode_greedy_step.argtypes = [_vp, _i, _vp]
         d.tl_decode_persist.argtypes = [_vp, _i, _vp, _vp]
         d.tl_decode_persist.restype = _i
+        d.tl_decode_chunks.argtypes = [_vp, _i, _vp, _i, _vp, _vp]
+        d.tl_decode_chunks.restype = _i
         d.tl_decode_persist_status.argtypes = [_vp, _vp]
         d.tl_decode_persist_status.restype = _i
         d.tl_decode_set_fused.argtypes = [_vp, _i]
