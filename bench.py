@@ -479,7 +479,7 @@ def model_of(name):
                 n_mtp=cfg["n_mtp"]), cfg["R"] // 256
 
 
-def bench_full_step(lib, host, stream, name, steps, warmup=3):
+def bench_full_step(lib, host, stream, name, steps, warmup=3, eager=False):
     """The whole training step on the device (host/tl_train.h): forward,
     backward with the MTP heads, gradnorm and AdamW -- tinylm.c's
     train_loop body (:2627-2633), every activation resident in HBM --
@@ -498,18 +498,23 @@ def bench_full_step(lib, host, stream, name, steps, warmup=3):
     tr.step(stream)                                   # sizes every scratch buffer
     loss0 = tr.loss(stream)
     phases = tr.time_phases(stream)
-    tr.graph_build(stream)
+    if eager:                                       # kernel by kernel (profilers trace these)
+        run = lambda: tr.step(stream)  # noqa: E731
+    else:
+        tr.graph_build(stream)
+        run = lambda: tr.graph_step(stream)  # noqa: E731
     for _ in range(warmup):
-        tr.graph_step(stream)
+        run()
     check(lib.tlg_stream_sync(stream), "sync")
-    ms, _ = time_steps(lib, lambda: tr.graph_step(stream), stream, steps)
+    ms, _ = time_steps(lib, run, stream, steps)
     loss1 = tr.loss(stream)
     ms_step = ms / steps
     return {"model": kw, "batch": B, "rows": N, "params": tr.np, "steps": steps,
             "ms_per_step": round(ms_step, 4), "tok_s": round(N / (ms_step / 1e3), 1),
             "phases_ms_eager": {"forward": round(phases[0], 4), "backward": round(phases[1], 4),
                                 "gradnorm_adamw": round(phases[2], 4)},
-            "loss_first": round(loss0, 4), "loss_after": round(loss1, 4)}
+            "loss_first": round(loss0, 4), "loss_after": round(loss1, 4),
+            "launch": "enqueued step by step" if eager else "one HIP graph per step"}
 
 
 DECODE_MODEL = dict(V=2048, D=384, L=8, H=12, KV=3, F=1024, T=256)
@@ -696,6 +701,8 @@ def main():
                     help="greedy decode steps in one persistent launch (tl_decode_persist); 0 skips")
     ap.add_argument("--full-steps", type=int, default=30,
                     help="timed whole training steps (forward + backward + AdamW on the device); 0 skips")
+    ap.add_argument("--full-eager", action="store_true",
+                    help="enqueue the whole training step launch by launch instead of replaying its graph")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
@@ -792,7 +799,7 @@ def main():
         log(f"[moe] {moe}")
     full = None
     if args.full_steps > 0:
-        full = bench_full_step(lib, host, stream, args.config, args.full_steps)
+        full = bench_full_step(lib, host, stream, args.config, args.full_steps, eager=args.full_eager)
         full["gemm_set_share"] = round(ms_step / full["ms_per_step"], 4)
         log(f"[full step] {full}")
     dec_full = None

@@ -932,7 +932,8 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
 //                                the k and v items store the MR new ring rows
 //                                of their KV head (kv_store, :3775-3780) and
 //                                publish them in the ring's precision
-//   ATT  H * MR items            head h, row j: softmax attention of q_j over
+//   ATT  H * MR items            head h, row j (ordered by KV head, then row,
+//                                then head): softmax attention of q_j over
 //                                the window of position pos + j (attn_body,
 //                                :3639-3715): ring keys before pos, the
 //                                chunk's new keys pos .. pos + j, and -- as the
@@ -1385,7 +1386,10 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_chunk(TlgDecPersist a, const in
             }
             // ---- ATT: head h, row j
             for (int g = PC_FIRST(kA); g < g0 + kO; g += NB) {
-                const int h = (g - g0 - kA) % H, j = (g - g0 - kA) / H, kvh = h / grp, p = pos + j;
+                // items (KV head, row, head of the group) in that order: the rows and
+                // heads reading one KV head's ring window are consecutive (one XCD)
+                const int ka = g - g0 - kA, kvh = ka / (MR * grp), j = (ka / grp) % MR;
+                const int h = kvh * grp + ka % grp, p = pos + j;
                 int lo, cnt;
                 pd_window(a, l, p, &lo, &cnt);
                 // ring words of the window's keys (those of the chunk's rows are
