@@ -1007,7 +1007,7 @@ extern "C" int tlg_tune_group_policy(const int *cands, int ncands, double min_wa
 
 extern "C" int tlg_tune_group(int cfg)
 {
-    if (cfg != -1 && cfg != 0 && cfg != 1 && cfg != 3 && cfg != 4 && (cfg < 8 || cfg > 21))
+    if (cfg != -1 && cfg != 0 && cfg != 1 && cfg != 3 && cfg != 4 && (cfg < 8 || cfg >= kNumCfgs))
         return tlg_fail(TLG_EINVAL, "tlg_tune_group: config %d", cfg);
     g_group_cfg = cfg;
     return TLG_OK;
