@@ -195,7 +195,8 @@ SHAPES = [
     (4096, 256, 768, 4, 2.0, ()),      # the MoE training config, skewed routing
     (4096, 256, 768, 4, 0.0, ()),
     (67, 32, 48, 3, 0.0, ()),          # ragged N, odd E
-    (2500, 64, 96, 5, 1.0, (3,)),      # crosses the 1024-token index rounds, an empty expert
+    (2500, 64, 96, 5, 1.0, (3,)),      # several 1024-token index chunks, an empty expert
+    (9000, 16, 32, 4, 1.0, ()),        # crosses the index kernel's 8192-token rounds
     (300, 16, 32, 64, 0.0, ()),        # the maximum E: most experts hold 0-10 rows
     (1, 8, 8, 4, 0.0, ()),             # one token
     (513, 32, 64, 1, 0.0, ()),         # one expert takes every token

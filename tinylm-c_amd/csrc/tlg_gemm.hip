@@ -52,20 +52,51 @@ enum { RC = 0, OC = 1 };
 
 // Stage one operand tile into registers.  OUTER = tile extent along the
 // operand's output index, rows/cols beyond `oext` or r beyond `rend` read 0.
-template <int LAY, int OUTER, int BK, bool VEC, int NT>
+//
+// Two forms serve the expert GEMMs of the MoE layer (float4 path only):
+//   G   gathered rows: the operand's memory row of tile row x is rs[q], read
+//       from a row map -- once per tile for an RC operand (rows(): the rows
+//       are output rows), once per stage for an OC operand (prep(): the rows
+//       are reduction steps; prep runs a full prefetch round ahead of the
+//       load that uses it, so waiting for the map never waits for the
+//       operand loads issued after it).
+//   PB  paired columns (OC only): tile columns [0, OUTER/2) come from P and
+//       [OUTER/2, OUTER) from P2, both at columns o0 + [0, OUTER/2).
+template <int LAY, int OUTER, int BK, bool VEC, int NT, bool G = false, bool PB = false>
 struct TileLoader {
     static constexpr int NCH = OUTER * BK / 4;        // float4 chunks per tile
     static constexpr int PER = NCH / NT;              // chunks per thread
+    static constexpr int HALF = OUTER / 2;
     static_assert(NCH % NT == 0, "tile must split evenly over the workgroup's threads");
+    static_assert(!PB || (LAY == OC && HALF % 4 == 0), "paired columns: OC tiles");
+    static_assert(!(G || PB) || VEC, "gathered / paired tiles load float4");
     f32x4 v[PER];
     unsigned ok;                                      // bit q: chunk q in range
+    int rs[G ? PER : 1];                              // gathered memory rows
+
+    __device__ __forceinline__ void rows(const int *__restrict__ map, int o0, int oext, int tid)
+    {
+#pragma unroll
+        for (int q = 0; q < PER; q++) {
+            const int e = tid + NT * q;
+            rs[q] = map[min(o0 + e / (BK / 4), oext - 1)];
+        }
+    }
+    __device__ __forceinline__ void prep(const int *__restrict__ map, int r0, int rend, int tid)
+    {
+#pragma unroll
+        for (int q = 0; q < PER; q++) {
+            const int e = tid + NT * q;
+            rs[q] = map[min(r0 + e / (OUTER / 4), rend - 1)];
+        }
+    }
 
     // The float4 path issues every load unconditionally from a clamped, in-
     // bounds address and zeroes out-of-range chunks at store time: branch-free
     // loads let the compiler count outstanding loads exactly, so waiting for
     // one stage does not wait for the stages prefetched after it.
     __device__ __forceinline__ void load(const float *__restrict__ P, int ld, int o0, int oext,
-                                         int r0, int rend, int tid)
+                                         int r0, int rend, int tid, const float *__restrict__ P2 = nullptr)
     {
         ok = 0;
 #pragma unroll
@@ -74,6 +105,8 @@ struct TileLoader {
             int o, r;
             if (LAY == RC) { o = e / (BK / 4); r = (e % (BK / 4)) * 4; }
             else           { r = e / (OUTER / 4); o = (e % (OUTER / 4)) * 4; }
+            const float *Pq = P;
+            if (PB && o >= HALF) { o -= HALF; Pq = P2; }
             const int go = o0 + o, gr = r0 + r;
             f32x4 x = {0.f, 0.f, 0.f, 0.f};
             if (VEC) {
@@ -82,7 +115,8 @@ struct TileLoader {
                 // oext-4, rows to rend-1 (rend, oext are multiples of 4 here)
                 const int gc = (LAY == RC) ? min(go, oext - 1) : min(go, oext - 4);
                 const int rc = (LAY == RC) ? min(gr, rend - 4) : min(gr, rend - 1);
-                const float *p = (LAY == RC) ? P + (size_t)gc * ld + rc : P + (size_t)rc * ld + gc;
+                const size_t row = G ? (size_t)rs[q] : (size_t)((LAY == RC) ? gc : rc);
+                const float *p = (LAY == RC) ? Pq + row * ld + rc : Pq + row * ld + gc;
                 x = *reinterpret_cast<const f32x4 *>(p);
             } else {
 #pragma unroll
@@ -172,11 +206,15 @@ struct Tile {
 
 // acc += A(i0.., r) B(r, j0..) over r in [rbeg, rend).  A tile's loads run
 // NR stages ahead through NR register sets; LDS is double buffered.
-template <class T, int LA, int LB, bool VEC>
+// GA: A's rows go through the row map `amap` (RC A: amap[i0 + x] for tile
+// row x; OC A: amap[r]).  PB: B is the column pair (B, B2) of TileLoader.
+template <class T, int LA, int LB, bool VEC, bool GA = false, bool PB = false>
 __device__ __forceinline__ void tile_accumulate(float *__restrict__ smem, const float *__restrict__ A,
                                                 const float *__restrict__ B, int lda, int ldb,
                                                 int i0, int j0, int Mo, int No, int rbeg, int rend,
-                                                f32x16 (&acc)[T::FM][T::FN][T::NCH])
+                                                f32x16 (&acc)[T::FM][T::FN][T::NCH],
+                                                const int *__restrict__ amap = nullptr,
+                                                const float *__restrict__ B2 = nullptr)
 {
     constexpr int BM = T::BM, BN = T::BN, BK = T::BK, RW = T::RW;
     constexpr int SA = LdsSize<LA, BM, BK>::value, SB = LdsSize<LB, BN, BK>::value;
@@ -191,15 +229,33 @@ __device__ __forceinline__ void tile_accumulate(float *__restrict__ smem, const 
     // the paths meet, and it would then wait for all of them, the prefetch
     // included, before every LDS store.
     auto stage_r = [&](int st) { return rbeg + min(st, nsteps - 1) * BK; };
-    TileLoader<LA, BM, BK, VEC, T::THREADS> la0, la1, la2;
-    TileLoader<LB, BN, BK, VEC, T::THREADS> lb0, lb1, lb2;
+    TileLoader<LA, BM, BK, VEC, T::THREADS, GA> la0, la1, la2;
+    TileLoader<LB, BN, BK, VEC, T::THREADS, false, PB> lb0, lb1, lb2;
+    if constexpr (GA && LA == RC) {
+        la0.rows(amap, i0, Mo, tid);
+        la1.rows(amap, i0, Mo, tid);
+        if constexpr (T::NR > 2) la2.rows(amap, i0, Mo, tid);
+    }
+    if constexpr (GA && LA == OC) {
+        la0.prep(amap, rbeg, rend, tid);
+        la1.prep(amap, stage_r(1), rend, tid);
+        if constexpr (T::NR > 2) la2.prep(amap, stage_r(2), rend, tid);
+    }
+    // an OC gather re-arms each register set's row map for the stage it
+    // loads next, NR stages on
+    auto reprep = [&](auto &l, int st) {
+        if constexpr (GA && LA == OC) l.prep(amap, stage_r(st), rend, tid);
+    };
     la0.load(A, lda, i0, Mo, rbeg, rend, tid);
-    lb0.load(B, ldb, j0, No, rbeg, rend, tid);
+    reprep(la0, T::NR);
+    lb0.load(B, ldb, j0, No, rbeg, rend, tid, B2);
     la1.load(A, lda, i0, Mo, stage_r(1), rend, tid);
-    lb1.load(B, ldb, j0, No, stage_r(1), rend, tid);
+    reprep(la1, 1 + T::NR);
+    lb1.load(B, ldb, j0, No, stage_r(1), rend, tid, B2);
     if constexpr (T::NR > 2) {
         la2.load(A, lda, i0, Mo, stage_r(2), rend, tid);
-        lb2.load(B, ldb, j0, No, stage_r(2), rend, tid);
+        reprep(la2, 2 + T::NR);
+        lb2.load(B, ldb, j0, No, stage_r(2), rend, tid, B2);
     }
     la0.store(smem, tid);
     lb0.store(smem + SA, tid);
@@ -227,7 +283,8 @@ __device__ __forceinline__ void tile_accumulate(float *__restrict__ smem, const 
     // into the other LDS buffer.  NR = 3 keeps loads three stages ahead.
     auto step = [&](int st, auto &lac, auto &lbc, auto &lan, auto &lbn) {
         lac.load(A, lda, i0, Mo, stage_r(st + T::NR), rend, tid);
-        lbc.load(B, ldb, j0, No, stage_r(st + T::NR), rend, tid);
+        reprep(lac, st + 2 * T::NR);
+        lbc.load(B, ldb, j0, No, stage_r(st + T::NR), rend, tid, B2);
         float *cur = smem + (st & 1) * (SA + SB);
         compute(cur, cur + SA);
         if (st + 1 < nsteps) {
@@ -251,15 +308,15 @@ __device__ __forceinline__ void tile_accumulate(float *__restrict__ smem, const 
     }
 }
 
-// C (beta ? += : =) acc for the valid part of the tile.  32x32 MFMA result
-// layout: lane l, register v holds row 8*(v/4) + 4*(l/32) + v%4, column l%32.
-// With WK > 1 the wave groups' partial tiles go through `red` (LDS, WK*BM*BN
-// floats, free once tile_accumulate has returned) and are summed in wave-group
-// order, so the result does not depend on timing.
-template <class T>
-__device__ __forceinline__ void tile_store(const f32x16 (&accs)[T::FM][T::FN][T::NCH], float *__restrict__ C,
-                                           int ldc, int beta, int Mo, int No, int i0, int j0,
-                                           float *__restrict__ red)
+// put(i, j, v) for every element (i, j) of the tile's valid part (i < Mo,
+// j < No), v its sum.  32x32 MFMA result layout: lane l, register v holds
+// row 8*(v/4) + 4*(l/32) + v%4, column l%32.  With WK > 1 the wave groups'
+// partial tiles go through `red` (LDS, WK*BM*BN floats, free once
+// tile_accumulate has returned) and are summed in wave-group order, so the
+// result does not depend on timing.
+template <class T, class Put>
+__device__ __forceinline__ void tile_epi(const f32x16 (&accs)[T::FM][T::FN][T::NCH], int Mo, int No, int i0,
+                                         int j0, float *__restrict__ red, Put put)
 {
     const int lane = threadIdx.x & 63;
     f32x16 acc[T::FM][T::FN];
@@ -283,10 +340,7 @@ __device__ __forceinline__ void tile_store(const f32x16 (&accs)[T::FM][T::FN][T:
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
                     const int i = i0 + wm * T::WM + a * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                    if (i < Mo) {
-                        float *p = C + (size_t)i * ldc + j;
-                        *p = beta ? (*p + acc[a][b][v]) : acc[a][b][v];
-                    }
+                    if (i < Mo) put(i, j, acc[a][b][v]);
                 }
             }
     } else {
@@ -310,13 +364,52 @@ __device__ __forceinline__ void tile_store(const f32x16 (&accs)[T::FM][T::FN][T:
             const int b = ab % T::FN, a = (ab / T::FN) % T::FM, gg = ab / (T::FN * T::FM);
             const int i = i0 + (gg / T::WGN) * T::WM + a * 32 + 8 * (v >> 2) + 4 * (l >> 5) + (v & 3);
             const int j = j0 + (gg % T::WGN) * T::WN + b * 32 + (l & 31);
-            if (i < Mo && j < No) {
-                float *p = C + (size_t)i * ldc + j;
-                *p = beta ? (*p + s) : s;
-            }
+            if (i < Mo && j < No) put(i, j, s);
         }
         __syncthreads();            // `red` aliases the stage buffers of the next tile
     }
+}
+
+// C (beta ? += : =) acc for the valid part of the tile.
+template <class T>
+__device__ __forceinline__ void tile_store(const f32x16 (&accs)[T::FM][T::FN][T::NCH], float *__restrict__ C,
+                                           int ldc, int beta, int Mo, int No, int i0, int j0,
+                                           float *__restrict__ red)
+{
+    tile_epi<T>(accs, Mo, No, i0, j0, red, [&](int i, int j, float v) {
+        float *p = C + (size_t)i * ldc + j;
+        *p = beta ? (*p + v) : v;
+    });
+}
+
+// SwiGLU epilogue of a paired-column tile (TileLoader PB): tile columns
+// [0, BN/2) hold g = X W1 and [BN/2, BN) hold u = X W3 for the output
+// columns jh + [0, BN/2).  The summed tile goes through LDS (after the WK
+// partials, which it must not overlap) so one thread sees both halves; then
+// a = silu(g) u  (tinylm.c:786, :882) for i < Mo, j < No, and g, u too where
+// Cg / Cu are given.
+template <class T>
+__device__ __forceinline__ void tile_swiglu(const f32x16 (&accs)[T::FM][T::FN][T::NCH], float *__restrict__ Ca,
+                                            float *__restrict__ Cg, float *__restrict__ Cu, int ldc, int Mo,
+                                            int No, int i0, int jh, float *__restrict__ red)
+{
+    constexpr int H = T::BN / 2, LD = T::BN + 1;
+    constexpr int OFF = T::WK > 1 ? T::WK * T::TILE : 0;
+    static_assert(OFF + T::BM * LD <= T::lds_max(), "paired tile fits beside the partials");
+    float *L = red + OFF;
+    tile_epi<T>(accs, T::BM, T::BN, 0, 0, red, [&](int i, int j, float v) { L[i * LD + j] = v; });
+    __syncthreads();
+    for (int f = threadIdx.x; f < T::BM * H; f += T::THREADS) {
+        const int x = f / H, c = f % H;
+        const int i = i0 + x, j = jh + c;
+        if (i >= Mo || j >= No) continue;
+        const float g = L[x * LD + c], u = L[x * LD + c + H];
+        const size_t o = (size_t)i * ldc + j;
+        Ca[o] = g / (1.0f + expf(-g)) * u;
+        if (Cg) Cg[o] = g;
+        if (Cu) Cu[o] = u;
+    }
+    __syncthreads();
 }
 
 template <int FM, int FN, int NCH>
@@ -414,6 +507,19 @@ struct Prob {
     const int *eoff;
     long long es;
     int nexp, unit;
+    // Fused forms of the MoE expert GEMMs (tinylm.c:876-888, :911-927):
+    //   amap  A rows gathered through it (the sorted row -> token index)
+    //   B2    NN: second weight of a column pair (W3 beside W1), SwiGLU
+    //         epilogue; tiles_n then counts BN/2-column tiles
+    //   epi   TLG_EPI_*: plain store, SwiGLU (C = a, X1 = g, X2 = u when
+    //         given), SwiGLU backward (da from the tile, g / u in X1 / X2
+    //         replaced by dg / du; C unused), or the top-1 combine (C = out,
+    //         out[omap[i]] = fin[..] + gate[..] * tile row i)
+    const int *amap, *omap;
+    const float *B2;
+    float *X1, *X2;
+    const float *fin, *gate;
+    int epi;
     Seg seg[TLG_MAXSEG];
 };
 struct GroupArgs {
@@ -450,6 +556,31 @@ __device__ __forceinline__ bool expert_of(const Prob &P, const int *eo, int t, i
     return false;
 }
 
+// Accumulation of one expert tile, with its gather / pair form chosen at run
+// time (uniform per problem): PB only for NN problems.
+template <class T, int LA, int LB>
+__device__ __forceinline__ void expert_acc(float *smem, const Prob &P, const Seg &s, const float *A,
+                                           const float *B, const int *amap, int i0, int j0, int Mo, int No,
+                                           int rbeg, int rend, f32x16 (&acc)[T::FM][T::FN][T::NCH])
+{
+    if constexpr (LA == RC && LB == OC) {
+        if (P.B2) {
+            const float *B2 = P.B2 + (B - s.B);
+            if (amap)
+                tile_accumulate<T, LA, LB, true, true, true>(smem, A, B, s.lda, s.ldb, i0, j0, Mo, No, rbeg,
+                                                             rend, acc, amap, B2);
+            else
+                tile_accumulate<T, LA, LB, true, false, true>(smem, A, B, s.lda, s.ldb, i0, j0, Mo, No, rbeg,
+                                                              rend, acc, nullptr, B2);
+            return;
+        }
+    }
+    if (amap)
+        tile_accumulate<T, LA, LB, true, true>(smem, A, B, s.lda, s.ldb, i0, j0, Mo, No, rbeg, rend, acc, amap);
+    else
+        tile_accumulate<T, LA, LB, true>(smem, A, B, s.lda, s.ldb, i0, j0, Mo, No, rbeg, rend, acc);
+}
+
 template <class T, int LA, int LB>
 __device__ __forceinline__ void expert_tile(float *smem, const Prob &P, int local, const int *eo)
 {
@@ -457,14 +588,67 @@ __device__ __forceinline__ void expert_tile(float *smem, const Prob &P, int loca
     int e, t, base, rows, slot0;
     if (P.kind != PK_TN) {
         if (!expert_of(P, eo, local / P.tiles_n, &e, &t, &base, &rows, &slot0)) return;
-        const int i0 = t * T::BM, j0 = (local % P.tiles_n) * T::BN;
+        // a paired tile covers BN/2 output columns
+        const int i0 = t * T::BM, j0 = (local % P.tiles_n) * (P.B2 ? T::BN / 2 : T::BN);
+        // combine: the tile rows' tokens and gates, staged before the
+        // accumulation so the epilogue waits on one load level, not three
+        __shared__ int s_tok[(LA == RC && LB == OC) ? T::BM : 1];
+        __shared__ float s_gate[(LA == RC && LB == OC) ? T::BM : 1];
+        if constexpr (LA == RC && LB == OC) {
+            if (P.epi == TLG_EPI_COMBINE && (int)threadIdx.x < T::BM) {
+                const int x = threadIdx.x, n = P.omap[base + min(i0 + x, rows - 1)];
+                s_tok[x] = n;
+                s_gate[x] = P.gate[n];
+            }
+        }
         zero_acc(acc);
         for (int k = 0; k < P.nseg; k++) {
             const Seg &s = P.seg[k];
-            tile_accumulate<T, LA, LB, true>(smem, s.A + (size_t)base * s.lda, s.B + (size_t)e * P.es, s.lda,
-                                             s.ldb, i0, j0, rows, P.No, 0, s.R, acc);
+            // gathered: rows of A through amap[base + x]; else A's expert rows
+            const float *A = P.amap ? s.A : s.A + (size_t)base * s.lda;
+            const int *amap = P.amap ? P.amap + base : nullptr;
+            expert_acc<T, LA, LB>(smem, P, s, A, s.B + (size_t)e * P.es, amap, i0, j0, rows, P.No, 0, s.R,
+                                  acc);
         }
-        tile_store<T>(acc, P.C + (size_t)base * P.ldc, P.ldc, P.beta, rows, P.No, i0, j0, smem);
+        const size_t cb = (size_t)base * P.ldc;
+        switch (P.epi) {
+        case TLG_EPI_SWIGLU:
+            tile_swiglu<T>(acc, P.C + cb, P.X1 ? P.X1 + cb : nullptr, P.X2 ? P.X2 + cb : nullptr, P.ldc, rows,
+                           P.No, i0, j0, smem);
+            break;
+        case TLG_EPI_SWIGLU_BWD: {
+            // In place: g <- da u silu'(g), u <- da silu(g)  (tinylm.c:923-925)
+            float *G = P.X1 + cb, *U = P.X2 + cb;
+            const int ld = P.ldc;
+            tile_epi<T>(acc, rows, P.No, i0, j0, smem, [&](int i, int j, float d) {
+                const size_t o = (size_t)i * ld + j;
+                const float z = G[o], uv = U[o];
+                const float sg = 1.0f / (1.0f + expf(-z));
+                const float si = z * sg;
+                const float ds = sg + z * sg * (1.0f - sg);
+                G[o] = d * uv * ds;
+                U[o] = d * si;
+            });
+            break;
+        }
+        case TLG_EPI_COMBINE: {
+            // out[n] = fin[n] + gate[n] y  for token n of sorted row i (:870, :886-888)
+            if constexpr (LA == RC && LB == OC) {
+                __syncthreads();          // the staged tokens, also when the reduction was empty
+                const int ld = P.ldc;
+                float *C = P.C;
+                const float *fin = P.fin;
+                tile_epi<T>(acc, rows, P.No, i0, j0, smem, [&](int i, int j, float y) {
+                    const int x = i - i0;
+                    const size_t o = (size_t)s_tok[x] * ld + j;
+                    C[o] = fmaf(s_gate[x], y, fin[o]);
+                });
+            }
+            break;
+        }
+        default:
+            tile_store<T>(acc, P.C + cb, P.ldc, P.beta, rows, P.No, i0, j0, smem);
+        }
     } else {
         if (!expert_of(P, eo, local / P.tiles, &e, &t, &base, &rows, &slot0)) return;
         const int tile = local % P.tiles;
@@ -472,7 +656,8 @@ __device__ __forceinline__ void expert_tile(float *smem, const Prob &P, int loca
         const int rbeg = base + t * P.unit, rend = min(base + rows, rbeg + P.unit);
         const Seg &s = P.seg[0];
         zero_acc(acc);
-        tile_accumulate<T, LA, LB, true>(smem, s.A, s.B, s.lda, s.ldb, i0, j0, P.Mo, P.No, rbeg, rend, acc);
+        // A's reduction rows are sorted rows; gathered ones map through amap
+        expert_acc<T, LA, LB>(smem, P, s, s.A, s.B, P.amap, i0, j0, P.Mo, P.No, rbeg, rend, acc);
         tile_store<T>(acc, (float *)P.ws + (size_t)(slot0 + t) * P.Mo * P.No, P.No, 0, P.Mo, P.No, i0, j0,
                       smem);
     }
@@ -503,10 +688,12 @@ __device__ __forceinline__ void expert_reduce(const Prob &P, int local, const in
     reduce_range(P.ws + (size_t)slot0 * n, C, P.No, P.No, ns, P.beta, e0, e1, n);
 }
 
-template <class T, int LA, int LB>
+template <class T, int LA, int LB, bool EXP>
 __device__ __forceinline__ void group_tile(float *smem, const Prob &P, int local, const int *eo)
 {
-    if (P.nexp) { expert_tile<T, LA, LB>(smem, P, local, eo); return; }
+    if constexpr (EXP) {
+        if (P.nexp) { expert_tile<T, LA, LB>(smem, P, local, eo); return; }
+    }
     const int z = local / P.tiles, tile = local % P.tiles;
     const int i0 = (tile / P.tiles_n) * T::BM, j0 = (tile % P.tiles_n) * T::BN;
     f32x16 acc[T::FM][T::FN][T::NCH];
@@ -547,7 +734,7 @@ __device__ __forceinline__ int group_item(const GroupArgs &g, int b, int *local,
 
 // `eo`: the expert row offsets of an expert-batched launch, staged in LDS
 // (nullptr for dense launches, which have no expert problems).
-template <class T>
+template <class T, bool EXP>
 __device__ __forceinline__ void group_body(const GroupArgs &g, float *smem, const int *eo)
 {
     int local = 0;
@@ -555,9 +742,9 @@ __device__ __forceinline__ void group_body(const GroupArgs &g, float *smem, cons
     if (p < 0) return;
     const Prob &P = g.p[p];
     switch (P.kind) {
-    case PK_NN: group_tile<T, RC, OC>(smem, P, local, eo); break;
-    case PK_NT: group_tile<T, RC, RC>(smem, P, local, eo); break;
-    case PK_TN: group_tile<T, OC, OC>(smem, P, local, eo); break;
+    case PK_NN: group_tile<T, RC, OC, EXP>(smem, P, local, eo); break;
+    case PK_NT: group_tile<T, RC, RC, EXP>(smem, P, local, eo); break;
+    case PK_TN: group_tile<T, OC, OC, EXP>(smem, P, local, eo); break;
     case PK_ZERO: {
         const size_t n = (size_t)P.Mo * P.No, e0 = (size_t)local * TLG_ZERO_CHUNK;
         const size_t e1 = e0 + TLG_ZERO_CHUNK < n ? e0 + TLG_ZERO_CHUNK : n;
@@ -565,7 +752,9 @@ __device__ __forceinline__ void group_body(const GroupArgs &g, float *smem, cons
         break;
     }
     default: {
-        if (P.nexp) { expert_reduce(P, local, eo); break; }
+        if constexpr (EXP) {
+            if (P.nexp) { expert_reduce(P, local, eo); break; }
+        }
         const size_t n = (size_t)P.Mo * P.No;
         const size_t e0 = (size_t)local * TLG_RED_CHUNK;
         const size_t e1 = e0 + TLG_RED_CHUNK < n ? e0 + TLG_RED_CHUNK : n;
@@ -578,23 +767,27 @@ template <class T>
 __global__ __launch_bounds__(T::THREADS) void k_group(GroupArgs g)
 {
     __shared__ __attribute__((aligned(16))) float smem[T::lds_max()];
-    group_body<T>(g, smem, nullptr);
+    group_body<T, false>(g, smem, nullptr);
 }
 
 // The same code for the expert-batched launches of the MoE layer, under its
 // own name so profiles separate MoE launches from the dense grouped GEMMs.
 // Every problem of such a launch shares one row-offset array; it is staged in
 // LDS once, so finding a work item's expert costs no dependent global loads.
+// The fused variants (gathered rows, paired columns, epilogues) are separate
+// inlined code paths; left alone the compiler gives their accumulators
+// disjoint AGPRs and the kernel drops to 3 waves per SIMD, so it is held to
+// the dense kernels' 4 (no spills at that bound).
 #define TLG_MAX_EXPERTS 64
 template <class T>
-__global__ __launch_bounds__(T::THREADS) void k_expert_group(GroupArgs g)
+__global__ __launch_bounds__(T::THREADS) __attribute__((amdgpu_waves_per_eu(4))) void k_expert_group(GroupArgs g)
 {
     __shared__ __attribute__((aligned(16))) float smem[T::lds_max()];
     __shared__ int eo[TLG_MAX_EXPERTS + 1];
     const int E = g.p[0].nexp;
     for (int i = threadIdx.x; i <= E; i += blockDim.x) eo[i] = g.p[0].eoff[i];
     __syncthreads();
-    group_body<T>(g, smem, eo);
+    group_body<T, true>(g, smem, eo);
 }
 
 __global__ void k_zero(float *__restrict__ p, size_t n)
@@ -1312,7 +1505,25 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
         P.eoff = eoff;
         P.nexp = E;
         P.es = c.es;
-        bool vec = c.C && (c.es % 4 == 0);
+        P.amap = c.amap;
+        P.omap = c.omap;
+        P.B2 = c.B2;
+        P.epi = c.epi;
+        P.X1 = c.X1;
+        P.X2 = c.X2;
+        P.fin = c.fin;
+        P.gate = c.gate;
+        // fused forms: the pair only with the SwiGLU epilogue of an NN call;
+        // SwiGLU backward on NT (da = dy W2^T); the combine on NN
+        const bool epi_ok =
+            (c.epi == TLG_EPI_STORE && !c.B2) ||
+            (c.epi == TLG_EPI_SWIGLU && c.op == 0 && c.B2 && al16(c.B2) && c.nseg == 1 && !c.beta) ||
+            (c.epi == TLG_EPI_SWIGLU_BWD && c.op == 1 && !c.B2 && c.X1 && c.X2) ||
+            (c.epi == TLG_EPI_COMBINE && c.op == 0 && !c.B2 && c.omap && c.fin && c.gate && c.nseg == 1 &&
+             !c.beta && !c.amap);
+        if (!epi_ok || (c.amap && c.nseg != 1))
+            return tlg_fail(TLG_EINVAL, "expert launch: call %d: bad epilogue %d / gather / pair", i, c.epi);
+        bool vec = (c.C || c.epi == TLG_EPI_SWIGLU_BWD) && (c.es % 4 == 0);
         for (int s = 0; s < c.nseg; s++) {
             const int Ns = s ? c.Nseg[s] : c.N;
             Seg &g = P.seg[s];
@@ -1347,7 +1558,7 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
         double t = 0;
         for (int i = 0; i < n; i++) {
             const Prob &P = probs[i];
-            const double tn = cdiv(P.No, c.bn);
+            const double tn = cdiv(P.No, P.B2 ? c.bn / 2 : c.bn);
             t += P.kind == PK_TN ? cdiv(P.Mo, c.bm) * tn * (rows / rps + E) : (cdiv(rows, c.bm) + E) * tn;
         }
         return t;
@@ -1360,7 +1571,7 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     int order[TLG_MAXPROB / 2];
     for (int i = 0; i < n; i++) {
         Prob &P = probs[i];
-        P.tiles_n = cdiv(P.No, tc.bn);
+        P.tiles_n = cdiv(P.No, P.B2 ? tc.bn / 2 : tc.bn);
         if (P.kind == PK_TN) {
             P.tiles = cdiv(P.Mo, tc.bm) * P.tiles_n;
             P.unit = rps;

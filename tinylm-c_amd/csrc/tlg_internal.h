@@ -54,6 +54,8 @@ int tlg_group_flush_launch(hipStream_t st);
 //   op 0 (mm):     C[rows]  = A[rows] B_e                 B_e = B + e*es
 //   op 1 (mm_bt):  C[rows] (beta)= sum_s A_s[rows] B_{s,e}^T  (nseg <= 2)
 //   op 2 (mm_atb): C_e (beta)= A[rows]^T B[rows]          C_e = C + e*es
+// Epilogues of an expert GEMM (TlgExpertCall.epi).
+enum { TLG_EPI_STORE = 0, TLG_EPI_SWIGLU = 1, TLG_EPI_SWIGLU_BWD = 2, TLG_EPI_COMBINE = 3 };
 struct TlgExpertCall {
     int op, beta;
     float *C;
@@ -63,6 +65,13 @@ struct TlgExpertCall {
     const float *B[2];
     int Nseg[2];
     long long es;
+    // fused forms (zero = none): A rows through amap; NN column pair B2
+    // (requires epi SWIGLU); epilogue epi with its operands
+    const int *amap, *omap;
+    const float *B2;
+    int epi;
+    float *X1, *X2;
+    const float *fin, *gate;
 };
 int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E, int rows, hipStream_t st);
 

@@ -7,10 +7,12 @@
 //
 // Data layout in HBM.  Token-order buffers are the caller's (fnorm, fin, out,
 // dout, d_fnorm: N x D; rprobs N x E; assign, gate: N).  The library keeps
-// one scratch arena with the expert-grouped ("sorted") rows: row i of Xg, g,
-// u, a, y, dy, da holds token idx[i]; expert e owns sorted rows
-// [eoff[e], eoff[e+1]) in ascending token order, the order in which the
-// reference gathers them (:876).  pos[n] is token n's sorted row.
+// one scratch arena with the expert-grouped ("sorted") rows: row i of g, u,
+// a, y, dy holds token idx[i]; expert e owns sorted rows [eoff[e],
+// eoff[e+1]) in ascending token order, the order in which the reference
+// gathers them (:876).  pos[n] is token n's sorted row.  The gathered
+// input rows Xg = fnorm[idx] are never stored: the expert GEMMs read fnorm
+// through idx.
 //
 // Kernels (one pass each over the data they touch):
 //   k_moe_route     router logits as the reference's own FMA chain over D
@@ -18,14 +20,17 @@
 //                   softmax, strict-greater argmax (ties -> lowest expert)
 //   k_moe_index     stable counting sort of the tokens by expert (one
 //                   workgroup, wave ballots; no atomics)
-//   k_gather_rows   Xg = fnorm[idx]
 //   expert GEMMs    tlg_expert_launch (grouped MFMA tiles, every expert in
-//                   one launch; the rows per expert stay on the device)
-//   k_swiglu(_bwd)  a = silu(g) u and its backward
-//   k_moe_combine   out[n] = fin[n] + gate[n] y[pos[n]]
+//                   one launch; the rows per expert stay on the device),
+//                   with the MoE's elementwise steps fused in:
+//                     W1 | W3   one paired-column launch, rows gathered from
+//                               fnorm, a = silu(g) u in the epilogue
+//                     W2 (fwd)  out[n] = fin[n] + gate[n] y in the epilogue
+//                     da        the SwiGLU backward in the epilogue
+//                     dW1, dW3  fnorm rows gathered along the reduction
 //   k_moe_dgate     d_gate[n] = dout[n] . y[pos[n]],  dy = gate dout
-//   k_moe_router_bwd  softmax backward with the load-balance term
-//   k_moe_dfnorm    d_fnorm = dX[pos] + d_rt wr^T   (the router mm_bt, :944)
+//   k_moe_router_bwd  softmax backward with the load-balance term, then
+//                   d_fnorm = dX[pos] + d_rt wr^T   (the router mm_bt, :944)
 // and dWr += fnorm^T d_rt through the generic mm_atb launch (:945).
 #include "tlg_internal.h"
 #include <initializer_list>
@@ -53,15 +58,40 @@ __global__ __launch_bounds__(256) void k_moe_route(const float *__restrict__ X, 
     const int n0 = blockIdx.x * MOE_TOK, tid = threadIdx.x;
     for (int p = tid; p < MOE_TOK * E; p += 256) lg[p] = 0.f;
     for (int d0 = 0; d0 < D; d0 += dch) {
-        const int dn = min(dch, D - d0);
+        const int dn = min(dch, D - d0);        // a multiple of 4 (D and dch are)
         __syncthreads();
-        for (int p = tid; p < MOE_TOK * dch; p += 256) {
-            const int t = p / dch, d = p - t * dch;
-            xs[t * (dch + 1) + d] = (n0 + t < N && d < dn) ? X[(size_t)(n0 + t) * D + d0 + d] : 0.f;
+        // staging: RB loads per thread in flight before any is stored
+        constexpr int RB = 4;
+        const int nq = MOE_TOK * (dn / 4);
+        for (int q0 = tid; q0 < nq; q0 += 256 * RB) {
+            float4 v[RB];
+#pragma unroll
+            for (int k = 0; k < RB; k++) {
+                const int q = q0 + k * 256, t = q / (dn / 4), c = q - t * (dn / 4);
+                v[k] = (q < nq && n0 + t < N)
+                           ? *reinterpret_cast<const float4 *>(X + (size_t)(n0 + t) * D + d0 + 4 * c)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int k = 0; k < RB; k++) {
+                const int q = q0 + k * 256, t = q / (dn / 4), c = q - t * (dn / 4);
+                if (q < nq) {
+                    float *x = xs + t * (dch + 1) + 4 * c;
+                    x[0] = v[k].x; x[1] = v[k].y; x[2] = v[k].z; x[3] = v[k].w;
+                }
+            }
         }
-        for (int p = tid; p < dch * E; p += 256) {
-            const int d = p / E;
-            wsm[p] = d < dn ? Wr[(size_t)(d0 + d) * E + p % E] : 0.f;
+        const int nw = dn * E;
+        for (int p0 = tid; p0 < nw; p0 += 256 * RB) {
+            float v[RB];
+#pragma unroll
+            for (int k = 0; k < RB; k++) {
+                const int p = p0 + k * 256;
+                v[k] = p < nw ? Wr[(size_t)d0 * E + p] : 0.f;
+            }
+#pragma unroll
+            for (int k = 0; k < RB; k++)
+                if (p0 + k * 256 < nw) wsm[p0 + k * 256] = v[k];
         }
         __syncthreads();
         for (int p = tid; p < MOE_TOK * E; p += 256) {
@@ -118,143 +148,111 @@ static size_t route_lds(int dch, int E)
 
 // ------------------------------------------------------- expert index --
 // Stable counting sort of tokens by expert in one workgroup of 16 waves.
-// A wave finds each lane's rank among the lanes routed to the same expert
-// with one ballot per expert; per-wave counts are scanned in wave order, so
-// tokens keep ascending order inside each expert.  Tokens whose expert is
-// out of range are left out (pos = -1).
-__device__ __forceinline__ void wave_rank(int a, int E, int lane, int w, int (*wc)[TLG_MOE_MAXE], int *rank)
-{
-    for (int e = 0; e < E; e++) {
-        const unsigned long long m = __ballot(a == e);
-        if (a == e) *rank = __popcll(m & ((1ull << lane) - 1ull));
-        if (lane == 0) wc[w][e] = __popcll(m);
-    }
-}
-
+// Token n = (8 r + k) 1024 + 64 w + lane sits in round r, chunk k, wave w.
+// A round's assignments load at once (8 per thread); a wave ranks each
+// lane among the lanes of its chunk routed to the same expert with one
+// ballot per expert and keeps the per-(chunk, wave) counts in LDS; wave e
+// then scans expert e's counts in token order (two slots per lane and a
+// shuffle scan), carrying the running count across rounds.  So tokens keep
+// ascending order inside each expert, with no atomics.  A token whose
+// expert is out of range is left out (pos = -1) and, when `out` is given,
+// gets out[n] = fin[n] (moe_forward's residual alone, :870).
+#define MOE_IDX_CH 8
 __global__ __launch_bounds__(1024) void k_moe_index(const int *__restrict__ assign, int N, int E,
                                                     int *__restrict__ idx, int *__restrict__ pos,
-                                                    int *__restrict__ eoff)
+                                                    int *__restrict__ eoff, const float *__restrict__ fin,
+                                                    float *__restrict__ out, int D)
 {
-    __shared__ int wc[16][TLG_MOE_MAXE];
-    __shared__ int run[TLG_MOE_MAXE + 1];
+    __shared__ int wc[MOE_IDX_CH * 16][TLG_MOE_MAXE];    // (chunk, wave) slot x expert
+    __shared__ int run[TLG_MOE_MAXE];
     __shared__ int off[TLG_MOE_MAXE + 1];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    if (tid <= TLG_MOE_MAXE) run[tid] = 0;
+    const int per_round = MOE_IDX_CH * 1024;
+    const int rounds = (N + per_round - 1) / per_round;
+    if (tid < TLG_MOE_MAXE) run[tid] = 0;
+    int av[MOE_IDX_CH], rel[MOE_IDX_CH];
+    for (int rd = 0; rd < rounds; rd++) {
+        const int n0 = rd * per_round + tid;
+#pragma unroll
+        for (int k = 0; k < MOE_IDX_CH; k++) {
+            const int n = n0 + k * 1024;
+            av[k] = n < N ? assign[n] : -1;
+        }
+#pragma unroll
+        for (int k = 0; k < MOE_IDX_CH; k++) {
+            rel[k] = 0;
+            for (int e = 0; e < E; e++) {
+                const unsigned long long m = __ballot(av[k] == e);
+                if (av[k] == e) rel[k] = __popcll(m & ((1ull << lane) - 1ull));
+                if (lane == 0) wc[k * 16 + w][e] = __popcll(m);
+            }
+        }
+        __syncthreads();
+        // exclusive scan of expert e's 128 slot counts, plus the carry
+        for (int e = w; e < E; e += 16) {
+            const int c0 = wc[2 * lane][e], c1 = wc[2 * lane + 1][e];
+            int inc = c0 + c1;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int t = __shfl_up(inc, o);
+                if (lane >= o) inc += t;
+            }
+            const int ex = inc - (c0 + c1) + run[e];
+            wc[2 * lane][e] = ex;
+            wc[2 * lane + 1][e] = ex + c0;
+            const int tot = __shfl(inc, 63);
+            if (lane == 63) run[e] += tot;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < MOE_IDX_CH; k++) {
+            const int a = av[k];
+            rel[k] = (a >= 0 && a < E) ? rel[k] + wc[k * 16 + w][a] : -1;
+            const int n = n0 + k * 1024;
+            // several rounds: park the in-expert rank until the offsets exist
+            if (rounds > 1 && n < N) pos[n] = rel[k];
+        }
+        __syncthreads();
+    }
+    if (w == 0) {
+        // exclusive scan of the expert totals (E <= 64: one per lane)
+        const int c = lane < E ? run[lane] : 0;
+        int inc = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(inc, o);
+            if (lane >= o) inc += t;
+        }
+        if (lane < E) off[lane] = inc - c;
+        if (lane == 63) off[E] = inc;
+    }
     __syncthreads();
-    // pass 1: tokens per expert
-    for (int c0 = 0; c0 < N; c0 += 1024) {
-        const int n = c0 + tid;
-        const int a = n < N ? assign[n] : -1;
-        int rank = 0;
-        wave_rank(a, E, lane, w, wc, &rank);
-        __syncthreads();
-        if (tid < E) {
-            int r = run[tid];
-            for (int k = 0; k < 16; k++) r += wc[k][tid];
-            run[tid] = r;
+    if (tid <= E) eoff[tid] = off[tid];
+    for (int j = 0; j * 1024 < N; j++) {
+        const int n = j * 1024 + tid;
+        if (n >= N) break;
+        int a, r;
+        if (rounds == 1) {
+            a = av[0]; r = rel[0];
+#pragma unroll
+            for (int k = 1; k < MOE_IDX_CH; k++)
+                if (j == k) { a = av[k]; r = rel[k]; }
+        } else {
+            a = assign[n];
+            r = pos[n];
         }
-        __syncthreads();
-    }
-    if (tid == 0) {
-        int s = 0;
-        for (int e = 0; e < E; e++) { off[e] = s; s += run[e]; }
-        off[E] = s;
-    }
-    __syncthreads();
-    if (tid <= E) { eoff[tid] = off[tid]; run[tid] = 0; }
-    __syncthreads();
-    // pass 2: placement in token order
-    for (int c0 = 0; c0 < N; c0 += 1024) {
-        const int n = c0 + tid;
-        const int a = n < N ? assign[n] : -1;
-        int rank = 0;
-        wave_rank(a, E, lane, w, wc, &rank);
-        __syncthreads();
-        if (tid < E) {
-            int r = run[tid];
-            for (int k = 0; k < 16; k++) { const int c = wc[k][tid]; wc[k][tid] = r; r += c; }
-            run[tid] = r;
-        }
-        __syncthreads();
-        if (n < N) {
-            const bool ok = a >= 0 && a < E;
-            const int p = ok ? off[a] + wc[w][a] + rank : -1;
-            pos[n] = p;
-            if (ok) idx[p] = n;
-        }
-        __syncthreads();
+        const bool ok = a >= 0 && a < E;
+        const int p = ok ? off[a] + r : -1;
+        pos[n] = p;
+        if (ok) idx[p] = n;
+        else if (out)
+            for (int d = 0; d < D; d += 4)
+                *reinterpret_cast<float4 *>(out + (size_t)n * D + d) =
+                    *reinterpret_cast<const float4 *>(fin + (size_t)n * D + d);
     }
 }
 
-// ---------------------------------------------------------- elementwise --
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-// dst[i] = src[idx[i]] for the eoff[E] routed rows (D % 4 == 0).
-__global__ void k_gather_rows(const float *__restrict__ src, const int *__restrict__ idx,
-                              const int *__restrict__ eoff, int E, int D, float *__restrict__ dst)
-{
-    const int d4 = D >> 2;
-    const size_t total = (size_t)eoff[E] * d4;
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total; q += stride) {
-        const size_t i = q / d4, c = q % d4;
-        reinterpret_cast<f32x4 *>(dst)[i * d4 + c] =
-            reinterpret_cast<const f32x4 *>(src)[(size_t)idx[i] * d4 + c];
-    }
-}
-
-// a = silu(g) * u over the routed rows; silu(z) = z / (1 + e^-z) (:786).
-__global__ void k_swiglu(const float *__restrict__ g, const float *__restrict__ u, float *__restrict__ a,
-                         const int *__restrict__ eoff, int E, int F)
-{
-    const size_t total = (size_t)eoff[E] * F;
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-        const float z = g[i];
-        a[i] = z / (1.0f + expf(-z)) * u[i];
-    }
-}
-
-// In place: g <- da * u * silu'(g), u <- da * silu(g)  (:923-925).
-__global__ void k_swiglu_bwd(float *__restrict__ g, float *__restrict__ u, const float *__restrict__ da,
-                             const int *__restrict__ eoff, int E, int F)
-{
-    const size_t total = (size_t)eoff[E] * F;
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-        const float z = g[i], uv = u[i], d = da[i];
-        const float sg = 1.0f / (1.0f + expf(-z));
-        const float si = z * sg;
-        const float ds = sg + z * sg * (1.0f - sg);
-        g[i] = d * uv * ds;
-        u[i] = d * si;
-    }
-}
-
-// out[n] = fin[n] + gate[n] * y[pos[n]]  (:870, :886-888); fin alone for a
-// token with no expert.
-__global__ void k_moe_combine(const float *__restrict__ fin, const float *__restrict__ y,
-                              const int *__restrict__ pos, const float *__restrict__ gate, int N, int D,
-                              float *__restrict__ out)
-{
-    const int d4 = D >> 2;
-    const size_t total = (size_t)N * d4;
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total; q += stride) {
-        const size_t n = q / d4, c = q % d4;
-        const f32x4 f = reinterpret_cast<const f32x4 *>(fin)[q];
-        const int p = pos[n];
-        f32x4 o = f;
-        if (p >= 0) {
-            const float gt = gate[n];
-            const f32x4 v = reinterpret_cast<const f32x4 *>(y)[(size_t)p * d4 + c];
-            o[0] = fmaf(gt, v[0], f[0]); o[1] = fmaf(gt, v[1], f[1]);
-            o[2] = fmaf(gt, v[2], f[2]); o[3] = fmaf(gt, v[3], f[3]);
-        }
-        reinterpret_cast<f32x4 *>(out)[q] = o;
-    }
-}
-
+// ------------------------------------------------------------ backward --
 // One wave per routed row i (token n = idx[i]): d_gate[n] = dout[n] . y[i],
 // dy[i] = gate[n] dout[n]  (:916-919).
 __global__ __launch_bounds__(256) void k_moe_dgate(const float *__restrict__ dout, const float *__restrict__ y,
@@ -281,49 +279,58 @@ __global__ __launch_bounds__(256) void k_moe_dgate(const float *__restrict__ dou
     if (lane == 0) dgate[n] = s;
 }
 
-// Router backward per token (:933-943): dp_e = 0.01 E (cnt_e / N) / N, plus
-// d_gate on the chosen expert; d_rt = p (dp - p.dp).
-__global__ void k_moe_router_bwd(const float *__restrict__ rprobs, const int *__restrict__ pos,
-                                 const int *__restrict__ assign, const float *__restrict__ dgate,
-                                 const int *__restrict__ eoff, int N, int E, float *__restrict__ drt)
+// Router backward and d_fnorm (:928-944), MOE_TOK tokens per workgroup.
+// First, per token (:933-943): dp_e = 0.01 E (cnt_e / N) / N, plus d_gate on
+// the chosen expert; d_rt = p (dp - p.dp) -- kept in LDS and written out for
+// the dWr GEMM.  Then d_fnorm[n][d] = dX[pos[n]][d] + sum_e d_rt[n][e]
+// wr[d][e]: the expert scatter (:928-930) after the memset (:900), then the
+// router mm_bt (:944).
+__global__ __launch_bounds__(256) void k_moe_router_bwd(const float *__restrict__ rprobs, const int *__restrict__ pos,
+                                                        const int *__restrict__ assign, const float *__restrict__ dgate,
+                                                        const int *__restrict__ eoff, const float *__restrict__ dX,
+                                                        const float *__restrict__ wr, int N, int D, int E,
+                                                        float *__restrict__ drt, float *__restrict__ dfn)
 {
-    const int n = blockIdx.x * blockDim.x + threadIdx.x;
-    if (n >= N) return;
-    const float invN = 1.0f / (float)N;
-    const float auxw = 0.01f * (float)E;
-    const int a = pos[n] >= 0 ? assign[n] : -1;
-    const float dg = a >= 0 ? dgate[n] : 0.f;
-    const float *pr = rprobs + (size_t)n * E;
-    float dot = 0.f;
-    for (int e = 0; e < E; e++) {
-        float dp = auxw * ((float)(eoff[e + 1] - eoff[e]) * invN) * invN;
-        if (e == a) dp += dg;
-        dot = fmaf(pr[e], dp, dot);
+    __shared__ float sd[MOE_TOK][TLG_MOE_MAXE];
+    __shared__ int sp[MOE_TOK];
+    const int n0 = blockIdx.x * MOE_TOK, tid = threadIdx.x;
+    if (tid < MOE_TOK) sp[tid] = n0 + tid < N ? pos[n0 + tid] : -1;
+    if (tid < MOE_TOK && n0 + tid < N) {
+        const int n = n0 + tid;
+        const float invN = 1.0f / (float)N;
+        const float auxw = 0.01f * (float)E;
+        const int a = pos[n] >= 0 ? assign[n] : -1;
+        const float dg = a >= 0 ? dgate[n] : 0.f;
+        const float *pr = rprobs + (size_t)n * E;
+        float dot = 0.f;
+        for (int e = 0; e < E; e++) {
+            float dp = auxw * ((float)(eoff[e + 1] - eoff[e]) * invN) * invN;
+            if (e == a) dp += dg;
+            dot = fmaf(pr[e], dp, dot);
+        }
+        float *dr = drt + (size_t)n * E;
+        for (int e = 0; e < E; e++) {
+            float dp = auxw * ((float)(eoff[e + 1] - eoff[e]) * invN) * invN;
+            if (e == a) dp += dg;
+            const float v = pr[e] * (dp - dot);
+            sd[tid][e] = v;
+            dr[e] = v;
+        }
     }
-    float *dr = drt + (size_t)n * E;
-    for (int e = 0; e < E; e++) {
-        float dp = auxw * ((float)(eoff[e + 1] - eoff[e]) * invN) * invN;
-        if (e == a) dp += dg;
-        dr[e] = pr[e] * (dp - dot);
-    }
-}
-
-// d_fnorm[n][d] = dX[pos[n]][d] + sum_e d_rt[n][e] wr[d][e]: the expert
-// scatter (:928-930) after the memset (:900), then the router mm_bt (:944).
-__global__ void k_moe_dfnorm(const float *__restrict__ dX, const int *__restrict__ pos,
-                             const float *__restrict__ drt, const float *__restrict__ wr, int N, int D, int E,
-                             float *__restrict__ dfn)
-{
-    const size_t total = (size_t)N * D;
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total; q += stride) {
-        const size_t n = q / D, d = q % D;
-        const int p = pos[n];
-        const float x = p >= 0 ? dX[(size_t)p * D + d] : 0.f;
-        const float *r = drt + n * E, *w = wr + d * E;
-        float s = 0.f;
-        for (int e = 0; e < E; e++) s = fmaf(r[e], w[e], s);
-        dfn[q] = x + s;
+    __syncthreads();
+    // one column d per thread, the block's token rows loaded together
+    for (int d = tid; d < D; d += 256) {
+        float x[MOE_TOK];
+#pragma unroll
+        for (int t = 0; t < MOE_TOK; t++) x[t] = sp[t] >= 0 ? dX[(size_t)sp[t] * D + d] : 0.f;
+        const float *w = wr + (size_t)d * E;
+#pragma unroll
+        for (int t = 0; t < MOE_TOK; t++) {
+            if (n0 + t >= N) break;
+            float s = 0.f;
+            for (int e = 0; e < E; e++) s = fmaf(sd[t][e], w[e], s);
+            dfn[(size_t)(n0 + t) * D + d] = x[t] + s;
+        }
     }
 }
 
@@ -334,7 +341,7 @@ __global__ void k_moe_dfnorm(const float *__restrict__ dX, const int *__restrict
 // different streams must not overlap (they share the arena).
 struct MoeScratch {
     int *idx, *pos, *eoff;
-    float *dgate, *drt, *Xg, *y, *dy, *g, *u, *a, *da;
+    float *dgate, *drt, *y, *dy, *g, *u, *a;
 };
 static void *g_moe_mem = nullptr;
 static size_t g_moe_bytes = 0;
@@ -349,10 +356,10 @@ void tlg_moe_release(void)
 static int moe_scratch(int N, int D, int F, int E, MoeScratch *s)
 {
     const size_t n = (size_t)N;
-    const size_t sizes[12] = {n * 4, n * 4, (size_t)(TLG_MOE_MAXE + 1) * 4, n * 4, n * E * 4,
-                              n * D * 4, n * D * 4, n * D * 4, n * F * 4, n * F * 4, n * F * 4, n * F * 4};
-    size_t total = 0, offs[12];
-    for (int k = 0; k < 12; k++) {
+    const size_t sizes[10] = {n * 4, n * 4, (size_t)(TLG_MOE_MAXE + 1) * 4, n * 4, n * E * 4,
+                              n * D * 4, n * D * 4, n * F * 4, n * F * 4, n * F * 4};
+    size_t total = 0, offs[10];
+    for (int k = 0; k < 10; k++) {
         offs[k] = total;
         total += (sizes[k] + 255) & ~(size_t)255;
     }
@@ -372,24 +379,16 @@ static int moe_scratch(int N, int D, int F, int E, MoeScratch *s)
     s->eoff = (int *)(b + offs[2]);
     s->dgate = (float *)(b + offs[3]);
     s->drt = (float *)(b + offs[4]);
-    s->Xg = (float *)(b + offs[5]);
-    s->y = (float *)(b + offs[6]);
-    s->dy = (float *)(b + offs[7]);
-    s->g = (float *)(b + offs[8]);
-    s->u = (float *)(b + offs[9]);
-    s->a = (float *)(b + offs[10]);
-    s->da = (float *)(b + offs[11]);
+    s->y = (float *)(b + offs[5]);
+    s->dy = (float *)(b + offs[6]);
+    s->g = (float *)(b + offs[7]);
+    s->u = (float *)(b + offs[8]);
+    s->a = (float *)(b + offs[9]);
     return TLG_OK;
 }
 
 // ------------------------------------------------------------ launches --
 static inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
-static inline unsigned grid_for(size_t work, size_t per_block, unsigned cap)
-{
-    size_t b = (work + per_block - 1) / per_block;
-    if (b < 1) b = 1;
-    return (unsigned)(b > cap ? cap : b);
-}
 
 static int check_shape(int N, int D, int F, int E)
 {
@@ -408,35 +407,27 @@ static bool moe_ptrs_ok(std::initializer_list<const void *> ps)
 }
 
 // Per-expert row index of the routed tokens (idx, pos, eoff).
-static int moe_index(const int *assign, int N, int E, const MoeScratch &s, hipStream_t st)
+static int moe_index(const int *assign, int N, int E, const MoeScratch &s, const float *fin, float *out, int D,
+                     hipStream_t st)
 {
-    hipLaunchKernelGGL(k_moe_index, dim3(1), dim3(1024), 0, st, assign, N, E, s.idx, s.pos, s.eoff);
+    hipLaunchKernelGGL(k_moe_index, dim3(1), dim3(1024), 0, st, assign, N, E, s.idx, s.pos, s.eoff, fin, out, D);
     TLG_HIP(hipGetLastError());
     return TLG_OK;
 }
 
-// g, u = Xg W1_e, Xg W3_e;  a = silu(g) u;  y = a W2_e  (:880-884 / :911-914)
-static int moe_experts_fwd(const float *fnorm, int N, int D, int F, int E, const float *w1, const float *w3,
-                           const float *w2, const MoeScratch &s, hipStream_t st)
+// The W1 | W3 GEMM pair as one expert launch of paired-column tiles, X rows
+// gathered from fnorm by the sorted-row index (:876-878), the SwiGLU in the
+// epilogue (:880-883): a = silu(Xg W1_e) (Xg W3_e).  g and u are kept too
+// when the caller passes them (the backward needs them, :923-925).
+static int moe_w13(const float *fnorm, int N, int D, int F, int E, const float *w1, const float *w3,
+                   const MoeScratch &s, float *g, float *u, hipStream_t st)
 {
-    hipLaunchKernelGGL(k_gather_rows, dim3(grid_for((size_t)N * D / 4, 256, 4096)), dim3(256), 0, st, fnorm,
-                       s.idx, s.eoff, E, D, s.Xg);
-    TLG_HIP(hipGetLastError());
-    TlgExpertCall c[2];
-    memset(c, 0, sizeof c);
-    c[0].op = 0; c[0].C = s.g; c[0].K = D; c[0].N = F; c[0].nseg = 1;
-    c[0].A[0] = s.Xg; c[0].B[0] = w1; c[0].es = (long long)D * F;
-    c[1] = c[0];
-    c[1].C = s.u; c[1].B[0] = w3;
-    int rc = tlg_expert_launch(c, 2, s.eoff, E, N, st);
-    if (rc) return rc;
-    hipLaunchKernelGGL(k_swiglu, dim3(grid_for((size_t)N * F, 256, 8192)), dim3(256), 0, st, s.g, s.u, s.a,
-                       s.eoff, E, F);
-    TLG_HIP(hipGetLastError());
-    memset(c, 0, sizeof c);
-    c[0].op = 0; c[0].C = s.y; c[0].K = F; c[0].N = D; c[0].nseg = 1;
-    c[0].A[0] = s.a; c[0].B[0] = w2; c[0].es = (long long)F * D;
-    return tlg_expert_launch(c, 1, s.eoff, E, N, st);
+    TlgExpertCall c;
+    memset(&c, 0, sizeof c);
+    c.op = 0; c.C = s.a; c.K = D; c.N = F; c.nseg = 1;
+    c.A[0] = fnorm; c.B[0] = w1; c.es = (long long)D * F;
+    c.amap = s.idx; c.B2 = w3; c.epi = TLG_EPI_SWIGLU; c.X1 = g; c.X2 = u;
+    return tlg_expert_launch(&c, 1, s.eoff, E, N, st);
 }
 
 int tlg_moe_fwd_launch(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,
@@ -456,12 +447,16 @@ int tlg_moe_fwd_launch(const float *fnorm, const float *fin, float *out, int N, 
     hipLaunchKernelGGL(k_moe_route, dim3((N + MOE_TOK - 1) / MOE_TOK), dim3(256), route_lds(dch, E), st, fnorm, wr,
                        N, D, E, dch, rprobs, assign, gate);
     TLG_HIP(hipGetLastError());
-    if ((rc = moe_index(assign, N, E, s, st))) return rc;
-    if ((rc = moe_experts_fwd(fnorm, N, D, F, E, w1, w3, w2, s, st))) return rc;
-    hipLaunchKernelGGL(k_moe_combine, dim3(grid_for((size_t)N * D / 4, 256, 4096)), dim3(256), 0, st, fin, s.y,
-                       s.pos, gate, N, D, out);
-    TLG_HIP(hipGetLastError());
-    return TLG_OK;
+    // the index also sets out = fin for tokens without an expert
+    if ((rc = moe_index(assign, N, E, s, fin, out, D, st))) return rc;
+    if ((rc = moe_w13(fnorm, N, D, F, E, w1, w3, s, nullptr, nullptr, st))) return rc;
+    // y = a W2_e with the combine in the epilogue: out[n] = fin[n] + gate[n] y
+    TlgExpertCall c;
+    memset(&c, 0, sizeof c);
+    c.op = 0; c.C = out; c.K = F; c.N = D; c.nseg = 1;
+    c.A[0] = s.a; c.B[0] = w2; c.es = (long long)F * D;
+    c.epi = TLG_EPI_COMBINE; c.omap = s.idx; c.fin = fin; c.gate = gate;
+    return tlg_expert_launch(&c, 1, s.eoff, E, N, st);
 }
 
 int tlg_moe_bwd_launch(const float *fnorm, const float *dout, float *d_fnorm, const int *assign,
@@ -479,27 +474,34 @@ int tlg_moe_bwd_launch(const float *fnorm, const float *dout, float *d_fnorm, co
     if ((rc = tlg_group_flush_launch(st))) return rc;
     MoeScratch s;
     if ((rc = moe_scratch(N, D, F, E, &s))) return rc;
-    if ((rc = moe_index(assign, N, E, s, st))) return rc;
-    // recompute the forward of every expert (:910-914)
-    if ((rc = moe_experts_fwd(fnorm, N, D, F, E, w1, w3, w2, s, st))) return rc;
+    if ((rc = moe_index(assign, N, E, s, nullptr, nullptr, D, st))) return rc;
+    // recompute the forward of every expert (:910-914): g, u, a, then y
+    if ((rc = moe_w13(fnorm, N, D, F, E, w1, w3, s, s.g, s.u, st))) return rc;
+    {
+        TlgExpertCall c;
+        memset(&c, 0, sizeof c);
+        c.op = 0; c.C = s.y; c.K = F; c.N = D; c.nseg = 1;
+        c.A[0] = s.a; c.B[0] = w2; c.es = (long long)F * D;
+        if ((rc = tlg_expert_launch(&c, 1, s.eoff, E, N, st))) return rc;
+    }
     hipLaunchKernelGGL(k_moe_dgate, dim3((N + 3) / 4), dim3(256), 0, st, dout, s.y, s.idx, s.eoff, E, D, gate,
                        s.dgate, s.dy);
     TLG_HIP(hipGetLastError());
-    // dW2_e += a^T dy ;  da = dy W2_e^T   (:921-922)
+    // dW2_e += a^T dy ;  da = dy W2_e^T with the SwiGLU backward in its
+    // epilogue: g <- dg, u <- du  (:921-925)
     TlgExpertCall c[3];
     memset(c, 0, sizeof c);
     c[0].op = 2; c[0].beta = 1; c[0].C = gw2; c[0].K = F; c[0].N = D; c[0].nseg = 1;
     c[0].A[0] = s.a; c[0].B[0] = s.dy; c[0].es = (long long)F * D;
-    c[1].op = 1; c[1].beta = 0; c[1].C = s.da; c[1].K = F; c[1].N = D; c[1].nseg = 1;
+    c[1].op = 1; c[1].beta = 0; c[1].C = nullptr; c[1].K = F; c[1].N = D; c[1].nseg = 1;
     c[1].A[0] = s.dy; c[1].B[0] = w2; c[1].es = (long long)F * D;
+    c[1].epi = TLG_EPI_SWIGLU_BWD; c[1].X1 = s.g; c[1].X2 = s.u;
     if ((rc = tlg_expert_launch(c, 2, s.eoff, E, N, st))) return rc;
-    hipLaunchKernelGGL(k_swiglu_bwd, dim3(grid_for((size_t)N * F, 256, 8192)), dim3(256), 0, st, s.g, s.u, s.da,
-                       s.eoff, E, F);
-    TLG_HIP(hipGetLastError());
-    // dW1_e += Xg^T dg ; dW3_e += Xg^T du ; dX = dg W1_e^T + du W3_e^T (:926-927)
+    // dW1_e += Xg^T dg ; dW3_e += Xg^T du (Xg rows gathered from fnorm) ;
+    // dX = dg W1_e^T + du W3_e^T  (:926-927)
     memset(c, 0, sizeof c);
     c[0].op = 2; c[0].beta = 1; c[0].C = gw1; c[0].K = D; c[0].N = F; c[0].nseg = 1;
-    c[0].A[0] = s.Xg; c[0].B[0] = s.g; c[0].es = (long long)D * F;
+    c[0].A[0] = fnorm; c[0].amap = s.idx; c[0].B[0] = s.g; c[0].es = (long long)D * F;
     c[1] = c[0];
     c[1].C = gw3; c[1].B[0] = s.u;
     c[2].op = 1; c[2].beta = 0; c[2].C = s.y; c[2].K = D; c[2].N = F; c[2].nseg = 2;
@@ -507,11 +509,8 @@ int tlg_moe_bwd_launch(const float *fnorm, const float *dout, float *d_fnorm, co
     c[2].es = (long long)D * F;
     if ((rc = tlg_expert_launch(c, 3, s.eoff, E, N, st))) return rc;
     // router: softmax backward, d_fnorm, dWr  (:932-945)
-    hipLaunchKernelGGL(k_moe_router_bwd, dim3((N + 255) / 256), dim3(256), 0, st, rprobs, s.pos, assign, s.dgate,
-                       s.eoff, N, E, s.drt);
-    TLG_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_moe_dfnorm, dim3(grid_for((size_t)N * D, 256, 8192)), dim3(256), 0, st, s.y, s.pos,
-                       s.drt, wr, N, D, E, d_fnorm);
+    hipLaunchKernelGGL(k_moe_router_bwd, dim3((N + MOE_TOK - 1) / MOE_TOK), dim3(256), 0, st, rprobs, s.pos,
+                       assign, s.dgate, s.eoff, s.y, wr, N, D, E, s.drt, d_fnorm);
     TLG_HIP(hipGetLastError());
     return tlg_gemm_launch(TLG_TN, fnorm, s.drt, gwr, D, E, N, D, E, E, 1, st);
 }
