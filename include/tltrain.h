@@ -63,6 +63,19 @@ int tlg_dev_attn_bwd(const float *q, const float *k, const float *v, const float
                      const float *datt, float *dq, float *dk, float *dv, int B, int T, int H, int KV, int hd,
                      int win, void *stream);
 
+/* rope_apply fused into attention (no reference counterpart as one call: it
+ * replaces the sequence rope_apply(q), rope_apply(k), attn_fwd of
+ * tinylm.c:988-990 and attn_bwd, rope_apply^T(dq), rope_apply^T(dk) of
+ * :1130-1133).  q and k are the projections before rope_apply; cos_t / sin_t
+ * are rope_init's tables for positions 0..T-1 (row r of a sequence is at
+ * position r, :975), 16-byte aligned; dq and dk are the gradients of the
+ * pre-rope q and k.  H / KV must be a multiple of 4 (the GQA-group kernels). */
+int tlg_dev_attn_fwd_rope(const float *q, const float *k, const float *v, float *out, float *lse, int B, int T,
+                          int H, int KV, int hd, int win, const float *cos_t, const float *sin_t, void *stream);
+int tlg_dev_attn_bwd_rope(const float *q, const float *k, const float *v, const float *out, const float *lse,
+                          const float *datt, float *dq, float *dk, float *dv, int B, int T, int H, int KV, int hd,
+                          int win, const float *cos_t, const float *sin_t, void *stream);
+
 /* residual adds, tinylm.c:994-995, :1009-1010, :1062: y[i] += x[i]. */
 int tlg_dev_add(float *y, const float *x, size_t n, void *stream);
 

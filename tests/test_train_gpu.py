@@ -122,6 +122,7 @@ ATTN = [  # B, T, H, KV, win
     (2, 256, 12, 3, 0),     # m8 heads
     (3, 70, 2, 1, 0),       # ragged T
     (2, 100, 4, 2, 40),     # sliding window
+    (2, 100, 8, 2, 40),     # sliding window, GQA groups of 4 (the group kernels)
     (1, 33, 2, 2, 0),       # MHA
     (4, 1, 4, 1, 0),        # one token
 ]
@@ -163,6 +164,59 @@ def test_attention_fixture(lib, path):
     out, dq, dk, dv = gpu_attn(lib, d["q"], d["k"], d["v"], d["datt"], B, T, H, KV, win)
     for got, key in ((out, "out"), (dq, "dq"), (dk, "dk"), (dv, "dv")):
         assert normwise_rel(got, d[key]) <= TOL, key
+
+
+ATTN_ROPE = [  # B, T, H, KV, win: GQA groups of 4 or 8 heads
+    (2, 256, 8, 2, 0),      # m3 heads
+    (2, 256, 12, 3, 0),     # m8 heads
+    (3, 70, 4, 1, 0),       # ragged T
+    (2, 100, 8, 1, 40),     # sliding window, 8 heads per KV head
+    (4, 1, 4, 1, 0),        # one token
+]
+
+
+@pytest.mark.parametrize("B,T,H,KV,win", ATTN_ROPE)
+def test_attention_rope_fused(lib, st, B, T, H, KV, win):
+    """tlg_dev_attn_{fwd,bwd}_rope on pre-rope q, k against the reference's
+    sequence: rope_apply(q), rope_apply(k), attn_fwd; attn_bwd, then the
+    transposed rope_apply on dq and dk (tinylm.c:988-990, :1130-1133)."""
+    print("attention rope", B, T, H, KV, win, flush=True)
+    t = _t()
+    r = np.random.default_rng(T * 11 + H + win)
+    q = r.standard_normal((B * T, H * 32)).astype(np.float32)
+    k = r.standard_normal((B * T, KV * 32)).astype(np.float32)
+    v = r.standard_normal((B * T, KV * 32)).astype(np.float32)
+    datt = (0.01 * r.standard_normal((B * T, H * 32))).astype(np.float32)
+    cs, sn = st.rope_table(T, 32)
+    qr, kr = q.copy(), k.copy()
+    st.rope(qr, T, H, 32, 0)
+    st.rope(kr, T, KV, 32, 0)
+    want_out = st.attn_fwd(qr, kr, v, B, T, H, KV, 32, win)
+    wq, wk, wv = st.attn_bwd(qr, kr, v, datt, B, T, H, KV, 32, win)
+    st.rope(wq, T, H, 32, 1)
+    st.rope(wk, T, KV, 32, 1)
+    Q, K, Vv, C, S = dev(q), dev(k), dev(v), dev(cs), dev(sn)
+    out, lse = nan_like(q.shape), nan_like((B * T, H))
+    lib.check(lib.tlg_dev_attn_fwd_rope(Q.data_ptr(), K.data_ptr(), Vv.data_ptr(), out.data_ptr(), lse.data_ptr(), B,
+                                        T, H, KV, 32, win, C.data_ptr(), S.data_ptr(), stream()), "attn_fwd_rope")
+    dq, dk, dv, DA = nan_like(q.shape), nan_like(k.shape), nan_like(v.shape), dev(datt)
+    lib.check(lib.tlg_dev_attn_bwd_rope(Q.data_ptr(), K.data_ptr(), Vv.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                        DA.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, T, H, KV, 32,
+                                        win, C.data_ptr(), S.data_ptr(), stream()), "attn_bwd_rope")
+    t.cuda.synchronize()
+    # q and k are inputs: the fused kernels must leave them pre-rope
+    assert np.array_equal(host(Q), q) and np.array_equal(host(K), k)
+    assert normwise_rel(host(out), want_out) <= TOL
+    for got, want, name in ((host(dq), wq, "dq"), (host(dk), wk, "dk"), (host(dv), wv, "dv")):
+        assert normwise_rel(got, want) <= TOL, name
+
+
+def test_attention_rope_needs_groups_of_4(lib):
+    Z = dev(np.zeros(64 * 64, np.float32))
+    p = Z.data_ptr()
+    assert lib.tlg_dev_attn_fwd_rope(p, p, p, p, p, 1, 2, 2, 1, 32, 0, p, p, stream()) != 0
+    assert lib.tlg_dev_attn_fwd_rope(p, p, p, p, p, 1, 2, 4, 1, 32, 0, None, None, stream()) != 0
+    lib.tlg_last_error()
 
 
 def test_attention_rejects_bad_shapes(lib):

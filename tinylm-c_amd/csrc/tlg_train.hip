@@ -363,22 +363,21 @@ __global__ void k_rope4(float *__restrict__ buf, const int *__restrict__ pos, in
 // Row (within a 32 x 32 tile) of register r of lane l in the MFMA result.
 __device__ __forceinline__ int at_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
-// 16 contiguous floats from p (16-byte aligned), or zeros.
+// 16 contiguous floats from p (16-byte aligned), or zeros when !ok.  p must
+// be a valid address either way (callers clamp the row): every load in the
+// attention kernels is issued unconditionally and masked afterwards, so the
+// compiler counts outstanding loads exactly and a prefetch is not waited for
+// at the first branch join after it.
 __device__ __forceinline__ void ld16(const float *p, bool ok, float (&o)[16])
 {
-    if (ok) {
-        const f32x4 *q = reinterpret_cast<const f32x4 *>(p);
+    const f32x4 *q = reinterpret_cast<const f32x4 *>(p);
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const f32x4 t = q[k];
-            o[4 * k] = t.x;
-            o[4 * k + 1] = t.y;
-            o[4 * k + 2] = t.z;
-            o[4 * k + 3] = t.w;
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < 16; k++) o[k] = 0.f;
+    for (int k = 0; k < 4; k++) {
+        const f32x4 t = q[k];
+        o[4 * k] = ok ? t.x : 0.f;
+        o[4 * k + 1] = ok ? t.y : 0.f;
+        o[4 * k + 2] = ok ? t.z : 0.f;
+        o[4 * k + 3] = ok ? t.w : 0.f;
     }
 }
 
@@ -387,6 +386,14 @@ __device__ __forceinline__ void ld16(const float *p, bool ok, float (&o)[16])
 __device__ __forceinline__ bool at_visible(int s, int q, int T, int win)
 {
     return s <= q && q < T && (win <= 0 || s > q - win);
+}
+
+// Key block kb is visible in full from every valid query of block qb: below
+// the diagonal block and, with a window, inside it for the block's last
+// query (then also for every earlier one).  Such blocks need no mask.
+__device__ __forceinline__ bool at_full(int kb, int qb, int win)
+{
+    return kb < qb && (win <= 0 || kb * 32 > qb * 32 + 31 - win);
 }
 
 // First key block any query of block qb can see.
@@ -408,7 +415,8 @@ __device__ __forceinline__ void at_load_kv(const float *kb_, const float *vb_, i
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const int s = s0 + at_row(r, lane);
-        vv[r] = s < T ? vb_[(size_t)s * KD + (lane & 31)] : 0.f;
+        const float x = vb_[(size_t)min(s, T - 1) * KD + (lane & 31)];
+        vv[r] = s < T ? x : 0.f;
     }
 }
 
@@ -448,14 +456,15 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const float *__restrict__ q, c
     const float c2 = scale * 1.44269504088896341f;
     float m = -INFINITY, l = 0.f;
     float kn[16], vn[16];                       // next block's K / V (prefetched)
+    // block indices clamp to qb: loads past the wave's last block re-read it
     int kb = at_kb0(qb, win) + wave;
-    if (kb <= qb) at_load_kv(kb_, vb_, kb, T, KD, lane, kn, vn);
+    at_load_kv(kb_, vb_, min(kb, qb), T, KD, lane, kn, vn);
     for (; kb <= qb; kb += AT_W) {
         const int s0 = kb * 32;
         float kv[16], vv[16];
 #pragma unroll
         for (int j = 0; j < 16; j++) { kv[j] = kn[j]; vv[j] = vn[j]; }
-        if (kb + AT_W <= qb) at_load_kv(kb_, vb_, kb + AT_W, T, KD, lane, kn, vn);
+        at_load_kv(kb_, vb_, min(kb + AT_W, qb), T, KD, lane, kn, vn);
         f32x16 st;
 #pragma unroll
         for (int r = 0; r < 16; r++) st[r] = 0.f;
@@ -528,7 +537,8 @@ __device__ __forceinline__ void at_load_kvk(const float *kb_, const float *vb_, 
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const int s = s0 + at_row(r, lane);
-        kk[r] = s < T ? kb_[(size_t)s * KD + (lane & 31)] : 0.f;
+        const float x = kb_[(size_t)min(s, T - 1) * KD + (lane & 31)];
+        kk[r] = s < T ? x : 0.f;
     }
 }
 
@@ -564,7 +574,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const float *__restrict__ q
     dd += __shfl_xor(dd, 32);
     const size_t rh = (size_t)(b * T + (qok ? qi : 0)) * H + h;
     if (qok && hh == 0 && wave == 0) Dq[rh] = dd;
-    const float ls = qok ? lse[rh] : 0.f;
+    const float lsv = lse[rh];
+    const float ls = qok ? lsv : 0.f;
     const float *kb_ = k + (size_t)b * T * KD + kvh * AT_HD;
     const float *vb_ = v + (size_t)b * T * KD + kvh * AT_HD;
     const float c2 = scale * 1.44269504088896341f;
@@ -573,13 +584,13 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const float *__restrict__ q
     for (int r = 0; r < 16; r++) acc[r] = 0.f;
     float kn[16], vn[16], kkn[16];              // next block (prefetched)
     int kb = at_kb0(qb, win) + wave;
-    if (kb <= qb) at_load_kvk(kb_, vb_, kb, T, KD, lane, kn, vn, kkn);
+    at_load_kvk(kb_, vb_, min(kb, qb), T, KD, lane, kn, vn, kkn);
     for (; kb <= qb; kb += AT_W) {
         const int s0 = kb * 32;
         float kv[16], vv[16], kk[16];
 #pragma unroll
         for (int j = 0; j < 16; j++) { kv[j] = kn[j]; vv[j] = vn[j]; kk[j] = kkn[j]; }
-        if (kb + AT_W <= qb) at_load_kvk(kb_, vb_, kb + AT_W, T, KD, lane, kn, vn, kkn);
+        at_load_kvk(kb_, vb_, min(kb + AT_W, qb), T, KD, lane, kn, vn, kkn);
         f32x16 st, dp;
 #pragma unroll
         for (int r = 0; r < 16; r++) { st[r] = 0.f; dp[r] = 0.f; }
@@ -589,14 +600,22 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const float *__restrict__ q
             dp = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[j], dov[j], dp, 0, 0, 0);
         }
         float ds[16];
+        if (at_full(kb, qb, win)) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int s = s0 + at_row(r, lane);
-            if (at_visible(s, qi, T, win)) {
+            for (int r = 0; r < 16; r++) {
                 const float p = __builtin_amdgcn_exp2f(st[r] * c2 - ls);
                 ds[r] = p * (dp[r] - dd) * scale;
-            } else {
-                ds[r] = 0.f;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int s = s0 + at_row(r, lane);
+                if (at_visible(s, qi, T, win)) {
+                    const float p = __builtin_amdgcn_exp2f(st[r] * c2 - ls);
+                    ds[r] = p * (dp[r] - dd) * scale;
+                } else {
+                    ds[r] = 0.f;
+                }
             }
         }
         // dQ^T[d][q] += sum_s K[s][d] dS^T[s][q]
@@ -620,16 +639,52 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const float *__restrict__ q
             f32x4{acc[4 * g4], acc[4 * g4 + 1], acc[4 * g4 + 2], acc[4 * g4 + 3]};
 }
 
+// rope_apply on an A fragment (lane (row, half) holds dims 16 half + i of the
+// row at position t): the partner dims are in lane ^ 32.
+__device__ __forceinline__ void at_rot_a(float (&x)[16], int t, int lane, const float *__restrict__ cs,
+                                         const float *__restrict__ sn)
+{
+    const bool hi = lane >= 32;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const f32x4 c = *reinterpret_cast<const f32x4 *>(cs + (size_t)t * 16 + 4 * k);
+        const f32x4 s = *reinterpret_cast<const f32x4 *>(sn + (size_t)t * 16 + 4 * k);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float me = x[4 * k + i], pa = __shfl_xor(me, 32);
+            x[4 * k + i] = hi ? me * c[i] + pa * s[i] : me * c[i] - pa * s[i];
+        }
+    }
+}
+
+// rope_apply (back = 0) or its transpose (back = 1) on one element per lane:
+// dim d = lane % 32 of a row at position t, the partner dim in lane ^ 16.
+__device__ __forceinline__ float at_rot_1(float x, int t, int lane, const float *__restrict__ cs,
+                                          const float *__restrict__ sn, bool back)
+{
+    const int i = lane & 15;
+    const bool hi = (lane & 16) != 0;
+    const float c = cs[(size_t)t * 16 + i], s = sn[(size_t)t * 16 + i], pa = __shfl_xor(x, 16);
+    // forward: lo' = lo c - hi s, hi' = hi c + lo s; back: lo = lo' c + hi' s, hi = hi' c - lo' s
+    const float sg = (hi != back) ? 1.f : -1.f;
+    return x * c + sg * pa * s;
+}
+
 // dK, dV: one workgroup per (b, kv head, 32-key block), first key blocks
 // (most queries) first.  Its eight waves share the (head, query block) pairs
 // that see the block; each accumulates dV = P^T dO and dK = dS^T Q for its
 // pairs, and the partials are summed in wave order through LDS.
+// With ROPE, q is already rotated (the dQ kernel's copy) and k is taken
+// before rope_apply and rotated on load; dK is rotated back before it is
+// stored.
 #define AT_KW 8
+template <bool ROPE>
 __global__ __launch_bounds__(512) void k_attn_bwd_dkv(const float *__restrict__ q, const float *__restrict__ k,
                                                       const float *__restrict__ v, const float *__restrict__ dout,
                                                       const float *__restrict__ lse, const float *__restrict__ Dq,
                                                       float *__restrict__ dk, float *__restrict__ dv, int B, int T,
-                                                      int H, int KV, int win, float scale)
+                                                      int H, int KV, int win, float scale,
+                                                      const float *__restrict__ cs, const float *__restrict__ sn)
 {
     __shared__ float red[AT_KW - 1][2][16][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -646,6 +701,7 @@ __global__ __launch_bounds__(512) void k_attn_bwd_dkv(const float *__restrict__ 
     float kv[16], vv[16];
     ld16(k + koff, sok, kv);
     ld16(v + koff, sok, vv);
+    if (ROPE) at_rot_a(kv, sok ? sl : T - 1, lane, cs, sn);
     int qb_last = nkb - 1;
     if (win > 0) qb_last = min(qb_last, (s0 + 31 + win - 1) >> 5);
     const int npairs = G * (qb_last - kb + 1);
@@ -668,10 +724,11 @@ __global__ __launch_bounds__(512) void k_attn_bwd_dkv(const float *__restrict__ 
             const bool ok = qq < T;
             const size_t off = (size_t)(b * T + (ok ? qq : 0)) * D + h * AT_HD + lq;
             const size_t rh = (size_t)(b * T + (ok ? qq : 0)) * H + h;
-            dob[r] = ok ? dout[off] : 0.f;
-            qbv[r] = ok ? q[off] : 0.f;
-            lr[r] = ok ? lse[rh] : 0.f;
-            dr[r] = ok ? Dq[rh] : 0.f;
+            const float x0 = dout[off], x1 = q[off], x2 = lse[rh], x3 = Dq[rh];
+            dob[r] = ok ? x0 : 0.f;
+            qbv[r] = ok ? x1 : 0.f;
+            lr[r] = ok ? x2 : 0.f;
+            dr[r] = ok ? x3 : 0.f;
         }
         f32x16 st, dp;
 #pragma unroll
@@ -683,15 +740,25 @@ __global__ __launch_bounds__(512) void k_attn_bwd_dkv(const float *__restrict__ 
         }
         // st[r] = S[q0 + at_row(r)][sl], dp likewise
         float pp[16], ds[16];
+        // a fully visible pair still masks queries past T (their lse / Dq
+        // rows are clamped copies, not zeros)
+        if (at_full(kb, q0 >> 5, win) && q0 + 32 <= T) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int qq = q0 + at_row(r, lane);
-            if (at_visible(sl, qq, T, win)) {
+            for (int r = 0; r < 16; r++) {
                 pp[r] = __builtin_amdgcn_exp2f(st[r] * c2 - lr[r]);
                 ds[r] = pp[r] * (dp[r] - dr[r]) * scale;
-            } else {
-                pp[r] = 0.f;
-                ds[r] = 0.f;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int qq = q0 + at_row(r, lane);
+                if (at_visible(sl, qq, T, win)) {
+                    pp[r] = __builtin_amdgcn_exp2f(st[r] * c2 - lr[r]);
+                    ds[r] = pp[r] * (dp[r] - dr[r]) * scale;
+                } else {
+                    pp[r] = 0.f;
+                    ds[r] = 0.f;
+                }
             }
         }
         // dV[s][d] += sum_q P[q][s] dO[q][d];  dK[s][d] += sum_q dS[q][s] Q[q][d]
@@ -718,12 +785,382 @@ __global__ __launch_bounds__(512) void k_attn_bwd_dkv(const float *__restrict__ 
             c += red[w][1][r][lane];
         }
         const int s = s0 + at_row(r, lane);
+        if (ROPE) a = at_rot_1(a, min(s, T - 1), lane, cs, sn, true);
         if (s < T) {
             const size_t off = (size_t)(b * T + s) * KD + kvh * AT_HD + lq;
             dk[off] = a;
             dv[off] = c;
         }
     }
+}
+
+// ------------------------------------------------ GQA-group attention --
+// Forward and dQ for H / KV a multiple of 4.  One workgroup of 4 A4_KS waves
+// per (b, KV head, group of 4 query heads, 32-query block), latest blocks
+// first: wave w takes head w % 4 of the group and every A4_KS-th key block
+// from w / 4.
+// The four heads read the same K / V, so the workgroup stages up to A4_CH
+// key blocks at a time in LDS and every wave streams its blocks from there
+// with no barrier between blocks (the waves sharing a SIMD drift out of
+// phase, so one's softmax overlaps the others' MFMAs); the key splits of
+// each head merge through LDS in fixed order.  With ROPE the kernels take q
+// and k before rope_apply (tinylm.c:621-651) and rotate them while staging
+// -- pair (x[i], x[i + 16]) of a head by the row's position -- so rotated
+// copies reach HBM only where asked for (the dQ kernel's qrot, which the
+// dK / dV kernel reads); dQ is rotated back before it is stored.
+#define A4_LD 36        // LDS row stride of a staged 32 x 32 block (16-byte rows)
+#define A4_CH 8         // key blocks staged at once (K + V: 72 KB)
+#define A4_KS 2         // key splits per head: 4 heads x 2 splits = 8 waves (4 measured slower)
+
+// One staging task: dims [4c, 4c + 4) and [16 + 4c, 16 + 4c + 4) of one
+// 32-dim head row, rotated by position t when ROPE and `rot`, zeroed when !ok.
+template <bool ROPE>
+struct A4Task {
+    f32x4 a, b, c, s;
+    __device__ __forceinline__ void load(const float *__restrict__ row, int c4, int t, bool rot,
+                                         const float *__restrict__ cs, const float *__restrict__ sn)
+    {
+        a = *reinterpret_cast<const f32x4 *>(row + 4 * c4);
+        b = *reinterpret_cast<const f32x4 *>(row + 16 + 4 * c4);
+        if (ROPE && rot) {
+            c = *reinterpret_cast<const f32x4 *>(cs + (size_t)t * 16 + 4 * c4);
+            s = *reinterpret_cast<const f32x4 *>(sn + (size_t)t * 16 + 4 * c4);
+        }
+    }
+    __device__ __forceinline__ void rotate(bool rot)
+    {
+        if (ROPE && rot) {
+            const f32x4 x = a * c - b * s, y = b * c + a * s;
+            a = x;
+            b = y;
+        }
+    }
+    __device__ __forceinline__ void store(float *__restrict__ L, int c4, bool ok) const
+    {
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        *reinterpret_cast<f32x4 *>(L + 4 * c4) = ok ? a : z;
+        *reinterpret_cast<f32x4 *>(L + 16 + 4 * c4) = ok ? b : z;
+    }
+};
+
+// Item -> (b, kvh, first head h0 of the group, qb), latest query blocks first.
+__device__ __forceinline__ void a4_item(int item, int B, int H, int KV, int nqb, int *b, int *kvh, int *h0, int *qb)
+{
+    const int G = H / KV, HG = G / 4, per = B * KV * HG;
+    *qb = nqb - 1 - item / per;
+    int r = item % per;
+    const int hg = r % HG;
+    r /= HG;
+    *kvh = r % KV;
+    *b = r / KV;
+    *h0 = *kvh * G + hg * 4;
+}
+
+// Stage key blocks c0 .. c0 + nb - 1 of (b, kvh): K (rotated with ROPE) into
+// Ks[blk][32][A4_LD], V into Vs.  Task = (K or V, block, row, c4), two per
+// thread per round with all their loads issued first.
+template <bool ROPE>
+__device__ __forceinline__ void a4_stage_kv(float *Ks, float *Vs, const float *k, const float *v, int b, int kvh,
+                                            int T, int KV, int c0, int nb, const float *cs, const float *sn)
+{
+    const int ntask = nb * 32 * 4 * 2;           // per block: 32 rows x 4 c4, K and V
+    const int nt = blockDim.x;
+    for (int t0 = threadIdx.x; t0 < ntask; t0 += 2 * nt) {
+        A4Task<ROPE> tk[2];
+        bool ok[2], isk[2];
+        int slot[2], c4v[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int t = min(t0 + nt * u, ntask - 1);
+            const int kv_ = t & 1, rest = t >> 1;             // K / V interleaved
+            const int c4 = rest & 3, x = (rest >> 2) & 31, blk = rest >> 7;
+            const int s = (c0 + blk) * 32 + x, sc = min(s, T - 1);
+            isk[u] = kv_ == 0;
+            ok[u] = s < T;
+            slot[u] = (blk * 32 + x) * A4_LD;
+            c4v[u] = c4;
+            tk[u].load((isk[u] ? k : v) + (size_t)(b * T + sc) * (KV * AT_HD) + kvh * AT_HD, c4, sc, isk[u], cs, sn);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            if (t0 + nt * u >= ntask) break;
+            tk[u].rotate(isk[u]);
+            tk[u].store((isk[u] ? Ks : Vs) + slot[u], c4v[u], ok[u]);
+        }
+    }
+}
+
+// Q of the group's 4 heads for query block qb into Qs[4][32][A4_LD]
+// (rotated with ROPE), one task per thread; qrot (optional) receives the
+// rotated rows in q's layout.
+template <bool ROPE>
+__device__ __forceinline__ void a4_stage_q(float *Qs, const float *q, int b, int h0, int qb, int T, int H,
+                                           const float *cs, const float *sn, float *qrot)
+{
+    const int tid = threadIdx.x, hs = tid >> 7, x = (tid & 127) >> 2, c4 = tid & 3;
+    const int qr = qb * 32 + x, qc = min(qr, T - 1);
+    const size_t off = (size_t)(b * T + qc) * (H * AT_HD) + (h0 + hs) * AT_HD;
+    A4Task<ROPE> tq;
+    tq.load(q + off, c4, qc, true, cs, sn);
+    tq.rotate(true);
+    tq.store(Qs + (hs * 32 + x) * A4_LD, c4, qr < T);
+    if (qrot && qr < T) {
+        *reinterpret_cast<f32x4 *>(qrot + off + 4 * c4) = tq.a;
+        *reinterpret_cast<f32x4 *>(qrot + off + 16 + 4 * c4) = tq.b;
+    }
+}
+
+// 16 floats of row `row` of a staged block from column 16 * half (the MFMA
+// A / B fragment of lane (row, half)).
+__device__ __forceinline__ void a4_frag(const float *L, int row, int half, float (&o)[16])
+{
+    const float *p = L + row * A4_LD + 16 * half;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const f32x4 t = *reinterpret_cast<const f32x4 *>(p + 4 * k);
+        o[4 * k] = t.x; o[4 * k + 1] = t.y; o[4 * k + 2] = t.z; o[4 * k + 3] = t.w;
+    }
+}
+
+template <bool ROPE>
+__global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_fwd4(const float *__restrict__ q, const float *__restrict__ k,
+                                                   const float *__restrict__ v, float *__restrict__ out,
+                                                   float *__restrict__ lse, int B, int T, int H, int KV, int win,
+                                                   float scale, const float *__restrict__ cs,
+                                                   const float *__restrict__ sn)
+{
+    // K and V staging in one array: its whole extent is the merge area later
+    __shared__ __attribute__((aligned(16))) float KVs[2 * A4_CH * 32 * A4_LD], Qs[4 * 32 * A4_LD];
+    static_assert(2 * A4_CH * 32 * A4_LD >= 4 * (A4_KS - 1) * 18 * 64, "merge area");
+    float *Ks = KVs, *Vs = KVs + A4_CH * 32 * A4_LD;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hs = wave & 3, ks = wave >> 2;
+    const int nqb = (T + 31) >> 5;
+    int b, kvh, h0, qb;
+    a4_item(blockIdx.x, B, H, KV, nqb, &b, &kvh, &h0, &qb);
+    const int h = h0 + hs, D = H * AT_HD;
+    const int lq = lane & 31, hh = lane >> 5;
+    const int qi = qb * 32 + lq;
+    const int kb0 = at_kb0(qb, win);
+
+    if (tid < 512) a4_stage_q<ROPE>(Qs, q, b, h0, qb, T, H, cs, sn, nullptr);
+    const float c2 = scale * 1.44269504088896341f;
+    float qv[16];
+    f32x16 o;
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[r] = 0.f;
+    float m = -INFINITY, l = 0.f;
+    for (int c0 = kb0; c0 <= qb; c0 += A4_CH) {
+        const int nb = min(A4_CH, qb - c0 + 1);
+        if (c0 > kb0) __syncthreads();          // the previous chunk is read
+        a4_stage_kv<ROPE>(Ks, Vs, k, v, b, kvh, T, KV, c0, nb, cs, sn);
+        __syncthreads();
+        if (c0 == kb0) a4_frag(Qs + hs * 32 * A4_LD, lq, hh, qv);
+        for (int kb = c0 + ks; kb < c0 + nb; kb += A4_KS) {
+            const float *Kb = Ks + (kb - c0) * 32 * A4_LD, *Vb = Vs + (kb - c0) * 32 * A4_LD;
+            float kv[16];
+            a4_frag(Kb, lq, hh, kv);
+            f32x16 st;
+#pragma unroll
+            for (int r = 0; r < 16; r++) st[r] = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[i], qv[i], st, 0, 0, 0);
+            // st[r] = S^T[kb * 32 + at_row(r)][qi]; only blocks on the
+            // diagonal or the window edge are masked
+            float p[16], bm = -INFINITY;
+            const bool full = at_full(kb, qb, win);
+            if (full) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    p[r] = st[r] * c2;
+                    bm = fmaxf(bm, p[r]);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    p[r] = at_visible(kb * 32 + at_row(r, lane), qi, T, win) ? st[r] * c2 : -INFINITY;
+                    bm = fmaxf(bm, p[r]);
+                }
+            }
+            bm = fmaxf(bm, __shfl_xor(bm, 32));
+            const float mn = fmaxf(m, bm);
+            const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+            float ps = 0.f;
+            if (full) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    p[r] = __builtin_amdgcn_exp2f(p[r] - mn);
+                    ps += p[r];
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    p[r] = p[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(p[r] - mn);
+                    ps += p[r];
+                }
+            }
+            l = l * alpha + ps;
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[r] *= alpha;
+            // O^T[d][q] += sum_s V[s][d] P^T[s][q]
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                o = __builtin_amdgcn_mfma_f32_32x32x2f32(Vb[at_row(r, lane) * A4_LD + lq], p[r], o, 0, 0, 0);
+            m = mn;
+        }
+    }
+    __syncthreads();
+    // the other key splits' states join split 0's in split order (the K / V
+    // area is free by now)
+    float *mg = Ks + hs * (A4_KS - 1) * 18 * 64;
+    if (ks > 0) {
+        float *mine = mg + (ks - 1) * 18 * 64;
+#pragma unroll
+        for (int r = 0; r < 16; r++) mine[r * 64 + lane] = o[r];
+        mine[16 * 64 + lane] = m;
+        mine[17 * 64 + lane] = l;
+    }
+    __syncthreads();
+    if (ks > 0 || qi >= T) return;
+    float M = m;
+#pragma unroll
+    for (int w = 0; w < A4_KS - 1; w++) M = fmaxf(M, mg[w * 18 * 64 + 16 * 64 + lane]);
+    const float a0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+    l *= a0;
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[r] *= a0;
+#pragma unroll
+    for (int w = 0; w < A4_KS - 1; w++) {
+        const float *th = mg + w * 18 * 64;
+        const float mw = th[16 * 64 + lane];
+        const float aw = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+        l += th[17 * 64 + lane] * aw;
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[r] += th[r * 64 + lane] * aw;
+    }
+    l += __shfl_xor(l, 32);
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[r] *= inv;
+    float *orow = out + (size_t)(b * T + qi) * D + h * AT_HD;
+#pragma unroll
+    for (int g4 = 0; g4 < 4; g4++)
+        *reinterpret_cast<f32x4 *>(orow + 8 * g4 + 4 * hh) = f32x4{o[4 * g4], o[4 * g4 + 1], o[4 * g4 + 2], o[4 * g4 + 3]};
+    if (hh == 0) lse[(size_t)(b * T + qi) * H + h] = M + __builtin_amdgcn_logf(l);
+}
+
+// dQ for the same items; also writes Dq = dO . O per (row, head) for the
+// dK / dV kernel, and with ROPE the rotated q rows to qrot for it.
+// dS = P (dP - Dq) scale, dQ = dS K (attn_bwd, :750-768).
+template <bool ROPE>
+__global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_dq4(const float *__restrict__ q, const float *__restrict__ k,
+                                                  const float *__restrict__ v, const float *__restrict__ o,
+                                                  const float *__restrict__ dout, const float *__restrict__ lse,
+                                                  float *__restrict__ Dq, float *__restrict__ dq, int B, int T, int H,
+                                                  int KV, int win, float scale, const float *__restrict__ cs,
+                                                  const float *__restrict__ sn, float *__restrict__ qrot)
+{
+    // K and V staging in one array: its whole extent is the merge area later
+    __shared__ __attribute__((aligned(16))) float KVs[2 * A4_CH * 32 * A4_LD], Qs[4 * 32 * A4_LD];
+    static_assert(2 * A4_CH * 32 * A4_LD >= 4 * (A4_KS - 1) * 18 * 64, "merge area");
+    float *Ks = KVs, *Vs = KVs + A4_CH * 32 * A4_LD;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hs = wave & 3, ks = wave >> 2;
+    const int nqb = (T + 31) >> 5;
+    int b, kvh, h0, qb;
+    a4_item(blockIdx.x, B, H, KV, nqb, &b, &kvh, &h0, &qb);
+    const int h = h0 + hs, D = H * AT_HD;
+    const int lq = lane & 31, hh = lane >> 5;
+    const int qi = qb * 32 + lq;
+    const bool qok = qi < T;
+    const int kb0 = at_kb0(qb, win);
+
+    const size_t qoff = (size_t)(b * T + (qok ? qi : T - 1)) * D + h * AT_HD + 16 * hh;
+    float dov[16], ov[16];
+    ld16(dout + qoff, qok, dov);
+    ld16(o + qoff, qok, ov);
+    const size_t rh = (size_t)(b * T + (qok ? qi : T - 1)) * H + h;
+    const float lsv = lse[rh];
+    if (tid < 512) a4_stage_q<ROPE>(Qs, q, b, h0, qb, T, H, cs, sn, ROPE ? qrot : nullptr);
+    float dd = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) dd += dov[i] * ov[i];
+    dd += __shfl_xor(dd, 32);
+    if (qok && hh == 0 && ks == 0) Dq[rh] = dd;
+    const float ls = qok ? lsv : 0.f;
+    const float c2 = scale * 1.44269504088896341f;
+    float qv[16];
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.f;
+    for (int c0 = kb0; c0 <= qb; c0 += A4_CH) {
+        const int nb = min(A4_CH, qb - c0 + 1);
+        if (c0 > kb0) __syncthreads();
+        a4_stage_kv<ROPE>(Ks, Vs, k, v, b, kvh, T, KV, c0, nb, cs, sn);
+        __syncthreads();
+        if (c0 == kb0) a4_frag(Qs + hs * 32 * A4_LD, lq, hh, qv);
+        for (int kb = c0 + ks; kb < c0 + nb; kb += A4_KS) {
+            const float *Kb = Ks + (kb - c0) * 32 * A4_LD, *Vb = Vs + (kb - c0) * 32 * A4_LD;
+            float kv[16], vv[16];
+            a4_frag(Kb, lq, hh, kv);
+            a4_frag(Vb, lq, hh, vv);
+            f32x16 st, dp;
+#pragma unroll
+            for (int r = 0; r < 16; r++) { st[r] = 0.f; dp[r] = 0.f; }
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[i], qv[i], st, 0, 0, 0);
+                dp = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[i], dov[i], dp, 0, 0, 0);
+            }
+            float ds[16];
+            if (at_full(kb, qb, win)) {
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    ds[r] = __builtin_amdgcn_exp2f(st[r] * c2 - ls) * (dp[r] - dd) * scale;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const float pr = __builtin_amdgcn_exp2f(st[r] * c2 - ls);
+                    ds[r] = at_visible(kb * 32 + at_row(r, lane), qi, T, win) ? pr * (dp[r] - dd) * scale : 0.f;
+                }
+            }
+            // dQ^T[d][q] += sum_s K[s][d] dS^T[s][q]
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(Kb[at_row(r, lane) * A4_LD + lq], ds[r], acc, 0, 0, 0);
+        }
+    }
+    __syncthreads();
+    float *mg = Ks + hs * (A4_KS - 1) * 16 * 64;
+    if (ks > 0) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) mg[((ks - 1) * 16 + r) * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (ks > 0 || !qok) return;
+#pragma unroll
+    for (int w = 0; w < A4_KS - 1; w++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[r] += mg[(w * 16 + r) * 64 + lane];
+    if (ROPE) {
+        // rope_apply's transpose: lane holds dims 8 g + 4 hh + i and the
+        // same +16 (registers 4 g + i and 4 (g + 2) + i)
+#pragma unroll
+        for (int g4 = 0; g4 < 2; g4++) {
+            const int d = 8 * g4 + 4 * hh;
+            const f32x4 c = *reinterpret_cast<const f32x4 *>(cs + (size_t)qi * 16 + d);
+            const f32x4 sn4 = *reinterpret_cast<const f32x4 *>(sn + (size_t)qi * 16 + d);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float a = acc[4 * g4 + i], bb = acc[4 * (g4 + 2) + i];
+                acc[4 * g4 + i] = a * c[i] + bb * sn4[i];
+                acc[4 * (g4 + 2) + i] = -a * sn4[i] + bb * c[i];
+            }
+        }
+    }
+    float *orow = dq + (size_t)(b * T + qi) * D + h * AT_HD;
+#pragma unroll
+    for (int g4 = 0; g4 < 4; g4++)
+        *reinterpret_cast<f32x4 *>(orow + 8 * g4 + 4 * hh) =
+            f32x4{acc[4 * g4], acc[4 * g4 + 1], acc[4 * g4 + 2], acc[4 * g4 + 3]};
 }
 
 // ----------------------------------------------------------- elementwise --
@@ -1019,41 +1456,108 @@ static int attn_check(const char *who, int B, int T, int H, int KV, int hd)
     return TLG_OK;
 }
 
-extern "C" int tlg_dev_attn_fwd(const float *q, const float *k, const float *v, float *out, float *lse, int B, int T,
-                                int H, int KV, int hd, int win, void *stream)
+// Forward: the GQA-group kernel when H / KV is a multiple of 4, else one
+// workgroup per (b, head, query block).  Rope tables (cs, sn) given: q and k
+// are pre-rope (group kernel only).
+static int attn_fwd_launch(const float *q, const float *k, const float *v, float *out, float *lse, int B, int T,
+                           int H, int KV, int hd, int win, const float *cs, const float *sn, void *stream)
 {
     int rc = begin();
     if (rc || (rc = attn_check("attn_fwd", B, T, H, KV, hd))) return rc;
     if (!al16(q) || !al16(k) || !al16(v) || !al16(out) || !lse)
         return tlg_fail(TLG_EINVAL, "attn_fwd: unaligned operand or no lse buffer");
+    const bool g4 = (H / KV) % 4 == 0;
+    if (cs && (!g4 || !al16(cs) || !al16(sn)))
+        return tlg_fail(TLG_EINVAL, "attn_fwd_rope: needs H / KV a multiple of 4 and 16-byte aligned tables");
     if (B == 0 || T == 0) return TLG_OK;
-    const int items = B * H * ((T + 31) / 32);
-    hipLaunchKernelGGL(k_attn_fwd, dim3(items), dim3(64 * AT_W), 0, ST(stream), q, k, v, out, lse, B, T, H, KV,
-                       win, 1.0f / sqrtf((float)hd));
+    const float scale = 1.0f / sqrtf((float)hd);
+    const int nqb = (T + 31) / 32;
+    if (g4) {
+        const dim3 grid(B * KV * (H / KV / 4) * nqb);
+        if (cs)
+            hipLaunchKernelGGL(k_attn_fwd4<true>, grid, dim3(256 * A4_KS), 0, ST(stream), q, k, v, out, lse, B, T, H, KV, win,
+                               scale, cs, sn);
+        else
+            hipLaunchKernelGGL(k_attn_fwd4<false>, grid, dim3(256 * A4_KS), 0, ST(stream), q, k, v, out, lse, B, T, H, KV,
+                               win, scale, nullptr, nullptr);
+    } else {
+        hipLaunchKernelGGL(k_attn_fwd, dim3(B * H * nqb), dim3(64 * AT_W), 0, ST(stream), q, k, v, out, lse, B, T, H,
+                           KV, win, scale);
+    }
     LAUNCH_CHECK();
     return TLG_OK;
+}
+
+static int attn_bwd_launch(const float *q, const float *k, const float *v, const float *out, const float *lse,
+                           const float *datt, float *dq, float *dk, float *dv, int B, int T, int H, int KV, int hd,
+                           int win, const float *cs, const float *sn, void *stream)
+{
+    int rc = begin();
+    if (rc || (rc = attn_check("attn_bwd", B, T, H, KV, hd))) return rc;
+    if (!al16(q) || !al16(k) || !al16(v) || !al16(out) || !al16(datt) || !al16(dq) || !lse || !dk || !dv)
+        return tlg_fail(TLG_EINVAL, "attn_bwd: unaligned or missing operand");
+    const bool g4 = (H / KV) % 4 == 0;
+    if (cs && (!g4 || !al16(cs) || !al16(sn)))
+        return tlg_fail(TLG_EINVAL, "attn_bwd_rope: needs H / KV a multiple of 4 and 16-byte aligned tables");
+    if (B == 0 || T == 0) return TLG_OK;
+    // workspace: Dq [B*T][H], and with rope tables the rotated q [B*T][H*hd]
+    void *ws;
+    const size_t nDq = ((size_t)B * T * H + 63) & ~(size_t)63;
+    if ((rc = tr_scratch((nDq + (cs ? (size_t)B * T * H * hd : 0)) * 4, &ws))) return rc;
+    const float scale = 1.0f / sqrtf((float)hd);
+    const int nqb = (T + 31) / 32;
+    hipStream_t st = ST(stream);
+    float *Dq = (float *)ws, *qrot = Dq + nDq;
+    if (g4) {
+        const dim3 grid(B * KV * (H / KV / 4) * nqb);
+        if (cs)
+            hipLaunchKernelGGL(k_attn_dq4<true>, grid, dim3(256 * A4_KS), 0, st, q, k, v, out, datt, lse, Dq, dq, B, T, H, KV,
+                               win, scale, cs, sn, qrot);
+        else
+            hipLaunchKernelGGL(k_attn_dq4<false>, grid, dim3(256 * A4_KS), 0, st, q, k, v, out, datt, lse, Dq, dq, B, T, H,
+                               KV, win, scale, nullptr, nullptr, nullptr);
+    } else {
+        hipLaunchKernelGGL(k_attn_bwd_dq, dim3(B * H * nqb), dim3(64 * AT_W), 0, st, q, k, v, out, datt, lse, Dq, dq,
+                           B, T, H, KV, win, scale);
+    }
+    if (cs)
+        hipLaunchKernelGGL(k_attn_bwd_dkv<true>, dim3(nqb * B * KV), dim3(64 * AT_KW), 0, st, (const float *)qrot, k,
+                           v, datt, lse, (const float *)Dq, dk, dv, B, T, H, KV, win, scale, cs, sn);
+    else
+        hipLaunchKernelGGL(k_attn_bwd_dkv<false>, dim3(nqb * B * KV), dim3(64 * AT_KW), 0, st, q, k, v, datt, lse,
+                           (const float *)Dq, dk, dv, B, T, H, KV, win, scale, nullptr, nullptr);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_attn_fwd(const float *q, const float *k, const float *v, float *out, float *lse, int B, int T,
+                                int H, int KV, int hd, int win, void *stream)
+{
+    return attn_fwd_launch(q, k, v, out, lse, B, T, H, KV, hd, win, nullptr, nullptr, stream);
 }
 
 extern "C" int tlg_dev_attn_bwd(const float *q, const float *k, const float *v, const float *out, const float *lse,
                                 const float *datt, float *dq, float *dk, float *dv, int B, int T, int H, int KV,
                                 int hd, int win, void *stream)
 {
-    int rc = begin();
-    if (rc || (rc = attn_check("attn_bwd", B, T, H, KV, hd))) return rc;
-    if (!al16(q) || !al16(k) || !al16(v) || !al16(out) || !al16(datt) || !al16(dq) || !lse || !dk || !dv)
-        return tlg_fail(TLG_EINVAL, "attn_bwd: unaligned or missing operand");
-    if (B == 0 || T == 0) return TLG_OK;
-    void *ws;
-    if ((rc = tr_scratch((size_t)B * T * H * 4, &ws))) return rc;
-    const float scale = 1.0f / sqrtf((float)hd);
-    const int items = B * H * ((T + 31) / 32);
-    hipStream_t st = ST(stream);
-    hipLaunchKernelGGL(k_attn_bwd_dq, dim3(items), dim3(64 * AT_W), 0, st, q, k, v, out, datt, lse, (float *)ws, dq,
-                       B, T, H, KV, win, scale);
-    hipLaunchKernelGGL(k_attn_bwd_dkv, dim3(((T + 31) / 32) * B * KV), dim3(64 * AT_KW), 0, st, q, k, v, datt, lse,
-                       (const float *)ws, dk, dv, B, T, H, KV, win, scale);
-    LAUNCH_CHECK();
-    return TLG_OK;
+    return attn_bwd_launch(q, k, v, out, lse, datt, dq, dk, dv, B, T, H, KV, hd, win, nullptr, nullptr, stream);
+}
+
+extern "C" int tlg_dev_attn_fwd_rope(const float *q, const float *k, const float *v, float *out, float *lse, int B,
+                                     int T, int H, int KV, int hd, int win, const float *cos_t, const float *sin_t,
+                                     void *stream)
+{
+    if (!cos_t || !sin_t) return tlg_fail(TLG_EINVAL, "attn_fwd_rope: no rope tables");
+    return attn_fwd_launch(q, k, v, out, lse, B, T, H, KV, hd, win, cos_t, sin_t, stream);
+}
+
+extern "C" int tlg_dev_attn_bwd_rope(const float *q, const float *k, const float *v, const float *out,
+                                     const float *lse, const float *datt, float *dq, float *dk, float *dv, int B,
+                                     int T, int H, int KV, int hd, int win, const float *cos_t, const float *sin_t,
+                                     void *stream)
+{
+    if (!cos_t || !sin_t) return tlg_fail(TLG_EINVAL, "attn_bwd_rope: no rope tables");
+    return attn_bwd_launch(q, k, v, out, lse, datt, dq, dk, dv, B, T, H, KV, hd, win, cos_t, sin_t, stream);
 }
 
 static int ew(int op, size_t n, float *y, float *y2, const float *x, const float *a, const float *b, void *stream)

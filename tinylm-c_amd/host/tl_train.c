@@ -259,6 +259,10 @@ static TlgGemmCall BTN(float *dX, int beta, int M, int K, int n, const float *co
 #define GROUP(st, ...) do { TlgGemmCall cs_[] = {__VA_ARGS__}; \
         CK(tlg_dev_gemm_group(cs_, (int)(sizeof cs_ / sizeof cs_[0]), st)); } while (0)
 
+/* rope_apply runs inside the attention kernels when the GQA-group kernels
+ * take the model (H / KV a multiple of 4); else as its own pass. */
+static int rope_fused(const TlModel *m) { return (m->H / m->KV) % 4 == 0; }
+
 /* ---- forward, tinylm.c:968-1029 ------------------------------------------- */
 int tl_train_forward(TlTrain *t, void *st)
 {
@@ -275,9 +279,15 @@ int tl_train_forward(TlTrain *t, void *st)
               *v = t->v + l * NK, *cx = t->ctx + l * ND, *fi = t->f_in + l * ND, *fnl = t->f_norm + l * ND;
         CK(tlg_dev_rmsnorm_fwd(xin, P + w.an1, an, t->a_rinv + (size_t)l * N, N, D, st));
         GROUP(st, MM(q, an, P + w.wq, N, D, D), MM(k, an, P + w.wk, N, D, KD), MM(v, an, P + w.wv, N, D, KD));
-        CK(tlg_dev_rope(q, NULL, T, N, H, t->hd, t->rcos, t->rsin, T, 0, st));
-        CK(tlg_dev_rope(k, NULL, T, N, KV, t->hd, t->rcos, t->rsin, T, 0, st));
-        CK(tlg_dev_attn_fwd(q, k, v, cx, t->lse + (size_t)l * N * H, t->B, T, H, KV, t->hd, lwin(m, l), st));
+        if (rope_fused(m)) {
+            /* q, k stay pre-rope; the attention kernels rotate as they load */
+            CK(tlg_dev_attn_fwd_rope(q, k, v, cx, t->lse + (size_t)l * N * H, t->B, T, H, KV, t->hd, lwin(m, l),
+                                     t->rcos, t->rsin, st));
+        } else {
+            CK(tlg_dev_rope(q, NULL, T, N, H, t->hd, t->rcos, t->rsin, T, 0, st));
+            CK(tlg_dev_rope(k, NULL, T, N, KV, t->hd, t->rcos, t->rsin, T, 0, st));
+            CK(tlg_dev_attn_fwd(q, k, v, cx, t->lse + (size_t)l * N * H, t->B, T, H, KV, t->hd, lwin(m, l), st));
+        }
         GROUP(st, MM(fi, cx, P + w.wo, N, D, D));
         CK(tlg_dev_add(fi, xin, ND, st));
         CK(tlg_dev_rmsnorm_fwd(fi, P + w.an2, fnl, t->f_rinv + (size_t)l * N, N, D, st));
@@ -349,10 +359,15 @@ int tl_train_backward(TlTrain *t, void *st)
         CK(tlg_dev_rmsnorm_bwd(fi, P + w.an2, t->f_rinv + (size_t)l * N, t->dfnorm, dout, t->dfin, G + w.an2, N, D,
                                st));
         GROUP(st, BT(t->datt, 0, t->dfin, P + w.wo, N, D, D), ATB(G + w.wo, cx, t->dfin, N, D, D));
-        CK(tlg_dev_attn_bwd(q, k, v, cx, t->lse + (size_t)l * N * H, t->datt, t->dq, t->dk, t->dv, t->B, T, H, KV,
-                            t->hd, lwin(m, l), st));
-        CK(tlg_dev_rope(t->dq, NULL, T, N, H, t->hd, t->rcos, t->rsin, T, 1, st));
-        CK(tlg_dev_rope(t->dk, NULL, T, N, KV, t->hd, t->rcos, t->rsin, T, 1, st));
+        if (rope_fused(m)) {
+            CK(tlg_dev_attn_bwd_rope(q, k, v, cx, t->lse + (size_t)l * N * H, t->datt, t->dq, t->dk, t->dv, t->B, T,
+                                     H, KV, t->hd, lwin(m, l), t->rcos, t->rsin, st));
+        } else {
+            CK(tlg_dev_attn_bwd(q, k, v, cx, t->lse + (size_t)l * N * H, t->datt, t->dq, t->dk, t->dv, t->B, T, H,
+                                KV, t->hd, lwin(m, l), st));
+            CK(tlg_dev_rope(t->dq, NULL, T, N, H, t->hd, t->rcos, t->rsin, T, 1, st));
+            CK(tlg_dev_rope(t->dk, NULL, T, N, KV, t->hd, t->rcos, t->rsin, T, 1, st));
+        }
         const float *dy[3] = {t->dq, t->dk, t->dv}, *wt[3] = {P + w.wq, P + w.wk, P + w.wv};
         const int ns[3] = {D, KD, KD};
         GROUP(st, BTN(t->dnorm, 0, N, D, 3, dy, wt, ns), ATB(G + w.wq, an, t->dq, N, D, D),

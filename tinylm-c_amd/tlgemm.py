@@ -82,6 +82,9 @@ SIGNATURES = {
     "tlg_dev_rope": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp]),
     "tlg_dev_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "tlg_dev_attn_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "tlg_dev_attn_fwd_rope": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
+    "tlg_dev_attn_bwd_rope": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp,
+                                   _vp]),
     "tlg_dev_add": (_i, [_vp, _vp, _sz, _vp]),
     "tlg_dev_swiglu_fwd": (_i, [_vp, _vp, _vp, _sz, _vp]),
     "tlg_dev_swiglu_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _vp]),
