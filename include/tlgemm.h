@@ -118,8 +118,27 @@ typedef struct {
     const float *A[3];       /* X / dY_s / X  (first operand of segment s) */
     const float *B[3];       /* W / W_s  / dY (second operand of segment s) */
     int Nseg[3];             /* N_s for s >= 1 (mm_bt chains) */
+    const float *R;          /* mm only, optional: C = R + X W, the residual add
+                              * that follows mm in the reference (tinylm.c:994-995,
+                              * :1009-1010) fused into the store; R [M x N] is
+                              * read, not written, and may not alias C */
 } TlgGemmCall;
 int tlg_dev_gemm_group(const TlgGemmCall *calls, int n, void *stream);
+
+/* The dense SwiGLU FFN's GEMMs with their elementwise neighbours fused (no
+ * single reference counterpart).  swiglu_mm replaces mm(g, X, W1), mm(u, X,
+ * W3) and act = silu(g) u (tinylm.c:1002-1006): X [M x K], W1 / W3 [K x N],
+ * act [M x N]; g and u (may be NULL) receive the two products.  It is also
+ * the backward's recompute of act (:1098-1100) when act is kept.
+ * mm_bt_swiglu_bwd replaces memset(dact), mm_bt(dact, dY, W2, M, K, N) and
+ * the SwiGLU backward (:1102-1109): dact = dY W2^T (dY [M x N], W2 [K x N]),
+ * then in place g <- dact u silu'(g) (dg) and u <- dact silu(g) (du), g / u
+ * [M x K].  Both flush or carry the pending split reductions of grouped
+ * launches like any grouped launch. */
+int tlg_dev_swiglu_mm(const float *X, const float *W1, const float *W3, float *act, float *g, float *u, int M, int K,
+                      int N, void *stream);
+int tlg_dev_mm_bt_swiglu_bwd(const float *dY, const float *W2, float *g, float *u, int M, int K, int N,
+                             void *stream);
 int tlg_dev_gemm_flush(void *stream);
 /* Number of split reductions still pending (what a flush would launch). */
 int tlg_dev_gemm_pending(void);

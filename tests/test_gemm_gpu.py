@@ -208,6 +208,124 @@ def test_gemv_group(lib):
             assert lib.tlg_group_kernel().decode().startswith("k_gemv")
 
 
+@pytest.mark.parametrize("M,K,N", [(4096, 256, 256), (67, 36, 44), (5, 8, 12)])
+def test_residual_mm(lib, M, K, N):
+    """TlgGemmCall.R: C = R + X W in the store, bit for bit the mm result plus
+    R (the reference adds after mm, tinylm.c:994-995); M <= 8 leaves the
+    GEMV kernels for the MFMA tiles."""
+    t = _torch()
+    X = seeded((M, K), 1.0, "rX")
+    W = seeded((K, N), 0.05, "rW")
+    Rr = seeded((M, N), 1.0, "rR")
+    x, w, r = dev(X), dev(W), dev(Rr)
+    y = t.full((M, N), float("nan"), device="cuda")
+    fused = t.full((M, N), float("nan"), device="cuda")
+    lib.group([dict(op="mm", C=y.data_ptr(), M=M, K=K, N=N, A=[x.data_ptr()], B=[w.data_ptr()])], stream())
+    lib.group([dict(op="mm", C=fused.data_ptr(), M=M, K=K, N=N, A=[x.data_ptr()], B=[w.data_ptr()],
+                    R=r.data_ptr())], stream())
+    if M > 8:
+        assert np.array_equal(fused.cpu().numpy(), y.cpu().numpy() + Rr)
+    ref = Rr.astype(np.float64) + X.astype(np.float64) @ W.astype(np.float64)
+    assert normwise_rel(fused.cpu().numpy(), ref) <= TOL
+
+
+def test_residual_reads_pending_reduction(lib, orc):
+    """A residual operand that a deferred split reduction still has to write
+    is flushed first: mm_atb (split at this shape) into dW, then mm with
+    R = dW."""
+    t = _torch()
+    X = seeded((4096, 256), 1.0, "pX")
+    dY = seeded((4096, 64), 0.01, "pdY")
+    A2 = seeded((32, 64), 1.0, "pA")
+    W2 = seeded((64, 64), 0.1, "pW")
+    dw = t.zeros((256, 64), device="cuda")
+    x, dy, a2, w2 = dev(X), dev(dY), dev(A2), dev(W2)
+    y = t.full((32, 64), float("nan"), device="cuda")
+    lib.group([dict(op="mm_atb", beta=1, C=dw.data_ptr(), M=4096, K=256, N=64, A=[x.data_ptr()],
+                    B=[dy.data_ptr()])], stream(), flush=False)
+    lib.group([dict(op="mm", C=y.data_ptr(), M=32, K=64, N=64, A=[a2.data_ptr()], B=[w2.data_ptr()],
+                    R=dw.data_ptr())], stream())
+    dW = orc.mm_atb_f64(np.zeros((256, 64), np.float32), X, dY)
+    assert normwise_rel(dw.cpu().numpy(), dW) <= TOL
+    ref = dW[:32] + A2.astype(np.float64) @ W2.astype(np.float64)
+    assert normwise_rel(y.cpu().numpy(), ref) <= TOL
+
+
+def _silu64(z):
+    return z / (1.0 + np.exp(-z))
+
+
+FFN = [(4096, 256, 768), (4096, 768, 256), (67, 32, 48), (1, 16, 8), (300, 64, 96)]
+
+
+@pytest.mark.parametrize("M,K,N", FFN)
+def test_swiglu_mm(lib, M, K, N):
+    """tlg_dev_swiglu_mm: g = X W1, u = X W3, act = silu(g) u (tinylm.c:1002-1006)
+    from one launch, against float64; without g / u it still writes act."""
+    t = _torch()
+    X = seeded((M, K), 1.0, "sX")
+    W1 = seeded((K, N), 0.1, "sW1")
+    W3 = seeded((K, N), 0.1, "sW3")
+    x, w1, w3 = dev(X), dev(W1), dev(W3)
+    act, g, u = (t.full((M, N), float("nan"), device="cuda") for _ in range(3))
+    lib.check(lib.tlg_dev_swiglu_mm(x.data_ptr(), w1.data_ptr(), w3.data_ptr(), act.data_ptr(), g.data_ptr(),
+                                    u.data_ptr(), M, K, N, stream()), "swiglu_mm")
+    g64 = X.astype(np.float64) @ W1.astype(np.float64)
+    u64 = X.astype(np.float64) @ W3.astype(np.float64)
+    assert normwise_rel(g.cpu().numpy(), g64) <= TOL
+    assert normwise_rel(u.cpu().numpy(), u64) <= TOL
+    assert normwise_rel(act.cpu().numpy(), _silu64(g64) * u64) <= TOL
+    act2 = t.full((M, N), float("nan"), device="cuda")
+    lib.check(lib.tlg_dev_swiglu_mm(x.data_ptr(), w1.data_ptr(), w3.data_ptr(), act2.data_ptr(), None, None, M, K,
+                                    N, stream()), "swiglu_mm")
+    assert np.array_equal(act2.cpu().numpy(), act.cpu().numpy())
+
+
+@pytest.mark.parametrize("M,K,N", FFN)
+def test_mm_bt_swiglu_bwd(lib, M, K, N):
+    """tlg_dev_mm_bt_swiglu_bwd: dact = dY W2^T, then dg = dact u silu'(g) and
+    du = dact silu(g) in place of g, u (tinylm.c:1102-1109), against float64."""
+    t = _torch()
+    dY = seeded((M, N), 1.0, "bdY")
+    W2 = seeded((K, N), 0.1, "bW2")
+    G0 = seeded((M, K), 1.0, "bG")
+    U0 = seeded((M, K), 1.0, "bU")
+    dy, w2, g, u = dev(dY), dev(W2), dev(G0), dev(U0)
+    lib.check(lib.tlg_dev_mm_bt_swiglu_bwd(dy.data_ptr(), w2.data_ptr(), g.data_ptr(), u.data_ptr(), M, K, N,
+                                           stream()), "mm_bt_swiglu_bwd")
+    dact = dY.astype(np.float64) @ W2.astype(np.float64).T
+    z = G0.astype(np.float64)
+    sg = 1.0 / (1.0 + np.exp(-z))
+    assert normwise_rel(g.cpu().numpy(), dact * U0 * (sg + z * sg * (1 - sg))) <= TOL
+    assert normwise_rel(u.cpu().numpy(), dact * z * sg) <= TOL
+
+
+def test_fused_ffn_carries_pending_reduction(lib, orc):
+    """A dense fused launch after a grouped launch with a split mm_atb: the
+    deferred reduction rides along (or is flushed) and both results hold."""
+    t = _torch()
+    X = seeded((4096, 256), 1.0, "cX")
+    dYa = seeded((4096, 64), 0.01, "cdY")
+    dw = t.zeros((256, 64), device="cuda")
+    x, dya = dev(X), dev(dYa)
+    lib.group([dict(op="mm_atb", beta=1, C=dw.data_ptr(), M=4096, K=256, N=64, A=[x.data_ptr()],
+                    B=[dya.data_ptr()])], stream(), flush=False)
+    assert lib.tlg_dev_gemm_pending() > 0
+    dY = seeded((512, 64), 1.0, "cdY2")
+    W2 = seeded((96, 64), 0.1, "cW2")
+    G0 = seeded((512, 96), 1.0, "cG")
+    U0 = seeded((512, 96), 1.0, "cU")
+    dy, w2, g, u = dev(dY), dev(W2), dev(G0), dev(U0)
+    lib.check(lib.tlg_dev_mm_bt_swiglu_bwd(dy.data_ptr(), w2.data_ptr(), g.data_ptr(), u.data_ptr(), 512, 96, 64,
+                                           stream()), "mm_bt_swiglu_bwd")
+    assert lib.tlg_dev_gemm_pending() == 0
+    assert normwise_rel(dw.cpu().numpy(), orc.mm_atb_f64(np.zeros((256, 64), np.float32), X, dYa)) <= TOL
+    dact = dY.astype(np.float64) @ W2.astype(np.float64).T
+    z = G0.astype(np.float64)
+    sg = 1.0 / (1.0 + np.exp(-z))
+    assert normwise_rel(u.cpu().numpy(), dact * z * sg) <= TOL
+
+
 def test_empty_dimensions(lib):
     t = _torch()
     # K = 0: mm clears Y (tinylm.c:461), the accumulating forms leave theirs

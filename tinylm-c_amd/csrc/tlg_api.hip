@@ -380,6 +380,48 @@ extern "C" int tlg_dev_gemm_pending(void) { return tlg_group_pending(); }
 const char *tlg_group_kernel_name(void);
 extern "C" const char *tlg_group_kernel(void) { return tlg_group_kernel_name(); }
 
+// ------------------------------------------------ dense SwiGLU FFN pair --
+// The dense FFN's GEMMs with their elementwise neighbours in the epilogue,
+// run by the expert-batched launch with one expert owning every row.
+static int ffn_check(const char *who, const float *A, const float *B, int M, int K, int N)
+{
+    int rc = tlg_ensure_init();
+    if (rc) return rc;
+    if (M < 0 || K <= 0 || N <= 0 || K % 4 || N % 4 || !A || !B || ((uintptr_t)A & 15) || ((uintptr_t)B & 15))
+        return tlg_fail(TLG_EINVAL, "%s: M=%d K=%d N=%d (widths %% 4 == 0, aligned operands)", who, M, K, N);
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_swiglu_mm(const float *X, const float *W1, const float *W3, float *act, float *g, float *u,
+                                 int M, int K, int N, void *stream)
+{
+    int rc = ffn_check("tlg_dev_swiglu_mm", X, W1, M, K, N);
+    if (rc) return rc;
+    if (!W3 || !act || ((uintptr_t)W3 & 15) || ((uintptr_t)act & 15) || ((uintptr_t)g & 15) || ((uintptr_t)u & 15))
+        return tlg_fail(TLG_EINVAL, "tlg_dev_swiglu_mm: missing or unaligned operand");
+    TlgExpertCall c;
+    memset(&c, 0, sizeof c);
+    c.op = 0; c.C = act; c.K = K; c.N = N; c.nseg = 1;
+    c.A[0] = X; c.B[0] = W1; c.B2 = W3;
+    c.epi = TLG_EPI_SWIGLU; c.X1 = g; c.X2 = u;
+    return tlg_expert_launch(&c, 1, nullptr, 1, M, (hipStream_t)stream);
+}
+
+extern "C" int tlg_dev_mm_bt_swiglu_bwd(const float *dY, const float *W2, float *g, float *u, int M, int K, int N,
+                                        void *stream)
+{
+    int rc = ffn_check("tlg_dev_mm_bt_swiglu_bwd", dY, W2, M, K, N);
+    if (rc) return rc;
+    if (!g || !u || ((uintptr_t)g & 15) || ((uintptr_t)u & 15))
+        return tlg_fail(TLG_EINVAL, "tlg_dev_mm_bt_swiglu_bwd: missing or unaligned g / u");
+    TlgExpertCall c;
+    memset(&c, 0, sizeof c);
+    c.op = 1; c.C = nullptr; c.K = K; c.N = N; c.nseg = 1;
+    c.A[0] = dY; c.B[0] = W2;
+    c.epi = TLG_EPI_SWIGLU_BWD; c.X1 = g; c.X2 = u;
+    return tlg_expert_launch(&c, 1, nullptr, 1, M, (hipStream_t)stream);
+}
+
 // ------------------------------------------------------------- top-1 MoE --
 int tlg_moe_fwd_launch(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,
                        const float *wr, const float *w1, const float *w3, const float *w2, int *assign,

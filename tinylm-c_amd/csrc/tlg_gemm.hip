@@ -524,6 +524,7 @@ struct Prob {
 };
 struct GroupArgs {
     int nprob;
+    int rows1;            // expert launches: > 0 = one expert owning rows [0, rows1)
     Prob p[TLG_MAXPROB];
 };
 
@@ -709,6 +710,17 @@ __device__ __forceinline__ void group_tile(float *smem, const Prob &P, int local
         const Seg &s = P.seg[k];
         tile_accumulate<T, LA, LB, true>(smem, s.A, s.B, s.lda, s.ldb, i0, j0, P.Mo, P.No, 0, s.R, acc);
     }
+    if (LA == RC && LB == OC && P.fin) {
+        // mm with its residual add: C = R + acc (R in `fin`, C's layout)
+        float *C = P.C;
+        const float *Rr = P.fin;
+        const int ld = P.ldc;
+        tile_epi<T>(acc, P.Mo, P.No, i0, j0, smem, [&](int i, int j, float v) {
+            const size_t o = (size_t)i * ld + j;
+            C[o] = Rr[o] + v;
+        });
+        return;
+    }
     tile_store<T>(acc, P.C, P.ldc, P.beta, P.Mo, P.No, i0, j0, smem);
 }
 
@@ -785,7 +797,11 @@ __global__ __launch_bounds__(T::THREADS) __attribute__((amdgpu_waves_per_eu(4)))
     __shared__ __attribute__((aligned(16))) float smem[T::lds_max()];
     __shared__ int eo[TLG_MAX_EXPERTS + 1];
     const int E = g.p[0].nexp;
-    for (int i = threadIdx.x; i <= E; i += blockDim.x) eo[i] = g.p[0].eoff[i];
+    if (g.rows1 > 0) {
+        if (threadIdx.x < 2) eo[threadIdx.x] = threadIdx.x ? g.rows1 : 0;
+    } else {
+        for (int i = threadIdx.x; i <= E; i += blockDim.x) eo[i] = g.p[0].eoff[i];
+    }
     __syncthreads();
     group_body<T, true>(g, smem, eo);
 }
@@ -1266,6 +1282,7 @@ int tlg_group_flush_launch(hipStream_t st)
     if (g_npending == 0) return TLG_OK;
     GroupArgs a;
     a.nprob = 0;
+    a.rows1 = 0;
     add_reductions(a);
     launch_group(3, a, group_grid(a), st);
     TLG_HIP(hipGetLastError());
@@ -1311,11 +1328,13 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
     group_env();
     if (n > TLG_MAXPROB / 2) return tlg_fail(TLG_EINVAL, "tlg_dev_gemm_group: at most %d calls", TLG_MAXPROB / 2);
 
-    // Decode runs (every call mm / mm_bt at M <= 8) go to the GEMV kernels.
+    // Decode runs (every call mm / mm_bt at M <= 8, no residual) go to the
+    // GEMV kernels.
     bool gemv = true;
     int mmax = 1;
     for (int i = 0; i < n && gemv; i++) {
-        gemv = (calls[i].op == 0 || calls[i].op == 1) && calls[i].M >= 1 && calls[i].M <= 8 && calls[i].K > 0 &&
+        gemv = (calls[i].op == 0 || calls[i].op == 1) && !calls[i].R && calls[i].M >= 1 && calls[i].M <= 8 &&
+               calls[i].K > 0 &&
                calls[i].N > 0 && calls[i].nseg >= 1 && calls[i].nseg <= TLG_MAXSEG &&
                (calls[i].nseg == 1 || calls[i].op == 1);
         if (calls[i].M > mmax) mmax = calls[i].M;
@@ -1348,6 +1367,11 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
                 else if (op == 1) { span(c.A[s], c.M, Ns, Ns, &x0, &x1); span(c.B[s], c.K, Ns, Ns, &y0, &y1); }
                 else              { span(c.A[s], c.M, c.K, c.K, &x0, &x1); span(c.B[s], c.M, Ns, Ns, &y0, &y1); }
                 hit = overlap(c0, c1, x0, x1) || overlap(c0, c1, y0, y1);
+            }
+            if (!hit && op == 0 && c.R) {
+                const char *r0, *r1;
+                span(c.R, c.M, c.N, c.N, &r0, &r1);
+                hit = overlap(c0, c1, r0, r1);
             }
             if (hit) { rc = tlg_group_flush_launch(st); if (rc) return rc; break; }
         }
@@ -1402,6 +1426,11 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
         P.ldc = P.No;
         if (!vec || !c.C || R == 0 || P.Mo == 0 || P.No == 0)
             return tlg_fail(TLG_EINVAL, "tlg_dev_gemm_group: call %d needs aligned, non-empty operands", i);
+        if (c.R) {
+            if (c.op != 0 || !al16(c.R) || c.R == c.C)
+                return tlg_fail(TLG_EINVAL, "tlg_dev_gemm_group: call %d: residual only on mm, aligned, not C", i);
+            P.fin = c.R;
+        }
         Rtot[i] = R;
         if (c.op != 2 && R > rmax) rmax = R;
     }
@@ -1433,6 +1462,7 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
 
     GroupArgs a;
     a.nprob = 0;
+    a.rows1 = 0;
     add_reductions(a);
     float *ws = g_tlg.ws + (size_t)g_ws_half * (g_tlg.ws_floats / 2);
     size_t ws_used = 0;
@@ -1483,12 +1513,39 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     int rc = tlg_ensure_init();
     if (rc) return rc;
     if (n > TLG_MAXPROB / 2) return tlg_fail(TLG_EINVAL, "expert launch: at most %d calls", TLG_MAXPROB / 2);
-    if (!eoff || E < 1 || E > TLG_MAX_EXPERTS || rows < 0)
+    // eoff NULL: one expert owning every row (dense rows, known on the host)
+    const bool dense = eoff == nullptr;
+    if ((dense && E != 1) || E < 1 || E > TLG_MAX_EXPERTS || rows < 0)
         return tlg_fail(TLG_EINVAL, "expert launch: bad row offsets or %d experts", E);
     if (rows == 0) return TLG_OK;
-    // the partial slots below reuse the whole workspace
-    rc = tlg_group_flush_launch(st);
-    if (rc) return rc;
+    // Pending split reductions of grouped launches ride along when this
+    // launch writes no partial slots (they reuse the whole workspace) and
+    // touches none of their outputs; otherwise they are flushed first.
+    bool ride = dense;
+    for (int i = 0; i < n && ride; i++) {
+        const TlgExpertCall &c = calls[i];
+        if (c.op == 2 || c.amap || c.omap) { ride = false; break; }
+        const int Nr = c.op == 0 ? c.N : c.K;          // output / epilogue row width
+        const int Na = c.op == 0 ? c.K : c.N;          // A row width
+        const char *r0[7], *r1[7];
+        int m = 0;
+        if (c.C) span(c.C, rows, Nr, Nr, &r0[m], &r1[m]), m++;
+        if (c.X1) span(c.X1, rows, Nr, Nr, &r0[m], &r1[m]), m++;
+        if (c.X2) span(c.X2, rows, Nr, Nr, &r0[m], &r1[m]), m++;
+        if (c.fin) span(c.fin, rows, Nr, Nr, &r0[m], &r1[m]), m++;
+        span(c.A[0], rows, Na, Na, &r0[m], &r1[m]), m++;
+        span(c.B[0], c.K, c.N, c.N, &r0[m], &r1[m]), m++;
+        if (c.B2) span(c.B2, c.K, c.N, c.N, &r0[m], &r1[m]), m++;
+        for (int k = 0; k < g_npending && ride; k++) {
+            const char *c0, *c1;
+            span(g_pending[k].C, g_pending[k].Mo, g_pending[k].No, g_pending[k].ldc, &c0, &c1);
+            for (int j = 0; j < m && ride; j++) ride = !overlap(c0, c1, r0[j], r1[j]);
+        }
+    }
+    if (!ride) {
+        rc = tlg_group_flush_launch(st);
+        if (rc) return rc;
+    }
 
     group_env();
     Prob probs[TLG_MAXPROB / 2];
@@ -1565,8 +1622,10 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     };
     const int ci = items_for(kCfgs[3]) >= g_min_waves * 256 ? 3 : 14;
     const TileCfg &tc = kCfgs[ci];
-    GroupArgs a, red;
-    a.nprob = red.nprob = 0;
+    GroupArgs a, red, pend;
+    a.nprob = red.nprob = pend.nprob = 0;
+    a.rows1 = red.rows1 = pend.rows1 = dense ? rows : 0;
+    if (ride) add_reductions(pend);
     size_t used = 0;
     int order[TLG_MAXPROB / 2];
     for (int i = 0; i < n; i++) {
@@ -1605,6 +1664,8 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
             red.p[red.nprob++] = r;
         }
     }
+    // the grouped launches' reductions that ride along go last (short items)
+    for (int k = 0; k < pend.nprob; k++) a.p[a.nprob++] = pend.p[k];
     // an XCD's share of the real items can exceed its share of the upper
     // bound by one per expert problem
     static_assert(sizeof(GroupArgs) <= 4096, "kernel arguments");

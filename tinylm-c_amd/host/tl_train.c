@@ -30,10 +30,9 @@ struct TlTrain {
     int *tok, *tgt, *tgt_mtp, *assign;
     float *hyper, *loss, *gnorm, *rcos, *rsin;
     /* per layer, L slices each (the Acts fields the backward pass reads) */
-    float *a_in, *a_norm, *q, *k, *v, *ctx, *f_in, *f_norm, *g, *u, *a_rinv, *f_rinv, *lse, *gate, *rprobs;
+    float *a_in, *a_norm, *q, *k, *v, *ctx, *f_in, *f_norm, *g, *u, *act, *a_rinv, *f_rinv, *lse, *gate, *rprobs;
     /* one each */
-    float *x_final, *fn, *fn_rinv, *logits, *dl, *dout, *act, *dg, *du, *dfnorm, *dfin, *datt, *dq, *dk, *dv,
-          *dnorm, *dain, *dfn;
+    float *x_final, *fn, *fn_rinv, *logits, *dl, *dout, *dfnorm, *dfin, *datt, *dq, *dk, *dv, *dnorm, *dain, *dfn;
     float hyper_host[8];
     void *graph;
 };
@@ -106,8 +105,7 @@ TlTrain *tl_train_new(const TlModel *m, int B)
         {(void **)&t->rprobs, 4 * L * N * E},
         {(void **)&t->x_final, 4 * ND}, {(void **)&t->fn, 4 * ND}, {(void **)&t->fn_rinv, 4 * N},
         {(void **)&t->logits, 4 * N * V}, {(void **)&t->dl, 4 * N * V}, {(void **)&t->dout, 4 * ND},
-        {(void **)&t->act, dense ? 4 * NF : 0}, {(void **)&t->dg, dense ? 4 * NF : 0},
-        {(void **)&t->du, dense ? 4 * NF : 0}, {(void **)&t->dfnorm, 4 * ND}, {(void **)&t->dfin, 4 * ND},
+        {(void **)&t->act, dense ? 4 * L * NF : 0}, {(void **)&t->dfnorm, 4 * ND}, {(void **)&t->dfin, 4 * ND},
         {(void **)&t->datt, 4 * ND}, {(void **)&t->dq, 4 * ND}, {(void **)&t->dk, 4 * NK},
         {(void **)&t->dv, 4 * NK}, {(void **)&t->dnorm, 4 * ND}, {(void **)&t->dain, 4 * ND},
         {(void **)&t->dfn, 4 * ND},
@@ -172,7 +170,7 @@ float *tl_train_act(TlTrain *t, const char *name, int layer)
     struct { const char *n; float *p; size_t per; } tab[] = {
         {"a_in", t->a_in, ND}, {"a_norm", t->a_norm, ND}, {"q", t->q, ND}, {"k", t->k, NK}, {"v", t->v, NK},
         {"att_ctx", t->ctx, ND}, {"f_in", t->f_in, ND}, {"f_norm", t->f_norm, ND}, {"g", t->g, NF},
-        {"u", t->u, NF}, {"a_rinv", t->a_rinv, N}, {"f_rinv", t->f_rinv, N}, {"lse", t->lse, N * t->m.H},
+        {"u", t->u, NF}, {"act", t->act, NF}, {"a_rinv", t->a_rinv, N}, {"f_rinv", t->f_rinv, N}, {"lse", t->lse, N * t->m.H},
         {"x_final", t->x_final, 0}, {"fn_norm", t->fn, 0}, {"fn_rinv", t->fn_rinv, 0},
         {"logits", t->logits, 0}, {"dlogits", t->dl, 0}, {"dfn", t->dfn, 0},
     };
@@ -233,6 +231,13 @@ static TlgGemmCall MM(float *Y, const float *X, const float *W, int M, int K, in
     c.op = 0; c.C = Y; c.M = M; c.K = K; c.N = N; c.nseg = 1; c.A[0] = X; c.B[0] = W;
     return c;
 }
+/* Y = R + X W: mm and the residual add after it in one call */
+static TlgGemmCall MMR(float *Y, const float *X, const float *W, int M, int K, int N, const float *R)
+{
+    TlgGemmCall c = MM(Y, X, W, M, K, N);
+    c.R = R;
+    return c;
+}
 static TlgGemmCall BT(float *dX, int beta, const float *dY, const float *W, int M, int K, int N)
 {
     TlgGemmCall c = MM(dX, dY, W, M, K, N);
@@ -288,8 +293,7 @@ int tl_train_forward(TlTrain *t, void *st)
             CK(tlg_dev_rope(k, NULL, T, N, KV, t->hd, t->rcos, t->rsin, T, 0, st));
             CK(tlg_dev_attn_fwd(q, k, v, cx, t->lse + (size_t)l * N * H, t->B, T, H, KV, t->hd, lwin(m, l), st));
         }
-        GROUP(st, MM(fi, cx, P + w.wo, N, D, D));
-        CK(tlg_dev_add(fi, xin, ND, st));
+        GROUP(st, MMR(fi, cx, P + w.wo, N, D, D, xin));                 /* + residual, :994-995 */
         CK(tlg_dev_rmsnorm_fwd(fi, P + w.an2, fnl, t->f_rinv + (size_t)l * N, N, D, st));
         float *out = l + 1 < m->L ? t->a_in + (l + 1) * ND : t->x_final;
         if (E > 0) {
@@ -297,11 +301,11 @@ int tl_train_forward(TlTrain *t, void *st)
                                        t->assign + (size_t)l * N, t->gate + (size_t)l * N,
                                        t->rprobs + (size_t)l * N * E, st));
         } else {
-            float *g = t->g + l * NF, *u = t->u + l * NF;
-            GROUP(st, MM(g, fnl, P + w.w1, N, D, F), MM(u, fnl, P + w.w3, N, D, F));
-            CK(tlg_dev_swiglu_fwd(t->act, g, u, NF, st));
-            GROUP(st, MM(out, t->act, P + w.w2, N, F, D));
-            CK(tlg_dev_add(out, fi, ND, st));
+            /* g, u and act = silu(g) u (:1002-1006) from one launch; act is
+             * kept per layer, so the backward's recompute (:1098-1100) is a read */
+            float *g = t->g + l * NF, *u = t->u + l * NF, *act = t->act + l * NF;
+            CK(tlg_dev_swiglu_mm(fnl, P + w.w1, P + w.w3, act, g, u, N, D, F, st));
+            GROUP(st, MMR(out, act, P + w.w2, N, F, D, fi));               /* + residual, :1009-1010 */
         }
     }
     CK(tlg_dev_rmsnorm_fwd(t->x_final, P + w.nf, t->fn, t->fn_rinv, N, D, st));
@@ -347,14 +351,14 @@ int tl_train_backward(TlTrain *t, void *st)
                                        t->rprobs + (size_t)l * N * E, N, D, F, E, P + w.wr, P + w.w1, P + w.w3,
                                        P + w.w2, G + w.wr, G + w.w1, G + w.w3, G + w.w2, st));
         } else {
-            float *g = t->g + l * NF, *u = t->u + l * NF;
-            CK(tlg_dev_swiglu_fwd(t->du, g, u, NF, st));                 /* act recompute, :1097-1098 */
-            GROUP(st, ATB(G + w.w2, t->du, dout, N, F, D), BT(t->act, 0, dout, P + w.w2, N, F, D));
-            CK(tlg_dev_swiglu_bwd(t->act, g, u, t->dg, t->du, NF, st));
-            const float *dy[2] = {t->dg, t->du}, *wt[2] = {P + w.w1, P + w.w3};
+            /* d_act = dout W2^T with the SwiGLU backward in its epilogue
+             * (:1103-1109): g, u of this layer become dg, du in place */
+            float *g = t->g + l * NF, *u = t->u + l * NF, *act = t->act + l * NF;
+            CK(tlg_dev_mm_bt_swiglu_bwd(dout, P + w.w2, g, u, N, F, D, st));
+            const float *dy[2] = {g, u}, *wt[2] = {P + w.w1, P + w.w3};
             const int ns[2] = {F, F};
-            GROUP(st, BTN(t->dfnorm, 0, N, D, 2, dy, wt, ns), ATB(G + w.w1, fnl, t->dg, N, D, F),
-                  ATB(G + w.w3, fnl, t->du, N, D, F));
+            GROUP(st, BTN(t->dfnorm, 0, N, D, 2, dy, wt, ns), ATB(G + w.w1, fnl, g, N, D, F),
+                  ATB(G + w.w3, fnl, u, N, D, F), ATB(G + w.w2, act, dout, N, F, D));   /* dW2, :1101 */
         }
         CK(tlg_dev_rmsnorm_bwd(fi, P + w.an2, t->f_rinv + (size_t)l * N, t->dfnorm, dout, t->dfin, G + w.an2, N, D,
                                st));

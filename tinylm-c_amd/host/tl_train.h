@@ -37,8 +37,11 @@ size_t   tl_train_nparams(const TlTrain *t);
 /* Device buffers: 0 P, 1 G, 2 AdamW M, 3 AdamW V (tl_train_nparams floats). */
 float   *tl_train_buf(TlTrain *t, int which);
 /* Device address of a named activation ("logits", "dlogits", "x_final",
- * "fn_norm", "a_in", "q", "k", "v", "att_ctx", "lse", "f_in", ...; per-layer
- * ones at `layer`), for tests; NULL if unknown. */
+ * "fn_norm", "a_in", "q", "k", "v", "att_ctx", "lse", "f_in", "act", ...;
+ * per-layer ones at `layer`), for tests; NULL if unknown.  When H / KV is a
+ * multiple of 4, "q" and "k" hold the projections before rope_apply (the
+ * attention kernels rotate as they load); after a backward pass a dense
+ * layer's "g" and "u" hold dg and du. */
 float   *tl_train_act(TlTrain *t, const char *name, int layer);
 
 /* Copy a host parameter vector into P and clear M and V. */

@@ -82,6 +82,8 @@ SIGNATURES = {
     "tlg_dev_rope": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp]),
     "tlg_dev_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "tlg_dev_attn_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "tlg_dev_swiglu_mm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "tlg_dev_mm_bt_swiglu_bwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "tlg_dev_attn_fwd_rope": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
     "tlg_dev_attn_bwd_rope": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp,
                                    _vp]),
@@ -127,7 +129,7 @@ class TlgGemmCall(ctypes.Structure):
     """include/tlgemm.h TlgGemmCall: one call of a grouped launch."""
     _fields_ = [("op", ctypes.c_int), ("beta", ctypes.c_int), ("C", _vp),
                 ("M", ctypes.c_int), ("K", ctypes.c_int), ("N", ctypes.c_int), ("nseg", ctypes.c_int),
-                ("A", _vp * 3), ("B", _vp * 3), ("Nseg", ctypes.c_int * 3)]
+                ("A", _vp * 3), ("B", _vp * 3), ("Nseg", ctypes.c_int * 3), ("R", _vp)]
 
 
 class TlgDecGemv(ctypes.Structure):
@@ -187,19 +189,21 @@ class Lib:
                                                            gw2, stream),
                           "tlg_dev_moe_grouped_bwd")
 
-    def group(self, calls, stream=0):
-        """tlg_dev_gemm_group over dicts {op, beta, C, M, K, N, A: [..], B: [..], Nseg: [..]}."""
+    def group(self, calls, stream=0, flush=True):
+        """tlg_dev_gemm_group over dicts {op, beta, C, M, K, N, A: [..], B: [..], Nseg: [..], R}."""
         arr = (TlgGemmCall * len(calls))()
         for i, c in enumerate(calls):
             a = arr[i]
             a.op, a.beta, a.C = {"mm": 0, "mm_bt": 1, "mm_atb": 2}[c["op"]], c.get("beta", 0), c["C"]
+            a.R = c.get("R", None)
             a.M, a.K, a.N = c["M"], c["K"], c["N"]
             a.nseg = len(c["A"])
             for s_ in range(a.nseg):
                 a.A[s_], a.B[s_] = c["A"][s_], c["B"][s_]
                 a.Nseg[s_] = c.get("Nseg", [c["N"]] * 3)[s_]
         self.check(self.dll.tlg_dev_gemm_group(arr, len(calls), stream), "tlg_dev_gemm_group")
-        return self.check(self.dll.tlg_dev_gemm_flush(stream), "tlg_dev_gemm_flush")
+        if flush:
+            self.check(self.dll.tlg_dev_gemm_flush(stream), "tlg_dev_gemm_flush")
 
     def kernel_name(self, op, M, K, N):
         """(rocprof kernel name, splits) a device call of op 'mm'/'mm_bt'/'mm_atb' uses."""
