@@ -516,6 +516,44 @@ class Decoder:
             pass
 
 
+DEC_LIB = os.path.join(HERE, "_ref", "libtlref_dec.so")
+
+
+class DecAttn:
+    """One layer's decode attention step -- the new rows' ring stores, then
+    attention of the query rows over their windows -- from the oracle
+    (orc_dec_attn) or from the reference's own kv_store and attn_body
+    (_ref/libtlref_dec.so, forward_chunk's unsplit path, tinylm.c:3759-3795).
+    Ring of W = T positions, f32 (kvdt 0) or f16 (kvdt 1), fast_expf."""
+
+    def __init__(self, which, D, H, KV, T, L=1, win=0, full_every=0, kvdt=1):
+        self.D, self.KD = D, KV * (D // H)
+        if which == "oracle":
+            d = ctypes.CDLL(LIB)
+            d.orc_dec_new.argtypes = [ctypes.POINTER(OrcModel), _i, _i, _i, _i]
+            d.orc_dec_new.restype = ctypes.c_void_p
+            d.orc_dec_attn.argtypes = [ctypes.c_void_p, _i, _fp, _fp, _fp, _i, _i, _fp]
+            self.m = model(1, D, L, H, KV, 4, T, win=win, full_every=full_every)
+            self.h = d.orc_dec_new(ctypes.byref(self.m), T, kvdt, 0, T)
+            self.fn = d.orc_dec_attn
+        else:
+            d = ctypes.CDLL(DEC_LIB)
+            d.tlref_dec_new.argtypes = [_i] * 8
+            d.tlref_dec_new.restype = ctypes.c_void_p
+            d.tlref_dec_attn.argtypes = [ctypes.c_void_p, _i, _fp, _fp, _fp, _i, _i, _fp]
+            d.tlref_dec_attn.restype = _i
+            self.h = d.tlref_dec_new(D, H, KV, T, L, win, full_every, kvdt)
+            self.fn = d.tlref_dec_attn
+        self.dll = d
+
+    def attn(self, l, q, k, v, start):
+        q, k, v = (np.ascontiguousarray(a, np.float32) for a in (q, k, v))
+        m = q.shape[0]
+        ctx = np.empty((m, self.D), np.float32)
+        self.fn(self.h, l, _f(q), _f(k), _f(v), m, start, _f(ctx))
+        return ctx
+
+
 def ref_forward_logits(m, B, P, tok, path=SEQ_LIB):
     """forward()'s logits [B*T][V] from the reference's own code."""
     d = ctypes.CDLL(path)

@@ -124,6 +124,11 @@ typedef struct OrcDec OrcDec;
 OrcDec *orc_dec_new(const OrcModel *m, int W, int kvdt, int exact_exp, int maxpos);
 void    orc_dec_free(OrcDec *d);
 void    orc_dec_chunk(OrcDec *d, const float *P, const int *tok, int m, int start_pos, float *logits);
+/* One layer's attention step of orc_dec_chunk: ring stores of the m new K / V
+ * rows, then attention of the m query rows (q [m][D], k / v [m][KD], ctx
+ * [m][D]). */
+void    orc_dec_attn(OrcDec *d, int l, const float *q, const float *k, const float *v, int m, int start_pos,
+                     float *ctx);
 float          orc_fast_expf(float x);         /* :3181-3191 */
 unsigned short orc_f2h(float f);               /* :3158-3168 (F16C path) */
 float          orc_h2f(unsigned short h);      /* :3147-3157 */

@@ -522,19 +522,70 @@ static float dec_val(const void *row, int i, int kvdt)
     return kvdt ? orc_h2f(((const unsigned short *)row)[i]) : ((const float *)row)[i];
 }
 
+/* One layer's decode attention for m rows at positions start..start+m-1:
+ * the m new K / V rows go into the ring first (forward_chunk's hoisted
+ * kv_store, :3765-3780), then every (row, head) attends over its window
+ * (attn_body's unsplit path, :3639-3715); ctx [m][D]. */
+void orc_dec_attn(OrcDec *d, int l, const float *q, const float *k, const float *v, int m, int start, float *ctx)
+{
+    const OrcModel *md = &d->m;
+    const int D = md->D, H = md->H, KV = md->KV, hd = D / H, KD = KV * hd, W = d->W, grp = H / KV,
+              esz = d->kvdt ? 2 : 4;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float *pr = zalloc(W);
+    int eff = layer_win(md, l), wlim = (eff > 0 && eff < W) ? eff : W;
+    for (int j = 0; j < m; j++) {               /* kv_store into the ring */
+        const int slot = (start + j) % W;
+        for (int i = 0; i < KD; i++) {
+            if (d->kvdt) {
+                ((unsigned short *)d->K[l])[(size_t)slot * KD + i] = orc_f2h(k[(size_t)j * KD + i]);
+                ((unsigned short *)d->V[l])[(size_t)slot * KD + i] = orc_f2h(v[(size_t)j * KD + i]);
+            } else {
+                ((float *)d->K[l])[(size_t)slot * KD + i] = k[(size_t)j * KD + i];
+                ((float *)d->V[l])[(size_t)slot * KD + i] = v[(size_t)j * KD + i];
+            }
+        }
+    }
+    for (int j = 0; j < m; j++)
+        for (int h = 0; h < H; h++) {
+            const int p = start + j, lo = p >= wlim ? p - wlim + 1 : 0, cnt = p - lo + 1, kh = h / grp;
+            const float *qh = q + (size_t)j * D + (size_t)h * hd;
+            float mx = -1e30f;
+            for (int t = 0; t < cnt; t++) {
+                const int slot = (lo + t) % W;
+                const char *kr = (const char *)d->K[l] + ((size_t)slot * KD + (size_t)kh * hd) * esz;
+                pr[t] = dec_dot(qh, kr, hd, d->kvdt) * scale;
+                if (pr[t] > mx) mx = pr[t];
+            }
+            float s = 0.0f;
+            for (int t = 0; t < cnt; t++) {
+                pr[t] = d->exact ? expf(pr[t] - mx) : orc_fast_expf(pr[t] - mx);
+                s += pr[t];
+            }
+            const float inv = s > 0 ? 1.0f / s : 0.0f;
+            for (int t = 0; t < cnt; t++) pr[t] *= inv;
+            float *acc = ctx + (size_t)j * D + (size_t)h * hd;
+            for (int i = 0; i < hd; i++) acc[i] = 0.0f;
+            for (int t = 0; t < cnt; t++) {
+                const int slot = (lo + t) % W;
+                const char *vr = (const char *)d->V[l] + ((size_t)slot * KD + (size_t)kh * hd) * esz;
+                for (int i = 0; i < hd; i++) acc[i] = fmaf(pr[t], dec_val(vr, i, d->kvdt), acc[i]);
+            }
+        }
+    free(pr);
+}
+
 /* m tokens at positions start..start+m-1; logits [m][V] (main head). */
 void orc_dec_chunk(OrcDec *d, const float *P, const int *tok, int m, int start, float *logits)
 {
     const OrcModel *md = &d->m;
-    const int D = md->D, H = md->H, KV = md->KV, hd = D / H, KD = KV * hd, F = md->F, V = md->V, W = d->W,
-              grp = H / KV, esz = d->kvdt ? 2 : 4;
-    const float scale = 1.0f / sqrtf((float)hd);
+    const int D = md->D, H = md->H, KV = md->KV, hd = D / H, KD = KV * hd, F = md->F, V = md->V;
     OrcLayerMap w;
     orc_param_map(md, 0, &w);
     float *x = zalloc((size_t)m * D), *xn = zalloc((size_t)m * D), *q = zalloc((size_t)m * D),
           *k = zalloc((size_t)m * KD), *v = zalloc((size_t)m * KD), *ctx = zalloc((size_t)m * D),
           *tmp = zalloc((size_t)m * D), *g = zalloc((size_t)m * F), *u = zalloc((size_t)m * F),
-          *rinv = zalloc(m), *pr = zalloc(W);
+          *rinv = zalloc(m);
     int *pos = calloc(m, sizeof(int));
     for (int j = 0; j < m; j++) {
         memcpy(x + (size_t)j * D, P + w.emb + (size_t)tok[j] * D, sizeof(float) * D);
@@ -548,45 +599,7 @@ void orc_dec_chunk(OrcDec *d, const float *P, const int *tok, int m, int start, 
         orc_mm(v, xn, P + w.wv, m, D, KD);
         orc_rope(q, pos, 1, m, H, hd, d->cs, d->sn, 0);
         orc_rope(k, pos, 1, m, KV, hd, d->cs, d->sn, 0);
-        int eff = layer_win(md, l), wlim = (eff > 0 && eff < W) ? eff : W;
-        for (int j = 0; j < m; j++) {               /* kv_store into the ring */
-            const int slot = (start + j) % W;
-            for (int i = 0; i < KD; i++) {
-                if (d->kvdt) {
-                    ((unsigned short *)d->K[l])[(size_t)slot * KD + i] = orc_f2h(k[(size_t)j * KD + i]);
-                    ((unsigned short *)d->V[l])[(size_t)slot * KD + i] = orc_f2h(v[(size_t)j * KD + i]);
-                } else {
-                    ((float *)d->K[l])[(size_t)slot * KD + i] = k[(size_t)j * KD + i];
-                    ((float *)d->V[l])[(size_t)slot * KD + i] = v[(size_t)j * KD + i];
-                }
-            }
-        }
-        for (int j = 0; j < m; j++)
-            for (int h = 0; h < H; h++) {
-                const int p = pos[j], lo = p >= wlim ? p - wlim + 1 : 0, cnt = p - lo + 1, kh = h / grp;
-                const float *qh = q + (size_t)j * D + (size_t)h * hd;
-                float mx = -1e30f;
-                for (int t = 0; t < cnt; t++) {
-                    const int slot = (lo + t) % W;
-                    const char *kr = (const char *)d->K[l] + ((size_t)slot * KD + (size_t)kh * hd) * esz;
-                    pr[t] = dec_dot(qh, kr, hd, d->kvdt) * scale;
-                    if (pr[t] > mx) mx = pr[t];
-                }
-                float s = 0.0f;
-                for (int t = 0; t < cnt; t++) {
-                    pr[t] = d->exact ? expf(pr[t] - mx) : orc_fast_expf(pr[t] - mx);
-                    s += pr[t];
-                }
-                const float inv = s > 0 ? 1.0f / s : 0.0f;
-                for (int t = 0; t < cnt; t++) pr[t] *= inv;
-                float *acc = ctx + (size_t)j * D + (size_t)h * hd;
-                for (int i = 0; i < hd; i++) acc[i] = 0.0f;
-                for (int t = 0; t < cnt; t++) {
-                    const int slot = (lo + t) % W;
-                    const char *vr = (const char *)d->V[l] + ((size_t)slot * KD + (size_t)kh * hd) * esz;
-                    for (int i = 0; i < hd; i++) acc[i] = fmaf(pr[t], dec_val(vr, i, d->kvdt), acc[i]);
-                }
-            }
+        orc_dec_attn(d, l, q, k, v, m, start, ctx);
         orc_mm(tmp, ctx, P + w.wo, m, D, D);
         for (size_t i = 0; i < (size_t)m * D; i++) x[i] += tmp[i];
         orc_rmsnorm_fwd(x, P + w.an2, xn, rinv, m, D);
@@ -600,7 +613,7 @@ void orc_dec_chunk(OrcDec *d, const float *P, const int *tok, int m, int start, 
     orc_rmsnorm_fwd(x, P + w.nf, xn, rinv, m, D);
     memset(logits, 0, sizeof(float) * (size_t)m * V);
     orc_mm_bt(logits, xn, P + w.emb, m, V, D);
-    float *all[] = {x, xn, q, k, v, ctx, tmp, g, u, rinv, pr};
+    float *all[] = {x, xn, q, k, v, ctx, tmp, g, u, rinv};
     for (size_t i = 0; i < sizeof all / sizeof all[0]; i++) free(all[i]);
     free(pos);
 }

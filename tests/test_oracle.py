@@ -219,3 +219,62 @@ def test_moe_oracle_against_fp64_autograd(orc):
     assert normwise_rel(dfn, x.grad.numpy()) < 1e-4
     for got, ref in zip(z, (wr.grad, w1.grad, w3.grad, w2.grad)):
         assert normwise_rel(got, ref.numpy()) < 1e-4
+
+
+# ---- the decoder's attention step against the reference's own attn_body --
+DEC_ATTN = [  # D, H, KV, T (ring), win, full_every, kvdt, steps of m rows
+    (128, 4, 2, 64, 0, 0, 0, [1] * 80),               # f32 ring, 80 single steps: wraps at 64
+    (128, 4, 2, 64, 0, 0, 1, [1] * 80),               # f16 ring
+    (384, 12, 3, 96, 0, 0, 1, [16, 1, 1, 7, 1] * 6),  # m8 heads, chunks and steps, wraps
+    (128, 4, 1, 64, 24, 0, 1, [5] + [1] * 70),        # sliding window of 24 (cfg_lwin)
+    (128, 4, 1, 64, 24, 2, 0, [3] + [1] * 40),        # window on odd layers only (full_every 2), f32
+]
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(os.path.dirname(__file__), "..", "oracle", "_ref",
+                                                    "libtlref_dec.so")),
+                    reason="oracle/_ref not built (needs /root/reference)")
+@pytest.mark.parametrize("D,H,KV,T,win,full_every,kvdt,steps", DEC_ATTN,
+                         ids=["f32", "f16", "m8_chunks", "window", "window_every2"])
+def test_decode_attention_matches_reference(D, H, KV, T, win, full_every, kvdt, steps):
+    """orc_dec_attn, the attention of the oracle Decoder (ring store, window,
+    scores, fast_expf, normalise, weighted V sum), against the reference's
+    kv_store + attn_body on the same q / k / v streams -- on both ring types,
+    through ring wrap, with chunks and single steps, and with the sliding
+    window on every layer or on alternate ones (layers 0 and 1).
+
+    Bar: within 1e-6 of the reference, not bit for bit: the reference builds
+    its scalar dot (dot_f, the f32 ring) and its softmax sum with
+    -O3 -ffast-math, so gcc reassociates them into vector reductions (1-3 ulp
+    here).  The pieces whose rounding matters more are pinned bit for bit on
+    their own (f2h / h2f / fast_expf against the reference's, above); a wrong
+    ring type, slot, window bound or scale moves ctx by 1e-3 or more, and a
+    planted f32 ring in place of f16 is checked to fail this bar below."""
+    from oracle import DecAttn
+    L = 2
+    orc = DecAttn("oracle", D, H, KV, T, L, win, full_every, kvdt)
+    ref = DecAttn("reference", D, H, KV, T, L, win, full_every, kvdt)
+    r = np.random.default_rng(D + T + win + kvdt)
+    KD = orc.KD
+    pos = 0
+    for m in steps:
+        for l in range(L):
+            q = r.standard_normal((m, D)).astype(np.float32)
+            k = r.standard_normal((m, KD)).astype(np.float32)
+            v = r.standard_normal((m, KD)).astype(np.float32)
+            a, b = orc.attn(l, q, k, v, pos), ref.attn(l, q, k, v, pos)
+            assert np.abs(a - b).max() <= 1e-6 * (1.0 + np.abs(b).max()), (pos, m, l, float(np.abs(a - b).max()))
+        pos += m
+    if kvdt == 1:
+        # the bar has teeth: the oracle with an f32 ring against the reference's f16 ring
+        wrong = DecAttn("oracle", D, H, KV, T, L, win, full_every, 0)
+        ref2 = DecAttn("reference", D, H, KV, T, L, win, full_every, 1)
+        pos, worst = 0, 0.0
+        for m in steps[:4]:
+            q = r.standard_normal((m, D)).astype(np.float32)
+            k = r.standard_normal((m, KD)).astype(np.float32)
+            v = r.standard_normal((m, KD)).astype(np.float32)
+            a, b = wrong.attn(0, q, k, v, pos), ref2.attn(0, q, k, v, pos)
+            worst = max(worst, float(np.abs(a - b).max() / (1.0 + np.abs(b).max())))
+            pos += m
+        assert worst > 1e-5, worst
