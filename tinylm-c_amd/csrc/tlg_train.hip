@@ -674,17 +674,12 @@ __device__ __forceinline__ float at_rot_1(float x, int t, int lane, const float 
 // (most queries) first.  Its eight waves share the (head, query block) pairs
 // that see the block; each accumulates dV = P^T dO and dK = dS^T Q for its
 // pairs, and the partials are summed in wave order through LDS.
-// With ROPE, q is already rotated (the dQ kernel's copy) and k is taken
-// before rope_apply and rotated on load; dK is rotated back before it is
-// stored.
 #define AT_KW 8
-template <bool ROPE>
 __global__ __launch_bounds__(512) void k_attn_bwd_dkv(const float *__restrict__ q, const float *__restrict__ k,
                                                       const float *__restrict__ v, const float *__restrict__ dout,
                                                       const float *__restrict__ lse, const float *__restrict__ Dq,
                                                       float *__restrict__ dk, float *__restrict__ dv, int B, int T,
-                                                      int H, int KV, int win, float scale,
-                                                      const float *__restrict__ cs, const float *__restrict__ sn)
+                                                      int H, int KV, int win, float scale)
 {
     __shared__ float red[AT_KW - 1][2][16][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -701,7 +696,6 @@ __global__ __launch_bounds__(512) void k_attn_bwd_dkv(const float *__restrict__ 
     float kv[16], vv[16];
     ld16(k + koff, sok, kv);
     ld16(v + koff, sok, vv);
-    if (ROPE) at_rot_a(kv, sok ? sl : T - 1, lane, cs, sn);
     int qb_last = nkb - 1;
     if (win > 0) qb_last = min(qb_last, (s0 + 31 + win - 1) >> 5);
     const int npairs = G * (qb_last - kb + 1);
@@ -785,7 +779,6 @@ __global__ __launch_bounds__(512) void k_attn_bwd_dkv(const float *__restrict__ 
             c += red[w][1][r][lane];
         }
         const int s = s0 + at_row(r, lane);
-        if (ROPE) a = at_rot_1(a, min(s, T - 1), lane, cs, sn, true);
         if (s < T) {
             const size_t off = (size_t)(b * T + s) * KD + kvh * AT_HD + lq;
             dk[off] = a;
@@ -805,9 +798,8 @@ __global__ __launch_bounds__(512) void k_attn_bwd_dkv(const float *__restrict__ 
 // phase, so one's softmax overlaps the others' MFMAs); the key splits of
 // each head merge through LDS in fixed order.  With ROPE the kernels take q
 // and k before rope_apply (tinylm.c:621-651) and rotate them while staging
-// -- pair (x[i], x[i + 16]) of a head by the row's position -- so rotated
-// copies reach HBM only where asked for (the dQ kernel's qrot, which the
-// dK / dV kernel reads); dQ is rotated back before it is stored.
+// -- pair (x[i], x[i + 16]) of a head by the row's position -- so no rotated
+// copy reaches HBM; dQ is rotated back before it is stored.
 #define A4_LD 36        // LDS row stride of a staged 32 x 32 block (16-byte rows)
 #define A4_CH 8         // key blocks staged at once (K + V: 72 KB)
 #define A4_KS 2         // key splits per head: 4 heads x 2 splits = 8 waves (4 measured slower)
@@ -891,11 +883,10 @@ __device__ __forceinline__ void a4_stage_kv(float *Ks, float *Vs, const float *k
 }
 
 // Q of the group's 4 heads for query block qb into Qs[4][32][A4_LD]
-// (rotated with ROPE), one task per thread; qrot (optional) receives the
-// rotated rows in q's layout.
+// (rotated with ROPE), one task per thread.
 template <bool ROPE>
 __device__ __forceinline__ void a4_stage_q(float *Qs, const float *q, int b, int h0, int qb, int T, int H,
-                                           const float *cs, const float *sn, float *qrot)
+                                           const float *cs, const float *sn)
 {
     const int tid = threadIdx.x, hs = tid >> 7, x = (tid & 127) >> 2, c4 = tid & 3;
     const int qr = qb * 32 + x, qc = min(qr, T - 1);
@@ -904,10 +895,6 @@ __device__ __forceinline__ void a4_stage_q(float *Qs, const float *q, int b, int
     tq.load(q + off, c4, qc, true, cs, sn);
     tq.rotate(true);
     tq.store(Qs + (hs * 32 + x) * A4_LD, c4, qr < T);
-    if (qrot && qr < T) {
-        *reinterpret_cast<f32x4 *>(qrot + off + 4 * c4) = tq.a;
-        *reinterpret_cast<f32x4 *>(qrot + off + 16 + 4 * c4) = tq.b;
-    }
 }
 
 // 16 floats of row `row` of a staged block from column 16 * half (the MFMA
@@ -942,7 +929,7 @@ __global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_fwd4(const float *__res
     const int qi = qb * 32 + lq;
     const int kb0 = at_kb0(qb, win);
 
-    if (tid < 512) a4_stage_q<ROPE>(Qs, q, b, h0, qb, T, H, cs, sn, nullptr);
+    if (tid < 512) a4_stage_q<ROPE>(Qs, q, b, h0, qb, T, H, cs, sn);
     const float c2 = scale * 1.44269504088896341f;
     float qv[16];
     f32x16 o;
@@ -1049,7 +1036,7 @@ __global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_fwd4(const float *__res
 }
 
 // dQ for the same items; also writes Dq = dO . O per (row, head) for the
-// dK / dV kernel, and with ROPE the rotated q rows to qrot for it.
+// dK / dV kernel.
 // dS = P (dP - Dq) scale, dQ = dS K (attn_bwd, :750-768).
 template <bool ROPE>
 __global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_dq4(const float *__restrict__ q, const float *__restrict__ k,
@@ -1057,7 +1044,7 @@ __global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_dq4(const float *__rest
                                                   const float *__restrict__ dout, const float *__restrict__ lse,
                                                   float *__restrict__ Dq, float *__restrict__ dq, int B, int T, int H,
                                                   int KV, int win, float scale, const float *__restrict__ cs,
-                                                  const float *__restrict__ sn, float *__restrict__ qrot)
+                                                  const float *__restrict__ sn)
 {
     // K and V staging in one array: its whole extent is the merge area later
     __shared__ __attribute__((aligned(16))) float KVs[2 * A4_CH * 32 * A4_LD], Qs[4 * 32 * A4_LD];
@@ -1079,7 +1066,7 @@ __global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_dq4(const float *__rest
     ld16(o + qoff, qok, ov);
     const size_t rh = (size_t)(b * T + (qok ? qi : T - 1)) * H + h;
     const float lsv = lse[rh];
-    if (tid < 512) a4_stage_q<ROPE>(Qs, q, b, h0, qb, T, H, cs, sn, ROPE ? qrot : nullptr);
+    if (tid < 512) a4_stage_q<ROPE>(Qs, q, b, h0, qb, T, H, cs, sn);
     float dd = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; i++) dd += dov[i] * ov[i];
@@ -1161,6 +1148,172 @@ __global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_dq4(const float *__rest
     for (int g4 = 0; g4 < 4; g4++)
         *reinterpret_cast<f32x4 *>(orow + 8 * g4 + 4 * hh) =
             f32x4{acc[4 * g4], acc[4 * g4 + 1], acc[4 * g4 + 2], acc[4 * g4 + 3]};
+}
+
+// dK / dV for H / KV a multiple of 4.  One workgroup of 8 waves per (b, KV
+// head, 32-key block), first key blocks first.  Per step the workgroup
+// stages two query blocks of one group of 4 heads in LDS -- q (rotated with
+// ROPE), dO, and the rows' lse and Dq, loaded as whole rows -- with the next
+// step's loads in flight during this step's MFMAs; wave w takes head w % 4
+// and query block w / 4 of the pair.  Its dV = P^T dO and dK = dS^T Q sum
+// over its pairs in registers, the 8 waves' sums add in wave order through
+// LDS (so every head of the KV group and every query block is summed in a
+// fixed order), and dK is rotated back before it is stored.
+#define A4_DKV_ST (2 * 4 * 32 * A4_LD)          // one staged array: 2 query blocks x 4 heads x 32 rows
+
+template <bool ROPE>
+struct Dkv4Stage {
+    A4Task<ROPE> tq[2];       // q rows, query block 0 / 1 of the pair
+    f32x4 da[2][2];           // dO rows (the two halves of the head row)
+    f32x4 ld;                 // lse or Dq of one row, 4 heads
+    bool okq[2], okl;
+
+    // thread task: (head hs, row x, c4) of both query blocks; threads < 128
+    // also one lse / Dq float4 (query block tid >> 6, lse or Dq, row)
+    __device__ __forceinline__ void load(const float *q, const float *dout, const float *lse, const float *Dq,
+                                         int b, int h0, int T, int H, int qb0, int qb_last, const float *cs,
+                                         const float *sn)
+    {
+        const int tid = threadIdx.x, hs = tid >> 7, x = (tid & 127) >> 2, c4 = tid & 3;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int qb = min(qb0 + u, qb_last), qr = qb * 32 + x, qc = min(qr, T - 1);
+            okq[u] = qr < T && qb0 + u <= qb_last;
+            const size_t off = (size_t)(b * T + qc) * (H * AT_HD) + (h0 + hs) * AT_HD;
+            tq[u].load(q + off, c4, qc, true, cs, sn);
+            da[u][0] = *reinterpret_cast<const f32x4 *>(dout + off + 4 * c4);
+            da[u][1] = *reinterpret_cast<const f32x4 *>(dout + off + 16 + 4 * c4);
+        }
+        const int u = (tid >> 6) & 1, isd = (tid >> 5) & 1, xr = tid & 31;
+        const int qb = min(qb0 + u, qb_last), qr = qb * 32 + xr, qc = min(qr, T - 1);
+        okl = qr < T && qb0 + u <= qb_last;
+        ld = *reinterpret_cast<const f32x4 *>((isd ? Dq : lse) + (size_t)(b * T + qc) * H + h0);
+    }
+    __device__ __forceinline__ void store(float *Qs, float *Ds, float *LDs)
+    {
+        const int tid = threadIdx.x, hs = tid >> 7, x = (tid & 127) >> 2, c4 = tid & 3;
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int row = ((u * 4 + hs) * 32 + x) * A4_LD;
+            tq[u].rotate(true);
+            tq[u].store(Qs + row, c4, okq[u]);
+            *reinterpret_cast<f32x4 *>(Ds + row + 4 * c4) = okq[u] ? da[u][0] : z;
+            *reinterpret_cast<f32x4 *>(Ds + row + 16 + 4 * c4) = okq[u] ? da[u][1] : z;
+        }
+        if (tid < 128) {
+            const int u = (tid >> 6) & 1, isd = (tid >> 5) & 1, xr = tid & 31;
+            *reinterpret_cast<f32x4 *>(LDs + ((isd * 2 + u) * 32 + xr) * 4) = okl ? ld : z;
+        }
+    }
+};
+
+template <bool ROPE>
+__global__ __launch_bounds__(512) void k_attn_dkv4(const float *__restrict__ q, const float *__restrict__ k,
+                                                   const float *__restrict__ v, const float *__restrict__ dout,
+                                                   const float *__restrict__ lse, const float *__restrict__ Dq,
+                                                   float *__restrict__ dk, float *__restrict__ dv, int B, int T,
+                                                   int H, int KV, int win, float scale,
+                                                   const float *__restrict__ cs, const float *__restrict__ sn)
+{
+    // staged q, dO (2 query blocks x 4 heads) and lse / Dq; the wave sums at the end reuse it
+    __shared__ __attribute__((aligned(16))) float Sm[2 * A4_DKV_ST + 2 * 2 * 32 * 4];
+    static_assert(2 * A4_DKV_ST >= 7 * 2 * 16 * 64, "wave sums fit the staging area");
+    float *Qs = Sm, *Ds = Sm + A4_DKV_ST, *LDs = Sm + 2 * A4_DKV_ST;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hs = wave & 3, qs = wave >> 2;
+    const int nkb = (T + 31) >> 5;
+    const int item = blockIdx.x;
+    const int kb = item / (B * KV), bkv = item % (B * KV);
+    const int b = bkv / KV, kvh = bkv % KV, G = H / KV, HG = G / 4;
+    const int KD = KV * AT_HD;
+    const int lq = lane & 31, hh = lane >> 5;
+    const int s0 = kb * 32, sl = s0 + lq;
+    const bool sok = sl < T;
+    int qb_last = nkb - 1;
+    if (win > 0) qb_last = min(qb_last, (s0 + 31 + win - 1) >> 5);
+    const int nch = (qb_last - kb + 2) >> 1, nsteps = HG * nch;
+
+    Dkv4Stage<ROPE> stg;
+    stg.load(q, dout, lse, Dq, b, kvh * G, T, H, kb, qb_last, cs, sn);
+    const size_t koff = (size_t)(b * T + (sok ? sl : T - 1)) * KD + kvh * AT_HD + 16 * hh;
+    float kv[16], vv[16];
+    ld16(k + koff, sok, kv);
+    ld16(v + koff, sok, vv);
+    if (ROPE) at_rot_a(kv, sok ? sl : T - 1, lane, cs, sn);
+    const float c2 = scale * 1.44269504088896341f;
+    f32x16 ak, av;
+#pragma unroll
+    for (int r = 0; r < 16; r++) { ak[r] = 0.f; av[r] = 0.f; }
+    for (int st = 0; st < nsteps; st++) {
+        const int qb = kb + 2 * (st % nch) + qs;
+        stg.store(Qs, Ds, LDs);
+        __syncthreads();
+        {   // the next step's rows in flight (the last step re-reads its own)
+            const int nx = min(st + 1, nsteps - 1);
+            stg.load(q, dout, lse, Dq, b, kvh * G + (nx / nch) * 4, T, H, kb + 2 * (nx % nch), qb_last, cs, sn);
+        }
+        if (qb <= qb_last) {
+            const float *Qw = Qs + (qs * 4 + hs) * 32 * A4_LD, *Dw = Ds + (qs * 4 + hs) * 32 * A4_LD;
+            const float *Lw = LDs + qs * 32 * 4, *Pw = LDs + (2 + qs) * 32 * 4;
+            float qa[16], da[16];
+            a4_frag(Qw, lq, hh, qa);
+            a4_frag(Dw, lq, hh, da);
+            f32x16 sc, dp;
+#pragma unroll
+            for (int r = 0; r < 16; r++) { sc[r] = 0.f; dp[r] = 0.f; }
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                sc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[i], kv[i], sc, 0, 0, 0);
+                dp = __builtin_amdgcn_mfma_f32_32x32x2f32(da[i], vv[i], dp, 0, 0, 0);
+            }
+            // sc[r] = S[qb * 32 + at_row(r)][sl], dp likewise
+            const bool full = at_full(kb, qb, win);
+            float pp[16], ds[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int x = at_row(r, lane);
+                const float lr = Lw[x * 4 + hs], dr = Pw[x * 4 + hs];
+                const bool vis = full || at_visible(sl, qb * 32 + x, T, win);
+                const float p = __builtin_amdgcn_exp2f(sc[r] * c2 - lr);
+                pp[r] = vis ? p : 0.f;
+                ds[r] = vis ? p * (dp[r] - dr) * scale : 0.f;
+            }
+            // dV[s][d] += sum_q P[q][s] dO[q][d];  dK[s][d] += sum_q dS[q][s] Q[q][d]
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int x = at_row(r, lane);
+                av = __builtin_amdgcn_mfma_f32_32x32x2f32(pp[r], Dw[x * A4_LD + lq], av, 0, 0, 0);
+                ak = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[r], Qw[x * A4_LD + lq], ak, 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+    // the 8 waves' sums, in wave order
+    float *red = Sm;
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            red[(((wave - 1) * 2 + 0) * 16 + r) * 64 + lane] = ak[r];
+            red[(((wave - 1) * 2 + 1) * 16 + r) * 64 + lane] = av[r];
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        float a = ak[r], c = av[r];
+        for (int w = 0; w < 7; w++) {
+            a += red[((w * 2 + 0) * 16 + r) * 64 + lane];
+            c += red[((w * 2 + 1) * 16 + r) * 64 + lane];
+        }
+        const int s = s0 + at_row(r, lane);
+        if (ROPE) a = at_rot_1(a, min(s, T - 1), lane, cs, sn, true);
+        if (s < T) {
+            const size_t off = (size_t)(b * T + s) * KD + kvh * AT_HD + lq;
+            dk[off] = a;
+            dv[off] = c;
+        }
+    }
 }
 
 // ----------------------------------------------------------- elementwise --
@@ -1500,32 +1653,36 @@ static int attn_bwd_launch(const float *q, const float *k, const float *v, const
     if (cs && (!g4 || !al16(cs) || !al16(sn)))
         return tlg_fail(TLG_EINVAL, "attn_bwd_rope: needs H / KV a multiple of 4 and 16-byte aligned tables");
     if (B == 0 || T == 0) return TLG_OK;
-    // workspace: Dq [B*T][H], and with rope tables the rotated q [B*T][H*hd]
+    // workspace: Dq [B*T][H]
     void *ws;
-    const size_t nDq = ((size_t)B * T * H + 63) & ~(size_t)63;
-    if ((rc = tr_scratch((nDq + (cs ? (size_t)B * T * H * hd : 0)) * 4, &ws))) return rc;
+    if ((rc = tr_scratch((size_t)B * T * H * 4, &ws))) return rc;
     const float scale = 1.0f / sqrtf((float)hd);
     const int nqb = (T + 31) / 32;
     hipStream_t st = ST(stream);
-    float *Dq = (float *)ws, *qrot = Dq + nDq;
+    float *Dq = (float *)ws;
     if (g4) {
         const dim3 grid(B * KV * (H / KV / 4) * nqb);
         if (cs)
             hipLaunchKernelGGL(k_attn_dq4<true>, grid, dim3(256 * A4_KS), 0, st, q, k, v, out, datt, lse, Dq, dq, B, T, H, KV,
-                               win, scale, cs, sn, qrot);
+                               win, scale, cs, sn);
         else
             hipLaunchKernelGGL(k_attn_dq4<false>, grid, dim3(256 * A4_KS), 0, st, q, k, v, out, datt, lse, Dq, dq, B, T, H,
-                               KV, win, scale, nullptr, nullptr, nullptr);
+                               KV, win, scale, nullptr, nullptr);
     } else {
         hipLaunchKernelGGL(k_attn_bwd_dq, dim3(B * H * nqb), dim3(64 * AT_W), 0, st, q, k, v, out, datt, lse, Dq, dq,
                            B, T, H, KV, win, scale);
     }
-    if (cs)
-        hipLaunchKernelGGL(k_attn_bwd_dkv<true>, dim3(nqb * B * KV), dim3(64 * AT_KW), 0, st, (const float *)qrot, k,
-                           v, datt, lse, (const float *)Dq, dk, dv, B, T, H, KV, win, scale, cs, sn);
-    else
-        hipLaunchKernelGGL(k_attn_bwd_dkv<false>, dim3(nqb * B * KV), dim3(64 * AT_KW), 0, st, q, k, v, datt, lse,
+    // the group dK / dV kernel reads lse rows as float4 (4 heads)
+    if (g4 && cs && !al16(lse)) return tlg_fail(TLG_EINVAL, "attn_bwd_rope: lse must be 16-byte aligned");
+    if (g4 && cs)
+        hipLaunchKernelGGL(k_attn_dkv4<true>, dim3(nqb * B * KV), dim3(512), 0, st, q, k, v, datt, lse,
+                           (const float *)Dq, dk, dv, B, T, H, KV, win, scale, cs, sn);
+    else if (g4 && al16(lse))
+        hipLaunchKernelGGL(k_attn_dkv4<false>, dim3(nqb * B * KV), dim3(512), 0, st, q, k, v, datt, lse,
                            (const float *)Dq, dk, dv, B, T, H, KV, win, scale, nullptr, nullptr);
+    else
+        hipLaunchKernelGGL(k_attn_bwd_dkv, dim3(nqb * B * KV), dim3(64 * AT_KW), 0, st, q, k, v, datt, lse,
+                           (const float *)Dq, dk, dv, B, T, H, KV, win, scale);
     LAUNCH_CHECK();
     return TLG_OK;
 }
