@@ -520,7 +520,7 @@ def bench_full_step(lib, host, stream, name, steps, warmup=3, eager=False):
 DECODE_MODEL = dict(V=2048, D=384, L=8, H=12, KV=3, F=1024, T=256)
 
 
-def bench_decode_step(lib, host, stream, steps, pool=6, prompt_len=16, warmup=8, fused=1):
+def bench_decode_step(lib, host, stream, steps, pool=6, prompt_len=16, warmup=8, fused=1, eager=False):
     """The whole decode step on the device (host/tl_decode.h): greedy
     single-token steps of the m8 model through a 256-position f16 KV ring
     with the reference's fast_expf (its decode defaults), token and position
@@ -538,17 +538,26 @@ def bench_decode_step(lib, host, stream, steps, pool=6, prompt_len=16, warmup=8,
     t0 = time.perf_counter()
     dec.prime(prompt, stream)
     prefill_ms = (time.perf_counter() - t0) * 1e3
-    dec.graph_build(stream)
+    if eager:                       # launch by launch (profilers trace these), copies rotating
+        cnt = [0]
+
+        def step():
+            cnt[0] += 1
+            return dec.greedy_step(stream, (cnt[0] - 1) % pool)
+    else:
+        dec.graph_build(stream)
+        step = lambda: dec.graph_step(stream)  # noqa: E731
     for _ in range(warmup):
-        dec.graph_step(stream)
+        step()
     check(lib.tlg_stream_sync(stream), "sync")
-    ms, _ = time_steps(lib, lambda: dec.graph_step(stream), stream, steps)
+    ms, _ = time_steps(lib, step, stream, steps)
     state = dec.state(stream)
     per = ms / steps
     return {"model": DECODE_MODEL, "kv_cache": "f16 ring, 256 positions", "exp": "fast_expf",
             "weights_pool": pool, "steps": steps, "ms_per_token": round(per, 4),
             "tok_s": round(1e3 / per, 1), "prefill_ms_host_timed": round(prefill_ms, 3),
             "final_position": state[0], "fused": bool(fused),
+            "launch": "enqueued step by step" if eager else "one HIP graph per step",
             "launches_per_token": 1 + 8 * 5 + 2 if fused else 1 + 8 * 13 + 3}
 
 
@@ -703,6 +712,8 @@ def main():
                     help="timed whole training steps (forward + backward + AdamW on the device); 0 skips")
     ap.add_argument("--full-eager", action="store_true",
                     help="enqueue the whole training step launch by launch instead of replaying its graph")
+    ap.add_argument("--decode-eager", action="store_true",
+                    help="enqueue the decode step launch by launch instead of replaying its graphs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
@@ -805,12 +816,13 @@ def main():
     dec_full = None
     if args.decode_full_steps > 0:
         if args.decode_mode == "unfused":
-            dec_full = bench_decode_step(lib, host, stream, args.decode_full_steps, fused=0)
+            dec_full = bench_decode_step(lib, host, stream, args.decode_full_steps, fused=0, eager=args.decode_eager)
         else:
-            dec_full = bench_decode_step(lib, host, stream, args.decode_full_steps)
+            dec_full = bench_decode_step(lib, host, stream, args.decode_full_steps, eager=args.decode_eager)
         log(f"[decode step] {dec_full}")
         if args.decode_mode == "both":
-            dec_full["unfused"] = bench_decode_step(lib, host, stream, min(args.decode_full_steps, 128), fused=0)
+            dec_full["unfused"] = bench_decode_step(lib, host, stream, min(args.decode_full_steps, 128), fused=0,
+                                                    eager=args.decode_eager)
             log(f"[decode step, unfused] {dec_full['unfused']}")
     dec_persist = None
     if args.decode_persist_steps > 0:
