@@ -101,7 +101,10 @@ int tlg_dev_dec_argmax(const float *logits, int V, int m, int *state, int *tok, 
  * the last step's logits row and toks_out[i] (if not NULL) = the token that
  * step i chose.  Arithmetic: the reference's formulas (RMSNorm, RoPE,
  * fast_expf or expf, SwiGLU, f16 or f32 ring elements), with fp32 sums in a
- * fixed order that differs from the reference's sequential one.
+ * fixed order that differs from the reference's sequential one.  `exact`
+ * selects expf for the attention exponentials only: SwiGLU's silu, the
+ * softmax normalisation and RMSNorm's 1/sqrt use the hardware exp2,
+ * reciprocal and rsqrt either way (within the fp32 bar, not bit for bit).
  *
  * xbuf is an exchange area of tlg_dec_persist_xbytes() bytes that must be
  * zero before the first launch and after every reset of state[3] (the
