@@ -479,7 +479,7 @@ def model_of(name):
                 n_mtp=cfg["n_mtp"]), cfg["R"] // 256
 
 
-def bench_full_step(lib, host, stream, name, steps, warmup=3, eager=False):
+def bench_full_step(lib, host, stream, name, steps, warmup=3, eager=False, tune=True):
     """The whole training step on the device (host/tl_train.h): forward,
     backward with the MTP heads, gradnorm and AdamW -- tinylm.c's
     train_loop body (:2627-2633), every activation resident in HBM --
@@ -497,6 +497,9 @@ def bench_full_step(lib, host, stream, name, steps, warmup=3, eager=False):
     tr.set_hyper(3e-4, 0.9, 0.95, 0.1, 1, stream)
     tr.step(stream)                                   # sizes every scratch buffer
     loss0 = tr.loss(stream)
+    # per grouped launch, the fastest tile configuration (forward + backward
+    # passes only: the parameters stay as the first step left them)
+    tiles = tr.autotune(list(AUTOTUNE_CANDS), 3, stream) if tune else None
     phases = tr.time_phases(stream)
     if eager:                                       # kernel by kernel (profilers trace these)
         run = lambda: tr.step(stream)  # noqa: E731
@@ -514,7 +517,9 @@ def bench_full_step(lib, host, stream, name, steps, warmup=3, eager=False):
             "phases_ms_eager": {"forward": round(phases[0], 4), "backward": round(phases[1], 4),
                                 "gradnorm_adamw": round(phases[2], 4)},
             "loss_first": round(loss0, 4), "loss_after": round(loss1, 4),
-            "launch": "enqueued step by step" if eager else "one HIP graph per step"}
+            "launch": "enqueued step by step" if eager else "one HIP graph per step",
+            "tiles": ("per grouped launch, tl_train_autotune over " + str(list(AUTOTUNE_CANDS)) + ": "
+                      + str(tiles)) if tune else "the library's automatic policy"}
 
 
 DECODE_MODEL = dict(V=2048, D=384, L=8, H=12, KV=3, F=1024, T=256)
@@ -810,7 +815,8 @@ def main():
         log(f"[moe] {moe}")
     full = None
     if args.full_steps > 0:
-        full = bench_full_step(lib, host, stream, args.config, args.full_steps, eager=args.full_eager)
+        full = bench_full_step(lib, host, stream, args.config, args.full_steps, eager=args.full_eager,
+                               tune=not args.no_autotune)
         full["gemm_set_share"] = round(ms_step / full["ms_per_step"], 4)
         log(f"[full step] {full}")
     dec_full = None

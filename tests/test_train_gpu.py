@@ -462,3 +462,50 @@ def test_graph_replays_match_eager(lib, st):
         assert l == eager_l, rep
         assert np.array_equal(P, eager_P), rep
     assert eager_l[2] < eager_l[0]                # AdamW steps lower the loss on a fixed batch
+
+
+def test_autotuned_step_matches_and_replays(lib, st):
+    """tl_train_autotune pins a tile configuration per grouped launch: the
+    parameters are left as they were, a step with the table gives the
+    untuned step's loss and gradients within the bar (only the tile shapes
+    change), and the graph captured after it replays the eager tuned step
+    bit for bit."""
+    import tlgemm
+    kw, B = dict(V=256, D=128, L=2, H=4, KV=1, F=192, T=64, n_mtp=1), 4
+    m = model(**kw)
+    P0 = st.init_params(m, 5)
+    r = np.random.default_rng(11)
+    N = B * m.T
+    tok, tgt = (r.integers(0, m.V, N).astype(np.int32) for _ in range(2))
+    tm = r.integers(0, m.V, (1, N)).astype(np.int32)
+    s = lib.tlg_stream_create()
+
+    def fetch(tr, which):
+        X = np.empty_like(P0)
+        lib.check(lib.tlg_memcpy_d2h(X.ctypes.data, tr.buf(which), X.nbytes, s), "d2h")
+        lib.check(lib.tlg_stream_sync(s), "sync")
+        return X
+
+    def one_step(tr, graph=False):
+        tr.upload(P0, s)
+        tr.set_batch(tok, tgt, tm, s)
+        tr.set_hyper(1e-3, 0.9, 0.95, 0.1, 1, s)
+        if graph:
+            tr.graph_step(s)
+        else:
+            tr.step(s)
+        return tr.loss(s), fetch(tr, 1)            # loss and the step's gradients
+
+    l0, G_auto = one_step(tlgemm.host().train(kw, B))
+    tuned = tlgemm.host().train(kw, B)
+    one_step(tuned)                                  # sizes the scratch
+    tuned.upload(P0, s)
+    tiles = tuned.autotune([3, 14, 15, 20], 1, s)
+    assert tiles and all(c in (3, 14, 15, 20) for c in tiles), tiles
+    assert np.array_equal(fetch(tuned, 0), P0)      # autotuning does not step the model
+    l1, G_tuned = one_step(tuned)
+    assert abs(l1 - l0) <= 1e-5 * abs(l0)
+    assert normwise_rel(G_tuned, G_auto) <= TOL
+    tuned.graph_build(s)
+    l2, G_graph = one_step(tuned, graph=True)
+    assert l2 == l1 and np.array_equal(G_graph, G_tuned)

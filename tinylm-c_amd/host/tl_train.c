@@ -35,6 +35,11 @@ struct TlTrain {
     float *x_final, *fn, *fn_rinv, *logits, *dl, *dout, *dfnorm, *dfin, *datt, *dq, *dk, *dv, *dnorm, *dain, *dfn;
     float hyper_host[8];
     void *graph;
+    /* per grouped GEMM launch of a step, in call order: tile configuration + 1
+     * (0 = the library's automatic policy); tl_train_autotune fills it */
+    int gi, lcfg[TL_TRAIN_MAXG];
+    void **tev;                         /* timing events (autotune only): 2 per launch */
+    int tcap;
 };
 
 /* map_weights (tinylm.c:361-393) without QK-norm: emb | per layer an1 wq wk
@@ -261,8 +266,26 @@ static TlgGemmCall BTN(float *dX, int beta, int M, int K, int n, const float *co
 }
 
 #define CK(x) do { int rc_ = (x); if (rc_) return rc_; } while (0)
+
+/* One grouped GEMM launch, the step's k-th: pinned to its tile configuration
+ * when the step has a table, bracketed by events while autotuning. */
+static int group(TlTrain *t, const TlgGemmCall *cs, int n, void *st)
+{
+    const int k = t->gi++;
+    const int cfg = k < TL_TRAIN_MAXG ? t->lcfg[k] : 0;
+    const int timed = t->tev && k < t->tcap;
+    int rc = cfg > 0 ? tlg_tune_group(cfg - 1) : 0;
+    if (!rc && timed) rc = tlg_event_record(t->tev[2 * k], st);
+    if (!rc) rc = tlg_dev_gemm_group(cs, n, st);
+    if (!rc && timed) rc = tlg_event_record(t->tev[2 * k + 1], st);
+    if (cfg > 0) {
+        const int r2 = tlg_tune_group(-1);
+        if (!rc) rc = r2;
+    }
+    return rc;
+}
 #define GROUP(st, ...) do { TlgGemmCall cs_[] = {__VA_ARGS__}; \
-        CK(tlg_dev_gemm_group(cs_, (int)(sizeof cs_ / sizeof cs_[0]), st)); } while (0)
+        CK(group(t, cs_, (int)(sizeof cs_ / sizeof cs_[0]), st)); } while (0)
 
 /* rope_apply runs inside the attention kernels when the GQA-group kernels
  * take the model (H / KV a multiple of 4); else as its own pass. */
@@ -277,6 +300,7 @@ int tl_train_forward(TlTrain *t, void *st)
     const float *P = t->P;
     Map w;
     wmap(t, 0, &w);
+    t->gi = 0;                                   /* the step's first grouped launch */
     CK(tlg_dev_embed_fwd(t->a_in, P + w.emb, t->tok, N, D, V, st));
     for (int l = 0; l < m->L; l++) {
         wmap(t, l, &w);
@@ -417,6 +441,66 @@ int tl_train_graph_step(TlTrain *t, void *st)
 {
     if (!t->graph) return TLG_EINVAL;
     return tlg_graph_launch(t->graph, st);
+}
+
+/* Per grouped launch, the fastest of `cands` over `reps` timed forward +
+ * backward passes (P, M and V are not touched; G and the activations are). */
+int tl_train_autotune(TlTrain *t, const int *cands, int ncands, int reps, void *st)
+{
+    if (!t || !cands || ncands <= 0 || reps <= 0) return TLG_EINVAL;
+    for (int c = 0; c < ncands; c++)
+        if (cands[c] < 0) return TLG_EINVAL;
+    memset(t->lcfg, 0, sizeof t->lcfg);
+    CK(tl_train_forward(t, st));                  /* counts the launches, sizes the scratch */
+    CK(tl_train_backward(t, st));
+    const int ng = t->gi;
+    if (ng <= 0 || ng > TL_TRAIN_MAXG) return TLG_EINVAL;
+    void **ev = calloc((size_t)2 * ng, sizeof(void *));
+    double *best = malloc(sizeof(double) * (size_t)ng), *acc = malloc(sizeof(double) * (size_t)ng);
+    int *pick = calloc((size_t)ng, sizeof(int));
+    int rc = (!ev || !best || !acc || !pick) ? TLG_ENOMEM : 0;
+    for (int i = 0; !rc && i < 2 * ng; i++)
+        if (!(ev[i] = tlg_event_create())) rc = TLG_EHIP;
+    for (int k = 0; k < ng && best; k++) best[k] = 1e30;
+    for (int c = 0; !rc && c < ncands; c++) {
+        for (int k = 0; k < ng; k++) t->lcfg[k] = cands[c] + 1;
+        t->tev = NULL;
+        rc = tl_train_forward(t, st);            /* warm this shape up */
+        if (!rc) rc = tl_train_backward(t, st);
+        for (int k = 0; k < ng; k++) acc[k] = 0.0;
+        t->tev = ev;
+        t->tcap = ng;
+        for (int r = 0; !rc && r < reps; r++) {
+            rc = tl_train_forward(t, st);
+            if (!rc) rc = tl_train_backward(t, st);
+            if (!rc) rc = tlg_stream_sync(st);
+            for (int k = 0; !rc && k < ng; k++) {
+                const float ms = tlg_event_elapsed_ms(ev[2 * k], ev[2 * k + 1]);
+                if (ms < 0) rc = TLG_EHIP;
+                acc[k] += ms;
+            }
+        }
+        for (int k = 0; !rc && k < ng; k++)
+            if (acc[k] < best[k]) { best[k] = acc[k]; pick[k] = cands[c] + 1; }
+    }
+    t->tev = NULL;
+    t->tcap = 0;
+    if (!rc) memcpy(t->lcfg, pick, sizeof(int) * (size_t)ng);
+    else memset(t->lcfg, 0, sizeof t->lcfg);
+    for (int i = 0; ev && i < 2 * ng; i++)
+        if (ev[i]) tlg_event_destroy(ev[i]);
+    free(ev); free(best); free(acc); free(pick);
+    return rc;
+}
+
+int tl_train_tiles(const TlTrain *t, int *cfg, int cap)
+{
+    int n = 0;
+    for (int k = 0; k < TL_TRAIN_MAXG && k < cap; k++) {
+        cfg[k] = t->lcfg[k] - 1;
+        if (t->lcfg[k]) n = k + 1;
+    }
+    return n;
 }
 
 int tl_train_time_phases(TlTrain *t, float *ms, void *st)

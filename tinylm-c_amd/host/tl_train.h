@@ -69,6 +69,15 @@ int  tl_train_graph_step(TlTrain *t, void *stream);
 /* Per-phase timing of one eager step: ms[0] forward, ms[1] backward,
  * ms[2] optimizer (HIP events on `stream`). */
 int  tl_train_time_phases(TlTrain *t, float *ms, void *stream);
+/* Tile configuration of each grouped GEMM launch of the step: per launch the
+ * fastest of cands (tlg_tune_group indices) over reps timed forward + backward
+ * passes (the parameters and AdamW moments are untouched).  Later steps, and
+ * graphs built after it, launch with that table.  tl_train_tiles copies the
+ * table (cfg[k] = configuration of launch k, -1 = automatic) and returns the
+ * number of launches it covers. */
+#define TL_TRAIN_MAXG 512
+int  tl_train_autotune(TlTrain *t, const int *cands, int ncands, int reps, void *stream);
+int  tl_train_tiles(const TlTrain *t, int *cfg, int cap);
 
 #ifdef __cplusplus
 }

@@ -350,6 +350,18 @@ class Train:
         self._ck(self.host.dll.tl_train_time_phases(self.h, ms, stream), "tl_train_time_phases")
         return list(ms)
 
+    def autotune(self, cands, reps, stream):
+        """Per grouped launch of the step, the fastest tile configuration of
+        `cands` (tl_train_autotune); returns the chosen table."""
+        arr = (ctypes.c_int * len(cands))(*cands)
+        self._ck(self.host.dll.tl_train_autotune(self.h, arr, len(cands), reps, stream), "tl_train_autotune")
+        return self.tiles()
+
+    def tiles(self):
+        buf = (ctypes.c_int * 512)()
+        n = self.host.dll.tl_train_tiles(self.h, buf, 512)
+        return list(buf[:n])
+
     def __del__(self):
         try:
             if self.h:
@@ -586,6 +598,8 @@ class Host:
             getattr(d, n).argtypes = [_vp, _vp]
             getattr(d, n).restype = ctypes.c_float
         d.tl_train_time_phases.argtypes = [_vp, ctypes.POINTER(ctypes.c_float), _vp]
+        d.tl_train_autotune.argtypes = [_vp, ctypes.POINTER(ctypes.c_int), _i, _i, _vp]
+        d.tl_train_tiles.argtypes = [_vp, ctypes.POINTER(ctypes.c_int), _i]
         # host/tl_decode.h
         d.tl_decode_new.argtypes = [ctypes.POINTER(TlModel), _i, _i, _i, _i, _i, _i]
         d.tl_decode_new.restype = _vp
