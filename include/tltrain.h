@@ -41,6 +41,20 @@ int tlg_dev_rmsnorm_fwd(const float *x, const float *g, float *out, float *rinv,
 int tlg_dev_rmsnorm_bwd(const float *x, const float *g, const float *rinv, const float *dy, const float *dx_in,
                         float *dx, float *dg, int rows, int D, void *stream);
 
+/* rmsnorm_bwd as above (tinylm.c:565-588) with the dg sum deferred: the
+ * per-row-block partials of dg go to `part` (at least ceil(rows/16) * D
+ * floats, 16-byte aligned, owned by the caller), and their fixed-order
+ * column sum into dg rides along in the next grouped GEMM or expert launch
+ * on the stream (or tlg_dev_gemm_flush), as a split GEMM's reduction does.
+ * dg is complete only after that launch; `part` must not be written before
+ * it (a later call on the same `part` flushes the earlier sum first).  No
+ * counterpart in the reference, whose rmsnorm_bwd adds into dg directly: it
+ * saves the gain-sum launch of every RMSNorm backward in a training step.
+ * The result equals tlg_dev_rmsnorm_bwd's bit for bit. */
+int tlg_dev_rmsnorm_bwd_defer(const float *x, const float *g, const float *rinv, const float *dy,
+                              const float *dx_in, float *dx, float *dg, int rows, int D, float *part,
+                              size_t part_floats, void *stream);
+
 /* rope_apply, tinylm.c:630-651, in place on [rows][nheads*hd]: row r is at
  * position pos[r] (device ints), or r % T when pos is NULL (forward's
  * pos[n] = n % T, :975).  cos_t / sin_t are rope_init's tables

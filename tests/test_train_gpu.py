@@ -83,6 +83,58 @@ def test_rmsnorm(lib, st, rows, D):
         assert normwise_rel(host(DG) - dg0, wdg - dg0) <= TOL, mode
 
 
+@pytest.mark.parametrize("rows,D", [(4096, 256), (1027, 384), (37, 48), (5, 2048)])
+def test_rmsnorm_bwd_defer(lib, rows, D):
+    """The deferred gain sum equals tlg_dev_rmsnorm_bwd's bit for bit, when it
+    rides along in the next grouped GEMM launch, when a second call on the
+    same partials flushes it first, and through tlg_dev_gemm_flush."""
+    print("rmsnorm_bwd_defer", rows, D, flush=True)
+    t = _t()
+    r = np.random.default_rng(7 * rows + D)
+    x = r.standard_normal((rows, D)).astype(np.float32)
+    g = (1 + 0.1 * r.standard_normal(D)).astype(np.float32)
+    rr = (1 + 0.1 * r.random(rows)).astype(np.float32)
+    dys = [(0.01 * r.standard_normal((rows, D))).astype(np.float32) for _ in range(2)]
+    base = r.standard_normal((rows, D)).astype(np.float32)
+    dg0 = (0.01 * r.standard_normal(D)).astype(np.float32)
+    X, Gn, RI, B = dev(x), dev(g), dev(rr), dev(base)
+    want = []
+    for dy in dys:
+        DX, DG = nan_like((rows, D)), dev(dg0)
+        lib.check(lib.tlg_dev_rmsnorm_bwd(X.data_ptr(), Gn.data_ptr(), RI.data_ptr(), dev(dy).data_ptr(),
+                                          B.data_ptr(), DX.data_ptr(), DG.data_ptr(), rows, D, stream()), "bwd")
+        want.append((host(DX), host(DG)))
+    nblk = (rows + 15) // 16
+    part = t.empty(nblk * D, dtype=t.float32, device="cuda")
+    # a GEMM to ride on (its own buffers)
+    M, K, N = 256, 64, 128
+    Xg, Wg = dev(r.standard_normal((M, K)).astype(np.float32)), dev(r.standard_normal((K, N)).astype(np.float32))
+    Yg = nan_like((M, N))
+    gemm = dict(op="mm", C=Yg.data_ptr(), M=M, K=K, N=N, A=[Xg.data_ptr()], B=[Wg.data_ptr()])
+    for how in ("ride", "twice", "flush"):
+        DYs = [dev(dy) for dy in dys]
+        DXs, DGs = [nan_like((rows, D)) for _ in dys], [dev(dg0) for _ in dys]
+        n = 2 if how == "twice" else 1
+        for i in range(n):
+            lib.check(lib.tlg_dev_rmsnorm_bwd_defer(X.data_ptr(), Gn.data_ptr(), RI.data_ptr(), DYs[i].data_ptr(),
+                                                    B.data_ptr(), DXs[i].data_ptr(), DGs[i].data_ptr(), rows, D,
+                                                    part.data_ptr(), nblk * D, stream()), "defer")
+        if how == "flush":
+            lib.check(lib.tlg_dev_gemm_flush(stream()), "flush")
+        else:
+            lib.group([gemm], stream(), flush=False)
+            lib.check(lib.tlg_dev_gemm_flush(stream()), "flush")
+        for i in range(n):
+            assert np.array_equal(host(DXs[i]), want[i][0]), (how, i)
+            assert np.array_equal(host(DGs[i]), want[i][1]), (how, i)
+        assert normwise_rel(host(Yg), host(Xg).astype(np.float64) @ host(Wg).astype(np.float64)) <= TOL
+    import tlgemm
+    with pytest.raises(tlgemm.TlgError):
+        lib.check(lib.tlg_dev_rmsnorm_bwd_defer(X.data_ptr(), Gn.data_ptr(), RI.data_ptr(), DYs[0].data_ptr(),
+                                                None, DXs[0].data_ptr(), DGs[0].data_ptr(), rows, D,
+                                                part.data_ptr(), nblk * D - 1, stream()), "short partials")
+
+
 def test_rmsnorm_fixture(lib):
     d = load_npz(golden("step_rmsnorm.npz")[0])
     rows, D = d["x"].shape

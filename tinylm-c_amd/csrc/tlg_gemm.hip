@@ -483,7 +483,7 @@ __global__ void k_split_reduce(const float *__restrict__ ws, float *__restrict__
 }
 
 // ------------------------------------------------------ grouped problems --
-enum { PK_NN = 0, PK_NT = 1, PK_TN = 2, PK_RED = 3, PK_ZERO = 4 };
+enum { PK_NN = 0, PK_NT = 1, PK_TN = 2, PK_RED = 3, PK_ZERO = 4, PK_COLSUM = 5 };
 #define TLG_ZERO_CHUNK 4096          // floats a clear's work item sets to 0
 #define TLG_MAXSEG 3
 #define TLG_MAXPROB 16
@@ -746,6 +746,32 @@ __device__ __forceinline__ int group_item(const GroupArgs &g, int b, int *local,
 
 // `eo`: the expert row offsets of an expert-batched launch, staged in LDS
 // (nullptr for dense launches, which have no expert problems).
+// PK_COLSUM: C[0, No) (beta ? += : =) the sum of the `splits` partial rows
+// ws[z][0, No) (a row-block reduction queued by tlg_defer_colsum).  Item
+// `local` covers float4 columns [16 local, 16 local + 16), one wave per
+// column at a time: lane l adds rows l, l + 64, ... in order, then a fixed
+// butterfly, so the sum does not depend on timing.
+#define TLG_COLSUM_CH 16
+__device__ __forceinline__ void colsum(const Prob &P, int local)
+{
+    const int lane = threadIdx.x & 63, nw = blockDim.x >> 6, w = threadIdx.x >> 6;
+    const int c4 = P.No >> 2, cend = min(TLG_COLSUM_CH * (local + 1), c4);
+    for (int c = TLG_COLSUM_CH * local + w; c < cend; c += nw) {
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+        for (int z = lane; z < P.splits; z += 64) s += reinterpret_cast<const f32x4 *>(P.ws + (size_t)z * P.No)[c];
+        for (int o = 32; o > 0; o >>= 1) {
+            s.x += __shfl_xor(s.x, o);
+            s.y += __shfl_xor(s.y, o);
+            s.z += __shfl_xor(s.z, o);
+            s.w += __shfl_xor(s.w, o);
+        }
+        if (lane == 0) {
+            f32x4 *out = reinterpret_cast<f32x4 *>(P.C) + c;
+            *out = P.beta ? *out + s : s;
+        }
+    }
+}
+
 template <class T, bool EXP>
 __device__ __forceinline__ void group_body(const GroupArgs &g, float *smem, const int *eo)
 {
@@ -757,6 +783,7 @@ __device__ __forceinline__ void group_body(const GroupArgs &g, float *smem, cons
     case PK_NN: group_tile<T, RC, OC, EXP>(smem, P, local, eo); break;
     case PK_NT: group_tile<T, RC, RC, EXP>(smem, P, local, eo); break;
     case PK_TN: group_tile<T, OC, OC, EXP>(smem, P, local, eo); break;
+    case PK_COLSUM: colsum(P, local); break;
     case PK_ZERO: {
         const size_t n = (size_t)P.Mo * P.No, e0 = (size_t)local * TLG_ZERO_CHUNK;
         const size_t e1 = e0 + TLG_ZERO_CHUNK < n ? e0 + TLG_ZERO_CHUNK : n;
@@ -1267,8 +1294,12 @@ static int add_reductions(GroupArgs &a)
 {
     for (int k = 0; k < g_npending; k++) {
         Prob r = g_pending[k];
-        r.kind = PK_RED;
-        r.items = (int)(((size_t)r.Mo * r.No + TLG_RED_CHUNK - 1) / TLG_RED_CHUNK);
+        if (r.kind == PK_COLSUM) {
+            r.items = cdiv(r.No / 4, TLG_COLSUM_CH);
+        } else {
+            r.kind = PK_RED;
+            r.items = (int)(((size_t)r.Mo * r.No + TLG_RED_CHUNK - 1) / TLG_RED_CHUNK);
+        }
         a.p[a.nprob++] = r;
     }
     g_npending = 0;
@@ -1276,6 +1307,32 @@ static int add_reductions(GroupArgs &a)
 }
 
 int tlg_group_pending(void) { return g_npending; }
+
+// Queue C[0, No) (beta ? += : =) sum over z of part[z][0, No) (z < splits,
+// No % 4 == 0, 16-byte aligned rows) to ride along in the next grouped or
+// expert launch (or tlg_dev_gemm_flush) on the stream.  A reduction still
+// queued on the same partials, or a full queue, is flushed first, so `part`
+// may be rewritten by the caller's next kernel only after this call.
+int tlg_defer_colsum(const float *part, float *C, int splits, int No, int beta, hipStream_t st)
+{
+    bool busy = g_npending >= TLG_MAXPROB / 2 - 1;
+    for (int k = 0; k < g_npending && !busy; k++) busy = g_pending[k].ws == part;
+    if (busy) {
+        const int rc = tlg_group_flush_launch(st);
+        if (rc) return rc;
+    }
+    Prob &r = g_pending[g_npending++];
+    memset(&r, 0, sizeof r);
+    r.kind = PK_COLSUM;
+    r.C = C;
+    r.ws = part;
+    r.Mo = 1;
+    r.No = No;
+    r.ldc = No;
+    r.beta = beta ? 1 : 0;
+    r.splits = splits;
+    return TLG_OK;
+}
 
 int tlg_group_flush_launch(hipStream_t st)
 {

@@ -46,6 +46,7 @@ int tlg_zero_launch(float *dst, size_t n, hipStream_t st);
 int tlg_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len, int *splits);
 int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st);
 int tlg_group_flush_launch(hipStream_t st);
+int tlg_defer_colsum(const float *part, float *C, int splits, int No, int beta, hipStream_t st);
 
 // One GEMM over every expert of a top-1 MoE layer whose token rows are
 // grouped by expert: expert e owns rows [eoff[e], eoff[e+1]) of each row

@@ -200,70 +200,95 @@ __global__ __launch_bounds__(256) void k_rms_fwd(const float *__restrict__ x, co
 
 // dx = base + s g dy - (s^3 / D) (x . g dy) x (base = dx_in, or 0 when
 // dx_in is null; dx_in may be dx itself) for RMS_ROWS rows per
-// workgroup (one wave per row); the workgroup's share of dg = sum_r x s dy
-// goes to part[blockIdx.x][D] (summed in a fixed order by k_rms_dg).
+// workgroup (one wave per row, RMS_ROWS / 4 rows per wave); the workgroup's
+// share of dg = sum_r x s dy goes to part[blockIdx.x][D] (summed in a fixed
+// order by k_rms_dg or a deferred column sum).  NV float4 columns per lane;
+// a wave issues the loads of RB rows before it reduces any of them, so the
+// rows' load latencies overlap instead of adding up (loads use clamped,
+// in-bounds indices; rows past `rows` and columns past D are masked at use).
 #define RMS_ROWS 16
 #define RMS_MAXV 8            // float4 columns per lane: D <= 64 * 4 * 8
+template <int NV>
 __global__ __launch_bounds__(256) void k_rms_bwd(const float *__restrict__ x, const float *__restrict__ g,
                                                  const float *__restrict__ rinv, const float *__restrict__ dy,
                                                  const float *dx_in, float *dx, int rows, int D,
                                                  float *__restrict__ part)
 {
-    __shared__ f32x4 red[3][64 * RMS_MAXV];
+    constexpr int PER = RMS_ROWS / 4;                 // rows per wave
+    constexpr int RB = NV >= PER ? 1 : PER / NV;      // rows in flight per wave
+    __shared__ f32x4 red[3][64 * NV];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int d4 = D >> 2;
     const f32x4 *g4 = reinterpret_cast<const f32x4 *>(g);
-    f32x4 acc[RMS_MAXV];
+    f32x4 gv[NV], acc[NV];
 #pragma unroll
-    for (int j = 0; j < RMS_MAXV; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int r0 = blockIdx.x * RMS_ROWS;
-    for (int rr = wave; rr < RMS_ROWS; rr += 4) {
-        const int r = r0 + rr;
-        if (r >= rows) break;
-        const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (size_t)r * D);
-        const f32x4 *dr = reinterpret_cast<const f32x4 *>(dy + (size_t)r * D);
-        const float s = rinv[r];
-        float c = 0.f;
+    for (int j = 0; j < NV; j++) {
+        gv[j] = g4[min(lane + 64 * j, d4 - 1)];
+        acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const int r0 = blockIdx.x * RMS_ROWS + wave;
 #pragma unroll
-        for (int j = 0; j < RMS_MAXV; j++) {
-            const int i = lane + 64 * j;
-            if (i < d4) {
-                const f32x4 a = xr[i], w = g4[i], d = dr[i];
-                c += a.x * w.x * d.x + a.y * w.y * d.y + a.z * w.z * d.z + a.w * w.w * d.w;
+    for (int p = 0; p < PER; p += RB) {
+        f32x4 xa[RB][NV], da[RB][NV], ba[RB][NV];
+        float s[RB], c[RB];
+#pragma unroll
+        for (int b = 0; b < RB; b++) {
+            const size_t r = (size_t)min(r0 + 4 * (p + b), rows - 1);
+            s[b] = rinv[r];
+#pragma unroll
+            for (int j = 0; j < NV; j++) {
+                const size_t i = r * d4 + min(lane + 64 * j, d4 - 1);
+                xa[b][j] = reinterpret_cast<const f32x4 *>(x)[i];
+                da[b][j] = reinterpret_cast<const f32x4 *>(dy)[i];
+                ba[b][j] = dx_in ? reinterpret_cast<const f32x4 *>(dx_in)[i] : f32x4{0.f, 0.f, 0.f, 0.f};
             }
         }
-        for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
-        const float coef = s * s * s / (float)D * c;
-        const f32x4 *xin = dx_in ? reinterpret_cast<const f32x4 *>(dx_in + (size_t)r * D) : nullptr;
-        f32x4 *xo = reinterpret_cast<f32x4 *>(dx + (size_t)r * D);
 #pragma unroll
-        for (int j = 0; j < RMS_MAXV; j++) {
-            const int i = lane + 64 * j;
-            if (i < d4) {
-                const f32x4 a = xr[i], w = g4[i], d = dr[i];
-                const f32x4 base = xin ? xin[i] : f32x4{0.f, 0.f, 0.f, 0.f};
-                f32x4 o;
-                o.x = base.x + (s * w.x * d.x - coef * a.x);
-                o.y = base.y + (s * w.y * d.y - coef * a.y);
-                o.z = base.z + (s * w.z * d.z - coef * a.z);
-                o.w = base.w + (s * w.w * d.w - coef * a.w);
-                xo[i] = o;
-                acc[j].x += a.x * s * d.x;
-                acc[j].y += a.y * s * d.y;
-                acc[j].z += a.z * s * d.z;
-                acc[j].w += a.w * s * d.w;
+        for (int b = 0; b < RB; b++) {
+            c[b] = 0.f;
+#pragma unroll
+            for (int j = 0; j < NV; j++) {
+                const f32x4 a = xa[b][j], w = gv[j], d = da[b][j];
+                if (lane + 64 * j < d4) c[b] += a.x * w.x * d.x + a.y * w.y * d.y + a.z * w.z * d.z + a.w * w.w * d.w;
+            }
+        }
+        for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+            for (int b = 0; b < RB; b++) c[b] += __shfl_xor(c[b], o);
+#pragma unroll
+        for (int b = 0; b < RB; b++) {
+            const int r = r0 + 4 * (p + b);
+            if (r >= rows) break;
+            const float sb = s[b], coef = sb * sb * sb / (float)D * c[b];
+            f32x4 *xo = reinterpret_cast<f32x4 *>(dx + (size_t)r * D);
+#pragma unroll
+            for (int j = 0; j < NV; j++) {
+                const int i = lane + 64 * j;
+                if (i < d4) {
+                    const f32x4 a = xa[b][j], w = gv[j], d = da[b][j], base = ba[b][j];
+                    f32x4 o;
+                    o.x = base.x + (sb * w.x * d.x - coef * a.x);
+                    o.y = base.y + (sb * w.y * d.y - coef * a.y);
+                    o.z = base.z + (sb * w.z * d.z - coef * a.z);
+                    o.w = base.w + (sb * w.w * d.w - coef * a.w);
+                    xo[i] = o;
+                    acc[j].x += a.x * sb * d.x;
+                    acc[j].y += a.y * sb * d.y;
+                    acc[j].z += a.z * sb * d.z;
+                    acc[j].w += a.w * sb * d.w;
+                }
             }
         }
     }
     if (wave > 0) {
 #pragma unroll
-        for (int j = 0; j < RMS_MAXV; j++) red[wave - 1][j * 64 + lane] = acc[j];
+        for (int j = 0; j < NV; j++) red[wave - 1][j * 64 + lane] = acc[j];
     }
     __syncthreads();
     if (wave == 0) {
         f32x4 *pr = reinterpret_cast<f32x4 *>(part + (size_t)blockIdx.x * D);
 #pragma unroll
-        for (int j = 0; j < RMS_MAXV; j++) {
+        for (int j = 0; j < NV; j++) {
             const int i = lane + 64 * j;
             if (i < d4) {
                 f32x4 t = acc[j];
@@ -1562,6 +1587,20 @@ extern "C" int tlg_dev_rmsnorm_fwd(const float *x, const float *g, float *out, f
     return TLG_OK;
 }
 
+static void rms_bwd_launch(const float *x, const float *g, const float *rinv, const float *dy, const float *dx_in,
+                           float *dx, int rows, int D, float *part, int nblk, hipStream_t st)
+{
+    const int nv = (D / 4 + 63) / 64;
+    if (nv <= 1)
+        hipLaunchKernelGGL(k_rms_bwd<1>, dim3(nblk), dim3(256), 0, st, x, g, rinv, dy, dx_in, dx, rows, D, part);
+    else if (nv <= 2)
+        hipLaunchKernelGGL(k_rms_bwd<2>, dim3(nblk), dim3(256), 0, st, x, g, rinv, dy, dx_in, dx, rows, D, part);
+    else if (nv <= 4)
+        hipLaunchKernelGGL(k_rms_bwd<4>, dim3(nblk), dim3(256), 0, st, x, g, rinv, dy, dx_in, dx, rows, D, part);
+    else
+        hipLaunchKernelGGL(k_rms_bwd<8>, dim3(nblk), dim3(256), 0, st, x, g, rinv, dy, dx_in, dx, rows, D, part);
+}
+
 extern "C" int tlg_dev_rmsnorm_bwd(const float *x, const float *g, const float *rinv, const float *dy,
                                    const float *dx_in, float *dx, float *dg, int rows, int D, void *stream)
 {
@@ -1576,8 +1615,31 @@ extern "C" int tlg_dev_rmsnorm_bwd(const float *x, const float *g, const float *
     void *ws;
     if ((rc = tr_scratch((size_t)nblk * D * 4, &ws))) return rc;
     hipStream_t st = ST(stream);
-    hipLaunchKernelGGL(k_rms_bwd, dim3(nblk), dim3(256), 0, st, x, g, rinv, dy, dx_in, dx, rows, D, (float *)ws);
+    rms_bwd_launch(x, g, rinv, dy, dx_in, dx, rows, D, (float *)ws, nblk, st);
     hipLaunchKernelGGL(k_rms_dg, dim3((D / 4 + 3) / 4), dim3(256), 0, st, (const float *)ws, nblk, D, dg);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_rmsnorm_bwd_defer(const float *x, const float *g, const float *rinv, const float *dy,
+                                         const float *dx_in, float *dx, float *dg, int rows, int D, float *part,
+                                         size_t part_floats, void *stream)
+{
+    int rc = begin();
+    if (rc) return rc;
+    if (rows < 0 || D <= 0 || D % 4 || D > 256 * RMS_MAXV || !al16(x) || !al16(g) || !al16(dy) || !al16(dx) ||
+        !al16(dg) || (dx_in && !al16(dx_in)) || !part || !al16(part))
+        return tlg_fail(TLG_EINVAL, "rmsnorm_bwd_defer: rows=%d D=%d (D %% 4 == 0, D <= %d, aligned rows)", rows,
+                        D, 256 * RMS_MAXV);
+    if (rows == 0) return TLG_OK;
+    const int nblk = (rows + RMS_ROWS - 1) / RMS_ROWS;
+    if (part_floats < (size_t)nblk * D)
+        return tlg_fail(TLG_EINVAL, "rmsnorm_bwd_defer: partials need %zu floats, have %zu", (size_t)nblk * D,
+                        part_floats);
+    hipStream_t st = ST(stream);
+    // a column sum still queued on these partials lands before they are rewritten
+    if ((rc = tlg_defer_colsum(part, dg, nblk, D, 1, st))) return rc;
+    rms_bwd_launch(x, g, rinv, dy, dx_in, dx, rows, D, part, nblk, st);
     LAUNCH_CHECK();
     return TLG_OK;
 }

@@ -33,6 +33,10 @@ struct TlTrain {
     float *a_in, *a_norm, *q, *k, *v, *ctx, *f_in, *f_norm, *g, *u, *act, *a_rinv, *f_rinv, *lse, *gate, *rprobs;
     /* one each */
     float *x_final, *fn, *fn_rinv, *logits, *dl, *dout, *dfnorm, *dfin, *datt, *dq, *dk, *dv, *dnorm, *dain, *dfn;
+    /* RMSNorm backward's per-row-block gain partials; their column sum rides
+     * along in the next grouped GEMM launch */
+    float *rms_part;
+    size_t rms_part_n;
     float hyper_host[8];
     void *graph;
     /* per grouped GEMM launch of a step, in call order: tile configuration + 1
@@ -95,6 +99,7 @@ TlTrain *tl_train_new(const TlModel *m, int B)
     const size_t N = t->N, L = m->L, D = m->D, KD = t->KD, F = m->F, V = m->V, H = m->H, E = t->E;
     const size_t ND = N * D, NK = N * KD, NF = N * F, half = t->hd / 2;
     const int dense = E == 0;
+    t->rms_part_n = (N + 15) / 16 * D;       /* RMSNorm backward: 16 rows per workgroup */
     Slot s[] = {
         {(void **)&t->P, 4 * t->np}, {(void **)&t->G, 4 * t->np}, {(void **)&t->Mo, 4 * t->np},
         {(void **)&t->Vo, 4 * t->np}, {(void **)&t->tok, 4 * N}, {(void **)&t->tgt, 4 * N},
@@ -113,7 +118,7 @@ TlTrain *tl_train_new(const TlModel *m, int B)
         {(void **)&t->act, dense ? 4 * L * NF : 0}, {(void **)&t->dfnorm, 4 * ND}, {(void **)&t->dfin, 4 * ND},
         {(void **)&t->datt, 4 * ND}, {(void **)&t->dq, 4 * ND}, {(void **)&t->dk, 4 * NK},
         {(void **)&t->dv, 4 * NK}, {(void **)&t->dnorm, 4 * ND}, {(void **)&t->dain, 4 * ND},
-        {(void **)&t->dfn, 4 * ND},
+        {(void **)&t->dfn, 4 * ND}, {(void **)&t->rms_part, 4 * t->rms_part_n},
     };
     const int ns = (int)(sizeof s / sizeof s[0]);
     size_t total = 0;
@@ -365,7 +370,8 @@ int tl_train_backward(TlTrain *t, void *st)
         GROUP(st, ATB(G + w.mtp0 + (size_t)h * D * D, t->fn, dt1, N, D, D), BT(t->dfn, 1, dt1, Wk, N, D, D));
     }
     float *dout = t->dout, *dain = t->dain;
-    CK(tlg_dev_rmsnorm_bwd(t->x_final, P + w.nf, t->fn_rinv, t->dfn, NULL, dout, G + w.nf, N, D, st));
+    CK(tlg_dev_rmsnorm_bwd_defer(t->x_final, P + w.nf, t->fn_rinv, t->dfn, NULL, dout, G + w.nf, N, D,
+                                 t->rms_part, t->rms_part_n, st));
     for (int l = m->L - 1; l >= 0; l--) {
         wmap(t, l, &w);
         float *xin = t->a_in + l * ND, *an = t->a_norm + l * ND, *q = t->q + l * ND, *k = t->k + l * NK,
@@ -384,8 +390,8 @@ int tl_train_backward(TlTrain *t, void *st)
             GROUP(st, BTN(t->dfnorm, 0, N, D, 2, dy, wt, ns), ATB(G + w.w1, fnl, g, N, D, F),
                   ATB(G + w.w3, fnl, u, N, D, F), ATB(G + w.w2, act, dout, N, F, D));   /* dW2, :1101 */
         }
-        CK(tlg_dev_rmsnorm_bwd(fi, P + w.an2, t->f_rinv + (size_t)l * N, t->dfnorm, dout, t->dfin, G + w.an2, N, D,
-                               st));
+        CK(tlg_dev_rmsnorm_bwd_defer(fi, P + w.an2, t->f_rinv + (size_t)l * N, t->dfnorm, dout, t->dfin,
+                                     G + w.an2, N, D, t->rms_part, t->rms_part_n, st));
         GROUP(st, BT(t->datt, 0, t->dfin, P + w.wo, N, D, D), ATB(G + w.wo, cx, t->dfin, N, D, D));
         if (rope_fused(m)) {
             CK(tlg_dev_attn_bwd_rope(q, k, v, cx, t->lse + (size_t)l * N * H, t->datt, t->dq, t->dk, t->dv, t->B, T,
@@ -400,8 +406,8 @@ int tl_train_backward(TlTrain *t, void *st)
         const int ns[3] = {D, KD, KD};
         GROUP(st, BTN(t->dnorm, 0, N, D, 3, dy, wt, ns), ATB(G + w.wq, an, t->dq, N, D, D),
               ATB(G + w.wk, an, t->dk, N, D, KD), ATB(G + w.wv, an, t->dv, N, D, KD));
-        CK(tlg_dev_rmsnorm_bwd(xin, P + w.an1, t->a_rinv + (size_t)l * N, t->dnorm, t->dfin, dain, G + w.an1, N, D,
-                               st));
+        CK(tlg_dev_rmsnorm_bwd_defer(xin, P + w.an1, t->a_rinv + (size_t)l * N, t->dnorm, t->dfin, dain,
+                                     G + w.an1, N, D, t->rms_part, t->rms_part_n, st));
         float *tmp = dout; dout = dain; dain = tmp;                    /* memcpy(dout, dain), :1146 */
     }
     wmap(t, 0, &w);

@@ -79,6 +79,7 @@ SIGNATURES = {
     "tlg_dev_embed_bwd": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "tlg_dev_rmsnorm_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp]),
     "tlg_dev_rmsnorm_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp]),
+    "tlg_dev_rmsnorm_bwd_defer": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp]),
     "tlg_dev_rope": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp]),
     "tlg_dev_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "tlg_dev_attn_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
