@@ -314,6 +314,21 @@ def bench_moe(lib, stream, steps):
     for _ in range(3):
         check(step(), "moe warmup")
     ms, _ = time_steps(lib, step, stream, steps)
+    # the same pair from a kept forward state (tlg_dev_moe_grouped_fwd_keep /
+    # _bwd_kept: no index rebuild, no W1 | W3 and W2 recompute in the backward)
+    kb = lib.tlg_moe_keep_bytes(N, D, F, E)
+    dev["keep"] = lib.tlg_dev_malloc(kb)
+
+    def step_kept():
+        rc = lib.tlg_dev_moe_grouped_fwd_keep(d["fnorm"], d["fin"], d["out"], N, D, F, E, d["wr"], d["w1"],
+                                              d["w3"], d["w2"], d["assign"], d["gate"], d["rprobs"], d["keep"], kb,
+                                              stream)
+        return rc or lib.tlg_dev_moe_grouped_bwd_kept(d["fnorm"], d["dout"], d["dfn"], d["assign"], d["gate"],
+                                                      d["rprobs"], N, D, F, E, d["wr"], d["w1"], d["w3"], d["w2"],
+                                                      d["gwr"], d["gw1"], d["gw3"], d["gw2"], d["keep"], kb, stream)
+    for _ in range(3):
+        check(step_kept(), "moe kept warmup")
+    ms_k, _ = time_steps(lib, step_kept, stream, steps)
     assign = np.empty(N, np.int32)
     check(lib.tlg_memcpy_d2h(assign.ctypes.data, d["assign"], assign.nbytes, stream), "download")
     check(lib.tlg_stream_sync(stream), "sync")
@@ -331,6 +346,11 @@ def bench_moe(lib, stream, steps):
         "gflop_algorithmic": round(algo / 1e9, 3), "gflop_executed": round(executed / 1e9, 3),
         "tflops_algorithmic": round(algo / (per * 1e-3) / 1e12, 2),
         "tflops_executed": round(executed / (per * 1e-3) / 1e12, 2),
+        "kept_state": {
+            "entries": "tlg_dev_moe_grouped_fwd_keep + tlg_dev_moe_grouped_bwd_kept (same results bit for bit)",
+            "ms_per_step": round(ms_k / steps, 4), "tok_s": round(N / (ms_k / steps * 1e-3), 1),
+            "keep_bytes": kb, "tflops_algorithmic": round(algo / (ms_k / steps * 1e-3) / 1e12, 2),
+        },
     }
 
 

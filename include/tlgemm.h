@@ -182,6 +182,25 @@ int  tlg_dev_moe_grouped_bwd(const float *fnorm, const float *dout, float *d_fno
                              const float *gate, const float *rprobs, int N, int D, int F, int E,
                              const float *wr, const float *w1, const float *w3, const float *w2,
                              float *gwr, float *gw1, float *gw3, float *gw2, void *stream);
+/* Kept-state pair: no counterpart in the reference, whose moe_backward
+ * recomputes the expert forward from fnorm (tinylm.c:906-914).  The forward
+ * also stores, in a caller buffer of tlg_moe_keep_bytes(N, D, F, E) bytes
+ * (16-byte aligned), the expert row index and the expert rows g, u, a and y
+ * it computes anyway; the backward reads them instead of rebuilding the index
+ * and recomputing W1 | W3 and W2 (3 of its launches), with the same results
+ * bit for bit.  The backward overwrites g and u (they become dg and du), so
+ * one kept state serves one backward.  For training steps that can hold
+ * N (3F + D) floats per MoE layer until the backward. */
+size_t tlg_moe_keep_bytes(int N, int D, int F, int E);   /* 0 for a bad shape */
+int  tlg_dev_moe_grouped_fwd_keep(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,
+                                  const float *wr, const float *w1, const float *w3, const float *w2,
+                                  int *assign, float *gate, float *rprobs, void *keep, size_t keep_bytes,
+                                  void *stream);
+int  tlg_dev_moe_grouped_bwd_kept(const float *fnorm, const float *dout, float *d_fnorm, const int *assign,
+                                  const float *gate, const float *rprobs, int N, int D, int F, int E,
+                                  const float *wr, const float *w1, const float *w3, const float *w2,
+                                  float *gwr, float *gw1, float *gw3, float *gw2, void *kept,
+                                  size_t kept_bytes, void *stream);
 void tlg_moe_grouped_fwd(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,
                          const float *wr, const float *w1, const float *w3, const float *w2,
                          int *assign, float *gate, float *rprobs);

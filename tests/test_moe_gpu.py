@@ -248,6 +248,77 @@ def test_deterministic(lib):
         assert np.array_equal(x, y)
 
 
+def gpu_pair_kept(lib, c, interleave=None):
+    """Forward with kept state, then (after `interleave()`, other MoE calls
+    that reuse the library's scratch) the backward from that state."""
+    t = _torch()
+    N, D = c["fnorm"].shape
+    E, F = c["wr"].shape[1], c["w1"].shape[2]
+    ins = {k: dev(c[k]) for k in ("fnorm", "fin", "wr", "w1", "w3", "w2", "dout")}
+    grads = [dev(c[k]) for k in ("gwr0", "gw10", "gw30", "gw20")]
+    out = t.full((N, D), float("nan"), dtype=t.float32, device="cuda")
+    assign = t.full((N,), -7, dtype=t.int32, device="cuda")
+    gate = t.full((N,), float("nan"), dtype=t.float32, device="cuda")
+    rprobs = t.full((N, E), float("nan"), dtype=t.float32, device="cuda")
+    nb = lib.tlg_moe_keep_bytes(N, D, F, E)
+    assert nb > 0
+    keep = t.full((nb // 4,), float("nan"), dtype=t.float32, device="cuda")
+    p = {k: v.data_ptr() for k, v in ins.items()}
+    lib.moe_fwd_keep(p["fnorm"], p["fin"], out.data_ptr(), N, D, F, E, p["wr"], p["w1"], p["w3"], p["w2"],
+                     assign.data_ptr(), gate.data_ptr(), rprobs.data_ptr(), keep.data_ptr(), nb, stream())
+    if interleave:
+        interleave()
+    dfn = t.full((N, D), float("nan"), dtype=t.float32, device="cuda")
+    g = [x.data_ptr() for x in grads]
+    lib.moe_bwd_kept(p["fnorm"], p["dout"], dfn.data_ptr(), assign.data_ptr(), gate.data_ptr(), rprobs.data_ptr(),
+                     N, D, F, E, p["wr"], p["w1"], p["w3"], p["w2"], g[0], g[1], g[2], g[3], keep.data_ptr(), nb,
+                     stream())
+    fwd = (out.cpu().numpy(), assign.cpu().numpy(), gate.cpu().numpy(), rprobs.cpu().numpy())
+    return fwd, dfn.cpu().numpy(), [x.cpu().numpy() for x in grads]
+
+
+@pytest.mark.parametrize("N,D,F,E,skew,dead", [(4096, 256, 768, 4, 2.0, ()), (67, 32, 48, 3, 0.0, ()),
+                                              (2500, 64, 96, 5, 1.0, (3,)), (513, 32, 64, 1, 0.0, ())])
+def test_kept_state_pair_is_bit_identical(lib, N, D, F, E, skew, dead):
+    """tlg_dev_moe_grouped_fwd_keep + _bwd_kept give the recomputing pair's
+    results bit for bit, also when other MoE calls run between them."""
+    print("kept pair", N, D, F, E, flush=True)
+    c = case(N, D, F, E, zlib.crc32(f"kept {N} {D} {F} {E}".encode()), skew, dead)
+    ref_f = gpu_forward(lib, c["fnorm"], c["fin"], c["wr"], c["w1"], c["w3"], c["w2"])
+    g0 = [c[k] for k in ("gwr0", "gw10", "gw30", "gw20")]
+    ref_b = gpu_backward(lib, c["fnorm"], c["dout"], ref_f[1], ref_f[2], ref_f[3], c["wr"], c["w1"], c["w3"],
+                         c["w2"], *g0)
+    other = case(300, 16, 32, 7, 5)
+
+    def interleave():
+        f = gpu_forward(lib, other["fnorm"], other["fin"], other["wr"], other["w1"], other["w3"], other["w2"])
+        gpu_backward(lib, other["fnorm"], other["dout"], f[1], f[2], f[3], other["wr"], other["w1"], other["w3"],
+                     other["w2"], *[other[k] for k in ("gwr0", "gw10", "gw30", "gw20")])
+
+    for inter in (None, interleave):
+        fwd, dfn, grads = gpu_pair_kept(lib, c, inter)
+        for x, y in zip(fwd, ref_f):
+            assert np.array_equal(x, y)
+        assert np.array_equal(dfn, ref_b[0])
+        for x, y in zip(grads, ref_b[1]):
+            assert np.array_equal(x, y)
+
+
+def test_kept_state_size_checked(lib):
+    import tlgemm
+    t = _torch()
+    N, D, F, E = 64, 16, 32, 4
+    nb = lib.tlg_moe_keep_bytes(N, D, F, E)
+    assert nb >= 4 * N * (3 * F + D) and lib.tlg_moe_keep_bytes(N, D, F, 65) == 0
+    buf = t.zeros(1 << 16, dtype=t.float32, device="cuda")
+    p = buf.data_ptr()
+    ip = t.zeros(N, dtype=t.int32, device="cuda").data_ptr()
+    with pytest.raises(tlgemm.TlgError):
+        lib.moe_fwd_keep(p, p, p, N, D, F, E, p, p, p, p, ip, p, p, p, nb - 16, stream())
+    with pytest.raises(tlgemm.TlgError):
+        lib.moe_bwd_kept(p, p, p, ip, p, p, N, D, F, E, p, p, p, p, p, p, p, p, p, nb - 16, stream())
+
+
 def test_bad_shapes_rejected(lib):
     import tlgemm
     t = _torch()

@@ -425,17 +425,17 @@ extern "C" int tlg_dev_mm_bt_swiglu_bwd(const float *dY, const float *W2, float 
 // ------------------------------------------------------------- top-1 MoE --
 int tlg_moe_fwd_launch(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,
                        const float *wr, const float *w1, const float *w3, const float *w2, int *assign,
-                       float *gate, float *rprobs, hipStream_t st);
+                       float *gate, float *rprobs, void *keep, size_t keep_bytes, hipStream_t st);
 int tlg_moe_bwd_launch(const float *fnorm, const float *dout, float *d_fnorm, const int *assign,
                        const float *gate, const float *rprobs, int N, int D, int F, int E, const float *wr,
                        const float *w1, const float *w3, const float *w2, float *gwr, float *gw1, float *gw3,
-                       float *gw2, hipStream_t st);
+                       float *gw2, void *kept, size_t kept_bytes, hipStream_t st);
 
 extern "C" int tlg_dev_moe_grouped_fwd(const float *fnorm, const float *fin, float *out, int N, int D, int F,
                                        int E, const float *wr, const float *w1, const float *w3,
                                        const float *w2, int *assign, float *gate, float *rprobs, void *stream)
 {
-    return tlg_moe_fwd_launch(fnorm, fin, out, N, D, F, E, wr, w1, w3, w2, assign, gate, rprobs,
+    return tlg_moe_fwd_launch(fnorm, fin, out, N, D, F, E, wr, w1, w3, w2, assign, gate, rprobs, nullptr, 0,
                               (hipStream_t)stream);
 }
 
@@ -446,7 +446,28 @@ extern "C" int tlg_dev_moe_grouped_bwd(const float *fnorm, const float *dout, fl
                                        void *stream)
 {
     return tlg_moe_bwd_launch(fnorm, dout, d_fnorm, assign, gate, rprobs, N, D, F, E, wr, w1, w3, w2, gwr, gw1,
-                              gw3, gw2, (hipStream_t)stream);
+                              gw3, gw2, nullptr, 0, (hipStream_t)stream);
+}
+
+extern "C" int tlg_dev_moe_grouped_fwd_keep(const float *fnorm, const float *fin, float *out, int N, int D,
+                                            int F, int E, const float *wr, const float *w1, const float *w3,
+                                            const float *w2, int *assign, float *gate, float *rprobs, void *keep,
+                                            size_t keep_bytes, void *stream)
+{
+    if (!keep) return tlg_fail(TLG_EINVAL, "tlg_dev_moe_grouped_fwd_keep: NULL kept-state buffer");
+    return tlg_moe_fwd_launch(fnorm, fin, out, N, D, F, E, wr, w1, w3, w2, assign, gate, rprobs, keep, keep_bytes,
+                              (hipStream_t)stream);
+}
+
+extern "C" int tlg_dev_moe_grouped_bwd_kept(const float *fnorm, const float *dout, float *d_fnorm,
+                                            const int *assign, const float *gate, const float *rprobs, int N,
+                                            int D, int F, int E, const float *wr, const float *w1,
+                                            const float *w3, const float *w2, float *gwr, float *gw1, float *gw3,
+                                            float *gw2, void *kept, size_t kept_bytes, void *stream)
+{
+    if (!kept) return tlg_fail(TLG_EINVAL, "tlg_dev_moe_grouped_bwd_kept: NULL kept-state buffer");
+    return tlg_moe_bwd_launch(fnorm, dout, d_fnorm, assign, gate, rprobs, N, D, F, E, wr, w1, w3, w2, gwr, gw1,
+                              gw3, gw2, kept, kept_bytes, (hipStream_t)stream);
 }
 
 // Host-pointer operands of a MoE call: device addresses (mirror or staging
@@ -495,7 +516,7 @@ static int host_moe_fwd(const float *fnorm, const float *fin, float *out, int N,
     int *das = h.get(assign, (size_t)N * 4, false, true);
     float *dg = h.get(gate, (size_t)N * 4, false, true), *dpr = h.get(rprobs, (size_t)N * E * 4, false, true);
     if (h.rc) return h.rc;
-    rc = tlg_moe_fwd_launch(dfn, dfi, dout, N, D, F, E, dwr, d1, d3, d2, das, dg, dpr, g_tlg.stream);
+    rc = tlg_moe_fwd_launch(dfn, dfi, dout, N, D, F, E, dwr, d1, d3, d2, das, dg, dpr, nullptr, 0, g_tlg.stream);
     if (rc) return rc;
     return h.finish();
 }
@@ -520,7 +541,8 @@ static int host_moe_bwd(const float *fnorm, const float *dout, float *d_fnorm, c
     float *gr = h.get(gwr, (size_t)D * E * 4, true, true);
     float *g1 = h.get(gw1, wf, true, true), *g3 = h.get(gw3, wf, true, true), *g2 = h.get(gw2, wf, true, true);
     if (h.rc) return h.rc;
-    rc = tlg_moe_bwd_launch(dfn, ddo, ddf, das, dg, dpr, N, D, F, E, dwr, d1, d3, d2, gr, g1, g3, g2, g_tlg.stream);
+    rc = tlg_moe_bwd_launch(dfn, ddo, ddf, das, dg, dpr, N, D, F, E, dwr, d1, d3, d2, gr, g1, g3, g2, nullptr, 0,
+                            g_tlg.stream);
     if (rc) return rc;
     return h.finish();
 }

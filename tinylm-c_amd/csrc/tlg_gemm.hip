@@ -382,6 +382,14 @@ __device__ __forceinline__ void tile_store(const f32x16 (&accs)[T::FM][T::FN][T:
     });
 }
 
+// LDS of an expert-launch workgroup: the tile's stages or partials, and the
+// SwiGLU epilogue's staged tile beside the partials.
+template <class T>
+__host__ __device__ constexpr int expert_lds()
+{
+    return T::mx(T::lds_max(), (T::WK > 1 ? T::WK * T::TILE : 0) + T::BM * (T::BN + 1));
+}
+
 // SwiGLU epilogue of a paired-column tile (TileLoader PB): tile columns
 // [0, BN/2) hold g = X W1 and [BN/2, BN) hold u = X W3 for the output
 // columns jh + [0, BN/2).  The summed tile goes through LDS (after the WK
@@ -395,7 +403,7 @@ __device__ __forceinline__ void tile_swiglu(const f32x16 (&accs)[T::FM][T::FN][T
 {
     constexpr int H = T::BN / 2, LD = T::BN + 1;
     constexpr int OFF = T::WK > 1 ? T::WK * T::TILE : 0;
-    static_assert(OFF + T::BM * LD <= T::lds_max(), "paired tile fits beside the partials");
+    static_assert(OFF + T::BM * LD <= expert_lds<T>(), "paired tile fits beside the partials");
     float *L = red + OFF;
     tile_epi<T>(accs, T::BM, T::BN, 0, 0, red, [&](int i, int j, float v) { L[i * LD + j] = v; });
     __syncthreads();
@@ -514,7 +522,8 @@ struct Prob {
     //   epi   TLG_EPI_*: plain store, SwiGLU (C = a, X1 = g, X2 = u when
     //         given), SwiGLU backward (da from the tile, g / u in X1 / X2
     //         replaced by dg / du; C unused), or the top-1 combine (C = out,
-    //         out[omap[i]] = fin[..] + gate[..] * tile row i)
+    //         out[omap[i]] = fin[..] + gate[..] * tile row i; X1 = the rows
+    //         themselves, sorted order, when given)
     const int *amap, *omap;
     const float *B2;
     float *X1, *X2;
@@ -639,10 +648,12 @@ __device__ __forceinline__ void expert_tile(float *smem, const Prob &P, int loca
                 const int ld = P.ldc;
                 float *C = P.C;
                 const float *fin = P.fin;
+                float *Y = P.X1 ? P.X1 + cb : nullptr;      // the expert rows too, when kept
                 tile_epi<T>(acc, rows, P.No, i0, j0, smem, [&](int i, int j, float y) {
                     const int x = i - i0;
                     const size_t o = (size_t)s_tok[x] * ld + j;
                     C[o] = fmaf(s_gate[x], y, fin[o]);
+                    if (Y) Y[(size_t)i * ld + j] = y;
                 });
             }
             break;
@@ -821,7 +832,7 @@ __global__ __launch_bounds__(T::THREADS) void k_group(GroupArgs g)
 template <class T>
 __global__ __launch_bounds__(T::THREADS) __attribute__((amdgpu_waves_per_eu(4))) void k_expert_group(GroupArgs g)
 {
-    __shared__ __attribute__((aligned(16))) float smem[T::lds_max()];
+    __shared__ __attribute__((aligned(16))) float smem[expert_lds<T>()];
     __shared__ int eo[TLG_MAX_EXPERTS + 1];
     const int E = g.p[0].nexp;
     if (g.rows1 > 0) {
@@ -1164,6 +1175,7 @@ static double g_min_waves = 3.0;
 static int g_cand[4] = {3, 14, -1, -1};   // 64x64, then 64x32 (2 x 2 waves)
 static int g_rtarget = 512;
 static int g_erps = 1024;                // expert TN slice (TLG_EXPERT_RPS)
+static int g_expert_cfg = -1;            // expert tile shape pinned (TLG_EXPERT_CFG: 3, 14, 15)
 static int g_group_last = 3;          // shape of the most recent grouped launch
 static const char *g_group_last_name = nullptr;   // set when that launch was a GEMV group
 
@@ -1188,6 +1200,8 @@ static void group_env(void)
     }
     e = getenv("TLG_EXPERT_RPS");
     if (e && atoi(e) >= 64) g_erps = atoi(e);
+    e = getenv("TLG_EXPERT_CFG");
+    if (e && (atoi(e) == 3 || atoi(e) == 14 || atoi(e) == 15)) g_expert_cfg = atoi(e);
     e = getenv("TLG_GROUP_RTARGET");
     if (e && atoi(e) >= 64) g_rtarget = atoi(e);
 }
@@ -1666,8 +1680,11 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     if (need(rps) > g_tlg.ws_floats)
         return tlg_fail(TLG_ENOMEM, "expert launch: %d experts' partials exceed the workspace", E);
 
-    // tile shape as for dense grouped launches: 64x64 tiles when the launch
-    // has about g_min_waves x 256 of them, else 64x32 split-stage tiles
+    // tile shape: the largest of 64x64, 64x32 (2 x 2 waves) and 32x32 (a
+    // quarter stage per wave) that gives about g_min_waves x 256 items, as
+    // for dense grouped launches (measured at configs[4]: W2's N = 256
+    // launches run 15 % faster on 32x32 tiles than on 64x32; the 8-wave
+    // 64x64 tile was slower on every expert launch)
     auto items_for = [&](const TileCfg &c) {
         double t = 0;
         for (int i = 0; i < n; i++) {
@@ -1677,7 +1694,9 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
         }
         return t;
     };
-    const int ci = items_for(kCfgs[3]) >= g_min_waves * 256 ? 3 : 14;
+    const double enough = g_min_waves * 256;
+    const int ci = g_expert_cfg >= 0 ? g_expert_cfg
+                 : items_for(kCfgs[3]) >= enough ? 3 : items_for(kCfgs[14]) >= enough ? 14 : 15;
     const TileCfg &tc = kCfgs[ci];
     GroupArgs a, red, pend;
     a.nprob = red.nprob = pend.nprob = 0;
@@ -1726,10 +1745,12 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     // an XCD's share of the real items can exceed its share of the upper
     // bound by one per expert problem
     static_assert(sizeof(GroupArgs) <= 4096, "kernel arguments");
-    if (ci == 3)
-        hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(a) + 8 * n), dim3(T3::THREADS), 0, st, a);
-    else
-        hipLaunchKernelGGL((k_expert_group<T14>), dim3(group_grid(a) + 8 * n), dim3(T14::THREADS), 0, st, a);
+    const dim3 eg(group_grid(a) + 8 * n);
+    switch (ci) {
+    case 3: hipLaunchKernelGGL((k_expert_group<T3>), eg, dim3(T3::THREADS), 0, st, a); break;
+    case 15: hipLaunchKernelGGL((k_expert_group<T15>), eg, dim3(T15::THREADS), 0, st, a); break;
+    default: hipLaunchKernelGGL((k_expert_group<T14>), eg, dim3(T14::THREADS), 0, st, a); break;
+    }
     TLG_HIP(hipGetLastError());
     if (red.nprob) {
         hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(red)), dim3(T3::THREADS), 0, st, red);

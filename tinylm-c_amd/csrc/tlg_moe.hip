@@ -430,54 +430,97 @@ static int moe_w13(const float *fnorm, int N, int D, int F, int E, const float *
     return tlg_expert_launch(&c, 1, s.eoff, E, N, st);
 }
 
-int tlg_moe_fwd_launch(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,
-                       const float *wr, const float *w1, const float *w3, const float *w2, int *assign,
-                       float *gate, float *rprobs, hipStream_t st)
+// Kept forward state (tlg_dev_moe_grouped_fwd_keep): the index and the
+// expert rows the backward would otherwise recompute, in one caller buffer:
+// idx, pos (N ints each), eoff (E + 1 ints), then g, u, a (N x F) and y
+// (N x D), each 256-byte aligned.
+static size_t keep_layout(int N, int D, int F, int E, size_t *offs)
 {
-    int rc = check_shape(N, D, F, E);
-    if (rc) return rc;
-    if (N == 0) return TLG_OK;
-    if (!MOE_PTRS_OK(fnorm, fin, out, w1, w3, w2) || !wr || !assign || !gate || !rprobs)
-        return tlg_fail(TLG_EINVAL, "MoE forward: NULL or misaligned (16-byte) pointer");
-    if ((rc = tlg_ensure_init())) return rc;
-    if ((rc = tlg_group_flush_launch(st))) return rc;
-    MoeScratch s;
-    if ((rc = moe_scratch(N, D, F, E, &s))) return rc;
+    const size_t n = (size_t)N;
+    const size_t sizes[7] = {n * 4, n * 4, (size_t)(E + 1) * 4, n * F * 4, n * F * 4, n * F * 4, n * D * 4};
+    size_t total = 0;
+    for (int k = 0; k < 7; k++) {
+        if (offs) offs[k] = total;
+        total += (sizes[k] + 255) & ~(size_t)255;
+    }
+    return total;
+}
+
+extern "C" size_t tlg_moe_keep_bytes(int N, int D, int F, int E)
+{
+    if (N < 0 || D <= 0 || F <= 0 || E < 1 || E > TLG_MOE_MAXE) return 0;
+    return keep_layout(N, D, F, E, nullptr);
+}
+
+static void keep_view(void *keep, int N, int D, int F, int E, MoeScratch *s)
+{
+    size_t o[7];
+    keep_layout(N, D, F, E, o);
+    char *b = (char *)keep;
+    s->idx = (int *)(b + o[0]);
+    s->pos = (int *)(b + o[1]);
+    s->eoff = (int *)(b + o[2]);
+    s->g = (float *)(b + o[3]);
+    s->u = (float *)(b + o[4]);
+    s->a = (float *)(b + o[5]);
+    s->y = (float *)(b + o[6]);
+}
+
+// keep: store the index, g, u, a and y in s (a kept view) as well
+static int moe_fwd(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E, const float *wr,
+                   const float *w1, const float *w3, const float *w2, int *assign, float *gate, float *rprobs,
+                   const MoeScratch &s, bool keep, hipStream_t st)
+{
+    int rc;
     const int dch = route_dch(D, E);
     hipLaunchKernelGGL(k_moe_route, dim3((N + MOE_TOK - 1) / MOE_TOK), dim3(256), route_lds(dch, E), st, fnorm, wr,
                        N, D, E, dch, rprobs, assign, gate);
     TLG_HIP(hipGetLastError());
     // the index also sets out = fin for tokens without an expert
     if ((rc = moe_index(assign, N, E, s, fin, out, D, st))) return rc;
-    if ((rc = moe_w13(fnorm, N, D, F, E, w1, w3, s, nullptr, nullptr, st))) return rc;
+    if ((rc = moe_w13(fnorm, N, D, F, E, w1, w3, s, keep ? s.g : nullptr, keep ? s.u : nullptr, st))) return rc;
     // y = a W2_e with the combine in the epilogue: out[n] = fin[n] + gate[n] y
     TlgExpertCall c;
     memset(&c, 0, sizeof c);
     c.op = 0; c.C = out; c.K = F; c.N = D; c.nseg = 1;
     c.A[0] = s.a; c.B[0] = w2; c.es = (long long)F * D;
     c.epi = TLG_EPI_COMBINE; c.omap = s.idx; c.fin = fin; c.gate = gate;
+    if (keep) c.X1 = s.y;
     return tlg_expert_launch(&c, 1, s.eoff, E, N, st);
 }
 
-int tlg_moe_bwd_launch(const float *fnorm, const float *dout, float *d_fnorm, const int *assign,
-                       const float *gate, const float *rprobs, int N, int D, int F, int E, const float *wr,
-                       const float *w1, const float *w3, const float *w2, float *gwr, float *gw1, float *gw3,
-                       float *gw2, hipStream_t st)
+int tlg_moe_fwd_launch(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,
+                       const float *wr, const float *w1, const float *w3, const float *w2, int *assign,
+                       float *gate, float *rprobs, void *keep, size_t keep_bytes, hipStream_t st)
 {
     int rc = check_shape(N, D, F, E);
     if (rc) return rc;
     if (N == 0) return TLG_OK;
-    if (!MOE_PTRS_OK(fnorm, dout, d_fnorm, w1, w3, w2, gw1, gw3, gw2) || !wr || !gwr || !assign || !gate ||
-        !rprobs)
-        return tlg_fail(TLG_EINVAL, "MoE backward: NULL or misaligned (16-byte) pointer");
+    if (!MOE_PTRS_OK(fnorm, fin, out, w1, w3, w2) || !wr || !assign || !gate || !rprobs)
+        return tlg_fail(TLG_EINVAL, "MoE forward: NULL or misaligned (16-byte) pointer");
+    if (keep && (!al16(keep) || keep_bytes < keep_layout(N, D, F, E, nullptr)))
+        return tlg_fail(TLG_EINVAL, "MoE forward: kept state needs %zu bytes, 16-byte aligned",
+                        keep_layout(N, D, F, E, nullptr));
     if ((rc = tlg_ensure_init())) return rc;
     if ((rc = tlg_group_flush_launch(st))) return rc;
     MoeScratch s;
     if ((rc = moe_scratch(N, D, F, E, &s))) return rc;
-    if ((rc = moe_index(assign, N, E, s, nullptr, nullptr, D, st))) return rc;
-    // recompute the forward of every expert (:910-914): g, u, a, then y
-    if ((rc = moe_w13(fnorm, N, D, F, E, w1, w3, s, s.g, s.u, st))) return rc;
-    {
+    if (keep) keep_view(keep, N, D, F, E, &s);
+    return moe_fwd(fnorm, fin, out, N, D, F, E, wr, w1, w3, w2, assign, gate, rprobs, s, keep != nullptr, st);
+}
+
+// kept: s's index, g, u, a and y come from a kept forward (no recompute);
+// g and u are overwritten (dg, du) as in the recomputing backward
+static int moe_bwd(const float *fnorm, const float *dout, float *d_fnorm, const int *assign, const float *gate,
+                   const float *rprobs, int N, int D, int F, int E, const float *wr, const float *w1, const float *w3,
+                   const float *w2, float *gwr, float *gw1, float *gw3, float *gw2, const MoeScratch &s, bool kept,
+                   hipStream_t st)
+{
+    int rc;
+    if (!kept) {
+        if ((rc = moe_index(assign, N, E, s, nullptr, nullptr, D, st))) return rc;
+        // recompute the forward of every expert (:910-914): g, u, a, then y
+        if ((rc = moe_w13(fnorm, N, D, F, E, w1, w3, s, s.g, s.u, st))) return rc;
         TlgExpertCall c;
         memset(&c, 0, sizeof c);
         c.op = 0; c.C = s.y; c.K = F; c.N = D; c.nseg = 1;
@@ -513,4 +556,27 @@ int tlg_moe_bwd_launch(const float *fnorm, const float *dout, float *d_fnorm, co
                        assign, s.dgate, s.eoff, s.y, wr, N, D, E, s.drt, d_fnorm);
     TLG_HIP(hipGetLastError());
     return tlg_gemm_launch(TLG_TN, fnorm, s.drt, gwr, D, E, N, D, E, E, 1, st);
+}
+
+int tlg_moe_bwd_launch(const float *fnorm, const float *dout, float *d_fnorm, const int *assign,
+                       const float *gate, const float *rprobs, int N, int D, int F, int E, const float *wr,
+                       const float *w1, const float *w3, const float *w2, float *gwr, float *gw1, float *gw3,
+                       float *gw2, void *kept, size_t kept_bytes, hipStream_t st)
+{
+    int rc = check_shape(N, D, F, E);
+    if (rc) return rc;
+    if (N == 0) return TLG_OK;
+    if (!MOE_PTRS_OK(fnorm, dout, d_fnorm, w1, w3, w2, gw1, gw3, gw2) || !wr || !gwr || !assign || !gate ||
+        !rprobs)
+        return tlg_fail(TLG_EINVAL, "MoE backward: NULL or misaligned (16-byte) pointer");
+    if (kept && (!al16(kept) || kept_bytes < keep_layout(N, D, F, E, nullptr)))
+        return tlg_fail(TLG_EINVAL, "MoE backward: kept state needs %zu bytes, 16-byte aligned",
+                        keep_layout(N, D, F, E, nullptr));
+    if ((rc = tlg_ensure_init())) return rc;
+    if ((rc = tlg_group_flush_launch(st))) return rc;
+    MoeScratch s;
+    if ((rc = moe_scratch(N, D, F, E, &s))) return rc;
+    if (kept) keep_view(kept, N, D, F, E, &s);
+    return moe_bwd(fnorm, dout, d_fnorm, assign, gate, rprobs, N, D, F, E, wr, w1, w3, w2, gwr, gw1, gw3, gw2, s,
+                   kept != nullptr, st);
 }

@@ -37,6 +37,10 @@ struct TlTrain {
      * along in the next grouped GEMM launch */
     float *rms_part;
     size_t rms_part_n;
+    /* MoE layers: each layer's kept forward state (expert index and rows),
+     * read by its backward instead of a recompute */
+    char *moe_keep;
+    size_t moe_keep_b;
     float hyper_host[8];
     void *graph;
     /* per grouped GEMM launch of a step, in call order: tile configuration + 1
@@ -100,6 +104,7 @@ TlTrain *tl_train_new(const TlModel *m, int B)
     const size_t ND = N * D, NK = N * KD, NF = N * F, half = t->hd / 2;
     const int dense = E == 0;
     t->rms_part_n = (N + 15) / 16 * D;       /* RMSNorm backward: 16 rows per workgroup */
+    t->moe_keep_b = dense ? 0 : (tlg_moe_keep_bytes((int)N, (int)D, (int)F, (int)E) + 255) & ~(size_t)255;
     Slot s[] = {
         {(void **)&t->P, 4 * t->np}, {(void **)&t->G, 4 * t->np}, {(void **)&t->Mo, 4 * t->np},
         {(void **)&t->Vo, 4 * t->np}, {(void **)&t->tok, 4 * N}, {(void **)&t->tgt, 4 * N},
@@ -119,6 +124,7 @@ TlTrain *tl_train_new(const TlModel *m, int B)
         {(void **)&t->datt, 4 * ND}, {(void **)&t->dq, 4 * ND}, {(void **)&t->dk, 4 * NK},
         {(void **)&t->dv, 4 * NK}, {(void **)&t->dnorm, 4 * ND}, {(void **)&t->dain, 4 * ND},
         {(void **)&t->dfn, 4 * ND}, {(void **)&t->rms_part, 4 * t->rms_part_n},
+        {(void **)&t->moe_keep, L * t->moe_keep_b},
     };
     const int ns = (int)(sizeof s / sizeof s[0]);
     size_t total = 0;
@@ -326,9 +332,10 @@ int tl_train_forward(TlTrain *t, void *st)
         CK(tlg_dev_rmsnorm_fwd(fi, P + w.an2, fnl, t->f_rinv + (size_t)l * N, N, D, st));
         float *out = l + 1 < m->L ? t->a_in + (l + 1) * ND : t->x_final;
         if (E > 0) {
-            CK(tlg_dev_moe_grouped_fwd(fnl, fi, out, N, D, F, E, P + w.wr, P + w.w1, P + w.w3, P + w.w2,
-                                       t->assign + (size_t)l * N, t->gate + (size_t)l * N,
-                                       t->rprobs + (size_t)l * N * E, st));
+            CK(tlg_dev_moe_grouped_fwd_keep(fnl, fi, out, N, D, F, E, P + w.wr, P + w.w1, P + w.w3, P + w.w2,
+                                            t->assign + (size_t)l * N, t->gate + (size_t)l * N,
+                                            t->rprobs + (size_t)l * N * E, t->moe_keep + l * t->moe_keep_b,
+                                            t->moe_keep_b, st));
         } else {
             /* g, u and act = silu(g) u (:1002-1006) from one launch; act is
              * kept per layer, so the backward's recompute (:1098-1100) is a read */
@@ -377,9 +384,10 @@ int tl_train_backward(TlTrain *t, void *st)
         float *xin = t->a_in + l * ND, *an = t->a_norm + l * ND, *q = t->q + l * ND, *k = t->k + l * NK,
               *v = t->v + l * NK, *cx = t->ctx + l * ND, *fi = t->f_in + l * ND, *fnl = t->f_norm + l * ND;
         if (E > 0) {
-            CK(tlg_dev_moe_grouped_bwd(fnl, dout, t->dfnorm, t->assign + (size_t)l * N, t->gate + (size_t)l * N,
-                                       t->rprobs + (size_t)l * N * E, N, D, F, E, P + w.wr, P + w.w1, P + w.w3,
-                                       P + w.w2, G + w.wr, G + w.w1, G + w.w3, G + w.w2, st));
+            CK(tlg_dev_moe_grouped_bwd_kept(fnl, dout, t->dfnorm, t->assign + (size_t)l * N,
+                                            t->gate + (size_t)l * N, t->rprobs + (size_t)l * N * E, N, D, F, E,
+                                            P + w.wr, P + w.w1, P + w.w3, P + w.w2, G + w.wr, G + w.w1, G + w.w3,
+                                            G + w.w2, t->moe_keep + l * t->moe_keep_b, t->moe_keep_b, st));
         } else {
             /* d_act = dout W2^T with the SwiGLU backward in its epilogue
              * (:1103-1109): g, u of this layer become dg, du in place */

@@ -53,6 +53,9 @@ int  tl_train_set_batch(TlTrain *t, const int *tok, const int *tgt, const int *t
  * device, so captured steps replay with the current values. */
 int  tl_train_set_hyper(TlTrain *t, float lr, float b1, float b2, float wd, int step, void *stream);
 
+/* A backward reads activations of the forward before it; with MoE layers it
+ * also consumes their kept expert state (g, u become dg, du), so each
+ * backward needs a forward of its own. */
 int  tl_train_forward(TlTrain *t, void *stream);   /* loss -> device         */
 int  tl_train_backward(TlTrain *t, void *stream);  /* G = d loss / d P        */
 int  tl_train_optimize(TlTrain *t, void *stream);  /* gradnorm + AdamW        */

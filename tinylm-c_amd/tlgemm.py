@@ -71,6 +71,11 @@ SIGNATURES = {
     "tlg_dev_moe_grouped_fwd": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tlg_dev_moe_grouped_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp,
                                      _vp, _vp, _vp, _vp, _vp]),
+    "tlg_moe_keep_bytes": (_sz, [_i, _i, _i, _i]),
+    "tlg_dev_moe_grouped_fwd_keep": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                          _vp, _sz, _vp]),
+    "tlg_dev_moe_grouped_bwd_kept": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp,
+                                          _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "tlg_moe_grouped_fwd": (None, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tlg_moe_grouped_bwd": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp,
                                    _vp, _vp, _vp, _vp]),
@@ -181,6 +186,21 @@ class Lib:
         return self.check(self.dll.tlg_dev_moe_grouped_fwd(fnorm, fin, out, N, D, F, E, wr, w1, w3, w2,
                                                            assign, gate, rprobs, stream),
                           "tlg_dev_moe_grouped_fwd")
+
+    def moe_fwd_keep(self, fnorm, fin, out, N, D, F, E, wr, w1, w3, w2, assign, gate, rprobs, keep, keep_bytes,
+                     stream=0):
+        """MoE forward that also keeps the index and expert rows for moe_bwd_kept."""
+        return self.check(self.dll.tlg_dev_moe_grouped_fwd_keep(fnorm, fin, out, N, D, F, E, wr, w1, w3, w2, assign,
+                                                                gate, rprobs, keep, keep_bytes, stream),
+                          "tlg_dev_moe_grouped_fwd_keep")
+
+    def moe_bwd_kept(self, fnorm, dout, d_fnorm, assign, gate, rprobs, N, D, F, E, wr, w1, w3, w2,
+                     gwr, gw1, gw3, gw2, kept, kept_bytes, stream=0):
+        """MoE backward from a kept forward state (no recompute)."""
+        return self.check(self.dll.tlg_dev_moe_grouped_bwd_kept(fnorm, dout, d_fnorm, assign, gate, rprobs,
+                                                                N, D, F, E, wr, w1, w3, w2, gwr, gw1, gw3,
+                                                                gw2, kept, kept_bytes, stream),
+                          "tlg_dev_moe_grouped_bwd_kept")
 
     def moe_bwd(self, fnorm, dout, d_fnorm, assign, gate, rprobs, N, D, F, E, wr, w1, w3, w2,
                 gwr, gw1, gw3, gw2, stream=0):
