@@ -333,6 +333,30 @@ def test_embedding_bit_exact(lib, st):
     assert np.array_equal(host(DE), want)
 
 
+@pytest.mark.parametrize("V,D,N", [(2048, 384, 8192), (50, 128, 5000), (37, 36, 77), (2048, 1028, 300),
+                                   (64, 64, 4100)])
+def test_embedding_bwd_shapes(lib, V, D, N):
+    """The one-launch scatter (D <= 1024: several 4096-token passes, heavy
+    buckets, ragged D / 4) and the counting-sort path (D > 1024) against
+    token-order float32 adds; ids outside [0, V) are skipped."""
+    print("embed_bwd", V, D, N, flush=True)
+    r = np.random.default_rng(V + D + N)
+    tok = r.integers(0, V, N).astype(np.int32)
+    tok[N // 3: N // 3 + min(N // 3, 2000)] = V // 2          # a heavy bucket
+    tok[::97] = -1
+    tok[5::101] = V
+    dout = r.standard_normal((N, D)).astype(np.float32)
+    de0 = r.standard_normal((V, D)).astype(np.float32)
+    DE, DO, T = dev(de0), dev(dout), dev(tok)
+    lib.check(lib.tlg_dev_embed_bwd(DE.data_ptr(), DO.data_ptr(), T.data_ptr(), N, D, V, stream()), "bwd")
+    want = de0.copy()
+    for n in range(N):
+        t = int(tok[n])
+        if 0 <= t < V:
+            want[t] += dout[n]
+    assert np.array_equal(host(DE), want)
+
+
 def test_elementwise(lib):
     r = np.random.default_rng(2)
     n = 100003

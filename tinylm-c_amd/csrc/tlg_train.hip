@@ -172,6 +172,104 @@ __global__ __launch_bounds__(256) void k_embed_bwd(const float *__restrict__ dou
     }
 }
 
+// The same scatter in one launch (D % 4 == 0, D <= 1024): workgroup b owns
+// vocabulary rows [8b, 8b + 8), wave w rows 8b + w and 8b + w + 4.  A pass
+// takes 4096 tokens: every thread loads its 16 ids at once, then per chunk
+// of 256 ids the matching positions are appended, in token order, to a list
+// in LDS (wave ballots and a prefix over the four waves; a pass cannot
+// overflow the list); then each wave adds the dout rows of its entries in
+// list order, four rows' loads in flight at a time.  Each vocabulary row
+// receives its rows in increasing n starting from demb's value, as above.
+#define EMB_VB 8
+#define EMB_PASS 4096
+template <int NV>
+__global__ __launch_bounds__(256) void k_embed_bwd1(const float *__restrict__ dout, const int *__restrict__ tok,
+                                                    int N, int D, int V, float *__restrict__ demb)
+{
+    __shared__ int lst[EMB_PASS];
+    __shared__ int wcnt[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int v0 = blockIdx.x * EMB_VB, d4 = D >> 2, vend = min(v0 + EMB_VB, V);
+    const f32x4 *dout4 = reinterpret_cast<const f32x4 *>(dout);
+    f32x4 *de4 = reinterpret_cast<f32x4 *>(demb);
+    f32x4 acc[2][NV];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int v = min(v0 + wave + 4 * r, V - 1);
+#pragma unroll
+        for (int j = 0; j < NV; j++) acc[r][j] = de4[(size_t)v * d4 + min(lane + 64 * j, d4 - 1)];
+    }
+    for (int p0 = 0; p0 < N; p0 += EMB_PASS) {
+        int tk[EMB_PASS / 256];
+#pragma unroll
+        for (int c = 0; c < EMB_PASS / 256; c++) {
+            const int n = p0 + c * 256 + tid;
+            tk[c] = tok[min(n, N - 1)];
+            if (n >= N) tk[c] = -1;
+        }
+        int cnt = 0;
+#pragma unroll
+        for (int c = 0; c < EMB_PASS / 256; c++) {
+            const int t = tk[c];
+            const bool m = t >= v0 && t < vend;
+            const unsigned long long bal = __ballot(m);
+            if (lane == 0) wcnt[wave] = __popcll(bal);
+            __syncthreads();
+            int off = cnt, tot = cnt;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const int k = wcnt[w];
+                off += w < wave ? k : 0;
+                tot += k;
+            }
+            if (m) lst[off + __popcll(bal & ((1ull << lane) - 1ull))] = ((p0 + c * 256 + tid) << 3) | (t - v0);
+            cnt = tot;
+            __syncthreads();
+        }
+        for (int e0 = 0; e0 < cnt; e0 += 64) {
+            const int e = e0 + lane;
+            const int ent = e < cnt ? lst[e] : 0;
+            unsigned long long mb = __ballot(e < cnt && ((ent & 7) & 3) == wave);
+            while (mb) {
+                int nn[4], rr[4];
+                bool ok[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    ok[k] = mb != 0;
+                    const int b = ok[k] ? __ffsll((long long)mb) - 1 : 0;
+                    if (ok[k]) mb &= mb - 1;
+                    const int en = __shfl(ent, b);
+                    nn[k] = ok[k] ? en >> 3 : 0;
+                    rr[k] = (en & 7) >> 2;
+                }
+                f32x4 rv[4][NV];
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+#pragma unroll
+                    for (int j = 0; j < NV; j++) rv[k][j] = dout4[(size_t)nn[k] * d4 + min(lane + 64 * j, d4 - 1)];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    if (!ok[k]) break;
+#pragma unroll
+                    for (int j = 0; j < NV; j++) {
+                        if (rr[k]) acc[1][j] += rv[k][j];
+                        else acc[0][j] += rv[k][j];
+                    }
+                }
+            }
+        }
+        __syncthreads();                            // the list is refilled next pass
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int v = v0 + wave + 4 * r;
+        if (v >= V) continue;
+#pragma unroll
+        for (int j = 0; j < NV; j++)
+            if (lane + 64 * j < d4) de4[(size_t)v * d4 + lane + 64 * j] = acc[r][j];
+    }
+}
+
 // -------------------------------------------------------------- rmsnorm --
 // One wave per row: s = 1 / sqrt(sum(x^2) / D + 1e-5), out = x * s * g.
 __global__ __launch_bounds__(256) void k_rms_fwd(const float *__restrict__ x, const float *__restrict__ g,
@@ -1559,6 +1657,16 @@ extern "C" int tlg_dev_embed_bwd(float *demb, const float *dout, const int *tok,
     if (rc) return rc;
     if (N < 0 || D <= 0 || V <= 0) return tlg_fail(TLG_EINVAL, "embed_bwd: N=%d D=%d V=%d", N, D, V);
     if (N == 0) return TLG_OK;
+    const int nv = (D / 4 + 63) / 64;
+    if (D % 4 == 0 && nv <= 4 && al16(demb) && al16(dout) && N < (1 << 28)) {
+        const dim3 grid((V + EMB_VB - 1) / EMB_VB);
+        hipStream_t st = ST(stream);
+        if (nv == 1) hipLaunchKernelGGL(k_embed_bwd1<1>, grid, dim3(256), 0, st, dout, tok, N, D, V, demb);
+        else if (nv == 2) hipLaunchKernelGGL(k_embed_bwd1<2>, grid, dim3(256), 0, st, dout, tok, N, D, V, demb);
+        else hipLaunchKernelGGL(k_embed_bwd1<4>, grid, dim3(256), 0, st, dout, tok, N, D, V, demb);
+        LAUNCH_CHECK();
+        return TLG_OK;
+    }
     void *ws;
     const size_t vb = ((size_t)(V + 1) * 4 + 255) & ~(size_t)255;
     if ((rc = tr_scratch(3 * vb + (size_t)N * 4, &ws))) return rc;
