@@ -189,8 +189,11 @@ int  tlg_dev_moe_grouped_bwd(const float *fnorm, const float *dout, float *d_fno
  * it computes anyway; the backward reads them instead of rebuilding the index
  * and recomputing W1 | W3 and W2 (3 of its launches), with the same results
  * bit for bit.  The backward overwrites g and u (they become dg and du), so
- * one kept state serves one backward.  For training steps that can hold
- * N (3F + D) floats per MoE layer until the backward. */
+ * one kept state serves one backward, and its last summation of the router
+ * gradient is deferred like a split GEMM's reduction: gwr is complete after
+ * the next grouped or expert launch on the stream, or tlg_dev_gemm_flush
+ * (when gwr is 16-byte aligned; otherwise at return).  For training steps
+ * that can hold N (3F + D) floats per MoE layer until the backward. */
 size_t tlg_moe_keep_bytes(int N, int D, int F, int E);   /* 0 for a bad shape */
 int  tlg_dev_moe_grouped_fwd_keep(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,
                                   const float *wr, const float *w1, const float *w3, const float *w2,

@@ -273,6 +273,7 @@ def gpu_pair_kept(lib, c, interleave=None):
     lib.moe_bwd_kept(p["fnorm"], p["dout"], dfn.data_ptr(), assign.data_ptr(), gate.data_ptr(), rprobs.data_ptr(),
                      N, D, F, E, p["wr"], p["w1"], p["w3"], p["w2"], g[0], g[1], g[2], g[3], keep.data_ptr(), nb,
                      stream())
+    lib.check(lib.tlg_dev_gemm_flush(stream()), "flush")      # dWr's deferred column sum
     fwd = (out.cpu().numpy(), assign.cpu().numpy(), gate.cpu().numpy(), rprobs.cpu().numpy())
     return fwd, dfn.cpu().numpy(), [x.cpu().numpy() for x in grads]
 

@@ -1348,7 +1348,7 @@ int tlg_defer_colsum(const float *part, float *C, int splits, int No, int beta, 
     return TLG_OK;
 }
 
-int tlg_group_flush_launch(hipStream_t st)
+static int group_flush_dense(hipStream_t st)
 {
     if (g_npending == 0) return TLG_OK;
     GroupArgs a;
@@ -1358,6 +1358,14 @@ int tlg_group_flush_launch(hipStream_t st)
     launch_group(3, a, group_grid(a), st);
     TLG_HIP(hipGetLastError());
     return TLG_OK;
+}
+
+static int ecarry_flush(hipStream_t st);
+
+int tlg_group_flush_launch(hipStream_t st)
+{
+    const int rc = ecarry_flush(st);
+    return rc ? rc : group_flush_dense(st);
 }
 
 // [lo, hi) byte range touched by a row-major operand of `rows` x `cols`
@@ -1418,6 +1426,7 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
         return rc;
     }
 
+    if ((rc = ecarry_flush(st))) return rc;
     // Pending reductions write their C; a call that touches such a range must
     // see them first, so they go in a launch of their own.
     for (int k = 0; k < g_npending && g_npending; k++) {
@@ -1578,7 +1587,28 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
 // outputs.  Rows per expert live on the device (eoff), so the host sizes the
 // grid for the worst case: ceil(rows_e / u) summed over experts is at most
 // rows / u + E units of u rows.
-int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E, int rows, hipStream_t st)
+// Slice reductions an expert launch held back (carry TLG_ECARRY_OUT) for the
+// next expert launch over the same row offsets (carry TLG_ECARRY_IN), which
+// runs them as its last items and places its own partial slots after
+// theirs: the kernel boundary between the two makes the partials visible,
+// as for the grouped launches' deferred reductions.  Any other launch that
+// uses the workspace launches them first.
+static GroupArgs g_ecarry;              // nprob 0: nothing held
+static size_t g_ecarry_used = 0;        // workspace floats their partials occupy
+static const int *g_ecarry_eoff = nullptr;
+
+static int ecarry_flush(hipStream_t st)
+{
+    if (!g_ecarry.nprob) return TLG_OK;
+    hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(g_ecarry)), dim3(T3::THREADS), 0, st, g_ecarry);
+    g_ecarry.nprob = 0;
+    g_ecarry_used = 0;
+    TLG_HIP(hipGetLastError());
+    return TLG_OK;
+}
+
+int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E, int rows, hipStream_t st,
+                      int carry)
 {
     if (n <= 0) return TLG_OK;
     int rc = tlg_ensure_init();
@@ -1589,6 +1619,10 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     if ((dense && E != 1) || E < 1 || E > TLG_MAX_EXPERTS || rows < 0)
         return tlg_fail(TLG_EINVAL, "expert launch: bad row offsets or %d experts", E);
     if (rows == 0) return TLG_OK;
+    // held slice reductions join this launch only if it asks for them and
+    // shares their row offsets
+    const bool cin = carry == TLG_ECARRY_IN && g_ecarry.nprob && g_ecarry_eoff == eoff && !dense;
+    if (!cin && (rc = ecarry_flush(st))) return rc;
     // Pending split reductions of grouped launches ride along when this
     // launch writes no partial slots (they reuse the whole workspace) and
     // touches none of their outputs; otherwise they are flushed first.
@@ -1614,7 +1648,7 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
         }
     }
     if (!ride) {
-        rc = tlg_group_flush_launch(st);
+        rc = group_flush_dense(st);
         if (rc) return rc;
     }
 
@@ -1670,8 +1704,9 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     // reduction slices of the TN problems (g_erps rows, doubled until the
     // partials fit): short slices balance experts of very different sizes
     int rps = cdiv(g_erps, 64) * 64;
+    const size_t used0 = cin ? g_ecarry_used : 0;     // the held partials come first
     auto need = [&](int u) {
-        size_t t = 0;
+        size_t t = used0;
         for (int i = 0; i < n; i++)
             if (probs[i].kind == PK_TN) t += (size_t)(rows / u + E) * probs[i].Mo * probs[i].No;
         return t;
@@ -1702,7 +1737,7 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     a.nprob = red.nprob = pend.nprob = 0;
     a.rows1 = red.rows1 = pend.rows1 = dense ? rows : 0;
     if (ride) add_reductions(pend);
-    size_t used = 0;
+    size_t used = used0;
     int order[TLG_MAXPROB / 2];
     for (int i = 0; i < n; i++) {
         Prob &P = probs[i];
@@ -1740,8 +1775,15 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
             red.p[red.nprob++] = r;
         }
     }
-    // the grouped launches' reductions that ride along go last (short items)
+    // the grouped launches' reductions that ride along go last (short items),
+    // with the held slice reductions of the previous expert launch
     for (int k = 0; k < pend.nprob; k++) a.p[a.nprob++] = pend.p[k];
+    if (cin) {
+        if (a.nprob + g_ecarry.nprob > TLG_MAXPROB) return tlg_fail(TLG_EINVAL, "expert launch: too many problems");
+        for (int k = 0; k < g_ecarry.nprob; k++) a.p[a.nprob++] = g_ecarry.p[k];
+        g_ecarry.nprob = 0;
+        g_ecarry_used = 0;
+    }
     // an XCD's share of the real items can exceed its share of the upper
     // bound by one per expert problem
     static_assert(sizeof(GroupArgs) <= 4096, "kernel arguments");
@@ -1752,7 +1794,11 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     default: hipLaunchKernelGGL((k_expert_group<T14>), eg, dim3(T14::THREADS), 0, st, a); break;
     }
     TLG_HIP(hipGetLastError());
-    if (red.nprob) {
+    if (red.nprob && carry == TLG_ECARRY_OUT && !dense && g_npending == 0) {
+        g_ecarry = red;                  // the next expert launch runs them
+        g_ecarry_used = used;
+        g_ecarry_eoff = eoff;
+    } else if (red.nprob) {
         hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(red)), dim3(T3::THREADS), 0, st, red);
         TLG_HIP(hipGetLastError());
     }

@@ -74,7 +74,12 @@ struct TlgExpertCall {
     float *X1, *X2;
     const float *fin, *gate;
 };
-int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E, int rows, hipStream_t st);
+// carry: TLG_ECARRY_OUT holds this launch's expert slice reductions for the
+// next expert launch over the same eoff, which takes them with TLG_ECARRY_IN
+// (no other launch may come between; any other workspace user runs them).
+enum { TLG_ECARRY_NONE = 0, TLG_ECARRY_OUT = 1, TLG_ECARRY_IN = 2 };
+int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E, int rows, hipStream_t st,
+                      int carry = TLG_ECARRY_NONE);
 
 // M <= 8 forms of mm / mm_bt (tlg_gemv.hip): weight-streaming GEMV kernels.
 bool tlg_gemv_fits(TlgKind kind, int Mo);

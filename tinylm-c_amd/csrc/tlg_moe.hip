@@ -281,15 +281,17 @@ __global__ __launch_bounds__(256) void k_moe_dgate(const float *__restrict__ dou
 
 // Router backward and d_fnorm (:928-944), MOE_TOK tokens per workgroup.
 // First, per token (:933-943): dp_e = 0.01 E (cnt_e / N) / N, plus d_gate on
-// the chosen expert; d_rt = p (dp - p.dp) -- kept in LDS and written out for
-// the dWr GEMM.  Then d_fnorm[n][d] = dX[pos[n]][d] + sum_e d_rt[n][e]
-// wr[d][e]: the expert scatter (:928-930) after the memset (:900), then the
-// router mm_bt (:944).
+// the chosen expert; d_rt = p (dp - p.dp) -- kept in LDS and written out.
+// Then d_fnorm[n][d] = dX[pos[n]][d] + sum_e d_rt[n][e] wr[d][e]: the expert
+// scatter (:928-930) after the memset (:900), then the router mm_bt (:944).
+// With wpart, the workgroup's share of dWr = fnorm^T d_rt (:945) goes to
+// wpart[blockIdx.x][d * E + e] (its tokens in order), for a column sum.
 __global__ __launch_bounds__(256) void k_moe_router_bwd(const float *__restrict__ rprobs, const int *__restrict__ pos,
                                                         const int *__restrict__ assign, const float *__restrict__ dgate,
                                                         const int *__restrict__ eoff, const float *__restrict__ dX,
                                                         const float *__restrict__ wr, int N, int D, int E,
-                                                        float *__restrict__ drt, float *__restrict__ dfn)
+                                                        float *__restrict__ drt, float *__restrict__ dfn,
+                                                        const float *__restrict__ fnorm, float *__restrict__ wpart)
 {
     __shared__ float sd[MOE_TOK][TLG_MOE_MAXE];
     __shared__ int sp[MOE_TOK];
@@ -320,9 +322,12 @@ __global__ __launch_bounds__(256) void k_moe_router_bwd(const float *__restrict_
     __syncthreads();
     // one column d per thread, the block's token rows loaded together
     for (int d = tid; d < D; d += 256) {
-        float x[MOE_TOK];
+        float x[MOE_TOK], f[MOE_TOK];
 #pragma unroll
-        for (int t = 0; t < MOE_TOK; t++) x[t] = sp[t] >= 0 ? dX[(size_t)sp[t] * D + d] : 0.f;
+        for (int t = 0; t < MOE_TOK; t++) {
+            x[t] = sp[t] >= 0 ? dX[(size_t)sp[t] * D + d] : 0.f;
+            f[t] = wpart && n0 + t < N ? fnorm[(size_t)(n0 + t) * D + d] : 0.f;
+        }
         const float *w = wr + (size_t)d * E;
 #pragma unroll
         for (int t = 0; t < MOE_TOK; t++) {
@@ -330,6 +335,15 @@ __global__ __launch_bounds__(256) void k_moe_router_bwd(const float *__restrict_
             float s = 0.f;
             for (int e = 0; e < E; e++) s = fmaf(sd[t][e], w[e], s);
             dfn[(size_t)(n0 + t) * D + d] = x[t] + s;
+        }
+        if (wpart) {
+            float *wp = wpart + ((size_t)blockIdx.x * D + d) * E;
+            for (int e = 0; e < E; e++) {
+                float s = 0.f;
+#pragma unroll
+                for (int t = 0; t < MOE_TOK; t++) s = fmaf(f[t], n0 + t < N ? sd[t][e] : 0.f, s);
+                wp[e] = s;
+            }
         }
     }
 }
@@ -342,6 +356,7 @@ __global__ __launch_bounds__(256) void k_moe_router_bwd(const float *__restrict_
 struct MoeScratch {
     int *idx, *pos, *eoff;
     float *dgate, *drt, *y, *dy, *g, *u, *a;
+    float *wpart;            // dWr partials, one row of D x E per router workgroup
 };
 static void *g_moe_mem = nullptr;
 static size_t g_moe_bytes = 0;
@@ -356,10 +371,11 @@ void tlg_moe_release(void)
 static int moe_scratch(int N, int D, int F, int E, MoeScratch *s)
 {
     const size_t n = (size_t)N;
-    const size_t sizes[10] = {n * 4, n * 4, (size_t)(TLG_MOE_MAXE + 1) * 4, n * 4, n * E * 4,
-                              n * D * 4, n * D * 4, n * F * 4, n * F * 4, n * F * 4};
-    size_t total = 0, offs[10];
-    for (int k = 0; k < 10; k++) {
+    const size_t nblk = (n + MOE_TOK - 1) / MOE_TOK;
+    const size_t sizes[11] = {n * 4, n * 4, (size_t)(TLG_MOE_MAXE + 1) * 4, n * 4, n * E * 4,
+                              n * D * 4, n * D * 4, n * F * 4, n * F * 4, n * F * 4, nblk * D * E * 4};
+    size_t total = 0, offs[11];
+    for (int k = 0; k < 11; k++) {
         offs[k] = total;
         total += (sizes[k] + 255) & ~(size_t)255;
     }
@@ -384,6 +400,7 @@ static int moe_scratch(int N, int D, int F, int E, MoeScratch *s)
     s->g = (float *)(b + offs[7]);
     s->u = (float *)(b + offs[8]);
     s->a = (float *)(b + offs[9]);
+    s->wpart = (float *)(b + offs[10]);
     return TLG_OK;
 }
 
@@ -539,7 +556,8 @@ static int moe_bwd(const float *fnorm, const float *dout, float *d_fnorm, const 
     c[1].op = 1; c[1].beta = 0; c[1].C = nullptr; c[1].K = F; c[1].N = D; c[1].nseg = 1;
     c[1].A[0] = s.dy; c[1].B[0] = w2; c[1].es = (long long)F * D;
     c[1].epi = TLG_EPI_SWIGLU_BWD; c[1].X1 = s.g; c[1].X2 = s.u;
-    if ((rc = tlg_expert_launch(c, 2, s.eoff, E, N, st))) return rc;
+    // dW2's slice reduction runs as the last items of the next launch
+    if ((rc = tlg_expert_launch(c, 2, s.eoff, E, N, st, TLG_ECARRY_OUT))) return rc;
     // dW1_e += Xg^T dg ; dW3_e += Xg^T du (Xg rows gathered from fnorm) ;
     // dX = dg W1_e^T + du W3_e^T  (:926-927)
     memset(c, 0, sizeof c);
@@ -550,12 +568,20 @@ static int moe_bwd(const float *fnorm, const float *dout, float *d_fnorm, const 
     c[2].op = 1; c[2].beta = 0; c[2].C = s.y; c[2].K = D; c[2].N = F; c[2].nseg = 2;
     c[2].A[0] = s.g; c[2].B[0] = w1; c[2].A[1] = s.u; c[2].B[1] = w3; c[2].Nseg[1] = F;
     c[2].es = (long long)D * F;
-    if ((rc = tlg_expert_launch(c, 3, s.eoff, E, N, st))) return rc;
-    // router: softmax backward, d_fnorm, dWr  (:932-945)
-    hipLaunchKernelGGL(k_moe_router_bwd, dim3((N + MOE_TOK - 1) / MOE_TOK), dim3(256), 0, st, rprobs, s.pos,
-                       assign, s.dgate, s.eoff, s.y, wr, N, D, E, s.drt, d_fnorm);
+    if ((rc = tlg_expert_launch(c, 3, s.eoff, E, N, st, TLG_ECARRY_IN))) return rc;
+    // router: softmax backward, d_fnorm, dWr  (:932-945).  dWr's per-block
+    // partials are summed by a column-sum item: at once for the reference-
+    // shaped entry, in the next grouped launch for the kept-state one (as a
+    // split GEMM's reduction; the same sum either way).  An unaligned gwr
+    // takes the mm_atb launch instead.
+    const int nblk = (N + MOE_TOK - 1) / MOE_TOK;
+    const bool cs = al16(gwr);
+    hipLaunchKernelGGL(k_moe_router_bwd, dim3(nblk), dim3(256), 0, st, rprobs, s.pos, assign, s.dgate, s.eoff, s.y,
+                       wr, N, D, E, s.drt, d_fnorm, fnorm, cs ? s.wpart : nullptr);
     TLG_HIP(hipGetLastError());
-    return tlg_gemm_launch(TLG_TN, fnorm, s.drt, gwr, D, E, N, D, E, E, 1, st);
+    if (!cs) return tlg_gemm_launch(TLG_TN, fnorm, s.drt, gwr, D, E, N, D, E, E, 1, st);
+    if ((rc = tlg_defer_colsum(s.wpart, gwr, nblk, D * E, 1, st))) return rc;
+    return kept ? TLG_OK : tlg_group_flush_launch(st);
 }
 
 int tlg_moe_bwd_launch(const float *fnorm, const float *dout, float *d_fnorm, const int *assign,
