@@ -382,6 +382,13 @@ __device__ __forceinline__ void tile_store(const f32x16 (&accs)[T::FM][T::FN][T:
     });
 }
 
+// 1 / (1 + e^-z) with the hardware exp2 and reciprocal (within a few ulp of
+// the reference's expf and division; e^-z = inf gives 0, as there).
+__device__ __forceinline__ float hw_sigmoid(float z)
+{
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * -1.44269504088896341f));
+}
+
 // LDS of an expert-launch workgroup: the tile's stages or partials, and the
 // SwiGLU epilogue's staged tile beside the partials.
 template <class T>
@@ -413,7 +420,7 @@ __device__ __forceinline__ void tile_swiglu(const f32x16 (&accs)[T::FM][T::FN][T
         if (i >= Mo || j >= No) continue;
         const float g = L[x * LD + c], u = L[x * LD + c + H];
         const size_t o = (size_t)i * ldc + j;
-        Ca[o] = g / (1.0f + expf(-g)) * u;
+        Ca[o] = g * hw_sigmoid(g) * u;
         if (Cg) Cg[o] = g;
         if (Cu) Cu[o] = u;
     }
@@ -633,7 +640,7 @@ __device__ __forceinline__ void expert_tile(float *smem, const Prob &P, int loca
             tile_epi<T>(acc, rows, P.No, i0, j0, smem, [&](int i, int j, float d) {
                 const size_t o = (size_t)i * ld + j;
                 const float z = G[o], uv = U[o];
-                const float sg = 1.0f / (1.0f + expf(-z));
+                const float sg = hw_sigmoid(z);
                 const float si = z * sg;
                 const float ds = sg + z * sg * (1.0f - sg);
                 G[o] = d * uv * ds;
