@@ -766,10 +766,10 @@ __device__ __forceinline__ int group_item(const GroupArgs &g, int b, int *local,
 // (nullptr for dense launches, which have no expert problems).
 // PK_COLSUM: C[0, No) (beta ? += : =) the sum of the `splits` partial rows
 // ws[z][0, No) (a row-block reduction queued by tlg_defer_colsum).  Item
-// `local` covers float4 columns [16 local, 16 local + 16), one wave per
+// `local` covers float4 columns [4 local, 4 local + 4), one wave per
 // column at a time: lane l adds rows l, l + 64, ... in order, then a fixed
 // butterfly, so the sum does not depend on timing.
-#define TLG_COLSUM_CH 16
+#define TLG_COLSUM_CH 4
 __device__ __forceinline__ void colsum(const Prob &P, int local)
 {
     const int lane = threadIdx.x & 63, nw = blockDim.x >> 6, w = threadIdx.x >> 6;
