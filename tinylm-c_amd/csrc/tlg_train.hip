@@ -1281,7 +1281,8 @@ __global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_dq4(const float *__rest
 // and query block w / 4 of the pair.  Its dV = P^T dO and dK = dS^T Q sum
 // over its pairs in registers, the 8 waves' sums add in wave order through
 // LDS (so every head of the KV group and every query block is summed in a
-// fixed order), and dK is rotated back before it is stored.
+// fixed order; each thread of the workgroup sums a share of the outputs),
+// and dK is rotated back before it is stored.
 #define A4_DKV_ST (2 * 4 * 32 * A4_LD)          // one staged array: 2 query blocks x 4 heads x 32 rows
 
 template <bool ROPE>
@@ -1341,7 +1342,7 @@ __global__ __launch_bounds__(512) void k_attn_dkv4(const float *__restrict__ q, 
 {
     // staged q, dO (2 query blocks x 4 heads) and lse / Dq; the wave sums at the end reuse it
     __shared__ __attribute__((aligned(16))) float Sm[2 * A4_DKV_ST + 2 * 2 * 32 * 4];
-    static_assert(2 * A4_DKV_ST >= 7 * 2 * 16 * 64, "wave sums fit the staging area");
+    static_assert(2 * A4_DKV_ST >= 8 * 2 * 16 * 64, "wave sums fit the staging area");
     float *Qs = Sm, *Ds = Sm + A4_DKV_ST, *LDs = Sm + 2 * A4_DKV_ST;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hs = wave & 3, qs = wave >> 2;
     const int nkb = (T + 31) >> 5;
@@ -1411,31 +1412,48 @@ __global__ __launch_bounds__(512) void k_attn_dkv4(const float *__restrict__ q, 
         }
         __syncthreads();
     }
-    // the 8 waves' sums, in wave order
+    // the 8 waves' sums, in wave order, spread over the workgroup: thread t
+    // adds dK's pair of columns (d, d + 16) of MFMA register t / 32 (the RoPE
+    // pair, rotated back together) and two of dV's values
     float *red = Sm;
-    if (wave > 0) {
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            red[(((wave - 1) * 2 + 0) * 16 + r) * 64 + lane] = ak[r];
-            red[(((wave - 1) * 2 + 1) * 16 + r) * 64 + lane] = av[r];
-        }
-    }
-    __syncthreads();
-    if (wave != 0) return;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-        float a = ak[r], c = av[r];
-        for (int w = 0; w < 7; w++) {
-            a += red[((w * 2 + 0) * 16 + r) * 64 + lane];
-            c += red[((w * 2 + 1) * 16 + r) * 64 + lane];
+        red[((wave * 2 + 0) * 16 + r) * 64 + lane] = ak[r];
+        red[((wave * 2 + 1) * 16 + r) * 64 + lane] = av[r];
+    }
+    __syncthreads();
+    const size_t obase = (size_t)b * T * KD + kvh * AT_HD;
+    {
+        const int r = tid >> 5, lp = tid & 31;
+        const int l0 = (lp & 15) | ((lp & 16) << 1), l1 = l0 | 16;     // same row, columns d and d + 16
+        float a0 = red[(0 * 16 + r) * 64 + l0], a1 = red[(0 * 16 + r) * 64 + l1];
+#pragma unroll
+        for (int w = 1; w < 8; w++) {
+            a0 += red[((w * 2) * 16 + r) * 64 + l0];
+            a1 += red[((w * 2) * 16 + r) * 64 + l1];
         }
-        const int s = s0 + at_row(r, lane);
-        if (ROPE) a = at_rot_1(a, min(s, T - 1), lane, cs, sn, true);
+        const int s = s0 + at_row(r, l0);
+        if (ROPE) {
+            // rope_apply's transpose of the pair: lo = lo' c + hi' s, hi = hi' c - lo' s
+            const int t = min(s, T - 1), i = l0 & 15;
+            const float c = cs[(size_t)t * 16 + i], sv = sn[(size_t)t * 16 + i];
+            const float lo = a0 * c + a1 * sv, hi = a1 * c - a0 * sv;
+            a0 = lo;
+            a1 = hi;
+        }
         if (s < T) {
-            const size_t off = (size_t)(b * T + s) * KD + kvh * AT_HD + lq;
-            dk[off] = a;
-            dv[off] = c;
+            dk[obase + (size_t)s * KD + (l0 & 31)] = a0;
+            dk[obase + (size_t)s * KD + (l1 & 31)] = a1;
         }
+    }
+#pragma unroll
+    for (int k2 = 0; k2 < 2; k2++) {
+        const int e = tid + 512 * k2, r = e >> 6, l = e & 63;
+        float c = red[(16 + r) * 64 + l];
+#pragma unroll
+        for (int w = 1; w < 8; w++) c += red[((w * 2 + 1) * 16 + r) * 64 + l];
+        const int s = s0 + at_row(r, l);
+        if (s < T) dv[obase + (size_t)s * KD + (l & 31)] = c;
     }
 }
 
