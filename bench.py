@@ -166,17 +166,18 @@ def read_traffic(kernel):
     return None
 
 
-AUTOTUNE_CANDS = (3, 14, 13, 15, 0, 1, 20)
+AUTOTUNE_CANDS = (3, 14, 13, 15, 0, 1, 20, 21, 22, 23)
 
 # Tile configuration of every grouped launch of each training step: per launch
-# the choice tl_run_autotune made most often over 7 timing runs (5 timed steps
-# per candidate each) on an MI355X.  A fixed table keeps the step's kernels --
+# the choice tl_run_autotune made most often over 3 timing runs (10 timed
+# steps per candidate each; ties to the fastest run) on an MI355X, with the
+# candidates above plus 4 and 8 (never picked).  A fixed table keeps the step's kernels --
 # and so the roofline kernel and its rocprofv3 profiles -- the same from box
 # to box; --autotune re-times the candidates instead.
 TUNED = {
     "nano": [15, 15, 14, 15, 3, 15, 15, 15, 15, 15],
-    "m3": [13, 14, 3, 14, 14, 20, 3, 14, 14, 14, 3, 14, 14, 15, 3, 14, 14, 15, 3, 14, 14, 15, 3, 14, 3, 20, 3, 15, 13, 15, 3, 15, 13, 15, 3, 15, 13, 15, 3, 15, 13, 15, 20, 15, 13, 15, 3, 15, 13, 15],
-    "m8": [14, 3, 0, 20, 3, 3, 0, 3, 14, 3, 0, 3, 14, 3, 0, 3, 14, 3, 0, 3, 14, 3, 0, 3, 14, 3, 0, 3, 14, 3, 0, 3, 0, 3, 0, 3, 3, 0, 3, 14, 3, 3, 3, 3, 0, 3, 3, 3, 0, 3, 3, 3, 0, 3, 3, 3, 0, 3, 3, 3, 0, 3, 3, 3, 0, 3, 3, 3, 0, 3, 3, 3],
+    "m3": [21, 22, 20, 22, 14, 22, 20, 22, 13, 22, 20, 22, 13, 20, 20, 22, 14, 13, 20, 22, 14, 23, 20, 22, 0, 23, 3, 15, 13, 15, 3, 15, 13, 15, 3, 15, 14, 15, 3, 15, 13, 15, 3, 15, 13, 15, 3, 15, 13, 15],
+    "m8": [14, 20, 0, 20, 14, 20, 0, 20, 3, 20, 0, 20, 20, 20, 0, 20, 20, 20, 0, 20, 14, 20, 0, 20, 14, 20, 0, 20, 14, 3, 0, 20, 0, 20, 0, 20, 3, 0, 20, 14, 3, 20, 13, 3, 0, 20, 13, 3, 3, 20, 3, 3, 0, 20, 20, 3, 3, 20, 3, 3, 0, 20, 3, 3, 3, 20, 20, 3, 0, 20, 3, 3],
 }
 
 

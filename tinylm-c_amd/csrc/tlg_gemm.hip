@@ -281,20 +281,55 @@ __device__ __forceinline__ void tile_accumulate(float *__restrict__ smem, const 
     // st % NR.  Step st prefetches stage st+NR into the set stage st came
     // from, computes stage st, then moves stage st+1 from its register set
     // into the other LDS buffer.  NR = 3 keeps loads three stages ahead.
+    //
+    // Two loop forms, chosen by measurement on MI355X (m3 GEMM set 1.544 ->
+    // 1.51 ms, nano 0.130 -> 0.120 ms, m8 unchanged):
+    // * WK > 1 (the waves split each stage): whole rounds of NR steps with no
+    //   branch inside, the store of stage st+1 unconditional (past the last
+    //   stage it stores the clamped re-read, which nothing reads; the final
+    //   barrier orders it before the caller reuses the LDS), and a scheduling
+    //   fence that keeps a step's loads ahead of its fragment reads and MFMAs
+    //   (left alone the scheduler issues them after the MFMAs, their registers
+    //   doubling as fragment registers).  A guarded step or store would give
+    //   the loop header a predecessor with the other register set's loads
+    //   outstanding, and the compiler then waits for every load in flight --
+    //   the prefetch one step old included -- before each round's first
+    //   fragment read.
+    // * WK = 1: the guarded form, whose interleaving measured 1-4 % faster on
+    //   these tiles despite that wait; the fence, or a fence before the store
+    //   as well, cost up to 10 %.
     auto step = [&](int st, auto &lac, auto &lbc, auto &lan, auto &lbn) {
         lac.load(A, lda, i0, Mo, stage_r(st + T::NR), rend, tid);
         reprep(lac, st + 2 * T::NR);
         lbc.load(B, ldb, j0, No, stage_r(st + T::NR), rend, tid, B2);
+        if constexpr (T::WK > 1) __builtin_amdgcn_sched_barrier(0);
         float *cur = smem + (st & 1) * (SA + SB);
         compute(cur, cur + SA);
-        if (st + 1 < nsteps) {
+        if (T::WK > 1 || st + 1 < nsteps) {
             float *nxt = smem + ((st + 1) & 1) * (SA + SB);
             lan.store(nxt, tid);
             lbn.store(nxt + SA, tid);
         }
         __syncthreads();
     };
-    if constexpr (T::NR == 2) {
+    if constexpr (T::WK > 1) {
+        int st = 0;
+        if constexpr (T::NR == 2) {
+            for (; st + 1 < nsteps; st += 2) {
+                step(st, la0, lb0, la1, lb1);
+                step(st + 1, la1, lb1, la0, lb0);
+            }
+            if (st < nsteps) step(st, la0, lb0, la1, lb1);
+        } else {
+            for (; st + 2 < nsteps; st += 3) {
+                step(st, la0, lb0, la1, lb1);
+                step(st + 1, la1, lb1, la2, lb2);
+                step(st + 2, la2, lb2, la0, lb0);
+            }
+            if (st < nsteps) step(st, la0, lb0, la1, lb1);
+            if (st + 1 < nsteps) step(st + 1, la1, lb1, la2, lb2);
+        }
+    } else if constexpr (T::NR == 2) {
         for (int st = 0; st < nsteps; st += 2) {
             step(st, la0, lb0, la1, lb1);
             if (st + 1 < nsteps) step(st + 1, la1, lb1, la0, lb0);
@@ -896,6 +931,8 @@ static const TileCfg kCfgs[] = {
     {64, 64, 16, 2, 1},     // 19: same, loads three stages ahead
     {64, 64, 32, 2, 2, 8},  // 20: 8 waves, 32x32 per wave, half of each stage
     {64, 32, 64, 2, 2},     // 21: 32x32 per wave, half of each 64-step stage
+    {64, 64, 64, 2, 4, 16}, // 22: 16 waves, 32x32 per wave, a quarter of each 64-step stage
+    {64, 64, 64, 2, 2, 8},  // 23: 8 waves, 32x32 per wave, half of each 64-step stage
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
 using T0 = Tile<128, 128, 16, 2, 1>;
@@ -921,6 +958,8 @@ using T18 = Tile<64, 64, 16, 2, 1, 2, 0, 4>;
 using T19 = Tile<64, 64, 16, 2, 1, 3, 0, 4>;
 using T20 = Tile<64, 64, 32, 2, 2, 2, 0, 8>;
 using T21 = Tile<64, 32, 64, 2, 2, 2, 0, 4>;
+using T22 = Tile<64, 64, 64, 2, 4, 2, 0, 16>;
+using T23 = Tile<64, 64, 64, 2, 2, 2, 0, 8>;
 
 template <class T, int LA, int LB>
 static void launch_t(const GemmArgs &a, int grid, bool vec, hipStream_t st)
@@ -1239,6 +1278,8 @@ static void launch_group(int ci, const GroupArgs &a, int grid, hipStream_t st)
     case 19: lgroup<T19>(a, grid, st); break;
     case 20: lgroup<T20>(a, grid, st); break;
     case 21: lgroup<T21>(a, grid, st); break;
+    case 22: lgroup<T22>(a, grid, st); break;
+    case 23: lgroup<T23>(a, grid, st); break;
     default: lgroup<T3>(a, grid, st); break;
     }
     g_group_last = ci;
@@ -1291,6 +1332,8 @@ const char *tlg_group_kernel_name(void)
     case 19: return "k_group<Tile<64, 64, 16, 2, 1, 3, 0, 4> >";
     case 20: return "k_group<Tile<64, 64, 32, 2, 2, 2, 0, 8> >";
     case 21: return "k_group<Tile<64, 32, 64, 2, 2, 2, 0, 4> >";
+    case 22: return "k_group<Tile<64, 64, 64, 2, 4, 2, 0, 16> >";
+    case 23: return "k_group<Tile<64, 64, 64, 2, 2, 2, 0, 8> >";
     default: return "k_group<Tile<64, 64, 32, 2, 1, 2, 0, 4> >";
     }
 }
