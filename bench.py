@@ -167,32 +167,47 @@ def read_traffic(kernel):
 
 
 AUTOTUNE_CANDS = (3, 14, 13, 15, 0, 1, 20, 21, 22, 23)
+# split targets tried with each tile candidate (tlg_tune_group_split: reduction
+# steps per split work item of the mm_atb problems; 0 = the library's rule)
+AUTOTUNE_RTS = (0, 256, 512, 1024, 2048, 4096)
 
-# Tile configuration of every grouped launch of each training step: per launch
-# the choice tl_run_autotune made most often over 3 timing runs (10 timed
-# steps per candidate each; ties to the fastest run) on an MI355X, with the
-# candidates above plus 4 and 8 (never picked).  A fixed table keeps the step's kernels --
-# and so the roofline kernel and its rocprofv3 profiles -- the same from box
-# to box; --autotune re-times the candidates instead.
+# Tile configuration and split target of every grouped launch of each training
+# step: per launch the configuration tl_run_autotune_split chose most often
+# over 3 timing runs on an MI355X (10 timed steps per (configuration, split
+# target) pair, split targets 0, 256, 512, 1024, 2048 and 4096; ties to the
+# fastest run), and the split target those runs chose most often with it.  A
+# split target only changes launches with mm_atb problems (the backward ones);
+# elsewhere it is whatever the timing noise picked.  A fixed table keeps the
+# step's kernels -- and so the roofline kernel and its rocprofv3 profiles --
+# the same from box to box; --autotune re-times the candidates instead.
 TUNED = {
-    "nano": [15, 15, 14, 15, 3, 15, 15, 15, 15, 15],
-    "m3": [21, 22, 20, 22, 14, 22, 20, 22, 13, 22, 20, 22, 13, 20, 20, 22, 14, 13, 20, 22, 14, 23, 20, 22, 0, 23, 3, 15, 13, 15, 3, 15, 13, 15, 3, 15, 14, 15, 3, 15, 13, 15, 3, 15, 13, 15, 3, 15, 13, 15],
-    "m8": [14, 20, 0, 20, 14, 20, 0, 20, 3, 20, 0, 20, 20, 20, 0, 20, 20, 20, 0, 20, 14, 20, 0, 20, 14, 20, 0, 20, 14, 3, 0, 20, 0, 20, 0, 20, 3, 0, 20, 14, 3, 20, 13, 3, 0, 20, 13, 3, 3, 20, 3, 3, 0, 20, 20, 3, 3, 20, 3, 3, 0, 20, 3, 3, 3, 20, 20, 3, 0, 20, 3, 3],
+    "nano": [15, 15, 13, 15, 3, 15, 15, 15, 15, 15],
+    "m3": [14, 22, 3, 22, 14, 20, 3, 22, 14, 22, 3, 22, 14, 20, 3, 22, 14, 20, 3, 22, 14, 20, 3, 22, 3, 20, 20, 20, 14, 3, 3, 3, 13, 3, 3, 3, 13, 15, 3, 3, 13, 3, 3, 3, 13, 15, 3, 3, 13, 3],
+    "m8": [14, 20, 0, 20, 14, 20, 0, 20, 14, 20, 0, 20, 14, 20, 0, 20, 14, 20, 0, 20, 14, 20, 0, 20, 14, 20, 0, 20, 14, 20, 0, 20, 0, 20, 0, 20, 3, 0, 20, 3, 3, 3, 3, 3, 3, 20, 3, 3, 3, 20, 3, 3, 3, 20, 3, 3, 3, 20, 3, 3, 3, 20, 3, 3, 3, 20, 3, 3, 3, 20, 3, 3],
+}
+# (0 = the library's automatic rule)
+SPLITS = {
+    "nano": [1024, 1024, 1024, 512, 0, 1024, 512, 256, 256, 256],
+    "m3": [0, 2048, 1024, 1024, 512, 1024, 1024, 1024, 4096, 4096, 256, 512, 4096, 1024, 256, 0, 4096, 1024, 1024, 2048, 256, 1024, 256, 512, 256, 1024, 1024, 512, 0, 256, 512, 512, 0, 256, 512, 512, 0, 512, 512, 512, 0, 256, 512, 512, 0, 512, 512, 512, 0, 256],
+    "m8": [4096, 2048, 0, 4096, 256, 4096, 1024, 4096, 256, 2048, 0, 256, 256, 2048, 1024, 2048, 0, 2048, 0, 1024, 512, 512, 0, 512, 4096, 4096, 0, 1024, 256, 256, 1024, 4096, 1024, 4096, 512, 2048, 256, 1024, 2048, 256, 1024, 1024, 256, 512, 1024, 0, 256, 512, 1024, 4096, 256, 512, 1024, 4096, 256, 512, 1024, 4096, 256, 512, 1024, 4096, 256, 512, 1024, 4096, 256, 512, 1024, 4096, 256, 512],
 }
 
 
 def apply_tiles(lib, host, run, stream, name, retime=False, reps=3):
-    """Set each grouped launch's tile configuration (the TUNED table, or a
-    fresh timing when retime or the table does not fit); returns {config:
-    launches}."""
+    """Set each grouped launch's tile configuration and split target (the
+    TUNED and SPLITS tables, or a fresh timing when retime or a table does
+    not fit); returns {config: launches}."""
     L = host.dll.tl_run_grouped_launches(run)
-    table = TUNED.get(name)
-    if retime or table is None or len(table) != L:
+    table, splits = TUNED.get(name), SPLITS.get(name)
+    if retime or table is None or len(table) != L or splits is None or len(splits) != L:
         arr = (ctypes.c_int * len(AUTOTUNE_CANDS))(*AUTOTUNE_CANDS)
-        check(host.dll.tl_run_autotune(run, arr, len(AUTOTUNE_CANDS), reps, stream), "autotune")
+        rts = (ctypes.c_int * len(AUTOTUNE_RTS))(*AUTOTUNE_RTS)
+        check(host.dll.tl_run_autotune_split(run, arr, len(AUTOTUNE_CANDS), rts, len(AUTOTUNE_RTS), reps, stream),
+              "autotune")
     else:
-        for k, c in enumerate(table):
+        for k, (c, rt) in enumerate(zip(table, splits)):
             check(host.dll.tl_run_set_launch_config(run, k, c), "set tile config")
+            check(host.dll.tl_run_set_launch_split(run, k, rt), "set split target")
     picks = {}
     for k in range(L):
         c = host.dll.tl_run_launch_config(run, k)
@@ -520,7 +535,8 @@ def bench_full_step(lib, host, stream, name, steps, warmup=3, eager=False, tune=
     loss0 = tr.loss(stream)
     # per grouped launch, the fastest tile configuration (forward + backward
     # passes only: the parameters stay as the first step left them)
-    tiles = tr.autotune(list(AUTOTUNE_CANDS), 3, stream) if tune else None
+    tiles = tr.autotune(list(AUTOTUNE_CANDS), 3, stream, AUTOTUNE_RTS) if tune else None
+    splits = tr.splits() if tune else None
     phases = tr.time_phases(stream)
     if eager:                                       # kernel by kernel (profilers trace these)
         run = lambda: tr.step(stream)  # noqa: E731
@@ -539,8 +555,9 @@ def bench_full_step(lib, host, stream, name, steps, warmup=3, eager=False, tune=
                                 "gradnorm_adamw": round(phases[2], 4)},
             "loss_first": round(loss0, 4), "loss_after": round(loss1, 4),
             "launch": "enqueued step by step" if eager else "one HIP graph per step",
-            "tiles": ("per grouped launch, tl_train_autotune over " + str(list(AUTOTUNE_CANDS)) + ": "
-                      + str(tiles)) if tune else "the library's automatic policy"}
+            "tiles": ("per grouped launch, tl_train_autotune_split over " + str(list(AUTOTUNE_CANDS)) + " x split "
+                      "targets " + str(list(AUTOTUNE_RTS)) + ": " + str(tiles) + ", targets " + str(splits))
+                     if tune else "the library's automatic policy"}
 
 
 DECODE_MODEL = dict(V=2048, D=384, L=8, H=12, KV=3, F=1024, T=256)

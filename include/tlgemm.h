@@ -153,6 +153,12 @@ int tlg_tune_group(int cfg);
  * 0 keeps the list), min_waves (<= 0 keeps it) and the target reduction
  * steps per split work item (0 keeps it).  Applies to later launches. */
 int tlg_tune_group_policy(const int *cands, int ncands, double min_waves, int rtarget);
+/* Tuning hook: pin the target reduction steps per work item of the split
+ * (mm_atb) problems of later grouped launches: >= 64 splits every long
+ * reduction into pieces of about that many steps; 0 restores the automatic
+ * target (the launch's longest unsplit reduction, at least the policy's).
+ * The split partials are summed in split order either way. */
+int tlg_tune_group_split(int rtarget);
 
 /* ---- top-1 mixture-of-experts FFN --------------------------------------- */
 /* The MoE layer of tinylm.c with K = 1 routing and no router bias (the

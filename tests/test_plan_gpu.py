@@ -165,6 +165,45 @@ def test_group_tile_configs(lib, orc, gcfg):
             assert normwise_rel(got[bname][a:b], init[bname][a:b]) <= TOL, (gcfg, label)
 
 
+@pytest.mark.parametrize("cfg,rt", [(3, 64), (15, 256), (22, 512), (20, 2048), (14, 8192)])
+def test_split_targets_keep_results(lib, orc, cfg, rt):
+    """A pinned split target (tl_run_set_launch_split) changes only how the
+    mm_atb reductions are cut into work items (from 32 pieces of 64 rows to
+    none, over the nano step's 2048-row dW reductions): the step still meets
+    the bar against the oracle, and an eager step and a graph replay agree bit
+    for bit."""
+    host = tlgemm.host()
+    plan = host.plan_train(**bench.TRAIN["nano"])
+    run, stream = new_run(lib, host, plan, seed=cfg)
+    try:
+        L = host.dll.tl_run_grouped_launches(run)
+        for k in range(L):
+            assert host.dll.tl_run_set_launch_config(run, k, cfg) == 0
+            assert host.dll.tl_run_set_launch_split(run, k, rt) == 0
+        assert host.dll.tl_run_set_launch_split(run, 0, 63) != 0        # below the minimum
+        assert host.dll.tl_run_launch_split(run, 0) == rt
+        init = snapshot(lib, host, plan, run, stream)
+        lib.check(host.dll.tl_run_step_grouped(run, stream), "step")
+        got = snapshot(lib, host, plan, run, stream)
+        fill(lib, host, plan, run, stream, cfg)
+        lib.check(host.dll.tl_run_graph_build(run, stream, 1), "graph")
+        fill(lib, host, plan, run, stream, cfg)
+        lib.check(host.dll.tl_run_graph_step(run, stream), "replay")
+        replay = snapshot(lib, host, plan, run, stream)
+    finally:
+        host.dll.tl_run_free(run)
+    run_plan_cpu(plan, init, orc)
+    for bname, _, _ in plan.bufs:
+        assert np.array_equal(got[bname], replay[bname]), bname
+        for label, a, b in plan.regions(bname):
+            assert normwise_rel(got[bname][a:b], init[bname][a:b]) <= TOL, (cfg, rt, label)
+
+
+def test_split_target_hook_rejects_small_targets(lib):
+    assert lib.tlg_tune_group_split(63) != 0
+    assert lib.tlg_tune_group_split(0) == 0
+
+
 def test_autotuned_step_matches_oracle(lib, orc):
     """tl_run_autotune gives each grouped launch its own tile shape; the
     mixed step (eager and replayed from a graph) still meets the bar."""

@@ -1217,6 +1217,7 @@ static int g_ws_half = 0;
 // TLG_GROUP_RTARGET (or tlg_tune_group_policy) override the policy,
 // tlg_tune_group pins one shape.
 static int g_group_cfg = -1;
+static int g_group_rt = 0;               // split target pinned for the next launches (tlg_tune_group_split)
 static double g_min_waves = 3.0;
 static int g_cand[4] = {3, 14, -1, -1};   // 64x64, then 64x32 (2 x 2 waves)
 static int g_rtarget = 512;
@@ -1308,6 +1309,14 @@ extern "C" int tlg_tune_group(int cfg)
     if (cfg != -1 && cfg != 0 && cfg != 1 && cfg != 3 && cfg != 4 && (cfg < 8 || cfg >= kNumCfgs))
         return tlg_fail(TLG_EINVAL, "tlg_tune_group: config %d", cfg);
     g_group_cfg = cfg;
+    return TLG_OK;
+}
+
+extern "C" int tlg_tune_group_split(int rtarget)
+{
+    if (rtarget != 0 && rtarget < 64)
+        return tlg_fail(TLG_EINVAL, "tlg_tune_group_split: target %d (0 or >= 64)", rtarget);
+    g_group_rt = rtarget;
     return TLG_OK;
 }
 
@@ -1565,7 +1574,8 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
         if (c.op != 2 && R > rmax) rmax = R;
     }
     // split problems aim for about the per-item work of the unsplit ones
-    const int rtarget = rmax > g_rtarget ? rmax : g_rtarget;
+    // (or the pinned target)
+    const int rtarget = g_group_rt > 0 ? g_group_rt : rmax > g_rtarget ? rmax : g_rtarget;
 
     // tile shape: pinned, or the largest with >= g_min_waves waves of items
     int ci = g_group_cfg;

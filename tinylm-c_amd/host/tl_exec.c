@@ -32,6 +32,9 @@ struct TlRun {
     /* tile configuration of each grouped launch: 0 = the library's automatic
      * policy, else config + 1 (set by tl_run_autotune) */
     int lcfg[TL_MAXLAUNCH];
+    /* split target of each grouped launch (tlg_tune_group_split; 0 = the
+     * library's automatic target) */
+    int lrt[TL_MAXLAUNCH];
 };
 
 static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -207,9 +210,12 @@ static int group_launch(TlRun *r, Group *g, void *stream, int dry, int *launches
     int rc = dry ? 0 : mark(r, *launches, stream);
     if (!rc && !dry) {
         const int cfg = *launches < TL_MAXLAUNCH ? r->lcfg[*launches] - 1 : -1;
+        const int rt = *launches < TL_MAXLAUNCH ? r->lrt[*launches] : 0;
         if (cfg >= 0) rc = tlg_tune_group(cfg);
+        if (!rc && rt) rc = tlg_tune_group_split(rt);
         if (!rc) rc = tlg_dev_gemm_group(g->call, g->n, stream);
         if (cfg >= 0) { const int rc2 = tlg_tune_group(-1); if (!rc) rc = rc2; }
+        if (rt) { const int rc2 = tlg_tune_group_split(0); if (!rc) rc = rc2; }
     }
     if (!rc && !dry && *launches < TL_MAXLAUNCH) r->lname[*launches] = tlg_group_kernel();
     (*launches)++;
@@ -412,25 +418,38 @@ int tl_run_graph_step(TlRun *r, void *stream)
     return rc;
 }
 
-/* Per-launch tile choice by measurement: run `reps` timed steps with every
- * candidate configuration applied to all grouped launches, then give each
- * launch the candidate with the least time.  Numerically every candidate is
- * a valid schedule of the same sums (the plan tests cover each one). */
+/* Per-launch tile and split choice by measurement: run `reps` timed steps
+ * with every (configuration, split target) candidate pair applied to all
+ * grouped launches, then give each launch the pair with the least time.
+ * Numerically every candidate is a valid schedule of the same sums (the plan
+ * tests cover each one).  A launch's split target also moves work into the
+ * next launch (its partials are summed there), which the per-launch times
+ * see as they come. */
 int tl_run_autotune(TlRun *r, const int *cands, int ncands, int reps, void *stream)
 {
-    if (!r || !cands || ncands <= 0 || reps <= 0) return -1;
+    const int policy = 0;
+    return tl_run_autotune_split(r, cands, ncands, &policy, 1, reps, stream);
+}
+
+int tl_run_autotune_split(TlRun *r, const int *cands, int ncands, const int *rts, int nrts, int reps,
+                          void *stream)
+{
+    if (!r || !cands || ncands <= 0 || !rts || nrts <= 0 || reps <= 0) return -1;
+    for (int s = 0; s < nrts; s++)
+        if (rts[s] != 0 && rts[s] < 64) return -1;
     const int L = grouped(r, stream, 1);
     if (L < 0 || L + 2 > TL_MAXLAUNCH) return -1;
     double *best = malloc(sizeof(double) * (size_t)L);
     void **ev = malloc(sizeof(void *) * (size_t)(L + 2));
-    int *pick = malloc(sizeof(int) * (size_t)L);
-    if (!best || !ev || !pick) { free(best); free(ev); free(pick); return TLG_ENOMEM; }
+    int *pick = malloc(sizeof(int) * (size_t)L), *prt = malloc(sizeof(int) * (size_t)L);
+    if (!best || !ev || !pick || !prt) { free(best); free(ev); free(pick); free(prt); return TLG_ENOMEM; }
     int rc = 0, made = 0;
     for (; made < L + 2; made++)
         if (!(ev[made] = tlg_event_create())) { rc = -1; break; }
-    for (int k = 0; k < L; k++) { best[k] = 1e30; pick[k] = 0; }
-    for (int c = 0; c < ncands && !rc; c++) {
-        for (int k = 0; k < L; k++) r->lcfg[k] = cands[c] + 1;
+    for (int k = 0; k < L; k++) { best[k] = 1e30; pick[k] = 0; prt[k] = 0; }
+    for (int cs = 0; cs < ncands * nrts && !rc; cs++) {
+        const int c = cs / nrts, rt = rts[cs % nrts];
+        for (int k = 0; k < L; k++) { r->lcfg[k] = cands[c] + 1; r->lrt[k] = rt; }
         double *t = calloc((size_t)L, sizeof(double));
         if (!t) { rc = TLG_ENOMEM; break; }
         rc = tl_run_step_grouped(r, stream);                /* warm up this shape */
@@ -440,12 +459,12 @@ int tl_run_autotune(TlRun *r, const int *cands, int ncands, int reps, void *stre
             for (int k = 0; k < L && !rc; k++) t[k] += tlg_event_elapsed_ms(ev[k], ev[k + 1]);
         }
         for (int k = 0; k < L && !rc; k++)
-            if (r->lkind[k] == 0 && t[k] < best[k]) { best[k] = t[k]; pick[k] = cands[c] + 1; }
+            if (r->lkind[k] == 0 && t[k] < best[k]) { best[k] = t[k]; pick[k] = cands[c] + 1; prt[k] = rt; }
         free(t);
     }
-    for (int k = 0; k < L; k++) r->lcfg[k] = rc ? 0 : pick[k];
+    for (int k = 0; k < L; k++) { r->lcfg[k] = rc ? 0 : pick[k]; r->lrt[k] = rc ? 0 : prt[k]; }
     for (int k = 0; k < made; k++) tlg_event_destroy(ev[k]);
-    free(best); free(ev); free(pick);
+    free(best); free(ev); free(pick); free(prt);
     return rc;
 }
 
@@ -460,4 +479,17 @@ int tl_run_launch_config(TlRun *r, int k)
 {
     if (!r || k < 0 || k >= TL_MAXLAUNCH) return -1;
     return r->lcfg[k] - 1;
+}
+
+int tl_run_set_launch_split(TlRun *r, int k, int rtarget)
+{
+    if (!r || k < 0 || k >= TL_MAXLAUNCH || (rtarget != 0 && rtarget < 64)) return -1;
+    r->lrt[k] = rtarget;
+    return 0;
+}
+
+int tl_run_launch_split(TlRun *r, int k)
+{
+    if (!r || k < 0 || k >= TL_MAXLAUNCH) return -1;
+    return r->lrt[k];
 }

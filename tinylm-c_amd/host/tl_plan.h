@@ -121,6 +121,15 @@ int    tl_run_launch_config(TlRun *r, int k);
 /* Pin launch k's tile configuration (an index of the library's tile table,
  * -1 = the automatic policy): a tuned table applied without re-timing. */
 int    tl_run_set_launch_config(TlRun *r, int k, int cfg);
+/* The same with split targets as well: every (cands[c], rts[s]) pair is
+ * timed (rts: target reduction steps per split work item, tlg_tune_group_split
+ * values; 0 = the library's automatic target), each launch keeping its
+ * fastest pair; tl_run_autotune is this with rts = {0}.  tl_run_launch_split
+ * reports launch k's target, tl_run_set_launch_split pins it. */
+int    tl_run_autotune_split(TlRun *r, const int *cands, int ncands, const int *rts, int nrts, int reps,
+                             void *stream);
+int    tl_run_launch_split(TlRun *r, int k);
+int    tl_run_set_launch_split(TlRun *r, int k, int rtarget);
 /* Capture one step into a HIP graph and replay it (grouped != 0: the grouped
  * step, else call by call).  The graph is bound to
  * the pool copy current at capture; tl_run_graph_step replays the graph for

@@ -44,8 +44,9 @@ struct TlTrain {
     float hyper_host[8];
     void *graph;
     /* per grouped GEMM launch of a step, in call order: tile configuration + 1
-     * (0 = the library's automatic policy); tl_train_autotune fills it */
-    int gi, lcfg[TL_TRAIN_MAXG];
+     * (0 = the library's automatic policy) and split target (0 = automatic);
+     * tl_train_autotune(_split) fills them */
+    int gi, lcfg[TL_TRAIN_MAXG], lrt[TL_TRAIN_MAXG];
     void **tev;                         /* timing events (autotune only): 2 per launch */
     int tcap;
 };
@@ -284,13 +285,19 @@ static int group(TlTrain *t, const TlgGemmCall *cs, int n, void *st)
 {
     const int k = t->gi++;
     const int cfg = k < TL_TRAIN_MAXG ? t->lcfg[k] : 0;
+    const int rt = k < TL_TRAIN_MAXG ? t->lrt[k] : 0;
     const int timed = t->tev && k < t->tcap;
     int rc = cfg > 0 ? tlg_tune_group(cfg - 1) : 0;
+    if (!rc && rt) rc = tlg_tune_group_split(rt);
     if (!rc && timed) rc = tlg_event_record(t->tev[2 * k], st);
     if (!rc) rc = tlg_dev_gemm_group(cs, n, st);
     if (!rc && timed) rc = tlg_event_record(t->tev[2 * k + 1], st);
     if (cfg > 0) {
         const int r2 = tlg_tune_group(-1);
+        if (!rc) rc = r2;
+    }
+    if (rt) {
+        const int r2 = tlg_tune_group_split(0);
         if (!rc) rc = r2;
     }
     return rc;
@@ -457,27 +464,39 @@ int tl_train_graph_step(TlTrain *t, void *st)
     return tlg_graph_launch(t->graph, st);
 }
 
-/* Per grouped launch, the fastest of `cands` over `reps` timed forward +
- * backward passes (P, M and V are not touched; G and the activations are). */
+/* Per grouped launch, the fastest of `cands` (with each split target of rts)
+ * over `reps` timed forward + backward passes (P, M and V are not touched; G
+ * and the activations are). */
 int tl_train_autotune(TlTrain *t, const int *cands, int ncands, int reps, void *st)
 {
-    if (!t || !cands || ncands <= 0 || reps <= 0) return TLG_EINVAL;
+    const int policy = 0;
+    return tl_train_autotune_split(t, cands, ncands, &policy, 1, reps, st);
+}
+
+int tl_train_autotune_split(TlTrain *t, const int *cands, int ncands, const int *rts, int nrts, int reps,
+                            void *st)
+{
+    if (!t || !cands || ncands <= 0 || !rts || nrts <= 0 || reps <= 0) return TLG_EINVAL;
     for (int c = 0; c < ncands; c++)
         if (cands[c] < 0) return TLG_EINVAL;
+    for (int s = 0; s < nrts; s++)
+        if (rts[s] != 0 && rts[s] < 64) return TLG_EINVAL;
     memset(t->lcfg, 0, sizeof t->lcfg);
+    memset(t->lrt, 0, sizeof t->lrt);
     CK(tl_train_forward(t, st));                  /* counts the launches, sizes the scratch */
     CK(tl_train_backward(t, st));
     const int ng = t->gi;
     if (ng <= 0 || ng > TL_TRAIN_MAXG) return TLG_EINVAL;
     void **ev = calloc((size_t)2 * ng, sizeof(void *));
     double *best = malloc(sizeof(double) * (size_t)ng), *acc = malloc(sizeof(double) * (size_t)ng);
-    int *pick = calloc((size_t)ng, sizeof(int));
-    int rc = (!ev || !best || !acc || !pick) ? TLG_ENOMEM : 0;
+    int *pick = calloc((size_t)ng, sizeof(int)), *prt = calloc((size_t)ng, sizeof(int));
+    int rc = (!ev || !best || !acc || !pick || !prt) ? TLG_ENOMEM : 0;
     for (int i = 0; !rc && i < 2 * ng; i++)
         if (!(ev[i] = tlg_event_create())) rc = TLG_EHIP;
     for (int k = 0; k < ng && best; k++) best[k] = 1e30;
-    for (int c = 0; !rc && c < ncands; c++) {
-        for (int k = 0; k < ng; k++) t->lcfg[k] = cands[c] + 1;
+    for (int cs = 0; !rc && cs < ncands * nrts; cs++) {
+        const int c = cs / nrts, rt = rts[cs % nrts];
+        for (int k = 0; k < ng; k++) { t->lcfg[k] = cands[c] + 1; t->lrt[k] = rt; }
         t->tev = NULL;
         rc = tl_train_forward(t, st);            /* warm this shape up */
         if (!rc) rc = tl_train_backward(t, st);
@@ -495,16 +514,31 @@ int tl_train_autotune(TlTrain *t, const int *cands, int ncands, int reps, void *
             }
         }
         for (int k = 0; !rc && k < ng; k++)
-            if (acc[k] < best[k]) { best[k] = acc[k]; pick[k] = cands[c] + 1; }
+            if (acc[k] < best[k]) { best[k] = acc[k]; pick[k] = cands[c] + 1; prt[k] = rt; }
     }
     t->tev = NULL;
     t->tcap = 0;
-    if (!rc) memcpy(t->lcfg, pick, sizeof(int) * (size_t)ng);
-    else memset(t->lcfg, 0, sizeof t->lcfg);
+    if (!rc) {
+        memcpy(t->lcfg, pick, sizeof(int) * (size_t)ng);
+        memcpy(t->lrt, prt, sizeof(int) * (size_t)ng);
+    } else {
+        memset(t->lcfg, 0, sizeof t->lcfg);
+        memset(t->lrt, 0, sizeof t->lrt);
+    }
     for (int i = 0; ev && i < 2 * ng; i++)
         if (ev[i]) tlg_event_destroy(ev[i]);
-    free(ev); free(best); free(acc); free(pick);
+    free(ev); free(best); free(acc); free(pick); free(prt);
     return rc;
+}
+
+int tl_train_splits(const TlTrain *t, int *rt, int cap)
+{
+    int n = 0;
+    for (int k = 0; k < TL_TRAIN_MAXG && k < cap; k++) {
+        rt[k] = t->lrt[k];
+        if (t->lcfg[k]) n = k + 1;
+    }
+    return n;
 }
 
 int tl_train_tiles(const TlTrain *t, int *cfg, int cap)

@@ -81,6 +81,13 @@ int  tl_train_time_phases(TlTrain *t, float *ms, void *stream);
 #define TL_TRAIN_MAXG 512
 int  tl_train_autotune(TlTrain *t, const int *cands, int ncands, int reps, void *stream);
 int  tl_train_tiles(const TlTrain *t, int *cfg, int cap);
+/* The same with split targets (tlg_tune_group_split values, 0 = automatic):
+ * every (cands[c], rts[s]) pair is timed and each launch keeps its fastest
+ * pair; tl_train_autotune is this with rts = {0}.  tl_train_splits copies the
+ * split targets as tl_train_tiles copies the configurations. */
+int  tl_train_autotune_split(TlTrain *t, const int *cands, int ncands, const int *rts, int nrts, int reps,
+                             void *stream);
+int  tl_train_splits(const TlTrain *t, int *rt, int cap);
 
 #ifdef __cplusplus
 }

@@ -64,6 +64,7 @@ SIGNATURES = {
     "tlg_group_kernel": (ctypes.c_char_p, []),
     "tlg_tune_group": (_i, [_i]),
     "tlg_tune_group_policy": (_i, [_ip, _i, ctypes.c_double, _i]),
+    "tlg_tune_group_split": (_i, [_i]),
     "tlg_graph_begin": (_i, [_vp]),
     "tlg_graph_end": (_vp, [_vp]),
     "tlg_graph_launch": (_i, [_vp, _vp]),
@@ -371,16 +372,24 @@ class Train:
         self._ck(self.host.dll.tl_train_time_phases(self.h, ms, stream), "tl_train_time_phases")
         return list(ms)
 
-    def autotune(self, cands, reps, stream):
+    def autotune(self, cands, reps, stream, rts=(0,)):
         """Per grouped launch of the step, the fastest tile configuration of
-        `cands` (tl_train_autotune); returns the chosen table."""
+        `cands`, with each split target of `rts` (tl_train_autotune_split; 0 =
+        the library's automatic target); returns the chosen tile table."""
         arr = (ctypes.c_int * len(cands))(*cands)
-        self._ck(self.host.dll.tl_train_autotune(self.h, arr, len(cands), reps, stream), "tl_train_autotune")
+        rarr = (ctypes.c_int * len(rts))(*rts)
+        self._ck(self.host.dll.tl_train_autotune_split(self.h, arr, len(cands), rarr, len(rts), reps, stream),
+                 "tl_train_autotune_split")
         return self.tiles()
 
     def tiles(self):
         buf = (ctypes.c_int * 512)()
         n = self.host.dll.tl_train_tiles(self.h, buf, 512)
+        return list(buf[:n])
+
+    def splits(self):
+        buf = (ctypes.c_int * 512)()
+        n = self.host.dll.tl_train_splits(self.h, buf, 512)
         return list(buf[:n])
 
     def __del__(self):
@@ -590,6 +599,12 @@ class Host:
         d.tl_run_launch_config.restype = _i
         d.tl_run_set_launch_config.argtypes = [_vp, _i, _i]
         d.tl_run_set_launch_config.restype = _i
+        d.tl_run_autotune_split.argtypes = [_vp, _ip, _i, _ip, _i, _i, _vp]
+        d.tl_run_autotune_split.restype = _i
+        d.tl_run_launch_split.argtypes = [_vp, _i]
+        d.tl_run_launch_split.restype = _i
+        d.tl_run_set_launch_split.argtypes = [_vp, _i, _i]
+        d.tl_run_set_launch_split.restype = _i
         d.tl_run_launch_kernel.argtypes = [_vp, _i]
         d.tl_run_launch_kernel.restype = ctypes.c_char_p
         d.tl_run_call.argtypes = [_vp, _i, _vp]
@@ -621,6 +636,9 @@ class Host:
         d.tl_train_time_phases.argtypes = [_vp, ctypes.POINTER(ctypes.c_float), _vp]
         d.tl_train_autotune.argtypes = [_vp, ctypes.POINTER(ctypes.c_int), _i, _i, _vp]
         d.tl_train_tiles.argtypes = [_vp, ctypes.POINTER(ctypes.c_int), _i]
+        d.tl_train_autotune_split.argtypes = [_vp, ctypes.POINTER(ctypes.c_int), _i, ctypes.POINTER(ctypes.c_int),
+                                              _i, _i, _vp]
+        d.tl_train_splits.argtypes = [_vp, ctypes.POINTER(ctypes.c_int), _i]
         # host/tl_decode.h
         d.tl_decode_new.argtypes = [ctypes.POINTER(TlModel), _i, _i, _i, _i, _i, _i]
         d.tl_decode_new.restype = _vp
