@@ -1161,22 +1161,27 @@ __global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_fwd4(const float *__res
 // dQ for the same items; also writes Dq = dO . O per (row, head) for the
 // dK / dV kernel.
 // dS = P (dP - Dq) scale, dQ = dS K (attn_bwd, :750-768).
-template <bool ROPE>
-__global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_dq4(const float *__restrict__ q, const float *__restrict__ k,
-                                                  const float *__restrict__ v, const float *__restrict__ o,
-                                                  const float *__restrict__ dout, const float *__restrict__ lse,
-                                                  float *__restrict__ Dq, float *__restrict__ dq, int B, int T, int H,
-                                                  int KV, int win, float scale, const float *__restrict__ cs,
-                                                  const float *__restrict__ sn)
+#define A4_DQ_LDS (2 * A4_CH * 32 * A4_LD + 4 * 32 * A4_LD)    // K, V staging + Q of 4 heads
+
+// One dQ item (a4_item's numbering) on `lds` (A4_DQ_LDS floats).  WDQ: also
+// store Dq (else it was computed before and the dK / dV items may read it).
+template <bool ROPE, bool WDQ>
+__device__ __forceinline__ void attn_dq4_item(float *__restrict__ lds, int item, const float *__restrict__ q,
+                                              const float *__restrict__ k, const float *__restrict__ v,
+                                              const float *__restrict__ o, const float *__restrict__ dout,
+                                              const float *__restrict__ lse, float *__restrict__ Dq,
+                                              float *__restrict__ dq, int B, int T, int H, int KV, int win,
+                                              float scale, const float *__restrict__ cs,
+                                              const float *__restrict__ sn)
 {
     // K and V staging in one array: its whole extent is the merge area later
-    __shared__ __attribute__((aligned(16))) float KVs[2 * A4_CH * 32 * A4_LD], Qs[4 * 32 * A4_LD];
+    float *KVs = lds, *Qs = lds + 2 * A4_CH * 32 * A4_LD;
     static_assert(2 * A4_CH * 32 * A4_LD >= 4 * (A4_KS - 1) * 18 * 64, "merge area");
     float *Ks = KVs, *Vs = KVs + A4_CH * 32 * A4_LD;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hs = wave & 3, ks = wave >> 2;
     const int nqb = (T + 31) >> 5;
     int b, kvh, h0, qb;
-    a4_item(blockIdx.x, B, H, KV, nqb, &b, &kvh, &h0, &qb);
+    a4_item(item, B, H, KV, nqb, &b, &kvh, &h0, &qb);
     const int h = h0 + hs, D = H * AT_HD;
     const int lq = lane & 31, hh = lane >> 5;
     const int qi = qb * 32 + lq;
@@ -1194,7 +1199,7 @@ __global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_dq4(const float *__rest
 #pragma unroll
     for (int i = 0; i < 16; i++) dd += dov[i] * ov[i];
     dd += __shfl_xor(dd, 32);
-    if (qok && hh == 0 && ks == 0) Dq[rh] = dd;
+    if (WDQ && qok && hh == 0 && ks == 0) Dq[rh] = dd;
     const float ls = qok ? lsv : 0.f;
     const float c2 = scale * 1.44269504088896341f;
     float qv[16];
@@ -1273,6 +1278,18 @@ __global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_dq4(const float *__rest
             f32x4{acc[4 * g4], acc[4 * g4 + 1], acc[4 * g4 + 2], acc[4 * g4 + 3]};
 }
 
+template <bool ROPE>
+__global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_dq4(const float *__restrict__ q, const float *__restrict__ k,
+                                                  const float *__restrict__ v, const float *__restrict__ o,
+                                                  const float *__restrict__ dout, const float *__restrict__ lse,
+                                                  float *__restrict__ Dq, float *__restrict__ dq, int B, int T, int H,
+                                                  int KV, int win, float scale, const float *__restrict__ cs,
+                                                  const float *__restrict__ sn)
+{
+    __shared__ __attribute__((aligned(16))) float lds[A4_DQ_LDS];
+    attn_dq4_item<ROPE, true>(lds, blockIdx.x, q, k, v, o, dout, lse, Dq, dq, B, T, H, KV, win, scale, cs, sn);
+}
+
 // dK / dV for H / KV a multiple of 4.  One workgroup of 8 waves per (b, KV
 // head, 32-key block), first key blocks first.  Per step the workgroup
 // stages two query blocks of one group of 4 heads in LDS -- q (rotated with
@@ -1332,21 +1349,24 @@ struct Dkv4Stage {
     }
 };
 
+#define A4_DKV_LDS (2 * A4_DKV_ST + 2 * 2 * 32 * 4)
+
+// One dK / dV item (key block item / (B KV), first ones first) on `Sm`
+// (A4_DKV_LDS floats): staged q, dO (2 query blocks x 4 heads) and lse / Dq;
+// the wave sums at the end reuse it.
 template <bool ROPE>
-__global__ __launch_bounds__(512) void k_attn_dkv4(const float *__restrict__ q, const float *__restrict__ k,
-                                                   const float *__restrict__ v, const float *__restrict__ dout,
-                                                   const float *__restrict__ lse, const float *__restrict__ Dq,
-                                                   float *__restrict__ dk, float *__restrict__ dv, int B, int T,
-                                                   int H, int KV, int win, float scale,
-                                                   const float *__restrict__ cs, const float *__restrict__ sn)
+__device__ __forceinline__ void attn_dkv4_item(float *__restrict__ Sm, int item, const float *__restrict__ q,
+                                               const float *__restrict__ k, const float *__restrict__ v,
+                                               const float *__restrict__ dout, const float *__restrict__ lse,
+                                               const float *__restrict__ Dq, float *__restrict__ dk,
+                                               float *__restrict__ dv, int B, int T, int H, int KV, int win,
+                                               float scale, const float *__restrict__ cs,
+                                               const float *__restrict__ sn)
 {
-    // staged q, dO (2 query blocks x 4 heads) and lse / Dq; the wave sums at the end reuse it
-    __shared__ __attribute__((aligned(16))) float Sm[2 * A4_DKV_ST + 2 * 2 * 32 * 4];
     static_assert(2 * A4_DKV_ST >= 8 * 2 * 16 * 64, "wave sums fit the staging area");
     float *Qs = Sm, *Ds = Sm + A4_DKV_ST, *LDs = Sm + 2 * A4_DKV_ST;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hs = wave & 3, qs = wave >> 2;
     const int nkb = (T + 31) >> 5;
-    const int item = blockIdx.x;
     const int kb = item / (B * KV), bkv = item % (B * KV);
     const int b = bkv / KV, kvh = bkv % KV, G = H / KV, HG = G / 4;
     const int KD = KV * AT_HD;
@@ -1455,6 +1475,58 @@ __global__ __launch_bounds__(512) void k_attn_dkv4(const float *__restrict__ q, 
         const int s = s0 + at_row(r, l);
         if (s < T) dv[obase + (size_t)s * KD + (l & 31)] = c;
     }
+}
+
+// Dq[row][h] = dO[row][h] . O[row][h] (attn_bwd's per-row term, tinylm.c:750-768)
+// in the dQ item's order: the two 16-term halves, then their sum.
+__global__ __launch_bounds__(256) void k_attn_delta(const float *__restrict__ dout, const float *__restrict__ o,
+                                                    float *__restrict__ Dq, int n)
+{
+    const int t = blockIdx.x * 256 + threadIdx.x;        // (row, head) = row * H + h
+    if (t >= n) return;
+    const f32x4 *a = reinterpret_cast<const f32x4 *>(dout + (size_t)t * AT_HD);
+    const f32x4 *c = reinterpret_cast<const f32x4 *>(o + (size_t)t * AT_HD);
+    float h2[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        float d = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const f32x4 x = a[4 * hh + j], y = c[4 * hh + j];
+            d += x[0] * y[0];
+            d += x[1] * y[1];
+            d += x[2] * y[2];
+            d += x[3] * y[3];
+        }
+        h2[hh] = d;
+    }
+    Dq[t] = h2[0] + h2[1];
+}
+
+// dQ and dK / dV in one launch, after k_attn_delta: workgroups
+// 0 .. nkb B KV - 1 take the dK / dV items (first key blocks first, the
+// longest), the rest the dQ items (last query blocks first, the longest).
+// The two kinds are long at opposite ends of the causal triangle, so CUs
+// freed by short dK / dV items start the long dQ items while the long dK /
+// dV items still run (as two launches: dQ 22 us, dK / dV 30 us per m3
+// layer).
+template <bool ROPE>
+__global__ __launch_bounds__(512) void k_attn_bwd4(const float *__restrict__ q, const float *__restrict__ k,
+                                                   const float *__restrict__ v, const float *__restrict__ o,
+                                                   const float *__restrict__ dout, const float *__restrict__ lse,
+                                                   const float *__restrict__ Dq, float *__restrict__ dq,
+                                                   float *__restrict__ dk, float *__restrict__ dv, int B, int T,
+                                                   int H, int KV, int win, float scale,
+                                                   const float *__restrict__ cs, const float *__restrict__ sn)
+{
+    static_assert(64 * 4 * A4_KS == 512, "both item kinds run 8 waves");
+    __shared__ __attribute__((aligned(16))) float lds[A4_DQ_LDS > A4_DKV_LDS ? A4_DQ_LDS : A4_DKV_LDS];
+    const int ndkv = ((T + 31) >> 5) * B * KV;
+    if ((int)blockIdx.x < ndkv)
+        attn_dkv4_item<ROPE>(lds, blockIdx.x, q, k, v, dout, lse, Dq, dk, dv, B, T, H, KV, win, scale, cs, sn);
+    else
+        attn_dq4_item<ROPE, false>(lds, blockIdx.x - ndkv, q, k, v, o, dout, lse, nullptr, dq, B, T, H, KV, win,
+                                   scale, cs, sn);
 }
 
 // ----------------------------------------------------------- elementwise --
@@ -1848,29 +1920,29 @@ static int attn_bwd_launch(const float *q, const float *k, const float *v, const
     const int nqb = (T + 31) / 32;
     hipStream_t st = ST(stream);
     float *Dq = (float *)ws;
-    if (g4) {
-        const dim3 grid(B * KV * (H / KV / 4) * nqb);
+    // the group dK / dV items read lse rows as float4 (4 heads)
+    if (g4 && cs && !al16(lse)) return tlg_fail(TLG_EINVAL, "attn_bwd_rope: lse must be 16-byte aligned");
+    if (g4 && al16(lse)) {
+        // Dq first; then the dK / dV and dQ items of every group in one launch
+        hipLaunchKernelGGL(k_attn_delta, dim3((B * T * H + 255) / 256), dim3(256), 0, st, datt, out, Dq, B * T * H);
+        const dim3 grid(nqb * B * KV + B * KV * (H / KV / 4) * nqb);
         if (cs)
-            hipLaunchKernelGGL(k_attn_dq4<true>, grid, dim3(256 * A4_KS), 0, st, q, k, v, out, datt, lse, Dq, dq, B, T, H, KV,
-                               win, scale, cs, sn);
+            hipLaunchKernelGGL(k_attn_bwd4<true>, grid, dim3(512), 0, st, q, k, v, out, datt, lse, (const float *)Dq,
+                               dq, dk, dv, B, T, H, KV, win, scale, cs, sn);
         else
-            hipLaunchKernelGGL(k_attn_dq4<false>, grid, dim3(256 * A4_KS), 0, st, q, k, v, out, datt, lse, Dq, dq, B, T, H,
-                               KV, win, scale, nullptr, nullptr);
-    } else {
+            hipLaunchKernelGGL(k_attn_bwd4<false>, grid, dim3(512), 0, st, q, k, v, out, datt, lse,
+                               (const float *)Dq, dq, dk, dv, B, T, H, KV, win, scale, nullptr, nullptr);
+        LAUNCH_CHECK();
+        return TLG_OK;
+    }
+    if (g4)        // no rope tables here (they need an aligned lse)
+        hipLaunchKernelGGL(k_attn_dq4<false>, dim3(B * KV * (H / KV / 4) * nqb), dim3(256 * A4_KS), 0, st, q, k, v,
+                           out, datt, lse, Dq, dq, B, T, H, KV, win, scale, nullptr, nullptr);
+    else
         hipLaunchKernelGGL(k_attn_bwd_dq, dim3(B * H * nqb), dim3(64 * AT_W), 0, st, q, k, v, out, datt, lse, Dq, dq,
                            B, T, H, KV, win, scale);
-    }
-    // the group dK / dV kernel reads lse rows as float4 (4 heads)
-    if (g4 && cs && !al16(lse)) return tlg_fail(TLG_EINVAL, "attn_bwd_rope: lse must be 16-byte aligned");
-    if (g4 && cs)
-        hipLaunchKernelGGL(k_attn_dkv4<true>, dim3(nqb * B * KV), dim3(512), 0, st, q, k, v, datt, lse,
-                           (const float *)Dq, dk, dv, B, T, H, KV, win, scale, cs, sn);
-    else if (g4 && al16(lse))
-        hipLaunchKernelGGL(k_attn_dkv4<false>, dim3(nqb * B * KV), dim3(512), 0, st, q, k, v, datt, lse,
-                           (const float *)Dq, dk, dv, B, T, H, KV, win, scale, nullptr, nullptr);
-    else
-        hipLaunchKernelGGL(k_attn_bwd_dkv, dim3(nqb * B * KV), dim3(64 * AT_KW), 0, st, q, k, v, datt, lse,
-                           (const float *)Dq, dk, dv, B, T, H, KV, win, scale);
+    hipLaunchKernelGGL(k_attn_bwd_dkv, dim3(nqb * B * KV), dim3(64 * AT_KW), 0, st, q, k, v, datt, lse,
+                       (const float *)Dq, dk, dv, B, T, H, KV, win, scale);
     LAUNCH_CHECK();
     return TLG_OK;
 }
