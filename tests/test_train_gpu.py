@@ -209,6 +209,33 @@ def test_attention(lib, st, B, T, H, KV, win):
         assert normwise_rel(got, want) <= TOL, name
 
 
+def test_attention_unaligned_lse(lib, st):
+    """GQA groups of 4 with an lse array that is not 16-byte aligned: the
+    backward takes the dQ group kernel and the per-head dK / dV kernel instead
+    of the one-launch group path (which reads lse rows as float4)."""
+    B, T, H, KV, win = 2, 100, 8, 2, 0
+    t = _t()
+    r = np.random.default_rng(5)
+    q = r.standard_normal((B * T, H * 32)).astype(np.float32)
+    k = r.standard_normal((B * T, KV * 32)).astype(np.float32)
+    v = r.standard_normal((B * T, KV * 32)).astype(np.float32)
+    datt = (0.01 * r.standard_normal((B * T, H * 32))).astype(np.float32)
+    Q, K, Vv, DA = dev(q), dev(k), dev(v), dev(datt)
+    out, lse1 = nan_like(q.shape), nan_like((B * T * H + 4,))
+    lp = lse1.data_ptr() + 4                                   # one float in: 4-byte aligned only
+    lib.check(lib.tlg_dev_attn_fwd(Q.data_ptr(), K.data_ptr(), Vv.data_ptr(), out.data_ptr(), lp, B, T, H, KV, 32,
+                                   win, stream()), "attn_fwd")
+    dq, dk, dv = nan_like(q.shape), nan_like(k.shape), nan_like(v.shape)
+    lib.check(lib.tlg_dev_attn_bwd(Q.data_ptr(), K.data_ptr(), Vv.data_ptr(), out.data_ptr(), lp, DA.data_ptr(),
+                                   dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, T, H, KV, 32, win, stream()),
+              "attn_bwd")
+    t.cuda.synchronize()
+    wq, wk, wv = st.attn_bwd(q, k, v, datt, B, T, H, KV, 32, win)
+    assert normwise_rel(host(out), st.attn_fwd(q, k, v, B, T, H, KV, 32, win)) <= TOL
+    for got, want, name in ((host(dq), wq, "dq"), (host(dk), wk, "dk"), (host(dv), wv, "dv")):
+        assert normwise_rel(got, want) <= TOL, name
+
+
 @pytest.mark.parametrize("path", golden("step_attn_*.npz"), ids=os.path.basename)
 def test_attention_fixture(lib, path):
     d = load_npz(path)
