@@ -199,6 +199,37 @@ def test_split_targets_keep_results(lib, orc, cfg, rt):
             assert normwise_rel(got[bname][a:b], init[bname][a:b]) <= TOL, (cfg, rt, label)
 
 
+@pytest.mark.parametrize("name", ["nano", "m3", "m8"])
+def test_bench_tables_match_oracle(lib, orc, name):
+    """The configuration bench.py measures: every grouped launch on the tile
+    configuration and split target of bench.TUNED / bench.SPLITS; the step
+    (eager and replayed from a graph) meets the bar against the oracle."""
+    host = tlgemm.host()
+    plan = host.plan_train(**bench.TRAIN[name])
+    run, stream = new_run(lib, host, plan, seed=17)
+    try:
+        L = host.dll.tl_run_grouped_launches(run)
+        assert len(bench.TUNED[name]) == L and len(bench.SPLITS[name]) == L
+        for k in range(L):
+            assert host.dll.tl_run_set_launch_config(run, k, bench.TUNED[name][k]) == 0
+            assert host.dll.tl_run_set_launch_split(run, k, bench.SPLITS[name][k]) == 0
+        init = snapshot(lib, host, plan, run, stream)
+        lib.check(host.dll.tl_run_step_grouped(run, stream), "step")
+        got = snapshot(lib, host, plan, run, stream)
+        fill(lib, host, plan, run, stream, 17)
+        lib.check(host.dll.tl_run_graph_build(run, stream, 1), "graph")
+        fill(lib, host, plan, run, stream, 17)
+        lib.check(host.dll.tl_run_graph_step(run, stream), "replay")
+        replay = snapshot(lib, host, plan, run, stream)
+    finally:
+        host.dll.tl_run_free(run)
+    run_plan_cpu(plan, init, orc)
+    for bname, _, _ in plan.bufs:
+        assert np.array_equal(got[bname], replay[bname]), bname
+        for label, a, b in plan.regions(bname):
+            assert normwise_rel(got[bname][a:b], init[bname][a:b]) <= TOL, (name, label)
+
+
 def test_split_target_hook_rejects_small_targets(lib):
     assert lib.tlg_tune_group_split(63) != 0
     assert lib.tlg_tune_group_split(0) == 0
