@@ -926,6 +926,8 @@ __global__ __launch_bounds__(512) void k_attn_bwd_dkv(const float *__restrict__ 
 #define A4_LD 36        // LDS row stride of a staged 32 x 32 block (16-byte rows)
 #define A4_CH 8         // key blocks staged at once (K + V: 72 KB)
 #define A4_KS 2         // key splits per head: 4 heads x 2 splits = 8 waves (4 measured slower)
+#define A4_CH2 6        // key blocks staged at once by the 2-head forward items (K + V: 54 KB)
+#define A4_FNH 2        // heads per forward item (4 or 2)
 
 // One staging task: dims [4c, 4c + 4) and [16 + 4c, 16 + 4c + 4) of one
 // 32-dim head row, rotated by position t when ROPE and `rot`, zeroed when !ok.
@@ -969,6 +971,26 @@ __device__ __forceinline__ void a4_item(int item, int B, int H, int KV, int nqb,
     *kvh = r % KV;
     *b = r / KV;
     *h0 = *kvh * G + hg * 4;
+}
+
+// Forward item -> (b, kvh, first head h0 of its NH heads, qb).  NH = 4: as
+// a4_item.  NH = 2 (two workgroups per CU): the latest query blocks first for
+// the first half of the items, then the earliest first, so with items dealt
+// round-robin over the CUs one CU's two items see about nqb + 1 key blocks
+// together (query block nqb - 1 - j beside j).
+template <int NH>
+__device__ __forceinline__ void a4f_item(int item, int B, int H, int KV, int nqb, int *b, int *kvh, int *h0,
+                                         int *qb)
+{
+    const int G = H / KV, HG = G / NH, per = B * KV * HG, qhi = (nqb + 1) >> 1;
+    if (NH == 4 || item < qhi * per) *qb = nqb - 1 - item / per;
+    else *qb = (item - qhi * per) / per;
+    int r = item % per;
+    const int hg = r % HG;
+    r /= HG;
+    *kvh = r % KV;
+    *b = r / KV;
+    *h0 = *kvh * G + hg * NH;
 }
 
 // Stage key blocks c0 .. c0 + nb - 1 of (b, kvh): K (rotated with ROPE) into
@@ -1032,40 +1054,43 @@ __device__ __forceinline__ void a4_frag(const float *L, int row, int half, float
     }
 }
 
-template <bool ROPE>
-__global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_fwd4(const float *__restrict__ q, const float *__restrict__ k,
+template <bool ROPE, int NH>
+__global__ __launch_bounds__(512) void k_attn_fwd4(const float *__restrict__ q, const float *__restrict__ k,
                                                    const float *__restrict__ v, float *__restrict__ out,
                                                    float *__restrict__ lse, int B, int T, int H, int KV, int win,
                                                    float scale, const float *__restrict__ cs,
                                                    const float *__restrict__ sn)
 {
-    // K and V staging in one array: its whole extent is the merge area later
-    __shared__ __attribute__((aligned(16))) float KVs[2 * A4_CH * 32 * A4_LD], Qs[4 * 32 * A4_LD];
-    static_assert(2 * A4_CH * 32 * A4_LD >= 4 * (A4_KS - 1) * 18 * 64, "merge area");
-    float *Ks = KVs, *Vs = KVs + A4_CH * 32 * A4_LD;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hs = wave & 3, ks = wave >> 2;
+    // NH heads per item, KS = 8 / NH key splits per head (8 waves), CH key
+    // blocks staged at once; K and V staging in one array: its whole extent
+    // is the merge area later
+    constexpr int KS = 8 / NH, CH = NH == 4 ? A4_CH : A4_CH2;
+    __shared__ __attribute__((aligned(16))) float KVs[2 * CH * 32 * A4_LD], Qs[NH * 32 * A4_LD];
+    static_assert(2 * CH * 32 * A4_LD >= NH * (KS - 1) * 18 * 64, "merge area");
+    float *Ks = KVs, *Vs = KVs + CH * 32 * A4_LD;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hs = wave % NH, ks = wave / NH;
     const int nqb = (T + 31) >> 5;
     int b, kvh, h0, qb;
-    a4_item(blockIdx.x, B, H, KV, nqb, &b, &kvh, &h0, &qb);
+    a4f_item<NH>(blockIdx.x, B, H, KV, nqb, &b, &kvh, &h0, &qb);
     const int h = h0 + hs, D = H * AT_HD;
     const int lq = lane & 31, hh = lane >> 5;
     const int qi = qb * 32 + lq;
     const int kb0 = at_kb0(qb, win);
 
-    if (tid < 512) a4_stage_q<ROPE>(Qs, q, b, h0, qb, T, H, cs, sn);
+    if (tid < NH * 128) a4_stage_q<ROPE>(Qs, q, b, h0, qb, T, H, cs, sn);
     const float c2 = scale * 1.44269504088896341f;
     float qv[16];
     f32x16 o;
 #pragma unroll
     for (int r = 0; r < 16; r++) o[r] = 0.f;
     float m = -INFINITY, l = 0.f;
-    for (int c0 = kb0; c0 <= qb; c0 += A4_CH) {
-        const int nb = min(A4_CH, qb - c0 + 1);
+    for (int c0 = kb0; c0 <= qb; c0 += CH) {
+        const int nb = min(CH, qb - c0 + 1);
         if (c0 > kb0) __syncthreads();          // the previous chunk is read
         a4_stage_kv<ROPE>(Ks, Vs, k, v, b, kvh, T, KV, c0, nb, cs, sn);
         __syncthreads();
         if (c0 == kb0) a4_frag(Qs + hs * 32 * A4_LD, lq, hh, qv);
-        for (int kb = c0 + ks; kb < c0 + nb; kb += A4_KS) {
+        for (int kb = c0 + ks; kb < c0 + nb; kb += KS) {
             const float *Kb = Ks + (kb - c0) * 32 * A4_LD, *Vb = Vs + (kb - c0) * 32 * A4_LD;
             float kv[16];
             a4_frag(Kb, lq, hh, kv);
@@ -1121,7 +1146,7 @@ __global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_fwd4(const float *__res
     __syncthreads();
     // the other key splits' states join split 0's in split order (the K / V
     // area is free by now)
-    float *mg = Ks + hs * (A4_KS - 1) * 18 * 64;
+    float *mg = Ks + hs * (KS - 1) * 18 * 64;
     if (ks > 0) {
         float *mine = mg + (ks - 1) * 18 * 64;
 #pragma unroll
@@ -1133,13 +1158,13 @@ __global__ __launch_bounds__(64 * 4 * A4_KS) void k_attn_fwd4(const float *__res
     if (ks > 0 || qi >= T) return;
     float M = m;
 #pragma unroll
-    for (int w = 0; w < A4_KS - 1; w++) M = fmaxf(M, mg[w * 18 * 64 + 16 * 64 + lane]);
+    for (int w = 0; w < KS - 1; w++) M = fmaxf(M, mg[w * 18 * 64 + 16 * 64 + lane]);
     const float a0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
     l *= a0;
 #pragma unroll
     for (int r = 0; r < 16; r++) o[r] *= a0;
 #pragma unroll
-    for (int w = 0; w < A4_KS - 1; w++) {
+    for (int w = 0; w < KS - 1; w++) {
         const float *th = mg + w * 18 * 64;
         const float mw = th[16 * 64 + lane];
         const float aw = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
@@ -1886,13 +1911,13 @@ static int attn_fwd_launch(const float *q, const float *k, const float *v, float
     const float scale = 1.0f / sqrtf((float)hd);
     const int nqb = (T + 31) / 32;
     if (g4) {
-        const dim3 grid(B * KV * (H / KV / 4) * nqb);
+        const dim3 grid(B * KV * (H / KV / A4_FNH) * nqb);
         if (cs)
-            hipLaunchKernelGGL(k_attn_fwd4<true>, grid, dim3(256 * A4_KS), 0, ST(stream), q, k, v, out, lse, B, T, H, KV, win,
-                               scale, cs, sn);
+            hipLaunchKernelGGL((k_attn_fwd4<true, A4_FNH>), grid, dim3(512), 0, ST(stream), q, k, v, out, lse, B, T, H,
+                               KV, win, scale, cs, sn);
         else
-            hipLaunchKernelGGL(k_attn_fwd4<false>, grid, dim3(256 * A4_KS), 0, ST(stream), q, k, v, out, lse, B, T, H, KV,
-                               win, scale, nullptr, nullptr);
+            hipLaunchKernelGGL((k_attn_fwd4<false, A4_FNH>), grid, dim3(512), 0, ST(stream), q, k, v, out, lse, B, T, H,
+                               KV, win, scale, nullptr, nullptr);
     } else {
         hipLaunchKernelGGL(k_attn_fwd, dim3(B * H * nqb), dim3(64 * AT_W), 0, ST(stream), q, k, v, out, lse, B, T, H,
                            KV, win, scale);
