@@ -271,7 +271,12 @@ __global__ __launch_bounds__(256) void k_embed_bwd1(const float *__restrict__ do
 }
 
 // -------------------------------------------------------------- rmsnorm --
-// One wave per row: s = 1 / sqrt(sum(x^2) / D + 1e-5), out = x * s * g.
+// One wave per row: s = 1 / sqrt(sum(x^2) / D + 1e-5), out = x * s * g.  With
+// NV > 0 the row stays in registers between the sum and the output (NV float4
+// columns per lane, D <= 256 NV; loads use clamped, in-bounds indices, columns
+// past D are masked at use); NV = 0 takes any D and reads the row twice.  Both
+// forms add the same terms in the same order.
+template <int NV>
 __global__ __launch_bounds__(256) void k_rms_fwd(const float *__restrict__ x, const float *__restrict__ g,
                                                  float *__restrict__ out, float *__restrict__ rinv, int rows, int D)
 {
@@ -280,19 +285,45 @@ __global__ __launch_bounds__(256) void k_rms_fwd(const float *__restrict__ x, co
     if (r >= rows) return;
     const int d4 = D >> 2;
     const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (size_t)r * D);
-    float ms = 0.f;
-    for (int i = lane; i < d4; i += 64) {
-        const f32x4 v = xr[i];
-        ms += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-    }
-    for (int o = 32; o > 0; o >>= 1) ms += __shfl_xor(ms, o);
-    const float s = 1.0f / sqrtf(ms / (float)D + 1e-5f);
-    if (lane == 0 && rinv) rinv[r] = s;
-    f32x4 *orow = reinterpret_cast<f32x4 *>(out + (size_t)r * D);
     const f32x4 *g4 = reinterpret_cast<const f32x4 *>(g);
-    for (int i = lane; i < d4; i += 64) {
-        const f32x4 v = xr[i], w = g4[i];
-        orow[i] = f32x4{v.x * s * w.x, v.y * s * w.y, v.z * s * w.z, v.w * s * w.w};
+    f32x4 *orow = reinterpret_cast<f32x4 *>(out + (size_t)r * D);
+    float ms = 0.f;
+    if constexpr (NV == 0) {
+        for (int i = lane; i < d4; i += 64) {
+            const f32x4 v = xr[i];
+            ms += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        for (int o = 32; o > 0; o >>= 1) ms += __shfl_xor(ms, o);
+        const float s = 1.0f / sqrtf(ms / (float)D + 1e-5f);
+        if (lane == 0 && rinv) rinv[r] = s;
+        for (int i = lane; i < d4; i += 64) {
+            const f32x4 v = xr[i], w = g4[i];
+            orow[i] = f32x4{v.x * s * w.x, v.y * s * w.y, v.z * s * w.z, v.w * s * w.w};
+        }
+    } else {
+        f32x4 xa[NV], gv[NV];
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            xa[j] = xr[min(lane + 64 * j, d4 - 1)];
+            gv[j] = g4[min(lane + 64 * j, d4 - 1)];
+        }
+#pragma unroll
+        for (int j = 0; j < NV; j++)
+            if (lane + 64 * j < d4) {
+                const f32x4 v = xa[j];
+                ms += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+        for (int o = 32; o > 0; o >>= 1) ms += __shfl_xor(ms, o);
+        const float s = 1.0f / sqrtf(ms / (float)D + 1e-5f);
+        if (lane == 0 && rinv) rinv[r] = s;
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int i = lane + 64 * j;
+            if (i < d4) {
+                const f32x4 v = xa[j], w = gv[j];
+                orow[i] = f32x4{v.x * s * w.x, v.y * s * w.y, v.z * s * w.z, v.w * s * w.w};
+            }
+        }
     }
 }
 
@@ -1503,29 +1534,33 @@ __device__ __forceinline__ void attn_dkv4_item(float *__restrict__ Sm, int item,
 }
 
 // Dq[row][h] = dO[row][h] . O[row][h] (attn_bwd's per-row term, tinylm.c:750-768)
-// in the dQ item's order: the two 16-term halves, then their sum.
+// in the dQ item's order: the two 16-term halves, then their sum.  Eight lanes
+// per (row, head), lane q holding float4 q of both rows, so a wave's loads are
+// 1 KB contiguous; each half's chain passes through its four lanes in order
+// (lane q continues the sum lane q - 1 ended with).
 __global__ __launch_bounds__(256) void k_attn_delta(const float *__restrict__ dout, const float *__restrict__ o,
                                                     float *__restrict__ Dq, int n)
 {
-    const int t = blockIdx.x * 256 + threadIdx.x;        // (row, head) = row * H + h
-    if (t >= n) return;
-    const f32x4 *a = reinterpret_cast<const f32x4 *>(dout + (size_t)t * AT_HD);
-    const f32x4 *c = reinterpret_cast<const f32x4 *>(o + (size_t)t * AT_HD);
-    float h2[2];
+    const int q = threadIdx.x & 7;
+    const int t = (blockIdx.x * 256 + threadIdx.x) >> 3;     // (row, head) = row * H + h
+    const size_t tc = (size_t)min(t, n - 1);                 // every lane takes part in the shuffles
+    const f32x4 x = reinterpret_cast<const f32x4 *>(dout)[tc * (AT_HD / 4) + q];
+    const f32x4 y = reinterpret_cast<const f32x4 *>(o)[tc * (AT_HD / 4) + q];
+    float d = 0.f;
 #pragma unroll
-    for (int hh = 0; hh < 2; hh++) {
-        float d = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const f32x4 x = a[4 * hh + j], y = c[4 * hh + j];
-            d += x[0] * y[0];
-            d += x[1] * y[1];
-            d += x[2] * y[2];
-            d += x[3] * y[3];
+    for (int s = 0; s < 4; s++) {
+        const float in = __shfl_up(d, 1, 4);
+        if ((q & 3) == s) {
+            float c = s ? in : 0.f;
+            c += x[0] * y[0];
+            c += x[1] * y[1];
+            c += x[2] * y[2];
+            c += x[3] * y[3];
+            d = c;
         }
-        h2[hh] = d;
     }
-    Dq[t] = h2[0] + h2[1];
+    const float h0 = __shfl_up(d, 4, 8);
+    if (q == 7 && t < n) Dq[t] = h0 + d;
 }
 
 // dQ and dK / dV in one launch, after k_attn_delta: workgroups
@@ -1805,7 +1840,18 @@ extern "C" int tlg_dev_rmsnorm_fwd(const float *x, const float *g, float *out, f
     if (rows < 0 || D <= 0 || D % 4 || !al16(x) || !al16(g) || !al16(out))
         return tlg_fail(TLG_EINVAL, "rmsnorm_fwd: rows=%d D=%d (D %% 4 == 0, aligned rows)", rows, D);
     if (rows == 0) return TLG_OK;
-    hipLaunchKernelGGL(k_rms_fwd, dim3((rows + 3) / 4), dim3(256), 0, ST(stream), x, g, out, rinv, rows, D);
+    const dim3 grid((rows + 3) / 4);
+    const int nv = (D / 4 + 63) / 64;
+    if (nv <= 1)
+        hipLaunchKernelGGL(k_rms_fwd<1>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D);
+    else if (nv <= 2)
+        hipLaunchKernelGGL(k_rms_fwd<2>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D);
+    else if (nv <= 4)
+        hipLaunchKernelGGL(k_rms_fwd<4>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D);
+    else if (nv <= 8)
+        hipLaunchKernelGGL(k_rms_fwd<8>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D);
+    else
+        hipLaunchKernelGGL(k_rms_fwd<0>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D);
     LAUNCH_CHECK();
     return TLG_OK;
 }
@@ -1949,7 +1995,7 @@ static int attn_bwd_launch(const float *q, const float *k, const float *v, const
     if (g4 && cs && !al16(lse)) return tlg_fail(TLG_EINVAL, "attn_bwd_rope: lse must be 16-byte aligned");
     if (g4 && al16(lse)) {
         // Dq first; then the dK / dV and dQ items of every group in one launch
-        hipLaunchKernelGGL(k_attn_delta, dim3((B * T * H + 255) / 256), dim3(256), 0, st, datt, out, Dq, B * T * H);
+        hipLaunchKernelGGL(k_attn_delta, dim3((B * T * H + 31) / 32), dim3(256), 0, st, datt, out, Dq, B * T * H);
         const dim3 grid(nqb * B * KV + B * KV * (H / KV / 4) * nqb);
         if (cs)
             hipLaunchKernelGGL(k_attn_bwd4<true>, grid, dim3(512), 0, st, q, k, v, out, datt, lse, (const float *)Dq,
