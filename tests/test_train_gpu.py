@@ -52,6 +52,22 @@ def st():
 
 
 # ------------------------------------------------------------------ rmsnorm --
+@pytest.mark.parametrize("rows,D", [(9, 768), (3, 2052), (2, 4100)])
+def test_rmsnorm_fwd_wide(lib, st, rows, D):
+    """The forward's other row widths: 4 float4 columns per lane, and rows wider
+    than 2048 (read twice instead of kept in registers)."""
+    print("rmsnorm_fwd", rows, D, flush=True)
+    r = np.random.default_rng(rows * D)
+    x = r.standard_normal((rows, D)).astype(np.float32)
+    g = (1 + 0.1 * r.standard_normal(D)).astype(np.float32)
+    X, Gn = dev(x), dev(g)
+    out, rinv = nan_like((rows, D)), nan_like((rows,))
+    lib.check(lib.tlg_dev_rmsnorm_fwd(X.data_ptr(), Gn.data_ptr(), out.data_ptr(), rinv.data_ptr(), rows, D,
+                                      stream()), "rmsnorm_fwd")
+    ro, rr = st.rmsnorm_fwd(x, g)
+    assert normwise_rel(host(out), ro) <= TOL and normwise_rel(host(rinv), rr) <= TOL
+
+
 @pytest.mark.parametrize("rows,D", [(4096, 256), (1027, 384), (37, 48), (5, 2048)])
 def test_rmsnorm(lib, st, rows, D):
     print("rmsnorm", rows, D, flush=True)
