@@ -144,6 +144,12 @@ int tlg_dev_gemm_flush(void *stream);
 int tlg_dev_gemm_pending(void);
 /* Kernel instance grouped launches use, as rocprofv3 names it. */
 const char *tlg_group_kernel(void);
+/* 1 if an M <= 8 launch (the GEMV kernels behind mm / mm_bt at M <= 8 and
+ * tlg_dev_dec_gemv) ever timed out waiting for its split partial sums (its
+ * outputs were then written as NaN), 0 if none did, -1 if the flag cannot be
+ * read.  Synchronous.  No reference counterpart: a diagnostic of this
+ * library's split reduction. */
+int tlg_gemv_status(void);
 /* Tuning hook: pin the tile configuration of grouped launches (an index of
  * the kernel's tile table; -1 = automatic: 64x64 tiles when a launch has at
  * least 3 x 256 of them, else 64x32 tiles whose wave pairs split each stage). */

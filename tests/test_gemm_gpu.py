@@ -208,6 +208,38 @@ def test_gemv_group(lib):
             assert lib.tlg_group_kernel().decode().startswith("k_gemv")
 
 
+def test_gemv_split_repeats(lib):
+    """The M <= 8 mm splits W's rows over several workgroups whose partial
+    sums meet in a tagged workspace that is reused launch after launch: 120
+    back-to-back launches of interleaved shapes (different splits and
+    column blocks land on the same words), every result against fp64, the
+    same inputs bit-identical every time, and no wait ever timed out."""
+    from oracle import Oracle
+    orc = Oracle()
+    t = _torch()
+    shapes = [(1, 384, 1024), (8, 1024, 384), (2, 384, 96), (4, 5003, 64), (1, 1024, 384), (3, 384, 384)]
+    cases = []
+    for i, (M, K, N) in enumerate(shapes):
+        X = seeded((M, K), 1.0, f"rX{i}")
+        W = seeded((K, N), 0.02, f"rW{i}")
+        cases.append((M, K, N, dev(X), dev(W), orc.mm_f64(X, W)))
+    first = {}
+    for rep in range(20):
+        outs = []
+        for i, (M, K, N, x, w, _) in enumerate(cases):
+            Y = t.full((M, N), float("nan"), device="cuda")
+            lib.mm(Y.data_ptr(), x.data_ptr(), w.data_ptr(), M, K, N, stream())
+            outs.append(Y)
+        for i, Y in enumerate(outs):
+            got = Y.cpu().numpy()
+            assert normwise_rel(got, cases[i][5]) <= TOL, (rep, cases[i][:3])
+            if rep == 0:
+                first[i] = got
+            else:
+                assert np.array_equal(got, first[i]), (rep, cases[i][:3])
+    assert lib.tlg_gemv_status() == 0
+
+
 @pytest.mark.parametrize("M,K,N", [(4096, 256, 256), (67, 36, 44), (5, 8, 12)])
 def test_residual_mm(lib, M, K, N):
     """TlgGemmCall.R: C = R + X W in the store, bit for bit the mm result plus

@@ -44,6 +44,8 @@ static int init_locked(int device)
         return tlg_fail(TLG_ENOMEM, "tlg_init: workspace of %zu bytes", TLG_WS_FLOATS * sizeof(float));
     g_tlg.ws = (float *)p;
     g_tlg.ws_floats = TLG_WS_FLOATS;
+    int rc = tlg_gemv_init();
+    if (rc) return rc;
     TLG_HIP(hipDeviceSynchronize());
     g_tlg.device = device;
     g_tlg.initialised = 1;
@@ -138,6 +140,8 @@ extern "C" void tlg_shutdown(void)
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     if (!g_tlg.initialised) return;
     (void)hipDeviceSynchronize();
+    (void)tlg_group_drain(g_tlg.stream);       // queued reductions read the workspace
+    (void)hipDeviceSynchronize();
     for (auto &m : g_mirrors) (void)hipFree(m.dev);
     g_mirrors.clear();
     tlg_shutdown_impl();
@@ -159,6 +163,7 @@ void tlg_shutdown_impl(void)
     for (auto &s : g_stage) { (void)hipFree(s.p); s = Stage(); }
     tlg_moe_release();
     tlg_train_release();
+    tlg_gemv_release();
 }
 
 static int stage_ptr(int slot, size_t bytes, void **out)

@@ -1427,6 +1427,7 @@ int tlg_group_flush_launch(hipStream_t st)
     return rc ? rc : group_flush_dense(st);
 }
 
+
 // [lo, hi) byte range touched by a row-major operand of `rows` x `cols`
 // with leading dimension ld.
 static void span(const void *p, int rows, int cols, int ld, const char **lo, const char **hi)
@@ -1665,6 +1666,21 @@ static int ecarry_flush(hipStream_t st)
     g_ecarry_used = 0;
     TLG_HIP(hipGetLastError());
     return TLG_OK;
+}
+
+// Shutdown: the queued reductions (and an expert launch's held carry) run
+// on `st` while the workspace they read still exists; then the queue is
+// empty and the workspace halves start over, so nothing queued before a
+// tlg_shutdown can run against freed memory after a later tlg_init.
+int tlg_group_drain(hipStream_t st)
+{
+    const int rc = tlg_group_flush_launch(st);
+    g_npending = 0;
+    g_ecarry.nprob = 0;
+    g_ecarry_used = 0;
+    g_ecarry_eoff = nullptr;
+    g_ws_half = 0;
+    return rc;
 }
 
 int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E, int rows, hipStream_t st,

@@ -1,286 +1,584 @@
 // tlg_gemv.hip -- the M <= 8 forms of mm and mm_bt (KV-cache decode) on gfx950.
 //
 // At M <= 8 rows a GEMM is a matrix-vector product: every weight is used M
-// times, so the work is one pass over the weight matrix and its speed is set
-// by how many bytes per cycle the CUs pull from HBM.  MFMA tiles would waste
-// 24/32 of every block and stage weights through LDS for nothing; these
-// kernels stream the weights once, straight from global memory into FMAs.
-// The M activation rows are staged in LDS (4096 floats at a time), and each
-// workgroup spreads its reduction over many row slots so that every lane has
-// several weight loads in flight: a few microseconds of memory latency, not
-// a chain of dependent loads, bounds a launch.
+// times, so a launch is one pass over the weight matrix and its speed is set
+// by how much of that matrix is in flight at once.  The decode matrices are
+// small (0.15-3.1 MB) next to what HBM has in flight at full rate (about
+// 8 TB/s x 1.5 us = 12 MB), so a launch should request its whole matrix in
+// its first round of loads: every lane issues all of its weight loads (16-byte
+// vectors, each wave covering 256 contiguous bytes of a row) before it uses
+// any, and the matrix is cut into a few hundred workgroups of 4-16 KB so all
+// 256 CUs take part.
 //
-//   mm     Y[m][j] = sum_k X[m][k] W[k][j]       W rows are contiguous along
-//          the output index j: a workgroup owns 8 or 16 columns, as many
-//          lanes read one contiguous row segment, and the workgroup's 64 or
-//          32 row slots walk down W together.  The partial sums of a column
-//          meet in fixed order (shuffles, then LDS).
-//   mm_bt  dX[m][k] += sum_n dY[m][n] W[k][n]    W rows are contiguous along
-//          the reduction index n: a wave owns 2 W rows, its lanes stride n
-//          (coalesced), and each of the 2*M dot products ends in a butterfly
-//          reduction over the 64 lanes.
+//   mm     Y[m][j] = sum_k X[m][k] W[k][j]       W rows run along the output
+//          index j.  An item owns a 64-column block and a slice of KS rows:
+//          16 lanes read one row's 256 bytes, a wave 4 rows at a time.  The
+//          item's partial column sums meet in LDS in a fixed order.  When the
+//          rows are split over S items, the S-1 "producer" items store their
+//          partial block as tagged 64-bit words (value | 1 << 32) and the
+//          item of the last slice, the "reducer", adds the S partials in
+//          slice order and writes C, then clears the words it read.
+//   mm_bt  dX[m][k] += sum_n dY[m][n] W[k][n]    W rows run along the
+//          reduction.  An item owns 8 output rows, 2 per wave: 32 lanes read
+//          one row in 512-byte steps, each dot product ends in a butterfly
+//          over the 32 lanes.  No split is needed.
+//
+// Reducers wait: every producer item has a lower workgroup id than every
+// reducer item, and the dispatcher starts the workgroups of a launch in id
+// order, so a reducer only ever waits for items that have already started
+// and never wait themselves.  The wait is bounded (10 ms of the real-time
+// counter); past it the reducer writes NaN and sets an error word, so a fault
+// shows as a wrong result, never as a hang.  Partial words are written and
+// read with agent-scope accesses (they reach the device-coherent level, not
+// only one XCD's L2).  The workspace is a ring of regions, one per launch in
+// turn, so launches on different streams do not share words unless more than
+// GV_RING of them overlap.
 //
 // Reference: mm tinylm.c:438-449 (serial at M <= 4 through tl_for, :444-446),
 // mm_bt :480-489; the decode GEMV sites of forward_chunk :3748-3824 and the
 // head :3035.  Several GEMVs that the reference issues back to back (q, k, v
 // on the same input; w1, w3) run as one launch: a problem table in the
-// kernel arguments, workgroups dealt to problems in order.
+// kernel arguments.  Results match the reference to fp32 rounding: each
+// output is a fixed-order sum (lane, then row group, then slice), the same in
+// every launch.
 #include "tlg_internal.h"
 #include "../../include/tldecode.h"
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
-#define GV_WAVES 8              // waves per workgroup (512 threads)
-#define GV_NT_ROWS 2            // mm_bt: W rows per wave
-#define GV_ACHUNK 4096          // floats of the activation rows staged in LDS at a time
-#define NN_U 16                 // mm: weight rows per lane per batch of loads
-#define NT_U 8                  // mm_bt: reduction steps per lane per batch of loads
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned long long u64;
+typedef unsigned int u32;
+
+#define GV_T 256                      // threads per workgroup (4 waves)
 #define GV_MAXPROB 8
 #define GV_MAXSEG 3
+#define GV_NT_ROWS 8                  // mm_bt: output rows per item (2 per wave)
+#define GV_RING 16                    // workspace regions, used by launches in turn
+#define GV_REGION_WORDS ((size_t)256 << 10)   // 64-bit partial words per region (2 MiB)
+#define GV_SPIN 1000000ull            // 10 ms of the 100 MHz real-time counter
+#define GV_TAG (1ull << 32)
 
-// mm: output columns per workgroup.  Narrower column blocks give more
-// workgroups (more loads in flight across the chip) at the cost of shorter
-// row segments; measured on MI355X, 8 is best at M <= 2 and 16 above.
-__host__ __device__ constexpr int nn_cols(int mb) { return mb <= 2 ? 8 : 16; }
+// Every global access goes through global-address-space pointers: flat
+// accesses would also count against lgkmcnt, so the LDS barriers would wait
+// for the weight loads in flight.
+#define GAS __attribute__((address_space(1)))
 
 struct GvSeg { const float *A, *B; int R, lda, ldb; };
-// Activation prologues (decode: the glue before a GEMV, applied while the
-// rows are staged): GV_PRO_RMS stages x * s * gain with s = 1 / sqrt(sum(x^2)
-// / R + 1e-5) of the whole row (rmsnorm_fwd, tinylm.c:540-548); GV_PRO_SWIGLU
-// stages silu(a) * a2 with silu(z) = z / (1 + e^-z) (:786, :1005-1006).
+// Activation prologues (decode: the glue before a GEMV, applied as the rows
+// are read): GV_PRO_RMS uses x * s * gain with s = 1 / sqrt(sum(x^2) / R +
+// 1e-5) of the whole row (rmsnorm_fwd, tinylm.c:540-548); GV_PRO_SWIGLU uses
+// silu(a) * a2 with silu(z) = z / (1 + e^-z) (:786, :1005-1006).
 enum { GV_PRO_NONE = 0, GV_PRO_RMS = 1, GV_PRO_SWIGLU = 2 };
 struct GvProb {
     float *C;
     int kind;                    // TLG_NN or TLG_NT
     int M, No, ldc, beta, nseg;
-    int blocks;
-    int pro;                     // GV_PRO_* (single-segment problems only)
     const float *gain, *A2;      // RMS gain [R]; SwiGLU second operand (layout of A)
     GvSeg seg[GV_MAXSEG];
+    // decomposition (host): nb column (NN) or row (NT) blocks; NN rows split
+    // into S slices of KS rows; with S > 1 the partial words start at `part`
+    int nb, S, KS;
+    long long part;
+    int direct, reducers;        // items that never wait; reducer items (nb when S > 1)
+    int full;                    // NN over all K rows per item (16-column blocks, no split)
 };
 struct GvArgs {
     int nprob;
+    u64 *part;                   // this launch's region of partial words
+    u32 *err;                    // set to 1 by a reducer whose wait timed out
     GvProb p[GV_MAXPROB];
 };
 
-// Stage activation rows A[m][r0 .. r0+kc) (m < M) into LDS as As[m*kc + r-r0],
-// through the problem's prologue: SwiGLU completes here; RMSNorm stages the
-// raw rows and its gain (Gs) in the same pass -- one global round trip --
-// and rms_finish applies the scales.
-__device__ __forceinline__ void stage_rows(float *As, float *Gs, const GvProb &P, const GvSeg &g, int r0, int kc)
+template <int VEC> struct GvV;
+template <> struct GvV<4> { typedef f32x4 T; };
+template <> struct GvV<1> { typedef float T; };
+
+template <int VEC> __device__ __forceinline__ typename GvV<VEC>::T gv_ld(const float *p)
 {
-    for (int e = threadIdx.x; e < P.M * kc; e += blockDim.x) {
-        const int m = e / kc, r = e - m * kc;
-        const size_t i = (size_t)m * g.lda + r0 + r;
-        float a = g.A[i];
-        if (P.pro == GV_PRO_SWIGLU) a = a / (1.0f + expf(-a)) * P.A2[i];
-        else if (P.pro == GV_PRO_RMS && m == 0) Gs[r] = P.gain[r0 + r];
-        As[e] = a;
+    return *(const GAS typename GvV<VEC>::T *)p;
+}
+__device__ __forceinline__ float gv_ld1(const float *p) { return *(const GAS float *)p; }
+__device__ __forceinline__ float gv_el(const f32x4 &v, int i) { return v[i]; }
+__device__ __forceinline__ float gv_el(const float &v, int) { return v; }
+__device__ __forceinline__ void gv_set(f32x4 &v, int i, float x) { v[i] = x; }
+__device__ __forceinline__ void gv_set(float &v, int, float x) { v = x; }
+
+__device__ __forceinline__ u64 gv_ld_agent(const u64 *p)
+{
+    return __hip_atomic_load((GAS u64 *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void gv_st_agent(u64 *p, u64 v)
+{
+    __hip_atomic_store((GAS u64 *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float gv_silu_mul(float a, float b) { return a / (1.0f + expf(-a)) * b; }
+
+#define GV_FULL_ACT 8192               // full-K mm: activation floats staged in LDS (K x MB)
+#define GV_FULL_K 1024                // full-K mm: at most this many rows (32 loads per lane)
+
+template <int MB, int CB> struct __attribute__((aligned(16))) GvSmem {
+    union {
+        struct {                     // split mm
+            float red[16][MB][CB];   // per (wave, lane row) partial blocks
+            float own[MB * CB];      // this item's slice of the block
+            float grp[16][GV_T];     // reducer: per-group slice sums
+        } s;
+        struct {                     // full-K mm
+            float act[GV_FULL_ACT];  // activation rows, [k][MB]
+            float red[32][MB][32];   // per (wave, lane row) partial blocks
+        } f;
+    };
+    float rs[8];                     // RMS scale per row
+    int timeout;
+};
+
+// RMS prologue: s_m = 1 / sqrt(sum_r A[m][r]^2 / R + 1e-5) for m < M, one
+// wave per row (rows w and w + 4), into sh.rs; read after a barrier.  The
+// scale multiplies the finished dot products (sum_r x g w scaled by s equals
+// sum_r (x s g) w up to rounding), so the weight loads never wait for it.
+template <int MB, int CB>
+__device__ __forceinline__ void gv_rms_stats(const float *A, int lda, int R, int M, GvSmem<MB, CB> &sh)
+{
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int mm = 0; mm < 2; mm++) {
+        const int m = w + 4 * mm;
+        if (mm * 4 < MB && m < M) {
+            float ss = 0.f;
+            for (int r0 = 0; r0 < R; r0 += 1024) {
+                f32x4 x[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) x[i] = gv_ld<4>(A + (size_t)m * lda + min(r0 + 256 * i + 4 * lane, R - 4));
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const bool ok = r0 + 256 * i + 4 * lane < R;
+                    const f32x4 y = ok ? x[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+                    ss = fmaf(y.x, y.x, ss); ss = fmaf(y.y, y.y, ss);
+                    ss = fmaf(y.z, y.z, ss); ss = fmaf(y.w, y.w, ss);
+                }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+            if (lane == 0) sh.rs[m] = 1.0f / sqrtf(ss / (float)R + 1e-5f);
+        }
     }
 }
 
-// RMSNorm of the staged rows (the whole row is in LDS: M * R <= GV_ACHUNK):
-// s_m = 1 / sqrt(sum_k x^2 / R + 1e-5), one wave per row (M <= GV_WAVES),
-// then x * s_m * gain in place.
-__device__ __forceinline__ void rms_finish(float *As, const float *Gs, float *rsc, int M, int R)
+// The reducer's sum over slices [s_lo, s_hi) of output o: the words of up
+// to 16 slices are loaded at once, then checked and added in slice order;
+// slice s_own (the reducer's own) comes from own_v.  Repeats until every word
+// carries the tag or the wait runs past GV_SPIN (then timeout = 1), and
+// clears the words it read.
+__device__ __forceinline__ float gv_slices(u64 *pw, int nout, int o, int s_lo, int s_hi, int s_own, float own_v,
+                                           u64 t0, int &timeout)
 {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    if (w < M) {
-        float ms = 0.f;
-        for (int k = lane; k < R; k += 64) ms = fmaf(As[w * R + k], As[w * R + k], ms);
-        for (int o = 32; o > 0; o >>= 1) ms += __shfl_xor(ms, o);
-        if (lane == 0) rsc[w] = 1.0f / sqrtf(ms / (float)R + 1e-5f);
+    float v;
+    for (;;) {
+        bool ok = true;
+        v = 0.f;
+        for (int q0 = s_lo; q0 < s_hi; q0 += 16) {
+            u64 x[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) x[i] = gv_ld_agent(pw + (size_t)min(q0 + i, s_hi - 1) * nout + o);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int q = q0 + i;
+                if (q < s_hi) {
+                    if (q == s_own) v += own_v;
+                    else {
+                        ok = ok && (x[i] >> 32) == 1ull;
+                        v += __uint_as_float((u32)x[i]);
+                    }
+                }
+            }
+        }
+        if (ok) break;
+        if (wall_clock64() - t0 > GV_SPIN) { timeout = 1; break; }
+    }
+    for (int q = s_lo; q < s_hi; q++)
+        if (q != s_own) gv_st_agent(pw + (size_t)q * nout + o, 0ull);
+    return v;
+}
+
+// ------------------------------------------------------------------ mm --
+// Item (s, cb) of an NN problem: rows [s KS, min(R, s KS + KS)) of column
+// block cb.  Lane (r = lane / 16, c = lane % 16) of wave w reads row
+// kb + 16 u + 4 w + r, columns cb CB + VEC c .. + VEC - 1, for u < U.
+template <int MB, int VEC, int U, int PRO>
+__device__ __forceinline__ void gv_nn(const GvArgs &g, const GvProb &P, int s, int cb, GvSmem<MB, 16 * VEC> &sh)
+{
+    constexpr int CB = 16 * VEC;
+    typedef typename GvV<VEC>::T V;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r = lane >> 4, c = lane & 15;
+    const int M = P.M;
+    const GvSeg &G = P.seg[0];
+    const int j = cb * CB + c * VEC;
+    const int jc = j < P.No ? j : 0;                  // in-bounds address for edge lanes
+    const int k_lo = s * P.KS, k_hi = min(G.R, k_lo + P.KS);
+    float acc[MB][VEC];
+#pragma unroll
+    for (int m = 0; m < MB; m++)
+#pragma unroll
+        for (int v = 0; v < VEC; v++) acc[m][v] = 0.f;
+    // a batch: U rows per lane, every load first (clamped addresses), the
+    // rows past the slice zeroed when used
+    auto load = [&](V (&wv)[U], float (&av)[U][MB], int kb) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int k = min(kb + 16 * u + 4 * w + r, k_hi - 1);
+            wv[u] = gv_ld<VEC>(G.B + (size_t)k * G.ldb + jc);
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+                const size_t ai = (size_t)min(m, M - 1) * G.lda + k;
+                float a = gv_ld1(G.A + ai);
+                if (PRO == GV_PRO_SWIGLU) a = gv_silu_mul(a, gv_ld1(P.A2 + ai));
+                if (PRO == GV_PRO_RMS) a *= gv_ld1(P.gain + k);
+                av[u][m] = a;
+            }
+        }
+    };
+    auto fma_batch = [&](const V (&wv)[U], const float (&av)[U][MB], int kb) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const bool ok = kb + 16 * u + 4 * w + r < k_hi;
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+                const float a = ok ? av[u][m] : 0.f;
+#pragma unroll
+                for (int v = 0; v < VEC; v++) acc[m][v] = fmaf(a, gv_el(wv[u], v), acc[m][v]);
+            }
+        }
+    };
+    V wv[U];
+    float av[U][MB];
+    load(wv, av, k_lo);
+    // the RMS statistics' loads queue behind the first batch, in flight together
+    if (PRO == GV_PRO_RMS) gv_rms_stats<MB, CB>(G.A, G.lda, G.R, M, sh);
+    if (k_hi - k_lo <= 16 * U) {
+        fma_batch(wv, av, k_lo);
+    } else {
+        // longer slices: the next batch in flight while this one is used (the
+        // batch after the last re-reads the last rows, unused)
+        for (int kb = k_lo; kb < k_hi; kb += 16 * U) {
+            V nw[U];
+            float na[U][MB];
+            load(nw, na, min(kb + 16 * U, k_hi - 1));
+            fma_batch(wv, av, kb);
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                wv[u] = nw[u];
+#pragma unroll
+                for (int m = 0; m < MB; m++) av[u][m] = na[u][m];
+            }
+        }
+    }
+    // the 16 row groups of the item (4 lane rows x 4 waves), in fixed order
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+        V x;
+#pragma unroll
+        for (int v = 0; v < VEC; v++) gv_set(x, v, acc[m][v]);
+        *reinterpret_cast<V *>(&sh.s.red[w * 4 + r][m][c * VEC]) = x;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < M * R; e += blockDim.x) {
-        const int m = e / R, r = e - m * R;
-        As[e] = As[e] * rsc[m] * Gs[r];
+    const int nout = M * CB;
+    const bool split = P.S > 1, reducer = split && s == P.S - 1;
+    u64 *pw = g.part + P.part + (size_t)cb * P.S * nout;      // this block's S slices of nout words
+    for (int o = tid; o < nout; o += GV_T) {
+        const int m = o / CB, cc = o - m * CB;
+        float v = sh.s.red[0][m][cc];
+#pragma unroll
+        for (int q = 1; q < 16; q++) v += sh.s.red[q][m][cc];
+        if (!split) {
+            const int jj = cb * CB + cc;
+            if (jj < P.No) {
+                if (PRO == GV_PRO_RMS) v *= sh.rs[m];
+                float *out = P.C + (size_t)m * P.ldc + jj;
+                *out = P.beta ? *out + v : v;
+            }
+        } else if (!reducer) {
+            gv_st_agent(pw + (size_t)s * nout + o, GV_TAG | (u64)__float_as_uint(v));
+        } else {
+            sh.s.own[o] = v;
+        }
+    }
+    if (!reducer) return;
+    // the reducer: slices in order -- in G groups of consecutive slices per
+    // output when the outputs do not fill the workgroup, then the groups in
+    // order
+    if (tid == 0) sh.timeout = 0;
+    __syncthreads();
+    const int S = P.S;
+    const u64 t0 = wall_clock64();
+    if (nout >= GV_T) {
+        for (int o = tid; o < nout; o += GV_T)
+            sh.s.own[o] = gv_slices(pw, nout, o, 0, S, S - 1, sh.s.own[o], t0, sh.timeout);
+    } else {
+        const int G = GV_T / nout, grp = tid / nout, o = tid - grp * nout;
+        if (grp < G) sh.s.grp[grp][o] = gv_slices(pw, nout, o, grp * S / G, (grp + 1) * S / G, S - 1, sh.s.own[o], t0,
+                                                sh.timeout);
+    }
+    __syncthreads();
+    const bool bad = sh.timeout != 0;
+    for (int o = tid; o < nout; o += GV_T) {
+        const int m = o / CB, cc = o - m * CB, jj = cb * CB + cc;
+        float v;
+        if (nout >= GV_T) v = sh.s.own[o];
+        else {
+            const int G = GV_T / nout;
+            v = sh.s.grp[0][o];
+            for (int q = 1; q < G; q++) v += sh.s.grp[q][o];
+        }
+        if (jj < P.No) {
+            if (PRO == GV_PRO_RMS) v *= sh.rs[m];
+            float *out = P.C + (size_t)m * P.ldc + jj;
+            *out = bad ? __builtin_nanf("") : (P.beta ? *out + v : v);
+        }
+    }
+    if (bad && tid == 0) __hip_atomic_store((GAS u32 *)g.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------------------ mm, full K --
+// Item cb of a full-K NN problem owns columns [32 cb, 32 cb + 32) over all K
+// rows, so no other workgroup takes part in its sums.  Lane (rr = lane / 8,
+// c = lane % 8) of wave w reads rows 32 u + 8 w + rr, columns 32 cb + 4 c ..
+// + 3: 8 lanes cover one row's 128-byte line, and every load of the item
+// (16 UB per lane, K <= 512 UB) is issued before any is used.  The
+// activation rows are staged in LDS as [k][MB] through the prologue while the
+// weight loads are in flight; the 32 row groups of a column then meet in LDS
+// in a fixed order.
+template <int MB, int UB, int PRO>
+__device__ __forceinline__ void gv_nn_full(const GvProb &P, int cb, GvSmem<MB, 64> &sh)
+{
+    constexpr int UF = 16 * UB;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int rr = lane >> 3, c = lane & 7;
+    const int M = P.M;
+    const GvSeg &G = P.seg[0];
+    const int K = G.R;
+    const int j = cb * 32 + 4 * c;
+    const float *Bp = G.B + (j < P.No ? j : 0);
+    f32x4 wv[UF];
+#pragma unroll
+    for (int u = 0; u < UF; u++) wv[u] = gv_ld<4>(Bp + (size_t)min(32 * u + 8 * w + rr, K - 1) * G.ldb);
+    if (PRO == GV_PRO_RMS) gv_rms_stats<MB, 64>(G.A, G.lda, K, M, sh);
+    // the activation, [m][k] in memory -> act[k][m] in LDS: thread t takes
+    // columns 4 t .. 4 t + 3 of every row (K <= 1024), all loads first
+    {
+        constexpr int AU = (1024 / 4 + GV_T - 1) / GV_T;
+        f32x4 xa[AU][MB], xb[AU][MB];
+        const int K4 = K >> 2;
+#pragma unroll
+        for (int i = 0; i < AU; i++) {
+            const int k4 = min(tid + GV_T * i, K4 - 1);
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+                const size_t ai = (size_t)min(m, M - 1) * G.lda + 4 * k4;
+                xa[i][m] = gv_ld<4>(G.A + ai);
+                if (PRO == GV_PRO_SWIGLU) xb[i][m] = gv_ld<4>(P.A2 + ai);
+                if (PRO == GV_PRO_RMS && m == 0) xb[i][0] = gv_ld<4>(P.gain + 4 * k4);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < AU; i++) {
+            const int k4 = tid + GV_T * i;
+            if (k4 < K4) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    float a[MB];
+#pragma unroll
+                    for (int m = 0; m < MB; m++) {
+                        a[m] = xa[i][m][q];
+                        if (PRO == GV_PRO_SWIGLU) a[m] = gv_silu_mul(a[m], xb[i][m][q]);
+                        if (PRO == GV_PRO_RMS) a[m] *= xb[i][0][q];
+                    }
+                    float *dst = &sh.f.act[(4 * k4 + q) * MB];
+                    if (MB >= 4) {
+#pragma unroll
+                        for (int m4 = 0; m4 < MB; m4 += 4)
+                            *reinterpret_cast<f32x4 *>(dst + m4) = f32x4{a[m4], a[m4 + 1], a[m4 + 2], a[m4 + 3]};
+                    } else {
+#pragma unroll
+                        for (int m = 0; m < MB; m++) dst[m] = a[m];
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    float acc[MB][4];
+#pragma unroll
+    for (int m = 0; m < MB; m++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[m][v] = 0.f;
+#pragma unroll
+    for (int u = 0; u < UF; u++) {
+        const int k = 32 * u + 8 * w + rr;
+        const bool ok = k < K;
+        const float *ak = &sh.f.act[min(k, K - 1) * MB];
+        float a[MB];
+        if (MB >= 4) {
+#pragma unroll
+            for (int m4 = 0; m4 < MB; m4 += 4) {
+                const f32x4 t = *reinterpret_cast<const f32x4 *>(ak + m4);
+                a[m4] = t.x; a[m4 + 1] = t.y; a[m4 + 2] = t.z; a[m4 + 3] = t.w;
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < MB; m++) a[m] = ak[m];
+        }
+#pragma unroll
+        for (int m = 0; m < MB; m++) {
+            const float x = ok ? a[m] : 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[m][v] = fmaf(x, wv[u][v], acc[m][v]);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MB; m++)
+        *reinterpret_cast<f32x4 *>(&sh.f.red[w * 8 + rr][m][4 * c]) = f32x4{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
+    __syncthreads();
+    // the 32 row groups: NG groups of consecutive ones per output, then the
+    // groups in order (the partial sums reuse the activation's LDS)
+    constexpr int NO = 32 * MB, NG = GV_T / NO;
+    {
+        const int o = tid % NO, g = tid / NO, m = o / 32, cc = o % 32;
+        float v = sh.f.red[g * (32 / NG)][m][cc];
+#pragma unroll
+        for (int q = 1; q < 32 / NG; q++) v += sh.f.red[g * (32 / NG) + q][m][cc];
+        sh.f.act[g * NO + o] = v;
+    }
+    __syncthreads();
+    if (tid < NO) {
+        const int m = tid / 32, cc = tid % 32, jj = cb * 32 + cc;
+        float v = sh.f.act[tid];
+#pragma unroll
+        for (int g = 1; g < NG; g++) v += sh.f.act[g * NO + tid];
+        if (m < M && jj < P.No) {
+            if (PRO == GV_PRO_RMS) v *= sh.rs[m];
+            float *out = P.C + (size_t)m * P.ldc + jj;
+            *out = P.beta ? *out + v : v;
+        }
     }
 }
 
-// mm form.  Workgroup `blk` owns output columns [COLS blk, COLS blk + COLS).
-// Lane (c = lane % COLS, sub = lane / COLS) of wave w reads column c of W
-// rows k = q, q + SLOTS, q + 2 SLOTS, ... with q = (64 / COLS) w + sub: COLS
-// lanes cover 4 COLS contiguous bytes of a row, and the workgroup's SLOTS row
-// slots move through W together.  The partial sums of a column meet in fixed
-// order (shuffles within a wave, then LDS across waves).
-template <int MB, int COLS>
-__device__ __forceinline__ void gemv_nn(const GvProb &P, int blk, float *As, float *red, float *rsc, float *Gs)
+// --------------------------------------------------------------- mm_bt --
+// Item b of an NT problem: output rows o = 8 b + 2 w + lane / 32.  The 32
+// lanes of a half-wave read the row's reduction index in steps of 32 VEC
+// floats (U steps per batch, all loads of a batch first), then a butterfly
+// over the 32 lanes gives the M dot products.
+template <int MB, int VEC, int U, int PRO>
+__device__ __forceinline__ void gv_nt(const GvProb &P, int b, GvSmem<MB, 16 * VEC> &sh)
 {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    constexpr int SUBS = 64 / COLS, SLOTS = GV_WAVES * SUBS;
-    const int c = lane % COLS, q = w * SUBS + lane / COLS;
-    const int j = blk * COLS + c;
-    const int jc = j < P.No ? j : P.No - 1;      // in-bounds address for edge lanes
+    typedef typename GvV<VEC>::T V;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int l = lane & 31;
+    const int o = b * GV_NT_ROWS + 2 * w + (lane >> 5);
+    const int oc = min(o, P.No - 1);
+    const int M = P.M;
     float acc[MB];
 #pragma unroll
     for (int m = 0; m < MB; m++) acc[m] = 0.f;
-    for (int s = 0; s < P.nseg; s++) {
-        const GvSeg &g = P.seg[s];
-        const float *__restrict__ Bp = g.B + jc;
-        const int kc = GV_ACHUNK / P.M;
-        for (int r0 = 0; r0 < g.R; r0 += kc) {
-            const int kn = min(kc, g.R - r0);
-            // rows k = q + SLOTS u of this chunk, in batches of NN_U: every load
-            // of a batch is issued before any is used (rows past the chunk
-            // read a clamped address and are zeroed), and the next batch is
-            // in flight while the current one is consumed
-            float b[NN_U], nb[NN_U];
-            auto load = [&](float (&v)[NN_U], int k) {
+    auto load = [&](V (&wv)[U], V (&av)[U][MB], const GvSeg &G, const float *Brow, int r0) {
 #pragma unroll
-                for (int u = 0; u < NN_U; u++) {
-                    const int kk = k + SLOTS * u;
-                    const float x = Bp[(size_t)(r0 + min(kk, kn - 1)) * g.ldb];
-                    v[u] = kk < kn ? x : 0.f;
+        for (int u = 0; u < U; u++) {
+            const int rr = min(r0 + (32 * u + l) * VEC, G.R - VEC);
+            wv[u] = gv_ld<VEC>(Brow + rr);
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+                const size_t ai = (size_t)min(m, M - 1) * G.lda + rr;
+                V a = gv_ld<VEC>(G.A + ai);
+                if (PRO == GV_PRO_SWIGLU) {
+                    const V a2 = gv_ld<VEC>(P.A2 + ai);
+#pragma unroll
+                    for (int v = 0; v < VEC; v++) gv_set(a, v, gv_silu_mul(gv_el(a, v), gv_el(a2, v)));
                 }
-            };
-            load(b, q);
-            __syncthreads();                     // previous chunk fully read
-            stage_rows(As, Gs, P, g, r0, kn);
-            __syncthreads();
-            if (P.pro == GV_PRO_RMS) {
-                rms_finish(As, Gs, rsc, P.M, kn);
-                __syncthreads();
+                if (PRO == GV_PRO_RMS) {
+                    const V gn = gv_ld<VEC>(P.gain + rr);
+#pragma unroll
+                    for (int v = 0; v < VEC; v++) gv_set(a, v, gv_el(a, v) * gv_el(gn, v));
+                }
+                av[u][m] = a;
             }
-            for (int k = q; k < kn; k += SLOTS * NN_U) {
-                if (k + SLOTS * NN_U < kn) load(nb, k + SLOTS * NN_U);
+        }
+    };
+    auto fma_batch = [&](const V (&wv)[U], const V (&av)[U][MB], const GvSeg &G, int r0) {
 #pragma unroll
-                for (int m = 0; m < MB; m++)
-                    if (m < P.M)
+        for (int u = 0; u < U; u++) {
+            const bool ok = r0 + (32 * u + l) * VEC < G.R;
 #pragma unroll
-                        for (int u = 0; u < NN_U; u++)
-                            acc[m] = fmaf(As[m * kn + min(k + SLOTS * u, kn - 1)], b[u], acc[m]);
+            for (int m = 0; m < MB; m++)
 #pragma unroll
-                for (int u = 0; u < NN_U; u++) b[u] = nb[u];
+                for (int v = 0; v < VEC; v++)
+                    acc[m] = fmaf(ok ? gv_el(av[u][m], v) : 0.f, gv_el(wv[u], v), acc[m]);
+        }
+    };
+    for (int sg = 0; sg < P.nseg; sg++) {
+        const GvSeg &G = P.seg[sg];
+        const float *Brow = G.B + (size_t)oc * G.ldb;
+        V wv[U];
+        V av[U][MB];
+        load(wv, av, G, Brow, 0);
+        if (PRO == GV_PRO_RMS && sg == 0) gv_rms_stats<MB, 16 * VEC>(G.A, G.lda, G.R, M, sh);
+        if (G.R <= 32 * VEC * U) {
+            fma_batch(wv, av, G, 0);
+        } else {
+            for (int r0 = 0; r0 < G.R; r0 += 32 * VEC * U) {
+                V nw[U];
+                V na[U][MB];
+                load(nw, na, G, Brow, min(r0 + 32 * VEC * U, G.R - VEC));
+                fma_batch(wv, av, G, r0);
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    wv[u] = nw[u];
+#pragma unroll
+                    for (int m = 0; m < MB; m++) av[u][m] = na[u][m];
+                }
             }
         }
     }
-    // the 4 row slots of a wave, then the 8 waves, in fixed order
 #pragma unroll
     for (int m = 0; m < MB; m++) {
 #pragma unroll
-        for (int o = COLS; o < 64; o <<= 1) acc[m] += __shfl_xor(acc[m], o);
+        for (int x = 16; x > 0; x >>= 1) acc[m] += __shfl_xor(acc[m], x);
     }
-    if (lane < COLS)
+    if (PRO == GV_PRO_RMS) __syncthreads();           // sh.rs
+    if (l == 0 && o < P.No) {
 #pragma unroll
-        for (int m = 0; m < MB; m++) red[(w * MB + m) * COLS + lane] = acc[m];
-    __syncthreads();
-    const int t = threadIdx.x;
-    if (t < COLS * MB) {
-        const int m = t / COLS, cc = t % COLS, jj = blk * COLS + cc;
-        if (m < P.M && jj < P.No) {
-            float v = red[m * COLS + cc];
-#pragma unroll
-            for (int ww = 1; ww < GV_WAVES; ww++) v += red[(ww * MB + m) * COLS + cc];
-            float *o = P.C + (size_t)m * P.ldc + jj;
-            *o = P.beta ? *o + v : v;
-        }
+        for (int m = 0; m < MB; m++)
+            if (m < M) {
+                float v = acc[m];
+                if (PRO == GV_PRO_RMS) v *= sh.rs[m];
+                float *out = P.C + (size_t)m * P.ldc + o;
+                *out = P.beta ? *out + v : v;
+            }
     }
 }
 
-// mm_bt form.  Wave w of workgroup `blk` owns W rows k0, k0 + 1; its lanes
-// stride the reduction index n (coalesced), and each of the 2*M dot
-// products ends in a butterfly reduction over the 64 lanes.
-template <int MB>
-__device__ __forceinline__ void gemv_nt(const GvProb &P, int blk, float *As, float *rsc, float *Gs)
+// Workgroup b: the items that never wait first (every problem's direct
+// items in problem order), then the reducers.
+template <int MB, int VEC, int U, int PRO>
+__global__ __launch_bounds__(GV_T) void k_gemv(GvArgs g)
 {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int k0 = (blk * GV_WAVES + w) * GV_NT_ROWS;
-    float acc[GV_NT_ROWS][MB];
-#pragma unroll
-    for (int r = 0; r < GV_NT_ROWS; r++)
-#pragma unroll
-        for (int m = 0; m < MB; m++) acc[r][m] = 0.f;
-    for (int s = 0; s < P.nseg; s++) {
-        const GvSeg &g = P.seg[s];
-        const float *brow[GV_NT_ROWS];
-#pragma unroll
-        for (int r = 0; r < GV_NT_ROWS; r++) brow[r] = g.B + (size_t)min(k0 + r, P.No - 1) * g.ldb;
-        const int kc = GV_ACHUNK / P.M;
-        for (int r0 = 0; r0 < g.R; r0 += kc) {
-            const int kn = min(kc, g.R - r0);
-            // n = lane + 64 u in batches of NT_U, issued ahead as in gemv_nn
-            float b[GV_NT_ROWS][NT_U], nb[GV_NT_ROWS][NT_U];
-            auto load = [&](float (&v)[GV_NT_ROWS][NT_U], int n) {
-#pragma unroll
-                for (int r = 0; r < GV_NT_ROWS; r++)
-#pragma unroll
-                    for (int u = 0; u < NT_U; u++) {
-                        const int nn = n + 64 * u;
-                        const float x = brow[r][r0 + min(nn, kn - 1)];
-                        v[r][u] = nn < kn ? x : 0.f;
-                    }
-            };
-            load(b, lane);
-            __syncthreads();
-            stage_rows(As, Gs, P, g, r0, kn);
-            __syncthreads();
-            if (P.pro == GV_PRO_RMS) {
-                rms_finish(As, Gs, rsc, P.M, kn);
-                __syncthreads();
-            }
-            for (int n = lane; n < kn; n += 64 * NT_U) {
-                if (n + 64 * NT_U < kn) load(nb, n + 64 * NT_U);
-#pragma unroll
-                for (int m = 0; m < MB; m++)
-                    if (m < P.M)
-#pragma unroll
-                        for (int u = 0; u < NT_U; u++) {
-                            const float a = As[m * kn + min(n + 64 * u, kn - 1)];
-#pragma unroll
-                            for (int r = 0; r < GV_NT_ROWS; r++) acc[r][m] = fmaf(a, b[r][u], acc[r][m]);
-                        }
-#pragma unroll
-                for (int r = 0; r < GV_NT_ROWS; r++)
-#pragma unroll
-                    for (int u = 0; u < NT_U; u++) b[r][u] = nb[r][u];
-            }
-        }
+    __shared__ GvSmem<MB, 16 * VEC> sh;
+    int b = blockIdx.x, p = 0;
+    while (p < g.nprob && b >= g.p[p].direct) { b -= g.p[p].direct; p++; }
+    if (p < g.nprob) {
+        const GvProb &P = g.p[p];
+        if (P.kind == TLG_NN && P.full) {
+            if constexpr (VEC == 4) gv_nn_full<MB, (U >= 2 ? 2 : 1), PRO>(P, b, sh);
+        } else if (P.kind == TLG_NN) gv_nn<MB, VEC, U, PRO>(g, P, b / P.nb, b % P.nb, sh);
+        else gv_nt<MB, VEC, U, PRO>(P, b, sh);
+        return;
     }
-#pragma unroll
-    for (int r = 0; r < GV_NT_ROWS; r++)
-#pragma unroll
-        for (int m = 0; m < MB; m++) {
-            float v = acc[r][m];
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-            acc[r][m] = v;
-        }
-    if (lane < GV_NT_ROWS * MB) {
-        // lane (r, m) writes output (m, k0 + r); select its value without
-        // indexing the register array by a lane-dependent index
-        const int r = lane / MB, m = lane % MB;
-        float v = 0.f;
-#pragma unroll
-        for (int rr = 0; rr < GV_NT_ROWS; rr++)
-#pragma unroll
-            for (int mm = 0; mm < MB; mm++)
-                if (rr == r && mm == m) v = acc[rr][mm];
-        const int k = k0 + r;
-        if (k < P.No && m < P.M) {
-            float *o = P.C + (size_t)m * P.ldc + k;
-            *o = P.beta ? *o + v : v;
-        }
-    }
-}
-
-template <int MB, int COLS>
-__global__ __launch_bounds__(64 * GV_WAVES) void k_gemv(GvArgs g)
-{
-    __shared__ float As[GV_ACHUNK];
-    __shared__ float red[GV_WAVES * MB * COLS];
-    __shared__ float rsc[GV_WAVES];
-    __shared__ float Gs[GV_ACHUNK];
-    // consecutive column blocks share cache lines (a block reads COLS floats
-    // of each row, a line holds 32): dealt to one XCD they meet in its L2
-    // instead of being fetched from HBM once per XCD
-    int b = xcd_remap(blockIdx.x, gridDim.x), p = 0;
-    while (p < g.nprob && b >= g.p[p].blocks) { b -= g.p[p].blocks; p++; }
+    p = 0;
+    while (p < g.nprob && b >= g.p[p].reducers) { b -= g.p[p].reducers; p++; }
     if (p >= g.nprob) return;
     const GvProb &P = g.p[p];
-    if (P.kind == TLG_NN) gemv_nn<MB, COLS>(P, b, As, red, rsc, Gs);
-    else gemv_nt<MB>(P, b, As, rsc, Gs);
+    gv_nn<MB, VEC, U, PRO>(g, P, P.S - 1, b, sh);
 }
 
 // ---------------------------------------------------------------- host --
@@ -288,63 +586,195 @@ bool tlg_gemv_fits(TlgKind kind, int Mo) { return kind != TLG_TN && Mo >= 1 && M
 
 static int rows_bucket(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
-static void set_blocks(GvProb &P, int cols)
-{
-    const int per = P.kind == TLG_NN ? cols : GV_WAVES * GV_NT_ROWS;
-    P.blocks = (P.No + per - 1) / per;
-}
+static u64 *g_part;                 // GV_RING regions of GV_REGION_WORDS
+static u32 *g_err;
+static unsigned g_ring;
+static char g_last_name[48] = "k_gemv";
 
-// Columns per workgroup of the mm form for a launch: nn_cols(), unless
-// TLG_GEMV_COLS (4, 8 or 16) pins it for sweeps.
-static int launch_cols(int mb)
+int tlg_gemv_init(void)
 {
-    static int forced = -1;
-    if (forced < 0) {
-        const char *e = getenv("TLG_GEMV_COLS");
-        const int v = e ? atoi(e) : 0;
-        forced = (v == 4 || v == 8 || v == 16) ? v : 0;
-    }
-    return forced ? forced : nn_cols(mb);
-}
-
-template <int MB>
-static void launch_mb(const GvArgs &a, int grid, int cols, hipStream_t st)
-{
-    switch (cols) {
-    case 4: hipLaunchKernelGGL((k_gemv<MB, 4>), dim3(grid), dim3(64 * GV_WAVES), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((k_gemv<MB, 8>), dim3(grid), dim3(64 * GV_WAVES), 0, st, a); break;
-    default: hipLaunchKernelGGL((k_gemv<MB, 16>), dim3(grid), dim3(64 * GV_WAVES), 0, st, a); break;
-    }
-}
-
-static int launch(GvArgs &a, int mb, hipStream_t st)
-{
-    const int cols = launch_cols(mb);
-    int grid = 0;
-    for (int i = 0; i < a.nprob; i++) {
-        set_blocks(a.p[i], cols);
-        grid += a.p[i].blocks;
-    }
-    if (grid == 0) return TLG_OK;
-    switch (mb) {
-    case 1: launch_mb<1>(a, grid, cols, st); break;
-    case 2: launch_mb<2>(a, grid, cols, st); break;
-    case 4: launch_mb<4>(a, grid, cols, st); break;
-    default: launch_mb<8>(a, grid, cols, st); break;
-    }
-    TLG_HIP(hipGetLastError());
+    if (g_part) return TLG_OK;
+    void *p = nullptr;
+    const size_t bytes = GV_RING * GV_REGION_WORDS * sizeof(u64) + 256;
+    if (hipMalloc(&p, bytes) != hipSuccess) return tlg_fail(TLG_ENOMEM, "GEMV workspace of %zu bytes", bytes);
+    TLG_HIP(hipMemset(p, 0, bytes));
+    TLG_HIP(hipDeviceSynchronize());
+    g_part = (u64 *)p;
+    g_err = (u32 *)((char *)p + GV_RING * GV_REGION_WORDS * sizeof(u64));
+    g_ring = 0;
     return TLG_OK;
 }
 
+void tlg_gemv_release(void)
+{
+    if (g_part) (void)hipFree(g_part);
+    g_part = nullptr;
+    g_err = nullptr;
+}
+
+extern "C" int tlg_gemv_status(void)
+{
+    if (!g_err) return 0;
+    u32 v = 0;
+    if (hipMemcpy(&v, g_err, sizeof v, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    return (int)v;
+}
+
+// Rows per NN item: the launch's NN bytes over a target item count, in
+// multiples of 16 rows (TLG_GEMV_ITEMS, TLG_GEMV_KS override for sweeps).
+static int env_int(const char *name, int dflt)
+{
+    const char *e = getenv(name);
+    return e && *e ? atoi(e) : dflt;
+}
+
+template <int MB, int VEC, int PRO>
+static void launch_u(const GvArgs &a, int grid, int U, hipStream_t st)
+{
+    switch (U) {
+    case 1: hipLaunchKernelGGL((k_gemv<MB, VEC, 1, PRO>), dim3(grid), dim3(GV_T), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((k_gemv<MB, VEC, 2, PRO>), dim3(grid), dim3(GV_T), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((k_gemv<MB, VEC, 3, PRO>), dim3(grid), dim3(GV_T), 0, st, a); break;
+    default: hipLaunchKernelGGL((k_gemv<MB, VEC, 4, PRO>), dim3(grid), dim3(GV_T), 0, st, a); break;
+    }
+}
+template <int MB>
+static void launch_mb(const GvArgs &a, int grid, int vec, int U, int pro, hipStream_t st)
+{
+    if (vec == 1) { hipLaunchKernelGGL((k_gemv<MB, 1, 4, GV_PRO_NONE>), dim3(grid), dim3(GV_T), 0, st, a); return; }
+    switch (pro) {
+    case GV_PRO_RMS: launch_u<MB, 4, GV_PRO_RMS>(a, grid, U, st); break;
+    case GV_PRO_SWIGLU: launch_u<MB, 4, GV_PRO_SWIGLU>(a, grid, U, st); break;
+    default: launch_u<MB, 4, GV_PRO_NONE>(a, grid, U, st); break;
+    }
+}
+
+static bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// Decompose the problems, pick the instance and launch.  pro is the launch's
+// prologue (every problem shares it).
+static int launch(GvArgs &a, int pro, hipStream_t st)
+{
+    int rc = tlg_gemv_init();
+    if (rc) return rc;
+    int mb = 1, vec = 4;
+    for (int i = 0; i < a.nprob; i++) {
+        GvProb &P = a.p[i];
+        mb = max(mb, rows_bucket(P.M));
+        bool v4 = true;
+        for (int s = 0; s < P.nseg; s++) {
+            const GvSeg &g = P.seg[s];
+            if (P.kind == TLG_NN) v4 = v4 && P.No % 4 == 0 && g.ldb % 4 == 0 && al16(g.B);
+            else v4 = v4 && g.R % 4 == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 && al16(g.A) && al16(g.B);
+        }
+        if (pro == GV_PRO_SWIGLU) v4 = v4 && al16(P.A2);
+        if (pro == GV_PRO_RMS) v4 = v4 && al16(P.gain);
+        if (pro != GV_PRO_NONE) v4 = v4 && P.seg[0].R % 4 == 0 && P.seg[0].lda % 4 == 0 && al16(P.seg[0].A);
+        if (!v4) vec = 1;
+    }
+    if (vec == 1 && pro != GV_PRO_NONE)
+        return tlg_fail(TLG_EINVAL, "dec_gemv: prologue operands need 16-byte aligned rows of 4k floats");
+    const int CB = 16 * vec;
+    // full-K items where the activation fits LDS (TLG_GEMV_SPLIT=1 forces
+    // the split form, for sweeps)
+    const int force_split = env_int("TLG_GEMV_SPLIT", 0);
+    for (int i = 0; i < a.nprob; i++) {
+        GvProb &P = a.p[i];
+        const GvSeg &g = P.seg[0];
+        P.full = P.kind == TLG_NN && vec == 4 && !force_split && g.R % 4 == 0 && g.lda % 4 == 0 && al16(g.A) &&
+                 g.R <= GV_FULL_K && (long long)g.R * mb <= GV_FULL_ACT;
+    }
+    // rows per split NN item: the split problems' bytes over a target item
+    // count, in multiples of 16 rows (TLG_GEMV_ITEMS, TLG_GEMV_KS override)
+    double nn_bytes = 0;
+    int nt_items = 0, maxr_nt = 0, maxr_nn = 0;
+    bool any_split = false;
+    for (int i = 0; i < a.nprob; i++) {
+        GvProb &P = a.p[i];
+        if (P.kind == TLG_NN && !P.full) {
+            nn_bytes += 4.0 * P.seg[0].R * ((P.No + CB - 1) / CB) * CB;
+            maxr_nn = max(maxr_nn, P.seg[0].R);
+            any_split = true;
+        } else if (P.kind == TLG_NT) {
+            nt_items += (P.No + GV_NT_ROWS - 1) / GV_NT_ROWS;
+            for (int s = 0; s < P.nseg; s++) maxr_nt = max(maxr_nt, P.seg[s].R);
+        }
+    }
+    const int target = max(64, env_int("TLG_GEMV_ITEMS", 512) - nt_items);
+    int KS = env_int("TLG_GEMV_KS", 0);
+    if (KS <= 0) {
+        const double rows = nn_bytes / target / (4.0 * CB);
+        KS = 16 * max(1, (int)(rows / 16 + 0.5));
+    }
+    // at most 64 / M slices per column block: the reducer then reads at most
+    // 16 words per output and thread
+    const int smax = max(4, 64 / mb);
+    if (maxr_nn > (long long)smax * KS) KS = (maxr_nn + smax - 1) / smax;
+    KS = (KS + 15) / 16 * 16;
+    for (;;) {
+        size_t words = 0;
+        for (int i = 0; i < a.nprob; i++) {
+            GvProb &P = a.p[i];
+            if (P.kind != TLG_NN || P.full) continue;
+            P.nb = (P.No + CB - 1) / CB;
+            P.KS = KS;
+            P.S = (P.seg[0].R + KS - 1) / KS;
+            if (P.S > 1) words += (size_t)P.nb * P.S * P.M * CB;
+        }
+        if (words <= GV_REGION_WORDS) break;
+        KS *= 2;
+    }
+    long long off = 0;
+    int grid = 0;
+    for (int i = 0; i < a.nprob; i++) {
+        GvProb &P = a.p[i];
+        if (P.full) {
+            P.nb = (P.No + 31) / 32;
+            P.S = 1; P.KS = P.seg[0].R; P.part = 0;
+            P.direct = P.nb;
+            P.reducers = 0;
+        } else if (P.kind == TLG_NN) {
+            P.part = off;
+            if (P.S > 1) off += (long long)P.nb * P.S * P.M * CB;
+            P.reducers = P.S > 1 ? P.nb : 0;
+            P.direct = P.nb * P.S - P.reducers;
+        } else {
+            P.nb = (P.No + GV_NT_ROWS - 1) / GV_NT_ROWS;
+            P.S = 1; P.KS = 0; P.part = 0;
+            P.direct = P.nb; P.reducers = 0;
+        }
+        grid += P.direct + P.reducers;
+    }
+    if (grid == 0) return TLG_OK;
+    a.part = g_part + (size_t)(g_ring++ % GV_RING) * GV_REGION_WORDS;
+    a.err = g_err;
+    // batch depth of the split mm and mm_bt paths (full-K items use their own)
+    int U = 4;
+    if (vec == 4) {
+        int maxr_full = 0;
+        for (int i = 0; i < a.nprob; i++) if (a.p[i].full) maxr_full = max(maxr_full, a.p[i].seg[0].R);
+        const int u_nn = any_split ? min(4, KS / 16) : 0;
+        const int u_nt = maxr_nt ? min(4, (maxr_nt + 127) / 128) : 0;
+        const int u_full = maxr_full > 512 ? 2 : maxr_full ? 1 : 0;     // full-K batches: min(U, 2)
+        U = max(1, max(u_full, max(u_nn, u_nt)));
+    }
+    switch (mb) {
+    case 1: launch_mb<1>(a, grid, vec, U, pro, st); break;
+    case 2: launch_mb<2>(a, grid, vec, U, pro, st); break;
+    case 4: launch_mb<4>(a, grid, vec, U, pro, st); break;
+    default: launch_mb<8>(a, grid, vec, U, pro, st); break;
+    }
+    TLG_HIP(hipGetLastError());
+    snprintf(g_last_name, sizeof g_last_name, "k_gemv<%d, %d, %d, %d>", mb, vec, vec == 1 ? 4 : U,
+             vec == 1 ? 0 : pro);
+    return TLG_OK;
+}
+
+// The instance name of the last launch, as rocprofv3 prints it.
 const char *tlg_gemv_kernel_name(int M)
 {
-    // as rocprofv3 names the instance the launch uses
-    static char names[4][3][24];
-    const int mb = rows_bucket(M), cols = launch_cols(mb);
-    const int mi = mb == 1 ? 0 : mb == 2 ? 1 : mb == 4 ? 2 : 3, ci = cols == 4 ? 0 : cols == 8 ? 1 : 2;
-    char *n = names[mi][ci];
-    if (!n[0]) snprintf(n, sizeof names[0][0], "k_gemv<%d, %d>", mb, cols);
-    return n;
+    (void)M;
+    return g_last_name;
 }
 
 int tlg_gemv_launch(TlgKind kind, const float *A, const float *B, float *C, int Mo, int No, int R, int lda,
@@ -356,7 +786,7 @@ int tlg_gemv_launch(TlgKind kind, const float *A, const float *B, float *C, int 
     P.C = C; P.kind = kind; P.M = Mo; P.No = No; P.ldc = ldc; P.beta = beta; P.nseg = 1;
     P.seg[0] = GvSeg{A, B, R, lda, ldb};
     a.nprob = 1;
-    return launch(a, rows_bucket(Mo), st);
+    return launch(a, GV_PRO_NONE, st);
 }
 
 // A grouped launch whose calls are all mm / mm_bt at M <= 8 (decode runs).
@@ -365,7 +795,6 @@ int tlg_gemv_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
     if (n > GV_MAXPROB) return tlg_fail(TLG_EINVAL, "GEMV group: at most %d calls", GV_MAXPROB);
     GvArgs a;
     memset(&a, 0, sizeof a);
-    int mmax = 1;
     for (int i = 0; i < n; i++) {
         const TlgGemmCall &c = calls[i];
         GvProb &P = a.p[i];
@@ -386,50 +815,57 @@ int tlg_gemv_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
             if (!P.seg[s].A || !P.seg[s].B || P.seg[s].R <= 0)
                 return tlg_fail(TLG_EINVAL, "GEMV group: call %d: empty or NULL operand", i);
         if (!P.C || P.No <= 0) return tlg_fail(TLG_EINVAL, "GEMV group: call %d: empty output", i);
-        if (P.M > mmax) mmax = P.M;
     }
     a.nprob = n;
-    return launch(a, rows_bucket(mmax), st);
+    return launch(a, GV_PRO_NONE, st);
 }
 
 // A decode run with the glue folded in (include/tldecode.h): the calls'
-// prologues (RMSNorm, SwiGLU) apply while the activation rows are staged,
-// and beta = 1 adds the result into C (mm's residual add).
+// prologues (RMSNorm, SwiGLU) apply as the activation rows are read, and
+// beta = 1 adds the result into C (mm's residual add).  Calls with different
+// prologues go to separate launches, one per prologue, in call order.
 extern "C" int tlg_dev_dec_gemv(const TlgDecGemv *calls, int n, void *stream)
 {
     int rc = tlg_ensure_init();
     if (rc) return rc;
     if (!calls || n <= 0 || n > GV_MAXPROB) return tlg_fail(TLG_EINVAL, "dec_gemv: 1 to %d calls", GV_MAXPROB);
     hipStream_t st = (hipStream_t)stream;
-    rc = tlg_group_flush_launch(st);             // pending split reductions land first
-    if (rc) return rc;
-    GvArgs a;
-    memset(&a, 0, sizeof a);
-    int mmax = 1;
     for (int i = 0; i < n; i++) {
         const TlgDecGemv &c = calls[i];
-        GvProb &P = a.p[i];
+        const int R = c.op == 0 ? c.K : c.N;
         if ((c.op != 0 && c.op != 1) || c.M < 1 || c.M > 8 || c.K <= 0 || c.N <= 0 || !c.A || !c.B || !c.C ||
             c.pro < GV_PRO_NONE || c.pro > GV_PRO_SWIGLU || (c.pro == GV_PRO_RMS && !c.gain) ||
-            (c.pro == GV_PRO_SWIGLU && !c.A2) || (c.pro == GV_PRO_RMS && c.M * (c.op == 0 ? c.K : c.N) > GV_ACHUNK))
+            (c.pro == GV_PRO_SWIGLU && !c.A2) || (c.pro != GV_PRO_NONE && (R % 4 || !al16(c.A))))
             return tlg_fail(TLG_EINVAL, "dec_gemv: call %d: op=%d M=%d K=%d N=%d pro=%d", i, c.op, c.M, c.K, c.N,
                             c.pro);
-        P.C = c.C;
-        P.M = c.M;
-        P.nseg = 1;
-        P.beta = c.beta ? 1 : 0;
-        P.pro = c.pro;
-        P.gain = c.gain;
-        P.A2 = c.A2;
-        if (c.op == 0) {
-            P.kind = TLG_NN; P.No = c.N; P.ldc = c.N;
-            P.seg[0] = GvSeg{c.A, c.B, c.K, c.K, c.N};
-        } else {
-            P.kind = TLG_NT; P.No = c.K; P.ldc = c.K;
-            P.seg[0] = GvSeg{c.A, c.B, c.N, c.N, c.N};
-        }
-        if (c.M > mmax) mmax = c.M;
     }
-    a.nprob = n;
-    return launch(a, rows_bucket(mmax), st);
+    rc = tlg_group_flush_launch(st);             // pending split reductions land first
+    if (rc) return rc;
+    for (int pro = GV_PRO_NONE; pro <= GV_PRO_SWIGLU; pro++) {
+        GvArgs a;
+        memset(&a, 0, sizeof a);
+        for (int i = 0; i < n; i++) {
+            const TlgDecGemv &c = calls[i];
+            if (c.pro != pro) continue;
+            GvProb &P = a.p[a.nprob++];
+            P.C = c.C;
+            P.M = c.M;
+            P.nseg = 1;
+            P.beta = c.beta ? 1 : 0;
+            P.gain = c.gain;
+            P.A2 = c.A2;
+            if (c.op == 0) {
+                P.kind = TLG_NN; P.No = c.N; P.ldc = c.N;
+                P.seg[0] = GvSeg{c.A, c.B, c.K, c.K, c.N};
+            } else {
+                P.kind = TLG_NT; P.No = c.K; P.ldc = c.K;
+                P.seg[0] = GvSeg{c.A, c.B, c.N, c.N, c.N};
+            }
+        }
+        if (a.nprob) {
+            rc = launch(a, pro, st);
+            if (rc) return rc;
+        }
+    }
+    return TLG_OK;
 }

@@ -46,6 +46,7 @@ int tlg_zero_launch(float *dst, size_t n, hipStream_t st);
 int tlg_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len, int *splits);
 int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st);
 int tlg_group_flush_launch(hipStream_t st);
+int tlg_group_drain(hipStream_t st);
 int tlg_defer_colsum(const float *part, float *C, int splits, int No, int beta, hipStream_t st);
 
 // One GEMM over every expert of a top-1 MoE layer whose token rows are
@@ -87,6 +88,8 @@ int tlg_gemv_launch(TlgKind kind, const float *A, const float *B, float *C, int 
                     int ldb, int ldc, int beta, hipStream_t st);
 int tlg_gemv_group_launch(const TlgGemmCall *calls, int n, hipStream_t st);
 const char *tlg_gemv_kernel_name(int M);
+int tlg_gemv_init(void);
+void tlg_gemv_release(void);
 
 // Workgroup id -> logical work item, so that consecutive logical items land
 // on the same XCD (the dispatcher deals workgroups round-robin over the 8

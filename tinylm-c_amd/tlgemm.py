@@ -62,6 +62,7 @@ SIGNATURES = {
     "tlg_dev_gemm_flush": (_i, [_vp]),
     "tlg_dev_gemm_pending": (_i, []),
     "tlg_group_kernel": (ctypes.c_char_p, []),
+    "tlg_gemv_status": (_i, []),
     "tlg_tune_group": (_i, [_i]),
     "tlg_tune_group_policy": (_i, [_ip, _i, ctypes.c_double, _i]),
     "tlg_tune_group_split": (_i, [_i]),
