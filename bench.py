@@ -260,25 +260,31 @@ def bench_train_config(lib, host, stream, name, steps, tune=True, retime=False):
     }
 
 
-def bench_decode(lib, host, stream, steps, M=1, pool=6):
+def bench_decode(lib, host, stream, steps, M=1, pool=6, packed=False, eager=False):
     """cfg3: per token 8 layers x 7 GEMVs + unembed at M rows, one grouped
     launch per GEMV run (q/k/v, o, w1/w3, w2, head: the reference runs glue
     between them); the weights (52.7 MB) rotate through `pool` copies
-    (> 256 MB Infinity Cache).  Steps are enqueued directly: with one launch
-    per run a graph replay measured the same."""
-    plan = host.plan_decode(M, **DECODE)
+    (> 256 MB Infinity Cache).  packed: the decode layout (every linear
+    weight stored transposed, each mm as memset + mm_bt), as the device
+    decoder keeps its weights.  Steps are replayed from a HIP graph."""
+    plan = host.plan_decode(M, packed=packed, **DECODE)
     run = host.dll.tl_run_new(ctypes.byref(plan.raw), pool)
     if not run:
         raise RuntimeError("tl_run_new(decode) failed")
     check(host.dll.tl_run_fill(run, 7, stream), "fill")
-    step = lambda: host.dll.tl_run_step_grouped(run, stream)  # noqa: E731
+    if eager:                       # launch by launch (profilers trace these)
+        step = lambda: host.dll.tl_run_step_grouped(run, stream)  # noqa: E731
+    else:
+        check(host.dll.tl_run_graph_build(run, stream, 1), "decode graph")
+        step = lambda: host.dll.tl_run_graph_step(run, stream)  # noqa: E731
     for _ in range(2 * pool):
         check(step(), "decode warmup")
     ms, _ = time_steps(lib, step, stream, steps)
     launches = host.dll.tl_run_grouped_launches(run)
     wbytes = sum(4.0 * c["K"] * c["N"] for c in plan.calls if c["op"] != "zero")
-    allbytes = sum(4.0 * (c["M"] * c["K"] + c["K"] * c["N"] + c["M"] * c["N"] * (2 if c["op"] != "mm" else 1))
-                   for c in plan.calls if c["op"] != "zero")
+    # weights, the activation rows in, the output rows out (a clear folded
+    # into the GEMV makes every output a set)
+    allbytes = sum(4.0 * (c["K"] * c["N"] + c["M"] * (c["K"] + c["N"])) for c in plan.calls if c["op"] != "zero")
     per_tok_ms = ms / steps
     host.dll.tl_run_free(run)
     return {
@@ -290,6 +296,8 @@ def bench_decode(lib, host, stream, steps, M=1, pool=6):
         "gemv_calls_per_step": sum(1 for c in plan.calls if c["op"] != "zero"),
         "launches_per_step": launches,
         "weight_pool_copies": pool,
+        "layout": "decode (W^T, mm_bt form)" if packed else "reference (W [in][out], mm)",
+        "launch": "launch by launch" if eager else "one HIP graph per step",
     }
 
 
@@ -576,6 +584,7 @@ def bench_decode_step(lib, host, stream, steps, pool=6, prompt_len=16, warmup=8,
     dec.set_fused(fused)
     for c in range(pool):
         check(lib.tlg_dev_fill_normal(dec.params(c), dec.np, 77, 0.02, stream), "fill P")
+    dec.pack(stream)
     dec.reset(stream)
     prompt = np.random.default_rng(5).integers(0, DECODE_MODEL["V"], prompt_len).astype(np.int32)
     t0 = time.perf_counter()
@@ -614,6 +623,7 @@ def bench_decode_persist(lib, host, stream, steps, pool=6, prompt_len=16, warmup
     dec = host.decode(DECODE_MODEL, 256, kv_f16=1, exact_exp=0, maxpos=maxpos, mmax=8, pool=pool)
     for c in range(pool):
         check(lib.tlg_dev_fill_normal(dec.params(c), dec.np, 77, 0.02, stream), "fill P")
+    dec.pack(stream)
     dec.reset(stream)
     prompt = np.random.default_rng(5).integers(0, DECODE_MODEL["V"], prompt_len).astype(np.int32)
     dec.prime(prompt, stream)
@@ -644,6 +654,7 @@ def bench_decode_chunks(lib, host, stream, M, positions=512, pool=6, prompt_len=
     dec = host.decode(DECODE_MODEL, 256, kv_f16=1, exact_exp=0, maxpos=maxpos, mmax=8, pool=pool)
     for c in range(pool):
         check(lib.tlg_dev_fill_normal(dec.params(c), dec.np, 77, 0.02, stream), "fill P")
+    dec.pack(stream)
     dec.reset(stream)
     rng = np.random.default_rng(5)
     prompt = rng.integers(0, DECODE_MODEL["V"], prompt_len).astype(np.int32)
@@ -842,11 +853,15 @@ def main():
                 others[name] = bench_train_config(lib, host, stream, name, args.other_steps,
                                                   tune=not args.no_autotune, retime=args.autotune)
                 log(f"[train] {name}: {others[name]}")
-    decode = {}
+    decode, decode_packed = {}, {}
     if args.decode_steps > 0:
         for M in (1, 2, 4, 8):
-            decode[M] = bench_decode(lib, host, stream, args.decode_steps, M=M)
+            decode[M] = bench_decode(lib, host, stream, args.decode_steps, M=M, eager=args.decode_eager)
             log(f"[decode] M={M}: {decode[M]}")
+        for M in (1, 2, 4, 8):
+            decode_packed[M] = bench_decode(lib, host, stream, args.decode_steps, M=M, packed=True,
+                                            eager=args.decode_eager)
+            log(f"[decode, decode layout] M={M}: {decode_packed[M]}")
     moe = None
     if args.moe_steps > 0:
         moe = bench_moe(lib, stream, args.moe_steps)
@@ -940,6 +955,7 @@ def main():
         "other_configs": others,
         "decode_m1": decode.get(1),
         "decode": {str(k): v for k, v in decode.items()},
+        "decode_packed": {str(k): v for k, v in decode_packed.items()},
         "moe": moe,
         "train_step": full,
         "decode_step": dec_full,

@@ -66,6 +66,15 @@ typedef struct {
 /* Up to 8 independent GEMVs (none reads what another writes) in one launch. */
 int tlg_dev_dec_gemv(const TlgDecGemv *calls, int n, void *stream);
 
+/* The decode weight layout (no reference counterpart in fp32; the reference
+ * repacks its weights for the int8 decode path, qmat_KN3 / qmat_KN_ilv,
+ * tinylm.c:2945-2972): dst[c][r] = src[r][c] for a rows x cols matrix.  A
+ * linear weight W [K][N] (map_weights' [in][out]) stored as W^T [N][K] turns
+ * the decode GEMV mm(M, K, N) into an mm_bt form (op 1 with K and N swapped),
+ * whose rows run along the reduction: every workgroup streams whole
+ * contiguous rows.  dst and src must not overlap. */
+int tlg_dev_transpose(float *dst, const float *src, int rows, int cols, void *stream);
+
 /* RoPE, the ring store and the attention of forward_chunk (:3766-3815) in one
  * launch, for the m new rows at positions pos[j]: q [m][H*hd] and k [m][KD]
  * arrive before RoPE (rope_apply :645-651 with the tables cs / sn [maxpos][hd/2]

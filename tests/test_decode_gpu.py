@@ -100,6 +100,17 @@ def test_dec_gemv_prologues(lib):
         print("dec_gemv", M, "ok", flush=True)
 
 
+@pytest.mark.parametrize("rows,cols", [(1, 1), (384, 1024), (1024, 384), (37, 70), (96, 384)])
+def test_transpose_exact(lib, rows, cols):
+    """tlg_dev_transpose (the decode layout) moves every element exactly."""
+    t = _t()
+    a = np.random.default_rng(rows * 7 + cols).standard_normal((rows, cols)).astype(np.float32)
+    src = t.from_numpy(a).cuda()
+    dst = t.full((cols, rows), float("nan"), device="cuda")
+    lib.check(lib.tlg_dev_transpose(dst.data_ptr(), src.data_ptr(), rows, cols, stream()), "transpose")
+    assert np.array_equal(dst.cpu().numpy(), a.T)
+
+
 def test_dec_gemv_rejects_bad_calls(lib):
     import tlgemm
     C = tlgemm.TlgDecGemv

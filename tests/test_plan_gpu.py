@@ -100,11 +100,16 @@ def test_graph_replays_match_eager(lib, grouped):
         host.dll.tl_run_free(run)
 
 
+@pytest.mark.parametrize("packed", [False, True], ids=["reference_layout", "decode_layout"])
 @pytest.mark.parametrize("grouped", [0, 1], ids=["calls", "grouped"])
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
-def test_decode_step_matches_oracle(lib, orc, M, grouped):
+def test_decode_step_matches_oracle(lib, orc, M, grouped, packed):
+    """The decode GEMV set (forward_chunk's projections, tinylm.c:3748-3829)
+    against the oracle under the reference's decode dispatch, on the
+    reference's weight layout (mm) and on the decode layout (memset + mm_bt
+    over transposed weights)."""
     host = tlgemm.host()
-    plan = host.plan_decode(M, **bench.DECODE)
+    plan = host.plan_decode(M, packed=packed, **bench.DECODE)
     run, stream = new_run(lib, host, plan, pool=2, seed=3)
     try:
         init = snapshot(lib, host, plan, run, stream)

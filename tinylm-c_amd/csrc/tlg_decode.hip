@@ -399,6 +399,41 @@ __global__ __launch_bounds__(1024) void k_dec_argmax(const float *__restrict__ l
 }
 
 // ============================================================== entries ==
+// dst[c][r] = src[r][c] through a 32 x 33 LDS tile (conflict-free both ways):
+// 32 x 8 threads, each moving 4 elements in and 4 out.
+__global__ __launch_bounds__(256) void k_transpose(float *__restrict__ dst, const float *__restrict__ src, int rows,
+                                                   int cols)
+{
+    __shared__ float t[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32, tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = r0 + ty + 8 * i, c = c0 + tx;
+        if (r < rows && c < cols) t[ty + 8 * i][tx] = src[(size_t)r * cols + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = c0 + ty + 8 * i, r = r0 + tx;
+        if (r < rows && c < cols) dst[(size_t)c * rows + r] = t[tx][ty + 8 * i];
+    }
+}
+
+extern "C" int tlg_dev_transpose(float *dst, const float *src, int rows, int cols, void *stream)
+{
+    int rc = tlg_ensure_init();
+    if (rc) return rc;
+    if (!dst || !src || rows <= 0 || cols <= 0 || (cols + 31) / 32 > 0x7fffffff || (rows + 31) / 32 > 65535)
+        return tlg_fail(TLG_EINVAL, "transpose: rows=%d cols=%d", rows, cols);
+    const char *d0 = (const char *)dst, *s0 = (const char *)src;
+    const size_t bytes = (size_t)rows * cols * sizeof(float);
+    if (d0 < s0 + bytes && s0 < d0 + bytes) return tlg_fail(TLG_EINVAL, "transpose: dst and src overlap");
+    hipLaunchKernelGGL(k_transpose, dim3((cols + 31) / 32, (rows + 31) / 32), dim3(256), 0, (hipStream_t)stream, dst,
+                       src, rows, cols);
+    TLG_HIP(hipGetLastError());
+    return TLG_OK;
+}
+
 extern "C" int tlg_dev_dec_embed(float *x, int *pos, const float *emb, const int *tok, const int *state, int start,
                                  int m, int D, int V, void *stream)
 {

@@ -20,8 +20,8 @@
 //          slice order and writes C, then clears the words it read.
 //   mm_bt  dX[m][k] += sum_n dY[m][n] W[k][n]    W rows run along the
 //          reduction.  An item owns 8 output rows, 2 per wave: 32 lanes read
-//          one row in 512-byte steps, each dot product ends in a butterfly
-//          over the 32 lanes.  No split is needed.
+//          one row in 512-byte steps, each dot product ends in a fixed-order
+//          cross-lane sum over the 32 lanes (DPP).  No split is needed.
 //
 // Reducers wait: every producer item has a lower workgroup id than every
 // reducer item, and the dispatcher starts the workgroups of a launch in id
@@ -114,6 +114,24 @@ __device__ __forceinline__ void gv_st_agent(u64 *p, u64 v)
     __hip_atomic_store((GAS u64 *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float gv_silu_mul(float a, float b) { return a / (1.0f + expf(-a)) * b; }
+
+// Sums over each 32-lane half of a wave on the VALU (DPP), in a fixed order:
+// row_shr 1, 2, 4, 8 within the 16-lane rows, then row_bcast:15 adds row 0's
+// (row 2's) lane 15 into row 1 (row 3).  Lane 31 ends with the sum of lanes
+// 0-31, lane 63 with that of lanes 32-63.
+template <int CTRL, int ROWMASK> __device__ __forceinline__ float gv_dpp(float x)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWMASK, 0xf, false));
+}
+__device__ __forceinline__ float gv_half_sum(float x)
+{
+    x += gv_dpp<0x111, 0xf>(x);
+    x += gv_dpp<0x112, 0xf>(x);
+    x += gv_dpp<0x114, 0xf>(x);
+    x += gv_dpp<0x118, 0xf>(x);
+    x += gv_dpp<0x142, 0xa>(x);
+    return x;
+}
 
 #define GV_FULL_ACT 8192               // full-K mm: activation floats staged in LDS (K x MB)
 #define GV_FULL_K 1024                // full-K mm: at most this many rows (32 loads per lane)
@@ -468,7 +486,7 @@ __device__ __forceinline__ void gv_nn_full(const GvProb &P, int cb, GvSmem<MB, 6
 // --------------------------------------------------------------- mm_bt --
 // Item b of an NT problem: output rows o = 8 b + 2 w + lane / 32.  The 32
 // lanes of a half-wave read the row's reduction index in steps of 32 VEC
-// floats (U steps per batch, all loads of a batch first), then a butterfly
+// floats (U steps per batch, all loads of a batch first), then a DPP sum
 // over the 32 lanes gives the M dot products.
 template <int MB, int VEC, int U, int PRO>
 __device__ __forceinline__ void gv_nt(const GvProb &P, int b, GvSmem<MB, 16 * VEC> &sh)
@@ -541,12 +559,9 @@ __device__ __forceinline__ void gv_nt(const GvProb &P, int b, GvSmem<MB, 16 * VE
         }
     }
 #pragma unroll
-    for (int m = 0; m < MB; m++) {
-#pragma unroll
-        for (int x = 16; x > 0; x >>= 1) acc[m] += __shfl_xor(acc[m], x);
-    }
+    for (int m = 0; m < MB; m++) acc[m] = gv_half_sum(acc[m]);
     if (PRO == GV_PRO_RMS) __syncthreads();           // sh.rs
-    if (l == 0 && o < P.No) {
+    if (l == 31 && o < P.No) {
 #pragma unroll
         for (int m = 0; m < MB; m++)
             if (m < M) {

@@ -17,6 +17,7 @@ struct TlDecode {
     size_t np;
     void *arena;
     float *P[TLD_MAXPOOL];
+    float *Pt[TLD_MAXPOOL];      /* the decode layout: every linear weight transposed, same offsets */
     void **Kc, **Vc;
     float *rcos, *rsin, *x, *xn, *q, *k, *v, *ctx, *tmp, *g, *u, *act, *fn, *logits;
     int *pos, *tok, *state;
@@ -90,7 +91,7 @@ TlDecode *tl_decode_new(const TlModel *m, int W, int kv_f16, int exact_exp, int 
     for (int i = 0; i < nf; i++) total += (fixed[i].bytes + 255) & ~(size_t)255;
     d->xbytes = tlg_dec_persist_xbytes(m->V, m->D, m->L, m->F);
     total += (d->xbytes + 255) & ~(size_t)255;
-    total += (size_t)pool * ((4 * d->np + 255) & ~(size_t)255);
+    total += (size_t)2 * pool * ((4 * d->np + 255) & ~(size_t)255);
     total += (size_t)m->L * 2 * ((kvb + 255) & ~(size_t)255);
     d->arena = tlg_dev_malloc(total);
     if (!d->arena) { tl_decode_free(d); return NULL; }
@@ -99,6 +100,7 @@ TlDecode *tl_decode_new(const TlModel *m, int W, int kv_f16, int exact_exp, int 
     d->xbuf = p;
     p += (d->xbytes + 255) & ~(size_t)255;
     for (int c = 0; c < pool; c++) { d->P[c] = (float *)p; p += (4 * d->np + 255) & ~(size_t)255; }
+    for (int c = 0; c < pool; c++) { d->Pt[c] = (float *)p; p += (4 * d->np + 255) & ~(size_t)255; }
     for (int l = 0; l < m->L; l++) {
         d->Kc[l] = p; p += (kvb + 255) & ~(size_t)255;
         d->Vc[l] = p; p += (kvb + 255) & ~(size_t)255;
@@ -160,7 +162,30 @@ int tl_decode_upload(TlDecode *d, const float *P, void *st)
         int rc = tlg_memcpy_h2d(d->P[c], P, 4 * d->np, st);
         if (rc) return rc;
     }
-    return tl_decode_reset(d, st);
+    int rc = tl_decode_pack(d, st);
+    return rc ? rc : tl_decode_reset(d, st);
+}
+
+/* The decode layout of every copy (tldecode.h tlg_dev_transpose): each
+ * linear weight W [in][out] of P[c] as W^T [out][in] at the same offset of
+ * Pt[c]; the embedding and the norm gains are read from P[c]. */
+int tl_decode_pack(TlDecode *d, void *st)
+{
+    const int D = d->m.D, KD = d->KD, F = d->m.F;
+    for (int c = 0; c < d->pool; c++)
+        for (int l = 0; l < d->m.L; l++) {
+            DMap w;
+            dmap(d, l, &w);
+            const struct { size_t off; int rows, cols; } mats[] = {
+                {w.wq, D, D}, {w.wk, D, KD}, {w.wv, D, KD}, {w.wo, D, D}, {w.w1, D, F}, {w.w3, D, F}, {w.w2, F, D},
+            };
+            for (size_t i = 0; i < sizeof mats / sizeof mats[0]; i++) {
+                int rc = tlg_dev_transpose(d->Pt[c] + mats[i].off, d->P[c] + mats[i].off, mats[i].rows, mats[i].cols,
+                                           st);
+                if (rc) return rc;
+            }
+        }
+    return TLG_OK;
 }
 
 /* ---- forward_chunk ---------------------------------------------------------- */
@@ -196,21 +221,23 @@ static int run_chunk_fused(TlDecode *d, int m, int use_state, int start, int cop
 {
     const TlModel *md = &d->m;
     const int D = md->D, H = md->H, KV = md->KV, KD = d->KD, F = md->F, V = md->V, hd = d->hd;
-    const float *P = d->P[copy];
+    const float *P = d->P[copy], *Pt = d->Pt[copy];
     DMap w;
     dmap(d, 0, &w);
     CK(tlg_dev_dec_embed(d->x, d->pos, P + w.emb, d->tok, use_state ? d->state : NULL, start, m, D, V, st));
+    /* every projection mm(m, in, out) on the decode layout: the mm_bt form
+     * (op 1) of W^T [out][in], labels (m, out, in) */
     for (int l = 0; l < md->L; l++) {
         dmap(d, l, &w);
-        DGEMV(st, DG(0, 0, d->q, m, D, D, d->x, P + w.wq, 1, P + w.an1, NULL),
-              DG(0, 0, d->k, m, D, KD, d->x, P + w.wk, 1, P + w.an1, NULL),
-              DG(0, 0, d->v, m, D, KD, d->x, P + w.wv, 1, P + w.an1, NULL));
+        DGEMV(st, DG(1, 0, d->q, m, D, D, d->x, Pt + w.wq, 1, P + w.an1, NULL),
+              DG(1, 0, d->k, m, KD, D, d->x, Pt + w.wk, 1, P + w.an1, NULL),
+              DG(1, 0, d->v, m, KD, D, d->x, Pt + w.wv, 1, P + w.an1, NULL));
         CK(tlg_dev_dec_rope_attn(d->q, d->k, d->v, d->pos, d->rcos, d->rsin, d->maxpos, d->Kc[l], d->Vc[l], d->ctx, m,
                                  H, KV, hd, d->W, dwin(md, l), d->f16, d->exact, st));
-        DGEMV(st, DG(0, 1, d->x, m, D, D, d->ctx, P + w.wo, 0, NULL, NULL));
-        DGEMV(st, DG(0, 0, d->g, m, D, F, d->x, P + w.w1, 1, P + w.an2, NULL),
-              DG(0, 0, d->u, m, D, F, d->x, P + w.w3, 1, P + w.an2, NULL));
-        DGEMV(st, DG(0, 1, d->x, m, F, D, d->g, P + w.w2, 2, NULL, d->u));
+        DGEMV(st, DG(1, 1, d->x, m, D, D, d->ctx, Pt + w.wo, 0, NULL, NULL));
+        DGEMV(st, DG(1, 0, d->g, m, F, D, d->x, Pt + w.w1, 1, P + w.an2, NULL),
+              DG(1, 0, d->u, m, F, D, d->x, Pt + w.w3, 1, P + w.an2, NULL));
+        DGEMV(st, DG(1, 1, d->x, m, D, F, d->g, Pt + w.w2, 2, NULL, d->u));
     }
     dmap(d, 0, &w);
     DGEMV(st, DG(1, 0, d->logits, m, V, D, d->x, P + w.emb, 1, P + w.nf, NULL));   /* memset + mm_bt */

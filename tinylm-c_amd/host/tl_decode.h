@@ -42,8 +42,14 @@ size_t    tl_decode_nparams(const TlDecode *d);
 float    *tl_decode_params(TlDecode *d, int copy);      /* device P (copy < pool) */
 float    *tl_decode_logits(TlDecode *d);                /* device [mmax][V]        */
 
-/* Copy host weights into every copy; clear the caches and the state. */
+/* Copy host weights into every copy (and their decode layout, as
+ * tl_decode_pack); clear the caches and the state. */
 int tl_decode_upload(TlDecode *d, const float *P, void *stream);
+/* Rebuild the decode layout of every copy from its P (after writing P
+ * through tl_decode_params): the fused step's GEMVs read each linear weight
+ * transposed (tldecode.h tlg_dev_transpose); the unfused step and the
+ * persistent kernels read P. */
+int tl_decode_pack(TlDecode *d, void *stream);
 int tl_decode_reset(TlDecode *d, void *stream);
 /* forward_chunk of m host tokens at positions start..start+m-1 (weights
  * copy 0); logits -> tl_decode_logits. */

@@ -222,7 +222,18 @@ int tl_plan_train(TlPlan *p, int R, int D, int KD, int F, int V, int L, int n_mt
     return 0;
 }
 
-int tl_plan_decode(TlPlan *p, int M, int D, int KD, int F, int V, int L)
+/* A decode projection mm(M, K, N) into `out` (set): as the reference calls it
+ * (W [K][N]), or on the decode layout (W^T [N][K] at the same offset) as the
+ * memset + mm_bt form with labels (M, N, K). */
+static int dproj(TlPlan *p, int packed, int line, const char *what, int out, int in, int P, size_t wo, int M, int K,
+                 int N)
+{
+    if (!packed) return gemm(p, TL_MM, line, what, out, 0, in, 0, P, wo, M, K, N);
+    if (zero(p, line, what, out, 0, (size_t)M * N)) return -1;
+    return gemm(p, TL_MM_BT, line, what, out, 0, in, 0, P, wo, M, N, K);
+}
+
+static int plan_decode(TlPlan *p, int M, int D, int KD, int F, int V, int L, int packed)
 {
     memset(p, 0, sizeof *p);
     if (M <= 0 || D <= 0 || KD <= 0 || F <= 0 || V <= 0 || L <= 0) return -1;
@@ -245,21 +256,31 @@ int tl_plan_decode(TlPlan *p, int M, int D, int KD, int F, int V, int L)
     for (int l = 0; l < L; l++) {
         TlWeightMap w;
         tl_weight_map(V, D, KD, F, L, 0, l, &w);
-        CHK(gemm(p, TL_MM, 3748, "q", q, 0, xn, 0, P, w.wq, M, D, D));
-        CHK(gemm(p, TL_MM, 3749, "k", k, 0, xn, 0, P, w.wk, M, D, KD));
-        CHK(gemm(p, TL_MM, 3750, "v", v, 0, xn, 0, P, w.wv, M, D, KD));
+        CHK(dproj(p, packed, 3748, "q", q, xn, P, w.wq, M, D, D));
+        CHK(dproj(p, packed, 3749, "k", k, xn, P, w.wk, M, D, KD));
+        CHK(dproj(p, packed, 3750, "v", v, xn, P, w.wv, M, D, KD));
         glue(p);                                    /* RoPE, KV store, attention :3756-3810 */
-        CHK(gemm(p, TL_MM, 3812, "o", tmp, 0, ctx, 0, P, w.wo, M, D, D));
+        CHK(dproj(p, packed, 3812, "o", tmp, ctx, P, w.wo, M, D, D));
         glue(p);                                    /* residual, rmsnorm :3813-3815 */
-        CHK(gemm(p, TL_MM, 3821, "w1", g, 0, xn, 0, P, w.w1, M, D, F));
-        CHK(gemm(p, TL_MM, 3822, "w3", u, 0, xn, 0, P, w.w3, M, D, F));
+        CHK(dproj(p, packed, 3821, "w1", g, xn, P, w.w1, M, D, F));
+        CHK(dproj(p, packed, 3822, "w3", u, xn, P, w.w3, M, D, F));
         glue(p);                                    /* silu(g)*u :3823 */
-        CHK(gemm(p, TL_MM, 3824, "w2", tmp, 0, u, 0, P, w.w2, M, F, D));
+        CHK(dproj(p, packed, 3824, "w2", tmp, u, P, w.w2, M, F, D));
         glue(p);                                    /* residual, next rmsnorm :3825 */
     }
     CHK(zero(p, 3035, "logits", logits, 0, (size_t)M * V));
     CHK(gemm(p, TL_MM_BT, 3035, "head", logits, 0, fn, 0, P, m0.emb, M, V, D));
     return 0;
+}
+
+int tl_plan_decode(TlPlan *p, int M, int D, int KD, int F, int V, int L)
+{
+    return plan_decode(p, M, D, KD, F, V, L, 0);
+}
+
+int tl_plan_decode_packed(TlPlan *p, int M, int D, int KD, int F, int V, int L)
+{
+    return plan_decode(p, M, D, KD, F, V, L, 1);
 }
 
 double tl_call_flops(const TlCall *c)

@@ -72,6 +72,11 @@ int  tl_plan_train(TlPlan *p, int R, int D, int KD, int F, int V, int L, int n_m
 /* One decode step's fp32 GEMMs for M rows (forward_chunk, tinylm.c:3721-3830,
  * with no int8 copy: mm_dec -> mm, mmbt_dec -> memset + mm_bt, :3029-3036). */
 int  tl_plan_decode(TlPlan *p, int M, int D, int KD, int F, int V, int L);
+/* The same GEMVs on the decode layout (tldecode.h tlg_dev_transpose: each
+ * linear weight stored transposed at its map_weights offset): every
+ * mm(M, K, N) becomes memset + mm_bt(M, N, K), so each GEMV streams whole
+ * contiguous weight rows. */
+int  tl_plan_decode_packed(TlPlan *p, int M, int D, int KD, int F, int V, int L);
 void tl_plan_free(TlPlan *p);
 int  tl_plan_find(const TlPlan *p, const char *name);
 /* Algorithmic flops of call i (2*M*K*N for a GEMM, 0 for a clear) and the

@@ -109,6 +109,7 @@ SIGNATURES = {
     "tlg_dev_dec_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp]),
     "tlg_dev_dec_argmax": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "tlg_dev_dec_gemv": (_i, [_vp, _i, _vp]),
+    "tlg_dev_transpose": (_i, [_vp, _vp, _i, _i, _vp]),
     "tlg_dev_dec_rope_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i,
                                    _vp]),
     "tlg_dec_persist_xbytes": (_sz, [_i, _i, _i, _i]),
@@ -432,6 +433,10 @@ class Decode:
         """Device address of weight copy `copy`."""
         return self.host.dll.tl_decode_params(self.h, copy)
 
+    def pack(self, stream):
+        """Rebuild the decode layout after writing weights through params()."""
+        return self._ck(self.host.dll.tl_decode_pack(self.h, stream), "tl_decode_pack")
+
     def chunk(self, tok, start, stream):
         """forward_chunk of host tokens; returns the logits [m][V] (host)."""
         import numpy as np
@@ -559,8 +564,9 @@ class Host:
         P = ctypes.POINTER(TlPlan)
         d.tl_plan_train.argtypes = [P] + [_i] * 7
         d.tl_plan_train.restype = _i
-        d.tl_plan_decode.argtypes = [P] + [_i] * 6
-        d.tl_plan_decode.restype = _i
+        for n in ("tl_plan_decode", "tl_plan_decode_packed"):
+            getattr(d, n).argtypes = [P] + [_i] * 6
+            getattr(d, n).restype = _i
         d.tl_weight_map.argtypes = [_i] * 7 + [ctypes.POINTER(TlWeightMap)]
         d.tl_weight_map.restype = None
         d.tl_plan_free.argtypes = [P]
@@ -655,7 +661,7 @@ class Host:
         for n in ("tl_decode_upload", "tl_decode_state"):
             getattr(d, n).argtypes = [_vp, _vp, _vp]
             getattr(d, n).restype = _i
-        for n in ("tl_decode_reset", "tl_decode_graph_build", "tl_decode_graph_step"):
+        for n in ("tl_decode_reset", "tl_decode_pack", "tl_decode_graph_build", "tl_decode_graph_step"):
             getattr(d, n).argtypes = [_vp, _vp]
             getattr(d, n).restype = _i
         d.tl_decode_chunk.argtypes = [_vp, _vp, _i, _i, _vp]
@@ -703,9 +709,10 @@ class Host:
             raise ValueError("tl_plan_train failed")
         return Plan(self, raw)
 
-    def plan_decode(self, M, D, KD, F, V, L):
+    def plan_decode(self, M, D, KD, F, V, L, packed=False):
         raw = TlPlan()
-        if self.dll.tl_plan_decode(ctypes.byref(raw), M, D, KD, F, V, L) != 0:
+        fn = self.dll.tl_plan_decode_packed if packed else self.dll.tl_plan_decode
+        if fn(ctypes.byref(raw), M, D, KD, F, V, L) != 0:
             raise ValueError("tl_plan_decode failed")
         return Plan(self, raw)
 
