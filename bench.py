@@ -166,6 +166,35 @@ def read_traffic(kernel):
     return None
 
 
+def read_profile_row(fname, kernel):
+    """The tab-separated fields after `kernel` in a committed profiles/ summary
+    (its machine-readable tail), or None."""
+    path = os.path.join(REPO, "profiles", fname)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = line.rstrip("\n").split("\t")
+        if len(parts) >= 2 and parts[0] == kernel:
+            return parts[1:]
+    return None
+
+
+def read_rocprof_avg_us(kernel):
+    """rocprofv3's average duration of `kernel` in the committed m3 kernel
+    trace (profiles/m3_step_kernel_trace.md, the stats table), or None."""
+    path = os.path.join(REPO, "profiles", "m3_step_kernel_trace.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.split("|")]
+        if len(cells) > 4 and cells[1].strip("`") == "void " + kernel:
+            try:
+                return float(cells[3])
+            except ValueError:
+                return None
+    return None
+
+
 AUTOTUNE_CANDS = (3, 14, 13, 15, 0, 1, 20, 21, 22, 23)
 # split targets tried with each tile candidate (tlg_tune_group_split: reduction
 # steps per split work item of the mm_atb problems; 0 = the library's rule)
@@ -557,6 +586,7 @@ def bench_full_step(lib, host, stream, name, steps, warmup=3, eager=False, tune=
     ms, _ = time_steps(lib, run, stream, steps)
     loss1 = tr.loss(stream)
     ms_step = ms / steps
+    tr.close()
     return {"model": kw, "batch": B, "rows": N, "params": tr.np, "steps": steps,
             "ms_per_step": round(ms_step, 4), "tok_s": round(N / (ms_step / 1e3), 1),
             "phases_ms_eager": {"forward": round(phases[0], 4), "backward": round(phases[1], 4),
@@ -605,6 +635,7 @@ def bench_decode_step(lib, host, stream, steps, pool=6, prompt_len=16, warmup=8,
     ms, _ = time_steps(lib, step, stream, steps)
     state = dec.state(stream)
     per = ms / steps
+    dec.close()
     return {"model": DECODE_MODEL, "kv_cache": "f16 ring, 256 positions", "exp": "fast_expf",
             "weights_pool": pool, "steps": steps, "ms_per_token": round(per, 4),
             "tok_s": round(1e3 / per, 1), "prefill_ms_host_timed": round(prefill_ms, 3),
@@ -634,6 +665,7 @@ def bench_decode_persist(lib, host, stream, steps, pool=6, prompt_len=16, warmup
     state = dec.state(stream)
     per = ms / steps
     wbytes = 4 * (DECODE_MODEL["V"] * 384 + 8 * (384 * 384 * 2 + 2 * 384 * 96 + 3 * 384 * 1024))
+    dec.close()
     return {"model": DECODE_MODEL, "kv_cache": "f16 ring, 256 positions", "exp": "fast_expf",
             "weights_pool": pool, "steps": steps, "launches": 1, "ms_per_token": round(per, 4),
             "tok_s": round(1e3 / per, 1), "weight_bytes_per_token": wbytes,
@@ -670,6 +702,7 @@ def bench_decode_chunks(lib, host, stream, M, positions=512, pool=6, prompt_len=
     lib.tlg_dev_free(dtoks)
     per = ms / n
     wbytes = 4 * (DECODE_MODEL["V"] * 384 + 8 * (384 * 384 * 2 + 2 * 384 * 96 + 3 * 384 * 1024))
+    dec.close()
     return {"rows": M, "chunks": n, "launches": 1, "kv_cache": "f16 ring, 256 positions", "exp": "fast_expf",
             "weights_pool": pool, "us_per_chunk": round(per * 1e3, 3), "tok_s": round(M * 1e3 / per, 1),
             "weight_bytes_per_chunk": wbytes, "weight_gbs": round(wbytes / (per * 1e-3) / 1e9, 1),
@@ -914,6 +947,8 @@ def main():
             log(f"[cpu] decode {cpu['decode']}")
 
     host.dll.tl_run_free(run)
+    rocprof_avg = read_rocprof_avg_us(dom_name)            # profiles/m3_step_kernel_trace.md
+    mfma_row = read_profile_row("mfma_counters_m3_moe.txt", dom_name)
     result = {
         "metric": "train tokens/s (m3-scale); GEMM TFLOP/s & % roofline; M=1 decode tok/s",
         "value": round(tok_s, 1),
@@ -947,7 +982,14 @@ def main():
             "frac_of_achievable": round(achieved / peaks[("mfma_fp32_tflops" if bound == "mfma" else "hbm_copy_gbs")], 4)
             if peaks else None,
             "launches_per_step": dom["launches"], "avg_launch_us": round(avg_ms * 1e3, 3),
+            "avg_launch_us_source": "this run: the timed graph-replayed step apportioned by the launches' "
+                                    "event-census shares",
             "event_census_avg_us": round(event_avg_ms * 1e3, 3),
+            "rocprof_avg_us": rocprof_avg,
+            "frac_rocprof": (round(dom["flops"] / dom["launches"] / (rocprof_avg * 1e-6) / 1e12 / peak, 4)
+                             if rocprof_avg and bound == "mfma" else None),
+            "mfma_busy": float(mfma_row[0]) if mfma_row else None,
+            "mfma_executed_gflop_per_launch": float(mfma_row[1]) if mfma_row else None,
             "algorithmic_bytes_per_launch": round(dom["bytes"] / dom["launches"]),
             "algorithmic_flops_per_launch": round(dom["flops"] / dom["launches"]),
         },
@@ -964,6 +1006,13 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+    # tear down explicitly, before the interpreter exits: a profiler that has
+    # already finalised must not see the library's device memory and streams
+    # released by exit handlers
+    import gc
+    gc.collect()
+    lib.tlg_stream_destroy(stream)
+    lib.tlg_shutdown()
 
 
 if __name__ == "__main__":

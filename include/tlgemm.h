@@ -108,7 +108,9 @@ int tlg_dev_zero(float *dst, size_t n, void *stream);
  * partial sums are added into C by the NEXT grouped launch on the stream
  * (the kernel boundary makes them visible) or by tlg_dev_gemm_flush, which
  * must be called before C is read.  Any single-call entry point flushes
- * first.  One stream at a time may use grouped launches. */
+ * first.  A launch on another stream first runs the queued sums on the
+ * stream that wrote their partials (ordered after their producer); the
+ * caller orders its consumers of C after that stream, as for any result. */
 typedef struct {
     int op;                  /* 0 mm, 1 mm_bt, 2 mm_atb, 3 clear C[0, M*N) */
     int beta;                /* mm_bt / mm_atb: 1 add into C, 0 overwrite C */

@@ -45,7 +45,8 @@ int tlg_dev_rmsnorm_bwd(const float *x, const float *g, const float *rinv, const
  * per-row-block partials of dg go to `part` (at least ceil(rows/16) * D
  * floats, 16-byte aligned, owned by the caller), and their fixed-order
  * column sum into dg rides along in the next grouped GEMM or expert launch
- * on the stream (or tlg_dev_gemm_flush), as a split GEMM's reduction does.
+ * on the stream (or tlg_dev_gemm_flush), as a split GEMM's reduction does;
+ * a launch on another stream first runs it on this stream.
  * dg is complete only after that launch; `part` must not be written before
  * it (a later call on the same `part` flushes the earlier sum first).  No
  * counterpart in the reference, whose rmsnorm_bwd adds into dg directly: it

@@ -25,6 +25,7 @@ void *tlref_dec_new(int D, int H, int KV, int T, int L, int win, int full_every,
     d->c.rope_base = 10000.0f;
     cfg_derive(&d->c);
     d->gn = gen_new(&d->c, NULL, 0);
+    if (!d->gn) { free(d); return NULL; }
     return d;
 }
 
@@ -34,9 +35,10 @@ int tlref_dec_attn(void *h, int l, const float *q, const float *k, const float *
                    float *ctx)
 {
     TlrefDec *d = (TlrefDec *)h;
+    if (!d) return -1;
     const Cfg *c = &d->c;
     Gen *gn = d->gn;
-    if (!d || m < 1 || m > c->T || l < 0 || l >= c->L) return -1;
+    if (m < 1 || m > c->T || l < 0 || l >= c->L) return -1;
     const int D = c->D, KD = c->KD, KV = c->KV, hd = c->hd, W = c->T, grp = c->H / c->KV;
     memcpy(gn->q, q, sizeof(float) * (size_t)m * D);
     const int eff = cfg_lwin(c, l), wlim = (eff > 0 && eff < W) ? eff : W;

@@ -45,16 +45,17 @@ void orc_set_threads(int nt) {
  * x[row][k] * W[k][:] into the row: per element, y = fma(x_k, w_k, y) for
  * k = 0..K-1 in order (tinylm.c:456-467).  A short final block runs the same
  * chain one row at a time (tinylm.c:468-476). */
-static void mm_block_cols(float *restrict Y, const float *restrict X, const float *restrict W,
-                          int M, int K, int N, int b, int n0, int n1)
+static void mm_block_to(float *restrict Yb, int ldy, int ycol0, const float *restrict X, const float *restrict W,
+                        int M, int K, int N, int b, int n0, int n1)
 {
+    /* rows r0 .. r0+3 of the block go to Yb + i*ldy, column n at n - ycol0 */
     const int r0 = b * 4;
     const int nr = (M - r0 < 4) ? (M - r0) : 4;
     if (nr == 4) {
-        float *restrict ya = Y + (size_t)r0 * N;
-        float *restrict yb = ya + N;
-        float *restrict yc = yb + N;
-        float *restrict yd = yc + N;
+        float *restrict ya = Yb - ycol0;
+        float *restrict yb = ya + ldy;
+        float *restrict yc = yb + ldy;
+        float *restrict yd = yc + ldy;
         const float *restrict xa = X + (size_t)r0 * K;
         const float *restrict xb = xa + K;
         const float *restrict xc = xb + K;
@@ -71,7 +72,7 @@ static void mm_block_cols(float *restrict Y, const float *restrict X, const floa
         return;
     }
     for (int i = 0; i < nr; i++) {
-        float *restrict y = Y + (size_t)(r0 + i) * N;
+        float *restrict y = Yb + (size_t)i * ldy - ycol0;
         const float *restrict x = X + (size_t)(r0 + i) * K;
         for (int n = n0; n < n1; n++) y[n] = 0.0f;
         for (int k = 0; k < K; k++) {
@@ -81,6 +82,11 @@ static void mm_block_cols(float *restrict Y, const float *restrict X, const floa
         }
     }
 }
+static void mm_block_cols(float *restrict Y, const float *restrict X, const float *restrict W,
+                          int M, int K, int N, int b, int n0, int n1)
+{
+    mm_block_to(Y + (size_t)b * 4 * N, N, 0, X, W, M, K, N, b, n0, n1);
+}
 static void mm_block(float *restrict Y, const float *restrict X, const float *restrict W,
                      int M, int K, int N, int b)
 {
@@ -89,26 +95,57 @@ static void mm_block(float *restrict Y, const float *restrict X, const float *re
 
 /* The threaded GEMV variant of the CPU decode baseline (not the reference's
  * dispatch, which runs M <= 8 serially): M <= 8 calls split their outputs
- * over the OpenMP threads -- mm by column ranges, mm_bt by ranges of W rows
- * that start at multiples of 4 -- and every element keeps the reference's
- * own chain, so the results equal the serial ones. */
+ * over the OpenMP threads in contiguous ranges -- mm by column ranges of 16
+ * floats, mm_bt by ranges of W rows that start at multiples of 4 -- and
+ * every element keeps the reference's own chain, so the results equal the
+ * serial ones.  Inside orc_run_calls the whole call list runs in one
+ * parallel region (a barrier between calls), so no call pays for waking the
+ * threads. */
 static int g_gemv_split = 0;
 void orc_set_gemv_split(int on) { g_gemv_split = on != 0; }
-#define ORC_SPLIT_COLS 64
+
+/* this thread's share [*lo, *hi) of n items in units of `unit` */
+static void split_range(int n, int unit, int *lo, int *hi)
+{
+    int T = 1, t = 0;
+#ifdef _OPENMP
+    T = omp_get_num_threads();
+    t = omp_get_thread_num();
+#endif
+    const int nu = (n + unit - 1) / unit;
+    const int u0 = (int)((long long)nu * t / T), u1 = (int)((long long)nu * (t + 1) / T);
+    *lo = u0 * unit;
+    *hi = u1 * unit < n ? u1 * unit : n;
+}
 
 /* Dispatch rule of tinylm.c:444-448: a single block, or a live decode pool,
  * goes through tl_for (serial when the block count is below the worker count,
  * tinylm.c:239); otherwise OpenMP static over blocks. */
+/* M <= 8 mm, this thread's column range (called by every thread of a region) */
+static void mm_split_part(float *Y, const float *X, const float *W, int M, int K, int N)
+{
+    int n0, n1;
+    split_range(N, 16, &n0, &n1);
+    if (n0 >= n1) return;
+    /* each block's rows accumulate in this thread's own buffer (neighbouring
+     * threads' columns share cache lines of Y), then are copied out once */
+    const int w = n1 - n0;
+    float *t = malloc((size_t)4 * w * sizeof(float));
+    if (!t) abort();
+    for (int b = 0; b < (M + 3) / 4; b++) {
+        const int nr = M - 4 * b < 4 ? M - 4 * b : 4;
+        mm_block_to(t, w, n0, X, W, M, K, N, b, n0, n1);
+        for (int i = 0; i < nr; i++) memcpy(Y + (size_t)(4 * b + i) * N + n0, t + (size_t)i * w, (size_t)w * sizeof(float));
+    }
+    free(t);
+}
+
 void orc_mm(float *Y, const float *X, const float *W, int M, int K, int N)
 {
     const int nblk = (M + 3) / 4;
     if (g_gemv_split && M <= 8) {
-        const int nc = (N + ORC_SPLIT_COLS - 1) / ORC_SPLIT_COLS;
-        #pragma omp parallel for schedule(static)
-        for (int c = 0; c < nc; c++) {
-            const int n1 = (c + 1) * ORC_SPLIT_COLS < N ? (c + 1) * ORC_SPLIT_COLS : N;
-            for (int b = 0; b < nblk; b++) mm_block_cols(Y, X, W, M, K, N, b, c * ORC_SPLIT_COLS, n1);
-        }
+        #pragma omp parallel
+        mm_split_part(Y, X, W, M, K, N);
         return;
     }
     if (nblk == 1 || g_pool > 1) {
@@ -160,15 +197,19 @@ static void mmbt_row(float *restrict dX, const float *restrict dY, const float *
 }
 
 /* tinylm.c:486-488: M==1 or a live pool -> tl_for over rows, else OpenMP. */
+/* M <= 8 mm_bt, this thread's range of W rows (multiples of 4) */
+static void mmbt_split_part(float *dX, const float *dY, const float *W, int M, int K, int N)
+{
+    int k0, k1;
+    split_range(K, 4, &k0, &k1);
+    for (int m = 0; k0 < k1 && m < M; m++) mmbt_rows(dX, dY, W, K, N, m, k0, k1);
+}
+
 void orc_mm_bt(float *dX, const float *dY, const float *W, int M, int K, int N)
 {
     if (g_gemv_split && M <= 8) {
-        const int nc = (K + ORC_SPLIT_COLS - 1) / ORC_SPLIT_COLS;
-        #pragma omp parallel for schedule(static)
-        for (int c = 0; c < nc; c++) {
-            const int k1 = (c + 1) * ORC_SPLIT_COLS < K ? (c + 1) * ORC_SPLIT_COLS : K;
-            for (int m = 0; m < M; m++) mmbt_rows(dX, dY, W, K, N, m, c * ORC_SPLIT_COLS, k1);
-        }
+        #pragma omp parallel
+        mmbt_split_part(dX, dY, W, M, K, N);
         return;
     }
     if (M == 1 || g_pool > 1) {
@@ -449,6 +490,30 @@ void orc_moe_backward(int N, int D, int F, int E,
 
 void orc_run_calls(const OrcCall *c, int n, int reps)
 {
+    if (g_gemv_split) {
+        /* the threaded decode variant: one region for the whole list, the
+         * M <= 8 GEMVs split over its threads, everything else on one */
+        #pragma omp parallel
+        for (int r = 0; r < reps; r++)
+            for (int i = 0; i < n; i++) {
+                if (c[i].op == 0 && c[i].M <= 8) mm_split_part(c[i].out, c[i].a, c[i].b, c[i].M, c[i].K, c[i].N);
+                else if (c[i].op == 1 && c[i].M <= 8)
+                    mmbt_split_part(c[i].out, c[i].a, c[i].b, c[i].M, c[i].K, c[i].N);
+                else {
+                    #pragma omp single
+                    {
+                        switch (c[i].op) {
+                        case 0: orc_mm(c[i].out, c[i].a, c[i].b, c[i].M, c[i].K, c[i].N); break;
+                        case 1: orc_mm_bt(c[i].out, c[i].a, c[i].b, c[i].M, c[i].K, c[i].N); break;
+                        case 2: orc_mm_atb(c[i].out, c[i].a, c[i].b, c[i].M, c[i].K, c[i].N); break;
+                        default: memset(c[i].out, 0, c[i].n * sizeof(float)); break;
+                        }
+                    }
+                }
+                #pragma omp barrier
+            }
+        return;
+    }
     for (int r = 0; r < reps; r++)
         for (int i = 0; i < n; i++) {
             switch (c[i].op) {

@@ -61,6 +61,37 @@ def test_pool_dispatch_keeps_results(orc):
             orc.set_pool(1)
 
 
+@pytest.mark.parametrize("packed", [False, True])
+def test_split_call_list_keeps_results(orc, packed):
+    """The threaded decode baseline's call-list form (one parallel region, a
+    barrier between calls, each thread's columns accumulated privately) is
+    bit-identical to the serial reference dispatch on a whole decode GEMV set,
+    M = 1, 3 and 8 rows, on both weight layouts."""
+    import tlgemm
+    from oracle import plan_calls_native
+    host = tlgemm.host()
+    orc.set_threads(4)
+    try:
+        for M in (1, 3, 8):
+            plan = host.plan_decode(M, D=96, KD=32, F=160, V=256, L=2, packed=packed)
+            rng = np.random.default_rng(M)
+            init = {name: rng.standard_normal(n).astype(np.float32) for name, n, _ in plan.bufs}
+            outs = []
+            for split in (0, 1):
+                arrays = {k: v.copy() for k, v in init.items()}
+                calls = plan_calls_native(plan, arrays)
+                orc.dll.orc_set_gemv_split(split)
+                try:
+                    orc.run_calls(calls, 2)
+                finally:
+                    orc.dll.orc_set_gemv_split(0)
+                outs.append(arrays)
+            for k in init:
+                assert np.array_equal(outs[0][k], outs[1][k]), (M, k)
+    finally:
+        orc.set_threads(os.cpu_count() or 1)
+
+
 def test_split_gemv_keeps_results(orc):
     """The threaded GEMV variant of the CPU decode baseline (outputs split
     over threads) leaves every element's chain alone: bit-identical to the

@@ -1203,8 +1203,10 @@ extern "C" int tlg_dev_sgemm_tn_acc_noalloc(float *dW, const float *X, const flo
 // the halves alternate so a launch never overwrites partials still pending.
 static Prob g_pending[TLG_MAXPROB];
 static int g_npending = 0;
+static hipStream_t g_pending_st = nullptr;     // the stream their partials were written on
 #include <stdlib.h>
 static int g_ws_half = 0;
+static int flush_foreign(hipStream_t st);
 
 // Tile shape of a grouped launch (all problems of a group share it): the
 // first candidate that still gives every CU `g_min_waves` workgroups, else
@@ -1388,12 +1390,16 @@ int tlg_group_pending(void) { return g_npending; }
 // may be rewritten by the caller's next kernel only after this call.
 int tlg_defer_colsum(const float *part, float *C, int splits, int No, int beta, hipStream_t st)
 {
+    int rc = TLG_OK;
     bool busy = g_npending >= TLG_MAXPROB / 2 - 1;
     for (int k = 0; k < g_npending && !busy; k++) busy = g_pending[k].ws == part;
     if (busy) {
-        const int rc = tlg_group_flush_launch(st);
+        rc = tlg_group_flush_launch(st);
         if (rc) return rc;
     }
+    rc = flush_foreign(st);
+    if (rc) return rc;
+    g_pending_st = st;
     Prob &r = g_pending[g_npending++];
     memset(&r, 0, sizeof r);
     r.kind = PK_COLSUM;
@@ -1423,7 +1429,8 @@ static int ecarry_flush(hipStream_t st);
 
 int tlg_group_flush_launch(hipStream_t st)
 {
-    const int rc = ecarry_flush(st);
+    int rc = flush_foreign(st);
+    if (!rc) rc = ecarry_flush(st);
     return rc ? rc : group_flush_dense(st);
 }
 
@@ -1486,6 +1493,7 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
         return rc;
     }
 
+    if ((rc = flush_foreign(st))) return rc;
     if ((rc = ecarry_flush(st))) return rc;
     // Pending reductions write their C; a call that touches such a range must
     // see them first, so they go in a launch of their own.
@@ -1633,7 +1641,7 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
     for (int k = 0; k < n; k++) {
         const Prob &P = probs[order[k]];
         a.p[a.nprob++] = P;
-        if (P.splits > 1) g_pending[g_npending++] = P;
+        if (P.splits > 1) { g_pending[g_npending++] = P; g_pending_st = st; }
     }
     for (int k = 0; k < nred; k++) a.p[a.nprob++] = red[k];
     launch_group(ci, a, group_grid(a), st);
@@ -1657,6 +1665,24 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
 static GroupArgs g_ecarry;              // nprob 0: nothing held
 static size_t g_ecarry_used = 0;        // workspace floats their partials occupy
 static const int *g_ecarry_eoff = nullptr;
+static hipStream_t g_ecarry_st = nullptr;
+
+// Queued work whose producer ran on another stream than `st` runs first on
+// the producer's stream (ordered after the kernels that wrote its partials),
+// so a launch on `st` never sums partials it is not ordered after.  Work
+// queued on `st` itself keeps riding along.
+static int flush_foreign(hipStream_t st)
+{
+    if (g_ecarry.nprob && g_ecarry_st != st) {
+        const int rc = ecarry_flush(g_ecarry_st);
+        if (rc) return rc;
+    }
+    if (g_npending && g_pending_st != st) {
+        const int rc = group_flush_dense(g_pending_st);
+        if (rc) return rc;
+    }
+    return TLG_OK;
+}
 
 static int ecarry_flush(hipStream_t st)
 {
@@ -1695,6 +1721,7 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     if ((dense && E != 1) || E < 1 || E > TLG_MAX_EXPERTS || rows < 0)
         return tlg_fail(TLG_EINVAL, "expert launch: bad row offsets or %d experts", E);
     if (rows == 0) return TLG_OK;
+    if ((rc = flush_foreign(st))) return rc;
     // held slice reductions join this launch only if it asks for them and
     // shares their row offsets
     const bool cin = carry == TLG_ECARRY_IN && g_ecarry.nprob && g_ecarry_eoff == eoff && !dense;
@@ -1874,6 +1901,7 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
         g_ecarry = red;                  // the next expert launch runs them
         g_ecarry_used = used;
         g_ecarry_eoff = eoff;
+        g_ecarry_st = st;
     } else if (red.nprob) {
         hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(red)), dim3(T3::THREADS), 0, st, red);
         TLG_HIP(hipGetLastError());

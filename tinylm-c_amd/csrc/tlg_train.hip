@@ -1808,7 +1808,11 @@ extern "C" int tlg_dev_embed_bwd(float *demb, const float *dout, const int *tok,
     if (N < 0 || D <= 0 || V <= 0) return tlg_fail(TLG_EINVAL, "embed_bwd: N=%d D=%d V=%d", N, D, V);
     if (N == 0) return TLG_OK;
     const int nv = (D / 4 + 63) / 64;
-    if (D % 4 == 0 && nv <= 4 && al16(demb) && al16(dout) && N < (1 << 28)) {
+    // the one-launch form has each of the V / 8 workgroups scan all N ids
+    // (V N / 2 bytes of id reads in all): beyond V N = 2^26 (32 MB of scans,
+    // ~10x the m3 step's 2048 x 4096) the counting sort, which reads each id
+    // a fixed number of times, takes over
+    if (D % 4 == 0 && nv <= 4 && al16(demb) && al16(dout) && N < (1 << 28) && (long long)V * N <= (1LL << 26)) {
         const dim3 grid((V + EMB_VB - 1) / EMB_VB);
         hipStream_t st = ST(stream);
         if (nv == 1) hipLaunchKernelGGL(k_embed_bwd1<1>, grid, dim3(256), 0, st, dout, tok, N, D, V, demb);

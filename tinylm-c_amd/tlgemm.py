@@ -394,11 +394,15 @@ class Train:
         n = self.host.dll.tl_train_splits(self.h, buf, 512)
         return list(buf[:n])
 
+    def close(self):
+        """Free the device state now rather than at garbage collection."""
+        if self.h:
+            self.host.dll.tl_train_free(self.h)
+            self.h = None
+
     def __del__(self):
         try:
-            if self.h:
-                self.host.dll.tl_train_free(self.h)
-                self.h = None
+            self.close()
         except Exception:
             pass
 
@@ -491,11 +495,15 @@ class Decode:
         self._ck(self.host.dll.tl_decode_state(self.h, s, stream), "tl_decode_state")
         return list(s)
 
+    def close(self):
+        """Free the device state now rather than at garbage collection."""
+        if self.h:
+            self.host.dll.tl_decode_free(self.h)
+            self.h = None
+
     def __del__(self):
         try:
-            if self.h:
-                self.host.dll.tl_decode_free(self.h)
-                self.h = None
+            self.close()
         except Exception:
             pass
 
