@@ -61,10 +61,36 @@ typedef struct {
     int pro;                 /* 0 none, 1 rmsnorm with gain, 2 SwiGLU with A2 */
     const float *gain;       /* pro 1: [R] */
     const float *A2;         /* pro 2: [M][R] */
+    /* optional (zero = none), for a MoE layer's expert rows: the weight is
+     * B + bsel[0] * bstride with bsel in device memory (the row's expert,
+     * chosen on the device), and the result is multiplied by cgate[0] (the
+     * row's gate) before it is stored or added: out[n] += gate[n] * y
+     * (moe_scatter_body, tinylm.c:3347-3353) */
+    const int *bsel;
+    long long bstride;
+    const float *cgate;
 } TlgDecGemv;
 
 /* Up to 8 independent GEMVs (none reads what another writes) in one launch. */
 int tlg_dev_dec_gemv(const TlgDecGemv *calls, int n, void *stream);
+
+/* qknorm_apply (tinylm.c:597-605, applied to q and k before RoPE,
+ * :3752-3754): each of the m rows' H query heads of q [m][H*hd] and KV key
+ * heads of k [m][KV*hd] becomes v * s * gain with s = 1 / sqrt(sum(v^2) / hd +
+ * 1e-5), gain qn (queries) or kn (keys) of hd floats.  hd must be 32. */
+int tlg_dev_dec_qknorm(float *q, float *k, const float *qn, const float *kn, int m, int H, int KV, int hd,
+                       void *stream);
+/* The decode MoE router's top-1 (moe_rt_body, tinylm.c:3332-3341) for m <= 64
+ * rows of router logits rt [m][E] (E <= 64): softmax with expf, the first
+ * maximum of the normalised probabilities -> assign[j], its probability ->
+ * gate[j]. */
+int tlg_dev_dec_moe_route(const float *rt, int m, int E, int *assign, float *gate, void *stream);
+/* mtp_argmax's middle (tinylm.c:3933): hh[i] = fn[i] + silu(ht[i]), fn =
+ * rmsnorm_fwd(x, nf) (:540-548) of one row x [D]. */
+int tlg_dev_dec_mtp_mix(float *hh, const float *x, const float *nf, const float *ht, int D, void *stream);
+/* argmax_v (tinylm.c:3844, the first maximum) of each of m rows of logits
+ * [m][V] into out[m] (device), leaving the decode state alone. */
+int tlg_dev_argmax_rows(const float *logits, int V, int m, int *out, void *stream);
 
 /* The decode weight layout (no reference counterpart in fp32; the reference
  * repacks its weights for the int8 decode path, qmat_KN3 / qmat_KN_ilv,

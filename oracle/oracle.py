@@ -325,18 +325,20 @@ _fl = ctypes.c_float
 
 
 class OrcModel(ctypes.Structure):
-    """tl_oracle.h OrcModel: the model shape (tinylm.c Cfg without QK-norm)."""
+    """tl_oracle.h OrcModel: the model shape (tinylm.c Cfg without shared
+    experts)."""
     _fields_ = [(n, ctypes.c_int) for n in ("V", "D", "L", "H", "KV", "F", "T", "n_mtp", "n_exp", "win",
-                                            "full_every")] + [("rope_base", ctypes.c_float)]
+                                            "full_every")] + [("rope_base", ctypes.c_float),
+                                                              ("qknorm", ctypes.c_int)]
 
 
-def model(V, D, L, H, KV, F, T, n_mtp=0, n_exp=0, win=0, full_every=0, rope_base=10000.0):
-    return OrcModel(V, D, L, H, KV, F, T, n_mtp, n_exp, win, full_every, rope_base)
+def model(V, D, L, H, KV, F, T, n_mtp=0, n_exp=0, win=0, full_every=0, rope_base=10000.0, qknorm=0):
+    return OrcModel(V, D, L, H, KV, F, T, n_mtp, n_exp, win, full_every, rope_base, qknorm)
 
 
 class OrcLayerMap(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_size_t) for n in ("emb", "an1", "wq", "wk", "wv", "wo", "an2", "wr", "w1", "w3",
-                                               "w2", "nf", "mtp0", "total")]
+    _fields_ = [(n, ctypes.c_size_t) for n in ("emb", "an1", "wq", "wk", "wv", "wo", "qn", "kn", "an2", "wr",
+                                               "w1", "w3", "w2", "nf", "mtp0", "total")]
 
 
 class StepFns:
@@ -477,11 +479,12 @@ def param_regions(st, m):
     """(name, start, end) of every parameter tensor of model m in
     map_weights order (tinylm.c:361-393), from the oracle's layout."""
     D, KD, F, E = m.D, m.KV * (m.D // m.H), m.F, max(m.n_exp, 1)
+    hq = (m.D // m.H) if m.qknorm else 0
     out = [("emb", 0, m.V * D)]
     for l in range(m.L):
         w = st.layer_map(m, l)
-        sizes = dict(an1=D, wq=D * D, wk=D * KD, wv=D * KD, wo=D * D, an2=D, wr=D * m.n_exp, w1=E * D * F,
-                     w3=E * D * F, w2=E * F * D)
+        sizes = dict(an1=D, wq=D * D, wk=D * KD, wv=D * KD, wo=D * D, qn=hq, kn=hq, an2=D, wr=D * m.n_exp,
+                     w1=E * D * F, w3=E * D * F, w2=E * F * D)
         out += [(f"{k}[{l}]", w[k], w[k] + n) for k, n in sizes.items() if n]
     w = st.layer_map(m, 0)
     out.append(("nf", w["nf"], w["nf"] + D))
@@ -500,6 +503,9 @@ class Decoder:
         d.orc_dec_new.restype = ctypes.c_void_p
         d.orc_dec_free.argtypes = [ctypes.c_void_p]
         d.orc_dec_chunk.argtypes = [ctypes.c_void_p, _fp, _ip, _i, _i, _fp]
+        d.orc_dec_chunk_fn.argtypes = [ctypes.c_void_p, _fp, _ip, _i, _i, _fp, _fp]
+        d.orc_mtp_argmax.argtypes = [ctypes.POINTER(OrcModel), _fp, _fp, _i, _fp]
+        d.orc_mtp_argmax.restype = _i
         self.dll, self.m, self.P = d, m, np.ascontiguousarray(P, np.float32)
         self.h = d.orc_dec_new(ctypes.byref(m), W, kvdt, exact, maxpos)
 
@@ -508,6 +514,52 @@ class Decoder:
         out = np.empty((tok.size, self.m.V), np.float32)
         self.dll.orc_dec_chunk(self.h, _f(self.P), _n(tok), tok.size, start, _f(out))
         return out
+
+    def chunk_fn(self, tok, start):
+        """(logits [m][V], final-normed rows fn [m][D])."""
+        tok = np.ascontiguousarray(tok, np.int32)
+        out = np.empty((tok.size, self.m.V), np.float32)
+        fn = np.empty((tok.size, self.m.D), np.float32)
+        self.dll.orc_dec_chunk_fn(self.h, _f(self.P), _n(tok), tok.size, start, _f(out), _f(fn))
+        return out, fn
+
+    def mtp_argmax(self, fn1, k):
+        """MTP head k's draft token from a final-normed row (and its logits)."""
+        fn1 = np.ascontiguousarray(fn1, np.float32)
+        lg = np.empty(self.m.V, np.float32)
+        t = self.dll.orc_mtp_argmax(ctypes.byref(self.m), _f(self.P), _f(fn1), k, _f(lg))
+        return int(t), lg
+
+    def generate_spec(self, prompt, n, prefill):
+        """run_generation's greedy self-speculative loop (tinylm.c:3977-3995,
+        no stop token): prefill in chunks of `prefill` rows; then each round
+        takes x1 = argmax of the current logits row, the K heads' drafts from
+        its final-normed row, and one chunk of the K+1 tokens at pos; draft
+        r+1 is kept while it equals row r's argmax.  Returns (tokens, chunks,
+        rows) with rows[i] the logits row token i was chosen from."""
+        K = self.m.n_mtp
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        i = 0
+        while i < prompt.size:
+            mm = min(prefill, prompt.size - i)
+            lg, fn = self.chunk_fn(prompt[i:i + mm], i)
+            i += mm
+        pos, lg_cur, fn_cur = prompt.size, lg[-1], fn[-1]
+        out, rows, chunks = [], [], 0
+        while len(out) < n:
+            draft = [int(np.argmax(lg_cur))] + [self.mtp_argmax(fn_cur, k)[0] for k in range(K)]
+            lg, fn = self.chunk_fn(np.array(draft, np.int32), pos)
+            chunks += 1
+            out.append(draft[0])
+            rows.append(lg_cur)
+            acc = 0
+            while acc < K and len(out) < n and draft[acc + 1] == int(np.argmax(lg[acc])):
+                out.append(draft[acc + 1])
+                rows.append(lg[acc])
+                acc += 1
+            pos += acc + 1
+            lg_cur, fn_cur = lg[acc], fn[acc]
+        return out, chunks, rows
 
     def __del__(self):
         try:
@@ -552,6 +604,78 @@ class DecAttn:
         ctx = np.empty((m, self.D), np.float32)
         self.fn(self.h, l, _f(q), _f(k), _f(v), m, start, _f(ctx))
         return ctx
+
+
+def qknorm(buf, gain, nheads, which="oracle"):
+    """qknorm_apply (tinylm.c:597-605) on buf [rows][nheads*hd], a copy."""
+    buf = np.array(buf, np.float32, copy=True, order="C")
+    gain = np.ascontiguousarray(gain, np.float32)
+    rows = buf.shape[0]
+    hd = buf.shape[1] // nheads
+    if which == "oracle":
+        d = ctypes.CDLL(LIB)
+        d.orc_qknorm.argtypes = [_fp, _fp, _i, _i, _i]
+        d.orc_qknorm(_f(buf), _f(gain), rows, nheads, hd)
+    else:
+        d = ctypes.CDLL(DEC_LIB)
+        d.tlref_qknorm.argtypes = [_fp, _fp, _i, _i, _i]
+        d.tlref_qknorm(_f(buf), _f(gain), rows, nheads, hd)
+    return buf
+
+
+def dec_moe(fnorm, fin, wr, w1, w3, w2, E):
+    """The oracle's decode MoE layer (orc_dec_moe): (out, assign, gate, rprobs)."""
+    d = ctypes.CDLL(LIB)
+    d.orc_dec_moe.argtypes = [_i, _i, _i, _i, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _ip, _fp, _fp]
+    fnorm, fin = (np.ascontiguousarray(a, np.float32) for a in (fnorm, fin))
+    N, D = fnorm.shape
+    F = w1.size // (E * D)
+    out = np.empty_like(fin)
+    assign = np.empty(N, np.int32)
+    gate = np.empty(N, np.float32)
+    rprobs = np.empty((N, E), np.float32)
+    d.orc_dec_moe(N, D, F, E, _f(fnorm), _f(fin), _f(out), _f(np.ascontiguousarray(wr, np.float32)),
+                  _f(np.ascontiguousarray(w1, np.float32)), _f(np.ascontiguousarray(w3, np.float32)),
+                  _f(np.ascontiguousarray(w2, np.float32)), _n(assign), _f(gate), _f(rprobs))
+    return out, assign, gate, rprobs
+
+
+class RefDecode:
+    """The reference's own decode pieces (_ref/libtlref_dec.so): a whole
+    model's Gen (gen_new, no int8 copies) and, on the flat parameters P,
+    moe_forward_q8's fp32 branch for layer l (tinylm.c:3433-3458) and
+    mtp_argmax (:3930-3936).  Test infrastructure: built and run only where
+    /root/reference exists."""
+
+    def __init__(self, m, kvdt=1):
+        d = ctypes.CDLL(DEC_LIB)
+        d.tlref_gen_new.argtypes = [_i] * 11
+        d.tlref_gen_new.restype = ctypes.c_void_p
+        d.tlref_dec_moe.argtypes = [ctypes.c_void_p, _fp, _i, _fp, _fp, _fp, _i, _ip, _fp, _fp]
+        d.tlref_dec_moe.restype = _i
+        d.tlref_mtp_argmax.argtypes = [ctypes.c_void_p, _fp, _fp, _i, _fp]
+        d.tlref_mtp_argmax.restype = _i
+        self.dll, self.m = d, m
+        self.h = d.tlref_gen_new(m.V, m.D, m.H, m.KV, m.F, m.T, m.L, m.n_exp, m.n_mtp, m.qknorm, kvdt)
+
+    def moe(self, P, l, fnorm, fin):
+        P = np.ascontiguousarray(P, np.float32)
+        fnorm, fin = (np.ascontiguousarray(a, np.float32) for a in (fnorm, fin))
+        N = fnorm.shape[0]
+        out = np.empty_like(fin)
+        assign = np.empty(N, np.int32)
+        gate = np.empty(N, np.float32)
+        rprobs = np.empty((N, self.m.n_exp), np.float32)
+        rc = self.dll.tlref_dec_moe(self.h, _f(P), l, _f(fnorm), _f(fin), _f(out), N, _n(assign), _f(gate),
+                                    _f(rprobs))
+        assert rc == 0
+        return out, assign, gate, rprobs
+
+    def mtp_argmax(self, P, fn1, k):
+        P, fn1 = (np.ascontiguousarray(a, np.float32) for a in (P, fn1))
+        lg = np.empty(self.m.V, np.float32)
+        t = self.dll.tlref_mtp_argmax(self.h, _f(P), _f(fn1), k, _f(lg))
+        return int(t), lg
 
 
 def ref_forward_logits(m, B, P, tok, path=SEQ_LIB):

@@ -102,11 +102,13 @@ float  orc_gradnorm(const float *G, size_t n);                                  
 void   orc_adamw(float *P, const float *G, float *M, float *V, size_t n, float lr, float b1, float b2,
                  float wd, int t, float gscale);                                             /* :1159 */
 
-/* A model (tinylm.c Cfg :35-59 without QK-norm / shared experts) and its
- * flat parameter layout (map_weights :361-393; wr and the E expert slots when
- * n_exp > 0). */
-typedef struct { int V, D, L, H, KV, F, T, n_mtp, n_exp, win, full_every; float rope_base; } OrcModel;
-typedef struct { size_t emb, an1, wq, wk, wv, wo, an2, wr, w1, w3, w2, nf, mtp0, total; } OrcLayerMap;
+/* A model (tinylm.c Cfg :35-59 without shared experts) and its flat
+ * parameter layout (map_weights :361-393: the QK-norm gains qn, kn (hd each)
+ * between wo and an2 when qknorm, wr and the E expert slots when n_exp > 0).
+ * The training step runs qknorm = 0 only (the reference refuses to train
+ * QK-norm models, :2707-2713); the decoder runs both. */
+typedef struct { int V, D, L, H, KV, F, T, n_mtp, n_exp, win, full_every; float rope_base; int qknorm; } OrcModel;
+typedef struct { size_t emb, an1, wq, wk, wv, wo, qn, kn, an2, wr, w1, w3, w2, nf, mtp0, total; } OrcLayerMap;
 void  orc_param_map(const OrcModel *m, int layer, OrcLayerMap *o);
 /* init_params (:395-419) from the reference generator seeded with `seed` */
 void  orc_init_params(const OrcModel *m, float *P, uint64_t seed);
@@ -115,7 +117,17 @@ void  orc_init_params(const OrcModel *m, float *P, uint64_t seed);
 float orc_train_step(const OrcModel *m, int B, const float *P, float *G, const int *tok, const int *tgt,
                      const int *tgt_mtp);
 
-/* ---- decode: forward_chunk (:3721-3830), fp32 weights, dense FFN ---------
+/* qknorm_apply (:597-605): each of rows x nheads head vectors of hd values
+ * becomes v * s * gain with s = 1 / sqrt(sum(v^2) / hd + 1e-5). */
+void orc_qknorm(float *buf, const float *gain, int rows, int nheads, int hd);
+/* The decode MoE layer (moe_forward_q8's fp32 branch, :3433-3458): router
+ * logits fnorm . wr, softmax (expf) and the first maximum per row; out = fin,
+ * then per expert in order its rows (in row order): a = silu(x W1) * (x W3),
+ * out[n] += gate[n] * (a W2).  K = 1 routing, no router bias. */
+void orc_dec_moe(int N, int D, int F, int E, const float *fnorm, const float *fin, float *out, const float *wr,
+                 const float *w1, const float *w3, const float *w2, int *assign, float *gate, float *rprobs);
+
+/* ---- decode: forward_chunk (:3721-3830), fp32 weights ---------------------
  * A ring KV cache of W positions per layer stored as f32 (kvdt 0) or f16
  * (kvdt 1, the reference default), the unsplit attention path, and the
  * softmax exponential fast_expf (exact_exp 0, the default) or expf.  maxpos
@@ -124,6 +136,13 @@ typedef struct OrcDec OrcDec;
 OrcDec *orc_dec_new(const OrcModel *m, int W, int kvdt, int exact_exp, int maxpos);
 void    orc_dec_free(OrcDec *d);
 void    orc_dec_chunk(OrcDec *d, const float *P, const int *tok, int m, int start_pos, float *logits);
+/* orc_dec_chunk that also returns the final-normed rows fn [m][D] (the rows
+ * the MTP heads read, gn->fn of forward_chunk :3828). */
+void    orc_dec_chunk_fn(OrcDec *d, const float *P, const int *tok, int m, int start_pos, float *logits,
+                         float *fn);
+/* mtp_argmax (:3930-3936): head k's draft from a final-normed row fn1 [D]:
+ * argmax_v((fn1 + silu(fn1 Wk)) emb^T); its logits [V] into logits. */
+int     orc_mtp_argmax(const OrcModel *m, const float *P, const float *fn1, int k, float *logits);
 /* One layer's attention step of orc_dec_chunk: ring stores of the m new K / V
  * rows, then attention of the m query rows (q [m][D], k / v [m][KD], ctx
  * [m][D]). */

@@ -255,15 +255,18 @@ static int layer_win(const OrcModel *m, int l)
 /* map_weights (tinylm.c:361-393) without QK-norm */
 void orc_param_map(const OrcModel *m, int l, OrcLayerMap *o)
 {
-    const size_t D = m->D, KD = (size_t)m->KV * (m->D / m->H), F = m->F, E = m->n_exp > 0 ? m->n_exp : 1;
-    const size_t per = D + D * D + 2 * D * KD + D * D + D + (m->n_exp > 0 ? D * m->n_exp : 0) + E * 3 * D * F;
+    const size_t D = m->D, hd = (size_t)(m->D / m->H), KD = (size_t)m->KV * hd, F = m->F,
+                 E = m->n_exp > 0 ? m->n_exp : 1, QK = m->qknorm ? 2 * hd : 0;
+    const size_t per = D + D * D + 2 * D * KD + D * D + QK + D + (m->n_exp > 0 ? D * m->n_exp : 0) + E * 3 * D * F;
     o->emb = 0;
     o->an1 = (size_t)m->V * D + (size_t)l * per;
     o->wq = o->an1 + D;
     o->wk = o->wq + D * D;
     o->wv = o->wk + D * KD;
     o->wo = o->wv + D * KD;
-    o->an2 = o->wo + D * D;
+    o->qn = o->wo + D * D;                       /* QK-norm gains (hd each), when qknorm */
+    o->kn = o->qn + (m->qknorm ? hd : 0);
+    o->an2 = o->wo + D * D + QK;
     o->wr = o->an2 + D;
     o->w1 = o->wr + (m->n_exp > 0 ? D * m->n_exp : 0);
     o->w3 = o->w1 + E * D * F;
@@ -278,6 +281,7 @@ void orc_param_map(const OrcModel *m, int l, OrcLayerMap *o)
 float orc_train_step(const OrcModel *m, int B, const float *P, float *G, const int *tok, const int *tgt,
                      const int *tgt_mtp)
 {
+    if (m->qknorm) return NAN;                   /* the reference refuses to train these (:2707-2713) */
     const int T = m->T, N = B * T, D = m->D, H = m->H, KV = m->KV, hd = D / H, KD = KV * hd, F = m->F,
               V = m->V, L = m->L, E = m->n_exp;
     const size_t ND = (size_t)N * D, NK = (size_t)N * KD, NF = (size_t)N * F, NV = (size_t)N * V;
@@ -432,6 +436,8 @@ void orc_init_params(const OrcModel *m, float *P, uint64_t seed)
         orc_fill_normal(P + w.wk, D * KD, 0.02f);
         orc_fill_normal(P + w.wv, D * KD, 0.02f);
         orc_fill_normal(P + w.wo, D * D, scaled);
+        if (m->qknorm)
+            for (int i = 0; i < m->D / m->H; i++) { P[w.qn + i] = 1.0f; P[w.kn + i] = 1.0f; }
         orc_fill_normal(P + w.w1, E * D * F, 0.02f);
         orc_fill_normal(P + w.w3, E * D * F, 0.02f);
         orc_fill_normal(P + w.w2, E * F * D, scaled);
@@ -575,8 +581,80 @@ void orc_dec_attn(OrcDec *d, int l, const float *q, const float *k, const float 
     free(pr);
 }
 
+void orc_qknorm(float *buf, const float *gain, int rows, int nheads, int hd)
+{
+    for (int r = 0; r < rows * nheads; r++) {
+        float *v = buf + (size_t)r * hd;
+        float ss = 0.0f;
+        for (int i = 0; i < hd; i++) ss += v[i] * v[i];
+        const float sc = 1.0f / sqrtf(ss / hd + 1e-5f);
+        for (int i = 0; i < hd; i++) v[i] = v[i] * sc * gain[i];
+    }
+}
+
+void orc_dec_moe(int N, int D, int F, int E, const float *fnorm, const float *fin, float *out, const float *wr,
+                 const float *w1, const float *w3, const float *w2, int *assign, float *gate, float *rprobs)
+{
+    float *rt = zalloc((size_t)N * E), *X = zalloc((size_t)N * D), *g = zalloc((size_t)N * F),
+          *u = zalloc((size_t)N * F), *y = zalloc((size_t)N * D);
+    int *idx = calloc((size_t)N, sizeof(int));
+    orc_mm(rt, fnorm, wr, N, D, E);
+    for (int n = 0; n < N; n++) {                /* softmax, then the first maximum */
+        const float *r = rt + (size_t)n * E;
+        float *pr = rprobs + (size_t)n * E;
+        float mx = -1e30f;
+        for (int e = 0; e < E; e++) if (r[e] > mx) mx = r[e];
+        float sm = 0.0f;
+        for (int e = 0; e < E; e++) { pr[e] = expf(r[e] - mx); sm += pr[e]; }
+        const float inv = 1.0f / sm;
+        int best = 0;
+        for (int e = 0; e < E; e++) { pr[e] *= inv; if (pr[e] > pr[best]) best = e; }
+        assign[n] = best;
+        gate[n] = pr[best];
+    }
+    memcpy(out, fin, sizeof(float) * (size_t)N * D);
+    for (int e = 0; e < E; e++) {
+        int ne = 0;
+        for (int n = 0; n < N; n++) if (assign[n] == e) idx[ne++] = n;
+        if (!ne) continue;
+        for (int r = 0; r < ne; r++) memcpy(X + (size_t)r * D, fnorm + (size_t)idx[r] * D, sizeof(float) * D);
+        orc_mm(g, X, w1 + (size_t)e * D * F, ne, D, F);
+        orc_mm(u, X, w3 + (size_t)e * D * F, ne, D, F);
+        for (size_t i = 0; i < (size_t)ne * F; i++) u[i] = silu(g[i]) * u[i];
+        orc_mm(y, u, w2 + (size_t)e * F * D, ne, F, D);
+        for (int r = 0; r < ne; r++) {
+            const float gt = gate[idx[r]];
+            float *o = out + (size_t)idx[r] * D;
+            const float *yr = y + (size_t)r * D;
+            for (int i = 0; i < D; i++) o[i] += gt * yr[i];
+        }
+    }
+    free(rt); free(X); free(g); free(u); free(y); free(idx);
+}
+
+int orc_mtp_argmax(const OrcModel *md, const float *P, const float *fn1, int k, float *logits)
+{
+    const int D = md->D, V = md->V;
+    OrcLayerMap w;
+    orc_param_map(md, 0, &w);
+    float *ht = zalloc(D), *hh = zalloc(D);
+    orc_mm(ht, fn1, P + w.mtp0 + (size_t)k * D * D, 1, D, D);
+    for (int i = 0; i < D; i++) hh[i] = fn1[i] + silu(ht[i]);
+    memset(logits, 0, sizeof(float) * (size_t)V);
+    orc_mm_bt(logits, hh, P + w.emb, 1, V, D);
+    int best = 0;
+    for (int i = 1; i < V; i++) if (logits[i] > logits[best]) best = i;
+    free(ht); free(hh);
+    return best;
+}
+
 /* m tokens at positions start..start+m-1; logits [m][V] (main head). */
 void orc_dec_chunk(OrcDec *d, const float *P, const int *tok, int m, int start, float *logits)
+{
+    orc_dec_chunk_fn(d, P, tok, m, start, logits, NULL);
+}
+
+void orc_dec_chunk_fn(OrcDec *d, const float *P, const int *tok, int m, int start, float *logits, float *fn)
 {
     const OrcModel *md = &d->m;
     const int D = md->D, H = md->H, KV = md->KV, hd = D / H, KD = KV * hd, F = md->F, V = md->V;
@@ -597,12 +675,24 @@ void orc_dec_chunk(OrcDec *d, const float *P, const int *tok, int m, int start, 
         orc_mm(q, xn, P + w.wq, m, D, D);
         orc_mm(k, xn, P + w.wk, m, D, KD);
         orc_mm(v, xn, P + w.wv, m, D, KD);
+        if (md->qknorm) {                        /* :3752-3754 */
+            orc_qknorm(q, P + w.qn, m, H, hd);
+            orc_qknorm(k, P + w.kn, m, KV, hd);
+        }
         orc_rope(q, pos, 1, m, H, hd, d->cs, d->sn, 0);
         orc_rope(k, pos, 1, m, KV, hd, d->cs, d->sn, 0);
         orc_dec_attn(d, l, q, k, v, m, start, ctx);
         orc_mm(tmp, ctx, P + w.wo, m, D, D);
         for (size_t i = 0; i < (size_t)m * D; i++) x[i] += tmp[i];
         orc_rmsnorm_fwd(x, P + w.an2, xn, rinv, m, D);
+        if (md->n_exp > 0) {                      /* :3815-3818: out = tmp = x + ffn, then x = tmp */
+            int *as = calloc((size_t)m, sizeof(int));
+            float *gt = zalloc(m), *rp = zalloc((size_t)m * md->n_exp);
+            orc_dec_moe(m, D, F, md->n_exp, xn, x, tmp, P + w.wr, P + w.w1, P + w.w3, P + w.w2, as, gt, rp);
+            memcpy(x, tmp, sizeof(float) * (size_t)m * D);
+            free(as); free(gt); free(rp);
+            continue;
+        }
         orc_mm(g, xn, P + w.w1, m, D, F);
         orc_mm(u, xn, P + w.w3, m, D, F);
         for (size_t i = 0; i < (size_t)m * F; i++) u[i] = silu(g[i]) * u[i];
@@ -611,6 +701,7 @@ void orc_dec_chunk(OrcDec *d, const float *P, const int *tok, int m, int start, 
     }
     orc_param_map(md, 0, &w);
     orc_rmsnorm_fwd(x, P + w.nf, xn, rinv, m, D);
+    if (fn) memcpy(fn, xn, sizeof(float) * (size_t)m * D);
     memset(logits, 0, sizeof(float) * (size_t)m * V);
     orc_mm_bt(logits, xn, P + w.emb, m, V, D);
     float *all[] = {x, xn, q, k, v, ctx, tmp, g, u, rinv};

@@ -164,22 +164,24 @@ E_UNSUP = -6
 
 
 def test_models_the_step_cannot_run_are_refused(host, tmp_path):
-    """QK-norm gains shift every later weight (map_weights, tinylm.c:377-381),
-    shared experts are refused by the reference itself (check_supported,
+    """Shared experts are refused by the reference itself (check_supported,
     :1946-1953) and top-k > 1 routing is not the top-1 layer built here: the
-    header reads, but tl_ckpt_model refuses to describe such a model."""
+    header reads, but tl_ckpt_model refuses to describe such a model.  A
+    QK-norm model (TLM6/7) is described, with qknorm set: the decoder runs it
+    (the training step refuses it, as the reference does, :2707-2713)."""
     def model_rc(version, cfg):
         info = tlgemm.TlCkpt(version=version, **{k: int(cfg.get(k, 0)) for k in FIELDS[:HDR_INTS[version]]})
         m = tlgemm.TlModel()
         return host.dll.tl_ckpt_model(ctypes.byref(info), ctypes.byref(m)), m
 
     rc, m = model_rc(6, dict(BASE, qknorm=1))
-    assert rc == E_UNSUP and m.V == 0
+    assert rc == 0 and m.qknorm == 1 and m.V == BASE["V"]
+    assert host.dll.tl_train_new(ctypes.byref(m), 1) is None
     assert model_rc(6, dict(BASE, n_exp=4, n_shared=1))[0] == E_UNSUP
     assert model_rc(7, dict(BASE, n_exp=4, topk=2))[0] == E_UNSUP
     assert model_rc(7, dict(BASE, n_exp=4, topk=1))[0] == 0
     assert model_rc(7, dict(BASE, topk=2))[0] == 0                # dense: topk unused
-    assert host.dll.tl_ckpt_error(E_UNSUP).decode().startswith("model uses QK-norm")
+    assert host.dll.tl_ckpt_error(E_UNSUP).decode().startswith("model uses shared experts")
 
 
 def test_header_whose_count_overflows_is_refused(host, tmp_path):

@@ -575,3 +575,115 @@ def test_persist_chunks_equal_graph_chunks(lib):
     assert np.array_equal(one, many) and np.array_equal(lg1, lgm), "split launches must be bit-identical"
     assert list(one) == [int(np.argmax(row)) for g in grows for row in g]
     assert normwise_rel(lg1, grows[-1]) <= TOL
+
+
+# The reference's other decode forms (forward_chunk with QK-norm and MoE
+# layers, tinylm.c:3744-3747 and :3806-3808; the MTP heads' drafts,
+# mtp_argmax :3929-3936): small and m8 shapes with 4 top-1 experts per layer,
+# per-head QK RMSNorm and 2 MTP heads.
+FORMS = dict(SMALL, n_exp=4, n_mtp=2, qknorm=1)
+M8_FORMS = dict(M8, n_exp=4, n_mtp=2, qknorm=1)
+
+
+@pytest.mark.parametrize("fused", [1, 0], ids=["fused", "unfused"])
+@pytest.mark.parametrize("shape", ["small", "m8"])
+def test_forms_chunks_match_oracle(lib, shape, fused):
+    """Chunks of 1..8 rows of a QK-norm + MoE + MTP model on an f32 ring:
+    every chunk's logits within 1e-4 of the oracle's forward_chunk."""
+    import tlgemm
+    kw, W = (FORMS, 32) if shape == "small" else (M8_FORMS, 256)
+    m, P = params(kw, 21)
+    print("forms chunks", shape, fused, flush=True)
+    StepFns("oracle").dll.orc_set_threads(16)
+    dec = tlgemm.host().decode(kw, W, kv_f16=0, exact_exp=0, maxpos=512, mmax=8)
+    dec.set_fused(fused)
+    dec.upload(P, stream())
+    orc = Decoder(m, P, W, kvdt=0, exact=0, maxpos=512)
+    toks = np.random.default_rng(22).integers(0, m.V, 80).astype(np.int32)
+    pos, worst = 0, 0.0
+    for s in [1, 3, 8, 2, 5, 1, 7, 4, 8, 6, 1, 8, 8, 8, 1, 1, 1, 1, 1, 1]:
+        if pos + s > toks.size:
+            break
+        got = dec.chunk(toks[pos:pos + s], pos, stream())
+        e = normwise_rel(got, orc.chunk(toks[pos:pos + s], pos))
+        worst = max(worst, e)
+        assert e <= TOL, (pos, s, e)
+        pos += s
+    print("worst chunk", f"{worst:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("shape", ["small", "m8"])
+def test_mtp_draft_matches_oracle(lib, shape):
+    """tl_decode_mtp_draft from each row of a chunk and each head equals the
+    oracle's mtp_argmax on that row's final-normed vector, or lies within
+    1e-5 * max|logit| of it (a near-tie)."""
+    t = _t()
+    import tlgemm
+    kw, W = (FORMS, 32) if shape == "small" else (M8_FORMS, 256)
+    m, P = params(kw, 23)
+    dec = tlgemm.host().decode(kw, W, kv_f16=0, exact_exp=0, maxpos=512, mmax=8)
+    dec.upload(P, stream())
+    orc = Decoder(m, P, W, kvdt=0, exact=0, maxpos=512)
+    toks = np.random.default_rng(24).integers(0, m.V, 19).astype(np.int32)
+    dt = t.full((8,), -1, dtype=t.int32, device="cuda")
+    ties = 0
+    for pos, s in ((0, 8), (8, 3), (11, 8)):
+        dec.chunk(toks[pos:pos + s], pos, stream())
+        _, fn = orc.chunk_fn(toks[pos:pos + s], pos)
+        for r in range(s):
+            for k in range(m.n_mtp):
+                dec.mtp_draft(r, k, dt.data_ptr() + 4 * k, stream())
+            got = dt.cpu().tolist()
+            for k in range(m.n_mtp):
+                want, lg = orc.mtp_argmax(fn[r], k)
+                if got[k] != want:
+                    ties += 1
+                    assert lg[want] - lg[got[k]] <= 1e-5 * np.abs(lg).max(), (pos, r, k, got[k], want)
+    assert ties <= 1, ties
+
+
+@pytest.mark.parametrize("heads", ["random", "zero"])
+@pytest.mark.parametrize("shape", ["small", "m8"])
+def test_generate_spec_matches_oracle(lib, shape, heads):
+    """Self-speculative generation (tl_decode_generate_spec: drafts from the
+    MTP heads, one chunk of K+1 rows verifies them) against the oracle's
+    restatement of run_generation's loop on the same prefill chunking: the
+    same tokens and the same number of verification chunks.  Heads of zero
+    weight draft the current token, so drafts are kept exactly where the
+    stream repeats.  On the small shape the 32-slot ring wraps, where a
+    chunk's later rows overwrite slots its earlier rows still read (as the
+    reference's forward_chunk does); at m8 nothing wraps and the tokens are
+    also the greedy ones."""
+    import tlgemm
+    kw, W, n = (FORMS, 32, 40) if shape == "small" else (M8_FORMS, 256, 24)
+    m, P = params(kw, 25)
+    if heads == "zero":
+        mt = StepFns("oracle").layer_map(m, 0)["mtp0"]
+        P[mt:mt + m.n_mtp * m.D * m.D] = 0.0
+    prompt = np.random.default_rng(26).integers(0, m.V, 11).astype(np.int32)
+    StepFns("oracle").dll.orc_set_threads(16)
+    want, wchunks, rows = Decoder(m, P, W, kvdt=0, exact=0, maxpos=512).generate_spec(prompt, n, 8)
+    dec = tlgemm.host().decode(kw, W, kv_f16=0, exact_exp=0, maxpos=512, mmax=8)
+    dec.upload(P, stream())
+    got, chunks = dec.generate_spec(prompt, n, stream())
+    got = [int(v) for v in got]
+    print("spec", shape, heads, chunks, "chunks for", n, "tokens", want[:12], flush=True)
+    agree = same_stream(got, want, rows, 1e-5)
+    assert agree == n, (agree, got, want)
+    assert chunks == wchunks, (chunks, wchunks)
+    if shape == "m8":
+        greedy, _ = oracle_greedy(Decoder(m, P, W, kvdt=0, exact=0, maxpos=512), prompt, n)
+        assert got == greedy
+
+
+def test_persist_rejects_forms(lib):
+    """The persistent kernels run the dense model without QK-norm: a model
+    with either form is refused before anything is launched."""
+    import tlgemm
+    for kw in (dict(SMALL, qknorm=1), dict(SMALL, n_exp=4)):
+        m, P = params(kw, 27)
+        dec = tlgemm.host().decode(kw, 32, kv_f16=0, exact_exp=0, maxpos=128, mmax=8)
+        dec.upload(P, stream())
+        dec.prime(np.arange(5, dtype=np.int32), stream())
+        with pytest.raises(tlgemm.TlgError):
+            dec.persist(4, stream())

@@ -309,3 +309,152 @@ def test_decode_attention_matches_reference(D, H, KV, T, win, full_every, kvdt, 
             worst = max(worst, float(np.abs(a - b).max() / (1.0 + np.abs(b).max())))
             pos += m
         assert worst > 1e-5, worst
+
+
+# ---- decode forms beyond the dense model: QK-norm, MoE layers, MTP drafts ----
+def _ref_dec_available():
+    from oracle import DEC_LIB
+    return os.path.exists(DEC_LIB)
+
+
+DEC_FORMS = dict(V=96, D=64, L=2, H=2, KV=1, F=48, T=16, n_mtp=2, n_exp=4, qknorm=1)
+
+
+def _forms_params(seed):
+    from oracle import StepFns, model
+    m = model(**DEC_FORMS)
+    st = StepFns("oracle")
+    r = np.random.default_rng(seed)
+    P = (0.05 * r.standard_normal(st.param_count(m))).astype(np.float32)
+    return m, st, P
+
+
+@pytest.mark.skipif(not _ref_dec_available(), reason="oracle/_ref not built (needs /root/reference)")
+def test_qknorm_matches_reference():
+    """orc_qknorm against the reference's qknorm_apply (tinylm.c:597-605),
+    and a head scaled by c comes out the same (the norm is scale-free but for
+    the 1e-5 in the mean square)."""
+    from oracle import qknorm
+    r = np.random.default_rng(31)
+    for rows, nh in ((1, 12), (5, 3), (8, 1)):
+        buf = r.standard_normal((rows, nh * 32)).astype(np.float32)
+        gain = (1 + 0.1 * r.standard_normal(32)).astype(np.float32)
+        a, b = qknorm(buf, gain, nh), qknorm(buf, gain, nh, which="reference")
+        assert normwise_rel(a, b) <= 1e-6
+        c = qknorm(buf * np.float32(64.0), gain, nh)
+        assert normwise_rel(c, a) <= 1e-4      # the 1e-5 of the mean square moves it by ~5e-6 relative
+
+
+@pytest.mark.skipif(not _ref_dec_available(), reason="oracle/_ref not built (needs /root/reference)")
+def test_decode_moe_matches_reference():
+    """orc_dec_moe on the slices the oracle's layout gives (a QK-norm model,
+    so qn / kn shift every later weight) against the reference's own
+    moe_forward_q8 fp32 branch (:3433-3458), which maps P itself: the same
+    experts chosen, gates and outputs to fp32 rounding."""
+    from oracle import RefDecode, dec_moe
+    m, st, P = _forms_params(7)
+    ref = RefDecode(m)
+    r = np.random.default_rng(9)
+    for l in range(m.L):
+        w = st.layer_map(m, l)
+        E, D, F = m.n_exp, m.D, m.F
+        for N in (1, 3, 8):
+            fnorm = r.standard_normal((N, D)).astype(np.float32)
+            fin = r.standard_normal((N, D)).astype(np.float32)
+            got = dec_moe(fnorm, fin, P[w["wr"]:w["wr"] + D * E], P[w["w1"]:w["w1"] + E * D * F],
+                          P[w["w3"]:w["w3"] + E * D * F], P[w["w2"]:w["w2"] + E * F * D], E)
+            want = ref.moe(P, l, fnorm, fin)
+            assert np.array_equal(got[1], want[1]), (l, N)
+            assert normwise_rel(got[2], want[2]) <= 1e-6
+            assert normwise_rel(got[0] - fin, want[0] - fin) <= 1e-5
+
+
+@pytest.mark.skipif(not _ref_dec_available(), reason="oracle/_ref not built (needs /root/reference)")
+def test_mtp_argmax_matches_reference():
+    """The oracle's MTP draft against the reference's mtp_argmax
+    (:3930-3936): same token, logits to fp32 rounding; with a zero head the
+    draft is the main head's greedy token (hk = fn + silu(0) = fn)."""
+    from oracle import Decoder, RefDecode
+    m, st, P = _forms_params(11)
+    ref, dec = RefDecode(m), Decoder(m, P, W=m.T)
+    r = np.random.default_rng(12)
+    for k in range(m.n_mtp):
+        fn1 = r.standard_normal(m.D).astype(np.float32)
+        t, lg = dec.mtp_argmax(fn1, k)
+        tr, lgr = ref.mtp_argmax(P, fn1, k)
+        assert t == tr
+        assert normwise_rel(lg, lgr) <= 1e-6
+    w = st.layer_map(m, 0)
+    P0 = P.copy()
+    P0[w["mtp0"]:w["mtp0"] + m.D * m.D] = 0.0
+    fn1 = r.standard_normal(m.D).astype(np.float32)
+    t, lg = Decoder(m, P0, W=m.T).mtp_argmax(fn1, 0)
+    main = P0[:m.V * m.D].reshape(m.V, m.D).astype(np.float64) @ fn1.astype(np.float64)
+    assert t == int(np.argmax(main))
+
+
+def _greedy(dec, prompt, n):
+    lg = dec.chunk(prompt, 0)[-1]
+    out, pos = [], len(prompt)
+    for _ in range(n):
+        out.append(int(np.argmax(lg)))
+        lg = dec.chunk(np.array(out[-1:], np.int32), pos)[-1]
+        pos += 1
+    return out
+
+
+@pytest.mark.parametrize("heads", ["random", "zero"])
+def test_spec_loop_is_exact_greedy(heads):
+    """The oracle's self-speculative loop (tinylm.c:3977-3995) yields the
+    greedy tokens while the ring holds every position (the reference calls it
+    exact); with heads of zero weight (hh = fn, each head's logits the main
+    logits) every draft is the current token, so the chunks it runs follow
+    from the greedy stream's repeats.  A loop that kept a draft past a
+    mismatch, or advanced pos by the wrong count, changes the tokens."""
+    from oracle import Decoder, param_regions
+    m, st, P = _forms_params(7)
+    for name, a, b in param_regions(st, m):       # unit gains, larger layers: runs of
+        if name.split("[")[0] in ("an1", "an2", "nf", "qn", "kn"):   # repeats with changes
+            P[a:b] = 1.0
+        elif name != "emb" and not name.startswith("mtp"):
+            P[a:b] *= 2.0
+    mt = st.layer_map(m, 0)["mtp0"]
+    if heads == "zero":
+        P[mt:mt + m.n_mtp * m.D * m.D] = 0.0
+    prompt = np.array([3, 17, 40, 5, 77, 9], np.int32)
+    n = 20
+    want = _greedy(Decoder(m, P, W=64, kvdt=0, maxpos=64), prompt, n)
+    got, chunks, rows = Decoder(m, P, W=64, kvdt=0, maxpos=64).generate_spec(prompt, n, 4)
+    assert got == want
+    assert len(rows) == n and [int(np.argmax(r)) for r in rows] == want
+    if heads == "zero":
+        g, expect = 0, 0
+        while g < n:
+            expect, x1, g = expect + 1, want[g], g + 1
+            for _ in range(m.n_mtp):
+                if g >= n or want[g] != x1:
+                    break
+                g += 1
+        assert chunks == expect
+    assert chunks < n - 5                          # drafts were kept
+
+
+def test_decoder_forms_follow_their_definitions():
+    """The oracle decoder on a QK-norm + MoE + MTP model: the chunk's final
+    rows fn give the chunk's logits through the tied head, chunks of 1 and of
+    3 rows agree, and turning the QK-norm gains to c leaves the scores those
+    of gains 1 times c^2 (checked through the logits changing)."""
+    from oracle import Decoder
+    m, st, P = _forms_params(5)
+    tok = np.array([3, 17, 40, 5, 77], np.int32)
+    a = Decoder(m, P, W=m.T)
+    lg, fn = a.chunk_fn(tok, 0)
+    emb = P[:m.V * m.D].reshape(m.V, m.D).astype(np.float64)
+    assert normwise_rel(lg, fn.astype(np.float64) @ emb.T) <= 1e-5
+    b = Decoder(m, P, W=m.T)
+    rows = np.concatenate([b.chunk(tok[:2], 0), b.chunk(tok[2:], 2)])
+    assert normwise_rel(rows, lg) <= 1e-5
+    w = st.layer_map(m, 0)
+    P2 = P.copy()
+    P2[w["qn"]:w["qn"] + 32] *= 2.0
+    assert normwise_rel(Decoder(m, P2, W=m.T).chunk(tok, 0), lg) > 1e-4

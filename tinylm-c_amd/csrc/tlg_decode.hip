@@ -398,7 +398,161 @@ __global__ __launch_bounds__(1024) void k_dec_argmax(const float *__restrict__ l
     }
 }
 
+// qknorm_apply (tinylm.c:597-605) on the m new rows' q heads (H per row) and
+// k heads (KV per row), hd = 32: half a wave per head, the sum of squares on
+// the VALU (DPP row shifts, then row 0's (2's) lane 15 into row 1 (3)), then
+// v * s * gain with s = 1 / sqrt(ss / hd + 1e-5).
+template <int CTRL, int ROWMASK> __device__ __forceinline__ float dec_dpp(float x)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWMASK, 0xf, false));
+}
+__global__ __launch_bounds__(256) void k_dec_qknorm(float *__restrict__ q, float *__restrict__ k,
+                                                    const float *__restrict__ qn, const float *__restrict__ kn,
+                                                    int m, int H, int KV)
+{
+    const int head = blockIdx.x * 8 + (threadIdx.x >> 5), i = threadIdx.x & 31;
+    const int nq = m * H, n = nq + m * KV;
+    const bool live = head < n;
+    const int hh = live ? head : n - 1;            // whole waves reach the DPP sum
+    float *v;
+    const float *g;
+    if (hh < nq) { v = q + (size_t)(hh / H) * H * DEC_HD + (size_t)(hh % H) * DEC_HD; g = qn; }
+    else {
+        const int r = hh - nq;
+        v = k + (size_t)(r / KV) * KV * DEC_HD + (size_t)(r % KV) * DEC_HD;
+        g = kn;
+    }
+    const float x = v[i];
+    float ss = x * x;
+    ss += dec_dpp<0x111, 0xf>(ss);
+    ss += dec_dpp<0x112, 0xf>(ss);
+    ss += dec_dpp<0x114, 0xf>(ss);
+    ss += dec_dpp<0x118, 0xf>(ss);
+    ss += dec_dpp<0x142, 0xa>(ss);                   // lane 31 / 63: the half-wave's sum
+    ss = __shfl(ss, (threadIdx.x & 32) | 31);
+    const float sc = 1.0f / sqrtf(ss / (float)DEC_HD + 1e-5f);
+    if (live) v[i] = x * sc * g[i];
+}
+
+// The decode MoE router's top-1 (moe_rt_body, tinylm.c:3332-3341): per row
+// softmax of the E logits with expf and the first maximum of the normalised
+// probabilities (strictly greater, ties to the lowest expert); gate = that
+// probability.  One lane per row.
+__global__ __launch_bounds__(64) void k_dec_moe_route(const float *__restrict__ rt, int m, int E,
+                                                      int *__restrict__ assign, float *__restrict__ gate)
+{
+    const int j = threadIdx.x;
+    if (j >= m) return;
+    const float *r = rt + (size_t)j * E;
+    float mx = -1e30f;
+    for (int e = 0; e < E; e++) mx = r[e] > mx ? r[e] : mx;
+    float s = 0.f;
+    for (int e = 0; e < E; e++) s += expf(r[e] - mx);
+    const float inv = 1.0f / s;
+    int best = 0;
+    float pb = expf(r[0] - mx) * inv;
+    for (int e = 1; e < E; e++) {
+        const float p = expf(r[e] - mx) * inv;
+        if (p > pb) { pb = p; best = e; }
+    }
+    assign[j] = best;
+    gate[j] = pb;
+}
+
+// mtp_argmax's middle (tinylm.c:3933): hh = fn + silu(ht) with fn the final
+// RMSNorm of x (rmsnorm_fwd :540-548, gain nf) and silu(z) = z / (1 + e^-z).
+__global__ __launch_bounds__(256) void k_dec_mtp_mix(float *__restrict__ hh, const float *__restrict__ x,
+                                                     const float *__restrict__ nf, const float *__restrict__ ht,
+                                                     int D)
+{
+    __shared__ float red[4];
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < D; i += 256) ss = fmaf(x[i], x[i], ss);
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float t = (red[0] + red[1]) + (red[2] + red[3]);
+    const float sc = 1.0f / sqrtf(t / (float)D + 1e-5f);
+    for (int i = threadIdx.x; i < D; i += 256) {
+        const float z = ht[i];
+        hh[i] = x[i] * sc * nf[i] + z / (1.0f + expf(-z));
+    }
+}
+
+// argmax_v (tinylm.c:3844: the first maximum) of each of m rows of [m][V].
+__global__ __launch_bounds__(1024) void k_argmax_rows(const float *__restrict__ logits, int V, int *__restrict__ out)
+{
+    __shared__ float bv[1024];
+    __shared__ int bi[1024];
+    const float *row = logits + (size_t)blockIdx.x * V;
+    float best = -INFINITY;
+    int bidx = 0x7fffffff;
+    for (int i = threadIdx.x; i < V; i += 1024) {
+        const float x = row[i];
+        if (x > best) { best = x; bidx = i; }
+    }
+    bv[threadIdx.x] = best;
+    bi[threadIdx.x] = bidx;
+    __syncthreads();
+    for (int o = 512; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) {
+            const float x = bv[threadIdx.x + o];
+            const int xi = bi[threadIdx.x + o];
+            if (x > bv[threadIdx.x] || (x == bv[threadIdx.x] && xi < bi[threadIdx.x])) {
+                bv[threadIdx.x] = x;
+                bi[threadIdx.x] = xi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = bi[0] == 0x7fffffff ? 0 : bi[0];
+}
+
 // ============================================================== entries ==
+extern "C" int tlg_dev_dec_qknorm(float *q, float *k, const float *qn, const float *kn, int m, int H, int KV, int hd,
+                                  void *stream)
+{
+    int rc = tlg_ensure_init();
+    if (rc) return rc;
+    if (!q || !k || !qn || !kn || m <= 0 || H <= 0 || KV <= 0 || hd != DEC_HD)
+        return tlg_fail(TLG_EINVAL, "dec_qknorm: m=%d H=%d KV=%d hd=%d (hd must be %d)", m, H, KV, hd, DEC_HD);
+    const int n = m * (H + KV);
+    hipLaunchKernelGGL(k_dec_qknorm, dim3((n + 7) / 8), dim3(256), 0, (hipStream_t)stream, q, k, qn, kn, m, H, KV);
+    TLG_HIP(hipGetLastError());
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_dec_moe_route(const float *rt, int m, int E, int *assign, float *gate, void *stream)
+{
+    int rc = tlg_ensure_init();
+    if (rc) return rc;
+    if (!rt || !assign || !gate || m <= 0 || m > 64 || E < 1 || E > 64)
+        return tlg_fail(TLG_EINVAL, "dec_moe_route: m=%d E=%d", m, E);
+    hipLaunchKernelGGL(k_dec_moe_route, dim3(1), dim3(64), 0, (hipStream_t)stream, rt, m, E, assign, gate);
+    TLG_HIP(hipGetLastError());
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_dec_mtp_mix(float *hh, const float *x, const float *nf, const float *ht, int D, void *stream)
+{
+    int rc = tlg_ensure_init();
+    if (rc) return rc;
+    if (!hh || !x || !nf || !ht || D <= 0) return tlg_fail(TLG_EINVAL, "dec_mtp_mix: D=%d", D);
+    hipLaunchKernelGGL(k_dec_mtp_mix, dim3(1), dim3(256), 0, (hipStream_t)stream, hh, x, nf, ht, D);
+    TLG_HIP(hipGetLastError());
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_argmax_rows(const float *logits, int V, int m, int *out, void *stream)
+{
+    int rc = tlg_ensure_init();
+    if (rc) return rc;
+    if (!logits || !out || V <= 0 || m <= 0) return tlg_fail(TLG_EINVAL, "argmax_rows: V=%d m=%d", V, m);
+    hipLaunchKernelGGL(k_argmax_rows, dim3(m), dim3(1024), 0, (hipStream_t)stream, logits, V, out);
+    TLG_HIP(hipGetLastError());
+    return TLG_OK;
+}
+
 // dst[c][r] = src[r][c] through a 32 x 33 LDS tile (conflict-free both ways):
 // 32 x 8 threads, each moving 4 elements in and 4 out.
 __global__ __launch_bounds__(256) void k_transpose(float *__restrict__ dst, const float *__restrict__ src, int rows,

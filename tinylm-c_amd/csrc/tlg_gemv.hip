@@ -82,7 +82,10 @@ struct GvProb {
     int nb, S, KS;
     long long part;
     int direct, reducers;        // items that never wait; reducer items (nb when S > 1)
-    int full;                    // NN over all K rows per item (16-column blocks, no split)
+    int full;                    // NN over all K rows per item (32-column blocks, no split)
+    const int *bsel;             // optional: every segment's B is offset by bsel[0] * bstride
+    long long bstride;
+    const float *cgate;          // optional: results scaled by cgate[0] before the store
 };
 struct GvArgs {
     int nprob;
@@ -114,6 +117,17 @@ __device__ __forceinline__ void gv_st_agent(u64 *p, u64 v)
     __hip_atomic_store((GAS u64 *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float gv_silu_mul(float a, float b) { return a / (1.0f + expf(-a)) * b; }
+
+// The weight of segment g as the problem sees it (a device-selected expert
+// slice when bsel is set) and the output scale (1, or the row's gate).
+template <class P_, class G_> __device__ __forceinline__ const float *gv_B(const P_ &P, const G_ &g)
+{
+    return P.bsel ? g.B + (long long)*(const GAS int *)P.bsel * P.bstride : g.B;
+}
+template <class P_> __device__ __forceinline__ float gv_cgate(const P_ &P)
+{
+    return P.cgate ? *(const GAS float *)P.cgate : 1.0f;
+}
 
 // Sums over each 32-lane half of a wave on the VALU (DPP), in a fixed order:
 // row_shr 1, 2, 4, 8 within the 16-lane rows, then row_bcast:15 adds row 0's
@@ -236,6 +250,8 @@ __device__ __forceinline__ void gv_nn(const GvArgs &g, const GvProb &P, int s, i
     const int j = cb * CB + c * VEC;
     const int jc = j < P.No ? j : 0;                  // in-bounds address for edge lanes
     const int k_lo = s * P.KS, k_hi = min(G.R, k_lo + P.KS);
+    const float *Bb = gv_B(P, G);
+    const float cg = gv_cgate(P);
     float acc[MB][VEC];
 #pragma unroll
     for (int m = 0; m < MB; m++)
@@ -247,7 +263,7 @@ __device__ __forceinline__ void gv_nn(const GvArgs &g, const GvProb &P, int s, i
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int k = min(kb + 16 * u + 4 * w + r, k_hi - 1);
-            wv[u] = gv_ld<VEC>(G.B + (size_t)k * G.ldb + jc);
+            wv[u] = gv_ld<VEC>(Bb + (size_t)k * G.ldb + jc);
 #pragma unroll
             for (int m = 0; m < MB; m++) {
                 const size_t ai = (size_t)min(m, M - 1) * G.lda + k;
@@ -314,6 +330,7 @@ __device__ __forceinline__ void gv_nn(const GvArgs &g, const GvProb &P, int s, i
             const int jj = cb * CB + cc;
             if (jj < P.No) {
                 if (PRO == GV_PRO_RMS) v *= sh.rs[m];
+                v *= cg;
                 float *out = P.C + (size_t)m * P.ldc + jj;
                 *out = P.beta ? *out + v : v;
             }
@@ -352,6 +369,7 @@ __device__ __forceinline__ void gv_nn(const GvArgs &g, const GvProb &P, int s, i
         }
         if (jj < P.No) {
             if (PRO == GV_PRO_RMS) v *= sh.rs[m];
+            v *= cg;
             float *out = P.C + (size_t)m * P.ldc + jj;
             *out = bad ? __builtin_nanf("") : (P.beta ? *out + v : v);
         }
@@ -378,7 +396,8 @@ __device__ __forceinline__ void gv_nn_full(const GvProb &P, int cb, GvSmem<MB, 6
     const GvSeg &G = P.seg[0];
     const int K = G.R;
     const int j = cb * 32 + 4 * c;
-    const float *Bp = G.B + (j < P.No ? j : 0);
+    const float *Bp = gv_B(P, G) + (j < P.No ? j : 0);
+    const float cg = gv_cgate(P);
     f32x4 wv[UF];
 #pragma unroll
     for (int u = 0; u < UF; u++) wv[u] = gv_ld<4>(Bp + (size_t)min(32 * u + 8 * w + rr, K - 1) * G.ldb);
@@ -477,6 +496,7 @@ __device__ __forceinline__ void gv_nn_full(const GvProb &P, int cb, GvSmem<MB, 6
         for (int g = 1; g < NG; g++) v += sh.f.act[g * NO + tid];
         if (m < M && jj < P.No) {
             if (PRO == GV_PRO_RMS) v *= sh.rs[m];
+            v *= cg;
             float *out = P.C + (size_t)m * P.ldc + jj;
             *out = P.beta ? *out + v : v;
         }
@@ -497,6 +517,7 @@ __device__ __forceinline__ void gv_nt(const GvProb &P, int b, GvSmem<MB, 16 * VE
     const int o = b * GV_NT_ROWS + 2 * w + (lane >> 5);
     const int oc = min(o, P.No - 1);
     const int M = P.M;
+    const float cg = gv_cgate(P);
     float acc[MB];
 #pragma unroll
     for (int m = 0; m < MB; m++) acc[m] = 0.f;
@@ -536,7 +557,7 @@ __device__ __forceinline__ void gv_nt(const GvProb &P, int b, GvSmem<MB, 16 * VE
     };
     for (int sg = 0; sg < P.nseg; sg++) {
         const GvSeg &G = P.seg[sg];
-        const float *Brow = G.B + (size_t)oc * G.ldb;
+        const float *Brow = gv_B(P, G) + (size_t)oc * G.ldb;
         V wv[U];
         V av[U][MB];
         load(wv, av, G, Brow, 0);
@@ -567,6 +588,7 @@ __device__ __forceinline__ void gv_nt(const GvProb &P, int b, GvSmem<MB, 16 * VE
             if (m < M) {
                 float v = acc[m];
                 if (PRO == GV_PRO_RMS) v *= sh.rs[m];
+                v *= cg;
                 float *out = P.C + (size_t)m * P.ldc + o;
                 *out = P.beta ? *out + v : v;
             }
@@ -682,6 +704,7 @@ static int launch(GvArgs &a, int pro, hipStream_t st)
             if (P.kind == TLG_NN) v4 = v4 && P.No % 4 == 0 && g.ldb % 4 == 0 && al16(g.B);
             else v4 = v4 && g.R % 4 == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 && al16(g.A) && al16(g.B);
         }
+        if (P.bsel) v4 = v4 && P.bstride % 4 == 0;
         if (pro == GV_PRO_SWIGLU) v4 = v4 && al16(P.A2);
         if (pro == GV_PRO_RMS) v4 = v4 && al16(P.gain);
         if (pro != GV_PRO_NONE) v4 = v4 && P.seg[0].R % 4 == 0 && P.seg[0].lda % 4 == 0 && al16(P.seg[0].A);
@@ -869,6 +892,9 @@ extern "C" int tlg_dev_dec_gemv(const TlgDecGemv *calls, int n, void *stream)
             P.beta = c.beta ? 1 : 0;
             P.gain = c.gain;
             P.A2 = c.A2;
+            P.bsel = c.bsel;
+            P.bstride = c.bsel ? c.bstride : 0;
+            P.cgate = c.cgate;
             if (c.op == 0) {
                 P.kind = TLG_NN; P.No = c.N; P.ldc = c.N;
                 P.seg[0] = GvSeg{c.A, c.B, c.K, c.K, c.N};

@@ -111,17 +111,17 @@ int tl_ckpt_read(const char *path, const TlCkpt *c, float *P, size_t n)
 int tl_ckpt_model(const TlCkpt *c, TlModel *m)
 {
     memset(m, 0, sizeof *m);
-    /* Layouts the training step and the decoder would misread: QK-norm gains
-     * sit between Wo and an2 (map_weights, tinylm.c:377-381) and shift every
-     * later weight; shared experts are refused by the reference itself
-     * (check_supported, :1946-1953); routing to more than one expert is not
-     * the top-1 layer built here (moe_route, :814-827). */
-    if (c->qknorm != 0 || c->n_shared > 0 || (c->n_exp > 0 && c->topk > 1)) return TL_CKPT_EUNSUP;
+    /* Shared experts are refused by the reference itself (check_supported,
+     * :1946-1953); routing to more than one expert is not the top-1 layer
+     * built here (moe_route, :814-827).  QK-norm models (TLM6/7) decode; the
+     * training step refuses them, as the reference does (:2707-2713). */
+    if (c->n_shared > 0 || (c->n_exp > 0 && c->topk > 1)) return TL_CKPT_EUNSUP;
     m->V = c->V; m->D = c->D; m->L = c->L; m->H = c->H;
     m->KV = c->KV; m->F = c->F; m->T = c->T;
     m->n_mtp = c->n_mtp; m->n_exp = c->n_exp;
     m->win = c->win; m->full_every = c->full_every;
     m->rope_base = 10000.0f;
+    m->qknorm = c->qknorm;
     return TL_CKPT_OK;
 }
 
@@ -134,7 +134,7 @@ const char *tl_ckpt_error(int code)
     case TL_CKPT_EQUANT: return "quantized model file (TLQ1-TLQ4): not read by the fp32 path";
     case TL_CKPT_ESHAPE: return "header fields describe no model";
     case TL_CKPT_ETRUNC: return "file shorter than its header announces";
-    case TL_CKPT_EUNSUP: return "model uses QK-norm, shared experts or top-k > 1 routing, which this build does not run";
+    case TL_CKPT_EUNSUP: return "model uses shared experts or top-k > 1 routing, which this build does not run";
     default: return "unknown error";
     }
 }

@@ -59,8 +59,9 @@ size_t tl_ckpt_param_count(const TlCkpt *c);
 int tl_ckpt_read(const char *path, const TlCkpt *c, float *P, size_t n);
 
 /* The model fields the training step and the decoder take (rope_base 10000,
- * as cfg_from_hdr sets it).  TL_CKPT_OK, or TL_CKPT_EUNSUP (and *m zeroed)
- * for a model they would misread: QK-norm gains (qknorm != 0), shared
+ * as cfg_from_hdr sets it; qknorm as the header says: the decoder runs it,
+ * the training step refuses it as the reference does).  TL_CKPT_OK, or
+ * TL_CKPT_EUNSUP (and *m zeroed) for a model they would misread: shared
  * experts (n_shared > 0, which the reference refuses too) or MoE routing to
  * topk > 1 experts. */
 int tl_ckpt_model(const TlCkpt *c, TlModel *m);

@@ -8,8 +8,9 @@
 #include <string.h>
 
 #define TLD_MAXPOOL 16
+#define TLD_MAXM 8
 
-typedef struct { size_t emb, an1, wq, wk, wv, wo, an2, w1, w3, w2, nf, total; } DMap;
+typedef struct { size_t emb, an1, wq, wk, wv, wo, qn, kn, an2, wr, w1, w3, w2, nf, mtp0, total; } DMap;
 
 struct TlDecode {
     TlModel m;
@@ -20,7 +21,11 @@ struct TlDecode {
     float *Pt[TLD_MAXPOOL];      /* the decode layout: every linear weight transposed, same offsets */
     void **Kc, **Vc;
     float *rcos, *rsin, *x, *xn, *q, *k, *v, *ctx, *tmp, *g, *u, *act, *fn, *logits;
+    float *rt, *gt, *gu;         /* MoE: router logits [mmax][E], gates [mmax], expert rows [mmax][2F] */
+    float *ht, *hh, *hlog;       /* MTP draft of one row: fn Wk [D], fn + silu [D], logits [V] */
     int *pos, *tok, *state;
+    int *as;                     /* MoE: each row's expert [mmax] */
+    int *dtok;                   /* drafts and verified tokens [16] */
     void *xbuf;                  /* the persistent decode's exchange area */
     size_t xbytes;
     void *graph[TLD_MAXPOOL];
@@ -29,23 +34,30 @@ struct TlDecode {
     int unfused;                 /* 1: the glue as separate launches (tl_decode_set_fused) */
 };
 
-/* map_weights (tinylm.c:361-393), dense FFN, no QK-norm */
+/* map_weights (tinylm.c:361-393): the QK-norm gains qn, kn (hd each) between
+ * wo and an2 when qknorm; the router wr [D][E] and E expert slots of w1, w3,
+ * w2 when n_exp > 0; the n_mtp heads after nf */
 static void dmap(const TlDecode *d, int l, DMap *o)
 {
-    const size_t D = d->m.D, KD = d->KD, F = d->m.F;
-    const size_t per = D + D * D + 2 * D * KD + D * D + D + 3 * D * F;
+    const size_t D = d->m.D, KD = d->KD, F = d->m.F, hd = d->hd, E = d->m.n_exp > 0 ? d->m.n_exp : 1;
+    const size_t QK = d->m.qknorm ? 2 * hd : 0, R = d->m.n_exp > 0 ? D * d->m.n_exp : 0;
+    const size_t per = D + D * D + 2 * D * KD + D * D + QK + D + R + 3 * E * D * F;
     o->emb = 0;
     o->an1 = (size_t)d->m.V * D + (size_t)l * per;
     o->wq = o->an1 + D;
     o->wk = o->wq + D * D;
     o->wv = o->wk + D * KD;
     o->wo = o->wv + D * KD;
-    o->an2 = o->wo + D * D;
-    o->w1 = o->an2 + D;
-    o->w3 = o->w1 + D * F;
-    o->w2 = o->w3 + D * F;
+    o->qn = o->wo + D * D;
+    o->kn = o->qn + (d->m.qknorm ? hd : 0);
+    o->an2 = o->wo + D * D + QK;
+    o->wr = o->an2 + D;
+    o->w1 = o->wr + R;
+    o->w3 = o->w1 + E * D * F;
+    o->w2 = o->w3 + E * D * F;
     o->nf = (size_t)d->m.V * D + (size_t)d->m.L * per;
-    o->total = o->nf + D + (size_t)d->m.n_mtp * D * D;
+    o->mtp0 = o->nf + D;
+    o->total = o->mtp0 + (size_t)d->m.n_mtp * D * D;
 }
 
 static int dwin(const TlModel *m, int l)         /* cfg_lwin, tinylm.c:64-68 */
@@ -59,7 +71,8 @@ typedef struct { void **dst; size_t bytes; } DSlot;
 
 TlDecode *tl_decode_new(const TlModel *m, int W, int kv_f16, int exact_exp, int maxpos, int mmax, int pool)
 {
-    if (!m || m->n_exp != 0 || m->D <= 0 || m->H <= 0 || m->KV <= 0 || m->D % m->H || m->H % m->KV ||
+    if (!m || m->n_exp < 0 || m->n_exp == 1 || m->n_exp > 64 || m->n_mtp < 0 || m->D <= 0 || m->H <= 0 ||
+        m->KV <= 0 || m->D % m->H || m->H % m->KV ||
         m->D / m->H != 32 || m->D % 4 || m->F % 4 || m->V % 4 || m->L <= 0 || W <= 0 || W > 4096 ||
         maxpos <= 0 || mmax <= 0 || mmax > 8 || mmax > W || pool <= 0 || pool > TLD_MAXPOOL)
         return NULL;
@@ -85,6 +98,9 @@ TlDecode *tl_decode_new(const TlModel *m, int W, int kv_f16, int exact_exp, int 
         {(void **)&d->tmp, 4 * M * D}, {(void **)&d->g, 4 * M * F}, {(void **)&d->u, 4 * M * F},
         {(void **)&d->act, 4 * M * F}, {(void **)&d->fn, 4 * M * D}, {(void **)&d->logits, 4 * M * V},
         {(void **)&d->pos, 4 * M}, {(void **)&d->tok, 4 * M}, {(void **)&d->state, 16},
+        {(void **)&d->rt, 4 * M * (size_t)(m->n_exp > 0 ? m->n_exp : 1)}, {(void **)&d->gt, 4 * M},
+        {(void **)&d->gu, 8 * M * F}, {(void **)&d->as, 4 * M},
+        {(void **)&d->ht, 4 * D}, {(void **)&d->hh, 4 * D}, {(void **)&d->hlog, 4 * V}, {(void **)&d->dtok, 64},
     };
     const int nf = (int)(sizeof fixed / sizeof fixed[0]);
     size_t total = 0;
@@ -171,20 +187,47 @@ int tl_decode_upload(TlDecode *d, const float *P, void *st)
  * Pt[c]; the embedding and the norm gains are read from P[c]. */
 int tl_decode_pack(TlDecode *d, void *st)
 {
-    const int D = d->m.D, KD = d->KD, F = d->m.F;
-    for (int c = 0; c < d->pool; c++)
+    const int D = d->m.D, KD = d->KD, F = d->m.F, E = d->m.n_exp;
+    const size_t DF = (size_t)D * F;
+    for (int c = 0; c < d->pool; c++) {
+        float *Pt = d->Pt[c];
+        const float *P = d->P[c];
         for (int l = 0; l < d->m.L; l++) {
             DMap w;
             dmap(d, l, &w);
             const struct { size_t off; int rows, cols; } mats[] = {
-                {w.wq, D, D}, {w.wk, D, KD}, {w.wv, D, KD}, {w.wo, D, D}, {w.w1, D, F}, {w.w3, D, F}, {w.w2, F, D},
+                {w.wq, D, D}, {w.wk, D, KD}, {w.wv, D, KD}, {w.wo, D, D},
             };
             for (size_t i = 0; i < sizeof mats / sizeof mats[0]; i++) {
-                int rc = tlg_dev_transpose(d->Pt[c] + mats[i].off, d->P[c] + mats[i].off, mats[i].rows, mats[i].cols,
-                                           st);
+                int rc = tlg_dev_transpose(Pt + mats[i].off, P + mats[i].off, mats[i].rows, mats[i].cols, st);
                 if (rc) return rc;
             }
+            int rc = TLG_OK;
+            if (E == 0) {
+                rc = tlg_dev_transpose(Pt + w.w1, P + w.w1, D, F, st);
+                if (!rc) rc = tlg_dev_transpose(Pt + w.w3, P + w.w3, D, F, st);
+                if (!rc) rc = tlg_dev_transpose(Pt + w.w2, P + w.w2, F, D, st);
+                if (rc) return rc;
+                continue;
+            }
+            /* experts: W1_e^T and W3_e^T back to back at w1 + 2 e D F (one
+             * [2F][D] matrix per expert), W2_e^T [D][F] at w2 + e D F; the
+             * router as wr^T [E][D] */
+            rc = tlg_dev_transpose(Pt + w.wr, P + w.wr, D, E, st);
+            for (int e = 0; e < E && !rc; e++) {
+                rc = tlg_dev_transpose(Pt + w.w1 + 2 * e * DF, P + w.w1 + e * DF, D, F, st);
+                if (!rc) rc = tlg_dev_transpose(Pt + w.w1 + (2 * e + 1) * DF, P + w.w3 + e * DF, D, F, st);
+                if (!rc) rc = tlg_dev_transpose(Pt + w.w2 + e * DF, P + w.w2 + e * DF, F, D, st);
+            }
+            if (rc) return rc;
         }
+        DMap w0;
+        dmap(d, 0, &w0);
+        for (int k = 0; k < d->m.n_mtp; k++) {
+            int rc = tlg_dev_transpose(Pt + w0.mtp0 + (size_t)k * D * D, P + w0.mtp0 + (size_t)k * D * D, D, D, st);
+            if (rc) return rc;
+        }
+    }
     return TLG_OK;
 }
 
@@ -205,6 +248,7 @@ static TlgDecGemv DG(int op, int beta, float *C, int M, int K, int N, const floa
                      const float *gain, const float *A2)
 {
     TlgDecGemv c;
+    memset(&c, 0, sizeof c);
     c.op = op; c.beta = beta; c.C = C; c.M = M; c.K = K; c.N = N; c.A = A; c.B = Bw;
     c.pro = pro; c.gain = gain; c.A2 = A2;
     return c;
@@ -212,6 +256,59 @@ static TlgDecGemv DG(int op, int beta, float *C, int M, int K, int N, const floa
 
 #define DGEMV(st, ...) do { TlgDecGemv cs_[] = {__VA_ARGS__}; \
         CK(tlg_dev_dec_gemv(cs_, (int)(sizeof cs_ / sizeof cs_[0]), st)); } while (0)
+
+/* A MoE layer of forward_chunk (tinylm.c:3815-3818 with moe_forward_q8's fp32
+ * branch :3433-3458) on the decode layout: router logits of RMSNorm(x) (gain
+ * an2), each row's top-1 expert and gate on the device, then per row the
+ * chosen expert's [W1 | W3] (RMSNorm prologue) and W2 (SwiGLU prologue) with
+ * x += gate * y in the W2 store -- the residual copy out = fin and the
+ * scatter-add of moe_scatter_body in one step.  4 launches. */
+static int run_moe_fused(TlDecode *d, const DMap *w, int m, const float *P, const float *Pt, void *st)
+{
+    const int D = d->m.D, F = d->m.F, E = d->m.n_exp;
+    DGEMV(st, DG(1, 0, d->rt, m, E, D, d->x, Pt + w->wr, 1, P + w->an2, NULL));
+    CK(tlg_dev_dec_moe_route(d->rt, m, E, d->as, d->gt, st));
+    TlgDecGemv c13[TLD_MAXM], c2[TLD_MAXM];
+    for (int j = 0; j < m; j++) {
+        c13[j] = DG(1, 0, d->gu + (size_t)j * 2 * F, 1, 2 * F, D, d->x + (size_t)j * D, Pt + w->w1, 1, P + w->an2,
+                    NULL);
+        c13[j].bsel = d->as + j;
+        c13[j].bstride = 2LL * D * F;
+        c2[j] = DG(1, 1, d->x + (size_t)j * D, 1, D, F, d->gu + (size_t)j * 2 * F, Pt + w->w2, 2, NULL,
+                   d->gu + (size_t)j * 2 * F + F);
+        c2[j].bsel = d->as + j;
+        c2[j].bstride = (long long)D * F;
+        c2[j].cgate = d->gt + j;
+    }
+    CK(tlg_dev_dec_gemv(c13, m, st));
+    CK(tlg_dev_dec_gemv(c2, m, st));
+    return 0;
+}
+
+/* The same layer on the reference layout with the glue as separate launches,
+ * in the reference's order: RMSNorm, router mm, top-1, per row W1 and W3 of
+ * its expert, SwiGLU, per row W2 with out[n] = x[n] + gate[n] y. */
+static int run_moe_unfused(TlDecode *d, const DMap *w, int m, const float *P, void *st)
+{
+    const int D = d->m.D, F = d->m.F, E = d->m.n_exp;
+    CK(tlg_dev_rmsnorm_fwd(d->x, P + w->an2, d->xn, NULL, m, D, st));
+    DGEMV(st, DG(0, 0, d->rt, m, D, E, d->xn, P + w->wr, 0, NULL, NULL));
+    CK(tlg_dev_dec_moe_route(d->rt, m, E, d->as, d->gt, st));
+    TlgDecGemv c1[TLD_MAXM], c3[TLD_MAXM], c2[TLD_MAXM];
+    for (int j = 0; j < m; j++) {
+        c1[j] = DG(0, 0, d->g + (size_t)j * F, 1, D, F, d->xn + (size_t)j * D, P + w->w1, 0, NULL, NULL);
+        c3[j] = DG(0, 0, d->u + (size_t)j * F, 1, D, F, d->xn + (size_t)j * D, P + w->w3, 0, NULL, NULL);
+        c2[j] = DG(0, 1, d->x + (size_t)j * D, 1, F, D, d->act + (size_t)j * F, P + w->w2, 0, NULL, NULL);
+        c1[j].bsel = c3[j].bsel = c2[j].bsel = d->as + j;
+        c1[j].bstride = c3[j].bstride = c2[j].bstride = (long long)D * F;
+        c2[j].cgate = d->gt + j;
+    }
+    CK(tlg_dev_dec_gemv(c1, m, st));
+    CK(tlg_dev_dec_gemv(c3, m, st));
+    CK(tlg_dev_swiglu_fwd(d->act, d->g, d->u, (size_t)m * F, st));
+    CK(tlg_dev_dec_gemv(c2, m, st));
+    return 0;
+}
 
 /* The fused form: per layer 5 launches --
  *   [RMSNorm -> Q, K, V]  [RoPE, ring store, attention]  [O, x += ]
@@ -232,9 +329,14 @@ static int run_chunk_fused(TlDecode *d, int m, int use_state, int start, int cop
         DGEMV(st, DG(1, 0, d->q, m, D, D, d->x, Pt + w.wq, 1, P + w.an1, NULL),
               DG(1, 0, d->k, m, KD, D, d->x, Pt + w.wk, 1, P + w.an1, NULL),
               DG(1, 0, d->v, m, KD, D, d->x, Pt + w.wv, 1, P + w.an1, NULL));
+        if (md->qknorm) CK(tlg_dev_dec_qknorm(d->q, d->k, P + w.qn, P + w.kn, m, H, KV, hd, st));   /* :3752-3754 */
         CK(tlg_dev_dec_rope_attn(d->q, d->k, d->v, d->pos, d->rcos, d->rsin, d->maxpos, d->Kc[l], d->Vc[l], d->ctx, m,
                                  H, KV, hd, d->W, dwin(md, l), d->f16, d->exact, st));
         DGEMV(st, DG(1, 1, d->x, m, D, D, d->ctx, Pt + w.wo, 0, NULL, NULL));
+        if (md->n_exp > 0) {
+            CK(run_moe_fused(d, &w, m, P, Pt, st));
+            continue;
+        }
         DGEMV(st, DG(1, 0, d->g, m, F, D, d->x, Pt + w.w1, 1, P + w.an2, NULL),
               DG(1, 0, d->u, m, F, D, d->x, Pt + w.w3, 1, P + w.an2, NULL));
         DGEMV(st, DG(1, 1, d->x, m, D, F, d->g, Pt + w.w2, 2, NULL, d->u));
@@ -259,6 +361,7 @@ static int run_chunk(TlDecode *d, int m, int use_state, int start, int copy, voi
         CK(tlg_dev_rmsnorm_fwd(d->x, P + w.an1, d->xn, NULL, m, D, st));
         GROUP(st, MMc(d->q, d->xn, P + w.wq, m, D, D), MMc(d->k, d->xn, P + w.wk, m, D, KD),
               MMc(d->v, d->xn, P + w.wv, m, D, KD));
+        if (md->qknorm) CK(tlg_dev_dec_qknorm(d->q, d->k, P + w.qn, P + w.kn, m, H, KV, hd, st));
         CK(tlg_dev_rope(d->q, d->pos, 1, m, H, hd, d->rcos, d->rsin, d->maxpos, 0, st));
         CK(tlg_dev_rope(d->k, d->pos, 1, m, KV, hd, d->rcos, d->rsin, d->maxpos, 0, st));
         CK(tlg_dev_kv_store(d->k, d->v, d->pos, m, KD, d->W, d->f16, d->Kc[l], d->Vc[l], st));
@@ -266,6 +369,10 @@ static int run_chunk(TlDecode *d, int m, int use_state, int start, int copy, voi
                             d->exact, st));
         GROUP(st, MMc(d->tmp, d->ctx, P + w.wo, m, D, D));
         CK(tlg_dev_add(d->x, d->tmp, (size_t)m * D, st));
+        if (md->n_exp > 0) {
+            CK(run_moe_unfused(d, &w, m, P, st));
+            continue;
+        }
         CK(tlg_dev_rmsnorm_fwd(d->x, P + w.an2, d->xn, NULL, m, D, st));
         GROUP(st, MMc(d->g, d->xn, P + w.w1, m, D, F), MMc(d->u, d->xn, P + w.w3, m, D, F));
         CK(tlg_dev_swiglu_fwd(d->act, d->g, d->u, (size_t)m * F, st));
@@ -303,6 +410,63 @@ int tl_decode_prime(TlDecode *d, const int *prompt, int n, void *st)
     CK(tlg_memcpy_h2d(d->state, s, sizeof s, st));    /* state[3] (exchange sequence) is kept */
     CK(tlg_dev_dec_argmax(d->logits, d->m.V, m, d->state, d->tok, st));
     return tlg_stream_sync(st);
+}
+
+int tl_decode_mtp_draft(TlDecode *d, int row, int k, int *dtok_out, void *st)
+{
+    if (!d || !dtok_out || k < 0 || k >= d->m.n_mtp || row < 0 || row >= d->mmax) return TLG_EINVAL;
+    const int D = d->m.D, V = d->m.V;
+    const float *P = d->P[0], *Pt = d->Pt[0];
+    DMap w;
+    dmap(d, 0, &w);
+    const float *xr = d->x + (size_t)row * D;
+    /* ht = fn Wk (mm_dec(1, D, D), the head's W^T on the decode layout, with
+     * fn = RMSNorm(x, nf) as the prologue), hh = fn + silu(ht), logits_k =
+     * hh emb^T (mmbt_dec), argmax_v */
+    DGEMV(st, DG(1, 0, d->ht, 1, D, D, xr, Pt + w.mtp0 + (size_t)k * D * D, 1, P + w.nf, NULL));
+    CK(tlg_dev_dec_mtp_mix(d->hh, xr, P + w.nf, d->ht, D, st));
+    DGEMV(st, DG(1, 0, d->hlog, 1, V, D, d->hh, P + w.emb, 0, NULL, NULL));
+    return tlg_dev_argmax_rows(d->hlog, V, 1, dtok_out, st);
+}
+
+int tl_decode_generate_spec(TlDecode *d, const int *prompt, int np, int n, int *toks, int *chunks, void *st)
+{
+    const int K = d ? d->m.n_mtp : 0;
+    if (!d || !prompt || np <= 0 || n <= 0 || !toks || K < 1 || K + 1 > d->mmax || K + 1 > 16) return TLG_EINVAL;
+    /* prefill in chunks of mmax (positions 0..np-1), as tl_decode_prime */
+    int i = 0, m = 0;
+    while (i < np) {
+        m = np - i < d->mmax ? np - i : d->mmax;
+        CK(tl_decode_chunk(d, prompt + i, m, i, st));
+        i += m;
+    }
+    int pos = np, cur = m - 1, got = 0, nch = 0;
+    int draft[16], best[16];
+    while (got < n) {
+        /* x1 = argmax of the current row, the heads' drafts from its fn */
+        CK(tlg_dev_argmax_rows(d->logits + (size_t)cur * d->m.V, d->m.V, 1, d->dtok, st));
+        for (int k = 0; k < K; k++) CK(tl_decode_mtp_draft(d, cur, k, d->dtok + 1 + k, st));
+        CK(tlg_memcpy_d2h(draft, d->dtok, sizeof(int) * (size_t)(K + 1), st));
+        CK(tlg_stream_sync(st));
+        if (pos + K + 1 > d->maxpos) return TLG_EINVAL;
+        /* one chunk verifies the drafts: row r's argmax must equal draft r + 1 */
+        CK(tl_decode_chunk(d, draft, K + 1, pos, st));
+        nch++;
+        toks[got++] = draft[0];
+        CK(tlg_dev_argmax_rows(d->logits, d->m.V, K + 1, d->dtok, st));
+        CK(tlg_memcpy_d2h(best, d->dtok, sizeof(int) * (size_t)(K + 1), st));
+        CK(tlg_stream_sync(st));
+        int acc = 0;
+        for (int r = 0; r < K && got < n; r++) {
+            if (draft[r + 1] != best[r]) break;
+            toks[got++] = best[r];
+            acc++;
+        }
+        pos += acc + 1;
+        cur = acc;
+    }
+    if (chunks) *chunks = nch;
+    return 0;
 }
 
 int tl_decode_greedy_step(TlDecode *d, int copy, void *st)
@@ -381,7 +545,8 @@ static int persist_args(TlDecode *d, TlgDecPersist *pa, int *toks_out)
     const TlModel *md = &d->m;
     TlgDecPersist a;
     memset(&a, 0, sizeof a);
-    if (md->L > TLG_PD_MAXL) return TLG_EINVAL;
+    /* the persistent kernels run the dense model without QK-norm */
+    if (md->L > TLG_PD_MAXL || md->qknorm || md->n_exp > 0) return TLG_EINVAL;
     for (int c = 0; c < d->pool; c++) a.P[c] = d->P[c];
     a.pool = d->pool;
     a.copy0 = d->next_copy;

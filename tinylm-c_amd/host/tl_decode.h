@@ -17,7 +17,11 @@
  * Greedy decoding stays on the device: the argmax of the last logits row
  * becomes the next step's token and position in a device-side state, so one
  * captured step per weight copy replays token after token with no host
- * round trip.  Scope: dense FFN, head_dim 32, no QK-norm, W <= 4096.
+ * round trip.  Scope: head_dim 32, W <= 4096; dense or top-1 MoE layers
+ * (moe_forward_q8's fp32 branch, :3433-3458), with or without QK-norm; the
+ * MTP heads draft for self-speculative generation.  The persistent kernels
+ * (tl_decode_persist, tl_decode_chunks) run the dense model without QK-norm
+ * and return TLG_EINVAL for the others.
  */
 #ifndef TL_DECODE_H
 #define TL_DECODE_H
@@ -59,6 +63,19 @@ int tl_decode_chunk(TlDecode *d, const int *tok, int m, int start, void *stream)
 int tl_decode_prime(TlDecode *d, const int *prompt, int n, void *stream);
 /* One greedy token step from the device state (weights copy `copy`). */
 int tl_decode_greedy_step(TlDecode *d, int copy, void *stream);
+/* MTP head k's greedy draft (mtp_argmax, tinylm.c:3930-3936) from row `row`
+ * of the last chunk: fn = RMSNorm(x_row, nf), hh = fn + silu(fn Wk), the
+ * argmax_v of hh emb^T -> dtok_out[0] (device).  Weights copy 0. */
+int tl_decode_mtp_draft(TlDecode *d, int row, int k, int *dtok_out, void *stream);
+/* Greedy self-speculative generation with the MTP heads (run_generation's
+ * greedy path, tinylm.c:3985-4001): prefill the prompt (positions
+ * 0..np-1); then per round the current row's greedy token x1 and the n_mtp
+ * heads' drafts go through ONE chunk of n_mtp + 1 rows, and the drafts are
+ * kept while each equals the greedy token of the row before it.  Writes n
+ * tokens to toks (host) -- the same tokens greedy decoding gives -- and the
+ * number of verification chunks to *chunks.  Needs n_mtp >= 1 and n_mtp + 1
+ * <= mmax; weights copy 0. */
+int tl_decode_generate_spec(TlDecode *d, const int *prompt, int np, int n, int *toks, int *chunks, void *stream);
 /* Capture the greedy step once per weight copy; tl_decode_graph_step
  * replays the next copy's graph. */
 int tl_decode_graph_build(TlDecode *d, void *stream);

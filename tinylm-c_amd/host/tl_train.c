@@ -87,7 +87,7 @@ typedef struct { void **dst; size_t bytes; } Slot;
 TlTrain *tl_train_new(const TlModel *m, int B)
 {
     if (!m || B <= 0 || m->V <= 0 || m->D <= 0 || m->L <= 0 || m->H <= 0 || m->KV <= 0 || m->F <= 0 ||
-        m->T <= 0 || m->n_mtp < 0 || m->n_exp < 0 || m->n_exp == 1 || m->D % m->H || m->H % m->KV ||
+        m->T <= 0 || m->n_mtp < 0 || m->n_exp < 0 || m->n_exp == 1 || m->qknorm || m->D % m->H || m->H % m->KV ||
         m->D / m->H != 32 || m->D % 4 || m->F % 4 || m->V % 4)
         return NULL;
     TlTrain *t = calloc(1, sizeof *t);

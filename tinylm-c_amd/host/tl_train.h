@@ -24,6 +24,8 @@ typedef struct {
     int V, D, L, H, KV, F, T;
     int n_mtp, n_exp, win, full_every;
     float rope_base;
+    int qknorm;             /* QK-norm gains (tinylm.c Cfg :52): decode only, the
+                               reference refuses to train such models (:2707-2713) */
 } TlModel;
 
 typedef struct TlTrain TlTrain;

@@ -110,6 +110,10 @@ SIGNATURES = {
     "tlg_dev_dec_argmax": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "tlg_dev_dec_gemv": (_i, [_vp, _i, _vp]),
     "tlg_dev_transpose": (_i, [_vp, _vp, _i, _i, _vp]),
+    "tlg_dev_dec_qknorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "tlg_dev_dec_moe_route": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
+    "tlg_dev_dec_mtp_mix": (_i, [_vp, _vp, _vp, _vp, _i, _vp]),
+    "tlg_dev_argmax_rows": (_i, [_vp, _i, _i, _vp, _vp]),
     "tlg_dev_dec_rope_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i,
                                    _vp]),
     "tlg_dec_persist_xbytes": (_sz, [_i, _i, _i, _i]),
@@ -145,7 +149,8 @@ class TlgDecGemv(ctypes.Structure):
     """include/tldecode.h TlgDecGemv: one GEMV of a fused decode launch."""
     _fields_ = [("op", ctypes.c_int), ("beta", ctypes.c_int), ("C", _vp),
                 ("M", ctypes.c_int), ("K", ctypes.c_int), ("N", ctypes.c_int), ("A", _vp), ("B", _vp),
-                ("pro", ctypes.c_int), ("gain", _vp), ("A2", _vp)]
+                ("pro", ctypes.c_int), ("gain", _vp), ("A2", _vp), ("bsel", _vp), ("bstride", ctypes.c_longlong),
+                ("cgate", _vp)]
 
 
 class Lib:
@@ -296,9 +301,11 @@ class TlWeightMap(ctypes.Structure):
 
 
 class TlModel(ctypes.Structure):
-    """host/tl_train.h TlModel (tinylm.c Cfg fields of the training step)."""
+    """host/tl_train.h TlModel (tinylm.c Cfg fields of the training step and
+    the decoder)."""
     _fields_ = [(n, ctypes.c_int) for n in ("V", "D", "L", "H", "KV", "F", "T", "n_mtp", "n_exp", "win",
-                                            "full_every")] + [("rope_base", ctypes.c_float)]
+                                            "full_every")] + [("rope_base", ctypes.c_float),
+                                                              ("qknorm", ctypes.c_int)]
 
 
 class Train:
@@ -463,6 +470,22 @@ class Decode:
 
     def greedy_step(self, stream, copy=0):
         return self._ck(self.host.dll.tl_decode_greedy_step(self.h, copy, stream), "tl_decode_greedy_step")
+
+    def mtp_draft(self, row, k, dtok, stream):
+        """MTP head k's draft from row `row` of the last chunk into the device
+        int dtok (tl_decode_mtp_draft)."""
+        return self._ck(self.host.dll.tl_decode_mtp_draft(self.h, row, k, dtok, stream), "tl_decode_mtp_draft")
+
+    def generate_spec(self, prompt, n, stream):
+        """Greedy self-speculative generation (tl_decode_generate_spec):
+        (tokens, verification chunks)."""
+        import numpy as np
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(n, np.int32)
+        ch = ctypes.c_int(0)
+        self._ck(self.host.dll.tl_decode_generate_spec(self.h, p.ctypes.data, p.size, n, out.ctypes.data,
+                                                       ctypes.byref(ch), stream), "tl_decode_generate_spec")
+        return out, ch.value
 
     def graph_build(self, stream):
         return self._ck(self.host.dll.tl_decode_graph_build(self.h, stream), "tl_decode_graph_build")
@@ -683,6 +706,10 @@ class Host:
         d.tl_decode_persist_status.restype = _i
         d.tl_decode_set_fused.argtypes = [_vp, _i]
         d.tl_decode_set_fused.restype = _i
+        d.tl_decode_mtp_draft.argtypes = [_vp, _i, _i, _vp, _vp]
+        d.tl_decode_mtp_draft.restype = _i
+        d.tl_decode_generate_spec.argtypes = [_vp, _vp, _i, _i, _vp, _vp, _vp]
+        d.tl_decode_generate_spec.restype = _i
         self.dll = d
 
     def load_checkpoint(self, path):
