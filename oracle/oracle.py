@@ -506,8 +506,37 @@ class Decoder:
         d.orc_dec_chunk_fn.argtypes = [ctypes.c_void_p, _fp, _ip, _i, _i, _fp, _fp]
         d.orc_mtp_argmax.argtypes = [ctypes.POINTER(OrcModel), _fp, _fp, _i, _fp]
         d.orc_mtp_argmax.restype = _i
+        d.orc_dec_set_ring.argtypes = [ctypes.c_void_p, _i, ctypes.c_void_p, ctypes.c_void_p]
+        d.orc_dec_set_store.argtypes = [ctypes.c_void_p, _i]
+        d.orc_dec_ring.argtypes = [ctypes.c_void_p, _i, _i]
+        d.orc_dec_ring.restype = ctypes.c_void_p
         self.dll, self.m, self.P = d, m, np.ascontiguousarray(P, np.float32)
+        self.W, self.kvdt = W, kvdt
         self.h = d.orc_dec_new(ctypes.byref(m), W, kvdt, exact, maxpos)
+
+    def set_ring(self, l, K, V):
+        """Overwrite layer l's ring with K, V ([W][KD] of uint16 f16 bits for
+        an f16 ring, float32 for an f32 ring)."""
+        dt = np.uint16 if self.kvdt else np.float32
+        n = self.W * self.m.KV * (self.m.D // self.m.H)
+        K, V = (np.ascontiguousarray(a, dt).reshape(-1) for a in (K, V))
+        assert K.size == n and V.size == n
+        self.dll.orc_dec_set_ring(self.h, l, K.ctypes.data, V.ctypes.data)
+
+    def ring(self, l):
+        """Copies of layer l's K and V rings ([W][KD], as set_ring takes them)."""
+        dt = np.uint16 if self.kvdt else np.float32
+        KD = self.m.KV * (self.m.D // self.m.H)
+        out = []
+        for v in (0, 1):
+            buf = (ctypes.c_char * (self.W * KD * np.dtype(dt).itemsize)).from_address(
+                self.dll.orc_dec_ring(self.h, l, v))
+            out.append(np.frombuffer(buf, dt).reshape(self.W, KD).copy())
+        return out
+
+    def set_store(self, store):
+        """store False: chunks attend over the ring as set, storing nothing."""
+        self.dll.orc_dec_set_store(self.h, 1 if store else 0)
 
     def chunk(self, tok, start):
         tok = np.ascontiguousarray(tok, np.int32)

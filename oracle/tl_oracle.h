@@ -148,6 +148,14 @@ int     orc_mtp_argmax(const OrcModel *m, const float *P, const float *fn1, int 
  * [m][D]). */
 void    orc_dec_attn(OrcDec *d, int l, const float *q, const float *k, const float *v, int m, int start_pos,
                      float *ctx);
+/* Test hooks for checking a decoder whose f16 ring rounds K / V rows computed
+ * in another fp32 order: overwrite layer l's ring with given contents ([W][KD]
+ * in the ring's storage type), and switch the chunk's ring stores off (store
+ * 0) so attention reads the ring as given -- the state a chunk attends over
+ * after its hoisted stores, when the given ring was taken after that chunk. */
+void    orc_dec_set_ring(OrcDec *d, int l, const void *K, const void *V);
+const void *orc_dec_ring(const OrcDec *d, int l, int v);       /* layer l's K (v 0) or V ring */
+void    orc_dec_set_store(OrcDec *d, int store);
 float          orc_fast_expf(float x);         /* :3181-3191 */
 unsigned short orc_f2h(float f);               /* :3158-3168 (F16C path) */
 float          orc_h2f(unsigned short h);      /* :3147-3157 */

@@ -473,7 +473,7 @@ float orc_h2f(unsigned short h) { return _cvtsh_ss(h); }
 
 struct OrcDec {
     OrcModel m;
-    int W, kvdt, exact, maxpos;
+    int W, kvdt, exact, maxpos, nostore;
     void **K, **V;
     float *cs, *sn;
 };
@@ -494,6 +494,16 @@ OrcDec *orc_dec_new(const OrcModel *m, int W, int kvdt, int exact_exp, int maxpo
     orc_rope_table(d->cs, d->sn, maxpos, hd, m->rope_base);
     return d;
 }
+
+void orc_dec_set_ring(OrcDec *d, int l, const void *K, const void *V)
+{
+    const size_t bytes = (size_t)d->W * d->m.KV * (d->m.D / d->m.H) * (d->kvdt ? 2 : 4);
+    memcpy(d->K[l], K, bytes);
+    memcpy(d->V[l], V, bytes);
+}
+
+void orc_dec_set_store(OrcDec *d, int store) { d->nostore = !store; }
+const void *orc_dec_ring(const OrcDec *d, int l, int v) { return v ? d->V[l] : d->K[l]; }
 
 void orc_dec_free(OrcDec *d)
 {
@@ -540,7 +550,7 @@ void orc_dec_attn(OrcDec *d, int l, const float *q, const float *k, const float 
     const float scale = 1.0f / sqrtf((float)hd);
     float *pr = zalloc(W);
     int eff = layer_win(md, l), wlim = (eff > 0 && eff < W) ? eff : W;
-    for (int j = 0; j < m; j++) {               /* kv_store into the ring */
+    for (int j = 0; j < m && !d->nostore; j++) {   /* kv_store into the ring */
         const int slot = (start + j) % W;
         for (int i = 0; i < KD; i++) {
             if (d->kvdt) {

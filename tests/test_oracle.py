@@ -439,6 +439,31 @@ def test_spec_loop_is_exact_greedy(heads):
     assert chunks < n - 5                          # drafts were kept
 
 
+@pytest.mark.parametrize("kvdt", [0, 1])
+def test_decoder_over_a_given_ring(kvdt):
+    """The hooks the f16-ring GPU tests use: a decoder given another's rings
+    after each chunk, with its own ring stores off, computes that decoder's
+    logits bit for bit (the chunk attends over exactly the ring its stores
+    leave); with a perturbed ring the logits change."""
+    from oracle import Decoder
+    m, st, P = _forms_params(9)
+    a = Decoder(m, P, W=16, kvdt=kvdt, maxpos=64)
+    b = Decoder(m, P, W=16, kvdt=kvdt, maxpos=64)
+    b.set_store(False)
+    tok = np.random.default_rng(3).integers(0, m.V, 30).astype(np.int32)
+    pos = 0
+    for n in (5, 3, 8, 1, 1, 7, 4):        # wraps the 16-slot ring
+        want = a.chunk(tok[pos:pos + n], pos)
+        for l in range(m.L):
+            b.set_ring(l, *a.ring(l))
+        assert np.array_equal(b.chunk(tok[pos:pos + n], pos), want), pos
+        pos += n
+    K, V = a.ring(1)
+    K[pos % 16 - 1] = K[0]
+    b.set_ring(1, K, V)
+    assert not np.array_equal(b.chunk(tok[pos - 1:pos], pos - 1), a.chunk(tok[pos - 1:pos], pos - 1))
+
+
 def test_decoder_forms_follow_their_definitions():
     """The oracle decoder on a QK-norm + MoE + MTP model: the chunk's final
     rows fn give the chunk's logits through the tied head, chunks of 1 and of

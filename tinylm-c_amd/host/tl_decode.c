@@ -155,6 +155,10 @@ void tl_decode_free(TlDecode *d)
 size_t tl_decode_nparams(const TlDecode *d) { return d ? d->np : 0; }
 float *tl_decode_params(TlDecode *d, int copy) { return copy >= 0 && copy < d->pool ? d->P[copy] : NULL; }
 float *tl_decode_logits(TlDecode *d) { return d->logits; }
+void *tl_decode_ring(TlDecode *d, int l, int v)
+{
+    return d && l >= 0 && l < d->m.L ? (v ? d->Vc[l] : d->Kc[l]) : NULL;
+}
 
 int tl_decode_reset(TlDecode *d, void *st)
 {

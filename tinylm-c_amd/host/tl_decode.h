@@ -45,6 +45,9 @@ void      tl_decode_free(TlDecode *d);
 size_t    tl_decode_nparams(const TlDecode *d);
 float    *tl_decode_params(TlDecode *d, int copy);      /* device P (copy < pool) */
 float    *tl_decode_logits(TlDecode *d);                /* device [mmax][V]        */
+/* Device addresses of layer l's K and V rings ([W][KD], f16 bits or f32 as
+ * created; slot = position mod W); NULL for l out of range. */
+void     *tl_decode_ring(TlDecode *d, int l, int v);
 
 /* Copy host weights into every copy (and their decode layout, as
  * tl_decode_pack); clear the caches and the state. */

@@ -420,7 +420,7 @@ class Decode:
     def __init__(self, host, model, W, kv_f16, exact_exp, maxpos, mmax, pool):
         if isinstance(model, dict):
             model = TlModel(**{"rope_base": 10000.0, **model})
-        self.host, self.model = host, model
+        self.host, self.model, self.W, self.kv_f16 = host, model, W, kv_f16
         self.h = host.dll.tl_decode_new(ctypes.byref(model), W, kv_f16, exact_exp, maxpos, mmax, pool)
         if not self.h:
             raise TlgError("tl_decode_new failed: bad model shape or out of device memory")
@@ -460,6 +460,22 @@ class Decode:
         out = np.empty((m, self.model.V), np.float32)
         L = load()
         L.check(L.tlg_memcpy_d2h(out.ctypes.data, self.host.dll.tl_decode_logits(self.h), out.nbytes, stream), "d2h")
+        L.check(L.tlg_stream_sync(stream), "sync")
+        return out
+
+    def ring(self, l, stream):
+        """Layer l's K and V rings as host arrays [W][KD] (uint16 f16 bits or
+        float32, as the decoder stores them)."""
+        import numpy as np
+        L = load()
+        dt = np.uint16 if self.kv_f16 else np.float32
+        KD = self.model.KV * (self.model.D // self.model.H)
+        out = []
+        for v in (0, 1):
+            a = np.empty((self.W, KD), dt)
+            L.check(L.tlg_memcpy_d2h(a.ctypes.data, self.host.dll.tl_decode_ring(self.h, l, v), a.nbytes, stream),
+                    "d2h")
+            out.append(a)
         L.check(L.tlg_stream_sync(stream), "sync")
         return out
 
@@ -689,6 +705,8 @@ class Host:
             getattr(d, n).restype = _vp
         d.tl_decode_logits.argtypes = [_vp]
         d.tl_decode_logits.restype = _vp
+        d.tl_decode_ring.argtypes = [_vp, _i, _i]
+        d.tl_decode_ring.restype = _vp
         for n in ("tl_decode_upload", "tl_decode_state"):
             getattr(d, n).argtypes = [_vp, _vp, _vp]
             getattr(d, n).restype = _i
