@@ -208,6 +208,130 @@ def test_gemv_group(lib):
             assert lib.tlg_group_kernel().decode().startswith("k_gemv")
 
 
+def _one_alloc(parts):
+    """Matrices laid out back to back in one device allocation, as
+    map_weights lays out wq | wk | wv and w1 | w3 (tinylm.c:361-393)."""
+    flat = np.concatenate([p.ravel() for p in parts]).astype(np.float32)
+    d = dev(flat)
+    ptrs, off = [], 0
+    for p in parts:
+        ptrs.append(d.data_ptr() + 4 * off)
+        off += p.size
+    return d, ptrs
+
+
+ONE_MM = [(1, 384, (384, 96, 96)), (2, 96, (36, 100)), (3, 132, (1024, 1024)), (5, 1024, (384,)),
+          (8, 384, (384, 96, 96)), (8, 1024, (44,))]
+
+
+@pytest.mark.parametrize("tpb", ["128", "256"])
+@pytest.mark.parametrize("cl", ["8", "4", "2"])
+@pytest.mark.parametrize("M,K,segs", ONE_MM, ids=[f"{m}x{k}x{'-'.join(map(str, s))}" for m, k, s in ONE_MM])
+def test_gemv_one_matrix_mm(lib, M, K, segs, cl, tpb):
+    """Grouped M <= 8 mm calls over one input whose weight matrices follow
+    each other in memory run as one matrix (k_gemv_cols): 32-, 16- and 8-column
+    blocks, workgroups of 128 and 256 threads, ragged K and N, 1-3 segments,
+    every row bucket, against fp64 (shapes no instance covers take the
+    general kernel)."""
+    from oracle import Oracle
+    orc = Oracle()
+    t = _torch()
+    os.environ["TLG_GEMV_CL"] = cl
+    os.environ["TLG_GEMV_TPB"] = tpb
+    try:
+        X = seeded((M, K), 1.0, "omX")
+        Ws = [seeded((K, n), 0.02, f"omW{i}") for i, n in enumerate(segs)]
+        x = dev(X)
+        keep, ptrs = _one_alloc(Ws)
+        Ys = [t.full((M, n), float("nan"), device="cuda") for n in segs]
+        lib.group([dict(op="mm", C=y.data_ptr(), M=M, K=K, N=n, A=[x.data_ptr()], B=[b])
+                   for y, n, b in zip(Ys, segs, ptrs)], stream())
+        name = lib.tlg_group_kernel().decode()
+        rg = int(tpb) // int(cl)
+        need = -(-K // (4 * rg))
+        if need <= 4 or (need <= 8 and rg == 32):
+            assert name.startswith("k_gemv_cols") and f", {cl}, " in name and name.endswith(f", {tpb}>"), name
+        else:
+            assert name.startswith("k_gemv<"), name
+        for y, w in zip(Ys, Ws):
+            assert normwise_rel(y.cpu().numpy(), orc.mm_f64(X, w)) <= TOL, (M, K, segs)
+    finally:
+        del os.environ["TLG_GEMV_CL"]
+        del os.environ["TLG_GEMV_TPB"]
+
+
+ONE_BT = [(1, 384, (384, 96, 96)), (1, 1028, (13, 20, 7)), (2, 96, (2048,)), (3, 132, (1024, 1024)),
+          (4, 1024, (384,)), (7, 384, (100, 12)), (8, 1024, (384,)), (8, 260, (16, 8, 40))]
+
+
+@pytest.mark.parametrize("M,R,segs", ONE_BT, ids=[f"{m}x{r}x{'-'.join(map(str, s))}" for m, r, s in ONE_BT])
+def test_gemv_one_matrix_mm_bt(lib, M, R, segs):
+    """Grouped M <= 8 mm_bt calls over one input whose weights (decode
+    layout W^T [out][in]) follow each other in memory run as one matrix
+    (k_gemv_rows): 1-3 output segments of any row count, reductions shorter
+    and longer than one batch of loads, set and accumulate, against fp64."""
+    from oracle import Oracle
+    orc = Oracle()
+    t = _torch()
+    A = seeded((M, R), 1.0, "obA")
+    Wt = [seeded((n, R), 0.02, f"obW{i}") for i, n in enumerate(segs)]
+    a = dev(A)
+    keep, ptrs = _one_alloc(Wt)
+    for beta in (0, 1):
+        P = [seeded((M, n), 1.0, f"obP{i}") for i, n in enumerate(segs)]
+        Cs = [dev(p) if beta else t.full((M, n), float("nan"), device="cuda") for p, n in zip(P, segs)]
+        lib.group([dict(op="mm_bt", beta=beta, C=c.data_ptr(), M=M, K=n, N=R, A=[a.data_ptr()], B=[b])
+                   for c, n, b in zip(Cs, segs, ptrs)], stream())
+        assert lib.tlg_group_kernel().decode().startswith("k_gemv_rows")
+        for c, w, p in zip(Cs, Wt, P):
+            want = A.astype(np.float64) @ w.astype(np.float64).T
+            got = c.cpu().numpy()
+            if beta:
+                got = got - p
+            assert normwise_rel(got, want) <= TOL, (M, R, segs, beta)
+
+
+def test_gemv_one_matrix_decode_forms(lib):
+    """tlg_dev_dec_gemv on one matrix: q | k | v with the RMSNorm prologue at
+    M = 1, 3, 8, and a MoE expert row (weight slice chosen on the device,
+    gate-scaled, added into C) with the SwiGLU prologue, against fp64."""
+    import tlgemm
+    from oracle import StepFns
+    t = _torch()
+    st = StepFns("oracle")
+    r = np.random.default_rng(23)
+    D, KD, F, E = 384, 96, 1024, 4
+    C = tlgemm.TlgDecGemv
+    for M in (1, 3, 8):
+        x = r.standard_normal((M, D)).astype(np.float32)
+        gain = (1.0 + 0.1 * r.standard_normal(D)).astype(np.float32)
+        Wt = [(0.02 * r.standard_normal((n, D))).astype(np.float32) for n in (D, KD, KD)]
+        keep, ptrs = _one_alloc(Wt)
+        dx, dg = dev(x), dev(gain)
+        outs = [t.full((M, n), float("nan"), device="cuda") for n in (D, KD, KD)]
+        calls = (C * 3)(*[C(1, 0, o.data_ptr(), M, n, D, dx.data_ptr(), b, 1, dg.data_ptr(), None)
+                          for o, n, b in zip(outs, (D, KD, KD), ptrs)])
+        lib.check(lib.tlg_dev_dec_gemv(calls, 3, stream()), "dec_gemv qkv")
+        xn, _ = st.rmsnorm_fwd(x, gain)
+        for o, w in zip(outs, Wt):
+            assert normwise_rel(o.cpu().numpy(), xn.astype(np.float64) @ w.astype(np.float64).T) <= TOL, M
+    # MoE row: res += gate * (silu(g) * u) @ W2_e^T, expert e picked on the device
+    g = r.standard_normal((1, F)).astype(np.float32)
+    u = r.standard_normal((1, F)).astype(np.float32)
+    W2t = (0.02 * r.standard_normal((E, D, F))).astype(np.float32)
+    res = r.standard_normal((1, D)).astype(np.float32)
+    for e, gate in ((2, 0.625), (0, 1.5)):
+        dgg, du, dw, dres = dev(g), dev(u), dev(W2t), dev(res)
+        sel = t.tensor([e], dtype=t.int32, device="cuda")
+        gt = t.tensor([gate], dtype=t.float32, device="cuda")
+        one = (C * 1)(C(1, 1, dres.data_ptr(), 1, D, F, dgg.data_ptr(), dw.data_ptr(), 2, None, du.data_ptr(),
+                        sel.data_ptr(), D * F, gt.data_ptr()))
+        lib.check(lib.tlg_dev_dec_gemv(one, 1, stream()), "dec_gemv moe row")
+        act = g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64))) * u.astype(np.float64)
+        want = gate * (act @ W2t[e].astype(np.float64).T)
+        assert normwise_rel(dres.cpu().numpy() - res, want) <= TOL, e
+
+
 def test_gemv_split_repeats(lib):
     """The M <= 8 mm splits W's rows over several workgroups whose partial
     sums meet in a tagged workspace that is reused launch after launch: 120

@@ -1046,7 +1046,7 @@ int tlg_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len, int *s
         return TLG_OK;
     }
     if (tlg_gemv_fits(kind, Mo)) {
-        snprintf(buf, (size_t)len, "%s", tlg_gemv_kernel_name(Mo));
+        tlg_gemv_describe(kind, Mo, No, R, buf, len);
         if (splits) *splits = 1;
         return TLG_OK;
     }

@@ -618,6 +618,257 @@ __global__ __launch_bounds__(GV_T) void k_gemv(GvArgs g)
     gv_nn<MB, VEC, U, PRO>(g, P, P.S - 1, b, sh);
 }
 
+// ------------------------------------------------- mm_bt over one matrix --
+// The common decode launch: every problem of it is an mm_bt over the same
+// activation rows, and the problems' weights follow each other in memory (q |
+// k | v and w1 | w3 of the decode layout), so the launch is one matrix B
+// [nrows][K] whose row r gives output r - rs_s of segment s (rs_0 = 0, rs_1 =
+// r1, rs_2 = r2).  The arguments are plain scalars in the order the kernel
+// needs them, and the first 14 dwords (B, A, K, nrows, M | beta << 8, C0-C2,
+// r1 | r2 << 16: all that the 16 user SGPRs hold besides the argument-block
+// pointer) reach SGPRs before the first instruction (kernarg preload,
+// -amdgpu-kernarg-preload-count), so the weight loads issue at once and a
+// launch at M = 1 without a prologue or the MoE operands (SEL) reads nothing
+// from its argument block; a table of problems in
+// the argument block (k_gemv) puts a chain of dependent scalar loads in front
+// of them, ~1.2 us of a ~3.7 us launch (probe on the box: a 33-launch decode
+// GEMV set 124.7 us through k_gemv, 78.2 us through this form, 78.1 us for a
+// kernel that only streams the same bytes).
+//
+// Item b: rows 8 b + 2 w + lane / 32; the 32 lanes of a half-wave read the row
+// in steps of 128 floats, KU float4 per lane per batch, every load of a batch
+// first.  The activation rows come from global memory (hot in L2: every
+// workgroup reads them) into registers, so no LDS and no barrier; the RMS
+// prologue's sum of squares comes from the same registers (each half-wave
+// reads the whole row), reduced like the dot products.  Each output is a
+// fixed-order sum: lane partials (4 floats at a time, batch after batch),
+// then the DPP half-wave sum of gv_half_sum.
+struct GvRowsTail {               // what the kernel needs only after its weight loads are issued
+    int lda, ldc0, ldc1, ldc2;   // row strides (M > 1 only)
+    const float *gain, *A2;      // RMS gain [K]; SwiGLU second operand (layout of A)
+    const int *bsel;             // SEL: B is offset by bsel[0] * bstride
+    long long bstride;
+    const float *cgate;          // SEL: results scaled by cgate[0]
+};
+
+template <int MB, int KU, int PRO, int SEL>
+__global__ __launch_bounds__(GV_T) void k_gemv_rows(const float *B, const float *A, int K, int nrows, int mbeta,
+                                                    float *C0, float *C1, float *C2, int r12, GvRowsTail t)
+{
+    const int M = mbeta & 0xff, beta = mbeta >> 8, r1 = r12 & 0xffff, r2 = r12 >> 16;
+    const int lane = threadIdx.x & 63, l = lane & 31;
+    const int row = blockIdx.x * GV_NT_ROWS + (threadIdx.x >> 5);
+    const int rowc = min(row, nrows - 1);
+    const float *Bm = SEL ? B + (long long)*(const GAS int *)t.bsel * t.bstride : B;
+    const float *Brow = Bm + (size_t)rowc * K;
+    // activation row m (row 0 alone at MB = 1, so its stride is never read)
+    auto arow = [&](int m) { return MB == 1 ? (size_t)0 : (size_t)min(m, M - 1) * t.lda; };
+    constexpr int STEP = 128 * KU;
+    float acc[MB], ss[MB];
+#pragma unroll
+    for (int m = 0; m < MB; m++) acc[m] = ss[m] = 0.f;
+    auto load_w = [&](f32x4 (&wv)[KU], int k0) {
+#pragma unroll
+        for (int u = 0; u < KU; u++) wv[u] = gv_ld<4>(Brow + min(k0 + 4 * (32 * u + l), K - 4));
+    };
+    auto use = [&](const f32x4 (&wv)[KU], int k0) {
+        f32x4 av[MB][KU], gv[KU];
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int k = min(k0 + 4 * (32 * u + l), K - 4);
+#pragma unroll
+            for (int m = 0; m < MB; m++) av[m][u] = gv_ld<4>(A + arow(m) + k);
+            if (PRO == GV_PRO_RMS) gv[u] = gv_ld<4>(t.gain + k);
+            if (PRO == GV_PRO_SWIGLU) {
+#pragma unroll
+                for (int m = 0; m < MB; m++) {
+                    const f32x4 a2 = gv_ld<4>(t.A2 + arow(m) + k);
+#pragma unroll
+                    for (int v = 0; v < 4; v++) av[m][u][v] = gv_silu_mul(av[m][u][v], a2[v]);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const bool ok = k0 + 4 * (32 * u + l) < K;
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    float a = ok ? av[m][u][v] : 0.f;
+                    if (PRO == GV_PRO_RMS) {
+                        ss[m] = fmaf(a, a, ss[m]);
+                        a *= gv[u][v];
+                    }
+                    acc[m] = fmaf(a, wv[u][v], acc[m]);
+                }
+            }
+        }
+    };
+    f32x4 wv[KU];
+    load_w(wv, 0);
+    if (K <= STEP) {
+        use(wv, 0);
+    } else {
+        for (int k0 = 0; k0 < K; k0 += STEP) {          // the next batch in flight while this one is used
+            f32x4 nw[KU];
+            load_w(nw, min(k0 + STEP, K - 4));
+            use(wv, k0);
+#pragma unroll
+            for (int u = 0; u < KU; u++) wv[u] = nw[u];
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+        acc[m] = gv_half_sum(acc[m]);
+        if (PRO == GV_PRO_RMS) ss[m] = gv_half_sum(ss[m]);
+    }
+    if (l == 31 && row < nrows) {
+        const int s = (row >= r1) + (row >= r2);
+        float *C = s == 0 ? C0 : s == 1 ? C1 : C2;
+        const int col = row - (s == 0 ? 0 : s == 1 ? r1 : r2);
+        const float cg = SEL && t.cgate ? *(const GAS float *)t.cgate : 1.0f;
+#pragma unroll
+        for (int m = 0; m < MB; m++)
+            if (m < M) {
+                float v = acc[m];
+                if (PRO == GV_PRO_RMS) v *= 1.0f / sqrtf(ss[m] / (float)K + 1e-5f);
+                v *= cg;
+                float *out = C + col;
+                if (MB > 1) out += (size_t)m * (s == 0 ? t.ldc0 : s == 1 ? t.ldc1 : t.ldc2);
+                *out = beta ? *out + v : v;
+            }
+    }
+}
+
+// -------------------------------------------------- mm over one matrix --
+// The reference layout's decode launch (W [in][out], the drop-in's mm at
+// M <= 8): up to 3 problems over the same activation rows whose weights
+// follow each other in memory (wq | wk | wv, w1 | w3 of map_weights), with
+// the same scalar-argument design as k_gemv_rows (B, A, K, N0 | N1 << 16, N2,
+// M | beta << 8, C0-C2 preloaded).  Workgroup b owns CB = 4
+// CL columns of one segment over all K rows: CL lanes cover a row's 16 CL
+// bytes, the RG = 256 / CL row groups of the workgroup take rows 4 (g + RG
+// u4) + i (i < 4), so a lane reads 4 consecutive rows per step -- 4 weight
+// float4 and, at M = 1, one activation float4 straight from global memory.
+// At M > 1 the activation rows are staged in LDS ([k][MB]) behind one
+// barrier.  Partial sums: per lane over its rows in order, then the RG row
+// groups in LDS in a fixed order (NG groups of RG / NG, then the groups).
+#define GV_COLS_K 1024                 // rows per launch at most (one batch of loads)
+
+struct GvColsTail {
+    int lda, ldc0, ldc1, ldc2;       // row strides (M > 1 only)
+};
+
+template <int MB, int CL, int U4, int TPB>
+__global__ __launch_bounds__(TPB) void k_gemv_cols(const float *B, const float *A, int K, int N01, int N2, int mbeta,
+                                                   float *C0, float *C1, float *C2, GvColsTail t)
+{
+    const int N0 = N01 & 0xffff, N1 = N01 >> 16, M = mbeta & 0xff, beta = (mbeta >> 8) & 1, pair = mbeta >> 16;
+    constexpr int RG = TPB / CL, CB = 4 * CL, UF = 4 * U4;
+    __shared__ __attribute__((aligned(16))) float act[MB > 1 ? GV_COLS_K * MB : 4];
+    __shared__ __attribute__((aligned(16))) float red[RG][MB][CB];
+    const int tid = threadIdx.x, c = tid % CL, g = tid / CL;
+    // the workgroup's segment: blocks [0, nb0) of N0 columns, then N1, then N2
+    const int nb0 = (N0 + CB - 1) / CB, nb1 = (N1 + CB - 1) / CB;
+    int b = blockIdx.x, N = N0, seg = 0;
+    if (pair) {
+        // blocks 2p and 2p + 1 (the two halves of each 128-byte line) on
+        // workgroups 16 (p / 8) + p % 8 and that + 8: the same XCD
+        const int x = b & 7, i = b >> 3;
+        b = (((i >> 1) << 3) + x) * 2 + (i & 1);
+        if (b >= nb0 + nb1 + (N2 + CB - 1) / CB) return;
+    }
+    const float *Bs = B;
+    if (b >= nb0) {
+        b -= nb0; N = N1; seg = 1; Bs = B + (size_t)K * N0;
+        if (b >= nb1) { b -= nb1; N = N2; seg = 2; Bs += (size_t)K * N1; }
+    }
+    const int j = b * CB + 4 * c;
+    const float *Bc = Bs + min(j, N - 4);
+    f32x4 wv[UF];
+#pragma unroll
+    for (int u = 0; u < UF; u++) wv[u] = gv_ld<4>(Bc + (size_t)min(4 * (g + RG * (u >> 2)) + (u & 3), K - 1) * N);
+    __builtin_amdgcn_sched_barrier(0);                  // every weight load in flight before any is used
+    float acc[MB][4];
+#pragma unroll
+    for (int m = 0; m < MB; m++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[m][v] = 0.f;
+    if constexpr (MB == 1) {
+        f32x4 xv[U4];
+#pragma unroll
+        for (int u4 = 0; u4 < U4; u4++) xv[u4] = gv_ld<4>(A + min(4 * (g + RG * u4), K - 4));
+#pragma unroll
+        for (int u = 0; u < UF; u++) {
+            const float x = 4 * (g + RG * (u >> 2)) < K ? xv[u >> 2][u & 3] : 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[0][v] = fmaf(x, wv[u][v], acc[0][v]);
+        }
+    } else {
+        // activation rows [m][k] -> act[k][m]: thread t takes floats 4 t .. 4 t + 3 of every row
+        for (int k4 = tid; 4 * k4 < K; k4 += TPB) {
+            f32x4 xa[MB];
+#pragma unroll
+            for (int m = 0; m < MB; m++) xa[m] = gv_ld<4>(A + (size_t)min(m, M - 1) * t.lda + 4 * k4);
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int m4 = 0; m4 < MB; m4 += 4) {
+                    f32x4 y;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) y[i] = m4 + i < MB ? xa[min(m4 + i, MB - 1)][q] : 0.f;
+                    if (MB >= 4) *reinterpret_cast<f32x4 *>(&act[(4 * k4 + q) * MB + m4]) = y;
+                    else
+#pragma unroll
+                        for (int i = 0; i < MB; i++) act[(4 * k4 + q) * MB + i] = y[i];
+                }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < UF; u++) {
+            const int k = 4 * (g + RG * (u >> 2)) + (u & 3);
+            const bool ok = k < K;
+            const float *ak = &act[min(k, K - 1) * MB];
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+                const float x = ok ? ak[m] : 0.f;
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[m][v] = fmaf(x, wv[u][v], acc[m][v]);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MB; m++)
+        *reinterpret_cast<f32x4 *>(&red[g][m][4 * c]) = f32x4{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
+    __syncthreads();
+    // the RG row groups: NG groups of RG / NG consecutive ones per output,
+    // then the NG group sums in order
+    constexpr int NO = CB * MB, NG = TPB / NO >= 1 ? TPB / NO : 1;
+    float v = 0.f;
+    const int o = tid % NO, grp = tid / NO, m = o / CB, cc = o % CB;
+    if (grp < NG) {
+        v = red[grp * (RG / NG)][m][cc];
+#pragma unroll
+        for (int q = 1; q < RG / NG; q++) v += red[grp * (RG / NG) + q][m][cc];
+    }
+    __syncthreads();
+    if (grp < NG) (&red[0][0][0])[grp * NO + o] = v;
+    __syncthreads();
+    if (tid < NO) {
+        float r = (&red[0][0][0])[tid];
+#pragma unroll
+        for (int q = 1; q < NG; q++) r += (&red[0][0][0])[q * NO + tid];
+        const int jj = b * CB + cc;
+        if (m < M && jj < N) {
+            float *C = seg == 0 ? C0 : seg == 1 ? C1 : C2;
+            float *out = C + jj;
+            if (MB > 1) out += (size_t)m * (seg == 0 ? t.ldc0 : seg == 1 ? t.ldc1 : t.ldc2);
+            *out = beta ? *out + r : r;
+        }
+    }
+}
+
 // ---------------------------------------------------------------- host --
 bool tlg_gemv_fits(TlgKind kind, int Mo) { return kind != TLG_TN && Mo >= 1 && Mo <= 8; }
 
@@ -627,6 +878,10 @@ static u64 *g_part;                 // GV_RING regions of GV_REGION_WORDS
 static u32 *g_err;
 static unsigned g_ring;
 static char g_last_name[48] = "k_gemv";
+// A dry run (tlg_gemv_describe) picks the kernel without allocating or
+// launching and writes its name to g_name instead of g_last_name.
+static bool g_dry = false;
+static char *g_name = g_last_name;
 
 int tlg_gemv_init(void)
 {
@@ -688,12 +943,209 @@ static void launch_mb(const GvArgs &a, int grid, int vec, int U, int pro, hipStr
 
 static bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
+// k_gemv_rows: float4 batches per lane (KU) for a row of K floats at MB
+// activation rows, within a register budget of 16 activation float4 per lane.
+static int rows_ku(int K, int mb)
+{
+    const int cap = mb <= 2 ? 8 : mb == 4 ? 4 : 2;
+    const int need = (K + 127) / 128;
+    const int ku = need <= 1 ? 1 : need <= 2 ? 2 : need <= 3 ? 3 : need <= 4 ? 4 : 8;
+    return min(ku, cap);
+}
+
+struct GvRowsArgs {
+    const float *B, *A;
+    int K, nrows, mbeta;
+    float *C0, *C1, *C2;
+    int r12;
+    GvRowsTail t;
+};
+
+template <int MB, int KU, int SEL>
+static void launch_rows_sel(int pro, int grid, const GvRowsArgs &r, hipStream_t st)
+{
+#define GV_ROWS_ARGS r.B, r.A, r.K, r.nrows, r.mbeta, r.C0, r.C1, r.C2, r.r12, r.t
+    switch (pro) {
+    case GV_PRO_RMS:
+        hipLaunchKernelGGL((k_gemv_rows<MB, KU, GV_PRO_RMS, SEL>), dim3(grid), dim3(GV_T), 0, st, GV_ROWS_ARGS);
+        break;
+    case GV_PRO_SWIGLU:
+        hipLaunchKernelGGL((k_gemv_rows<MB, KU, GV_PRO_SWIGLU, SEL>), dim3(grid), dim3(GV_T), 0, st, GV_ROWS_ARGS);
+        break;
+    default:
+        hipLaunchKernelGGL((k_gemv_rows<MB, KU, GV_PRO_NONE, SEL>), dim3(grid), dim3(GV_T), 0, st, GV_ROWS_ARGS);
+        break;
+    }
+#undef GV_ROWS_ARGS
+}
+template <int MB, int KU>
+static void launch_rows_ku(int sel, int pro, int grid, const GvRowsArgs &r, hipStream_t st)
+{
+    if constexpr (MB == 1) {
+        if (sel) { launch_rows_sel<MB, KU, 1>(pro, grid, r, st); return; }
+    }
+    launch_rows_sel<MB, KU, 0>(pro, grid, r, st);
+}
+template <int MB>
+static void launch_rows_mb(int ku, int sel, int pro, int grid, const GvRowsArgs &r, hipStream_t st)
+{
+    switch (ku) {
+    case 1: launch_rows_ku<MB, 1>(sel, pro, grid, r, st); break;
+    case 2: launch_rows_ku<MB, 2>(sel, pro, grid, r, st); break;
+    case 3:
+        if constexpr (MB <= 4) launch_rows_ku<MB, 3>(sel, pro, grid, r, st);
+        break;
+    case 4:
+        if constexpr (MB <= 4) launch_rows_ku<MB, 4>(sel, pro, grid, r, st);
+        break;
+    default:
+        if constexpr (MB <= 2) launch_rows_ku<MB, 8>(sel, pro, grid, r, st);
+        break;
+    }
+}
+
+// The launch as one matrix (k_gemv_rows) when every problem is an mm_bt over
+// the same activation rows (same prologue operands, beta, weight selection
+// and gate), 16-byte aligned rows of a multiple of 4 floats, and each
+// problem's weight rows directly follow the previous problem's.  Weight
+// selection and gate (the MoE decode rows) only at M = 1.  Returns 1 when
+// launched, 0 when the launch needs the general kernel.
+static int launch_rows(const GvArgs &a, int pro, hipStream_t st)
+{
+    if (a.nprob < 1 || a.nprob > 3 || env_int("TLG_GEMV_ROWS", 1) == 0) return 0;
+    const GvProb &P0 = a.p[0];
+    const GvSeg &g0 = P0.seg[0];
+    const int K = g0.R;
+    if (P0.kind != TLG_NT || P0.nseg != 1 || K % 4 || g0.lda % 4 || g0.ldb != K || !al16(g0.A) || !al16(g0.B))
+        return 0;
+    if (pro == GV_PRO_RMS && !al16(P0.gain)) return 0;
+    if (pro == GV_PRO_SWIGLU && !al16(P0.A2)) return 0;
+    const int sel = P0.bsel || P0.cgate;
+    if (sel && (P0.M != 1 || !P0.bsel || P0.bstride % 4)) return 0;
+    const float *next = g0.B + (size_t)P0.No * K;
+    for (int i = 1; i < a.nprob; i++) {
+        const GvProb &P = a.p[i];
+        const GvSeg &g = P.seg[0];
+        if (P.kind != TLG_NT || P.nseg != 1 || g.R != K || g.lda != g0.lda || g.ldb != K || g.A != g0.A ||
+            g.B != next || P.M != P0.M || P.beta != P0.beta || P.gain != P0.gain || P.A2 != P0.A2 ||
+            P.bsel != P0.bsel || P.bstride != P0.bstride || P.cgate != P0.cgate)
+            return 0;
+        next += (size_t)P.No * K;
+    }
+    GvRowsArgs r;
+    memset(&r, 0, sizeof r);
+    float *C[3] = {P0.C, P0.C, P0.C};
+    int ldc[3] = {P0.ldc, P0.ldc, P0.ldc}, rs[3] = {0, 0, 0}, n = 0;
+    for (int i = 0; i < a.nprob; i++) {
+        rs[i] = n;
+        C[i] = a.p[i].C;
+        ldc[i] = a.p[i].ldc;
+        n += a.p[i].No;
+    }
+    if (n >= 0xffff) return 0;                       // r1, r2 in 16 bits each
+    r.B = g0.B; r.A = g0.A; r.K = K; r.nrows = n; r.mbeta = P0.M | (P0.beta ? 1 : 0) << 8;
+    r.C0 = C[0]; r.C1 = C[1]; r.C2 = C[2];
+    // segments past the last start at nrows, so no row selects them
+    r.r12 = (a.nprob > 1 ? rs[1] : n) | (a.nprob > 2 ? rs[2] : n) << 16;
+    r.t.lda = g0.lda;
+    r.t.ldc0 = ldc[0]; r.t.ldc1 = ldc[1]; r.t.ldc2 = ldc[2];
+    r.t.gain = P0.gain; r.t.A2 = P0.A2; r.t.bsel = P0.bsel; r.t.bstride = P0.bstride; r.t.cgate = P0.cgate;
+    const int mb = rows_bucket(P0.M), ku = rows_ku(K, mb);
+    const int grid = (n + GV_NT_ROWS - 1) / GV_NT_ROWS;
+    if (!g_dry) switch (mb) {
+    case 1: launch_rows_mb<1>(ku, sel, pro, grid, r, st); break;
+    case 2: launch_rows_mb<2>(ku, sel, pro, grid, r, st); break;
+    case 4: launch_rows_mb<4>(ku, sel, pro, grid, r, st); break;
+    default: launch_rows_mb<8>(ku, sel, pro, grid, r, st); break;
+    }
+    snprintf(g_name, sizeof g_last_name, "k_gemv_rows<%d, %d, %d, %d>", mb, ku, pro, sel);
+    return 1;
+}
+
+template <int MB, int CL, int TPB>
+static void launch_cols_cl(int u4, int grid, int pair, const float *B, const float *A, int K, const int *N, int M,
+                           int beta, float *const *C, const GvColsTail &t, hipStream_t st)
+{
+#define GV_COLS(U4)                                                                                      \
+    hipLaunchKernelGGL((k_gemv_cols<MB, CL, U4, TPB>), dim3(grid), dim3(TPB), 0, st, B, A, K,              \
+                       N[0] | N[1] << 16, N[2], M | (beta ? 1 : 0) << 8 | pair << 16, C[0], C[1], C[2], t)
+    switch (u4) {
+    case 1: GV_COLS(1); break;
+    case 2: GV_COLS(2); break;
+    case 3: GV_COLS(3); break;
+    case 4: GV_COLS(4); break;
+    default:
+        if constexpr (TPB / CL == 32) GV_COLS(8);
+        break;
+    }
+#undef GV_COLS
+}
+
+// The launch as one matrix in the reference layout (k_gemv_cols): every
+// problem an mm over the same activation rows with no prologue, weight
+// selection or gate, dense rows (ldb = N) of a multiple of 4 floats, K <=
+// GV_COLS_K, and each problem's weight matrix directly after the previous
+// one.  Returns 1 when launched, 0 when the launch needs the general kernel.
+static int launch_cols(const GvArgs &a, int pro, hipStream_t st)
+{
+    if (a.nprob < 1 || a.nprob > 3 || pro != GV_PRO_NONE || env_int("TLG_GEMV_ROWS", 1) == 0) return 0;
+    const GvProb &P0 = a.p[0];
+    const GvSeg &g0 = P0.seg[0];
+    const int K = g0.R;
+    if (K % 4 || K > GV_COLS_K || g0.lda % 4 || !al16(g0.A) || !al16(g0.B)) return 0;
+    const float *next = g0.B;
+    int N[3] = {0, 0, 0}, ldc[3] = {0, 0, 0}, nb = 0;
+    float *C[3] = {P0.C, P0.C, P0.C};
+    const int cle = env_int("TLG_GEMV_CL", 4), CL = cle == 8 ? 8 : cle == 2 ? 2 : 4, CB = 4 * CL;
+    for (int i = 0; i < a.nprob; i++) {
+        const GvProb &P = a.p[i];
+        const GvSeg &g = P.seg[0];
+        if (P.kind != TLG_NN || P.nseg != 1 || g.R != K || g.A != g0.A || g.lda != g0.lda || g.B != next ||
+            g.ldb != P.No || P.No % 4 || P.M != P0.M || P.beta != P0.beta || P.bsel || P.cgate)
+            return 0;
+        next += (size_t)K * P.No;
+        N[i] = P.No; C[i] = P.C; ldc[i] = P.ldc;
+        nb += (P.No + CB - 1) / CB;
+    }
+    if (N[0] >= 0x10000 || N[1] >= 0x8000) return 0;    // N0, N1 in 16 bits each
+    GvColsTail t = {g0.lda, ldc[0], ldc[1], ldc[2]};
+    const int tpb = env_int("TLG_GEMV_TPB", 256) == 128 ? 128 : 256;
+    const int RG = tpb / CL, need = (K + 4 * RG - 1) / (4 * RG);
+    if (need > 4 && (need > 8 || RG != 32)) return 0;    // instances: U4 <= 4, and 8 at 32 row groups
+    const int u4 = need <= 1 ? 1 : need <= 2 ? 2 : need <= 3 ? 3 : need <= 4 ? 4 : 8;
+    const int mb = rows_bucket(P0.M);
+    const int pair = CL < 8 && env_int("TLG_GEMV_PAIR", 1) ? 1 : 0;
+    const int grid = pair ? (nb + 15) / 16 * 16 : nb;
+#define GV_COLS_MB(MB)                                                                                     \
+    (tpb == 128 ? (CL == 8   ? launch_cols_cl<MB, 8, 128>(u4, grid, pair, g0.B, g0.A, K, N, P0.M, P0.beta, C, t, st)  \
+                   : CL == 4 ? launch_cols_cl<MB, 4, 128>(u4, grid, pair, g0.B, g0.A, K, N, P0.M, P0.beta, C, t, st)  \
+                             : launch_cols_cl<MB, 2, 128>(u4, grid, pair, g0.B, g0.A, K, N, P0.M, P0.beta, C, t, st)) \
+                : (CL == 8   ? launch_cols_cl<MB, 8, 256>(u4, grid, pair, g0.B, g0.A, K, N, P0.M, P0.beta, C, t, st)  \
+                   : CL == 4 ? launch_cols_cl<MB, 4, 256>(u4, grid, pair, g0.B, g0.A, K, N, P0.M, P0.beta, C, t, st)  \
+                             : launch_cols_cl<MB, 2, 256>(u4, grid, pair, g0.B, g0.A, K, N, P0.M, P0.beta, C, t, st)))
+    if (!g_dry) switch (mb) {
+    case 1: GV_COLS_MB(1); break;
+    case 2: GV_COLS_MB(2); break;
+    case 4: GV_COLS_MB(4); break;
+    default: GV_COLS_MB(8); break;
+    }
+#undef GV_COLS_MB
+    snprintf(g_name, sizeof g_last_name, "k_gemv_cols<%d, %d, %d, %d>", mb, CL, u4, tpb);
+    return 1;
+}
+
 // Decompose the problems, pick the instance and launch.  pro is the launch's
 // prologue (every problem shares it).
 static int launch(GvArgs &a, int pro, hipStream_t st)
 {
-    int rc = tlg_gemv_init();
-    if (rc) return rc;
+    if (!g_dry) {
+        int rc = tlg_gemv_init();
+        if (rc) return rc;
+    }
+    if (launch_rows(a, pro, st) || launch_cols(a, pro, st)) {
+        if (!g_dry) TLG_HIP(hipGetLastError());
+        return TLG_OK;
+    }
     int mb = 1, vec = 4;
     for (int i = 0; i < a.nprob; i++) {
         GvProb &P = a.p[i];
@@ -784,8 +1236,10 @@ static int launch(GvArgs &a, int pro, hipStream_t st)
         grid += P.direct + P.reducers;
     }
     if (grid == 0) return TLG_OK;
-    a.part = g_part + (size_t)(g_ring++ % GV_RING) * GV_REGION_WORDS;
-    a.err = g_err;
+    if (!g_dry) {
+        a.part = g_part + (size_t)(g_ring++ % GV_RING) * GV_REGION_WORDS;
+        a.err = g_err;
+    }
     // batch depth of the split mm and mm_bt paths (full-K items use their own)
     int U = 4;
     if (vec == 4) {
@@ -796,6 +1250,8 @@ static int launch(GvArgs &a, int pro, hipStream_t st)
         const int u_full = maxr_full > 512 ? 2 : maxr_full ? 1 : 0;     // full-K batches: min(U, 2)
         U = max(1, max(u_full, max(u_nn, u_nt)));
     }
+    snprintf(g_name, sizeof g_last_name, "k_gemv<%d, %d, %d, %d>", mb, vec, vec == 1 ? 4 : U, vec == 1 ? 0 : pro);
+    if (g_dry) return TLG_OK;
     switch (mb) {
     case 1: launch_mb<1>(a, grid, vec, U, pro, st); break;
     case 2: launch_mb<2>(a, grid, vec, U, pro, st); break;
@@ -803,8 +1259,6 @@ static int launch(GvArgs &a, int pro, hipStream_t st)
     default: launch_mb<8>(a, grid, vec, U, pro, st); break;
     }
     TLG_HIP(hipGetLastError());
-    snprintf(g_last_name, sizeof g_last_name, "k_gemv<%d, %d, %d, %d>", mb, vec, vec == 1 ? 4 : U,
-             vec == 1 ? 0 : pro);
     return TLG_OK;
 }
 
@@ -813,6 +1267,28 @@ const char *tlg_gemv_kernel_name(int M)
 {
     (void)M;
     return g_last_name;
+}
+
+// The instance a single device call (the drop-in's mm / mm_bt at M <= 8,
+// operands as tlg_gemv_launch receives them from the C ABI: 16-byte aligned,
+// dense rows) would launch, without launching it.
+void tlg_gemv_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len)
+{
+    GvArgs a;
+    memset(&a, 0, sizeof a);
+    GvProb &P = a.p[0];
+    float *const any = (float *)(uintptr_t)256;       // aligned stand-in, never dereferenced
+    P.C = any; P.kind = kind; P.M = Mo; P.No = No; P.ldc = No; P.beta = kind == TLG_NT; P.nseg = 1;
+    P.seg[0] = GvSeg{any, any, R, R, kind == TLG_NN ? No : R};
+    a.nprob = 1;
+    char name[48];
+    g_dry = true;
+    g_name = name;
+    snprintf(name, sizeof name, "k_gemv");
+    (void)launch(a, GV_PRO_NONE, 0);
+    g_dry = false;
+    g_name = g_last_name;
+    snprintf(buf, (size_t)len, "%s", name);
 }
 
 int tlg_gemv_launch(TlgKind kind, const float *A, const float *B, float *C, int Mo, int No, int R, int lda,

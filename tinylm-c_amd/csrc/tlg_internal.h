@@ -88,6 +88,7 @@ int tlg_gemv_launch(TlgKind kind, const float *A, const float *B, float *C, int 
                     int ldb, int ldc, int beta, hipStream_t st);
 int tlg_gemv_group_launch(const TlgGemmCall *calls, int n, hipStream_t st);
 const char *tlg_gemv_kernel_name(int M);
+void tlg_gemv_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len);
 int tlg_gemv_init(void);
 void tlg_gemv_release(void);
 
