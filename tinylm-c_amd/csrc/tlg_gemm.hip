@@ -536,11 +536,14 @@ __global__ void k_split_reduce(const float *__restrict__ ws, float *__restrict__
 enum { PK_NN = 0, PK_NT = 1, PK_TN = 2, PK_RED = 3, PK_ZERO = 4, PK_COLSUM = 5 };
 #define TLG_ZERO_CHUNK 4096          // floats a clear's work item sets to 0
 #define TLG_MAXSEG 3
-#define TLG_MAXPROB 16
+#define TLG_MAXPROB 16                // group_item pins 16 counts
 #define TLG_RED_CHUNK 256
 #define TLG_ERED_CHUNK 2048            // elements per work item of an expert reduction
 
 struct Seg { const float *A, *B; int R, lda, ldb; };
+// The fields every work item reads lie in the first 160 bytes (C to items,
+// then the segments), so a workgroup fetches them in a few scalar loads
+// issued together.
 struct Prob {
     float *C;
     const float *ws;      // PK_RED: partials; split GEMM: its partial slice base
@@ -548,6 +551,7 @@ struct Prob {
     int kind, nseg;
     int tiles_n, tiles, splits, rps;
     int items;            // work items: tiles * splits, or reduction chunks
+    Seg seg[TLG_MAXSEG];
     // Expert-batched problem (nexp > 0): the rows of a top-1 MoE layer are
     // grouped by expert, expert e owning rows [eoff[e], eoff[e+1]) of every
     // row operand.  NN / NT: the output rows are expert rows and the weight
@@ -571,11 +575,15 @@ struct Prob {
     float *X1, *X2;
     const float *fin, *gate;
     int epi;
-    Seg seg[TLG_MAXSEG];
 };
+// items / devcount: filled from p[] by group_seal() before every launch (0
+// past nprob), so the search for a workgroup's problem reads one contiguous
+// block of counts instead of one problem struct after another.
 struct GroupArgs {
     int nprob;
     int rows1;            // expert launches: > 0 = one expert owning rows [0, rows1)
+    int items[TLG_MAXPROB];
+    unsigned devcount;    // bit p: problem p's count is known only on the device (experts)
     Prob p[TLG_MAXPROB];
 };
 
@@ -783,13 +791,24 @@ __device__ __forceinline__ void group_tile(float *smem, const Prob &P, int local
 // XCD gets the same mix of long and short items), problem by problem in
 // list order (the host lists problems longest item first).  Workgroups past
 // their XCD's share exit at once.
+static_assert(TLG_MAXPROB == 16, "group_item pins exactly 16 item counts");
 __device__ __forceinline__ int group_item(const GroupArgs &g, int b, int *local, const int *eo)
 {
     const int x = b & 7;
     int slot = b >> 3;
-    for (int p = 0; p < g.nprob; p++) {
+    int cnt[TLG_MAXPROB];
+#pragma unroll
+    for (int p = 0; p < TLG_MAXPROB; p++) cnt[p] = g.items[p];
+    const unsigned dev = g.devcount;
+    // every count in flight at once: one round trip, then scalar arithmetic
+    // (counts past nprob are 0, so nprob itself is not needed)
+    asm volatile("" ::"s"(dev), "s"(cnt[0]), "s"(cnt[1]), "s"(cnt[2]), "s"(cnt[3]), "s"(cnt[4]), "s"(cnt[5]),
+                 "s"(cnt[6]), "s"(cnt[7]), "s"(cnt[8]), "s"(cnt[9]), "s"(cnt[10]), "s"(cnt[11]), "s"(cnt[12]),
+                 "s"(cnt[13]), "s"(cnt[14]), "s"(cnt[15]));
+#pragma unroll
+    for (int p = 0; p < TLG_MAXPROB; p++) {
         // expert-batched GEMMs: the real item count, known only on the device
-        const int n = (g.p[p].nexp && g.p[p].kind != PK_RED) ? expert_items(g.p[p], eo) : g.p[p].items;
+        const int n = (dev >> p & 1u) ? expert_items(g.p[p], eo) : cnt[p];
         const int lo = (x * n) >> 3, hi = ((x + 1) * n) >> 3;
         if (slot < hi - lo) { *local = lo + slot; return p; }
         slot -= hi - lo;
@@ -832,6 +851,11 @@ __device__ __forceinline__ void group_body(const GroupArgs &g, float *smem, cons
     const int p = group_item(g, blockIdx.x, &local, eo);
     if (p < 0) return;
     const Prob &P = g.p[p];
+    // The fields a tile reads first, fetched together: one round trip to the
+    // argument block before the tile's first loads, not one per field.
+    asm volatile("" ::"s"(P.kind), "s"(P.nseg), "s"(P.Mo), "s"(P.No), "s"(P.tiles), "s"(P.tiles_n),
+                 "s"(P.splits), "s"(P.rps), "s"(P.seg[0].A), "s"(P.seg[0].B), "s"(P.seg[0].R), "s"(P.seg[0].lda),
+                 "s"(P.seg[0].ldb));
     switch (P.kind) {
     case PK_NN: group_tile<T, RC, OC, EXP>(smem, P, local, eo); break;
     case PK_NT: group_tile<T, RC, RC, EXP>(smem, P, local, eo); break;
@@ -1255,10 +1279,23 @@ static void group_env(void)
     if (e && atoi(e) >= 64) g_rtarget = atoi(e);
 }
 
+// The item-count header of a launch's arguments (GroupArgs.items, devcount).
+static const GroupArgs &group_seal(const GroupArgs &a)
+{
+    static GroupArgs b;
+    b = a;
+    b.devcount = 0;
+    for (int p = 0; p < TLG_MAXPROB; p++) {
+        b.items[p] = p < a.nprob ? a.p[p].items : 0;
+        if (p < a.nprob && a.p[p].nexp && a.p[p].kind != PK_RED) b.devcount |= 1u << p;
+    }
+    return b;
+}
+
 template <class T>
 static void lgroup(const GroupArgs &a, int grid, hipStream_t st)
 {
-    hipLaunchKernelGGL((k_group<T>), dim3(grid), dim3(T::THREADS), 0, st, a);
+    hipLaunchKernelGGL((k_group<T>), dim3(grid), dim3(T::THREADS), 0, st, group_seal(a));
 }
 
 static void launch_group(int ci, const GroupArgs &a, int grid, hipStream_t st)
@@ -1687,7 +1724,8 @@ static int flush_foreign(hipStream_t st)
 static int ecarry_flush(hipStream_t st)
 {
     if (!g_ecarry.nprob) return TLG_OK;
-    hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(g_ecarry)), dim3(T3::THREADS), 0, st, g_ecarry);
+    hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(g_ecarry)), dim3(T3::THREADS), 0, st,
+                       group_seal(g_ecarry));
     g_ecarry.nprob = 0;
     g_ecarry_used = 0;
     TLG_HIP(hipGetLastError());
@@ -1892,9 +1930,9 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     static_assert(sizeof(GroupArgs) <= 4096, "kernel arguments");
     const dim3 eg(group_grid(a) + 8 * n);
     switch (ci) {
-    case 3: hipLaunchKernelGGL((k_expert_group<T3>), eg, dim3(T3::THREADS), 0, st, a); break;
-    case 15: hipLaunchKernelGGL((k_expert_group<T15>), eg, dim3(T15::THREADS), 0, st, a); break;
-    default: hipLaunchKernelGGL((k_expert_group<T14>), eg, dim3(T14::THREADS), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((k_expert_group<T3>), eg, dim3(T3::THREADS), 0, st, group_seal(a)); break;
+    case 15: hipLaunchKernelGGL((k_expert_group<T15>), eg, dim3(T15::THREADS), 0, st, group_seal(a)); break;
+    default: hipLaunchKernelGGL((k_expert_group<T14>), eg, dim3(T14::THREADS), 0, st, group_seal(a)); break;
     }
     TLG_HIP(hipGetLastError());
     if (red.nprob && carry == TLG_ECARRY_OUT && !dense && g_npending == 0) {
@@ -1903,7 +1941,7 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
         g_ecarry_eoff = eoff;
         g_ecarry_st = st;
     } else if (red.nprob) {
-        hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(red)), dim3(T3::THREADS), 0, st, red);
+        hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(red)), dim3(T3::THREADS), 0, st, group_seal(red));
         TLG_HIP(hipGetLastError());
     }
     return TLG_OK;
