@@ -126,7 +126,8 @@ int tlg_dev_dec_argmax(const float *logits, int V, int m, int *state, int *tok, 
  *
  * The step is forward_chunk at m = 1 on a dense model with head_dim 32
  * (D = 32 H <= 384), F <= 1024 and F % 32 == 0, V % 8 == 0 and V <= 4096,
- * W <= 256, L <= 32: per layer RMSNorm -> Q, K, V -> RoPE -> ring store ->
+ * W <= 256, L <= 32, with or without QK-norm (qknorm): per layer RMSNorm ->
+ * Q, K, V -> [QK-norm ->] RoPE -> ring store ->
  * attention over the window -> O + residual -> RMSNorm -> W1, W3 -> SwiGLU ->
  * W2 + residual; the final norm and the tied head; argmax_v (the first
  * maximum).  Token i of the launch decodes at position state[0] + i with
@@ -162,6 +163,10 @@ typedef struct {
     int *tok;                /* 1 int                                        */
     int *toks_out;           /* [n] or NULL                                  */
     void *xbuf;
+    int qknorm;              /* 1: QK-norm model (qknorm_apply, tinylm.c:597-605,
+                                on q and k before RoPE, :3752-3754; the gains qn,
+                                kn of 32 floats each lie after wo, as map_weights
+                                places them); tlg_dev_dec_persist only       */
 } TlgDecPersist;
 
 size_t tlg_dec_persist_xbytes(int V, int D, int L, int F);
@@ -177,7 +182,8 @@ int tlg_dev_dec_persist(const TlgDecPersist *a, int n, void *stream);
  * (if not NULL) = argmax_v of chunk i's row j.  Ring rows are stored as the
  * reference's hoisted kv_store leaves them (:3775-3780): a window key whose
  * slot a later row of the chunk overwrote reads that row's key.  xbuf, the
- * state and the abort behaviour are shared with tlg_dev_dec_persist. */
+ * state and the abort behaviour are shared with tlg_dev_dec_persist.  QK-norm
+ * models are refused (qknorm must be 0). */
 int tlg_dev_dec_chunks(const TlgDecPersist *a, int m, const int *toks, int n, void *stream);
 /* Synchronize `stream`; TLG_OK, or TLG_EHIP if a launch on xbuf aborted. */
 int tlg_dec_persist_status(void *xbuf, void *stream);

@@ -373,21 +373,24 @@ def _forced_steps(kw, P, W, prompt, steps, exact=0, pool=2):
     return toks, worst
 
 
-@pytest.mark.parametrize("shape,kvdt,exact", [("small", 0, 0), ("small", 1, 0), ("small", 0, 1), ("m8", 1, 0),
-                                              ("m8", 0, 0)])
-def test_persist_matches_oracle(lib, shape, kvdt, exact):
-    """Greedy decoding in one persistent launch (tlg_dev_dec_persist).  f32
-    ring: the token stream equals the oracle's and the last step's logits
-    match the oracle's on the same tokens.  f16 ring: launches of one step,
-    each checked against the oracle over the device's ring, give the tokens
-    of the one launch.  The state advances."""
+@pytest.mark.parametrize("shape,kvdt,exact,qk", [("small", 0, 0, 0), ("small", 1, 0, 0), ("small", 0, 1, 0),
+                                                 ("m8", 1, 0, 0), ("m8", 0, 0, 0), ("small", 0, 0, 1),
+                                                 ("small", 1, 0, 1), ("m8", 0, 0, 1), ("m8", 1, 0, 1)])
+def test_persist_matches_oracle(lib, shape, kvdt, exact, qk):
+    """Greedy decoding in one persistent launch (tlg_dev_dec_persist), dense
+    and QK-norm models.  f32 ring: the token stream equals the oracle's and
+    the last step's logits match the oracle's on the same tokens.  f16 ring:
+    launches of one step, each checked against the oracle over the device's
+    ring, give the tokens of the one launch.  The state advances."""
     kw = SMALL if shape == "small" else M8
+    if qk:
+        kw = dict(kw, qknorm=1)
     W = 32 if shape == "small" else 256
     steps = 40 if shape == "small" else 24
     m, P = params(kw, 7)
     prompt = np.random.default_rng(8).integers(0, m.V, 13).astype(np.int32)
     StepFns("oracle").dll.orc_set_threads(16)
-    print("persist", shape, kvdt, exact, flush=True)
+    print("persist", shape, kvdt, exact, qk, flush=True)
     _, got, row, st = _persist_run(kw, P, W, kvdt, prompt, [steps], exact=exact)
     assert st[0] == len(prompt) + steps and st[1] == 1
     assert got[steps] == int(np.argmax(row)) == st[2]
@@ -772,13 +775,22 @@ def test_generate_spec_matches_oracle(lib, shape, heads):
 
 
 def test_persist_rejects_forms(lib):
-    """The persistent kernels run the dense model without QK-norm: a model
-    with either form is refused before anything is launched."""
+    """The persistent kernels run the dense model, the single-token one also
+    with QK-norm: the chunk kernel refuses a QK-norm model and both refuse a
+    MoE model, before anything is launched."""
     import tlgemm
-    for kw in (dict(SMALL, qknorm=1), dict(SMALL, n_exp=4)):
+    t = _t()
+    for kw, single in ((dict(SMALL, qknorm=1), True), (dict(SMALL, n_exp=4), False)):
         m, P = params(kw, 27)
         dec = tlgemm.host().decode(kw, 32, kv_f16=0, exact_exp=0, maxpos=128, mmax=8)
         dec.upload(P, stream())
         dec.prime(np.arange(5, dtype=np.int32), stream())
-        with pytest.raises(tlgemm.TlgError):
+        if single:
             dec.persist(4, stream())
+            dec.persist_status(stream())
+        else:
+            with pytest.raises(tlgemm.TlgError):
+                dec.persist(4, stream())
+        toks = t.zeros(4, dtype=t.int32, device="cuda")
+        with pytest.raises(tlgemm.TlgError):
+            dec.persist_chunks(2, toks.data_ptr(), 2, stream())

@@ -374,11 +374,11 @@ template <int PAIRS> __device__ __forceinline__ float pd_colsum(f32x4 acc, f32x4
 // Every kind writes the whole panel, so it stays in registers.
 __device__ __forceinline__ void pd_load_item(f32x4 (&wb)[PD_WB], float &gn, const float *__restrict__ P, int g,
                                              int NPL, int NA, int NO, int NS, size_t lay0, size_t per, int D, int KD,
-                                             int F, int grp)
+                                             int F, int grp, int qk)
 {
     const int l = g / NPL, k = g % NPL;
     const size_t an1 = lay0 + (size_t)l * per, wq = an1 + D, wk = wq + (size_t)D * D, wv = wk + (size_t)D * KD,
-                 wo = wv + (size_t)D * KD, an2 = wo + (size_t)D * D, w1 = an2 + D, w3 = w1 + (size_t)D * F,
+                 wo = wv + (size_t)D * KD, an2 = wo + (size_t)D * D + qk, w1 = an2 + D, w3 = w1 + (size_t)D * F,
                  w2 = w3 + (size_t)D * F;
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     const int tid = threadIdx.x, c4 = tid & 7;
@@ -559,7 +559,8 @@ __device__ __forceinline__ bool pd_argmax(PdShared &sh, const u64 *cand, int NHI
 template <int F16>
 __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_WB], float rc, float rs,
                                              u64 (&kw)[PD_MAXR], u64 (&vw)[PD_MAXR], const TlgDecPersist &a,
-                                             int l, int h, int pos, int D, int KD, int grp, u64 *ctxout, u32 tag)
+                                             int l, int h, int pos, int D, int KD, int grp, const float *qkn,
+                                             u64 *ctxout, u32 tag)
 {
     typedef PdRing<F16> R;
     constexpr int NW = R::NW, KPR = PD_T / NW, MAXR = PD_MAXW / KPR;
@@ -585,7 +586,14 @@ __device__ __forceinline__ void pd_attention(PdShared &sh, const f32x4 (&wb)[PD_
     // column from the lane i ^ 16); new k and v in the ring's format
     if (tid < 192) {                     // wave m reads panel m, pairs (i, i + 16) in quads
         const int m = tid >> 6, i = pd_half_col<1>(tid);
-        const float c = pd_colsum_half(sh.red[m], i) * sn;
+        float c = pd_colsum_half(sh.red[m], i) * sn;
+        if (qkn && m < 2) {
+            // QK-norm (qknorm_apply, tinylm.c:597-605, before RoPE :3752-3754) of
+            // q (wave 0) and the new k (wave 1): v s gain, s = 1 / sqrt(sum v^2 /
+            // hd + 1e-5); each column sits in two lanes, one of them counted
+            const float ss = pd_wave_sum((tid & 1) ? 0.f : c * c);
+            c = c * (1.0f / sqrtf(ss / 32.0f + 1e-5f)) * gp(qkn)[32 * m + i];
+        }
         const float o = pd_pair_other(c);
         const bool inpos = pos >= 0 && pos < a.maxpos;
         const float rot = inpos ? (i < 16 ? c * rc - o * rs : c * rc + o * rs) : NAN;
@@ -744,7 +752,8 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
     const int D = a.D, F = a.F, V = a.V, L = a.L, H = a.H, KD = a.KV * 32, grp = a.H / a.KV;
     const int NA = H, NO = D / 32, NS = F / 16, NPL = NA + NO + NS + D / 32, NLI = L * NPL, NHI = V / 8;
     const u32 NPH = 4u * (u32)L + 1u;
-    const size_t per = (size_t)D + (size_t)D * D + 2 * (size_t)D * KD + (size_t)D * D + D + 3 * (size_t)D * F;
+    const int qk = a.qknorm ? 64 : 0;                 // the QK-norm gains qn, kn (hd = 32 each) after wo
+    const size_t per = (size_t)D + (size_t)D * D + 2 * (size_t)D * KD + (size_t)D * D + qk + D + 3 * (size_t)D * F;
     const size_t lay0 = (size_t)V * D;
     u64 *xb = reinterpret_cast<u64 *>(a.xbuf);
     const PdLayout lay = pd_layout(V, D, L, F);
@@ -769,7 +778,7 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
     f32x4 hb[2];
     u64 kw[PD_MAXR], vw[PD_MAXR];
     if (b < NLI)
-        pd_load_item(wb, gn, pd_uni(sh.P[a.copy0 % a.pool]), b, NPL, NA, NO, NS, lay0, per, D, KD, F, grp);
+        pd_load_item(wb, gn, pd_uni(sh.P[a.copy0 % a.pool]), b, NPL, NA, NO, NS, lay0, per, D, KD, F, grp, qk);
     // this workgroup's first attention item in layer l (query head), or -1
     auto attn_head = [&](int l) -> int {
         const int s = l * NPL, g = s + ((b - s) % NB + NB) % NB;
@@ -818,7 +827,7 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
     do {                                                                                                     \
         const int ng_ = (g) + NB < NLI ? (g) + NB : b, nt_ = min((g) + NB < NLI ? t : t + 1, n - 1);          \
         pd_load_item(wb, gn, pd_uni(sh.P[(a.copy0 + nt_) % a.pool]), ng_, NPL, NA, NO, NS, lay0, per, D, KD, F, \
-                     grp);                                                                                   \
+                     grp, qk);                                                                               \
     } while (0)
 
             for (int g = PD_FIRST(0); g < g0 + NA; g += NB) {
@@ -830,6 +839,8 @@ __global__ __launch_bounds__(PD_T, 1) void k_dec_persist(TlgDecPersist a, int n)
                     __syncthreads();
                 }
                 pd_attention<F16>(sh, wb, rc, rs, kw, vw, a, l, g - g0, pos, D, KD, grp,
+                                  qk ? P + lay0 + (size_t)l * per + D + 2 * (size_t)D * D + 2 * (size_t)D * KD
+                                     : nullptr,
                                   ctx + (size_t)(g - g0) * 32, tl);
                 PD_NEXT(g);
             }
@@ -1545,10 +1556,11 @@ extern "C" int tlg_dev_dec_persist(const TlgDecPersist *a, int n, void *stream)
     if (!a || n <= 0 || a->pool <= 0 || a->pool > 16 || a->copy0 < 0 || a->H <= 0 || a->KV <= 0 ||
         a->H % a->KV || a->D != 32 * a->H || a->D > PD_MAXD || a->F <= 0 || a->F % 32 || a->F > PD_MAXF ||
         a->V <= 0 || a->V % 8 || a->V / 8 > PD_MAXHI || a->L <= 0 || a->L > TLG_PD_MAXL || a->W <= 0 ||
-        a->W > PD_MAXW || a->maxpos <= 0 || !a->cs || !a->sn || !a->logits || !a->state || !a->tok || !a->xbuf)
+        a->W > PD_MAXW || a->maxpos <= 0 || !a->cs || !a->sn || !a->logits || !a->state || !a->tok || !a->xbuf ||
+        (a->qknorm != 0 && a->qknorm != 1))
         return tlg_fail(TLG_EINVAL,
                         "dec_persist: n=%d V=%d D=%d L=%d H=%d KV=%d F=%d W=%d pool=%d (head_dim 32, D <= %d, "
-                        "F %% 32 == 0 and F <= %d, V %% 8 == 0 and V <= %d, W <= %d, L <= %d)",
+                        "F %% 32 == 0 and F <= %d, V %% 8 == 0 and V <= %d, W <= %d, L <= %d, qknorm 0 or 1)",
                         n, a ? a->V : 0, a ? a->D : 0, a ? a->L : 0, a ? a->H : 0, a ? a->KV : 0, a ? a->F : 0,
                         a ? a->W : 0, a ? a->pool : 0, PD_MAXD, PD_MAXF, 8 * PD_MAXHI, PD_MAXW, TLG_PD_MAXL);
     for (int c = 0; c < a->pool; c++)
@@ -1596,6 +1608,7 @@ extern "C" int tlg_dev_dec_chunks(const TlgDecPersist *a, int m, const int *toks
         if (!a->Kc[l] || !a->Vc[l] || ((uintptr_t)a->Kc[l] & 63u) || ((uintptr_t)a->Vc[l] & 63u))
             return tlg_fail(TLG_EINVAL, "dec_chunks: cache of layer %d", l);
     if ((uintptr_t)a->xbuf & 15u) return tlg_fail(TLG_EINVAL, "dec_chunks: xbuf alignment");
+    if (a->qknorm) return tlg_fail(TLG_EINVAL, "dec_chunks: QK-norm models run on the graph step (tl_decode_chunk)");
     if (!g_pd_cus) {
         int cus = 0;
         TLG_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, g_tlg.device));

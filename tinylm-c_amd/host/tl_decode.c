@@ -549,8 +549,9 @@ static int persist_args(TlDecode *d, TlgDecPersist *pa, int *toks_out)
     const TlModel *md = &d->m;
     TlgDecPersist a;
     memset(&a, 0, sizeof a);
-    /* the persistent kernels run the dense model without QK-norm */
-    if (md->L > TLG_PD_MAXL || md->qknorm || md->n_exp > 0) return TLG_EINVAL;
+    /* the persistent kernels run the dense model (the single-token one also
+     * with QK-norm; tlg_dev_dec_chunks refuses it) */
+    if (md->L > TLG_PD_MAXL || md->n_exp > 0) return TLG_EINVAL;
     for (int c = 0; c < d->pool; c++) a.P[c] = d->P[c];
     a.pool = d->pool;
     a.copy0 = d->next_copy;
@@ -560,6 +561,7 @@ static int persist_args(TlDecode *d, TlgDecPersist *pa, int *toks_out)
     a.cs = d->rcos; a.sn = d->rsin;
     for (int l = 0; l < md->L; l++) { a.Kc[l] = d->Kc[l]; a.Vc[l] = d->Vc[l]; }
     a.logits = d->logits; a.state = d->state; a.tok = d->tok; a.toks_out = toks_out; a.xbuf = d->xbuf;
+    a.qknorm = md->qknorm ? 1 : 0;
     *pa = a;
     return 0;
 }
