@@ -203,10 +203,12 @@ int  tlg_dev_moe_grouped_bwd(const float *fnorm, const float *dout, float *d_fno
  * it computes anyway; the backward reads them instead of rebuilding the index
  * and recomputing W1 | W3 and W2 (3 of its launches), with the same results
  * bit for bit.  The backward overwrites g and u (they become dg and du), so
- * one kept state serves one backward, and its last summation of the router
- * gradient is deferred like a split GEMM's reduction: gwr is complete after
- * the next grouped or expert launch on the stream, or tlg_dev_gemm_flush
- * (when gwr is 16-byte aligned; otherwise at return).  For training steps
+ * one kept state serves one backward, and its last summations (the router
+ * gradient's column sum and the expert W1 / W3 gradients' slice sums) are
+ * deferred like a split GEMM's reduction: gwr, gw1 and gw3 are complete after
+ * the next grouped or expert launch on the stream, or tlg_dev_gemm_flush,
+ * which runs them in one launch (gwr at return when it is not 16-byte
+ * aligned).  For training steps
  * that can hold N (3F + D) floats per MoE layer until the backward. */
 size_t tlg_moe_keep_bytes(int N, int D, int F, int E);   /* 0 for a bad shape */
 int  tlg_dev_moe_grouped_fwd_keep(const float *fnorm, const float *fin, float *out, int N, int D, int F, int E,

@@ -1464,10 +1464,15 @@ static int group_flush_dense(hipStream_t st)
 
 static int ecarry_flush(hipStream_t st);
 
+static int ecarry_flush_with_pending(hipStream_t st, bool *done);
+
 int tlg_group_flush_launch(hipStream_t st)
 {
     int rc = flush_foreign(st);
-    if (!rc) rc = ecarry_flush(st);
+    if (rc) return rc;
+    bool done = false;
+    if ((rc = ecarry_flush_with_pending(st, &done)) || done) return rc;
+    rc = ecarry_flush(st);
     return rc ? rc : group_flush_dense(st);
 }
 
@@ -1732,6 +1737,25 @@ static int ecarry_flush(hipStream_t st)
     return TLG_OK;
 }
 
+// Held expert reductions and queued dense ones (column sums, split
+// reductions) on one stream: one launch for both, the held expert
+// reductions first (the expert kernel stages p[0]'s row offsets), then the
+// queued ones, which it runs as the dense kernel does.  *done = false when
+// there are not both kinds (or too many problems for one launch).
+static int ecarry_flush_with_pending(hipStream_t st, bool *done)
+{
+    *done = false;
+    if (!g_ecarry.nprob || !g_npending || g_ecarry.nprob + g_npending > TLG_MAXPROB) return TLG_OK;
+    GroupArgs a = g_ecarry;
+    add_reductions(a);
+    hipLaunchKernelGGL((k_expert_group<T3>), dim3(group_grid(a)), dim3(T3::THREADS), 0, st, group_seal(a));
+    g_ecarry.nprob = 0;
+    g_ecarry_used = 0;
+    TLG_HIP(hipGetLastError());
+    *done = true;
+    return TLG_OK;
+}
+
 // Shutdown: the queued reductions (and an expert launch's held carry) run
 // on `st` while the workspace they read still exists; then the queue is
 // empty and the workspace halves start over, so nothing queued before a
@@ -1762,7 +1786,7 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     if ((rc = flush_foreign(st))) return rc;
     // held slice reductions join this launch only if it asks for them and
     // shares their row offsets
-    const bool cin = carry == TLG_ECARRY_IN && g_ecarry.nprob && g_ecarry_eoff == eoff && !dense;
+    const bool cin = (carry & TLG_ECARRY_IN) && g_ecarry.nprob && g_ecarry_eoff == eoff && !dense;
     if (!cin && (rc = ecarry_flush(st))) return rc;
     // Pending split reductions of grouped launches ride along when this
     // launch writes no partial slots (they reuse the whole workspace) and
@@ -1935,7 +1959,7 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     default: hipLaunchKernelGGL((k_expert_group<T14>), eg, dim3(T14::THREADS), 0, st, group_seal(a)); break;
     }
     TLG_HIP(hipGetLastError());
-    if (red.nprob && carry == TLG_ECARRY_OUT && !dense && g_npending == 0) {
+    if (red.nprob && (carry & TLG_ECARRY_OUT) && !dense && g_npending == 0) {
         g_ecarry = red;                  // the next expert launch runs them
         g_ecarry_used = used;
         g_ecarry_eoff = eoff;

@@ -78,7 +78,9 @@ struct TlgExpertCall {
 // carry: TLG_ECARRY_OUT holds this launch's expert slice reductions for the
 // next expert launch over the same eoff, which takes them with TLG_ECARRY_IN
 // (no other launch may come between; any other workspace user runs them).
-enum { TLG_ECARRY_NONE = 0, TLG_ECARRY_OUT = 1, TLG_ECARRY_IN = 2 };
+// (flags: TLG_ECARRY_INOUT takes the held ones and holds its own; held
+// reductions left over run in the next tlg_group_flush_launch)
+enum { TLG_ECARRY_NONE = 0, TLG_ECARRY_OUT = 1, TLG_ECARRY_IN = 2, TLG_ECARRY_INOUT = 3 };
 int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E, int rows, hipStream_t st,
                       int carry = TLG_ECARRY_NONE);
 

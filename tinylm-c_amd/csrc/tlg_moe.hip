@@ -568,7 +568,9 @@ static int moe_bwd(const float *fnorm, const float *dout, float *d_fnorm, const 
     c[2].op = 1; c[2].beta = 0; c[2].C = s.y; c[2].K = D; c[2].N = F; c[2].nseg = 2;
     c[2].A[0] = s.g; c[2].B[0] = w1; c[2].A[1] = s.u; c[2].B[1] = w3; c[2].Nseg[1] = F;
     c[2].es = (long long)D * F;
-    if ((rc = tlg_expert_launch(c, 3, s.eoff, E, N, st, TLG_ECARRY_IN))) return rc;
+    // (its own slice reductions are held too: they run with dWr's column sum,
+    // in one launch at the flush)
+    if ((rc = tlg_expert_launch(c, 3, s.eoff, E, N, st, TLG_ECARRY_INOUT))) return rc;
     // router: softmax backward, d_fnorm, dWr  (:932-945).  dWr's per-block
     // partials are summed by a column-sum item: at once for the reference-
     // shaped entry, in the next grouped launch for the kept-state one (as a
