@@ -208,6 +208,44 @@ def test_gemv_group(lib):
             assert lib.tlg_group_kernel().decode().startswith("k_gemv")
 
 
+# Sched<> tile variants (configurations 24-33: a stage's fragment reads issued
+# before its MFMAs, out-of-range chunks loaded from a zero buffer) beside the
+# shapes they reorder
+SCHED_CFGS = [3, 24, 25, 14, 26, 20, 27, 22, 28, 13, 29, 15, 30, 0, 31, 1, 32, 8, 33]
+
+
+@pytest.mark.parametrize("gcfg", SCHED_CFGS)
+def test_group_ragged_tiles(lib, gcfg):
+    """One grouped launch of the three primitives on ragged shapes (777 rows,
+    a 260-step reduction, 132 columns: partial row tiles, column tiles and
+    stages) on each tile configuration, against fp64 -- set and accumulate,
+    a split mm_atb reduction included (its partials summed by the flush)."""
+    t = _torch()
+    M, K, N = 777, 260, 132
+    X = seeded((M, K), 1.0, "rgX")
+    W = seeded((K, N), 0.02, "rgW")
+    dY = seeded((M, N), 0.01, "rgdY")
+    P = seeded((M, K), 1.0, "rgP")
+    G = seeded((K, N), 1.0, "rgG")
+    x, w, dy = dev(X), dev(W), dev(dY)
+    y = t.full((M, N), float("nan"), device="cuda")
+    dx, dw = dev(P), dev(G)
+    lib.check(lib.tlg_tune_group(gcfg), "tune")
+    try:
+        lib.group([
+            dict(op="mm", C=y.data_ptr(), M=M, K=K, N=N, A=[x.data_ptr()], B=[w.data_ptr()]),
+            dict(op="mm_bt", beta=1, C=dx.data_ptr(), M=M, K=K, N=N, A=[dy.data_ptr()], B=[w.data_ptr()]),
+            dict(op="mm_atb", beta=1, C=dw.data_ptr(), M=M, K=K, N=N, A=[x.data_ptr()], B=[dy.data_ptr()]),
+        ], stream())
+        name = lib.tlg_group_kernel().decode()
+    finally:
+        lib.check(lib.tlg_tune_group(-1), "tune")
+    X64, W64, dY64 = (a.astype(np.float64) for a in (X, W, dY))
+    assert normwise_rel(y.cpu().numpy(), X64 @ W64) <= TOL, (gcfg, name, "mm")
+    assert normwise_rel(dx.cpu().numpy() - P, dY64 @ W64.T) <= TOL, (gcfg, name, "mm_bt")
+    assert normwise_rel(dw.cpu().numpy() - G, X64.T @ dY64) <= TOL, (gcfg, name, "mm_atb")
+
+
 def _one_alloc(parts):
     """Matrices laid out back to back in one device allocation, as
     map_weights lays out wq | wk | wv and w1 | w3 (tinylm.c:361-393)."""

@@ -62,7 +62,12 @@ enum { RC = 0, OC = 1 };
 //       operand loads issued after it).
 //   PB  paired columns (OC only): tile columns [0, OUTER/2) come from P and
 //       [OUTER/2, OUTER) from P2, both at columns o0 + [0, OUTER/2).
-template <int LAY, int OUTER, int BK, bool VEC, int NT, bool G = false, bool PB = false>
+// Sixteen zero bytes in global memory: with ZP a chunk outside the operand
+// is loaded from here instead of being zeroed after its load, so nothing
+// between a stage's loads and its LDS store waits on the loaded values.
+__device__ __attribute__((aligned(16))) float g_zero_chunk[4] = {0.f, 0.f, 0.f, 0.f};
+
+template <int LAY, int OUTER, int BK, bool VEC, int NT, bool G = false, bool PB = false, bool ZP = false>
 struct TileLoader {
     static constexpr int NCH = OUTER * BK / 4;        // float4 chunks per tile
     static constexpr int PER = NCH / NT;              // chunks per thread
@@ -110,13 +115,15 @@ struct TileLoader {
             const int go = o0 + o, gr = r0 + r;
             f32x4 x = {0.f, 0.f, 0.f, 0.f};
             if (VEC) {
-                ok |= (go < oext && gr < rend) ? (1u << q) : 0u;
+                const bool in = go < oext && gr < rend;
+                if (!ZP) ok |= in ? (1u << q) : 0u;
                 // RC: rows clamp to oext-1, r to rend-4; OC: columns clamp to
                 // oext-4, rows to rend-1 (rend, oext are multiples of 4 here)
                 const int gc = (LAY == RC) ? min(go, oext - 1) : min(go, oext - 4);
                 const int rc = (LAY == RC) ? min(gr, rend - 4) : min(gr, rend - 1);
                 const size_t row = G ? (size_t)rs[q] : (size_t)((LAY == RC) ? gc : rc);
                 const float *p = (LAY == RC) ? Pq + row * ld + rc : Pq + row * ld + gc;
+                if (ZP) p = in ? p : g_zero_chunk;
                 x = *reinterpret_cast<const f32x4 *>(p);
             } else {
 #pragma unroll
@@ -141,7 +148,7 @@ struct TileLoader {
             else           { r = e / (OUTER / 4); o = (e % (OUTER / 4)) * 4; }
             const int off = (LAY == RC) ? o * (BK + 4) + r : r * (OUTER + 4) + o;
             const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-            *reinterpret_cast<f32x4 *>(L + off) = (!VEC || ((ok >> q) & 1u)) ? v[q] : z;
+            *reinterpret_cast<f32x4 *>(L + off) = (!VEC || ZP || ((ok >> q) & 1u)) ? v[q] : z;
         }
     }
 };
@@ -180,6 +187,9 @@ __device__ __forceinline__ void read_frag(const float *__restrict__ L, int o_bas
 template <int BM_, int BN_, int BK_, int WGM_, int WK_, int NR_ = 2, int NCH_ = 0, int NW_ = 4>
 struct Tile {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WK = WK_, NR = NR_;
+    // instruction order of a stage (sched_step): 0 = the compiler's; Sched<>
+    // below selects the others
+    static constexpr int SCH = 0;
     static constexpr int NW = NW_, THREADS = 64 * NW_;      // waves / threads per workgroup
     static constexpr int WGN = NW / (WGM * WK);
     static constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 32, FN = WN / 32;
@@ -202,6 +212,36 @@ struct Tile {
     __device__ static int wk() { return wave() / (WGM * WGN); }
     __device__ static int wm() { return (wave() % (WGM * WGN)) / WGN; }
     __device__ static int wn() { return (wave() % (WGM * WGN)) % WGN; }
+};
+
+// Instruction order inside one stage's scheduling region (between two
+// barriers).  Left to itself the scheduler interleaves each fragment read
+// with the MFMA pair that consumes it, to save registers, so at one wave
+// per SIMD every MFMA pair waits out a full LDS round trip; the explicit
+// orders issue all of a stage's fragment reads first (the MFMAs then wait
+// only for the oldest ones), optionally behind the prefetch loads.
+template <class T>
+__device__ __forceinline__ void sched_step()
+{
+    constexpr int VMEM_RD = 0x020, DS_RD = 0x100, DS_WR = 0x200, MFMA = 0x008;
+    if constexpr (T::SCH == 1) {
+        __builtin_amdgcn_sched_group_barrier(DS_RD, 64, 0);
+        __builtin_amdgcn_sched_group_barrier(MFMA, 64, 0);
+        __builtin_amdgcn_sched_group_barrier(DS_WR, 32, 0);
+    } else if constexpr (T::SCH == 2) {
+        __builtin_amdgcn_sched_group_barrier(VMEM_RD, 32, 0);
+        __builtin_amdgcn_sched_group_barrier(DS_RD, 64, 0);
+        __builtin_amdgcn_sched_group_barrier(MFMA, 64, 0);
+        __builtin_amdgcn_sched_group_barrier(DS_WR, 32, 0);
+    }
+}
+
+// A tile shape with an explicit instruction order per stage: 1 = every
+// fragment read of the stage issued before its first MFMA; 2 = the prefetch
+// loads first, then the fragment reads, then the MFMAs.
+template <class T, int S>
+struct Sched : T {
+    static constexpr int SCH = S;
 };
 
 // acc += A(i0.., r) B(r, j0..) over r in [rbeg, rend).  A tile's loads run
@@ -229,8 +269,9 @@ __device__ __forceinline__ void tile_accumulate(float *__restrict__ smem, const 
     // the paths meet, and it would then wait for all of them, the prefetch
     // included, before every LDS store.
     auto stage_r = [&](int st) { return rbeg + min(st, nsteps - 1) * BK; };
-    TileLoader<LA, BM, BK, VEC, T::THREADS, GA> la0, la1, la2;
-    TileLoader<LB, BN, BK, VEC, T::THREADS, false, PB> lb0, lb1, lb2;
+    constexpr bool ZP = T::SCH > 0;
+    TileLoader<LA, BM, BK, VEC, T::THREADS, GA, false, ZP> la0, la1, la2;
+    TileLoader<LB, BN, BK, VEC, T::THREADS, false, PB, ZP> lb0, lb1, lb2;
     if constexpr (GA && LA == RC) {
         la0.rows(amap, i0, Mo, tid);
         la1.rows(amap, i0, Mo, tid);
@@ -302,17 +343,18 @@ __device__ __forceinline__ void tile_accumulate(float *__restrict__ smem, const 
         lac.load(A, lda, i0, Mo, stage_r(st + T::NR), rend, tid);
         reprep(lac, st + 2 * T::NR);
         lbc.load(B, ldb, j0, No, stage_r(st + T::NR), rend, tid, B2);
-        if constexpr (T::WK > 1) __builtin_amdgcn_sched_barrier(0);
+        if constexpr (T::WK > 1 && T::SCH == 0) __builtin_amdgcn_sched_barrier(0);
         float *cur = smem + (st & 1) * (SA + SB);
         compute(cur, cur + SA);
-        if (T::WK > 1 || st + 1 < nsteps) {
+        if (T::WK > 1 || T::SCH > 0 || st + 1 < nsteps) {
             float *nxt = smem + ((st + 1) & 1) * (SA + SB);
             lan.store(nxt, tid);
             lbn.store(nxt + SA, tid);
         }
+        sched_step<T>();
         __syncthreads();
     };
-    if constexpr (T::WK > 1) {
+    if constexpr (T::WK > 1 || T::SCH > 0) {
         int st = 0;
         if constexpr (T::NR == 2) {
             for (; st + 1 < nsteps; st += 2) {
@@ -957,6 +999,16 @@ static const TileCfg kCfgs[] = {
     {64, 32, 64, 2, 2},     // 21: 32x32 per wave, half of each 64-step stage
     {64, 64, 64, 2, 4, 16}, // 22: 16 waves, 32x32 per wave, a quarter of each 64-step stage
     {64, 64, 64, 2, 2, 8},  // 23: 8 waves, 32x32 per wave, half of each 64-step stage
+    {64, 64, 32, 2, 1},     // 24-25: 3 with a stage's fragment reads first (Sched 1, 2)
+    {64, 64, 32, 2, 1},
+    {64, 32, 32, 2, 2},     // 26: 14, Sched 1
+    {64, 64, 32, 2, 2, 8},  // 27: 20, Sched 1
+    {64, 64, 64, 2, 4, 16}, // 28: 22, Sched 1
+    {32, 64, 32, 1, 2},     // 29: 13, Sched 1
+    {32, 32, 32, 1, 4},     // 30: 15, Sched 1
+    {128, 128, 16, 2, 1},   // 31: 0, Sched 1
+    {128, 64, 32, 2, 1},    // 32: 1, Sched 1
+    {64, 64, 64, 2, 1},     // 33: 8, Sched 1
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
 using T0 = Tile<128, 128, 16, 2, 1>;
@@ -984,6 +1036,16 @@ using T20 = Tile<64, 64, 32, 2, 2, 2, 0, 8>;
 using T21 = Tile<64, 32, 64, 2, 2, 2, 0, 4>;
 using T22 = Tile<64, 64, 64, 2, 4, 2, 0, 16>;
 using T23 = Tile<64, 64, 64, 2, 2, 2, 0, 8>;
+using T24 = Sched<T3, 1>;
+using T25 = Sched<T3, 2>;
+using T26 = Sched<T14, 1>;
+using T27 = Sched<T20, 1>;
+using T28 = Sched<T22, 1>;
+using T29 = Sched<T13, 1>;
+using T30 = Sched<T15, 1>;
+using T31 = Sched<T0, 1>;
+using T32 = Sched<T1, 1>;
+using T33 = Sched<T8, 1>;
 
 template <class T, int LA, int LB>
 static void launch_t(const GemmArgs &a, int grid, bool vec, hipStream_t st)
@@ -1245,10 +1307,11 @@ static int flush_foreign(hipStream_t st);
 static int g_group_cfg = -1;
 static int g_group_rt = 0;               // split target pinned for the next launches (tlg_tune_group_split)
 static double g_min_waves = 3.0;
-static int g_cand[4] = {3, 14, -1, -1};   // 64x64, then 64x32 (2 x 2 waves)
+static int g_cand[4] = {24, 26, -1, -1};  // 64x64, then 64x32 (2 x 2 waves), both in the Sched<.., 1> order
 static int g_rtarget = 512;
 static int g_erps = 1024;                // expert TN slice (TLG_EXPERT_RPS)
 static int g_expert_cfg = -1;            // expert tile shape pinned (TLG_EXPERT_CFG: 3, 14, 15)
+static int g_expert_sched = 1;           // expert tiles in the Sched<.., 1> order (TLG_EXPERT_SCHED=0: not)
 static int g_group_last = 3;          // shape of the most recent grouped launch
 static const char *g_group_last_name = nullptr;   // set when that launch was a GEMV group
 
@@ -1275,6 +1338,7 @@ static void group_env(void)
     if (e && atoi(e) >= 64) g_erps = atoi(e);
     e = getenv("TLG_EXPERT_CFG");
     if (e && (atoi(e) == 3 || atoi(e) == 14 || atoi(e) == 15)) g_expert_cfg = atoi(e);
+    if ((e = getenv("TLG_EXPERT_SCHED"))) g_expert_sched = atoi(e) != 0;
     e = getenv("TLG_GROUP_RTARGET");
     if (e && atoi(e) >= 64) g_rtarget = atoi(e);
 }
@@ -1320,6 +1384,16 @@ static void launch_group(int ci, const GroupArgs &a, int grid, hipStream_t st)
     case 21: lgroup<T21>(a, grid, st); break;
     case 22: lgroup<T22>(a, grid, st); break;
     case 23: lgroup<T23>(a, grid, st); break;
+    case 24: lgroup<T24>(a, grid, st); break;
+    case 25: lgroup<T25>(a, grid, st); break;
+    case 26: lgroup<T26>(a, grid, st); break;
+    case 27: lgroup<T27>(a, grid, st); break;
+    case 28: lgroup<T28>(a, grid, st); break;
+    case 29: lgroup<T29>(a, grid, st); break;
+    case 30: lgroup<T30>(a, grid, st); break;
+    case 31: lgroup<T31>(a, grid, st); break;
+    case 32: lgroup<T32>(a, grid, st); break;
+    case 33: lgroup<T33>(a, grid, st); break;
     default: lgroup<T3>(a, grid, st); break;
     }
     g_group_last = ci;
@@ -1382,6 +1456,16 @@ const char *tlg_group_kernel_name(void)
     case 21: return "k_group<Tile<64, 32, 64, 2, 2, 2, 0, 4> >";
     case 22: return "k_group<Tile<64, 64, 64, 2, 4, 2, 0, 16> >";
     case 23: return "k_group<Tile<64, 64, 64, 2, 2, 2, 0, 8> >";
+    case 24: return "k_group<Sched<Tile<64, 64, 32, 2, 1, 2, 0, 4>, 1> >";
+    case 25: return "k_group<Sched<Tile<64, 64, 32, 2, 1, 2, 0, 4>, 2> >";
+    case 26: return "k_group<Sched<Tile<64, 32, 32, 2, 2, 2, 0, 4>, 1> >";
+    case 27: return "k_group<Sched<Tile<64, 64, 32, 2, 2, 2, 0, 8>, 1> >";
+    case 28: return "k_group<Sched<Tile<64, 64, 64, 2, 4, 2, 0, 16>, 1> >";
+    case 29: return "k_group<Sched<Tile<32, 64, 32, 1, 2, 2, 0, 4>, 1> >";
+    case 30: return "k_group<Sched<Tile<32, 32, 32, 1, 4, 2, 0, 4>, 1> >";
+    case 31: return "k_group<Sched<Tile<128, 128, 16, 2, 1, 2, 0, 4>, 1> >";
+    case 32: return "k_group<Sched<Tile<128, 64, 32, 2, 1, 2, 0, 4>, 1> >";
+    case 33: return "k_group<Sched<Tile<64, 64, 64, 2, 1, 2, 0, 4>, 1> >";
     default: return "k_group<Tile<64, 64, 32, 2, 1, 2, 0, 4> >";
     }
 }
@@ -1631,7 +1715,7 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
     // tile shape: pinned, or the largest with >= g_min_waves waves of items
     int ci = g_group_cfg;
     if (ci < 0) {
-        int last = 3;
+        int last = 24;
         ci = -1;
         for (int k = 0; k < 4 && g_cand[k] >= 0 && ci < 0; k++) {
             last = g_cand[k];
@@ -1953,10 +2037,13 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     // bound by one per expert problem
     static_assert(sizeof(GroupArgs) <= 4096, "kernel arguments");
     const dim3 eg(group_grid(a) + 8 * n);
-    switch (ci) {
+    switch (ci + (g_expert_sched ? 100 : 0)) {
     case 3: hipLaunchKernelGGL((k_expert_group<T3>), eg, dim3(T3::THREADS), 0, st, group_seal(a)); break;
     case 15: hipLaunchKernelGGL((k_expert_group<T15>), eg, dim3(T15::THREADS), 0, st, group_seal(a)); break;
-    default: hipLaunchKernelGGL((k_expert_group<T14>), eg, dim3(T14::THREADS), 0, st, group_seal(a)); break;
+    case 14: hipLaunchKernelGGL((k_expert_group<T14>), eg, dim3(T14::THREADS), 0, st, group_seal(a)); break;
+    case 103: hipLaunchKernelGGL((k_expert_group<T24>), eg, dim3(T24::THREADS), 0, st, group_seal(a)); break;
+    case 115: hipLaunchKernelGGL((k_expert_group<T30>), eg, dim3(T30::THREADS), 0, st, group_seal(a)); break;
+    default: hipLaunchKernelGGL((k_expert_group<T26>), eg, dim3(T26::THREADS), 0, st, group_seal(a)); break;
     }
     TLG_HIP(hipGetLastError());
     if (red.nprob && (carry & TLG_ECARRY_OUT) && !dense && g_npending == 0) {
