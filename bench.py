@@ -195,7 +195,7 @@ def read_rocprof_avg_us(kernel):
     return None
 
 
-AUTOTUNE_CANDS = (3, 14, 13, 15, 0, 1, 20, 21, 22, 23, 24, 26, 27, 28, 29, 30, 31, 32, 33)
+AUTOTUNE_CANDS = (3, 14, 13, 15, 0, 1, 20, 21, 22, 23, 24, 26, 27, 28, 29, 30, 31, 32, 33, 34, 35, 36, 37)
 # split targets tried with each tile candidate (tlg_tune_group_split: reduction
 # steps per split work item of the mm_atb problems; 0 = the library's rule)
 AUTOTUNE_RTS = (0, 256, 512, 1024, 2048, 4096)
@@ -210,15 +210,15 @@ AUTOTUNE_RTS = (0, 256, 512, 1024, 2048, 4096)
 # step's kernels -- and so the roofline kernel and its rocprofv3 profiles --
 # the same from box to box; --autotune re-times the candidates instead.
 TUNED = {
-    "nano": [15, 15, 14, 15, 3, 30, 15, 15, 15, 15],
-    "m3": [13, 22, 24, 22, 26, 22, 24, 28, 26, 22, 24, 22, 26, 22, 24, 28, 26, 20, 24, 22, 26, 20, 24, 22, 24, 27, 24, 24, 13, 24, 24, 24, 13, 24, 24, 24, 13, 24, 24, 24, 13, 24, 24, 24, 14, 24, 24, 24, 29, 24],
-    "m8": [26, 24, 31, 28, 26, 24, 31, 28, 26, 24, 31, 28, 26, 24, 31, 28, 26, 24, 31, 20, 26, 24, 31, 28, 26, 24, 31, 28, 26, 24, 31, 28, 0, 24, 0, 24, 24, 24, 28, 24, 24, 24, 31, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 24, 3, 24, 24, 24, 24, 24, 24, 24, 24],
+    "nano": [30, 30, 26, 15, 37, 30, 15, 30, 30, 30],
+    "m3": [26, 22, 37, 22, 26, 22, 37, 28, 26, 28, 37, 22, 26, 22, 37, 28, 26, 22, 37, 28, 26, 20, 37, 28, 24, 28, 24, 24, 13, 37, 24, 24, 13, 37, 24, 24, 13, 24, 24, 24, 13, 37, 37, 24, 14, 37, 24, 24, 13, 24],
+    "m8": [26, 37, 37, 28, 26, 37, 31, 28, 26, 37, 37, 28, 26, 37, 37, 28, 26, 37, 37, 28, 26, 37, 37, 28, 26, 37, 37, 28, 26, 37, 37, 28, 0, 37, 24, 37, 37, 24, 37, 24, 24, 24, 24, 37, 24, 24, 37, 37, 24, 37, 37, 37, 24, 37, 37, 37, 24, 37, 37, 37, 24, 37, 24, 37, 24, 37, 37, 37, 24, 37, 37, 37],
 }
 # (0 = the library's automatic rule)
 SPLITS = {
-    "nano": [2048, 256, 2048, 512, 0, 1024, 0, 256, 256, 256],
-    "m3": [256, 0, 512, 512, 4096, 4096, 512, 512, 4096, 512, 512, 1024, 4096, 4096, 512, 1024, 4096, 2048, 512, 512, 2048, 1024, 512, 1024, 1024, 1024, 0, 512, 0, 512, 512, 512, 0, 512, 512, 512, 0, 512, 512, 512, 0, 512, 512, 512, 0, 512, 512, 512, 0, 512],
-    "m8": [0, 2048, 1024, 4096, 256, 512, 1024, 256, 4096, 1024, 1024, 0, 256, 1024, 1024, 1024, 4096, 4096, 0, 4096, 4096, 512, 1024, 512, 256, 512, 1024, 0, 512, 256, 0, 1024, 0, 2048, 512, 1024, 256, 2048, 4096, 256, 1024, 2048, 256, 2048, 1024, 2048, 256, 2048, 1024, 1024, 256, 2048, 1024, 2048, 256, 2048, 1024, 2048, 256, 2048, 1024, 2048, 256, 512, 1024, 2048, 256, 2048, 1024, 1024, 256, 2048],
+    "nano": [4096, 256, 4096, 256, 2048, 1024, 0, 1024, 256, 256],
+    "m3": [256, 256, 256, 0, 2048, 4096, 256, 2048, 1024, 2048, 256, 512, 1024, 4096, 512, 512, 2048, 512, 512, 1024, 512, 512, 512, 256, 256, 2048, 0, 512, 0, 512, 512, 512, 0, 256, 512, 512, 0, 512, 512, 512, 0, 256, 256, 512, 0, 256, 512, 512, 0, 512],
+    "m8": [1024, 256, 1024, 1024, 256, 2048, 1024, 512, 256, 1024, 512, 1024, 256, 1024, 2048, 1024, 256, 2048, 2048, 512, 2048, 2048, 256, 512, 2048, 2048, 1024, 1024, 4096, 2048, 2048, 512, 1024, 2048, 512, 1024, 256, 2048, 1024, 256, 1024, 1024, 256, 512, 1024, 2048, 256, 512, 1024, 2048, 256, 1024, 1024, 1024, 256, 1024, 1024, 1024, 256, 1024, 1024, 1024, 256, 1024, 1024, 1024, 256, 1024, 1024, 1024, 256, 1024],
 }
 
 

@@ -1009,6 +1009,10 @@ static const TileCfg kCfgs[] = {
     {128, 128, 16, 2, 1},   // 31: 0, Sched 1
     {128, 64, 32, 2, 1},    // 32: 1, Sched 1
     {64, 64, 64, 2, 1},     // 33: 8, Sched 1
+    {64, 64, 32, 2, 1},     // 34: 11 (loads three stages ahead), Sched 1
+    {64, 32, 64, 2, 2},     // 35: 21, Sched 1
+    {64, 64, 64, 2, 2, 8},  // 36: 23, Sched 1
+    {64, 64, 16, 2, 1},     // 37: 18, Sched 1
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
 using T0 = Tile<128, 128, 16, 2, 1>;
@@ -1046,6 +1050,10 @@ using T30 = Sched<T15, 1>;
 using T31 = Sched<T0, 1>;
 using T32 = Sched<T1, 1>;
 using T33 = Sched<T8, 1>;
+using T34 = Sched<T11, 1>;
+using T35 = Sched<T21, 1>;
+using T36 = Sched<T23, 1>;
+using T37 = Sched<T18, 1>;
 
 template <class T, int LA, int LB>
 static void launch_t(const GemmArgs &a, int grid, bool vec, hipStream_t st)
@@ -1394,6 +1402,10 @@ static void launch_group(int ci, const GroupArgs &a, int grid, hipStream_t st)
     case 31: lgroup<T31>(a, grid, st); break;
     case 32: lgroup<T32>(a, grid, st); break;
     case 33: lgroup<T33>(a, grid, st); break;
+    case 34: lgroup<T34>(a, grid, st); break;
+    case 35: lgroup<T35>(a, grid, st); break;
+    case 36: lgroup<T36>(a, grid, st); break;
+    case 37: lgroup<T37>(a, grid, st); break;
     default: lgroup<T3>(a, grid, st); break;
     }
     g_group_last = ci;
@@ -1466,6 +1478,10 @@ const char *tlg_group_kernel_name(void)
     case 31: return "k_group<Sched<Tile<128, 128, 16, 2, 1, 2, 0, 4>, 1> >";
     case 32: return "k_group<Sched<Tile<128, 64, 32, 2, 1, 2, 0, 4>, 1> >";
     case 33: return "k_group<Sched<Tile<64, 64, 64, 2, 1, 2, 0, 4>, 1> >";
+    case 34: return "k_group<Sched<Tile<64, 64, 32, 2, 1, 3, 1, 4>, 1> >";
+    case 35: return "k_group<Sched<Tile<64, 32, 64, 2, 2, 2, 0, 4>, 1> >";
+    case 36: return "k_group<Sched<Tile<64, 64, 64, 2, 2, 2, 0, 8>, 1> >";
+    case 37: return "k_group<Sched<Tile<64, 64, 16, 2, 1, 2, 0, 4>, 1> >";
     default: return "k_group<Tile<64, 64, 32, 2, 1, 2, 0, 4> >";
     }
 }
