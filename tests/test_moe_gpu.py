@@ -225,6 +225,37 @@ def test_against_oracle_and_f64(lib, orc, N, D, F, E, skew, dead):
     check_backward(dfn, grads, r_dfn, ref_g, g0, (dfn64, g64))
 
 
+@pytest.mark.parametrize("cfg", [3, 14, 15, 22])
+@pytest.mark.parametrize("sched", [0, 1])
+def test_expert_tile_forms(lib, orc, cfg, sched):
+    """Every tile shape and stage order an expert launch can take (pinned with
+    tlg_tune_expert), on the MoE training config with skewed routing and on a
+    ragged one, against the oracle and fp64."""
+    lib.check(lib.tlg_tune_expert(cfg, sched), "tune expert")
+    try:
+        for N, D, F, E, skew in ((4096, 256, 768, 4, 2.0), (67, 32, 48, 3, 0.0)):
+            seed = zlib.crc32(f"moe tiles {N} {D} {F} {E} {skew}".encode())
+            print("case", cfg, sched, N, D, F, E, skew, "seed", seed, flush=True)
+            c = case(N, D, F, E, seed, skew, ())
+            r_out, r_assign, r_gate, r_rprobs = orc.moe_forward(c["fnorm"], c["fin"], c["wr"], c["w1"],
+                                                                 c["w3"], c["w2"])
+            got = gpu_forward(lib, c["fnorm"], c["fin"], c["wr"], c["w1"], c["w3"], c["w2"])
+            check_forward(got, r_out, r_assign, r_gate, r_rprobs, c["fin"])
+            g0 = [c[k] for k in ("gwr0", "gw10", "gw30", "gw20")]
+            ref_g = [x.copy() for x in g0]
+            r_dfn = orc.moe_backward(c["fnorm"], c["dout"], c["wr"], c["w1"], c["w3"], c["w2"], *ref_g,
+                                     r_assign, r_gate, r_rprobs)
+            dfn, grads = gpu_backward(lib, c["fnorm"], c["dout"], r_assign, r_gate, r_rprobs, c["wr"],
+                                      c["w1"], c["w3"], c["w2"], *g0)
+            o64, dfn64, *g64 = f64_moe(c["fnorm"], c["fin"], c["wr"], c["w1"], c["w3"], c["w2"], c["dout"],
+                                      r_assign)
+            assert_delta(got[0] - c["fin"], o64 - c["fin"], o64)
+            check_backward(dfn, grads, r_dfn, ref_g, g0, (dfn64, g64))
+    finally:
+        lib.check(lib.tlg_tune_expert(-1, 1), "tune expert")
+    assert lib.tlg_tune_expert(8, 1) != 0 and lib.tlg_tune_expert(3, 2) != 0
+
+
 def test_skewed_split(lib):
     """The skewed config really is unbalanced (so the test above exercises
     experts of very different row counts)."""

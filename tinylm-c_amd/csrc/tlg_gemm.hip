@@ -1318,8 +1318,10 @@ static double g_min_waves = 3.0;
 static int g_cand[4] = {24, 26, -1, -1};  // 64x64, then 64x32 (2 x 2 waves), both in the Sched<.., 1> order
 static int g_rtarget = 512;
 static int g_erps = 1024;                // expert TN slice (TLG_EXPERT_RPS)
-static int g_expert_cfg = -1;            // expert tile shape pinned (TLG_EXPERT_CFG: 3, 14, 15)
+static int g_expert_cfg = -1;            // expert tile shape pinned (TLG_EXPERT_CFG: 3, 14, 15, 22)
 static int g_expert_sched = 1;           // expert tiles in the Sched<.., 1> order (TLG_EXPERT_SCHED=0: not)
+static int g_expert_w16 = 0;             // 16-wave 64x64 tiles for launches short of 64x64 items (TLG_EXPERT_W16=1;
+                                         // measured slower: kept MoE pair 0.2345 -> 0.2489 ms)
 static int g_group_last = 3;          // shape of the most recent grouped launch
 static const char *g_group_last_name = nullptr;   // set when that launch was a GEMV group
 
@@ -1345,8 +1347,9 @@ static void group_env(void)
     e = getenv("TLG_EXPERT_RPS");
     if (e && atoi(e) >= 64) g_erps = atoi(e);
     e = getenv("TLG_EXPERT_CFG");
-    if (e && (atoi(e) == 3 || atoi(e) == 14 || atoi(e) == 15)) g_expert_cfg = atoi(e);
+    if (e && (atoi(e) == 3 || atoi(e) == 14 || atoi(e) == 15 || atoi(e) == 22)) g_expert_cfg = atoi(e);
     if ((e = getenv("TLG_EXPERT_SCHED"))) g_expert_sched = atoi(e) != 0;
+    if ((e = getenv("TLG_EXPERT_W16"))) g_expert_w16 = atoi(e) != 0;
     e = getenv("TLG_GROUP_RTARGET");
     if (e && atoi(e) >= 64) g_rtarget = atoi(e);
 }
@@ -1426,6 +1429,16 @@ extern "C" int tlg_tune_group_policy(const int *cands, int ncands, double min_wa
     }
     if (min_waves > 0) g_min_waves = min_waves;
     if (rtarget) g_rtarget = rtarget;
+    return TLG_OK;
+}
+
+extern "C" int tlg_tune_expert(int cfg, int sched)
+{
+    group_env();
+    if ((cfg != -1 && cfg != 3 && cfg != 14 && cfg != 15 && cfg != 22) || (sched != 0 && sched != 1))
+        return tlg_fail(TLG_EINVAL, "tlg_tune_expert: config %d, order %d", cfg, sched);
+    g_expert_cfg = cfg;
+    g_expert_sched = sched;
     return TLG_OK;
 }
 
@@ -1995,8 +2008,13 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
         return t;
     };
     const double enough = g_min_waves * 256;
+    // (TLG_EXPERT_W16=1: launches with fewer 64x64 items than that but about
+    // one per CU -- the N = 256 W2 launches -- run 64x64 tiles of 16 waves,
+    // as the dense W2 forward does; slower on every configs[4] launch)
     const int ci = g_expert_cfg >= 0 ? g_expert_cfg
-                 : items_for(kCfgs[3]) >= enough ? 3 : items_for(kCfgs[14]) >= enough ? 14 : 15;
+                 : items_for(kCfgs[3]) >= enough ? 3
+                 : (g_expert_w16 && items_for(kCfgs[22]) >= 240) ? 22
+                 : items_for(kCfgs[14]) >= enough ? 14 : 15;
     const TileCfg &tc = kCfgs[ci];
     GroupArgs a, red, pend;
     a.nprob = red.nprob = pend.nprob = 0;
@@ -2057,6 +2075,8 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     case 3: hipLaunchKernelGGL((k_expert_group<T3>), eg, dim3(T3::THREADS), 0, st, group_seal(a)); break;
     case 15: hipLaunchKernelGGL((k_expert_group<T15>), eg, dim3(T15::THREADS), 0, st, group_seal(a)); break;
     case 14: hipLaunchKernelGGL((k_expert_group<T14>), eg, dim3(T14::THREADS), 0, st, group_seal(a)); break;
+    case 22: hipLaunchKernelGGL((k_expert_group<T22>), eg, dim3(T22::THREADS), 0, st, group_seal(a)); break;
+    case 122: hipLaunchKernelGGL((k_expert_group<T28>), eg, dim3(T28::THREADS), 0, st, group_seal(a)); break;
     case 103: hipLaunchKernelGGL((k_expert_group<T24>), eg, dim3(T24::THREADS), 0, st, group_seal(a)); break;
     case 115: hipLaunchKernelGGL((k_expert_group<T30>), eg, dim3(T30::THREADS), 0, st, group_seal(a)); break;
     default: hipLaunchKernelGGL((k_expert_group<T26>), eg, dim3(T26::THREADS), 0, st, group_seal(a)); break;

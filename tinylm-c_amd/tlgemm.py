@@ -66,6 +66,7 @@ SIGNATURES = {
     "tlg_tune_group": (_i, [_i]),
     "tlg_tune_group_policy": (_i, [_ip, _i, ctypes.c_double, _i]),
     "tlg_tune_group_split": (_i, [_i]),
+    "tlg_tune_expert": (_i, [_i, _i]),
     "tlg_graph_begin": (_i, [_vp]),
     "tlg_graph_end": (_vp, [_vp]),
     "tlg_graph_launch": (_i, [_vp, _vp]),
