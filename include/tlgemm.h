@@ -168,9 +168,10 @@ int tlg_tune_group_policy(const int *cands, int ncands, double min_waves, int rt
  * The split partials are summed in split order either way. */
 int tlg_tune_group_split(int rtarget);
 /* Tuning hook: the tile shape of the MoE expert launches (tlg_dev_moe_*):
- * cfg -1 = automatic (64x64 tiles when a launch has about 3 x 256 of them,
- * else 64x32, else 32x32), or 3 (64x64), 14 (64x32), 15 (32x32), 22 (16-wave
- * 64x64, whose waves split each 64-step stage four ways) pinned;
+ * cfg -1 = automatic (64x64 tiles of 16-step stages when a launch has about
+ * 3 x 256 of them, else 64x32, else 32x32), or 3 (64x64), 18 (64x64, 16-step
+ * stages), 14 (64x32), 15 (32x32), 22 (16-wave 64x64, whose waves split each
+ * 64-step stage four ways) pinned;
  * sched 1 = each stage's fragment reads issued before its MFMAs (the
  * default), 0 = the compiler's order.  Applies to later launches. */
 int tlg_tune_expert(int cfg, int sched);

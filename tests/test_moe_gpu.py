@@ -225,7 +225,7 @@ def test_against_oracle_and_f64(lib, orc, N, D, F, E, skew, dead):
     check_backward(dfn, grads, r_dfn, ref_g, g0, (dfn64, g64))
 
 
-@pytest.mark.parametrize("cfg", [3, 14, 15, 22])
+@pytest.mark.parametrize("cfg", [3, 14, 15, 18, 22])
 @pytest.mark.parametrize("sched", [0, 1])
 def test_expert_tile_forms(lib, orc, cfg, sched):
     """Every tile shape and stage order an expert launch can take (pinned with

@@ -1318,8 +1318,9 @@ static double g_min_waves = 3.0;
 static int g_cand[4] = {24, 26, -1, -1};  // 64x64, then 64x32 (2 x 2 waves), both in the Sched<.., 1> order
 static int g_rtarget = 512;
 static int g_erps = 1024;                // expert TN slice (TLG_EXPERT_RPS)
-static int g_expert_cfg = -1;            // expert tile shape pinned (TLG_EXPERT_CFG: 3, 14, 15, 22)
+static int g_expert_cfg = -1;            // expert tile shape pinned (TLG_EXPERT_CFG: 3, 14, 15, 18, 22)
 static int g_expert_sched = 1;           // expert tiles in the Sched<.., 1> order (TLG_EXPERT_SCHED=0: not)
+static int g_expert_bk16 = 1;            // 64x64 expert tiles with 16-step stages (TLG_EXPERT_BK16=0: 32-step)
 static int g_expert_w16 = 0;             // 16-wave 64x64 tiles for launches short of 64x64 items (TLG_EXPERT_W16=1;
                                          // measured slower: kept MoE pair 0.2345 -> 0.2489 ms)
 static int g_group_last = 3;          // shape of the most recent grouped launch
@@ -1347,9 +1348,11 @@ static void group_env(void)
     e = getenv("TLG_EXPERT_RPS");
     if (e && atoi(e) >= 64) g_erps = atoi(e);
     e = getenv("TLG_EXPERT_CFG");
-    if (e && (atoi(e) == 3 || atoi(e) == 14 || atoi(e) == 15 || atoi(e) == 22)) g_expert_cfg = atoi(e);
+    if (e && (atoi(e) == 3 || atoi(e) == 14 || atoi(e) == 15 || atoi(e) == 18 || atoi(e) == 22))
+        g_expert_cfg = atoi(e);
     if ((e = getenv("TLG_EXPERT_SCHED"))) g_expert_sched = atoi(e) != 0;
     if ((e = getenv("TLG_EXPERT_W16"))) g_expert_w16 = atoi(e) != 0;
+    if ((e = getenv("TLG_EXPERT_BK16"))) g_expert_bk16 = atoi(e) != 0;
     e = getenv("TLG_GROUP_RTARGET");
     if (e && atoi(e) >= 64) g_rtarget = atoi(e);
 }
@@ -1435,7 +1438,7 @@ extern "C" int tlg_tune_group_policy(const int *cands, int ncands, double min_wa
 extern "C" int tlg_tune_expert(int cfg, int sched)
 {
     group_env();
-    if ((cfg != -1 && cfg != 3 && cfg != 14 && cfg != 15 && cfg != 22) || (sched != 0 && sched != 1))
+    if ((cfg != -1 && cfg != 3 && cfg != 14 && cfg != 15 && cfg != 18 && cfg != 22) || (sched != 0 && sched != 1))
         return tlg_fail(TLG_EINVAL, "tlg_tune_expert: config %d, order %d", cfg, sched);
     g_expert_cfg = cfg;
     g_expert_sched = sched;
@@ -2012,7 +2015,7 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     // one per CU -- the N = 256 W2 launches -- run 64x64 tiles of 16 waves,
     // as the dense W2 forward does; slower on every configs[4] launch)
     const int ci = g_expert_cfg >= 0 ? g_expert_cfg
-                 : items_for(kCfgs[3]) >= enough ? 3
+                 : items_for(kCfgs[3]) >= enough ? (g_expert_bk16 ? 18 : 3)
                  : (g_expert_w16 && items_for(kCfgs[22]) >= 240) ? 22
                  : items_for(kCfgs[14]) >= enough ? 14 : 15;
     const TileCfg &tc = kCfgs[ci];
@@ -2075,7 +2078,9 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     case 3: hipLaunchKernelGGL((k_expert_group<T3>), eg, dim3(T3::THREADS), 0, st, group_seal(a)); break;
     case 15: hipLaunchKernelGGL((k_expert_group<T15>), eg, dim3(T15::THREADS), 0, st, group_seal(a)); break;
     case 14: hipLaunchKernelGGL((k_expert_group<T14>), eg, dim3(T14::THREADS), 0, st, group_seal(a)); break;
+    case 18: hipLaunchKernelGGL((k_expert_group<T18>), eg, dim3(T18::THREADS), 0, st, group_seal(a)); break;
     case 22: hipLaunchKernelGGL((k_expert_group<T22>), eg, dim3(T22::THREADS), 0, st, group_seal(a)); break;
+    case 118: hipLaunchKernelGGL((k_expert_group<T37>), eg, dim3(T37::THREADS), 0, st, group_seal(a)); break;
     case 122: hipLaunchKernelGGL((k_expert_group<T28>), eg, dim3(T28::THREADS), 0, st, group_seal(a)); break;
     case 103: hipLaunchKernelGGL((k_expert_group<T24>), eg, dim3(T24::THREADS), 0, st, group_seal(a)); break;
     case 115: hipLaunchKernelGGL((k_expert_group<T30>), eg, dim3(T30::THREADS), 0, st, group_seal(a)); break;
