@@ -142,7 +142,8 @@ int tlg_dev_swiglu_mm(const float *X, const float *W1, const float *W3, float *a
 int tlg_dev_mm_bt_swiglu_bwd(const float *dY, const float *W2, float *g, float *u, int M, int K, int N,
                              void *stream);
 int tlg_dev_gemm_flush(void *stream);
-/* Number of split reductions still pending (what a flush would launch). */
+/* Number of split reductions still pending (what a flush would launch),
+ * the MoE backward's held expert reductions included. */
 int tlg_dev_gemm_pending(void);
 /* Kernel instance grouped launches use, as rocprofv3 names it. */
 const char *tlg_group_kernel(void);
@@ -173,7 +174,8 @@ int tlg_tune_group_split(int rtarget);
  * stages), 14 (64x32), 15 (32x32), 22 (16-wave 64x64, whose waves split each
  * 64-step stage four ways) pinned;
  * sched 1 = each stage's fragment reads issued before its MFMAs (the
- * default), 0 = the compiler's order.  Applies to later launches. */
+ * default), 2 = that order with the outputs written by streaming stores, 0 =
+ * the compiler's order.  Applies to later launches. */
 int tlg_tune_expert(int cfg, int sched);
 
 /* ---- top-1 mixture-of-experts FFN --------------------------------------- */
@@ -240,12 +242,17 @@ void tlg_moe_grouped_bwd(const float *fnorm, const float *dout, float *d_fnorm, 
 /* So the C step drivers (tinylm-c_amd/host) keep buffers and timing on the
  * device without including HIP headers.  No reference counterpart. */
 void *tlg_dev_malloc(size_t bytes);                       /* NULL on failure */
+/* Launches every queued reduction first (each on the stream its partials
+ * were written on: they may read or write p), then frees p; hipFree waits for
+ * the device.  Memory from another allocator must not be released while a
+ * reduction queued by a grouped, expert or MoE launch may still touch it:
+ * call tlg_dev_gemm_flush on that stream first. */
 int   tlg_dev_free(void *p);
 int   tlg_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
 int   tlg_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream);
 int   tlg_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream);
 void *tlg_stream_create(void);                            /* default priority */
-int   tlg_stream_destroy(void *stream);
+int   tlg_stream_destroy(void *stream);                   /* runs reductions queued on it first */
 int   tlg_stream_sync(void *stream);
 void *tlg_event_create(void);
 int   tlg_event_destroy(void *ev);

@@ -208,10 +208,11 @@ def test_gemv_group(lib):
             assert lib.tlg_group_kernel().decode().startswith("k_gemv")
 
 
-# Sched<> tile variants (configurations 24-37: a stage's fragment reads issued
+# Sched<> tile variants (configurations 24-50: a stage's fragment reads issued
 # before its MFMAs, out-of-range chunks loaded from a zero buffer) beside the
 # shapes they reorder
-SCHED_CFGS = [3, 24, 25, 14, 26, 20, 27, 22, 28, 13, 29, 15, 30, 0, 31, 1, 32, 8, 33, 11, 34, 21, 35, 23, 36, 18, 37]
+SCHED_CFGS = [3, 24, 25, 14, 26, 20, 27, 22, 28, 13, 29, 15, 30, 0, 31, 1, 32, 8, 33, 11, 34, 21, 35, 23, 36, 18, 37,
+              38, 39, 40, 41, 42, 43, 44, 45, 46, 47, 48, 49, 50]
 
 
 @pytest.mark.parametrize("gcfg", SCHED_CFGS)

@@ -226,7 +226,7 @@ def test_against_oracle_and_f64(lib, orc, N, D, F, E, skew, dead):
 
 
 @pytest.mark.parametrize("cfg", [3, 14, 15, 18, 22])
-@pytest.mark.parametrize("sched", [0, 1])
+@pytest.mark.parametrize("sched", [0, 1, 2])
 def test_expert_tile_forms(lib, orc, cfg, sched):
     """Every tile shape and stage order an expert launch can take (pinned with
     tlg_tune_expert), on the MoE training config with skewed routing and on a
@@ -253,7 +253,7 @@ def test_expert_tile_forms(lib, orc, cfg, sched):
             check_backward(dfn, grads, r_dfn, ref_g, g0, (dfn64, g64))
     finally:
         lib.check(lib.tlg_tune_expert(-1, 1), "tune expert")
-    assert lib.tlg_tune_expert(8, 1) != 0 and lib.tlg_tune_expert(3, 2) != 0
+    assert lib.tlg_tune_expert(8, 1) != 0 and lib.tlg_tune_expert(3, 3) != 0
 
 
 def test_skewed_split(lib):
@@ -279,9 +279,12 @@ def test_deterministic(lib):
         assert np.array_equal(x, y)
 
 
-def gpu_pair_kept(lib, c, interleave=None):
+def gpu_pair_kept(lib, c, interleave=None, finish="flush"):
     """Forward with kept state, then (after `interleave()`, other MoE calls
-    that reuse the library's scratch) the backward from that state."""
+    that reuse the library's scratch) the backward from that state.  The
+    backward leaves reductions queued (dWr's column sum, the dW1 / dW3 slice
+    sums); `finish` completes them with tlg_dev_gemm_flush, or ("free") with
+    tlg_dev_free of an unrelated buffer, which must launch them first."""
     t = _torch()
     N, D = c["fnorm"].shape
     E, F = c["wr"].shape[1], c["w1"].shape[2]
@@ -304,6 +307,11 @@ def gpu_pair_kept(lib, c, interleave=None):
     lib.moe_bwd_kept(p["fnorm"], p["dout"], dfn.data_ptr(), assign.data_ptr(), gate.data_ptr(), rprobs.data_ptr(),
                      N, D, F, E, p["wr"], p["w1"], p["w3"], p["w2"], g[0], g[1], g[2], g[3], keep.data_ptr(), nb,
                      stream())
+    if finish == "free":
+        assert lib.tlg_dev_gemm_pending() > 0, "the kept backward left nothing queued"
+        other = lib.tlg_dev_malloc(256)
+        lib.check(lib.tlg_dev_free(other), "tlg_dev_free")
+        assert lib.tlg_dev_gemm_pending() == 0, "tlg_dev_free left reductions queued"
     lib.check(lib.tlg_dev_gemm_flush(stream()), "flush")      # dWr's deferred column sum
     fwd = (out.cpu().numpy(), assign.cpu().numpy(), gate.cpu().numpy(), rprobs.cpu().numpy())
     return fwd, dfn.cpu().numpy(), [x.cpu().numpy() for x in grads]
@@ -313,7 +321,8 @@ def gpu_pair_kept(lib, c, interleave=None):
                                               (2500, 64, 96, 5, 1.0, (3,)), (513, 32, 64, 1, 0.0, ())])
 def test_kept_state_pair_is_bit_identical(lib, N, D, F, E, skew, dead):
     """tlg_dev_moe_grouped_fwd_keep + _bwd_kept give the recomputing pair's
-    results bit for bit, also when other MoE calls run between them."""
+    results bit for bit, also when other MoE calls run between them, and when
+    tlg_dev_free (not a flush) is what runs the reductions they leave queued."""
     print("kept pair", N, D, F, E, flush=True)
     c = case(N, D, F, E, zlib.crc32(f"kept {N} {D} {F} {E}".encode()), skew, dead)
     ref_f = gpu_forward(lib, c["fnorm"], c["fin"], c["wr"], c["w1"], c["w3"], c["w2"])
@@ -327,8 +336,8 @@ def test_kept_state_pair_is_bit_identical(lib, N, D, F, E, skew, dead):
         gpu_backward(lib, other["fnorm"], other["dout"], f[1], f[2], f[3], other["wr"], other["w1"], other["w3"],
                      other["w2"], *[other[k] for k in ("gwr0", "gw10", "gw30", "gw20")])
 
-    for inter in (None, interleave):
-        fwd, dfn, grads = gpu_pair_kept(lib, c, inter)
+    for inter, finish in ((None, "flush"), (interleave, "flush"), (None, "free")):
+        fwd, dfn, grads = gpu_pair_kept(lib, c, inter, finish)
         for x, y in zip(fwd, ref_f):
             assert np.array_equal(x, y)
         assert np.array_equal(dfn, ref_b[0])

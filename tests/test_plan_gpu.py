@@ -151,7 +151,8 @@ def test_use_hip_seam(lib, orc):
 
 
 @pytest.mark.parametrize("gcfg", [0, 1, 3, 4, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23,
-                                  24, 25, 26, 27, 28, 29, 30, 31, 32, 33, 34, 35, 36, 37])
+                                  24, 25, 26, 27, 28, 29, 30, 31, 32, 33, 34, 35, 36, 37, 38, 39, 40, 41,
+                                  42, 43, 44, 45, 46, 47, 48, 49, 50])
 def test_group_tile_configs(lib, orc, gcfg):
     """Every tile shape grouped launches can use, on the nano step."""
     host = tlgemm.host()

@@ -282,7 +282,17 @@ extern "C" void *tlg_dev_malloc(size_t bytes)
     }
     return p;
 }
-extern "C" int tlg_dev_free(void *p) { TLG_HIP(hipFree(p)); return TLG_OK; }
+// Queued split reductions (and held expert ones) may read or write p: they
+// are launched first, and hipFree waits for the device before releasing it.
+extern "C" int tlg_dev_free(void *p)
+{
+    if (g_tlg.initialised) {
+        const int rc = tlg_group_flush_all();
+        if (rc) return rc;
+    }
+    TLG_HIP(hipFree(p));
+    return TLG_OK;
+}
 extern "C" int tlg_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream)
 { TLG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream)); return TLG_OK; }
 extern "C" int tlg_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream)
@@ -296,7 +306,17 @@ extern "C" void *tlg_stream_create(void)
     if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
     return s;
 }
-extern "C" int tlg_stream_destroy(void *s) { TLG_HIP(hipStreamDestroy((hipStream_t)s)); return TLG_OK; }
+// Reductions queued on the stream (a grouped launch's split partials, the
+// MoE backward's held sums) run on it before the handle is destroyed.
+extern "C" int tlg_stream_destroy(void *s)
+{
+    if (g_tlg.initialised) {
+        const int rc = tlg_group_flush_stream((hipStream_t)s);
+        if (rc) return rc;
+    }
+    TLG_HIP(hipStreamDestroy((hipStream_t)s));
+    return TLG_OK;
+}
 extern "C" int tlg_stream_sync(void *s) { TLG_HIP(hipStreamSynchronize((hipStream_t)s)); return TLG_OK; }
 extern "C" void *tlg_event_create(void)
 {

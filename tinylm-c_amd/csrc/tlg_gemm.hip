@@ -224,11 +224,11 @@ template <class T>
 __device__ __forceinline__ void sched_step()
 {
     constexpr int VMEM_RD = 0x020, DS_RD = 0x100, DS_WR = 0x200, MFMA = 0x008;
-    if constexpr (T::SCH == 1) {
+    if constexpr ((T::SCH & 3) == 1) {
         __builtin_amdgcn_sched_group_barrier(DS_RD, 64, 0);
         __builtin_amdgcn_sched_group_barrier(MFMA, 64, 0);
         __builtin_amdgcn_sched_group_barrier(DS_WR, 32, 0);
-    } else if constexpr (T::SCH == 2) {
+    } else if constexpr ((T::SCH & 3) == 2) {
         __builtin_amdgcn_sched_group_barrier(VMEM_RD, 32, 0);
         __builtin_amdgcn_sched_group_barrier(DS_RD, 64, 0);
         __builtin_amdgcn_sched_group_barrier(MFMA, 64, 0);
@@ -238,7 +238,8 @@ __device__ __forceinline__ void sched_step()
 
 // A tile shape with an explicit instruction order per stage: 1 = every
 // fragment read of the stage issued before its first MFMA; 2 = the prefetch
-// loads first, then the fragment reads, then the MFMAs.
+// loads first, then the fragment reads, then the MFMAs.  + 4: the tile's
+// outputs leave with nontemporal (streaming) stores.
 template <class T, int S>
 struct Sched : T {
     static constexpr int SCH = S;
@@ -447,6 +448,16 @@ __device__ __forceinline__ void tile_epi(const f32x16 (&accs)[T::FM][T::FN][T::N
     }
 }
 
+// One output element of a tile: a streaming store for the Sched<T, 4 + ..>
+// shapes (it goes past the L2, so the kernel's end does not wait to write
+// back lines the next launch reads through another XCD's L2 anyway).
+template <class T>
+__device__ __forceinline__ void st_out(float *p, float v)
+{
+    if constexpr ((T::SCH & 4) != 0) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+
 // C (beta ? += : =) acc for the valid part of the tile.
 template <class T>
 __device__ __forceinline__ void tile_store(const f32x16 (&accs)[T::FM][T::FN][T::NCH], float *__restrict__ C,
@@ -455,7 +466,7 @@ __device__ __forceinline__ void tile_store(const f32x16 (&accs)[T::FM][T::FN][T:
 {
     tile_epi<T>(accs, Mo, No, i0, j0, red, [&](int i, int j, float v) {
         float *p = C + (size_t)i * ldc + j;
-        *p = beta ? (*p + v) : v;
+        st_out<T>(p, beta ? (*p + v) : v);
     });
 }
 
@@ -497,9 +508,9 @@ __device__ __forceinline__ void tile_swiglu(const f32x16 (&accs)[T::FM][T::FN][T
         if (i >= Mo || j >= No) continue;
         const float g = L[x * LD + c], u = L[x * LD + c + H];
         const size_t o = (size_t)i * ldc + j;
-        Ca[o] = g * hw_sigmoid(g) * u;
-        if (Cg) Cg[o] = g;
-        if (Cu) Cu[o] = u;
+        st_out<T>(Ca + o, g * hw_sigmoid(g) * u);
+        if (Cg) st_out<T>(Cg + o, g);
+        if (Cu) st_out<T>(Cu + o, u);
     }
     __syncthreads();
 }
@@ -728,8 +739,8 @@ __device__ __forceinline__ void expert_tile(float *smem, const Prob &P, int loca
                 const float sg = hw_sigmoid(z);
                 const float si = z * sg;
                 const float ds = sg + z * sg * (1.0f - sg);
-                G[o] = d * uv * ds;
-                U[o] = d * si;
+                st_out<T>(G + o, d * uv * ds);
+                st_out<T>(U + o, d * si);
             });
             break;
         }
@@ -744,8 +755,8 @@ __device__ __forceinline__ void expert_tile(float *smem, const Prob &P, int loca
                 tile_epi<T>(acc, rows, P.No, i0, j0, smem, [&](int i, int j, float y) {
                     const int x = i - i0;
                     const size_t o = (size_t)s_tok[x] * ld + j;
-                    C[o] = fmaf(s_gate[x], y, fin[o]);
-                    if (Y) Y[(size_t)i * ld + j] = y;
+                    st_out<T>(C + o, fmaf(s_gate[x], y, fin[o]));
+                    if (Y) st_out<T>(Y + (size_t)i * ld + j, y);
                 });
             }
             break;
@@ -820,7 +831,7 @@ __device__ __forceinline__ void group_tile(float *smem, const Prob &P, int local
         const int ld = P.ldc;
         tile_epi<T>(acc, P.Mo, P.No, i0, j0, smem, [&](int i, int j, float v) {
             const size_t o = (size_t)i * ld + j;
-            C[o] = Rr[o] + v;
+            st_out<T>(C + o, Rr[o] + v);
         });
         return;
     }
@@ -1013,6 +1024,19 @@ static const TileCfg kCfgs[] = {
     {64, 32, 64, 2, 2},     // 35: 21, Sched 1
     {64, 64, 64, 2, 2, 8},  // 36: 23, Sched 1
     {64, 64, 16, 2, 1},     // 37: 18, Sched 1
+    {64, 64, 32, 2, 1},     // 38: 3, Sched 1 + streaming stores
+    {64, 64, 16, 2, 1},     // 39: 18, Sched 1 + streaming stores
+    {64, 32, 32, 2, 2},     // 40: 14, Sched 1 + streaming stores
+    {64, 64, 64, 2, 4, 16}, // 41: 22, Sched 1 + streaming stores
+    {64, 64, 32, 2, 2, 8}, // 42: 20, Sched 1 + streaming stores
+    {32, 64, 32, 1, 2},    // 43: 13, Sched 1 + streaming stores
+    {32, 32, 32, 1, 4},    // 44: 15, Sched 1 + streaming stores
+    {128, 128, 16, 2, 1},  // 45: 0, Sched 1 + streaming stores
+    {128, 64, 32, 2, 1},   // 46: 1, Sched 1 + streaming stores
+    {64, 64, 64, 2, 1},    // 47: 8, Sched 1 + streaming stores
+    {64, 64, 32, 2, 1},    // 48: 11, Sched 1 + streaming stores
+    {64, 32, 64, 2, 2},    // 49: 21, Sched 1 + streaming stores
+    {64, 64, 64, 2, 2, 8}, // 50: 23, Sched 1 + streaming stores
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
 using T0 = Tile<128, 128, 16, 2, 1>;
@@ -1054,6 +1078,19 @@ using T34 = Sched<T11, 1>;
 using T35 = Sched<T21, 1>;
 using T36 = Sched<T23, 1>;
 using T37 = Sched<T18, 1>;
+using T38 = Sched<T3, 5>;
+using T39 = Sched<T18, 5>;
+using T40 = Sched<T14, 5>;
+using T41 = Sched<T22, 5>;
+using T42 = Sched<T20, 5>;
+using T43 = Sched<T13, 5>;
+using T44 = Sched<T15, 5>;
+using T45 = Sched<T0, 5>;
+using T46 = Sched<T1, 5>;
+using T47 = Sched<T8, 5>;
+using T48 = Sched<T11, 5>;
+using T49 = Sched<T21, 5>;
+using T50 = Sched<T23, 5>;
 
 template <class T, int LA, int LB>
 static void launch_t(const GemmArgs &a, int grid, bool vec, hipStream_t st)
@@ -1319,7 +1356,9 @@ static int g_cand[4] = {24, 26, -1, -1};  // 64x64, then 64x32 (2 x 2 waves), bo
 static int g_rtarget = 512;
 static int g_erps = 1024;                // expert TN slice (TLG_EXPERT_RPS)
 static int g_expert_cfg = -1;            // expert tile shape pinned (TLG_EXPERT_CFG: 3, 14, 15, 18, 22)
-static int g_expert_sched = 1;           // expert tiles in the Sched<.., 1> order (TLG_EXPERT_SCHED=0: not)
+static int g_expert_sched = 1;           // expert tiles: 0 the compiler's order, 1 Sched<.., 1>, 2 Sched<.., 5>
+                                         // (that order with streaming stores: MoE kept pair 0.232 -> 0.237 ms,
+                                         // training step 2.003 -> 1.995 ms) (TLG_EXPERT_SCHED)
 static int g_expert_bk16 = 1;            // 64x64 expert tiles with 16-step stages (TLG_EXPERT_BK16=0: 32-step)
 static int g_expert_w16 = 0;             // 16-wave 64x64 tiles for launches short of 64x64 items (TLG_EXPERT_W16=1;
                                          // measured slower: kept MoE pair 0.2345 -> 0.2489 ms)
@@ -1350,7 +1389,7 @@ static void group_env(void)
     e = getenv("TLG_EXPERT_CFG");
     if (e && (atoi(e) == 3 || atoi(e) == 14 || atoi(e) == 15 || atoi(e) == 18 || atoi(e) == 22))
         g_expert_cfg = atoi(e);
-    if ((e = getenv("TLG_EXPERT_SCHED"))) g_expert_sched = atoi(e) != 0;
+    if ((e = getenv("TLG_EXPERT_SCHED")) && atoi(e) >= 0 && atoi(e) <= 2) g_expert_sched = atoi(e);
     if ((e = getenv("TLG_EXPERT_W16"))) g_expert_w16 = atoi(e) != 0;
     if ((e = getenv("TLG_EXPERT_BK16"))) g_expert_bk16 = atoi(e) != 0;
     e = getenv("TLG_GROUP_RTARGET");
@@ -1412,6 +1451,19 @@ static void launch_group(int ci, const GroupArgs &a, int grid, hipStream_t st)
     case 35: lgroup<T35>(a, grid, st); break;
     case 36: lgroup<T36>(a, grid, st); break;
     case 37: lgroup<T37>(a, grid, st); break;
+    case 38: lgroup<T38>(a, grid, st); break;
+    case 39: lgroup<T39>(a, grid, st); break;
+    case 40: lgroup<T40>(a, grid, st); break;
+    case 41: lgroup<T41>(a, grid, st); break;
+    case 42: lgroup<T42>(a, grid, st); break;
+    case 43: lgroup<T43>(a, grid, st); break;
+    case 44: lgroup<T44>(a, grid, st); break;
+    case 45: lgroup<T45>(a, grid, st); break;
+    case 46: lgroup<T46>(a, grid, st); break;
+    case 47: lgroup<T47>(a, grid, st); break;
+    case 48: lgroup<T48>(a, grid, st); break;
+    case 49: lgroup<T49>(a, grid, st); break;
+    case 50: lgroup<T50>(a, grid, st); break;
     default: lgroup<T3>(a, grid, st); break;
     }
     g_group_last = ci;
@@ -1438,7 +1490,7 @@ extern "C" int tlg_tune_group_policy(const int *cands, int ncands, double min_wa
 extern "C" int tlg_tune_expert(int cfg, int sched)
 {
     group_env();
-    if ((cfg != -1 && cfg != 3 && cfg != 14 && cfg != 15 && cfg != 18 && cfg != 22) || (sched != 0 && sched != 1))
+    if ((cfg != -1 && cfg != 3 && cfg != 14 && cfg != 15 && cfg != 18 && cfg != 22) || sched < 0 || sched > 2)
         return tlg_fail(TLG_EINVAL, "tlg_tune_expert: config %d, order %d", cfg, sched);
     g_expert_cfg = cfg;
     g_expert_sched = sched;
@@ -1498,6 +1550,19 @@ const char *tlg_group_kernel_name(void)
     case 35: return "k_group<Sched<Tile<64, 32, 64, 2, 2, 2, 0, 4>, 1> >";
     case 36: return "k_group<Sched<Tile<64, 64, 64, 2, 2, 2, 0, 8>, 1> >";
     case 37: return "k_group<Sched<Tile<64, 64, 16, 2, 1, 2, 0, 4>, 1> >";
+    case 38: return "k_group<Sched<Tile<64, 64, 32, 2, 1, 2, 0, 4>, 5> >";
+    case 39: return "k_group<Sched<Tile<64, 64, 16, 2, 1, 2, 0, 4>, 5> >";
+    case 40: return "k_group<Sched<Tile<64, 32, 32, 2, 2, 2, 0, 4>, 5> >";
+    case 41: return "k_group<Sched<Tile<64, 64, 64, 2, 4, 2, 0, 16>, 5> >";
+    case 42: return "k_group<Sched<Tile<64, 64, 32, 2, 2, 2, 0, 8>, 5> >";
+    case 43: return "k_group<Sched<Tile<32, 64, 32, 1, 2, 2, 0, 4>, 5> >";
+    case 44: return "k_group<Sched<Tile<32, 32, 32, 1, 4, 2, 0, 4>, 5> >";
+    case 45: return "k_group<Sched<Tile<128, 128, 16, 2, 1, 2, 0, 4>, 5> >";
+    case 46: return "k_group<Sched<Tile<128, 64, 32, 2, 1, 2, 0, 4>, 5> >";
+    case 47: return "k_group<Sched<Tile<64, 64, 64, 2, 1, 2, 0, 4>, 5> >";
+    case 48: return "k_group<Sched<Tile<64, 64, 32, 2, 1, 3, 1, 4>, 5> >";
+    case 49: return "k_group<Sched<Tile<64, 32, 64, 2, 2, 2, 0, 4>, 5> >";
+    case 50: return "k_group<Sched<Tile<64, 64, 64, 2, 2, 2, 0, 8>, 5> >";
     default: return "k_group<Tile<64, 64, 32, 2, 1, 2, 0, 4> >";
     }
 }
@@ -1534,7 +1599,7 @@ static int add_reductions(GroupArgs &a)
     return TLG_OK;
 }
 
-int tlg_group_pending(void) { return g_npending; }
+int tlg_group_pending(void);     // (below: the queued reductions and the held expert ones)
 
 // Queue C[0, No) (beta ? += : =) sum over z of part[z][0, No) (z < splits,
 // No % 4 == 0, 16-byte aligned rows) to ride along in the next grouped or
@@ -1872,6 +1937,29 @@ static int ecarry_flush_with_pending(hipStream_t st, bool *done)
     return TLG_OK;
 }
 
+int tlg_group_pending(void) { return g_npending + g_ecarry.nprob; }
+
+// Every queued reduction (and an expert launch's held carry) launched now,
+// each on the stream its partials were written on: what tlg_dev_free runs
+// before it releases memory that queued work may read or write.
+int tlg_group_flush_all(void)
+{
+    if (g_ecarry.nprob) {
+        const int rc = tlg_group_flush_launch(g_ecarry_st);
+        if (rc) return rc;
+    }
+    return g_npending ? tlg_group_flush_launch(g_pending_st) : TLG_OK;
+}
+
+// Queued work whose partials were written on `st` launched now, on `st`:
+// what tlg_stream_destroy runs before the handle goes away.
+int tlg_group_flush_stream(hipStream_t st)
+{
+    if ((g_ecarry.nprob && g_ecarry_st == st) || (g_npending && g_pending_st == st))
+        return tlg_group_flush_launch(st);
+    return TLG_OK;
+}
+
 // Shutdown: the queued reductions (and an expert launch's held carry) run
 // on `st` while the workspace they read still exists; then the queue is
 // empty and the workspace halves start over, so nothing queued before a
@@ -2074,18 +2162,20 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     // bound by one per expert problem
     static_assert(sizeof(GroupArgs) <= 4096, "kernel arguments");
     const dim3 eg(group_grid(a) + 8 * n);
-    switch (ci + (g_expert_sched ? 100 : 0)) {
-    case 3: hipLaunchKernelGGL((k_expert_group<T3>), eg, dim3(T3::THREADS), 0, st, group_seal(a)); break;
-    case 15: hipLaunchKernelGGL((k_expert_group<T15>), eg, dim3(T15::THREADS), 0, st, group_seal(a)); break;
-    case 14: hipLaunchKernelGGL((k_expert_group<T14>), eg, dim3(T14::THREADS), 0, st, group_seal(a)); break;
-    case 18: hipLaunchKernelGGL((k_expert_group<T18>), eg, dim3(T18::THREADS), 0, st, group_seal(a)); break;
-    case 22: hipLaunchKernelGGL((k_expert_group<T22>), eg, dim3(T22::THREADS), 0, st, group_seal(a)); break;
-    case 118: hipLaunchKernelGGL((k_expert_group<T37>), eg, dim3(T37::THREADS), 0, st, group_seal(a)); break;
-    case 122: hipLaunchKernelGGL((k_expert_group<T28>), eg, dim3(T28::THREADS), 0, st, group_seal(a)); break;
-    case 103: hipLaunchKernelGGL((k_expert_group<T24>), eg, dim3(T24::THREADS), 0, st, group_seal(a)); break;
-    case 115: hipLaunchKernelGGL((k_expert_group<T30>), eg, dim3(T30::THREADS), 0, st, group_seal(a)); break;
-    default: hipLaunchKernelGGL((k_expert_group<T26>), eg, dim3(T26::THREADS), 0, st, group_seal(a)); break;
+    // +100: the Sched<.., 1> order; +200: that order with streaming stores
+    const int key = ci + 100 * g_expert_sched;
+#define TLG_EXPERT_CASE(k, TT)                                                                                  \
+    case k: hipLaunchKernelGGL((k_expert_group<TT>), eg, dim3(TT::THREADS), 0, st, group_seal(a)); break;
+    switch (key) {
+    TLG_EXPERT_CASE(3, T3) TLG_EXPERT_CASE(14, T14) TLG_EXPERT_CASE(15, T15) TLG_EXPERT_CASE(18, T18)
+    TLG_EXPERT_CASE(22, T22)
+    TLG_EXPERT_CASE(103, T24) TLG_EXPERT_CASE(114, T26) TLG_EXPERT_CASE(115, T30) TLG_EXPERT_CASE(118, T37)
+    TLG_EXPERT_CASE(122, T28)
+    TLG_EXPERT_CASE(203, T38) TLG_EXPERT_CASE(214, T40) TLG_EXPERT_CASE(215, T44) TLG_EXPERT_CASE(218, T39)
+    TLG_EXPERT_CASE(222, T41)
+    default: return tlg_fail(TLG_EINVAL, "expert launch: no kernel for tile form %d", key);
     }
+#undef TLG_EXPERT_CASE
     TLG_HIP(hipGetLastError());
     if (red.nprob && (carry & TLG_ECARRY_OUT) && !dense && g_npending == 0) {
         g_ecarry = red;                  // the next expert launch runs them

@@ -47,6 +47,8 @@ int tlg_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len, int *s
 int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st);
 int tlg_group_flush_launch(hipStream_t st);
 int tlg_group_drain(hipStream_t st);
+int tlg_group_flush_all(void);
+int tlg_group_flush_stream(hipStream_t st);
 int tlg_defer_colsum(const float *part, float *C, int splits, int No, int beta, hipStream_t st);
 
 // One GEMM over every expert of a top-1 MoE layer whose token rows are
