@@ -1099,9 +1099,30 @@ static void launch_t(const GemmArgs &a, int grid, bool vec, hipStream_t st)
     else     hipLaunchKernelGGL((k_gemm<T, LA, LB, false>), dim3(grid), dim3(256), 0, st, a);
 }
 
+// Single-call launches of the automatic plan's shapes (0-3) in the Sched<.., 5>
+// form (a stage's fragment reads before its MFMAs, streaming stores) unless
+// TLG_GEMM_SCHED=0.
+static int g_gemm_sched = -1;
+static bool gemm_sched(void)
+{
+    if (g_gemm_sched < 0) {
+        const char *e = getenv("TLG_GEMM_SCHED");
+        g_gemm_sched = (e && *e) ? (atoi(e) != 0) : 1;
+    }
+    return g_gemm_sched != 0;
+}
+
 template <int LA, int LB>
 static void launch_kind(int ci, const GemmArgs &a, int grid, bool vec, hipStream_t st)
 {
+    if (ci <= 3 && gemm_sched()) {
+        switch (ci) {
+        case 0: launch_t<Sched<T0, 5>, LA, LB>(a, grid, vec, st); return;
+        case 1: launch_t<Sched<T1, 5>, LA, LB>(a, grid, vec, st); return;
+        case 2: launch_t<Sched<T2, 5>, LA, LB>(a, grid, vec, st); return;
+        default: launch_t<Sched<T3, 5>, LA, LB>(a, grid, vec, st); return;
+        }
+    }
     switch (ci) {
     case 0: launch_t<T0, LA, LB>(a, grid, vec, st); break;
     case 1: launch_t<T1, LA, LB>(a, grid, vec, st); break;
@@ -1186,8 +1207,12 @@ int tlg_describe(TlgKind kind, int Mo, int No, int R, char *buf, int len, int *s
     const int la = (kind == TLG_TN) ? OC : RC;
     const int lb = (kind == TLG_NT) ? RC : OC;
     const bool vec = (la == RC ? (R % 4 == 0) : (Mo % 4 == 0)) && (lb == RC ? (R % 4 == 0) : (No % 4 == 0));
-    snprintf(buf, (size_t)len, "k_gemm<Tile<%d, %d, %d, %d, %d, 2, 0, 4>, %d, %d, %s>", c.bm, c.bn, c.bk, c.wgm,
-             c.wk, la, lb, vec ? "true" : "false");
+    if (p.ci <= 3 && gemm_sched())
+        snprintf(buf, (size_t)len, "k_gemm<Sched<Tile<%d, %d, %d, %d, %d, 2, 0, 4>, 5>, %d, %d, %s>", c.bm, c.bn,
+                 c.bk, c.wgm, c.wk, la, lb, vec ? "true" : "false");
+    else
+        snprintf(buf, (size_t)len, "k_gemm<Tile<%d, %d, %d, %d, %d, 2, 0, 4>, %d, %d, %s>", c.bm, c.bn, c.bk,
+                 c.wgm, c.wk, la, lb, vec ? "true" : "false");
     if (splits) *splits = p.splits;
     return TLG_OK;
 }
