@@ -34,6 +34,22 @@
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// The attention loops that feed each MFMA one LDS element (P V, dS K, P^T dO,
+// dS^T Q): left alone the compiler issues each read right before the MFMA
+// that consumes it, so at two waves per SIMD every MFMA pair waits out an LDS
+// round trip.  Called at the end of such a loop's scheduling region, this
+// asks for every LDS read of the region first, then its MFMAs.
+#ifndef TLG_ATT_SCHED
+#define TLG_ATT_SCHED 1
+#endif
+__device__ __forceinline__ void at_reads_first()
+{
+#if TLG_ATT_SCHED
+    __builtin_amdgcn_sched_group_barrier(0x100, 64, 0);    // LDS reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 64, 0);    // MFMAs
+#endif
+}
+
 static inline unsigned grid_for(size_t work, size_t per_block, unsigned cap)
 {
     size_t b = (work + per_block - 1) / per_block;
@@ -1171,6 +1187,7 @@ __global__ __launch_bounds__(512) void k_attn_fwd4(const float *__restrict__ q, 
 #pragma unroll
             for (int r = 0; r < 16; r++)
                 o = __builtin_amdgcn_mfma_f32_32x32x2f32(Vb[at_row(r, lane) * A4_LD + lq], p[r], o, 0, 0, 0);
+            at_reads_first();
             m = mn;
         }
     }
@@ -1297,6 +1314,7 @@ __device__ __forceinline__ void attn_dq4_item(float *__restrict__ lds, int item,
 #pragma unroll
             for (int r = 0; r < 16; r++)
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(Kb[at_row(r, lane) * A4_LD + lq], ds[r], acc, 0, 0, 0);
+            at_reads_first();
         }
     }
     __syncthreads();
@@ -1479,12 +1497,16 @@ __device__ __forceinline__ void attn_dkv4_item(float *__restrict__ Sm, int item,
                 ds[r] = vis ? p * (dp[r] - dr) * scale : 0.f;
             }
             // dV[s][d] += sum_q P[q][s] dO[q][d];  dK[s][d] += sum_q dS[q][s] Q[q][d]
+#if TLG_ATT_SCHED
+            __builtin_amdgcn_sched_barrier(0);      // this loop is a region of its own
+#endif
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int x = at_row(r, lane);
                 av = __builtin_amdgcn_mfma_f32_32x32x2f32(pp[r], Dw[x * A4_LD + lq], av, 0, 0, 0);
                 ak = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[r], Qw[x * A4_LD + lq], ak, 0, 0, 0);
             }
+            at_reads_first();
         }
         __syncthreads();
     }
