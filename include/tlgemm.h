@@ -173,9 +173,10 @@ int tlg_tune_group_split(int rtarget);
  * 3 x 256 of them, else 64x32, else 32x32), or 3 (64x64), 18 (64x64, 16-step
  * stages), 14 (64x32), 15 (32x32), 22 (16-wave 64x64, whose waves split each
  * 64-step stage four ways) pinned;
- * sched 1 = each stage's fragment reads issued before its MFMAs (the
- * default), 2 = that order with the outputs written by streaming stores, 0 =
- * the compiler's order.  Applies to later launches. */
+ * sched 1 = each stage's fragment reads issued before its MFMAs, 2 = that
+ * order with the outputs written by streaming stores, 0 = the compiler's
+ * order, -1 = automatic (2 for the fused SwiGLU launches of dense rows, 1 for
+ * MoE launches).  Applies to later launches. */
 int tlg_tune_expert(int cfg, int sched);
 
 /* ---- top-1 mixture-of-experts FFN --------------------------------------- */

@@ -252,7 +252,7 @@ def test_expert_tile_forms(lib, orc, cfg, sched):
             assert_delta(got[0] - c["fin"], o64 - c["fin"], o64)
             check_backward(dfn, grads, r_dfn, ref_g, g0, (dfn64, g64))
     finally:
-        lib.check(lib.tlg_tune_expert(-1, 1), "tune expert")
+        lib.check(lib.tlg_tune_expert(-1, -1), "tune expert")
     assert lib.tlg_tune_expert(8, 1) != 0 and lib.tlg_tune_expert(3, 3) != 0
 
 

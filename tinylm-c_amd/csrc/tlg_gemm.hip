@@ -1381,9 +1381,11 @@ static int g_cand[4] = {24, 26, -1, -1};  // 64x64, then 64x32 (2 x 2 waves), bo
 static int g_rtarget = 512;
 static int g_erps = 1024;                // expert TN slice (TLG_EXPERT_RPS)
 static int g_expert_cfg = -1;            // expert tile shape pinned (TLG_EXPERT_CFG: 3, 14, 15, 18, 22)
-static int g_expert_sched = 1;           // expert tiles: 0 the compiler's order, 1 Sched<.., 1>, 2 Sched<.., 5>
-                                         // (that order with streaming stores: MoE kept pair 0.232 -> 0.237 ms,
-                                         // training step 2.003 -> 1.995 ms) (TLG_EXPERT_SCHED)
+static int g_expert_sched = -1;          // expert tiles: 0 the compiler's order, 1 Sched<.., 1>, 2 Sched<.., 5>
+                                         // (that order with streaming stores), -1 automatic: 2 for launches of
+                                         // dense rows (the training step's fused SwiGLU: 2.003 -> 1.995 ms), 1 for
+                                         // MoE launches (streaming measured 0.232 -> 0.237 ms per kept pair: the
+                                         // next launch reads their g, u, a, y right away) (TLG_EXPERT_SCHED)
 static int g_expert_bk16 = 1;            // 64x64 expert tiles with 16-step stages (TLG_EXPERT_BK16=0: 32-step)
 static int g_expert_w16 = 0;             // 16-wave 64x64 tiles for launches short of 64x64 items (TLG_EXPERT_W16=1;
                                          // measured slower: kept MoE pair 0.2345 -> 0.2489 ms)
@@ -1414,7 +1416,7 @@ static void group_env(void)
     e = getenv("TLG_EXPERT_CFG");
     if (e && (atoi(e) == 3 || atoi(e) == 14 || atoi(e) == 15 || atoi(e) == 18 || atoi(e) == 22))
         g_expert_cfg = atoi(e);
-    if ((e = getenv("TLG_EXPERT_SCHED")) && atoi(e) >= 0 && atoi(e) <= 2) g_expert_sched = atoi(e);
+    if ((e = getenv("TLG_EXPERT_SCHED")) && atoi(e) >= -1 && atoi(e) <= 2) g_expert_sched = atoi(e);
     if ((e = getenv("TLG_EXPERT_W16"))) g_expert_w16 = atoi(e) != 0;
     if ((e = getenv("TLG_EXPERT_BK16"))) g_expert_bk16 = atoi(e) != 0;
     e = getenv("TLG_GROUP_RTARGET");
@@ -1515,7 +1517,7 @@ extern "C" int tlg_tune_group_policy(const int *cands, int ncands, double min_wa
 extern "C" int tlg_tune_expert(int cfg, int sched)
 {
     group_env();
-    if ((cfg != -1 && cfg != 3 && cfg != 14 && cfg != 15 && cfg != 18 && cfg != 22) || sched < 0 || sched > 2)
+    if ((cfg != -1 && cfg != 3 && cfg != 14 && cfg != 15 && cfg != 18 && cfg != 22) || sched < -1 || sched > 2)
         return tlg_fail(TLG_EINVAL, "tlg_tune_expert: config %d, order %d", cfg, sched);
     g_expert_cfg = cfg;
     g_expert_sched = sched;
@@ -2188,7 +2190,7 @@ int tlg_expert_launch(const TlgExpertCall *calls, int n, const int *eoff, int E,
     static_assert(sizeof(GroupArgs) <= 4096, "kernel arguments");
     const dim3 eg(group_grid(a) + 8 * n);
     // +100: the Sched<.., 1> order; +200: that order with streaming stores
-    const int key = ci + 100 * g_expert_sched;
+    const int key = ci + 100 * (g_expert_sched >= 0 ? g_expert_sched : dense ? 2 : 1);
 #define TLG_EXPERT_CASE(k, TT)                                                                                  \
     case k: hipLaunchKernelGGL((k_expert_group<TT>), eg, dim3(TT::THREADS), 0, st, group_seal(a)); break;
     switch (key) {
