@@ -124,6 +124,15 @@ typedef struct {
                               * that follows mm in the reference (tinylm.c:994-995,
                               * :1009-1010) fused into the store; R [M x N] is
                               * read, not written, and may not alias C */
+    /* mm_bt with beta 0 only, optional (both or neither): dotOut[i][b] =
+     * sum_{c < 32} dX[i][32 b + c] dotB[i][32 b + c] for every 32-column block
+     * b of dX (K % 32 == 0; dotB [M x K] 16-byte aligned, not C; dotOut
+     * [M x K/32]), each a 16-term fma chain over c < 16, another over c >= 16,
+     * then their sum.  The attention backward's D = dO . O per row and head
+     * (tinylm.c:750-768) made in the O-projection backward that forms dO (no
+     * counterpart). */
+    const float *dotB;
+    float *dotOut;
 } TlgGemmCall;
 int tlg_dev_gemm_group(const TlgGemmCall *calls, int n, void *stream);
 

@@ -90,6 +90,13 @@ int tlg_dev_attn_fwd_rope(const float *q, const float *k, const float *v, float 
 int tlg_dev_attn_bwd_rope(const float *q, const float *k, const float *v, const float *out, const float *lse,
                           const float *datt, float *dq, float *dk, float *dv, int B, int T, int H, int KV, int hd,
                           int win, const float *cos_t, const float *sin_t, void *stream);
+/* tlg_dev_attn_bwd_rope with the per-row term D[r][h] = datt[r][h] . out[r][h]
+ * (tinylm.c:750-768; [B*T][H]) given, as the O-projection backward's grouped
+ * launch forms it (TlgGemmCall.dotB / dotOut, include/tlgemm.h), so the
+ * backward starts with its dQ / dK / dV launch (no counterpart as one call). */
+int tlg_dev_attn_bwd_rope_d(const float *q, const float *k, const float *v, const float *out, const float *lse,
+                            const float *datt, const float *D, float *dq, float *dk, float *dv, int B, int T, int H,
+                            int KV, int hd, int win, const float *cos_t, const float *sin_t, void *stream);
 
 /* residual adds, tinylm.c:994-995, :1009-1010, :1062: y[i] += x[i]. */
 int tlg_dev_add(float *y, const float *x, size_t n, void *stream);

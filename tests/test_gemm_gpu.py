@@ -247,6 +247,57 @@ def test_group_ragged_tiles(lib, gcfg):
     assert normwise_rel(dw.cpu().numpy() - G, X64.T @ dY64) <= TOL, (gcfg, name, "mm_atb")
 
 
+@pytest.mark.parametrize("gcfg", [-1, 3, 24, 38, 39, 14, 40, 20, 22, 41, 15, 44, 13, 0, 45, 1])
+def test_group_block_dot(lib, gcfg):
+    """An mm_bt with the block-dot epilogue (TlgGemmCall.dotB / dotOut): dX as
+    without it, and dotOut[i][b] = the dot of dX's and dotB's 32-column block b
+    of row i, against fp64; on every kind of tile (one and several wave groups
+    per stage, the 128 x 128 shapes falling back to 64 x 64), a ragged row count,
+    beside an mm_atb of the same launch.  The attention backward's D =
+    dO . O per row and head (tinylm.c:750-768)."""
+    t = _torch()
+    for M, K, N in ((4096, 256, 256), (777, 96, 132)):
+        dY = seeded((M, N), 0.1, f"bdY{M}")
+        W = seeded((K, N), 0.02, f"bdW{M}")
+        O = seeded((M, K), 1.0, f"bdO{M}")
+        X = seeded((M, K), 1.0, f"bdX{M}")
+        G = seeded((K, N), 1.0, f"bdG{M}")
+        dy, w, o, x = dev(dY), dev(W), dev(O), dev(X)
+        dx = t.full((M, K), float("nan"), device="cuda")
+        d = t.full((M, K // 32), float("nan"), device="cuda")
+        dw = dev(G)
+        if gcfg >= 0:
+            lib.check(lib.tlg_tune_group(gcfg), "tune")
+        try:
+            lib.group([dict(op="mm_bt", beta=0, C=dx.data_ptr(), M=M, K=K, N=N, A=[dy.data_ptr()], B=[w.data_ptr()],
+                            dotB=o.data_ptr(), dotOut=d.data_ptr()),
+                       dict(op="mm_atb", beta=1, C=dw.data_ptr(), M=M, K=K, N=N, A=[x.data_ptr()],
+                            B=[dy.data_ptr()])], stream())
+        finally:
+            lib.check(lib.tlg_tune_group(-1), "tune")
+        want = dY.astype(np.float64) @ W.astype(np.float64).T
+        got = dx.cpu().numpy()
+        assert normwise_rel(got, want) <= TOL, (gcfg, M)
+        # D from the stored dX (the chains the epilogue runs, in its order)
+        ref = np.empty((M, K // 32), np.float32)
+        g32, o32 = got.reshape(M, K // 32, 32), O.reshape(M, K // 32, 32)
+        h0 = np.zeros((M, K // 32), np.float32)
+        h1 = np.zeros((M, K // 32), np.float32)
+        for c in range(16):
+            h0 = (h0.astype(np.float64) + g32[:, :, c].astype(np.float64) * o32[:, :, c]).astype(np.float32)
+            h1 = (h1.astype(np.float64) + g32[:, :, 16 + c].astype(np.float64) * o32[:, :, 16 + c]).astype(np.float32)
+        ref = h0 + h1
+        dd = d.cpu().numpy()
+        assert normwise_rel(dd, ref) <= 1e-6, (gcfg, M)
+        d64 = (want.reshape(M, K // 32, 32) * O.reshape(M, K // 32, 32)).sum(-1)
+        assert normwise_rel(dd, d64) <= TOL, (gcfg, M)
+        assert normwise_rel(dw.cpu().numpy() - G, X.astype(np.float64).T @ dY.astype(np.float64)) <= TOL
+    bad = [dict(op="mm_bt", beta=1, C=dx.data_ptr(), M=M, K=K, N=N, A=[dy.data_ptr()], B=[w.data_ptr()],
+                dotB=o.data_ptr(), dotOut=d.data_ptr())]
+    with pytest.raises(Exception):
+        lib.group(bad, stream())
+
+
 def _one_alloc(parts):
     """Matrices laid out back to back in one device allocation, as
     map_weights lays out wq | wk | wv and w1 | w3 (tinylm.c:361-393)."""

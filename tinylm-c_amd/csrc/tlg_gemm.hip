@@ -391,8 +391,10 @@ __device__ __forceinline__ void tile_accumulate(float *__restrict__ smem, const 
 // row 8*(v/4) + 4*(l/32) + v%4, column l%32.  With WK > 1 the wave groups'
 // partial tiles go through `red` (LDS, WK*BM*BN floats, free once
 // tile_accumulate has returned) and are summed in wave-group order, so the
-// result does not depend on timing.
-template <class T, class Put>
+// result does not depend on timing.  STASH: every element's value (valid
+// or not) is also left in red[f], f its fragment-order index (below), for a
+// row-wise epilogue after the next barrier; red must hold TILE floats.
+template <class T, bool STASH = false, class Put>
 __device__ __forceinline__ void tile_epi(const f32x16 (&accs)[T::FM][T::FN][T::NCH], int Mo, int No, int i0,
                                          int j0, float *__restrict__ red, Put put)
 {
@@ -409,6 +411,16 @@ __device__ __forceinline__ void tile_epi(const f32x16 (&accs)[T::FM][T::FN][T::N
     if constexpr (T::WK == 1) {
         const int wm = T::wm(), wn = T::wn();
         const int h = lane >> 5, col = lane & 31;
+        if constexpr (STASH) {
+            const int g = T::wave() % (T::WGM * T::WGN);
+#pragma unroll
+            for (int a = 0; a < T::FM; a++)
+#pragma unroll
+                for (int b = 0; b < T::FN; b++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++)
+                        red[(((g * T::FM + a) * T::FN + b) * 16 + v) * 64 + lane] = acc[a][b][v];
+        }
 #pragma unroll
         for (int a = 0; a < T::FM; a++)
 #pragma unroll
@@ -443,6 +455,7 @@ __device__ __forceinline__ void tile_epi(const f32x16 (&accs)[T::FM][T::FN][T::N
             const int i = i0 + (gg / T::WGN) * T::WM + a * 32 + 8 * (v >> 2) + 4 * (l >> 5) + (v & 3);
             const int j = j0 + (gg % T::WGN) * T::WN + b * 32 + (l & 31);
             if (i < Mo && j < No) put(i, j, s);
+            if constexpr (STASH) red[f] = s;     // only this thread reads slot f of slice 0
         }
         __syncthreads();            // `red` aliases the stage buffers of the next tile
     }
@@ -468,6 +481,63 @@ __device__ __forceinline__ void tile_store(const f32x16 (&accs)[T::FM][T::FN][T:
         float *p = C + (size_t)i * ldc + j;
         st_out<T>(p, beta ? (*p + v) : v);
     });
+}
+
+// C = acc (beta 0) and, for every 32-column block of each valid row, the dot
+// product of the block with the same block of O:  out[i][j / 32] =
+// sum_{c < 32} C[i][32 (j / 32) + c] O[i][32 (j / 32) + c] (O with C's row
+// stride, out [Mo][No / 32]).  This is the attention backward's per-row term
+// D = dO . O of each 32-wide head (tinylm.c:750-768) formed where dO is made
+// (the O-projection backward's dX tile), in the dQ item's order: two 16-term
+// fma chains, then their sum.  Needs No % 32 == 0 and TILE <= the LDS the
+// tile's stages use (every shape but the 128 x 128 ones; the host checks).
+template <class T>
+__device__ __forceinline__ void tile_store_dot(const f32x16 (&accs)[T::FM][T::FN][T::NCH], float *__restrict__ C,
+                                               int ldc, int Mo, int No, int i0, int j0, const float *__restrict__ O,
+                                               float *__restrict__ out, float *__restrict__ red)
+{
+    if constexpr (T::TILE <= T::lds_max()) {
+        tile_epi<T, true>(accs, Mo, No, i0, j0, red,
+                          [&](int i, int j, float v) { st_out<T>(C + (size_t)i * ldc + j, v); });
+        __syncthreads();
+        // eight lanes per (row, block), lane q holding float4 q of the block
+        // (a wave's O loads: eight 128-byte row segments); each half's chain
+        // passes through its four lanes in order, lane q continuing the sum
+        // lane q - 1 ended with.  Every count here is a multiple of 64, so
+        // whole waves take part in the shuffles.
+        constexpr int NB = T::BN / 32;
+        static_assert(T::BM * NB * 8 % 64 == 0, "whole waves");
+        const int q = threadIdx.x & 7;
+        for (int p8 = threadIdx.x; p8 < T::BM * NB * 8; p8 += T::THREADS) {
+            const int p = p8 >> 3, row = p / NB, cb = p % NB;
+            const int i = i0 + row, jb = j0 + cb * 32;
+            // fragment-order index of (row, column 0 of block cb)
+            const int rr = row % T::WM, a = rr / 32, r32 = rr % 32;
+            const int v = 4 * (r32 >> 3) + (r32 & 3), hb = (r32 >> 2) & 1;
+            const int b = ((cb * 32) % T::WN) / 32;
+            const int g = (row / T::WM) * T::WGN + (cb * 32) / T::WN;
+            const f32x4 x = *reinterpret_cast<const f32x4 *>(
+                red + ((((g * T::FM + a) * T::FN + b) * 16 + v) * 64 + hb * 32) + 4 * q);
+            const int ic = min(i, Mo - 1), jc = min(jb, No - 32);
+            const f32x4 y = *reinterpret_cast<const f32x4 *>(O + (size_t)ic * ldc + jc + 4 * q);
+            float d = 0.f;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const float in = __shfl_up(d, 1, 4);
+                if ((q & 3) == s) {
+                    float c = s ? in : 0.f;
+                    c += x[0] * y[0];
+                    c += x[1] * y[1];
+                    c += x[2] * y[2];
+                    c += x[3] * y[3];
+                    d = c;
+                }
+            }
+            const float h0 = __shfl_up(d, 4, 8);
+            if (q == 7 && i < Mo && jb < No) out[(size_t)i * (No / 32) + jb / 32] = h0 + d;
+        }
+        __syncthreads();
+    }
 }
 
 // 1 / (1 + e^-z) with the hardware exp2 and reciprocal (within a few ulp of
@@ -622,7 +692,9 @@ struct Prob {
     //         given), SwiGLU backward (da from the tile, g / u in X1 / X2
     //         replaced by dg / du; C unused), or the top-1 combine (C = out,
     //         out[omap[i]] = fin[..] + gate[..] * tile row i; X1 = the rows
-    //         themselves, sorted order, when given)
+    //         themselves, sorted order, when given); on a dense NT problem
+    //         ROWDOT: C stored, and X1 [Mo][No/32] the dot of each row's
+    //         32-column blocks with those of `fin` (tile_store_dot)
     const int *amap, *omap;
     const float *B2;
     float *X1, *X2;
@@ -834,6 +906,12 @@ __device__ __forceinline__ void group_tile(float *smem, const Prob &P, int local
             st_out<T>(C + o, Rr[o] + v);
         });
         return;
+    }
+    if constexpr (LA == RC && LB == RC) {
+        if (P.epi == TLG_EPI_ROWDOT) {
+            tile_store_dot<T>(acc, P.C, P.ldc, P.Mo, P.No, i0, j0, P.fin, P.X1, smem);
+            return;
+        }
     }
     tile_store<T>(acc, P.C, P.ldc, P.beta, P.Mo, P.No, i0, j0, smem);
 }
@@ -1729,7 +1807,8 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
     bool gemv = true;
     int mmax = 1;
     for (int i = 0; i < n && gemv; i++) {
-        gemv = (calls[i].op == 0 || calls[i].op == 1) && !calls[i].R && calls[i].M >= 1 && calls[i].M <= 8 &&
+        gemv = (calls[i].op == 0 || calls[i].op == 1) && !calls[i].R && !calls[i].dotOut && calls[i].M >= 1 &&
+               calls[i].M <= 8 &&
                calls[i].K > 0 &&
                calls[i].N > 0 && calls[i].nseg >= 1 && calls[i].nseg <= TLG_MAXSEG &&
                (calls[i].nseg == 1 || calls[i].op == 1);
@@ -1771,6 +1850,12 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
                 span(c.R, c.M, c.N, c.N, &r0, &r1);
                 hit = overlap(c0, c1, r0, r1);
             }
+            if (!hit && op == 1 && c.dotOut) {
+                const char *r0, *r1, *d0, *d1;
+                span(c.dotB, c.M, c.K, c.K, &r0, &r1);
+                span(c.dotOut, c.M, c.K / 32, c.K / 32, &d0, &d1);
+                hit = overlap(c0, c1, r0, r1) || overlap(c0, c1, d0, d1);
+            }
             if (hit) { rc = tlg_group_flush_launch(st); if (rc) return rc; break; }
         }
     }
@@ -1779,6 +1864,7 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
     Prob probs[TLG_MAXPROB / 2];
     int Rtot[TLG_MAXPROB / 2];
     int rmax = 0;
+    bool rowdot = false;
     for (int i = 0; i < n; i++) {
         const TlgGemmCall &c = calls[i];
         if (c.op == 3) {
@@ -1824,6 +1910,15 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
         P.ldc = P.No;
         if (!vec || !c.C || R == 0 || P.Mo == 0 || P.No == 0)
             return tlg_fail(TLG_EINVAL, "tlg_dev_gemm_group: call %d needs aligned, non-empty operands", i);
+        if (c.dotOut || c.dotB) {
+            if (c.op != 1 || c.beta || !c.dotOut || !c.dotB || !al16(c.dotB) || c.K % 32 || c.dotB == c.C)
+                return tlg_fail(TLG_EINVAL, "tlg_dev_gemm_group: call %d: block dot only on mm_bt with beta 0, "
+                                "K %% 32 == 0, an aligned dotB that is not C", i);
+            P.epi = TLG_EPI_ROWDOT;
+            P.fin = c.dotB;
+            P.X1 = c.dotOut;
+            rowdot = true;
+        }
         if (c.R) {
             if (c.op != 0 || !al16(c.R) || c.R == c.C)
                 return tlg_fail(TLG_EINVAL, "tlg_dev_gemm_group: call %d: residual only on mm, aligned, not C", i);
@@ -1856,6 +1951,9 @@ int tlg_group_launch(const TlgGemmCall *calls, int n, hipStream_t st)
         }
         if (ci < 0) ci = last;                 // smallest candidate
     }
+    // the block-dot epilogue stages a whole tile in the stage buffers: not on
+    // the 128 x 128 shapes, whose tile is larger than their stages
+    if (rowdot && ci >= 0 && ci < kNumCfgs && kCfgs[ci].bm * kCfgs[ci].bn > 64 * 128) ci = 38;
     // geometry of the chosen shape (the sweep variants 9-12 are 64x64 tiles)
     const TileCfg &tc = kCfgs[(ci >= 0 && ci < kNumCfgs) ? ci : 3];
 

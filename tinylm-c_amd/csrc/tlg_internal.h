@@ -59,7 +59,7 @@ int tlg_defer_colsum(const float *part, float *C, int splits, int No, int beta, 
 //   op 1 (mm_bt):  C[rows] (beta)= sum_s A_s[rows] B_{s,e}^T  (nseg <= 2)
 //   op 2 (mm_atb): C_e (beta)= A[rows]^T B[rows]          C_e = C + e*es
 // Epilogues of an expert GEMM (TlgExpertCall.epi).
-enum { TLG_EPI_STORE = 0, TLG_EPI_SWIGLU = 1, TLG_EPI_SWIGLU_BWD = 2, TLG_EPI_COMBINE = 3 };
+enum { TLG_EPI_STORE = 0, TLG_EPI_SWIGLU = 1, TLG_EPI_SWIGLU_BWD = 2, TLG_EPI_COMBINE = 3, TLG_EPI_ROWDOT = 4 };
 struct TlgExpertCall {
     int op, beta;
     float *C;

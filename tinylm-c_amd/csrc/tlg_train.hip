@@ -1998,9 +1998,11 @@ static int attn_fwd_launch(const float *q, const float *k, const float *v, float
     return TLG_OK;
 }
 
+// Dq_in: the per-row term D = dO . O [B*T][H], formed by the caller (the
+// O-projection backward's block-dot epilogue); NULL: k_attn_delta forms it.
 static int attn_bwd_launch(const float *q, const float *k, const float *v, const float *out, const float *lse,
                            const float *datt, float *dq, float *dk, float *dv, int B, int T, int H, int KV, int hd,
-                           int win, const float *cs, const float *sn, void *stream)
+                           int win, const float *cs, const float *sn, void *stream, const float *Dq_in = nullptr)
 {
     int rc = begin();
     if (rc || (rc = attn_check("attn_bwd", B, T, H, KV, hd))) return rc;
@@ -2019,9 +2021,16 @@ static int attn_bwd_launch(const float *q, const float *k, const float *v, const
     float *Dq = (float *)ws;
     // the group dK / dV items read lse rows as float4 (4 heads)
     if (g4 && cs && !al16(lse)) return tlg_fail(TLG_EINVAL, "attn_bwd_rope: lse must be 16-byte aligned");
+    if (Dq_in && !(g4 && al16(lse)))
+        return tlg_fail(TLG_EINVAL, "attn_bwd: a given D needs H / KV a multiple of 4 and an aligned lse");
     if (g4 && al16(lse)) {
-        // Dq first; then the dK / dV and dQ items of every group in one launch
-        hipLaunchKernelGGL(k_attn_delta, dim3((B * T * H + 31) / 32), dim3(256), 0, st, datt, out, Dq, B * T * H);
+        // Dq first (unless given); then the dK / dV and dQ items of every
+        // group in one launch
+        if (Dq_in)
+            Dq = const_cast<float *>(Dq_in);
+        else
+            hipLaunchKernelGGL(k_attn_delta, dim3((B * T * H + 31) / 32), dim3(256), 0, st, datt, out, Dq,
+                               B * T * H);
         const dim3 grid(nqb * B * KV + B * KV * (H / KV / 4) * nqb);
         if (cs)
             hipLaunchKernelGGL(k_attn_bwd4<true>, grid, dim3(512), 0, st, q, k, v, out, datt, lse, (const float *)Dq,
@@ -2072,6 +2081,15 @@ extern "C" int tlg_dev_attn_bwd_rope(const float *q, const float *k, const float
 {
     if (!cos_t || !sin_t) return tlg_fail(TLG_EINVAL, "attn_bwd_rope: no rope tables");
     return attn_bwd_launch(q, k, v, out, lse, datt, dq, dk, dv, B, T, H, KV, hd, win, cos_t, sin_t, stream);
+}
+
+extern "C" int tlg_dev_attn_bwd_rope_d(const float *q, const float *k, const float *v, const float *out,
+                                       const float *lse, const float *datt, const float *D, float *dq, float *dk,
+                                       float *dv, int B, int T, int H, int KV, int hd, int win, const float *cos_t,
+                                       const float *sin_t, void *stream)
+{
+    if (!cos_t || !sin_t || !D) return tlg_fail(TLG_EINVAL, "attn_bwd_rope_d: no rope tables or no D");
+    return attn_bwd_launch(q, k, v, out, lse, datt, dq, dk, dv, B, T, H, KV, hd, win, cos_t, sin_t, stream, D);
 }
 
 static int ew(int op, size_t n, float *y, float *y2, const float *x, const float *a, const float *b, void *stream)

@@ -33,6 +33,7 @@ struct TlTrain {
     float *a_in, *a_norm, *q, *k, *v, *ctx, *f_in, *f_norm, *g, *u, *act, *a_rinv, *f_rinv, *lse, *gate, *rprobs;
     /* one each */
     float *x_final, *fn, *fn_rinv, *logits, *dl, *dout, *dfnorm, *dfin, *datt, *dq, *dk, *dv, *dnorm, *dain, *dfn;
+    float *attn_d;             /* the attention backward's D = datt . ctx [N][H] */
     /* RMSNorm backward's per-row-block gain partials; their column sum rides
      * along in the next grouped GEMM launch */
     float *rms_part;
@@ -124,7 +125,8 @@ TlTrain *tl_train_new(const TlModel *m, int B)
         {(void **)&t->act, dense ? 4 * L * NF : 0}, {(void **)&t->dfnorm, 4 * ND}, {(void **)&t->dfin, 4 * ND},
         {(void **)&t->datt, 4 * ND}, {(void **)&t->dq, 4 * ND}, {(void **)&t->dk, 4 * NK},
         {(void **)&t->dv, 4 * NK}, {(void **)&t->dnorm, 4 * ND}, {(void **)&t->dain, 4 * ND},
-        {(void **)&t->dfn, 4 * ND}, {(void **)&t->rms_part, 4 * t->rms_part_n},
+        {(void **)&t->dfn, 4 * ND}, {(void **)&t->attn_d, 4 * (size_t)N * H},
+        {(void **)&t->rms_part, 4 * t->rms_part_n},
         {(void **)&t->moe_keep, L * t->moe_keep_b},
     };
     const int ns = (int)(sizeof s / sizeof s[0]);
@@ -407,11 +409,17 @@ int tl_train_backward(TlTrain *t, void *st)
         }
         CK(tlg_dev_rmsnorm_bwd_defer(fi, P + w.an2, t->f_rinv + (size_t)l * N, t->dfnorm, dout, t->dfin,
                                      G + w.an2, N, D, t->rms_part, t->rms_part_n, st));
-        GROUP(st, BT(t->datt, 0, t->dfin, P + w.wo, N, D, D), ATB(G + w.wo, cx, t->dfin, N, D, D));
         if (rope_fused(m)) {
-            CK(tlg_dev_attn_bwd_rope(q, k, v, cx, t->lse + (size_t)l * N * H, t->datt, t->dq, t->dk, t->dv, t->B, T,
-                                     H, KV, t->hd, lwin(m, l), t->rcos, t->rsin, st));
+            /* datt = dfin Wo^T with the attention backward's D = datt . ctx per
+             * row and head formed in the same launch (:750-768) */
+            TlgGemmCall ob = BT(t->datt, 0, t->dfin, P + w.wo, N, D, D);
+            ob.dotB = cx;
+            ob.dotOut = t->attn_d;
+            GROUP(st, ob, ATB(G + w.wo, cx, t->dfin, N, D, D));
+            CK(tlg_dev_attn_bwd_rope_d(q, k, v, cx, t->lse + (size_t)l * N * H, t->datt, t->attn_d, t->dq, t->dk,
+                                       t->dv, t->B, T, H, KV, t->hd, lwin(m, l), t->rcos, t->rsin, st));
         } else {
+            GROUP(st, BT(t->datt, 0, t->dfin, P + w.wo, N, D, D), ATB(G + w.wo, cx, t->dfin, N, D, D));
             CK(tlg_dev_attn_bwd(q, k, v, cx, t->lse + (size_t)l * N * H, t->datt, t->dq, t->dk, t->dv, t->B, T, H,
                                 KV, t->hd, lwin(m, l), st));
             CK(tlg_dev_rope(t->dq, NULL, T, N, H, t->hd, t->rcos, t->rsin, T, 1, st));

@@ -96,6 +96,8 @@ SIGNATURES = {
     "tlg_dev_attn_fwd_rope": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
     "tlg_dev_attn_bwd_rope": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp,
                                    _vp]),
+    "tlg_dev_attn_bwd_rope_d": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp,
+                                     _vp, _vp]),
     "tlg_dev_add": (_i, [_vp, _vp, _sz, _vp]),
     "tlg_dev_swiglu_fwd": (_i, [_vp, _vp, _vp, _sz, _vp]),
     "tlg_dev_swiglu_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _vp]),
@@ -143,7 +145,8 @@ class TlgGemmCall(ctypes.Structure):
     """include/tlgemm.h TlgGemmCall: one call of a grouped launch."""
     _fields_ = [("op", ctypes.c_int), ("beta", ctypes.c_int), ("C", _vp),
                 ("M", ctypes.c_int), ("K", ctypes.c_int), ("N", ctypes.c_int), ("nseg", ctypes.c_int),
-                ("A", _vp * 3), ("B", _vp * 3), ("Nseg", ctypes.c_int * 3), ("R", _vp)]
+                ("A", _vp * 3), ("B", _vp * 3), ("Nseg", ctypes.c_int * 3), ("R", _vp),
+                ("dotB", _vp), ("dotOut", _vp)]
 
 
 class TlgDecGemv(ctypes.Structure):
@@ -226,6 +229,7 @@ class Lib:
             a = arr[i]
             a.op, a.beta, a.C = {"mm": 0, "mm_bt": 1, "mm_atb": 2}[c["op"]], c.get("beta", 0), c["C"]
             a.R = c.get("R", None)
+            a.dotB, a.dotOut = c.get("dotB", None), c.get("dotOut", None)
             a.M, a.K, a.N = c["M"], c["K"], c["N"]
             a.nseg = len(c["A"])
             for s_ in range(a.nseg):
