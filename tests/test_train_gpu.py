@@ -266,6 +266,7 @@ ATTN_ROPE = [  # B, T, H, KV, win: GQA groups of 4 or 8 heads
     (2, 256, 12, 3, 0),     # m8 heads
     (3, 70, 4, 1, 0),       # ragged T
     (2, 100, 8, 1, 40),     # sliding window, 8 heads per KV head
+    (1, 256, 16, 2, 0),     # 8 heads per KV head, full causal (two dQ items per dK / dV item)
     (4, 1, 4, 1, 0),        # one token
 ]
 
