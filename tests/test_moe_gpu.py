@@ -345,6 +345,42 @@ def test_kept_state_pair_is_bit_identical(lib, N, D, F, E, skew, dead):
             assert np.array_equal(x, y)
 
 
+@pytest.mark.parametrize("N,E,skew,dead", [(4096, 4, 2.0, ()), (1, 3, 0.0, ()), (67, 3, 0.0, ()),
+                                          (2500, 5, 1.0, (3,)), (5000, 64, 0.0, ()), (513, 1, 0.0, ())])
+def test_forward_index_is_a_stable_sort(lib, N, E, skew, dead):
+    """The forward's expert index (the router's per-block counts and ranks,
+    then the many-workgroup placement), read from the kept state: idx lists
+    the tokens of expert 0, then 1, .. each in ascending order (moe_forward's
+    per-expert gather, tinylm.c:876-879), pos inverts idx, eoff is the
+    prefix of the per-expert counts; against numpy's stable argsort of the
+    assignments the forward returned."""
+    print("index", N, E, flush=True)
+    t = _torch()
+    D, F = 32, 16
+    c = case(N, D, F, E, zlib.crc32(f"index {N} {E}".encode()), skew, dead)
+    ins = {k: dev(c[k]) for k in ("fnorm", "fin", "wr", "w1", "w3", "w2")}
+    out = t.full((N, D), float("nan"), dtype=t.float32, device="cuda")
+    assign = t.full((N,), -7, dtype=t.int32, device="cuda")
+    gate = t.full((N,), float("nan"), dtype=t.float32, device="cuda")
+    rprobs = t.full((N, E), float("nan"), dtype=t.float32, device="cuda")
+    nb = lib.tlg_moe_keep_bytes(N, D, F, E)
+    keep = t.full((nb // 4,), -9, dtype=t.int32, device="cuda")
+    p = {k: v.data_ptr() for k, v in ins.items()}
+    lib.moe_fwd_keep(p["fnorm"], p["fin"], out.data_ptr(), N, D, F, E, p["wr"], p["w1"], p["w3"], p["w2"],
+                     assign.data_ptr(), gate.data_ptr(), rprobs.data_ptr(), keep.data_ptr(), nb, stream())
+    k = keep.cpu().numpy()
+    al = lambda x: (x + 255) // 256 * 256 // 4          # the kept layout's 256-byte slots, in ints
+    idx, pos, eoff = k[:N], k[al(4 * N):al(4 * N) + N], k[2 * al(4 * N):2 * al(4 * N) + E + 1]
+    a = assign.cpu().numpy()
+    assert a.min() >= 0 and a.max() < E
+    want = np.argsort(a, kind="stable")
+    assert np.array_equal(idx, want)
+    assert np.array_equal(pos[want], np.arange(N))
+    assert np.array_equal(eoff, np.concatenate([[0], np.cumsum(np.bincount(a, minlength=E))]))
+    for e in dead:
+        assert eoff[e + 1] == eoff[e]
+
+
 def test_kept_state_size_checked(lib):
     import tlgemm
     t = _torch()

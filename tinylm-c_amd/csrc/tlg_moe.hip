@@ -18,8 +18,12 @@
 //   k_moe_route     router logits as the reference's own FMA chain over D
 //                   (so the argmax sees the reference's logits bit for bit),
 //                   softmax, strict-greater argmax (ties -> lowest expert)
-//   k_moe_index     stable counting sort of the tokens by expert (one
-//                   workgroup, wave ballots; no atomics)
+//   k_moe_index_blk stable counting sort of the tokens by expert: the
+//                   router workgroups leave per-block expert counts and
+//                   in-block ranks, every index workgroup sums the counts
+//                   of the blocks before its own (no atomics)
+//   k_moe_index     the same sort in one workgroup, from the assignments
+//                   alone (the recomputing backward)
 //   expert GEMMs    tlg_expert_launch (grouped MFMA tiles, every expert in
 //                   one launch; the rows per expert stay on the device),
 //                   with the MoE's elementwise steps fused in:
@@ -47,10 +51,15 @@
 // d at a time, all of D when it fits), so one round of loads serves the
 // whole chain.
 #define MOE_TOK 16
+// With bcnt, the workgroup also leaves its expert counts in bcnt[blockIdx.x]
+// [E] and each token's rank among its block's tokens of the same expert in
+// rank[n] (k_moe_index_blk's inputs).
 __global__ __launch_bounds__(256) void k_moe_route(const float *__restrict__ X, const float *__restrict__ Wr,
                                                    int N, int D, int E, int dch, float *__restrict__ rprobs,
-                                                   int *__restrict__ assign, float *__restrict__ gate)
+                                                   int *__restrict__ assign, float *__restrict__ gate,
+                                                   int *__restrict__ rank, int *__restrict__ bcnt)
 {
+    __shared__ int sel_s[MOE_TOK];
     extern __shared__ float lds_route[];
     float *xs = lds_route;                          // [MOE_TOK][dch + 1]
     float *wsm = xs + MOE_TOK * (dch + 1);          // [dch][E]
@@ -113,25 +122,43 @@ __global__ __launch_bounds__(256) void k_moe_route(const float *__restrict__ X, 
     }
     __syncthreads();
     const int t = tid, n = n0 + t;
-    if (t >= MOE_TOK || n >= N) return;
-    // softmax over all E (:862-867), then moe_route's slot 0 (:818-825)
-    const float *r = lg + t * E;
-    float *pr = rprobs + (size_t)n * E;
-    float mx = -1e30f;
-    for (int e = 0; e < E; e++) if (r[e] > mx) mx = r[e];
-    float s = 0.f;
-    for (int e = 0; e < E; e++) { const float v = expf(r[e] - mx); pr[e] = v; s += v; }
-    const float inv = 1.0f / s;
-    int best = -1;
-    float bp = -1e30f;
-    for (int e = 0; e < E; e++) {
-        const float v = pr[e] * inv;
-        pr[e] = v;
-        if (v > bp) { bp = v; best = e; }
+    if (t < MOE_TOK) {
+        int sel = -1;
+        if (n < N) {
+            // softmax over all E (:862-867), then moe_route's slot 0 (:818-825)
+            const float *r = lg + t * E;
+            float *pr = rprobs + (size_t)n * E;
+            float mx = -1e30f;
+            for (int e = 0; e < E; e++) if (r[e] > mx) mx = r[e];
+            float s = 0.f;
+            for (int e = 0; e < E; e++) { const float v = expf(r[e] - mx); pr[e] = v; s += v; }
+            const float inv = 1.0f / s;
+            int best = -1;
+            float bp = -1e30f;
+            for (int e = 0; e < E; e++) {
+                const float v = pr[e] * inv;
+                pr[e] = v;
+                if (v > bp) { bp = v; best = e; }
+            }
+            sel = best < 0 ? 0 : best;
+            assign[n] = sel;
+            gate[n] = pr[sel];
+        }
+        sel_s[t] = sel;
     }
-    const int sel = best < 0 ? 0 : best;
-    assign[n] = sel;
-    gate[n] = pr[sel];
+    if (!bcnt) return;
+    __syncthreads();
+    if (t < MOE_TOK && n < N) {
+        const int a = sel_s[t];
+        int r = 0;
+        for (int j = 0; j < t; j++) r += sel_s[j] == a;
+        rank[n] = r;
+    }
+    for (int e = t; e < E; e += 256) {
+        int c = 0;
+        for (int j = 0; j < MOE_TOK; j++) c += sel_s[j] == e;
+        bcnt[(size_t)blockIdx.x * E + e] = c;
+    }
 }
 
 // LDS columns per round of k_moe_route: all of D when the staged rows and
@@ -252,6 +279,78 @@ __global__ __launch_bounds__(1024) void k_moe_index(const int *__restrict__ assi
     }
 }
 
+// The same sort from the router's per-block counts (bcnt [nblk][E], blocks of
+// MOE_TOK tokens) and in-block ranks (rank[n]): workgroup j places tokens
+// 256 j .. 256 j + 255 (router blocks b0 = 16 j .. b0 + 15).  Wave w sums
+// experts w, w + 4, ..: over the blocks before b0 (pre) and over all blocks
+// (tot), lanes striding the blocks, then a shuffle reduction (integer sums:
+// exact in any order).  Token n of in-workgroup block bb goes to
+//   eoff[a] + pre[a] + sum_{bb' < bb} bcnt[b0 + bb'][a] + rank[n],
+// which keeps ascending token order inside each expert, as k_moe_index does
+// (same idx, pos and eoff).  Every workgroup finds eoff; workgroup 0 writes it.
+#define MOE_IDX_TPB 256
+static_assert(MOE_IDX_TPB % MOE_TOK == 0, "whole router blocks per index workgroup");
+__global__ __launch_bounds__(MOE_IDX_TPB) void k_moe_index_blk(const int *__restrict__ assign,
+                                                             const int *__restrict__ bcnt, int N, int E,
+                                                             int *__restrict__ idx, int *__restrict__ pos,
+                                                             int *__restrict__ eoff, const float *__restrict__ fin,
+                                                             float *__restrict__ out, int D)
+{
+    constexpr int BPW = MOE_IDX_TPB / MOE_TOK;          // router blocks per workgroup
+    __shared__ int pre[TLG_MOE_MAXE], tot[TLG_MOE_MAXE], off[TLG_MOE_MAXE + 1];
+    __shared__ int loc[BPW][TLG_MOE_MAXE];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int nblk = (N + MOE_TOK - 1) / MOE_TOK, b0 = blockIdx.x * BPW;
+    for (int e = w; e < E; e += MOE_IDX_TPB / 64) {
+        int sp = 0, st = 0;
+        for (int b = lane; b < nblk; b += 64) {
+            const int c = bcnt[(size_t)b * E + e];
+            st += c;
+            if (b < b0) sp += c;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            sp += __shfl_xor(sp, o);
+            st += __shfl_xor(st, o);
+        }
+        if (lane == 0) { pre[e] = sp; tot[e] = st; }
+    }
+    for (int p = tid; p < BPW * E; p += MOE_IDX_TPB) {
+        const int bb = p / E, e = p % E;
+        loc[bb][e] = b0 + bb < nblk ? bcnt[(size_t)(b0 + bb) * E + e] : 0;
+    }
+    __syncthreads();
+    if (w == 0) {
+        // exclusive scan of the expert totals (E <= 64: one per lane)
+        const int c = lane < E ? tot[lane] : 0;
+        int inc = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(inc, o);
+            if (lane >= o) inc += t;
+        }
+        if (lane < E) off[lane] = inc - c;
+        if (lane == 63) off[E] = inc;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0 && tid <= E) eoff[tid] = off[tid];
+    const int n = blockIdx.x * MOE_IDX_TPB + tid;
+    if (n >= N) return;
+    const int a = assign[n], bb = tid / MOE_TOK;
+    if (a < 0 || a >= E) {          // not produced by k_moe_route; left out as k_moe_index does
+        pos[n] = -1;
+        if (out)
+            for (int d = 0; d < D; d += 4)
+                *reinterpret_cast<float4 *>(out + (size_t)n * D + d) =
+                    *reinterpret_cast<const float4 *>(fin + (size_t)n * D + d);
+        return;
+    }
+    int p = off[a] + pre[a] + pos[n];
+    for (int j = 0; j < bb; j++) p += loc[j][a];
+    pos[n] = p;
+    idx[p] = n;
+}
+
 // ------------------------------------------------------------ backward --
 // One wave per routed row i (token n = idx[i]): d_gate[n] = dout[n] . y[i],
 // dy[i] = gate[n] dout[n]  (:916-919).
@@ -357,6 +456,7 @@ struct MoeScratch {
     int *idx, *pos, *eoff;
     float *dgate, *drt, *y, *dy, *g, *u, *a;
     float *wpart;            // dWr partials, one row of D x E per router workgroup
+    int *bcnt;               // expert counts per router workgroup [nblk][E]
 };
 static void *g_moe_mem = nullptr;
 static size_t g_moe_bytes = 0;
@@ -372,10 +472,11 @@ static int moe_scratch(int N, int D, int F, int E, MoeScratch *s)
 {
     const size_t n = (size_t)N;
     const size_t nblk = (n + MOE_TOK - 1) / MOE_TOK;
-    const size_t sizes[11] = {n * 4, n * 4, (size_t)(TLG_MOE_MAXE + 1) * 4, n * 4, n * E * 4,
-                              n * D * 4, n * D * 4, n * F * 4, n * F * 4, n * F * 4, nblk * D * E * 4};
-    size_t total = 0, offs[11];
-    for (int k = 0; k < 11; k++) {
+    const size_t sizes[12] = {n * 4, n * 4, (size_t)(TLG_MOE_MAXE + 1) * 4, n * 4, n * E * 4,
+                              n * D * 4, n * D * 4, n * F * 4, n * F * 4, n * F * 4, nblk * D * E * 4,
+                              nblk * E * 4};
+    size_t total = 0, offs[12];
+    for (int k = 0; k < 12; k++) {
         offs[k] = total;
         total += (sizes[k] + 255) & ~(size_t)255;
     }
@@ -401,6 +502,7 @@ static int moe_scratch(int N, int D, int F, int E, MoeScratch *s)
     s->u = (float *)(b + offs[8]);
     s->a = (float *)(b + offs[9]);
     s->wpart = (float *)(b + offs[10]);
+    s->bcnt = (int *)(b + offs[11]);
     return TLG_OK;
 }
 
@@ -490,11 +592,15 @@ static int moe_fwd(const float *fnorm, const float *fin, float *out, int N, int 
 {
     int rc;
     const int dch = route_dch(D, E);
+    // the router leaves per-block counts and in-block ranks (in pos) for the
+    // many-workgroup index
     hipLaunchKernelGGL(k_moe_route, dim3((N + MOE_TOK - 1) / MOE_TOK), dim3(256), route_lds(dch, E), st, fnorm, wr,
-                       N, D, E, dch, rprobs, assign, gate);
+                       N, D, E, dch, rprobs, assign, gate, s.pos, s.bcnt);
     TLG_HIP(hipGetLastError());
     // the index also sets out = fin for tokens without an expert
-    if ((rc = moe_index(assign, N, E, s, fin, out, D, st))) return rc;
+    hipLaunchKernelGGL(k_moe_index_blk, dim3((N + MOE_IDX_TPB - 1) / MOE_IDX_TPB), dim3(MOE_IDX_TPB), 0, st, assign,
+                       s.bcnt, N, E, s.idx, s.pos, s.eoff, fin, out, D);
+    TLG_HIP(hipGetLastError());
     if ((rc = moe_w13(fnorm, N, D, F, E, w1, w3, s, keep ? s.g : nullptr, keep ? s.u : nullptr, st))) return rc;
     // y = a W2_e with the combine in the epilogue: out[n] = fin[n] + gate[n] y
     TlgExpertCall c;
