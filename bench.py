@@ -60,6 +60,18 @@ def roofline_class(flops, nbytes):
     return "mfma" if flops / max(nbytes, 1.0) >= RIDGE else "hbm"
 
 
+def warm_for(lib, fn, stream, seconds=0.1, label="warmup"):
+    """Untimed steps for about `seconds` of GPU work (at least 8), so the
+    clocks have ramped before a phase's timed region."""
+    t0, n = time.perf_counter(), 0
+    while n < 8 or time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            check(fn(), label)
+        n += 8
+        check(lib.tlg_stream_sync(stream), "sync")
+    return n
+
+
 def time_steps(lib, fn, stream, n):
     e0, e1 = lib.tlg_event_create(), lib.tlg_event_create()
     check(lib.tlg_stream_sync(stream), "sync")
@@ -274,8 +286,7 @@ def bench_train_config(lib, host, stream, name, steps, tune=True, retime=False):
     tuned = apply_tiles(lib, host, run, stream, name, retime) if tune else None
     check(host.dll.tl_run_graph_build(run, stream, 1), "graph build")
     step = lambda: host.dll.tl_run_graph_step(run, stream)  # noqa: E731
-    for _ in range(5):
-        check(step(), "warmup")
+    warm_for(lib, step, stream)
     ms, _ = time_steps(lib, step, stream, steps)
     per = ms / steps
     roof = roof_time_ms(plan)
@@ -365,8 +376,7 @@ def bench_moe(lib, stream, steps):
         return rc or lib.tlg_dev_moe_grouped_bwd(d["fnorm"], d["dout"], d["dfn"], d["assign"], d["gate"],
                                                  d["rprobs"], N, D, F, E, d["wr"], d["w1"], d["w3"], d["w2"],
                                                  d["gwr"], d["gw1"], d["gw3"], d["gw2"], stream)
-    for _ in range(3):
-        check(step(), "moe warmup")
+    warm_for(lib, step, stream, label="moe warmup")
     ms, _ = time_steps(lib, step, stream, steps)
     # the same pair from a kept forward state (tlg_dev_moe_grouped_fwd_keep /
     # _bwd_kept: no index rebuild, no W1 | W3 and W2 recompute in the backward)
@@ -380,8 +390,7 @@ def bench_moe(lib, stream, steps):
         return rc or lib.tlg_dev_moe_grouped_bwd_kept(d["fnorm"], d["dout"], d["dfn"], d["assign"], d["gate"],
                                                       d["rprobs"], N, D, F, E, d["wr"], d["w1"], d["w3"], d["w2"],
                                                       d["gwr"], d["gw1"], d["gw3"], d["gw2"], d["keep"], kb, stream)
-    for _ in range(3):
-        check(step_kept(), "moe kept warmup")
+    warm_for(lib, step_kept, stream, label="moe kept warmup")
     ms_k, _ = time_steps(lib, step_kept, stream, steps)
     # the kept backward leaves dWr's column sum and the dW1 / dW3 slice sums
     # queued (they read the kept index and write gwr, gw1, gw3): run them
