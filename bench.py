@@ -318,8 +318,7 @@ def bench_decode(lib, host, stream, steps, M=1, pool=6, packed=False, eager=Fals
     else:
         check(host.dll.tl_run_graph_build(run, stream, 1), "decode graph")
         step = lambda: host.dll.tl_run_graph_step(run, stream)  # noqa: E731
-    for _ in range(2 * pool):
-        check(step(), "decode warmup")
+    warm_for(lib, step, stream, label="decode warmup")    # every weight copy, many times over
     ms, _ = time_steps(lib, step, stream, steps)
     launches = host.dll.tl_run_grouped_launches(run)
     wbytes = sum(4.0 * c["K"] * c["N"] for c in plan.calls if c["op"] != "zero")
