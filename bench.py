@@ -819,7 +819,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
-              "(the path would shard M across GPUs with one all-reduce of dW; see DESIGN.md)",
+              "(the path would shard M across GPUs with one all-reduce of dW)",
               file=sys.stderr)
         sys.exit(2)
 

@@ -61,7 +61,7 @@ def test_plan_counts_and_flops(name):
     # 7 forward + 14 backward per layer, 3 head GEMMs, 6 per MTP head
     assert len(g) == 21 * L + 3 + 6 * n_mtp
     if name == "m3":
-        assert abs(p.flops() / 1e9 - 124.02) < 0.01       # SURVEY 8(d) figure for cfg1
+        assert abs(p.flops() / 1e9 - 124.02) < 0.01       # cfg1's GEMM flop per step
     # every accumulating GEMM into an activation buffer has a clear before it
     # since that buffer's last setting write
     cleared = set()
@@ -78,7 +78,7 @@ def test_decode_plan_shapes():
     g = [c for c in p.calls if c["op"] != "zero"]
     assert len(g) == 8 * 7 + 1
     wbytes = sum(4 * c["K"] * c["N"] for c in g)
-    assert abs(wbytes / 1e6 - 52.69) < 0.01                # SURVEY 8(a) a6 figure
+    assert abs(wbytes / 1e6 - 52.69) < 0.01                # cfg3's weight bytes per decode step
     assert g[-1]["op"] == "mm_bt" and (g[-1]["K"], g[-1]["N"]) == (2048, 384)
 
 
