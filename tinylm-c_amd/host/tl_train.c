@@ -17,6 +17,7 @@
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <limits.h>
 #include <string.h>
 
 typedef struct { size_t emb, an1, wq, wk, wv, wo, an2, wr, w1, w3, w2, nf, mtp0, total; } Map;
@@ -312,7 +313,10 @@ static int group(TlTrain *t, const TlgGemmCall *cs, int n, void *st)
 static int rope_fused(const TlModel *m) { return (m->H / m->KV) % 4 == 0; }
 
 /* ---- forward, tinylm.c:968-1029 ------------------------------------------- */
-int tl_train_forward(TlTrain *t, void *st)
+/* clear_g: memset(G) (:2628) rides in the logits launch (a clear item of the
+ * grouped launch, nothing there reads or writes G), so a step's backward
+ * need not launch it */
+static int forward_impl(TlTrain *t, int clear_g, void *st)
 {
     const TlModel *m = &t->m;
     const int N = t->N, D = m->D, KD = t->KD, F = m->F, V = m->V, H = m->H, KV = m->KV, T = m->T, E = t->E;
@@ -354,14 +358,24 @@ int tl_train_forward(TlTrain *t, void *st)
         }
     }
     CK(tlg_dev_rmsnorm_fwd(t->x_final, P + w.nf, t->fn, t->fn_rinv, N, D, st));
-    GROUP(st, BT(t->logits, 0, t->fn, P + w.emb, N, V, D));
+    if (clear_g) {
+        TlgGemmCall z;
+        memset(&z, 0, sizeof z);
+        z.op = 3; z.C = t->G; z.M = 1; z.N = (int)t->np;
+        GROUP(st, BT(t->logits, 0, t->fn, P + w.emb, N, V, D), z);
+    } else {
+        GROUP(st, BT(t->logits, 0, t->fn, P + w.emb, N, V, D));
+    }
     /* softmax-CE, with backward's dlogits (:1076-1082) from the same pass */
     CK(tlg_dev_xent(t->logits, t->tgt, t->dl, t->loss, 1.0f / N, N, V, st));
     return 0;
 }
 
+int tl_train_forward(TlTrain *t, void *st) { return forward_impl(t, 0, st); }
+
 /* ---- backward, tinylm.c:1072-1154 with mtp_grad :1036-1069 ---------------- */
-int tl_train_backward(TlTrain *t, void *st)
+/* g_clear: G was cleared by the forward before it (forward_impl) */
+static int backward_impl(TlTrain *t, int g_clear, void *st)
 {
     const TlModel *m = &t->m;
     const int N = t->N, D = m->D, KD = t->KD, F = m->F, V = m->V, H = m->H, KV = m->KV, T = m->T, E = t->E;
@@ -370,7 +384,7 @@ int tl_train_backward(TlTrain *t, void *st)
     float *G = t->G;
     Map w;
     wmap(t, 0, &w);
-    CK(tlg_dev_zero(G, t->np, st));                                   /* memset(G), :2628 */
+    if (!g_clear) CK(tlg_dev_zero(G, t->np, st));                     /* memset(G), :2628 */
     GROUP(st, MM(t->dfn, t->dl, P + w.emb, N, V, D), ATB(G + w.emb, t->dl, t->fn, N, V, D));
     for (int h = 0; h < m->n_mtp; h++) {
         const float wk = 0.2f * powf(0.8f, (float)h);
@@ -439,6 +453,8 @@ int tl_train_backward(TlTrain *t, void *st)
     return 0;
 }
 
+int tl_train_backward(TlTrain *t, void *st) { return backward_impl(t, 0, st); }
+
 /* ---- global_gradnorm + AdamW, tinylm.c:2630-2633 -------------------------- */
 int tl_train_optimize(TlTrain *t, void *st)
 {
@@ -449,8 +465,9 @@ int tl_train_optimize(TlTrain *t, void *st)
 
 int tl_train_step(TlTrain *t, void *st)
 {
-    CK(tl_train_forward(t, st));
-    CK(tl_train_backward(t, st));
+    const int fold = t->np <= (size_t)INT_MAX;         /* the clear item's extent is an int */
+    CK(forward_impl(t, fold, st));
+    CK(backward_impl(t, fold, st));
     return tl_train_optimize(t, st);
 }
 
