@@ -124,8 +124,20 @@ int tlg_dev_silu_bwd(float *dt1, const float *dhk, const float *t1, size_t n, vo
 int tlg_dev_xent(const float *logits, const int *tgt, float *dlogits, float *loss, float scale, int N, int V,
                  void *stream);
 
+/* tlg_dev_xent without the loss sum: each row's -log(p[target] + 1e-12) goes
+ * to rows[N] (doubles, caller-owned), for tlg_dev_gradnorm_loss to average
+ * later in the step (no counterpart as one call). */
+int tlg_dev_xent_rows(const float *logits, const int *tgt, float *dlogits, double *rows, float scale, int N, int V,
+                      void *stream);
+
 /* global_gradnorm, tinylm.c:1171-1176: norm[0] = sqrt(sum G^2) (double sum). */
 int tlg_dev_gradnorm(const float *G, size_t n, float *norm, void *stream);
+/* tlg_dev_gradnorm that also sets loss[0] = the mean of rows[0, N) from
+ * tlg_dev_xent_rows, the same sum in the same order as tlg_dev_xent's loss
+ * (:1026-1028), in the norm's last kernel: a training step's loss costs no
+ * launch of its own (no counterpart as one call). */
+int tlg_dev_gradnorm_loss(const float *G, size_t n, float *norm, const double *rows, int N, float *loss,
+                          void *stream);
 
 /* adamw, tinylm.c:1159-1170, with the clip of train_loop folded in
  * (:2630-2633): hyper = device floats {lr, b1, b2, wd, 1 - b1^t, 1 - b2^t};

@@ -357,6 +357,36 @@ def test_xent(lib, st, N, V, scale, spread):
     assert (np.abs(got - d64) / rowmax).max() <= 1e-6
 
 
+@pytest.mark.parametrize("N,V", [(300, 2048), (4, 50), (4096, 2048)])
+def test_loss_in_gradnorm_is_bit_identical(lib, N, V):
+    """The training step's split of tlg_dev_xent: tlg_dev_xent_rows (per-row
+    losses, no sum) then tlg_dev_gradnorm_loss (the norm and the loss mean in
+    one last kernel) give tlg_dev_xent's loss and dlogits and
+    tlg_dev_gradnorm's norm bit for bit."""
+    t = _t()
+    r = np.random.default_rng(N + V)
+    lg = r.standard_normal((N, V)).astype(np.float32)
+    tgt = r.integers(0, V, N).astype(np.int32)
+    G = (0.01 * r.standard_normal(200_003)).astype(np.float32)
+    LG, TG, Gd = dev(lg), dev(tgt), dev(G)
+    dl0, dl1 = nan_like((N, V)), nan_like((N, V))
+    loss0, loss1, n0, n1 = nan_like((1,)), nan_like((1,)), nan_like((1,)), nan_like((1,))
+    rows = t.full((N,), float("nan"), dtype=t.float64, device="cuda")
+    lib.check(lib.tlg_dev_xent(LG.data_ptr(), TG.data_ptr(), dl0.data_ptr(), loss0.data_ptr(), 1.0 / N, N, V,
+                               stream()), "xent")
+    lib.check(lib.tlg_dev_gradnorm(Gd.data_ptr(), G.size, n0.data_ptr(), stream()), "gradnorm")
+    lib.check(lib.tlg_dev_xent_rows(LG.data_ptr(), TG.data_ptr(), dl1.data_ptr(), rows.data_ptr(), 1.0 / N, N, V,
+                                    stream()), "xent_rows")
+    lib.check(lib.tlg_dev_gradnorm_loss(Gd.data_ptr(), G.size, n1.data_ptr(), rows.data_ptr(), N,
+                                        loss1.data_ptr(), stream()), "gradnorm_loss")
+    assert np.array_equal(host(dl0), host(dl1))
+    assert host(loss0)[0] == host(loss1)[0] and host(n0)[0] == host(n1)[0]
+    p = Gd.data_ptr()
+    assert lib.tlg_dev_gradnorm_loss(p, 10, p, 0, N, p, stream()) != 0            # no rows
+    assert lib.tlg_dev_xent_rows(p, p, p, 0, 1.0, N, V, stream()) != 0            # no rows
+    lib.tlg_last_error()
+
+
 def test_embedding_bit_exact(lib, st):
     import ctypes
     r = np.random.default_rng(1)

@@ -1739,9 +1739,11 @@ __global__ __launch_bounds__(256) void k_xent_reg(const float *__restrict__ logi
 }
 
 // Sum of n doubles by one workgroup in a fixed order; out = (float)(sum / n).
-__global__ __launch_bounds__(1024) void k_sum_loss(const double *__restrict__ rowloss, int n, float *__restrict__ out)
+// the mean of rowloss[0, n) by 1024 threads: strided per-thread sums, then a
+// fixed tree over them (s: 1024 doubles of LDS)
+__device__ __forceinline__ void sum_loss_1024(const double *__restrict__ rowloss, int n, float *__restrict__ out,
+                                              double *s)
 {
-    __shared__ double s[1024];
     double a = 0.0;
     for (int i = threadIdx.x; i < n; i += 1024) a += rowloss[i];
     s[threadIdx.x] = a;
@@ -1751,6 +1753,12 @@ __global__ __launch_bounds__(1024) void k_sum_loss(const double *__restrict__ ro
         __syncthreads();
     }
     if (threadIdx.x == 0) out[0] = (float)(s[0] / n);
+}
+
+__global__ __launch_bounds__(1024) void k_sum_loss(const double *__restrict__ rowloss, int n, float *__restrict__ out)
+{
+    __shared__ double s[1024];
+    sum_loss_1024(rowloss, n, out, s);
 }
 
 // ------------------------------------------------------ gradnorm, AdamW --
@@ -1772,7 +1780,11 @@ __global__ __launch_bounds__(256) void k_sumsq(const float *__restrict__ G, size
     if (threadIdx.x == 0) part[blockIdx.x] = s[0];
 }
 
-__global__ __launch_bounds__(1024) void k_norm_final(const double *__restrict__ part, float *__restrict__ norm)
+// With rowloss: also loss[0] = the mean of rowloss[0, n), exactly as
+// k_sum_loss forms it (after the norm, in the same LDS).
+__global__ __launch_bounds__(1024) void k_norm_final(const double *__restrict__ part, float *__restrict__ norm,
+                                                     const double *__restrict__ rowloss, int n,
+                                                     float *__restrict__ loss)
 {
     __shared__ double s[1024];
     s[threadIdx.x] = part[threadIdx.x];
@@ -1782,6 +1794,9 @@ __global__ __launch_bounds__(1024) void k_norm_final(const double *__restrict__ 
         __syncthreads();
     }
     if (threadIdx.x == 0) norm[0] = (float)sqrt(s[0]);
+    if (!rowloss) return;
+    __syncthreads();                      // s[0] is read before the loss sum reuses s
+    sum_loss_1024(rowloss, n, loss, s);
 }
 
 // hyper = {lr, b1, b2, wd, bc1, bc2}; gscale = 1 / norm when norm > 1.
@@ -2124,15 +2139,14 @@ extern "C" int tlg_dev_silu_bwd(float *dt1, const float *dhk, const float *t1, s
     return ew(EW_SILU_BWD, n, dt1, nullptr, dhk, t1, nullptr, stream);
 }
 
-extern "C" int tlg_dev_xent(const float *logits, const int *tgt, float *dlogits, float *loss, float scale, int N,
-                            int V, void *stream)
+static int xent_launch(const float *logits, const int *tgt, float *dlogits, double *rows, float *loss, float scale,
+                       int N, int V, void *stream)
 {
     int rc = begin();
     if (rc) return rc;
     if (N < 0 || V <= 0) return tlg_fail(TLG_EINVAL, "xent: N=%d V=%d", N, V);
     if (N == 0) return TLG_OK;
-    double *rows = nullptr;
-    if (loss) {
+    if (loss && !rows) {
         void *ws;
         if ((rc = tr_scratch((size_t)N * 8, &ws))) return rc;
         rows = (double *)ws;
@@ -2147,6 +2161,19 @@ extern "C" int tlg_dev_xent(const float *logits, const int *tgt, float *dlogits,
     return TLG_OK;
 }
 
+extern "C" int tlg_dev_xent(const float *logits, const int *tgt, float *dlogits, float *loss, float scale, int N,
+                            int V, void *stream)
+{
+    return xent_launch(logits, tgt, dlogits, nullptr, loss, scale, N, V, stream);
+}
+
+extern "C" int tlg_dev_xent_rows(const float *logits, const int *tgt, float *dlogits, double *rows, float scale,
+                                 int N, int V, void *stream)
+{
+    if (!rows) return tlg_fail(TLG_EINVAL, "xent_rows: no row buffer");
+    return xent_launch(logits, tgt, dlogits, rows, nullptr, scale, N, V, stream);
+}
+
 extern "C" int tlg_dev_gradnorm(const float *G, size_t n, float *norm, void *stream)
 {
     int rc = begin();
@@ -2155,7 +2182,22 @@ extern "C" int tlg_dev_gradnorm(const float *G, size_t n, float *norm, void *str
     if ((rc = tr_scratch(GN_BLOCKS * 8, &ws))) return rc;
     hipStream_t st = ST(stream);
     hipLaunchKernelGGL(k_sumsq, dim3(GN_BLOCKS), dim3(256), 0, st, G, n, (double *)ws);
-    hipLaunchKernelGGL(k_norm_final, dim3(1), dim3(1024), 0, st, (const double *)ws, norm);
+    hipLaunchKernelGGL(k_norm_final, dim3(1), dim3(1024), 0, st, (const double *)ws, norm, nullptr, 0, nullptr);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_gradnorm_loss(const float *G, size_t n, float *norm, const double *rows, int N, float *loss,
+                                     void *stream)
+{
+    int rc = begin();
+    if (rc) return rc;
+    if (!rows || !loss || N <= 0) return tlg_fail(TLG_EINVAL, "gradnorm_loss: rows, loss and N > 0 required");
+    void *ws;
+    if ((rc = tr_scratch(GN_BLOCKS * 8, &ws))) return rc;
+    hipStream_t st = ST(stream);
+    hipLaunchKernelGGL(k_sumsq, dim3(GN_BLOCKS), dim3(256), 0, st, G, n, (double *)ws);
+    hipLaunchKernelGGL(k_norm_final, dim3(1), dim3(1024), 0, st, (const double *)ws, norm, rows, N, loss);
     LAUNCH_CHECK();
     return TLG_OK;
 }

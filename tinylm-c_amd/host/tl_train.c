@@ -35,6 +35,7 @@ struct TlTrain {
     /* one each */
     float *x_final, *fn, *fn_rinv, *logits, *dl, *dout, *dfnorm, *dfin, *datt, *dq, *dk, *dv, *dnorm, *dain, *dfn;
     float *attn_d;             /* the attention backward's D = datt . ctx [N][H] */
+    double *lrows;             /* per-row losses of a step's forward [N] */
     /* RMSNorm backward's per-row-block gain partials; their column sum rides
      * along in the next grouped GEMM launch */
     float *rms_part;
@@ -126,7 +127,7 @@ TlTrain *tl_train_new(const TlModel *m, int B)
         {(void **)&t->act, dense ? 4 * L * NF : 0}, {(void **)&t->dfnorm, 4 * ND}, {(void **)&t->dfin, 4 * ND},
         {(void **)&t->datt, 4 * ND}, {(void **)&t->dq, 4 * ND}, {(void **)&t->dk, 4 * NK},
         {(void **)&t->dv, 4 * NK}, {(void **)&t->dnorm, 4 * ND}, {(void **)&t->dain, 4 * ND},
-        {(void **)&t->dfn, 4 * ND}, {(void **)&t->attn_d, 4 * (size_t)N * H},
+        {(void **)&t->dfn, 4 * ND}, {(void **)&t->attn_d, 4 * (size_t)N * H}, {(void **)&t->lrows, 8 * (size_t)N},
         {(void **)&t->rms_part, 4 * t->rms_part_n},
         {(void **)&t->moe_keep, L * t->moe_keep_b},
     };
@@ -313,9 +314,10 @@ static int group(TlTrain *t, const TlgGemmCall *cs, int n, void *st)
 static int rope_fused(const TlModel *m) { return (m->H / m->KV) % 4 == 0; }
 
 /* ---- forward, tinylm.c:968-1029 ------------------------------------------- */
-/* clear_g: memset(G) (:2628) rides in the logits launch (a clear item of the
- * grouped launch, nothing there reads or writes G), so a step's backward
- * need not launch it */
+/* clear_g (inside a step): memset(G) (:2628) rides in the logits launch (a
+ * clear item of the grouped launch, nothing there reads or writes G), so the
+ * backward need not launch it; and the per-row losses go to lrows, averaged
+ * by the gradnorm's last kernel (tl_train_optimize's), not by a kernel here */
 static int forward_impl(TlTrain *t, int clear_g, void *st)
 {
     const TlModel *m = &t->m;
@@ -367,7 +369,10 @@ static int forward_impl(TlTrain *t, int clear_g, void *st)
         GROUP(st, BT(t->logits, 0, t->fn, P + w.emb, N, V, D));
     }
     /* softmax-CE, with backward's dlogits (:1076-1082) from the same pass */
-    CK(tlg_dev_xent(t->logits, t->tgt, t->dl, t->loss, 1.0f / N, N, V, st));
+    if (clear_g)
+        CK(tlg_dev_xent_rows(t->logits, t->tgt, t->dl, t->lrows, 1.0f / N, N, V, st));
+    else
+        CK(tlg_dev_xent(t->logits, t->tgt, t->dl, t->loss, 1.0f / N, N, V, st));
     return 0;
 }
 
@@ -456,19 +461,26 @@ static int backward_impl(TlTrain *t, int g_clear, void *st)
 int tl_train_backward(TlTrain *t, void *st) { return backward_impl(t, 0, st); }
 
 /* ---- global_gradnorm + AdamW, tinylm.c:2630-2633 -------------------------- */
-int tl_train_optimize(TlTrain *t, void *st)
+/* loss_rows: also average the forward's lrows into loss (forward_impl's
+ * clear_g form) */
+static int optimize_impl(TlTrain *t, int loss_rows, void *st)
 {
-    CK(tlg_dev_gradnorm(t->G, t->np, t->gnorm, st));
+    if (loss_rows)
+        CK(tlg_dev_gradnorm_loss(t->G, t->np, t->gnorm, t->lrows, t->N, t->loss, st));
+    else
+        CK(tlg_dev_gradnorm(t->G, t->np, t->gnorm, st));
     CK(tlg_dev_adamw(t->P, t->G, t->Mo, t->Vo, t->np, t->hyper, t->gnorm, st));
     return 0;
 }
+
+int tl_train_optimize(TlTrain *t, void *st) { return optimize_impl(t, 0, st); }
 
 int tl_train_step(TlTrain *t, void *st)
 {
     const int fold = t->np <= (size_t)INT_MAX;         /* the clear item's extent is an int */
     CK(forward_impl(t, fold, st));
     CK(backward_impl(t, fold, st));
-    return tl_train_optimize(t, st);
+    return optimize_impl(t, fold, st);
 }
 
 int tl_train_graph_build(TlTrain *t, void *st)
