@@ -34,6 +34,13 @@ int tlg_dev_embed_bwd(float *demb, const float *dout, const int *tok, int N, int
  * rinv[r] = s (if rinv), out = x * s * g. */
 int tlg_dev_rmsnorm_fwd(const float *x, const float *g, float *out, float *rinv, int rows, int D, void *stream);
 
+/* tlg_dev_embed_fwd into x, then tlg_dev_rmsnorm_fwd of x, in one pass: the
+ * forward's embedding gather (:972-976) and its first layer's norm
+ * (:540-563), the same x, out and rinv bit for bit (no counterpart as one
+ * call).  emb [V][D]; x, out [N][D]. */
+int tlg_dev_embed_rmsnorm_fwd(const float *emb, const int *tok, int V, float *x, const float *g, float *out,
+                              float *rinv, int N, int D, void *stream);
+
 /* rmsnorm_bwd, tinylm.c:565-588: dx = base + s g dy - (s^3/D)(x . g dy) x with
  * base = dx_in, which may be dx itself (the reference's dx +=), or zero when
  * dx_in is NULL (the memset + rmsnorm_bwd of :1089-1090); dg += sum_r x s dy

@@ -407,6 +407,33 @@ def test_embedding_bit_exact(lib, st):
     assert np.array_equal(host(DE), want)
 
 
+@pytest.mark.parametrize("V,D,N", [(2048, 256, 4096), (50, 36, 77), (300, 1028, 130), (40, 2048, 9),
+                                   (30, 2052, 5)])
+def test_embed_rmsnorm_fwd_is_bit_identical(lib, V, D, N):
+    """tlg_dev_embed_rmsnorm_fwd against tlg_dev_embed_fwd then
+    tlg_dev_rmsnorm_fwd: x, out and rinv bit for bit, NaN rows for tokens
+    outside [0, V) included; D of one to eight float4 columns per lane, and
+    D > 2048 (the two-pass fallback)."""
+    print("embed_rmsnorm", V, D, N, flush=True)
+    r = np.random.default_rng(V * D + N)
+    emb = r.standard_normal((V, D)).astype(np.float32)
+    g = (1.0 + 0.1 * r.standard_normal(D)).astype(np.float32)
+    tok = r.integers(0, V, N).astype(np.int32)
+    tok[::5] = V                                        # outside [0, V): NaN rows
+    tok[1::7] = -3
+    EM, G, T = dev(emb), dev(g), dev(tok)
+    x0, o0, x1, o1 = nan_like((N, D)), nan_like((N, D)), nan_like((N, D)), nan_like((N, D))
+    r0, r1 = nan_like((N,)), nan_like((N,))
+    lib.check(lib.tlg_dev_embed_fwd(x0.data_ptr(), EM.data_ptr(), T.data_ptr(), N, D, V, stream()), "embed")
+    lib.check(lib.tlg_dev_rmsnorm_fwd(x0.data_ptr(), G.data_ptr(), o0.data_ptr(), r0.data_ptr(), N, D, stream()),
+              "rms")
+    lib.check(lib.tlg_dev_embed_rmsnorm_fwd(EM.data_ptr(), T.data_ptr(), V, x1.data_ptr(), G.data_ptr(),
+                                            o1.data_ptr(), r1.data_ptr(), N, D, stream()), "embed_rms")
+    for a0, a1 in ((x0, x1), (o0, o1), (r0, r1)):
+        assert np.array_equal(host(a0), host(a1), equal_nan=True)
+    assert np.isnan(host(x1)[::5]).all() and not np.isnan(host(x1)[2]).any()
+
+
 @pytest.mark.parametrize("V,D,N", [(2048, 384, 8192), (50, 128, 5000), (37, 36, 77), (2048, 1028, 300),
                                    (64, 64, 4100)])
 def test_embedding_bwd_shapes(lib, V, D, N):

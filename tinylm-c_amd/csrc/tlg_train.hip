@@ -292,15 +292,28 @@ __global__ __launch_bounds__(256) void k_embed_bwd1(const float *__restrict__ do
 // columns per lane, D <= 256 NV; loads use clamped, in-bounds indices, columns
 // past D are masked at use); NV = 0 takes any D and reads the row twice.  Both
 // forms add the same terms in the same order.
+// With tok (NV > 0 only): row r is the embedding row x[tok[r]] (x = the
+// table of V rows; NaN for a token outside [0, V), as k_embed_fwd), also
+// stored to xout[r] -- the embedding gather (:972-976) and the first norm in
+// one pass.
 template <int NV>
 __global__ __launch_bounds__(256) void k_rms_fwd(const float *__restrict__ x, const float *__restrict__ g,
-                                                 float *__restrict__ out, float *__restrict__ rinv, int rows, int D)
+                                                 float *__restrict__ out, float *__restrict__ rinv, int rows, int D,
+                                                 const int *__restrict__ tok = nullptr, int V = 0,
+                                                 float *__restrict__ xout = nullptr)
 {
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
     const int d4 = D >> 2;
-    const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (size_t)r * D);
+    int tr = r;
+    bool bad = false;
+    if (NV > 0 && tok) {
+        tr = tok[r];
+        bad = tr < 0 || tr >= V;
+        if (bad) tr = 0;
+    }
+    const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (size_t)tr * D);
     const f32x4 *g4 = reinterpret_cast<const f32x4 *>(g);
     f32x4 *orow = reinterpret_cast<f32x4 *>(out + (size_t)r * D);
     float ms = 0.f;
@@ -322,6 +335,14 @@ __global__ __launch_bounds__(256) void k_rms_fwd(const float *__restrict__ x, co
         for (int j = 0; j < NV; j++) {
             xa[j] = xr[min(lane + 64 * j, d4 - 1)];
             gv[j] = g4[min(lane + 64 * j, d4 - 1)];
+        }
+        if (tok) {
+            f32x4 *xo = reinterpret_cast<f32x4 *>(xout + (size_t)r * D);
+#pragma unroll
+            for (int j = 0; j < NV; j++) {
+                if (bad) xa[j] = f32x4{NAN, NAN, NAN, NAN};
+                if (lane + 64 * j < d4) xo[lane + 64 * j] = xa[j];
+            }
         }
 #pragma unroll
         for (int j = 0; j < NV; j++)
@@ -1884,15 +1905,47 @@ extern "C" int tlg_dev_rmsnorm_fwd(const float *x, const float *g, float *out, f
     const dim3 grid((rows + 3) / 4);
     const int nv = (D / 4 + 63) / 64;
     if (nv <= 1)
-        hipLaunchKernelGGL(k_rms_fwd<1>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D);
+        hipLaunchKernelGGL(k_rms_fwd<1>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D,
+                           (const int *)nullptr, 0, (float *)nullptr);
     else if (nv <= 2)
-        hipLaunchKernelGGL(k_rms_fwd<2>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D);
+        hipLaunchKernelGGL(k_rms_fwd<2>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D,
+                           (const int *)nullptr, 0, (float *)nullptr);
     else if (nv <= 4)
-        hipLaunchKernelGGL(k_rms_fwd<4>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D);
+        hipLaunchKernelGGL(k_rms_fwd<4>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D,
+                           (const int *)nullptr, 0, (float *)nullptr);
     else if (nv <= 8)
-        hipLaunchKernelGGL(k_rms_fwd<8>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D);
+        hipLaunchKernelGGL(k_rms_fwd<8>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D,
+                           (const int *)nullptr, 0, (float *)nullptr);
     else
-        hipLaunchKernelGGL(k_rms_fwd<0>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D);
+        hipLaunchKernelGGL(k_rms_fwd<0>, grid, dim3(256), 0, ST(stream), x, g, out, rinv, rows, D,
+                           (const int *)nullptr, 0, (float *)nullptr);
+    LAUNCH_CHECK();
+    return TLG_OK;
+}
+
+extern "C" int tlg_dev_embed_rmsnorm_fwd(const float *emb, const int *tok, int V, float *x, const float *g, float *out,
+                                         float *rinv, int N, int D, void *stream)
+{
+    int rc = begin();
+    if (rc) return rc;
+    const int nv = (D / 4 + 63) / 64;
+    if (N < 0 || D <= 0 || D % 4 || V <= 0 || !tok || !al16(emb) || !al16(x) || !al16(g) || !al16(out))
+        return tlg_fail(TLG_EINVAL, "embed_rmsnorm_fwd: N=%d D=%d V=%d (D %% 4 == 0, aligned rows)", N, D, V);
+    if (N == 0) return TLG_OK;
+    if (nv > 8) {        // rows wider than 2048: the two passes
+        if ((rc = tlg_dev_embed_fwd(x, emb, tok, N, D, V, stream))) return rc;
+        return tlg_dev_rmsnorm_fwd(x, g, out, rinv, N, D, stream);
+    }
+    const dim3 grid((N + 3) / 4);
+    hipStream_t st = ST(stream);
+    if (nv <= 1)
+        hipLaunchKernelGGL(k_rms_fwd<1>, grid, dim3(256), 0, st, emb, g, out, rinv, N, D, tok, V, x);
+    else if (nv <= 2)
+        hipLaunchKernelGGL(k_rms_fwd<2>, grid, dim3(256), 0, st, emb, g, out, rinv, N, D, tok, V, x);
+    else if (nv <= 4)
+        hipLaunchKernelGGL(k_rms_fwd<4>, grid, dim3(256), 0, st, emb, g, out, rinv, N, D, tok, V, x);
+    else
+        hipLaunchKernelGGL(k_rms_fwd<8>, grid, dim3(256), 0, st, emb, g, out, rinv, N, D, tok, V, x);
     LAUNCH_CHECK();
     return TLG_OK;
 }

@@ -327,12 +327,15 @@ static int forward_impl(TlTrain *t, int clear_g, void *st)
     Map w;
     wmap(t, 0, &w);
     t->gi = 0;                                   /* the step's first grouped launch */
-    CK(tlg_dev_embed_fwd(t->a_in, P + w.emb, t->tok, N, D, V, st));
+    const float *emb = P + w.emb;
     for (int l = 0; l < m->L; l++) {
         wmap(t, l, &w);
         float *xin = t->a_in + l * ND, *an = t->a_norm + l * ND, *q = t->q + l * ND, *k = t->k + l * NK,
               *v = t->v + l * NK, *cx = t->ctx + l * ND, *fi = t->f_in + l * ND, *fnl = t->f_norm + l * ND;
-        CK(tlg_dev_rmsnorm_fwd(xin, P + w.an1, an, t->a_rinv + (size_t)l * N, N, D, st));
+        if (l == 0)     /* the embedding gather and the first norm in one pass */
+            CK(tlg_dev_embed_rmsnorm_fwd(emb, t->tok, V, xin, P + w.an1, an, t->a_rinv, N, D, st));
+        else
+            CK(tlg_dev_rmsnorm_fwd(xin, P + w.an1, an, t->a_rinv + (size_t)l * N, N, D, st));
         GROUP(st, MM(q, an, P + w.wq, N, D, D), MM(k, an, P + w.wk, N, D, KD), MM(v, an, P + w.wv, N, D, KD));
         if (rope_fused(m)) {
             /* q, k stay pre-rope; the attention kernels rotate as they load */

@@ -105,6 +105,7 @@ SIGNATURES = {
     "tlg_dev_silu_bwd": (_i, [_vp, _vp, _vp, _sz, _vp]),
     "tlg_dev_xent": (_i, [_vp, _vp, _vp, _vp, ctypes.c_float, _i, _i, _vp]),
     "tlg_dev_gradnorm": (_i, [_vp, _sz, _vp, _vp]),
+    "tlg_dev_embed_rmsnorm_fwd": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _vp]),
     "tlg_dev_xent_rows": (_i, [_vp, _vp, _vp, _vp, ctypes.c_float, _i, _i, _vp]),
     "tlg_dev_gradnorm_loss": (_i, [_vp, _sz, _vp, _vp, _i, _vp, _vp]),
     "tlg_dev_adamw": (_i, [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp]),
