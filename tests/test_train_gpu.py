@@ -357,6 +357,19 @@ def test_xent(lib, st, N, V, scale, spread):
     assert (np.abs(got - d64) / rowmax).max() <= 1e-6
 
 
+@pytest.mark.parametrize("n,off", [(1_000_003, 0), (1_000_003, 1), (5, 0), (3, 2)])
+def test_gradnorm_any_alignment(lib, n, off):
+    """The norm's float4 pass (16-byte aligned G) and its element-wise pass
+    (G offset by one or two floats, and the n % 4 tail) against float64."""
+    r = np.random.default_rng(n + off)
+    G = (0.01 * r.standard_normal(n + off)).astype(np.float32)
+    Gd = dev(G)
+    norm = nan_like((1,))
+    lib.check(lib.tlg_dev_gradnorm(Gd.data_ptr() + 4 * off, n, norm.data_ptr(), stream()), "gradnorm")
+    want = np.sqrt((G[off:].astype(np.float64) ** 2).sum())
+    assert abs(float(host(norm)[0]) - want) <= 1e-6 * want
+
+
 @pytest.mark.parametrize("N,V", [(300, 2048), (4, 50), (4096, 2048)])
 def test_loss_in_gradnorm_is_bit_identical(lib, N, V):
     """The training step's split of tlg_dev_xent: tlg_dev_xent_rows (per-row
